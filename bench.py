@@ -1,0 +1,291 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused non-GEMM layer primitives on one MI355X.
+
+Default workload: the non-GEMM work of one
+Qwen3-TTS-0.6B talker layer at prefill -- 512 tokens x hidden 1024, f32
+activations ~N(0,1), BF16 norm gains, 16 q / 8 kv heads x 128, NEOX rope theta
+1e6 at positions 0..511, SwiGLU 3072 -- plus the BF16 text-embedding gather
+from a 151936 x 2048 table ~N(0, 0.02) with 512 uniform ids. One step is six
+launches through the C ABI, in graph order:
+
+    get_rows(bf16 table)        talker.cpp:44
+    rms_norm_mul (input norm)   operations.cpp:86
+    qk_norm_rope (q and k)      operations.cpp:98-104
+    add_rms_norm_mul (+sum)     operations.cpp:143-145
+    swiglu                      operations.cpp:39-41
+    add (layer output)          operations.cpp:147
+
+Each step is replayed from a HIP graph (captured once per input set), the way
+a decode loop would issue it. Cold-cache protocol: inputs rotate over enough
+sets that the working set exceeds 512 MB (twice the 256 MB MALL), so every
+step reads from HBM. value = algorithmic bytes per step x steps / elapsed.
+
+Also reported: per-op launch durations (each op replayed alone over the same
+rotation), the dominant kernel's roofline, the 28-layer decode step's non-GEMM
+time per layer (config 1 shape), and the CPU restatement of the same step
+timed on this host (ggml-style thread split), as a baseline only.
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "synthesize.cpp_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+PEAK_GBS = 8000.0
+METRIC = "achieved HBM GB/s (% of peak) per fused op; µs/talker-layer non-GEMM step"
+SEED = 20260728
+COLD_BYTES = 512 << 20
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=400)
+    p.add_argument("--warmup", type=int, default=40)
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
+    p.add_argument("--no-cpu", action="store_true")
+    return p.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# the step
+# ---------------------------------------------------------------------------
+
+class PrefillStep:
+    T, HIDDEN, HEADS, KV_HEADS, HEAD_DIM, FFN = 512, 1024, 16, 8, 128, 3072
+    VOCAB, TEXT_HIDDEN = 151936, 2048
+    EPS, THETA = 1e-6, 1e6
+
+    def __init__(self, S, torch):
+        self.S, self.torch = S, torch
+        T, H, D = self.T, self.HIDDEN, self.HEAD_DIM
+        f32 = 4
+        self.op_bytes = {
+            "get_rows_bf16": T * (4 + self.TEXT_HIDDEN * 2 + self.TEXT_HIDDEN * f32),
+            "rms_norm_mul": 2 * T * H * f32 + H * 2,
+            "qk_norm_rope": 2 * (self.HEADS + self.KV_HEADS) * D * T * f32 + T * 4 + 2 * D * 2,
+            "add_rms_norm_mul": 4 * T * H * f32 + H * 2,
+            "swiglu": 3 * T * self.FFN * f32,
+            "add": 3 * T * H * f32,
+        }
+        self.step_bytes = sum(self.op_bytes.values())
+        per_set = self.step_bytes
+        self.nsets = max(2, -(-COLD_BYTES // per_set) + 1)
+        g = torch.Generator(device="cuda")
+        g.manual_seed(SEED)
+        dev = "cuda"
+        randn = lambda *shape: torch.randn(shape, generator=g, device=dev, dtype=torch.float32)
+        gain = lambda n: (1.0 + 0.1 * randn(n)).to(torch.bfloat16)
+        self.table = (0.02 * randn(self.VOCAB, self.TEXT_HIDDEN)).to(torch.bfloat16)
+        self.w_in, self.w_post = gain(H), gain(H)
+        self.wq, self.wk = gain(D), gain(D)
+        self.pos = torch.arange(T, dtype=torch.int32, device=dev)
+        self.sets = []
+        for _ in range(self.nsets):
+            s = dict(
+                ids=torch.randint(0, self.VOCAB, (T,), generator=g, device=dev, dtype=torch.int32),
+                x=randn(T, H), q=randn(T, self.HEADS, D), k=randn(T, self.KV_HEADS, D), proj=randn(T, H),
+                gate=randn(T, self.FFN), up=randn(T, self.FFN), mlp=randn(T, H),
+            )
+            s.update(emb=torch.empty(T, self.TEXT_HIDDEN, device=dev), normed=torch.empty(T, H, device=dev),
+                     qo=torch.empty_like(s["q"]), ko=torch.empty_like(s["k"]), resid=torch.empty(T, H, device=dev),
+                     mlp_in=torch.empty(T, H, device=dev), act=torch.empty(T, self.FFN, device=dev),
+                     out=torch.empty(T, H, device=dev))
+            self.sets.append(s)
+        torch.cuda.synchronize()
+
+    def ops(self, s):
+        S, c = self.S, self.sets[s]
+        return [
+            ("get_rows_bf16", lambda: S.get_rows(self.table, c["ids"], out=c["emb"])),
+            ("rms_norm_mul", lambda: S.rms_norm_mul(c["x"], self.w_in, self.EPS, out=c["normed"])),
+            ("qk_norm_rope", lambda: S.qk_norm_rope(c["q"], c["k"], self.wq, self.wk, self.EPS, self.pos,
+                                                    self.HEAD_DIM, self.THETA, q_out=c["qo"], k_out=c["ko"])),
+            ("add_rms_norm_mul", lambda: S.add_rms_norm_mul(c["x"], c["proj"], self.w_post, self.EPS,
+                                                            out=c["mlp_in"], sum_out=c["resid"])),
+            ("swiglu", lambda: S.swiglu(c["gate"], c["up"], out=c["act"])),
+            ("add", lambda: S.add(c["resid"], c["mlp"], out=c["out"])),
+        ]
+
+
+def capture(torch, fns):
+    """One HIP graph replaying `fns` in order (each already run eagerly once)."""
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for f in fns:
+                f()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    return graph
+
+
+def time_graphs(torch, graphs, reps):
+    """Replays graphs round-robin `reps` times between two events; returns ms."""
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(reps):
+        graphs[i % len(graphs)].replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end)
+
+
+# ---------------------------------------------------------------------------
+# decode step: 28 layers x (add+norm, qk-norm+rope, add+norm, swiglu) at T=1
+# ---------------------------------------------------------------------------
+
+def decode_layer_us(S, torch, layers=28, reps=50):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(SEED + 1)
+    randn = lambda *shape: torch.randn(shape, generator=g, device="cuda", dtype=torch.float32)
+    gain = lambda n: (1.0 + 0.1 * randn(n)).to(torch.bfloat16)
+    L = []
+    for _ in range(layers):
+        L.append(dict(a=randn(1, 1024), b=randn(1, 1024), w1=gain(1024), w2=gain(1024), wq=gain(128),
+                      wk=gain(128), q=randn(1, 16, 128), k=randn(1, 8, 128), proj=randn(1, 1024),
+                      gate=randn(1, 3072), up=randn(1, 3072), s1=torch.empty(1, 1024, device="cuda"),
+                      y1=torch.empty(1, 1024, device="cuda"), s2=torch.empty(1, 1024, device="cuda"),
+                      y2=torch.empty(1, 1024, device="cuda"), qo=torch.empty(1, 16, 128, device="cuda"),
+                      ko=torch.empty(1, 8, 128, device="cuda"), act=torch.empty(1, 3072, device="cuda")))
+    pos = torch.tensor([37], dtype=torch.int32, device="cuda")
+
+    def layer_fns(c):
+        return [lambda: S.add_rms_norm_mul(c["a"], c["b"], c["w1"], 1e-6, out=c["y1"], sum_out=c["s1"]),
+                lambda: S.qk_norm_rope(c["q"], c["k"], c["wq"], c["wk"], 1e-6, pos, 128, 1e6, q_out=c["qo"],
+                                       k_out=c["ko"]),
+                lambda: S.add_rms_norm_mul(c["s1"], c["proj"], c["w2"], 1e-6, out=c["y2"], sum_out=c["s2"]),
+                lambda: S.swiglu(c["gate"], c["up"], out=c["act"])]
+
+    fns = [f for c in L for f in layer_fns(c)]
+    for f in fns:
+        f()
+    graph = capture(torch, fns)
+    time_graphs(torch, [graph], 5)
+    ms = time_graphs(torch, [graph], reps)
+    return ms * 1e3 / (reps * layers)
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the same step as ggml node runs on the restatement
+# ---------------------------------------------------------------------------
+
+def cpu_baseline(step, torch, seconds):
+    import numpy as np
+    import ggml_ref as R
+
+    c = step.sets[0]
+    h = lambda t: t.detach().cpu().contiguous().numpy()
+    bits = lambda t: h(t.view(torch.int16)).view(np.uint16)
+    table, ids = bits(step.table), h(c["ids"])
+    x, q, k, proj, gate, up, mlp = (h(c[n]) for n in ("x", "q", "k", "proj", "gate", "up", "mlp"))
+    w_in, w_post, wq, wk = bits(step.w_in), bits(step.w_post), bits(step.wq), bits(step.wk)
+    pos = h(step.pos)
+    eps, theta = np.float32(step.EPS), np.float32(step.THETA)
+
+    def build(g):
+        g.get_rows(table, R.BF16, step.TEXT_HIDDEN, ids)
+        R.rms_norm_w(g, x, w_in, eps, R.BF16)
+        R.qk_norm_rope(g, q, k, wq, wk, eps, pos, step.HEAD_DIM, theta, R.BF16)
+        s, _ = R.add_rms_norm_w(g, x, proj, w_post, eps, R.BF16)
+        R.swiglu(g, gate, up)
+        g.add(s, mlp)
+
+    g = R.Graph()
+    build(g)
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    nth = max(1, min(cores, 16))
+    probe = g.time(nth, 1, 1)[0]
+    reps = int(max(3, min(400, 0.5 * seconds / max(probe, 1e-6))))
+    t_many = statistics.median(g.time(nth, 2, reps))
+    probe1 = g.time(1, 0, 1)[0]
+    reps1 = int(max(2, min(100, 0.5 * seconds / max(probe1, 1e-6))))
+    t_one = statistics.median(g.time(1, 1, reps1))
+    return {
+        "value": round(step.step_bytes / t_many / 1e9, 2), "unit": "GB/s", "cores": nth, "kind": "port",
+        "sample": "the same configs[1] prefill step (gather + norm + qk-norm/rope + add/norm + swiglu + add, "
+                  "%d ggml nodes) on the ggml-CPU restatement, median of %d reps at %d threads; "
+                  "1 thread: %.2f GB/s (median of %d)" % (len(g.nodes), reps, nth, step.step_bytes / t_one / 1e9,
+                                                          reps1),
+        "ms_per_step": round(t_many * 1e3, 3), "value_1thread": round(step.step_bytes / t_one / 1e9, 3),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build is single-GPU by design (the primitives are "
+              "row-independent; see DESIGN.md for how they shard). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import synth_hip as S
+
+    torch.cuda.set_device(0)
+    S.load()
+    step = PrefillStep(S, torch)
+
+    # eager run of every op of every set (loads the code objects before capture)
+    per_set_ops = [step.ops(s) for s in range(step.nsets)]
+    for ops in per_set_ops:
+        for _, f in ops:
+            f()
+    torch.cuda.synchronize()
+    ref_out = step.sets[0]["out"].clone()
+    ref_q = step.sets[0]["qo"].clone()
+
+    step_graphs = [capture(torch, [f for _, f in ops]) for ops in per_set_ops]
+    time_graphs(torch, step_graphs, args.warmup)
+    ms = time_graphs(torch, step_graphs, args.steps)
+    ms_per_step = ms / args.steps
+    value = step.step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # replays must reproduce the eager results bit for bit
+    assert torch.equal(step.sets[0]["out"], ref_out) and torch.equal(step.sets[0]["qo"], ref_q)
+
+    # per-op launch durations: each op alone, one graph over all sets
+    names = [n for n, _ in per_set_ops[0]]
+    per_op = {}
+    reps = max(args.steps // step.nsets, 4)
+    for i, name in enumerate(names):
+        graph = capture(torch, [per_set_ops[s][i][1] for s in range(step.nsets)])
+        time_graphs(torch, [graph], 2)
+        us = time_graphs(torch, [graph], reps) * 1e3 / (reps * step.nsets)
+        gbs = step.op_bytes[name] / (us * 1e-6) / 1e9
+        per_op[name] = {"us": round(us, 3), "bytes": step.op_bytes[name], "GB/s": round(gbs, 1),
+                        "frac": round(gbs / PEAK_GBS, 4)}
+    dom = max(per_op, key=lambda n: per_op[n]["us"])
+    roof = {"bound": "hbm", "kernel": dom, "achieved": per_op[dom]["GB/s"], "peak": PEAK_GBS, "unit": "GB/s",
+            "frac": per_op[dom]["frac"], "traffic": None}
+
+    layer_us = decode_layer_us(S, torch)
+
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "configs[1]: Qwen3-TTS-0.6B talker layer non-GEMM prefill step, 512 tokens x hidden "
+                               "1024, 16/8 heads x 128, SwiGLU 3072, BF16 gains + BF16 151936x2048 text-embedding "
+                               "gather of 512 ids; HIP-graph replay, %d rotating input sets (cold cache)" % step.nsets,
+                   "tokens": step.T, "hidden": step.HIDDEN, "bytes_per_step": step.step_bytes,
+                   "frac_of_peak": round(value / PEAK_GBS, 4)},
+        "ops": per_op,
+        "decode_layer_us": round(layer_us, 3),
+        "roofline": roof,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(step, torch, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

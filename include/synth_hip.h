@@ -1,0 +1,221 @@
+/*
+ * synth_hip.h -- C ABI of libsynth_hip, the MI355X (gfx950) kernels for the
+ * memory-bound non-GEMM primitives that synthesize.cpp's graph builders emit.
+ *
+ * Every entry point keeps the semantics of the ggml op (or the ggml op run)
+ * the reference graphs build today, so a ggml backend module can map nodes
+ * onto these calls without changing any graph. Citations name the reference
+ * call site (paths relative to the synthesize.cpp checkout) whose node or
+ * node run each entry point replaces.
+ *
+ * Conventions (all entry points):
+ *   - Tensors are described by shp_tensor, which mirrors ggml_tensor's
+ *     ne[4]/nb[4]/type/data: ne[0] is the fastest dimension, nb[] are byte
+ *     strides, type is a ggml type id. data is a DEVICE pointer owned by
+ *     the caller.
+ *   - Rows (the ne[0] extent) must be contiguous (nb[0] == element size);
+ *     rows may be strided in dims 1..3 exactly as ggml views allow.
+ *   - `stream` is a hipStream_t (NULL = the null stream). Every call is
+ *     asynchronous and ordered on that stream; nothing is allocated,
+ *     nothing synchronises, and no exception crosses this boundary.
+ *   - Return value is a shp_status_t. SHP_ERR_UNSUPPORTED means "valid for
+ *     ggml, not implemented here": a backend module should report
+ *     supports_op == false for such a node so it falls back, as
+ *     docs/backends.md:269-274 describes.
+ *   - Calls on distinct streams may run concurrently from different host
+ *     threads (no global mutable state in the launch path).
+ */
+#ifndef SYNTH_HIP_H
+#define SYNTH_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SHP_ABI_VERSION 1u
+
+typedef int32_t shp_status_t;
+#define SHP_OK              ((shp_status_t) 0)
+#define SHP_ERR_INVALID_ARG ((shp_status_t) 1)  /* where ggml would assert: null, shape/type mismatch */
+#define SHP_ERR_UNSUPPORTED ((shp_status_t) 2)  /* legal ggml, not handled here: fall back */
+#define SHP_ERR_BACKEND     ((shp_status_t) 17) /* HIP launch failure; same value as SYNTH_ERR_BACKEND */
+
+/* ggml_type values (upstream enum ggml_type). */
+#define SHP_TYPE_F32  0
+#define SHP_TYPE_F16  1
+#define SHP_TYPE_Q8_0 8
+#define SHP_TYPE_I32  26
+#define SHP_TYPE_BF16 30
+
+/* ggml rope mode bit (GGML_ROPE_TYPE_NEOX); src/arch/qwen3-tts/operations.cpp:16. */
+#define SHP_ROPE_TYPE_NEOX 2
+
+typedef struct shp_tensor {
+    int32_t type;     /* SHP_TYPE_* */
+    int32_t reserved; /* must be 0 */
+    int64_t ne[4];    /* extents, ne[0] fastest */
+    size_t  nb[4];    /* byte strides */
+    void *  data;     /* device pointer */
+} shp_tensor;
+
+typedef void * shp_stream_t; /* hipStream_t */
+
+uint32_t     shp_abi_version(void);
+const char * shp_status_string(shp_status_t status);
+
+/*
+ * ggml_get_rows(src, ids): dst[:, r, i11, i12] = to_f32(src[:, ids[r, i11, i12], i11, i12]).
+ * src F32/F16/BF16/Q8_0; ids I32 [n, ne11, ne12]; dst F32 [ne00, n, ne11, ne12].
+ * Conversions are exact (Q8_0: one product q*d per element), so results are
+ * bit-identical to ggml-CPU. An id outside [0, src.ne[1]) is never read:
+ * its output row is filled with quiet NaN (ggml-CPU aborts instead; callers
+ * pre-validate ids on the host, src/arch/qwen3-tts/talker-host.cpp:42).
+ * Replaces: src/arch/qwen3-tts/talker.cpp:44 and :86,
+ *           src/arch/qwen3-tts/code-predictor.cpp:31,
+ *           src/arch/qwen3-tts/model.cpp:1347,1449.
+ */
+shp_status_t shp_get_rows(const shp_tensor * src, const shp_tensor * ids, shp_tensor * dst, shp_stream_t stream);
+
+/*
+ * Multi-codebook gather->sum: the node run of sum_code_embeddings,
+ * src/arch/qwen3-tts/code-predictor.cpp:82-107 (one ggml_get_rows per group,
+ * then ggml_add in group order). tables[g] are [ne0, rows_g] of one common
+ * type (F32/F16/BF16/Q8_0); ids is I32 [frames, n_tables] contiguous, frames
+ * fastest (code-predictor.cpp:86-99); dst is F32 [ne0, frames].
+ * dst[:, f] = ((row_0 + row_1) + row_2) + ... in f32, in group order, so the
+ * result is bit-identical to the unfused node run. Out-of-range ids give a
+ * NaN row as in shp_get_rows. n_tables in [1, 64].
+ */
+shp_status_t shp_get_rows_sum(const shp_tensor * tables,
+                              int32_t            n_tables,
+                              const shp_tensor * ids,
+                              shp_tensor *       dst,
+                              shp_stream_t       stream);
+
+/*
+ * ggml_rms_norm(x, eps) followed by ggml_mul(., w): the rms_norm() helper,
+ * src/arch/qwen3-tts/operations.cpp:27-32 (with as_f32's BF16->F32 cast of
+ * the gain folded in, :20-25). Per row: sum of f32 squares accumulated in
+ * double, mean = (float)(sum/ne0), scale = 1.0f/sqrtf(mean+eps),
+ * y = (x*scale)*w. x, y F32 of one shape; w F32/BF16/F16 with exactly ne0
+ * elements (broadcast over rows), or NULL for a bare ggml_rms_norm.
+ * Also replaces talker.cpp:168, code-predictor.cpp:68 and the per-head
+ * QK-norm at operations.cpp:98-99 when called on the [head_dim, heads, T] view.
+ */
+shp_status_t shp_rms_norm_mul(const shp_tensor * x,
+                              const shp_tensor * w,
+                              float              eps,
+                              shp_tensor *       y,
+                              shp_stream_t       stream);
+
+/*
+ * ggml_add(a, b) followed by rms_norm()*w: the residual add feeding the
+ * post-attention norm (operations.cpp:143-145) and the layer-output add
+ * feeding the next layer's input norm (:147 -> :86). s = a + b (f32) is
+ * written to `sum` when it is non-NULL (the residual the graph carries on);
+ * y = rms_norm(s)*w. a, b, sum, y F32 of one shape.
+ */
+shp_status_t shp_add_rms_norm_mul(const shp_tensor * a,
+                                  const shp_tensor * b,
+                                  const shp_tensor * w,
+                                  float              eps,
+                                  shp_tensor *       sum,
+                                  shp_tensor *       y,
+                                  shp_stream_t       stream);
+
+/*
+ * ggml_rope_ext(x, pos, NULL, n_dims, mode, n_ctx_orig, freq_base,
+ * freq_scale, ext_factor, attn_factor, beta_fast, beta_slow) in NEOX mode,
+ * as at src/arch/qwen3-tts/operations.cpp:101-104. x, y F32
+ * [head_dim, heads, T, 1]; pos I32 [T]. theta for pair i at position p is
+ * the ggml-CPU recurrence theta_0 = p, theta_{i+1} = theta_i * powf(base,
+ * -2/n_dims) in f32 (replayed exactly), rotated by cos/sin of
+ * freq_scale*theta times attn_factor. Elements >= n_dims are copied.
+ * Supported: mode == SHP_ROPE_TYPE_NEOX, ext_factor == 0 (beta_* unused).
+ */
+shp_status_t shp_rope_ext(const shp_tensor * x,
+                          const shp_tensor * pos,
+                          int32_t            n_dims,
+                          int32_t            mode,
+                          float              freq_base,
+                          float              freq_scale,
+                          float              ext_factor,
+                          float              attn_factor,
+                          shp_tensor *       y,
+                          shp_stream_t       stream);
+
+/*
+ * Fused per-head QK-norm then NEOX rope for q and k in one launch: the node
+ * run rms_norm(q)*w_q -> rope_ext(q) and rms_norm(k)*w_k -> rope_ext(k) of
+ * src/arch/qwen3-tts/operations.cpp:98-104. q [head_dim, q_heads, T],
+ * k [head_dim, kv_heads, T] F32 (k may be NULL with k_out/wk NULL); wq, wk
+ * [head_dim] F32/BF16/F16; pos I32 [T]. Same arithmetic, in the same order,
+ * as the two unfused node runs (norm, mul, rope each rounded in f32).
+ */
+shp_status_t shp_qk_norm_rope(const shp_tensor * q,
+                              const shp_tensor * k,
+                              const shp_tensor * wq,
+                              const shp_tensor * wk,
+                              float              eps,
+                              const shp_tensor * pos,
+                              int32_t            n_dims,
+                              float              freq_base,
+                              float              freq_scale,
+                              shp_tensor *       q_out,
+                              shp_tensor *       k_out,
+                              shp_stream_t       stream);
+
+/*
+ * ggml_silu(g) followed by ggml_mul(., u): the SwiGLU of
+ * src/arch/qwen3-tts/operations.cpp:39-41 (== ggml_swiglu_split(g, u)).
+ * y = (g / (1 + expf(-g))) * u in f32. g, u, y F32 of one shape.
+ * u == NULL gives a bare ggml_silu (talker.cpp:47).
+ */
+shp_status_t shp_swiglu(const shp_tensor * g, const shp_tensor * u, shp_tensor * y, shp_stream_t stream);
+
+/*
+ * ggml_swiglu(a) / ggml_swiglu_swapped(a): single-tensor GLU. a is F32
+ * [2n, rows...]; gate is the first half of each row (second when swapped),
+ * up the other half; y is F32 [n, rows...].
+ */
+shp_status_t shp_glu_swiglu(const shp_tensor * a, int32_t swapped, shp_tensor * y, shp_stream_t stream);
+
+/*
+ * Snake: the five-node run of src/arch/kokoro/operations.cpp:137-147,
+ * t = x*alpha_c; s = sinf(t); q = s*s; r = q/alpha_c; y = x + r (each
+ * rounded in f32, in this order). x, y F32 [C, T] channels fastest
+ * (ne[0] == C); alpha F32 with exactly C elements ([1, C, 1] or [C]).
+ */
+shp_status_t shp_snake(const shp_tensor * x, const shp_tensor * alpha, shp_tensor * y, shp_stream_t stream);
+
+/*
+ * ggml_add(a, b) then ggml_leaky_relu(., slope, false): the residual carry
+ * of src/arch/vits/waveform-decoder.cpp:150-158 (layer l's closing add and
+ * layer l+1's opening leaky) and kokoro/generator.cpp:115,180.
+ * s = a + b; y = (s > 0 ? s : 0) + slope*(s < 0 ? s : 0) (so -0 -> +0,
+ * NaN -> 0), bit-identical to the two ggml nodes. b == NULL gives a bare
+ * leaky_relu of a (waveform-decoder.cpp:205,225). sum == NULL skips the
+ * residual output. All F32 of one shape.
+ */
+shp_status_t shp_add_leaky_relu(const shp_tensor * a,
+                                const shp_tensor * b,
+                                float              slope,
+                                shp_tensor *       sum,
+                                shp_tensor *       y,
+                                shp_stream_t       stream);
+
+/*
+ * ggml_add(a, b) with b the same shape as a or one row broadcast over
+ * rows (ggml_can_repeat_rows). The plain residual add at
+ * src/arch/qwen3-tts/operations.cpp:143,147 when it is not fused into a norm.
+ */
+shp_status_t shp_add(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SYNTH_HIP_H */

@@ -1,0 +1,595 @@
+/*
+ * ggml_cpu_ref.c -- TEST INFRASTRUCTURE ONLY (see ggml_cpu_ref.h).
+ *
+ * A restatement of ggml-CPU op arithmetic for the nodes synthesize.cpp's graph
+ * builders emit on the fused-primitive path. The upstream ggml-cpu sources
+ * (ops.cpp, vec.h, ggml-quants.c) are not present in the reference checkout
+ * (its ggml/ submodule is empty), so each op states the published algorithm
+ * and cites the reference site that builds the node. Built with
+ * -ffp-contract=off so that every f32 operation is rounded on its own, which
+ * is the order the formulas below are written in.
+ *
+ * Last-ulp points this restatement fixes by choice (ggml's own build may
+ * differ there, and the tests absorb that in tolerance):
+ *   - silu uses libm expf for every element (ggml vectorises it with its own
+ *     SIMD expf, within ~1 ulp of libm);
+ *   - rope is computed without fused multiply-add.
+ */
+#define _GNU_SOURCE
+#include "ggml_cpu_ref.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <sched.h>
+#include <stdatomic.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+
+/* ------------------------------------------------------------------ */
+/* conversions                                                         */
+/* ------------------------------------------------------------------ */
+
+float orc_fp16_to_fp32(uint16_t h) {
+    const uint32_t sign = (uint32_t) (h & 0x8000u) << 16;
+    const uint32_t e    = (h >> 10) & 0x1fu;
+    const uint32_t m    = h & 0x3ffu;
+    uint32_t       bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {
+            /* subnormal half: m * 2^-24, exact in f32 */
+            const float v = (float) m * 5.9604644775390625e-8f;
+            memcpy(&bits, &v, 4);
+            bits |= sign;
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7f800000u | (m << 13);
+    } else {
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float out;
+    memcpy(&out, &bits, 4);
+    return out;
+}
+
+float orc_bf16_to_fp32(uint16_t h) {
+    const uint32_t bits = (uint32_t) h << 16;
+    float          out;
+    memcpy(&out, &bits, 4);
+    return out;
+}
+
+uint16_t orc_fp32_to_fp16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax   = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) {
+        return (uint16_t) (sign | 0x7e00u | ((ax >> 13) & 0x3ffu));
+    }
+    if (ax >= 0x477ff000u) { /* >= 65520 rounds to infinity */
+        return (uint16_t) (sign | 0x7c00u);
+    }
+    if (ax < 0x38800000u) { /* below the smallest normal half, 2^-14 */
+        float v;
+        memcpy(&v, &ax, 4);
+        const uint32_t m = (uint32_t) rintf(v * 16777216.0f); /* v / 2^-24, round half even */
+        return (uint16_t) (sign | m);
+    }
+    const uint32_t e    = (ax >> 23) - 112u;
+    const uint32_t mant = ax & 0x7fffffu;
+    uint32_t       h    = (e << 10) | (mant >> 13);
+    const uint32_t rem  = mant & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) {
+        h += 1u;
+    }
+    return (uint16_t) (sign | h);
+}
+
+/* ggml's fp32 -> bf16: round half to even, NaN forced quiet. */
+uint16_t orc_fp32_to_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+        return (uint16_t) ((u >> 16) | 64u);
+    }
+    return (uint16_t) ((u + (0x7fffu + ((u >> 16) & 1u))) >> 16);
+}
+
+static float to_f32(int type, const void * row, int64_t i) {
+    switch (type) {
+        case ORC_F32:
+            return ((const float *) row)[i];
+        case ORC_F16:
+            return orc_fp16_to_fp32(((const uint16_t *) row)[i]);
+        case ORC_BF16:
+            return orc_bf16_to_fp32(((const uint16_t *) row)[i]);
+        default:
+            return NAN;
+    }
+}
+
+static size_t row_bytes(int type, int64_t ne0) {
+    switch (type) {
+        case ORC_F32:
+            return (size_t) ne0 * 4u;
+        case ORC_F16:
+        case ORC_BF16:
+            return (size_t) ne0 * 2u;
+        case ORC_Q8_0:
+            return (size_t) (ne0 / 32) * 34u;
+        default:
+            return 0;
+    }
+}
+
+/* dequantize_row_q8_0: y[32b + j] = qs[j] * fp16(d), one rounding (exact). */
+static void dequantize_row_q8_0(const uint8_t * x, float * y, int64_t k) {
+    const int64_t nb = k / 32;
+    for (int64_t b = 0; b < nb; ++b) {
+        const uint8_t * blk = x + b * 34;
+        uint16_t        dh;
+        memcpy(&dh, blk, 2);
+        const float    d  = orc_fp16_to_fp32(dh);
+        const int8_t * qs = (const int8_t *) (blk + 2);
+        for (int j = 0; j < 32; ++j) {
+            y[b * 32 + j] = (float) qs[j] * d;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* ops: each runs thread ith's share of rows, as ggml-CPU splits them  */
+/* ------------------------------------------------------------------ */
+
+static atomic_int g_node_error;
+
+static void chunk(int64_t nr, int ith, int nth, int64_t * r0, int64_t * r1) {
+    const int64_t dr = (nr + nth - 1) / nth;
+    *r0              = dr * ith;
+    *r1              = *r0 + dr < nr ? *r0 + dr : nr;
+}
+
+/* ggml_add / ggml_mul / ggml_div, src1 repeated over rows or along a row.
+ * Sites: qwen3-tts/operations.cpp:31,41,143,147; kokoro/operations.cpp:143-146;
+ * code-predictor.cpp:104; vits/waveform-decoder.cpp:157. */
+static void op_binary(const orc_node * n, int ith, int nth) {
+    int64_t r0, r1;
+    chunk(n->nrows, ith, nth, &r0, &r1);
+    const int64_t ne0 = n->ne0;
+    for (int64_t r = r0; r < r1; ++r) {
+        const float * a = (const float *) n->src0 + r * ne0;
+        const float * b;
+        int           scalar = 0;
+        const int64_t brow   = n->src1_rows == 1 ? 0 : r;
+        if (n->src1_ne0 == 1) {
+            b      = (const float *) n->src1 + brow;
+            scalar = 1;
+        } else {
+            b = (const float *) n->src1 + brow * ne0;
+        }
+        float * d = (float *) n->dst + r * ne0;
+        for (int64_t i = 0; i < ne0; ++i) {
+            const float bv = scalar ? b[0] : b[i];
+            switch (n->op) {
+                case ORC_OP_ADD:
+                    d[i] = a[i] + bv;
+                    break;
+                case ORC_OP_MUL:
+                    d[i] = a[i] * bv;
+                    break;
+                default:
+                    d[i] = a[i] / bv;
+                    break;
+            }
+        }
+    }
+}
+
+/* ggml_rms_norm: rows interleaved over threads; f32 squares summed in double,
+ * mean rounded to f32, scale = 1/sqrtf(mean + eps), y = x*scale.
+ * Sites: qwen3-tts/operations.cpp:31 (via rms_norm :27-32), :86, :98-99, :145. */
+static void op_rms_norm(const orc_node * n, int ith, int nth) {
+    const int64_t ne0 = n->ne0;
+    const float   eps = n->f[0];
+    for (int64_t r = ith; r < n->nrows; r += nth) {
+        const float * x   = (const float *) n->src0 + r * ne0;
+        float *       y   = (float *) n->dst + r * ne0;
+        double        sum = 0.0;
+        for (int64_t i = 0; i < ne0; ++i) {
+            sum += (double) (x[i] * x[i]);
+        }
+        const float mean = (float) (sum / (double) ne0);
+        if (y != x) {
+            memmove(y, x, (size_t) ne0 * sizeof(float));
+        }
+        const float scale = 1.0f / sqrtf(mean + eps);
+        for (int64_t i = 0; i < ne0; ++i) {
+            y[i] = y[i] * scale;
+        }
+    }
+}
+
+/* ggml_rope_ext, NEOX mode, ext_factor 0: per position a cos/sin cache built
+ * from theta_0 = p, theta_{i+1} = theta_i * powf(base, -2/n_dims) (f32), each
+ * entry cosf/sinf(freq_scale*theta) * attn_factor; pair (ic, ic + n_dims/2)
+ * rotated; elements >= n_dims copied. Site: qwen3-tts/operations.cpp:101-104.
+ * i[1] = 1 evaluates cos/sin in double and rounds once (correctly rounded
+ * almost always) instead of libm cosf/sinf; everything else is unchanged. */
+static void op_rope_neox(const orc_node * n, int ith, int nth) {
+    const int64_t   ne0         = n->ne0;
+    const int64_t   ne1         = n->ne1;
+    const int       n_dims      = n->i[0];
+    const int       cs_mode     = n->i[1];
+    const float     freq_base   = n->f[0];
+    const float     freq_scale  = n->f[1];
+    const float     attn_factor = n->f[2];
+    const float     theta_scale = powf(freq_base, -2.0f / (float) n_dims);
+    const int32_t * pos         = (const int32_t *) n->src1;
+    const int64_t   half        = n_dims / 2;
+
+    int64_t r0, r1;
+    chunk(n->nrows, ith, nth, &r0, &r1);
+    if (r0 >= r1) {
+        return;
+    }
+    float * cache = (float *) malloc((size_t) (ne0 + 2) * sizeof(float));
+    if (cache == NULL) {
+        atomic_store(&g_node_error, -3);
+        return;
+    }
+    const int64_t p_first = r0 / ne1;
+    const int64_t p_last  = (r1 - 1) / ne1;
+    for (int64_t pi = p_first; pi <= p_last; ++pi) {
+        float theta = (float) pos[pi];
+        for (int64_t i0 = 0; i0 < ne0; i0 += 2) {
+            const float th = freq_scale * theta;
+            if (cs_mode == 0) {
+                cache[i0 + 0] = cosf(th) * attn_factor;
+                cache[i0 + 1] = sinf(th) * attn_factor;
+            } else {
+                cache[i0 + 0] = (float) cos((double) th) * attn_factor;
+                cache[i0 + 1] = (float) sin((double) th) * attn_factor;
+            }
+            theta = theta * theta_scale;
+        }
+        for (int64_t h = 0; h < ne1; ++h) {
+            const int64_t r = pi * ne1 + h;
+            if (r < r0 || r >= r1) {
+                continue;
+            }
+            const float * src = (const float *) n->src0 + r * ne0;
+            float *       dst = (float *) n->dst + r * ne0;
+            for (int64_t i0 = 0; i0 < n_dims; i0 += 2) {
+                const int64_t ic = i0 / 2;
+                const float   c  = cache[i0 + 0];
+                const float   s  = cache[i0 + 1];
+                const float   x0 = src[ic];
+                const float   x1 = src[ic + half];
+                dst[ic]          = x0 * c - x1 * s;
+                dst[ic + half]   = x0 * s + x1 * c;
+            }
+            for (int64_t i0 = n_dims; i0 < ne0; ++i0) {
+                dst[i0] = src[i0];
+            }
+        }
+    }
+    free(cache);
+}
+
+static inline float silu_f32(float x) {
+    return x / (1.0f + expf(-x));
+}
+
+/* Unary ops, rows chunked over threads. silu: qwen3-tts/operations.cpp:39,
+ * talker.cpp:47; sin: kokoro/operations.cpp:144; sqr/exp: qwen3-tts/codec.cpp:
+ * 192-195; leaky: vits/waveform-decoder.cpp:152,155,205,225; scale_bias:
+ * qwen3-tts/codec.cpp:197, omnivoice/codec.cpp:66. */
+static void op_unary(const orc_node * n, int ith, int nth) {
+    int64_t r0, r1;
+    chunk(n->nrows, ith, nth, &r0, &r1);
+    const int64_t ne0 = n->ne0;
+    for (int64_t r = r0; r < r1; ++r) {
+        const float * x = (const float *) n->src0 + r * ne0;
+        float *       y = (float *) n->dst + r * ne0;
+        switch (n->op) {
+            case ORC_OP_SILU:
+                for (int64_t i = 0; i < ne0; ++i) {
+                    y[i] = silu_f32(x[i]);
+                }
+                break;
+            case ORC_OP_SIN:
+                for (int64_t i = 0; i < ne0; ++i) {
+                    y[i] = sinf(x[i]);
+                }
+                break;
+            case ORC_OP_SQR:
+                for (int64_t i = 0; i < ne0; ++i) {
+                    y[i] = x[i] * x[i];
+                }
+                break;
+            case ORC_OP_EXP:
+                for (int64_t i = 0; i < ne0; ++i) {
+                    y[i] = expf(x[i]);
+                }
+                break;
+            case ORC_OP_LEAKY_RELU: {
+                const float ns = n->f[0];
+                for (int64_t i = 0; i < ne0; ++i) {
+                    y[i] = ((x[i] > 0.0f) ? x[i] : 0.0f) + ns * ((x[i] < 0.0f) ? x[i] : 0.0f);
+                }
+                break;
+            }
+            case ORC_OP_SCALE_BIAS: {
+                const float s = n->f[0];
+                const float b = n->f[1];
+                for (int64_t i = 0; i < ne0; ++i) {
+                    y[i] = x[i] * s + b;
+                }
+                break;
+            }
+            default:
+                break;
+        }
+    }
+}
+
+/* ggml_get_rows: ids chunked over threads; each row converted to f32.
+ * Sites: qwen3-tts/talker.cpp:44,86; code-predictor.cpp:31; model.cpp:1347,1449. */
+static void op_get_rows(const orc_node * n, int ith, int nth) {
+    int64_t r0, r1;
+    chunk(n->nrows, ith, nth, &r0, &r1);
+    const int64_t   ne0 = n->ne0;
+    const size_t    rb  = row_bytes(n->type0, ne0);
+    const int32_t * ids = (const int32_t *) n->src1;
+    for (int64_t r = r0; r < r1; ++r) {
+        const int32_t id = ids[r];
+        float *       y  = (float *) n->dst + r * ne0;
+        if (id < 0 || id >= n->src1_rows) {
+            atomic_store(&g_node_error, -2); /* ggml-CPU asserts here */
+            continue;
+        }
+        const uint8_t * row = (const uint8_t *) n->src0 + (size_t) id * rb;
+        if (n->type0 == ORC_Q8_0) {
+            dequantize_row_q8_0(row, y, ne0);
+        } else {
+            for (int64_t i = 0; i < ne0; ++i) {
+                y[i] = to_f32(n->type0, row, i);
+            }
+        }
+    }
+}
+
+/* ggml_cast to F32 (as_f32, qwen3-tts/operations.cpp:20-25). */
+static void op_cast(const orc_node * n, int ith, int nth) {
+    int64_t r0, r1;
+    chunk(n->nrows, ith, nth, &r0, &r1);
+    const int64_t ne0 = n->ne0;
+    const size_t  rb  = row_bytes(n->type0, ne0);
+    for (int64_t r = r0; r < r1; ++r) {
+        const uint8_t * row = (const uint8_t *) n->src0 + (size_t) r * rb;
+        float *         y   = (float *) n->dst + r * ne0;
+        for (int64_t i = 0; i < ne0; ++i) {
+            y[i] = to_f32(n->type0, row, i);
+        }
+    }
+}
+
+/* ggml_swiglu (single tensor): gate = first half of each row (second when
+ * swapped), y = silu(gate) * other half. */
+static void op_glu_swiglu(const orc_node * n, int ith, int nth) {
+    int64_t r0, r1;
+    chunk(n->nrows, ith, nth, &r0, &r1);
+    const int64_t nc      = n->ne0;
+    const int     swapped = n->i[0];
+    for (int64_t r = r0; r < r1; ++r) {
+        const float * row  = (const float *) n->src0 + r * 2 * nc;
+        const float * gate = row + (swapped ? nc : 0);
+        const float * up   = row + (swapped ? 0 : nc);
+        float *       y    = (float *) n->dst + r * nc;
+        for (int64_t i = 0; i < nc; ++i) {
+            y[i] = silu_f32(gate[i]) * up[i];
+        }
+    }
+}
+
+static void run_node(const orc_node * n, int ith, int nth) {
+    switch (n->op) {
+        case ORC_OP_ADD:
+        case ORC_OP_MUL:
+        case ORC_OP_DIV:
+            op_binary(n, ith, nth);
+            break;
+        case ORC_OP_RMS_NORM:
+            op_rms_norm(n, ith, nth);
+            break;
+        case ORC_OP_ROPE_NEOX:
+            op_rope_neox(n, ith, nth);
+            break;
+        case ORC_OP_SILU:
+        case ORC_OP_SIN:
+        case ORC_OP_SQR:
+        case ORC_OP_EXP:
+        case ORC_OP_LEAKY_RELU:
+        case ORC_OP_SCALE_BIAS:
+            op_unary(n, ith, nth);
+            break;
+        case ORC_OP_GET_ROWS:
+            op_get_rows(n, ith, nth);
+            break;
+        case ORC_OP_CAST_F32:
+            op_cast(n, ith, nth);
+            break;
+        case ORC_OP_GLU_SWIGLU:
+            op_glu_swiglu(n, ith, nth);
+            break;
+        default:
+            atomic_store(&g_node_error, -1);
+            break;
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* persistent thread pool with a spin barrier between nodes (as ggml)  */
+/* ------------------------------------------------------------------ */
+
+#define ORC_MAX_THREADS 512
+
+static inline void cpu_relax(void) {
+#if defined(__x86_64__) || defined(__i386__)
+    __builtin_ia32_pause();
+#else
+    sched_yield();
+#endif
+}
+
+static struct {
+    int              n;
+    pthread_t        th[ORC_MAX_THREADS];
+    atomic_int       gen;
+    atomic_int       stop;
+    atomic_int       bar_count;
+    atomic_int       bar_sense;
+    const orc_node * nodes;
+    int              n_nodes;
+} g_pool;
+
+static pthread_mutex_t g_pool_lock = PTHREAD_MUTEX_INITIALIZER;
+static _Thread_local int t_sense   = 0;
+
+static void barrier(int nth) {
+    const int s = !t_sense;
+    t_sense     = s;
+    if (atomic_fetch_add(&g_pool.bar_count, 1) == nth - 1) {
+        atomic_store(&g_pool.bar_count, 0);
+        atomic_store(&g_pool.bar_sense, s);
+    } else {
+        while (atomic_load(&g_pool.bar_sense) != s) {
+            cpu_relax();
+        }
+    }
+}
+
+static void run_job(int ith, int nth) {
+    const orc_node * nodes   = g_pool.nodes;
+    const int        n_nodes = g_pool.n_nodes;
+    for (int k = 0; k < n_nodes; ++k) {
+        run_node(&nodes[k], ith, nth);
+        barrier(nth);
+    }
+}
+
+static void * worker_main(void * arg) {
+    const int ith  = (int) (intptr_t) arg;
+    int       seen = 0;
+    t_sense        = atomic_load(&g_pool.bar_sense);
+    for (;;) {
+        long spins = 0;
+        int  g;
+        while ((g = atomic_load(&g_pool.gen)) == seen) {
+            if (++spins < (1L << 18)) {
+                cpu_relax();
+            } else {
+                struct timespec ts = { 0, 50000 };
+                nanosleep(&ts, NULL);
+            }
+        }
+        seen = g;
+        if (atomic_load(&g_pool.stop)) {
+            break;
+        }
+        run_job(ith, g_pool.n);
+    }
+    return NULL;
+}
+
+static void pool_shutdown(void) {
+    if (g_pool.n > 1) {
+        atomic_store(&g_pool.stop, 1);
+        atomic_fetch_add(&g_pool.gen, 1);
+        for (int i = 1; i < g_pool.n; ++i) {
+            pthread_join(g_pool.th[i], NULL);
+        }
+    }
+    g_pool.n = 0;
+    atomic_store(&g_pool.stop, 0);
+}
+
+static int pool_ensure(int n) {
+    if (g_pool.n == n) {
+        return 0;
+    }
+    pool_shutdown();
+    atomic_store(&g_pool.bar_count, 0);
+    t_sense = atomic_load(&g_pool.bar_sense);
+    atomic_store(&g_pool.gen, 0);
+    g_pool.n = n;
+    for (int i = 1; i < n; ++i) {
+        if (pthread_create(&g_pool.th[i], NULL, worker_main, (void *) (intptr_t) i) != 0) {
+            g_pool.n = i;
+            pool_shutdown();
+            return -4;
+        }
+    }
+    return 0;
+}
+
+static int compute_locked(const orc_node * nodes, int32_t n_nodes, int32_t n_threads) {
+    atomic_store(&g_node_error, 0);
+    if (n_threads <= 1) {
+        for (int k = 0; k < n_nodes; ++k) {
+            run_node(&nodes[k], 0, 1);
+        }
+        return atomic_load(&g_node_error);
+    }
+    const int rc = pool_ensure(n_threads);
+    if (rc != 0) {
+        return rc;
+    }
+    g_pool.nodes   = nodes;
+    g_pool.n_nodes = n_nodes;
+    atomic_fetch_add(&g_pool.gen, 1);
+    run_job(0, n_threads);
+    return atomic_load(&g_node_error);
+}
+
+int orc_compute(const orc_node * nodes, int32_t n_nodes, int32_t n_threads) {
+    if (nodes == NULL || n_nodes < 0 || n_threads < 1 || n_threads > ORC_MAX_THREADS) {
+        return -1;
+    }
+    pthread_mutex_lock(&g_pool_lock);
+    const int rc = compute_locked(nodes, n_nodes, n_threads);
+    pthread_mutex_unlock(&g_pool_lock);
+    return rc;
+}
+
+double orc_now(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double) ts.tv_sec + 1e-9 * (double) ts.tv_nsec;
+}
+
+int orc_time_nodes(const orc_node * nodes, int32_t n_nodes, int32_t n_threads, int32_t warmup, int32_t reps,
+                   double * times) {
+    if (nodes == NULL || times == NULL || reps < 1 || n_threads < 1 || n_threads > ORC_MAX_THREADS) {
+        return -1;
+    }
+    pthread_mutex_lock(&g_pool_lock);
+    int rc = 0;
+    for (int i = 0; i < warmup && rc == 0; ++i) {
+        rc = compute_locked(nodes, n_nodes, n_threads);
+    }
+    for (int i = 0; i < reps && rc == 0; ++i) {
+        const double t0 = orc_now();
+        rc              = compute_locked(nodes, n_nodes, n_threads);
+        times[i]        = orc_now() - t0;
+    }
+    pthread_mutex_unlock(&g_pool_lock);
+    return rc;
+}
+
+__attribute__((destructor)) static void orc_fini(void) {
+    pool_shutdown();
+}

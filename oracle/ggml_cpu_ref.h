@@ -1,0 +1,103 @@
+/*
+ * ggml_cpu_ref.h -- TEST INFRASTRUCTURE ONLY. A CPU restatement of the
+ * ggml-CPU arithmetic for the ops synthesize.cpp's graph builders emit on the
+ * fused-primitive path. Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it, and only as the checker or as the timed CPU
+ * baseline; the product (libsynth_hip) never links or calls it.
+ *
+ * The upstream ggml sources are not available (the reference's ggml/ is an
+ * uninitialised submodule), so each op restates the published ggml-CPU
+ * algorithm and cites the reference call site that emits the node. The
+ * restatement is pinned against the reference's own golden vectors and
+ * against closed forms in tests/.
+ *
+ * Execution mirrors ggml's CPU graph compute: a persistent pool of n_threads
+ * threads runs every node, thread ith taking its ggml share of rows, with a
+ * barrier between nodes.
+ */
+#ifndef GGML_CPU_REF_H
+#define GGML_CPU_REF_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum orc_type { ORC_F32 = 0, ORC_F16 = 1, ORC_Q8_0 = 8, ORC_I32 = 26, ORC_BF16 = 30 };
+
+enum orc_op {
+    ORC_OP_ADD = 1,      /* dst = src0 + src1                       ggml_add            */
+    ORC_OP_MUL,          /* dst = src0 * src1                       ggml_mul            */
+    ORC_OP_DIV,          /* dst = src0 / src1                       ggml_div            */
+    ORC_OP_RMS_NORM,     /* dst = x * 1/sqrt(mean(x^2)+eps)         ggml_rms_norm       */
+    ORC_OP_ROPE_NEOX,    /* NEOX rotary                             ggml_rope_ext       */
+    ORC_OP_SILU,         /* x/(1+exp(-x))                           ggml_silu           */
+    ORC_OP_SIN,          /* sinf(x)                                 ggml_sin            */
+    ORC_OP_SQR,          /* x*x                                     ggml_sqr            */
+    ORC_OP_EXP,          /* expf(x)                                 ggml_exp            */
+    ORC_OP_LEAKY_RELU,   /* (x>0?x:0) + slope*(x<0?x:0)             ggml_leaky_relu     */
+    ORC_OP_SCALE_BIAS,   /* x*s + b                                 ggml_scale_bias     */
+    ORC_OP_GET_ROWS,     /* dst[:, r] = to_f32(src0[:, ids[r]])     ggml_get_rows       */
+    ORC_OP_CAST_F32,     /* BF16/F16/F32 -> F32                     ggml_cast           */
+    ORC_OP_GLU_SWIGLU,   /* single-tensor swiglu                    ggml_swiglu         */
+};
+
+/*
+ * One graph node. All tensors are contiguous row-major: `nrows` rows of `ne0`
+ * elements. Binary ops take src1 either with `nrows` rows or with one row that
+ * is broadcast over every row (src1_rows == 1), which is ggml's
+ * ggml_can_repeat_rows case, or with one element per row (src1_ne0 == 1,
+ * broadcast along the row).
+ *
+ *   ROPE_NEOX : src0 [ne0=head_dim, ne1=heads, nrows/ne1 positions], src1 = I32
+ *               positions; i[0] = n_dims; f[0] = freq_base, f[1] = freq_scale,
+ *               f[2] = attn_factor; i[1] = 0: cos/sin from libm cosf/sinf (as
+ *               ggml-CPU), 1: from double cos/sin rounded once to f32.
+ *   RMS_NORM  : f[0] = eps.
+ *   LEAKY_RELU: f[0] = negative slope.
+ *   SCALE_BIAS: f[0] = scale, f[1] = bias.
+ *   GET_ROWS  : src0 is a table of `src1_rows` rows of ne0 elements of type
+ *               `type0`; src1 = I32 ids (nrows of them); dst F32.
+ *   CAST_F32  : src0 of type `type0`.
+ *   GLU_SWIGLU: src0 rows of 2*ne0 elements; i[0] = swapped.
+ */
+typedef struct orc_node {
+    int32_t      op;
+    int32_t      type0;
+    int64_t      ne0;
+    int64_t      nrows;
+    int64_t      ne1;
+    int64_t      src1_rows;
+    int64_t      src1_ne0;
+    const void * src0;
+    const void * src1;
+    void *       dst;
+    float        f[4];
+    int32_t      i[4];
+} orc_node;
+
+/* Runs the nodes in order on n_threads threads (1 = inline). Returns 0, or a
+ * negative value for an unknown op / bad argument. */
+int orc_compute(const orc_node * nodes, int32_t n_nodes, int32_t n_threads);
+
+/* Scalar conversions (exact), and the ggml data-generation roundings. */
+float    orc_fp16_to_fp32(uint16_t h);
+float    orc_bf16_to_fp32(uint16_t h);
+uint16_t orc_fp32_to_fp16(float f);
+uint16_t orc_fp32_to_bf16(float f);
+
+/* Wall-clock helper for the CPU baseline (CLOCK_MONOTONIC, seconds). */
+double orc_now(void);
+
+/* Times `reps` repetitions of the node list on n_threads threads after
+ * `warmup` untimed ones; writes each repetition's seconds into times[]. */
+int orc_time_nodes(const orc_node * nodes, int32_t n_nodes, int32_t n_threads, int32_t warmup, int32_t reps,
+                   double * times);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

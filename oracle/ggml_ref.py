@@ -1,0 +1,396 @@
+"""TEST INFRASTRUCTURE ONLY: Python face of the ggml-CPU restatement.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this module, and only as the checker or the timed CPU baseline. The product
+(libsynth_hip and its binding) never imports it.
+
+The arithmetic of every hot-path op lives in ggml_cpu_ref.c (built into
+libggml_cpu_ref.so by oracle/Makefile). This module builds node lists for it in
+the order the reference graph builders emit them, and adds what the tiny golden
+configurations also need around the hot ops (mul_mat, soft_max_ext, the KV
+cache), written with numpy.
+
+Layout: a ggml tensor [ne0, ne1, ne2] is a C-contiguous numpy array of shape
+(ne2, ne1, ne0); e.g. a Qwen3 activation [hidden, T] is np.float32 (T, hidden).
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libggml_cpu_ref.so")
+
+F32, F16, Q8_0, I32, BF16 = 0, 1, 8, 26, 30
+
+(OP_ADD, OP_MUL, OP_DIV, OP_RMS_NORM, OP_ROPE_NEOX, OP_SILU, OP_SIN, OP_SQR, OP_EXP, OP_LEAKY_RELU, OP_SCALE_BIAS,
+ OP_GET_ROWS, OP_CAST_F32, OP_GLU_SWIGLU) = range(1, 15)
+
+
+class OrcNode(ctypes.Structure):
+    _fields_ = [
+        ("op", ctypes.c_int32), ("type0", ctypes.c_int32),
+        ("ne0", ctypes.c_int64), ("nrows", ctypes.c_int64), ("ne1", ctypes.c_int64),
+        ("src1_rows", ctypes.c_int64), ("src1_ne0", ctypes.c_int64),
+        ("src0", ctypes.c_void_p), ("src1", ctypes.c_void_p), ("dst", ctypes.c_void_p),
+        ("f", ctypes.c_float * 4), ("i", ctypes.c_int32 * 4),
+    ]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError("oracle not built: run `make -C oracle` (or __graft_entry__.build())")
+        L = ctypes.CDLL(LIB_PATH)
+        L.orc_compute.argtypes = [ctypes.POINTER(OrcNode), ctypes.c_int32, ctypes.c_int32]
+        L.orc_compute.restype = ctypes.c_int
+        L.orc_time_nodes.argtypes = [ctypes.POINTER(OrcNode), ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                     ctypes.c_int32, ctypes.POINTER(ctypes.c_double)]
+        L.orc_time_nodes.restype = ctypes.c_int
+        for name in ("orc_fp16_to_fp32", "orc_bf16_to_fp32"):
+            getattr(L, name).argtypes = [ctypes.c_uint16]
+            getattr(L, name).restype = ctypes.c_float
+        for name in ("orc_fp32_to_fp16", "orc_fp32_to_bf16"):
+            getattr(L, name).argtypes = [ctypes.c_float]
+            getattr(L, name).restype = ctypes.c_uint16
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def _rows(a):
+    return int(a.size // a.shape[-1]) if a.ndim else 1
+
+
+class Graph:
+    """An ordered node list over numpy buffers, run by the C restatement.
+
+    Each method appends one ggml node, allocates its output and returns it; the
+    values are only valid after compute(). Inputs must stay alive (the graph
+    keeps references)."""
+
+    def __init__(self):
+        self.nodes = []
+        self.keep = []
+
+    def _node(self, op, dst, src0, src1=None, **kw):
+        n = OrcNode()
+        n.op = op
+        n.type0 = kw.get("type0", F32)
+        n.ne0 = kw.get("ne0", dst.shape[-1])
+        n.nrows = kw.get("nrows", _rows(dst))
+        n.ne1 = kw.get("ne1", 0)
+        n.src1_rows = kw.get("src1_rows", 0)
+        n.src1_ne0 = kw.get("src1_ne0", 0)
+        n.src0 = _ptr(src0)
+        n.src1 = _ptr(src1) if src1 is not None else None
+        n.dst = _ptr(dst)
+        for k, v in enumerate(kw.get("f", ())):
+            n.f[k] = v
+        for k, v in enumerate(kw.get("i", ())):
+            n.i[k] = v
+        self.nodes.append(n)
+        self.keep += [dst, src0] + ([src1] if src1 is not None else [])
+        return dst
+
+    @staticmethod
+    def _f32(a):
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        return a
+
+    def _binary(self, op, a, b):
+        a = self._f32(a)
+        b = self._f32(b)
+        dst = np.empty_like(a)
+        ne0 = a.shape[-1]
+        if b.shape == a.shape:
+            src1_rows, src1_ne0 = _rows(a), ne0
+        elif b.size == ne0:
+            src1_rows, src1_ne0 = 1, ne0          # one row repeated over rows
+        elif b.size == _rows(a) and b.shape[-1] == 1:
+            src1_rows, src1_ne0 = _rows(a), 1     # one value per row
+        else:
+            raise ValueError("unsupported broadcast %s vs %s" % (a.shape, b.shape))
+        return self._node(op, dst, a, b, src1_rows=src1_rows, src1_ne0=src1_ne0)
+
+    def add(self, a, b):
+        return self._binary(OP_ADD, a, b)
+
+    def mul(self, a, b):
+        return self._binary(OP_MUL, a, b)
+
+    def div(self, a, b):
+        return self._binary(OP_DIV, a, b)
+
+    def _unary(self, op, x, f=()):
+        x = self._f32(x)
+        return self._node(op, np.empty_like(x), x, f=f)
+
+    def rms_norm(self, x, eps):
+        return self._unary(OP_RMS_NORM, x, f=(eps,))
+
+    def silu(self, x):
+        return self._unary(OP_SILU, x)
+
+    def sin(self, x):
+        return self._unary(OP_SIN, x)
+
+    def sqr(self, x):
+        return self._unary(OP_SQR, x)
+
+    def exp(self, x):
+        return self._unary(OP_EXP, x)
+
+    def leaky_relu(self, x, slope):
+        return self._unary(OP_LEAKY_RELU, x, f=(slope,))
+
+    def scale_bias(self, x, s, b):
+        return self._unary(OP_SCALE_BIAS, x, f=(s, b))
+
+    def rope_neox(self, x, pos, n_dims, freq_base, freq_scale=1.0, attn_factor=1.0, cs_rounded=False):
+        """x: (T, heads, head_dim) f32; pos: (T,) int32. cs_rounded: cos/sin from
+        double rounded once to f32 instead of libm cosf/sinf (ggml-CPU's)."""
+        x = self._f32(x)
+        pos = np.ascontiguousarray(pos, dtype=np.int32)
+        assert x.ndim == 3 and pos.shape == (x.shape[0],)
+        return self._node(OP_ROPE_NEOX, np.empty_like(x), x, pos, ne1=x.shape[1], nrows=x.shape[0] * x.shape[1],
+                          f=(freq_base, freq_scale, attn_factor), i=(n_dims, 1 if cs_rounded else 0))
+
+    def get_rows(self, table, type0, ne0, ids):
+        """table: numpy array of raw rows (any dtype, C-contiguous, one row per
+        leading index: (rows, row_elems) for F32/F16(bits)/BF16(bits), (rows,
+        row_bytes) uint8 for Q8_0); ids: (n,) int32 -> (n, ne0) f32."""
+        table = np.ascontiguousarray(table)
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        dst = np.empty((ids.size, ne0), dtype=np.float32)
+        return self._node(OP_GET_ROWS, dst, table, ids, type0=type0, ne0=ne0, nrows=ids.size,
+                          src1_rows=table.shape[0])
+
+    def cast_f32(self, x, type0):
+        x = np.ascontiguousarray(x)
+        dst = np.empty(x.shape, dtype=np.float32)
+        return self._node(OP_CAST_F32, dst, x, type0=type0)
+
+    def glu_swiglu(self, a, swapped=False):
+        a = self._f32(a)
+        nc = a.shape[-1] // 2
+        dst = np.empty(a.shape[:-1] + (nc,), dtype=np.float32)
+        return self._node(OP_GLU_SWIGLU, dst, a, ne0=nc, nrows=_rows(dst), i=(1 if swapped else 0,))
+
+    def _array(self):
+        arr = (OrcNode * len(self.nodes))(*self.nodes)
+        return arr
+
+    def compute(self, n_threads=1):
+        arr = self._array()
+        rc = lib().orc_compute(arr, len(self.nodes), int(n_threads))
+        if rc != 0:
+            raise RuntimeError("oracle compute failed (%d)" % rc)
+
+    def time(self, n_threads, warmup, reps):
+        arr = self._array()
+        times = (ctypes.c_double * reps)()
+        rc = lib().orc_time_nodes(arr, len(self.nodes), int(n_threads), int(warmup), int(reps), times)
+        if rc != 0:
+            raise RuntimeError("oracle timing failed (%d)" % rc)
+        return list(times)
+
+
+# ---------------------------------------------------------------------------
+# node runs the reference graph builders emit
+# ---------------------------------------------------------------------------
+
+def as_f32(g, w, wtype=F32):
+    """as_f32, src/arch/qwen3-tts/operations.cpp:20-25 (ggml_cast when not F32)."""
+    return w if wtype == F32 else g.cast_f32(w, wtype)
+
+
+def rms_norm_w(g, x, w, eps, wtype=F32):
+    """rms_norm(), src/arch/qwen3-tts/operations.cpp:27-32: ggml_rms_norm then ggml_mul."""
+    return g.mul(g.rms_norm(x, eps), as_f32(g, w, wtype))
+
+
+def swiglu(g, gate, up):
+    """src/arch/qwen3-tts/operations.cpp:39-41: ggml_silu(gate) then ggml_mul(., up)."""
+    return g.mul(g.silu(gate), up)
+
+
+def qk_norm_rope(g, q, k, wq, wk, eps, pos, n_dims, theta, wtype=F32, cs_rounded=False):
+    """src/arch/qwen3-tts/operations.cpp:98-104: per-head rms_norm()*w then NEOX rope,
+    for q (T, heads, hd) and k (T, kv_heads, hd)."""
+    qn = rms_norm_w(g, q, wq, eps, wtype)
+    kn = rms_norm_w(g, k, wk, eps, wtype)
+    return (g.rope_neox(qn, pos, n_dims, theta, cs_rounded=cs_rounded),
+            g.rope_neox(kn, pos, n_dims, theta, cs_rounded=cs_rounded))
+
+
+def add_rms_norm_w(g, a, b, w, eps, wtype=F32):
+    """src/arch/qwen3-tts/operations.cpp:143-145: residual ggml_add then rms_norm()."""
+    s = g.add(a, b)
+    return s, rms_norm_w(g, s, w, eps, wtype)
+
+
+def snake(g, x, alpha):
+    """src/arch/kokoro/operations.cpp:137-147: mul, sin, mul(s, s), div, add. x (T, C)."""
+    scaled = g.mul(x, alpha)
+    sine = g.sin(scaled)
+    squared = g.mul(sine, sine)
+    return g.add(x, g.div(squared, alpha))
+
+
+def snake_beta(g, x, log_alpha, log_beta):
+    """codec_snake_beta, src/arch/qwen3-tts/codec.cpp:184-199:
+    x + sin(x*exp(a))^2 / (exp(b) + 1e-9)."""
+    alpha = g.exp(log_alpha)
+    beta = g.exp(log_beta)
+    squared = g.sqr(g.sin(g.mul(x, alpha)))
+    guard = g.scale_bias(beta, 1.0, 1e-9)
+    return g.add(x, g.div(squared, guard))
+
+
+def add_leaky(g, a, b, slope):
+    """src/arch/vits/waveform-decoder.cpp:150-158: layer l's closing ggml_add, then layer
+    l+1's ggml_leaky_relu. Returns (sum, y)."""
+    s = g.add(a, b)
+    return s, g.leaky_relu(s, slope)
+
+
+def sum_code_embeddings(g, tables, type0, ne0, codes):
+    """src/arch/qwen3-tts/code-predictor.cpp:82-107: get_rows per group, added in group
+    order. codes: (groups, frames) int32 (ggml [frames, groups], frames fastest)."""
+    total = None
+    for t, table in enumerate(tables):
+        rows = g.get_rows(table, type0, ne0, codes[t])
+        total = rows if total is None else g.add(total, rows)
+    return total
+
+
+def run(build, n_threads=1):
+    """Builds a graph with `build(g)` and computes it; returns build's result."""
+    g = Graph()
+    out = build(g)
+    g.compute(n_threads)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# the rest of a Qwen3 block, for the tiny golden configurations
+# ---------------------------------------------------------------------------
+
+def mul_mat(w, x):
+    """ggml_mul_mat(w, x) with w [in, out] (numpy (out, in)) and x (T, in): (T, out).
+    Accumulated in double and rounded once, which is within the goldens' 1e-4 of
+    ggml's f32 SIMD dot products."""
+    return (x.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32)
+
+
+def soft_max_ext(scores, mask, scale):
+    """ggml_soft_max_ext(scores, mask, scale, 0): softmax over the last axis of
+    scores*scale + mask, sum in double."""
+    w = scores.astype(np.float32) * np.float32(scale)
+    if mask is not None:
+        w = w + mask.astype(np.float32)
+    m = w.max(axis=-1, keepdims=True)
+    e = np.exp((w - m).astype(np.float64))
+    return (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
+
+
+class LcgStream:
+    """The reference tests' weight stream: 64-bit LCG, float(state>>40)/2^23 - 1
+    (tests/qwen3_tts_decoder_layer_test.cpp:51-70)."""
+
+    MUL = 6364136223846793005
+    INC = 1442695040888963407
+    MASK = (1 << 64) - 1
+
+    def __init__(self, seed):
+        self.state = seed & self.MASK
+
+    def fill(self, count, scale, offset):
+        out = np.empty(count, dtype=np.float32)
+        s = self.state
+        for k in range(count):
+            s = (s * self.MUL + self.INC) & self.MASK
+            out[k] = np.float32(s >> 40) / np.float32(8388608.0) - np.float32(1.0)
+        self.state = s
+        return out * np.float32(scale) + np.float32(offset)
+
+
+def decoder_layer(x, pos, mask, W, shape, cache, filled, ops=None):
+    """decoder_layer, src/arch/qwen3-tts/operations.cpp:44-148, over x (T, hidden).
+
+    W holds numpy weights in ggml memory order ((out, in) for projections).
+    cache = {"k": (cap, kv_heads, hd), "v": ...} is written in place at
+    [filled, filled+T). `ops` replaces the hot-path node runs (default: this
+    restatement); the GPU parity tests pass the HIP versions here."""
+    ops = ops or OracleOps()
+    T = x.shape[0]
+    hd, H, KVH = shape["head_dim"], shape["heads"], shape["kv_heads"]
+    eps, theta = shape["rms_norm_eps"], shape["rope_theta"]
+    residual = x
+    normed = ops.rms_norm_w(x, W["input_layernorm"], eps)
+    q = mul_mat(W["q_proj"], normed).reshape(T, H, hd)
+    k = mul_mat(W["k_proj"], normed).reshape(T, KVH, hd)
+    v = mul_mat(W["v_proj"], normed).reshape(T, KVH, hd)
+    q, k = ops.qk_norm_rope(q, k, W["q_norm"], W["k_norm"], eps, pos, hd, theta)
+    cache["k"][filled:filled + T] = k
+    cache["v"][filled:filled + T] = v
+    total = filled + T
+    kc, vc = cache["k"][:total], cache["v"][:total]
+    group = H // KVH
+    attended = np.empty((T, H, hd), dtype=np.float32)
+    for h in range(H):
+        kv = h // group  # ggml_mul_mat's broadcast: blocked grouping (operations.cpp:127-131)
+        scores = (q[:, h, :].astype(np.float64) @ kc[:, kv, :].astype(np.float64).T).astype(np.float32)
+        p = soft_max_ext(scores, mask, 1.0 / np.sqrt(np.float32(hd)))
+        attended[:, h, :] = (p.astype(np.float64) @ vc[:, kv, :].astype(np.float64)).astype(np.float32)
+    projected = mul_mat(W["o_proj"], attended.reshape(T, H * hd))
+    after_attention, mlp_in = ops.add_rms_norm_w(residual, projected, W["post_attention_layernorm"], eps)
+    gate = mul_mat(W["gate_proj"], mlp_in)
+    up = mul_mat(W["up_proj"], mlp_in)
+    mlp = mul_mat(W["down_proj"], ops.swiglu(gate, up))
+    return ops.add(after_attention, mlp)
+
+
+class OracleOps:
+    """The hot-path node runs of decoder_layer, evaluated by the restatement."""
+
+    def rms_norm_w(self, x, w, eps):
+        return run(lambda g: rms_norm_w(g, x, w, eps))
+
+    def qk_norm_rope(self, q, k, wq, wk, eps, pos, n_dims, theta):
+        return run(lambda g: qk_norm_rope(g, q, k, wq, wk, eps, pos, n_dims, theta))
+
+    def add_rms_norm_w(self, a, b, w, eps):
+        return run(lambda g: add_rms_norm_w(g, a, b, w, eps))
+
+    def swiglu(self, gate, up):
+        return run(lambda g: swiglu(g, gate, up))
+
+    def add(self, a, b):
+        return run(lambda g: g.add(a, b))
+
+    def get_rows(self, table, ids):
+        return run(lambda g: g.get_rows(table, F32, table.shape[-1], ids))
+
+
+def layer_weights(stream, hidden, heads, kv_heads, head_dim, intermediate):
+    """One decoder layer's weights in the reference tests' fill order
+    (tests/qwen3_tts_decoder_layer_test.cpp:146-158), numpy (out, in)."""
+    spec = [("input_layernorm", (hidden,), 0.25, 1.0), ("q_proj", (heads * head_dim, hidden), 0.5, 0.0),
+            ("k_proj", (kv_heads * head_dim, hidden), 0.5, 0.0), ("v_proj", (kv_heads * head_dim, hidden), 0.5, 0.0),
+            ("o_proj", (hidden, heads * head_dim), 0.5, 0.0), ("q_norm", (head_dim,), 0.25, 1.0),
+            ("k_norm", (head_dim,), 0.25, 1.0), ("post_attention_layernorm", (hidden,), 0.25, 1.0),
+            ("gate_proj", (intermediate, hidden), 0.5, 0.0), ("up_proj", (intermediate, hidden), 0.5, 0.0),
+            ("down_proj", (hidden, intermediate), 0.5, 0.0)]
+    W = {}
+    for name, shp, scale, offset in spec:
+        W[name] = stream.fill(int(np.prod(shp)), scale, offset).reshape(shp)
+    return W

@@ -1,0 +1,237 @@
+// Internal helpers shared by the libsynth_hip translation units: ggml-style row
+// addressing, exact element conversions, wave64 reductions and the host-side
+// argument checks every entry point applies before it launches anything.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "synth_hip.h"
+
+namespace shp {
+
+constexpr int kWave = 64;
+
+// Addresses row r of a ggml tensor whose rows are the flattened dims 1..3
+// (r = i1 + ne1*(i2 + ne2*i3)). When the rows are evenly strided the offset is
+// r*rs, with no division; otherwise it is decomposed per dimension.
+struct RowMap {
+    int64_t ne1;
+    int64_t ne2;
+    int64_t nb1;
+    int64_t nb2;
+    int64_t nb3;
+    int64_t rs;
+    int32_t flat;
+    int32_t pad;
+};
+
+__device__ __forceinline__ int64_t row_offset(const RowMap & m, int64_t r) {
+    if (m.flat) {
+        return r * m.rs;
+    }
+    const int64_t i1 = r % m.ne1;
+    const int64_t q  = r / m.ne1;
+    const int64_t i2 = q % m.ne2;
+    const int64_t i3 = q / m.ne2;
+    return i1 * m.nb1 + i2 * m.nb2 + i3 * m.nb3;
+}
+
+// bf16 -> f32 is a 16-bit shift; f16 -> f32 is the exact hardware conversion.
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+    return __uint_as_float(h << 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+// Weight element loaders: WT 1 = F32, 2 = BF16, 3 = F16.
+enum WeightKind { kWNone = 0, kWF32 = 1, kWBF16 = 2, kWF16 = 3 };
+
+template <int WT> __device__ __forceinline__ float load_w1(const void * w, int64_t i) {
+    if constexpr (WT == kWF32) {
+        return static_cast<const float *>(w)[i];
+    } else if constexpr (WT == kWBF16) {
+        return bf16_bits_to_f32(static_cast<const uint16_t *>(w)[i]);
+    } else if constexpr (WT == kWF16) {
+        return f16_bits_to_f32(static_cast<const uint16_t *>(w)[i]);
+    } else {
+        return 1.0f;
+    }
+}
+
+// Four consecutive weights starting at element e (e % 4 == 0, base 8-byte aligned).
+template <int WT> __device__ __forceinline__ float4 load_w4(const void * w, int64_t e) {
+    if constexpr (WT == kWF32) {
+        return reinterpret_cast<const float4 *>(static_cast<const float *>(w) + e)[0];
+    } else {
+        const uint2 h = reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(w) + e)[0];
+        if constexpr (WT == kWBF16) {
+            return make_float4(bf16_bits_to_f32(h.x & 0xffffu), bf16_bits_to_f32(h.x >> 16),
+                               bf16_bits_to_f32(h.y & 0xffffu), bf16_bits_to_f32(h.y >> 16));
+        } else {
+            return make_float4(f16_bits_to_f32(h.x & 0xffffu), f16_bits_to_f32(h.x >> 16), f16_bits_to_f32(h.y & 0xffffu),
+                               f16_bits_to_f32(h.y >> 16));
+        }
+    }
+}
+
+// Two consecutive weights at element e (e % 2 == 0).
+template <int WT> __device__ __forceinline__ float2 load_w2(const void * w, int64_t e) {
+    if constexpr (WT == kWF32) {
+        return reinterpret_cast<const float2 *>(static_cast<const float *>(w) + e)[0];
+    } else {
+        const uint32_t h = reinterpret_cast<const uint32_t *>(static_cast<const uint16_t *>(w) + e)[0];
+        if constexpr (WT == kWBF16) {
+            return make_float2(bf16_bits_to_f32(h & 0xffffu), bf16_bits_to_f32(h >> 16));
+        } else {
+            return make_float2(f16_bits_to_f32(h & 0xffffu), f16_bits_to_f32(h >> 16));
+        }
+    }
+}
+
+// Sum of a double over groups of W consecutive lanes (W a power of two <= 64).
+template <int W> __device__ __forceinline__ double group_sum(double v) {
+#pragma unroll
+    for (int off = W / 2; off > 0; off >>= 1) {
+        v += __shfl_xor(v, off, W);
+    }
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+inline size_t type_size(int32_t type) {
+    switch (type) {
+        case SHP_TYPE_F32:
+        case SHP_TYPE_I32:
+            return 4;
+        case SHP_TYPE_F16:
+        case SHP_TYPE_BF16:
+            return 2;
+        default:
+            return 0;
+    }
+}
+
+// Bytes of one ne0-long row; Q8_0 rows are ne0/32 blocks of 34 bytes.
+inline size_t row_bytes(int32_t type, int64_t ne0) {
+    if (type == SHP_TYPE_Q8_0) {
+        return static_cast<size_t>(ne0 / 32) * 34u;
+    }
+    return static_cast<size_t>(ne0) * type_size(type);
+}
+
+inline int64_t nrows(const shp_tensor & t) {
+    return t.ne[1] * t.ne[2] * t.ne[3];
+}
+
+inline int64_t nelements(const shp_tensor & t) {
+    return t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
+}
+
+inline bool same_shape(const shp_tensor & a, const shp_tensor & b) {
+    return a.ne[0] == b.ne[0] && a.ne[1] == b.ne[1] && a.ne[2] == b.ne[2] && a.ne[3] == b.ne[3];
+}
+
+// A descriptor is well formed when its type is known, extents are positive,
+// rows are contiguous (nb[0] is the element size, or the block size for Q8_0)
+// and data is non-null.
+inline bool well_formed(const shp_tensor * t) {
+    if (t == nullptr || t->data == nullptr || t->reserved != 0) {
+        return false;
+    }
+    for (int d = 0; d < 4; ++d) {
+        if (t->ne[d] <= 0) {
+            return false;
+        }
+    }
+    if (t->type == SHP_TYPE_Q8_0) {
+        return t->ne[0] % 32 == 0 && t->nb[0] == 34u;
+    }
+    const size_t ts = type_size(t->type);
+    return ts != 0 && t->nb[0] == ts;
+}
+
+inline RowMap make_rowmap(const shp_tensor & t) {
+    RowMap m{};
+    m.ne1  = t.ne[1];
+    m.ne2  = t.ne[2];
+    m.nb1  = static_cast<int64_t>(t.nb[1]);
+    m.nb2  = static_cast<int64_t>(t.nb[2]);
+    m.nb3  = static_cast<int64_t>(t.nb[3]);
+    m.flat = 1;
+    m.rs   = 0;
+    int64_t expect = -1;
+    for (int d = 1; d < 4; ++d) {
+        if (t.ne[d] == 1) {
+            continue;
+        }
+        const int64_t nb = static_cast<int64_t>(t.nb[d]);
+        if (expect < 0) {
+            m.rs   = nb;
+            expect = nb * t.ne[d];
+        } else if (nb == expect) {
+            expect *= t.ne[d];
+        } else {
+            m.flat = 0;
+        }
+    }
+    return m;
+}
+
+// True when every row start of `t` is `align`-byte aligned.
+inline bool rows_aligned(const shp_tensor & t, size_t align) {
+    if (reinterpret_cast<uintptr_t>(t.data) % align != 0) {
+        return false;
+    }
+    for (int d = 1; d < 4; ++d) {
+        if (t.ne[d] > 1 && t.nb[d] % align != 0) {
+            return false;
+        }
+    }
+    return true;
+}
+
+// Fully contiguous (ggml_is_contiguous) in the element-size sense.
+inline bool contiguous(const shp_tensor & t) {
+    size_t expect = t.nb[0] * static_cast<size_t>(t.ne[0]);
+    if (t.type == SHP_TYPE_Q8_0) {
+        expect = row_bytes(t.type, t.ne[0]);
+    }
+    for (int d = 1; d < 4; ++d) {
+        if (t.ne[d] > 1 && t.nb[d] != expect) {
+            return false;
+        }
+        expect *= static_cast<size_t>(t.ne[d]);
+    }
+    return true;
+}
+
+inline int weight_kind(int32_t type) {
+    switch (type) {
+        case SHP_TYPE_F32:
+            return kWF32;
+        case SHP_TYPE_BF16:
+            return kWBF16;
+        case SHP_TYPE_F16:
+            return kWF16;
+        default:
+            return -1;
+    }
+}
+
+inline hipStream_t as_stream(shp_stream_t s) {
+    return static_cast<hipStream_t>(s);
+}
+
+inline shp_status_t launch_status() {
+    return hipGetLastError() == hipSuccess ? SHP_OK : SHP_ERR_BACKEND;
+}
+
+}  // namespace shp

@@ -1,0 +1,272 @@
+"""Python host binding of libsynth_hip (ctypes over the C ABI in include/synth_hip.h).
+
+The functions mirror the ggml op (or node run) each C entry point replaces --
+same names, same argument meaning, ggml [ne0, ne1, ...] shapes expressed as
+torch tensors of shape (..., ne1, ne0) -- and raise ShpError on a non-zero
+status, which is how the reference's builders report a node they cannot build.
+
+torch is used only as device-memory plumbing: tensors carry the device
+pointers and every call is enqueued on torch's current HIP stream. torch must
+be imported before the library is loaded, because torch ships its own copy of
+libamdhip64.so.7 and one process must run one HIP runtime.
+
+There is no CPU fallback: without the built library every call raises.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsynth_hip.so")
+
+OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_BACKEND = 0, 1, 2, 17
+TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_I32, TYPE_BF16 = 0, 1, 8, 26, 30
+ROPE_TYPE_NEOX = 2
+Q8_0_BLOCK_BYTES, Q8_0_BLOCK_ELEMS = 34, 32
+
+
+class ShpTensor(ctypes.Structure):
+    _fields_ = [("type", ctypes.c_int32), ("reserved", ctypes.c_int32), ("ne", ctypes.c_int64 * 4),
+                ("nb", ctypes.c_size_t * 4), ("data", ctypes.c_void_p)]
+
+
+class ShpError(RuntimeError):
+    def __init__(self, status, what):
+        super().__init__("%s failed: %s (%d)" % (what, status_string(status), status))
+        self.status = status
+
+
+_lib = None
+_PT = ctypes.POINTER(ShpTensor)
+
+
+def load(path=None):
+    """Loads the built library once (raises if it is missing)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    try:
+        import torch  # noqa: F401  -- share torch's HIP runtime (see module docstring)
+    except ImportError:
+        pass
+    path = path or LIB_PATH
+    if not os.path.exists(path):
+        raise RuntimeError("libsynth_hip.so is not built (%s); run __graft_entry__.build() or make -C "
+                           "synthesize.cpp_amd" % path)
+    L = ctypes.CDLL(path)
+    vp, f, i32 = ctypes.c_void_p, ctypes.c_float, ctypes.c_int32
+    sigs = {
+        "shp_get_rows": [_PT, _PT, _PT, vp],
+        "shp_get_rows_sum": [_PT, i32, _PT, _PT, vp],
+        "shp_rms_norm_mul": [_PT, _PT, f, _PT, vp],
+        "shp_add_rms_norm_mul": [_PT, _PT, _PT, f, _PT, _PT, vp],
+        "shp_rope_ext": [_PT, _PT, i32, i32, f, f, f, f, _PT, vp],
+        "shp_qk_norm_rope": [_PT, _PT, _PT, _PT, f, _PT, i32, f, f, _PT, _PT, vp],
+        "shp_swiglu": [_PT, _PT, _PT, vp],
+        "shp_glu_swiglu": [_PT, i32, _PT, vp],
+        "shp_snake": [_PT, _PT, _PT, vp],
+        "shp_add_leaky_relu": [_PT, _PT, f, _PT, _PT, vp],
+        "shp_add": [_PT, _PT, _PT, vp],
+    }
+    for name, args in sigs.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = ctypes.c_int32
+    L.shp_abi_version.restype = ctypes.c_uint32
+    L.shp_abi_version.argtypes = []
+    L.shp_status_string.restype = ctypes.c_char_p
+    L.shp_status_string.argtypes = [ctypes.c_int32]
+    _lib = L
+    return L
+
+
+def status_string(status):
+    return load().shp_status_string(int(status)).decode()
+
+
+def abi_version():
+    return int(load().shp_abi_version())
+
+
+# ---------------------------------------------------------------------------
+# descriptors
+# ---------------------------------------------------------------------------
+
+class Q8Tensor:
+    """A Q8_0 tensor held as raw blocks: `data` is a uint8 torch tensor of shape
+    (..., rows, ne0/32*34); ne0 is the logical row length."""
+
+    def __init__(self, data, ne0):
+        assert ne0 % Q8_0_BLOCK_ELEMS == 0
+        assert data.shape[-1] == ne0 // Q8_0_BLOCK_ELEMS * Q8_0_BLOCK_BYTES
+        self.data, self.ne0 = data, ne0
+
+    @property
+    def rows(self):
+        return self.data.shape[-2]
+
+
+def _torch_type(t):
+    import torch
+    return {torch.float32: TYPE_F32, torch.float16: TYPE_F16, torch.bfloat16: TYPE_BF16,
+            torch.int32: TYPE_I32}[t.dtype]
+
+
+def desc(t):
+    """shp_tensor for a torch tensor (or Q8Tensor); None stays None."""
+    if t is None:
+        return None
+    d = ShpTensor()
+    if isinstance(t, Q8Tensor):
+        raw = t.data
+        shape = list(raw.shape[::-1])
+        strides = list(raw.stride()[::-1])
+        d.type = TYPE_Q8_0
+        shape[0] = t.ne0
+        strides[0] = Q8_0_BLOCK_BYTES
+        item = 1
+    else:
+        shape = list(t.shape[::-1]) or [1]
+        strides = list(t.stride()[::-1]) or [1]
+        d.type = _torch_type(t)
+        item = t.element_size()
+        strides = [s * item for s in strides]
+        raw = t
+    if len(shape) > 4:
+        raise ValueError("at most 4 dimensions")
+    while len(shape) < 4:
+        strides.append(strides[-1] * shape[-1] if item else 0)
+        shape.append(1)
+    d.reserved = 0
+    for k in range(4):
+        d.ne[k] = int(shape[k])
+        d.nb[k] = int(strides[k])
+    d.data = raw.data_ptr()
+    return d
+
+
+def _ref(d):
+    return ctypes.byref(d) if d is not None else None
+
+
+def _stream():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _check(status, what):
+    if status != OK:
+        raise ShpError(status, what)
+
+
+def _empty_like_f32(shape, device):
+    import torch
+    return torch.empty(shape, dtype=torch.float32, device=device)
+
+
+# ---------------------------------------------------------------------------
+# ops (ggml names)
+# ---------------------------------------------------------------------------
+
+def get_rows(src, ids, out=None):
+    """ggml_get_rows(src, ids) -> f32. src (rows, ne0) torch F32/F16/BF16 or Q8Tensor;
+    ids int32 (n,). Batched forms follow ggml's [ne0, rows, ne2, ne3] x [n, ne2, ne3]."""
+    raw = src.data if isinstance(src, Q8Tensor) else src
+    ne0 = src.ne0 if isinstance(src, Q8Tensor) else src.shape[-1]
+    if out is None:
+        out = _empty_like_f32(tuple(ids.shape) + (ne0,), raw.device)
+    _check(load().shp_get_rows(_ref(desc(src)), _ref(desc(ids)), _ref(desc(out)), _stream()), "get_rows")
+    return out
+
+
+def get_rows_sum(tables, codes, out=None):
+    """sum_code_embeddings: codes int32 (groups, frames) (ggml [frames, groups]); tables
+    one per group; returns f32 (frames, ne0) = ordered sum of the gathered rows."""
+    n = len(tables)
+    arr = (ShpTensor * n)(*[desc(t) for t in tables])
+    first = tables[0]
+    ne0 = first.ne0 if isinstance(first, Q8Tensor) else first.shape[-1]
+    raw = first.data if isinstance(first, Q8Tensor) else first
+    if out is None:
+        out = _empty_like_f32((codes.shape[-1], ne0), raw.device)
+    _check(load().shp_get_rows_sum(arr, n, _ref(desc(codes)), _ref(desc(out)), _stream()), "get_rows_sum")
+    return out
+
+
+def rms_norm_mul(x, w, eps, out=None):
+    """rms_norm() of src/arch/qwen3-tts/operations.cpp:27-32 (w None: bare ggml_rms_norm)."""
+    out = x.new_empty(x.shape) if out is None else out
+    _check(load().shp_rms_norm_mul(_ref(desc(x)), _ref(desc(w)), float(eps), _ref(desc(out)), _stream()),
+           "rms_norm_mul")
+    return out
+
+
+def add_rms_norm_mul(a, b, w, eps, out=None, sum_out=None, want_sum=True):
+    """ggml_add(a, b) then rms_norm()*w; returns (sum or None, y)."""
+    out = a.new_empty(a.shape) if out is None else out
+    if sum_out is None and want_sum:
+        sum_out = a.new_empty(a.shape)
+    _check(load().shp_add_rms_norm_mul(_ref(desc(a)), _ref(desc(b)), _ref(desc(w)), float(eps), _ref(desc(sum_out)),
+                                       _ref(desc(out)), _stream()), "add_rms_norm_mul")
+    return sum_out, out
+
+
+def rope_ext(x, pos, n_dims, mode, freq_base, freq_scale=1.0, ext_factor=0.0, attn_factor=1.0, out=None):
+    """ggml_rope_ext on x (T, heads, head_dim) with I32 positions (T,)."""
+    out = x.new_empty(x.shape) if out is None else out
+    _check(load().shp_rope_ext(_ref(desc(x)), _ref(desc(pos)), int(n_dims), int(mode), float(freq_base),
+                               float(freq_scale), float(ext_factor), float(attn_factor), _ref(desc(out)), _stream()),
+           "rope_ext")
+    return out
+
+
+def qk_norm_rope(q, k, wq, wk, eps, pos, n_dims, freq_base, freq_scale=1.0, q_out=None, k_out=None):
+    """Per-head rms_norm()*w then NEOX rope for q (T, H, hd) and k (T, KVH, hd)."""
+    q_out = q.new_empty(q.shape) if q_out is None else q_out
+    if k is not None and k_out is None:
+        k_out = k.new_empty(k.shape)
+    _check(load().shp_qk_norm_rope(_ref(desc(q)), _ref(desc(k)), _ref(desc(wq)), _ref(desc(wk)), float(eps),
+                                   _ref(desc(pos)), int(n_dims), float(freq_base), float(freq_scale),
+                                   _ref(desc(q_out)), _ref(desc(k_out)), _stream()), "qk_norm_rope")
+    return q_out, k_out
+
+
+def swiglu(g, u=None, out=None):
+    """ggml_silu(g) then ggml_mul(., u) (u None: bare silu)."""
+    out = g.new_empty(g.shape) if out is None else out
+    _check(load().shp_swiglu(_ref(desc(g)), _ref(desc(u)), _ref(desc(out)), _stream()), "swiglu")
+    return out
+
+
+def glu_swiglu(a, swapped=False, out=None):
+    """ggml_swiglu(a) / ggml_swiglu_swapped(a) on a (..., 2n) -> (..., n)."""
+    out = a.new_empty(tuple(a.shape[:-1]) + (a.shape[-1] // 2,)) if out is None else out
+    _check(load().shp_glu_swiglu(_ref(desc(a)), 1 if swapped else 0, _ref(desc(out)), _stream()), "glu_swiglu")
+    return out
+
+
+def snake(x, alpha, out=None):
+    """Kokoro Snake on x (T, C) (ggml [C, T], channels fastest), alpha (C,)."""
+    out = x.new_empty(x.shape) if out is None else out
+    _check(load().shp_snake(_ref(desc(x)), _ref(desc(alpha)), _ref(desc(out)), _stream()), "snake")
+    return out
+
+
+def add_leaky_relu(a, b, slope, out=None, sum_out=None, want_sum=False):
+    """ggml_add(a, b) then ggml_leaky_relu(., slope); returns (sum or None, y)."""
+    out = a.new_empty(a.shape) if out is None else out
+    if sum_out is None and want_sum:
+        sum_out = a.new_empty(a.shape)
+    _check(load().shp_add_leaky_relu(_ref(desc(a)), _ref(desc(b)), float(slope), _ref(desc(sum_out)),
+                                     _ref(desc(out)), _stream()), "add_leaky_relu")
+    return sum_out, out
+
+
+def leaky_relu(a, slope, out=None):
+    return add_leaky_relu(a, None, slope, out=out)[1]
+
+
+def add(a, b, out=None):
+    """ggml_add(a, b), b the same shape or one broadcast row."""
+    out = a.new_empty(a.shape) if out is None else out
+    _check(load().shp_add(_ref(desc(a)), _ref(desc(b)), _ref(desc(out)), _stream()), "add")
+    return out

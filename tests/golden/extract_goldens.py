@@ -1,0 +1,108 @@
+"""Writes the reference's golden vectors for this path as JSON fixtures.
+
+Run in the build container, where the synthesize.cpp checkout is mounted read
+only; it reads the reference's test sources as text and copies out only the
+numeric literals (the expected outputs) plus the fixture configuration they
+were produced under. Nothing from the reference is executed or imported.
+
+    python tests/golden/extract_goldens.py [/path/to/synthesize.cpp]
+
+Sources:
+  G1 tests/qwen3_tts_decoder_layer_test.cpp:30-47   (kExpectedHidden, config)
+  G2 tests/qwen3_tts_code_predictor_test.cpp:33-61  (logits, codes, summed embedding)
+  G3 tests/qwen3_tts_codec_ops_test.cpp:34-82       (kExpectedSnakeBeta, config)
+"""
+import json
+import os
+import re
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def literal_array(text, name):
+    m = re.search(r"%s\[\]\s*=\s*\{(.*?)\};" % re.escape(name), text, re.S)
+    if m is None:
+        raise SystemExit("array %s not found" % name)
+    body = m.group(1)
+    out = []
+    for tok in body.replace("\n", " ").split(","):
+        tok = tok.strip()
+        if not tok:
+            continue
+        out.append(float(tok.rstrip("fF")) if ("." in tok or "e" in tok.lower()) else int(tok))
+    return out
+
+
+def constant(text, name):
+    m = re.search(r"constexpr\s+\w+\s+%s\s*=\s*([-0-9.eEfu]+)\s*;" % re.escape(name), text)
+    if m is None:
+        raise SystemExit("constant %s not found" % name)
+    tok = m.group(1).rstrip("fFuU")
+    return float(tok) if ("." in tok or "e" in tok.lower()) else int(tok)
+
+
+def main():
+    root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+    read = lambda rel: open(os.path.join(root, rel), encoding="utf-8").read()
+
+    t = read("tests/qwen3_tts_decoder_layer_test.cpp")
+    g1 = {
+        "source": "tests/qwen3_tts_decoder_layer_test.cpp:30-47,146-172",
+        "hidden": constant(t, "kHidden"), "heads": constant(t, "kHeads"), "kv_heads": constant(t, "kKvHeads"),
+        "head_dim": constant(t, "kHeadDim"), "intermediate": constant(t, "kIntermediate"),
+        "positions": constant(t, "kPositions"), "prefill": constant(t, "kPrefill"),
+        "rms_norm_eps": constant(t, "kRmsNormEps"), "rope_theta": constant(t, "kRopeTheta"),
+        "seed": constant(t, "kSeed"),
+        # (tensor, scale, offset) in LCG fill order, :146-158; hidden state last, :165.
+        "fill_order": [["input_layernorm", 0.25, 1.0], ["q_proj", 0.5, 0.0], ["k_proj", 0.5, 0.0],
+                       ["v_proj", 0.5, 0.0], ["o_proj", 0.5, 0.0], ["q_norm", 0.25, 1.0], ["k_norm", 0.25, 1.0],
+                       ["post_attention_layernorm", 0.25, 1.0], ["gate_proj", 0.5, 0.0], ["up_proj", 0.5, 0.0],
+                       ["down_proj", 0.5, 0.0], ["hidden", 0.5, 0.0]],
+        "tolerance_cpu": 1e-4, "tolerance_gpu": 5e-3,
+        "expected_hidden": literal_array(t, "kExpectedHidden"),
+    }
+
+    t = read("tests/qwen3_tts_code_predictor_test.cpp")
+    g2 = {
+        "source": "tests/qwen3_tts_code_predictor_test.cpp:33-61,159-214",
+        "hidden": constant(t, "kHidden"), "heads": constant(t, "kHeads"), "kv_heads": constant(t, "kKvHeads"),
+        "head_dim": constant(t, "kHeadDim"), "intermediate": constant(t, "kIntermediate"),
+        "layers": constant(t, "kLayers"), "vocab": constant(t, "kVocab"), "code_groups": constant(t, "kCodeGroups"),
+        "rms_norm_eps": constant(t, "kRmsNormEps"), "rope_theta": constant(t, "kRopeTheta"),
+        "seed": constant(t, "kSeed"),
+        "tolerance_cpu": 1e-4, "tolerance_gpu": 5e-3,
+        "expected_logits": literal_array(t, "kExpectedLogits"),
+        "expected_codes": literal_array(t, "kExpectedCodes"),
+        "expected_summed_embedding": literal_array(t, "kExpectedSummedEmbedding"),
+    }
+
+    t = read("tests/qwen3_tts_codec_ops_test.cpp")
+    g3 = {
+        "source": "tests/qwen3_tts_codec_ops_test.cpp:34-82,184-234",
+        "length": constant(t, "kLength"), "channels": constant(t, "kChannels"),
+        "out_channels": constant(t, "kOutChannels"), "kernel": constant(t, "kKernel"),
+        "stride": constant(t, "kStride"), "seed": constant(t, "kSeed"),
+        # element counts drawn before alpha/beta, in fill order (:185-196)
+        "draws_before_alpha": {
+            "signal": constant(t, "kChannels") * constant(t, "kLength"),
+            "conv_weight": constant(t, "kKernel") * constant(t, "kChannels") * constant(t, "kOutChannels"),
+            "conv_bias": constant(t, "kOutChannels"),
+            "depthwise_weight": constant(t, "kKernel") * constant(t, "kChannels"),
+            "depthwise_bias": constant(t, "kChannels"),
+            "transposed_weight": 2 * constant(t, "kStride") * constant(t, "kOutChannels") * constant(t, "kChannels"),
+            "transposed_bias": constant(t, "kOutChannels"),
+        },
+        "tolerance_cpu": 1e-4, "tolerance_gpu": 5e-3,
+        "expected_snake_beta": literal_array(t, "kExpectedSnakeBeta"),
+    }
+
+    for name, obj in (("qwen3_decoder_layer", g1), ("qwen3_code_predictor", g2), ("qwen3_codec_snake_beta", g3)):
+        with open(os.path.join(HERE, name + ".json"), "w") as f:
+            json.dump(obj, f, indent=1)
+            f.write("\n")
+        print("wrote", name)
+
+
+if __name__ == "__main__":
+    main()

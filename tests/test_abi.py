@@ -1,0 +1,129 @@
+"""The C ABI without a GPU: the library loads, exports every entry point the
+header declares, and rejects malformed arguments before launching anything
+(argument checks are host code; no device pointer is dereferenced)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import synth_hip as S
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "synth_hip.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(shp_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = S.load()
+    names = declared_symbols()
+    assert len(names) >= 13
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_status_strings():
+    assert S.abi_version() == 1
+    assert S.status_string(S.OK) == "ok"
+    assert "invalid" in S.status_string(S.ERR_INVALID_ARG)
+    assert "unsupported" in S.status_string(S.ERR_UNSUPPORTED)
+    assert "HIP" in S.status_string(S.ERR_BACKEND)
+
+
+FAKE = 0x10000  # never dereferenced: every call below fails validation first
+
+
+def mk(type_, ne, nb=None, data=FAKE):
+    t = S.ShpTensor()
+    t.type = type_
+    size = {S.TYPE_F32: 4, S.TYPE_I32: 4, S.TYPE_F16: 2, S.TYPE_BF16: 2, S.TYPE_Q8_0: 34}[type_]
+    ne = list(ne) + [1] * (4 - len(ne))
+    if nb is None:
+        nb = [size]
+        row = size * (ne[0] // 32 if type_ == S.TYPE_Q8_0 else ne[0])
+        nb.append(row)
+        nb.append(row * ne[1])
+        nb.append(row * ne[1] * ne[2])
+    for k in range(4):
+        t.ne[k], t.nb[k] = ne[k], nb[k]
+    t.data = data
+    return t
+
+
+def R(x):
+    return ctypes.byref(x) if x is not None else None
+
+
+def test_argument_validation():
+    L = S.load()
+    x = mk(S.TYPE_F32, [1024, 8])
+    y = mk(S.TYPE_F32, [1024, 8])
+    w = mk(S.TYPE_F32, [1024])
+    bad_w = mk(S.TYPE_F32, [512])
+    assert L.shp_rms_norm_mul(None, R(w), 1e-6, R(y), None) == S.ERR_INVALID_ARG
+    assert L.shp_rms_norm_mul(R(x), R(w), 1e-6, R(mk(S.TYPE_F32, [1024, 7])), None) == S.ERR_INVALID_ARG
+    assert L.shp_rms_norm_mul(R(x), R(bad_w), 1e-6, R(y), None) == S.ERR_UNSUPPORTED
+    assert L.shp_rms_norm_mul(R(mk(S.TYPE_F16, [1024, 8])), R(w), 1e-6, R(y), None) == S.ERR_UNSUPPORTED
+    assert L.shp_rms_norm_mul(R(mk(S.TYPE_F32, [1024, 8], data=0)), R(w), 1e-6, R(y), None) == S.ERR_INVALID_ARG
+    assert L.shp_add_rms_norm_mul(R(x), None, R(w), 1e-6, None, R(y), None) == S.ERR_INVALID_ARG
+    xt = mk(S.TYPE_F32, [1024, 8])
+    xt.nb[0] = 8  # non-contiguous rows
+    assert L.shp_rms_norm_mul(R(xt), R(w), 1e-6, R(y), None) == S.ERR_INVALID_ARG
+    xr = mk(S.TYPE_F32, [1024, 8])
+    xr.reserved = 1
+    assert L.shp_rms_norm_mul(R(xr), R(w), 1e-6, R(y), None) == S.ERR_INVALID_ARG
+
+    q = mk(S.TYPE_F32, [128, 16, 5])
+    k = mk(S.TYPE_F32, [128, 8, 5])
+    pos = mk(S.TYPE_I32, [5])
+    assert L.shp_rope_ext(R(q), R(pos), 128, 0, 1e6, 1, 0, 1, R(q), None) == S.ERR_UNSUPPORTED  # normal mode
+    assert L.shp_rope_ext(R(q), R(pos), 128, 2, 1e6, 1, 0.5, 1, R(q), None) == S.ERR_UNSUPPORTED  # yarn
+    assert L.shp_rope_ext(R(q), R(mk(S.TYPE_I32, [4])), 128, 2, 1e6, 1, 0, 1, R(q), None) == S.ERR_INVALID_ARG
+    assert L.shp_rope_ext(R(q), R(pos), 130, 2, 1e6, 1, 0, 1, R(q), None) == S.ERR_INVALID_ARG
+    assert L.shp_rope_ext(R(q), R(pos), 127, 2, 1e6, 1, 0, 1, R(q), None) == S.ERR_INVALID_ARG
+    wq = mk(S.TYPE_BF16, [128])
+    wk = mk(S.TYPE_F32, [128])
+    assert L.shp_qk_norm_rope(R(q), R(k), R(wq), R(wk), 1e-6, R(pos), 128, 1e6, 1, R(q), R(k), None) == \
+        S.ERR_UNSUPPORTED  # mixed gain types
+    assert L.shp_qk_norm_rope(R(q), R(k), R(wq), None, 1e-6, R(pos), 128, 1e6, 1, R(q), R(k), None) == \
+        S.ERR_INVALID_ARG
+    assert L.shp_qk_norm_rope(R(q), R(k), R(wq), R(wq), 1e-6, R(pos), 128, 1e6, 1, R(q), None, None) == \
+        S.ERR_INVALID_ARG
+
+    tab = mk(S.TYPE_Q8_0, [1024, 100])
+    ids = mk(S.TYPE_I32, [7])
+    out = mk(S.TYPE_F32, [1024, 7])
+    assert L.shp_get_rows(R(tab), R(mk(S.TYPE_F32, [7])), R(out), None) == S.ERR_INVALID_ARG
+    assert L.shp_get_rows(R(tab), R(ids), R(mk(S.TYPE_F32, [1024, 6])), None) == S.ERR_INVALID_ARG
+    assert L.shp_get_rows(R(tab), R(ids), R(mk(S.TYPE_F16, [1024, 7])), None) == S.ERR_UNSUPPORTED
+    odd = mk(S.TYPE_Q8_0, [1024, 100])
+    odd.ne[0] = 1000  # not whole blocks
+    assert L.shp_get_rows(R(odd), R(ids), R(out), None) == S.ERR_INVALID_ARG
+    tabs = (S.ShpTensor * 2)(mk(S.TYPE_Q8_0, [1024, 100]), mk(S.TYPE_BF16, [1024, 100]))
+    codes = mk(S.TYPE_I32, [7, 2])
+    assert L.shp_get_rows_sum(tabs, 2, R(codes), R(out), None) == S.ERR_UNSUPPORTED  # mixed table types
+    assert L.shp_get_rows_sum(tabs, 0, R(codes), R(out), None) == S.ERR_INVALID_ARG
+    assert L.shp_get_rows_sum(tabs, 65, R(codes), R(out), None) == S.ERR_INVALID_ARG
+    assert L.shp_get_rows_sum(tabs, 1, R(codes), R(out), None) == S.ERR_INVALID_ARG  # codes has 2 groups
+
+    a = mk(S.TYPE_F32, [256, 4])
+    assert L.shp_snake(R(a), R(mk(S.TYPE_F32, [255])), R(a), None) == S.ERR_INVALID_ARG
+    assert L.shp_add_leaky_relu(R(a), None, 0.1, R(a), R(a), None) == S.ERR_INVALID_ARG
+    assert L.shp_add(R(a), R(mk(S.TYPE_F32, [256, 3])), R(a), None) == S.ERR_INVALID_ARG
+    assert L.shp_glu_swiglu(R(a), 0, R(a), None) == S.ERR_INVALID_ARG
+    assert L.shp_swiglu(R(a), R(mk(S.TYPE_F32, [256, 5])), R(a), None) == S.ERR_INVALID_ARG
+
+
+def test_binding_fails_loudly_without_library(tmp_path):
+    with pytest.raises(RuntimeError):
+        import importlib
+        mod = importlib.reload(S)
+        mod._lib = None
+        mod.load(str(tmp_path / "missing.so"))
+    import importlib
+    importlib.reload(S)

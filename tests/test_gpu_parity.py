@@ -1,0 +1,490 @@
+"""GPU parity: every libsynth_hip entry point against the ggml-CPU restatement on
+the same seeded inputs, through the C ABI.
+
+Bars: bit-exact for gathers, sums of gathers, adds and leaky-ReLU (compared as
+raw 32-bit patterns, NaN payloads included); for RMSNorm, SwiGLU and Snake an
+elementwise relative error <= 1e-5 with the denominator floored at 1e-3 * RMS
+of the reference row (so near-zero outputs do not blow the ratio up).
+
+Rope: the kernel evaluates cos/sin in double and rounds once (correctly
+rounded), while ggml-CPU calls glibc cosf/sinf, which land one ulp away in
+about 1.3% of arguments. A rotated component that nearly cancels
+(x0*c - x1*s ~ 0) then differs by ~1e-7 of the pair's length, which an
+elementwise ratio reports as a large relative error of a tiny number. So rope
+outputs are held to 1e-5 relative to the length of their NEOX pair (which the
+rotation preserves), AND the kernel is checked bit-exact against the
+restatement run with correctly rounded cos/sin -- which isolates libm's last
+ulp as the only difference.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import formats as F
+import ggml_ref as R
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-5
+SEED = 20260728
+
+
+def _t(gpu, a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _bits16(gpu, bits, dtype):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).cuda().view(dtype)
+
+
+def _np(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def assert_bitexact(got, ref):
+    got = np.ascontiguousarray(got, np.float32)
+    ref = np.ascontiguousarray(ref, np.float32)
+    assert got.shape == ref.shape
+    bad = got.view(np.uint32) != ref.view(np.uint32)
+    assert not bad.any(), "%d of %d differ; first at %s: %r vs %r" % (
+        bad.sum(), bad.size, np.argwhere(bad)[0], got[bad][0], ref[bad][0])
+
+
+def assert_close(got, ref, tol=REL_TOL):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape
+    rows = ref.reshape(-1, ref.shape[-1])
+    rms = np.sqrt((rows ** 2).mean(axis=-1, keepdims=True))
+    floor = np.broadcast_to(1e-3 * rms, rows.shape).reshape(ref.shape)
+    den = np.maximum(np.abs(ref), floor)
+    den = np.where(den == 0, 1.0, den)
+    rel = np.abs(got - ref) / den
+    worst = rel.max()
+    assert worst <= tol, "max rel err %.3g at %s (got %r ref %r)" % (
+        worst, np.unravel_index(rel.argmax(), rel.shape), got.flat[rel.argmax()], ref.flat[rel.argmax()])
+    return float(worst), float((got == ref).mean())
+
+
+def assert_rope_close(got, ref, n_dims, tol=REL_TOL):
+    """|got - ref| <= tol * |(ref_i, ref_{i+n_dims/2})| per NEOX pair; elements
+    past n_dims (copied) elementwise."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape
+    half = n_dims // 2
+    pair = np.hypot(ref[..., :half], ref[..., half:n_dims])
+    den = np.concatenate([pair, pair], axis=-1)
+    den = np.where(den == 0, 1.0, den)
+    rel = np.abs(got[..., :n_dims] - ref[..., :n_dims]) / den
+    assert rel.max() <= tol, "max pair-relative err %.3g" % rel.max()
+    if n_dims < ref.shape[-1]:
+        assert_close(got[..., n_dims:], ref[..., n_dims:], tol)
+    return float(rel.max())
+
+
+# ---------------------------------------------------------------------------
+# gathers
+# ---------------------------------------------------------------------------
+
+def _table(rng, kind, rows, ne0):
+    """Returns (oracle raw rows, oracle type, torch tensor or Q8Tensor builder input)."""
+    if kind == "f32":
+        a = rng.standard_normal((rows, ne0)).astype(np.float32)
+        return a, R.F32
+    if kind == "bf16":
+        return F.f32_to_bf16_bits(rng.standard_normal((rows, ne0)).astype(np.float32) * 0.02), R.BF16
+    if kind == "f16":
+        return F.f32_to_f16_bits(rng.standard_normal((rows, ne0)).astype(np.float32)), R.F16
+    return F.q8_0_synthetic(rng, rows, ne0), R.Q8_0
+
+
+def _dev_table(gpu, raw, kind, ne0):
+    import torch
+    if kind == "f32":
+        return _t(gpu, raw)
+    if kind == "bf16":
+        return _bits16(gpu, raw, torch.bfloat16)
+    if kind == "f16":
+        return _bits16(gpu, raw, torch.float16)
+    return gpu.Q8Tensor(_t(gpu, raw), ne0)
+
+
+@pytest.mark.parametrize("kind", ["f32", "f16", "bf16", "q8_0"])
+@pytest.mark.parametrize("ne0", [64, 1024, 2048, 96, 4096])
+def test_get_rows_bitexact(gpu, kind, ne0):
+    if kind == "q8_0" and ne0 % 32:
+        pytest.skip("Q8_0 rows are whole blocks")
+    rng = np.random.default_rng(SEED + ne0)
+    rows, n = 300, 257
+    raw, otype = _table(rng, kind, rows, ne0)
+    ids = rng.integers(0, rows, n).astype(np.int32)
+    ids[:2] = [0, rows - 1]
+    ref = R.run(lambda g: g.get_rows(raw, otype, ne0, ids))
+    got = gpu.get_rows(_dev_table(gpu, raw, kind, ne0), _t(gpu, ids))
+    assert_bitexact(_np(got), ref)
+
+
+def test_get_rows_special_values(gpu):
+    """BF16 NaN/Inf payloads and -0, F16 subnormals/Inf/NaN, Q8_0 with d = 0,
+    negative d, subnormal f16 d and qs = +-127/-128: all exact, as the closed
+    forms say."""
+    import torch
+    specials = np.array([0x0000, 0x8000, 0x7F80, 0xFF80, 0x7FC1, 0xFFA5, 0x0001, 0x807F, 0x3F80, 0xC2F7] * 13,
+                        np.uint16)[:128]
+    bf = np.tile(specials, (4, 1))
+    ref = R.run(lambda g: g.get_rows(bf, R.BF16, 128, np.array([3, 0, 2], np.int32)))
+    got = gpu.get_rows(_bits16(gpu, bf, torch.bfloat16), _t(gpu, np.array([3, 0, 2], np.int32)))
+    assert_bitexact(_np(got), ref)
+    assert_bitexact(ref, F.bf16_bits_to_f32(bf[[3, 0, 2]]))
+
+    h = np.array([0x0001, 0x03FF, 0x8001, 0x7C00, 0xFC00, 0x7E01, 0x0000, 0x8000, 0x3C00, 0x7BFF] * 13,
+                 np.uint16)[:128]
+    hf = np.tile(h, (2, 1))
+    ref = R.run(lambda g: g.get_rows(hf, R.F16, 128, np.array([1, 0], np.int32)))
+    got = gpu.get_rows(_bits16(gpu, hf, torch.float16), _t(gpu, np.array([1, 0], np.int32)))
+    assert_bitexact(_np(got), ref)
+    assert_bitexact(ref, F.f16_bits_to_f32(hf[[1, 0]]))
+
+    rng = np.random.default_rng(5)
+    nb = 4
+    d = np.array([[0x0000, 0x8C00, 0x0003, 0x2E66]], np.uint16).repeat(3, 0)  # 0, negative, subnormal, ~0.1
+    qs = rng.integers(-128, 128, (3, nb, 32), dtype=np.int8)
+    qs[:, :, 0], qs[:, :, 1], qs[:, :, 2] = 127, -127, -128
+    raw = F.q8_0_pack(d, qs)
+    ids = np.array([2, 1, 0], np.int32)
+    ref = R.run(lambda g: g.get_rows(raw, R.Q8_0, 128, ids))
+    got = gpu.get_rows(gpu.Q8Tensor(_t(gpu, raw), 128), _t(gpu, ids))
+    assert_bitexact(_np(got), ref)
+    assert_bitexact(ref, F.q8_0_dequant(raw, 128)[ids])
+
+
+def test_get_rows_batched_and_out_of_range(gpu):
+    import torch
+    rng = np.random.default_rng(7)
+    # ggml_get_rows batch form: src [ne0, rows, 2], ids [n, 2] -> [ne0, n, 2]
+    src = rng.standard_normal((2, 50, 256)).astype(np.float32)
+    ids = rng.integers(0, 50, (2, 9)).astype(np.int32)
+    got = _np(gpu.get_rows(_t(gpu, src), _t(gpu, ids)))
+    for b in range(2):
+        assert_bitexact(got[b], src[b][ids[b]])
+    # An id outside the table is never read; its row comes back as NaN.
+    tab = _t(gpu, rng.standard_normal((10, 1024)).astype(np.float32))
+    bad = _t(gpu, np.array([3, 10, -1, 9], np.int32))
+    out = _np(gpu.get_rows(tab, bad))
+    assert np.isnan(out[1]).all() and np.isnan(out[2]).all()
+    assert_bitexact(out[[0, 3]], _np(tab)[[3, 9]])
+    raw = F.q8_0_synthetic(rng, 10, 1024)
+    out = _np(gpu.get_rows(gpu.Q8Tensor(_t(gpu, raw), 1024), bad))
+    assert np.isnan(out[1]).all() and np.isnan(out[2]).all()
+    assert_bitexact(out[[0, 3]], F.q8_0_dequant(raw, 1024)[[3, 9]])
+    del torch
+
+
+@pytest.mark.parametrize("kind,ne0,groups", [("q8_0", 1024, 16), ("q8_0", 2048, 15), ("q8_0", 4096, 3),
+                                             ("q8_0", 96, 5), ("bf16", 1024, 16), ("f16", 2048, 4),
+                                             ("f32", 1024, 15), ("f32", 8, 4), ("f32", 3000, 2)])
+def test_get_rows_sum_bitexact(gpu, kind, ne0, groups):
+    rng = np.random.default_rng(SEED + ne0 + groups)
+    rows, frames = 200, 301
+    tabs = [_table(rng, kind, rows, ne0) for _ in range(groups)]
+    codes = rng.integers(0, rows, (groups, frames)).astype(np.int32)
+    ref = R.run(lambda g: R.sum_code_embeddings(g, [t for t, _ in tabs], tabs[0][1], ne0, codes))
+    got = gpu.get_rows_sum([_dev_table(gpu, t, kind, ne0) for t, _ in tabs], _t(gpu, codes))
+    assert_bitexact(_np(got), ref)
+
+
+def test_get_rows_sum_order_matters_and_nan_on_bad_id(gpu):
+    rng = np.random.default_rng(11)
+    tabs = [(rng.standard_normal((64, 1024)) * 10.0 ** rng.integers(-3, 3, (64, 1))).astype(np.float32)
+            for _ in range(4)]
+    codes = rng.integers(0, 64, (4, 100)).astype(np.int32)
+    dev = [_t(gpu, t) for t in tabs]
+    fwd = _np(gpu.get_rows_sum(dev, _t(gpu, codes)))
+    rev = _np(gpu.get_rows_sum(dev[::-1], _t(gpu, np.ascontiguousarray(codes[::-1]))))
+    assert not np.array_equal(fwd.view(np.uint32), rev.view(np.uint32))  # f32 addition is not associative
+    bad = codes.copy()
+    bad[2, 5] = 64
+    out = _np(gpu.get_rows_sum(dev, _t(gpu, bad)))
+    assert np.isnan(out[5]).all()
+    assert_bitexact(np.delete(out, 5, 0), np.delete(fwd, 5, 0))
+
+
+# ---------------------------------------------------------------------------
+# norms and rope
+# ---------------------------------------------------------------------------
+
+def _weights(rng, n, kind):
+    w = rng.normal(1.0, 0.1, n).astype(np.float32)
+    if kind == "bf16":
+        return F.f32_to_bf16_bits(w), R.BF16
+    if kind == "f16":
+        return F.f32_to_f16_bits(w), R.F16
+    return w, R.F32
+
+
+def _dev_w(gpu, w, kind):
+    import torch
+    if kind == "bf16":
+        return _bits16(gpu, w, torch.bfloat16)
+    if kind == "f16":
+        return _bits16(gpu, w, torch.float16)
+    return _t(gpu, w)
+
+
+@pytest.mark.parametrize("shape,wkind", [((512, 1024), "bf16"), ((64, 2048), "f32"), ((7, 24, 128), "f16"),
+                                         ((33, 1000), "f32"), ((5, 8), "f32"), ((3, 4096), "bf16"),
+                                         ((40, 3072), "f32"), ((9, 64), "none"), ((4, 256), "bf16"),
+                                         ((6, 512), "f32")])
+def test_rms_norm_mul(gpu, shape, wkind):
+    rng = np.random.default_rng(SEED + sum(shape))
+    x = rng.standard_normal(shape).astype(np.float32)
+    x[0] = 0.0  # an all-zero row: scale = 1/sqrt(eps), output exactly 0
+    eps = np.float32(1e-6)
+    if wkind == "none":
+        ref = R.run(lambda g: g.rms_norm(x, eps))
+        got = gpu.rms_norm_mul(_t(gpu, x), None, eps)
+    else:
+        w, wt = _weights(rng, shape[-1], wkind)
+        ref = R.run(lambda g: R.rms_norm_w(g, x, w, eps, wt))
+        got = gpu.rms_norm_mul(_t(gpu, x), _dev_w(gpu, w, wkind), eps)
+    got = _np(got)
+    assert (got[0] == 0).all()
+    _, same = assert_close(got, ref)
+    assert same > 0.999  # double-accumulated squares: the GPU lands on the CPU's bits
+
+
+@pytest.mark.parametrize("shape,wkind", [((512, 1024), "bf16"), ((64, 2048), "f32"), ((3, 1000), "f32")])
+def test_add_rms_norm_mul(gpu, shape, wkind):
+    rng = np.random.default_rng(SEED + 3 * sum(shape))
+    a = rng.standard_normal(shape).astype(np.float32)
+    b = rng.standard_normal(shape).astype(np.float32)
+    w, wt = _weights(rng, shape[-1], wkind)
+    eps = np.float32(1e-6)
+    s_ref, y_ref = R.run(lambda g: R.add_rms_norm_w(g, a, b, w, eps, wt))
+    s, y = gpu.add_rms_norm_mul(_t(gpu, a), _t(gpu, b), _dev_w(gpu, w, wkind), eps)
+    assert_bitexact(_np(s), s_ref)
+    assert_close(_np(y), y_ref)
+    _, y2 = gpu.add_rms_norm_mul(_t(gpu, a), _t(gpu, b), _dev_w(gpu, w, wkind), eps, want_sum=False)
+    assert_bitexact(_np(y2), _np(y))
+
+
+def _positions(rng, T, hi):
+    p = rng.integers(0, hi, T).astype(np.int32)
+    p[0] = 0
+    return p
+
+
+@pytest.mark.parametrize("T,H,hd,n_dims,hi", [(512, 16, 128, 128, 512), (64, 8, 128, 128, 8192),
+                                              (17, 4, 96, 64, 8192), (3, 4, 4, 4, 4), (9, 2, 128, 64, 1000)])
+def test_rope_ext_neox(gpu, T, H, hd, n_dims, hi):
+    rng = np.random.default_rng(SEED + T + hd)
+    x = rng.standard_normal((T, H, hd)).astype(np.float32)
+    pos = _positions(rng, T, hi)
+    theta = np.float32(1e6)
+    ref = R.run(lambda g: g.rope_neox(x, pos, n_dims, theta))
+    got = _np(gpu.rope_ext(_t(gpu, x), _t(gpu, pos), n_dims, gpu.ROPE_TYPE_NEOX, theta))
+    assert_rope_close(got, ref, n_dims)
+    assert_bitexact(got, R.run(lambda g: g.rope_neox(x, pos, n_dims, theta, cs_rounded=True)))
+    assert_bitexact(got[0], x[0])  # position 0 is the identity rotation (cos 0 = 1, sin 0 = 0)
+    if n_dims < hd:
+        assert_bitexact(got[..., n_dims:], x[..., n_dims:])
+
+
+def test_rope_in_place_and_scaled(gpu):
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((40, 16, 128)).astype(np.float32)
+    pos = _positions(rng, 40, 8192)
+    ref = R.run(lambda g: g.rope_neox(x, pos, 128, np.float32(1e4), np.float32(0.5), np.float32(1.25)))
+    xt = _t(gpu, x)
+    gpu.rope_ext(xt, _t(gpu, pos), 128, gpu.ROPE_TYPE_NEOX, 1e4, 0.5, 0.0, 1.25, out=xt)
+    assert_rope_close(_np(xt), ref, 128)
+    assert_bitexact(_np(xt), R.run(lambda g: g.rope_neox(x, pos, 128, np.float32(1e4), np.float32(0.5),
+                                                          np.float32(1.25), cs_rounded=True)))
+
+
+@pytest.mark.parametrize("T,hi,wkind", [(1, 64, "bf16"), (512, 512, "bf16"), (300, 8192, "f32"), (64, 8192, "f16")])
+def test_qk_norm_rope(gpu, T, hi, wkind):
+    rng = np.random.default_rng(SEED + T)
+    q = rng.standard_normal((T, 16, 128)).astype(np.float32)
+    k = rng.standard_normal((T, 8, 128)).astype(np.float32)
+    wq, wt = _weights(rng, 128, wkind)
+    wk, _ = _weights(rng, 128, wkind)
+    pos = _positions(rng, T, hi)
+    eps, theta = np.float32(1e-6), np.float32(1e6)
+    qr, kr = R.run(lambda g: R.qk_norm_rope(g, q, k, wq, wk, eps, pos, 128, theta, wt))
+    qo, ko = gpu.qk_norm_rope(_t(gpu, q), _t(gpu, k), _dev_w(gpu, wq, wkind), _dev_w(gpu, wk, wkind), eps,
+                              _t(gpu, pos), 128, theta)
+    assert_rope_close(_np(qo), qr, 128)
+    assert_rope_close(_np(ko), kr, 128)
+    qc, kc = R.run(lambda g: R.qk_norm_rope(g, q, k, wq, wk, eps, pos, 128, theta, wt, cs_rounded=True))
+    assert_bitexact(_np(qo), qc)
+    assert_bitexact(_np(ko), kc)
+
+
+def test_qk_norm_rope_generic_head_dim(gpu):
+    rng = np.random.default_rng(13)
+    q = rng.standard_normal((6, 4, 64)).astype(np.float32)
+    k = rng.standard_normal((6, 2, 64)).astype(np.float32)
+    wq = rng.normal(1, 0.1, 64).astype(np.float32)
+    wk = rng.normal(1, 0.1, 64).astype(np.float32)
+    pos = _positions(rng, 6, 100)
+    qr, kr = R.run(lambda g: R.qk_norm_rope(g, q, k, wq, wk, np.float32(1e-6), pos, 64, np.float32(1e6)))
+    qo, ko = gpu.qk_norm_rope(_t(gpu, q), _t(gpu, k), _t(gpu, wq), _t(gpu, wk), 1e-6, _t(gpu, pos), 64, 1e6)
+    assert_rope_close(_np(qo), qr, 64)
+    assert_rope_close(_np(ko), kr, 64)
+
+
+# ---------------------------------------------------------------------------
+# elementwise
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("shape", [(512, 3072), (3, 6144), (7, 1001), (1, 3072), (16, 4)])
+def test_swiglu_and_silu(gpu, shape):
+    rng = np.random.default_rng(SEED + sum(shape))
+    gt = (rng.standard_normal(shape) * 4).astype(np.float32)
+    up = rng.standard_normal(shape).astype(np.float32)
+    ref = R.run(lambda g: R.swiglu(g, gt, up))
+    assert_close(_np(gpu.swiglu(_t(gpu, gt), _t(gpu, up))), ref)
+    ref = R.run(lambda g: g.silu(gt))
+    assert_close(_np(gpu.swiglu(_t(gpu, gt))), ref)
+
+
+@pytest.mark.parametrize("swapped", [False, True])
+def test_glu_swiglu_single_tensor(gpu, swapped):
+    rng = np.random.default_rng(17)
+    a = rng.standard_normal((33, 2 * 384)).astype(np.float32)
+    ref = R.run(lambda g: g.glu_swiglu(a, swapped))
+    assert_close(_np(gpu.glu_swiglu(_t(gpu, a), swapped)), ref)
+
+
+@pytest.mark.parametrize("T,C", [(256, 512), (64, 128), (31, 30), (5, 1024)])
+def test_snake(gpu, T, C):
+    rng = np.random.default_rng(SEED + T + C)
+    x = rng.standard_normal((T, C)).astype(np.float32)
+    alpha = np.exp(rng.uniform(np.log(0.1), np.log(10.0), C)).astype(np.float32)
+    ref = R.run(lambda g: R.snake(g, x, alpha))
+    assert_close(_np(gpu.snake(_t(gpu, x), _t(gpu, alpha))), ref)
+
+
+def _specials(n, rng):
+    v = rng.standard_normal(n).astype(np.float32)
+    sp = np.array([0.0, -0.0, np.nan, -np.nan, np.inf, -np.inf, 1e-45, -1e-45, 1e-38, -3e-39, 3.4e38, -3.4e38],
+                  np.float32)
+    m = min(n, sp.size)
+    v[:m] = sp[:m]
+    return v
+
+
+@pytest.mark.parametrize("shape", [(128, 8192), (33, 77), (1, 4)])
+@pytest.mark.parametrize("slope", [0.1, 0.01])
+def test_add_leaky_relu_bitexact(gpu, shape, slope):
+    rng = np.random.default_rng(SEED + shape[1])
+    a = _specials(int(np.prod(shape)), rng).reshape(shape)
+    b = rng.standard_normal(shape).astype(np.float32)
+    b.reshape(-1)[:12] = 0.0  # the specials reach the leaky unchanged
+    s_ref, y_ref = R.run(lambda g: R.add_leaky(g, a, b, np.float32(slope)))
+    s, y = gpu.add_leaky_relu(_t(gpu, a), _t(gpu, b), slope, want_sum=True)
+    assert_bitexact(_np(s), s_ref)
+    assert_bitexact(_np(y), y_ref)
+    # -0 -> +0 and NaN -> +0, exactly as ggml's (x>0?x:0) + slope*(x<0?x:0)
+    yv = _np(y).reshape(-1)
+    assert yv[1] == 0 and not np.signbit(yv[1]) and yv[2] == 0 and yv[3] == 0
+    y_only = gpu.leaky_relu(_t(gpu, a), slope)
+    assert_bitexact(_np(y_only), R.run(lambda g: g.leaky_relu(a, np.float32(slope))))
+
+
+@pytest.mark.parametrize("bshape", ["full", "row"])
+def test_add(gpu, bshape):
+    rng = np.random.default_rng(19)
+    a = rng.standard_normal((37, 1024)).astype(np.float32)
+    b = rng.standard_normal((37, 1024) if bshape == "full" else (1024,)).astype(np.float32)
+    assert_bitexact(_np(gpu.add(_t(gpu, a), _t(gpu, b))), R.run(lambda g: g.add(a, b)))
+
+
+def test_strided_views(gpu):
+    """ggml views: rows strided in dims 1..3 (a q/k head view of a fused qkv
+    buffer) go through the row path with the same results."""
+    import torch
+    rng = np.random.default_rng(23)
+    qkv = rng.standard_normal((10, 32, 128)).astype(np.float32)  # T, heads(16 q + 8 k + 8 v), hd
+    dev = _t(gpu, qkv)
+    q, k = dev[:, :16, :], dev[:, 16:24, :]
+    pos = _positions(rng, 10, 500)
+    wq = rng.normal(1, 0.1, 128).astype(np.float32)
+    wk = rng.normal(1, 0.1, 128).astype(np.float32)
+    qr, kr = R.run(lambda g: R.qk_norm_rope(g, qkv[:, :16], qkv[:, 16:24], wq, wk, np.float32(1e-6), pos, 128,
+                                            np.float32(1e6)))
+    qo, ko = gpu.qk_norm_rope(q, k, _t(gpu, wq), _t(gpu, wk), 1e-6, _t(gpu, pos), 128, 1e6)
+    assert_rope_close(_np(qo), qr, 128)
+    assert_rope_close(_np(ko), kr, 128)
+    x = dev.reshape(10, 32 * 128)[:, :1024]  # strided rows
+    w = rng.normal(1, 0.1, 1024).astype(np.float32)
+    ref = R.run(lambda g: R.rms_norm_w(g, qkv.reshape(10, -1)[:, :1024], w, np.float32(1e-6)))
+    assert_close(_np(gpu.rms_norm_mul(x, _t(gpu, w), 1e-6)), ref)
+    out = torch.empty((10, 4096), device="cuda")
+    y = out[:, 1000:2024]
+    gpu.swiglu(x, x, out=y)
+    assert_close(_np(y), R.run(lambda g: R.swiglu(g, qkv.reshape(10, -1)[:, :1024], qkv.reshape(10, -1)[:, :1024])))
+
+
+# ---------------------------------------------------------------------------
+# the reference's goldens through the HIP kernels
+# ---------------------------------------------------------------------------
+
+class HipOps(R.OracleOps):
+    """decoder_layer's hot-path node runs on the GPU through the C ABI."""
+
+    def __init__(self, gpu):
+        self.g = gpu
+
+    def rms_norm_w(self, x, w, eps):
+        return _np(self.g.rms_norm_mul(_t(self.g, x), _t(self.g, w), eps))
+
+    def qk_norm_rope(self, q, k, wq, wk, eps, pos, n_dims, theta):
+        qo, ko = self.g.qk_norm_rope(_t(self.g, q), _t(self.g, k), _t(self.g, wq), _t(self.g, wk), eps,
+                                     _t(self.g, pos), n_dims, theta)
+        return _np(qo), _np(ko)
+
+    def add_rms_norm_w(self, a, b, w, eps):
+        s, y = self.g.add_rms_norm_mul(_t(self.g, a), _t(self.g, b), _t(self.g, w), eps)
+        return _np(s), _np(y)
+
+    def swiglu(self, gate, up):
+        return _np(self.g.swiglu(_t(self.g, gate), _t(self.g, up)))
+
+    def add(self, a, b):
+        return _np(self.g.add(_t(self.g, a), _t(self.g, b)))
+
+    def get_rows(self, table, ids):
+        return _np(self.g.get_rows(_t(self.g, table), _t(self.g, ids)))
+
+
+def _golden(name):
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name)) as f:
+        return json.load(f)
+
+
+def test_golden_g1_decoder_layer_on_gpu(gpu):
+    import test_oracle_goldens as G
+    d = _golden("qwen3_decoder_layer.json")
+    got = G.run_decoder_golden(d, HipOps(gpu))
+    exp = np.array(d["expected_hidden"], np.float32)
+    assert np.abs(got - exp).max() < d["tolerance_gpu"]
+    assert np.abs(got - exp).max() < d["tolerance_cpu"]
+    assert_close(got.reshape(4, -1), G.run_decoder_golden(d).reshape(4, -1))
+
+
+def test_golden_g2_summed_embedding_on_gpu(gpu):
+    import test_oracle_goldens as G
+    d = _golden("qwen3_code_predictor.json")
+    _, codes, summed_ref, tables = G.run_code_predictor(d)
+    got = _np(gpu.get_rows_sum([_t(gpu, t) for t in tables], _t(gpu, np.array([[c] for c in codes], np.int32))))
+    assert_bitexact(got.reshape(-1), summed_ref)
+    assert np.abs(got.reshape(-1) - np.array(d["expected_summed_embedding"], np.float32)).max() < d["tolerance_cpu"]

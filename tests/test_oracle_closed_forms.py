@@ -1,0 +1,278 @@
+"""Pins the ggml-CPU restatement where the reference's goldens leave it open:
+exact conversions (all 65536 half/bf16 patterns), the Q8_0 closed form and a
+pure-Python brute force, RMSNorm invariants, rope identities and a
+double-precision closed form at large positions, SwiGLU / Snake against double
+closed forms, leaky-ReLU's signed-zero and NaN behaviour, and thread-count
+invariance of the ggml-style row split. Planted mistakes check that each test
+can fail."""
+import math
+import struct
+
+import numpy as np
+import pytest
+
+import formats as F
+import ggml_ref as R
+
+ULP = np.finfo(np.float32).eps
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+# ---------------------------------------------------------------------------
+# conversions and gathers
+# ---------------------------------------------------------------------------
+
+def test_half_and_bf16_conversions_all_patterns():
+    # Through get_rows, so results stay in f32 buffers (a ctypes float return
+    # would pass through a Python double and quiet signalling NaNs).
+    allp = np.arange(65536, dtype=np.uint16).reshape(512, 128)
+    ids = np.arange(512, dtype=np.int32)
+    h = R.run(lambda g: g.get_rows(allp, R.F16, 128, ids))
+    np.testing.assert_array_equal(bits(h), bits(allp.view(np.float16).astype(np.float32)))
+    b = R.run(lambda g: g.get_rows(allp, R.BF16, 128, ids))
+    np.testing.assert_array_equal(bits(b), (allp.astype(np.uint32) << 16))
+
+
+def test_fp32_to_half_and_bf16_rounding():
+    L = R.lib()
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.standard_normal(4000).astype(np.float32) * 10.0 ** rng.integers(-9, 6, 4000),
+                        np.array([65504, 65519.99, 65520, 1e-8, 6.1e-5, 5.96e-8, 2.98e-8, 2.99e-8, -0.0, np.inf,
+                                  -np.inf], np.float32)]).astype(np.float32)
+    got = np.array([L.orc_fp32_to_fp16(float(v)) for v in x], np.uint16)
+    np.testing.assert_array_equal(got, x.astype(np.float16).view(np.uint16))
+    got = np.array([L.orc_fp32_to_bf16(float(v)) for v in x], np.uint16)
+    np.testing.assert_array_equal(got, F.f32_to_bf16_bits(x))
+    # round half to even at the bf16 boundary: 1 + 2^-8 ties to 1, 1 + 3*2^-8 ties up
+    np.testing.assert_array_equal(F.f32_to_bf16_bits(np.array([1 + 2 ** -8, 1 + 3 * 2 ** -8], np.float32)),
+                                  [0x3F80, 0x3F82])
+
+
+def q8_brute(raw, ne0, ids):
+    """Pure-Python dequant of Q8_0 rows: d from the f16 bit pattern by its
+    definition, each element q*d (exact), no numpy arithmetic."""
+    out = []
+    nb = ne0 // 32
+    for i in ids:
+        row = bytes(raw[i])
+        vals = []
+        for b in range(nb):
+            blk = row[34 * b: 34 * b + 34]
+            (dh,) = struct.unpack("<H", blk[:2])
+            sign = -1.0 if dh & 0x8000 else 1.0
+            e, m = (dh >> 10) & 31, dh & 1023
+            d = sign * (m * 2.0 ** -24 if e == 0 else (1 + m / 1024.0) * 2.0 ** (e - 15))
+            for q in struct.unpack("<32b", blk[2:]):
+                vals.append(q * d)
+        out.append(vals)
+    return np.array(out, np.float32)
+
+
+@pytest.mark.parametrize("kind", ["f32", "f16", "bf16", "q8_0"])
+def test_get_rows_closed_form(kind):
+    rng = np.random.default_rng(2)
+    rows, ne0 = 40, 128
+    ids = rng.integers(0, rows, 23).astype(np.int32)
+    if kind == "f32":
+        tab = rng.standard_normal((rows, ne0)).astype(np.float32)
+        ref, t = tab[ids], R.F32
+    elif kind == "f16":
+        tab = F.f32_to_f16_bits(rng.standard_normal((rows, ne0)))
+        ref, t = F.f16_bits_to_f32(tab[ids]), R.F16
+    elif kind == "bf16":
+        tab = F.f32_to_bf16_bits(rng.standard_normal((rows, ne0)))
+        ref, t = F.bf16_bits_to_f32(tab[ids]), R.BF16
+    else:
+        d, qs = F.q8_0_unpack(F.q8_0_synthetic(rng, rows, ne0), ne0)
+        d = d.copy()
+        d[3], d[4], d[5] = 0x0000, 0x8001, 0xBC00  # zero, negative subnormal, -1
+        ids[:3] = [3, 4, 5]
+        tab = F.q8_0_pack(d, qs)
+        ref, t = q8_brute(tab, ne0, ids), R.Q8_0
+        np.testing.assert_array_equal(bits(F.q8_0_dequant(tab, ne0)[ids]), bits(ref))
+    got = R.run(lambda g: g.get_rows(tab, t, ne0, ids))
+    np.testing.assert_array_equal(bits(got), bits(ref))
+
+
+def test_get_rows_rejects_out_of_range():
+    tab = np.zeros((4, 32), np.float32)
+    with pytest.raises(RuntimeError):
+        R.run(lambda g: g.get_rows(tab, R.F32, 32, np.array([4], np.int32)))
+
+
+def test_q8_0_pack_roundtrip_and_quantizer():
+    rng = np.random.default_rng(3)
+    raw = F.q8_0_synthetic(rng, 7, 256)
+    d, qs = F.q8_0_unpack(raw, 256)
+    np.testing.assert_array_equal(F.q8_0_pack(d, qs), raw)
+    x = rng.standard_normal((5, 256)).astype(np.float32)
+    qraw = F.q8_0_quantize(x)
+    deq = F.q8_0_dequant(qraw, 256)
+    dd = F.f16_bits_to_f32(F.q8_0_unpack(qraw, 256)[0])
+    assert (np.abs(deq - x).reshape(5, 8, 32) <= 0.51 * dd[:, :, None] + 1e-3 * np.abs(x).max()).all()
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm
+# ---------------------------------------------------------------------------
+
+def test_rms_norm_invariants():
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((64, 1024)).astype(np.float32)
+    y = R.run(lambda g: g.rms_norm(x, np.float32(0.0)))
+    # unit mean square
+    assert np.abs((y.astype(np.float64) ** 2).mean(axis=1) - 1).max() < 1e-6
+    # with eps = 0 a power-of-two rescale of the row changes nothing, bit for bit
+    y4 = R.run(lambda g: g.rms_norm(x * np.float32(4.0), np.float32(0.0)))
+    np.testing.assert_array_equal(bits(y), bits(y4))
+    # against the textbook double form: within 2 ulp
+    ref = x / np.sqrt((x.astype(np.float64) ** 2).mean(axis=1, keepdims=True))
+    assert (np.abs(y - ref) <= 2 * ULP * np.abs(ref) + 1e-30).all()
+    # zero row: scale 1/sqrt(eps) times 0; constant row: c / sqrt(c^2 + eps)
+    z = R.run(lambda g: g.rms_norm(np.zeros((1, 64), np.float32), np.float32(1e-6)))
+    assert (z == 0).all()
+    c = np.full((1, 64), 0.5, np.float32)
+    yc = R.run(lambda g: g.rms_norm(c, np.float32(1e-6)))
+    assert abs(float(yc[0, 0]) - 0.5 / math.sqrt(0.25 + 1e-6)) < 2 * ULP
+
+
+def test_rms_norm_eps_is_inside_the_sqrt():
+    x = np.full((1, 16), 1e-3, np.float32)
+    eps = np.float32(1e-6)
+    y = R.run(lambda g: g.rms_norm(x, eps))[0, 0]
+    inside = 1e-3 / math.sqrt(1e-6 + 1e-6)
+    outside = 1e-3 / (math.sqrt(1e-6) + 1e-6)
+    assert abs(y - inside) < 1e-5 < abs(y - outside)
+
+
+# ---------------------------------------------------------------------------
+# rope
+# ---------------------------------------------------------------------------
+
+def _theta_recurrence(p, i, base, n_dims):
+    ts = np.float32(base) ** np.float32(-2.0 / n_dims)
+    ts = np.float32(math.pow(np.float32(base), np.float32(-2.0) / np.float32(n_dims)))
+    th = np.float32(p)
+    for _ in range(i):
+        th = np.float32(th * ts)
+    return th, ts
+
+
+def test_rope_identities_and_double_closed_form():
+    rng = np.random.default_rng(6)
+    T, H, hd = 24, 3, 128
+    x = rng.standard_normal((T, H, hd)).astype(np.float32)
+    pos = np.concatenate([[0], rng.integers(1, 8192, T - 1)]).astype(np.int32)
+    y = R.run(lambda g: g.rope_neox(x, pos, hd, np.float32(1e6)))
+    np.testing.assert_array_equal(bits(y[0]), bits(x[0]))  # p = 0 is the identity
+    half = hd // 2
+    n_in = np.hypot(x[..., :half].astype(np.float64), x[..., half:])
+    n_out = np.hypot(y[..., :half].astype(np.float64), y[..., half:])
+    assert np.abs(n_out - n_in).max() <= 4 * ULP * n_in.max()  # rotation keeps each pair's length
+    for t in range(1, T):
+        for i in (0, 1, 7, 31, 63):
+            th, _ = _theta_recurrence(int(pos[t]), i, 1e6, hd)
+            c, s = math.cos(float(th)), math.sin(float(th))
+            x0, x1 = x[t, :, i].astype(np.float64), x[t, :, i + half].astype(np.float64)
+            scale = np.maximum(np.abs(x0), np.abs(x1))
+            assert (np.abs(y[t, :, i] - (x0 * c - x1 * s)) <= 4 * ULP * scale).all()
+            assert (np.abs(y[t, :, i + half] - (x0 * s + x1 * c)) <= 4 * ULP * scale).all()
+
+
+def test_rope_recurrence_is_not_the_pow_form_at_large_positions():
+    """ggml-CPU's cache multiplies theta by theta_scale once per pair in f32; a
+    pos*theta_scale^i evaluation drifts from it by ~1 ulp per step, which at
+    p = 8191 is far outside 1e-5 -- so the restatement (and the kernel) must
+    replay the recurrence."""
+    p, n_dims, base = 8191, 128, 1e6
+    half = n_dims // 2
+    x = np.zeros((half, 1, n_dims), np.float32)
+    for i in range(half):
+        x[i, 0, i] = 1.0  # row i probes pair i: y[i] = cos(theta_i)
+    y = R.run(lambda g: g.rope_neox(x, np.full(half, p, np.int32), n_dims, np.float32(base)))
+    gap = 0.0
+    for i in range(half):
+        th_rec, ts = _theta_recurrence(p, i, base, n_dims)
+        th_pow = np.float32(np.float32(p) * np.float32(math.pow(float(ts), i)))
+        assert abs(y[i, 0, i] - math.cos(float(th_rec))) < 1e-6
+        gap = max(gap, abs(math.cos(float(th_rec)) - math.cos(float(th_pow))))
+    assert gap > 1e-5
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU, Snake, leaky
+# ---------------------------------------------------------------------------
+
+def test_swiglu_double_closed_form():
+    rng = np.random.default_rng(8)
+    g_ = (rng.standard_normal((16, 3072)) * 5).astype(np.float32)
+    u = rng.standard_normal((16, 3072)).astype(np.float32)
+    y = R.run(lambda g: R.swiglu(g, g_, u))
+    gd = g_.astype(np.float64)
+    ref = gd / (1 + np.exp(-gd)) * u
+    assert (np.abs(y - ref) <= 4 * ULP * np.abs(ref) + 1e-37).all()
+    yg = R.run(lambda g: g.glu_swiglu(np.concatenate([g_, u], axis=1), False))
+    np.testing.assert_array_equal(bits(yg), bits(y))
+    ys = R.run(lambda g: g.glu_swiglu(np.concatenate([u, g_], axis=1), True))
+    np.testing.assert_array_equal(bits(ys), bits(y))
+
+
+def test_snake_double_closed_form():
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((100, 64)).astype(np.float32)
+    a = np.exp(rng.uniform(np.log(0.1), np.log(10), 64)).astype(np.float32)
+    y = R.run(lambda g: R.snake(g, x, a))
+    ad = a.astype(np.float64)
+    ref = x + np.sin(ad * x) ** 2 / ad
+    assert (np.abs(y - ref) <= 8 * ULP * np.maximum(np.abs(ref), 1e-3)).all()
+
+
+def test_leaky_relu_signed_zero_and_nan():
+    x = np.array([[-0.0, 0.0, np.nan, -np.nan, np.inf, -np.inf, -1e-45, 2.5, -2.5, -3e-39]], np.float32)
+    y = R.run(lambda g: g.leaky_relu(x, np.float32(0.1)))[0]
+    assert y[0] == 0 and not np.signbit(y[0])  # -0 -> +0
+    assert y[2] == 0 and y[3] == 0  # NaN -> 0
+    assert y[4] == np.inf and y[5] == -np.inf
+    assert y[6] == 0 and not np.signbit(y[6])  # 0.1 * -1e-45 underflows to -0, then 0 + -0 = +0
+    assert y[7] == np.float32(2.5) and y[8] == np.float32(-0.25)
+    assert y[9] == np.float32(np.float32(0.1) * np.float32(-3e-39))
+    # a max(x, slope*x) formulation differs exactly on those cases
+    alt = np.maximum(x[0], np.float32(0.1) * x[0])
+    assert np.signbit(alt[0]) or np.isnan(alt[2])
+
+
+# ---------------------------------------------------------------------------
+# the ggml-style thread split does not change results
+# ---------------------------------------------------------------------------
+
+def _step_graph(rng, T=64):
+    x = rng.standard_normal((T, 1024)).astype(np.float32)
+    w = F.f32_to_bf16_bits(rng.normal(1, 0.1, 1024))
+    q = rng.standard_normal((T, 16, 128)).astype(np.float32)
+    k = rng.standard_normal((T, 8, 128)).astype(np.float32)
+    wq = F.f32_to_bf16_bits(rng.normal(1, 0.1, 128))
+    pos = rng.integers(0, 8192, T).astype(np.int32)
+    gt = rng.standard_normal((T, 3072)).astype(np.float32)
+    tab = F.q8_0_synthetic(rng, 100, 1024)
+    codes = rng.integers(0, 100, (3, T)).astype(np.int32)
+    a = rng.standard_normal((T, 512)).astype(np.float32)
+    al = np.exp(rng.uniform(-2, 2, 512)).astype(np.float32)
+
+    def build(g):
+        return [R.rms_norm_w(g, x, w, np.float32(1e-6), R.BF16),
+                *R.qk_norm_rope(g, q, k, wq, wq, np.float32(1e-6), pos, 128, np.float32(1e6), R.BF16),
+                R.swiglu(g, gt, gt), R.sum_code_embeddings(g, [tab] * 3, R.Q8_0, 1024, codes),
+                R.snake(g, a, al), R.add_leaky(g, a, a, np.float32(0.1))[1]]
+    return build
+
+
+def test_thread_split_invariance():
+    build = _step_graph(np.random.default_rng(10))
+    one = R.run(build, n_threads=1)
+    for nth in (3, 8):
+        many = R.run(build, n_threads=nth)
+        for a, b in zip(one, many):
+            np.testing.assert_array_equal(bits(a), bits(b))

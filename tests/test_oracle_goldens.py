@@ -1,0 +1,217 @@
+"""Pins the ggml-CPU restatement against the reference's own golden vectors.
+
+G1: tests/qwen3_tts_decoder_layer_test.cpp:42-47 (a whole Qwen3 block, prefill
+    then cached step) -- pins rms_norm eps placement, QK-norm before rope, NEOX
+    half pairing, theta, silu*up and both residual adds.
+G2: tests/qwen3_tts_code_predictor_test.cpp:46-61 (two-layer predictor logits,
+    greedy codes, and the ordered multi-codebook embedding sum).
+G3: tests/qwen3_tts_codec_ops_test.cpp:77-82 (SnakeBeta: the sin^2 Snake family
+    through exp, sin, sqr, scale_bias, div and add nodes).
+G4: tests/kokoro_decoder_test.cpp:81-90 (double-precision host Snake, layout
+    t*C + c).
+Each test also plants a plausible mistake in the restatement's composition and
+checks that the golden rejects it, so the golden is shown to constrain the
+part it is claimed to pin.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import ggml_ref as R
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _load(name):
+    with open(os.path.join(GOLDEN, name)) as f:
+        return json.load(f)
+
+
+def _shape(d):
+    return {"head_dim": d["head_dim"], "heads": d["heads"], "kv_heads": d["kv_heads"],
+            "rms_norm_eps": np.float32(d["rms_norm_eps"]), "rope_theta": np.float32(d["rope_theta"])}
+
+
+def _causal(n):
+    m = np.zeros((n, n), dtype=np.float32)
+    m[np.triu_indices(n, 1)] = -np.inf
+    return m
+
+
+def run_decoder_golden(d, ops=None):
+    s = R.LcgStream(d["seed"])
+    W = R.layer_weights(s, d["hidden"], d["heads"], d["kv_heads"], d["head_dim"], d["intermediate"])
+    P, pre, H = d["positions"], d["prefill"], d["hidden"]
+    hidden = s.fill(P * H, 0.5, 0.0).reshape(P, H)
+    cache = {"k": np.zeros((P, d["kv_heads"], d["head_dim"]), np.float32),
+             "v": np.zeros((P, d["kv_heads"], d["head_dim"]), np.float32)}
+    shape = _shape(d)
+    out_pre = R.decoder_layer(hidden[:pre], np.arange(pre, dtype=np.int32), _causal(pre), W, shape, cache, 0, ops)
+    out_step = R.decoder_layer(hidden[pre:], np.array([pre], np.int32), None, W, shape, cache, pre, ops)
+    return np.concatenate([out_pre, out_step]).reshape(-1)
+
+
+def test_g1_decoder_layer():
+    d = _load("qwen3_decoder_layer.json")
+    got = run_decoder_golden(d)
+    diff = np.abs(got - np.array(d["expected_hidden"], np.float32)).max()
+    assert diff < d["tolerance_cpu"], diff
+
+
+class _GptjRope(R.OracleOps):
+    """Planted mistake: interleaved (GPT-J) pairing instead of NEOX halves."""
+
+    def qk_norm_rope(self, q, k, wq, wk, eps, pos, n_dims, theta):
+        qn = R.run(lambda g: R.rms_norm_w(g, q, wq, eps))
+        kn = R.run(lambda g: R.rms_norm_w(g, k, wk, eps))
+
+        def gptj(x):
+            y = x.copy()
+            ts = np.float32(theta) ** np.float32(-2.0 / n_dims)
+            for t, p in enumerate(pos):
+                th = np.float32(p)
+                for i in range(n_dims // 2):
+                    c, s_ = np.float32(np.cos(th)), np.float32(np.sin(th))
+                    x0, x1 = x[t, :, 2 * i], x[t, :, 2 * i + 1]
+                    y[t, :, 2 * i], y[t, :, 2 * i + 1] = x0 * c - x1 * s_, x0 * s_ + x1 * c
+                    th = np.float32(th * ts)
+            return y
+        return gptj(qn), gptj(kn)
+
+
+class _NormAfterRope(R.OracleOps):
+    """Planted mistake: rope before the per-head norm."""
+
+    def qk_norm_rope(self, q, k, wq, wk, eps, pos, n_dims, theta):
+        qr = R.run(lambda g: g.rope_neox(q, pos, n_dims, theta))
+        kr = R.run(lambda g: g.rope_neox(k, pos, n_dims, theta))
+        return (R.run(lambda g: R.rms_norm_w(g, qr, wq, eps)), R.run(lambda g: R.rms_norm_w(g, kr, wk, eps)))
+
+
+class _EpsOutsideSqrt(R.OracleOps):
+    """Planted mistake: eps added after the square root (1/(sqrt(mean)+eps))."""
+
+    def rms_norm_w(self, x, w, eps):
+        ms = (x.astype(np.float64) ** 2).mean(axis=-1, keepdims=True)
+        return (x / (np.sqrt(ms) + 1e-2)).astype(np.float32) * w
+
+
+class _SiluOnUp(R.OracleOps):
+    """Planted mistake: silu applied to the up projection instead of the gate."""
+
+    def swiglu(self, gate, up):
+        return R.run(lambda g: R.swiglu(g, up, gate))
+
+
+@pytest.mark.parametrize("ops", [_GptjRope(), _NormAfterRope(), _EpsOutsideSqrt(), _SiluOnUp()],
+                         ids=["gptj-pairing", "norm-after-rope", "eps-outside-sqrt", "silu-on-up"])
+def test_g1_rejects_planted_mistakes(ops):
+    d = _load("qwen3_decoder_layer.json")
+    got = run_decoder_golden(d, ops)
+    diff = np.abs(got - np.array(d["expected_hidden"], np.float32)).max()
+    assert diff > 10 * d["tolerance_cpu"], diff
+
+
+def run_code_predictor(d, reverse_sum=False):
+    s = R.LcgStream(d["seed"])
+    H, V, G = d["hidden"], d["vocab"], d["code_groups"]
+    layers = [R.layer_weights(s, H, d["heads"], d["kv_heads"], d["head_dim"], d["intermediate"])
+              for _ in range(d["layers"])]
+    norm = s.fill(H, 0.25, 1.0)
+    tables = [s.fill(V * H, 0.5, 0.0).reshape(V, H) for _ in range(G - 1)]
+    heads = [s.fill(V * H, 0.5, 0.0).reshape(V, H) for _ in range(G - 1)]
+    prefill = s.fill(2 * H, 0.5, 0.0).reshape(2, H)
+    shape = _shape(d)
+    caches = [{"k": np.zeros((G, d["kv_heads"], d["head_dim"]), np.float32),
+               "v": np.zeros((G, d["kv_heads"], d["head_dim"]), np.float32)} for _ in layers]
+    logits_all, codes, filled = [], [], 0
+    # code_predictor_schedule, src/arch/qwen3-tts/code-predictor-host.cpp:15-42
+    schedule = [(None, 0, 0, 2)] + [(g - 1, g, g + 1, 1) for g in range(1, G - 1)]
+    for table, head, first, count in schedule:
+        if table is None:
+            x, pos, mask = prefill, np.array([0, 1], np.int32), _causal(2)
+        else:
+            x = R.OracleOps().get_rows(tables[table], np.array([codes[-1]], np.int32))
+            pos, mask = np.array([first], np.int32), None
+        assert first == filled
+        for W, cache in zip(layers, caches):
+            x = R.decoder_layer(x, pos, mask, W, shape, cache, filled)
+        x = R.run(lambda g: R.rms_norm_w(g, x, norm, shape["rms_norm_eps"]))
+        logits = R.mul_mat(heads[head], x[-1:])[0]
+        logits_all.append(logits)
+        codes.append(int(np.argmax(logits)))
+        filled += count
+    order = list(range(G - 1))
+    if reverse_sum:
+        order = order[::-1]
+    code_ids = np.array([[codes[t]] for t in order], np.int32)
+    summed = R.run(lambda g: R.sum_code_embeddings(g, [tables[t] for t in order], R.F32, H, code_ids))
+    return np.concatenate(logits_all), codes, summed.reshape(-1), tables
+
+
+def test_g2_code_predictor_logits_codes_and_sum():
+    d = _load("qwen3_code_predictor.json")
+    logits, codes, summed, _ = run_code_predictor(d)
+    assert codes == d["expected_codes"]
+    assert np.abs(logits - np.array(d["expected_logits"], np.float32)).max() < d["tolerance_cpu"]
+    assert np.abs(summed - np.array(d["expected_summed_embedding"], np.float32)).max() < d["tolerance_cpu"]
+
+
+def test_g2_sum_is_ordered_and_table_specific():
+    """The summed embedding pins which table each group reads: reading every
+    code through table 0 misses the golden."""
+    d = _load("qwen3_code_predictor.json")
+    _, codes, _, tables = run_code_predictor(d)
+    wrong = R.run(lambda g: R.sum_code_embeddings(g, [tables[0]] * len(codes), R.F32, d["hidden"],
+                                                  np.array([[c] for c in codes], np.int32)))
+    assert np.abs(wrong.reshape(-1) - np.array(d["expected_summed_embedding"], np.float32)).max() > 1e-2
+
+
+def snake_beta_inputs(d):
+    s = R.LcgStream(d["seed"])
+    C, L = d["channels"], d["length"]
+    raw = s.fill(C * L, 0.5, 0.0)
+    x = np.ascontiguousarray(raw.reshape(C, L).T)  # [C, L] channels fastest = numpy (L, C)
+    for name, count in d["draws_before_alpha"].items():
+        if name != "signal":
+            s.fill(count, 1.0, 0.0)
+    alpha = s.fill(C, 0.5, 0.0)
+    beta = s.fill(C, 0.5, 0.0)
+    return x, alpha, beta
+
+
+def test_g3_snake_beta():
+    d = _load("qwen3_codec_snake_beta.json")
+    x, a, b = snake_beta_inputs(d)
+    got = R.run(lambda g: R.snake_beta(g, x, a, b)).reshape(-1)
+    assert np.abs(got - np.array(d["expected_snake_beta"], np.float32)).max() < d["tolerance_cpu"]
+
+
+def test_g3_rejects_guard_and_layout_mistakes():
+    d = _load("qwen3_codec_snake_beta.json")
+    x, a, b = snake_beta_inputs(d)
+    exp = np.array(d["expected_snake_beta"], np.float32)
+    # alpha in the denominator instead of beta
+    wrong = R.run(lambda g: g.add(x, g.div(g.sqr(g.sin(g.mul(x, g.exp(a)))), g.exp(a)))).reshape(-1)
+    assert np.abs(wrong - exp).max() > 1e-2
+    # time-fastest layout (coefficients applied along the wrong axis)
+    xt = np.ascontiguousarray(x.T)
+    wrong = R.run(lambda g: R.snake_beta(g, xt, np.resize(a, xt.shape[1]), np.resize(b, xt.shape[1])))
+    assert np.abs(wrong.T.reshape(-1) - exp).max() > 1e-2
+
+
+def test_g4_kokoro_snake_matches_double_host_reference():
+    """reference_snake, tests/kokoro_decoder_test.cpp:81-90: y = x + sin(a x)^2 / a in
+    double on [C, T] (element (c, t) at t*C + c); compared at the test's 1e-4."""
+    rng = np.random.default_rng(20260728)
+    C, T = 16, 37
+    x = rng.standard_normal((T, C)).astype(np.float32)
+    alpha = np.exp(rng.uniform(np.log(0.1), np.log(10.0), C)).astype(np.float32)
+    got = R.run(lambda g: R.snake(g, x, alpha))
+    a = alpha.astype(np.float64)
+    ref = x + np.sin(a * x) ** 2 / a
+    assert np.abs(got - ref).max() < 1e-4
+    # f32 node-by-node rounding stays within a few ulp of the double form
+    assert np.abs(got - ref).max() < 8 * np.finfo(np.float32).eps * np.abs(ref).max()
