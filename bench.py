@@ -27,6 +27,7 @@ timed on this host (ggml-style thread split), as a baseline only.
 """
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -48,6 +49,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=40)
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--suite", metavar="JSON", help="instead: measure every op on every BASELINE config "
+                   "(cold-cache protocol), print a markdown table and write the figures to JSON")
+    p.add_argument("--only", default="", help="with --suite: comma-separated config names to run")
     return p.parse_args()
 
 
@@ -221,6 +225,178 @@ def cpu_baseline(step, torch, seconds):
     }
 
 
+# ---------------------------------------------------------------------------
+# --suite: every op on every BASELINE config
+# ---------------------------------------------------------------------------
+
+def measure_op(torch, make, nbytes, reps_target=200, cold=True):
+    """Average launch duration (µs) of the op built by make() -> callable, over
+    enough rotating input sets to exceed COLD_BYTES (cold=False: one set,
+    cache resident), replayed from one graph."""
+    nsets = 1 if (nbytes >= COLD_BYTES or not cold) else -(-COLD_BYTES // nbytes) + 1
+    nsets = min(nsets, 4096)
+    fns = [make() for _ in range(nsets)]
+    for f in fns:
+        f()
+    if nsets == 1:
+        fns = fns * (4 if cold else 256)  # warm: enough nodes to amortise the graph launch
+    graph = capture(torch, fns)
+    time_graphs(torch, [graph], 2)
+    reps = max(2, reps_target // len(fns))
+    us = time_graphs(torch, [graph], reps) * 1e3 / (reps * len(fns))
+    del graph, fns
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return us, nsets
+
+
+def suite(args, S, torch):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(SEED + 7)
+    randn = lambda *shape: torch.randn(shape, generator=g, device="cuda", dtype=torch.float32)
+    empty = lambda *shape: torch.empty(shape, device="cuda", dtype=torch.float32)
+    bf16 = lambda n: (1.0 + 0.1 * randn(n)).to(torch.bfloat16)
+    f32 = 4
+    rows = []
+
+    def run(cfg, name, nbytes, make, note="", cold=True):
+        us, nsets = measure_op(torch, make, nbytes, cold=cold)
+        if not cold:
+            note = ("warm " + note).strip()
+        gbs = nbytes / (us * 1e-6) / 1e9
+        rows.append({"config": cfg, "op": name, "bytes": nbytes, "us": round(us, 3), "GB/s": round(gbs, 1),
+                     "frac": round(gbs / PEAK_GBS, 4), "sets": nsets, "note": note})
+        print("%-5s %-38s %12d B %9.3f us %8.1f GB/s %6.1f%%  sets=%d %s" % (cfg, name, nbytes, us, gbs,
+                                                                            100 * gbs / PEAK_GBS, nsets, note),
+              flush=True)
+
+    want = set(filter(None, args.only.split(",")))
+    on = lambda c: not want or c in want
+
+    if on("calib"):
+        # what a plain device copy and a read-only reduction reach on this box
+        n = (1 << 30) // 4
+        src, dst = randn(n), empty(n)
+        acc = torch.empty((), device="cuda", dtype=torch.float32)
+        run("calib", "torch copy_ 1 GiB (read+write)", 2 * n * 4, lambda: (lambda: dst.copy_(src)))
+        run("calib", "torch sum 1 GiB (read only)", n * 4, lambda: (lambda: torch.sum(src, dim=0, out=acc)))
+        del src, dst
+
+    def norm_case(cfg, T, H, add=False, wsum=True, cold=True):
+        def make():
+            a, b, w, y, s = randn(T, H), randn(T, H), bf16(H), empty(T, H), empty(T, H)
+            if add:
+                return lambda: S.add_rms_norm_mul(a, b, w, 1e-6, out=y, sum_out=s if wsum else None,
+                                                  want_sum=wsum)
+            return lambda: S.rms_norm_mul(a, w, 1e-6, out=y)
+        n = (4 if wsum else 3) if add else 2
+        run(cfg, ("add_rms_norm_mul%s [%d,%d]" % ("+sum" if wsum else "", H, T)) if add else
+            "rms_norm_mul [%d,%d]" % (H, T), n * T * H * f32 + H * 2, make, cold=cold)
+
+    def qk_case(cfg, T, hi, cold=True):
+        def make():
+            q, k = randn(T, 16, 128), randn(T, 8, 128)
+            qo, ko = torch.empty_like(q), torch.empty_like(k)
+            wq, wk = bf16(128), bf16(128)
+            pos = torch.randint(0, hi, (T,), generator=g, device="cuda", dtype=torch.int32)
+            return lambda: S.qk_norm_rope(q, k, wq, wk, 1e-6, pos, 128, 1e6, q_out=qo, k_out=ko)
+        run(cfg, "qk_norm_rope q[128,16,%d] k[128,8,%d]" % (T, T), 2 * 24 * 128 * T * f32 + T * 4 + 512, make,
+            cold=cold)
+
+    def swiglu_case(cfg, T, F_, cold=True):
+        def make():
+            a, b, y = randn(T, F_), randn(T, F_), empty(T, F_)
+            return lambda: S.swiglu(a, b, out=y)
+        run(cfg, "swiglu [%d,%d]" % (F_, T), 3 * T * F_ * f32, make, cold=cold)
+
+    def add_case(cfg, T, H, cold=True):
+        def make():
+            a, b, y = randn(T, H), randn(T, H), empty(T, H)
+            return lambda: S.add(a, b, out=y)
+        run(cfg, "add [%d,%d]" % (H, T), 3 * T * H * f32, make, cold=cold)
+
+    if on("cfg1"):
+        def make_tiny():
+            a, b = randn(1), empty(1)
+            return lambda: torch.add(a, a, out=b)
+        run("cfg1", "graph launch floor (torch 1-element add)", 12, make_tiny, cold=False)
+        for cold in (True, False):
+            norm_case("cfg1", 1, 1024, cold=cold)
+            norm_case("cfg1", 1, 1024, add=True, cold=cold)
+            qk_case("cfg1", 1, 64, cold=cold)
+            swiglu_case("cfg1", 1, 3072, cold=cold)
+            add_case("cfg1", 1, 1024, cold=cold)
+        us = decode_layer_us(S, torch)
+        rows.append({"config": "cfg1", "op": "talker layer non-GEMM step (28-layer graph, 4 launches/layer)",
+                     "us": round(us, 3), "note": "per layer"})
+        print("cfg1  decode layer non-GEMM step: %.3f us/layer" % us, flush=True)
+
+    if on("cfg2"):
+        norm_case("cfg2", 512, 1024)
+        qk_case("cfg2", 512, 512)
+        norm_case("cfg2", 512, 1024, add=True)
+        swiglu_case("cfg2", 512, 3072)
+        add_case("cfg2", 512, 1024)
+        table = (0.02 * randn(151936, 2048)).to(torch.bfloat16)
+
+        def make_gather():
+            ids = torch.randint(0, 151936, (512,), generator=g, device="cuda", dtype=torch.int32)
+            out = empty(512, 2048)
+            return lambda: S.get_rows(table, ids, out=out)
+        run("cfg2", "get_rows bf16 [2048,151936] x512", 512 * (4 + 2048 * 2 + 2048 * f32), make_gather)
+        del table
+
+    if on("cfg3"):
+        import numpy as np
+        import formats as F
+        rng = np.random.default_rng(SEED + 3)
+        tabs = [S.Q8Tensor(torch.from_numpy(F.q8_0_synthetic(rng, 2048, 1024)).cuda(), 1024) for _ in range(16)]
+        row = 1024 // 32 * 34
+
+        def make_sum():
+            codes = torch.randint(0, 2048, (16, 4096), generator=g, device="cuda", dtype=torch.int32)
+            out = empty(4096, 1024)
+            return lambda: S.get_rows_sum(tabs, codes, out=out)
+        run("cfg3", "get_rows_sum q8_0 16x[1024,2048] x4096", 4096 * (16 * (row + 4) + 1024 * f32), make_sum,
+            "logical bytes; compulsory ~47.9 MB")
+
+        def make_q8():
+            ids = torch.randint(0, 2048, (4096,), generator=g, device="cuda", dtype=torch.int32)
+            out = empty(4096, 1024)
+            return lambda: S.get_rows(tabs[0], ids, out=out)
+        run("cfg3", "get_rows q8_0 [1024,2048] x4096", 4096 * (row + 4 + 1024 * f32), make_q8,
+            "logical bytes; compulsory ~19.1 MB")
+        del tabs
+
+    if on("cfg4"):
+        for C, T in ((512, 8192), (256, 32768), (128, 131072)):
+            n = C * T
+
+            def make_snake(C=C, T=T):
+                x, y = randn(T, C), empty(T, C)
+                al = torch.exp(torch.empty(C, device="cuda").uniform_(math.log(0.1), math.log(10.0), generator=g))
+                return lambda: S.snake(x, al, out=y)
+            run("cfg4", "snake [%d,%d]" % (C, T), 8 * n + 4 * C, make_snake)
+
+            def make_leaky(C=C, T=T, with_s=False):
+                a, b, y, s = randn(T, C), randn(T, C), empty(T, C), empty(T, C)
+                return lambda: S.add_leaky_relu(a, b, 0.1, out=y, sum_out=s if with_s else None)
+            run("cfg4", "add_leaky_relu [%d,%d]" % (C, T), 12 * n, make_leaky)
+            run("cfg4", "add_leaky_relu+sum [%d,%d]" % (C, T), 16 * n, lambda: make_leaky(with_s=True))
+
+    if on("cfg5"):
+        norm_case("cfg5", 8192, 2048)
+        norm_case("cfg5", 8192, 2048, add=True)
+        qk_case("cfg5", 8192, 8192)
+        swiglu_case("cfg5", 8192, 6144)
+        norm_case("cfg5", 64, 1024, add=True)
+        qk_case("cfg5", 64, 8192)
+        swiglu_case("cfg5", 64, 3072)
+
+    with open(args.suite, "w") as f:
+        json.dump({"peak_GBps": PEAK_GBS, "cold_bytes": COLD_BYTES, "rows": rows}, f, indent=1)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -232,6 +408,9 @@ def main():
 
     torch.cuda.set_device(0)
     S.load()
+    if args.suite:
+        suite(args, S, torch)
+        return
     step = PrefillStep(S, torch)
 
     # eager run of every op of every set (loads the code objects before capture)

@@ -15,6 +15,7 @@
 #include <cmath>
 
 #include "shp_internal.hpp"
+#include "shp_trig.hpp"
 
 namespace shp {
 namespace {
@@ -67,6 +68,15 @@ template <int LPR, int VPL, int WT, int MODE> __global__ __launch_bounds__(256) 
     for (int k = 0; k < VPL; ++k) {
         v[k] = xp[k * LPR + l];
     }
+    // The gains are loaded with the row, not after the reduction, so the kernel
+    // waits on one memory round trip, not two.
+    float4 wv[VPL];
+    if constexpr (WT != kWNone) {
+#pragma unroll
+        for (int k = 0; k < VPL; ++k) {
+            wv[k] = load_w4<WT>(a.w, static_cast<int64_t>(k * LPR + l) * 4);
+        }
+    }
     if constexpr (MODE != kPlain) {
         const float4 * bp =
             reinterpret_cast<const float4 *>(reinterpret_cast<const char *>(a.b) + row_offset(a.bm, row));
@@ -99,8 +109,7 @@ template <int LPR, int VPL, int WT, int MODE> __global__ __launch_bounds__(256) 
     for (int k = 0; k < VPL; ++k) {
         float4 o = make_float4(v[k].x * scale, v[k].y * scale, v[k].z * scale, v[k].w * scale);
         if constexpr (WT != kWNone) {
-            const float4 w4 = load_w4<WT>(a.w, static_cast<int64_t>(k * LPR + l) * 4);
-            o               = make_float4(o.x * w4.x, o.y * w4.y, o.z * w4.z, o.w * w4.w);
+            o = make_float4(o.x * wv[k].x, o.y * wv[k].y, o.z * wv[k].z, o.w * wv[k].w);
         }
         yp[k * LPR + l] = o;
     }
@@ -294,6 +303,8 @@ struct RopeArgs {
     float           freq_scale;
     float           attn_factor;
     float           eps;
+    int32_t         ppb;  // fast path: positions per block
+    int32_t         pad;
 };
 
 // cos/sin of the pair-k angle at position p: theta is replayed through the f32
@@ -306,86 +317,156 @@ __device__ __forceinline__ void rope_cs(int32_t p, int k, const RopeArgs & a, fl
         theta = theta * a.theta_scale;
     }
     const float th = a.freq_scale * theta;
-    double      sd, cd;
-    sincos(static_cast<double>(th), &sd, &cd);
-    c = static_cast<float>(cd) * a.attn_factor;
-    s = static_cast<float>(sd) * a.attn_factor;
+    float       sf, cf;
+    if (!sincos_f32_rn(th, sf, cf)) {
+        double sd, cd;  // beyond the fast reduction's range (|angle| > 2^19 pi/2)
+        sincos(static_cast<double>(th), &sd, &cd);
+        sf = static_cast<float>(sd);
+        cf = static_cast<float>(cd);
+    }
+    c = cf * a.attn_factor;
+    s = sf * a.attn_factor;
 }
 
-// Fast path: head_dim == n_dims == 128. One block per position; a 32-lane
-// half-wave owns a head row; lane j holds elements {2j, 2j+1} and
-// {64+2j, 65+2j}, i.e. both halves of NEOX pairs 2j and 2j+1, so the rotation
-// needs no data exchange. The 64-entry cos/sin cache of the position is built
-// once per block in LDS while the row loads are in flight.
-template <bool NORM, int WT> __global__ __launch_bounds__(1024) void k_rope128(const RopeArgs a) {
-    __shared__ float s_cos[64];
-    __shared__ float s_sin[64];
+// Fast path: head_dim == n_dims == 128.
+//
+// A head row is owned by 16 lanes; lane j holds x[4j..4j+3] and
+// x[64+4j..64+4j+3] as two float4, i.e. both halves of NEOX pairs 4j..4j+3,
+// so the rotation needs no data exchange and every load is 128-bit. A block
+// (16 row slots) covers `ppb` consecutive positions; each slot prefetches up
+// to kRopeRows of its rows before anything waits, while the block builds the
+// positions' 64-entry cos/sin caches in LDS.
+constexpr int kRopeLanes    = 16;
+constexpr int kRopeSlots    = 256 / kRopeLanes;
+constexpr int kRopeRows     = 4;
+constexpr int kRopeMaxPos   = 4;
 
-    const int64_t pi    = blockIdx.x;
-    const int32_t p     = a.pos[pi];
-    const int     sub   = threadIdx.x / 32;
-    const int     nsub  = blockDim.x / 32;
-    const int     l     = threadIdx.x % 32;
+template <bool NORM, int WT> __global__ __launch_bounds__(256) void k_rope128(const RopeArgs a) {
+    __shared__ float s_cos[kRopeMaxPos][64];
+    __shared__ float s_sin[kRopeMaxPos][64];
+
+    const int64_t p0    = static_cast<int64_t>(blockIdx.x) * a.ppb;
+    const int     np    = static_cast<int>(a.npos - p0 < a.ppb ? a.npos - p0 : a.ppb);
     const int     total = a.part[0].heads + a.part[1].heads;
+    const int     nrows = np * total;
+    const int     slot  = threadIdx.x / kRopeLanes;
+    const int     l     = threadIdx.x % kRopeLanes;
 
-    auto row_ptrs = [&](int hh, const float *& xr, float *& yr, const void *& w) {
-        const int       t  = hh < a.part[0].heads ? 0 : 1;
-        const int       h  = t == 0 ? hh : hh - a.part[0].heads;
+    auto locate = [&](int row, int & pp, const float *& xr, float *& yr, int & t) {
+        pp               = row / total;
+        const int hh     = row - pp * total;
+        t                = hh < a.part[0].heads ? 0 : 1;
+        const int h      = t == 0 ? hh : hh - a.part[0].heads;
         const RopePart & P = a.part[t];
+        const int64_t    pi = p0 + pp;
         xr = reinterpret_cast<const float *>(reinterpret_cast<const char *>(P.x) + h * P.xnb1 + pi * P.xnb2);
         yr = reinterpret_cast<float *>(reinterpret_cast<char *>(P.y) + h * P.ynb1 + pi * P.ynb2);
-        w  = P.w;
     };
 
-    // Issue the first row's loads before the cache is built.
-    float2       lo = make_float2(0.0f, 0.0f), hi = make_float2(0.0f, 0.0f);
-    const float * xr = nullptr;
-    float *       yr = nullptr;
-    const void *  wr = nullptr;
-    if (sub < total) {
-        row_ptrs(sub, xr, yr, wr);
-        lo = reinterpret_cast<const float2 *>(xr)[l];
-        hi = reinterpret_cast<const float2 *>(xr + 64)[l];
-    }
-    if (threadIdx.x < 64) {
-        float c, s;
-        rope_cs(p, threadIdx.x, a, c, s);
-        s_cos[threadIdx.x] = c;
-        s_sin[threadIdx.x] = s;
-    }
-    __syncthreads();
-
-    for (int hh = sub; hh < total; hh += nsub) {
-        if (hh != sub) {
-            row_ptrs(hh, xr, yr, wr);
-            lo = reinterpret_cast<const float2 *>(xr)[l];
-            hi = reinterpret_cast<const float2 *>(xr + 64)[l];
-        }
-        if constexpr (NORM) {
-            double acc = static_cast<double>(lo.x * lo.x);
-            acc += static_cast<double>(lo.y * lo.y);
-            acc += static_cast<double>(hi.x * hi.x);
-            acc += static_cast<double>(hi.y * hi.y);
-            acc               = group_sum<32>(acc);
-            const float scale = norm_scale(acc, 128, a.eps);
-            lo                = make_float2(lo.x * scale, lo.y * scale);
-            hi                = make_float2(hi.x * scale, hi.y * scale);
-            if constexpr (WT != kWNone) {
-                const float2 wl = load_w2<WT>(wr, 2 * l);
-                const float2 wh = load_w2<WT>(wr, 64 + 2 * l);
-                lo              = make_float2(lo.x * wl.x, lo.y * wl.y);
-                hi              = make_float2(hi.x * wh.x, hi.y * wh.y);
+    // Both heads' gains for this lane's eight elements, loaded once up front.
+    float4 wlo[2] = { make_float4(1.f, 1.f, 1.f, 1.f), make_float4(1.f, 1.f, 1.f, 1.f) };
+    float4 whi[2] = { wlo[0], wlo[0] };
+    if constexpr (NORM && WT != kWNone) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            if (a.part[t].heads > 0) {
+                wlo[t] = load_w4<WT>(a.part[t].w, 4 * l);
+                whi[t] = load_w4<WT>(a.part[t].w, 64 + 4 * l);
             }
         }
-        const float c0 = s_cos[2 * l], s0 = s_sin[2 * l];
-        const float c1 = s_cos[2 * l + 1], s1 = s_sin[2 * l + 1];
-        float2      olo, ohi;
-        olo.x = lo.x * c0 - hi.x * s0;
-        ohi.x = lo.x * s0 + hi.x * c0;
-        olo.y = lo.y * c1 - hi.y * s1;
-        ohi.y = lo.y * s1 + hi.y * c1;
-        reinterpret_cast<float2 *>(yr)[l]      = olo;
-        reinterpret_cast<float2 *>(yr + 64)[l] = ohi;
+    }
+
+    auto finish = [&](int pp, float4 lo, float4 hi, float * yr, int t) {
+        if constexpr (NORM) {
+            double acc        = sq4(lo) + sq4(hi);
+            acc               = group_sum<kRopeLanes>(acc);
+            const float scale = norm_scale(acc, 128, a.eps);
+            lo = make_float4(lo.x * scale, lo.y * scale, lo.z * scale, lo.w * scale);
+            hi = make_float4(hi.x * scale, hi.y * scale, hi.z * scale, hi.w * scale);
+            if constexpr (WT != kWNone) {
+                const float4 wl = t == 0 ? wlo[0] : wlo[1];
+                const float4 wh = t == 0 ? whi[0] : whi[1];
+                lo = make_float4(lo.x * wl.x, lo.y * wl.y, lo.z * wl.z, lo.w * wl.w);
+                hi = make_float4(hi.x * wh.x, hi.y * wh.y, hi.z * wh.z, hi.w * wh.w);
+            }
+        }
+        const float * cs = s_cos[pp] + 4 * l;
+        const float * sn = s_sin[pp] + 4 * l;
+        float4        olo, ohi;
+        olo.x = lo.x * cs[0] - hi.x * sn[0];
+        ohi.x = lo.x * sn[0] + hi.x * cs[0];
+        olo.y = lo.y * cs[1] - hi.y * sn[1];
+        ohi.y = lo.y * sn[1] + hi.y * cs[1];
+        olo.z = lo.z * cs[2] - hi.z * sn[2];
+        ohi.z = lo.z * sn[2] + hi.z * cs[2];
+        olo.w = lo.w * cs[3] - hi.w * sn[3];
+        ohi.w = lo.w * sn[3] + hi.w * cs[3];
+        reinterpret_cast<float4 *>(yr)[l]      = olo;
+        reinterpret_cast<float4 *>(yr + 64)[l] = ohi;
+    };
+
+    // 1. issue every prefetched row load of this slot
+    float4  lo[kRopeRows], hi[kRopeRows];
+    int     pps[kRopeRows];
+    int     ts[kRopeRows];
+    float * yrs[kRopeRows];
+#pragma unroll
+    for (int r = 0; r < kRopeRows; ++r) {
+        const int row = slot + r * kRopeSlots;
+        pps[r]        = 0;
+        ts[r]         = 0;
+        yrs[r]        = nullptr;
+        if (row < nrows) {
+            const float * xr;
+            locate(row, pps[r], xr, yrs[r], ts[r]);
+            lo[r] = reinterpret_cast<const float4 *>(xr)[l];
+            hi[r] = reinterpret_cast<const float4 *>(xr + 64)[l];
+        }
+    }
+    // 2. the positions' cos/sin caches, meanwhile: lane 0 of wave pp replays
+    //    position pp's f32 theta recurrence (inherently serial), then 64 lanes
+    //    per position evaluate cos/sin in parallel.
+    if (threadIdx.x % kWave == 0 && static_cast<int>(threadIdx.x / kWave) < np) {
+        const int pp = threadIdx.x / kWave;
+        float     th = static_cast<float>(a.pos[p0 + pp]);
+#pragma unroll
+        for (int k = 0; k < 64; ++k) {
+            s_sin[pp][k] = a.freq_scale * th;  // angle k, overwritten by its sine below
+            th           = th * a.theta_scale;
+        }
+    }
+    __syncthreads();
+    float cv = 0.0f, sv = 0.0f;
+    const int epp = threadIdx.x / 64, ek = threadIdx.x % 64;
+    if (epp < np) {
+        const float th = s_sin[epp][ek];
+        if (!sincos_f32_rn(th, sv, cv)) {
+            double sd, cd;
+            sincos(static_cast<double>(th), &sd, &cd);
+            sv = static_cast<float>(sd);
+            cv = static_cast<float>(cd);
+        }
+    }
+    __syncthreads();
+    if (epp < np) {
+        s_cos[epp][ek] = cv * a.attn_factor;
+        s_sin[epp][ek] = sv * a.attn_factor;
+    }
+    __syncthreads();
+    // 3. normalise, rotate, store
+#pragma unroll
+    for (int r = 0; r < kRopeRows; ++r) {
+        if (slot + r * kRopeSlots < nrows) {
+            finish(pps[r], lo[r], hi[r], yrs[r], ts[r]);
+        }
+    }
+    // rows past the prefetch window (only when a position has > 64 head rows)
+    for (int row = slot + kRopeRows * kRopeSlots; row < nrows; row += kRopeSlots) {
+        int           pp, t;
+        const float * xr;
+        float *       yr;
+        locate(row, pp, xr, yr, t);
+        finish(pp, reinterpret_cast<const float4 *>(xr)[l], reinterpret_cast<const float4 *>(xr + 64)[l], yr, t);
     }
 }
 
@@ -443,12 +524,8 @@ template <bool NORM, int WT> __global__ __launch_bounds__(256) void k_rope_gener
 template <bool NORM, int WT> shp_status_t launch_rope(const RopeArgs & a, bool fast, hipStream_t stream) {
     const int total = a.part[0].heads + a.part[1].heads;
     if (fast) {
-        int threads = 32 * total;
-        threads     = (threads + 63) / 64 * 64;
-        if (threads > 1024) {
-            threads = 1024;
-        }
-        hipLaunchKernelGGL((k_rope128<NORM, WT>), dim3(static_cast<unsigned>(a.npos)), dim3(threads), 0, stream, a);
+        const int64_t blocks = (a.npos + a.ppb - 1) / a.ppb;
+        hipLaunchKernelGGL((k_rope128<NORM, WT>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
         return launch_status();
     }
     const int64_t rows   = a.npos * total;
@@ -479,7 +556,12 @@ bool rope_part_ok(const shp_tensor * x, const shp_tensor * y) {
 }
 
 bool part_aligned(const shp_tensor & t) {
-    return reinterpret_cast<uintptr_t>(t.data) % 8 == 0 && t.nb[1] % 8 == 0 && t.nb[2] % 8 == 0;
+    return reinterpret_cast<uintptr_t>(t.data) % 16 == 0 && t.nb[1] % 16 == 0 && t.nb[2] % 16 == 0;
+}
+
+// float4 gain loads: 16-byte aligned F32, 8-byte aligned BF16/F16.
+bool gain_aligned(const shp_tensor * w) {
+    return w == nullptr || reinterpret_cast<uintptr_t>(w->data) % (w->type == SHP_TYPE_F32 ? 16 : 8) == 0;
 }
 
 shp_status_t rope_entry(const shp_tensor * q,
@@ -577,9 +659,17 @@ shp_status_t rope_entry(const shp_tensor * q,
     if (k != nullptr) {
         fast = fast && part_aligned(*k) && part_aligned(*k_out);
     }
-    if (norm && wq != nullptr) {
-        fast = fast && reinterpret_cast<uintptr_t>(wq->data) % 8 == 0 &&
-               (k == nullptr || wk == nullptr || reinterpret_cast<uintptr_t>(wk->data) % 8 == 0);
+    if (norm) {
+        fast = fast && gain_aligned(wq) && gain_aligned(wk);
+    }
+    // Positions per block: fill the 16 row slots x kRopeRows prefetch window.
+    // Short sequences are latency-bound: one position per block spreads them
+    // over more CUs.
+    const int total = static_cast<int>(a.part[0].heads + a.part[1].heads);
+    a.ppb           = total > 0 ? (kRopeSlots * kRopeRows) / total : 1;
+    a.ppb           = a.ppb < 1 ? 1 : (a.ppb > kRopeMaxPos ? kRopeMaxPos : a.ppb);
+    if (a.npos < 2048) {
+        a.ppb = 1;
     }
     if (a.npos > INT32_MAX) {
         return SHP_ERR_UNSUPPORTED;
