@@ -41,7 +41,7 @@ struct GatherArgs {
     int64_t         ne11;
     int64_t         total;
     int32_t         ne0;
-    int32_t         pad;
+    int32_t         batched;
 };
 
 constexpr int kMaxGroups = 64;
@@ -147,10 +147,13 @@ template <int TYPE> __device__ __forceinline__ float elem(const char * row, int 
 
 __device__ __forceinline__ void gather_coords(const GatherArgs & a, int64_t R, int32_t & id, const char *& srow,
                                               float *& drow) {
-    const int64_t r   = R % a.n;
-    const int64_t q   = R / a.n;
-    const int64_t i11 = q % a.ne11;
-    const int64_t i12 = q / a.ne11;
+    int64_t r = R, i11 = 0, i12 = 0;
+    if (a.batched) {  // ids [n, ne11, ne12]: 64-bit divisions only for the batched form
+        r             = R % a.n;
+        const int64_t q = R / a.n;
+        i11           = q % a.ne11;
+        i12           = q / a.ne11;
+    }
     id   = *reinterpret_cast<const int32_t *>(reinterpret_cast<const char *>(a.ids) + r * a.inb0 + i11 * a.inb1 +
                                             i12 * a.inb2);
     srow = a.src + static_cast<int64_t>(id) * a.snb1 + i11 * a.snb2 + i12 * a.snb3;
@@ -159,8 +162,11 @@ __device__ __forceinline__ void gather_coords(const GatherArgs & a, int64_t R, i
 
 constexpr uint32_t kQNaN = 0x7fc00000u;
 
-// F32/F16/BF16, 16-byte chunks, LPR lanes per row, up to 4 chunks per lane in
-// flight before the first store.
+// F32/F16/BF16, 16-byte chunks, LPR lanes per row (up to 256: a 2048-wide
+// BF16 row is one block with one chunk per lane). The id is read first; the
+// row chunk load depends on it; the f32 output is streamed out with
+// nontemporal stores. Table rows use ordinary loads so that rows gathered
+// again (repeated tokens, a table that fits the Infinity Cache) can hit.
 template <int TYPE, int LPR> __global__ __launch_bounds__(256) void k_get_rows_vec(const GatherArgs a) {
     constexpr int EPC = elems_per_chunk<TYPE>();
     const int     l   = threadIdx.x % LPR;
@@ -173,34 +179,21 @@ template <int TYPE, int LPR> __global__ __launch_bounds__(256) void k_get_rows_v
     float *      drow;
     gather_coords(a, R, id, srow, drow);
     const int nch = a.ne0 / EPC;
+    f32x4 *   out = reinterpret_cast<f32x4 *>(drow);
     if (id < 0 || id >= a.srows) {
         const float nan = __uint_as_float(kQNaN);
         for (int e = l; e < a.ne0 / 4; e += LPR) {
-            reinterpret_cast<float4 *>(drow)[e] = make_float4(nan, nan, nan, nan);
+            st_stream(out + e, splat4(nan));
         }
         return;
     }
-    for (int c0 = 0; c0 < nch; c0 += 4 * LPR) {
-        uint4 v[4];
+    for (int c = l; c < nch; c += LPR) {
+        const uint4 v = reinterpret_cast<const uint4 *>(srow)[c];
+        float       o[EPC];
+        cvt_chunk<TYPE>(v, o);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int c = c0 + j * LPR + l;
-            if (c < nch) {
-                v[j] = reinterpret_cast<const uint4 *>(srow)[c];
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int c = c0 + j * LPR + l;
-            if (c < nch) {
-                float o[EPC];
-                cvt_chunk<TYPE>(v[j], o);
-#pragma unroll
-                for (int k = 0; k < EPC / 4; ++k) {
-                    reinterpret_cast<float4 *>(drow + c * EPC)[k] =
-                        make_float4(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]);
-                }
-            }
+        for (int k = 0; k < EPC / 4; ++k) {
+            st_stream(out + c * (EPC / 4) + k, f32x4{ o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3] });
         }
     }
 }
@@ -429,9 +422,16 @@ template <int TYPE> shp_status_t launch_get_rows(const GatherArgs & a, bool vec,
                 hipLaunchKernelGGL(k_get_rows_q8<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
             }
         } else {
-            const int     lpr    = lanes_for(a.ne0 / elems_per_chunk<TYPE>());
+            const int64_t nch    = a.ne0 / elems_per_chunk<TYPE>();
+            const int     lpr    = nch >= 256 ? 256 : (nch >= 128 ? 128 : lanes_for(nch));
             const int64_t blocks = (a.total * lpr + 255) / 256;
-            if (lpr == 64) {
+            if (lpr == 256) {
+                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 256>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                                   stream, a);
+            } else if (lpr == 128) {
+                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 128>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                                   stream, a);
+            } else if (lpr == 64) {
                 hipLaunchKernelGGL((k_get_rows_vec<TYPE, 64>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                                    stream, a);
             } else if (lpr == 32) {
@@ -527,6 +527,7 @@ extern "C" shp_status_t shp_get_rows(const shp_tensor * src,
     a.n     = ids->ne[0];
     a.ne11  = ids->ne[1];
     a.total = ids->ne[0] * ids->ne[1] * ids->ne[2];
+    a.batched = ids->ne[1] > 1 || ids->ne[2] > 1;
     a.ne0   = static_cast<int32_t>(src->ne[0]);
     if ((a.total + 3) / 4 > INT32_MAX) {
         return SHP_ERR_UNSUPPORTED;

@@ -8,9 +8,10 @@
 // of the CPU cache. This file is compiled with -ffp-contract=off so nothing is
 // fused into an FMA behind the formulas' back.
 //
-// Layout: a row (ne0 contiguous floats) is owned by a group of LPR lanes; each
+// Layout: a row (ne0 contiguous floats) is owned by a group of TPR lanes; each
 // lane holds VPL float4 of it in registers between the reduction and the
-// scaled store, so x is read from HBM once.
+// scaled store, so x is read from HBM once. Activations are streamed with
+// nontemporal loads and stores; gains stay cacheable (every row reads them).
 
 #include <cmath>
 
@@ -37,12 +38,17 @@ struct NormArgs {
 
 enum NormMode { kPlain = 0, kAdd = 1, kAddSum = 2 };
 
-__device__ __forceinline__ float4 add4(float4 a, float4 b) {
-    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+__device__ __forceinline__ float norm_scale(double sum, int32_t ne0, float eps) {
+    const float mean = static_cast<float>(sum / static_cast<double>(ne0));
+    return 1.0f / __builtin_sqrtf(mean + eps);
 }
 
-__device__ __forceinline__ double sq4(float4 v) {
-    // Each square is an f32 product; the accumulation is double, in element order.
+__device__ __forceinline__ f32x4 add4v(f32x4 a, f32x4 b) {
+    return f32x4{ a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w };
+}
+
+// Each square is an f32 product; the accumulation is double, in element order.
+__device__ __forceinline__ double sq4v(f32x4 v) {
     double acc = static_cast<double>(v.x * v.x);
     acc += static_cast<double>(v.y * v.y);
     acc += static_cast<double>(v.z * v.z);
@@ -50,68 +56,142 @@ __device__ __forceinline__ double sq4(float4 v) {
     return acc;
 }
 
-__device__ __forceinline__ float norm_scale(double sum, int32_t ne0, float eps) {
-    const float mean = static_cast<float>(sum / static_cast<double>(ne0));
-    return 1.0f / __builtin_sqrtf(mean + eps);
+template <int WT> __device__ __forceinline__ f32x4 load_w4v(const void * w, int64_t e) {
+    const float4 v = load_w4<WT>(w, e);
+    return f32x4{ v.x, v.y, v.z, v.w };
 }
 
-template <int LPR, int VPL, int WT, int MODE> __global__ __launch_bounds__(256) void k_rms_norm_vec(const NormArgs a) {
-    constexpr int kRowsPerBlock = 256 / LPR;
-    const int     l             = threadIdx.x % LPR;
-    const int64_t row           = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / LPR;
-    if (row >= a.nrows) {
-        return;  // the whole LPR-lane group of this row leaves together
+// Four gains at element e as loaded (f32, or 16-bit patterns), converted later.
+template <int WT> struct WRaw {
+    uint32_t v[WT == kWF32 ? 4 : 2];
+};
+
+template <int WT> __device__ __forceinline__ WRaw<WT> load_wraw(const void * w, int64_t e) {
+    WRaw<WT> r;
+    if constexpr (WT == kWF32) {
+        const uint4 u = *reinterpret_cast<const uint4 *>(static_cast<const float *>(w) + e);
+        r.v[0] = u.x;
+        r.v[1] = u.y;
+        r.v[2] = u.z;
+        r.v[3] = u.w;
+    } else if constexpr (WT != kWNone) {
+        const uint2 u = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(w) + e);
+        r.v[0] = u.x;
+        r.v[1] = u.y;
     }
-    const float4 * xp = reinterpret_cast<const float4 *>(reinterpret_cast<const char *>(a.x) + row_offset(a.xm, row));
-    float4         v[VPL];
+    return r;
+}
+
+template <int WT> __device__ __forceinline__ f32x4 cvt_wraw(const WRaw<WT> & r) {
+    if constexpr (WT == kWF32) {
+        return f32x4{ __uint_as_float(r.v[0]), __uint_as_float(r.v[1]), __uint_as_float(r.v[2]), __uint_as_float(r.v[3]) };
+    } else if constexpr (WT == kWBF16) {
+        return f32x4{ bf16_bits_to_f32(r.v[0] & 0xffffu), bf16_bits_to_f32(r.v[0] >> 16), bf16_bits_to_f32(r.v[1] & 0xffffu),
+                      bf16_bits_to_f32(r.v[1] >> 16) };
+    } else if constexpr (WT == kWF16) {
+        return f32x4{ f16_bits_to_f32(r.v[0] & 0xffffu), f16_bits_to_f32(r.v[0] >> 16), f16_bits_to_f32(r.v[1] & 0xffffu),
+                      f16_bits_to_f32(r.v[1] >> 16) };
+    } else {
+        return splat4(1.0f);
+    }
+}
+
+// Vector path (ne0 % 4 == 0, 16-byte aligned rows, ne0 <= 256*4*VPL).
+//
+// A row is spread over TPR lanes (16..256) so that each lane streams at most
+// VPL float4 of it: a 1024-wide row is one 256-lane block with one float4 per
+// lane, which keeps the most waves -- and so the most loads -- in flight per
+// CU. Every load (x, the residual b, the gains) is issued before anything
+// waits. The double sum of squares is reduced across the TPR lanes with
+// shuffles, and across waves (TPR > 64) through LDS in a fixed order. Lanes
+// past the end of the row or of the tensor still take part in the barrier.
+template <int TPR, int VPL, int WT, int MODE> __global__ __launch_bounds__(256) void k_rms_norm_vec(const NormArgs a) {
+    constexpr int kRowsPerBlock = 256 / TPR;
+    constexpr int kWavesPerRow  = TPR > kWave ? TPR / kWave : 1;
+    __shared__ double s_part[TPR > kWave ? 256 / kWave : 1];
+
+    const int     l     = threadIdx.x % TPR;
+    const int64_t row   = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / TPR;
+    const bool    live  = row < a.nrows;
+    const int     nvec  = a.ne0 / 4;
+    const int64_t rrow  = live ? row : 0;
+    const f32x4 * xp    = reinterpret_cast<const f32x4 *>(reinterpret_cast<const char *>(a.x) + row_offset(a.xm, rrow));
+    f32x4         v[VPL];
+    f32x4         bv[VPL];
+    f32x4         wv[VPL];
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
-        v[k] = xp[k * LPR + l];
+        const int c = k * TPR + l;
+        v[k]        = (live && c < nvec) ? ld_stream(xp + c) : splat4(0.0f);
     }
-    // The gains are loaded with the row, not after the reduction, so the kernel
-    // waits on one memory round trip, not two.
-    float4 wv[VPL];
+    if constexpr (MODE != kPlain) {
+        const f32x4 * bp =
+            reinterpret_cast<const f32x4 *>(reinterpret_cast<const char *>(a.b) + row_offset(a.bm, rrow));
+#pragma unroll
+        for (int k = 0; k < VPL; ++k) {
+            const int c = k * TPR + l;
+            bv[k]       = (live && c < nvec) ? ld_stream(bp + c) : splat4(0.0f);
+        }
+    }
     if constexpr (WT != kWNone) {
 #pragma unroll
         for (int k = 0; k < VPL; ++k) {
-            wv[k] = load_w4<WT>(a.w, static_cast<int64_t>(k * LPR + l) * 4);
+            const int c = k * TPR + l;
+            wv[k]       = c < nvec ? load_w4v<WT>(a.w, static_cast<int64_t>(c) * 4) : splat4(0.0f);
         }
     }
     if constexpr (MODE != kPlain) {
-        const float4 * bp =
-            reinterpret_cast<const float4 *>(reinterpret_cast<const char *>(a.b) + row_offset(a.bm, row));
-        float4 bv[VPL];
 #pragma unroll
         for (int k = 0; k < VPL; ++k) {
-            bv[k] = bp[k * LPR + l];
-        }
-#pragma unroll
-        for (int k = 0; k < VPL; ++k) {
-            v[k] = add4(v[k], bv[k]);
+            v[k] = add4v(v[k], bv[k]);
         }
         if constexpr (MODE == kAddSum) {
-            float4 * sp = reinterpret_cast<float4 *>(reinterpret_cast<char *>(a.s) + row_offset(a.sm, row));
+            f32x4 * sp = reinterpret_cast<f32x4 *>(reinterpret_cast<char *>(a.s) + row_offset(a.sm, rrow));
 #pragma unroll
             for (int k = 0; k < VPL; ++k) {
-                sp[k * LPR + l] = v[k];
+                const int c = k * TPR + l;
+                if (live && c < nvec) {
+                    st_stream(sp + c, v[k]);
+                }
             }
         }
     }
     double acc = 0.0;
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
-        acc += sq4(v[k]);
+        acc += sq4v(v[k]);
     }
-    acc               = group_sum<LPR>(acc);
+    if constexpr (TPR <= kWave) {
+        acc = group_sum<TPR>(acc);
+    } else {
+        acc             = group_sum<kWave>(acc);
+        const int wave  = threadIdx.x / kWave;
+        if (threadIdx.x % kWave == 0) {
+            s_part[wave] = acc;
+        }
+        __syncthreads();
+        const int first = (threadIdx.x / TPR) * kWavesPerRow;
+        acc             = s_part[first];
+#pragma unroll
+        for (int k = 1; k < kWavesPerRow; ++k) {
+            acc += s_part[first + k];
+        }
+    }
+    if (!live) {
+        return;
+    }
     const float scale = norm_scale(acc, a.ne0, a.eps);
-    float4 *    yp    = reinterpret_cast<float4 *>(reinterpret_cast<char *>(a.y) + row_offset(a.ym, row));
+    f32x4 *     yp    = reinterpret_cast<f32x4 *>(reinterpret_cast<char *>(a.y) + row_offset(a.ym, row));
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
-        float4 o = make_float4(v[k].x * scale, v[k].y * scale, v[k].z * scale, v[k].w * scale);
-        if constexpr (WT != kWNone) {
-            o = make_float4(o.x * wv[k].x, o.y * wv[k].y, o.z * wv[k].z, o.w * wv[k].w);
+        const int c = k * TPR + l;
+        if (c < nvec) {
+            f32x4 o = f32x4{ v[k].x * scale, v[k].y * scale, v[k].z * scale, v[k].w * scale };
+            if constexpr (WT != kWNone) {
+                o = f32x4{ o.x * wv[k].x, o.y * wv[k].y, o.z * wv[k].z, o.w * wv[k].w };
+            }
+            st_stream(yp + c, o);
         }
-        yp[k * LPR + l] = o;
     }
 }
 
@@ -164,37 +244,42 @@ template <int WT, int MODE> __global__ __launch_bounds__(256) void k_rms_norm_ge
 }
 
 template <int WT, int MODE> shp_status_t launch_norm(const NormArgs & a, bool vec, hipStream_t stream) {
-    if (vec) {
-        const int ne0 = a.ne0;
-        auto      go  = [&](auto kernel, int rows_per_block) {
-            const int64_t blocks = (a.nrows + rows_per_block - 1) / rows_per_block;
-            hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
-            return launch_status();
-        };
-        switch (ne0) {
-            case 64:
-                return go(k_rms_norm_vec<16, 1, WT, MODE>, 16);
-            case 128:
-                return go(k_rms_norm_vec<32, 1, WT, MODE>, 8);
-            case 256:
-                return go(k_rms_norm_vec<64, 1, WT, MODE>, 4);
-            case 512:
-                return go(k_rms_norm_vec<64, 2, WT, MODE>, 4);
-            case 1024:
-                return go(k_rms_norm_vec<64, 4, WT, MODE>, 4);
-            case 2048:
-                return go(k_rms_norm_vec<64, 8, WT, MODE>, 4);
-            case 3072:
-                return go(k_rms_norm_vec<64, 12, WT, MODE>, 4);
-            case 4096:
-                return go(k_rms_norm_vec<64, 16, WT, MODE>, 4);
+    auto go = [&](auto kernel, int rows_per_block) {
+        const int64_t blocks = (a.nrows + rows_per_block - 1) / rows_per_block;
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+        return launch_status();
+    };
+    const int nvec = a.ne0 / 4;
+    if (vec && nvec <= 256 * 8) {
+        if (nvec <= 16) {
+            return go(k_rms_norm_vec<16, 1, WT, MODE>, 16);
+        }
+        if (nvec <= 32) {
+            return go(k_rms_norm_vec<32, 1, WT, MODE>, 8);
+        }
+        if (nvec <= 64) {
+            return go(k_rms_norm_vec<64, 1, WT, MODE>, 4);
+        }
+        if (nvec <= 128) {
+            return go(k_rms_norm_vec<128, 1, WT, MODE>, 2);
+        }
+        switch ((nvec + 255) / 256) {
+            case 1:
+                return go(k_rms_norm_vec<256, 1, WT, MODE>, 1);
+            case 2:
+                return go(k_rms_norm_vec<256, 2, WT, MODE>, 1);
+            case 3:
+                return go(k_rms_norm_vec<256, 3, WT, MODE>, 1);
+            case 4:
+                return go(k_rms_norm_vec<256, 4, WT, MODE>, 1);
+            case 5:
+            case 6:
+                return go(k_rms_norm_vec<256, 6, WT, MODE>, 1);
             default:
-                break;
+                return go(k_rms_norm_vec<256, 8, WT, MODE>, 1);
         }
     }
-    const int64_t blocks = (a.nrows + 3) / 4;
-    hipLaunchKernelGGL((k_rms_norm_generic<WT, MODE>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
-    return launch_status();
+    return go(k_rms_norm_generic<WT, MODE>, 4);
 }
 
 template <int MODE> shp_status_t dispatch_norm_w(const NormArgs & a, int wk, bool vec, hipStream_t stream) {
@@ -294,7 +379,7 @@ struct RopePart {
 };
 
 struct RopeArgs {
-    RopePart        part[2];
+    RopePart        part[2];  // q, then k (heads == 0 when absent)
     const int32_t * pos;
     int64_t         npos;
     int32_t         ne0;
@@ -303,9 +388,40 @@ struct RopeArgs {
     float           freq_scale;
     float           attn_factor;
     float           eps;
-    int32_t         ppb;  // fast path: positions per block
-    int32_t         pad;
 };
+
+// Fields of head row hh (q rows first, then k rows) as selects between the two
+// parts' kernel arguments, which stay in scalar registers. Indexing part[]
+// with a per-lane value instead would read the argument block through vector
+// memory and put a dependent round trip in front of every row load.
+struct RowRef {
+    const float * x;
+    float *       y;
+    const void *  w;
+};
+
+__device__ __forceinline__ RowRef rope_row(const RopeArgs & a, int hh, int64_t pi) {
+    const RopePart & q   = a.part[0];
+    const RopePart & k   = a.part[1];
+    const bool       isk = hh >= q.heads;
+    const int64_t    h   = isk ? hh - q.heads : hh;
+    const char *     xb  = reinterpret_cast<const char *>(isk ? k.x : q.x);
+    char *           yb  = reinterpret_cast<char *>(isk ? k.y : q.y);
+    const int64_t    xo  = h * (isk ? k.xnb1 : q.xnb1) + pi * (isk ? k.xnb2 : q.xnb2);
+    const int64_t    yo  = h * (isk ? k.ynb1 : q.ynb1) + pi * (isk ? k.ynb2 : q.ynb2);
+    return RowRef{ reinterpret_cast<const float *>(xb + xo), reinterpret_cast<float *>(yb + yo), isk ? k.w : q.w };
+}
+
+// cos/sin of an f32 angle: evaluated in double and rounded once (the fast
+// Cody-Waite path covers |angle| < 2^19 * pi/2; OCML's double sincos beyond).
+__device__ __forceinline__ void rope_sincos(float th, float & s, float & c) {
+    if (!sincos_f32_rn(th, s, c)) {
+        double sd, cd;
+        sincos(static_cast<double>(th), &sd, &cd);
+        s = static_cast<float>(sd);
+        c = static_cast<float>(cd);
+    }
+}
 
 // cos/sin of the pair-k angle at position p: theta is replayed through the f32
 // recurrence theta <- theta*theta_scale exactly k times (the CPU cache's order),
@@ -316,157 +432,105 @@ __device__ __forceinline__ void rope_cs(int32_t p, int k, const RopeArgs & a, fl
     for (int i = 0; i < k; ++i) {
         theta = theta * a.theta_scale;
     }
-    const float th = a.freq_scale * theta;
-    float       sf, cf;
-    if (!sincos_f32_rn(th, sf, cf)) {
-        double sd, cd;  // beyond the fast reduction's range (|angle| > 2^19 pi/2)
-        sincos(static_cast<double>(th), &sd, &cd);
-        sf = static_cast<float>(sd);
-        cf = static_cast<float>(cd);
-    }
+    float sf, cf;
+    rope_sincos(a.freq_scale * theta, sf, cf);
     c = cf * a.attn_factor;
     s = sf * a.attn_factor;
 }
 
-// Fast path: head_dim == n_dims == 128.
+// Fast path: head_dim == n_dims == 128, one block per position.
 //
 // A head row is owned by 16 lanes; lane j holds x[4j..4j+3] and
 // x[64+4j..64+4j+3] as two float4, i.e. both halves of NEOX pairs 4j..4j+3,
-// so the rotation needs no data exchange and every load is 128-bit. A block
-// (16 row slots) covers `ppb` consecutive positions; each slot prefetches up
-// to kRopeRows of its rows before anything waits, while the block builds the
-// positions' 64-entry cos/sin caches in LDS.
-constexpr int kRopeLanes    = 16;
-constexpr int kRopeSlots    = 256 / kRopeLanes;
-constexpr int kRopeRows     = 4;
-constexpr int kRopeMaxPos   = 4;
+// so the rotation needs no data exchange and every access is 128-bit. The
+// block has one 16-lane group per head row of the position (q heads, then k
+// heads; 24 rows = 384 lanes for Qwen3-TTS), so every row load is issued at
+// once. Meanwhile wave 0 builds the position's 64-entry cos/sin cache: all 64
+// lanes run the same serial f32 theta chain and lane k keeps the k-th value,
+// evaluates its cos/sin in double and writes them to LDS; one barrier later
+// every lane reads the 4 pairs it needs.
+constexpr int kRopeLanes   = 16;
+constexpr int kRopeMaxRows = 1024 / kRopeLanes;
 
-template <bool NORM, int WT> __global__ __launch_bounds__(256) void k_rope128(const RopeArgs a) {
-    __shared__ float s_cos[kRopeMaxPos][64];
-    __shared__ float s_sin[kRopeMaxPos][64];
+template <bool NORM, int WT> __global__ __launch_bounds__(1024) void k_rope128(const RopeArgs a) {
+    __shared__ f32x4 s_cos[16];
+    __shared__ f32x4 s_sin[16];
 
-    const int64_t p0    = static_cast<int64_t>(blockIdx.x) * a.ppb;
-    const int     np    = static_cast<int>(a.npos - p0 < a.ppb ? a.npos - p0 : a.ppb);
+    const int64_t pi    = blockIdx.x;
     const int     total = a.part[0].heads + a.part[1].heads;
-    const int     nrows = np * total;
-    const int     slot  = threadIdx.x / kRopeLanes;
+    const int     slots = blockDim.x / kRopeLanes;
+    const int     g     = threadIdx.x / kRopeLanes;
     const int     l     = threadIdx.x % kRopeLanes;
 
-    auto locate = [&](int row, int & pp, const float *& xr, float *& yr, int & t) {
-        pp               = row / total;
-        const int hh     = row - pp * total;
-        t                = hh < a.part[0].heads ? 0 : 1;
-        const int h      = t == 0 ? hh : hh - a.part[0].heads;
-        const RopePart & P = a.part[t];
-        const int64_t    pi = p0 + pp;
-        xr = reinterpret_cast<const float *>(reinterpret_cast<const char *>(P.x) + h * P.xnb1 + pi * P.xnb2);
-        yr = reinterpret_cast<float *>(reinterpret_cast<char *>(P.y) + h * P.ynb1 + pi * P.ynb2);
-    };
-
-    // Both heads' gains for this lane's eight elements, loaded once up front.
-    float4 wlo[2] = { make_float4(1.f, 1.f, 1.f, 1.f), make_float4(1.f, 1.f, 1.f, 1.f) };
-    float4 whi[2] = { wlo[0], wlo[0] };
+    // 1. this lane's first row, and its gains (both issued before any wait)
+    const bool live = g < total;
+    RowRef     r    = rope_row(a, live ? g : 0, pi);
+    f32x4      lo   = splat4(0.0f);
+    f32x4      hi   = splat4(0.0f);
+    if (live) {
+        lo = ld_stream(reinterpret_cast<const f32x4 *>(r.x) + l);
+        hi = ld_stream(reinterpret_cast<const f32x4 *>(r.x + 64) + l);
+    }
+    // Gains stay raw until after the barrier: converting them here would make
+    // wave 0 wait for every outstanding load before its theta chain.
+    WRaw<WT> wlo_raw{}, whi_raw{};
     if constexpr (NORM && WT != kWNone) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            if (a.part[t].heads > 0) {
-                wlo[t] = load_w4<WT>(a.part[t].w, 4 * l);
-                whi[t] = load_w4<WT>(a.part[t].w, 64 + 4 * l);
-            }
+        if (live) {
+            wlo_raw = load_wraw<WT>(r.w, 4 * l);
+            whi_raw = load_wraw<WT>(r.w, 64 + 4 * l);
         }
     }
 
-    auto finish = [&](int pp, float4 lo, float4 hi, float * yr, int t) {
+    // 2. the cos/sin cache of this position (wave 0)
+    if (threadIdx.x < 64) {
+        const int k   = threadIdx.x;
+        float     th  = static_cast<float>(a.pos[pi]);
+        float     mth = th;
+#pragma unroll
+        for (int i = 1; i < 64; ++i) {
+            th  = th * a.theta_scale;
+            mth = k == i ? th : mth;
+        }
+        float sv, cv;
+        rope_sincos(a.freq_scale * mth, sv, cv);
+        reinterpret_cast<float *>(s_cos)[k] = cv * a.attn_factor;
+        reinterpret_cast<float *>(s_sin)[k] = sv * a.attn_factor;
+    }
+    __syncthreads();
+    const f32x4 cs = s_cos[l];
+    const f32x4 sn = s_sin[l];
+
+    // 3. normalise, rotate, store; rows beyond the first slot pass (more than
+    //    64 heads) are loaded here
+    for (int row = g; row < total; row += slots) {
+        if (row != g) {
+            r  = rope_row(a, row, pi);
+            lo = ld_stream(reinterpret_cast<const f32x4 *>(r.x) + l);
+            hi = ld_stream(reinterpret_cast<const f32x4 *>(r.x + 64) + l);
+            if constexpr (NORM && WT != kWNone) {
+                wlo_raw = load_wraw<WT>(r.w, 4 * l);
+                whi_raw = load_wraw<WT>(r.w, 64 + 4 * l);
+            }
+        }
         if constexpr (NORM) {
-            double acc        = sq4(lo) + sq4(hi);
+            double acc        = sq4v(lo) + sq4v(hi);
             acc               = group_sum<kRopeLanes>(acc);
             const float scale = norm_scale(acc, 128, a.eps);
-            lo = make_float4(lo.x * scale, lo.y * scale, lo.z * scale, lo.w * scale);
-            hi = make_float4(hi.x * scale, hi.y * scale, hi.z * scale, hi.w * scale);
+            lo                = f32x4{ lo.x * scale, lo.y * scale, lo.z * scale, lo.w * scale };
+            hi                = f32x4{ hi.x * scale, hi.y * scale, hi.z * scale, hi.w * scale };
             if constexpr (WT != kWNone) {
-                const float4 wl = t == 0 ? wlo[0] : wlo[1];
-                const float4 wh = t == 0 ? whi[0] : whi[1];
-                lo = make_float4(lo.x * wl.x, lo.y * wl.y, lo.z * wl.z, lo.w * wl.w);
-                hi = make_float4(hi.x * wh.x, hi.y * wh.y, hi.z * wh.z, hi.w * wh.w);
+                const f32x4 wlo = cvt_wraw<WT>(wlo_raw);
+                const f32x4 whi = cvt_wraw<WT>(whi_raw);
+                lo = f32x4{ lo.x * wlo.x, lo.y * wlo.y, lo.z * wlo.z, lo.w * wlo.w };
+                hi = f32x4{ hi.x * whi.x, hi.y * whi.y, hi.z * whi.z, hi.w * whi.w };
             }
         }
-        const float * cs = s_cos[pp] + 4 * l;
-        const float * sn = s_sin[pp] + 4 * l;
-        float4        olo, ohi;
-        olo.x = lo.x * cs[0] - hi.x * sn[0];
-        ohi.x = lo.x * sn[0] + hi.x * cs[0];
-        olo.y = lo.y * cs[1] - hi.y * sn[1];
-        ohi.y = lo.y * sn[1] + hi.y * cs[1];
-        olo.z = lo.z * cs[2] - hi.z * sn[2];
-        ohi.z = lo.z * sn[2] + hi.z * cs[2];
-        olo.w = lo.w * cs[3] - hi.w * sn[3];
-        ohi.w = lo.w * sn[3] + hi.w * cs[3];
-        reinterpret_cast<float4 *>(yr)[l]      = olo;
-        reinterpret_cast<float4 *>(yr + 64)[l] = ohi;
-    };
-
-    // 1. issue every prefetched row load of this slot
-    float4  lo[kRopeRows], hi[kRopeRows];
-    int     pps[kRopeRows];
-    int     ts[kRopeRows];
-    float * yrs[kRopeRows];
-#pragma unroll
-    for (int r = 0; r < kRopeRows; ++r) {
-        const int row = slot + r * kRopeSlots;
-        pps[r]        = 0;
-        ts[r]         = 0;
-        yrs[r]        = nullptr;
-        if (row < nrows) {
-            const float * xr;
-            locate(row, pps[r], xr, yrs[r], ts[r]);
-            lo[r] = reinterpret_cast<const float4 *>(xr)[l];
-            hi[r] = reinterpret_cast<const float4 *>(xr + 64)[l];
-        }
-    }
-    // 2. the positions' cos/sin caches, meanwhile: lane 0 of wave pp replays
-    //    position pp's f32 theta recurrence (inherently serial), then 64 lanes
-    //    per position evaluate cos/sin in parallel.
-    if (threadIdx.x % kWave == 0 && static_cast<int>(threadIdx.x / kWave) < np) {
-        const int pp = threadIdx.x / kWave;
-        float     th = static_cast<float>(a.pos[p0 + pp]);
-#pragma unroll
-        for (int k = 0; k < 64; ++k) {
-            s_sin[pp][k] = a.freq_scale * th;  // angle k, overwritten by its sine below
-            th           = th * a.theta_scale;
-        }
-    }
-    __syncthreads();
-    float cv = 0.0f, sv = 0.0f;
-    const int epp = threadIdx.x / 64, ek = threadIdx.x % 64;
-    if (epp < np) {
-        const float th = s_sin[epp][ek];
-        if (!sincos_f32_rn(th, sv, cv)) {
-            double sd, cd;
-            sincos(static_cast<double>(th), &sd, &cd);
-            sv = static_cast<float>(sd);
-            cv = static_cast<float>(cd);
-        }
-    }
-    __syncthreads();
-    if (epp < np) {
-        s_cos[epp][ek] = cv * a.attn_factor;
-        s_sin[epp][ek] = sv * a.attn_factor;
-    }
-    __syncthreads();
-    // 3. normalise, rotate, store
-#pragma unroll
-    for (int r = 0; r < kRopeRows; ++r) {
-        if (slot + r * kRopeSlots < nrows) {
-            finish(pps[r], lo[r], hi[r], yrs[r], ts[r]);
-        }
-    }
-    // rows past the prefetch window (only when a position has > 64 head rows)
-    for (int row = slot + kRopeRows * kRopeSlots; row < nrows; row += kRopeSlots) {
-        int           pp, t;
-        const float * xr;
-        float *       yr;
-        locate(row, pp, xr, yr, t);
-        finish(pp, reinterpret_cast<const float4 *>(xr)[l], reinterpret_cast<const float4 *>(xr + 64)[l], yr, t);
+        const f32x4 olo{ lo.x * cs.x - hi.x * sn.x, lo.y * cs.y - hi.y * sn.y, lo.z * cs.z - hi.z * sn.z,
+                         lo.w * cs.w - hi.w * sn.w };
+        const f32x4 ohi{ lo.x * sn.x + hi.x * cs.x, lo.y * sn.y + hi.y * cs.y, lo.z * sn.z + hi.z * cs.z,
+                         lo.w * sn.w + hi.w * cs.w };
+        st_stream(reinterpret_cast<f32x4 *>(r.y) + l, olo);
+        st_stream(reinterpret_cast<f32x4 *>(r.y + 64) + l, ohi);
     }
 }
 
@@ -479,14 +543,12 @@ template <bool NORM, int WT> __global__ __launch_bounds__(256) void k_rope_gener
     if (row >= a.npos * total) {
         return;
     }
-    const int64_t    pi = row / total;
-    const int        hh = static_cast<int>(row % total);
-    const int        t  = hh < a.part[0].heads ? 0 : 1;
-    const int        h  = t == 0 ? hh : hh - a.part[0].heads;
-    const RopePart & P  = a.part[t];
-    const float *    xr = reinterpret_cast<const float *>(reinterpret_cast<const char *>(P.x) + h * P.xnb1 + pi * P.xnb2);
-    float *          yr = reinterpret_cast<float *>(reinterpret_cast<char *>(P.y) + h * P.ynb1 + pi * P.ynb2);
-    const int32_t    p  = a.pos[pi];
+    const int64_t pi = row / total;
+    const int     hh = static_cast<int>(row % total);
+    const RowRef  rr = rope_row(a, hh, pi);
+    const float * xr = rr.x;
+    float *       yr = rr.y;
+    const int32_t p  = a.pos[pi];
 
     float scale = 1.0f;
     if constexpr (NORM) {
@@ -502,7 +564,7 @@ template <bool NORM, int WT> __global__ __launch_bounds__(256) void k_rope_gener
         if constexpr (NORM) {
             v = v * scale;
             if constexpr (WT != kWNone) {
-                v = v * load_w1<WT>(P.w, i);
+                v = v * load_w1<WT>(rr.w, i);
             }
         }
         return v;
@@ -524,8 +586,9 @@ template <bool NORM, int WT> __global__ __launch_bounds__(256) void k_rope_gener
 template <bool NORM, int WT> shp_status_t launch_rope(const RopeArgs & a, bool fast, hipStream_t stream) {
     const int total = a.part[0].heads + a.part[1].heads;
     if (fast) {
-        const int64_t blocks = (a.npos + a.ppb - 1) / a.ppb;
-        hipLaunchKernelGGL((k_rope128<NORM, WT>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+        const int rows    = total < kRopeMaxRows ? total : kRopeMaxRows;
+        const int threads = ((rows * kRopeLanes + kWave - 1) / kWave) * kWave;
+        hipLaunchKernelGGL((k_rope128<NORM, WT>), dim3(static_cast<unsigned>(a.npos)), dim3(threads), 0, stream, a);
         return launch_status();
     }
     const int64_t rows   = a.npos * total;
@@ -661,15 +724,6 @@ shp_status_t rope_entry(const shp_tensor * q,
     }
     if (norm) {
         fast = fast && gain_aligned(wq) && gain_aligned(wk);
-    }
-    // Positions per block: fill the 16 row slots x kRopeRows prefetch window.
-    // Short sequences are latency-bound: one position per block spreads them
-    // over more CUs.
-    const int total = static_cast<int>(a.part[0].heads + a.part[1].heads);
-    a.ppb           = total > 0 ? (kRopeSlots * kRopeRows) / total : 1;
-    a.ppb           = a.ppb < 1 ? 1 : (a.ppb > kRopeMaxPos ? kRopeMaxPos : a.ppb);
-    if (a.npos < 2048) {
-        a.ppb = 1;
     }
     if (a.npos > INT32_MAX) {
         return SHP_ERR_UNSUPPORTED;

@@ -14,6 +14,62 @@ namespace shp {
 
 constexpr int kWave = 64;
 
+// A native 4 x f32 vector: what the nontemporal builtins and 128-bit global
+// loads/stores operate on.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Streaming accesses. Activations are read or written exactly once per
+// launch, so they are fetched and stored with the nontemporal hint: the lines
+// are not kept in L2 / the Infinity Cache at the expense of data that is
+// reused (gains, Snake alpha, positions, gathered table rows).
+__device__ __forceinline__ f32x4 ld_stream(const f32x4 * p) {
+    return __builtin_nontemporal_load(p);
+}
+
+__device__ __forceinline__ void st_stream(f32x4 * p, f32x4 v) {
+    __builtin_nontemporal_store(v, p);
+}
+
+__device__ __forceinline__ f32x4 splat4(float v) {
+    return f32x4{ v, v, v, v };
+}
+
+// Unsigned 32-bit division by a launch constant d >= 1 without an integer
+// divide: q = (umulhi(n, m) + n) >> l, with l = ceil(log2 d) and
+// m = floor(2^32 (2^l - d) / d) + 1 (Granlund & Montgomery, "Division by
+// invariant integers using multiplication", 1994, section 4).
+struct FastDiv {
+    uint32_t d;
+    uint32_t m;
+    uint32_t l;
+    uint32_t pad;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+    FastDiv f{};
+    f.d = d;
+    uint32_t l = 0;
+    while (l < 32 && (uint64_t{ 1 } << l) < d) {
+        ++l;
+    }
+    f.l = l;
+    f.m = static_cast<uint32_t>(((uint64_t{ 1 } << 32) * ((uint64_t{ 1 } << l) - d)) / d + 1);
+    return f;
+}
+
+__host__ __device__ __forceinline__ uint32_t fastdiv(uint32_t n, const FastDiv & f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uint64_t t = __umulhi(n, f.m);
+#else
+    const uint64_t t = (static_cast<uint64_t>(n) * f.m) >> 32;
+#endif
+    return static_cast<uint32_t>((t + n) >> f.l);
+}
+
+__host__ __device__ __forceinline__ uint32_t fastmod(uint32_t n, const FastDiv & f) {
+    return n - fastdiv(n, f) * f.d;
+}
+
 // Addresses row r of a ggml tensor whose rows are the flattened dims 1..3
 // (r = i1 + ne1*(i2 + ne2*i3)). When the rows are evenly strided the offset is
 // r*rs, with no division; otherwise it is decomposed per dimension.
