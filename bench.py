@@ -40,6 +40,8 @@ PEAK_GBS = 8000.0
 METRIC = "achieved HBM GB/s (% of peak) per fused op; µs/talker-layer non-GEMM step"
 SEED = 20260728
 COLD_BYTES = 512 << 20
+CALIB_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_configs1_step.txt")
 
 
 def parse():
@@ -52,6 +54,9 @@ def parse():
     p.add_argument("--suite", metavar="JSON", help="instead: measure every op on every BASELINE config "
                    "(cold-cache protocol), print a markdown table and write the figures to JSON")
     p.add_argument("--only", default="", help="with --suite: comma-separated config names to run")
+    p.add_argument("--pmc-pass", action="store_true", help="instead: run each op of the step eagerly over every "
+                   "input set a few times, plus a %d MiB device copy of known size, for rocprofv3 --pmc "
+                   "FETCH_SIZE / WRITE_SIZE passes (few dispatches, no graphs)" % (CALIB_BYTES >> 20))
     return p.parse_args()
 
 
@@ -397,6 +402,37 @@ def suite(args, S, torch):
         json.dump({"peak_GBps": PEAK_GBS, "cold_bytes": COLD_BYTES, "rows": rows}, f, indent=1)
 
 
+def pmc_pass(step, torch):
+    """Each op of the step, eagerly, 3 times over every input set, between two
+    copies of CALIB_BYTES (a plain device-to-device copy: CALIB_BYTES read and
+    CALIB_BYTES written), for counter collection."""
+    n = CALIB_BYTES // 4
+    src = torch.randn(n, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    for _ in range(3):
+        for s in range(step.nsets):
+            for _, f in step.ops(s):
+                f()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_pass": "done", "sets": step.nsets, "calib_bytes": CALIB_BYTES, "op_bytes": step.op_bytes}))
+
+
+def read_traffic(op):
+    """HBM bytes per launch of `op` from the committed counter summary (two
+    rocprofv3 --pmc passes, FETCH_SIZE then WRITE_SIZE, each scaled by what the
+    counter reads for the calibration copy), or None when it has no line."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        fields = dict(kv.split("=", 1) for kv in line.split() if "=" in kv)
+        if fields.get("op") == op and "hbm_bytes" in fields:
+            return int(float(fields["hbm_bytes"]))
+    return None
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -412,6 +448,9 @@ def main():
         suite(args, S, torch)
         return
     step = PrefillStep(S, torch)
+    if args.pmc_pass:
+        pmc_pass(step, torch)
+        return
 
     # eager run of every op of every set (loads the code objects before capture)
     per_set_ops = [step.ops(s) for s in range(step.nsets)]
@@ -444,7 +483,8 @@ def main():
                         "frac": round(gbs / PEAK_GBS, 4)}
     dom = max(per_op, key=lambda n: per_op[n]["us"])
     roof = {"bound": "hbm", "kernel": dom, "achieved": per_op[dom]["GB/s"], "peak": PEAK_GBS, "unit": "GB/s",
-            "frac": per_op[dom]["frac"], "traffic": None}
+            "frac": per_op[dom]["frac"], "traffic": read_traffic(dom),
+            "algorithmic_bytes": step.op_bytes[dom], "us_per_launch": per_op[dom]["us"]}
 
     layer_us = decode_layer_us(S, torch)
 
