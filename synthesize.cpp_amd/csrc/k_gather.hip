@@ -7,14 +7,15 @@
 // bits and therefore never rounds. The gather->sum adds group rows in group
 // order in f32, exactly as the unfused ggml_add chain does.
 //
-// Q8_0 layout: 32-element blocks of {f16 d; int8 qs[32]} = 34 bytes. Two
-// consecutive blocks are 68 bytes = 17 dwords, and a row of ne0 % 64 == 0
-// elements starts every block pair on a 4-byte boundary. A lane therefore owns
-// one block pair: it loads 17 aligned dwords with wide loads, shifts block
-// 2k's bytes into place with v_alignbyte (they sit 2 bytes off), and decodes
-// 64 outputs in registers without any LDS traffic.
+// Q8_0 layout: 32-element blocks of {f16 d; int8 qs[32]} = 34 bytes, so
+// blocks are only 2-byte aligned. Rows of 256..4096 elements are read by
+// half-blocks (16 quants per lane, from a 4-byte aligned 5-dword window plus
+// the scale's dword, shifted into place with v_alignbyte); other widths that
+// are a multiple of 64 by block pairs (68 bytes = 17 aligned dwords per lane).
+// Either way the decode is in registers, with no LDS traffic.
 
 #include "shp_internal.hpp"
+#include "shp_q8.hpp"
 
 namespace shp {
 namespace {
@@ -42,6 +43,8 @@ struct GatherArgs {
     int64_t         total;
     int32_t         ne0;
     int32_t         batched;
+    int32_t         staged;  // Q8_0 through LDS: ne0 in {1024, 2048, 4096}, rows 16-byte aligned
+    int32_t         pad;
 };
 
 constexpr int kMaxGroups = 64;
@@ -57,6 +60,12 @@ struct GatherSumArgs {
     int64_t         frames;
     int32_t         ngroups;
     int32_t         ne0;
+    // Q8_0 half-block path only: every table has rows of `rowbytes` bytes and
+    // fewer than 2^31 bytes in all, so a row offset is 32-bit; slots from
+    // ngroups up to the next multiple of 16 repeat group 0's table.
+    uint32_t        rows32[kMaxGroups];
+    uint32_t        rowbytes;
+    int32_t         staged;  // ... and through LDS: ne0 in {1024, 2048, 4096}, tables 16-byte aligned
 };
 
 template <int TYPE> constexpr int elems_per_chunk() {
@@ -231,6 +240,313 @@ template <int LPR> __global__ __launch_bounds__(256) void k_get_rows_q8(const Ga
     }
 }
 
+__device__ __forceinline__ int32_t group_id(const GatherSumArgs & a, int g, int64_t f) {
+    return *reinterpret_cast<const int32_t *>(reinterpret_cast<const char *>(a.ids) + g * a.ids_gstride + f * 4);
+}
+
+// ---------------------------------------------------------------------------
+// Q8_0 by half-blocks: lane l of a row owns elements 16l..16l+15 (geometry in
+// shp_q8.hpp). A 1024-wide row is one wave: its 64 lanes' reads tile the
+// row's 1088 bytes.
+// ---------------------------------------------------------------------------
+
+struct Q8Half {
+    uint32_t w[6];  // [0] the dword holding d, [1..4] the dwordx4, [5] the tail dword
+};
+
+// The lane's three reads; shp_q8.hpp states why each stays inside the row.
+__device__ __forceinline__ Q8Half q8_half_load(const char * row, const Q8HalfPos & p) {
+    Q8Half         h;
+    const u32x4_a4 v = *reinterpret_cast<const u32x4_a4 *>(row + p.qbase);
+    h.w[0]           = *reinterpret_cast<const uint32_t *>(row + p.dbase);
+    h.w[1]           = v.x;
+    h.w[2]           = v.y;
+    h.w[3]           = v.z;
+    h.w[4]           = v.w;
+    h.w[5]           = *reinterpret_cast<const uint32_t *>(row + p.tail);
+    return h;
+}
+
+// The 16 dequantised values q * fp16(d), each one exact product.
+__device__ __forceinline__ void q8_half_decode(const Q8Half & h, const Q8HalfPos & p, float (&o)[16]) {
+    const float d = f16_bits_to_f32(q8_half_dbits(h.w, p));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t q = q8_half_quads(h.w, p, i);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            o[4 * i + k] = sbyte(q, k) * d;
+        }
+    }
+}
+
+__device__ __forceinline__ void store16(float * dst, const float (&o)[16]) {
+    f32x4 * out = reinterpret_cast<f32x4 *>(dst);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        st_stream(out + k, f32x4{ o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3] });
+    }
+}
+
+// Row index of this lane's group; for LPR >= 64 every lane of a wave has the
+// same row, which readfirstlane makes visible to the compiler so that the id
+// and the table row base are scalar.
+template <int LPR> __device__ __forceinline__ int row_in_block() {
+    const int r = static_cast<int>(threadIdx.x) / LPR;
+    if constexpr (LPR >= kWave) {
+        return __builtin_amdgcn_readfirstlane(r);
+    } else {
+        return r;
+    }
+}
+
+// Q8_0 get_rows: LPR = ne0/16 lanes per row.
+template <int LPR> __global__ __launch_bounds__(256) void k_get_rows_q8h(const GatherArgs a) {
+    const int64_t R = static_cast<int64_t>(blockIdx.x) * (256 / LPR) + row_in_block<LPR>();
+    if (R >= a.total) {
+        return;
+    }
+    const int l = static_cast<int>(threadIdx.x) % LPR;
+    int32_t      id;
+    const char * srow;
+    float *      drow;
+    gather_coords(a, R, id, srow, drow);
+    float o[16];
+    if (id < 0 || id >= a.srows) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            o[j] = __uint_as_float(kQNaN);
+        }
+    } else {
+        const Q8HalfPos p = q8_half_pos(l);
+        q8_half_decode(q8_half_load(srow, p), p, o);
+    }
+    store16(drow + 16 * l, o);
+}
+
+// Q8_0 gather->sum: LPR = ne0/16 lanes per frame. Groups are taken in chunks
+// of 16 in three phases -- every id, then every row offset, then every row
+// load (6 dwords per group per lane) -- so a chunk costs one id round trip and
+// one row round trip, not one per group. The ids are vector loads (in-order
+// vmcnt lets all 16 overlap). Per group the kernel keeps only the table base
+// and a 32-bit row count in scalar registers; row offsets are 32-bit. Slots
+// past the last group read group 0's table (the host fills them) and are
+// masked out of the sum. The sum is taken in group order from -0.0f, the
+// identity of f32 addition (-0 + v == v bit for bit), so group 0 needs no
+// special case.
+constexpr int kSumChunk = 16;
+
+template <bool FIRST>
+__device__ __forceinline__ void q8_sum_chunk(const GatherSumArgs & a, int g0, int64_t f, const Q8HalfPos & p,
+                                             float (&acc)[16], uint32_t & bad) {
+    uint32_t id[kSumChunk];
+#pragma unroll
+    for (int j = 0; j < kSumChunk; ++j) {
+        const int g = FIRST ? j : g0 + j;
+        id[j]       = static_cast<uint32_t>(group_id(a, g < a.ngroups ? g : 0, f));
+    }
+    uint32_t off[kSumChunk];
+#pragma unroll
+    for (int j = 0; j < kSumChunk; ++j) {
+        const int      g  = FIRST ? j : g0 + j;
+        const uint32_t ok = id[j] < a.rows32[g] ? 1u : 0u;  // unsigned: a negative id is out of range too
+        bad |= (g < a.ngroups) ? (ok ^ 1u) : 0u;
+        off[j] = (ok ? id[j] : 0u) * a.rowbytes;
+    }
+    Q8Half h[kSumChunk];
+#pragma unroll
+    for (int j = 0; j < kSumChunk; ++j) {
+        h[j] = q8_half_load(a.tab[FIRST ? j : g0 + j] + off[j], p);
+    }
+#pragma unroll
+    for (int j = 0; j < kSumChunk; ++j) {
+        float o[16];
+        q8_half_decode(h[j], p, o);
+        if ((FIRST ? j : g0 + j) < a.ngroups) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                acc[k] = acc[k] + o[k];
+            }
+        }
+    }
+}
+
+template <int LPR> __global__ __launch_bounds__(256) void k_get_rows_sum_q8h(const GatherSumArgs a) {
+    const int64_t f = static_cast<int64_t>(blockIdx.x) * (256 / LPR) + static_cast<int>(threadIdx.x) / LPR;
+    if (f >= a.frames) {
+        return;
+    }
+    const int       l = static_cast<int>(threadIdx.x) % LPR;
+    const Q8HalfPos p = q8_half_pos(l);
+    float           acc[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        acc[j] = -0.0f;
+    }
+    uint32_t bad = 0;
+    q8_sum_chunk<true>(a, 0, f, p, acc, bad);
+    for (int g0 = kSumChunk; g0 < a.ngroups; g0 += kSumChunk) {
+        q8_sum_chunk<false>(a, g0, f, p, acc, bad);
+    }
+    if (bad != 0) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            acc[k] = __uint_as_float(kQNaN);
+        }
+    }
+    store16(reinterpret_cast<float *>(reinterpret_cast<char *>(a.dst) + f * a.dnb1) + 16 * l, acc);
+}
+
+// ---------------------------------------------------------------------------
+// Q8_0 through LDS (ne0 = 256*NQ with NQ = 4, 8, 16; rows 16-byte aligned;
+// geometry and its bounds in shp_q8.hpp). One wave per output row: the row's
+// bytes arrive with aligned dwordx4 loads, go through a wave-private LDS
+// buffer, and each lane decodes the elements of its coalesced float4 stores
+// (elements 256k + 4l..+3), so every load and every store of the wave is a
+// contiguous, aligned run.
+// ---------------------------------------------------------------------------
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int NQ> struct Q8Row {
+    u32x4    v[NQ / 4];  // dwords 256r + 4l .. 256r + 4l + 3
+    uint32_t x;          // dword 256*(NQ/4) + l, for lanes l < 4*NQ
+};
+
+template <int NQ> __device__ __forceinline__ Q8Row<NQ> q8_row_load(const char * row, int l) {
+    Q8Row<NQ>     r;
+    const u32x4 * v = reinterpret_cast<const u32x4 *>(row);
+#pragma unroll
+    for (int q = 0; q < NQ / 4; ++q) {
+        r.v[q] = v[64 * q + l];
+    }
+    r.x = l < 4 * NQ ? reinterpret_cast<const uint32_t *>(row)[256 * (NQ / 4) + l] : 0u;
+    return r;
+}
+
+template <int NQ> __device__ __forceinline__ void q8_row_stage(uint32_t * lds, const Q8Row<NQ> & r, int l) {
+#pragma unroll
+    for (int q = 0; q < NQ / 4; ++q) {
+        reinterpret_cast<u32x4 *>(lds)[64 * q + l] = r.v[q];
+    }
+    if (l < 4 * NQ) {
+        lds[256 * (NQ / 4) + l] = r.x;
+    }
+}
+
+// Quad k of lane l: the four values q * fp16(d), each one exact product.
+template <int NQ> __device__ __forceinline__ void q8_row_decode(const uint32_t * lds, int l, float (&o)[4 * NQ]) {
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        const Q8QuadPos p = q8_quad_pos(k, l);
+        const uint32_t  q = bytes_at(lds[p.adw + 1], lds[p.adw], p.sh);
+        const float     d = f16_bits_to_f32((lds[p.ddw] >> p.dsh) & 0xffffu);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            o[4 * k + i] = sbyte(q, i) * d;
+        }
+    }
+}
+
+template <int NQ> __device__ __forceinline__ void q8_row_store(float * drow, int l, const float (&o)[4 * NQ]) {
+    f32x4 * out = reinterpret_cast<f32x4 *>(drow);
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        st_stream(out + 64 * k + l, f32x4{ o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3] });
+    }
+}
+
+constexpr int kQ8StageWaves = 4;  // waves (rows or frames) per 256-thread block
+
+template <int NQ> __global__ __launch_bounds__(256) void k_get_rows_q8s(const GatherArgs a) {
+    __shared__ uint32_t s_row[kQ8StageWaves][q8_row_dwords(NQ) + kQ8StagePadDwords];
+    const int           w = static_cast<int>(threadIdx.x) / kWave;
+    const int           l = static_cast<int>(threadIdx.x) % kWave;
+    const int64_t       R = static_cast<int64_t>(blockIdx.x) * kQ8StageWaves + w;
+    if (R >= a.total) {
+        return;  // no block barrier below: only this wave uses s_row[w]
+    }
+    int32_t      id;
+    const char * srow;
+    float *      drow;
+    gather_coords(a, R, id, srow, drow);
+    float o[4 * NQ];
+    if (id < 0 || id >= a.srows) {
+#pragma unroll
+        for (int j = 0; j < 4 * NQ; ++j) {
+            o[j] = __uint_as_float(kQNaN);
+        }
+    } else {
+        const Q8Row<NQ> r = q8_row_load<NQ>(srow, l);
+        q8_row_stage<NQ>(s_row[w], r, l);
+        __syncwarp();
+        q8_row_decode<NQ>(s_row[w], l, o);
+    }
+    q8_row_store<NQ>(drow, l, o);
+}
+
+// Gather->sum through LDS: one wave per frame. Groups go in chunks of GC: the
+// chunk's ids are loaded together, then its rows (into registers), then each
+// row in group order is staged in the wave's LDS buffer, decoded and added.
+// Slots past the last group read group 0's table (the host fills them) and
+// are not added. The sum starts at -0.0f, the identity of f32 addition.
+template <int NQ, int GC> __global__ __launch_bounds__(256) void k_get_rows_sum_q8s(const GatherSumArgs a) {
+    __shared__ uint32_t s_row[kQ8StageWaves][q8_row_dwords(NQ) + kQ8StagePadDwords];
+    const int           w = static_cast<int>(threadIdx.x) / kWave;
+    const int           l = static_cast<int>(threadIdx.x) % kWave;
+    const int64_t       f = static_cast<int64_t>(blockIdx.x) * kQ8StageWaves + w;
+    if (f >= a.frames) {
+        return;  // no block barrier below: only this wave uses s_row[w]
+    }
+    float acc[4 * NQ];
+#pragma unroll
+    for (int j = 0; j < 4 * NQ; ++j) {
+        acc[j] = -0.0f;
+    }
+    uint32_t bad = 0;
+    for (int g0 = 0; g0 < a.ngroups; g0 += GC) {
+        uint32_t id[GC];
+#pragma unroll
+        for (int j = 0; j < GC; ++j) {
+            const int g = g0 + j;
+            id[j]       = static_cast<uint32_t>(group_id(a, g < a.ngroups ? g : 0, f));
+        }
+        // Every lane of the wave read the same id (one frame per wave): move it
+        // to a scalar register, so the bounds check and the row base are scalar
+        // and each row load is a scalar base plus the lane's small offset.
+        Q8Row<NQ> r[GC];
+#pragma unroll
+        for (int j = 0; j < GC; ++j) {
+            const int      g   = g0 + j;
+            const uint32_t sid = __builtin_amdgcn_readfirstlane(id[j]);
+            const uint32_t ok  = sid < a.rows32[g] ? 1u : 0u;  // unsigned: a negative id is out of range too
+            bad |= (g < a.ngroups) ? (ok ^ 1u) : 0u;
+            r[j] = q8_row_load<NQ>(a.tab[g] + static_cast<uint64_t>(ok ? sid : 0u) * a.rowbytes, l);
+        }
+#pragma unroll
+        for (int j = 0; j < GC; ++j) {
+            if (g0 + j < a.ngroups) {
+                q8_row_stage<NQ>(s_row[w], r[j], l);
+                __syncwarp();
+                float o[4 * NQ];
+                q8_row_decode<NQ>(s_row[w], l, o);
+                __syncwarp();
+#pragma unroll
+                for (int k = 0; k < 4 * NQ; ++k) {
+                    acc[k] = acc[k] + o[k];
+                }
+            }
+        }
+    }
+    if (bad != 0) {
+#pragma unroll
+        for (int k = 0; k < 4 * NQ; ++k) {
+            acc[k] = __uint_as_float(kQNaN);
+        }
+    }
+    q8_row_store<NQ>(reinterpret_cast<float *>(reinterpret_cast<char *>(a.dst) + f * a.dnb1), l, acc);
+}
+
 // Any type / alignment: one wave per row, element by element.
 template <int TYPE> __global__ __launch_bounds__(256) void k_get_rows_generic(const GatherArgs a) {
     const int     lane = threadIdx.x % kWave;
@@ -251,83 +567,6 @@ template <int TYPE> __global__ __launch_bounds__(256) void k_get_rows_generic(co
 // ---------------------------------------------------------------------------
 // gather -> ordered sum over groups
 // ---------------------------------------------------------------------------
-
-__device__ __forceinline__ int32_t group_id(const GatherSumArgs & a, int g, int64_t f) {
-    return *reinterpret_cast<const int32_t *>(reinterpret_cast<const char *>(a.ids) + g * a.ids_gstride + f * 4);
-}
-
-// Q8_0 sum: lane owns one block pair of the frame's output row (LPR = ne0/64),
-// accumulates 64 floats over the groups in order. Two groups' loads are issued
-// before either is decoded.
-template <int LPR> __global__ __launch_bounds__(256) void k_get_rows_sum_q8(const GatherSumArgs a) {
-    const int     l = threadIdx.x % LPR;
-    const int64_t f = static_cast<int64_t>(blockIdx.x) * (256 / LPR) + threadIdx.x / LPR;
-    if (f >= a.frames) {
-        return;
-    }
-    float acc[64];
-    bool  bad = false;
-    int   g   = 0;
-    for (; g + 1 < a.ngroups; g += 2) {
-        const int32_t id0 = group_id(a, g, f);
-        const int32_t id1 = group_id(a, g + 1, f);
-        const bool    ok0 = id0 >= 0 && id0 < a.trows[g];
-        const bool    ok1 = id1 >= 0 && id1 < a.trows[g + 1];
-        bad               = bad || !ok0 || !ok1;
-        uint32_t D0[17], D1[17];
-        q8_load_pair(a.tab[g] + static_cast<int64_t>(ok0 ? id0 : 0) * a.tnb1[g], l, D0);
-        q8_load_pair(a.tab[g + 1] + static_cast<int64_t>(ok1 ? id1 : 0) * a.tnb1[g + 1], l, D1);
-        float o[64];
-        q8_decode_pair(D0, o);
-        if (g == 0) {
-#pragma unroll
-            for (int j = 0; j < 64; ++j) {
-                acc[j] = o[j];
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 64; ++j) {
-                acc[j] = acc[j] + o[j];
-            }
-        }
-        q8_decode_pair(D1, o);
-#pragma unroll
-        for (int j = 0; j < 64; ++j) {
-            acc[j] = acc[j] + o[j];
-        }
-    }
-    if (g < a.ngroups) {
-        const int32_t id = group_id(a, g, f);
-        const bool    ok = id >= 0 && id < a.trows[g];
-        bad              = bad || !ok;
-        uint32_t D[17];
-        q8_load_pair(a.tab[g] + static_cast<int64_t>(ok ? id : 0) * a.tnb1[g], l, D);
-        float o[64];
-        q8_decode_pair(D, o);
-        if (g == 0) {
-#pragma unroll
-            for (int j = 0; j < 64; ++j) {
-                acc[j] = o[j];
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 64; ++j) {
-                acc[j] = acc[j] + o[j];
-            }
-        }
-    }
-    if (bad) {
-#pragma unroll
-        for (int j = 0; j < 64; ++j) {
-            acc[j] = __uint_as_float(kQNaN);
-        }
-    }
-    float4 * out = reinterpret_cast<float4 *>(reinterpret_cast<char *>(a.dst) + f * a.dnb1) + l * 16;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        out[k] = make_float4(acc[4 * k], acc[4 * k + 1], acc[4 * k + 2], acc[4 * k + 3]);
-    }
-}
 
 // F32/F16/BF16 sum: lane owns CPL 16-byte chunks of the frame's row.
 template <int TYPE, int CPL> __global__ __launch_bounds__(256) void k_get_rows_sum_vec(const GatherSumArgs a) {
@@ -412,6 +651,43 @@ int lanes_for(int64_t units) {
 template <int TYPE> shp_status_t launch_get_rows(const GatherArgs & a, bool vec, hipStream_t stream) {
     if (vec) {
         if constexpr (TYPE == SHP_TYPE_Q8_0) {
+            if (a.staged) {
+                const int64_t blocks = (a.total + kQ8StageWaves - 1) / kQ8StageWaves;
+                switch (a.ne0) {
+                    case 1024:
+                        hipLaunchKernelGGL(k_get_rows_q8s<4>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                        break;
+                    case 2048:
+                        hipLaunchKernelGGL(k_get_rows_q8s<8>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                        break;
+                    default:
+                        hipLaunchKernelGGL(k_get_rows_q8s<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                        break;
+                }
+                return launch_status();
+            }
+            const int nhalf = a.ne0 / 16;
+            if (nhalf >= 16 && nhalf <= 256 && (nhalf & (nhalf - 1)) == 0) {
+                const int64_t blocks = (a.total * nhalf + 255) / 256;
+                switch (nhalf) {
+                    case 16:
+                        hipLaunchKernelGGL(k_get_rows_q8h<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                        break;
+                    case 32:
+                        hipLaunchKernelGGL(k_get_rows_q8h<32>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                        break;
+                    case 64:
+                        hipLaunchKernelGGL(k_get_rows_q8h<64>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                        break;
+                    case 128:
+                        hipLaunchKernelGGL(k_get_rows_q8h<128>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                        break;
+                    default:
+                        hipLaunchKernelGGL(k_get_rows_q8h<256>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                        break;
+                }
+                return launch_status();
+            }
             const int lpr = lanes_for(a.ne0 / 64);
             const int64_t blocks = (a.total * lpr + 255) / 256;
             if (lpr == 64) {
@@ -452,18 +728,49 @@ template <int TYPE> shp_status_t launch_get_rows(const GatherArgs & a, bool vec,
 template <int TYPE> shp_status_t launch_get_rows_sum(const GatherSumArgs & a, bool vec, hipStream_t stream) {
     if (vec) {
         if constexpr (TYPE == SHP_TYPE_Q8_0) {
-            const int     lpr    = a.ne0 / 64;
-            const int64_t blocks = (a.frames * lpr + 255) / 256;
-            if (lpr == 64) {
-                hipLaunchKernelGGL(k_get_rows_sum_q8<64>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
-                                   a);
-            } else if (lpr == 32) {
-                hipLaunchKernelGGL(k_get_rows_sum_q8<32>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
-                                   a);
-            } else {
-                hipLaunchKernelGGL(k_get_rows_sum_q8<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
-                                   a);
+            if (a.staged) {
+                const int64_t blocks = (a.frames + kQ8StageWaves - 1) / kQ8StageWaves;
+                switch (a.ne0) {
+                    case 1024:
+                        hipLaunchKernelGGL((k_get_rows_sum_q8s<4, 8>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                                           stream, a);
+                        break;
+                    case 2048:
+                        hipLaunchKernelGGL((k_get_rows_sum_q8s<8, 4>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                                           stream, a);
+                        break;
+                    default:
+                        hipLaunchKernelGGL((k_get_rows_sum_q8s<16, 2>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                                           stream, a);
+                        break;
+                }
+                return launch_status();
             }
+            const int nhalf = a.ne0 / 16;
+            if (nhalf >= 16 && nhalf <= 256 && (nhalf & (nhalf - 1)) == 0) {
+                const int64_t blocks = (a.frames * nhalf + 255) / 256;
+                switch (nhalf) {
+                    case 16:
+                        hipLaunchKernelGGL(k_get_rows_sum_q8h<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                        break;
+                    case 32:
+                        hipLaunchKernelGGL(k_get_rows_sum_q8h<32>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                        break;
+                    case 64:
+                        hipLaunchKernelGGL(k_get_rows_sum_q8h<64>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                        break;
+                    case 128:
+                        hipLaunchKernelGGL(k_get_rows_sum_q8h<128>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                        break;
+                    default:
+                        hipLaunchKernelGGL(k_get_rows_sum_q8h<256>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                        break;
+                }
+                return launch_status();
+            }
+            const int64_t blocks = (a.frames + 3) / 4;
+            hipLaunchKernelGGL(k_get_rows_sum_generic<TYPE>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                               a);
         } else {
             const int     cpl    = (a.ne0 / elems_per_chunk<TYPE>() + kWave - 1) / kWave;
             const int64_t blocks = (a.frames + 3) / 4;
@@ -483,6 +790,11 @@ template <int TYPE> shp_status_t launch_get_rows_sum(const GatherSumArgs & a, bo
     const int64_t blocks = (a.frames + 3) / 4;
     hipLaunchKernelGGL(k_get_rows_sum_generic<TYPE>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
     return launch_status();
+}
+
+// Q8_0 widths the LDS-staged kernels take (one wave per row, NQ = ne0/256).
+bool q8_staged_width(int64_t ne0) {
+    return ne0 == 1024 || ne0 == 2048 || ne0 == 4096;
 }
 
 bool gather_type_ok(int32_t t) {
@@ -528,6 +840,8 @@ extern "C" shp_status_t shp_get_rows(const shp_tensor * src,
     a.ne11  = ids->ne[1];
     a.total = ids->ne[0] * ids->ne[1] * ids->ne[2];
     a.batched = ids->ne[1] > 1 || ids->ne[2] > 1;
+    a.staged  = src->type == SHP_TYPE_Q8_0 && q8_staged_width(src->ne[0]) && rows_aligned(*src, 16) &&
+               rows_aligned(*dst, 16);
     a.ne0   = static_cast<int32_t>(src->ne[0]);
     if ((a.total + 3) / 4 > INT32_MAX) {
         return SHP_ERR_UNSUPPORTED;
@@ -581,6 +895,27 @@ extern "C" shp_status_t shp_get_rows_sum(const shp_tensor * tables,
         a.trows[g] = t.ne[1];
         vec        = vec && rows_aligned(t, type == SHP_TYPE_Q8_0 ? 4 : 16);
     }
+    // Q8_0 half-block path: one row size for every table, 32-bit offsets.
+    bool q8h = type == SHP_TYPE_Q8_0;
+    for (int g = 0; g < n_tables && q8h; ++g) {
+        const shp_tensor & t = tables[g];
+        q8h = t.nb[1] == row_bytes(type, ne0) && t.ne[1] <= INT32_MAX &&
+              static_cast<uint64_t>(t.ne[1]) * t.nb[1] < (uint64_t{ 1 } << 31);
+    }
+    if (q8h) {
+        a.staged = q8_staged_width(ne0) && rows_aligned(*dst, 16);
+        for (int g = 0; g < n_tables; ++g) {
+            a.staged = a.staged && reinterpret_cast<uintptr_t>(tables[g].data) % 16 == 0;
+        }
+        a.rowbytes = static_cast<uint32_t>(row_bytes(type, ne0));
+        for (int g = 0; g < kMaxGroups; ++g) {
+            const int src = g < n_tables ? g : 0;
+            a.rows32[g]   = static_cast<uint32_t>(tables[src].ne[1]);
+            if (g >= n_tables) {
+                a.tab[g] = a.tab[0];
+            }
+        }
+    }
     a.ids         = static_cast<const int32_t *>(ids->data);
     a.ids_gstride = static_cast<int64_t>(ids->nb[1]);
     a.dst         = static_cast<float *>(dst->data);
@@ -600,7 +935,6 @@ extern "C" shp_status_t shp_get_rows_sum(const shp_tensor * tables,
         case SHP_TYPE_BF16:
             return launch_get_rows_sum<SHP_TYPE_BF16>(a, vec && ne0 % 8 == 0 && ne0 <= 8 * 4 * kWave, st);
         default:
-            return launch_get_rows_sum<SHP_TYPE_Q8_0>(
-                a, vec && (ne0 == 16 * 64 || ne0 == 32 * 64 || ne0 == 64 * 64), st);
+            return launch_get_rows_sum<SHP_TYPE_Q8_0>(a, vec && q8h, st);
     }
 }

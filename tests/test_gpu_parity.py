@@ -188,6 +188,7 @@ def test_get_rows_batched_and_out_of_range(gpu):
 
 
 @pytest.mark.parametrize("kind,ne0,groups", [("q8_0", 1024, 16), ("q8_0", 2048, 15), ("q8_0", 4096, 3),
+                                             ("q8_0", 1024, 20), ("q8_0", 4096, 5), ("q8_0", 512, 7),
                                              ("q8_0", 96, 5), ("bf16", 1024, 16), ("f16", 2048, 4),
                                              ("f32", 1024, 15), ("f32", 8, 4), ("f32", 3000, 2)])
 def test_get_rows_sum_bitexact(gpu, kind, ne0, groups):
@@ -488,3 +489,57 @@ def test_golden_g2_summed_embedding_on_gpu(gpu):
     got = _np(gpu.get_rows_sum([_t(gpu, t) for t in tables], _t(gpu, np.array([[c] for c in codes], np.int32))))
     assert_bitexact(got.reshape(-1), summed_ref)
     assert np.abs(got.reshape(-1) - np.array(d["expected_summed_embedding"], np.float32)).max() < d["tolerance_cpu"]
+
+
+def test_q8_last_row_at_end_of_allocation(gpu):
+    """Regression: 16 Q8_0 tables stacked in one allocation of exactly 34 MiB (a
+    multiple of the allocator's 2 MiB granularity, so nothing follows the last
+    row of table 15). Gathering that last row, alone and in the gather->sum,
+    must read only inside the row and match the oracle bit for bit."""
+    import torch
+    rng = np.random.default_rng(SEED + 34)
+    groups, rows, ne0 = 16, 2048, 1024
+    raw = np.stack([F.q8_0_synthetic(rng, rows, ne0) for _ in range(groups)])
+    assert raw.nbytes == 34 << 20
+    dev = torch.from_numpy(raw).cuda()
+    tabs = [gpu.Q8Tensor(dev[t], ne0) for t in range(groups)]
+    ids = np.array([rows - 1, 0, rows - 1, 17], np.int32)
+    got = _np(gpu.get_rows(tabs[-1], _t(gpu, ids)))
+    assert_bitexact(got, F.q8_0_dequant(raw[-1], ne0)[ids])
+    codes = rng.integers(0, rows, (groups, 64)).astype(np.int32)
+    codes[:, :3] = rows - 1
+    ref = R.run(lambda g: R.sum_code_embeddings(g, list(raw), R.Q8_0, ne0, codes))
+    assert_bitexact(_np(gpu.get_rows_sum(tabs, _t(gpu, codes))), ref)
+
+
+@pytest.mark.parametrize("ne0", [1024, 2048])
+def test_q8_unaligned_table_and_bad_id_in_sum(gpu, ne0):
+    """A Q8_0 table view that starts 4 bytes into its allocation (4-byte but not
+    16-byte aligned rows) takes the register-decode kernels instead of the
+    LDS-staged ones and still matches bit for bit; an out-of-range id in one
+    group of a Q8_0 gather->sum turns that frame into NaN and leaves the
+    others exact."""
+    import torch
+    rng = np.random.default_rng(SEED + ne0 + 4)
+    rows, rb = 64, ne0 // 32 * 34
+    raw = F.q8_0_synthetic(rng, rows, ne0)
+    buf = torch.zeros(rows * rb + 16, dtype=torch.uint8, device="cuda")
+    buf[4:4 + rows * rb] = torch.from_numpy(raw.reshape(-1)).cuda()
+    view = gpu.Q8Tensor(buf[4:4 + rows * rb].view(rows, rb), ne0)
+    ids = rng.integers(0, rows, 40).astype(np.int32)
+    assert_bitexact(_np(gpu.get_rows(view, _t(gpu, ids))), F.q8_0_dequant(raw, ne0)[ids])
+    tabs = [F.q8_0_synthetic(rng, rows, ne0) for _ in range(6)]
+    codes = rng.integers(0, rows, (6, 50)).astype(np.int32)
+    ref = R.run(lambda g: R.sum_code_embeddings(g, tabs, R.Q8_0, ne0, codes))
+    dev = [gpu.Q8Tensor(_t(gpu, t), ne0) for t in tabs]
+    assert_bitexact(_np(gpu.get_rows_sum(dev, _t(gpu, codes))), ref)
+    mixed = [view] + dev[1:]
+    ref_mixed = R.run(lambda g: R.sum_code_embeddings(g, [raw] + tabs[1:], R.Q8_0, ne0, codes))
+    assert_bitexact(_np(gpu.get_rows_sum(mixed, _t(gpu, codes))), ref_mixed)
+    bad = codes.copy()
+    bad[3, 7] = rows
+    bad[1, 9] = -1
+    out = _np(gpu.get_rows_sum(dev, _t(gpu, bad)))
+    assert np.isnan(out[7]).all() and np.isnan(out[9]).all()
+    keep = [f for f in range(50) if f not in (7, 9)]
+    assert_bitexact(out[keep], ref[keep])
