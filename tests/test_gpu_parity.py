@@ -365,13 +365,42 @@ def test_glu_swiglu_single_tensor(gpu, swapped):
     assert_close(_np(gpu.glu_swiglu(_t(gpu, a), swapped)), ref)
 
 
-@pytest.mark.parametrize("T,C", [(256, 512), (64, 128), (31, 30), (5, 1024)])
+@pytest.mark.parametrize("T,C", [(256, 512), (64, 128), (31, 30), (5, 1024), (9, 2048), (3, 1028)])
 def test_snake(gpu, T, C):
+    """C % 4 == 0: the flat kernel (4 rows per lane, division through a double
+    reciprocal; T % 4 != 0 leaves a partial group); C % 4 != 0: the row kernel.
+    Row 0 holds large x, so |alpha*x| crosses 2^15 and those elements take
+    OCML's sine instead of the fast one."""
     rng = np.random.default_rng(SEED + T + C)
     x = rng.standard_normal((T, C)).astype(np.float32)
+    x[0, ::3] *= 20000.0
     alpha = np.exp(rng.uniform(np.log(0.1), np.log(10.0), C)).astype(np.float32)
     ref = R.run(lambda g: R.snake(g, x, alpha))
     assert_close(_np(gpu.snake(_t(gpu, x), _t(gpu, alpha))), ref)
+
+
+def test_snake_special_alphas(gpu):
+    """Channels whose alpha is 0, -0, +-inf or NaN take the f32 division, the
+    others the reciprocal route; power-of-two, negative, subnormal and extreme
+    alphas exercise exact ties, overflow to inf and underflow. NaN and inf land
+    where the oracle puts them; finite outputs meet the Snake tolerance. 37 rows
+    also leave a partial group of the kernel's 4 rows per lane."""
+    rng = np.random.default_rng(SEED + 99)
+    T, C = 37, 64
+    x = rng.standard_normal((T, C)).astype(np.float32)
+    x[0, :] = 0.0
+    alpha = np.exp(rng.uniform(np.log(0.1), np.log(10.0), C)).astype(np.float32)
+    alpha[:16] = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 2.0, 0.125, -4.0, 1e-39, -1e-30, 3e38, 1e-45,
+                           2.0 ** -126, 2.0 ** 100, -0.5, 1.0], np.float32)
+    with np.errstate(all="ignore"):
+        ref = R.run(lambda g: R.snake(g, x, alpha))
+    got = _np(gpu.snake(_t(gpu, x), _t(gpu, alpha)))
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    inf = np.isinf(ref)
+    assert np.array_equal(np.isinf(got), inf) and np.array_equal(got[inf], ref[inf])
+    fin = np.isfinite(ref)
+    den = np.maximum(np.abs(ref[fin]).astype(np.float64), 1e-3)
+    assert (np.abs(got[fin].astype(np.float64) - ref[fin]) / den).max() <= REL_TOL
 
 
 def _specials(n, rng):

@@ -5,6 +5,11 @@
   of every row width the kernels take, and decodes each lane's scale and quants.
 - trig_check: the rope's double-precision cos/sin (shp_trig.hpp) rounds to the
   same f32 as libm's double sin/cos.
+- div_check: Snake's division by a per-channel double reciprocal (shp_div.hpp)
+  gives the IEEE f32 quotient, also with a reciprocal one ulp off, and the
+  device's Newton steps give that reciprocal.
+- sinf_check: Snake's branch-free sine (shp_sinf.hpp) is within 1 ulp of the
+  correctly rounded sine over its whole range.
 """
 import os
 import subprocess
@@ -17,8 +22,8 @@ CSRC = os.path.join(os.path.dirname(HERE), "synthesize.cpp_amd", "csrc")
 
 def _build_and_run(tmp_path, name):
     exe = tmp_path / name
-    subprocess.run(["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", "-I" + CSRC, "-o", str(exe),
-                    os.path.join(HERE, "host", name + ".cpp")], check=True)
+    subprocess.run(["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", "-ffp-contract=off", "-I" + CSRC, "-o", str(exe),
+                    os.path.join(HERE, "host", name + ".cpp"), "-lm"], check=True)
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
     return r.returncode, r.stdout
 
@@ -32,3 +37,15 @@ def test_q8_half_block_reads_stay_inside_the_row(tmp_path):
 def test_rope_sincos_is_correctly_rounded(tmp_path):
     rc, out = _build_and_run(tmp_path, "trig_check")
     assert rc == 0, out
+
+
+def test_snake_division_by_reciprocal_is_the_ieee_quotient(tmp_path):
+    rc, out = _build_and_run(tmp_path, "div_check")
+    pairs, bad, rcps, rcp_bad = map(int, out.split()[-4:])
+    assert rc == 0 and bad == 0 and rcp_bad == 0 and pairs > 10 ** 7 and rcps > 10 ** 6, out
+
+
+def test_snake_fast_sine_within_one_ulp(tmp_path):
+    rc, out = _build_and_run(tmp_path, "sinf_check")
+    tested, worst, _exact, _glibc = out.split()[-4:]
+    assert rc == 0 and int(tested) > 8 * 10 ** 6 and float(worst) <= 1.0, out
