@@ -279,13 +279,19 @@ def suite(args, S, torch):
     on = lambda c: not want or c in want
 
     if on("calib"):
-        # what a plain device copy and a read-only reduction reach on this box
+        # what a plain device copy, a read-only reduction and this library's
+        # copy-like kernel (bare leaky-ReLU: one read, one write) reach on this box
         n = (1 << 30) // 4
         src, dst = randn(n), empty(n)
         acc = torch.empty((), device="cuda", dtype=torch.float32)
         run("calib", "torch copy_ 1 GiB (read+write)", 2 * n * 4, lambda: (lambda: dst.copy_(src)))
         run("calib", "torch sum 1 GiB (read only)", n * 4, lambda: (lambda: torch.sum(src, dim=0, out=acc)))
         del src, dst
+
+        def make_floor():
+            x, y = randn(8192, 2048), empty(8192, 2048)
+            return lambda: S.leaky_relu(x, 0.1, out=y)
+        run("calib", "copy-like floor: bare leaky [2048,8192]", 8 * 8192 * 2048, make_floor)
 
     def norm_case(cfg, T, H, add=False, wsum=True, cold=True):
         def make():

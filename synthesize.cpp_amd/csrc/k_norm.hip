@@ -105,10 +105,11 @@ template <int WT> __device__ __forceinline__ f32x4 cvt_wraw(const WRaw<WT> & r) 
 // waits. The double sum of squares is reduced across the TPR lanes with
 // shuffles, and across waves (TPR > 64) through LDS in a fixed order. Lanes
 // past the end of the row or of the tensor still take part in the barrier.
-template <int TPR, int VPL, int WT, int MODE> __global__ __launch_bounds__(256) void k_rms_norm_vec(const NormArgs a) {
-    constexpr int kRowsPerBlock = 256 / TPR;
+template <int TPR, int VPL, int WT, int MODE, int BLOCK = 256>
+__global__ __launch_bounds__(BLOCK) void k_rms_norm_vec(const NormArgs a) {
+    constexpr int kRowsPerBlock = BLOCK / TPR;
     constexpr int kWavesPerRow  = TPR > kWave ? TPR / kWave : 1;
-    __shared__ double s_part[TPR > kWave ? 256 / kWave : 1];
+    __shared__ double s_part[TPR > kWave ? BLOCK / kWave : 1];
 
     const int     l     = threadIdx.x % TPR;
     const int64_t row   = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / TPR;
@@ -244,9 +245,9 @@ template <int WT, int MODE> __global__ __launch_bounds__(256) void k_rms_norm_ge
 }
 
 template <int WT, int MODE> shp_status_t launch_norm(const NormArgs & a, bool vec, hipStream_t stream) {
-    auto go = [&](auto kernel, int rows_per_block) {
+    auto go = [&](auto kernel, int rows_per_block, int block = 256) {
         const int64_t blocks = (a.nrows + rows_per_block - 1) / rows_per_block;
-        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(block), 0, stream, a);
         return launch_status();
     };
     const int nvec = a.ne0 / 4;
