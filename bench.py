@@ -412,6 +412,22 @@ def suite(args, S, torch):
             run("cfg4", "add_leaky_relu [%d,%d]" % (C, T), 12 * n, make_leaky)
             run("cfg4", "add_leaky_relu+sum [%d,%d]" % (C, T), 16 * n, lambda: make_leaky(with_s=True))
 
+            def make_snake_var(C=C, T=T, beta=False):
+                x, y = randn(T, C), empty(T, C)
+                la = torch.empty(C, device="cuda").uniform_(-3.0, 3.0, generator=g)
+                if beta:
+                    lb = torch.empty(C, device="cuda").uniform_(-3.0, 3.0, generator=g)
+                    return lambda: S.snake_beta(x, la, lb, out=y)
+                al = torch.exp(la)
+                return lambda: S.snake_guarded(x, al, out=y)
+            run("cfg4", "snake_guarded [%d,%d]" % (C, T), 8 * n + 4 * C, make_snake_var)
+            run("cfg4", "snake_beta [%d,%d]" % (C, T), 8 * n + 8 * C, lambda: make_snake_var(beta=True))
+
+            def make_branch(C=C, T=T):
+                ts, y = [randn(T, C) for _ in range(3)], empty(T, C)
+                return lambda: S.sum_scale_leaky_relu(ts, 1.0 / 3.0, 0.1, out=y)
+            run("cfg4", "branch mean 3->scale->leaky [%d,%d]" % (C, T), 16 * n, make_branch)
+
     if on("cfg5"):
         norm_case("cfg5", 8192, 2048)
         norm_case("cfg5", 8192, 2048, add=True)

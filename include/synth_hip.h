@@ -192,6 +192,26 @@ shp_status_t shp_glu_swiglu(const shp_tensor * a, int32_t swapped, shp_tensor * 
 shp_status_t shp_snake(const shp_tensor * x, const shp_tensor * alpha, shp_tensor * y, shp_stream_t stream);
 
 /*
+ * Guarded Snake (Snake1d): codec_snake of src/arch/omnivoice/codec.cpp:51-68,
+ * t = x*alpha_c; s = sinf(t); q = s*s; g = alpha_c*1 + 1e-9 (ggml_scale_bias);
+ * r = q/g; y = x + r, each rounded in f32. Shapes as shp_snake.
+ */
+shp_status_t shp_snake_guarded(const shp_tensor * x, const shp_tensor * alpha, shp_tensor * y, shp_stream_t stream);
+
+/*
+ * SnakeBeta: codec_snake_beta of src/arch/qwen3-tts/codec.cpp:184-199,
+ * a_c = expf(log_alpha_c); b_c = expf(log_beta_c); t = x*a_c; s = sinf(t);
+ * q = s*s (ggml_sqr); g = b_c*1 + 1e-9 (ggml_scale_bias); r = q/g; y = x + r,
+ * each rounded in f32. x, y F32 [C, T]; log_alpha and log_beta F32 with
+ * exactly C elements each ([C] or [C, 1]).
+ */
+shp_status_t shp_snake_beta(const shp_tensor * x,
+                            const shp_tensor * log_alpha,
+                            const shp_tensor * log_beta,
+                            shp_tensor *       y,
+                            shp_stream_t       stream);
+
+/*
  * ggml_add(a, b) then ggml_leaky_relu(., slope, false): the residual carry
  * of src/arch/vits/waveform-decoder.cpp:150-158 (layer l's closing add and
  * layer l+1's opening leaky) and kokoro/generator.cpp:115,180.
@@ -213,6 +233,40 @@ shp_status_t shp_add_leaky_relu(const shp_tensor * a,
  * src/arch/qwen3-tts/operations.cpp:143,147 when it is not fused into a norm.
  */
 shp_status_t shp_add(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream);
+
+/*
+ * ggml_exp: y = expf(x) per element, F32 of one shape
+ * (src/arch/qwen3-tts/codec.cpp:193-194, vits/latent-sampling.cpp:30).
+ */
+shp_status_t shp_exp(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
+
+/*
+ * ggml_scale_bias(x, s, b) and ggml_scale(x, s) (b == 0): y = x*s when
+ * b == 0 (one multiply, so -0 stays -0), else y = fma(x, s, b) rounded once,
+ * as ggml-CPU's vectorised path computes it. With s == 1 (the guards of
+ * omnivoice/codec.cpp:68 and qwen3-tts/codec.cpp:197) every evaluation order
+ * gives the same f32. F32 of one shape.
+ */
+shp_status_t shp_scale_bias(const shp_tensor * x, float s, float b, shp_tensor * y, shp_stream_t stream);
+
+/*
+ * The branch average of src/arch/vits/waveform-decoder.cpp:214-225 and
+ * src/arch/kokoro/generator.cpp:165-179: summed = ((t0 + t1) + t2) + ...
+ * (ggml_add in term order), current = summed*scale (ggml_scale, a plain
+ * multiply), y = leaky_relu(current, slope) as in shp_add_leaky_relu. Pass
+ * scale = 1/n as the builders compute it (1.0f/(float)n); a single term with
+ * scale 1 is the bare leaky_relu, as the builders skip the scale there and
+ * x*1 is exact. terms points to n_terms (1..8) F32 tensors of y's shape;
+ * mean (optional) receives current. All tensors contiguous (a strided view
+ * gives SHP_ERR_UNSUPPORTED).
+ */
+shp_status_t shp_sum_scale_leaky_relu(const shp_tensor * terms,
+                                      int32_t            n_terms,
+                                      float              scale,
+                                      float              slope,
+                                      shp_tensor *       mean,
+                                      shp_tensor *       y,
+                                      shp_stream_t       stream);
 
 #ifdef __cplusplus
 }

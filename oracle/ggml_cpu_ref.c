@@ -13,7 +13,9 @@
  * differ there, and the tests absorb that in tolerance):
  *   - silu uses libm expf for every element (ggml vectorises it with its own
  *     SIMD expf, within ~1 ulp of libm);
- *   - rope is computed without fused multiply-add.
+ *   - rope is computed without fused multiply-add;
+ *   - scale_bias with a non-zero bias is one fused multiply-add (ggml's
+ *     vectorised path on FMA hardware; its scalar tail may round twice).
  */
 #define _GNU_SOURCE
 #include "ggml_cpu_ref.h"
@@ -323,10 +325,19 @@ static void op_unary(const orc_node * n, int ith, int nth) {
                 break;
             }
             case ORC_OP_SCALE_BIAS: {
+                /* ggml-CPU's forward_scale: with b == 0 a plain multiply
+                 * (ggml_vec_scale_f32, so -0 stays -0), else the vectorised
+                 * x*s + b, one fused multiply-add on FMA hardware. */
                 const float s = n->f[0];
                 const float b = n->f[1];
-                for (int64_t i = 0; i < ne0; ++i) {
-                    y[i] = x[i] * s + b;
+                if (b == 0.0f) {
+                    for (int64_t i = 0; i < ne0; ++i) {
+                        y[i] = x[i] * s;
+                    }
+                } else {
+                    for (int64_t i = 0; i < ne0; ++i) {
+                        y[i] = fmaf(x[i], s, b);
+                    }
                 }
                 break;
             }

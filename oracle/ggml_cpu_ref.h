@@ -38,7 +38,7 @@ enum orc_op {
     ORC_OP_SQR,          /* x*x                                     ggml_sqr            */
     ORC_OP_EXP,          /* expf(x)                                 ggml_exp            */
     ORC_OP_LEAKY_RELU,   /* (x>0?x:0) + slope*(x<0?x:0)             ggml_leaky_relu     */
-    ORC_OP_SCALE_BIAS,   /* x*s + b                                 ggml_scale_bias     */
+    ORC_OP_SCALE_BIAS,   /* b==0: x*s; else fma(x, s, b)            ggml_scale_bias     */
     ORC_OP_GET_ROWS,     /* dst[:, r] = to_f32(src0[:, ids[r]])     ggml_get_rows       */
     ORC_OP_CAST_F32,     /* BF16/F16/F32 -> F32                     ggml_cast           */
     ORC_OP_GLU_SWIGLU,   /* single-tensor swiglu                    ggml_swiglu         */

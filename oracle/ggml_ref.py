@@ -154,6 +154,10 @@ class Graph:
     def scale_bias(self, x, s, b):
         return self._unary(OP_SCALE_BIAS, x, f=(s, b))
 
+    def scale(self, x, s):
+        """ggml_scale: ggml_scale_bias with bias 0."""
+        return self._unary(OP_SCALE_BIAS, x, f=(s, 0.0))
+
     def rope_neox(self, x, pos, n_dims, freq_base, freq_scale=1.0, attn_factor=1.0, cs_rounded=False):
         """x: (T, heads, head_dim) f32; pos: (T,) int32. cs_rounded: cos/sin from
         double rounded once to f32 instead of libm cosf/sinf (ggml-CPU's)."""
@@ -253,6 +257,27 @@ def snake_beta(g, x, log_alpha, log_beta):
     squared = g.sqr(g.sin(g.mul(x, alpha)))
     guard = g.scale_bias(beta, 1.0, 1e-9)
     return g.add(x, g.div(squared, guard))
+
+
+def snake_guarded(g, x, alpha):
+    """codec_snake, src/arch/omnivoice/codec.cpp:51-68: mul, sin, mul(s, s),
+    scale_bias(alpha, 1, 1e-9), div, add. x (T, C)."""
+    scaled = g.mul(x, alpha)
+    sine = g.sin(scaled)
+    squared = g.mul(sine, sine)
+    guard = g.scale_bias(alpha, 1.0, 1e-9)
+    return g.add(x, g.div(squared, guard))
+
+
+def sum_scale_leaky(g, terms, scale, slope):
+    """The branch average of src/arch/vits/waveform-decoder.cpp:214-225 and
+    src/arch/kokoro/generator.cpp:165-179: ggml_add over the terms in order,
+    ggml_scale (skipped for one term), then ggml_leaky_relu. Returns (current, y)."""
+    summed = None
+    for t in terms:
+        summed = t if summed is None else g.add(summed, t)
+    current = summed if len(terms) == 1 else g.scale(summed, scale)
+    return current, g.leaky_relu(current, slope)
 
 
 def add_leaky(g, a, b, slope):

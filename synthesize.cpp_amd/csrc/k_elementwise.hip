@@ -1,11 +1,12 @@
 // Elementwise primitives for gfx950: SwiGLU (silu(g)*u), bare silu, the
-// single-tensor GLU, Snake, add->leaky-ReLU with the residual carried out, bare
-// leaky-ReLU, and the plain residual add.
+// single-tensor GLU, the Snake family (Kokoro's Snake, the guarded Snake and
+// SnakeBeta), add->leaky-ReLU with the residual carried out, bare leaky-ReLU,
+// the branch average sum->scale->leaky-ReLU, exp, scale/scale_bias and the
+// plain residual add.
 //
 // Each fused op reproduces the f32 rounding sequence of the unfused ggml node
-// run it replaces (compiled with -ffp-contract=off, IEEE divide, full-range
-// OCML expf/sinf), so the only difference from ggml-CPU is the last ulp of the
-// transcendental itself.
+// run it replaces (compiled with -ffp-contract=off, IEEE divide), so the only
+// difference from ggml-CPU can be the last ulp of a transcendental.
 //
 // Two launch shapes: a flat kernel for fully contiguous, 16-byte aligned
 // tensors (the large vocoder and MLP tensors), one float4 per lane per operand;
@@ -13,6 +14,7 @@
 // stream activations with nontemporal loads and stores.
 
 #include <cmath>
+#include <type_traits>
 
 #include "shp_div.hpp"
 #include "shp_internal.hpp"
@@ -21,7 +23,16 @@
 namespace shp {
 namespace {
 
-enum EwOp { kSwiglu = 0, kSilu = 1, kAdd = 2, kAddLeaky = 3, kLeaky = 4, kSnake = 5 };
+enum EwOp { kSwiglu = 0, kSilu = 1, kAdd = 2, kAddLeaky = 3, kLeaky = 4, kExp = 5, kScale = 6, kScaleBias = 7 };
+
+// Snake family: y = x + sin(x*al)^2 / den with per-channel al and den.
+//   kSnakePlain   (kokoro/operations.cpp:137-147):   al = den = alpha
+//   kSnakeGuarded (omnivoice/codec.cpp:51-68):        al = alpha, den = alpha + 1e-9
+//   kSnakeBeta    (qwen3-tts/codec.cpp:184-199):      al = exp(log_alpha), den = exp(log_beta) + 1e-9
+enum SnakeKind { kSnakePlain = 0, kSnakeGuarded = 1, kSnakeBeta = 2 };
+
+// The fixed guard of Snake1d/SnakeBeta, added by ggml_scale_bias(c, 1.0f, 1e-9f).
+constexpr float kSnakeGuard = 1e-9f;
 
 struct EwArgs {
     const float * a;
@@ -32,7 +43,8 @@ struct EwArgs {
     RowMap        ym;
     float *       s;
     RowMap        sm;
-    const float * alpha;
+    const float * alpha;   // Snake: first per-channel curve
+    const float * beta;    // SnakeBeta: second per-channel curve
     int64_t       nrows;
     int64_t       n4;
     int32_t       ne0;
@@ -40,6 +52,8 @@ struct EwArgs {
     FastDiv       quads;   // Snake flat path: float4 per row (ne0/4)
     int64_t       ntask;   // Snake flat path: lanes = row blocks x quads per row
     float         slope;
+    float         scale;  // kScale / kScaleBias
+    float         bias;   // kScaleBias
     int32_t       pad;
 };
 
@@ -54,9 +68,17 @@ __device__ __forceinline__ float leaky(float x, float slope) {
     return pos + slope * neg;
 }
 
-// One element of the op. `b` is the second input (or the broadcast row value),
-// `al` the Snake channel coefficient; `s` receives the carried sum.
-template <int OP> __device__ __forceinline__ float ew(float a, float b, float al, float slope, float & s) {
+// e^x rounded once to f32: the double exp is within 1 ulp of double, so its
+// f32 rounding is the correctly rounded value unless e^x lies within ~2^-52
+// relative of an f32 rounding boundary. glibc's expf (what ggml_exp calls per
+// element) is also correctly rounded outside such cases.
+__device__ __forceinline__ float exp_f32(float x) {
+    return static_cast<float>(exp(static_cast<double>(x)));
+}
+
+// One element of the op. `b` is the second input (or the broadcast row value);
+// `s` receives the carried sum.
+template <int OP> __device__ __forceinline__ float ew(float a, float b, const EwArgs & g, float & s) {
     if constexpr (OP == kSwiglu) {
         return silu(a) * b;
     } else if constexpr (OP == kSilu) {
@@ -65,23 +87,25 @@ template <int OP> __device__ __forceinline__ float ew(float a, float b, float al
         return a + b;
     } else if constexpr (OP == kAddLeaky) {
         s = a + b;
-        return leaky(s, slope);
+        return leaky(s, g.slope);
     } else if constexpr (OP == kLeaky) {
-        return leaky(a, slope);
+        return leaky(a, g.slope);
+    } else if constexpr (OP == kExp) {
+        return exp_f32(a);
+    } else if constexpr (OP == kScale) {
+        // ggml_scale (bias 0): a plain multiply, so -0 stays -0.
+        return a * g.scale;
     } else {
-        // Snake, kokoro/operations.cpp:143-146: mul, sin, mul, div, add.
-        const float t  = a * al;
-        const float sn = sinf(t);
-        const float q  = sn * sn;
-        const float r  = q / al;
-        return a + r;
+        // ggml_scale_bias with a non-zero bias: one fused multiply-add, as
+        // ggml-CPU's vectorised path computes it on FMA hardware.
+        return fmaf(a, g.scale, g.bias);
     }
 }
 
-template <int OP> __device__ __forceinline__ f32x4 ew4(f32x4 a, f32x4 b, f32x4 al, float slope, f32x4 & s) {
+template <int OP> __device__ __forceinline__ f32x4 ew4(f32x4 a, f32x4 b, const EwArgs & g, f32x4 & s) {
     float       s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
-    const f32x4 o{ ew<OP>(a.x, b.x, al.x, slope, s0), ew<OP>(a.y, b.y, al.y, slope, s1),
-                   ew<OP>(a.z, b.z, al.z, slope, s2), ew<OP>(a.w, b.w, al.w, slope, s3) };
+    const f32x4 o{ ew<OP>(a.x, b.x, g, s0), ew<OP>(a.y, b.y, g, s1), ew<OP>(a.z, b.z, g, s2),
+                   ew<OP>(a.w, b.w, g, s3) };
     s = f32x4{ s0, s1, s2, s3 };
     return o;
 }
@@ -99,14 +123,12 @@ template <int OP, bool HAS_B, bool BCAST, bool HAS_S>
 __global__ __launch_bounds__(256) void k_ew_flat(const EwArgs a) {
     const f32x4 * A    = reinterpret_cast<const f32x4 *>(a.a);
     const f32x4 * B    = reinterpret_cast<const f32x4 *>(a.b);
-    const f32x4 * AL   = reinterpret_cast<const f32x4 *>(a.alpha);
     f32x4 *       Y    = reinterpret_cast<f32x4 *>(a.y);
     f32x4 *       S    = reinterpret_cast<f32x4 *>(a.s);
     const int64_t step = static_cast<int64_t>(gridDim.x) * 256;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < a.n4; i += step) {
-        const f32x4 av  = ld_stream(A + i);
-        f32x4       bv  = splat4(0.0f);
-        f32x4       alv = splat4(1.0f);
+        const f32x4 av = ld_stream(A + i);
+        f32x4       bv = splat4(0.0f);
         if constexpr (HAS_B) {
             if constexpr (BCAST) {
                 bv = B[fastmod(static_cast<uint32_t>(i * 4), a.period) / 4];
@@ -114,79 +136,126 @@ __global__ __launch_bounds__(256) void k_ew_flat(const EwArgs a) {
                 bv = ld_stream(B + i);
             }
         }
-        if constexpr (OP == kSnake) {
-            alv = AL[fastmod(static_cast<uint32_t>(i * 4), a.period) / 4];
-        }
         f32x4 sv = splat4(0.0f);
-        st_stream(Y + i, ew4<OP>(av, bv, alv, a.slope, sv));
+        st_stream(Y + i, ew4<OP>(av, bv, a, sv));
         if constexpr (HAS_S) {
             st_stream(S + i, sv);
         }
     }
 }
 
-// Snake, flat path. The five-node formula is ALU-heavy for a streaming op
-// (a sine and a division per element), so two of its costs are cut without
-// changing its result:
-//   - the division by alpha: a lane owns one quad of channels (4 consecutive
-//     alphas) in kSnakeRows consecutive rows, forms the 4 double reciprocals
-//     once, and q / alpha becomes (float)((double)q * rcp), which is the IEEE
-//     quotient (shp_div.hpp). Lanes whose alphas include 0, inf or NaN take
-//     the f32 division.
-//   - sinf: shp::sin_f32_fast, branch-free and within 1 ulp of the correctly
-//     rounded sine for |t| < 2^15 (shp_sinf.hpp); OCML's sinf beyond that.
-// Each of the wave's loads and stores is still one contiguous 1 KB run (64
-// lanes, consecutive quads of one row). Measured on MI355X at [128,131072]:
-// ~6% faster than one float4 per lane with OCML's sinf and the f32 division.
-constexpr int kSnakeRows = 4;
+// Per-channel coefficients of the Snake family from the stored curves c0
+// (alpha or log alpha) and c1 (log beta). ggml_scale_bias(c, 1.0f, 1e-9f)
+// is c*1 + 1e-9 with c*1 exact, so every evaluation order gives c + 1e-9
+// rounded once.
+struct SnakeCoef {
+    float al;   // multiplier of x inside the sine
+    float den;  // divisor of the squared sine
+};
 
-// kokoro/operations.cpp:143-146: mul, sin, mul, div, add, each rounded in f32.
-template <bool RCP> __device__ __forceinline__ float snake1(float x, float al, double rcp) {
+template <int K> __device__ __forceinline__ SnakeCoef snake_coef(float c0, float c1) {
+    if constexpr (K == kSnakePlain) {
+        return { c0, c0 };
+    } else if constexpr (K == kSnakeGuarded) {
+        return { c0, c0 + kSnakeGuard };
+    } else {
+        return { exp_f32(c0), exp_f32(c1) + kSnakeGuard };
+    }
+}
+
+// The node run mul, sin, mul (or sqr), div, add, each rounded in f32. RCP:
+// divide through the double reciprocal of den (IEEE quotient, shp_div.hpp).
+template <bool RCP> __device__ __forceinline__ float snake1(float x, float al, float den, double rcp) {
     const float t  = x * al;
     const float sn = sin_fast_ok(t) ? sin_f32_fast(t) : sinf(t);
     const float q  = sn * sn;
-    const float r  = RCP ? div_by_rcp(q, rcp) : q / al;
+    const float r  = RCP ? div_by_rcp(q, rcp) : q / den;
     return x + r;
 }
 
-template <bool RCP>
-__device__ __forceinline__ void snake_rows(const f32x4 (&xv)[kSnakeRows], f32x4 al, const double (&rc)[4], int64_t i0,
+// Snake, flat path. The formula is ALU-heavy for a streaming op (a sine and
+// a division per element, and for SnakeBeta two exps per channel), so its
+// costs are cut without changing its result:
+//   - a lane owns one quad of channels (4 consecutive coefficients) in R
+//     consecutive rows, so the per-channel work (the exps, the guard and the
+//     4 double reciprocals) is done once per R rows;
+//   - the division: q / den becomes (float)((double)q * rcp), which is the
+//     IEEE quotient (shp_div.hpp). Lanes whose den include 0, inf or NaN take
+//     the f32 division;
+//   - sinf: shp::sin_f32_fast, branch-free and within 1 ulp of the correctly
+//     rounded sine for |t| < 2^15 (shp_sinf.hpp); OCML's sinf beyond that.
+// The curves are loaded before the rows, so the per-channel work overlaps the
+// row loads. Each of the wave's loads and stores is one contiguous 1 KB run
+// (64 lanes, consecutive quads of one row). Measured on MI355X at
+// [128,131072], plain Snake: ~6% faster than one float4 per lane with OCML's
+// sinf and the f32 division.
+template <int K> struct SnakeRows {
+    static constexpr int R = 4;
+};
+
+template <int K, int R, bool RCP>
+__device__ __forceinline__ void snake_rows(const f32x4 (&xv)[R], f32x4 al, f32x4 den, const double (&rc)[4], int64_t i0,
                                            int64_t c4, int64_t n4, f32x4 * Y) {
 #pragma unroll
-    for (int r = 0; r < kSnakeRows; ++r) {
+    for (int r = 0; r < R; ++r) {
         const int64_t i = i0 + r * c4;
         if (i < n4) {
             const f32x4 v = xv[r];
-            st_stream(Y + i, f32x4{ snake1<RCP>(v.x, al.x, rc[0]), snake1<RCP>(v.y, al.y, rc[1]),
-                                    snake1<RCP>(v.z, al.z, rc[2]), snake1<RCP>(v.w, al.w, rc[3]) });
+            st_stream(Y + i, f32x4{ snake1<RCP>(v.x, al.x, den.x, rc[0]), snake1<RCP>(v.y, al.y, den.y, rc[1]),
+                                    snake1<RCP>(v.z, al.z, den.z, rc[2]), snake1<RCP>(v.w, al.w, den.w, rc[3]) });
         }
     }
 }
 
-__global__ __launch_bounds__(256) void k_snake_flat(const EwArgs a) {
+template <int K> __global__ __launch_bounds__(256) void k_snake_flat(const EwArgs a) {
+    constexpr int R    = SnakeRows<K>::R;
     const f32x4 * X    = reinterpret_cast<const f32x4 *>(a.a);
-    const f32x4 * AL   = reinterpret_cast<const f32x4 *>(a.alpha);
+    const f32x4 * C0   = reinterpret_cast<const f32x4 *>(a.alpha);
+    const f32x4 * C1   = reinterpret_cast<const f32x4 *>(a.beta);
     f32x4 *       Y    = reinterpret_cast<f32x4 *>(a.y);
     const int64_t c4   = a.quads.d;
     const int64_t step = static_cast<int64_t>(gridDim.x) * 256;
     for (int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; t < a.ntask; t += step) {
         const uint32_t rb = fastdiv(static_cast<uint32_t>(t), a.quads);  // row block
         const uint32_t q  = static_cast<uint32_t>(t) - rb * a.quads.d;  // channel quad
-        const int64_t  i0 = static_cast<int64_t>(rb) * kSnakeRows * c4 + q;
-        f32x4          xv[kSnakeRows];
+        const int64_t  i0 = static_cast<int64_t>(rb) * R * c4 + q;
+        const f32x4    c0 = C0[q];
+        f32x4          c1 = splat4(0.0f);
+        if constexpr (K == kSnakeBeta) {
+            c1 = C1[q];
+        }
+        f32x4 xv[R];
 #pragma unroll
-        for (int r = 0; r < kSnakeRows; ++r) {
+        for (int r = 0; r < R; ++r) {
             const int64_t i = i0 + r * c4;
             xv[r]           = i < a.n4 ? ld_stream(X + i) : splat4(0.0f);
         }
-        const f32x4 al = AL[q];
-        if (rcp_route_ok(al.x) && rcp_route_ok(al.y) && rcp_route_ok(al.z) && rcp_route_ok(al.w)) {
-            const double rc[4] = { rcp_d(static_cast<double>(al.x)), rcp_d(static_cast<double>(al.y)),
-                                   rcp_d(static_cast<double>(al.z)), rcp_d(static_cast<double>(al.w)) };
-            snake_rows<true>(xv, al, rc, i0, c4, a.n4, Y);
+        const SnakeCoef k0 = snake_coef<K>(c0.x, c1.x);
+        const SnakeCoef k1 = snake_coef<K>(c0.y, c1.y);
+        const SnakeCoef k2 = snake_coef<K>(c0.z, c1.z);
+        const SnakeCoef k3 = snake_coef<K>(c0.w, c1.w);
+        const f32x4     al{ k0.al, k1.al, k2.al, k3.al };
+        const f32x4     den{ k0.den, k1.den, k2.den, k3.den };
+        if (rcp_route_ok(den.x) && rcp_route_ok(den.y) && rcp_route_ok(den.z) && rcp_route_ok(den.w)) {
+            const double rc[4] = { rcp_d(static_cast<double>(den.x)), rcp_d(static_cast<double>(den.y)),
+                                   rcp_d(static_cast<double>(den.z)), rcp_d(static_cast<double>(den.w)) };
+            snake_rows<K, R, true>(xv, al, den, rc, i0, c4, a.n4, Y);
         } else {
             const double rc[4] = { 0.0, 0.0, 0.0, 0.0 };
-            snake_rows<false>(xv, al, rc, i0, c4, a.n4, Y);
+            snake_rows<K, R, false>(xv, al, den, rc, i0, c4, a.n4, Y);
+        }
+    }
+}
+
+// Snake, row path: any byte strides for x and y (curves contiguous); rows
+// grid-strided over blocks, channels over threads.
+template <int K> __global__ __launch_bounds__(256) void k_snake_rows(const EwArgs a) {
+    for (int64_t r = blockIdx.x; r < a.nrows; r += gridDim.x) {
+        const float * xr = reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.a) + row_offset(a.am, r));
+        float *       yr = reinterpret_cast<float *>(reinterpret_cast<char *>(a.y) + row_offset(a.ym, r));
+        for (int c = threadIdx.x; c < a.ne0; c += blockDim.x) {
+            const SnakeCoef k = snake_coef<K>(a.alpha[c], K == kSnakeBeta ? a.beta[c] : 0.0f);
+            yr[c]             = snake1<false>(xr[c], k.al, k.den, 0.0);
         }
     }
 }
@@ -208,40 +277,92 @@ __global__ __launch_bounds__(256) void k_ew_rows(const EwArgs a) {
         }
         if constexpr (VEC) {
             for (int c = threadIdx.x; c < a.ne0 / 4; c += blockDim.x) {
-                const f32x4 av  = ld_stream(reinterpret_cast<const f32x4 *>(ar) + c);
-                f32x4       bv  = splat4(0.0f);
-                f32x4       alv = splat4(1.0f);
+                const f32x4 av = ld_stream(reinterpret_cast<const f32x4 *>(ar) + c);
+                f32x4       bv = splat4(0.0f);
                 if constexpr (HAS_B) {
                     bv = BCAST ? reinterpret_cast<const f32x4 *>(br)[c] : ld_stream(reinterpret_cast<const f32x4 *>(br) + c);
                 }
-                if constexpr (OP == kSnake) {
-                    alv = reinterpret_cast<const f32x4 *>(a.alpha)[c];
-                }
                 f32x4 sv = splat4(0.0f);
-                st_stream(reinterpret_cast<f32x4 *>(yr) + c, ew4<OP>(av, bv, alv, a.slope, sv));
+                st_stream(reinterpret_cast<f32x4 *>(yr) + c, ew4<OP>(av, bv, a, sv));
                 if constexpr (HAS_S) {
                     st_stream(reinterpret_cast<f32x4 *>(sr) + c, sv);
                 }
             }
         } else {
             for (int c = threadIdx.x; c < a.ne0; c += blockDim.x) {
-                const float av  = reinterpret_cast<const float *>(ar)[c];
-                float       bv  = 0.0f;
-                float       alv = 1.0f;
+                const float av = reinterpret_cast<const float *>(ar)[c];
+                float       bv = 0.0f;
                 if constexpr (HAS_B) {
                     bv = reinterpret_cast<const float *>(br)[c];
                 }
-                if constexpr (OP == kSnake) {
-                    alv = a.alpha[c];
-                }
-                float sv                            = 0.0f;
-                reinterpret_cast<float *>(yr)[c]    = ew<OP>(av, bv, alv, a.slope, sv);
+                float sv                         = 0.0f;
+                reinterpret_cast<float *>(yr)[c] = ew<OP>(av, bv, a, sv);
                 if constexpr (HAS_S) {
                     reinterpret_cast<float *>(sr)[c] = sv;
                 }
             }
         }
     }
+}
+
+// Branch average: summed = t0 + t1 + ... (in term order), current =
+// summed * scale, y = leaky(current, slope). The node run add.., scale,
+// leaky_relu of vits/waveform-decoder.cpp:214-225 and kokoro/generator.cpp:
+// 165-179. Contiguous tensors only; VEC streams one float4 per lane per term.
+constexpr int kMaxTerms = 8;
+
+struct TermArgs {
+    const float * t[kMaxTerms];
+    float *       y;
+    float *       m;  // the scaled sum (`current`), or null
+    int64_t       n;  // elements, or float4s when VEC
+    float         scale;
+    float         slope;
+};
+
+template <int N, bool HAS_M, bool VEC> __global__ __launch_bounds__(256) void k_sum_scale_leaky(const TermArgs a) {
+    using V            = typename std::conditional<VEC, f32x4, float>::type;
+    const int64_t step = static_cast<int64_t>(gridDim.x) * 256;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < a.n; i += step) {
+        V v[N];
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            v[j] = ld_stream(reinterpret_cast<const V *>(a.t[j]) + i);
+        }
+        V s = v[0];
+#pragma unroll
+        for (int j = 1; j < N; ++j) {
+            s = s + v[j];
+        }
+        const V cur = s * a.scale;
+        if constexpr (HAS_M) {
+            st_stream(reinterpret_cast<V *>(a.m) + i, cur);
+        }
+        if constexpr (VEC) {
+            st_stream(reinterpret_cast<V *>(a.y) + i, f32x4{ leaky(cur.x, a.slope), leaky(cur.y, a.slope),
+                                                          leaky(cur.z, a.slope), leaky(cur.w, a.slope) });
+        } else {
+            st_stream(reinterpret_cast<V *>(a.y) + i, leaky(cur, a.slope));
+        }
+    }
+}
+
+template <int N> shp_status_t launch_sum_scale_leaky(const TermArgs & a, bool vec, hipStream_t stream) {
+    int64_t blocks = (a.n + 255) / 256;
+    blocks         = blocks < kMaxFlatBlocks ? blocks : kMaxFlatBlocks;
+    const dim3 grid(static_cast<unsigned>(blocks));
+    if (a.m != nullptr) {
+        if (vec) {
+            hipLaunchKernelGGL((k_sum_scale_leaky<N, true, true>), grid, dim3(256), 0, stream, a);
+        } else {
+            hipLaunchKernelGGL((k_sum_scale_leaky<N, true, false>), grid, dim3(256), 0, stream, a);
+        }
+    } else if (vec) {
+        hipLaunchKernelGGL((k_sum_scale_leaky<N, false, true>), grid, dim3(256), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((k_sum_scale_leaky<N, false, false>), grid, dim3(256), 0, stream, a);
+    }
+    return launch_status();
 }
 
 template <int OP, bool HAS_B, bool BCAST, bool HAS_S>
@@ -364,15 +485,26 @@ extern "C" shp_status_t shp_glu_swiglu(const shp_tensor * a, int32_t swapped, sh
     return launch_ew<kSwiglu, true, false, false>(plan.args, false, plan.vec, as_stream(stream));
 }
 
-extern "C" shp_status_t shp_snake(const shp_tensor * x, const shp_tensor * alpha, shp_tensor * y, shp_stream_t stream) {
-    if (!well_formed(alpha) || !well_formed(x)) {
+namespace shp {
+namespace {
+
+// A per-channel curve: F32, contiguous, exactly C elements (any of the
+// [C], [C,1] or [1,C,1] shapes the builders store it in).
+bool channel_curve(const shp_tensor * c, int64_t channels) {
+    return nelements(*c) == channels && contiguous(*c);
+}
+
+template <int K>
+shp_status_t launch_snake(const shp_tensor * x, const shp_tensor * c0, const shp_tensor * c1, shp_tensor * y,
+                          hipStream_t stream) {
+    if (!well_formed(x) || !well_formed(c0) || (K == kSnakeBeta && !well_formed(c1))) {
         return SHP_ERR_INVALID_ARG;
     }
-    if (alpha->type != SHP_TYPE_F32) {
+    if (c0->type != SHP_TYPE_F32 || (K == kSnakeBeta && c1->type != SHP_TYPE_F32)) {
         return SHP_ERR_UNSUPPORTED;
     }
     // One coefficient per channel; channels are ne[0] (kokoro_decoder_test.cpp:46-49).
-    if (nelements(*alpha) != x->ne[0] || !contiguous(*alpha)) {
+    if (!channel_curve(c0, x->ne[0]) || (K == kSnakeBeta && !channel_curve(c1, x->ne[0]))) {
         return SHP_ERR_INVALID_ARG;
     }
     EwPlan             plan;
@@ -380,20 +512,47 @@ extern "C" shp_status_t shp_snake(const shp_tensor * x, const shp_tensor * alpha
     if (st != SHP_OK) {
         return st;
     }
-    plan.args.alpha = static_cast<const float *>(alpha->data);
-    const bool al16 = reinterpret_cast<uintptr_t>(alpha->data) % 16 == 0;
-    if (plan.flat && al16) {
-        EwArgs &      g      = plan.args;
+    EwArgs & g = plan.args;
+    g.alpha    = static_cast<const float *>(c0->data);
+    g.beta     = K == kSnakeBeta ? static_cast<const float *>(c1->data) : nullptr;
+    const bool c16 =
+        reinterpret_cast<uintptr_t>(g.alpha) % 16 == 0 && reinterpret_cast<uintptr_t>(g.beta) % 16 == 0;
+    if (plan.flat && c16) {
+        constexpr int R      = SnakeRows<K>::R;
         const int64_t quads  = x->ne[0] / 4;
         const int64_t rows   = g.n4 / quads;
         g.quads              = make_fastdiv(static_cast<uint32_t>(quads));
-        g.ntask              = (rows + kSnakeRows - 1) / kSnakeRows * quads;
+        g.ntask              = (rows + R - 1) / R * quads;
         int64_t       blocks = (g.ntask + 255) / 256;
         blocks               = blocks < kMaxFlatBlocks ? blocks : kMaxFlatBlocks;
-        hipLaunchKernelGGL(k_snake_flat, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream), g);
+        hipLaunchKernelGGL(k_snake_flat<K>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, g);
         return launch_status();
     }
-    return launch_ew<kSnake, false, false, false>(plan.args, false, plan.vec && al16, as_stream(stream));
+    const int64_t blocks = g.nrows < 65536 ? g.nrows : 65536;
+    hipLaunchKernelGGL(k_snake_rows<K>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, g);
+    return launch_status();
+}
+
+}  // namespace
+}  // namespace shp
+
+extern "C" shp_status_t shp_snake(const shp_tensor * x, const shp_tensor * alpha, shp_tensor * y, shp_stream_t stream) {
+    return launch_snake<kSnakePlain>(x, alpha, nullptr, y, as_stream(stream));
+}
+
+extern "C" shp_status_t shp_snake_guarded(const shp_tensor * x,
+                                          const shp_tensor * alpha,
+                                          shp_tensor *       y,
+                                          shp_stream_t       stream) {
+    return launch_snake<kSnakeGuarded>(x, alpha, nullptr, y, as_stream(stream));
+}
+
+extern "C" shp_status_t shp_snake_beta(const shp_tensor * x,
+                                       const shp_tensor * log_alpha,
+                                       const shp_tensor * log_beta,
+                                       shp_tensor *       y,
+                                       shp_stream_t       stream) {
+    return launch_snake<kSnakeBeta>(x, log_alpha, log_beta, y, as_stream(stream));
 }
 
 extern "C" shp_status_t shp_add_leaky_relu(const shp_tensor * a,
@@ -436,4 +595,87 @@ extern "C" shp_status_t shp_add(const shp_tensor * a, const shp_tensor * b, shp_
         return launch_ew<kAdd, true, true, false>(plan.args, plan.flat && b16, plan.vec && b16, ss);
     }
     return launch_ew<kAdd, true, false, false>(plan.args, plan.flat, plan.vec, ss);
+}
+
+extern "C" shp_status_t shp_exp(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
+    EwPlan             plan;
+    const shp_status_t st = plan_ew(x, nullptr, false, y, nullptr, plan);
+    if (st != SHP_OK) {
+        return st;
+    }
+    return launch_ew<kExp, false, false, false>(plan.args, plan.flat, plan.vec, as_stream(stream));
+}
+
+extern "C" shp_status_t shp_scale_bias(const shp_tensor * x, float s, float b, shp_tensor * y, shp_stream_t stream) {
+    EwPlan             plan;
+    const shp_status_t st = plan_ew(x, nullptr, false, y, nullptr, plan);
+    if (st != SHP_OK) {
+        return st;
+    }
+    plan.args.scale      = s;
+    plan.args.bias       = b;
+    const hipStream_t ss = as_stream(stream);
+    if (b == 0.0f) {
+        return launch_ew<kScale, false, false, false>(plan.args, plan.flat, plan.vec, ss);
+    }
+    return launch_ew<kScaleBias, false, false, false>(plan.args, plan.flat, plan.vec, ss);
+}
+
+extern "C" shp_status_t shp_sum_scale_leaky_relu(const shp_tensor * terms,
+                                                 int32_t            n_terms,
+                                                 float              scale,
+                                                 float              slope,
+                                                 shp_tensor *       mean,
+                                                 shp_tensor *       y,
+                                                 shp_stream_t       stream) {
+    if (terms == nullptr || n_terms < 1 || n_terms > kMaxTerms || !well_formed(y) ||
+        (mean != nullptr && !well_formed(mean))) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    TermArgs a{};
+    bool     vec = reinterpret_cast<uintptr_t>(y->data) % 16 == 0 && y->ne[0] % 4 == 0;
+    for (int j = 0; j < n_terms; ++j) {
+        const shp_tensor * t = &terms[j];
+        if (!well_formed(t)) {
+            return SHP_ERR_INVALID_ARG;
+        }
+        if (t->type != SHP_TYPE_F32) {
+            return SHP_ERR_UNSUPPORTED;
+        }
+        if (!same_shape(*t, *y)) {
+            return SHP_ERR_INVALID_ARG;
+        }
+        if (!contiguous(*t)) {
+            return SHP_ERR_UNSUPPORTED;
+        }
+        a.t[j] = static_cast<const float *>(t->data);
+        vec    = vec && reinterpret_cast<uintptr_t>(t->data) % 16 == 0;
+    }
+    if (y->type != SHP_TYPE_F32 || (mean != nullptr && mean->type != SHP_TYPE_F32)) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    if (mean != nullptr && !same_shape(*mean, *y)) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    if (!contiguous(*y) || (mean != nullptr && !contiguous(*mean))) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    const int64_t n = nelements(*y);
+    vec             = vec && (mean == nullptr || reinterpret_cast<uintptr_t>(mean->data) % 16 == 0);
+    a.y     = static_cast<float *>(y->data);
+    a.m     = mean != nullptr ? static_cast<float *>(mean->data) : nullptr;
+    a.n     = vec ? n / 4 : n;
+    a.scale = scale;
+    a.slope = slope;
+    const hipStream_t ss = as_stream(stream);
+    switch (n_terms) {
+        case 1: return launch_sum_scale_leaky<1>(a, vec, ss);
+        case 2: return launch_sum_scale_leaky<2>(a, vec, ss);
+        case 3: return launch_sum_scale_leaky<3>(a, vec, ss);
+        case 4: return launch_sum_scale_leaky<4>(a, vec, ss);
+        case 5: return launch_sum_scale_leaky<5>(a, vec, ss);
+        case 6: return launch_sum_scale_leaky<6>(a, vec, ss);
+        case 7: return launch_sum_scale_leaky<7>(a, vec, ss);
+        default: return launch_sum_scale_leaky<8>(a, vec, ss);
+    }
 }

@@ -30,6 +30,14 @@ __device__ __forceinline__ void st_stream(f32x4 * p, f32x4 v) {
     __builtin_nontemporal_store(v, p);
 }
 
+__device__ __forceinline__ float ld_stream(const float * p) {
+    return __builtin_nontemporal_load(p);
+}
+
+__device__ __forceinline__ void st_stream(float * p, float v) {
+    __builtin_nontemporal_store(v, p);
+}
+
 __device__ __forceinline__ f32x4 splat4(float v) {
     return f32x4{ v, v, v, v };
 }

@@ -66,6 +66,11 @@ def load(path=None):
         "shp_snake": [_PT, _PT, _PT, vp],
         "shp_add_leaky_relu": [_PT, _PT, f, _PT, _PT, vp],
         "shp_add": [_PT, _PT, _PT, vp],
+        "shp_snake_guarded": [_PT, _PT, _PT, vp],
+        "shp_snake_beta": [_PT, _PT, _PT, _PT, vp],
+        "shp_exp": [_PT, _PT, vp],
+        "shp_scale_bias": [_PT, f, f, _PT, vp],
+        "shp_sum_scale_leaky_relu": [_PT, i32, f, f, _PT, _PT, vp],
     }
     for name, args in sigs.items():
         fn = getattr(L, name)
@@ -249,6 +254,47 @@ def snake(x, alpha, out=None):
     out = x.new_empty(x.shape) if out is None else out
     _check(load().shp_snake(_ref(desc(x)), _ref(desc(alpha)), _ref(desc(out)), _stream()), "snake")
     return out
+
+
+def snake_guarded(x, alpha, out=None):
+    """codec_snake (omnivoice): x + sin(x*alpha)^2 / (alpha + 1e-9), x (T, C), alpha C values."""
+    out = x.new_empty(x.shape) if out is None else out
+    _check(load().shp_snake_guarded(_ref(desc(x)), _ref(desc(alpha)), _ref(desc(out)), _stream()), "snake_guarded")
+    return out
+
+
+def snake_beta(x, log_alpha, log_beta, out=None):
+    """codec_snake_beta (qwen3-tts): x + sin(x*exp(la))^2 / (exp(lb) + 1e-9), x (T, C)."""
+    out = x.new_empty(x.shape) if out is None else out
+    _check(load().shp_snake_beta(_ref(desc(x)), _ref(desc(log_alpha)), _ref(desc(log_beta)), _ref(desc(out)),
+                                 _stream()), "snake_beta")
+    return out
+
+
+def exp(x, out=None):
+    """ggml_exp."""
+    out = x.new_empty(x.shape) if out is None else out
+    _check(load().shp_exp(_ref(desc(x)), _ref(desc(out)), _stream()), "exp")
+    return out
+
+
+def scale_bias(x, s, b=0.0, out=None):
+    """ggml_scale_bias(x, s, b); b == 0 is ggml_scale(x, s)."""
+    out = x.new_empty(x.shape) if out is None else out
+    _check(load().shp_scale_bias(_ref(desc(x)), float(s), float(b), _ref(desc(out)), _stream()), "scale_bias")
+    return out
+
+
+def sum_scale_leaky_relu(terms, scale, slope, out=None, mean_out=None, want_mean=False):
+    """Branch average: leaky_relu((t0 + t1 + ...) * scale, slope); returns (mean or None, y)."""
+    n = len(terms)
+    arr = (ShpTensor * n)(*[desc(t) for t in terms])
+    out = terms[0].new_empty(terms[0].shape) if out is None else out
+    if mean_out is None and want_mean:
+        mean_out = terms[0].new_empty(terms[0].shape)
+    _check(load().shp_sum_scale_leaky_relu(arr, n, float(scale), float(slope), _ref(desc(mean_out)),
+                                           _ref(desc(out)), _stream()), "sum_scale_leaky_relu")
+    return mean_out, out
 
 
 def add_leaky_relu(a, b, slope, out=None, sum_out=None, want_sum=False):

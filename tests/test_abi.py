@@ -118,6 +118,24 @@ def test_argument_validation():
     assert L.shp_glu_swiglu(R(a), 0, R(a), None) == S.ERR_INVALID_ARG
     assert L.shp_swiglu(R(a), R(mk(S.TYPE_F32, [256, 5])), R(a), None) == S.ERR_INVALID_ARG
 
+    c = mk(S.TYPE_F32, [256])
+    assert L.shp_snake_guarded(R(a), R(mk(S.TYPE_F32, [128])), R(a), None) == S.ERR_INVALID_ARG
+    assert L.shp_snake_guarded(R(a), R(mk(S.TYPE_F16, [256])), R(a), None) == S.ERR_UNSUPPORTED
+    assert L.shp_snake_beta(R(a), R(c), None, R(a), None) == S.ERR_INVALID_ARG
+    assert L.shp_snake_beta(R(a), R(c), R(mk(S.TYPE_F32, [255])), R(a), None) == S.ERR_INVALID_ARG
+    assert L.shp_snake_beta(R(a), R(c), R(mk(S.TYPE_F32, [256, 2])), R(a), None) == S.ERR_INVALID_ARG
+    assert L.shp_exp(R(a), R(mk(S.TYPE_F32, [256, 5])), None) == S.ERR_INVALID_ARG
+    assert L.shp_scale_bias(R(mk(S.TYPE_F16, [256, 4])), 1.0, 0.0, R(a), None) == S.ERR_UNSUPPORTED
+    terms = (S.ShpTensor * 3)(mk(S.TYPE_F32, [256, 4]), mk(S.TYPE_F32, [256, 4]), mk(S.TYPE_F32, [256, 3]))
+    assert L.shp_sum_scale_leaky_relu(terms, 3, 1 / 3, 0.1, None, R(a), None) == S.ERR_INVALID_ARG  # shape
+    assert L.shp_sum_scale_leaky_relu(terms, 2, 0.5, 0.1, R(mk(S.TYPE_F32, [256, 5])), R(a), None) == \
+        S.ERR_INVALID_ARG
+    assert L.shp_sum_scale_leaky_relu(terms, 0, 1.0, 0.1, None, R(a), None) == S.ERR_INVALID_ARG
+    assert L.shp_sum_scale_leaky_relu(terms, 9, 1.0, 0.1, None, R(a), None) == S.ERR_INVALID_ARG
+    assert L.shp_sum_scale_leaky_relu(None, 1, 1.0, 0.1, None, R(a), None) == S.ERR_INVALID_ARG
+    strided = (S.ShpTensor * 1)(mk(S.TYPE_F32, [256, 4], nb=[4, 2048, 8192, 8192]))
+    assert L.shp_sum_scale_leaky_relu(strided, 1, 1.0, 0.1, None, R(a), None) == S.ERR_UNSUPPORTED
+
 
 def test_binding_fails_loudly_without_library(tmp_path):
     with pytest.raises(RuntimeError):

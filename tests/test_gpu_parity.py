@@ -1,10 +1,13 @@
 """GPU parity: every libsynth_hip entry point against the ggml-CPU restatement on
 the same seeded inputs, through the C ABI.
 
-Bars: bit-exact for gathers, sums of gathers, adds and leaky-ReLU (compared as
-raw 32-bit patterns, NaN payloads included); for RMSNorm, SwiGLU and Snake an
-elementwise relative error <= 1e-5 with the denominator floored at 1e-3 * RMS
-of the reference row (so near-zero outputs do not blow the ratio up).
+Bars: bit-exact for gathers, sums of gathers, adds, leaky-ReLU, scale and the
+branch average (compared as raw 32-bit patterns, NaN payloads included); for
+RMSNorm, SwiGLU and Snake an elementwise relative error <= 1e-5 with the
+denominator floored at 1e-3 * RMS of the reference row (so near-zero outputs do
+not blow the ratio up). The guarded Snake and SnakeBeta, whose closing add
+x + r can cancel, take the same 1e-5 relative to max(|y|, |x|); exp is held to
+one ulp.
 
 Rope: the kernel evaluates cos/sin in double and rounds once (correctly
 rounded), while ggml-CPU calls glibc cosf/sinf, which land one ulp away in
@@ -70,6 +73,25 @@ def assert_close(got, ref, tol=REL_TOL):
     assert worst <= tol, "max rel err %.3g at %s (got %r ref %r)" % (
         worst, np.unravel_index(rel.argmax(), rel.shape), got.flat[rel.argmax()], ref.flat[rel.argmax()])
     return float(worst), float((got == ref).mean())
+
+
+def assert_snake_close(got, ref, x, tol=REL_TOL):
+    """Snake family: y = x + r ends in an add whose operands can cancel (a large
+    term over a small beta against an x of the opposite sign), so the error is
+    measured relative to the operands of that add, max(|y|, |x|) >= |r| / 2,
+    floored as in assert_close. A last-ulp difference of the sine or the exp
+    then stays a last-ulp difference."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape
+    rows = ref.reshape(-1, ref.shape[-1])
+    rms = np.sqrt((rows ** 2).mean(axis=-1, keepdims=True))
+    floor = np.broadcast_to(1e-3 * rms, rows.shape).reshape(ref.shape)
+    den = np.maximum(np.maximum(np.abs(ref), np.abs(np.asarray(x, np.float64))), floor)
+    den = np.where(den == 0, 1.0, den)
+    rel = np.abs(got - ref) / den
+    assert rel.max() <= tol, "max rel err %.3g at %s (got %r ref %r)" % (
+        rel.max(), np.unravel_index(rel.argmax(), rel.shape), got.flat[rel.argmax()], ref.flat[rel.argmax()])
 
 
 def assert_rope_close(got, ref, n_dims, tol=REL_TOL):
@@ -401,6 +423,94 @@ def test_snake_special_alphas(gpu):
     fin = np.isfinite(ref)
     den = np.maximum(np.abs(ref[fin]).astype(np.float64), 1e-3)
     assert (np.abs(got[fin].astype(np.float64) - ref[fin]) / den).max() <= REL_TOL
+
+
+@pytest.mark.parametrize("T,C", [(256, 512), (37, 64), (31, 30), (3, 1028)])
+def test_snake_guarded(gpu, T, C):
+    """codec_snake (omnivoice): alpha = 0 and alphas near 1e-9 next to |x| ~ 1e4
+    are where the 1e-9 guard changes the result; row 0's large x crosses the
+    fast sine's range. C % 4 != 0 takes the row kernel."""
+    rng = np.random.default_rng(SEED + 7 * T + C)
+    x = rng.standard_normal((T, C)).astype(np.float32)
+    x[0, ::3] *= 20000.0
+    alpha = np.exp(rng.uniform(np.log(1e-9), np.log(10.0), C)).astype(np.float32)
+    alpha[:4] = np.array([0.0, 1e-9, 1e-7, 1e-4], np.float32)
+    x[:, :4] *= 1e4
+    ref = R.run(lambda g: R.snake_guarded(g, x, alpha))
+    got = _np(gpu.snake_guarded(_t(gpu, x), _t(gpu, alpha)))
+    assert_snake_close(got, ref, x)
+    assert_bitexact(got[:, 0], x[:, 0])  # alpha = 0: the guard keeps sin(0)^2 / 1e-9 = 0
+
+
+@pytest.mark.parametrize("T,C", [(256, 512), (37, 64), (31, 30), (9, 2048), (4, 1028)])
+def test_snake_beta(gpu, T, C):
+    """codec_snake_beta (qwen3-tts): log curves over [-3, 3], so alpha/beta span
+    e^+-3 and the two exps, the guard and the division all matter."""
+    rng = np.random.default_rng(SEED + 11 * T + C)
+    x = rng.standard_normal((T, C)).astype(np.float32)
+    la = rng.uniform(-3, 3, C).astype(np.float32)
+    lb = rng.uniform(-3, 3, C).astype(np.float32)
+    ref = R.run(lambda g: R.snake_beta(g, x, la, lb))
+    assert_snake_close(_np(gpu.snake_beta(_t(gpu, x), _t(gpu, la), _t(gpu, lb))), ref, x)
+
+
+def test_golden_g3_snake_beta_on_gpu(gpu):
+    """kExpectedSnakeBeta, tests/qwen3_tts_codec_ops_test.cpp:77-82, at the
+    test's CPU tolerance (1e-4, tighter than its 5e-3 for accelerators)."""
+    import test_oracle_goldens as G
+    d = _golden("qwen3_codec_snake_beta.json")
+    x, a, b = G.snake_beta_inputs(d)
+    got = _np(gpu.snake_beta(_t(gpu, x), _t(gpu, a), _t(gpu, b)))
+    exp = np.array(d["expected_snake_beta"], np.float32)
+    assert np.abs(got.reshape(-1) - exp).max() < d["tolerance_cpu"]
+    assert_snake_close(got, R.run(lambda g: R.snake_beta(g, x, a, b)), x)
+
+
+@pytest.mark.parametrize("shape", [(333, 256), (17, 75)])
+def test_exp(gpu, shape):
+    """ggml_exp: the kernel rounds the double exp once (correctly rounded but for
+    arguments within ~2^-52 of a rounding boundary); glibc's expf lands one ulp
+    away for ~0.06% of arguments. So: at most one ulp apart everywhere, >99.9%
+    identical; inf, 0, subnormal and NaN results where the oracle has them."""
+    rng = np.random.default_rng(SEED + shape[1])
+    x = rng.uniform(-104, 89, shape).astype(np.float32)
+    x.reshape(-1)[:8] = [0.0, -0.0, np.inf, -np.inf, np.nan, 88.8, -87.5, -103.9]
+    with np.errstate(over="ignore"):
+        ref = R.run(lambda g: g.exp(x))
+    got = _np(gpu.exp(_t(gpu, x)))
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    d = np.abs(got[ok].view(np.int32).astype(np.int64) - ref[ok].view(np.int32).astype(np.int64))
+    assert d.max() <= 1 and (d == 0).mean() > 0.999
+
+
+@pytest.mark.parametrize("shape", [(37, 1024), (33, 77)])
+@pytest.mark.parametrize("s,b", [(0.7853982, 0.0), (-1.5, 0.0), (0.7853982, -0.3183099), (1.0, 1e-9)])
+def test_scale_bias_bitexact(gpu, shape, s, b):
+    rng = np.random.default_rng(SEED + shape[1])
+    x = _specials(int(np.prod(shape)), rng).reshape(shape)
+    s, b = np.float32(s), np.float32(b)
+    with np.errstate(all="ignore"):
+        ref = R.run(lambda g: g.scale_bias(x, s, b))
+    assert_bitexact(_np(gpu.scale_bias(_t(gpu, x), s, b)), ref)
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 5, 8])
+@pytest.mark.parametrize("shape", [(64, 4096), (33, 77)])
+def test_sum_scale_leaky_relu_bitexact(gpu, n, shape):
+    """The branch average: terms added in order, scaled by 1/n (skipped for one
+    term), then leaky; the scaled sum too. (33, 77) takes the scalar kernel."""
+    rng = np.random.default_rng(SEED + 13 * n + shape[1])
+    terms = [rng.standard_normal(shape).astype(np.float32) for _ in range(n)]
+    terms[0] = _specials(int(np.prod(shape)), rng).reshape(shape)
+    scale, slope = np.float32(1.0 / n), np.float32(0.1)
+    with np.errstate(all="ignore"):
+        cur_ref, y_ref = R.run(lambda g: R.sum_scale_leaky(g, terms, scale, slope))
+    cur, y = gpu.sum_scale_leaky_relu([_t(gpu, t) for t in terms], scale, slope, want_mean=True)
+    assert_bitexact(_np(cur), cur_ref)
+    assert_bitexact(_np(y), y_ref)
+    _, y_only = gpu.sum_scale_leaky_relu([_t(gpu, t) for t in terms], scale, slope)
+    assert_bitexact(_np(y_only), y_ref)
 
 
 def _specials(n, rng):

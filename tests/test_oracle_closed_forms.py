@@ -230,6 +230,129 @@ def test_snake_double_closed_form():
     assert (np.abs(y - ref) <= 8 * ULP * np.maximum(np.abs(ref), 1e-3)).all()
 
 
+def test_guarded_snake_double_closed_form_and_guard():
+    """codec_snake (omnivoice/codec.cpp:51-68) against x + sin(a x)^2 / (a + 1e-9) in
+    double. The guard shows where the Snake term is visible next to x: alpha = 0
+    (0/0 without it) and alphas near 1e-9 with |x| ~ 1e4. Dropping it (the
+    Kokoro form) fails the same check."""
+    rng = np.random.default_rng(21)
+    C = 64
+    x = rng.standard_normal((50, C)).astype(np.float32)
+    a = np.exp(rng.uniform(np.log(1e-9), np.log(10), C)).astype(np.float32)
+    a[:5] = np.array([0.0, 1e-9, 3e-9, 1e-7, 1e-4], np.float32)
+    x[:, :5] *= 1e4
+    y = R.run(lambda g: R.snake_guarded(g, x, a))
+    ad = a.astype(np.float64)
+    den = np.float32(a + np.float32(1e-9)).astype(np.float64)  # the guard add is one f32 rounding
+
+    def ok(v, d):
+        with np.errstate(invalid="ignore", divide="ignore"):
+            ref = x + np.sin(ad * x) ** 2 / d
+            return (np.abs(v - ref) <= 8 * ULP * np.maximum(np.abs(ref), 1e-3)).all()
+    assert ok(y, den)
+    with np.errstate(invalid="ignore"):
+        assert not ok(R.run(lambda g: R.snake(g, x, a)), den)
+    assert not ok(y, ad)
+    np.testing.assert_array_equal(y[:, 0], x[:, 0])  # alpha = 0: sin(0)^2 / 1e-9 = 0
+
+
+def test_snake_beta_double_closed_form():
+    """codec_snake_beta against x + sin(t)^2 / (e^lb + 1e-9), t = x e^la, in double
+    after the f32 roundings of the two exps, the guard and the product t (a
+    large alpha over a small beta amplifies t's rounding far beyond y's ulp,
+    so t is rounded as ggml rounds it). Tolerance: 8 ulp of the larger of |x|
+    and the Snake term. Swapping the curves fails."""
+    rng = np.random.default_rng(22)
+    C = 48
+    x = rng.standard_normal((40, C)).astype(np.float32)
+    la = rng.uniform(-3, 3, C).astype(np.float32)
+    lb = rng.uniform(-3, 3, C).astype(np.float32)
+    y = R.run(lambda g: R.snake_beta(g, x, la, lb))
+
+    def close(ca, cb):
+        a = np.exp(ca.astype(np.float64)).astype(np.float32)
+        b = np.float32(np.exp(cb.astype(np.float64)).astype(np.float32) + np.float32(1e-9)).astype(np.float64)
+        t = (x * a).astype(np.float64)  # one f32 rounding, as ggml_mul
+        r = np.sin(t) ** 2 / b
+        scale = np.maximum(np.maximum(np.abs(x), r), 1e-3)
+        return (np.abs(y - (x + r)) <= 8 * ULP * scale).all()
+    assert close(la, lb)
+    assert not close(lb, la)
+
+
+def test_exp_is_correctly_rounded_almost_everywhere():
+    """ggml_exp: glibc expf against e^x in double rounded once to f32 (the
+    correctly rounded value unless e^x lies within ~2^-52 of a rounding
+    boundary): every result within one ulp, nearly all identical (glibc's
+    expf is documented at 0.502 ulp and lands on the other side of a
+    midpoint for ~0.06% of arguments). Overflow to inf, underflow to
+    subnormals and zero, and exp(0) = 1 exactly."""
+    rng = np.random.default_rng(23)
+    x = np.concatenate([rng.uniform(-104, 89, 200000), [0.0, -0.0, 88.8, -104.0, -87.5, 1e-30, np.inf, -np.inf]])
+    x = x.astype(np.float32).reshape(-1, 8)
+    y = R.run(lambda g: g.exp(x)).reshape(-1)
+    with np.errstate(over="ignore"):
+        ref = np.exp(x.astype(np.float64)).astype(np.float32).reshape(-1)
+    same = bits(y) == bits(ref)
+    assert same.mean() > 0.999
+    diff = np.abs(bits(y).astype(np.int64) - bits(ref).astype(np.int64))
+    assert diff.max() <= 1
+    xs = x.reshape(-1)
+    assert y[xs == 0].tolist() == [1.0, 1.0] and y[xs == np.inf][0] == np.inf and y[xs == -np.inf][0] == 0
+    assert y[xs == np.float32(88.8)][0] == np.inf and 0 < y[xs == np.float32(-87.5)][0] < 2 ** -126
+
+
+def test_scale_bias_rounding():
+    """ggml_scale (b == 0) is one multiply, so -0 stays -0; ggml_scale_bias with
+    b != 0 rounds x*s + b once. Checked against numpy's f32 multiply and against
+    the exact value: x*s is exact in double, so double(x*s) + b rounds once in
+    double and once more to f32, which is the single rounding except when the
+    double sum lands on an f32 midpoint (excluded). A two-rounding mul+add is
+    planted and fails."""
+    rng = np.random.default_rng(24)
+    x = rng.standard_normal((1000, 16)).astype(np.float32)
+    x[0, :4] = [-0.0, 0.0, np.inf, np.nan]
+    s, b = np.float32(0.7853982), np.float32(-0.3183099)
+    y0 = R.run(lambda g: g.scale(x, s))
+    np.testing.assert_array_equal(bits(y0), bits(x * s))
+    assert np.signbit(y0[0, 0])
+    y = R.run(lambda g: g.scale_bias(x, s, b)).reshape(-1)
+    d = x.reshape(-1).astype(np.float64) * np.float64(s) + np.float64(b)
+    ref = d.astype(np.float32)
+    lo = np.nextafter(ref, np.float32(-np.inf)).astype(np.float64)
+    hi = np.nextafter(ref, np.float32(np.inf)).astype(np.float64)
+    mid = (d == (ref.astype(np.float64) + lo) / 2) | (d == (ref.astype(np.float64) + hi) / 2)
+    fin = np.isfinite(d) & ~mid
+    np.testing.assert_array_equal(bits(y[fin]), bits(ref[fin]))
+    two = (x.reshape(-1) * s + b).astype(np.float32)
+    assert (bits(two[fin]) != bits(ref[fin])).any()
+    # with s == 1 (the Snake guards) every evaluation order agrees
+    np.testing.assert_array_equal(bits(R.run(lambda g: g.scale_bias(x, np.float32(1.0), np.float32(1e-9)))),
+                                  bits(x + np.float32(1e-9)))
+
+
+def test_branch_average_order_and_invariants():
+    """sum_scale_leaky (waveform-decoder.cpp:214-225): the terms are added in
+    order, so (1e8 + 1) - 1e8 is 0 where another order gives 1; two equal
+    terms scaled by 0.5 give back the term exactly (doubling and halving are
+    exact), so y = leaky(t) bit for bit; one term is the bare leaky."""
+    big = np.array([[1e8, 3.0, -2.0, 5.0]], np.float32)
+    one = np.array([[1.0, 1.0, 1.0, 1.0]], np.float32)
+    cur, y = R.run(lambda g: R.sum_scale_leaky(g, [big, one, -big], np.float32(1 / 3), np.float32(0.1)))
+    assert cur[0, 0] == 0.0 and cur[0, 1] == np.float32(np.float32(3.0 + 1.0 - 3.0) * np.float32(1 / 3))
+    cur2, _ = R.run(lambda g: R.sum_scale_leaky(g, [big, -big, one], np.float32(1 / 3), np.float32(0.1)))
+    assert cur2[0, 0] == np.float32(1 / 3)
+    rng = np.random.default_rng(25)
+    t = rng.standard_normal((30, 64)).astype(np.float32)
+    t[0, :4] = [-0.0, np.nan, 1e-45, -3e-39]
+    c, y = R.run(lambda g: R.sum_scale_leaky(g, [t, t], np.float32(0.5), np.float32(0.1)))
+    np.testing.assert_array_equal(bits(c[np.isfinite(t)]), bits(t[np.isfinite(t)]))
+    ly = R.run(lambda g: g.leaky_relu(t, np.float32(0.1)))
+    np.testing.assert_array_equal(bits(y), bits(ly))
+    c1, y1 = R.run(lambda g: R.sum_scale_leaky(g, [t], np.float32(1.0), np.float32(0.1)))
+    np.testing.assert_array_equal(bits(y1), bits(ly))
+
+
 def test_leaky_relu_signed_zero_and_nan():
     x = np.array([[-0.0, 0.0, np.nan, -np.nan, np.inf, -np.inf, -1e-45, 2.5, -2.5, -3e-39]], np.float32)
     y = R.run(lambda g: g.leaky_relu(x, np.float32(0.1)))[0]
