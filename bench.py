@@ -151,27 +151,42 @@ def time_graphs(torch, graphs, reps):
 # decode step: 28 layers x (add+norm, qk-norm+rope, add+norm, swiglu) at T=1
 # ---------------------------------------------------------------------------
 
-def decode_layer_us(S, torch, layers=28, reps=50):
+def decode_layer_us(S, torch, layers=28, reps=50, kv=False, total=512):
+    """µs per talker layer of the decode step's non-GEMM ops, replayed as one
+    graph of `layers` layers. kv: qk-norm+rope also writes this step's k and v
+    into the layer's cache (slot total-1) and the step adds the attention
+    softmax over `total` keys for the 16 heads (5 launches per layer)."""
     g = torch.Generator(device="cuda")
     g.manual_seed(SEED + 1)
     randn = lambda *shape: torch.randn(shape, generator=g, device="cuda", dtype=torch.float32)
     gain = lambda n: (1.0 + 0.1 * randn(n)).to(torch.bfloat16)
     L = []
     for _ in range(layers):
-        L.append(dict(a=randn(1, 1024), b=randn(1, 1024), w1=gain(1024), w2=gain(1024), wq=gain(128),
-                      wk=gain(128), q=randn(1, 16, 128), k=randn(1, 8, 128), proj=randn(1, 1024),
-                      gate=randn(1, 3072), up=randn(1, 3072), s1=torch.empty(1, 1024, device="cuda"),
-                      y1=torch.empty(1, 1024, device="cuda"), s2=torch.empty(1, 1024, device="cuda"),
-                      y2=torch.empty(1, 1024, device="cuda"), qo=torch.empty(1, 16, 128, device="cuda"),
-                      ko=torch.empty(1, 8, 128, device="cuda"), act=torch.empty(1, 3072, device="cuda")))
-    pos = torch.tensor([37], dtype=torch.int32, device="cuda")
+        c = dict(a=randn(1, 1024), b=randn(1, 1024), w1=gain(1024), w2=gain(1024), wq=gain(128),
+                 wk=gain(128), q=randn(1, 16, 128), k=randn(1, 8, 128), proj=randn(1, 1024),
+                 gate=randn(1, 3072), up=randn(1, 3072), s1=torch.empty(1, 1024, device="cuda"),
+                 y1=torch.empty(1, 1024, device="cuda"), s2=torch.empty(1, 1024, device="cuda"),
+                 y2=torch.empty(1, 1024, device="cuda"), qo=torch.empty(1, 16, 128, device="cuda"),
+                 ko=torch.empty(1, 8, 128, device="cuda"), act=torch.empty(1, 3072, device="cuda"))
+        if kv:
+            c.update(v=randn(1, 8, 128), kc=randn(total, 8, 128), vc=randn(total, 8, 128),
+                     sc=randn(16, 1, total), p=torch.empty(16, 1, total, device="cuda"))
+        L.append(c)
+    pos = torch.tensor([total - 1], dtype=torch.int32, device="cuda")
+    scale = 1.0 / math.sqrt(128.0)
 
     def layer_fns(c):
-        return [lambda: S.add_rms_norm_mul(c["a"], c["b"], c["w1"], 1e-6, out=c["y1"], sum_out=c["s1"]),
-                lambda: S.qk_norm_rope(c["q"], c["k"], c["wq"], c["wk"], 1e-6, pos, 128, 1e6, q_out=c["qo"],
-                                       k_out=c["ko"]),
-                lambda: S.add_rms_norm_mul(c["s1"], c["proj"], c["w2"], 1e-6, out=c["y2"], sum_out=c["s2"]),
-                lambda: S.swiglu(c["gate"], c["up"], out=c["act"])]
+        if kv:
+            rope = lambda: S.qk_norm_rope_kv(c["q"], c["k"], c["v"], c["wq"], c["wk"], 1e-6, pos, 128, 1e6, c["kc"],
+                                             c["vc"], total - 1, q_out=c["qo"])
+        else:
+            rope = lambda: S.qk_norm_rope(c["q"], c["k"], c["wq"], c["wk"], 1e-6, pos, 128, 1e6, q_out=c["qo"],
+                                          k_out=c["ko"])
+        fns = [lambda: S.add_rms_norm_mul(c["a"], c["b"], c["w1"], 1e-6, out=c["y1"], sum_out=c["s1"]), rope]
+        if kv:
+            fns.append(lambda: S.soft_max_ext(c["sc"], None, scale, out=c["p"]))
+        return fns + [lambda: S.add_rms_norm_mul(c["s1"], c["proj"], c["w2"], 1e-6, out=c["y2"], sum_out=c["s2"]),
+                      lambda: S.swiglu(c["gate"], c["up"], out=c["act"])]
 
     fns = [f for c in L for f in layer_fns(c)]
     for f in fns:
@@ -341,6 +356,24 @@ def suite(args, S, torch):
         rows.append({"config": "cfg1", "op": "talker layer non-GEMM step (28-layer graph, 4 launches/layer)",
                      "us": round(us, 3), "note": "per layer"})
         print("cfg1  decode layer non-GEMM step: %.3f us/layer" % us, flush=True)
+        us_kv = decode_layer_us(S, torch, kv=True)
+        rows.append({"config": "cfg1", "op": "talker layer non-GEMM step + KV-cache write + soft_max over 512 keys "
+                     "(28-layer graph, 5 launches/layer)", "us": round(us_kv, 3), "note": "per layer"})
+        print("cfg1  decode layer + KV write + soft_max: %.3f us/layer" % us_kv, flush=True)
+
+        def make_kv():
+            q, k, v = randn(1, 16, 128), randn(1, 8, 128), randn(1, 8, 128)
+            kc, vc, qo = randn(512, 8, 128), randn(512, 8, 128), empty(1, 16, 128)
+            w = bf16(128)
+            pos = torch.tensor([511], dtype=torch.int32, device="cuda")
+            return lambda: S.qk_norm_rope_kv(q, k, v, w, w, 1e-6, pos, 128, 1e6, kc, vc, 511, q_out=qo)
+        run("cfg1", "qk_norm_rope_kv [128,16+8(+8 v),1]", (2 * 32) * 128 * f32 + 4 + 2 * 128 * 2, make_kv, cold=False)
+
+        def make_sm(T=1, N=512):
+            sc, p = randn(16, T, N), empty(16, T, N)
+            return lambda: S.soft_max_ext(sc, None, 1.0 / math.sqrt(128.0), out=p)
+        run("cfg1", "soft_max_ext [512,1,16]", 2 * 16 * 512 * f32, make_sm, cold=False)
+        run("cfg2", "soft_max_ext causal-size [512,512,16]", 2 * 16 * 512 * 512 * f32, lambda: make_sm(512, 512))
 
     if on("cfg2"):
         norm_case("cfg2", 512, 1024)

@@ -169,6 +169,33 @@ shp_status_t shp_qk_norm_rope(const shp_tensor * q,
                               shp_stream_t       stream);
 
 /*
+ * shp_qk_norm_rope plus this step's KV-cache write, in one launch: the node
+ * runs of src/arch/qwen3-tts/operations.cpp:98-116, i.e. q and k normalised
+ * and rotated as in shp_qk_norm_rope, then ggml_cpy(k) and ggml_cpy(v) into
+ * the cache views ggml_view_3d(cache, head_dim, kv_heads, T, nb1, nb2,
+ * filled*nb2). q_out receives q; the rotated k goes straight to rows
+ * [filled, filled + T) of k_cache and v (copied unchanged) to the same rows
+ * of v_cache. k_cache, v_cache: F32 [head_dim, kv_heads, capacity, 1] with
+ * capacity >= filled + T (operations.cpp:71-76); v F32 of k's shape. No other
+ * cache row is touched.
+ */
+shp_status_t shp_qk_norm_rope_kv(const shp_tensor * q,
+                                 const shp_tensor * k,
+                                 const shp_tensor * v,
+                                 const shp_tensor * wq,
+                                 const shp_tensor * wk,
+                                 float              eps,
+                                 const shp_tensor * pos,
+                                 int32_t            n_dims,
+                                 float              freq_base,
+                                 float              freq_scale,
+                                 shp_tensor *       q_out,
+                                 shp_tensor *       k_cache,
+                                 shp_tensor *       v_cache,
+                                 int64_t            filled,
+                                 shp_stream_t       stream);
+
+/*
  * ggml_silu(g) followed by ggml_mul(., u): the SwiGLU of
  * src/arch/qwen3-tts/operations.cpp:39-41 (== ggml_swiglu_split(g, u)).
  * y = (g / (1 + expf(-g))) * u in f32. g, u, y F32 of one shape.
@@ -233,6 +260,22 @@ shp_status_t shp_add_leaky_relu(const shp_tensor * a,
  * src/arch/qwen3-tts/operations.cpp:143,147 when it is not fused into a norm.
  */
 shp_status_t shp_add(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream);
+
+/*
+ * ggml_soft_max_ext(a, mask, scale, max_bias): the attention softmax of
+ * src/arch/qwen3-tts/operations.cpp:131-133. Per row: w = a*scale + mask
+ * (f32), v = expf(w - max w), y = v * (float)(1/sum v) with the sum in
+ * double. a, y F32 [ne0, ne1, ne2, ne3] (y may alias a); mask NULL or F32
+ * [ne0, >= ne1, ne2 | divisor, ne3 | divisor], row i1 of head i2 reading mask
+ * row i1 of mask head i2 % mask->ne[2]. max_bias != 0 (ALiBi) gives
+ * SHP_ERR_UNSUPPORTED.
+ */
+shp_status_t shp_soft_max_ext(const shp_tensor * a,
+                              const shp_tensor * mask,
+                              float              scale,
+                              float              max_bias,
+                              shp_tensor *       y,
+                              shp_stream_t       stream);
 
 /*
  * ggml_exp: y = expf(x) per element, F32 of one shape

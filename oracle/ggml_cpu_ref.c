@@ -406,6 +406,55 @@ static void op_glu_swiglu(const orc_node * n, int ith, int nth) {
     }
 }
 
+/* ggml_soft_max_ext(x, mask, scale, max_bias = 0), ggml-CPU's per-row order:
+ * w = x*scale, then w += 1*mask (slope 1 without ALiBi); max over the row by
+ * the sequential (max > w ? max : w); v = expf(w - max) with each v added to a
+ * double sum; y = v * (float)(1.0/sum). Rows interleaved over threads.
+ * Site: qwen3-tts/operations.cpp:131-133 (scale 1/sqrt(head_dim), causal mask
+ * of tests/qwen3_tts_decoder_layer_test.cpp:174-181). */
+static void op_soft_max(const orc_node * n, int ith, int nth) {
+    const int64_t ne0    = n->ne0;
+    const int64_t ne1    = n->ne1;
+    const int64_t mrows  = n->src1_rows;
+    const int64_t mheads = n->i[0] > 0 ? n->i[0] : 1;
+    const float   scale  = n->f[0];
+    float *       w      = (float *) malloc((size_t) ne0 * sizeof(float));
+    if (w == NULL) {
+        atomic_store(&g_node_error, -2);
+        return;
+    }
+    for (int64_t r = ith; r < n->nrows; r += nth) {
+        const float * x = (const float *) n->src0 + r * ne0;
+        float *       y = (float *) n->dst + r * ne0;
+        for (int64_t i = 0; i < ne0; ++i) {
+            w[i] = x[i] * scale;
+        }
+        if (n->src1 != NULL) {
+            const int64_t i1 = r % ne1;
+            const int64_t h  = r / ne1;
+            const float * m  = (const float *) n->src1 + ((h % mheads) * mrows + i1) * ne0;
+            for (int64_t i = 0; i < ne0; ++i) {
+                w[i] += 1.0f * m[i];
+            }
+        }
+        float mx = -INFINITY;
+        for (int64_t i = 0; i < ne0; ++i) {
+            mx = mx > w[i] ? mx : w[i];
+        }
+        double sum = 0.0;
+        for (int64_t i = 0; i < ne0; ++i) {
+            const float v = expf(w[i] - mx);
+            sum += (double) v;
+            y[i] = v;
+        }
+        const float inv = (float) (1.0 / sum);
+        for (int64_t i = 0; i < ne0; ++i) {
+            y[i] *= inv;
+        }
+    }
+    free(w);
+}
+
 static void run_node(const orc_node * n, int ith, int nth) {
     switch (n->op) {
         case ORC_OP_ADD:
@@ -435,6 +484,9 @@ static void run_node(const orc_node * n, int ith, int nth) {
             break;
         case ORC_OP_GLU_SWIGLU:
             op_glu_swiglu(n, ith, nth);
+            break;
+        case ORC_OP_SOFT_MAX:
+            op_soft_max(n, ith, nth);
             break;
         default:
             atomic_store(&g_node_error, -1);

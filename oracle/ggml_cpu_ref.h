@@ -42,6 +42,7 @@ enum orc_op {
     ORC_OP_GET_ROWS,     /* dst[:, r] = to_f32(src0[:, ids[r]])     ggml_get_rows       */
     ORC_OP_CAST_F32,     /* BF16/F16/F32 -> F32                     ggml_cast           */
     ORC_OP_GLU_SWIGLU,   /* single-tensor swiglu                    ggml_swiglu         */
+    ORC_OP_SOFT_MAX,     /* softmax(x*scale + mask) per row         ggml_soft_max_ext   */
 };
 
 /*
@@ -62,6 +63,9 @@ enum orc_op {
  *               `type0`; src1 = I32 ids (nrows of them); dst F32.
  *   CAST_F32  : src0 of type `type0`.
  *   GLU_SWIGLU: src0 rows of 2*ne0 elements; i[0] = swapped.
+ *   SOFT_MAX  : src0 rows of ne0 scores, ne1 rows per head; src1 = F32 mask or
+ *               NULL, with src1_rows rows per mask head and i[0] mask heads
+ *               (head h reads mask head h % i[0]); f[0] = scale.
  */
 typedef struct orc_node {
     int32_t      op;

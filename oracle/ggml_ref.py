@@ -24,7 +24,7 @@ LIB_PATH = os.path.join(HERE, "libggml_cpu_ref.so")
 F32, F16, Q8_0, I32, BF16 = 0, 1, 8, 26, 30
 
 (OP_ADD, OP_MUL, OP_DIV, OP_RMS_NORM, OP_ROPE_NEOX, OP_SILU, OP_SIN, OP_SQR, OP_EXP, OP_LEAKY_RELU, OP_SCALE_BIAS,
- OP_GET_ROWS, OP_CAST_F32, OP_GLU_SWIGLU) = range(1, 15)
+ OP_GET_ROWS, OP_CAST_F32, OP_GLU_SWIGLU, OP_SOFT_MAX) = range(1, 16)
 
 
 class OrcNode(ctypes.Structure):
@@ -188,6 +188,21 @@ class Graph:
         dst = np.empty(a.shape[:-1] + (nc,), dtype=np.float32)
         return self._node(OP_GLU_SWIGLU, dst, a, ne0=nc, nrows=_rows(dst), i=(1 if swapped else 0,))
 
+    def soft_max_ext(self, x, mask, scale):
+        """x (heads, rows, cols) or (rows, cols) = ggml [cols, rows, heads]; mask None,
+        (mrows, cols) or (mheads, mrows, cols) with mrows >= rows and heads % mheads == 0."""
+        x = self._f32(x)
+        x3 = x.reshape((-1,) + x.shape[-2:])
+        ne1 = x3.shape[1]
+        mheads, mrows = 1, 0
+        if mask is not None:
+            mask = self._f32(mask)
+            m3 = mask.reshape((-1,) + mask.shape[-2:])
+            mheads, mrows = m3.shape[0], m3.shape[1]
+            assert m3.shape[2] == x.shape[-1] and mrows >= ne1 and x3.shape[0] % mheads == 0
+        return self._node(OP_SOFT_MAX, np.empty_like(x), x, mask, ne1=ne1, src1_rows=mrows, i=(mheads,),
+                          f=(scale,))
+
     def _array(self):
         arr = (OrcNode * len(self.nodes))(*self.nodes)
         return arr
@@ -317,14 +332,9 @@ def mul_mat(w, x):
 
 
 def soft_max_ext(scores, mask, scale):
-    """ggml_soft_max_ext(scores, mask, scale, 0): softmax over the last axis of
-    scores*scale + mask, sum in double."""
-    w = scores.astype(np.float32) * np.float32(scale)
-    if mask is not None:
-        w = w + mask.astype(np.float32)
-    m = w.max(axis=-1, keepdims=True)
-    e = np.exp((w - m).astype(np.float64))
-    return (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
+    """ggml_soft_max_ext(scores, mask, scale, 0) over the last axis, through the
+    C restatement (ggml-CPU's rounding order)."""
+    return run(lambda g: g.soft_max_ext(scores, mask, np.float32(scale)))
 
 
 class LcgStream:
@@ -364,9 +374,7 @@ def decoder_layer(x, pos, mask, W, shape, cache, filled, ops=None):
     q = mul_mat(W["q_proj"], normed).reshape(T, H, hd)
     k = mul_mat(W["k_proj"], normed).reshape(T, KVH, hd)
     v = mul_mat(W["v_proj"], normed).reshape(T, KVH, hd)
-    q, k = ops.qk_norm_rope(q, k, W["q_norm"], W["k_norm"], eps, pos, hd, theta)
-    cache["k"][filled:filled + T] = k
-    cache["v"][filled:filled + T] = v
+    q = ops.qk_norm_rope_kv(q, k, v, W["q_norm"], W["k_norm"], eps, pos, hd, theta, cache, filled)
     total = filled + T
     kc, vc = cache["k"][:total], cache["v"][:total]
     group = H // KVH
@@ -374,7 +382,7 @@ def decoder_layer(x, pos, mask, W, shape, cache, filled, ops=None):
     for h in range(H):
         kv = h // group  # ggml_mul_mat's broadcast: blocked grouping (operations.cpp:127-131)
         scores = (q[:, h, :].astype(np.float64) @ kc[:, kv, :].astype(np.float64).T).astype(np.float32)
-        p = soft_max_ext(scores, mask, 1.0 / np.sqrt(np.float32(hd)))
+        p = ops.soft_max_ext(scores, mask, np.float32(1.0) / np.sqrt(np.float32(hd)))
         attended[:, h, :] = (p.astype(np.float64) @ vc[:, kv, :].astype(np.float64)).astype(np.float32)
     projected = mul_mat(W["o_proj"], attended.reshape(T, H * hd))
     after_attention, mlp_in = ops.add_rms_norm_w(residual, projected, W["post_attention_layernorm"], eps)
@@ -392,6 +400,18 @@ class OracleOps:
 
     def qk_norm_rope(self, q, k, wq, wk, eps, pos, n_dims, theta):
         return run(lambda g: qk_norm_rope(g, q, k, wq, wk, eps, pos, n_dims, theta))
+
+    def qk_norm_rope_kv(self, q, k, v, wq, wk, eps, pos, n_dims, theta, cache, filled):
+        """operations.cpp:98-116: q and k normalised and rotated, then k and v
+        copied (ggml_cpy) into cache rows [filled, filled + T); returns q."""
+        q, k = self.qk_norm_rope(q, k, wq, wk, eps, pos, n_dims, theta)
+        T = q.shape[0]
+        cache["k"][filled:filled + T] = k
+        cache["v"][filled:filled + T] = v
+        return q
+
+    def soft_max_ext(self, scores, mask, scale):
+        return soft_max_ext(scores, mask, scale)
 
     def add_rms_norm_w(self, a, b, w, eps):
         return run(lambda g: add_rms_norm_w(g, a, b, w, eps))

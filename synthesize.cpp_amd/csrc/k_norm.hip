@@ -380,7 +380,7 @@ struct RopePart {
 };
 
 struct RopeArgs {
-    RopePart        part[2];  // q, then k (heads == 0 when absent)
+    RopePart        part[3];  // q, k, then v (heads == 0 when absent); v rows are copied unchanged
     const int32_t * pos;
     int64_t         npos;
     int32_t         ne0;
@@ -391,26 +391,36 @@ struct RopeArgs {
     float           eps;
 };
 
-// Fields of head row hh (q rows first, then k rows) as selects between the two
-// parts' kernel arguments, which stay in scalar registers. Indexing part[]
-// with a per-lane value instead would read the argument block through vector
-// memory and put a dependent round trip in front of every row load.
+// Fields of head row hh (q rows first, then k rows, then v rows) as selects
+// between the parts' kernel arguments, which stay in scalar registers.
+// Indexing part[] with a per-lane value instead would read the argument block
+// through vector memory and put a dependent round trip in front of every row
+// load. KV: the launch has v rows (copied, no gain).
 struct RowRef {
     const float * x;
     float *       y;
     const void *  w;
+    bool          copy;
 };
 
-__device__ __forceinline__ RowRef rope_row(const RopeArgs & a, int hh, int64_t pi) {
+template <bool KV> __device__ __forceinline__ RowRef rope_row(const RopeArgs & a, int hh, int64_t pi) {
     const RopePart & q   = a.part[0];
     const RopePart & k   = a.part[1];
-    const bool       isk = hh >= q.heads;
-    const int64_t    h   = isk ? hh - q.heads : hh;
-    const char *     xb  = reinterpret_cast<const char *>(isk ? k.x : q.x);
-    char *           yb  = reinterpret_cast<char *>(isk ? k.y : q.y);
-    const int64_t    xo  = h * (isk ? k.xnb1 : q.xnb1) + pi * (isk ? k.xnb2 : q.xnb2);
-    const int64_t    yo  = h * (isk ? k.ynb1 : q.ynb1) + pi * (isk ? k.ynb2 : q.ynb2);
-    return RowRef{ reinterpret_cast<const float *>(xb + xo), reinterpret_cast<float *>(yb + yo), isk ? k.w : q.w };
+    const RopePart & v   = a.part[2];
+    const int        qk  = q.heads + k.heads;
+    const bool       isv = KV && hh >= qk;
+    const bool       isk = !isv && hh >= q.heads;
+    const int64_t    h   = isv ? hh - qk : (isk ? hh - q.heads : hh);
+    const char *     xb  = reinterpret_cast<const char *>(isv ? v.x : (isk ? k.x : q.x));
+    char *           yb  = reinterpret_cast<char *>(isv ? v.y : (isk ? k.y : q.y));
+    const int64_t    xo  = h * (isv ? v.xnb1 : (isk ? k.xnb1 : q.xnb1)) + pi * (isv ? v.xnb2 : (isk ? k.xnb2 : q.xnb2));
+    const int64_t    yo  = h * (isv ? v.ynb1 : (isk ? k.ynb1 : q.ynb1)) + pi * (isv ? v.ynb2 : (isk ? k.ynb2 : q.ynb2));
+    return RowRef{ reinterpret_cast<const float *>(xb + xo), reinterpret_cast<float *>(yb + yo),
+                   isv ? nullptr : (isk ? k.w : q.w), isv };
+}
+
+template <bool KV> __device__ __forceinline__ int rope_rows(const RopeArgs & a) {
+    return a.part[0].heads + a.part[1].heads + (KV ? a.part[2].heads : 0);
 }
 
 // cos/sin of an f32 angle: evaluated in double and rounded once (the fast
@@ -445,27 +455,27 @@ __device__ __forceinline__ void rope_cs(int32_t p, int k, const RopeArgs & a, fl
 // x[64+4j..64+4j+3] as two float4, i.e. both halves of NEOX pairs 4j..4j+3,
 // so the rotation needs no data exchange and every access is 128-bit. The
 // block has one 16-lane group per head row of the position (q heads, then k
-// heads; 24 rows = 384 lanes for Qwen3-TTS), so every row load is issued at
-// once. Meanwhile wave 0 builds the position's 64-entry cos/sin cache: all 64
+// heads; 24 rows = 384 lanes for Qwen3-TTS; with the KV-cache write, v heads
+// follow and are stored unchanged), so every row load is issued at once. Meanwhile wave 0 builds the position's 64-entry cos/sin cache: all 64
 // lanes run the same serial f32 theta chain and lane k keeps the k-th value,
 // evaluates its cos/sin in double and writes them to LDS; one barrier later
 // every lane reads the 4 pairs it needs.
 constexpr int kRopeLanes   = 16;
 constexpr int kRopeMaxRows = 1024 / kRopeLanes;
 
-template <bool NORM, int WT> __global__ __launch_bounds__(1024) void k_rope128(const RopeArgs a) {
+template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(1024) void k_rope128(const RopeArgs a) {
     __shared__ f32x4 s_cos[16];
     __shared__ f32x4 s_sin[16];
 
     const int64_t pi    = blockIdx.x;
-    const int     total = a.part[0].heads + a.part[1].heads;
+    const int     total = rope_rows<KV>(a);
     const int     slots = blockDim.x / kRopeLanes;
     const int     g     = threadIdx.x / kRopeLanes;
     const int     l     = threadIdx.x % kRopeLanes;
 
     // 1. this lane's first row, and its gains (both issued before any wait)
     const bool live = g < total;
-    RowRef     r    = rope_row(a, live ? g : 0, pi);
+    RowRef     r    = rope_row<KV>(a, live ? g : 0, pi);
     f32x4      lo   = splat4(0.0f);
     f32x4      hi   = splat4(0.0f);
     if (live) {
@@ -476,7 +486,7 @@ template <bool NORM, int WT> __global__ __launch_bounds__(1024) void k_rope128(c
     // wave 0 wait for every outstanding load before its theta chain.
     WRaw<WT> wlo_raw{}, whi_raw{};
     if constexpr (NORM && WT != kWNone) {
-        if (live) {
+        if (live && !r.copy) {
             wlo_raw = load_wraw<WT>(r.w, 4 * l);
             whi_raw = load_wraw<WT>(r.w, 64 + 4 * l);
         }
@@ -505,14 +515,18 @@ template <bool NORM, int WT> __global__ __launch_bounds__(1024) void k_rope128(c
     //    64 heads) are loaded here
     for (int row = g; row < total; row += slots) {
         if (row != g) {
-            r  = rope_row(a, row, pi);
+            r  = rope_row<KV>(a, row, pi);
             lo = ld_stream(reinterpret_cast<const f32x4 *>(r.x) + l);
             hi = ld_stream(reinterpret_cast<const f32x4 *>(r.x + 64) + l);
             if constexpr (NORM && WT != kWNone) {
-                wlo_raw = load_wraw<WT>(r.w, 4 * l);
-                whi_raw = load_wraw<WT>(r.w, 64 + 4 * l);
+                if (!r.copy) {
+                    wlo_raw = load_wraw<WT>(r.w, 4 * l);
+                    whi_raw = load_wraw<WT>(r.w, 64 + 4 * l);
+                }
             }
         }
+        const f32x4 rawlo = lo;
+        const f32x4 rawhi = hi;
         if constexpr (NORM) {
             double acc        = sq4v(lo) + sq4v(hi);
             acc               = group_sum<kRopeLanes>(acc);
@@ -530,26 +544,33 @@ template <bool NORM, int WT> __global__ __launch_bounds__(1024) void k_rope128(c
                          lo.w * cs.w - hi.w * sn.w };
         const f32x4 ohi{ lo.x * sn.x + hi.x * cs.x, lo.y * sn.y + hi.y * cs.y, lo.z * sn.z + hi.z * cs.z,
                          lo.w * sn.w + hi.w * cs.w };
-        st_stream(reinterpret_cast<f32x4 *>(r.y) + l, olo);
-        st_stream(reinterpret_cast<f32x4 *>(r.y + 64) + l, ohi);
+        // a v row (whole 16-lane group) stores its input unchanged
+        st_stream(reinterpret_cast<f32x4 *>(r.y) + l, KV && r.copy ? rawlo : olo);
+        st_stream(reinterpret_cast<f32x4 *>(r.y + 64) + l, KV && r.copy ? rawhi : ohi);
     }
 }
 
 // Any head_dim / n_dims: one wave per head row; the theta recurrence is
 // replayed per pair (fine for the small shapes that take this path).
-template <bool NORM, int WT> __global__ __launch_bounds__(256) void k_rope_generic(const RopeArgs a) {
+template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(256) void k_rope_generic(const RopeArgs a) {
     const int     lane  = threadIdx.x % kWave;
-    const int     total = a.part[0].heads + a.part[1].heads;
+    const int     total = rope_rows<KV>(a);
     const int64_t row   = static_cast<int64_t>(blockIdx.x) * (256 / kWave) + threadIdx.x / kWave;
     if (row >= a.npos * total) {
         return;
     }
     const int64_t pi = row / total;
     const int     hh = static_cast<int>(row % total);
-    const RowRef  rr = rope_row(a, hh, pi);
+    const RowRef  rr = rope_row<KV>(a, hh, pi);
     const float * xr = rr.x;
     float *       yr = rr.y;
-    const int32_t p  = a.pos[pi];
+    if (KV && rr.copy) {  // a v row: the cache write, a plain copy (ggml_cpy F32 -> F32)
+        for (int i = lane; i < a.ne0; i += kWave) {
+            yr[i] = xr[i];
+        }
+        return;
+    }
+    const int32_t p = a.pos[pi];
 
     float scale = 1.0f;
     if constexpr (NORM) {
@@ -584,30 +605,32 @@ template <bool NORM, int WT> __global__ __launch_bounds__(256) void k_rope_gener
     }
 }
 
-template <bool NORM, int WT> shp_status_t launch_rope(const RopeArgs & a, bool fast, hipStream_t stream) {
-    const int total = a.part[0].heads + a.part[1].heads;
+template <bool NORM, int WT, bool KV> shp_status_t launch_rope(const RopeArgs & a, bool fast, hipStream_t stream) {
+    const int total = a.part[0].heads + a.part[1].heads + a.part[2].heads;
     if (fast) {
         const int rows    = total < kRopeMaxRows ? total : kRopeMaxRows;
         const int threads = ((rows * kRopeLanes + kWave - 1) / kWave) * kWave;
-        hipLaunchKernelGGL((k_rope128<NORM, WT>), dim3(static_cast<unsigned>(a.npos)), dim3(threads), 0, stream, a);
+        hipLaunchKernelGGL((k_rope128<NORM, WT, KV>), dim3(static_cast<unsigned>(a.npos)), dim3(threads), 0, stream,
+                           a);
         return launch_status();
     }
     const int64_t rows   = a.npos * total;
     const int64_t blocks = (rows + 3) / 4;
-    hipLaunchKernelGGL((k_rope_generic<NORM, WT>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((k_rope_generic<NORM, WT, KV>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
     return launch_status();
 }
 
-template <bool NORM> shp_status_t dispatch_rope_w(const RopeArgs & a, int wk, bool fast, hipStream_t stream) {
+template <bool NORM, bool KV>
+shp_status_t dispatch_rope_w(const RopeArgs & a, int wk, bool fast, hipStream_t stream) {
     switch (wk) {
         case kWNone:
-            return launch_rope<NORM, kWNone>(a, fast, stream);
+            return launch_rope<NORM, kWNone, KV>(a, fast, stream);
         case kWF32:
-            return launch_rope<NORM, kWF32>(a, fast, stream);
+            return launch_rope<NORM, kWF32, KV>(a, fast, stream);
         case kWBF16:
-            return launch_rope<NORM, kWBF16>(a, fast, stream);
+            return launch_rope<NORM, kWBF16, KV>(a, fast, stream);
         case kWF16:
-            return launch_rope<NORM, kWF16>(a, fast, stream);
+            return launch_rope<NORM, kWF16, KV>(a, fast, stream);
         default:
             return SHP_ERR_UNSUPPORTED;
     }
@@ -630,6 +653,7 @@ bool gain_aligned(const shp_tensor * w) {
 
 shp_status_t rope_entry(const shp_tensor * q,
                         const shp_tensor * k,
+                        const shp_tensor * v,
                         const shp_tensor * wq,
                         const shp_tensor * wk,
                         bool               norm,
@@ -641,14 +665,18 @@ shp_status_t rope_entry(const shp_tensor * q,
                         float              attn_factor,
                         shp_tensor *       q_out,
                         shp_tensor *       k_out,
+                        shp_tensor *       v_out,
                         shp_stream_t       stream) {
     if (!rope_part_ok(q, q_out) || !well_formed(pos) || pos->type != SHP_TYPE_I32) {
         return SHP_ERR_INVALID_ARG;
     }
-    if ((k == nullptr) != (k_out == nullptr)) {
+    if ((k == nullptr) != (k_out == nullptr) || (v == nullptr) != (v_out == nullptr) || (v != nullptr && k == nullptr)) {
         return SHP_ERR_INVALID_ARG;
     }
     if (k != nullptr && (!rope_part_ok(k, k_out) || k->ne[0] != q->ne[0] || k->ne[2] != q->ne[2])) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    if (v != nullptr && (!rope_part_ok(v, v_out) || !same_shape(*v, *k))) {
         return SHP_ERR_INVALID_ARG;
     }
     // ggml_rope_ext: positions are an I32 vector of ne[2] entries.
@@ -685,7 +713,7 @@ shp_status_t rope_entry(const shp_tensor * q,
             return SHP_ERR_INVALID_ARG;
         }
     }
-    if (q->ne[1] + (k != nullptr ? k->ne[1] : 0) > INT32_MAX) {
+    if (q->ne[1] + (k != nullptr ? k->ne[1] : 0) + (v != nullptr ? v->ne[1] : 0) > INT32_MAX) {
         return SHP_ERR_UNSUPPORTED;
     }
 
@@ -707,6 +735,12 @@ shp_status_t rope_entry(const shp_tensor * q,
         a.part[1]       = a.part[0];
         a.part[1].heads = 0;
     }
+    if (v != nullptr) {
+        fill(a.part[2], v, v_out, nullptr);
+    } else {
+        a.part[2]       = a.part[0];
+        a.part[2].heads = 0;
+    }
     a.pos         = static_cast<const int32_t *>(pos->data);
     a.npos        = q->ne[2];
     a.ne0         = static_cast<int32_t>(q->ne[0]);
@@ -723,6 +757,9 @@ shp_status_t rope_entry(const shp_tensor * q,
     if (k != nullptr) {
         fast = fast && part_aligned(*k) && part_aligned(*k_out);
     }
+    if (v != nullptr) {
+        fast = fast && part_aligned(*v) && part_aligned(*v_out);
+    }
     if (norm) {
         fast = fast && gain_aligned(wq) && gain_aligned(wk);
     }
@@ -730,7 +767,24 @@ shp_status_t rope_entry(const shp_tensor * q,
         return SHP_ERR_UNSUPPORTED;
     }
     const hipStream_t st = as_stream(stream);
-    return norm ? dispatch_rope_w<true>(a, wkind, fast, st) : dispatch_rope_w<false>(a, kWNone, fast, st);
+    if (v != nullptr) {
+        return norm ? dispatch_rope_w<true, true>(a, wkind, fast, st) : dispatch_rope_w<false, true>(a, kWNone, fast, st);
+    }
+    return norm ? dispatch_rope_w<true, false>(a, wkind, fast, st) : dispatch_rope_w<false, false>(a, kWNone, fast, st);
+}
+
+// The rows [filled, filled + T) of a KV cache [head_dim, kv_heads, capacity, 1]
+// as a [head_dim, kv_heads, T] view: ggml_view_3d(cache, hd, kv, T, nb1, nb2,
+// filled*nb2) of qwen3-tts/operations.cpp:109-116.
+bool cache_view(const shp_tensor * cache, const shp_tensor * src, int64_t filled, shp_tensor & view) {
+    if (!well_formed(cache) || src == nullptr || cache->type != SHP_TYPE_F32 || cache->ne[0] != src->ne[0] ||
+        cache->ne[1] != src->ne[1] || cache->ne[3] != 1 || filled < 0 || src->ne[2] > cache->ne[2] - filled) {
+        return false;
+    }
+    view       = *cache;
+    view.ne[2] = src->ne[2];
+    view.data  = static_cast<char *>(cache->data) + static_cast<size_t>(filled) * cache->nb[2];
+    return true;
 }
 
 }  // namespace
@@ -770,8 +824,8 @@ extern "C" shp_status_t shp_rope_ext(const shp_tensor * x,
     if (mode != SHP_ROPE_TYPE_NEOX || ext_factor != 0.0f) {
         return SHP_ERR_UNSUPPORTED;
     }
-    return shp::rope_entry(x, nullptr, nullptr, nullptr, false, 0.0f, pos, n_dims, freq_base, freq_scale, attn_factor,
-                           y, nullptr, stream);
+    return shp::rope_entry(x, nullptr, nullptr, nullptr, nullptr, false, 0.0f, pos, n_dims, freq_base, freq_scale,
+                           attn_factor, y, nullptr, nullptr, stream);
 }
 
 extern "C" shp_status_t shp_qk_norm_rope(const shp_tensor * q,
@@ -786,5 +840,32 @@ extern "C" shp_status_t shp_qk_norm_rope(const shp_tensor * q,
                                          shp_tensor *       q_out,
                                          shp_tensor *       k_out,
                                          shp_stream_t       stream) {
-    return shp::rope_entry(q, k, wq, wk, true, eps, pos, n_dims, freq_base, freq_scale, 1.0f, q_out, k_out, stream);
+    return shp::rope_entry(q, k, nullptr, wq, wk, true, eps, pos, n_dims, freq_base, freq_scale, 1.0f, q_out, k_out,
+                           nullptr, stream);
+}
+
+extern "C" shp_status_t shp_qk_norm_rope_kv(const shp_tensor * q,
+                                            const shp_tensor * k,
+                                            const shp_tensor * v,
+                                            const shp_tensor * wq,
+                                            const shp_tensor * wk,
+                                            float              eps,
+                                            const shp_tensor * pos,
+                                            int32_t            n_dims,
+                                            float              freq_base,
+                                            float              freq_scale,
+                                            shp_tensor *       q_out,
+                                            shp_tensor *       k_cache,
+                                            shp_tensor *       v_cache,
+                                            int64_t            filled,
+                                            shp_stream_t       stream) {
+    if (!shp::well_formed(k) || !shp::well_formed(v) || k_cache == nullptr || v_cache == nullptr) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    shp_tensor kview{}, vview{};
+    if (!shp::cache_view(k_cache, k, filled, kview) || !shp::cache_view(v_cache, v, filled, vview)) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    return shp::rope_entry(q, k, v, wq, wk, true, eps, pos, n_dims, freq_base, freq_scale, 1.0f, q_out, &kview,
+                           &vview, stream);
 }

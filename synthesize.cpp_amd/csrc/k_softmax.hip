@@ -1,0 +1,248 @@
+// ggml_soft_max_ext(a, mask, scale, max_bias = 0) for gfx950: the attention
+// softmax of src/arch/qwen3-tts/operations.cpp:131-133 (scores over the cached
+// keys, scaled by 1/sqrt(head_dim), causal mask).
+//
+// Per row, in ggml-CPU's rounding order:
+//   w_i  = x_i*scale + 1*mask_i          (f32; the slope is 1 without ALiBi)
+//   m    = max_i w_i
+//   v_i  = exp(w_i - m)                  (f32 difference, exp rounded to f32)
+//   sum  = sum_i (double) v_i            (double)
+//   y_i  = v_i * (float)(1/sum)          (the reciprocal in double, rounded to f32)
+// The exp is the double exp rounded once to f32, which is glibc's expf except
+// within ~2^-52 of a rounding boundary; the double sum is added in a
+// different order than the CPU's loop, which moves the f32 reciprocal only
+// when the sum lies within ~1e-16 of a rounding boundary. A row holding a NaN
+// or +inf (or only -inf) comes out NaN, as on the CPU: the max is then NaN or
+// inf, or the NaN reaches the sum.
+//
+// Launch shapes: rows up to 2048 wide take one wave per row with the row in
+// registers (K elements per lane, wave-level reductions only: no LDS, no
+// barrier), which is what the decode step's few short rows need; wider rows
+// take one 256-thread block per row and three passes over the row.
+
+#include <cmath>
+
+#include "shp_internal.hpp"
+
+namespace shp {
+namespace {
+
+struct SoftMaxArgs {
+    const float * x;
+    RowMap        xm;
+    const float * mask;  // null: no mask
+    int64_t       mnb1;
+    int64_t       mnb2;
+    int64_t       mnb3;
+    int64_t       mne2;  // mask heads (broadcast: head i2 reads mask head i2 % mne2)
+    int64_t       mne3;
+    float *       y;
+    RowMap        ym;
+    int64_t       nrows;
+    int64_t       ne1;   // rows per head
+    int64_t       ne2;   // heads
+    int32_t       ne0;
+    float         scale;
+};
+
+constexpr int kSoftMaxWaveMax = 2048;  // widest row of the one-wave kernel
+constexpr int kSoftMaxBlock   = 256;
+
+__device__ __forceinline__ float exp_f32(float x) {
+    return static_cast<float>(exp(static_cast<double>(x)));
+}
+
+// Mask row of score row r = (i1, i2, i3): ggml's i11 = i1, i12 = i2 % ne12,
+// i13 = i3 % ne13.
+__device__ __forceinline__ const float * mask_row(const SoftMaxArgs & a, int64_t r) {
+    const int64_t i1 = r % a.ne1;
+    const int64_t q  = r / a.ne1;
+    const int64_t i2 = q % a.ne2;
+    const int64_t i3 = q / a.ne2;
+    return reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.mask) + i1 * a.mnb1 +
+                                           (i2 % a.mne2) * a.mnb2 + (i3 % a.mne3) * a.mnb3);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        v = fmaxf(v, __shfl_xor(v, off, kWave));
+    }
+    return v;
+}
+
+// One wave per row, element lane + 64k in register k (k < K, 64K >= ne0).
+template <int K, bool MASK> __global__ __launch_bounds__(256) void k_soft_max_wave(const SoftMaxArgs a) {
+    const int     lane = threadIdx.x % kWave;
+    const int64_t r    = static_cast<int64_t>(blockIdx.x) * (256 / kWave) + threadIdx.x / kWave;
+    if (r >= a.nrows) {
+        return;  // whole wave
+    }
+    const float * xr = reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.x) + row_offset(a.xm, r));
+    float *       yr = reinterpret_cast<float *>(reinterpret_cast<char *>(a.y) + row_offset(a.ym, r));
+    const float * mr = MASK ? mask_row(a, r) : nullptr;
+    float         w[K];
+    float         mk[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int i = lane + kWave * k;
+        w[k]        = i < a.ne0 ? xr[i] : 0.0f;
+        mk[k]       = MASK && i < a.ne0 ? mr[i] : 0.0f;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int i = lane + kWave * k;
+        w[k]        = w[k] * a.scale;
+        if constexpr (MASK) {
+            w[k] = w[k] + mk[k];
+        }
+        mx = i < a.ne0 ? fmaxf(mx, w[k]) : mx;
+    }
+    mx         = wave_max(mx);
+    double sum = 0.0;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int i = lane + kWave * k;
+        w[k]        = exp_f32(w[k] - mx);
+        sum += i < a.ne0 ? static_cast<double>(w[k]) : 0.0;
+    }
+    sum             = group_sum<kWave>(sum);
+    const float inv = static_cast<float>(1.0 / sum);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int i = lane + kWave * k;
+        if (i < a.ne0) {
+            yr[i] = w[k] * inv;
+        }
+    }
+}
+
+// One block per row, three passes: the max, the sum, the scaled exps.
+template <bool MASK> __device__ __forceinline__ float sm_w(const SoftMaxArgs & a, const float * xr, const float * mr, int i) {
+    float w = xr[i] * a.scale;
+    if constexpr (MASK) {
+        w = w + mr[i];
+    }
+    return w;
+}
+
+template <bool MASK> __global__ __launch_bounds__(kSoftMaxBlock) void k_soft_max_block(const SoftMaxArgs a) {
+    __shared__ float  s_max[kSoftMaxBlock / kWave];
+    __shared__ double s_sum[kSoftMaxBlock / kWave];
+    const int64_t r    = blockIdx.x;
+    const int     lane = threadIdx.x % kWave;
+    const int     wv   = threadIdx.x / kWave;
+    const float * xr   = reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.x) + row_offset(a.xm, r));
+    float *       yr   = reinterpret_cast<float *>(reinterpret_cast<char *>(a.y) + row_offset(a.ym, r));
+    const float * mr   = MASK ? mask_row(a, r) : nullptr;
+
+    float mx = -INFINITY;
+    for (int i = threadIdx.x; i < a.ne0; i += kSoftMaxBlock) {
+        mx = fmaxf(mx, sm_w<MASK>(a, xr, mr, i));
+    }
+    mx = wave_max(mx);
+    if (lane == 0) {
+        s_max[wv] = mx;
+    }
+    __syncthreads();
+    mx = s_max[0];
+#pragma unroll
+    for (int j = 1; j < kSoftMaxBlock / kWave; ++j) {
+        mx = fmaxf(mx, s_max[j]);
+    }
+
+    double sum = 0.0;
+    for (int i = threadIdx.x; i < a.ne0; i += kSoftMaxBlock) {
+        sum += static_cast<double>(exp_f32(sm_w<MASK>(a, xr, mr, i) - mx));
+    }
+    sum = group_sum<kWave>(sum);
+    if (lane == 0) {
+        s_sum[wv] = sum;
+    }
+    __syncthreads();
+    sum = s_sum[0];
+#pragma unroll
+    for (int j = 1; j < kSoftMaxBlock / kWave; ++j) {
+        sum += s_sum[j];
+    }
+    const float inv = static_cast<float>(1.0 / sum);
+    for (int i = threadIdx.x; i < a.ne0; i += kSoftMaxBlock) {
+        yr[i] = exp_f32(sm_w<MASK>(a, xr, mr, i) - mx) * inv;
+    }
+}
+
+template <bool MASK> shp_status_t launch_soft_max(const SoftMaxArgs & a, hipStream_t stream) {
+    if (a.ne0 > kSoftMaxWaveMax) {
+        hipLaunchKernelGGL((k_soft_max_block<MASK>), dim3(static_cast<unsigned>(a.nrows)), dim3(kSoftMaxBlock), 0,
+                           stream, a);
+        return launch_status();
+    }
+    const dim3 grid(static_cast<unsigned>((a.nrows + 3) / 4));
+    const int  k = (a.ne0 + kWave - 1) / kWave;
+    if (k <= 1) {
+        hipLaunchKernelGGL((k_soft_max_wave<1, MASK>), grid, dim3(256), 0, stream, a);
+    } else if (k <= 2) {
+        hipLaunchKernelGGL((k_soft_max_wave<2, MASK>), grid, dim3(256), 0, stream, a);
+    } else if (k <= 4) {
+        hipLaunchKernelGGL((k_soft_max_wave<4, MASK>), grid, dim3(256), 0, stream, a);
+    } else if (k <= 8) {
+        hipLaunchKernelGGL((k_soft_max_wave<8, MASK>), grid, dim3(256), 0, stream, a);
+    } else if (k <= 16) {
+        hipLaunchKernelGGL((k_soft_max_wave<16, MASK>), grid, dim3(256), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((k_soft_max_wave<32, MASK>), grid, dim3(256), 0, stream, a);
+    }
+    return launch_status();
+}
+
+}  // namespace
+}  // namespace shp
+
+using namespace shp;
+
+extern "C" shp_status_t shp_soft_max_ext(const shp_tensor * a,
+                                         const shp_tensor * mask,
+                                         float              scale,
+                                         float              max_bias,
+                                         shp_tensor *       y,
+                                         shp_stream_t       stream) {
+    if (!well_formed(a) || !well_formed(y) || (mask != nullptr && !well_formed(mask))) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    if (a->type != SHP_TYPE_F32 || y->type != SHP_TYPE_F32 || (mask != nullptr && mask->type != SHP_TYPE_F32)) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    if (max_bias != 0.0f) {
+        return SHP_ERR_UNSUPPORTED;  // ALiBi slopes: not on this path
+    }
+    if (!same_shape(*a, *y) || a->ne[0] > INT32_MAX || nrows(*a) > INT32_MAX) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    // ggml_soft_max_ext's mask contract: same row length, at least as many
+    // rows, heads and batches broadcast by whole repeats.
+    if (mask != nullptr && (mask->ne[0] != a->ne[0] || mask->ne[1] < a->ne[1] || a->ne[2] % mask->ne[2] != 0 ||
+                            a->ne[3] % mask->ne[3] != 0)) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    SoftMaxArgs g{};
+    g.x     = static_cast<const float *>(a->data);
+    g.xm    = make_rowmap(*a);
+    g.y     = static_cast<float *>(y->data);
+    g.ym    = make_rowmap(*y);
+    g.nrows = nrows(*a);
+    g.ne1   = a->ne[1];
+    g.ne2   = a->ne[2];
+    g.ne0   = static_cast<int32_t>(a->ne[0]);
+    g.scale = scale;
+    if (mask != nullptr) {
+        g.mask = static_cast<const float *>(mask->data);
+        g.mnb1 = static_cast<int64_t>(mask->nb[1]);
+        g.mnb2 = static_cast<int64_t>(mask->nb[2]);
+        g.mnb3 = static_cast<int64_t>(mask->nb[3]);
+        g.mne2 = mask->ne[2];
+        g.mne3 = mask->ne[3];
+        return launch_soft_max<true>(g, as_stream(stream));
+    }
+    return launch_soft_max<false>(g, as_stream(stream));
+}

@@ -66,9 +66,11 @@ def load(path=None):
         "shp_snake": [_PT, _PT, _PT, vp],
         "shp_add_leaky_relu": [_PT, _PT, f, _PT, _PT, vp],
         "shp_add": [_PT, _PT, _PT, vp],
+        "shp_qk_norm_rope_kv": [_PT, _PT, _PT, _PT, _PT, f, _PT, i32, f, f, _PT, _PT, _PT, ctypes.c_int64, vp],
         "shp_snake_guarded": [_PT, _PT, _PT, vp],
         "shp_snake_beta": [_PT, _PT, _PT, _PT, vp],
         "shp_exp": [_PT, _PT, vp],
+        "shp_soft_max_ext": [_PT, _PT, f, f, _PT, vp],
         "shp_scale_bias": [_PT, f, f, _PT, vp],
         "shp_sum_scale_leaky_relu": [_PT, i32, f, f, _PT, _PT, vp],
     }
@@ -235,6 +237,19 @@ def qk_norm_rope(q, k, wq, wk, eps, pos, n_dims, freq_base, freq_scale=1.0, q_ou
     return q_out, k_out
 
 
+def qk_norm_rope_kv(q, k, v, wq, wk, eps, pos, n_dims, freq_base, k_cache, v_cache, filled, freq_scale=1.0,
+                    q_out=None):
+    """qk_norm_rope plus the step's cache write: the rotated k and v land in rows
+    [filled, filled + T) of k_cache / v_cache (T, ...) = torch (capacity, kv_heads,
+    head_dim); returns q_out."""
+    q_out = q.new_empty(q.shape) if q_out is None else q_out
+    _check(load().shp_qk_norm_rope_kv(_ref(desc(q)), _ref(desc(k)), _ref(desc(v)), _ref(desc(wq)), _ref(desc(wk)),
+                                      float(eps), _ref(desc(pos)), int(n_dims), float(freq_base), float(freq_scale),
+                                      _ref(desc(q_out)), _ref(desc(k_cache)), _ref(desc(v_cache)), int(filled),
+                                      _stream()), "qk_norm_rope_kv")
+    return q_out
+
+
 def swiglu(g, u=None, out=None):
     """ggml_silu(g) then ggml_mul(., u) (u None: bare silu)."""
     out = g.new_empty(g.shape) if out is None else out
@@ -268,6 +283,15 @@ def snake_beta(x, log_alpha, log_beta, out=None):
     out = x.new_empty(x.shape) if out is None else out
     _check(load().shp_snake_beta(_ref(desc(x)), _ref(desc(log_alpha)), _ref(desc(log_beta)), _ref(desc(out)),
                                  _stream()), "snake_beta")
+    return out
+
+
+def soft_max_ext(a, mask, scale, max_bias=0.0, out=None):
+    """ggml_soft_max_ext over the last axis of a (..., ne1, ne0); mask None or
+    (ne1', ne0) / (heads', ne1', ne0) broadcast as ggml does."""
+    out = a.new_empty(a.shape) if out is None else out
+    _check(load().shp_soft_max_ext(_ref(desc(a)), _ref(desc(mask)), float(scale), float(max_bias), _ref(desc(out)),
+                                   _stream()), "soft_max_ext")
     return out
 
 

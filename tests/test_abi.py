@@ -133,6 +133,21 @@ def test_argument_validation():
     assert L.shp_sum_scale_leaky_relu(terms, 0, 1.0, 0.1, None, R(a), None) == S.ERR_INVALID_ARG
     assert L.shp_sum_scale_leaky_relu(terms, 9, 1.0, 0.1, None, R(a), None) == S.ERR_INVALID_ARG
     assert L.shp_sum_scale_leaky_relu(None, 1, 1.0, 0.1, None, R(a), None) == S.ERR_INVALID_ARG
+    kc = mk(S.TYPE_F32, [128, 8, 64])
+    v = mk(S.TYPE_F32, [128, 8, 5])
+    args = lambda filled, cache=kc, vv=v: (R(q), R(k), R(vv), R(wk), R(wk), 1e-6, R(pos), 128, 1e6, 1.0, R(q),
+                                           R(cache), R(kc), filled, None)
+    assert L.shp_qk_norm_rope_kv(*args(60)) == S.ERR_INVALID_ARG  # 60 + 5 rows > capacity 64
+    assert L.shp_qk_norm_rope_kv(*args(-1)) == S.ERR_INVALID_ARG
+    assert L.shp_qk_norm_rope_kv(*args(0, cache=mk(S.TYPE_F32, [128, 4, 64]))) == S.ERR_INVALID_ARG  # kv heads
+    assert L.shp_qk_norm_rope_kv(*args(0, vv=mk(S.TYPE_F32, [128, 8, 4]))) == S.ERR_INVALID_ARG  # v shape
+    assert L.shp_qk_norm_rope_kv(*args(0, cache=mk(S.TYPE_F16, [128, 8, 64]))) == S.ERR_INVALID_ARG  # cache type
+    sc = mk(S.TYPE_F32, [37, 1, 16])
+    assert L.shp_soft_max_ext(R(sc), None, 0.1, 0.5, R(sc), None) == S.ERR_UNSUPPORTED  # ALiBi
+    assert L.shp_soft_max_ext(R(sc), R(mk(S.TYPE_F32, [36, 1])), 0.1, 0.0, R(sc), None) == S.ERR_INVALID_ARG
+    assert L.shp_soft_max_ext(R(sc), R(mk(S.TYPE_F32, [37, 1, 3])), 0.1, 0.0, R(sc), None) == S.ERR_INVALID_ARG
+    assert L.shp_soft_max_ext(R(sc), R(mk(S.TYPE_F16, [37, 1])), 0.1, 0.0, R(sc), None) == S.ERR_UNSUPPORTED
+    assert L.shp_soft_max_ext(R(sc), None, 0.1, 0.0, R(mk(S.TYPE_F32, [37, 2, 16])), None) == S.ERR_INVALID_ARG
     strided = (S.ShpTensor * 1)(mk(S.TYPE_F32, [256, 4], nb=[4, 2048, 8192, 8192]))
     assert L.shp_sum_scale_leaky_relu(strided, 1, 1.0, 0.1, None, R(a), None) == S.ERR_UNSUPPORTED
 

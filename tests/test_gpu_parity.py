@@ -364,6 +364,96 @@ def test_qk_norm_rope_generic_head_dim(gpu):
     assert_rope_close(_np(ko), kr, 64)
 
 
+@pytest.mark.parametrize("T,filled,cap,hd,wkind", [(1, 37, 64, 128, "bf16"), (16, 0, 16, 128, "f32"),
+                                                     (5, 10, 32, 64, "f32"), (3, 4, 8, 128, "f16")])
+def test_qk_norm_rope_kv(gpu, T, filled, cap, hd, wkind):
+    """The fused cache write (operations.cpp:98-116): q_out and the cache rows
+    [filled, filled + T) of k equal the unfused qk_norm_rope's outputs bit for
+    bit and the oracle's within the rope bar (and bit-exact against the oracle
+    with correctly rounded cos/sin); v lands in the same rows unchanged; every
+    other cache row keeps its sentinel. hd = 64 takes the generic kernel."""
+    rng = np.random.default_rng(SEED + 3 * T + filled)
+    H, KVH = 16, 8
+    q = rng.standard_normal((T, H, hd)).astype(np.float32)
+    k = rng.standard_normal((T, KVH, hd)).astype(np.float32)
+    v = rng.standard_normal((T, KVH, hd)).astype(np.float32)
+    wq, wt = _weights(rng, hd, wkind)
+    wk, _ = _weights(rng, hd, wkind)
+    pos = (filled + np.arange(T)).astype(np.int32)
+    eps, theta = np.float32(1e-6), np.float32(1e6)
+    sentinel = np.full((cap, KVH, hd), 7.25, np.float32)
+    sentinel[:, :, 1::3] = np.nan
+    kc, vc = _t(gpu, sentinel), _t(gpu, sentinel)
+    qo = gpu.qk_norm_rope_kv(_t(gpu, q), _t(gpu, k), _t(gpu, v), _dev_w(gpu, wq, wkind), _dev_w(gpu, wk, wkind), eps,
+                             _t(gpu, pos), hd, theta, kc, vc, filled)
+    qo, kc, vc = _np(qo), _np(kc), _np(vc)
+    qu, ku = gpu.qk_norm_rope(_t(gpu, q), _t(gpu, k), _dev_w(gpu, wq, wkind), _dev_w(gpu, wk, wkind), eps,
+                              _t(gpu, pos), hd, theta)
+    rows = slice(filled, filled + T)
+    assert_bitexact(qo, _np(qu))
+    assert_bitexact(kc[rows], _np(ku))
+    qr, kr = R.run(lambda g: R.qk_norm_rope(g, q, k, wq, wk, eps, pos, hd, theta, wt))
+    assert_rope_close(qo, qr, hd)
+    assert_rope_close(kc[rows], kr, hd)
+    qcr, kcr = R.run(lambda g: R.qk_norm_rope(g, q, k, wq, wk, eps, pos, hd, theta, wt, cs_rounded=True))
+    assert_bitexact(kc[rows], kcr)
+    assert_bitexact(vc[rows], v)
+    outside = np.ones(cap, bool)
+    outside[rows] = False
+    assert_bitexact(kc[outside], sentinel[outside])
+    assert_bitexact(vc[outside], sentinel[outside])
+
+
+def _ulps_apart(got, ref):
+    g = np.ascontiguousarray(got, np.float32).view(np.int32).astype(np.int64)
+    r = np.ascontiguousarray(ref, np.float32).view(np.int32).astype(np.int64)
+    return np.abs(g - r)
+
+
+@pytest.mark.parametrize("H,T,N,mask", [(16, 1, 37, "none"), (16, 64, 64, "causal"), (4, 7, 2500, "heads2"),
+                                        (3, 5, 64, "rows+"), (2, 3, 1, "none"), (8, 33, 2048, "causal"),
+                                        (2, 2, 4097, "none")])
+def test_soft_max_ext(gpu, H, T, N, mask):
+    """ggml_soft_max_ext with scale 1/sqrt(128): decode rows (1 x 37), a causal
+    prefill, a mask broadcast over 2 heads, a mask with more rows than the
+    scores, a one-element row, and rows past the one-wave kernel (2500, 4097).
+    The kernel's exp is the correctly rounded one and its double sum runs in
+    another order, so: at most 2 ulp from the oracle, and > 99% identical."""
+    rng = np.random.default_rng(SEED + H * T + N)
+    x = (rng.standard_normal((H, T, N)) * 3).astype(np.float32)
+    m = None
+    if mask == "causal":
+        m = np.zeros((T, N), np.float32)
+        m[np.triu_indices(T, N - T + 1, N)] = -np.inf
+    elif mask == "heads2":
+        m = rng.uniform(-5, 0, (2, T, N)).astype(np.float32)
+        m[1, :, :100] = -np.inf
+    elif mask == "rows+":
+        m = rng.uniform(-5, 0, (T + 4, N)).astype(np.float32)
+    scale = np.float32(1.0) / np.sqrt(np.float32(128))
+    ref = R.run(lambda g: g.soft_max_ext(x, m, scale))
+    got = _np(gpu.soft_max_ext(_t(gpu, x), None if m is None else _t(gpu, m), scale))
+    d = _ulps_apart(got, ref)
+    assert d.max() <= 2 and (d == 0).mean() > 0.99
+
+
+def test_soft_max_ext_special_rows(gpu):
+    """A fully masked row (all -inf) and a row holding NaN or +inf come out NaN,
+    as on the CPU; -inf entries next to finite ones give exact zeros."""
+    x = np.zeros((4, 8), np.float32)
+    x[1, 3] = np.nan
+    x[2, 5] = np.inf
+    m = np.zeros((4, 8), np.float32)
+    m[0, :] = -np.inf
+    m[3, :4] = -np.inf
+    with np.errstate(invalid="ignore"):
+        ref = R.run(lambda g: g.soft_max_ext(x, m, np.float32(1.0)))
+    got = _np(gpu.soft_max_ext(_t(gpu, x), _t(gpu, m), 1.0))
+    assert np.isnan(ref[:3]).all() and np.isnan(got[:3]).all()
+    assert_bitexact(got[3], ref[3])
+    assert (got[3, :4] == 0).all()
+
+
 # ---------------------------------------------------------------------------
 # elementwise
 # ---------------------------------------------------------------------------
@@ -591,6 +681,17 @@ class HipOps(R.OracleOps):
         qo, ko = self.g.qk_norm_rope(_t(self.g, q), _t(self.g, k), _t(self.g, wq), _t(self.g, wk), eps,
                                      _t(self.g, pos), n_dims, theta)
         return _np(qo), _np(ko)
+
+    def qk_norm_rope_kv(self, q, k, v, wq, wk, eps, pos, n_dims, theta, cache, filled):
+        kc, vc = _t(self.g, cache["k"]), _t(self.g, cache["v"])
+        qo = self.g.qk_norm_rope_kv(_t(self.g, q), _t(self.g, k), _t(self.g, v), _t(self.g, wq), _t(self.g, wk), eps,
+                                    _t(self.g, pos), n_dims, theta, kc, vc, filled)
+        cache["k"][...] = _np(kc)
+        cache["v"][...] = _np(vc)
+        return _np(qo)
+
+    def soft_max_ext(self, scores, mask, scale):
+        return _np(self.g.soft_max_ext(_t(self.g, scores), None if mask is None else _t(self.g, mask), scale))
 
     def add_rms_norm_w(self, a, b, w, eps):
         s, y = self.g.add_rms_norm_mul(_t(self.g, a), _t(self.g, b), _t(self.g, w), eps)

@@ -353,6 +353,49 @@ def test_branch_average_order_and_invariants():
     np.testing.assert_array_equal(bits(y1), bits(ly))
 
 
+def _softmax_double(w):
+    e = np.exp(w.astype(np.float64) - w.max(axis=-1, keepdims=True))
+    return e / e.sum(axis=-1, keepdims=True)
+
+
+def test_soft_max_closed_form_and_exact_cases():
+    """soft_max_ext against the double softmax of the same f32 w = x*scale + mask:
+    within 3 ulp (one expf, the f32 reciprocal, one multiply). A uniform row
+    gives exactly (float)(1/n); -inf mask entries give exactly 0; every row
+    sums to 1 within n ulp; scaling after adding the mask is planted and fails."""
+    rng = np.random.default_rng(26)
+    H, T, N = 4, 9, 300
+    x = rng.standard_normal((H, T, N)).astype(np.float32) * 4
+    mask = rng.uniform(-3, 0, (T, N)).astype(np.float32)
+    mask[:, -50:] = -np.inf
+    scale = np.float32(1.0) / np.sqrt(np.float32(128))
+    y = R.run(lambda g: g.soft_max_ext(x, mask, scale))
+    w = x * scale + mask
+    ref = _softmax_double(w)
+    assert (np.abs(y - ref) <= 3 * ULP * ref + 1e-45).all()
+    assert (y[..., -50:] == 0).all()
+    assert np.abs(y.astype(np.float64).sum(-1) - 1).max() <= N * ULP
+    wrong = _softmax_double((x + mask) * scale)
+    assert not (np.abs(y - wrong) <= 3 * ULP * wrong + 1e-45).all()
+    u = R.run(lambda g: g.soft_max_ext(np.full((2, 37), 0.3, np.float32), None, np.float32(1.0)))
+    assert (u == np.float32(1.0 / 37)).all()
+
+
+def test_soft_max_mask_head_broadcast():
+    """Head h reads mask head h % mask_heads (ggml's i12 = i02 % ne12) and score
+    row i1 reads mask row i1 (the mask may have more rows)."""
+    rng = np.random.default_rng(27)
+    H, T, N = 6, 5, 40
+    x = rng.standard_normal((H, T, N)).astype(np.float32)
+    mask = rng.uniform(-4, 0, (2, T + 3, N)).astype(np.float32)
+    y = R.run(lambda g: g.soft_max_ext(x, mask, np.float32(0.5)))
+    for h in range(H):
+        one = R.run(lambda g: g.soft_max_ext(x[h], mask[h % 2, :T], np.float32(0.5)))
+        np.testing.assert_array_equal(bits(y[h]), bits(one))
+    other = R.run(lambda g: g.soft_max_ext(x[1], mask[0, :T], np.float32(0.5)))
+    assert (bits(y[1]) != bits(other)).any()
+
+
 def test_leaky_relu_signed_zero_and_nan():
     x = np.array([[-0.0, 0.0, np.nan, -np.nan, np.inf, -np.inf, -1e-45, 2.5, -2.5, -3e-39]], np.float32)
     y = R.run(lambda g: g.leaky_relu(x, np.float32(0.1)))[0]
