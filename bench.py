@@ -470,6 +470,46 @@ def suite(args, S, torch):
         qk_case("cfg5", 64, 8192)
         swiglu_case("cfg5", 64, 3072)
 
+    if on("gguf"):
+        # A package's lookup tables streamed file -> HBM by shp_gguf_load_tensor
+        # (page cache warm after the first pass): the BF16 text embedding of
+        # configs[1] and the 16 Q8_0 codebooks of configs[2].
+        import tempfile
+        import time
+        import numpy as np
+        import formats as F
+        from gguf_write import write_gguf
+        rng = np.random.default_rng(SEED + 5)
+        with tempfile.TemporaryDirectory() as tmp:
+            path = os.path.join(tmp, "tables.gguf")
+            bf = F.f32_to_bf16_bits(rng.standard_normal((151936, 2048), dtype=np.float32) * 0.02)
+            q8 = F.q8_0_synthetic(rng, 2048, 1024)
+            tensors = [("talker.model.text_embedding.weight", 30, [2048, 151936], bf.tobytes())]
+            del bf
+            tensors += [("talker.code_predictor.model.codec_embedding.%d.weight" % k, 8, [1024, 2048],
+                         q8.tobytes()) for k in range(16)]
+            write_gguf(path, tensors)
+            del tensors
+            with S.GgufFile(path) as f:
+                for label, names in (("gguf load BF16 [2048,151936] file->HBM", ["talker.model.text_embedding.weight"]),
+                                     ("gguf load 16 x Q8_0 [1024,2048] file->HBM",
+                                      ["talker.code_predictor.model.codec_embedding.%d.weight" % k
+                                       for k in range(16)])):
+                    nbytes = sum(f.info(n)[1] for n in names)
+                    best = None
+                    for _ in range(3):
+                        torch.cuda.synchronize()
+                        t0 = time.perf_counter()
+                        out = [f.load(n) for n in names]
+                        torch.cuda.synchronize()
+                        dt = time.perf_counter() - t0
+                        best = dt if best is None else min(best, dt)
+                        del out
+                    gbs = nbytes / best / 1e9
+                    rows.append({"config": "gguf", "op": label, "bytes": nbytes, "us": round(best * 1e6, 1),
+                                 "GB/s": round(gbs, 2), "note": "page cache warm; PCIe host->device bound"})
+                    print("gguf  %-44s %12d B %11.1f us %8.2f GB/s" % (label, nbytes, best * 1e6, gbs), flush=True)
+
     with open(args.suite, "w") as f:
         json.dump({"peak_GBps": PEAK_GBS, "cold_bytes": COLD_BYTES, "rows": rows}, f, indent=1)
 

@@ -78,6 +78,23 @@ def load(path=None):
         fn = getattr(L, name)
         fn.argtypes = args
         fn.restype = ctypes.c_int32
+    vpp, u64p = ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_uint64)
+    gsigs = {
+        "shp_gguf_open": ([ctypes.c_char_p, vpp], ctypes.c_int32),
+        "shp_gguf_close": ([vp], None),
+        "shp_gguf_version": ([vp], ctypes.c_uint32),
+        "shp_gguf_tensor_count": ([vp], ctypes.c_int64),
+        "shp_gguf_tensor_name": ([vp, ctypes.c_int64], ctypes.c_char_p),
+        "shp_gguf_tensor_info": ([vp, ctypes.c_char_p, _PT, u64p, u64p], ctypes.c_int32),
+        "shp_gguf_kv_u32": ([vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32)], ctypes.c_int32),
+        "shp_gguf_kv_string": ([vp, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t], ctypes.c_int32),
+        "shp_gguf_load_tensor": ([vp, ctypes.c_char_p, vp, ctypes.c_size_t, _PT, vp], ctypes.c_int32),
+        "shp_table_type_for_profile": ([ctypes.c_char_p, ctypes.POINTER(ctypes.c_int32)], ctypes.c_int32),
+    }
+    for name, (args, res) in gsigs.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
     L.shp_abi_version.restype = ctypes.c_uint32
     L.shp_abi_version.argtypes = []
     L.shp_status_string.restype = ctypes.c_char_p
@@ -340,3 +357,87 @@ def add(a, b, out=None):
     out = a.new_empty(a.shape) if out is None else out
     _check(load().shp_add(_ref(desc(a)), _ref(desc(b)), _ref(desc(out)), _stream()), "add")
     return out
+
+
+# ---------------------------------------------------------------------------
+# GGUF packages (include/synth_gguf.h)
+# ---------------------------------------------------------------------------
+
+class GgufFile:
+    """A GGUF package opened by libsynth_hip's reader. info() and the metadata
+    getters run host code only; load() streams a tensor into a new device
+    buffer and returns it as a torch tensor (or Q8Tensor) the gathers take."""
+
+    def __init__(self, path):
+        self._h = ctypes.c_void_p()
+        _check(load().shp_gguf_open(os.fsencode(path), ctypes.byref(self._h)), "gguf_open")
+
+    def close(self):
+        if self._h:
+            load().shp_gguf_close(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def version(self):
+        return int(load().shp_gguf_version(self._h))
+
+    def tensor_names(self):
+        L = load()
+        # names are UTF-8 by the format; undecodable bytes round-trip through surrogateescape
+        return [L.shp_gguf_tensor_name(self._h, i).decode("utf-8", "surrogateescape")
+                for i in range(L.shp_gguf_tensor_count(self._h))]
+
+    def info(self, name):
+        """(shp_tensor with data NULL, nbytes, absolute file offset)."""
+        d, nbytes, off = ShpTensor(), ctypes.c_uint64(), ctypes.c_uint64()
+        _check(load().shp_gguf_tensor_info(self._h, name.encode("utf-8", "surrogateescape"), ctypes.byref(d),
+                                           ctypes.byref(nbytes),
+                                           ctypes.byref(off)), "gguf_tensor_info")
+        return d, int(nbytes.value), int(off.value)
+
+    def kv_u32(self, key):
+        v = ctypes.c_uint32()
+        _check(load().shp_gguf_kv_u32(self._h, key.encode(), ctypes.byref(v)), "gguf_kv_u32")
+        return int(v.value)
+
+    def kv_string(self, key, capacity=4096):
+        buf = ctypes.create_string_buffer(capacity)
+        _check(load().shp_gguf_kv_string(self._h, key.encode(), buf, capacity), "gguf_kv_string")
+        return buf.value.decode()
+
+    def load(self, name, device="cuda"):
+        import torch
+        d, nbytes, _ = self.info(name)
+        raw = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        out = ShpTensor()
+        _check(load().shp_gguf_load_tensor(self._h, name.encode("utf-8", "surrogateescape"),
+                                           ctypes.c_void_p(raw.data_ptr()), nbytes,
+                                           ctypes.byref(out), _stream()), "gguf_load_tensor")
+        ne = [int(out.ne[k]) for k in range(4)]
+        nd = max([k + 1 for k in range(4) if ne[k] != 1] or [1])
+        if out.type == TYPE_Q8_0:
+            rows = ne[1] * ne[2] * ne[3]
+            return Q8Tensor(raw.view(rows, ne[0] // Q8_0_BLOCK_ELEMS * Q8_0_BLOCK_BYTES), ne[0])
+        dt = {TYPE_F32: torch.float32, TYPE_F16: torch.float16, TYPE_BF16: torch.bfloat16,
+              TYPE_I32: torch.int32}[out.type]
+        return raw.view(dt).view(tuple(reversed(ne[:nd])))
+
+
+def table_type_for_profile(profile):
+    """The table type the catalog requires under a quantization profile (raises
+    ShpError(ERR_UNSUPPORTED) for a k-quant profile)."""
+    t = ctypes.c_int32()
+    _check(load().shp_table_type_for_profile(profile.encode(), ctypes.byref(t)), "table_type_for_profile")
+    return int(t.value)

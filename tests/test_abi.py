@@ -10,11 +10,11 @@ import pytest
 import synth_hip as S
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "synth_hip.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("synth_hip.h", "synth_gguf.h")]
 
 
 def declared_symbols():
-    text = open(HEADER).read()
+    text = "".join(open(h).read() for h in HEADERS)
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(shp_[a-z0-9_]+)\s*\(", text)))
 
@@ -22,7 +22,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = S.load()
     names = declared_symbols()
-    assert len(names) >= 13
+    assert len(names) >= 30
     for name in names:
         assert hasattr(lib, name), name
 
