@@ -8,20 +8,24 @@
 //   v_i  = exp(w_i - m)                  (f32 difference, exp rounded to f32)
 //   sum  = sum_i (double) v_i            (double)
 //   y_i  = v_i * (float)(1/sum)          (the reciprocal in double, rounded to f32)
-// The exp is the double exp rounded once to f32, which is glibc's expf except
-// within ~2^-52 of a rounding boundary; the double sum is added in a
+// The exp is shp_expf.hpp's table-driven exp, within ~2^-44 before its f32
+// rounding: it differs from the correctly rounded exp on 19 of the 2^32 f32
+// inputs, glibc's expf (the CPU's) on 170,648. The double sum is added in a
 // different order than the CPU's loop, which moves the f32 reciprocal only
 // when the sum lies within ~1e-16 of a rounding boundary. A row holding a NaN
 // or +inf (or only -inf) comes out NaN, as on the CPU: the max is then NaN or
 // inf, or the NaN reaches the sum.
 //
-// Launch shapes: rows up to 2048 wide take one wave per row with the row in
-// registers (K elements per lane, wave-level reductions only: no LDS, no
-// barrier), which is what the decode step's few short rows need; wider rows
-// take one 256-thread block per row and three passes over the row.
+// Launch shapes: rows up to 2048 wide are held in registers. With float4
+// rows, a row takes one wave (wave-level reductions only: no LDS, no barrier)
+// when there are enough rows to fill the chip, else 2 or 4 waves (the decode
+// step's 16 rows of ~512, a short prefill's 1024 rows of 2048); other rows
+// take one wave each with scalar accesses. Wider rows take one 256-thread
+// block per row and three passes over the row.
 
 #include <cmath>
 
+#include "shp_expf.hpp"
 #include "shp_internal.hpp"
 
 namespace shp {
@@ -48,8 +52,25 @@ struct SoftMaxArgs {
 constexpr int kSoftMaxWaveMax = 2048;  // widest row of the one-wave kernel
 constexpr int kSoftMaxBlock   = 256;
 
+// exp through the wave's own LDS copy of kExpTable (one ds_read_b64 per
+// lookup; measured ~3% faster on the softmax than reading the table from
+// memory or shuffling a per-lane entry).
+__device__ __forceinline__ float exp_f32_lds(float x, const double * tab) {
+    return exp_f32_rn(x, [tab](int j) { return tab[j]; });
+}
+
+// Fills the calling wave's 64-entry table (lane l writes entry l) and makes it
+// visible to the whole wave.
+__device__ __forceinline__ const double * wave_exp_table(double (*s_tab)[64], int lane) {
+    double * t = s_tab[threadIdx.x / kWave];
+    t[lane]    = kExpTable[lane];
+    __syncwarp();
+    return t;
+}
+
+// exp with the table read from memory (divergent loops).
 __device__ __forceinline__ float exp_f32(float x) {
-    return static_cast<float>(exp(static_cast<double>(x)));
+    return exp_f32_rn(x, [](int j) { return kExpTable[j]; });
 }
 
 // Mask row of score row r = (i1, i2, i3): ggml's i11 = i1, i12 = i2 % ne12,
@@ -73,6 +94,7 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // One wave per row, element lane + 64k in register k (k < K, 64K >= ne0).
 template <int K, bool MASK> __global__ __launch_bounds__(256) void k_soft_max_wave(const SoftMaxArgs a) {
+    __shared__ double s_tab[256 / kWave][64];
     const int     lane = threadIdx.x % kWave;
     const int64_t r    = static_cast<int64_t>(blockIdx.x) * (256 / kWave) + threadIdx.x / kWave;
     if (r >= a.nrows) {
@@ -89,6 +111,7 @@ template <int K, bool MASK> __global__ __launch_bounds__(256) void k_soft_max_wa
         w[k]        = i < a.ne0 ? xr[i] : 0.0f;
         mk[k]       = MASK && i < a.ne0 ? mr[i] : 0.0f;
     }
+    const double * tab = wave_exp_table(s_tab, lane);
     float mx = -INFINITY;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -104,7 +127,7 @@ template <int K, bool MASK> __global__ __launch_bounds__(256) void k_soft_max_wa
 #pragma unroll
     for (int k = 0; k < K; ++k) {
         const int i = lane + kWave * k;
-        w[k]        = exp_f32(w[k] - mx);
+        w[k]        = exp_f32_lds(w[k] - mx, tab);
         sum += i < a.ne0 ? static_cast<double>(w[k]) : 0.0;
     }
     sum             = group_sum<kWave>(sum);
@@ -114,6 +137,95 @@ template <int K, bool MASK> __global__ __launch_bounds__(256) void k_soft_max_wa
         const int i = lane + kWave * k;
         if (i < a.ne0) {
             yr[i] = w[k] * inv;
+        }
+    }
+}
+
+// float4 rows (16-byte aligned rows, ne0 % 4 == 0), WPR waves per row: lane q
+// of the row's 64*WPR lanes holds chunks q + 64*WPR*k in registers k (k < K4).
+// WPR > 1 spreads the few long rows of a decode or short prefill over more
+// waves; the row's waves then combine their max and sum through LDS, in wave
+// order.
+template <int WPR, int K4, bool MASK> __global__ __launch_bounds__(256) void k_soft_max_rows4(const SoftMaxArgs a) {
+    constexpr int kLanes = kWave * WPR;
+    __shared__ float  s_max[256 / kWave];
+    __shared__ double s_sum[256 / kWave];
+    __shared__ double s_tab[256 / kWave][64];
+    const int     lane = threadIdx.x % kWave;
+    const int     q    = threadIdx.x % kLanes;
+    const int     slot = threadIdx.x / kLanes;  // row of this block
+    const int     wv   = threadIdx.x / kWave;
+    const int64_t r    = static_cast<int64_t>(blockIdx.x) * (256 / kLanes) + slot;
+    const bool    live = r < a.nrows;
+    if (WPR == 1 && !live) {
+        return;  // whole wave; the one-wave form has no barrier
+    }
+    const int64_t rr = live ? r : 0;
+    const f32x4 * xr =
+        reinterpret_cast<const f32x4 *>(reinterpret_cast<const char *>(a.x) + row_offset(a.xm, rr));
+    f32x4 *       yr    = reinterpret_cast<f32x4 *>(reinterpret_cast<char *>(a.y) + row_offset(a.ym, rr));
+    const f32x4 * mr    = MASK ? reinterpret_cast<const f32x4 *>(mask_row(a, rr)) : nullptr;
+    const int     n4 = live ? a.ne0 / 4 : 0;
+    f32x4         w[K4];
+    f32x4         mk[K4];
+#pragma unroll
+    for (int k = 0; k < K4; ++k) {
+        const int c = q + kLanes * k;
+        w[k]        = c < n4 ? xr[c] : splat4(0.0f);
+        mk[k]       = MASK && c < n4 ? mr[c] : splat4(0.0f);
+    }
+    const double * tab = wave_exp_table(s_tab, lane);
+    float          mx  = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < K4; ++k) {
+        const int c = q + kLanes * k;
+        w[k]        = f32x4{ w[k].x * a.scale, w[k].y * a.scale, w[k].z * a.scale, w[k].w * a.scale };
+        if constexpr (MASK) {
+            w[k] = f32x4{ w[k].x + mk[k].x, w[k].y + mk[k].y, w[k].z + mk[k].z, w[k].w + mk[k].w };
+        }
+        const float m4 = fmaxf(fmaxf(w[k].x, w[k].y), fmaxf(w[k].z, w[k].w));
+        mx             = c < n4 ? fmaxf(mx, m4) : mx;
+    }
+    mx = wave_max(mx);
+    if constexpr (WPR > 1) {
+        if (lane == 0) {
+            s_max[wv] = mx;
+        }
+        __syncthreads();
+        mx = s_max[slot * WPR];
+#pragma unroll
+        for (int j = 1; j < WPR; ++j) {
+            mx = fmaxf(mx, s_max[slot * WPR + j]);
+        }
+    }
+    double sum = 0.0;
+#pragma unroll
+    for (int k = 0; k < K4; ++k) {
+        const int c = q + kLanes * k;
+        w[k] = f32x4{ exp_f32_lds(w[k].x - mx, tab), exp_f32_lds(w[k].y - mx, tab), exp_f32_lds(w[k].z - mx, tab),
+                      exp_f32_lds(w[k].w - mx, tab) };
+        const double s4 = (static_cast<double>(w[k].x) + static_cast<double>(w[k].y)) +
+                          (static_cast<double>(w[k].z) + static_cast<double>(w[k].w));
+        sum += c < n4 ? s4 : 0.0;
+    }
+    sum = group_sum<kWave>(sum);
+    if constexpr (WPR > 1) {
+        if (lane == 0) {
+            s_sum[wv] = sum;
+        }
+        __syncthreads();
+        sum = s_sum[slot * WPR];
+#pragma unroll
+        for (int j = 1; j < WPR; ++j) {
+            sum += s_sum[slot * WPR + j];
+        }
+    }
+    const float inv = static_cast<float>(1.0 / sum);
+#pragma unroll
+    for (int k = 0; k < K4; ++k) {
+        const int c = q + kLanes * k;
+        if (c < n4) {
+            yr[c] = f32x4{ w[k].x * inv, w[k].y * inv, w[k].z * inv, w[k].w * inv };
         }
     }
 }
@@ -172,14 +284,45 @@ template <bool MASK> __global__ __launch_bounds__(kSoftMaxBlock) void k_soft_max
     }
 }
 
-template <bool MASK> shp_status_t launch_soft_max(const SoftMaxArgs & a, hipStream_t stream) {
+template <bool MASK> shp_status_t launch_soft_max(const SoftMaxArgs & a, bool vec, hipStream_t stream) {
     if (a.ne0 > kSoftMaxWaveMax) {
         hipLaunchKernelGGL((k_soft_max_block<MASK>), dim3(static_cast<unsigned>(a.nrows)), dim3(kSoftMaxBlock), 0,
                            stream, a);
         return launch_status();
     }
     const dim3 grid(static_cast<unsigned>((a.nrows + 3) / 4));
-    const int  k = (a.ne0 + kWave - 1) / kWave;
+    if (vec) {
+        // Few rows (under 8 waves per CU at one wave per row): 2 or 4 waves per row.
+        const int n4  = a.ne0 / 4;
+        const int wpr = a.nrows >= 2048 ? 1 : (n4 >= 256 ? 4 : (n4 >= 128 ? 2 : 1));
+        const int k4  = (n4 + kWave * wpr - 1) / (kWave * wpr);
+        const dim3 g4(static_cast<unsigned>((a.nrows * wpr + 3) / 4));
+        if (wpr == 4) {
+            if (k4 <= 1) {
+                hipLaunchKernelGGL((k_soft_max_rows4<4, 1, MASK>), g4, dim3(256), 0, stream, a);
+            } else {
+                hipLaunchKernelGGL((k_soft_max_rows4<4, 2, MASK>), g4, dim3(256), 0, stream, a);
+            }
+        } else if (wpr == 2) {
+            if (k4 <= 1) {
+                hipLaunchKernelGGL((k_soft_max_rows4<2, 1, MASK>), g4, dim3(256), 0, stream, a);
+            } else if (k4 <= 2) {
+                hipLaunchKernelGGL((k_soft_max_rows4<2, 2, MASK>), g4, dim3(256), 0, stream, a);
+            } else {
+                hipLaunchKernelGGL((k_soft_max_rows4<2, 4, MASK>), g4, dim3(256), 0, stream, a);
+            }
+        } else if (k4 <= 1) {
+            hipLaunchKernelGGL((k_soft_max_rows4<1, 1, MASK>), g4, dim3(256), 0, stream, a);
+        } else if (k4 <= 2) {
+            hipLaunchKernelGGL((k_soft_max_rows4<1, 2, MASK>), g4, dim3(256), 0, stream, a);
+        } else if (k4 <= 4) {
+            hipLaunchKernelGGL((k_soft_max_rows4<1, 4, MASK>), g4, dim3(256), 0, stream, a);
+        } else {
+            hipLaunchKernelGGL((k_soft_max_rows4<1, 8, MASK>), g4, dim3(256), 0, stream, a);
+        }
+        return launch_status();
+    }
+    const int k = (a.ne0 + kWave - 1) / kWave;
     if (k <= 1) {
         hipLaunchKernelGGL((k_soft_max_wave<1, MASK>), grid, dim3(256), 0, stream, a);
     } else if (k <= 2) {
@@ -242,7 +385,11 @@ extern "C" shp_status_t shp_soft_max_ext(const shp_tensor * a,
         g.mnb3 = static_cast<int64_t>(mask->nb[3]);
         g.mne2 = mask->ne[2];
         g.mne3 = mask->ne[3];
-        return launch_soft_max<true>(g, as_stream(stream));
     }
-    return launch_soft_max<false>(g, as_stream(stream));
+    // float4 rows: every row start of the scores, the output and the mask
+    // 16-byte aligned and whole float4s per row
+    const bool vec = a->ne[0] % 4 == 0 && rows_aligned(*a, 16) && rows_aligned(*y, 16) &&
+                     (mask == nullptr || rows_aligned(*mask, 16));
+    return mask != nullptr ? launch_soft_max<true>(g, vec, as_stream(stream))
+                           : launch_soft_max<false>(g, vec, as_stream(stream));
 }

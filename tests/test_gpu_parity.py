@@ -412,11 +412,14 @@ def _ulps_apart(got, ref):
 
 @pytest.mark.parametrize("H,T,N,mask", [(16, 1, 37, "none"), (16, 64, 64, "causal"), (4, 7, 2500, "heads2"),
                                         (3, 5, 64, "rows+"), (2, 3, 1, "none"), (8, 33, 2048, "causal"),
-                                        (2, 2, 4097, "none")])
+                                        (2, 2, 4097, "none"), (16, 1, 512, "none"), (3, 1, 512, "rows+"),
+                                        (6, 3, 1024, "heads2"), (16, 512, 512, "causal")])
 def test_soft_max_ext(gpu, H, T, N, mask):
-    """ggml_soft_max_ext with scale 1/sqrt(128): decode rows (1 x 37), a causal
-    prefill, a mask broadcast over 2 heads, a mask with more rows than the
-    scores, a one-element row, and rows past the one-wave kernel (2500, 4097).
+    """ggml_soft_max_ext with scale 1/sqrt(128): decode rows (1 x 37, 1 x 512),
+    causal prefills, a mask broadcast over 2 heads, a mask with more rows than
+    the scores, a one-element row, rows spread over 2 waves (512 wide; 3 rows
+    leave the last block half empty) and 4 waves (1024, 2048 wide), and rows
+    past the register kernels (2500, 4097).
     The kernel's exp is the correctly rounded one and its double sum runs in
     another order, so: at most 2 ulp from the oracle, and > 99% identical."""
     rng = np.random.default_rng(SEED + H * T + N)

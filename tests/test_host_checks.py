@@ -10,6 +10,9 @@
   device's Newton steps give that reciprocal.
 - sinf_check: Snake's branch-free sine (shp_sinf.hpp) is within 1 ulp of the
   correctly rounded sine over its whole range.
+- expf_check: the table-driven exp of the softmax, SnakeBeta and ggml_exp
+  (shp_expf.hpp) against the double exp rounded once, over all 2^32 f32 inputs
+  (multi-threaded, ~30 s on 8 cores).
 """
 import os
 import subprocess
@@ -23,8 +26,8 @@ CSRC = os.path.join(os.path.dirname(HERE), "synthesize.cpp_amd", "csrc")
 def _build_and_run(tmp_path, name):
     exe = tmp_path / name
     subprocess.run(["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", "-ffp-contract=off", "-I" + CSRC, "-o", str(exe),
-                    os.path.join(HERE, "host", name + ".cpp"), "-lm"], check=True)
-    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+                    os.path.join(HERE, "host", name + ".cpp"), "-lm", "-pthread"], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=600)
     return r.returncode, r.stdout
 
 
@@ -49,3 +52,11 @@ def test_snake_fast_sine_within_one_ulp(tmp_path):
     rc, out = _build_and_run(tmp_path, "sinf_check")
     tested, worst, _exact, _glibc = out.split()[-4:]
     assert rc == 0 and int(tested) > 8 * 10 ** 6 and float(worst) <= 1.0, out
+
+
+def test_table_exp_matches_the_rounded_double_exp_on_every_input(tmp_path):
+    """At most 1 ulp anywhere, NaN kept, and mismatches on at most 1 input in
+    10^6 (measured: 19 of 4,294,967,296; glibc's expf: 170,648)."""
+    rc, out = _build_and_run(tmp_path, "expf_check")
+    inputs, mismatches, max_ulp, _glibc = map(int, out.split()[-4:])
+    assert rc == 0 and inputs == 2 ** 32 and max_ulp <= 1 and mismatches <= 100, out
