@@ -196,6 +196,33 @@ shp_status_t shp_qk_norm_rope_kv(const shp_tensor * q,
                                  shp_stream_t       stream);
 
 /*
+ * shp_qk_norm_rope_kv with the cache slot in device memory, so that one
+ * captured HIP graph of a decode step can be replayed step after step (the
+ * reference rebuilds its graph every step, src/arch/qwen3-tts/model.cpp:1311,
+ * 1437): slot is an I32 tensor of one element holding `filled`, read by the
+ * kernel when it runs. If slot < 0 or slot + T > the caches' rows, no cache
+ * row is written (q_out still is) and, when status (an I32 tensor of one
+ * element, or NULL) is given, *status is set to 1; the library never clears
+ * it. k_cache and v_cache as in shp_qk_norm_rope_kv, with at least T rows.
+ */
+shp_status_t shp_qk_norm_rope_kv_at(const shp_tensor * q,
+                                    const shp_tensor * k,
+                                    const shp_tensor * v,
+                                    const shp_tensor * wq,
+                                    const shp_tensor * wk,
+                                    float              eps,
+                                    const shp_tensor * pos,
+                                    int32_t            n_dims,
+                                    float              freq_base,
+                                    float              freq_scale,
+                                    shp_tensor *       q_out,
+                                    shp_tensor *       k_cache,
+                                    shp_tensor *       v_cache,
+                                    const shp_tensor * slot,
+                                    shp_tensor *       status,
+                                    shp_stream_t       stream);
+
+/*
  * ggml_silu(g) followed by ggml_mul(., u): the SwiGLU of
  * src/arch/qwen3-tts/operations.cpp:39-41 (== ggml_swiglu_split(g, u)).
  * y = (g / (1 + expf(-g))) * u in f32. g, u, y F32 of one shape.

@@ -382,6 +382,9 @@ struct RopePart {
 struct RopeArgs {
     RopePart        part[3];  // q, k, then v (heads == 0 when absent); v rows are copied unchanged
     const int32_t * pos;
+    const int32_t * slot;     // KV launches: first cache row from device memory, or null (then 0)
+    int32_t *       status;   // with `slot`: set to 1 when the rows do not fit the cache (none written)
+    int64_t         cap;      // with `slot`: cache rows
     int64_t         npos;
     int32_t         ne0;
     int32_t         n_dims;
@@ -400,10 +403,13 @@ struct RowRef {
     const float * x;
     float *       y;
     const void *  w;
-    bool          copy;
+    bool          copy;  // a v row: stored unchanged
+    bool          kv;    // a k or v row: lands in the cache
 };
 
-template <bool KV> __device__ __forceinline__ RowRef rope_row(const RopeArgs & a, int hh, int64_t pi) {
+// slot: the KV launches' first cache row (k and v output rows only).
+template <bool KV>
+__device__ __forceinline__ RowRef rope_row(const RopeArgs & a, int hh, int64_t pi, int64_t slot = 0) {
     const RopePart & q   = a.part[0];
     const RopePart & k   = a.part[1];
     const RopePart & v   = a.part[2];
@@ -411,12 +417,34 @@ template <bool KV> __device__ __forceinline__ RowRef rope_row(const RopeArgs & a
     const bool       isv = KV && hh >= qk;
     const bool       isk = !isv && hh >= q.heads;
     const int64_t    h   = isv ? hh - qk : (isk ? hh - q.heads : hh);
+    const int64_t    py  = KV && (isk || isv) ? pi + slot : pi;
     const char *     xb  = reinterpret_cast<const char *>(isv ? v.x : (isk ? k.x : q.x));
     char *           yb  = reinterpret_cast<char *>(isv ? v.y : (isk ? k.y : q.y));
     const int64_t    xo  = h * (isv ? v.xnb1 : (isk ? k.xnb1 : q.xnb1)) + pi * (isv ? v.xnb2 : (isk ? k.xnb2 : q.xnb2));
-    const int64_t    yo  = h * (isv ? v.ynb1 : (isk ? k.ynb1 : q.ynb1)) + pi * (isv ? v.ynb2 : (isk ? k.ynb2 : q.ynb2));
+    const int64_t    yo  = h * (isv ? v.ynb1 : (isk ? k.ynb1 : q.ynb1)) + py * (isv ? v.ynb2 : (isk ? k.ynb2 : q.ynb2));
     return RowRef{ reinterpret_cast<const float *>(xb + xo), reinterpret_cast<float *>(yb + yo),
-                   isv ? nullptr : (isk ? k.w : q.w), isv };
+                   isv ? nullptr : (isk ? k.w : q.w), isv, isk || isv };
+}
+
+// The KV launches' cache slot: 0 without a device slot; with one, its value,
+// or -1 when the T rows from it do not fit the cache (block 0 then raises
+// *status; no cache row is written).
+template <bool KV> __device__ __forceinline__ int64_t rope_slot(const RopeArgs & a) {
+    if constexpr (!KV) {
+        return 0;
+    } else {
+        if (a.slot == nullptr) {
+            return 0;
+        }
+        const int64_t sl = *a.slot;
+        if (sl >= 0 && sl <= a.cap - a.npos) {
+            return sl;
+        }
+        if (blockIdx.x == 0 && threadIdx.x == 0 && a.status != nullptr) {
+            *a.status = 1;
+        }
+        return -1;
+    }
 }
 
 template <bool KV> __device__ __forceinline__ int rope_rows(const RopeArgs & a) {
@@ -474,8 +502,9 @@ template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(1024) void k_
     const int     l     = threadIdx.x % kRopeLanes;
 
     // 1. this lane's first row, and its gains (both issued before any wait)
-    const bool live = g < total;
-    RowRef     r    = rope_row<KV>(a, live ? g : 0, pi);
+    const bool    live = g < total;
+    const int64_t slot = rope_slot<KV>(a);  // -1: cache rows skipped
+    RowRef        r    = rope_row<KV>(a, live ? g : 0, pi, slot);
     f32x4      lo   = splat4(0.0f);
     f32x4      hi   = splat4(0.0f);
     if (live) {
@@ -515,7 +544,7 @@ template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(1024) void k_
     //    64 heads) are loaded here
     for (int row = g; row < total; row += slots) {
         if (row != g) {
-            r  = rope_row<KV>(a, row, pi);
+            r  = rope_row<KV>(a, row, pi, slot);
             lo = ld_stream(reinterpret_cast<const f32x4 *>(r.x) + l);
             hi = ld_stream(reinterpret_cast<const f32x4 *>(r.x + 64) + l);
             if constexpr (NORM && WT != kWNone) {
@@ -545,8 +574,10 @@ template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(1024) void k_
         const f32x4 ohi{ lo.x * sn.x + hi.x * cs.x, lo.y * sn.y + hi.y * cs.y, lo.z * sn.z + hi.z * cs.z,
                          lo.w * sn.w + hi.w * cs.w };
         // a v row (whole 16-lane group) stores its input unchanged
-        st_stream(reinterpret_cast<f32x4 *>(r.y) + l, KV && r.copy ? rawlo : olo);
-        st_stream(reinterpret_cast<f32x4 *>(r.y + 64) + l, KV && r.copy ? rawhi : ohi);
+        if (!KV || slot >= 0 || !r.kv) {
+            st_stream(reinterpret_cast<f32x4 *>(r.y) + l, KV && r.copy ? rawlo : olo);
+            st_stream(reinterpret_cast<f32x4 *>(r.y + 64) + l, KV && r.copy ? rawhi : ohi);
+        }
     }
 }
 
@@ -559,11 +590,15 @@ template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(256) void k_r
     if (row >= a.npos * total) {
         return;
     }
-    const int64_t pi = row / total;
-    const int     hh = static_cast<int>(row % total);
-    const RowRef  rr = rope_row<KV>(a, hh, pi);
-    const float * xr = rr.x;
-    float *       yr = rr.y;
+    const int64_t pi   = row / total;
+    const int     hh   = static_cast<int>(row % total);
+    const int64_t slot = rope_slot<KV>(a);
+    const RowRef  rr   = rope_row<KV>(a, hh, pi, slot);
+    const float * xr   = rr.x;
+    float *       yr   = rr.y;
+    if (KV && rr.kv && slot < 0) {
+        return;  // the rows do not fit the cache: nothing written
+    }
     if (KV && rr.copy) {  // a v row: the cache write, a plain copy (ggml_cpy F32 -> F32)
         for (int i = lane; i < a.ne0; i += kWave) {
             yr[i] = xr[i];
@@ -666,7 +701,10 @@ shp_status_t rope_entry(const shp_tensor * q,
                         shp_tensor *       q_out,
                         shp_tensor *       k_out,
                         shp_tensor *       v_out,
-                        shp_stream_t       stream) {
+                        shp_stream_t       stream,
+                        const int32_t *    slot   = nullptr,
+                        int32_t *          status = nullptr,
+                        int64_t            cap    = 0) {
     if (!rope_part_ok(q, q_out) || !well_formed(pos) || pos->type != SHP_TYPE_I32) {
         return SHP_ERR_INVALID_ARG;
     }
@@ -742,6 +780,9 @@ shp_status_t rope_entry(const shp_tensor * q,
         a.part[2].heads = 0;
     }
     a.pos         = static_cast<const int32_t *>(pos->data);
+    a.slot        = slot;
+    a.status      = status;
+    a.cap         = cap;
     a.npos        = q->ne[2];
     a.ne0         = static_cast<int32_t>(q->ne[0]);
     a.n_dims      = n_dims;
@@ -868,4 +909,37 @@ extern "C" shp_status_t shp_qk_norm_rope_kv(const shp_tensor * q,
     }
     return shp::rope_entry(q, k, v, wq, wk, true, eps, pos, n_dims, freq_base, freq_scale, 1.0f, q_out, &kview,
                            &vview, stream);
+}
+
+extern "C" shp_status_t shp_qk_norm_rope_kv_at(const shp_tensor * q,
+                                               const shp_tensor * k,
+                                               const shp_tensor * v,
+                                               const shp_tensor * wq,
+                                               const shp_tensor * wk,
+                                               float              eps,
+                                               const shp_tensor * pos,
+                                               int32_t            n_dims,
+                                               float              freq_base,
+                                               float              freq_scale,
+                                               shp_tensor *       q_out,
+                                               shp_tensor *       k_cache,
+                                               shp_tensor *       v_cache,
+                                               const shp_tensor * slot,
+                                               shp_tensor *       status,
+                                               shp_stream_t       stream) {
+    if (!shp::well_formed(k) || !shp::well_formed(v) || k_cache == nullptr || v_cache == nullptr ||
+        !shp::well_formed(slot) || slot->type != SHP_TYPE_I32 || shp::nelements(*slot) != 1 ||
+        (status != nullptr && (!shp::well_formed(status) || status->type != SHP_TYPE_I32 ||
+                               shp::nelements(*status) != 1))) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    // The views start at row 0 and must fit T rows; the device slot moves them.
+    shp_tensor kview{}, vview{};
+    if (!shp::cache_view(k_cache, k, 0, kview) || !shp::cache_view(v_cache, v, 0, vview)) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    const int64_t cap = k_cache->ne[2] < v_cache->ne[2] ? k_cache->ne[2] : v_cache->ne[2];
+    return shp::rope_entry(q, k, v, wq, wk, true, eps, pos, n_dims, freq_base, freq_scale, 1.0f, q_out, &kview, &vview,
+                           stream, static_cast<const int32_t *>(slot->data),
+                           status != nullptr ? static_cast<int32_t *>(status->data) : nullptr, cap);
 }

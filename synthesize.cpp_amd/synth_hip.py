@@ -67,6 +67,7 @@ def load(path=None):
         "shp_add_leaky_relu": [_PT, _PT, f, _PT, _PT, vp],
         "shp_add": [_PT, _PT, _PT, vp],
         "shp_qk_norm_rope_kv": [_PT, _PT, _PT, _PT, _PT, f, _PT, i32, f, f, _PT, _PT, _PT, ctypes.c_int64, vp],
+        "shp_qk_norm_rope_kv_at": [_PT, _PT, _PT, _PT, _PT, f, _PT, i32, f, f, _PT, _PT, _PT, _PT, _PT, vp],
         "shp_snake_guarded": [_PT, _PT, _PT, vp],
         "shp_snake_beta": [_PT, _PT, _PT, _PT, vp],
         "shp_exp": [_PT, _PT, vp],
@@ -264,6 +265,19 @@ def qk_norm_rope_kv(q, k, v, wq, wk, eps, pos, n_dims, freq_base, k_cache, v_cac
                                       float(eps), _ref(desc(pos)), int(n_dims), float(freq_base), float(freq_scale),
                                       _ref(desc(q_out)), _ref(desc(k_cache)), _ref(desc(v_cache)), int(filled),
                                       _stream()), "qk_norm_rope_kv")
+    return q_out
+
+
+def qk_norm_rope_kv_at(q, k, v, wq, wk, eps, pos, n_dims, freq_base, k_cache, v_cache, slot, status=None,
+                       freq_scale=1.0, q_out=None):
+    """qk_norm_rope_kv with the first cache row read from the int32 device tensor
+    `slot` when the kernel runs (graph-replayable); `status` (int32, one element)
+    is set to 1 when the rows do not fit the cache."""
+    q_out = q.new_empty(q.shape) if q_out is None else q_out
+    _check(load().shp_qk_norm_rope_kv_at(_ref(desc(q)), _ref(desc(k)), _ref(desc(v)), _ref(desc(wq)), _ref(desc(wk)),
+                                         float(eps), _ref(desc(pos)), int(n_dims), float(freq_base), float(freq_scale),
+                                         _ref(desc(q_out)), _ref(desc(k_cache)), _ref(desc(v_cache)), _ref(desc(slot)),
+                                         _ref(desc(status)), _stream()), "qk_norm_rope_kv_at")
     return q_out
 
 

@@ -142,6 +142,15 @@ def test_argument_validation():
     assert L.shp_qk_norm_rope_kv(*args(0, cache=mk(S.TYPE_F32, [128, 4, 64]))) == S.ERR_INVALID_ARG  # kv heads
     assert L.shp_qk_norm_rope_kv(*args(0, vv=mk(S.TYPE_F32, [128, 8, 4]))) == S.ERR_INVALID_ARG  # v shape
     assert L.shp_qk_norm_rope_kv(*args(0, cache=mk(S.TYPE_F16, [128, 8, 64]))) == S.ERR_INVALID_ARG  # cache type
+    slot, st = mk(S.TYPE_I32, [1]), mk(S.TYPE_I32, [1])
+    at = lambda cache=kc, sl=slot, stt=st: (R(q), R(k), R(v), R(wk), R(wk), 1e-6, R(pos), 128, 1e6, 1.0, R(q),
+                                             R(cache), R(kc), R(sl), R(stt), None)
+    assert L.shp_qk_norm_rope_kv_at(*at(sl=mk(S.TYPE_F32, [1]))) == S.ERR_INVALID_ARG  # slot type
+    assert L.shp_qk_norm_rope_kv_at(*at(sl=mk(S.TYPE_I32, [2]))) == S.ERR_INVALID_ARG  # one element
+    assert L.shp_qk_norm_rope_kv_at(*at(stt=mk(S.TYPE_F32, [1]))) == S.ERR_INVALID_ARG  # status type
+    assert L.shp_qk_norm_rope_kv_at(*at(cache=mk(S.TYPE_F32, [128, 8, 4]))) == S.ERR_INVALID_ARG  # < T rows
+    assert L.shp_qk_norm_rope_kv_at(R(q), R(k), R(v), R(wk), R(wk), 1e-6, R(pos), 128, 1e6, 1.0, R(q), R(kc), R(kc),
+                                    None, None, None) == S.ERR_INVALID_ARG  # no slot
     sc = mk(S.TYPE_F32, [37, 1, 16])
     assert L.shp_soft_max_ext(R(sc), None, 0.1, 0.5, R(sc), None) == S.ERR_UNSUPPORTED  # ALiBi
     assert L.shp_soft_max_ext(R(sc), R(mk(S.TYPE_F32, [36, 1])), 0.1, 0.0, R(sc), None) == S.ERR_INVALID_ARG

@@ -404,6 +404,102 @@ def test_qk_norm_rope_kv(gpu, T, filled, cap, hd, wkind):
     assert_bitexact(vc[outside], sentinel[outside])
 
 
+def _kv_inputs(rng, T, hd=128, H=16, KVH=8):
+    q = rng.standard_normal((T, H, hd)).astype(np.float32)
+    k = rng.standard_normal((T, KVH, hd)).astype(np.float32)
+    v = rng.standard_normal((T, KVH, hd)).astype(np.float32)
+    wq = F.f32_to_bf16_bits(rng.normal(1, 0.1, hd))
+    wk = F.f32_to_bf16_bits(rng.normal(1, 0.1, hd))
+    return q, k, v, wq, wk
+
+
+@pytest.mark.parametrize("T,filled,cap", [(1, 37, 64), (4, 60, 64), (3, 5, 16)])
+def test_qk_norm_rope_kv_device_slot_matches_host_slot(gpu, T, filled, cap):
+    """shp_qk_norm_rope_kv_at with `filled` in device memory writes exactly what
+    shp_qk_norm_rope_kv writes with it as an argument (q_out and both caches,
+    bit for bit); a slot whose rows do not fit (cap - T + 1, and -1) writes no
+    cache row, still writes q_out, and raises the status word."""
+    import torch
+    rng = np.random.default_rng(SEED + 17 * T + filled)
+    q, k, v, wq, wk = _kv_inputs(rng, T)
+    pos = (filled + np.arange(T)).astype(np.int32)
+    sentinel = rng.standard_normal((cap, 8, 128)).astype(np.float32)
+    args = lambda kc, vc: (_t(gpu, q), _t(gpu, k), _t(gpu, v), _bits16(gpu, wq, torch.bfloat16),
+                           _bits16(gpu, wk, torch.bfloat16), 1e-6, _t(gpu, pos), 128, 1e6, kc, vc)
+    kc0, vc0 = _t(gpu, sentinel), _t(gpu, sentinel)
+    q0 = gpu.qk_norm_rope_kv(*args(kc0, vc0), filled)
+    kc1, vc1 = _t(gpu, sentinel), _t(gpu, sentinel)
+    slot = torch.tensor([filled], dtype=torch.int32, device="cuda")
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    q1 = gpu.qk_norm_rope_kv_at(*args(kc1, vc1), slot, status)
+    for a, b in ((q0, q1), (kc0, kc1), (vc0, vc1)):
+        assert_bitexact(_np(b), _np(a))
+    assert int(_np(status)[0]) == 0
+    for bad in (cap - T + 1, -1):
+        kc2, vc2 = _t(gpu, sentinel), _t(gpu, sentinel)
+        status.zero_()
+        q2 = gpu.qk_norm_rope_kv_at(*args(kc2, vc2), torch.tensor([bad], dtype=torch.int32, device="cuda"), status)
+        assert_bitexact(_np(q2), _np(q0))
+        assert_bitexact(_np(kc2), sentinel)
+        assert_bitexact(_np(vc2), sentinel)
+        assert int(_np(status)[0]) == 1
+
+
+def test_decode_steps_replay_one_captured_graph(gpu):
+    """One HIP graph holding [qk-norm+rope+cache write at the device slot,
+    slot += 1, position += 1] is captured once and replayed for 5 decode steps;
+    after every replay (with eager work and a synchronisation in between) the
+    caches equal those of 5 eager steps with `filled` passed from the host."""
+    import torch
+    rng = np.random.default_rng(SEED + 23)
+    cap, steps = 16, 5
+    q, k, v, wq, wk = _kv_inputs(rng, 1)
+    dq, dk, dv = _t(gpu, q), _t(gpu, k), _t(gpu, v)
+    dwq, dwk = _bits16(gpu, wq, torch.bfloat16), _bits16(gpu, wk, torch.bfloat16)
+    sentinel = np.full((cap, 8, 128), -3.5, np.float32)
+    # eager reference: steps with filled and the position from the host
+    ek, ev, eq = _t(gpu, sentinel), _t(gpu, sentinel), []
+    expect = []
+    for n in range(steps):
+        p = torch.tensor([n], dtype=torch.int32, device="cuda")
+        eq.append(_np(gpu.qk_norm_rope_kv(dq, dk, dv, dwq, dwk, 1e-6, p, 128, 1e6, ek, ev, n)))
+        expect.append((_np(ek).copy(), _np(ev).copy()))
+    # the graph
+    gk, gv = _t(gpu, sentinel), _t(gpu, sentinel)
+    slot = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pos = torch.zeros(1, dtype=torch.int32, device="cuda")
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    qo = torch.empty_like(dq)
+
+    def step():
+        gpu.qk_norm_rope_kv_at(dq, dk, dv, dwq, dwk, 1e-6, pos, 128, 1e6, gk, gv, slot, status, q_out=qo)
+        slot.add_(1)
+        pos.add_(1)
+
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    # capture ran nothing: the caches are still the sentinel and the slot 0
+    assert_bitexact(_np(gk), sentinel)
+    assert int(_np(slot)[0]) == 0
+    for n in range(steps):
+        graph.replay()
+        torch.cuda.synchronize()
+        junk = torch.randn(1024, device="cuda").sum()  # eager work between the replays
+        torch.cuda.synchronize()
+        assert torch.isfinite(junk)
+        assert_bitexact(_np(gk), expect[n][0])
+        assert_bitexact(_np(gv), expect[n][1])
+        assert_bitexact(_np(qo), eq[n])
+        assert int(_np(slot)[0]) == n + 1
+    assert int(_np(status)[0]) == 0
+
+
 def _ulps_apart(got, ref):
     g = np.ascontiguousarray(got, np.float32).view(np.int32).astype(np.int64)
     r = np.ascontiguousarray(ref, np.float32).view(np.int32).astype(np.int64)
