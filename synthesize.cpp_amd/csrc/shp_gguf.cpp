@@ -16,7 +16,8 @@
 // Opening parses and validates the header in host code only (no HIP call), so
 // a package can be inspected on a machine without a GPU. Loading streams a
 // tensor's bytes from the file into device memory through two pinned staging
-// buffers: the read of chunk i+1 overlaps the host-to-device copy of chunk i.
+// buffers: the read of chunk i+1 (split over up to 8 threads) overlaps the
+// host-to-device copy of chunk i.
 
 #include <hip/hip_runtime.h>
 
@@ -24,11 +25,14 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
+#include <atomic>
 #include <cerrno>
 #include <cstdint>
 #include <cstring>
 #include <map>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "shp_internal.hpp"
@@ -42,6 +46,8 @@ constexpr uint64_t kMaxStringBytes  = uint64_t{ 1 } << 30;
 constexpr uint64_t kMaxCount        = uint64_t{ 1 } << 40;
 constexpr int      kMaxDims         = 4;
 constexpr size_t   kStageBytes      = size_t{ 32 } << 20;
+constexpr unsigned kReadThreads     = 8;                   // parallel reads per staging chunk
+constexpr size_t   kReadSplitMin    = size_t{ 1 } << 20;   // below this a chunk is read by one thread
 
 enum GgufValueType : uint32_t {
     kU8 = 0, kI8 = 1, kU16 = 2, kI16 = 3, kU32 = 4, kI32 = 5, kF32 = 6, kBool = 7,
@@ -376,6 +382,57 @@ bool loadable_type(uint32_t t) {
     return t == SHP_TYPE_F32 || t == SHP_TYPE_F16 || t == SHP_TYPE_BF16 || t == SHP_TYPE_Q8_0 || t == SHP_TYPE_I32;
 }
 
+// Reads n bytes at file offset off into dst; false on a short read. Large
+// reads are split over up to kReadThreads threads (a single thread copying
+// out of the page cache, not PCIe, bounds the load otherwise).
+bool read_range(int fd, char * dst, size_t n, uint64_t off) {
+    auto one = [fd](char * d, size_t len, uint64_t o) {
+        size_t got = 0;
+        while (got < len) {
+            const ssize_t rd = pread(fd, d + got, len - got, static_cast<off_t>(o + got));
+            if (rd < 0 && errno == EINTR) {
+                continue;
+            }
+            if (rd <= 0) {
+                return false;
+            }
+            got += static_cast<size_t>(rd);
+        }
+        return true;
+    };
+    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+    const unsigned nt = static_cast<unsigned>(std::min<size_t>({ kReadThreads, hw, n / kReadSplitMin }));
+    if (nt <= 1) {
+        return one(dst, n, off);
+    }
+    std::atomic<bool>        ok{ true };
+    std::vector<std::thread> th;
+    const size_t             part    = (n / nt + 4095) & ~size_t{ 4095 };
+    unsigned                 started = 0;
+    for (; started < nt; ++started) {
+        const size_t b = std::min(n, part * started), e = std::min(n, part * (started + 1));
+        if (b >= e) {
+            continue;
+        }
+        try {
+            th.emplace_back([&, b, e] {
+                if (!one(dst + b, e - b, off + b)) {
+                    ok = false;
+                }
+            });
+        } catch (...) {  // no more threads: this thread reads what is left
+            break;
+        }
+    }
+    if (started < nt && !one(dst + part * started, n - std::min(n, part * started), off + part * started)) {
+        ok = false;
+    }
+    for (auto & t : th) {
+        t.join();
+    }
+    return ok;
+}
+
 void release_staging(shp_gguf * g) {
     for (int k = 0; k < 2; ++k) {
         if (g->done[k] != nullptr) {
@@ -527,18 +584,9 @@ extern "C" shp_status_t shp_gguf_load_tensor(shp_gguf *   g,
         if (hipEventSynchronize(g->done[k]) != hipSuccess) {
             return SHP_ERR_BACKEND;
         }
-        size_t got = 0;
-        while (got < n) {
-            const ssize_t rd = pread(g->fd, static_cast<char *>(g->stage[k]) + got, n - got,
-                                     static_cast<off_t>(g->data_start + ti->offset + done_bytes + got));
-            if (rd < 0 && errno == EINTR) {
-                continue;
-            }
-            if (rd <= 0) {
-                (void) hipStreamSynchronize(s);
-                return SHP_ERR_INVALID_ARG;  // the file shrank under us
-            }
-            got += static_cast<size_t>(rd);
+        if (!read_range(g->fd, static_cast<char *>(g->stage[k]), n, g->data_start + ti->offset + done_bytes)) {
+            (void) hipStreamSynchronize(s);
+            return SHP_ERR_INVALID_ARG;  // the file shrank under us
         }
         if (hipMemcpyAsync(static_cast<char *>(device_dst) + done_bytes, g->stage[k], n, hipMemcpyHostToDevice, s) !=
                 hipSuccess ||
