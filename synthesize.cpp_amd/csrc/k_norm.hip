@@ -264,6 +264,17 @@ template <int WT, int MODE> shp_status_t launch_norm(const NormArgs & a, bool ve
         if (nvec <= 128) {
             return go(k_rms_norm_vec<128, 1, WT, MODE>, 2);
         }
+        // Rows of 1024 / 2048: with at least 4096 of them, one wave per row
+        // (no LDS round trip, no barrier) is faster -- measured on MI355X:
+        // rms_norm [1024,8192] -20 %, [2048,4096] and [2048,8192] -6 %,
+        // add+norm [2048,4096] -9 %; with fewer rows, and for the add forms
+        // at 1024 (+3 %), four waves per row keep more loads in flight and win.
+        if (a.nrows >= 4096 && nvec == 256 && MODE == kPlain) {
+            return go(k_rms_norm_vec<64, 4, WT, MODE>, 4);
+        }
+        if (a.nrows >= 4096 && nvec == 512) {
+            return go(k_rms_norm_vec<64, 8, WT, MODE>, 4);
+        }
         switch ((nvec + 255) / 256) {
             case 1:
                 return go(k_rms_norm_vec<256, 1, WT, MODE>, 1);

@@ -264,8 +264,10 @@ def _dev_w(gpu, w, kind):
 @pytest.mark.parametrize("shape,wkind", [((512, 1024), "bf16"), ((64, 2048), "f32"), ((7, 24, 128), "f16"),
                                          ((33, 1000), "f32"), ((5, 8), "f32"), ((3, 4096), "bf16"),
                                          ((40, 3072), "f32"), ((9, 64), "none"), ((4, 256), "bf16"),
-                                         ((6, 512), "f32")])
+                                         ((6, 512), "f32"), ((4101, 1024), "bf16"), ((4098, 2048), "f32")])
 def test_rms_norm_mul(gpu, shape, wkind):
+    """(4101, 1024) and (4098, 2048) take the one-wave-per-row launch (>= 4096
+    rows), with a partly empty last block."""
     rng = np.random.default_rng(SEED + sum(shape))
     x = rng.standard_normal(shape).astype(np.float32)
     x[0] = 0.0  # an all-zero row: scale = 1/sqrt(eps), output exactly 0
@@ -283,7 +285,8 @@ def test_rms_norm_mul(gpu, shape, wkind):
     assert same > 0.999  # double-accumulated squares: the GPU lands on the CPU's bits
 
 
-@pytest.mark.parametrize("shape,wkind", [((512, 1024), "bf16"), ((64, 2048), "f32"), ((3, 1000), "f32")])
+@pytest.mark.parametrize("shape,wkind", [((512, 1024), "bf16"), ((64, 2048), "f32"), ((3, 1000), "f32"),
+                                         ((4099, 1024), "f16"), ((4096, 2048), "bf16")])
 def test_add_rms_norm_mul(gpu, shape, wkind):
     rng = np.random.default_rng(SEED + 3 * sum(shape))
     a = rng.standard_normal(shape).astype(np.float32)
