@@ -57,6 +57,8 @@ def parse():
     p.add_argument("--pmc-pass", action="store_true", help="instead: run each op of the step eagerly over every "
                    "input set a few times, plus a %d MiB device copy of known size, for rocprofv3 --pmc "
                    "FETCH_SIZE / WRITE_SIZE passes (few dispatches, no graphs)" % (CALIB_BYTES >> 20))
+    p.add_argument("--pmc-large", action="store_true", help="instead: run one launch of each op at the large "
+                   "configs' shapes, three times, for rocprofv3 --pmc occupancy / VALU passes")
     return p.parse_args()
 
 
@@ -151,28 +153,31 @@ def time_graphs(torch, graphs, reps):
 # decode step: 28 layers x (add+norm, qk-norm+rope, add+norm, swiglu) at T=1
 # ---------------------------------------------------------------------------
 
-def decode_layer_us(S, torch, layers=28, reps=50, kv=False, total=512):
+def decode_layer_us(S, torch, layers=28, reps=50, kv=False, total=512, streams=1):
     """µs per talker layer of the decode step's non-GEMM ops, replayed as one
     graph of `layers` layers. kv: qk-norm+rope also writes this step's k and v
     into the layer's cache (slot total-1) and the step adds the attention
-    softmax over `total` keys for the 16 heads (5 launches per layer)."""
+    softmax over `total` keys for the 16 heads (5 launches per layer).
+    streams: concurrent decode streams batched into each op (one token each)."""
+    assert not (kv and streams != 1), "the KV variant models one stream"
     g = torch.Generator(device="cuda")
     g.manual_seed(SEED + 1)
     randn = lambda *shape: torch.randn(shape, generator=g, device="cuda", dtype=torch.float32)
     gain = lambda n: (1.0 + 0.1 * randn(n)).to(torch.bfloat16)
     L = []
     for _ in range(layers):
-        c = dict(a=randn(1, 1024), b=randn(1, 1024), w1=gain(1024), w2=gain(1024), wq=gain(128),
-                 wk=gain(128), q=randn(1, 16, 128), k=randn(1, 8, 128), proj=randn(1, 1024),
-                 gate=randn(1, 3072), up=randn(1, 3072), s1=torch.empty(1, 1024, device="cuda"),
-                 y1=torch.empty(1, 1024, device="cuda"), s2=torch.empty(1, 1024, device="cuda"),
-                 y2=torch.empty(1, 1024, device="cuda"), qo=torch.empty(1, 16, 128, device="cuda"),
-                 ko=torch.empty(1, 8, 128, device="cuda"), act=torch.empty(1, 3072, device="cuda"))
+        n = streams
+        c = dict(a=randn(n, 1024), b=randn(n, 1024), w1=gain(1024), w2=gain(1024), wq=gain(128),
+                 wk=gain(128), q=randn(n, 16, 128), k=randn(n, 8, 128), proj=randn(n, 1024),
+                 gate=randn(n, 3072), up=randn(n, 3072), s1=torch.empty(n, 1024, device="cuda"),
+                 y1=torch.empty(n, 1024, device="cuda"), s2=torch.empty(n, 1024, device="cuda"),
+                 y2=torch.empty(n, 1024, device="cuda"), qo=torch.empty(n, 16, 128, device="cuda"),
+                 ko=torch.empty(n, 8, 128, device="cuda"), act=torch.empty(n, 3072, device="cuda"))
         if kv:
             c.update(v=randn(1, 8, 128), kc=randn(total, 8, 128), vc=randn(total, 8, 128),
                      sc=randn(16, 1, total), p=torch.empty(16, 1, total, device="cuda"))
         L.append(c)
-    pos = torch.tensor([total - 1], dtype=torch.int32, device="cuda")
+    pos = torch.full((streams,), total - 1, dtype=torch.int32, device="cuda")
     scale = 1.0 / math.sqrt(128.0)
 
     def layer_fns(c):
@@ -469,6 +474,10 @@ def suite(args, S, torch):
         norm_case("cfg5", 64, 1024, add=True)
         qk_case("cfg5", 64, 8192)
         swiglu_case("cfg5", 64, 3072)
+        us64 = decode_layer_us(S, torch, streams=64)
+        rows.append({"config": "cfg5", "op": "64 concurrent decode streams: talker layer non-GEMM step "
+                     "(28-layer graph, 4 launches/layer, 64 rows per launch)", "us": round(us64, 3), "note": "per layer"})
+        print("cfg5  64-stream decode layer non-GEMM step: %.3f us/layer" % us64, flush=True)
 
     if on("gguf"):
         # A package's lookup tables streamed file -> HBM by shp_gguf_load_tensor
@@ -532,6 +541,45 @@ def pmc_pass(step, torch):
     print(json.dumps({"pmc_pass": "done", "sets": step.nsets, "calib_bytes": CALIB_BYTES, "op_bytes": step.op_bytes}))
 
 
+def pmc_large(S, torch):
+    """One launch each of the ops at the large configs' shapes, three times
+    (rocprofv3 --pmc occupancy and VALU passes read them per dispatch)."""
+    import numpy as np
+    import formats as F
+    g = torch.Generator(device="cuda")
+    g.manual_seed(SEED + 9)
+    randn = lambda *shape: torch.randn(shape, generator=g, device="cuda", dtype=torch.float32)
+    bf16 = lambda n: (1.0 + 0.1 * randn(n)).to(torch.bfloat16)
+    rng = np.random.default_rng(SEED + 9)
+    x2, w2 = randn(8192, 2048), bf16(2048)
+    q, k, wq, wk = randn(8192, 16, 128), randn(8192, 8, 128), bf16(128), bf16(128)
+    pos = torch.arange(8192, dtype=torch.int32, device="cuda")
+    gt, up = randn(8192, 6144), randn(8192, 6144)
+    xs, al = randn(131072, 128), torch.exp(torch.empty(128, device="cuda").uniform_(-2.3, 2.3, generator=g))
+    la, lb = torch.empty(128, device="cuda").uniform_(-3, 3, generator=g), torch.empty(128, device="cuda").uniform_(
+        -3, 3, generator=g)
+    a4, b4 = randn(131072, 128), randn(131072, 128)
+    tabs = [S.Q8Tensor(torch.from_numpy(F.q8_0_synthetic(rng, 2048, 1024)).cuda(), 1024) for _ in range(16)]
+    codes = torch.randint(0, 2048, (16, 4096), generator=g, device="cuda", dtype=torch.int32)
+    sc = randn(16, 512, 512)
+    ops = [("rms_norm_mul [2048,8192]", lambda: S.rms_norm_mul(x2, w2, 1e-6)),
+           ("add_rms_norm_mul [2048,8192]", lambda: S.add_rms_norm_mul(x2, x2, w2, 1e-6)),
+           ("qk_norm_rope [128,16+8,8192]", lambda: S.qk_norm_rope(q, k, wq, wk, 1e-6, pos, 128, 1e6)),
+           ("swiglu [6144,8192]", lambda: S.swiglu(gt, up)),
+           ("snake [128,131072]", lambda: S.snake(xs, al)),
+           ("snake_beta [128,131072]", lambda: S.snake_beta(xs, la, lb)),
+           ("add_leaky_relu [128,131072]", lambda: S.add_leaky_relu(a4, b4, 0.1)),
+           ("get_rows_sum q8_0 16x4096", lambda: S.get_rows_sum(tabs, codes)),
+           ("get_rows q8_0 x4096", lambda: S.get_rows(tabs[0], codes[0])),
+           ("soft_max_ext [512,512,16]", lambda: S.soft_max_ext(sc, None, 0.0884))]
+    torch.cuda.synchronize()
+    for _ in range(3):
+        for _, f in ops:
+            f()
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_large": [name for name, _ in ops]}))
+
+
 def read_traffic(op):
     """HBM bytes per launch of `op` from the committed counter summary (two
     rocprofv3 --pmc passes, FETCH_SIZE then WRITE_SIZE, each scaled by what the
@@ -558,6 +606,9 @@ def main():
     S.load()
     if args.suite:
         suite(args, S, torch)
+        return
+    if args.pmc_large:
+        pmc_large(S, torch)
         return
     step = PrefillStep(S, torch)
     if args.pmc_pass:
