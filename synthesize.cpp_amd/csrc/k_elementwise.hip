@@ -179,8 +179,8 @@ template <bool RCP> __device__ __forceinline__ float snake1(float x, float al, f
 // a division per element, and for SnakeBeta two exps per channel), so its
 // costs are cut without changing its result:
 //   - a lane owns one quad of channels (4 consecutive coefficients) in R
-//     consecutive rows, so the per-channel work (the exps, the guard and the
-//     4 double reciprocals) is done once per R rows;
+//     consecutive rows (SnakeRows), so the per-channel work (the exps, the
+//     guard and the 4 double reciprocals) is done once per R rows;
 //   - the division: q / den becomes (float)((double)q * rcp), which is the
 //     IEEE quotient (shp_div.hpp). Lanes whose den include 0, inf or NaN take
 //     the f32 division;
@@ -191,8 +191,12 @@ template <bool RCP> __device__ __forceinline__ float snake1(float x, float al, f
 // (64 lanes, consecutive quads of one row). Measured on MI355X at
 // [128,131072], plain Snake: ~6% faster than one float4 per lane with OCML's
 // sinf and the f32 division.
+// Rows per lane, measured on MI355X over the cfg4 shapes: 2 for Snake and the
+// guarded Snake (3-6 % faster than 4), 8 for SnakeBeta, whose two exps per
+// channel then spread over 32 elements (9-11 % faster than 4 at [256,32768]
+// and [128,131072]).
 template <int K> struct SnakeRows {
-    static constexpr int R = 4;
+    static constexpr int R = K == kSnakeBeta ? 8 : 2;
 };
 
 template <int K, int R, bool RCP>

@@ -581,8 +581,8 @@ def test_glu_swiglu_single_tensor(gpu, swapped):
 
 @pytest.mark.parametrize("T,C", [(256, 512), (64, 128), (31, 30), (5, 1024), (9, 2048), (3, 1028)])
 def test_snake(gpu, T, C):
-    """C % 4 == 0: the flat kernel (4 rows per lane, division through a double
-    reciprocal; T % 4 != 0 leaves a partial group); C % 4 != 0: the row kernel.
+    """C % 4 == 0: the flat kernel (2 rows per lane, division through a double
+    reciprocal; odd T leaves a partial group); C % 4 != 0: the row kernel.
     Row 0 holds large x, so |alpha*x| crosses 2^15 and those elements take
     OCML's sine instead of the fast one."""
     rng = np.random.default_rng(SEED + T + C)
@@ -598,7 +598,7 @@ def test_snake_special_alphas(gpu):
     others the reciprocal route; power-of-two, negative, subnormal and extreme
     alphas exercise exact ties, overflow to inf and underflow. NaN and inf land
     where the oracle puts them; finite outputs meet the Snake tolerance. 37 rows
-    also leave a partial group of the kernel's 4 rows per lane."""
+    also leave a partial group of the kernel's 2 rows per lane."""
     rng = np.random.default_rng(SEED + 99)
     T, C = 37, 64
     x = rng.standard_normal((T, C)).astype(np.float32)
@@ -637,7 +637,8 @@ def test_snake_guarded(gpu, T, C):
 @pytest.mark.parametrize("T,C", [(256, 512), (37, 64), (31, 30), (9, 2048), (4, 1028)])
 def test_snake_beta(gpu, T, C):
     """codec_snake_beta (qwen3-tts): log curves over [-3, 3], so alpha/beta span
-    e^+-3 and the two exps, the guard and the division all matter."""
+    e^+-3 and the two exps, the guard and the division all matter. The flat
+    kernel takes 8 rows per lane: T = 37, 9 and 4 leave partial groups."""
     rng = np.random.default_rng(SEED + 11 * T + C)
     x = rng.standard_normal((T, C)).astype(np.float32)
     la = rng.uniform(-3, 3, C).astype(np.float32)
