@@ -767,6 +767,57 @@ def test_strided_views(gpu):
     assert_close(_np(y), R.run(lambda g: R.swiglu(g, qkv.reshape(10, -1)[:, :1024], qkv.reshape(10, -1)[:, :1024])))
 
 
+def test_strided_views_newer_ops(gpu):
+    """Views for the Snake variants, exp, scale_bias and soft_max_ext (the row
+    kernels; float4 rows with a strided RowMap, and scalar rows with a
+    non-flat one), and the fused cache write fed by q, k, v head views of one
+    qkv buffer, as the attention's projection leaves them."""
+    import torch
+    rng = np.random.default_rng(29)
+    buf = rng.standard_normal((10, 32, 128)).astype(np.float32)
+    dev = _t(gpu, buf)
+    flat = buf.reshape(10, -1)
+    xv = dev.reshape(10, 4096)[:, 8:1032]            # rows 16 KB apart, 32 B in
+    xr = flat[:, 8:1032]
+    out = torch.full((10, 4096), 7.0, device="cuda")
+    yv = out[:, 2048:3072]
+    la = rng.uniform(-3, 3, 1024).astype(np.float32)
+    lb = rng.uniform(-3, 3, 1024).astype(np.float32)
+    gpu.snake_beta(xv, _t(gpu, la), _t(gpu, lb), out=yv)
+    assert_snake_close(_np(yv), R.run(lambda g: R.snake_beta(g, xr, la, lb)), xr)
+    al = np.exp(rng.uniform(np.log(1e-3), np.log(10.0), 1024)).astype(np.float32)
+    assert_snake_close(_np(gpu.snake_guarded(xv, _t(gpu, al))), R.run(lambda g: R.snake_guarded(g, xr, al)), xr)
+    with np.errstate(over="ignore"):
+        e_ref = R.run(lambda g: g.exp(xr))
+    d = _ulps_apart(_np(gpu.exp(xv)), e_ref)
+    assert d.max() <= 1 and (d == 0).mean() > 0.99
+    assert_bitexact(_np(gpu.scale_bias(xv, 0.75, -0.25)), R.run(lambda g: g.scale_bias(xr, np.float32(0.75),
+                                                                                     np.float32(-0.25))))
+    assert (_np(out)[:, :2048] == 7.0).all() and (_np(out)[:, 3072:] == 7.0).all()  # only the view written
+    for cols in (100, 97):  # float4 rows (strided, flat map) and scalar rows (non-flat map)
+        sv = dev[:, :16, :cols] if cols == 97 else dev[:, :, :cols]
+        sr = buf[:, :16, :cols] if cols == 97 else buf[:, :, :cols]
+        m = rng.uniform(-2, 0, (sr.shape[1], cols)).astype(np.float32)
+        ref = R.run(lambda g: g.soft_max_ext(sr, m, np.float32(0.125)))
+        got = _np(gpu.soft_max_ext(sv, _t(gpu, m), 0.125))
+        d = _ulps_apart(got, ref)
+        assert d.max() <= 2 and (d == 0).mean() > 0.99
+    # q, k, v as head views of one [T, 16 + 8 + 8, 128] qkv buffer
+    q, k, v = dev[:, :16, :], dev[:, 16:24, :], dev[:, 24:32, :]
+    wq = F.f32_to_bf16_bits(rng.normal(1, 0.1, 128))
+    wk = F.f32_to_bf16_bits(rng.normal(1, 0.1, 128))
+    pos = (20 + np.arange(10)).astype(np.int32)
+    kc, vc = torch.zeros(40, 8, 128, device="cuda"), torch.zeros(40, 8, 128, device="cuda")
+    qo = gpu.qk_norm_rope_kv(q, k, v, _bits16(gpu, wq, torch.bfloat16), _bits16(gpu, wk, torch.bfloat16), 1e-6,
+                             _t(gpu, pos), 128, 1e6, kc, vc, 20)
+    qr, kr = R.run(lambda g: R.qk_norm_rope(g, buf[:, :16], buf[:, 16:24], wq, wk, np.float32(1e-6), pos, 128,
+                                            np.float32(1e6), R.BF16))
+    assert_rope_close(_np(qo), qr, 128)
+    assert_rope_close(_np(kc)[20:30], kr, 128)
+    assert_bitexact(_np(vc)[20:30], buf[:, 24:32])
+    assert (_np(kc)[:20] == 0).all() and (_np(vc)[30:] == 0).all()
+
+
 # ---------------------------------------------------------------------------
 # the reference's goldens through the HIP kernels
 # ---------------------------------------------------------------------------
