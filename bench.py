@@ -645,9 +645,18 @@ def main():
         per_op[name] = {"us": round(us, 3), "bytes": step.op_bytes[name], "GB/s": round(gbs, 1),
                         "frac": round(gbs / PEAK_GBS, 4)}
     dom = max(per_op, key=lambda n: per_op[n]["us"])
+    # What a one-read-one-write stream of the same bytes reaches at this size in
+    # the same run (this library's bare leaky-ReLU over the same rotation
+    # protocol): a 19 MB launch cannot approach the HBM peak, and this says how
+    # close the dominant kernel is to what its size allows.
+    floor_elems = step.op_bytes[dom] // 8
+    floor_us, _ = measure_op(torch, lambda: (lambda x, y: (lambda: S.leaky_relu(x, 0.1, out=y)))(
+        torch.randn(floor_elems, device="cuda"), torch.empty(floor_elems, device="cuda")), 8 * floor_elems)
     roof = {"bound": "hbm", "kernel": dom, "achieved": per_op[dom]["GB/s"], "peak": PEAK_GBS, "unit": "GB/s",
             "frac": per_op[dom]["frac"], "traffic": read_traffic(dom),
-            "algorithmic_bytes": step.op_bytes[dom], "us_per_launch": per_op[dom]["us"]}
+            "algorithmic_bytes": step.op_bytes[dom], "us_per_launch": per_op[dom]["us"],
+            "same_bytes_copy_like_us": round(floor_us, 3),
+            "frac_of_same_bytes_copy_like": round(floor_us / per_op[dom]["us"], 4)}
 
     layer_us = decode_layer_us(S, torch)
 
