@@ -165,14 +165,18 @@ template <int K> __device__ __forceinline__ SnakeCoef snake_coef(float c0, float
     }
 }
 
-// The node run mul, sin, mul (or sqr), div, add, each rounded in f32. RCP:
-// divide through the double reciprocal of den (IEEE quotient, shp_div.hpp).
-template <bool RCP> __device__ __forceinline__ float snake1(float x, float al, float den, double rcp) {
-    const float t  = x * al;
-    const float sn = sin_fast_ok(t) ? sin_f32_fast(t) : sinf(t);
+// The node run mul, sin, mul (or sqr), div, add, each rounded in f32, from
+// t = x*al. FAST: t is known to be inside the fast sine's range. RCP: divide
+// through the double reciprocal of den (IEEE quotient, shp_div.hpp).
+template <bool FAST, bool RCP> __device__ __forceinline__ float snake_t(float x, float t, float den, double rcp) {
+    const float sn = FAST ? sin_f32_fast(t) : (sin_fast_ok(t) ? sin_f32_fast(t) : sinf(t));
     const float q  = sn * sn;
     const float r  = RCP ? div_by_rcp(q, rcp) : q / den;
     return x + r;
+}
+
+template <bool RCP> __device__ __forceinline__ float snake1(float x, float al, float den, double rcp) {
+    return snake_t<false, RCP>(x, x * al, den, rcp);
 }
 
 // Snake, flat path. The formula is ALU-heavy for a streaming op (a sine and
@@ -195,20 +199,62 @@ template <bool RCP> __device__ __forceinline__ float snake1(float x, float al, f
 // guarded Snake (3-6 % faster than 4), 8 for SnakeBeta, whose two exps per
 // channel then spread over 32 elements (9-11 % faster than 4 at [256,32768]
 // and [128,131072]).
+// Rows per lane, measured on MI355X over the cfg4 shapes: 2 for Snake and the
+// guarded Snake (3-6 % faster than 4), 8 for SnakeBeta, whose two exps per
+// channel then spread over 32 elements (9-11 % faster than 4 at [256,32768]
+// and [128,131072]).
 template <int K> struct SnakeRows {
     static constexpr int R = K == kSnakeBeta ? 8 : 2;
 };
 
+// A lane's elements, two rows (8 elements) at a time: every t first, then one
+// range test for the 8, so the common case is straight-line code whose
+// independent sine/division chains the compiler interleaves (a test per
+// element puts a branch between every pair of them; testing all R rows at
+// once holds too many registers at R = 8).
+constexpr int kSnakeSub = 2;
+
 template <int K, int R, bool RCP>
 __device__ __forceinline__ void snake_rows(const f32x4 (&xv)[R], f32x4 al, f32x4 den, const double (&rc)[4], int64_t i0,
                                            int64_t c4, int64_t n4, f32x4 * Y) {
+    static_assert(R % kSnakeSub == 0, "rows per lane in whole sub-blocks");
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int64_t i = i0 + r * c4;
-        if (i < n4) {
-            const f32x4 v = xv[r];
-            st_stream(Y + i, f32x4{ snake1<RCP>(v.x, al.x, den.x, rc[0]), snake1<RCP>(v.y, al.y, den.y, rc[1]),
-                                    snake1<RCP>(v.z, al.z, den.z, rc[2]), snake1<RCP>(v.w, al.w, den.w, rc[3]) });
+    for (int r0 = 0; r0 < R; r0 += kSnakeSub) {
+        f32x4    t[kSnakeSub];
+        unsigned fast = 1u;  // bitwise: a short-circuit && would branch per element again
+#pragma unroll
+        for (int r = 0; r < kSnakeSub; ++r) {
+            const f32x4 x = xv[r0 + r];
+            t[r]          = f32x4{ x.x * al.x, x.y * al.y, x.z * al.z, x.w * al.w };
+            fast &= static_cast<unsigned>(sin_fast_ok(t[r].x)) & static_cast<unsigned>(sin_fast_ok(t[r].y)) &
+                    static_cast<unsigned>(sin_fast_ok(t[r].z)) & static_cast<unsigned>(sin_fast_ok(t[r].w));
+        }
+        f32x4 y[kSnakeSub];
+        if (fast != 0u) {
+#pragma unroll
+            for (int r = 0; r < kSnakeSub; ++r) {
+                const f32x4 x = xv[r0 + r];
+                y[r]          = f32x4{ snake_t<true, RCP>(x.x, t[r].x, den.x, rc[0]),
+                                       snake_t<true, RCP>(x.y, t[r].y, den.y, rc[1]),
+                                       snake_t<true, RCP>(x.z, t[r].z, den.z, rc[2]),
+                                       snake_t<true, RCP>(x.w, t[r].w, den.w, rc[3]) };
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < kSnakeSub; ++r) {
+                const f32x4 x = xv[r0 + r];
+                y[r]          = f32x4{ snake_t<false, RCP>(x.x, t[r].x, den.x, rc[0]),
+                                       snake_t<false, RCP>(x.y, t[r].y, den.y, rc[1]),
+                                       snake_t<false, RCP>(x.z, t[r].z, den.z, rc[2]),
+                                       snake_t<false, RCP>(x.w, t[r].w, den.w, rc[3]) };
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kSnakeSub; ++r) {
+            const int64_t i = i0 + (r0 + r) * c4;
+            if (i < n4) {
+                st_stream(Y + i, y[r]);
+            }
         }
     }
 }
