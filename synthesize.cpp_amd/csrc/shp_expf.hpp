@@ -60,11 +60,12 @@ constexpr double kExpC3        = 0x1.c6b08d704a0c0p-23;
 constexpr double kExpC4        = 0x1.3b2ab6fba4e77p-31;
 
 // tab(j) must return kExpTable[j] for j in [0, 63].
+// Branch-free (a NaN is carried through a select, not an early return), so a
+// caller's loop over independent elements stays straight-line code whose
+// table reads overlap.
 template <class Tab> SHP_HD inline float exp_f32_rn(float x, const Tab & tab) {
-    if (x != x) {
-        return x;
-    }
-    const float  xc = x < -104.0f ? -104.0f : (x > 89.0f ? 89.0f : x);
+    const bool   nan = x != x;
+    const float  xc  = std::fmin(std::fmax(x, -104.0f), 89.0f);  // max/min instructions; a NaN gives -104
     const double z  = static_cast<double>(xc) * kExp64OverLn2;
     const double kd = std::rint(z);
     const double r  = z - kd;
@@ -74,7 +75,8 @@ template <class Tab> SHP_HD inline float exp_f32_rn(float x, const Tab & tab) {
     p               = std::fma(p, r, 1.0);
     const int k     = static_cast<int>(kd);
     const int j     = k & 63;
-    return static_cast<float>(std::ldexp(tab(j) * p, (k - j) / 64));
+    const float  e  = static_cast<float>(std::ldexp(tab(j) * p, (k - j) / 64));
+    return nan ? x : e;
 }
 
 // Host form: the table indexed directly.
