@@ -8,11 +8,16 @@
 // order in f32, exactly as the unfused ggml_add chain does.
 //
 // Q8_0 layout: 32-element blocks of {f16 d; int8 qs[32]} = 34 bytes, so
-// blocks are only 2-byte aligned. Rows of 256..4096 elements are read by
-// half-blocks (16 quants per lane, from a 4-byte aligned 5-dword window plus
-// the scale's dword, shifted into place with v_alignbyte); other widths that
-// are a multiple of 64 by block pairs (68 bytes = 17 aligned dwords per lane).
-// Either way the decode is in registers, with no LDS traffic.
+// blocks are only 2-byte aligned. get_rows of 1024/2048/4096-wide rows in
+// 16-byte aligned tables stages each row through LDS with aligned loads; other
+// rows of 256..4096 elements are read by half-blocks (16 quants per lane, from
+// a 4-byte aligned 5-dword window plus the scale's dword, shifted into place
+// with v_alignbyte); other widths that are a multiple of 64 by block pairs (68
+// bytes = 17 aligned dwords per lane). The gather->sum of 1024/2048/4096-wide
+// rows reads one five-dword window per lane and group and decodes it in
+// registers. (Geometry of every read: shp_q8.hpp.)
+
+#include <atomic>
 
 #include "shp_internal.hpp"
 #include "shp_q8.hpp"
@@ -60,12 +65,14 @@ struct GatherSumArgs {
     int64_t         frames;
     int32_t         ngroups;
     int32_t         ne0;
-    // Q8_0 half-block path only: every table has rows of `rowbytes` bytes and
-    // fewer than 2^31 bytes in all, so a row offset is 32-bit; slots from
-    // ngroups up to the next multiple of 16 repeat group 0's table.
+    // Q8_0 kernels only: every table has fewer than 2^31 bytes, so a row
+    // offset is 32-bit: row id * rstride[g]. A slot g past the last group
+    // (the kernels read whole chunks of slots) reads row 0 of kQ8NegZeroRow
+    // (tab[g] = its address, rstride[g] = 0), which adds nothing to the sum,
+    // and carries group 0's row count (group 0's id is read for it, so its
+    // bounds check repeats group 0's).
     uint32_t        rows32[kMaxGroups];
-    uint32_t        rowbytes;
-    int32_t         staged;  // ... and through LDS: ne0 in {1024, 2048, 4096}, tables 16-byte aligned
+    uint32_t        rstride[kMaxGroups];
 };
 
 template <int TYPE> constexpr int elems_per_chunk() {
@@ -170,6 +177,11 @@ __device__ __forceinline__ void gather_coords(const GatherArgs & a, int64_t R, i
 }
 
 constexpr uint32_t kQNaN = 0x7fc00000u;
+
+// The row the Q8_0 gather->sum kernels read for slots past the last group
+// (shp_q8.hpp: every block d = -0.0, zero quants). Only read; the host passes
+// its address (hipGetSymbolAddress) in the slot's table pointer.
+__device__ Q8NegZeroRow kQ8NegZeroRow = q8_neg_zero_row();
 
 // F32/F16/BF16, 16-byte chunks, LPR lanes per row (up to 256: a 2048-wide
 // BF16 row is one block with one chunk per lane). The id is read first; the
@@ -330,10 +342,9 @@ template <int LPR> __global__ __launch_bounds__(256) void k_get_rows_q8h(const G
 // one row round trip, not one per group. The ids are vector loads (in-order
 // vmcnt lets all 16 overlap). Per group the kernel keeps only the table base
 // and a 32-bit row count in scalar registers; row offsets are 32-bit. Slots
-// past the last group read group 0's table (the host fills them) and are
-// masked out of the sum. The sum is taken in group order from -0.0f, the
-// identity of f32 addition (-0 + v == v bit for bit), so group 0 needs no
-// special case.
+// past the last group read kQ8NegZeroRow and add nothing. The sum is taken in
+// group order from -0.0f, the identity of f32 addition (-0 + v == v bit for
+// bit), so group 0 needs no special case.
 constexpr int kSumChunk = 16;
 
 template <bool FIRST>
@@ -350,8 +361,8 @@ __device__ __forceinline__ void q8_sum_chunk(const GatherSumArgs & a, int g0, in
     for (int j = 0; j < kSumChunk; ++j) {
         const int      g  = FIRST ? j : g0 + j;
         const uint32_t ok = id[j] < a.rows32[g] ? 1u : 0u;  // unsigned: a negative id is out of range too
-        bad |= (g < a.ngroups) ? (ok ^ 1u) : 0u;
-        off[j] = (ok ? id[j] : 0u) * a.rowbytes;
+        bad |= ok ^ 1u;
+        off[j] = (ok ? id[j] : 0u) * a.rstride[g];
     }
     Q8Half h[kSumChunk];
 #pragma unroll
@@ -362,11 +373,9 @@ __device__ __forceinline__ void q8_sum_chunk(const GatherSumArgs & a, int g0, in
     for (int j = 0; j < kSumChunk; ++j) {
         float o[16];
         q8_half_decode(h[j], p, o);
-        if ((FIRST ? j : g0 + j) < a.ngroups) {
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                acc[k] = acc[k] + o[k];
-            }
+        for (int k = 0; k < 16; ++k) {
+            acc[k] = acc[k] + o[k];
         }
     }
 }
@@ -395,6 +404,109 @@ template <int LPR> __global__ __launch_bounds__(256) void k_get_rows_sum_q8h(con
         }
     }
     store16(reinterpret_cast<float *>(reinterpret_cast<char *>(a.dst) + f * a.dnb1) + 16 * l, acc);
+}
+
+// Q8_0 gather->sum by five-dword windows (ne0 = 1024*NS, rows 4-byte aligned;
+// geometry and its bounds in shp_q8.hpp). One wave per 1024-element slab of a
+// frame; lane l owns elements 16l..16l+15 of the slab. A chunk of G groups
+// costs two round trips: one vector load brings the G ids (lane j reads group
+// j's) and readlane makes them scalar; then every group's window (a dword and
+// a dwordx4 at a scalar row base plus the lane's offset) is requested before
+// the first is decoded, and each is decoded in group order as it arrives. No
+// LDS and no branches: a slot past the last group reads kQ8NegZeroRow, which
+// adds exactly nothing. Each value enters the sum as fma(q, d, acc): q*d has
+// at most 19 significant bits, so it is exact in f32 and the fused form rounds
+// once, exactly as acc + q*d does -- one instruction less per element, and
+// the decode is what bounds this kernel. The sum starts at -0.0f, the
+// identity of f32 addition. FIRST: the chunk of groups 0..G-1, whose kernel
+// argument slots are compile-time offsets. The kernel is built for at most 4
+// waves per SIMD (128 VGPRs): a 4096-frame sum at ne0 = 1024 is 16 waves per
+// CU, all resident at once, so the registers buy every window of a chunk in
+// flight rather than occupancy the launch cannot use.
+template <int G, bool FIRST>
+__device__ __forceinline__ void q8w_chunk(const GatherSumArgs & a, int g0, int64_t f, uint32_t off, const Q8WinPos & p,
+                                          float (&acc)[16], uint32_t & bad) {
+    const int      l   = static_cast<int>(threadIdx.x) % kWave;
+    const int      gl  = (FIRST ? 0 : g0) + l % G;
+    const uint32_t ids = static_cast<uint32_t>(group_id(a, gl < a.ngroups ? gl : 0, f));
+    uint32_t w[G][5];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        const int      g    = (FIRST ? 0 : g0) + j;
+        const uint32_t id   = __builtin_amdgcn_readlane(ids, j);
+        const uint32_t ok   = id < a.rows32[g] ? 1u : 0u;  // unsigned: a negative id is out of range too
+        bad |= ok ^ 1u;
+        const char *   src  = a.tab[g] + (ok ? id : 0u) * a.rstride[g] + off;
+        const u32x4_a4 v   = *reinterpret_cast<const u32x4_a4 *>(src + 4);
+        w[j][0]            = *reinterpret_cast<const uint32_t *>(src);
+        w[j][1]            = v.x;
+        w[j][2]            = v.y;
+        w[j][3]            = v.z;
+        w[j][4]            = v.w;
+    }
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        // quad_perm(0,0,2,2): both lanes of a pair take the even lane's w[0].
+        const uint32_t dw =
+            static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(w[j][0]), 0xA0, 0xF, 0xF, false));
+        const float d = f16_bits_to_f32(dw >> p.dsh);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t q = perm_bytes(w[j][i + 1], w[j][i], p.sel);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                acc[4 * i + k] = __builtin_fmaf(sbyte(q, k), d, acc[4 * i + k]);
+            }
+        }
+    }
+}
+
+template <int NS, int G>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_get_rows_sum_q8w(
+    const GatherSumArgs a) {
+    __shared__ f32x4 s_out[4][kQ8SlabElems / 4];  // one slab per wave, for the store transpose
+    const int     wi = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    const int64_t wv = static_cast<int64_t>(blockIdx.x) * 4 + wi;
+    const int64_t f    = wv / NS;
+    const int     slab = static_cast<int>(wv % NS);
+    if (f >= a.frames) {
+        return;
+    }
+    const int      l   = static_cast<int>(threadIdx.x) % kWave;
+    const Q8WinPos p   = q8_win_pos(l);
+    const uint32_t off = static_cast<uint32_t>(slab) * kQ8SlabBytes + p.base;
+    float          acc[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        acc[k] = -0.0f;
+    }
+    uint32_t bad = 0;
+    q8w_chunk<G, true>(a, 0, f, off, p, acc, bad);
+    for (int g0 = G; g0 < a.ngroups; g0 += G) {
+        q8w_chunk<G, false>(a, g0, f, off, p, acc, bad);
+    }
+    if (bad != 0) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            acc[k] = __uint_as_float(kQNaN);
+        }
+    }
+    // The lane's 16 sums are contiguous; stored straight, each store
+    // instruction would put 16 bytes into each of 64 different 64-byte
+    // segments (four times the write requests of a contiguous store, ~15 %
+    // of this kernel's time). A wave-private LDS transpose makes store k the
+    // contiguous kilobyte 256k..256k+255 of the slab.
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        s_out[wi][4 * l + k] = f32x4{ acc[4 * k], acc[4 * k + 1], acc[4 * k + 2], acc[4 * k + 3] };
+    }
+    __syncwarp();
+    f32x4 * out = reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(reinterpret_cast<char *>(a.dst) + f * a.dnb1) +
+                                            kQ8SlabElems * slab);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        st_stream(out + 64 * k + l, s_out[wi][64 * k + l]);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -483,68 +595,6 @@ template <int NQ> __global__ __launch_bounds__(256) void k_get_rows_q8s(const Ga
         q8_row_decode<NQ>(s_row[w], l, o);
     }
     q8_row_store<NQ>(drow, l, o);
-}
-
-// Gather->sum through LDS: one wave per frame. Groups go in chunks of GC: the
-// chunk's ids are loaded together, then its rows (into registers), then each
-// row in group order is staged in the wave's LDS buffer, decoded and added.
-// Slots past the last group read group 0's table (the host fills them) and
-// are not added. The sum starts at -0.0f, the identity of f32 addition.
-template <int NQ, int GC> __global__ __launch_bounds__(256) void k_get_rows_sum_q8s(const GatherSumArgs a) {
-    __shared__ uint32_t s_row[kQ8StageWaves][q8_row_dwords(NQ) + kQ8StagePadDwords];
-    const int           w = static_cast<int>(threadIdx.x) / kWave;
-    const int           l = static_cast<int>(threadIdx.x) % kWave;
-    const int64_t       f = static_cast<int64_t>(blockIdx.x) * kQ8StageWaves + w;
-    if (f >= a.frames) {
-        return;  // no block barrier below: only this wave uses s_row[w]
-    }
-    float acc[4 * NQ];
-#pragma unroll
-    for (int j = 0; j < 4 * NQ; ++j) {
-        acc[j] = -0.0f;
-    }
-    uint32_t bad = 0;
-    for (int g0 = 0; g0 < a.ngroups; g0 += GC) {
-        uint32_t id[GC];
-#pragma unroll
-        for (int j = 0; j < GC; ++j) {
-            const int g = g0 + j;
-            id[j]       = static_cast<uint32_t>(group_id(a, g < a.ngroups ? g : 0, f));
-        }
-        // Every lane of the wave read the same id (one frame per wave): move it
-        // to a scalar register, so the bounds check and the row base are scalar
-        // and each row load is a scalar base plus the lane's small offset.
-        Q8Row<NQ> r[GC];
-#pragma unroll
-        for (int j = 0; j < GC; ++j) {
-            const int      g   = g0 + j;
-            const uint32_t sid = __builtin_amdgcn_readfirstlane(id[j]);
-            const uint32_t ok  = sid < a.rows32[g] ? 1u : 0u;  // unsigned: a negative id is out of range too
-            bad |= (g < a.ngroups) ? (ok ^ 1u) : 0u;
-            r[j] = q8_row_load<NQ>(a.tab[g] + static_cast<uint64_t>(ok ? sid : 0u) * a.rowbytes, l);
-        }
-#pragma unroll
-        for (int j = 0; j < GC; ++j) {
-            if (g0 + j < a.ngroups) {
-                q8_row_stage<NQ>(s_row[w], r[j], l);
-                __syncwarp();
-                float o[4 * NQ];
-                q8_row_decode<NQ>(s_row[w], l, o);
-                __syncwarp();
-#pragma unroll
-                for (int k = 0; k < 4 * NQ; ++k) {
-                    acc[k] = acc[k] + o[k];
-                }
-            }
-        }
-    }
-    if (bad != 0) {
-#pragma unroll
-        for (int k = 0; k < 4 * NQ; ++k) {
-            acc[k] = __uint_as_float(kQNaN);
-        }
-    }
-    q8_row_store<NQ>(reinterpret_cast<float *>(reinterpret_cast<char *>(a.dst) + f * a.dnb1), l, acc);
 }
 
 // Any type / alignment: one wave per row, element by element.
@@ -725,24 +775,34 @@ template <int TYPE> shp_status_t launch_get_rows(const GatherArgs & a, bool vec,
     return launch_status();
 }
 
+// Q8_0 widths the LDS-staged get_rows takes (one wave per row, NQ = ne0/256)
+// and the windowed gather->sum takes (ne0/1024 waves per frame).
+bool q8_staged_width(int64_t ne0) {
+    return ne0 == 1024 || ne0 == 2048 || ne0 == 4096;
+}
+
+// The windowed Q8_0 gather->sum: NS waves per frame, G = 8 group slots when
+// 8 groups or fewer are summed, else 16.
+template <int NS> void launch_q8w(const GatherSumArgs & a, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((a.frames * NS + 3) / 4));
+    if (a.ngroups <= 8) {
+        hipLaunchKernelGGL((k_get_rows_sum_q8w<NS, 8>), grid, dim3(256), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((k_get_rows_sum_q8w<NS, 16>), grid, dim3(256), 0, stream, a);
+    }
+}
+
 template <int TYPE> shp_status_t launch_get_rows_sum(const GatherSumArgs & a, bool vec, hipStream_t stream) {
     if (vec) {
         if constexpr (TYPE == SHP_TYPE_Q8_0) {
-            if (a.staged) {
-                const int64_t blocks = (a.frames + kQ8StageWaves - 1) / kQ8StageWaves;
-                switch (a.ne0) {
-                    case 1024:
-                        hipLaunchKernelGGL((k_get_rows_sum_q8s<4, 8>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                                           stream, a);
-                        break;
-                    case 2048:
-                        hipLaunchKernelGGL((k_get_rows_sum_q8s<8, 4>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                                           stream, a);
-                        break;
-                    default:
-                        hipLaunchKernelGGL((k_get_rows_sum_q8s<16, 2>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                                           stream, a);
-                        break;
+            if (q8_staged_width(a.ne0)) {
+                const int ns = a.ne0 / static_cast<int>(kQ8SlabElems);
+                if (ns == 1) {
+                    launch_q8w<1>(a, stream);
+                } else if (ns == 2) {
+                    launch_q8w<2>(a, stream);
+                } else {
+                    launch_q8w<4>(a, stream);
                 }
                 return launch_status();
             }
@@ -792,10 +852,6 @@ template <int TYPE> shp_status_t launch_get_rows_sum(const GatherSumArgs & a, bo
     return launch_status();
 }
 
-// Q8_0 widths the LDS-staged kernels take (one wave per row, NQ = ne0/256).
-bool q8_staged_width(int64_t ne0) {
-    return ne0 == 1024 || ne0 == 2048 || ne0 == 4096;
-}
 
 bool gather_type_ok(int32_t t) {
     return t == SHP_TYPE_F32 || t == SHP_TYPE_F16 || t == SHP_TYPE_BF16 || t == SHP_TYPE_Q8_0;
@@ -860,6 +916,27 @@ extern "C" shp_status_t shp_get_rows(const shp_tensor * src,
     }
 }
 
+// kQ8NegZeroRow's address on the current device (each device holds its own
+// copy), looked up once per device; null if HIP reports an error.
+const char * q8_neg_zero_row_address() {
+    constexpr int                    kMaxDevices = 64;
+    static std::atomic<const char *> cache[kMaxDevices];
+    int                              dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        return nullptr;
+    }
+    const char * p = cache[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        void * q = nullptr;
+        if (hipGetSymbolAddress(&q, HIP_SYMBOL(kQ8NegZeroRow)) != hipSuccess || q == nullptr) {
+            return nullptr;
+        }
+        p = static_cast<const char *>(q);
+        cache[dev].store(p, std::memory_order_release);
+    }
+    return p;
+}
+
 extern "C" shp_status_t shp_get_rows_sum(const shp_tensor * tables,
                                          int32_t            n_tables,
                                          const shp_tensor * ids,
@@ -903,16 +980,16 @@ extern "C" shp_status_t shp_get_rows_sum(const shp_tensor * tables,
               static_cast<uint64_t>(t.ne[1]) * t.nb[1] < (uint64_t{ 1 } << 31);
     }
     if (q8h) {
-        a.staged = q8_staged_width(ne0) && rows_aligned(*dst, 16);
-        for (int g = 0; g < n_tables; ++g) {
-            a.staged = a.staged && reinterpret_cast<uintptr_t>(tables[g].data) % 16 == 0;
+        const char * zero = q8_neg_zero_row_address();
+        if (zero == nullptr) {
+            return SHP_ERR_BACKEND;
         }
-        a.rowbytes = static_cast<uint32_t>(row_bytes(type, ne0));
         for (int g = 0; g < kMaxGroups; ++g) {
-            const int src = g < n_tables ? g : 0;
-            a.rows32[g]   = static_cast<uint32_t>(tables[src].ne[1]);
-            if (g >= n_tables) {
-                a.tab[g] = a.tab[0];
+            const bool live = g < n_tables;
+            a.rows32[g]     = static_cast<uint32_t>(tables[live ? g : 0].ne[1]);
+            a.rstride[g]    = live ? static_cast<uint32_t>(row_bytes(type, ne0)) : 0u;
+            if (!live) {
+                a.tab[g] = zero;
             }
         }
     }

@@ -73,6 +73,71 @@ SHP_HD inline uint32_t q8_half_quads(const uint32_t (&w)[6], const Q8HalfPos & p
 }
 
 // ---------------------------------------------------------------------------
+// Five-dword windows (the gather->sum over 1024-element slabs).
+//
+// Lane l again owns half h = l & 1 of block b = l >> 1 of a 1088-byte slab,
+// with quants at qs = 34b + 2 + 16h, but reads one window of five aligned
+// dwords [base, base + 20), base = (qs - 2) & ~3: the quants are bytes
+// shift..shift+15 of it, shift = qs - base, which is 2 (qs = 2 mod 4) or 4
+// (qs = 0 mod 4). Quant dword i is bytes shift..shift+3 of w[i+1]:w[i], one
+// v_perm_b32 with a per-lane selector. For the even lane (h = 0) the window
+// starts at d or two bytes before it, so w[0] holds d -- in its high half
+// exactly when shift is 4; the odd lane of the pair has the same b, the same
+// shift, and takes w[0] from its even neighbour. Every window lies inside
+// [34b - 2, 34b + 34), so inside the slab: lane 0 starts at byte 0 and lane 63
+// ends at byte 1088.
+// ---------------------------------------------------------------------------
+
+constexpr uint32_t kQ8SlabElems = 1024;
+constexpr uint32_t kQ8SlabBytes = kQ8SlabElems / kQ8BlockElems * kQ8BlockBytes;  // 1088
+
+struct Q8WinPos {
+    uint32_t base;  // byte offset of the window in the slab (4-aligned)
+    uint32_t sel;   // v_perm_b32 selector: bytes 2..5 or 4..7 of hi:lo
+    uint32_t dsh;   // bit shift of d within the (even lane's) w[0]: 0 or 16
+};
+
+SHP_HD inline Q8WinPos q8_win_pos(int l) {
+    const uint32_t b     = static_cast<uint32_t>(l) >> 1;
+    const uint32_t qs    = kQ8BlockBytes * b + 2u + 16u * (static_cast<uint32_t>(l) & 1u);
+    const uint32_t base  = (qs - 2u) & ~3u;
+    const bool     four  = qs - base == 4u;
+    return Q8WinPos{ base, four ? 0x07060504u : 0x05040302u, four ? 16u : 0u };
+}
+
+// Four slabs of a Q8_0 row whose every block is d = -0.0 (f16 0x8000) and 32
+// zero quants: a window of it decodes to 0 * -0.0 = -0.0, and acc + -0.0 ==
+// acc for every f32 acc (including -0.0 and NaN), so a gather->sum slot that
+// reads it adds nothing. Two blocks are 68 bytes = 17 dwords: d of the first
+// is the low half of dword 0, d of the second the high half of dword 8.
+struct Q8NegZeroRow {
+    uint32_t w[4 * kQ8SlabBytes / 4];
+};
+
+SHP_HD constexpr Q8NegZeroRow q8_neg_zero_row() {
+    Q8NegZeroRow r{};
+    for (uint32_t i = 0; i < 4 * kQ8SlabBytes / 4; ++i) {
+        r.w[i] = i % 17u == 0u ? 0x00008000u : (i % 17u == 8u ? 0x80000000u : 0u);
+    }
+    return r;
+}
+
+// Bytes of hi:lo (lo = bytes 0..3) picked by the four selector bytes (each
+// 0..7): one v_perm_b32 on the device.
+SHP_HD inline uint32_t perm_bytes(uint32_t hi, uint32_t lo, uint32_t sel) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_amdgcn_perm(hi, lo, sel);
+#else
+    const uint64_t v = (static_cast<uint64_t>(hi) << 32) | lo;
+    uint32_t       r = 0;
+    for (int i = 0; i < 4; ++i) {
+        r |= static_cast<uint32_t>((v >> (8u * ((sel >> (8 * i)) & 7u))) & 0xffu) << (8 * i);
+    }
+    return r;
+#endif
+}
+
+// ---------------------------------------------------------------------------
 // LDS-staged rows (ne0 = 1024, 2048, 4096; rows 16-byte aligned).
 //
 // A wave copies one row (68 dwords per 256 elements) into a private LDS

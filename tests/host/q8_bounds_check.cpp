@@ -8,7 +8,9 @@
 //      read directly.
 // The row is filled with random bytes and placed at the very end of a buffer
 // followed by guard bytes that no read may touch. Also checks the block-pair
-// reads (68 bytes at 68*bp) of the other widths that are multiples of 64.
+// reads (68 bytes at 68*bp) of the other widths that are multiples of 64, the
+// LDS-staged quads, and the gather->sum's five-dword windows per 1024-element
+// slab.
 // Prints "<lanes checked> <failures>" and exits non-zero on any failure.
 #include <cstdint>
 #include <cstdio>
@@ -145,6 +147,74 @@ static void check_quads(int ne0, std::mt19937 & rng) {
     }
 }
 
+// Five-dword windows of the gather->sum: every lane of every 1088-byte slab
+// of the row reads [base, base + 20) inside its slab (hence the row); the
+// even lane of each pair finds d at dsh in its own w[0], which the odd lane
+// borrows; perm_bytes(w[i+1], w[i], sel) are the lane's 16 quants.
+static void check_windows(int ne0, std::mt19937 & rng) {
+    const uint32_t rowbytes = static_cast<uint32_t>(ne0 / 32) * shp::kQ8BlockBytes;
+    std::vector<uint8_t> buf(rowbytes);
+    for (auto & b : buf) {
+        b = static_cast<uint8_t>(rng());
+    }
+    for (int s = 0; s < ne0 / static_cast<int>(shp::kQ8SlabElems); ++s) {
+        const uint32_t slab0 = static_cast<uint32_t>(s) * shp::kQ8SlabBytes;
+        uint32_t       w0_even = 0;
+        for (int l = 0; l < 64; ++l) {
+            ++checked;
+            const shp::Q8WinPos p = shp::q8_win_pos(l);
+            bool                ok = p.base + 20u <= shp::kQ8SlabBytes;
+            uint32_t            w[5];
+            for (int i = 0; i < 5 && ok; ++i) {
+                w[i] = load_dword(buf, 0, slab0 + p.base + 4u * i, rowbytes, ne0, l, ok);
+            }
+            if (!ok) {
+                fail("window outside the slab", ne0, l);
+                continue;
+            }
+            if ((l & 1) == 0) {
+                w0_even = w[0];
+            }
+            const int       b     = s * 32 + (l >> 1);
+            const int       h     = l & 1;
+            const uint8_t * blk   = buf.data() + static_cast<size_t>(b) * shp::kQ8BlockBytes;
+            const uint32_t  dbits = static_cast<uint32_t>(blk[0]) | (static_cast<uint32_t>(blk[1]) << 8);
+            if (((w0_even >> p.dsh) & 0xffffu) != dbits) {
+                fail("window scale bits", ne0, l);
+            }
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t q = shp::perm_bytes(w[i + 1], w[i], p.sel);
+                for (int k = 0; k < 4; ++k) {
+                    if (static_cast<uint8_t>(q >> (8 * k)) != blk[2 + 16 * h + 4 * i + k]) {
+                        fail("window quant byte", ne0, l);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// The row read for gather->sum slots past the last group: every block of its
+// four slabs is d = -0.0 (f16 0x8000) and 32 zero quants.
+static void check_neg_zero_row() {
+    constexpr shp::Q8NegZeroRow r = shp::q8_neg_zero_row();
+    const uint8_t *             b = reinterpret_cast<const uint8_t *>(r.w);
+    for (uint32_t blk = 0; blk < 4 * shp::kQ8SlabElems / shp::kQ8BlockElems; ++blk) {
+        ++checked;
+        const uint8_t * p = b + blk * shp::kQ8BlockBytes;
+        bool            ok = p[0] == 0x00 && p[1] == 0x80;
+        for (int i = 2; i < 34; ++i) {
+            ok = ok && p[i] == 0;
+        }
+        if (!ok) {
+            fail("negative-zero row block", 4096, static_cast<int>(blk));
+        }
+    }
+    if (sizeof(r.w) != 4 * shp::kQ8SlabBytes) {
+        fail("negative-zero row size", 4096, -1);
+    }
+}
+
 static void check_pairs(int ne0) {
     const uint32_t rowbytes = static_cast<uint32_t>(ne0 / 32) * shp::kQ8BlockBytes;
     for (int bp = 0; bp < ne0 / 64; ++bp) {
@@ -166,8 +236,10 @@ int main() {
     for (int ne0 : { 1024, 2048, 4096 }) {
         for (int rep = 0; rep < 4; ++rep) {
             check_quads(ne0, rng);
+            check_windows(ne0, rng);
         }
     }
+    check_neg_zero_row();
     for (int ne0 : { 64, 128, 192, 320, 3072, 6144 }) {
         check_pairs(ne0);
     }

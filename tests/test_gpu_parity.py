@@ -239,6 +239,32 @@ def test_get_rows_sum_order_matters_and_nan_on_bad_id(gpu):
     assert_bitexact(np.delete(out, 5, 0), np.delete(fwd, 5, 0))
 
 
+@pytest.mark.parametrize("ne0,groups", [(1024, 16), (1024, 15), (2048, 9), (4096, 3), (512, 7), (1024, 20)])
+def test_get_rows_sum_q8_special_scales_and_signed_zero(gpu, ne0, groups):
+    """Q8_0 gather->sum over scales -0, +0, negative, f16-subnormal and the
+    largest f16, with quants +-127/-128/0, bit for bit against the ordered f32
+    sum. Row 0 of every table is all-zero quants under d = -0, so frame 0
+    (every group on row 0) sums to -0.0 in every element: one +0 slipped into
+    the chain (say, from a slot past the last group) would flip it to +0. The
+    group counts leave 0, 1, 7, 5 and 12 slots past the last group."""
+    rng = np.random.default_rng(SEED + 77 + ne0 + groups)
+    rows, nb = 40, ne0 // 32
+    specials = np.array([0x8000, 0x0000, 0x8C00, 0x0003, 0x7BFF, 0x2E66, 0xBC00, 0x0400], np.uint16)
+    tabs = []
+    for _ in range(groups):
+        d = specials[rng.integers(0, len(specials), (rows, nb))]
+        qs = rng.integers(-128, 128, (rows, nb, 32)).astype(np.int8)
+        qs[:, :, :3] = [127, -128, 0]
+        d[0], qs[0] = 0x8000, 0
+        tabs.append(F.q8_0_pack(d, qs))
+    codes = rng.integers(0, rows, (groups, 33)).astype(np.int32)
+    codes[:, 0] = 0
+    ref = R.run(lambda g: R.sum_code_embeddings(g, tabs, R.Q8_0, ne0, codes))
+    assert (ref[0].view(np.uint32) == 0x80000000).all()
+    got = _np(gpu.get_rows_sum([gpu.Q8Tensor(_t(gpu, t), ne0) for t in tabs], _t(gpu, codes)))
+    assert_bitexact(got, ref)
+
+
 # ---------------------------------------------------------------------------
 # norms and rope
 # ---------------------------------------------------------------------------
@@ -909,8 +935,9 @@ def test_q8_last_row_at_end_of_allocation(gpu):
 @pytest.mark.parametrize("ne0", [1024, 2048])
 def test_q8_unaligned_table_and_bad_id_in_sum(gpu, ne0):
     """A Q8_0 table view that starts 4 bytes into its allocation (4-byte but not
-    16-byte aligned rows) takes the register-decode kernels instead of the
-    LDS-staged ones and still matches bit for bit; an out-of-range id in one
+    16-byte aligned rows) takes the register-decode get_rows instead of the
+    LDS-staged one, and the gather->sum's windows at 4-byte alignment, and
+    still matches bit for bit; an out-of-range id in one
     group of a Q8_0 gather->sum turns that frame into NaN and leaves the
     others exact."""
     import torch
