@@ -237,16 +237,22 @@ def cpu_baseline(step, torch, seconds):
     probe = g.time(nth, 1, 1)[0]
     reps = int(max(3, min(400, 0.5 * seconds / max(probe, 1e-6))))
     t_many = statistics.median(g.time(nth, 2, reps))
+    # max(1, N/2) threads is the reference's default CPU parallelism
+    # (cpu-parallelism.h:21-39); N and 1 bracket it.
+    half = max(1, nth // 2)
+    t_half = statistics.median(g.time(half, 1, max(3, reps // 2)))
     probe1 = g.time(1, 0, 1)[0]
-    reps1 = int(max(2, min(100, 0.5 * seconds / max(probe1, 1e-6))))
+    reps1 = int(max(2, min(100, 0.25 * seconds / max(probe1, 1e-6))))
     t_one = statistics.median(g.time(1, 1, reps1))
+    gbs = lambda t: step.step_bytes / t / 1e9
     return {
-        "value": round(step.step_bytes / t_many / 1e9, 2), "unit": "GB/s", "cores": nth, "kind": "port",
+        "value": round(gbs(t_many), 2), "unit": "GB/s", "cores": nth, "kind": "port",
         "sample": "the same configs[1] prefill step (gather + norm + qk-norm/rope + add/norm + swiglu + add, "
                   "%d ggml nodes) on the ggml-CPU restatement, median of %d reps at %d threads; "
-                  "1 thread: %.2f GB/s (median of %d)" % (len(g.nodes), reps, nth, step.step_bytes / t_one / 1e9,
-                                                          reps1),
-        "ms_per_step": round(t_many * 1e3, 3), "value_1thread": round(step.step_bytes / t_one / 1e9, 3),
+                  "%d threads (the reference's default, N/2): %.2f GB/s; 1 thread: %.2f GB/s (median of %d)" % (
+                      len(g.nodes), reps, nth, half, gbs(t_half), gbs(t_one), reps1),
+        "ms_per_step": round(t_many * 1e3, 3), "value_half_threads": round(gbs(t_half), 3), "half_threads": half,
+        "value_1thread": round(gbs(t_one), 3),
     }
 
 

@@ -72,7 +72,16 @@ def assert_close(got, ref, tol=REL_TOL):
     worst = rel.max()
     assert worst <= tol, "max rel err %.3g at %s (got %r ref %r)" % (
         worst, np.unravel_index(rel.argmax(), rel.shape), got.flat[rel.argmax()], ref.flat[rel.argmax()])
+    assert normwise(got, ref) <= tol
     return float(worst), float((got == ref).mean())
+
+
+def normwise(got, ref):
+    """||got - ref|| / ||ref|| (2-norms over the whole tensor, in double)."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    n = np.linalg.norm(ref)
+    return float(np.linalg.norm(got - ref) / (n if n > 0 else 1.0))
 
 
 def assert_snake_close(got, ref, x, tol=REL_TOL):
@@ -964,3 +973,61 @@ def test_q8_unaligned_table_and_bad_id_in_sum(gpu, ne0):
     assert np.isnan(out[7]).all() and np.isnan(out[9]).all()
     keep = [f for f in range(50) if f not in (7, 9)]
     assert_bitexact(out[keep], ref[keep])
+
+
+def test_float_parity_report(gpu):
+    """The floating-point ops at their configs[1]/[3] shapes: the worst
+    elementwise relative error (floored as in assert_close, or pair-relative for
+    rope), the normwise error ||got - ref|| / ||ref|| and the share of outputs
+    bit-identical to the ggml-CPU restatement, each held to the 1e-5 bar. With
+    SHP_PARITY_REPORT set, the figures are also written there as JSON."""
+    rng = np.random.default_rng(SEED + 4242)
+    eps, theta = np.float32(1e-6), np.float32(1e6)
+    rows = []
+
+    def record(op, shape, got, ref, pair_dims=None):
+        if pair_dims:
+            worst = assert_rope_close(got, ref, pair_dims)
+        else:
+            worst, _ = assert_close(got, ref)
+        nw = normwise(got, ref)
+        assert nw <= REL_TOL
+        rows.append({"op": op, "shape": list(shape), "max_rel": worst, "normwise": nw,
+                     "bit_identical": float((np.asarray(got, np.float32).view(np.uint32) ==
+                                             np.asarray(ref, np.float32).view(np.uint32)).mean())})
+
+    x = rng.standard_normal((512, 1024)).astype(np.float32)
+    w, wt = _weights(rng, 1024, "bf16")
+    record("rms_norm_mul", x.shape, _np(gpu.rms_norm_mul(_t(gpu, x), _dev_w(gpu, w, "bf16"), eps)),
+           R.run(lambda g: R.rms_norm_w(g, x, w, eps, wt)))
+    b = rng.standard_normal((512, 1024)).astype(np.float32)
+    _, y_ref = R.run(lambda g: R.add_rms_norm_w(g, x, b, w, eps, wt))
+    _, y = gpu.add_rms_norm_mul(_t(gpu, x), _t(gpu, b), _dev_w(gpu, w, "bf16"), eps)
+    record("add_rms_norm_mul", x.shape, _np(y), y_ref)
+    q = rng.standard_normal((512, 16, 128)).astype(np.float32)
+    k = rng.standard_normal((512, 8, 128)).astype(np.float32)
+    wq, _ = _weights(rng, 128, "bf16")
+    wk, _ = _weights(rng, 128, "bf16")
+    pos = np.arange(512, dtype=np.int32)
+    qr, kr = R.run(lambda g: R.qk_norm_rope(g, q, k, wq, wk, eps, pos, 128, theta, R.BF16))
+    qo, ko = gpu.qk_norm_rope(_t(gpu, q), _t(gpu, k), _dev_w(gpu, wq, "bf16"), _dev_w(gpu, wk, "bf16"), eps,
+                              _t(gpu, pos), 128, theta)
+    record("qk_norm_rope q", q.shape, _np(qo), qr, 128)
+    record("qk_norm_rope k", k.shape, _np(ko), kr, 128)
+    gt = rng.standard_normal((512, 3072)).astype(np.float32)
+    up = rng.standard_normal((512, 3072)).astype(np.float32)
+    record("swiglu", gt.shape, _np(gpu.swiglu(_t(gpu, gt), _t(gpu, up))), R.run(lambda g: R.swiglu(g, gt, up)))
+    xs = rng.standard_normal((8192, 512)).astype(np.float32)
+    alpha = np.exp(rng.uniform(np.log(0.1), np.log(10.0), 512)).astype(np.float32)
+    record("snake", xs.shape, _np(gpu.snake(_t(gpu, xs), _t(gpu, alpha))), R.run(lambda g: R.snake(g, xs, alpha)))
+    s_ = rng.standard_normal((16, 512, 512)).astype(np.float32) * 3
+    m = np.zeros((512, 512), np.float32)
+    m[np.triu_indices(512, 1, 512)] = -np.inf
+    scale = np.float32(1.0) / np.sqrt(np.float32(128))
+    record("soft_max_ext causal", s_.shape, _np(gpu.soft_max_ext(_t(gpu, s_), _t(gpu, m), scale)),
+           R.run(lambda g: g.soft_max_ext(s_, m, scale)))
+    out = os.environ.get("SHP_PARITY_REPORT")
+    if out:
+        with open(out, "w") as f:
+            json.dump(rows, f, indent=1)
+
