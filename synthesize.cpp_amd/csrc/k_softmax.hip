@@ -47,6 +47,14 @@ struct SoftMaxArgs {
     int64_t       ne2;   // heads
     int32_t       ne0;
     float         scale;
+    // Every row index and mask extent below 2^32: the mask row's indices come
+    // from multiply-shift divisions (FastDiv) instead of 64-bit divisions.
+    int32_t       mfast;
+    int32_t       pad;
+    FastDiv       fne1;
+    FastDiv       fne2;
+    FastDiv       fmne2;
+    FastDiv       fmne3;
 };
 
 constexpr int kSoftMaxWaveMax = 2048;  // widest row of the one-wave kernel
@@ -59,11 +67,16 @@ __device__ __forceinline__ float exp_f32_lds(float x, const double * tab) {
     return exp_f32_rn(x, [tab](int j) { return tab[j]; });
 }
 
-// Fills the calling wave's 64-entry table (lane l writes entry l) and makes it
-// visible to the whole wave.
-__device__ __forceinline__ const double * wave_exp_table(double (*s_tab)[64], int lane) {
+// Fills the calling wave's 64-entry table with the entries the lanes loaded
+// (lane l holds entry l) and makes it visible to the whole wave. The entry is
+// loaded (exp_table_entry) before the row, so both are in flight together.
+__device__ __forceinline__ double exp_table_entry(int lane) {
+    return kExpTable[lane];
+}
+
+__device__ __forceinline__ const double * wave_exp_table(double (*s_tab)[64], int lane, double entry) {
     double * t = s_tab[threadIdx.x / kWave];
-    t[lane]    = kExpTable[lane];
+    t[lane]    = entry;
     __syncwarp();
     return t;
 }
@@ -76,6 +89,14 @@ __device__ __forceinline__ float exp_f32(float x) {
 // Mask row of score row r = (i1, i2, i3): ggml's i11 = i1, i12 = i2 % ne12,
 // i13 = i3 % ne13.
 __device__ __forceinline__ const float * mask_row(const SoftMaxArgs & a, int64_t r) {
+    if (a.mfast) {
+        const uint32_t q  = fastdiv(static_cast<uint32_t>(r), a.fne1);
+        const uint32_t i1 = static_cast<uint32_t>(r) - q * a.fne1.d;
+        const uint32_t i3 = fastdiv(q, a.fne2);
+        const uint32_t i2 = q - i3 * a.fne2.d;
+        return reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.mask) + i1 * a.mnb1 +
+                                               fastmod(i2, a.fmne2) * a.mnb2 + fastmod(i3, a.fmne3) * a.mnb3);
+    }
     const int64_t i1 = r % a.ne1;
     const int64_t q  = r / a.ne1;
     const int64_t i2 = q % a.ne2;
@@ -96,7 +117,8 @@ __device__ __forceinline__ float wave_max(float v) {
 template <int K, bool MASK> __global__ __launch_bounds__(256) void k_soft_max_wave(const SoftMaxArgs a) {
     __shared__ double s_tab[256 / kWave][64];
     const int     lane = threadIdx.x % kWave;
-    const int64_t r    = static_cast<int64_t>(blockIdx.x) * (256 / kWave) + threadIdx.x / kWave;
+    const int64_t r    = static_cast<int64_t>(blockIdx.x) * (256 / kWave) +
+                      __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
     if (r >= a.nrows) {
         return;  // whole wave
     }
@@ -105,14 +127,25 @@ template <int K, bool MASK> __global__ __launch_bounds__(256) void k_soft_max_wa
     const float * mr = MASK ? mask_row(a, r) : nullptr;
     float         w[K];
     float         mk[K];
+    // The exp table's entry is loaded with the row. Loads are unconditional
+    // (a lane past the row re-reads element 0) and out-of-row values are
+    // zeroed by selects afterwards: a guarded load becomes a branch with a
+    // wait of its own.
+    const double entry = exp_table_entry(lane);
 #pragma unroll
     for (int k = 0; k < K; ++k) {
         const int i = lane + kWave * k;
-        w[k]        = i < a.ne0 ? xr[i] : 0.0f;
-        mk[k]       = MASK && i < a.ne0 ? mr[i] : 0.0f;
+        w[k]        = xr[i < a.ne0 ? i : 0];
+        mk[k]       = MASK ? mr[i < a.ne0 ? i : 0] : 0.0f;
     }
-    const double * tab = wave_exp_table(s_tab, lane);
-    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const bool in = lane + kWave * k < a.ne0;
+        w[k]          = in ? w[k] : 0.0f;
+        mk[k]         = in ? mk[k] : 0.0f;
+    }
+    const double * tab = wave_exp_table(s_tab, lane, entry);
+    float          mx  = -INFINITY;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
         const int i = lane + kWave * k;
@@ -153,8 +186,8 @@ template <int WPR, int K4, bool MASK> __global__ __launch_bounds__(256) void k_s
     __shared__ double s_tab[256 / kWave][64];
     const int     lane = threadIdx.x % kWave;
     const int     q    = threadIdx.x % kLanes;
-    const int     slot = threadIdx.x / kLanes;  // row of this block
-    const int     wv   = threadIdx.x / kWave;
+    const int     wv   = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    const int     slot = wv / WPR;  // row of this block
     const int64_t r    = static_cast<int64_t>(blockIdx.x) * (256 / kLanes) + slot;
     const bool    live = r < a.nrows;
     if (WPR == 1 && !live) {
@@ -168,13 +201,24 @@ template <int WPR, int K4, bool MASK> __global__ __launch_bounds__(256) void k_s
     const int     n4 = live ? a.ne0 / 4 : 0;
     f32x4         w[K4];
     f32x4         mk[K4];
+    // The exp table's entry is loaded with the row, so it is not a round trip
+    // of its own. Loads are unconditional (a lane past the row re-reads chunk
+    // 0 of row rr), zeroed by selects afterwards: a guarded load becomes a
+    // branch with a wait of its own.
+    const double entry = exp_table_entry(lane);
 #pragma unroll
     for (int k = 0; k < K4; ++k) {
         const int c = q + kLanes * k;
-        w[k]        = c < n4 ? xr[c] : splat4(0.0f);
-        mk[k]       = MASK && c < n4 ? mr[c] : splat4(0.0f);
+        w[k]        = xr[c < n4 ? c : 0];
+        mk[k]       = MASK ? mr[c < n4 ? c : 0] : splat4(0.0f);
     }
-    const double * tab = wave_exp_table(s_tab, lane);
+#pragma unroll
+    for (int k = 0; k < K4; ++k) {
+        const bool in = q + kLanes * k < n4;
+        w[k]          = in ? w[k] : splat4(0.0f);
+        mk[k]         = in ? mk[k] : splat4(0.0f);
+    }
+    const double * tab = wave_exp_table(s_tab, lane, entry);
     float          mx  = -INFINITY;
 #pragma unroll
     for (int k = 0; k < K4; ++k) {
@@ -385,6 +429,14 @@ extern "C" shp_status_t shp_soft_max_ext(const shp_tensor * a,
         g.mnb3 = static_cast<int64_t>(mask->nb[3]);
         g.mne2 = mask->ne[2];
         g.mne3 = mask->ne[3];
+        constexpr int64_t kU32 = int64_t{ UINT32_MAX };
+        g.mfast = g.nrows <= kU32 && g.ne1 <= kU32 && g.ne2 <= kU32 && g.mne2 <= kU32 && g.mne3 <= kU32;
+        if (g.mfast) {
+            g.fne1  = make_fastdiv(static_cast<uint32_t>(g.ne1));
+            g.fne2  = make_fastdiv(static_cast<uint32_t>(g.ne2));
+            g.fmne2 = make_fastdiv(static_cast<uint32_t>(g.mne2));
+            g.fmne3 = make_fastdiv(static_cast<uint32_t>(g.mne3));
+        }
     }
     // float4 rows: every row start of the scores, the output and the mask
     // 16-byte aligned and whole float4s per row
