@@ -65,12 +65,13 @@ struct GatherSumArgs {
     int64_t         frames;
     int32_t         ngroups;
     int32_t         ne0;
-    // Q8_0 kernels only: every table has fewer than 2^31 bytes, so a row
-    // offset is 32-bit: row id * rstride[g]. A slot g past the last group
-    // (the kernels read whole chunks of slots) reads row 0 of kQ8NegZeroRow
-    // (tab[g] = its address, rstride[g] = 0), which adds nothing to the sum,
+    // A slot g past the last group (the kernels read whole chunks of slots)
+    // reads row 0 of a -0.0 row (tab[g] = kQ8NegZeroRow, kNegZeroF32 or
+    // kNegZero16; tnb1[g] = rstride[g] = 0), which adds nothing to the sum,
     // and carries group 0's row count (group 0's id is read for it, so its
     // bounds check repeats group 0's).
+    // Q8_0 kernels only: every table has fewer than 2^31 bytes, so a row
+    // offset is 32-bit: row id * rstride[g].
     uint32_t        rows32[kMaxGroups];
     uint32_t        rstride[kMaxGroups];
 };
@@ -182,6 +183,23 @@ constexpr uint32_t kQNaN = 0x7fc00000u;
 // (shp_q8.hpp: every block d = -0.0, zero quants). Only read; the host passes
 // its address (hipGetSymbolAddress) in the slot's table pointer.
 __device__ Q8NegZeroRow kQ8NegZeroRow = q8_neg_zero_row();
+
+// The same for the F32 / F16 / BF16 gather->sum: rows of up to kSumVecMaxNe0
+// elements that are all -0.0 (f32 0x80000000; f16 and bf16 0x8000 in each
+// half of a dword).
+constexpr int kSumVecMaxNe0 = 2048;
+
+template <uint32_t W> struct NegZeroDwords {
+    uint32_t w[kSumVecMaxNe0];
+    constexpr NegZeroDwords() : w{} {
+        for (int i = 0; i < kSumVecMaxNe0; ++i) {
+            w[i] = W;
+        }
+    }
+};
+
+__device__ __align__(16) NegZeroDwords<0x80000000u> kNegZeroF32;
+__device__ __align__(16) NegZeroDwords<0x80008000u> kNegZero16;
 
 // F32/F16/BF16, 16-byte chunks, LPR lanes per row (up to 256: a 2048-wide
 // BF16 row is one block with one chunk per lane). The id is read first; the
@@ -618,55 +636,110 @@ template <int TYPE> __global__ __launch_bounds__(256) void k_get_rows_generic(co
 // gather -> ordered sum over groups
 // ---------------------------------------------------------------------------
 
-// F32/F16/BF16 sum: lane owns CPL 16-byte chunks of the frame's row.
-template <int TYPE, int CPL> __global__ __launch_bounds__(256) void k_get_rows_sum_vec(const GatherSumArgs a) {
-    constexpr int EPC = elems_per_chunk<TYPE>();
-    const int     l   = threadIdx.x % kWave;
-    const int64_t f   = static_cast<int64_t>(blockIdx.x) * (256 / kWave) + threadIdx.x / kWave;
+// F32/F16/BF16 gather->sum, one wave per frame. Lane l owns the 4-element
+// chunks l + 64j (j < CPL) of the row: one 16-byte (F32) or 8-byte (F16/BF16)
+// load each and one float4 store each, so every load and store instruction
+// of the wave covers one contiguous run. A chunk of G groups costs two round
+// trips: one vector load brings the G ids (lane j reads group j's; readlane
+// makes them scalar), then every group's chunks are requested before the
+// first is added. Group 0 is copied (ggml's acc = rows_0) and the others are
+// added in group order. A slot past the last group reads a row of -0.0
+// (kNegZeroF32 / kNegZero16, the host's pointer and a row stride of 0), and
+// acc + -0.0 == acc for every f32 acc, so the slots cost no branch. (G = 1
+// when there is one group, so its copy is never followed by such an add.)
+template <int TYPE> struct SumChunk {
+    typedef uint2 type;  // four 16-bit values
+};
+
+template <> struct SumChunk<SHP_TYPE_F32> {
+    typedef uint4 type;
+};
+
+template <int TYPE> __device__ __forceinline__ f32x4 cvt_sum_chunk(const typename SumChunk<TYPE>::type & v) {
+    if constexpr (TYPE == SHP_TYPE_F32) {
+        return f32x4{ __uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w) };
+    } else if constexpr (TYPE == SHP_TYPE_BF16) {
+        return f32x4{ bf16_bits_to_f32(v.x & 0xffffu), bf16_bits_to_f32(v.x >> 16), bf16_bits_to_f32(v.y & 0xffffu),
+                      bf16_bits_to_f32(v.y >> 16) };
+    } else {
+        return f32x4{ f16_bits_to_f32(v.x & 0xffffu), f16_bits_to_f32(v.x >> 16), f16_bits_to_f32(v.y & 0xffffu),
+                      f16_bits_to_f32(v.y >> 16) };
+    }
+}
+
+template <int TYPE, int CPL, int G, bool FIRST>
+__device__ __forceinline__ void vsum_chunk(const GatherSumArgs & a, int g0, int64_t f, int n4, f32x4 (&acc)[CPL],
+                                           uint32_t & bad) {
+    typedef typename SumChunk<TYPE>::type Chunk;
+    const int     l   = static_cast<int>(threadIdx.x) % kWave;
+    const int     gl  = (FIRST ? 0 : g0) + l % G;
+    const int32_t ids = group_id(a, gl < a.ngroups ? gl : 0, f);
+    Chunk         v[G][CPL];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        const int     g  = (FIRST ? 0 : g0) + j;
+        const int32_t id = __builtin_amdgcn_readlane(ids, j);
+        const bool    ok = id >= 0 && id < a.trows[g];
+        bad |= ok ? 0u : 1u;
+        const Chunk * row = reinterpret_cast<const Chunk *>(a.tab[g] + static_cast<int64_t>(ok ? id : 0) * a.tnb1[g]);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int i = c * kWave + l;
+            v[j][c]     = row[i < n4 ? i : 0];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const f32x4 o = cvt_sum_chunk<TYPE>(v[j][c]);
+            if (FIRST && j == 0) {
+                acc[c] = o;
+            } else {
+                acc[c] = f32x4{ acc[c].x + o.x, acc[c].y + o.y, acc[c].z + o.z, acc[c].w + o.w };
+            }
+        }
+    }
+}
+
+template <int TYPE, int CPL, int G> __global__ __launch_bounds__(256) void k_get_rows_sum_vec(const GatherSumArgs a) {
+    const int64_t f =
+        static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
     if (f >= a.frames) {
         return;
     }
-    const int nch = a.ne0 / EPC;
-    float     acc[CPL][EPC];
-    bool      bad = false;
-    for (int g = 0; g < a.ngroups; ++g) {
-        const int32_t id = group_id(a, g, f);
-        const bool    ok = id >= 0 && id < a.trows[g];
-        bad              = bad || !ok;
-        const char * row = a.tab[g] + static_cast<int64_t>(ok ? id : 0) * a.tnb1[g];
-        uint4        v[CPL];
+    const int l  = static_cast<int>(threadIdx.x) % kWave;
+    const int n4 = a.ne0 / 4;
+    f32x4     acc[CPL];
+    uint32_t  bad = 0;
+    vsum_chunk<TYPE, CPL, G, true>(a, 0, f, n4, acc, bad);
+    for (int g0 = G; g0 < a.ngroups; g0 += G) {
+        vsum_chunk<TYPE, CPL, G, false>(a, g0, f, n4, acc, bad);
+    }
+    f32x4 * drow = reinterpret_cast<f32x4 *>(reinterpret_cast<char *>(a.dst) + f * a.dnb1);
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const int c = j * kWave + l;
-            if (c < nch) {
-                v[j] = reinterpret_cast<const uint4 *>(row)[c];
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            float o[EPC];
-            cvt_chunk<TYPE>(v[j], o);
-#pragma unroll
-            for (int k = 0; k < EPC; ++k) {
-                acc[j][k] = g == 0 ? o[k] : acc[j][k] + o[k];
-            }
+    for (int c = 0; c < CPL; ++c) {
+        const int i = c * kWave + l;
+        if (i < n4) {
+            drow[i] = bad != 0 ? splat4(__uint_as_float(kQNaN)) : acc[c];
         }
     }
-    float * drow = reinterpret_cast<float *>(reinterpret_cast<char *>(a.dst) + f * a.dnb1);
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        const int c = j * kWave + l;
-        if (c < nch) {
-#pragma unroll
-            for (int k = 0; k < EPC / 4; ++k) {
-                float4 o = make_float4(acc[j][4 * k], acc[j][4 * k + 1], acc[j][4 * k + 2], acc[j][4 * k + 3]);
-                if (bad) {
-                    const float nan = __uint_as_float(kQNaN);
-                    o               = make_float4(nan, nan, nan, nan);
-                }
-                reinterpret_cast<float4 *>(drow + c * EPC)[k] = o;
-            }
-        }
+}
+
+// Group slots per chunk of the F32/F16/BF16 sum: about 64 VGPRs of loads in
+// flight (CPL chunks of 4 or 2 dwords per group), at most 16.
+template <int TYPE> constexpr int vsum_slots(int cpl) {
+    const int words = cpl * (TYPE == SHP_TYPE_F32 ? 4 : 2);
+    return 64 / words > 16 ? 16 : (64 / words < 1 ? 1 : 64 / words);
+}
+
+template <int TYPE, int CPL> void launch_vsum(const GatherSumArgs & a, hipStream_t stream) {
+    constexpr int G = vsum_slots<TYPE>(CPL);
+    const dim3    grid(static_cast<unsigned>((a.frames + 3) / 4));
+    if (a.ngroups == 1) {
+        hipLaunchKernelGGL((k_get_rows_sum_vec<TYPE, CPL, 1>), grid, dim3(256), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((k_get_rows_sum_vec<TYPE, CPL, G>), grid, dim3(256), 0, stream, a);
     }
 }
 
@@ -832,17 +905,15 @@ template <int TYPE> shp_status_t launch_get_rows_sum(const GatherSumArgs & a, bo
             hipLaunchKernelGGL(k_get_rows_sum_generic<TYPE>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
                                a);
         } else {
-            const int     cpl    = (a.ne0 / elems_per_chunk<TYPE>() + kWave - 1) / kWave;
-            const int64_t blocks = (a.frames + 3) / 4;
+            const int cpl = (a.ne0 / 4 + kWave - 1) / kWave;
             if (cpl <= 1) {
-                hipLaunchKernelGGL((k_get_rows_sum_vec<TYPE, 1>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                                   stream, a);
+                launch_vsum<TYPE, 1>(a, stream);
             } else if (cpl <= 2) {
-                hipLaunchKernelGGL((k_get_rows_sum_vec<TYPE, 2>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                                   stream, a);
+                launch_vsum<TYPE, 2>(a, stream);
+            } else if (cpl <= 4) {
+                launch_vsum<TYPE, 4>(a, stream);
             } else {
-                hipLaunchKernelGGL((k_get_rows_sum_vec<TYPE, 4>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                                   stream, a);
+                launch_vsum<TYPE, 8>(a, stream);
             }
         }
         return launch_status();
@@ -916,23 +987,28 @@ extern "C" shp_status_t shp_get_rows(const shp_tensor * src,
     }
 }
 
-// kQ8NegZeroRow's address on the current device (each device holds its own
-// copy), looked up once per device; null if HIP reports an error.
-const char * q8_neg_zero_row_address() {
+// The address of a -0.0 row (kQ8NegZeroRow, kNegZeroF32 or kNegZero16, by
+// table type) on the current device, where each device holds its own copy;
+// looked up once per device and type; null if HIP reports an error.
+const char * neg_zero_row_address(int32_t type) {
     constexpr int                    kMaxDevices = 64;
-    static std::atomic<const char *> cache[kMaxDevices];
+    static std::atomic<const char *> cache[kMaxDevices][3];
+    const int                        k   = type == SHP_TYPE_Q8_0 ? 0 : (type == SHP_TYPE_F32 ? 1 : 2);
     int                              dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
         return nullptr;
     }
-    const char * p = cache[dev].load(std::memory_order_acquire);
+    const char * p = cache[dev][k].load(std::memory_order_acquire);
     if (p == nullptr) {
-        void * q = nullptr;
-        if (hipGetSymbolAddress(&q, HIP_SYMBOL(kQ8NegZeroRow)) != hipSuccess || q == nullptr) {
+        void *     q  = nullptr;
+        hipError_t rc = k == 0 ? hipGetSymbolAddress(&q, HIP_SYMBOL(kQ8NegZeroRow))
+                               : (k == 1 ? hipGetSymbolAddress(&q, HIP_SYMBOL(kNegZeroF32))
+                                         : hipGetSymbolAddress(&q, HIP_SYMBOL(kNegZero16)));
+        if (rc != hipSuccess || q == nullptr) {
             return nullptr;
         }
         p = static_cast<const char *>(q);
-        cache[dev].store(p, std::memory_order_release);
+        cache[dev][k].store(p, std::memory_order_release);
     }
     return p;
 }
@@ -979,18 +1055,23 @@ extern "C" shp_status_t shp_get_rows_sum(const shp_tensor * tables,
         q8h = t.nb[1] == row_bytes(type, ne0) && t.ne[1] <= INT32_MAX &&
               static_cast<uint64_t>(t.ne[1]) * t.nb[1] < (uint64_t{ 1 } << 31);
     }
+    // Slots past the last group (the kernels read whole chunks of slots):
+    // a -0.0 row with a row stride of 0, group 0's row count (group 0's id is
+    // read for them).
+    const char * zero = neg_zero_row_address(type);
+    if (zero == nullptr) {
+        return SHP_ERR_BACKEND;
+    }
+    for (int g = n_tables; g < kMaxGroups; ++g) {
+        a.tab[g]   = zero;
+        a.tnb1[g]  = 0;
+        a.trows[g] = a.trows[0];
+    }
     if (q8h) {
-        const char * zero = q8_neg_zero_row_address();
-        if (zero == nullptr) {
-            return SHP_ERR_BACKEND;
-        }
         for (int g = 0; g < kMaxGroups; ++g) {
             const bool live = g < n_tables;
             a.rows32[g]     = static_cast<uint32_t>(tables[live ? g : 0].ne[1]);
             a.rstride[g]    = live ? static_cast<uint32_t>(row_bytes(type, ne0)) : 0u;
-            if (!live) {
-                a.tab[g] = zero;
-            }
         }
     }
     a.ids         = static_cast<const int32_t *>(ids->data);
@@ -1006,11 +1087,11 @@ extern "C" shp_status_t shp_get_rows_sum(const shp_tensor * tables,
     const hipStream_t st = as_stream(stream);
     switch (type) {
         case SHP_TYPE_F32:
-            return launch_get_rows_sum<SHP_TYPE_F32>(a, vec && ne0 % 4 == 0 && ne0 <= 4 * 4 * kWave, st);
+            return launch_get_rows_sum<SHP_TYPE_F32>(a, vec && ne0 % 4 == 0 && ne0 <= kSumVecMaxNe0, st);
         case SHP_TYPE_F16:
-            return launch_get_rows_sum<SHP_TYPE_F16>(a, vec && ne0 % 8 == 0 && ne0 <= 8 * 4 * kWave, st);
+            return launch_get_rows_sum<SHP_TYPE_F16>(a, vec && ne0 % 4 == 0 && ne0 <= kSumVecMaxNe0, st);
         case SHP_TYPE_BF16:
-            return launch_get_rows_sum<SHP_TYPE_BF16>(a, vec && ne0 % 8 == 0 && ne0 <= 8 * 4 * kWave, st);
+            return launch_get_rows_sum<SHP_TYPE_BF16>(a, vec && ne0 % 4 == 0 && ne0 <= kSumVecMaxNe0, st);
         default:
             return launch_get_rows_sum<SHP_TYPE_Q8_0>(a, vec && q8h, st);
     }

@@ -248,6 +248,55 @@ def test_get_rows_sum_order_matters_and_nan_on_bad_id(gpu):
     assert_bitexact(np.delete(out, 5, 0), np.delete(fwd, 5, 0))
 
 
+@pytest.mark.parametrize("kind,ne0,groups", [("bf16", 1024, 16), ("bf16", 2048, 15), ("f16", 1024, 3),
+                                             ("f32", 1024, 17), ("f32", 2048, 2), ("bf16", 64, 5),
+                                             ("f16", 12, 40), ("f32", 1020, 9)])
+def test_get_rows_sum_float_tables_special_values(gpu, kind, ne0, groups):
+    """F32/F16/BF16 gather->sum over +-0, subnormals, +inf and ordinary
+    values, bit for bit against the ordered f32 sum (-inf is left out: inf -
+    inf is a NaN whose bits the CPU and the GPU choose differently). Row 0 of
+    every table is
+    all -0.0, so frame 0 (every group on row 0) must stay -0.0: a +0 slipped
+    into the chain (from a slot past the last group, or a sum started at +0)
+    flips it. The group counts leave slots past the last group in every chunk
+    size the kernel picks; widths 12 and 1020 leave lanes past the row."""
+    rng = np.random.default_rng(SEED + 91 + ne0 + groups)
+    rows = 30
+    if kind == "f32":
+        pool = np.array([0.0, -0.0, 1e-40, -3e-42, np.inf, 1.5, -2.25, 3e38], np.float32).view(np.uint32)
+        tabs = [rng.standard_normal((rows, ne0)).astype(np.float32) for _ in range(groups)]
+        for t in tabs:
+            t.view(np.uint32)[:, ::3] = pool[rng.integers(0, len(pool), (rows, len(range(0, ne0, 3))))]
+            t[0] = -0.0
+    else:
+        pool = np.array([0x0000, 0x8000, 0x0001, 0x8003, 0x7C00 if kind == "f16" else 0x7F80,
+                         0x3C00 if kind == "f16" else 0x3F80], np.uint16)
+        conv = F.f32_to_f16_bits if kind == "f16" else F.f32_to_bf16_bits
+        tabs = [conv(rng.standard_normal((rows, ne0)).astype(np.float32)) for _ in range(groups)]
+        for t in tabs:
+            t[:, ::3] = pool[rng.integers(0, len(pool), (rows, len(range(0, ne0, 3))))]
+            t[0] = 0x8000
+    otype = {"f32": R.F32, "f16": R.F16, "bf16": R.BF16}[kind]
+    codes = rng.integers(0, rows, (groups, 41)).astype(np.int32)
+    codes[:, 0] = 0
+    with np.errstate(all="ignore"):
+        ref = R.run(lambda g: R.sum_code_embeddings(g, tabs, otype, ne0, codes))
+    assert (ref[0].view(np.uint32) == 0x80000000).all()
+    got = _np(gpu.get_rows_sum([_dev_table(gpu, t, kind, ne0) for t in tabs], _t(gpu, codes)))
+    assert_bitexact(got, ref)
+
+
+def test_get_rows_sum_one_group_is_a_copy(gpu):
+    """One group: ggml's sum is rows_0 itself, so BF16 NaN payloads, signalling
+    NaNs included, come through bit for bit (an add would quiet them)."""
+    rng = np.random.default_rng(SEED + 93)
+    t = F.f32_to_bf16_bits(rng.standard_normal((20, 1024)).astype(np.float32))
+    t[:, :8] = [0x7F81, 0xFF81, 0x7FC1, 0xFFFF, 0x7F80, 0x8000, 0x0001, 0x7FA5]
+    codes = rng.integers(0, 20, (1, 33)).astype(np.int32)
+    got = _np(gpu.get_rows_sum([_dev_table(gpu, t, "bf16", 1024)], _t(gpu, codes)))
+    assert_bitexact(got, F.bf16_bits_to_f32(t[codes[0]]))
+
+
 @pytest.mark.parametrize("ne0,groups", [(1024, 16), (1024, 15), (2048, 9), (4096, 3), (512, 7), (1024, 20)])
 def test_get_rows_sum_q8_special_scales_and_signed_zero(gpu, ne0, groups):
     """Q8_0 gather->sum over scales -0, +0, negative, f16-subnormal and the
