@@ -199,10 +199,6 @@ template <bool RCP> __device__ __forceinline__ float snake1(float x, float al, f
 // guarded Snake (3-6 % faster than 4), 8 for SnakeBeta, whose two exps per
 // channel then spread over 32 elements (9-11 % faster than 4 at [256,32768]
 // and [128,131072]).
-// Rows per lane, measured on MI355X over the cfg4 shapes: 2 for Snake and the
-// guarded Snake (3-6 % faster than 4), 8 for SnakeBeta, whose two exps per
-// channel then spread over 32 elements (9-11 % faster than 4 at [256,32768]
-// and [128,131072]).
 template <int K> struct SnakeRows {
     static constexpr int R = K == kSnakeBeta ? 8 : 2;
 };
@@ -295,6 +291,59 @@ template <int K> __global__ __launch_bounds__(256) void k_snake_flat(const EwArg
         } else {
             const double rc[4] = { 0.0, 0.0, 0.0, 0.0 };
             snake_rows<K, R, false>(xv, al, den, rc, i0, c4, a.n4, Y);
+        }
+    }
+}
+
+
+// SnakeBeta on tensors of at least kSnakeLdsMinTasks lane tasks and at most
+// kSnakeLdsMaxC channels: each block first evaluates every channel's exp
+// curves, guard and double reciprocal once into LDS, then steps through its
+// share of the tasks (2 rows of one channel quad each, as plain Snake) with
+// a grid stride, so the two exps per channel are spread over the block's
+// whole share instead of 8 rows. Measured on MI355X at [128,131072]: 8 %
+// faster than the 8-row kernel; at [256,32768] and below, where a block's
+// share is only one or two tasks, the table does not pay for itself, and for
+// plain Snake, whose per-channel work is only the reciprocal, the grid stride
+// measured 4-7 % slower than one task per lane.
+constexpr int     kSnakeLdsMaxC     = 1024;
+constexpr int     kSnakeLdsBlocks   = 2048;
+constexpr int64_t kSnakeLdsMinTasks = int64_t{ 4 } * kSnakeLdsBlocks * 256;
+
+__global__ __launch_bounds__(256) void k_snake_beta_lds(const EwArgs a) {
+    __shared__ __align__(16) float  s_al[kSnakeLdsMaxC];
+    __shared__ __align__(16) float  s_den[kSnakeLdsMaxC];
+    __shared__ __align__(16) double s_rc[kSnakeLdsMaxC];
+    const int nc = static_cast<int>(a.quads.d) * 4;
+    for (int c = threadIdx.x; c < nc; c += 256) {
+        const SnakeCoef k = snake_coef<kSnakeBeta>(a.alpha[c], a.beta[c]);
+        s_al[c]           = k.al;
+        s_den[c]          = k.den;
+        s_rc[c]           = rcp_route_ok(k.den) ? rcp_d(static_cast<double>(k.den)) : 0.0;
+    }
+    __syncthreads();
+    constexpr int R    = 2;
+    const f32x4 * X    = reinterpret_cast<const f32x4 *>(a.a);
+    f32x4 *       Y    = reinterpret_cast<f32x4 *>(a.y);
+    const int64_t c4   = a.quads.d;
+    const int64_t step = static_cast<int64_t>(gridDim.x) * 256;
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; t < a.ntask; t += step) {
+        const uint32_t rb = fastdiv(static_cast<uint32_t>(t), a.quads);  // row block
+        const uint32_t q  = static_cast<uint32_t>(t) - rb * a.quads.d;  // channel quad
+        const int64_t  i0 = static_cast<int64_t>(rb) * R * c4 + q;
+        f32x4          xv[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int64_t i = i0 + r * c4;
+            xv[r]           = i < a.n4 ? ld_stream(X + i) : splat4(0.0f);
+        }
+        const f32x4  al    = reinterpret_cast<const f32x4 *>(s_al)[q];
+        const f32x4  den   = reinterpret_cast<const f32x4 *>(s_den)[q];
+        const double rc[4] = { s_rc[4 * q], s_rc[4 * q + 1], s_rc[4 * q + 2], s_rc[4 * q + 3] };
+        if (rcp_route_ok(den.x) && rcp_route_ok(den.y) && rcp_route_ok(den.z) && rcp_route_ok(den.w)) {
+            snake_rows<kSnakeBeta, R, true>(xv, al, den, rc, i0, c4, a.n4, Y);
+        } else {
+            snake_rows<kSnakeBeta, R, false>(xv, al, den, rc, i0, c4, a.n4, Y);
         }
     }
 }
@@ -569,6 +618,16 @@ shp_status_t launch_snake(const shp_tensor * x, const shp_tensor * c0, const shp
     g.beta     = K == kSnakeBeta ? static_cast<const float *>(c1->data) : nullptr;
     const bool c16 =
         reinterpret_cast<uintptr_t>(g.alpha) % 16 == 0 && reinterpret_cast<uintptr_t>(g.beta) % 16 == 0;
+    if (K == kSnakeBeta && plan.flat && c16 && x->ne[0] <= kSnakeLdsMaxC) {
+        const int64_t quads = x->ne[0] / 4;
+        const int64_t ntask = (g.n4 / quads + 1) / 2 * quads;
+        if (ntask >= kSnakeLdsMinTasks && ntask <= UINT32_MAX) {
+            g.quads = make_fastdiv(static_cast<uint32_t>(quads));
+            g.ntask = ntask;
+            hipLaunchKernelGGL(k_snake_beta_lds, dim3(kSnakeLdsBlocks), dim3(256), 0, stream, g);
+            return launch_status();
+        }
+    }
     if (plan.flat && c16) {
         constexpr int R      = SnakeRows<K>::R;
         const int64_t quads  = x->ne[0] / 4;

@@ -731,6 +731,23 @@ def test_snake_beta(gpu, T, C):
     assert_snake_close(_np(gpu.snake_beta(_t(gpu, x), _t(gpu, la), _t(gpu, lb))), ref, x)
 
 
+def test_snake_beta_large_channel_table(gpu):
+    """[128, 131072] is large enough for the kernel that evaluates each
+    channel's curves once per block into LDS (at least 4 lane tasks per lane
+    of a 2048-block grid); rows 0 and 1 carry large x, so some sines leave the
+    fast range, and channels 0-3 hold extreme curves."""
+    rng = np.random.default_rng(SEED + 131)
+    T, C = 131072, 128
+    x = rng.standard_normal((T, C), dtype=np.float32)
+    x[:2, ::5] *= 30000.0
+    la = rng.uniform(-3, 3, C).astype(np.float32)
+    lb = rng.uniform(-3, 3, C).astype(np.float32)
+    la[:4] = [-30.0, 30.0, 0.0, -3.0]
+    lb[:4] = [-30.0, 3.0, 30.0, -25.0]
+    ref = R.run(lambda g: R.snake_beta(g, x, la, lb))
+    assert_snake_close(_np(gpu.snake_beta(_t(gpu, x), _t(gpu, la), _t(gpu, lb))), ref, x)
+
+
 def test_golden_g3_snake_beta_on_gpu(gpu):
     """kExpectedSnakeBeta, tests/qwen3_tts_codec_ops_test.cpp:77-82, at the
     test's CPU tolerance (1e-4, tighter than its 5e-3 for accelerators)."""
