@@ -127,8 +127,10 @@ __global__ __launch_bounds__(256) void k_ew_flat(const EwArgs a) {
     const f32x4 * B    = reinterpret_cast<const f32x4 *>(a.b);
     f32x4 *       Y    = reinterpret_cast<f32x4 *>(a.y);
     f32x4 *       S    = reinterpret_cast<f32x4 *>(a.s);
+    const int64_t n4   = a.n4;
     const int64_t step = static_cast<int64_t>(gridDim.x) * 256;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < a.n4; i += step) {
+    args_in_sgprs(A, B, Y, n4, step);
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n4; i += step) {
         const f32x4 av = ld_stream(A + i);
         f32x4       bv = splat4(0.0f);
         if constexpr (HAS_B) {
@@ -263,6 +265,7 @@ template <int K> __global__ __launch_bounds__(256) void k_snake_flat(const EwArg
     f32x4 *       Y    = reinterpret_cast<f32x4 *>(a.y);
     const int64_t c4   = a.quads.d;
     const int64_t step = static_cast<int64_t>(gridDim.x) * 256;
+    args_in_sgprs(X, C0, C1, a.quads.d, a.quads.m, a.quads.l, a.ntask, a.n4, step);
     for (int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; t < a.ntask; t += step) {
         const uint32_t rb = fastdiv(static_cast<uint32_t>(t), a.quads);  // row block
         const uint32_t q  = static_cast<uint32_t>(t) - rb * a.quads.d;  // channel quad
@@ -314,6 +317,7 @@ __global__ __launch_bounds__(256) void k_snake_beta_lds(const EwArgs a) {
     __shared__ __align__(16) float  s_al[kSnakeLdsMaxC];
     __shared__ __align__(16) float  s_den[kSnakeLdsMaxC];
     __shared__ __align__(16) double s_rc[kSnakeLdsMaxC];
+    args_in_sgprs(a.alpha, a.beta, a.quads.d);
     const int nc = static_cast<int>(a.quads.d) * 4;
     for (int c = threadIdx.x; c < nc; c += 256) {
         const SnakeCoef k = snake_coef<kSnakeBeta>(a.alpha[c], a.beta[c]);
@@ -424,7 +428,13 @@ struct TermArgs {
 template <int N, bool HAS_M, bool VEC> __global__ __launch_bounds__(256) void k_sum_scale_leaky(const TermArgs a) {
     using V            = typename std::conditional<VEC, f32x4, float>::type;
     const int64_t step = static_cast<int64_t>(gridDim.x) * 256;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < a.n; i += step) {
+    const int64_t n    = a.n;
+    args_in_sgprs(n, step);
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        arg_in_sgpr(a.t[j]);
+    }
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += step) {
         V v[N];
 #pragma unroll
         for (int j = 0; j < N; ++j) {

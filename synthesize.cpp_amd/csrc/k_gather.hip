@@ -45,11 +45,13 @@ struct GatherArgs {
     int64_t         dnb3;
     int64_t         n;
     int64_t         ne11;
-    int64_t         total;
+    int64_t         total;   // < 2^32
     int32_t         ne0;
-    int32_t         batched;
     int32_t         staged;  // Q8_0 through LDS: ne0 in {1024, 2048, 4096}, rows 16-byte aligned
-    int32_t         pad;
+    // Output row R = r + n*(i11 + ne11*i12) by multiply-shift divisions, with
+    // no branch on the batch form: an unbatched gather is n = total, ne11 = 1.
+    FastDiv         fn;
+    FastDiv         fne11;
 };
 
 constexpr int kMaxGroups = 64;
@@ -75,32 +77,6 @@ struct GatherSumArgs {
     uint32_t        rows32[kMaxGroups];
     uint32_t        rstride[kMaxGroups];
 };
-
-template <int TYPE> constexpr int elems_per_chunk() {
-    return TYPE == SHP_TYPE_F32 ? 4 : 8;
-}
-
-// Converts one 16-byte chunk of a row into EPC floats.
-template <int TYPE> __device__ __forceinline__ void cvt_chunk(uint4 v, float * o) {
-    if constexpr (TYPE == SHP_TYPE_F32) {
-        o[0] = __uint_as_float(v.x);
-        o[1] = __uint_as_float(v.y);
-        o[2] = __uint_as_float(v.z);
-        o[3] = __uint_as_float(v.w);
-    } else {
-        const uint32_t w[4] = { v.x, v.y, v.z, v.w };
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            if constexpr (TYPE == SHP_TYPE_BF16) {
-                o[2 * k]     = bf16_bits_to_f32(w[k] & 0xffffu);
-                o[2 * k + 1] = bf16_bits_to_f32(w[k] >> 16);
-            } else {
-                o[2 * k]     = f16_bits_to_f32(w[k] & 0xffffu);
-                o[2 * k + 1] = f16_bits_to_f32(w[k] >> 16);
-            }
-        }
-    }
-}
 
 __device__ __forceinline__ float sbyte(uint32_t w, int k) {
     return static_cast<float>(static_cast<int32_t>(w << (24 - 8 * k)) >> 24);
@@ -162,17 +138,20 @@ template <int TYPE> __device__ __forceinline__ float elem(const char * row, int 
     }
 }
 
+// The kernel arguments a gather wave needs before its first load.
+__device__ __forceinline__ void gather_args_in_sgprs(const GatherArgs & a) {
+    args_in_sgprs(a.total, a.ids, a.inb0, a.inb1, a.inb2, a.fn.d, a.fn.m, a.fn.l, a.fne11.d, a.fne11.m, a.fne11.l,
+                  a.src, a.snb1, a.snb2, a.snb3, a.srows, a.ne0);
+}
+
 __device__ __forceinline__ void gather_coords(const GatherArgs & a, int64_t R, int32_t & id, const char *& srow,
                                               float *& drow) {
-    int64_t r = R, i11 = 0, i12 = 0;
-    if (a.batched) {  // ids [n, ne11, ne12]: 64-bit divisions only for the batched form
-        r             = R % a.n;
-        const int64_t q = R / a.n;
-        i11           = q % a.ne11;
-        i12           = q / a.ne11;
-    }
+    const uint32_t q   = fastdiv(static_cast<uint32_t>(R), a.fn);
+    const uint32_t i12 = fastdiv(q, a.fne11);
+    const int64_t  r   = R - static_cast<int64_t>(q) * a.fn.d;
+    const int64_t  i11 = q - i12 * a.fne11.d;
     id   = *reinterpret_cast<const int32_t *>(reinterpret_cast<const char *>(a.ids) + r * a.inb0 + i11 * a.inb1 +
-                                            i12 * a.inb2);
+                                            static_cast<int64_t>(i12) * a.inb2);
     srow = a.src + static_cast<int64_t>(id) * a.snb1 + i11 * a.snb2 + i12 * a.snb3;
     drow = reinterpret_cast<float *>(reinterpret_cast<char *>(a.dst) + r * a.dnb1 + i11 * a.dnb2 + i12 * a.dnb3);
 }
@@ -201,15 +180,54 @@ template <uint32_t W> struct NegZeroDwords {
 __device__ __align__(16) NegZeroDwords<0x80000000u> kNegZeroF32;
 __device__ __align__(16) NegZeroDwords<0x80008000u> kNegZero16;
 
-// F32/F16/BF16, 16-byte chunks, LPR lanes per row (up to 256: a 2048-wide
-// BF16 row is one block with one chunk per lane). The id is read first; the
-// row chunk load depends on it; the f32 output is streamed out with
-// nontemporal stores. Table rows use ordinary loads so that rows gathered
-// again (repeated tokens, a table that fits the Infinity Cache) can hit.
-template <int TYPE, int LPR> __global__ __launch_bounds__(256) void k_get_rows_vec(const GatherArgs a) {
-    constexpr int EPC = elems_per_chunk<TYPE>();
-    const int     l   = threadIdx.x % LPR;
-    const int64_t R   = static_cast<int64_t>(blockIdx.x) * (256 / LPR) + threadIdx.x / LPR;
+// A 4-element chunk of an F32 (16 bytes) or F16/BF16 (8 bytes) row, and its
+// exact conversion to f32.
+template <int TYPE> struct SumChunk {
+    typedef uint2 type;  // four 16-bit values
+};
+
+template <> struct SumChunk<SHP_TYPE_F32> {
+    typedef uint4 type;
+};
+
+template <int TYPE> __device__ __forceinline__ f32x4 cvt_sum_chunk(const typename SumChunk<TYPE>::type & v) {
+    if constexpr (TYPE == SHP_TYPE_F32) {
+        return f32x4{ __uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w) };
+    } else if constexpr (TYPE == SHP_TYPE_BF16) {
+        return f32x4{ bf16_bits_to_f32(v.x & 0xffffu), bf16_bits_to_f32(v.x >> 16), bf16_bits_to_f32(v.y & 0xffffu),
+                      bf16_bits_to_f32(v.y >> 16) };
+    } else {
+        return f32x4{ f16_bits_to_f32(v.x & 0xffffu), f16_bits_to_f32(v.x >> 16), f16_bits_to_f32(v.y & 0xffffu),
+                      f16_bits_to_f32(v.y >> 16) };
+    }
+}
+
+// Row index of this lane's group; for LPR >= 64 every lane of a wave has the
+// same row, which readfirstlane makes visible to the compiler so that the id
+// and the table row base are scalar.
+template <int LPR> __device__ __forceinline__ int row_in_block() {
+    const int r = static_cast<int>(threadIdx.x) / LPR;
+    if constexpr (LPR >= kWave) {
+        return __builtin_amdgcn_readfirstlane(r);
+    } else {
+        return r;
+    }
+}
+
+// F32/F16/BF16 get_rows, LPR lanes per row (up to 256: a 2048-wide BF16 row
+// is one block). Lane l owns the 4-element chunks l + LPR*j (j < CPL): one
+// 16-byte (F32) or 8-byte (F16/BF16) load each and one float4 store each, so
+// each load and store instruction of a wave covers one contiguous run. For
+// LPR >= 64 the row is uniform over the wave, so the id is a scalar load and
+// the row base scalar. The row loads are unconditional (a lane past the row
+// re-reads chunk 0). Table rows use ordinary loads so that rows gathered again
+// (repeated tokens, a table that fits the Infinity Cache) can hit; the f32
+// output is streamed out with nontemporal stores.
+template <int TYPE, int LPR, int CPL> __global__ __launch_bounds__(256) void k_get_rows_vec(const GatherArgs a) {
+    gather_args_in_sgprs(a);
+    typedef typename SumChunk<TYPE>::type Chunk;
+    const int     l = threadIdx.x % LPR;
+    const int64_t R = static_cast<int64_t>(blockIdx.x) * (256 / LPR) + row_in_block<LPR>();
     if (R >= a.total) {
         return;
     }
@@ -217,28 +235,28 @@ template <int TYPE, int LPR> __global__ __launch_bounds__(256) void k_get_rows_v
     const char * srow;
     float *      drow;
     gather_coords(a, R, id, srow, drow);
-    const int nch = a.ne0 / EPC;
-    f32x4 *   out = reinterpret_cast<f32x4 *>(drow);
-    if (id < 0 || id >= a.srows) {
-        const float nan = __uint_as_float(kQNaN);
-        for (int e = l; e < a.ne0 / 4; e += LPR) {
-            st_stream(out + e, splat4(nan));
-        }
-        return;
-    }
-    for (int c = l; c < nch; c += LPR) {
-        const uint4 v = reinterpret_cast<const uint4 *>(srow)[c];
-        float       o[EPC];
-        cvt_chunk<TYPE>(v, o);
+    const bool    ok  = id >= 0 && id < a.srows;
+    const int     n4  = a.ne0 / 4;
+    const Chunk * row = reinterpret_cast<const Chunk *>(ok ? srow : a.src);
+    Chunk         v[CPL];
 #pragma unroll
-        for (int k = 0; k < EPC / 4; ++k) {
-            st_stream(out + c * (EPC / 4) + k, f32x4{ o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3] });
+    for (int j = 0; j < CPL; ++j) {
+        const int c = l + LPR * j;
+        v[j]        = row[c < n4 ? c : 0];
+    }
+    f32x4 * out = reinterpret_cast<f32x4 *>(drow);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int c = l + LPR * j;
+        if (c < n4) {
+            st_stream(out + c, ok ? cvt_sum_chunk<TYPE>(v[j]) : splat4(__uint_as_float(kQNaN)));
         }
     }
 }
 
 // Q8_0, one block pair per lane, LPR lanes per row.
 template <int LPR> __global__ __launch_bounds__(256) void k_get_rows_q8(const GatherArgs a) {
+    gather_args_in_sgprs(a);
     const int     l = threadIdx.x % LPR;
     const int64_t R = static_cast<int64_t>(blockIdx.x) * (256 / LPR) + threadIdx.x / LPR;
     if (R >= a.total) {
@@ -318,20 +336,9 @@ __device__ __forceinline__ void store16(float * dst, const float (&o)[16]) {
     }
 }
 
-// Row index of this lane's group; for LPR >= 64 every lane of a wave has the
-// same row, which readfirstlane makes visible to the compiler so that the id
-// and the table row base are scalar.
-template <int LPR> __device__ __forceinline__ int row_in_block() {
-    const int r = static_cast<int>(threadIdx.x) / LPR;
-    if constexpr (LPR >= kWave) {
-        return __builtin_amdgcn_readfirstlane(r);
-    } else {
-        return r;
-    }
-}
-
 // Q8_0 get_rows: LPR = ne0/16 lanes per row.
 template <int LPR> __global__ __launch_bounds__(256) void k_get_rows_q8h(const GatherArgs a) {
+    gather_args_in_sgprs(a);
     const int64_t R = static_cast<int64_t>(blockIdx.x) * (256 / LPR) + row_in_block<LPR>();
     if (R >= a.total) {
         return;
@@ -482,6 +489,7 @@ __device__ __forceinline__ void q8w_chunk(const GatherSumArgs & a, int g0, int64
 template <int NS, int G>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_get_rows_sum_q8w(
     const GatherSumArgs a) {
+    args_in_sgprs(a.frames, a.ids, a.ids_gstride, a.ngroups);
     __shared__ f32x4 s_out[4][kQ8SlabElems / 4];  // one slab per wave, for the store transpose
     const int     wi = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
     const int64_t wv = static_cast<int64_t>(blockIdx.x) * 4 + wi;
@@ -589,6 +597,7 @@ template <int NQ> __device__ __forceinline__ void q8_row_store(float * drow, int
 constexpr int kQ8StageWaves = 4;  // waves (rows or frames) per 256-thread block
 
 template <int NQ> __global__ __launch_bounds__(256) void k_get_rows_q8s(const GatherArgs a) {
+    gather_args_in_sgprs(a);
     __shared__ uint32_t s_row[kQ8StageWaves][q8_row_dwords(NQ) + kQ8StagePadDwords];
     const int           w = static_cast<int>(threadIdx.x) / kWave;
     const int           l = static_cast<int>(threadIdx.x) % kWave;
@@ -647,26 +656,6 @@ template <int TYPE> __global__ __launch_bounds__(256) void k_get_rows_generic(co
 // (kNegZeroF32 / kNegZero16, the host's pointer and a row stride of 0), and
 // acc + -0.0 == acc for every f32 acc, so the slots cost no branch. (G = 1
 // when there is one group, so its copy is never followed by such an add.)
-template <int TYPE> struct SumChunk {
-    typedef uint2 type;  // four 16-bit values
-};
-
-template <> struct SumChunk<SHP_TYPE_F32> {
-    typedef uint4 type;
-};
-
-template <int TYPE> __device__ __forceinline__ f32x4 cvt_sum_chunk(const typename SumChunk<TYPE>::type & v) {
-    if constexpr (TYPE == SHP_TYPE_F32) {
-        return f32x4{ __uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w) };
-    } else if constexpr (TYPE == SHP_TYPE_BF16) {
-        return f32x4{ bf16_bits_to_f32(v.x & 0xffffu), bf16_bits_to_f32(v.x >> 16), bf16_bits_to_f32(v.y & 0xffffu),
-                      bf16_bits_to_f32(v.y >> 16) };
-    } else {
-        return f32x4{ f16_bits_to_f32(v.x & 0xffffu), f16_bits_to_f32(v.x >> 16), f16_bits_to_f32(v.y & 0xffffu),
-                      f16_bits_to_f32(v.y >> 16) };
-    }
-}
-
 template <int TYPE, int CPL, int G, bool FIRST>
 __device__ __forceinline__ void vsum_chunk(const GatherSumArgs & a, int g0, int64_t f, int n4, f32x4 (&acc)[CPL],
                                            uint32_t & bad) {
@@ -703,6 +692,7 @@ __device__ __forceinline__ void vsum_chunk(const GatherSumArgs & a, int g0, int6
 }
 
 template <int TYPE, int CPL, int G> __global__ __launch_bounds__(256) void k_get_rows_sum_vec(const GatherSumArgs a) {
+    args_in_sgprs(a.frames, a.ids, a.ids_gstride, a.ngroups, a.ne0);
     const int64_t f =
         static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
     if (f >= a.frames) {
@@ -821,24 +811,28 @@ template <int TYPE> shp_status_t launch_get_rows(const GatherArgs & a, bool vec,
                 hipLaunchKernelGGL(k_get_rows_q8<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
             }
         } else {
-            const int64_t nch    = a.ne0 / elems_per_chunk<TYPE>();
-            const int     lpr    = nch >= 256 ? 256 : (nch >= 128 ? 128 : lanes_for(nch));
-            const int64_t blocks = (a.total * lpr + 255) / 256;
+            // 4-element chunks: up to 256 lanes per row, 1..8 chunks per lane.
+            const int64_t n4     = a.ne0 / 4;
+            const int     lpr    = n4 >= 256 ? 256 : (n4 >= 128 ? 128 : lanes_for(n4));
+            const dim3    grid(static_cast<unsigned>((a.total * lpr + 255) / 256));
             if (lpr == 256) {
-                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 256>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                                   stream, a);
+                if (n4 <= 256) {
+                    hipLaunchKernelGGL((k_get_rows_vec<TYPE, 256, 1>), grid, dim3(256), 0, stream, a);
+                } else if (n4 <= 512) {
+                    hipLaunchKernelGGL((k_get_rows_vec<TYPE, 256, 2>), grid, dim3(256), 0, stream, a);
+                } else if (n4 <= 1024) {
+                    hipLaunchKernelGGL((k_get_rows_vec<TYPE, 256, 4>), grid, dim3(256), 0, stream, a);
+                } else {
+                    hipLaunchKernelGGL((k_get_rows_vec<TYPE, 256, 8>), grid, dim3(256), 0, stream, a);
+                }
             } else if (lpr == 128) {
-                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 128>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                                   stream, a);
+                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 128, 2>), grid, dim3(256), 0, stream, a);
             } else if (lpr == 64) {
-                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 64>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                                   stream, a);
+                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 64, 2>), grid, dim3(256), 0, stream, a);
             } else if (lpr == 32) {
-                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 32>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                                   stream, a);
+                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 32, 2>), grid, dim3(256), 0, stream, a);
             } else {
-                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 16>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                                   stream, a);
+                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 16, 2>), grid, dim3(256), 0, stream, a);
             }
         }
         return launch_status();
@@ -966,22 +960,26 @@ extern "C" shp_status_t shp_get_rows(const shp_tensor * src,
     a.n     = ids->ne[0];
     a.ne11  = ids->ne[1];
     a.total = ids->ne[0] * ids->ne[1] * ids->ne[2];
-    a.batched = ids->ne[1] > 1 || ids->ne[2] > 1;
     a.staged  = src->type == SHP_TYPE_Q8_0 && q8_staged_width(src->ne[0]) && rows_aligned(*src, 16) &&
                rows_aligned(*dst, 16);
     a.ne0   = static_cast<int32_t>(src->ne[0]);
-    if ((a.total + 3) / 4 > INT32_MAX) {
+    if (a.total > int64_t{ UINT32_MAX } / 256) {  // output rows (and their lanes) by 32-bit divisions
         return SHP_ERR_UNSUPPORTED;
     }
+    a.fn    = make_fastdiv(static_cast<uint32_t>(a.n));
+    a.fne11 = make_fastdiv(static_cast<uint32_t>(a.ne11));
     const bool dst16 = rows_aligned(*dst, 16);
     const hipStream_t st = as_stream(stream);
     switch (src->type) {
         case SHP_TYPE_F32:
-            return launch_get_rows<SHP_TYPE_F32>(a, dst16 && rows_aligned(*src, 16) && src->ne[0] % 4 == 0, st);
+            return launch_get_rows<SHP_TYPE_F32>(a, dst16 && rows_aligned(*src, 16) && src->ne[0] % 4 == 0 &&
+                                                        src->ne[0] <= 8192, st);
         case SHP_TYPE_F16:
-            return launch_get_rows<SHP_TYPE_F16>(a, dst16 && rows_aligned(*src, 16) && src->ne[0] % 8 == 0, st);
+            return launch_get_rows<SHP_TYPE_F16>(a, dst16 && rows_aligned(*src, 16) && src->ne[0] % 4 == 0 &&
+                                                        src->ne[0] <= 8192, st);
         case SHP_TYPE_BF16:
-            return launch_get_rows<SHP_TYPE_BF16>(a, dst16 && rows_aligned(*src, 16) && src->ne[0] % 8 == 0, st);
+            return launch_get_rows<SHP_TYPE_BF16>(a, dst16 && rows_aligned(*src, 16) && src->ne[0] % 4 == 0 &&
+                                                         src->ne[0] <= 8192, st);
         default:
             return launch_get_rows<SHP_TYPE_Q8_0>(a, dst16 && rows_aligned(*src, 4) && src->ne[0] % 64 == 0, st);
     }

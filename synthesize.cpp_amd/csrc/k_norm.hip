@@ -111,6 +111,13 @@ __global__ __launch_bounds__(BLOCK) void k_rms_norm_vec(const NormArgs a) {
     constexpr int kWavesPerRow  = TPR > kWave ? TPR / kWave : 1;
     __shared__ double s_part[TPR > kWave ? BLOCK / kWave : 1];
 
+    args_in_sgprs(a.x, a.xm.flat, a.xm.rs, a.w, a.nrows, a.ne0, a.y, a.ym.flat, a.ym.rs);
+    if constexpr (MODE != kPlain) {
+        args_in_sgprs(a.b, a.bm.flat, a.bm.rs);
+    }
+    if constexpr (MODE == kAddSum) {
+        args_in_sgprs(a.s, a.sm.flat, a.sm.rs);
+    }
     const int     l     = threadIdx.x % TPR;
     const int64_t row   = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / TPR;
     const bool    live  = row < a.nrows;

@@ -113,9 +113,19 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// The kernel arguments a softmax wave needs before its first load.
+template <bool MASK> __device__ __forceinline__ void softmax_args_in_sgprs(const SoftMaxArgs & a) {
+    args_in_sgprs(a.x, a.xm.flat, a.xm.rs, a.y, a.ym.flat, a.ym.rs, a.nrows, a.ne0, a.scale);
+    if constexpr (MASK) {
+        args_in_sgprs(a.mask, a.mfast, a.fne1.d, a.fne1.m, a.fne1.l, a.fne2.d, a.fne2.m, a.fne2.l, a.fmne2.d,
+                      a.fmne2.m, a.fmne2.l, a.fmne3.d, a.fmne3.m, a.fmne3.l, a.mnb1, a.mnb2, a.mnb3);
+    }
+}
+
 // One wave per row, element lane + 64k in register k (k < K, 64K >= ne0).
 template <int K, bool MASK> __global__ __launch_bounds__(256) void k_soft_max_wave(const SoftMaxArgs a) {
     __shared__ double s_tab[256 / kWave][64];
+    softmax_args_in_sgprs<MASK>(a);
     const int     lane = threadIdx.x % kWave;
     const int64_t r    = static_cast<int64_t>(blockIdx.x) * (256 / kWave) +
                       __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
@@ -184,6 +194,7 @@ template <int WPR, int K4, bool MASK> __global__ __launch_bounds__(256) void k_s
     __shared__ float  s_max[256 / kWave];
     __shared__ double s_sum[256 / kWave];
     __shared__ double s_tab[256 / kWave][64];
+    softmax_args_in_sgprs<MASK>(a);
     const int     lane = threadIdx.x % kWave;
     const int     q    = threadIdx.x % kLanes;
     const int     wv   = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);

@@ -42,6 +42,25 @@ __device__ __forceinline__ f32x4 splat4(float v) {
     return f32x4{ v, v, v, v };
 }
 
+// Kernel arguments arrive by scalar loads from the kernel-argument segment,
+// and the compiler issues them where they are first needed: a bound checked
+// before the first data load puts a branch -- and a full scalar round trip --
+// between that bound and the pointers. Listing the values a wave needs before
+// its first data load here makes them all live in SGPRs at this point, so
+// their loads go out together and cost one round trip. Emits no instruction.
+// Measured on MI355X: SwiGLU [3072,512] 4.58 us against 4.80-4.86 us.
+// The statement counts as a side effect, so a later load of kernel data (not
+// arguments) is no longer known to read unwritten memory and is not made a
+// scalar load: the rope kernels, whose wave 0 reads its position with one,
+// do not use it.
+template <class T> __device__ __forceinline__ void arg_in_sgpr(const T & v) {
+    asm volatile("" ::"s"(v));
+}
+
+template <class... T> __device__ __forceinline__ void args_in_sgprs(const T &... v) {
+    (arg_in_sgpr(v), ...);
+}
+
 // Unsigned 32-bit division by a launch constant d >= 1 without an integer
 // divide: q = (umulhi(n, m) + n) >> l, with l = ceil(log2 d) and
 // m = floor(2^32 (2^l - d) / d) + 1 (Granlund & Montgomery, "Division by
