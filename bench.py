@@ -488,7 +488,8 @@ def suite(args, S, torch):
     if on("gguf"):
         # A package's lookup tables streamed file -> HBM by shp_gguf_load_tensor
         # (page cache warm after the first pass): the BF16 text embedding of
-        # configs[1] and the 16 Q8_0 codebooks of configs[2].
+        # configs[1] and the 16 Q8_0 codebooks of configs[2], those one call
+        # per tensor and in one shp_gguf_load_tensors call.
         import tempfile
         import time
         import numpy as np
@@ -506,16 +507,17 @@ def suite(args, S, torch):
             write_gguf(path, tensors)
             del tensors
             with S.GgufFile(path) as f:
-                for label, names in (("gguf load BF16 [2048,151936] file->HBM", ["talker.model.text_embedding.weight"]),
-                                     ("gguf load 16 x Q8_0 [1024,2048] file->HBM",
-                                      ["talker.code_predictor.model.codec_embedding.%d.weight" % k
-                                       for k in range(16)])):
+                codecs = ["talker.code_predictor.model.codec_embedding.%d.weight" % k for k in range(16)]
+                for label, names, many in (
+                        ("gguf load BF16 [2048,151936] file->HBM", ["talker.model.text_embedding.weight"], False),
+                        ("gguf load 16 x Q8_0 [1024,2048] file->HBM", codecs, False),
+                        ("gguf load 16 x Q8_0 [1024,2048] file->HBM, one call", codecs, True)):
                     nbytes = sum(f.info(n)[1] for n in names)
                     best = None
                     for _ in range(3):
                         torch.cuda.synchronize()
                         t0 = time.perf_counter()
-                        out = [f.load(n) for n in names]
+                        out = f.load_many(names) if many else [f.load(n) for n in names]
                         torch.cuda.synchronize()
                         dt = time.perf_counter() - t0
                         best = dt if best is None else min(best, dt)

@@ -73,6 +73,26 @@ shp_status_t shp_gguf_load_tensor(shp_gguf *   g,
                                   shp_stream_t stream);
 
 /*
+ * Loads `count` named tensors in one pass, as the reference's weight loader
+ * does for a whole package (src/gguf-metadata.cpp:20-46: every tensor of the
+ * weights context read and uploaded in turn). Tensor i goes to
+ * device_dsts[i] (capacities[i] bytes) and is described in descs[i], as
+ * shp_gguf_load_tensor does. Every name, type and capacity is checked before
+ * anything is read (the first failure's status is returned and nothing is
+ * copied). The tensors' bytes then go through the staging buffers back to
+ * back -- a chunk carries as many small tensors as fit, read by parallel
+ * threads -- with one synchronisation at the end instead of one per tensor.
+ * count = 0 does nothing and returns SHP_OK.
+ */
+shp_status_t shp_gguf_load_tensors(shp_gguf *          g,
+                                   const char * const * names,
+                                   int32_t              count,
+                                   void * const *       device_dsts,
+                                   const size_t *       capacities,
+                                   shp_tensor *         descs,
+                                   shp_stream_t         stream);
+
+/*
  * The type the catalog requires of the talker half's matrix tensors -- the
  * text and codec embedding tables included -- under a quantization profile
  * (synthesize.quantization.profile): "BF16" -> BF16, "F16" -> F16,

@@ -385,21 +385,23 @@ bool loadable_type(uint32_t t) {
 // Reads n bytes at file offset off into dst; false on a short read. Large
 // reads are split over up to kReadThreads threads (a single thread copying
 // out of the page cache, not PCIe, bounds the load otherwise).
-bool read_range(int fd, char * dst, size_t n, uint64_t off) {
-    auto one = [fd](char * d, size_t len, uint64_t o) {
-        size_t got = 0;
-        while (got < len) {
-            const ssize_t rd = pread(fd, d + got, len - got, static_cast<off_t>(o + got));
-            if (rd < 0 && errno == EINTR) {
-                continue;
-            }
-            if (rd <= 0) {
-                return false;
-            }
-            got += static_cast<size_t>(rd);
+bool pread_all(int fd, char * d, size_t len, uint64_t o) {
+    size_t got = 0;
+    while (got < len) {
+        const ssize_t rd = pread(fd, d + got, len - got, static_cast<off_t>(o + got));
+        if (rd < 0 && errno == EINTR) {
+            continue;
         }
-        return true;
-    };
+        if (rd <= 0) {
+            return false;
+        }
+        got += static_cast<size_t>(rd);
+    }
+    return true;
+}
+
+bool read_range(int fd, char * dst, size_t n, uint64_t off) {
+    auto one = [fd](char * d, size_t len, uint64_t o) { return pread_all(fd, d, len, o); };
     const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
     const unsigned nt = static_cast<unsigned>(std::min<size_t>({ kReadThreads, hw, n / kReadSplitMin }));
     if (nt <= 1) {
@@ -602,6 +604,166 @@ extern "C" shp_status_t shp_gguf_load_tensor(shp_gguf *   g,
     }
     describe(*ti, desc);
     desc->data = device_dst;
+    return SHP_OK;
+}
+
+namespace {
+
+// One piece of a staging chunk: n bytes of the file at file_off, staged at
+// stage_off, bound for dst.
+struct Piece {
+    size_t   stage_off;
+    uint64_t file_off;
+    size_t   n;
+    char *   dst;
+};
+
+// Reads a chunk's pieces into the staging buffer: the chunk's filled bytes
+// are split into up to kReadThreads equal parts, and each part's thread reads
+// the parts of the pieces that fall in it, so a chunk of many small tensors
+// is read as much in parallel as one large tensor.
+bool read_pieces(int fd, char * stage, const std::vector<Piece> & ps, size_t fill) {
+    auto span = [&](size_t b, size_t e) {
+        for (const Piece & p : ps) {
+            const size_t lo = std::max(b, p.stage_off), hi = std::min(e, p.stage_off + p.n);
+            if (lo < hi && !pread_all(fd, stage + lo, hi - lo, p.file_off + (lo - p.stage_off))) {
+                return false;
+            }
+        }
+        return true;
+    };
+    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+    const unsigned nt = static_cast<unsigned>(std::min<size_t>({ kReadThreads, hw, fill / kReadSplitMin }));
+    if (nt <= 1) {
+        return span(0, fill);
+    }
+    std::atomic<bool>        ok{ true };
+    std::vector<std::thread> th;
+    const size_t             part = (fill / nt + 4095) & ~size_t{ 4095 };
+    size_t                   b    = 0;
+    for (unsigned t = 0; t < nt && b < fill; ++t, b += part) {
+        const size_t e = std::min(fill, b + part);
+        try {
+            th.emplace_back([&, b, e] {
+                if (!span(b, e)) {
+                    ok = false;
+                }
+            });
+        } catch (...) {  // no more threads: this thread reads what is left
+            break;
+        }
+    }
+    if (b < fill && !span(b, fill)) {
+        ok = false;
+    }
+    for (auto & t : th) {
+        t.join();
+    }
+    return ok;
+}
+
+}  // namespace
+
+extern "C" shp_status_t shp_gguf_load_tensors(shp_gguf *          g,
+                                              const char * const * names,
+                                              int32_t              count,
+                                              void * const *       device_dsts,
+                                              const size_t *       capacities,
+                                              shp_tensor *         descs,
+                                              shp_stream_t         stream) {
+    if (g == nullptr || count < 0 || (count > 0 && (names == nullptr || device_dsts == nullptr ||
+                                                    capacities == nullptr || descs == nullptr))) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    // Every tensor is checked before anything is read.
+    std::vector<const TensorInfo *> tis(static_cast<size_t>(count));
+    for (int32_t i = 0; i < count; ++i) {
+        const TensorInfo * ti = names[i] != nullptr ? find_tensor(g, names[i]) : nullptr;
+        if (ti == nullptr || device_dsts[i] == nullptr) {
+            return SHP_ERR_INVALID_ARG;
+        }
+        if (!loadable_type(ti->type)) {
+            return SHP_ERR_UNSUPPORTED;
+        }
+        if (ti->nbytes > capacities[i]) {
+            return SHP_ERR_INVALID_ARG;
+        }
+        tis[static_cast<size_t>(i)] = ti;
+    }
+    if (count == 0) {
+        return SHP_OK;
+    }
+    const hipStream_t s = shp::as_stream(stream);
+    for (int k = 0; k < 2; ++k) {
+        if (g->stage[k] == nullptr) {
+            if (hipHostMalloc(&g->stage[k], kStageBytes, hipHostMallocDefault) != hipSuccess ||
+                hipEventCreateWithFlags(&g->done[k], hipEventDisableTiming) != hipSuccess) {
+                release_staging(g);
+                return SHP_ERR_BACKEND;
+            }
+        }
+    }
+    // The tensors' bytes go through the staging buffers back to back: a chunk
+    // holds the ends and starts of as many tensors as fit, its pieces are read
+    // in parallel, and each piece is one copy to its destination.
+    std::vector<Piece> ps;
+    size_t             fill = 0;
+    int                k    = 0;
+    auto flush = [&]() -> shp_status_t {
+        if (fill == 0) {
+            return SHP_OK;
+        }
+        if (hipEventSynchronize(g->done[k]) != hipSuccess) {  // the chunk's previous copies
+            return SHP_ERR_BACKEND;
+        }
+        char * stage = static_cast<char *>(g->stage[k]);
+        if (!read_pieces(g->fd, stage, ps, fill)) {
+            (void) hipStreamSynchronize(s);
+            return SHP_ERR_INVALID_ARG;  // the file shrank under us
+        }
+        for (const Piece & p : ps) {
+            if (hipMemcpyAsync(p.dst, stage + p.stage_off, p.n, hipMemcpyHostToDevice, s) != hipSuccess) {
+                (void) hipStreamSynchronize(s);
+                return SHP_ERR_BACKEND;
+            }
+        }
+        if (hipEventRecord(g->done[k], s) != hipSuccess) {
+            (void) hipStreamSynchronize(s);
+            return SHP_ERR_BACKEND;
+        }
+        ps.clear();
+        fill = 0;
+        k ^= 1;
+        return SHP_OK;
+    };
+    for (int32_t i = 0; i < count; ++i) {
+        const TensorInfo * ti  = tis[static_cast<size_t>(i)];
+        uint64_t           off = 0;
+        while (off < ti->nbytes) {
+            const size_t take = static_cast<size_t>(std::min<uint64_t>(kStageBytes - fill, ti->nbytes - off));
+            ps.push_back(Piece{ fill, g->data_start + ti->offset + off, take,
+                                static_cast<char *>(device_dsts[i]) + off });
+            fill += take;
+            off += take;
+            if (fill == kStageBytes) {
+                const shp_status_t st = flush();
+                if (st != SHP_OK) {
+                    return st;
+                }
+            }
+        }
+    }
+    const shp_status_t st = flush();
+    if (st != SHP_OK) {
+        return st;
+    }
+    if (hipStreamSynchronize(s) != hipSuccess) {
+        return SHP_ERR_BACKEND;
+    }
+    for (int32_t i = 0; i < count; ++i) {
+        describe(*tis[static_cast<size_t>(i)], &descs[i]);
+        descs[i].data = device_dsts[i];
+    }
     return SHP_OK;
 }
 

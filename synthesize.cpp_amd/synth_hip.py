@@ -90,6 +90,8 @@ def load(path=None):
         "shp_gguf_kv_u32": ([vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32)], ctypes.c_int32),
         "shp_gguf_kv_string": ([vp, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t], ctypes.c_int32),
         "shp_gguf_load_tensor": ([vp, ctypes.c_char_p, vp, ctypes.c_size_t, _PT, vp], ctypes.c_int32),
+        "shp_gguf_load_tensors": ([vp, ctypes.POINTER(ctypes.c_char_p), ctypes.c_int32, ctypes.POINTER(vp),
+                                   ctypes.POINTER(ctypes.c_size_t), _PT, vp], ctypes.c_int32),
         "shp_table_type_for_profile": ([ctypes.c_char_p, ctypes.POINTER(ctypes.c_int32)], ctypes.c_int32),
     }
     for name, (args, res) in gsigs.items():
@@ -439,14 +441,35 @@ class GgufFile:
         _check(load().shp_gguf_load_tensor(self._h, name.encode("utf-8", "surrogateescape"),
                                            ctypes.c_void_p(raw.data_ptr()), nbytes,
                                            ctypes.byref(out), _stream()), "gguf_load_tensor")
-        ne = [int(out.ne[k]) for k in range(4)]
-        nd = max([k + 1 for k in range(4) if ne[k] != 1] or [1])
-        if out.type == TYPE_Q8_0:
-            rows = ne[1] * ne[2] * ne[3]
-            return Q8Tensor(raw.view(rows, ne[0] // Q8_0_BLOCK_ELEMS * Q8_0_BLOCK_BYTES), ne[0])
-        dt = {TYPE_F32: torch.float32, TYPE_F16: torch.float16, TYPE_BF16: torch.bfloat16,
-              TYPE_I32: torch.int32}[out.type]
-        return raw.view(dt).view(tuple(reversed(ne[:nd])))
+        return _typed_view(raw, out)
+
+    def load_many(self, names, device="cuda"):
+        """Several tensors in one pass (shp_gguf_load_tensors), in the order of
+        `names`; each as load() returns it."""
+        import torch
+        names = list(names)
+        raws = [torch.empty(self.info(n)[1], dtype=torch.uint8, device=device) for n in names]
+        n = len(names)
+        descs = (ShpTensor * max(n, 1))()
+        _check(load().shp_gguf_load_tensors(
+            self._h, (ctypes.c_char_p * max(n, 1))(*[x.encode("utf-8", "surrogateescape") for x in names]), n,
+            (ctypes.c_void_p * max(n, 1))(*[r.data_ptr() for r in raws]),
+            (ctypes.c_size_t * max(n, 1))(*[r.numel() for r in raws]), descs, _stream()), "gguf_load_tensors")
+        return [_typed_view(r, descs[i]) for i, r in enumerate(raws)]
+
+
+def _typed_view(raw, desc):
+    """A loaded tensor's device bytes as the torch tensor (or Q8Tensor) its
+    descriptor names."""
+    import torch
+    ne = [int(desc.ne[k]) for k in range(4)]
+    nd = max([k + 1 for k in range(4) if ne[k] != 1] or [1])
+    if desc.type == TYPE_Q8_0:
+        rows = ne[1] * ne[2] * ne[3]
+        return Q8Tensor(raw.view(rows, ne[0] // Q8_0_BLOCK_ELEMS * Q8_0_BLOCK_BYTES), ne[0])
+    dt = {TYPE_F32: torch.float32, TYPE_F16: torch.float16, TYPE_BF16: torch.bfloat16,
+          TYPE_I32: torch.int32}[desc.type]
+    return raw.view(dt).view(tuple(reversed(ne[:nd])))
 
 
 def table_type_for_profile(profile):

@@ -227,6 +227,23 @@ def test_load_rejects_without_touching_the_device(tmp_path):
         assert L.shp_gguf_load_tensor(f._h, b"nope", fake, 64, ctypes.byref(d), None) == S.ERR_INVALID_ARG
         assert L.shp_gguf_load_tensor(f._h, b"t", None, 64, ctypes.byref(d), None) == S.ERR_INVALID_ARG
 
+        # The list form checks every entry before it reads or copies anything.
+        def many(names, dsts, caps):
+            n = len(names)
+            descs = (S.ShpTensor * max(n, 1))()
+            return L.shp_gguf_load_tensors(f._h, (ctypes.c_char_p * max(n, 1))(*names), n,
+                                           (ctypes.c_void_p * max(n, 1))(*dsts),
+                                           (ctypes.c_size_t * max(n, 1))(*caps), descs, None)
+        assert many([b"t", b"q"], [0x10000, 0x20000], [64, 1 << 20]) == S.ERR_UNSUPPORTED
+        assert many([b"t", b"t"], [0x10000, 0x20000], [64, 31]) == S.ERR_INVALID_ARG
+        assert many([b"t", b"nope"], [0x10000, 0x20000], [64, 64]) == S.ERR_INVALID_ARG
+        assert many([b"t", b"t"], [0x10000, None], [64, 64]) == S.ERR_INVALID_ARG
+        assert many([b"t", None], [0x10000, 0x20000], [64, 64]) == S.ERR_INVALID_ARG
+        assert many([], [], []) == S.OK
+        assert L.shp_gguf_load_tensors(f._h, None, 1, None, None, None, None) == S.ERR_INVALID_ARG
+        assert L.shp_gguf_load_tensors(None, None, 0, None, None, None, None) == S.ERR_INVALID_ARG
+        assert L.shp_gguf_load_tensors(f._h, None, -1, None, None, None, None) == S.ERR_INVALID_ARG
+
 
 def test_table_type_for_profile():
     assert S.table_type_for_profile("BF16") == S.TYPE_BF16

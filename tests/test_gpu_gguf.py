@@ -76,3 +76,30 @@ def test_load_into_a_smaller_buffer_is_refused(gpu, tmp_path):
         torch.cuda.synchronize()
         np.testing.assert_array_equal(dst.cpu().numpy().view(np.float32), np.arange(256, dtype=np.float32))
         assert d.data == dst.data_ptr() and d.ne[0] == 256
+
+
+def test_load_many_matches_the_file_across_chunk_boundaries(gpu, tmp_path):
+    """shp_gguf_load_tensors over the whole package in a shuffled order: the
+    41 MB BF16 table spans two 32 MiB staging chunks and the small tensors
+    share chunks with it and with each other; every device tensor equals the
+    file's bytes, and the gathers read the loaded tables as before."""
+    import torch
+    rng = np.random.default_rng(43)
+    p, bf, q8 = _package(tmp_path, rng)
+    raw = p.read_bytes()
+    with gpu.GgufFile(p) as f:
+        names = list(f.tensor_names())
+        order = [names[i] for i in rng.permutation(len(names))]
+        loaded = f.load_many(order)
+        for name, t in zip(order, loaded):
+            _, nbytes, off = f.info(name)
+            data = t.data if isinstance(t, gpu.Q8Tensor) else t
+            assert bytes(data.contiguous().view(torch.uint8).cpu().numpy().tobytes()) == raw[off:off + nbytes], name
+        assert f.load_many([]) == []
+        one = f.load_many([TEXT])[0]
+        assert torch.equal(one.view(torch.int16), loaded[order.index(TEXT)].view(torch.int16))
+    codec = [loaded[order.index(CODEC % g)] for g in range(15)]
+    codes = rng.integers(0, 2048, (15, 64)).astype(np.int32)
+    got = gpu.get_rows_sum(codec, torch.from_numpy(codes).cuda())
+    ref = R.run(lambda g: R.sum_code_embeddings(g, q8, R.Q8_0, 1024, codes))
+    np.testing.assert_array_equal(got.cpu().numpy().view(np.uint32), ref.view(np.uint32))
