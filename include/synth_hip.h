@@ -289,6 +289,55 @@ shp_status_t shp_add_leaky_relu(const shp_tensor * a,
 shp_status_t shp_add(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream);
 
 /*
+ * The non-GEMM node runs of one Qwen3 decoder layer,
+ * src/arch/qwen3-tts/operations.cpp:84-147, in the layer's order. The
+ * layer's matrix products and its attention run between these node runs in
+ * a model, so their outputs are inputs here:
+ *   normed       = rms_norm(x)*w_in                        (:85-86)
+ *   q_out, k_out = rope(rms_norm(q)*wq), rope(rms_norm(k)*wk)  (:98-104)
+ *   resid        = x + attn_out                            (:143)
+ *   mlp_in       = rms_norm(resid)*w_post                  (:145)
+ *   act          = silu(gate)*up                           (:39-41 via :146)
+ *   out          = resid + mlp_out                         (:147)
+ * Five launches on `stream`, each the launch of shp_rms_norm_mul,
+ * shp_qk_norm_rope, shp_add_rms_norm_mul, shp_swiglu and shp_add, with the
+ * same results. Every tensor's presence, type and shape is checked first:
+ * a malformed step returns SHP_ERR_INVALID_ARG with nothing enqueued.
+ * x, normed, attn_out, resid, mlp_in, mlp_out, out: F32 [hidden, T];
+ * q, q_out: F32 [head_dim, q_heads, T]; k, k_out: F32 [head_dim, kv_heads, T];
+ * gate, up, act: F32 [ffn, T]; pos: I32 [T]; w_in, w_post: [hidden] and
+ * wq, wk: [head_dim], each F32, BF16 or F16. NEOX rope over n_dims, with
+ * freq_scale 1.
+ */
+typedef struct shp_layer_step {
+    const shp_tensor * x;
+    const shp_tensor * w_in;
+    shp_tensor *       normed;
+    const shp_tensor * q;
+    const shp_tensor * k;
+    const shp_tensor * wq;
+    const shp_tensor * wk;
+    const shp_tensor * pos;
+    shp_tensor *       q_out;
+    shp_tensor *       k_out;
+    const shp_tensor * attn_out;
+    const shp_tensor * w_post;
+    shp_tensor *       resid;
+    shp_tensor *       mlp_in;
+    const shp_tensor * gate;
+    const shp_tensor * up;
+    shp_tensor *       act;
+    const shp_tensor * mlp_out;
+    shp_tensor *       out;
+    float              eps;
+    float              freq_base;
+    int32_t            n_dims;
+    int32_t            reserved; /* must be 0 */
+} shp_layer_step;
+
+shp_status_t shp_layer_nongemm_step(const shp_layer_step * step, shp_stream_t stream);
+
+/*
  * ggml_soft_max_ext(a, mask, scale, max_bias): the attention softmax of
  * src/arch/qwen3-tts/operations.cpp:131-133. Per row: w = a*scale + mask
  * (f32), v = expf(w - max w), y = v * (float)(1/sum v) with the sum in

@@ -29,6 +29,14 @@ class ShpTensor(ctypes.Structure):
                 ("nb", ctypes.c_size_t * 4), ("data", ctypes.c_void_p)]
 
 
+class ShpLayerStep(ctypes.Structure):
+    _fields_ = [(n, ctypes.POINTER(ShpTensor)) for n in (
+        "x", "w_in", "normed", "q", "k", "wq", "wk", "pos", "q_out", "k_out", "attn_out", "w_post", "resid",
+        "mlp_in", "gate", "up", "act", "mlp_out", "out")] + [
+        ("eps", ctypes.c_float), ("freq_base", ctypes.c_float), ("n_dims", ctypes.c_int32),
+        ("reserved", ctypes.c_int32)]
+
+
 class ShpError(RuntimeError):
     def __init__(self, status, what):
         super().__init__("%s failed: %s (%d)" % (what, status_string(status), status))
@@ -74,6 +82,7 @@ def load(path=None):
         "shp_soft_max_ext": [_PT, _PT, f, f, _PT, vp],
         "shp_scale_bias": [_PT, f, f, _PT, vp],
         "shp_sum_scale_leaky_relu": [_PT, i32, f, f, _PT, _PT, vp],
+        "shp_layer_nongemm_step": [ctypes.POINTER(ShpLayerStep), vp],
     }
     for name, args in sigs.items():
         fn = getattr(L, name)
@@ -373,6 +382,32 @@ def add(a, b, out=None):
     out = a.new_empty(a.shape) if out is None else out
     _check(load().shp_add(_ref(desc(a)), _ref(desc(b)), _ref(desc(out)), _stream()), "add")
     return out
+
+
+LAYER_OUTPUTS = ("normed", "q_out", "k_out", "resid", "mlp_in", "act", "out")
+
+
+def layer_nongemm_step(x, w_in, q, k, wq, wk, pos, attn_out, w_post, gate, up, mlp_out, eps, n_dims, freq_base,
+                       outs=None):
+    """The non-GEMM node runs of one Qwen3 decoder layer
+    (src/arch/qwen3-tts/operations.cpp:84-147) in one call: x, attn_out, mlp_out
+    (T, hidden); q (T, heads, hd); k (T, kv_heads, hd); gate, up (T, ffn); pos
+    int32 (T,). Returns a dict of the outputs named in LAYER_OUTPUTS (`outs`
+    may supply any of them)."""
+    outs = dict(outs or {})
+    like = {"normed": x, "q_out": q, "k_out": k, "resid": x, "mlp_in": x, "act": gate, "out": x}
+    for name in LAYER_OUTPUTS:
+        if outs.get(name) is None:
+            outs[name] = like[name].new_empty(like[name].shape)
+    ins = dict(x=x, w_in=w_in, q=q, k=k, wq=wq, wk=wk, pos=pos, attn_out=attn_out, w_post=w_post, gate=gate, up=up,
+               mlp_out=mlp_out)
+    descs = {n: desc(t) for n, t in list(ins.items()) + list(outs.items())}
+    step = ShpLayerStep()
+    for n, d in descs.items():
+        setattr(step, n, ctypes.pointer(d) if d is not None else None)
+    step.eps, step.freq_base, step.n_dims, step.reserved = float(eps), float(freq_base), int(n_dims), 0
+    _check(load().shp_layer_nongemm_step(ctypes.byref(step), _stream()), "layer_nongemm_step")
+    return outs
 
 
 # ---------------------------------------------------------------------------

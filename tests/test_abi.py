@@ -169,3 +169,68 @@ def test_binding_fails_loudly_without_library(tmp_path):
         mod.load(str(tmp_path / "missing.so"))
     import importlib
     importlib.reload(S)
+
+
+def layer_step(**over):
+    """A well-formed step of 5 positions (hidden 256, 4+2 heads of 64, ffn 512)
+    with fake pointers; keyword arguments replace a field."""
+    t = 5
+    f = dict(x=mk(S.TYPE_F32, [256, t]), w_in=mk(S.TYPE_BF16, [256]), normed=mk(S.TYPE_F32, [256, t]),
+             q=mk(S.TYPE_F32, [64, 4, t]), k=mk(S.TYPE_F32, [64, 2, t]), wq=mk(S.TYPE_BF16, [64]),
+             wk=mk(S.TYPE_BF16, [64]), pos=mk(S.TYPE_I32, [t]), q_out=mk(S.TYPE_F32, [64, 4, t]),
+             k_out=mk(S.TYPE_F32, [64, 2, t]), attn_out=mk(S.TYPE_F32, [256, t]), w_post=mk(S.TYPE_BF16, [256]),
+             resid=mk(S.TYPE_F32, [256, t]), mlp_in=mk(S.TYPE_F32, [256, t]), gate=mk(S.TYPE_F32, [512, t]),
+             up=mk(S.TYPE_F32, [512, t]), act=mk(S.TYPE_F32, [512, t]), mlp_out=mk(S.TYPE_F32, [256, t]),
+             out=mk(S.TYPE_F32, [256, t]))
+    scal = dict(eps=1e-6, freq_base=1e6, n_dims=64, reserved=0)
+    for key, val in over.items():
+        (scal if key in scal else f)[key] = val
+    step = S.ShpLayerStep()
+    for key, val in f.items():
+        setattr(step, key, ctypes.pointer(val) if val is not None else None)
+    for key, val in scal.items():
+        setattr(step, key, val)
+    step._keep = f
+    return step
+
+
+LAYER_TENSORS = ("x", "w_in", "normed", "q", "k", "wq", "wk", "pos", "q_out", "k_out", "attn_out", "w_post",
+                 "resid", "mlp_in", "gate", "up", "act", "mlp_out", "out")
+
+
+def test_layer_step_rejects_a_malformed_step_before_any_launch():
+    """Every tensor of the step is checked before the first of its five
+    launches: each case below changes one field of a well-formed step."""
+    L = S.load()
+    call = lambda **over: L.shp_layer_nongemm_step(ctypes.byref(layer_step(**over)), None)
+    assert L.shp_layer_nongemm_step(None, None) == S.ERR_INVALID_ARG
+    assert call(reserved=1) == S.ERR_INVALID_ARG
+    for name in LAYER_TENSORS:
+        assert call(**{name: None}) == S.ERR_INVALID_ARG, name
+    # one wrong extent per tensor, in the last (position) dimension or the row
+    for name in ("normed", "attn_out", "resid", "mlp_in", "mlp_out", "out"):
+        assert call(**{name: mk(S.TYPE_F32, [256, 4])}) == S.ERR_INVALID_ARG, name
+        assert call(**{name: mk(S.TYPE_F32, [252, 5])}) == S.ERR_INVALID_ARG, name
+    for name in ("up", "act"):
+        assert call(**{name: mk(S.TYPE_F32, [512, 6])}) == S.ERR_INVALID_ARG, name
+        assert call(**{name: mk(S.TYPE_F32, [508, 5])}) == S.ERR_INVALID_ARG, name
+    assert call(q_out=mk(S.TYPE_F32, [64, 2, 5])) == S.ERR_INVALID_ARG
+    assert call(k_out=mk(S.TYPE_F32, [64, 4, 5])) == S.ERR_INVALID_ARG
+    assert call(k=mk(S.TYPE_F32, [32, 2, 5])) == S.ERR_INVALID_ARG  # head_dim differs from q's
+    assert call(q=mk(S.TYPE_F32, [64, 4, 4])) == S.ERR_INVALID_ARG  # positions differ from x's
+    assert call(x=mk(S.TYPE_F32, [256, 5, 2])) == S.ERR_INVALID_ARG  # a 3-d hidden state
+    assert call(out=mk(S.TYPE_F16, [256, 5])) == S.ERR_INVALID_ARG
+    assert call(pos=mk(S.TYPE_I32, [4])) == S.ERR_INVALID_ARG
+    assert call(pos=mk(S.TYPE_F32, [5])) == S.ERR_INVALID_ARG
+    assert call(w_in=mk(S.TYPE_BF16, [255])) == S.ERR_INVALID_ARG
+    assert call(w_post=mk(S.TYPE_Q8_0, [256])) == S.ERR_INVALID_ARG
+    assert call(wq=mk(S.TYPE_BF16, [32])) == S.ERR_INVALID_ARG
+    assert call(wk=mk(S.TYPE_F32, [64])) == S.ERR_UNSUPPORTED  # q and k gains of two types
+    assert call(n_dims=63) == S.ERR_INVALID_ARG
+    assert call(n_dims=66) == S.ERR_INVALID_ARG
+    assert call(n_dims=0) == S.ERR_INVALID_ARG
+    assert call(eps=-1e-6) == S.ERR_INVALID_ARG
+    assert call(eps=float("nan")) == S.ERR_INVALID_ARG
+    bad_nb = mk(S.TYPE_F32, [256, 5])
+    bad_nb.nb[0] = 8
+    assert call(resid=bad_nb) == S.ERR_INVALID_ARG

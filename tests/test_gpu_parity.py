@@ -842,6 +842,53 @@ def test_add(gpu, bshape):
     assert_bitexact(_np(gpu.add(_t(gpu, a), _t(gpu, b))), R.run(lambda g: g.add(a, b)))
 
 
+@pytest.mark.parametrize("T,hd,wkind", [(1, 128, "bf16"), (37, 128, "f32"), (5, 64, "f16")])
+def test_layer_nongemm_step(gpu, T, hd, wkind):
+    """One call for a Qwen3 layer's non-GEMM node runs
+    (qwen3-tts/operations.cpp:84-147): every output equals the single entry
+    points' bit for bit, and the oracle's -- adds bit-exact, norms and SwiGLU
+    within 1e-5, q/k bit-exact against the restatement with correctly rounded
+    cos/sin. hidden 1024, 16 q and 8 kv heads, ffn 3072 (the talker's shape)."""
+    rng = np.random.default_rng(SEED + 7 * T + hd)
+    hidden, heads, kv_heads, ffn = 1024, 16, 8, 3072
+    eps, theta = np.float32(1e-6), np.float32(1e6)
+    x = rng.standard_normal((T, hidden)).astype(np.float32)
+    q = rng.standard_normal((T, heads, hd)).astype(np.float32)
+    k = rng.standard_normal((T, kv_heads, hd)).astype(np.float32)
+    attn = rng.standard_normal((T, hidden)).astype(np.float32)
+    gate = (rng.standard_normal((T, ffn)) * 4).astype(np.float32)
+    up = rng.standard_normal((T, ffn)).astype(np.float32)
+    mlp = rng.standard_normal((T, hidden)).astype(np.float32)
+    pos = _positions(rng, T, 8192)
+    (w_in, wt), (w_post, _), (wq, _), (wk, _) = [_weights(rng, n, wkind) for n in (hidden, hidden, hd, hd)]
+    d = {n: _t(gpu, a) for n, a in dict(x=x, q=q, k=k, attn=attn, gate=gate, up=up, mlp=mlp, pos=pos).items()}
+    dw = {n: _dev_w(gpu, a, wkind) for n, a in dict(w_in=w_in, w_post=w_post, wq=wq, wk=wk).items()}
+
+    outs = gpu.layer_nongemm_step(d["x"], dw["w_in"], d["q"], d["k"], dw["wq"], dw["wk"], d["pos"], d["attn"],
+                                  dw["w_post"], d["gate"], d["up"], d["mlp"], eps, hd, theta)
+    got = {n: _np(t) for n, t in outs.items()}
+
+    normed = gpu.rms_norm_mul(d["x"], dw["w_in"], eps)
+    qo, ko = gpu.qk_norm_rope(d["q"], d["k"], dw["wq"], dw["wk"], eps, d["pos"], hd, theta)
+    resid, mlp_in = gpu.add_rms_norm_mul(d["x"], d["attn"], dw["w_post"], eps)
+    act = gpu.swiglu(d["gate"], d["up"])
+    out = gpu.add(resid, d["mlp"])
+    single = dict(normed=normed, q_out=qo, k_out=ko, resid=resid, mlp_in=mlp_in, act=act, out=out)
+    assert sorted(single) == sorted(gpu.LAYER_OUTPUTS)
+    for n, t in single.items():
+        assert_bitexact(got[n], _np(t))
+
+    assert_close(got["normed"], R.run(lambda g: R.rms_norm_w(g, x, w_in, eps, wt)))
+    qc, kc = R.run(lambda g: R.qk_norm_rope(g, q, k, wq, wk, eps, pos, hd, theta, wt, cs_rounded=True))
+    assert_bitexact(got["q_out"], qc)
+    assert_bitexact(got["k_out"], kc)
+    s_ref, y_ref = R.run(lambda g: R.add_rms_norm_w(g, x, attn, w_post, eps, wt))
+    assert_bitexact(got["resid"], s_ref)
+    assert_close(got["mlp_in"], y_ref)
+    assert_close(got["act"], R.run(lambda g: R.swiglu(g, gate, up)))
+    assert_bitexact(got["out"], R.run(lambda g: g.add(s_ref, mlp)))
+
+
 def test_strided_views(gpu):
     """ggml views: rows strided in dims 1..3 (a q/k head view of a fused qkv
     buffer) go through the row path with the same results."""
