@@ -655,6 +655,115 @@ def test_swiglu_and_silu(gpu, shape):
     assert_close(_np(gpu.swiglu(_t(gpu, gt))), ref)
 
 
+def assert_same_specials(got, ref):
+    """NaN where the oracle has NaN, the same signed infinities and the same
+    sign on zeros; returns the mask of the oracle's finite entries."""
+    got = np.asarray(got, np.float32)
+    ref = np.asarray(ref, np.float32)
+    assert got.shape == ref.shape
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    inf = np.isinf(ref)
+    assert np.array_equal(np.isinf(got), inf) and np.array_equal(got[inf], ref[inf])
+    zero = ref == 0
+    assert np.array_equal(got[zero] == 0, np.ones(zero.sum(), bool))
+    assert np.array_equal(np.signbit(got[zero]), np.signbit(ref[zero]))
+    return np.isfinite(ref)
+
+
+def test_norms_special_rows(gpu):
+    """RMSNorm (plain, x gain, after an add) on rows holding NaN, +-inf, a value
+    whose f32 square overflows (2e19: sum inf, scale 0), subnormals (squares
+    that underflow to 0, so scale = 1/sqrt(eps)) and zeros: every such row is
+    bit-identical to the oracle (NaN compared as NaN), the ordinary row within
+    the float bar."""
+    rng = np.random.default_rng(SEED + 41)
+    x = rng.standard_normal((9, 1024)).astype(np.float32)
+    x[0] = 0.0
+    x[1, 5] = np.nan
+    x[2, 7] = np.inf
+    x[3, 9] = -np.inf
+    x[4, 11] = 2e19
+    x[5] = np.float32(1e-41) * np.sign(x[5])
+    x[6] = 3e-20
+    x[7, :3] = [np.inf, -np.inf, 1.0]
+    b = rng.standard_normal((9, 1024)).astype(np.float32)
+    b[1:8] = 0.0  # the add keeps the special rows as they are
+    w, wt = _weights(rng, 1024, "bf16")
+    eps = np.float32(1e-6)
+    ref = R.run(lambda g: R.rms_norm_w(g, x, w, eps, wt))
+    got = _np(gpu.rms_norm_mul(_t(gpu, x), _dev_w(gpu, w, "bf16"), eps))
+    fin = assert_same_specials(got, ref)
+    assert_bitexact(np.where(fin, got, 0)[:8], np.where(fin, ref, 0)[:8])
+    assert_close(got[8:], ref[8:])
+    ref = R.run(lambda g: g.rms_norm(x, eps))
+    got = _np(gpu.rms_norm_mul(_t(gpu, x), None, eps))
+    fin = assert_same_specials(got, ref)
+    assert_bitexact(np.where(fin, got, 0)[:8], np.where(fin, ref, 0)[:8])
+    s_ref, y_ref = R.run(lambda g: R.add_rms_norm_w(g, x, b, w, eps, wt))
+    s, y = gpu.add_rms_norm_mul(_t(gpu, x), _t(gpu, b), _dev_w(gpu, w, "bf16"), eps)
+    assert_same_specials(_np(s), s_ref)
+    fin = assert_same_specials(_np(y), y_ref)
+    assert_bitexact(np.where(fin, _np(y), 0)[1:8], np.where(fin, y_ref, 0)[1:8])
+
+
+def test_rope_and_qk_norm_rope_special_values(gpu):
+    """NaN and +-inf components through the NEOX rotation (inf * sin 0 is NaN
+    at position 0, as in the CPU formula; no identity shortcut), on the
+    128-wide fast path and the generic one: NaN and inf where the oracle has
+    them, everything else bit-exact against the restatement with correctly
+    rounded cos/sin."""
+    rng = np.random.default_rng(SEED + 43)
+    for hd in (128, 64):
+        x = rng.standard_normal((4, 4, hd)).astype(np.float32)
+        x[0, 0, 1] = np.inf
+        x[0, 1, hd // 2 + 2] = -np.inf
+        x[1, 2, 3] = np.nan
+        x[2, 3, :] = 0.0
+        x[3, 0, 0] = 3e38
+        x[3, 0, hd // 2] = -3e38
+        pos = np.array([0, 37, 8191, 5], np.int32)
+        theta = np.float32(1e6)
+        ref = R.run(lambda g: g.rope_neox(x, pos, hd, theta, cs_rounded=True))
+        got = _np(gpu.rope_ext(_t(gpu, x), _t(gpu, pos), hd, gpu.ROPE_TYPE_NEOX, theta))
+        fin = assert_same_specials(got, ref)
+        assert_bitexact(np.where(fin, got, 0), np.where(fin, ref, 0))
+        k = rng.standard_normal((4, 2, hd)).astype(np.float32)
+        k[1, 1, 4] = np.inf
+        wq = rng.normal(1, 0.1, hd).astype(np.float32)
+        wk = rng.normal(1, 0.1, hd).astype(np.float32)
+        eps = np.float32(1e-6)
+        qr, kr = R.run(lambda g: R.qk_norm_rope(g, x, k, wq, wk, eps, pos, hd, theta, cs_rounded=True))
+        qo, ko = gpu.qk_norm_rope(_t(gpu, x), _t(gpu, k), _t(gpu, wq), _t(gpu, wk), eps, _t(gpu, pos), hd, theta)
+        for a, b in ((_np(qo), qr), (_np(ko), kr)):
+            fin = assert_same_specials(a, b)
+            assert_bitexact(np.where(fin, a, 0), np.where(fin, b, 0))
+
+
+def test_swiglu_special_values(gpu):
+    """silu(g)*u with g over zeros, +-inf, NaN, subnormals, values where
+    exp(-g) overflows or underflows, and u over zeros, inf and NaN: NaN, inf
+    and signed zeros where the oracle has them, finite values within 1e-5."""
+    gp = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, -100.0, 100.0, 88.7, -88.7, -103.0, 1e-45, -1e-45,
+                   1e-38, 20.0, -20.0, 0.5], np.float32)
+    up = np.array([1.0, -1.0, 0.0, -0.0, np.inf, -np.inf, np.nan, 2.5], np.float32)
+    g = np.repeat(gp, up.size).reshape(1, -1)
+    u = np.tile(up, gp.size).reshape(1, -1)
+    g = np.tile(g, (3, 8))
+    u = np.tile(u, (3, 8))
+    ref = R.run(lambda gr: R.swiglu(gr, g, u))
+    got = _np(gpu.swiglu(_t(gpu, g), _t(gpu, u)))
+    fin = assert_same_specials(got, ref)
+    nz = fin & (ref != 0)
+    rel = np.abs(got[nz].astype(np.float64) - ref[nz]) / np.abs(ref[nz].astype(np.float64))
+    assert rel.max() <= REL_TOL
+    ref = R.run(lambda gr: gr.silu(g))
+    got = _np(gpu.swiglu(_t(gpu, g)))
+    fin = assert_same_specials(got, ref)
+    nz = fin & (ref != 0)
+    rel = np.abs(got[nz].astype(np.float64) - ref[nz]) / np.abs(ref[nz].astype(np.float64))
+    assert rel.max() <= REL_TOL
+
+
 @pytest.mark.parametrize("swapped", [False, True])
 def test_glu_swiglu_single_tensor(gpu, swapped):
     rng = np.random.default_rng(17)
@@ -682,11 +791,18 @@ def test_snake_special_alphas(gpu):
     others the reciprocal route; power-of-two, negative, subnormal and extreme
     alphas exercise exact ties, overflow to inf and underflow. NaN and inf land
     where the oracle puts them; finite outputs meet the Snake tolerance. 37 rows
-    also leave a partial group of the kernel's 2 rows per lane."""
+    also leave a partial group of the kernel's 2 rows per lane. Rows 1-2 hold
+    special x: +-inf and NaN (sin gives NaN), +-3e38, subnormals, and
+    arguments on both sides of the fast sine's |a*x| < 2^15 range, up to 1e30
+    (the full-range sine)."""
     rng = np.random.default_rng(SEED + 99)
     T, C = 37, 64
     x = rng.standard_normal((T, C)).astype(np.float32)
     x[0, :] = 0.0
+    xs = np.array([np.inf, -np.inf, np.nan, 3e38, -3e38, 1e-45, -1e-40, 40000.0, -1e6, 1e30, 32767.99, 32768.0,
+                   -32768.0, 12345.678, 3276.8, 1e-3], np.float32)
+    x[1, :] = np.tile(xs, C // xs.size)
+    x[2, :] = np.roll(x[1, :], 5)
     alpha = np.exp(rng.uniform(np.log(0.1), np.log(10.0), C)).astype(np.float32)
     alpha[:16] = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 2.0, 0.125, -4.0, 1e-39, -1e-30, 3e38, 1e-45,
                            2.0 ** -126, 2.0 ** 100, -0.5, 1.0], np.float32)
