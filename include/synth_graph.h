@@ -1,0 +1,142 @@
+/*
+ * synth_graph.h -- node-run executor of libsynth_hip: the graph_compute core
+ * of a ggml backend module, without ggml's headers.
+ *
+ * A ggml backend receives the nodes the scheduler placed on it as an ordered
+ * list (ggml_cgraph, topological, the order ggml_build_forward_expand visits
+ * them: src[0] before src[1]) and must run them in that order; a fusing
+ * backend runs a recognised node run as one launch when the run's
+ * intermediate tensors are read nowhere else (no other node of the list, no
+ * later split, not a graph output). This file is that logic over
+ * plain descriptors: the module's glue turns each ggml_tensor node into an
+ * shp_node (op kind, op_params words, dst and src descriptors, and for each
+ * src the index of the node that produced it) and calls shp_graph_compute
+ * from its graph_compute, and shp_graph_node_supported from supports_op
+ * (src/backend-plan.cpp:120-131 builds the scheduler that asks both).
+ *
+ * Runs recognised (each one launch, bit-identical to running its nodes one by
+ * one, which is what the reference's graphs compute today):
+ *   RMS_NORM [CPY] MUL [ROPE [CPY]]  rms_norm()*w, with the gain cast and a
+ *        following NEOX rope and cache copy folded in
+ *        (src/arch/qwen3-tts/operations.cpp:20-32, 98-116)
+ *   ADD RMS_NORM [CPY] MUL           residual add + post-attention norm
+ *        (:143-145, :147 -> :86); the sum is written when read elsewhere
+ *   SILU MUL                         SwiGLU (:39-41)
+ *   ADD LEAKY_RELU                   residual carry
+ *        (src/arch/vits/waveform-decoder.cpp:150-158)
+ *   ADD.. SCALE LEAKY_RELU           branch average (:214-225)
+ *   MUL SIN MUL|SQR DIV ADD          Snake (src/arch/kokoro/operations.cpp:137-147)
+ *   MUL SIN MUL|SQR SCALE DIV ADD    guarded Snake (src/arch/omnivoice/codec.cpp:51-68)
+ *   EXP MUL SIN SQR|MUL EXP SCALE DIV ADD  SnakeBeta (src/arch/qwen3-tts/codec.cpp:184-200)
+ *   GET_ROWS (GET_ROWS ADD)+         multi-codebook gather->sum
+ *        (src/arch/qwen3-tts/code-predictor.cpp:82-107)
+ * Any other supported node runs alone through its entry point in
+ * synth_hip.h. View-like nodes (NONE, VIEW, RESHAPE, PERMUTE, TRANSPOSE)
+ * are SHP_NODE_NOP: no work.
+ */
+#ifndef SYNTH_GRAPH_H
+#define SYNTH_GRAPH_H
+
+#include "synth_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Node kinds, named for the ggml op (and unary/GLU op) each stands for. The
+ * values are this library's own; the glue maps ggml's enums by name. op_params
+ * hold the words ggml's op constructor stored, in its layout. */
+typedef enum shp_node_op {
+    SHP_NODE_NOP = 0,    /* GGML_OP_NONE, VIEW, RESHAPE, PERMUTE, TRANSPOSE */
+    SHP_NODE_ADD,        /* GGML_OP_ADD */
+    SHP_NODE_MUL,        /* GGML_OP_MUL */
+    SHP_NODE_DIV,        /* GGML_OP_DIV */
+    SHP_NODE_SQR,        /* GGML_OP_SQR */
+    SHP_NODE_SIN,        /* GGML_OP_SIN */
+    SHP_NODE_SCALE,      /* GGML_OP_SCALE: f32 {s, b} */
+    SHP_NODE_CPY,        /* GGML_OP_CPY (ggml_cpy, ggml_cast): src[0] into dst */
+    SHP_NODE_GET_ROWS,   /* GGML_OP_GET_ROWS: src[0] table, src[1] ids */
+    SHP_NODE_RMS_NORM,   /* GGML_OP_RMS_NORM: f32 {eps} */
+    SHP_NODE_SOFT_MAX,   /* GGML_OP_SOFT_MAX: f32 {scale, max_bias}; src[1] mask or absent */
+    SHP_NODE_ROPE,       /* GGML_OP_ROPE: i32 {n_past, n_dims, mode, n_ctx, n_ctx_orig},
+                            f32 [5..10] {freq_base, freq_scale, ext_factor, attn_factor,
+                            beta_fast, beta_slow}; src[1] positions, src[2] freq factors */
+    SHP_NODE_LEAKY_RELU, /* GGML_OP_LEAKY_RELU: f32 {negative_slope} */
+    SHP_NODE_SILU,       /* GGML_OP_UNARY, GGML_UNARY_OP_SILU */
+    SHP_NODE_EXP,        /* GGML_OP_UNARY, GGML_UNARY_OP_EXP */
+    SHP_NODE_GLU_SWIGLU, /* GGML_OP_GLU, GGML_GLU_OP_SWIGLU: i32 [1] swapped; src[1] absent
+                            (single tensor) or the second half (split form) */
+    SHP_NODE_OP_COUNT
+} shp_node_op;
+
+#define SHP_NODE_MAX_SRC     3
+#define SHP_NODE_FLAG_OUTPUT 1u /* dst is read after this graph (GGML_TENSOR_FLAG_OUTPUT) */
+
+typedef struct shp_node {
+    int32_t    op;                         /* shp_node_op */
+    uint32_t   flags;                      /* SHP_NODE_FLAG_* */
+    int32_t    src_node[SHP_NODE_MAX_SRC]; /* index in this list of the node whose dst
+                                              src[i] is, or -1 (a leaf, a tensor from
+                                              outside the list, or no src) */
+    int32_t    uses;                       /* reads of dst in the whole graph (ggml's use
+                                              count, later splits included), or 0 when
+                                              this list holds every read */
+    int32_t    op_params[16];
+    shp_tensor dst;
+    shp_tensor src[SHP_NODE_MAX_SRC]; /* data == NULL: no such src */
+} shp_node;
+
+typedef enum shp_run_kind {
+    SHP_RUN_UNSUPPORTED = -1, /* the node cannot run here */
+    SHP_RUN_NOP         = 0,  /* view-like node */
+    SHP_RUN_SINGLE,           /* one node through its own entry point */
+    SHP_RUN_NORM_MUL,
+    SHP_RUN_NORM_MUL_ROPE,
+    SHP_RUN_ADD_NORM_MUL,
+    SHP_RUN_SILU_MUL,
+    SHP_RUN_ADD_LEAKY,
+    SHP_RUN_ADD_SCALE_LEAKY,
+    SHP_RUN_SNAKE,
+    SHP_RUN_SNAKE_GUARDED,
+    SHP_RUN_SNAKE_BETA,
+    SHP_RUN_GATHER_SUM
+} shp_run_kind;
+
+typedef struct shp_graph_run {
+    int32_t kind;  /* shp_run_kind */
+    int32_t first; /* index of the run's first node */
+    int32_t last;  /* index of its last node (the run's result); view-like nodes
+                      between first and last belong to no run */
+    int32_t nodes; /* nodes the run executes */
+} shp_graph_run;
+
+/* 1 when the node can run here on its own (supports_op), else 0. */
+int32_t shp_graph_node_supported(const shp_node * node);
+
+/*
+ * Splits the list into runs, in order, without launching anything (host code
+ * only). runs may be NULL to count them; *n_runs receives the count.
+ * SHP_ERR_INVALID_ARG for a malformed list: a src_node not naming an earlier
+ * node, a src_node without its src, a negative uses or one below the reads
+ * the list itself makes, an unknown op.
+ */
+shp_status_t shp_graph_plan(const shp_node * nodes,
+                            int32_t          n_nodes,
+                            shp_graph_run *  runs,
+                            int32_t          capacity,
+                            int32_t *        n_runs);
+
+/*
+ * Runs the list on `stream`, run by run. A list holding an unsupported node
+ * returns SHP_ERR_UNSUPPORTED with nothing enqueued (ggml's scheduler never
+ * hands a backend such a node when supports_op said no). Otherwise the first
+ * failing launch's status is returned (runs before it have been enqueued),
+ * as graph_compute's ggml_status is.
+ */
+shp_status_t shp_graph_compute(const shp_node * nodes, int32_t n_nodes, shp_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SYNTH_GRAPH_H */

@@ -289,6 +289,29 @@ shp_status_t shp_add_leaky_relu(const shp_tensor * a,
 shp_status_t shp_add(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream);
 
 /*
+ * Single nodes of the runs above, for graphs where a run does not stay
+ * together (the node executor in synth_graph.h falls back to them), each
+ * bit-identical to its ggml-CPU node except where noted:
+ *   shp_mul  ggml_mul, b as in shp_add: SwiGLU's mul when an up-projection
+ *            sits between it and the silu (qwen3-tts/operations.cpp:39-41),
+ *            the Snake multiplies (kokoro/operations.cpp:143,145)
+ *   shp_div  ggml_div, b as in shp_add (kokoro/operations.cpp:146), IEEE
+ *   shp_sin  ggml_sin (kokoro/operations.cpp:144): the Snake kernels' sine,
+ *            within 1 ulp of the correctly rounded one as libm's sinf is
+ *            (so a Snake run and its nodes one by one agree bit for bit)
+ *   shp_sqr  ggml_sqr (qwen3-tts/codec.cpp:196)
+ *   shp_cpy  ggml_cpy / ggml_cast into F32 of the same shape from F32, F16
+ *            or BF16 (qwen3-tts/operations.cpp:20-25, the KV-cache writes
+ *            :109-116); rows may be strided on either side
+ * All F32 unless stated; y has a's shape.
+ */
+shp_status_t shp_mul(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream);
+shp_status_t shp_div(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream);
+shp_status_t shp_sin(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
+shp_status_t shp_sqr(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
+shp_status_t shp_cpy(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
+
+/*
  * The non-GEMM node runs of one Qwen3 decoder layer,
  * src/arch/qwen3-tts/operations.cpp:84-147, in the layer's order. The
  * layer's matrix products and its attention run between these node runs in

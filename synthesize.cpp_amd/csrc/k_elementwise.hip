@@ -24,7 +24,21 @@
 namespace shp {
 namespace {
 
-enum EwOp { kSwiglu = 0, kSilu = 1, kAdd = 2, kAddLeaky = 3, kLeaky = 4, kExp = 5, kScale = 6, kScaleBias = 7 };
+enum EwOp {
+    kSwiglu    = 0,
+    kSilu      = 1,
+    kAdd       = 2,
+    kAddLeaky  = 3,
+    kLeaky     = 4,
+    kExp       = 5,
+    kScale     = 6,
+    kScaleBias = 7,
+    kMul       = 8,
+    kDiv       = 9,
+    kSin       = 10,
+    kSqr       = 11,
+    kCopy      = 12
+};
 
 // Snake family: y = x + sin(x*al)^2 / den with per-channel al and den.
 //   kSnakePlain   (kokoro/operations.cpp:137-147):   al = den = alpha
@@ -97,10 +111,25 @@ template <int OP> __device__ __forceinline__ float ew(float a, float b, const Ew
     } else if constexpr (OP == kScale) {
         // ggml_scale (bias 0): a plain multiply, so -0 stays -0.
         return a * g.scale;
-    } else {
+    } else if constexpr (OP == kScaleBias) {
         // ggml_scale_bias with a non-zero bias: one fused multiply-add, as
         // ggml-CPU's vectorised path computes it on FMA hardware.
         return fmaf(a, g.scale, g.bias);
+    } else if constexpr (OP == kMul) {
+        return a * b;
+    } else if constexpr (OP == kDiv) {
+        return a / b;
+    } else if constexpr (OP == kSin) {
+        // The sine of the Snake kernels, so a Snake run and its nodes one by
+        // one agree bit for bit. Its reduction turns -0 into +0 (-0 - 0*pi/2 is
+        // +0); sinf keeps the sign of a zero, so zeros pass through (inside
+        // Snake the sine is squared and the sign does not matter).
+        return a == 0.0f ? a : (sin_fast_ok(a) ? sin_f32_fast(a) : sinf(a));
+    } else if constexpr (OP == kSqr) {
+        return a * a;
+    } else {
+        static_assert(OP == kCopy, "unknown elementwise op");
+        return a;
     }
 }
 
@@ -701,7 +730,13 @@ extern "C" shp_status_t shp_add_leaky_relu(const shp_tensor * a,
     return launch_ew<kAddLeaky, true, false, true>(plan.args, plan.flat, plan.vec, ss);
 }
 
-extern "C" shp_status_t shp_add(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream) {
+namespace shp {
+namespace {
+
+// ggml_add / ggml_mul / ggml_div: b the same shape as a, or one contiguous row
+// of ne0 elements repeated over every row.
+template <int OP>
+shp_status_t binary_entry(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream) {
     if (b == nullptr) {
         return SHP_ERR_INVALID_ARG;
     }
@@ -713,18 +748,102 @@ extern "C" shp_status_t shp_add(const shp_tensor * a, const shp_tensor * b, shp_
     const hipStream_t ss = as_stream(stream);
     if (plan.bcast) {
         const bool b16 = reinterpret_cast<uintptr_t>(b->data) % 16 == 0;
-        return launch_ew<kAdd, true, true, false>(plan.args, plan.flat && b16, plan.vec && b16, ss);
+        return launch_ew<OP, true, true, false>(plan.args, plan.flat && b16, plan.vec && b16, ss);
     }
-    return launch_ew<kAdd, true, false, false>(plan.args, plan.flat, plan.vec, ss);
+    return launch_ew<OP, true, false, false>(plan.args, plan.flat, plan.vec, ss);
 }
 
-extern "C" shp_status_t shp_exp(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
+template <int OP> shp_status_t unary_entry(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
     EwPlan             plan;
     const shp_status_t st = plan_ew(x, nullptr, false, y, nullptr, plan);
     if (st != SHP_OK) {
         return st;
     }
-    return launch_ew<kExp, false, false, false>(plan.args, plan.flat, plan.vec, as_stream(stream));
+    return launch_ew<OP, false, false, false>(plan.args, plan.flat, plan.vec, as_stream(stream));
+}
+
+// ggml_cpy / ggml_cast of an F16 or BF16 tensor into F32 of the same shape:
+// one exact conversion per element, rows addressed through their byte strides.
+// (The weight casts of as_f32, qwen3-tts/operations.cpp:20-25, when they are
+// not folded into the norm that reads the gain.)
+struct CastArgs {
+    const void * x;
+    RowMap       xm;
+    float *      y;
+    RowMap       ym;
+    int64_t      nrows;
+    int32_t      ne0;
+    int32_t      pad;
+};
+
+template <int TYPE> __global__ __launch_bounds__(256) void k_cast_rows(const CastArgs a) {
+    for (int64_t r = blockIdx.x; r < a.nrows; r += gridDim.x) {
+        const uint16_t * xr =
+            reinterpret_cast<const uint16_t *>(static_cast<const char *>(a.x) + row_offset(a.xm, r));
+        float * yr = reinterpret_cast<float *>(reinterpret_cast<char *>(a.y) + row_offset(a.ym, r));
+        for (int c = static_cast<int>(threadIdx.x); c < a.ne0; c += 256) {
+            const uint32_t h = xr[c];
+            yr[c]            = TYPE == SHP_TYPE_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+        }
+    }
+}
+
+}  // namespace
+}  // namespace shp
+
+extern "C" shp_status_t shp_add(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream) {
+    return binary_entry<kAdd>(a, b, y, stream);
+}
+
+extern "C" shp_status_t shp_mul(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream) {
+    return binary_entry<kMul>(a, b, y, stream);
+}
+
+extern "C" shp_status_t shp_div(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream) {
+    return binary_entry<kDiv>(a, b, y, stream);
+}
+
+extern "C" shp_status_t shp_sin(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
+    return unary_entry<kSin>(x, y, stream);
+}
+
+extern "C" shp_status_t shp_sqr(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
+    return unary_entry<kSqr>(x, y, stream);
+}
+
+extern "C" shp_status_t shp_cpy(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
+    if (!well_formed(x) || !well_formed(y)) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    if (y->type != SHP_TYPE_F32 || (x->type != SHP_TYPE_F32 && x->type != SHP_TYPE_F16 && x->type != SHP_TYPE_BF16)) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    if (!same_shape(*x, *y) || x->ne[0] > INT32_MAX) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    if (x->type == SHP_TYPE_F32) {
+        return unary_entry<kCopy>(x, y, stream);
+    }
+    CastArgs a{};
+    a.x              = x->data;
+    a.xm             = make_rowmap(*x);
+    a.y              = static_cast<float *>(y->data);
+    a.ym             = make_rowmap(*y);
+    a.nrows          = nrows(*x);
+    a.ne0            = static_cast<int32_t>(x->ne[0]);
+    const int64_t bl = a.nrows < 65536 ? a.nrows : 65536;
+    if (x->type == SHP_TYPE_BF16) {
+        hipLaunchKernelGGL((k_cast_rows<SHP_TYPE_BF16>), dim3(static_cast<unsigned>(bl)), dim3(256), 0,
+                           as_stream(stream), a);
+    } else {
+        hipLaunchKernelGGL((k_cast_rows<SHP_TYPE_F16>), dim3(static_cast<unsigned>(bl)), dim3(256), 0,
+                           as_stream(stream), a);
+    }
+    return launch_status();
+}
+
+extern "C" shp_status_t shp_exp(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
+    return unary_entry<kExp>(x, y, stream);
 }
 
 extern "C" shp_status_t shp_scale_bias(const shp_tensor * x, float s, float b, shp_tensor * y, shp_stream_t stream) {

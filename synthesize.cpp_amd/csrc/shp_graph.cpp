@@ -1,0 +1,872 @@
+// Node-run executor: splits an ordered ggml-style node list into runs (a fused
+// run where the reference's graphs emit one, else one node at a time) and
+// launches each through the entry points of synth_hip.h.
+//
+// A run is recognised from its last node (its result) backwards through the
+// src_node links, and is taken only when the nodes it reaches are exactly the
+// next nodes of the list (view-like nodes aside) and every intermediate result
+// it does not write is read by nothing outside the run and is not a graph
+// output. That is the condition under which skipping the intermediate writes
+// cannot be observed. Every fused launch computes what the nodes compute one
+// by one, bit for bit.
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+#include "shp_internal.hpp"
+#include "synth_graph.h"
+#include "synth_hip.h"
+
+namespace shp {
+namespace {
+
+float fparam(const shp_node & n, int i) {
+    float f;
+    std::memcpy(&f, &n.op_params[i], sizeof(f));
+    return f;
+}
+
+bool present(const shp_tensor & t) {
+    return t.data != nullptr;
+}
+
+// The same tensor: same memory, shape and strides.
+bool same_tensor(const shp_tensor & a, const shp_tensor & b) {
+    return a.data == b.data && a.type == b.type && same_shape(a, b) && a.nb[0] == b.nb[0] && a.nb[1] == b.nb[1] &&
+           a.nb[2] == b.nb[2] && a.nb[3] == b.nb[3];
+}
+
+bool f32_of(const shp_tensor & t) {
+    return well_formed(&t) && t.type == SHP_TYPE_F32 && t.ne[0] <= INT32_MAX;
+}
+
+// ggml_mul / ggml_add / ggml_div operand b: a's shape, or one contiguous row of
+// a.ne[0] elements repeated over a's rows.
+bool row_operand(const shp_tensor & a, const shp_tensor & b) {
+    return f32_of(b) && (same_shape(a, b) || (nelements(b) == a.ne[0] && contiguous(b)));
+}
+
+// A gain vector of n elements: F32, BF16 or F16, one contiguous row.
+bool gain_vector(const shp_tensor & w, int64_t n) {
+    return well_formed(&w) && weight_kind(w.type) >= 0 && nelements(w) == n && contiguous(w);
+}
+
+bool unary_ok(const shp_node & n) {
+    return f32_of(n.src[0]) && f32_of(n.dst) && same_shape(n.src[0], n.dst);
+}
+
+bool binary_ok(const shp_node & n) {
+    return f32_of(n.src[0]) && f32_of(n.dst) && same_shape(n.src[0], n.dst) && row_operand(n.src[0], n.src[1]);
+}
+
+bool rope_params_ok(const shp_node & n) {
+    const int32_t n_dims = n.op_params[1];
+    const int32_t mode   = n.op_params[2];
+    const auto &  x      = n.src[0];
+    const auto &  pos    = n.src[1];
+    return mode == SHP_ROPE_TYPE_NEOX && fparam(n, 7) == 0.0f && !present(n.src[2]) && f32_of(x) && f32_of(n.dst) &&
+           same_shape(x, n.dst) && x.ne[3] == 1 && well_formed(&pos) && pos.type == SHP_TYPE_I32 &&
+           nelements(pos) == x.ne[2] && contiguous(pos) && n_dims > 0 && n_dims % 2 == 0 && n_dims <= x.ne[0];
+}
+
+bool single_ok(const shp_node & n) {
+    for (int k = 0; k < SHP_NODE_MAX_SRC; ++k) {
+        if (present(n.src[k]) && !well_formed(&n.src[k])) {
+            return false;
+        }
+    }
+    switch (n.op) {
+        case SHP_NODE_NOP:
+            return true;
+        case SHP_NODE_ADD:
+        case SHP_NODE_MUL:
+        case SHP_NODE_DIV:
+            return binary_ok(n);
+        case SHP_NODE_SQR:
+        case SHP_NODE_SIN:
+        case SHP_NODE_SILU:
+        case SHP_NODE_EXP:
+        case SHP_NODE_LEAKY_RELU:
+        case SHP_NODE_SCALE:
+            return unary_ok(n);
+        case SHP_NODE_CPY:
+            return well_formed(&n.src[0]) &&
+                   (n.src[0].type == SHP_TYPE_F32 || n.src[0].type == SHP_TYPE_F16 ||
+                    n.src[0].type == SHP_TYPE_BF16) &&
+                   f32_of(n.dst) && same_shape(n.src[0], n.dst);
+        case SHP_NODE_GET_ROWS: {
+            const auto & t   = n.src[0];
+            const auto & ids = n.src[1];
+            const bool   tt  = t.type == SHP_TYPE_F32 || t.type == SHP_TYPE_F16 || t.type == SHP_TYPE_BF16 ||
+                            t.type == SHP_TYPE_Q8_0;
+            return well_formed(&t) && tt && well_formed(&ids) && ids.type == SHP_TYPE_I32 && f32_of(n.dst) &&
+                   n.dst.ne[0] == t.ne[0] && n.dst.ne[1] == ids.ne[0] && n.dst.ne[2] == ids.ne[1] &&
+                   n.dst.ne[3] == ids.ne[2] && ids.ne[3] == 1;
+        }
+        case SHP_NODE_RMS_NORM:
+            return unary_ok(n) && fparam(n, 0) >= 0.0f;
+        case SHP_NODE_SOFT_MAX: {
+            const auto & m = n.src[1];
+            return unary_ok(n) && fparam(n, 1) == 0.0f && !present(n.src[2]) &&
+                   (!present(m) || (f32_of(m) && m.ne[0] == n.src[0].ne[0] && m.ne[1] >= n.src[0].ne[1]));
+        }
+        case SHP_NODE_ROPE:
+            return rope_params_ok(n);
+        case SHP_NODE_GLU_SWIGLU: {
+            const auto & a = n.src[0];
+            if (!f32_of(a) || !f32_of(n.dst)) {
+                return false;
+            }
+            if (present(n.src[1])) {
+                return same_shape(a, n.src[1]) && f32_of(n.src[1]) && same_shape(a, n.dst);
+            }
+            return a.ne[0] % 2 == 0 && n.dst.ne[0] * 2 == a.ne[0] && n.dst.ne[1] == a.ne[1] &&
+                   n.dst.ne[2] == a.ne[2] && n.dst.ne[3] == a.ne[3];
+        }
+        default:
+            return false;
+    }
+}
+
+// What a run launches: which entry point, and its operands.
+struct Launch {
+    int                     kind  = SHP_RUN_SINGLE;
+    int                     first = 0;
+    int                     last  = 0;
+    int                     count = 0;
+    const shp_tensor *      x     = nullptr;
+    const shp_tensor *      b     = nullptr;
+    const shp_tensor *      w     = nullptr;
+    const shp_tensor *      c1    = nullptr;
+    shp_tensor *            y     = nullptr;
+    shp_tensor *            sum   = nullptr;
+    float                   f0    = 0.0f;
+    float                   f1    = 0.0f;
+    float                   f2    = 0.0f;
+    int32_t                 i0    = 0;
+    std::vector<shp_tensor> terms;
+    shp_tensor              codes{};
+};
+
+class Planner {
+  public:
+    Planner(const shp_node * nodes, int n) : nodes_(nodes), n_(n) {}
+
+    shp_status_t init() {
+        consumers_.assign(n_, {});
+        for (int i = 0; i < n_; ++i) {
+            const shp_node & nd = nodes_[i];
+            if (nd.uses < 0 || nd.op < 0 || nd.op >= SHP_NODE_OP_COUNT) {
+                return SHP_ERR_INVALID_ARG;
+            }
+            for (int k = 0; k < SHP_NODE_MAX_SRC; ++k) {
+                const int j = nd.src_node[k];
+                if (j == -1) {
+                    continue;
+                }
+                if (j < 0 || j >= i || !present(nd.src[k])) {
+                    return SHP_ERR_INVALID_ARG;
+                }
+                consumers_[j].push_back(i);
+            }
+            if (nd.op != SHP_NODE_NOP) {
+                order_.push_back(i);
+            }
+        }
+        for (int j = 0; j < n_; ++j) {
+            if (nodes_[j].uses != 0 && nodes_[j].uses < static_cast<int32_t>(consumers_[j].size())) {
+                return SHP_ERR_INVALID_ARG;
+            }
+        }
+        return SHP_OK;
+    }
+
+    // Every run of the list, in order; NOP nodes are runs of their own.
+    std::vector<Launch> plan() const {
+        std::vector<Launch> out;
+        size_t              p = 0;
+        int                 i = 0;
+        while (i < n_) {
+            if (nodes_[i].op == SHP_NODE_NOP) {
+                Launch l;
+                l.kind  = SHP_RUN_NOP;
+                l.first = l.last = i;
+                out.push_back(l);
+                ++i;
+                continue;
+            }
+            Launch l;
+            const int used = match(p, l);
+            if (used == 0) {
+                l       = Launch{};
+                l.kind  = single_ok(nodes_[i]) ? SHP_RUN_SINGLE : SHP_RUN_UNSUPPORTED;
+                l.first = l.last = i;
+                l.count          = 1;
+                out.push_back(l);
+                ++p;
+                ++i;
+                continue;
+            }
+            l.first = order_[p];
+            l.last  = order_[p + used - 1];
+            l.count = used;
+            out.push_back(l);
+            // NOP nodes inside the span become their own runs after it.
+            for (int j = l.first + 1; j < l.last; ++j) {
+                if (nodes_[j].op == SHP_NODE_NOP) {
+                    Launch v;
+                    v.kind  = SHP_RUN_NOP;
+                    v.first = v.last = j;
+                    out.push_back(v);
+                }
+            }
+            p += used;
+            i = l.last + 1;
+        }
+        return out;
+    }
+
+    const shp_node & node(int i) const { return nodes_[i]; }
+
+  private:
+    const shp_node *              nodes_;
+    int                           n_;
+    std::vector<int>              order_;
+    std::vector<std::vector<int>> consumers_;
+
+    // Node index at window position p + k, or -1 past the end.
+    int at(size_t p, int k) const { return p + k < order_.size() ? order_[p + k] : -1; }
+
+    // The window order_[p, p + k) is exactly `members` (each listed once).
+    bool window_is(size_t p, const std::vector<int> & members) const {
+        if (p + members.size() > order_.size()) {
+            return false;
+        }
+        std::vector<char> seen(members.size(), 0);
+        for (size_t k = 0; k < members.size(); ++k) {
+            bool found = false;
+            for (size_t m = 0; m < members.size(); ++m) {
+                if (!seen[m] && members[m] == order_[p + k]) {
+                    seen[m] = 1;
+                    found   = true;
+                    break;
+                }
+            }
+            if (!found) {
+                return false;
+            }
+        }
+        return true;
+    }
+
+    // j's result may go unwritten: not an output, read by no later split and
+    // by no node of the list outside `members`.
+    bool internal(int j, const std::vector<int> & members) const {
+        if (nodes_[j].flags & SHP_NODE_FLAG_OUTPUT) {
+            return false;
+        }
+        if (consumers_[j].empty() || nodes_[j].uses > static_cast<int32_t>(consumers_[j].size())) {
+            return false;
+        }
+        for (int c : consumers_[j]) {
+            bool in = false;
+            for (int m : members) {
+                in = in || m == c;
+            }
+            if (!in) {
+                return false;
+            }
+        }
+        return true;
+    }
+
+    // j's result is read outside `members` (or is an output): it must be written.
+    bool needed_outside(int j, const std::vector<int> & members) const {
+        return (nodes_[j].flags & SHP_NODE_FLAG_OUTPUT) || !internal(j, members);
+    }
+
+    bool is(int j, int op) const { return j >= 0 && nodes_[j].op == op; }
+
+    int src(int j, int k) const { return nodes_[j].src_node[k]; }
+
+    int match(size_t p, Launch & l) const {
+        int used;
+        if ((used = match_gather_sum(p, l)) != 0) {
+            return used;
+        }
+        for (int k : { 8, 6, 5 }) {
+            if ((used = match_snake(p, k, l)) != 0) {
+                return used;
+            }
+        }
+        for (int k : { 4, 3 }) {
+            if ((used = match_add_norm(p, k, l)) != 0) {
+                return used;
+            }
+        }
+        for (int k : { 5, 4, 3, 2 }) {
+            if ((used = match_norm(p, k, l)) != 0) {
+                return used;
+            }
+        }
+        for (int k = 2 + 7; k >= 3; --k) {
+            if ((used = match_add_scale_leaky(p, k, l)) != 0) {
+                return used;
+            }
+        }
+        if ((used = match_add_leaky(p, l)) != 0) {
+            return used;
+        }
+        return match_silu_mul(p, l);
+    }
+
+    // GET_ROWS, then (GET_ROWS, ADD(acc, rows)) per further group: the tables
+    // share a type and row length, the ids are the columns of one contiguous
+    // I32 [frames, groups] tensor (consecutive views, code-predictor.cpp:99).
+    int match_gather_sum(size_t p, Launch & l) const {
+        const int g0 = at(p, 0);
+        if (!is(g0, SHP_NODE_GET_ROWS) || !single_ok(nodes_[g0])) {
+            return 0;
+        }
+        const shp_tensor & t0   = nodes_[g0].src[0];
+        const shp_tensor & ids0 = nodes_[g0].src[1];
+        const int64_t      fr   = ids0.ne[0];
+        if (ids0.ne[1] != 1 || ids0.ne[2] != 1 || !contiguous(ids0) || !contiguous(nodes_[g0].dst)) {
+            return 0;
+        }
+        std::vector<int> members{ g0 };
+        int              acc    = g0;
+        int              groups = 1;
+        int              best   = 0;
+        std::vector<int> best_members;
+        while (groups < 64) {
+            const int gr = at(p, 2 * groups - 1);
+            const int ad = at(p, 2 * groups);
+            if (!is(gr, SHP_NODE_GET_ROWS) || !is(ad, SHP_NODE_ADD)) {
+                break;
+            }
+            const shp_node & G = nodes_[gr];
+            const shp_node & A = nodes_[ad];
+            const bool order_ok = (src(ad, 0) == acc && src(ad, 1) == gr) || (src(ad, 1) == acc && src(ad, 0) == gr);
+            const auto & ids    = G.src[1];
+            const bool   ids_ok = well_formed(&ids) && ids.type == SHP_TYPE_I32 && ids.ne[0] == fr && ids.ne[1] == 1 &&
+                                ids.ne[2] == 1 && ids.ne[3] == 1 &&
+                                static_cast<const char *>(ids.data) ==
+                                    static_cast<const char *>(ids0.data) + static_cast<size_t>(groups) * fr * 4;
+            const bool tab_ok = well_formed(&G.src[0]) && G.src[0].type == t0.type && G.src[0].ne[0] == t0.ne[0] &&
+                                single_ok(G);
+            if (!order_ok || !ids_ok || !tab_ok || !f32_of(A.dst) || !same_shape(A.dst, nodes_[g0].dst)) {
+                break;
+            }
+            members.push_back(gr);
+            members.push_back(ad);
+            acc = ad;
+            ++groups;
+            bool ok = true;
+            for (size_t m = 0; m + 1 < members.size(); ++m) {
+                ok = ok && internal(members[m], members);
+            }
+            if (ok) {
+                best         = groups;
+                best_members = members;
+            }
+        }
+        if (best < 2) {
+            return 0;
+        }
+        l.kind = SHP_RUN_GATHER_SUM;
+        l.terms.clear();
+        l.terms.push_back(t0);
+        for (int g = 1; g < best; ++g) {
+            l.terms.push_back(nodes_[best_members[2 * g - 1]].src[0]);
+        }
+        l.codes       = ids0;
+        l.codes.ne[1] = best;
+        l.codes.nb[1] = static_cast<size_t>(fr) * 4;
+        l.codes.nb[2] = l.codes.nb[1] * best;
+        l.codes.nb[3] = l.codes.nb[2];
+        l.y           = const_cast<shp_tensor *>(&nodes_[best_members.back()].dst);
+        return 2 * best - 1;
+    }
+
+    // The Snake family, k = 5 (Snake), 6 (guarded), 8 (SnakeBeta):
+    //   ADD(x, DIV(SQ(SIN(MUL(x, al))), den)) with SQ = MUL(s, s) or SQR(s);
+    //   Snake: den = al; guarded: den = SCALE(al, 1, 1e-9);
+    //   SnakeBeta: al = EXP(la), den = SCALE(EXP(lb), 1, 1e-9).
+    int match_snake(size_t p, int k, Launch & l) const {
+        const int ad = at(p, k - 1);
+        if (!is(ad, SHP_NODE_ADD)) {
+            return 0;
+        }
+        const shp_node & A  = nodes_[ad];
+        const int        dv = src(ad, 1);
+        if (!is(dv, SHP_NODE_DIV)) {
+            return 0;
+        }
+        const int sq = src(dv, 0);
+        int       sn = -1;
+        if (is(sq, SHP_NODE_MUL) && src(sq, 0) >= 0 && src(sq, 0) == src(sq, 1)) {
+            sn = src(sq, 0);
+        } else if (is(sq, SHP_NODE_SQR)) {
+            sn = src(sq, 0);
+        }
+        if (!is(sn, SHP_NODE_SIN)) {
+            return 0;
+        }
+        const int ml = src(sn, 0);
+        if (!is(ml, SHP_NODE_MUL)) {
+            return 0;
+        }
+        const shp_node & M = nodes_[ml];
+        const shp_tensor & x = A.src[0];
+        if (!f32_of(x) || !same_tensor(M.src[0], x) || !f32_of(A.dst) || !same_shape(A.dst, x)) {
+            return 0;
+        }
+        const int64_t C = x.ne[0];
+        const int     den = src(dv, 1);
+        std::vector<int> members{ ml, sn, sq, dv, ad };
+        auto curve_ok = [C](const shp_tensor & c) {
+            return well_formed(&c) && c.type == SHP_TYPE_F32 && nelements(c) == C && contiguous(c);
+        };
+        auto guard_ok = [&](int j) {
+            return is(j, SHP_NODE_SCALE) && fparam(nodes_[j], 0) == 1.0f && fparam(nodes_[j], 1) == 1e-9f;
+        };
+        int kind;
+        if (k == 5) {
+            if (den != -1 && src(ml, 1) != den) {
+                return 0;
+            }
+            if (!curve_ok(M.src[1]) || !same_tensor(nodes_[dv].src[1], M.src[1])) {
+                return 0;
+            }
+            kind = SHP_RUN_SNAKE;
+            l.w  = &M.src[1];
+        } else if (k == 6) {
+            if (!guard_ok(den) || !curve_ok(M.src[1]) || !same_tensor(nodes_[den].src[0], M.src[1])) {
+                return 0;
+            }
+            members.push_back(den);
+            kind = SHP_RUN_SNAKE_GUARDED;
+            l.w  = &M.src[1];
+        } else {
+            const int ea = src(ml, 1);
+            if (!is(ea, SHP_NODE_EXP) || !guard_ok(den)) {
+                return 0;
+            }
+            const int eb = src(den, 0);
+            if (!is(eb, SHP_NODE_EXP) || eb == ea || !curve_ok(nodes_[ea].src[0]) || !curve_ok(nodes_[eb].src[0])) {
+                return 0;
+            }
+            members.push_back(den);
+            members.push_back(ea);
+            members.push_back(eb);
+            kind = SHP_RUN_SNAKE_BETA;
+            l.w  = &nodes_[ea].src[0];
+            l.c1 = &nodes_[eb].src[0];
+        }
+        if (static_cast<int>(members.size()) != k || !window_is(p, members)) {
+            return 0;
+        }
+        for (int j : members) {
+            if (j != ad && !internal(j, members)) {
+                return 0;
+            }
+        }
+        l.kind = kind;
+        l.x    = &A.src[0];
+        l.y    = const_cast<shp_tensor *>(&A.dst);
+        return k;
+    }
+
+    // MUL(n, w) whose n is the RMS_NORM `nrm`. When `cast` (a window node, or
+    // -1) produced w, the gain is that CPY's source (the as_f32 cast folded
+    // in) and `cast` is returned; otherwise w itself must be an F32 gain and
+    // -2 is returned. -1: not a gain multiply.
+    int gain_of(int mul, int nrm, int cast, const shp_tensor *& w, int64_t ne0) const {
+        const shp_node & M = nodes_[mul];
+        if (src(mul, 0) != nrm) {
+            return -1;
+        }
+        if (cast >= 0) {
+            if (src(mul, 1) != cast || !is(cast, SHP_NODE_CPY)) {
+                return -1;
+            }
+            const shp_node & Cp = nodes_[cast];
+            if (!gain_vector(Cp.src[0], ne0) || !f32_of(Cp.dst) || !same_shape(Cp.src[0], Cp.dst)) {
+                return -1;
+            }
+            w = &Cp.src[0];
+            return cast;
+        }
+        if (!gain_vector(M.src[1], ne0) || M.src[1].type != SHP_TYPE_F32) {
+            return -1;
+        }
+        w = &M.src[1];
+        return -2;
+    }
+
+    // RMS_NORM [CPY] MUL [ROPE [CPY]], k nodes.
+    int match_norm(size_t p, int k, Launch & l) const {
+        const int nrm = at(p, 0);
+        if (!is(nrm, SHP_NODE_RMS_NORM) || at(p, k - 1) < 0) {
+            return 0;
+        }
+        const shp_node & N = nodes_[nrm];
+        if (!unary_ok(N) || !(fparam(N, 0) >= 0.0f)) {
+            return 0;
+        }
+        const int64_t ne0 = N.src[0].ne[0];
+        // Find the MUL: position 1 or 2.
+        for (int mpos : { 1, 2 }) {
+            const int mul = at(p, mpos);
+            if (!is(mul, SHP_NODE_MUL) || mpos >= k) {
+                continue;
+            }
+            const shp_tensor * w    = nullptr;
+            const int          cast = gain_of(mul, nrm, mpos == 2 ? at(p, 1) : -1, w, ne0);
+            if (cast == -1) {
+                continue;
+            }
+            if (!f32_of(nodes_[mul].dst) || !same_shape(nodes_[mul].dst, N.src[0])) {
+                continue;
+            }
+            std::vector<int> members{ nrm, mul };
+            if (cast >= 0) {
+                members.push_back(cast);
+            }
+            const int rest = k - static_cast<int>(members.size());
+            int       rope = -1, cp = -1;
+            if (rest >= 1) {
+                rope = at(p, mpos + 1);
+                if (!is(rope, SHP_NODE_ROPE) || src(rope, 0) != mul || !rope_params_ok(nodes_[rope]) ||
+                    fparam(nodes_[rope], 8) != 1.0f) {
+                    continue;
+                }
+                members.push_back(rope);
+            }
+            if (rest == 2) {
+                cp = at(p, mpos + 2);
+                if (!is(cp, SHP_NODE_CPY) || src(cp, 0) != rope || !f32_of(nodes_[cp].dst) ||
+                    !same_shape(nodes_[cp].dst, nodes_[rope].dst)) {
+                    continue;
+                }
+                members.push_back(cp);
+            }
+            if (rest > 2 || !window_is(p, members)) {
+                continue;
+            }
+            const int sink = cp >= 0 ? cp : (rope >= 0 ? rope : mul);
+            bool      ok   = true;
+            for (int j : members) {
+                ok = ok && (j == sink || internal(j, members));
+            }
+            if (!ok) {
+                continue;
+            }
+            l.x  = &N.src[0];
+            l.w  = w;
+            l.f0 = fparam(N, 0);
+            l.y  = const_cast<shp_tensor *>(&nodes_[sink].dst);
+            if (rope >= 0) {
+                const shp_node & R = nodes_[rope];
+                l.kind             = SHP_RUN_NORM_MUL_ROPE;
+                l.b                = &R.src[1];
+                l.i0               = R.op_params[1];
+                l.f1               = fparam(R, 5);
+                l.f2               = fparam(R, 6);
+            } else {
+                l.kind = SHP_RUN_NORM_MUL;
+            }
+            return k;
+        }
+        return 0;
+    }
+
+    // ADD RMS_NORM [CPY] MUL, k nodes; the sum is written when read elsewhere.
+    int match_add_norm(size_t p, int k, Launch & l) const {
+        const int ad  = at(p, 0);
+        const int nrm = at(p, 1);
+        const int mul = at(p, k - 1);
+        if (!is(ad, SHP_NODE_ADD) || !is(nrm, SHP_NODE_RMS_NORM) || !is(mul, SHP_NODE_MUL) || src(nrm, 0) != ad) {
+            return 0;
+        }
+        const shp_node & A = nodes_[ad];
+        const shp_node & N = nodes_[nrm];
+        if (!f32_of(A.src[0]) || !f32_of(A.src[1]) || !same_shape(A.src[0], A.src[1]) || !f32_of(A.dst) ||
+            !same_shape(A.src[0], A.dst) || !unary_ok(N) || !(fparam(N, 0) >= 0.0f)) {
+            return 0;
+        }
+        const shp_tensor * w    = nullptr;
+        const int          cast = gain_of(mul, nrm, k == 4 ? at(p, 2) : -1, w, A.dst.ne[0]);
+        if (cast == -1) {
+            return 0;
+        }
+        if (!f32_of(nodes_[mul].dst) || !same_shape(nodes_[mul].dst, A.dst)) {
+            return 0;
+        }
+        std::vector<int> members{ ad, nrm, mul };
+        if (cast >= 0) {
+            members.push_back(cast);
+        }
+        if (!window_is(p, members) || !internal(nrm, members) || (cast >= 0 && !internal(cast, members))) {
+            return 0;
+        }
+        l.kind = SHP_RUN_ADD_NORM_MUL;
+        l.x    = &A.src[0];
+        l.b    = &A.src[1];
+        l.w    = w;
+        l.f0   = fparam(N, 0);
+        l.sum  = needed_outside(ad, members) ? const_cast<shp_tensor *>(&A.dst) : nullptr;
+        l.y    = const_cast<shp_tensor *>(&nodes_[mul].dst);
+        return k;
+    }
+
+    // ADD x (k-2), SCALE(b = 0), LEAKY_RELU: the terms in add order.
+    int match_add_scale_leaky(size_t p, int k, Launch & l) const {
+        const int nadd = k - 2;
+        const int sc   = at(p, k - 2);
+        const int lk   = at(p, k - 1);
+        if (nadd < 1 || nadd > 7 || !is(sc, SHP_NODE_SCALE) || !is(lk, SHP_NODE_LEAKY_RELU) || src(lk, 0) != sc ||
+            fparam(nodes_[sc], 1) != 0.0f) {
+            return 0;
+        }
+        std::vector<int>        members;
+        std::vector<shp_tensor> terms;
+        int                     acc = -1;
+        for (int a = 0; a < nadd; ++a) {
+            const int ad = at(p, a);
+            if (!is(ad, SHP_NODE_ADD)) {
+                return 0;
+            }
+            const shp_node & A = nodes_[ad];
+            if (!f32_of(A.src[0]) || !f32_of(A.src[1]) || !same_shape(A.src[0], A.src[1]) || !f32_of(A.dst) ||
+                !same_shape(A.dst, A.src[0]) || !contiguous(A.src[0]) || !contiguous(A.src[1])) {
+                return 0;
+            }
+            if (a == 0) {
+                terms.push_back(A.src[0]);
+                terms.push_back(A.src[1]);
+            } else if (src(ad, 0) == acc) {
+                terms.push_back(A.src[1]);
+            } else if (src(ad, 1) == acc) {
+                terms.push_back(A.src[0]);
+            } else {
+                return 0;
+            }
+            acc = ad;
+            members.push_back(ad);
+        }
+        if (src(sc, 0) != acc) {
+            return 0;
+        }
+        members.push_back(sc);
+        members.push_back(lk);
+        for (int a = 0; a < nadd; ++a) {
+            if (!internal(members[a], members)) {
+                return 0;
+            }
+        }
+        const shp_node & S = nodes_[sc];
+        const shp_node & L = nodes_[lk];
+        if (!f32_of(L.dst) || !same_shape(L.dst, S.dst) || !contiguous(L.dst) || !contiguous(S.dst)) {
+            return 0;
+        }
+        l.kind  = SHP_RUN_ADD_SCALE_LEAKY;
+        l.terms = terms;
+        l.f0    = fparam(S, 0);
+        l.f1    = fparam(L, 0);
+        l.sum   = needed_outside(sc, members) ? const_cast<shp_tensor *>(&S.dst) : nullptr;
+        l.y     = const_cast<shp_tensor *>(&L.dst);
+        return k;
+    }
+
+    int match_add_leaky(size_t p, Launch & l) const {
+        const int ad = at(p, 0);
+        const int lk = at(p, 1);
+        if (!is(ad, SHP_NODE_ADD) || !is(lk, SHP_NODE_LEAKY_RELU) || src(lk, 0) != ad) {
+            return 0;
+        }
+        const shp_node & A = nodes_[ad];
+        const shp_node & L = nodes_[lk];
+        if (!f32_of(A.src[0]) || !f32_of(A.src[1]) || !same_shape(A.src[0], A.src[1]) || !f32_of(A.dst) ||
+            !same_shape(A.dst, A.src[0]) || !unary_ok(L)) {
+            return 0;
+        }
+        const std::vector<int> members{ ad, lk };
+        l.kind = SHP_RUN_ADD_LEAKY;
+        l.x    = &A.src[0];
+        l.b    = &A.src[1];
+        l.f0   = fparam(L, 0);
+        l.sum  = needed_outside(ad, members) ? const_cast<shp_tensor *>(&A.dst) : nullptr;
+        l.y    = const_cast<shp_tensor *>(&L.dst);
+        return 2;
+    }
+
+    // SILU(g) then MUL(silu, u) (either operand order: the product commutes).
+    int match_silu_mul(size_t p, Launch & l) const {
+        const int si = at(p, 0);
+        const int mu = at(p, 1);
+        if (!is(si, SHP_NODE_SILU) || !is(mu, SHP_NODE_MUL)) {
+            return 0;
+        }
+        const shp_node & M = nodes_[mu];
+        int              other;
+        if (src(mu, 0) == si && src(mu, 1) != si) {
+            other = 1;
+        } else if (src(mu, 1) == si && src(mu, 0) != si) {
+            other = 0;
+        } else {
+            return 0;
+        }
+        const shp_node & S = nodes_[si];
+        if (!unary_ok(S) || !f32_of(M.src[other]) || !same_shape(M.src[other], S.dst) || !f32_of(M.dst) ||
+            !same_shape(M.dst, S.dst) || !internal(si, { si, mu })) {
+            return 0;
+        }
+        l.kind = SHP_RUN_SILU_MUL;
+        l.x    = &S.src[0];
+        l.b    = &M.src[other];
+        l.y    = const_cast<shp_tensor *>(&M.dst);
+        return 2;
+    }
+};
+
+shp_status_t launch_single(const shp_node & n, shp_stream_t st) {
+    shp_tensor * y = const_cast<shp_tensor *>(&n.dst);
+    switch (n.op) {
+        case SHP_NODE_NOP:
+            return SHP_OK;
+        case SHP_NODE_ADD:
+            return shp_add(&n.src[0], &n.src[1], y, st);
+        case SHP_NODE_MUL:
+            return shp_mul(&n.src[0], &n.src[1], y, st);
+        case SHP_NODE_DIV:
+            return shp_div(&n.src[0], &n.src[1], y, st);
+        case SHP_NODE_SQR:
+            return shp_sqr(&n.src[0], y, st);
+        case SHP_NODE_SIN:
+            return shp_sin(&n.src[0], y, st);
+        case SHP_NODE_SCALE:
+            return shp_scale_bias(&n.src[0], fparam(n, 0), fparam(n, 1), y, st);
+        case SHP_NODE_CPY:
+            return shp_cpy(&n.src[0], y, st);
+        case SHP_NODE_GET_ROWS:
+            return shp_get_rows(&n.src[0], &n.src[1], y, st);
+        case SHP_NODE_RMS_NORM:
+            return shp_rms_norm_mul(&n.src[0], nullptr, fparam(n, 0), y, st);
+        case SHP_NODE_SOFT_MAX:
+            return shp_soft_max_ext(&n.src[0], present(n.src[1]) ? &n.src[1] : nullptr, fparam(n, 0), fparam(n, 1), y,
+                                    st);
+        case SHP_NODE_ROPE:
+            return shp_rope_ext(&n.src[0], &n.src[1], n.op_params[1], n.op_params[2], fparam(n, 5), fparam(n, 6),
+                                fparam(n, 7), fparam(n, 8), y, st);
+        case SHP_NODE_LEAKY_RELU:
+            return shp_add_leaky_relu(&n.src[0], nullptr, fparam(n, 0), nullptr, y, st);
+        case SHP_NODE_SILU:
+            return shp_swiglu(&n.src[0], nullptr, y, st);
+        case SHP_NODE_EXP:
+            return shp_exp(&n.src[0], y, st);
+        case SHP_NODE_GLU_SWIGLU:
+            if (present(n.src[1])) {
+                const bool swapped = n.op_params[1] != 0;
+                return shp_swiglu(swapped ? &n.src[1] : &n.src[0], swapped ? &n.src[0] : &n.src[1], y, st);
+            }
+            return shp_glu_swiglu(&n.src[0], n.op_params[1], y, st);
+        default:
+            return SHP_ERR_UNSUPPORTED;
+    }
+}
+
+shp_status_t launch_run(const Planner & pl, const Launch & l, shp_stream_t st) {
+    switch (l.kind) {
+        case SHP_RUN_NOP:
+            return SHP_OK;
+        case SHP_RUN_SINGLE:
+            return launch_single(pl.node(l.first), st);
+        case SHP_RUN_NORM_MUL:
+            return shp_rms_norm_mul(l.x, l.w, l.f0, l.y, st);
+        case SHP_RUN_NORM_MUL_ROPE:
+            return shp_qk_norm_rope(l.x, nullptr, l.w, nullptr, l.f0, l.b, l.i0, l.f1, l.f2, l.y, nullptr, st);
+        case SHP_RUN_ADD_NORM_MUL:
+            return shp_add_rms_norm_mul(l.x, l.b, l.w, l.f0, l.sum, l.y, st);
+        case SHP_RUN_SILU_MUL:
+            return shp_swiglu(l.x, l.b, l.y, st);
+        case SHP_RUN_ADD_LEAKY:
+            return shp_add_leaky_relu(l.x, l.b, l.f0, l.sum, l.y, st);
+        case SHP_RUN_ADD_SCALE_LEAKY:
+            return shp_sum_scale_leaky_relu(l.terms.data(), static_cast<int32_t>(l.terms.size()), l.f0, l.f1, l.sum,
+                                            l.y, st);
+        case SHP_RUN_SNAKE:
+            return shp_snake(l.x, l.w, l.y, st);
+        case SHP_RUN_SNAKE_GUARDED:
+            return shp_snake_guarded(l.x, l.w, l.y, st);
+        case SHP_RUN_SNAKE_BETA:
+            return shp_snake_beta(l.x, l.w, l.c1, l.y, st);
+        case SHP_RUN_GATHER_SUM:
+            return shp_get_rows_sum(l.terms.data(), static_cast<int32_t>(l.terms.size()), &l.codes, l.y, st);
+        default:
+            return SHP_ERR_UNSUPPORTED;
+    }
+}
+
+}  // namespace
+}  // namespace shp
+
+extern "C" int32_t shp_graph_node_supported(const shp_node * node) {
+    if (node == nullptr || node->uses < 0 || node->op < 0 || node->op >= SHP_NODE_OP_COUNT) {
+        return 0;
+    }
+    return shp::single_ok(*node) ? 1 : 0;
+}
+
+extern "C" shp_status_t shp_graph_plan(const shp_node * nodes,
+                                       int32_t          n_nodes,
+                                       shp_graph_run *  runs,
+                                       int32_t          capacity,
+                                       int32_t *        n_runs) {
+    if (n_runs == nullptr || n_nodes < 0 || (n_nodes > 0 && nodes == nullptr) || (runs != nullptr && capacity < 0)) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    shp::Planner       pl(nodes, n_nodes);
+    const shp_status_t st = pl.init();
+    if (st != SHP_OK) {
+        return st;
+    }
+    const auto plan = pl.plan();
+    *n_runs         = static_cast<int32_t>(plan.size());
+    if (runs != nullptr) {
+        if (static_cast<int64_t>(plan.size()) > capacity) {
+            return SHP_ERR_INVALID_ARG;
+        }
+        for (size_t r = 0; r < plan.size(); ++r) {
+            runs[r].kind  = plan[r].kind;
+            runs[r].first = plan[r].first;
+            runs[r].last  = plan[r].last;
+            runs[r].nodes = plan[r].count;
+        }
+    }
+    return SHP_OK;
+}
+
+extern "C" shp_status_t shp_graph_compute(const shp_node * nodes, int32_t n_nodes, shp_stream_t stream) {
+    if (n_nodes < 0 || (n_nodes > 0 && nodes == nullptr)) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    shp::Planner pl(nodes, n_nodes);
+    shp_status_t st = pl.init();
+    if (st != SHP_OK) {
+        return st;
+    }
+    const auto plan = pl.plan();
+    for (const auto & l : plan) {
+        if (l.kind == SHP_RUN_UNSUPPORTED) {
+            return SHP_ERR_UNSUPPORTED;
+        }
+    }
+    for (const auto & l : plan) {
+        if ((st = shp::launch_run(pl, l, stream)) != SHP_OK) {
+            return st;
+        }
+    }
+    return SHP_OK;
+}

@@ -83,6 +83,13 @@ def load(path=None):
         "shp_scale_bias": [_PT, f, f, _PT, vp],
         "shp_sum_scale_leaky_relu": [_PT, i32, f, f, _PT, _PT, vp],
         "shp_layer_nongemm_step": [ctypes.POINTER(ShpLayerStep), vp],
+        "shp_mul": [_PT, _PT, _PT, vp],
+        "shp_div": [_PT, _PT, _PT, vp],
+        "shp_sin": [_PT, _PT, vp],
+        "shp_sqr": [_PT, _PT, vp],
+        "shp_cpy": [_PT, _PT, vp],
+        "shp_graph_compute": [ctypes.POINTER(ShpNode), i32, vp],
+        "shp_graph_plan": [ctypes.POINTER(ShpNode), i32, ctypes.POINTER(ShpGraphRun), i32, ctypes.POINTER(i32)],
     }
     for name, args in sigs.items():
         fn = getattr(L, name)
@@ -107,6 +114,8 @@ def load(path=None):
         fn = getattr(L, name)
         fn.argtypes = args
         fn.restype = res
+    L.shp_graph_node_supported.argtypes = [ctypes.POINTER(ShpNode)]
+    L.shp_graph_node_supported.restype = ctypes.c_int32
     L.shp_abi_version.restype = ctypes.c_uint32
     L.shp_abi_version.argtypes = []
     L.shp_status_string.restype = ctypes.c_char_p
@@ -408,6 +417,250 @@ def layer_nongemm_step(x, w_in, q, k, wq, wk, pos, attn_out, w_post, gate, up, m
     step.eps, step.freq_base, step.n_dims, step.reserved = float(eps), float(freq_base), int(n_dims), 0
     _check(load().shp_layer_nongemm_step(ctypes.byref(step), _stream()), "layer_nongemm_step")
     return outs
+
+
+def mul(a, b, out=None):
+    """ggml_mul(a, b), b the same shape or one broadcast row."""
+    out = a.new_empty(a.shape) if out is None else out
+    _check(load().shp_mul(_ref(desc(a)), _ref(desc(b)), _ref(desc(out)), _stream()), "mul")
+    return out
+
+
+def div(a, b, out=None):
+    """ggml_div(a, b), b the same shape or one broadcast row."""
+    out = a.new_empty(a.shape) if out is None else out
+    _check(load().shp_div(_ref(desc(a)), _ref(desc(b)), _ref(desc(out)), _stream()), "div")
+    return out
+
+
+def sin(x, out=None):
+    """ggml_sin."""
+    out = x.new_empty(x.shape) if out is None else out
+    _check(load().shp_sin(_ref(desc(x)), _ref(desc(out)), _stream()), "sin")
+    return out
+
+
+def sqr(x, out=None):
+    """ggml_sqr."""
+    out = x.new_empty(x.shape) if out is None else out
+    _check(load().shp_sqr(_ref(desc(x)), _ref(desc(out)), _stream()), "sqr")
+    return out
+
+
+def cpy(x, out=None):
+    """ggml_cpy / ggml_cast into F32 of x's shape (x F32, F16 or BF16)."""
+    import torch
+    out = torch.empty(x.shape, dtype=torch.float32, device=x.device) if out is None else out
+    _check(load().shp_cpy(_ref(desc(x)), _ref(desc(out)), _stream()), "cpy")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# node-run executor (include/synth_graph.h)
+# ---------------------------------------------------------------------------
+
+(NODE_NOP, NODE_ADD, NODE_MUL, NODE_DIV, NODE_SQR, NODE_SIN, NODE_SCALE, NODE_CPY, NODE_GET_ROWS, NODE_RMS_NORM,
+ NODE_SOFT_MAX, NODE_ROPE, NODE_LEAKY_RELU, NODE_SILU, NODE_EXP, NODE_GLU_SWIGLU) = range(16)
+NODE_FLAG_OUTPUT = 1
+RUN_KINDS = {-1: "unsupported", 0: "nop", 1: "single", 2: "norm_mul", 3: "norm_mul_rope", 4: "add_norm_mul",
+             5: "silu_mul", 6: "add_leaky", 7: "add_scale_leaky", 8: "snake", 9: "snake_guarded", 10: "snake_beta",
+             11: "gather_sum"}
+
+
+class ShpNode(ctypes.Structure):
+    _fields_ = [("op", ctypes.c_int32), ("flags", ctypes.c_uint32), ("src_node", ctypes.c_int32 * 3),
+                ("uses", ctypes.c_int32), ("op_params", ctypes.c_int32 * 16), ("dst", ShpTensor),
+                ("src", ShpTensor * 3)]
+
+
+class ShpGraphRun(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int32), ("first", ctypes.c_int32), ("last", ctypes.c_int32),
+                ("nodes", ctypes.c_int32)]
+
+
+class GVal:
+    """A tensor of a Graph: `t` (torch tensor or Q8Tensor) and the node that
+    computes it (None for a leaf: weights, inputs, outputs of other graphs)."""
+
+    def __init__(self, t, node=None):
+        self.t, self.node = t, node
+
+
+def _f32_bits(v):
+    import struct
+    return struct.unpack("<i", struct.pack("<f", float(v)))[0]
+
+
+class Graph:
+    """A ggml-style graph over torch tensors, run by shp_graph_compute.
+
+    Each op method mirrors the ggml constructor of the same name: it appends a
+    node, allocates the node's F32 result on the device of its first operand
+    and returns it as a GVal. order() lists the nodes reachable from the given
+    results as ggml_build_forward_expand does (depth first, src[0] first, each
+    node once), which is the order a ggml backend receives them in; compute()
+    runs that list, plan() shows the runs the executor splits it into."""
+
+    def __init__(self):
+        self._outputs = []
+
+    @staticmethod
+    def _v(x):
+        return x if isinstance(x, GVal) or x is None else GVal(x)
+
+    @staticmethod
+    def _t(x):
+        return x.t if isinstance(x, GVal) else x
+
+    def _op(self, op, dst, srcs, ints=None, floats=None):
+        params = [0] * 16
+        for k, v in (ints or {}).items():
+            params[k] = int(v)
+        for k, v in (floats or {}).items():
+            params[k] = _f32_bits(v)
+        node = {"op": op, "srcs": [self._v(s) for s in srcs], "params": params}
+        val = GVal(dst, node)
+        node["val"] = val
+        return val
+
+    def _like(self, x, shape=None):
+        import torch
+        t = self._t(x)
+        raw = t.data if isinstance(t, Q8Tensor) else t
+        return torch.empty(tuple(t.shape) if shape is None else shape, dtype=torch.float32, device=raw.device)
+
+    # binary and unary nodes -------------------------------------------------
+    def add(self, a, b):
+        return self._op(NODE_ADD, self._like(a), [a, b])
+
+    def mul(self, a, b):
+        return self._op(NODE_MUL, self._like(a), [a, b])
+
+    def div(self, a, b):
+        return self._op(NODE_DIV, self._like(a), [a, b])
+
+    def sqr(self, x):
+        return self._op(NODE_SQR, self._like(x), [x])
+
+    def sin(self, x):
+        return self._op(NODE_SIN, self._like(x), [x])
+
+    def silu(self, x):
+        return self._op(NODE_SILU, self._like(x), [x])
+
+    def exp(self, x):
+        return self._op(NODE_EXP, self._like(x), [x])
+
+    def scale(self, x, s):
+        return self._op(NODE_SCALE, self._like(x), [x], floats={0: s, 1: 0.0})
+
+    def scale_bias(self, x, s, b):
+        return self._op(NODE_SCALE, self._like(x), [x], floats={0: s, 1: b})
+
+    def leaky_relu(self, x, slope):
+        return self._op(NODE_LEAKY_RELU, self._like(x), [x], floats={0: slope})
+
+    def rms_norm(self, x, eps):
+        return self._op(NODE_RMS_NORM, self._like(x), [x], floats={0: eps})
+
+    def rope_ext(self, x, pos, n_dims, mode, freq_base, freq_scale=1.0, ext_factor=0.0, attn_factor=1.0):
+        return self._op(NODE_ROPE, self._like(x), [x, pos], ints={1: n_dims, 2: mode},
+                        floats={5: freq_base, 6: freq_scale, 7: ext_factor, 8: attn_factor})
+
+    def soft_max_ext(self, x, mask, scale, max_bias=0.0):
+        return self._op(NODE_SOFT_MAX, self._like(x), [x, mask], floats={0: scale, 1: max_bias})
+
+    def get_rows(self, table, ids):
+        t = self._t(table)
+        ne0 = t.ne0 if isinstance(t, Q8Tensor) else t.shape[-1]
+        return self._op(NODE_GET_ROWS, self._like(ids, tuple(self._t(ids).shape) + (ne0,)), [table, ids])
+
+    def cast(self, x):
+        """ggml_cast(x, F32)."""
+        return self._op(NODE_CPY, self._like(x), [x])
+
+    def cpy(self, x, dst):
+        """ggml_cpy(x, dst): dst a torch tensor (a view of a cache, say)."""
+        return self._op(NODE_CPY, dst, [x])
+
+    def glu_swiglu(self, a, b=None, swapped=False):
+        t = self._t(a)
+        shape = tuple(t.shape) if b is not None else tuple(t.shape[:-1]) + (t.shape[-1] // 2,)
+        return self._op(NODE_GLU_SWIGLU, self._like(a, shape), [a, b], ints={1: 1 if swapped else 0})
+
+    @staticmethod
+    def read_later(v, uses):
+        """Declares that v is read `uses` times in the whole graph (ggml's use
+        count), some of them by nodes outside this list (a later split)."""
+        v.node["uses"] = int(uses)
+        return v
+
+    def view(self, x, t):
+        """A view-like node (ggml_view/reshape/permute): `t` is the torch view of x's memory."""
+        return self._op(NODE_NOP, t, [x])
+
+    # ordering and running ---------------------------------------------------
+    def order(self, *outputs):
+        """The nodes reachable from `outputs`, in ggml_build_forward_expand order."""
+        seen, out = set(), []
+        for o in outputs:
+            stack = [(o, False)]
+            while stack:
+                v, done = stack.pop()
+                n = v.node if isinstance(v, GVal) else None
+                if n is None:
+                    continue
+                if done:
+                    out.append(n)
+                    continue
+                if id(n) in seen:
+                    continue
+                seen.add(id(n))
+                stack.append((v, True))
+                for s in reversed(n["srcs"]):
+                    if s is not None:
+                        stack.append((s, False))
+        return out
+
+    def nodes(self, *outputs, flag_outputs=True):
+        """The shp_node array for order(*outputs); the results in `outputs`
+        carry SHP_NODE_FLAG_OUTPUT. Returns (array, keep-alive list)."""
+        order = self.order(*outputs)
+        index = {id(n): i for i, n in enumerate(order)}
+        outs = {id(o.node) for o in outputs if isinstance(o, GVal) and o.node is not None}
+        arr = (ShpNode * max(1, len(order)))()
+        keep = []
+        for i, n in enumerate(order):
+            c = arr[i]
+            c.op = n["op"]
+            c.flags = NODE_FLAG_OUTPUT if flag_outputs and id(n) in outs else 0
+            c.uses = n.get("uses", 0)
+            for k in range(16):
+                c.op_params[k] = n["params"][k]
+            c.dst = desc(n["val"].t)
+            for k in range(3):
+                c.src_node[k] = -1
+                s = n["srcs"][k] if k < len(n["srcs"]) else None
+                if s is not None:
+                    c.src[k] = desc(s.t)
+                    if s.node is not None:
+                        c.src_node[k] = index[id(s.node)]
+            keep.append(n)
+        return arr, len(order), keep
+
+    def plan(self, *outputs):
+        """[(run kind, first node, last node, nodes executed)] for order(*outputs)."""
+        arr, n, _ = self.nodes(*outputs)
+        count = ctypes.c_int32()
+        _check(load().shp_graph_plan(arr, n, None, 0, ctypes.byref(count)), "graph_plan")
+        runs = (ShpGraphRun * max(1, count.value))()
+        _check(load().shp_graph_plan(arr, n, runs, count.value, ctypes.byref(count)), "graph_plan")
+        return [(RUN_KINDS[r.kind], r.first, r.last, r.nodes) for r in runs[:count.value]]
+
+    def compute(self, *outputs):
+        arr, n, _ = self.nodes(*outputs)
+        _check(load().shp_graph_compute(arr, n, _stream()), "graph_compute")
+        return outputs[0] if len(outputs) == 1 else outputs
 
 
 # ---------------------------------------------------------------------------

@@ -10,7 +10,7 @@ import pytest
 import synth_hip as S
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("synth_hip.h", "synth_gguf.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("synth_hip.h", "synth_gguf.h", "synth_graph.h")]
 
 
 def declared_symbols():

@@ -1,0 +1,270 @@
+"""The node-run executor on the GPU: node lists in the order the reference's
+graphs reach a backend (ggml_build_forward_expand order), run by
+shp_graph_compute, against the restatement and against the same lists run node
+by node (an intermediate marked as a graph output keeps a run from fusing).
+
+Bars as in test_gpu_parity: bit-exact for adds, products, quotients, squares,
+casts, gathers and sums; 1e-5 for norms, SwiGLU and Snake; rope bit-exact
+against the restatement with correctly rounded cos/sin. Fused and node-by-node
+runs of one list are bit-identical.
+"""
+import numpy as np
+import pytest
+
+import formats as F
+import ggml_ref as R
+from test_gpu_parity import (SEED, _np, _positions, _t, assert_bitexact, assert_close, assert_rope_close,
+                              assert_snake_close)
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16(gpu, bits):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).cuda().view(torch.bfloat16)
+
+
+def test_single_node_entry_points(gpu):
+    """shp_mul / shp_div (same shape and a broadcast row), shp_sin, shp_sqr and
+    shp_cpy (F32 copy into a strided view, BF16 and F16 casts) against the
+    restatement's nodes."""
+    import torch
+    rng = np.random.default_rng(SEED + 201)
+    a = rng.standard_normal((37, 1024)).astype(np.float32)
+    b = rng.standard_normal((37, 1024)).astype(np.float32)
+    row = rng.standard_normal(1024).astype(np.float32)
+    row[:4] = [0.0, -0.0, 1e-40, np.inf]
+    for op in ("mul", "div"):
+        for bb in (b, row):
+            with np.errstate(all="ignore"):
+                ref = R.run(lambda g: getattr(g, op)(a, bb))
+            got = _np(getattr(gpu, op)(_t(gpu, a), _t(gpu, bb)))
+            assert np.array_equal(np.isnan(got), np.isnan(ref))
+            assert_bitexact(np.where(np.isnan(ref), 0, got), np.where(np.isnan(ref), 0, ref))
+    x = (rng.standard_normal((64, 512)) * 20).astype(np.float32)
+    x[0, :8] = [0.0, -0.0, 1e5, -3e4, 40000.0, 1e-30, -1e-30, -1e-45]
+    assert_bitexact(_np(gpu.sqr(_t(gpu, x))), R.run(lambda g: g.sqr(x)))
+    ref = R.run(lambda g: g.sin(x))
+    got = _np(gpu.sin(_t(gpu, x)))
+    ulps = np.abs(got.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+    # libm's sinf and the kernel's sine (the Snake kernels' own) are each within
+    # 1 ulp of the exact sine; they agree on the sign of zeros
+    assert ulps.max() <= 1
+    assert (ulps == 0).mean() > 0.8
+    cache = torch.zeros(16, 8, 64, device="cuda")
+    k = rng.standard_normal((5, 8, 64)).astype(np.float32)
+    gpu.cpy(_t(gpu, k), out=cache[3:8])
+    assert_bitexact(_np(cache[3:8]), k)
+    assert (_np(cache[:3]) == 0).all() and (_np(cache[8:]) == 0).all()
+    w = rng.normal(1, 0.1, 3000).astype(np.float32)
+    bits = F.f32_to_bf16_bits(w)
+    assert_bitexact(_np(gpu.cpy(_bf16(gpu, bits))), R.run(lambda g: g.cast_f32(bits, R.BF16)))
+    h = F.f32_to_f16_bits(w)
+    got = _np(gpu.cpy(torch.from_numpy(h.view(np.int16)).cuda().view(torch.float16)))
+    assert_bitexact(got, R.run(lambda g: g.cast_f32(h, R.F16)))
+
+
+def _layer_inputs(rng, T, H=1024, heads=16, kv=8, hd=128, cap=64):
+    d = dict(x=rng.standard_normal((T, H)), attn=rng.standard_normal((T, H)), mlp=rng.standard_normal((T, H)),
+             q=rng.standard_normal((T, heads, hd)), k=rng.standard_normal((T, kv, hd)))
+    d = {n: a.astype(np.float32) for n, a in d.items()}
+    for n, size in (("w_in", H), ("w_post", H), ("wq", hd), ("wk", hd)):
+        d[n] = F.f32_to_bf16_bits(rng.normal(1.0, 0.1, size).astype(np.float32))
+    d["pos"] = _positions(rng, T, 8192)
+    return d
+
+
+@pytest.mark.parametrize("T", [1, 37])
+def test_qwen3_layer_graph(gpu, T):
+    """The non-GEMM nodes of a Qwen3 layer (operations.cpp:80-147) in expand
+    order, with BF16 gains through ggml_cast: 4 fused runs and one add, every
+    output as the restatement computes it; the same list with every
+    intermediate marked as an output runs node by node, bit-identical."""
+    import torch
+    rng = np.random.default_rng(SEED + 300 + T)
+    d = _layer_inputs(rng, T)
+    eps, theta, hd, filled = np.float32(1e-6), np.float32(1e6), 128, 5
+    dev = {n: (_bf16(gpu, a) if n.startswith("w") else _t(gpu, a)) for n, a in d.items()}
+
+    def build(keep_all):
+        g = gpu.Graph()
+        cache = torch.zeros(64, 8, hd, device="cuda")
+        mids = []
+
+        def m(v):
+            mids.append(v)
+            return v
+        normed = g.mul(m(g.rms_norm(dev["x"], eps)), m(g.cast(dev["w_in"])))
+        qr = g.rope_ext(m(g.mul(m(g.rms_norm(dev["q"], eps)), m(g.cast(dev["wq"])))), dev["pos"], hd,
+                        gpu.ROPE_TYPE_NEOX, theta)
+        kr = m(g.rope_ext(m(g.mul(m(g.rms_norm(dev["k"], eps)), m(g.cast(dev["wk"])))), dev["pos"], hd,
+                          gpu.ROPE_TYPE_NEOX, theta))
+        kc = g.cpy(kr, cache[filled:filled + T])
+        after = g.add(dev["x"], dev["attn"])
+        mlp_in = g.mul(m(g.rms_norm(after, eps)), m(g.cast(dev["w_post"])))
+        out = g.add(after, dev["mlp"])
+        outs = [kc, normed, qr, mlp_in, out, after]
+        return g, outs + (mids if keep_all else []), cache
+
+    g, outs, cache = build(False)
+    kinds = [k for k, *_ in g.plan(*outs) if k != "nop"]
+    assert kinds == ["norm_mul_rope", "norm_mul", "norm_mul_rope", "add_norm_mul", "single"]
+    g.compute(*outs)
+    _, normed, qr, mlp_in, out, after = [_np(v.t) for v in outs]
+    kc = _np(cache)
+    g2, outs2, cache2 = build(True)
+    assert all(k in ("single", "nop") for k, *_ in g2.plan(*outs2))
+    g2.compute(*outs2)
+    for a, b in zip(outs[1:6], outs2[1:6]):
+        assert_bitexact(_np(a.t), _np(b.t))
+    assert_bitexact(_np(cache2), kc)
+
+    x, q, k = d["x"], d["q"], d["k"]
+    assert_close(normed, R.run(lambda gr: R.rms_norm_w(gr, x, d["w_in"], eps, R.BF16)))
+    qc, kc_ref = R.run(lambda gr: R.qk_norm_rope(gr, q, k, d["wq"], d["wk"], eps, d["pos"], hd, theta, R.BF16,
+                                                 cs_rounded=True))
+    assert_bitexact(qr, qc)
+    assert_bitexact(kc[filled:filled + T], kc_ref)
+    assert (kc[:filled] == 0).all() and (kc[filled + T:] == 0).all()
+    s_ref, y_ref = R.run(lambda gr: R.add_rms_norm_w(gr, x, d["attn"], d["w_post"], eps, R.BF16))
+    assert_bitexact(after, s_ref)
+    assert_close(mlp_in, y_ref)
+    assert_bitexact(out, R.run(lambda gr: gr.add(s_ref, d["mlp"])))
+
+
+@pytest.mark.parametrize("kind", ["plain", "guarded", "beta"])
+def test_snake_family_graph(gpu, kind):
+    """Kokoro Snake, the guarded Snake and SnakeBeta as their node lists: one
+    fused run each, equal to the node-by-node run (sine marked as an output)
+    bit for bit and to the restatement within the Snake bar (1e-5 of the
+    closing add's operands)."""
+    from test_graph_plan import snake_graph
+    rng = np.random.default_rng(SEED + 400)
+    T, C = 300, 256
+    x = rng.standard_normal((T, C)).astype(np.float32)
+    if kind == "beta":
+        la = rng.uniform(-1, 1, C).astype(np.float32)
+        lb = rng.uniform(-1, 1, C).astype(np.float32)
+        alpha = (_t(gpu, la), _t(gpu, lb))
+        ref = R.run(lambda g: R.snake_beta(g, x, la, lb))
+    else:
+        al = np.exp(rng.uniform(np.log(0.1), np.log(10.0), C)).astype(np.float32)
+        alpha = _t(gpu, al.reshape(1, C, 1))
+        ref = R.run(lambda g: (R.snake if kind == "plain" else R.snake_guarded)(g, x, al))
+    g = gpu.Graph()
+    y = snake_graph(g, _t(gpu, x), alpha, kind)
+    assert [k for k, *_ in g.plan(y) if k != "nop"] == [{"plain": "snake", "guarded": "snake_guarded",
+                                                          "beta": "snake_beta"}[kind]]
+    fused = _np(g.compute(y).t)
+    # the same list with the sine read outside: every node alone
+    g2 = gpu.Graph()
+    y2 = snake_graph(g2, _t(gpu, x), alpha, kind)
+    sine = [v for v in _walk(y2) if v.node["op"] == gpu.NODE_SIN][0]
+    assert all(k in ("single", "nop") for k, *_ in g2.plan(y2, sine))
+    g2.compute(y2, sine)
+    assert_bitexact(fused, _np(y2.t))
+    assert_snake_close(fused, ref, x)
+
+
+def _walk(v):
+    out, stack, seen = [], [v], set()
+    while stack:
+        u = stack.pop()
+        if u is None or u.node is None or id(u.node) in seen:
+            continue
+        seen.add(id(u.node))
+        out.append(u)
+        stack.extend(u.node["srcs"])
+    return out
+
+
+def test_gather_sum_graph(gpu):
+    """sum_code_embeddings (code-predictor.cpp:82-107) as 16 get_rows over the
+    column views of one codes tensor and 15 adds: one fused run, bit-exact; the
+    list cut by an intermediate output runs as a 2-group run plus nodes, with
+    the same bits."""
+    import torch
+    rng = np.random.default_rng(SEED + 500)
+    groups, rows, ne0, frames = 16, 2048, 1024, 333
+    tabs = [F.q8_0_synthetic(rng, rows, ne0) for _ in range(groups)]
+    codes = rng.integers(0, rows, (groups, frames)).astype(np.int32)
+    ref = R.run(lambda g: R.sum_code_embeddings(g, tabs, R.Q8_0, ne0, codes))
+    dt = [gpu.Q8Tensor(_t(gpu, t), ne0) for t in tabs]
+    dc = _t(gpu, codes)
+
+    def build(cut):
+        g = gpu.Graph()
+        total, mid = None, None
+        for t in range(groups):
+            r = g.get_rows(dt[t], g.view(dc, dc[t]))
+            total = r if total is None else g.add(total, r)
+            if t == 1:
+                mid = total
+        return g, ([total, mid] if cut else [total])
+    g, outs = build(False)
+    assert [k for k, *_ in g.plan(*outs) if k != "nop"] == ["gather_sum"]
+    g.compute(*outs)
+    assert_bitexact(_np(outs[0].t), ref)
+    g, outs = build(True)
+    assert [k for k, *_ in g.plan(*outs) if k != "nop"] == ["gather_sum"] + ["single"] * 28
+    g.compute(*outs)
+    assert_bitexact(_np(outs[0].t), ref)
+    torch.cuda.synchronize()
+
+
+def test_vits_runs_graph(gpu):
+    """The residual carry (waveform-decoder.cpp:150-158, the sum read by the
+    next layer's add) and the branch average (:214-225): bit-exact."""
+    rng = np.random.default_rng(SEED + 600)
+    sh = (4096, 192)
+    a, b, c, b0, b1, b2 = [rng.standard_normal(sh).astype(np.float32) for _ in range(6)]
+    s_ref, y_ref = R.run(lambda g: R.add_leaky(g, a, b, 0.1))
+    nxt_ref = R.run(lambda g: g.add(c, s_ref))
+    cur_ref, avg_ref = R.run(lambda g: R.sum_scale_leaky(g, [b0, b1, b2], np.float32(1.0 / 3), 0.1))
+    g = gpu.Graph()
+    s = g.add(_t(gpu, a), _t(gpu, b))
+    y = g.leaky_relu(s, 0.1)
+    nxt = g.add(_t(gpu, c), s)
+    summed = g.add(g.add(_t(gpu, b0), _t(gpu, b1)), _t(gpu, b2))
+    avg = g.leaky_relu(g.scale(summed, np.float32(1.0 / 3)), 0.1)
+    assert [k for k, *_ in g.plan(y, nxt, avg) if k != "nop"] == ["add_leaky", "single", "add_scale_leaky"]
+    g.compute(y, nxt, avg)
+    assert_bitexact(_np(y.t), y_ref)
+    assert_bitexact(_np(s.t), s_ref)
+    assert_bitexact(_np(nxt.t), nxt_ref)
+    assert_bitexact(_np(avg.t), avg_ref)
+
+
+def test_single_nodes_graph(gpu):
+    """Nodes that run alone: rope, soft_max_ext with a causal mask, the
+    single-tensor GLU, exp, and an unfused silu then mul (an up-projection
+    between them in the reference's order)."""
+    rng = np.random.default_rng(SEED + 700)
+    x = rng.standard_normal((9, 4, 64)).astype(np.float32)
+    pos = _positions(rng, 9, 1000)
+    sc = rng.standard_normal((2, 9, 12)).astype(np.float32)
+    mask = np.zeros((9, 12), np.float32)
+    mask[np.triu_indices(9, 4, 12)] = -np.inf
+    glu = rng.standard_normal((5, 96)).astype(np.float32)
+    e = rng.uniform(-80, 80, (7, 33)).astype(np.float32)
+    gate, up = rng.standard_normal((2, 7, 300)).astype(np.float32)
+    g = gpu.Graph()
+    r = g.rope_ext(_t(gpu, x), _t(gpu, pos), 64, gpu.ROPE_TYPE_NEOX, 1e4)
+    p = g.soft_max_ext(_t(gpu, sc), _t(gpu, mask), 0.125)
+    gl = g.glu_swiglu(_t(gpu, glu))
+    ex = g.exp(_t(gpu, e))
+    si = g.silu(_t(gpu, gate))
+    between = g.add(_t(gpu, up), _t(gpu, up))  # stands for the up-projection
+    mu = g.mul(si, between)
+    outs = [r, p, gl, ex, mu]
+    assert [k for k, *_ in g.plan(*outs) if k != "nop"] == ["single"] * 7
+    g.compute(*outs)
+    assert_bitexact(_np(r.t), R.run(lambda gr: gr.rope_neox(x, pos, 64, np.float32(1e4), cs_rounded=True)))
+    assert_rope_close(_np(r.t), R.run(lambda gr: gr.rope_neox(x, pos, 64, np.float32(1e4))), 64)
+    ref = R.run(lambda gr: gr.soft_max_ext(sc, mask, np.float32(0.125)))
+    got = _np(p.t)
+    assert np.abs(got.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64)).max() <= 2
+    assert_close(_np(gl.t), R.run(lambda gr: gr.glu_swiglu(glu)))
+    ref = R.run(lambda gr: gr.exp(e))
+    assert np.abs(_np(ex.t).view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64)).max() <= 1
+    assert_close(_np(mu.t), R.run(lambda gr: gr.mul(gr.silu(gate), gr.add(up, up))))

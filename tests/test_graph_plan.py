@@ -1,0 +1,245 @@
+"""The node-run executor's planner on the CPU (include/synth_graph.h): which
+runs it finds in node lists ordered as ggml_build_forward_expand orders the
+reference's graphs, and when it must not fuse. Host code only: the tensors are
+CPU tensors whose pointers are never dereferenced, and nothing is launched."""
+import ctypes
+
+import pytest
+import torch
+
+import synth_hip as S
+
+F32 = torch.float32
+
+
+def z(*shape, dtype=F32):
+    return torch.zeros(shape, dtype=dtype)
+
+
+def kinds(plan):
+    return [k for k, _, _, _ in plan if k != "nop"]
+
+
+def qwen3_layer(g, T=5, H=64, heads=4, kv=2, hd=16, ffn=96, cast=True, cache_rows=32):
+    """The non-GEMM nodes of decoder_layer (src/arch/qwen3-tts/operations.cpp:
+    80-147) with the GEMM outputs as leaves: returns the results a backend
+    hands back to the GEMMs and the cache write."""
+    wt = torch.bfloat16 if cast else F32
+    x, attn, mlp = z(T, H), z(T, H), z(T, H)
+    q, k = z(T, heads, hd), z(T, kv, hd)
+    w_in, w_post, wq, wk = z(H, dtype=wt), z(H, dtype=wt), z(hd, dtype=wt), z(hd, dtype=wt)
+    pos = z(T, dtype=torch.int32)
+    cache = z(cache_rows, kv, hd)
+    f = (lambda w: g.cast(w)) if cast else (lambda w: w)
+    normed = g.mul(g.rms_norm(x, 1e-6), f(w_in))
+    qr = g.rope_ext(g.mul(g.rms_norm(q, 1e-6), f(wq)), pos, hd, S.ROPE_TYPE_NEOX, 1e6)
+    kr = g.rope_ext(g.mul(g.rms_norm(k, 1e-6), f(wk)), pos, hd, S.ROPE_TYPE_NEOX, 1e6)
+    kc = g.cpy(kr, cache[3:3 + T])
+    after = g.add(x, attn)
+    mlp_in = g.mul(g.rms_norm(after, 1e-6), f(w_post))
+    out = g.add(after, mlp)
+    return kc, normed, qr, mlp_in, out
+
+
+def test_qwen3_layer_runs():
+    g = S.Graph()
+    kc, normed, qr, mlp_in, out = qwen3_layer(g)
+    plan = g.plan(kc, normed, qr, mlp_in, out)
+    # expand order: the k path first (the cache write), then the input norm, q, the add+norm, the output add
+    assert kinds(plan) == ["norm_mul_rope", "norm_mul", "norm_mul_rope", "add_norm_mul", "single"]
+    nodes = [n for k, _, _, n in plan if k != "nop"]
+    assert nodes == [5, 3, 4, 4, 1]
+    g = S.Graph()
+    res = qwen3_layer(g, cast=False)
+    assert kinds(g.plan(*res)) == ["norm_mul_rope", "norm_mul", "norm_mul_rope", "add_norm_mul", "single"]
+    assert [n for k, _, _, n in g.plan(*res) if k != "nop"] == [4, 2, 3, 3, 1]
+
+
+def test_a_read_in_a_later_split_keeps_a_result_written():
+    """after_attention (operations.cpp:143) is read by the post-attention norm
+    in this split and by the layer's output add after the MLP's GEMMs, in a
+    later split: its ggml use count (2) exceeds the reads in the list (1), so
+    the add+norm run writes the sum; the same holds for a skipped gain cast or
+    norm, which then run as nodes."""
+    g = S.Graph()
+    x, attn, w = z(4, 64), z(4, 64), z(64)
+    after = g.add(x, attn)
+    mlp_in = g.mul(g.rms_norm(after, 1e-6), w)
+    arr, n, _ = g.nodes(mlp_in)
+    runs = (S.ShpGraphRun * 4)()
+    count = ctypes.c_int32()
+    L = S.load()
+    assert L.shp_graph_plan(arr, n, runs, 4, ctypes.byref(count)) == S.OK
+    assert [runs[i].kind for i in range(count.value)] == [4]  # add_norm_mul
+    g = S.Graph()
+    after = g.read_later(g.add(x, attn), 2)
+    nrm = g.rms_norm(after, 1e-6)
+    mlp_in = g.mul(nrm, w)
+    assert kinds(g.plan(mlp_in)) == ["add_norm_mul"]
+    g = S.Graph()
+    nrm = g.read_later(g.rms_norm(x, 1e-6), 2)
+    assert kinds(g.plan(g.mul(nrm, w))) == ["single", "single"]
+
+
+def test_layer_output_add_fuses_into_the_next_input_norm():
+    """:147 -> :86: the layer output add followed by the next layer's input
+    norm is one add+norm run that writes the sum (the next residual)."""
+    g = S.Graph()
+    after, mlp, w = z(4, 64), z(4, 64), z(64, dtype=torch.bfloat16)
+    out = g.add(after, mlp)
+    nxt = g.mul(g.rms_norm(out, 1e-6), g.cast(w))
+    resid = g.add(out, z(4, 64))
+    assert kinds(g.plan(nxt, resid)) == ["add_norm_mul", "single"]
+
+
+def test_swiglu_fuses_only_when_adjacent():
+    g = S.Graph()
+    gate, up = z(3, 96), z(3, 96)
+    assert kinds(g.plan(g.mul(g.silu(gate), up))) == ["silu_mul"]
+    g = S.Graph()
+    assert kinds(g.plan(g.mul(up, g.silu(gate)))) == ["silu_mul"]
+    g = S.Graph()
+    s = g.silu(gate)
+    other = g.add(s, up)  # the silu is read twice
+    assert kinds(g.plan(g.mul(s, up), other)) == ["single", "single", "single"]
+
+
+def snake_graph(g, x, alpha, kind):
+    per = g.view(alpha, alpha.reshape(-1)) if kind != "beta" else None
+    if kind == "plain":
+        sq = g.sin(g.mul(x, per))
+        return g.add(x, g.div(g.mul(sq, sq), per))
+    if kind == "guarded":
+        sq = g.sin(g.mul(x, per))
+        return g.add(x, g.div(g.mul(sq, sq), g.scale_bias(per, 1.0, 1e-9)))
+    la, lb = alpha
+    a = g.exp(g.view(la, la.reshape(-1, 1)))
+    b = g.exp(g.view(lb, lb.reshape(-1, 1)))
+    sq = g.sqr(g.sin(g.mul(x, a)))
+    return g.add(x, g.div(sq, g.scale_bias(b, 1.0, 1e-9)))
+
+
+@pytest.mark.parametrize("kind,run,n", [("plain", "snake", 5), ("guarded", "snake_guarded", 6),
+                                        ("beta", "snake_beta", 8)])
+def test_snake_family_runs(kind, run, n):
+    """kokoro/operations.cpp:137-147, omnivoice/codec.cpp:51-68 and
+    qwen3-tts/codec.cpp:184-200 in expand order (the curves' reshapes are view
+    nodes inside the span)."""
+    g = S.Graph()
+    x = z(7, 32)
+    alpha = (z(32), z(32)) if kind == "beta" else z(1, 32, 1)
+    plan = g.plan(snake_graph(g, x, alpha, kind))
+    assert kinds(plan) == [run]
+    assert [p[3] for p in plan if p[0] == run] == [n]
+
+
+def test_snake_not_fused_when_an_intermediate_is_read_elsewhere():
+    g = S.Graph()
+    x, alpha = z(7, 32), z(32)
+    t = g.mul(x, alpha)
+    sn = g.sin(t)
+    y = g.add(x, g.div(g.mul(sn, sn), alpha))
+    assert kinds(g.plan(y, sn)) == ["single"] * 5  # the sine is a graph output
+    g = S.Graph()
+    t = g.mul(x, alpha)
+    sn = g.sin(t)
+    y = g.add(x, g.div(g.mul(sn, sn), z(32)))  # another tensor as the divisor
+    assert kinds(g.plan(y)) == ["single"] * 5
+    g = S.Graph()
+    sn = g.sin(g.mul(x, alpha))
+    y = g.add(x, g.div(g.mul(sn, sn), g.scale_bias(alpha, 1.0, 1e-8)))  # not Snake1d's guard
+    assert kinds(g.plan(y)) == ["single"] * 6
+
+
+def test_gather_sum_runs():
+    """code-predictor.cpp:82-107: one view per group column of codes, a get_rows
+    per group, added in group order."""
+    groups, frames = 16, 9
+    tables = [S.Q8Tensor(z(64, 2 * 34, dtype=torch.uint8), 64) for _ in range(groups)]
+    codes = z(groups, frames, dtype=torch.int32)
+    g = S.Graph()
+    total = None
+    for t in range(groups):
+        rows = g.get_rows(tables[t], g.view(codes, codes[t]))
+        total = rows if total is None else g.add(total, rows)
+    plan = g.plan(total)
+    assert kinds(plan) == ["gather_sum"]
+    assert [p[3] for p in plan if p[0] == "gather_sum"] == [2 * groups - 1]
+    # ids from two separate tensors are not columns of one codes tensor
+    other = z(groups, frames, dtype=torch.int32)
+    g = S.Graph()
+    r0 = g.get_rows(tables[0], codes[0])
+    r1 = g.get_rows(tables[1], other[1])
+    assert kinds(g.plan(g.add(r0, r1))) == ["single"] * 3
+    # an intermediate sum read elsewhere stops the run after it
+    g = S.Graph()
+    acc = g.get_rows(tables[0], codes[0])
+    acc = g.add(acc, g.get_rows(tables[1], codes[1]))
+    mid = acc
+    acc = g.add(acc, g.get_rows(tables[2], codes[2]))
+    assert kinds(g.plan(acc, mid)) == ["gather_sum", "single", "single"]
+
+
+def test_vits_residual_and_branch_average_runs():
+    """waveform-decoder.cpp:150-158 (the add's sum is the next residual) and
+    :214-225 (the last branch add, the scale by 1/n, the stage's leaky)."""
+    g = S.Graph()
+    a, b = z(16, 8), z(16, 8)
+    s = g.add(a, b)
+    y = g.leaky_relu(s, 0.1)
+    nxt = g.add(z(16, 8), s)
+    assert kinds(g.plan(y, nxt)) == ["add_leaky", "single"]
+    g = S.Graph()
+    b0, b1, b2 = z(16, 8), z(16, 8), z(16, 8)
+    summed = g.add(g.add(b0, b1), b2)
+    y = g.leaky_relu(g.scale(summed, 1.0 / 3), 0.1)
+    plan = g.plan(y)
+    assert kinds(plan) == ["add_scale_leaky"]
+    assert [p[3] for p in plan if p[0] != "nop"] == [4]
+
+
+def test_singles_and_support():
+    g = S.Graph()
+    x = z(4, 2, 8)
+    pos = z(4, dtype=torch.int32)
+    outs = [g.rope_ext(x, pos, 8, S.ROPE_TYPE_NEOX, 1e4), g.soft_max_ext(z(3, 5), None, 0.5),
+            g.glu_swiglu(z(3, 8)), g.exp(z(3, 4)), g.cast(z(8, dtype=torch.float16))]
+    assert kinds(g.plan(*outs)) == ["single"] * 5
+    g = S.Graph()
+    normal = g.rope_ext(x, pos, 8, 0, 1e4)  # GPT-J pairing: not here
+    assert kinds(g.plan(normal)) == ["unsupported"]
+    arr, n, _ = g.nodes(normal)
+    assert S.load().shp_graph_node_supported(ctypes.byref(arr[0])) == 0
+    assert S.load().shp_graph_compute(arr, n, None) == S.ERR_UNSUPPORTED  # nothing launched
+    g = S.Graph()
+    alibi = g.soft_max_ext(z(3, 5), None, 0.5, max_bias=8.0)
+    assert kinds(g.plan(alibi)) == ["unsupported"]
+
+
+def test_malformed_lists_are_rejected():
+    g = S.Graph()
+    y = g.add(g.add(z(4, 8), z(4, 8)), z(4, 8))
+    arr, n, _ = g.nodes(y)
+    count = ctypes.c_int32()
+    L = S.load()
+    assert L.shp_graph_plan(arr, n, None, 0, ctypes.byref(count)) == S.OK and count.value == 2
+    arr[1].src_node[0] = 1  # not an earlier node
+    assert L.shp_graph_plan(arr, n, None, 0, ctypes.byref(count)) == S.ERR_INVALID_ARG
+    arr[1].src_node[0] = 0
+    arr[0].uses = -1
+    assert L.shp_graph_compute(arr, n, None) == S.ERR_INVALID_ARG
+    arr[0].uses = 1  # read once by the list: consistent
+    assert L.shp_graph_plan(arr, n, None, 0, ctypes.byref(count)) == S.OK
+    arr[0].uses = 0
+    g2 = S.Graph()
+    s = g2.add(z(4, 8), z(4, 8))
+    y2 = g2.mul(s, s)
+    arr2, n2, _ = g2.nodes(y2)
+    arr2[0].uses = 1  # below the two reads the list makes
+    assert L.shp_graph_plan(arr2, n2, None, 0, ctypes.byref(count)) == S.ERR_INVALID_ARG
+    arr[1].op = 99
+    assert L.shp_graph_plan(arr, n, None, 0, ctypes.byref(count)) == S.ERR_INVALID_ARG
+    arr[1].op = S.NODE_ADD
+    runs = (S.ShpGraphRun * 1)()
+    assert L.shp_graph_plan(arr, n, runs, 1, ctypes.byref(count)) == S.ERR_INVALID_ARG  # capacity
+    assert L.shp_graph_plan(arr, 0, None, 0, ctypes.byref(count)) == S.OK and count.value == 0
