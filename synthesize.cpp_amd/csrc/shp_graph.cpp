@@ -11,6 +11,7 @@
 // by one, bit for bit.
 #include <cstdint>
 #include <cstring>
+#include <initializer_list>
 #include <vector>
 
 #include "shp_internal.hpp"
@@ -128,6 +129,28 @@ bool single_ok(const shp_node & n) {
     }
 }
 
+// The nodes of a candidate run (at most 2*64 - 1: the longest gather->sum).
+struct Members {
+    int v[128];
+    int n = 0;
+    Members() = default;
+    Members(std::initializer_list<int> xs) {
+        for (int x : xs) {
+            v[n++] = x;
+        }
+    }
+    void push(int x) { v[n++] = x; }
+    int  back() const { return v[n - 1]; }
+    bool has(int x) const {
+        for (int i = 0; i < n; ++i) {
+            if (v[i] == x) {
+                return true;
+            }
+        }
+        return false;
+    }
+};
+
 // What a run launches: which entry point, and its operands.
 struct Launch {
     int                     kind  = SHP_RUN_SINGLE;
@@ -152,8 +175,10 @@ class Planner {
   public:
     Planner(const shp_node * nodes, int n) : nodes_(nodes), n_(n) {}
 
+    // Checks the list and indexes each node's readers (one entry per src
+    // reference, in a flat array: cons_[cstart_[j] .. cstart_[j + 1])).
     shp_status_t init() {
-        consumers_.assign(n_, {});
+        cstart_.assign(n_ + 1, 0);
         for (int i = 0; i < n_; ++i) {
             const shp_node & nd = nodes_[i];
             if (nd.uses < 0 || nd.op < 0 || nd.op >= SHP_NODE_OP_COUNT) {
@@ -167,14 +192,27 @@ class Planner {
                 if (j < 0 || j >= i || !present(nd.src[k])) {
                     return SHP_ERR_INVALID_ARG;
                 }
-                consumers_[j].push_back(i);
+                ++cstart_[j + 1];
             }
             if (nd.op != SHP_NODE_NOP) {
                 order_.push_back(i);
             }
         }
         for (int j = 0; j < n_; ++j) {
-            if (nodes_[j].uses != 0 && nodes_[j].uses < static_cast<int32_t>(consumers_[j].size())) {
+            cstart_[j + 1] += cstart_[j];
+        }
+        cons_.assign(cstart_[n_], 0);
+        std::vector<int> fill(cstart_.begin(), cstart_.end() - 1);
+        for (int i = 0; i < n_; ++i) {
+            for (int k = 0; k < SHP_NODE_MAX_SRC; ++k) {
+                const int j = nodes_[i].src_node[k];
+                if (j >= 0) {
+                    cons_[fill[j]++] = i;
+                }
+            }
+        }
+        for (int j = 0; j < n_; ++j) {
+            if (nodes_[j].uses != 0 && nodes_[j].uses < readers(j)) {
                 return SHP_ERR_INVALID_ARG;
             }
         }
@@ -231,28 +269,23 @@ class Planner {
   private:
     const shp_node *              nodes_;
     int                           n_;
-    std::vector<int>              order_;
-    std::vector<std::vector<int>> consumers_;
+    std::vector<int> order_;
+    std::vector<int> cstart_;
+    std::vector<int> cons_;
+
+    int readers(int j) const { return cstart_[j + 1] - cstart_[j]; }
 
     // Node index at window position p + k, or -1 past the end.
     int at(size_t p, int k) const { return p + k < order_.size() ? order_[p + k] : -1; }
 
-    // The window order_[p, p + k) is exactly `members` (each listed once).
-    bool window_is(size_t p, const std::vector<int> & members) const {
-        if (p + members.size() > order_.size()) {
+    // The window order_[p, p + members.n) holds exactly `members` (distinct
+    // node indices).
+    bool window_is(size_t p, const Members & members) const {
+        if (p + members.n > order_.size()) {
             return false;
         }
-        std::vector<char> seen(members.size(), 0);
-        for (size_t k = 0; k < members.size(); ++k) {
-            bool found = false;
-            for (size_t m = 0; m < members.size(); ++m) {
-                if (!seen[m] && members[m] == order_[p + k]) {
-                    seen[m] = 1;
-                    found   = true;
-                    break;
-                }
-            }
-            if (!found) {
+        for (int k = 0; k < members.n; ++k) {
+            if (!members.has(order_[p + k])) {
                 return false;
             }
         }
@@ -261,19 +294,15 @@ class Planner {
 
     // j's result may go unwritten: not an output, read by no later split and
     // by no node of the list outside `members`.
-    bool internal(int j, const std::vector<int> & members) const {
+    bool internal(int j, const Members & members) const {
         if (nodes_[j].flags & SHP_NODE_FLAG_OUTPUT) {
             return false;
         }
-        if (consumers_[j].empty() || nodes_[j].uses > static_cast<int32_t>(consumers_[j].size())) {
+        if (readers(j) == 0 || nodes_[j].uses > readers(j)) {
             return false;
         }
-        for (int c : consumers_[j]) {
-            bool in = false;
-            for (int m : members) {
-                in = in || m == c;
-            }
-            if (!in) {
+        for (int c = cstart_[j]; c < cstart_[j + 1]; ++c) {
+            if (!members.has(cons_[c])) {
                 return false;
             }
         }
@@ -281,7 +310,7 @@ class Planner {
     }
 
     // j's result is read outside `members` (or is an output): it must be written.
-    bool needed_outside(int j, const std::vector<int> & members) const {
+    bool needed_outside(int j, const Members & members) const {
         return (nodes_[j].flags & SHP_NODE_FLAG_OUTPUT) || !internal(j, members);
     }
 
@@ -289,35 +318,46 @@ class Planner {
 
     int src(int j, int k) const { return nodes_[j].src_node[k]; }
 
+    // The longest run that starts at window position p (0: none). Runs are
+    // tried by the op of their first node.
     int match(size_t p, Launch & l) const {
-        int used;
-        if ((used = match_gather_sum(p, l)) != 0) {
-            return used;
+        int used = 0;
+        switch (nodes_[order_[p]].op) {
+            case SHP_NODE_GET_ROWS:
+                return match_gather_sum(p, l);
+            case SHP_NODE_MUL:
+            case SHP_NODE_EXP:
+            case SHP_NODE_SCALE:
+                for (int k : { 8, 6, 5 }) {
+                    if ((used = match_snake(p, k, l)) != 0) {
+                        return used;
+                    }
+                }
+                return 0;
+            case SHP_NODE_ADD:
+                for (int k : { 4, 3 }) {
+                    if ((used = match_add_norm(p, k, l)) != 0) {
+                        return used;
+                    }
+                }
+                for (int k = 2 + 7; k >= 3; --k) {
+                    if ((used = match_add_scale_leaky(p, k, l)) != 0) {
+                        return used;
+                    }
+                }
+                return match_add_leaky(p, l);
+            case SHP_NODE_RMS_NORM:
+                for (int k : { 5, 4, 3, 2 }) {
+                    if ((used = match_norm(p, k, l)) != 0) {
+                        return used;
+                    }
+                }
+                return 0;
+            case SHP_NODE_SILU:
+                return match_silu_mul(p, l);
+            default:
+                return 0;
         }
-        for (int k : { 8, 6, 5 }) {
-            if ((used = match_snake(p, k, l)) != 0) {
-                return used;
-            }
-        }
-        for (int k : { 4, 3 }) {
-            if ((used = match_add_norm(p, k, l)) != 0) {
-                return used;
-            }
-        }
-        for (int k : { 5, 4, 3, 2 }) {
-            if ((used = match_norm(p, k, l)) != 0) {
-                return used;
-            }
-        }
-        for (int k = 2 + 7; k >= 3; --k) {
-            if ((used = match_add_scale_leaky(p, k, l)) != 0) {
-                return used;
-            }
-        }
-        if ((used = match_add_leaky(p, l)) != 0) {
-            return used;
-        }
-        return match_silu_mul(p, l);
     }
 
     // GET_ROWS, then (GET_ROWS, ADD(acc, rows)) per further group: the tables
@@ -334,11 +374,11 @@ class Planner {
         if (ids0.ne[1] != 1 || ids0.ne[2] != 1 || !contiguous(ids0) || !contiguous(nodes_[g0].dst)) {
             return 0;
         }
-        std::vector<int> members{ g0 };
-        int              acc    = g0;
-        int              groups = 1;
-        int              best   = 0;
-        std::vector<int> best_members;
+        Members members{ g0 };
+        int     acc    = g0;
+        int     groups = 1;
+        int     best   = 0;
+        int     last   = -1;
         while (groups < 64) {
             const int gr = at(p, 2 * groups - 1);
             const int ad = at(p, 2 * groups);
@@ -358,17 +398,18 @@ class Planner {
             if (!order_ok || !ids_ok || !tab_ok || !f32_of(A.dst) || !same_shape(A.dst, nodes_[g0].dst)) {
                 break;
             }
-            members.push_back(gr);
-            members.push_back(ad);
+            members.push(gr);
+            members.push(ad);
             acc = ad;
             ++groups;
+            // Every result before the last add is read only inside the run.
             bool ok = true;
-            for (size_t m = 0; m + 1 < members.size(); ++m) {
-                ok = ok && internal(members[m], members);
+            for (int m = 0; m + 1 < members.n; ++m) {
+                ok = ok && internal(members.v[m], members);
             }
             if (ok) {
-                best         = groups;
-                best_members = members;
+                best = groups;
+                last = ad;
             }
         }
         if (best < 2) {
@@ -378,14 +419,14 @@ class Planner {
         l.terms.clear();
         l.terms.push_back(t0);
         for (int g = 1; g < best; ++g) {
-            l.terms.push_back(nodes_[best_members[2 * g - 1]].src[0]);
+            l.terms.push_back(nodes_[members.v[2 * g - 1]].src[0]);
         }
         l.codes       = ids0;
         l.codes.ne[1] = best;
         l.codes.nb[1] = static_cast<size_t>(fr) * 4;
         l.codes.nb[2] = l.codes.nb[1] * best;
         l.codes.nb[3] = l.codes.nb[2];
-        l.y           = const_cast<shp_tensor *>(&nodes_[best_members.back()].dst);
+        l.y           = const_cast<shp_tensor *>(&nodes_[last].dst);
         return 2 * best - 1;
     }
 
@@ -424,7 +465,7 @@ class Planner {
         }
         const int64_t C = x.ne[0];
         const int     den = src(dv, 1);
-        std::vector<int> members{ ml, sn, sq, dv, ad };
+        Members members{ ml, sn, sq, dv, ad };
         auto curve_ok = [C](const shp_tensor & c) {
             return well_formed(&c) && c.type == SHP_TYPE_F32 && nelements(c) == C && contiguous(c);
         };
@@ -445,7 +486,7 @@ class Planner {
             if (!guard_ok(den) || !curve_ok(M.src[1]) || !same_tensor(nodes_[den].src[0], M.src[1])) {
                 return 0;
             }
-            members.push_back(den);
+            members.push(den);
             kind = SHP_RUN_SNAKE_GUARDED;
             l.w  = &M.src[1];
         } else {
@@ -457,18 +498,18 @@ class Planner {
             if (!is(eb, SHP_NODE_EXP) || eb == ea || !curve_ok(nodes_[ea].src[0]) || !curve_ok(nodes_[eb].src[0])) {
                 return 0;
             }
-            members.push_back(den);
-            members.push_back(ea);
-            members.push_back(eb);
+            members.push(den);
+            members.push(ea);
+            members.push(eb);
             kind = SHP_RUN_SNAKE_BETA;
             l.w  = &nodes_[ea].src[0];
             l.c1 = &nodes_[eb].src[0];
         }
-        if (static_cast<int>(members.size()) != k || !window_is(p, members)) {
+        if (members.n != k || !window_is(p, members)) {
             return 0;
         }
-        for (int j : members) {
-            if (j != ad && !internal(j, members)) {
+        for (int m = 0; m < members.n; ++m) {
+            if (members.v[m] != ad && !internal(members.v[m], members)) {
                 return 0;
             }
         }
@@ -530,11 +571,11 @@ class Planner {
             if (!f32_of(nodes_[mul].dst) || !same_shape(nodes_[mul].dst, N.src[0])) {
                 continue;
             }
-            std::vector<int> members{ nrm, mul };
+            Members members{ nrm, mul };
             if (cast >= 0) {
-                members.push_back(cast);
+                members.push(cast);
             }
-            const int rest = k - static_cast<int>(members.size());
+            const int rest = k - members.n;
             int       rope = -1, cp = -1;
             if (rest >= 1) {
                 rope = at(p, mpos + 1);
@@ -542,7 +583,7 @@ class Planner {
                     fparam(nodes_[rope], 8) != 1.0f) {
                     continue;
                 }
-                members.push_back(rope);
+                members.push(rope);
             }
             if (rest == 2) {
                 cp = at(p, mpos + 2);
@@ -550,15 +591,15 @@ class Planner {
                     !same_shape(nodes_[cp].dst, nodes_[rope].dst)) {
                     continue;
                 }
-                members.push_back(cp);
+                members.push(cp);
             }
             if (rest > 2 || !window_is(p, members)) {
                 continue;
             }
             const int sink = cp >= 0 ? cp : (rope >= 0 ? rope : mul);
             bool      ok   = true;
-            for (int j : members) {
-                ok = ok && (j == sink || internal(j, members));
+            for (int m = 0; m < members.n; ++m) {
+                ok = ok && (members.v[m] == sink || internal(members.v[m], members));
             }
             if (!ok) {
                 continue;
@@ -604,9 +645,9 @@ class Planner {
         if (!f32_of(nodes_[mul].dst) || !same_shape(nodes_[mul].dst, A.dst)) {
             return 0;
         }
-        std::vector<int> members{ ad, nrm, mul };
+        Members members{ ad, nrm, mul };
         if (cast >= 0) {
-            members.push_back(cast);
+            members.push(cast);
         }
         if (!window_is(p, members) || !internal(nrm, members) || (cast >= 0 && !internal(cast, members))) {
             return 0;
@@ -630,7 +671,7 @@ class Planner {
             fparam(nodes_[sc], 1) != 0.0f) {
             return 0;
         }
-        std::vector<int>        members;
+        Members                 members;
         std::vector<shp_tensor> terms;
         int                     acc = -1;
         for (int a = 0; a < nadd; ++a) {
@@ -654,15 +695,15 @@ class Planner {
                 return 0;
             }
             acc = ad;
-            members.push_back(ad);
+            members.push(ad);
         }
         if (src(sc, 0) != acc) {
             return 0;
         }
-        members.push_back(sc);
-        members.push_back(lk);
+        members.push(sc);
+        members.push(lk);
         for (int a = 0; a < nadd; ++a) {
-            if (!internal(members[a], members)) {
+            if (!internal(members.v[a], members)) {
                 return 0;
             }
         }
@@ -692,7 +733,7 @@ class Planner {
             !same_shape(A.dst, A.src[0]) || !unary_ok(L)) {
             return 0;
         }
-        const std::vector<int> members{ ad, lk };
+        const Members members{ ad, lk };
         l.kind = SHP_RUN_ADD_LEAKY;
         l.x    = &A.src[0];
         l.b    = &A.src[1];
@@ -720,7 +761,7 @@ class Planner {
         }
         const shp_node & S = nodes_[si];
         if (!unary_ok(S) || !f32_of(M.src[other]) || !same_shape(M.src[other], S.dst) || !f32_of(M.dst) ||
-            !same_shape(M.dst, S.dst) || !internal(si, { si, mu })) {
+            !same_shape(M.dst, S.dst) || !internal(si, Members{ si, mu })) {
             return 0;
         }
         l.kind = SHP_RUN_SILU_MUL;
