@@ -268,3 +268,45 @@ def test_single_nodes_graph(gpu):
     ref = R.run(lambda gr: gr.exp(e))
     assert np.abs(_np(ex.t).view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64)).max() <= 1
     assert_close(_np(mu.t), R.run(lambda gr: gr.mul(gr.silu(gate), gr.add(up, up))))
+
+
+def test_executor_inside_a_captured_hip_graph(gpu):
+    """A layer list run by shp_graph_compute inside a HIP graph capture: three
+    replays, with eager work and a synchronisation between them and new inputs
+    copied in before each, every replay bit-equal to the eager run of the same
+    list on the same inputs."""
+    import torch
+    rng = np.random.default_rng(SEED + 800)
+    T, hd = 3, 128
+    d = _layer_inputs(rng, T)
+    dev = {n: (_bf16(gpu, a) if n.startswith("w") else _t(gpu, a)) for n, a in d.items()}
+    g = gpu.Graph()
+    normed = g.mul(g.rms_norm(dev["x"], 1e-6), g.cast(dev["w_in"]))
+    qr = g.rope_ext(g.mul(g.rms_norm(dev["q"], 1e-6), g.cast(dev["wq"])), dev["pos"], hd, gpu.ROPE_TYPE_NEOX, 1e6)
+    after = g.add(dev["x"], dev["attn"])
+    mlp_in = g.mul(g.rms_norm(after, 1e-6), g.cast(dev["w_post"]))
+    outs = (normed, qr, mlp_in, after)
+    arr, n, keep = g.nodes(*outs)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        g.compute(*outs)  # warm-up on the capture stream
+        with torch.cuda.graph(graph, stream=stream):
+            assert gpu.load().shp_graph_compute(arr, n, gpu._stream()) == gpu.OK
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        new = {k: rng.standard_normal(dev[k].shape).astype(np.float32) for k in ("x", "q", "attn")}
+        for k, a in new.items():
+            dev[k].copy_(torch.from_numpy(a).cuda())
+        junk = torch.randn(1 << 20, device="cuda").sum()  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [_np(v.t).copy() for v in outs]
+        g.compute(*outs)  # eager, same list, same inputs
+        want = [_np(v.t) for v in outs]
+        for a, b in zip(got, want):
+            assert_bitexact(a, b)
+        assert bool(torch.isfinite(junk))
