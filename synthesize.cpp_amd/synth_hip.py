@@ -16,7 +16,8 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libsynth_hip.so")
+# SHP_LIB selects another build of the library (the sanitized one of `make asan`).
+LIB_PATH = os.environ.get("SHP_LIB") or os.path.join(HERE, "libsynth_hip.so")
 
 OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_BACKEND = 0, 1, 2, 17
 TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_I32, TYPE_BF16 = 0, 1, 8, 26, 30
