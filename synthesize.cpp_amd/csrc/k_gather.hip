@@ -986,22 +986,37 @@ extern "C" shp_status_t shp_get_rows(const shp_tensor * src,
 }
 
 // The address of a -0.0 row (kQ8NegZeroRow, kNegZeroF32 or kNegZero16, by
-// table type) on the current device, where each device holds its own copy;
-// looked up once per device and type; null if HIP reports an error.
-const char * neg_zero_row_address(int32_t type) {
+// table type) on the device that `stream` runs on (the current device for the
+// null stream), where each device holds its own copy; looked up once per
+// device and type, with that device made current for the lookup and the
+// caller's device restored after it; null if HIP reports an error.
+const char * neg_zero_row_address(int32_t type, hipStream_t stream) {
     constexpr int                    kMaxDevices = 64;
     static std::atomic<const char *> cache[kMaxDevices][3];
     const int                        k   = type == SHP_TYPE_Q8_0 ? 0 : (type == SHP_TYPE_F32 ? 1 : 2);
-    int                              dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    int                              cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) {
+        return nullptr;
+    }
+    hipDevice_t dev = cur;
+    if (stream != nullptr && hipStreamGetDevice(stream, &dev) != hipSuccess) {
+        return nullptr;
+    }
+    if (dev < 0 || dev >= kMaxDevices) {
         return nullptr;
     }
     const char * p = cache[dev][k].load(std::memory_order_acquire);
     if (p == nullptr) {
+        if (dev != cur && hipSetDevice(dev) != hipSuccess) {
+            return nullptr;
+        }
         void *     q  = nullptr;
         hipError_t rc = k == 0 ? hipGetSymbolAddress(&q, HIP_SYMBOL(kQ8NegZeroRow))
                                : (k == 1 ? hipGetSymbolAddress(&q, HIP_SYMBOL(kNegZeroF32))
                                          : hipGetSymbolAddress(&q, HIP_SYMBOL(kNegZero16)));
+        if (dev != cur && hipSetDevice(cur) != hipSuccess) {
+            return nullptr;
+        }
         if (rc != hipSuccess || q == nullptr) {
             return nullptr;
         }
@@ -1056,7 +1071,7 @@ extern "C" shp_status_t shp_get_rows_sum(const shp_tensor * tables,
     // Slots past the last group (the kernels read whole chunks of slots):
     // a -0.0 row with a row stride of 0, group 0's row count (group 0's id is
     // read for them).
-    const char * zero = neg_zero_row_address(type);
+    const char * zero = neg_zero_row_address(type, as_stream(stream));
     if (zero == nullptr) {
         return SHP_ERR_BACKEND;
     }
