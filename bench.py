@@ -202,6 +202,22 @@ def decode_layer_us(S, torch, layers=28, reps=50, kv=False, total=512, streams=1
     return ms * 1e3 / (reps * layers)
 
 
+def decode_layer_bytes(streams=1, kv=False, total=512):
+    """Algorithmic bytes of one layer of decode_layer_us's graph, every operand
+    once: add+norm (a, b read; sum, y written; BF16 gain), qk-norm+rope (q, k
+    read and written; two BF16 gains; one I32 position per stream), add+norm
+    again, SwiGLU 3072 (gate, up read; act written). kv adds this step's v row
+    (read, and written with k into the caches) and the 16-head softmax over
+    `total` keys (read and written)."""
+    f32 = 4
+    per_stream = 2 * (4 * 1024 * f32) + 2 * (24 * 128 * f32) + 3 * 3072 * f32 + 4
+    fixed = 2 * 1024 * 2 + 2 * 128 * 2
+    if kv:
+        per_stream += 2 * 8 * 128 * f32
+        fixed += 2 * 16 * total * f32
+    return streams * per_stream + fixed
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline: the same step as ggml node runs on the restatement
 # ---------------------------------------------------------------------------
@@ -364,13 +380,18 @@ def suite(args, S, torch):
             swiglu_case("cfg1", 1, 3072, cold=cold)
             add_case("cfg1", 1, 1024, cold=cold)
         us = decode_layer_us(S, torch)
+        b1 = decode_layer_bytes()
         rows.append({"config": "cfg1", "op": "talker layer non-GEMM step (28-layer graph, 4 launches/layer)",
-                     "us": round(us, 3), "note": "per layer"})
-        print("cfg1  decode layer non-GEMM step: %.3f us/layer" % us, flush=True)
+                     "us": round(us, 3), "bytes": b1, "GB/s": round(b1 / (us * 1e3), 1), "note": "per layer"})
+        print("cfg1  decode layer non-GEMM step: %.3f us/layer (%d B, %.1f GB/s)" % (us, b1, b1 / (us * 1e3)),
+              flush=True)
         us_kv = decode_layer_us(S, torch, kv=True)
+        bkv = decode_layer_bytes(kv=True)
         rows.append({"config": "cfg1", "op": "talker layer non-GEMM step + KV-cache write + soft_max over 512 keys "
-                     "(28-layer graph, 5 launches/layer)", "us": round(us_kv, 3), "note": "per layer"})
-        print("cfg1  decode layer + KV write + soft_max: %.3f us/layer" % us_kv, flush=True)
+                     "(28-layer graph, 5 launches/layer)", "us": round(us_kv, 3), "bytes": bkv,
+                     "GB/s": round(bkv / (us_kv * 1e3), 1), "note": "per layer"})
+        print("cfg1  decode layer + KV write + soft_max: %.3f us/layer (%d B, %.1f GB/s)" % (us_kv, bkv,
+                                                                                        bkv / (us_kv * 1e3)), flush=True)
 
         def make_kv():
             q, k, v = randn(1, 16, 128), randn(1, 8, 128), randn(1, 8, 128)
@@ -481,9 +502,13 @@ def suite(args, S, torch):
         qk_case("cfg5", 64, 8192)
         swiglu_case("cfg5", 64, 3072)
         us64 = decode_layer_us(S, torch, streams=64)
+        b64 = decode_layer_bytes(streams=64)
         rows.append({"config": "cfg5", "op": "64 concurrent decode streams: talker layer non-GEMM step "
-                     "(28-layer graph, 4 launches/layer, 64 rows per launch)", "us": round(us64, 3), "note": "per layer"})
-        print("cfg5  64-stream decode layer non-GEMM step: %.3f us/layer" % us64, flush=True)
+                     "(28-layer graph, 4 launches/layer, 64 rows per launch)", "us": round(us64, 3), "bytes": b64,
+                     "GB/s": round(b64 / (us64 * 1e3), 1),
+                     "note": "per layer; per 28-layer step %.1f us, %d B" % (28 * us64, 28 * b64)})
+        print("cfg5  64-stream decode layer non-GEMM step: %.3f us/layer (%d B, %.1f GB/s; 28-layer step %.1f us)"
+              % (us64, b64, b64 / (us64 * 1e3), 28 * us64), flush=True)
 
     if on("gguf"):
         # A package's lookup tables streamed file -> HBM by shp_gguf_load_tensor
@@ -703,6 +728,7 @@ def main():
                    "frac_of_peak": round(value / PEAK_GBS, 4)},
         "ops": per_op,
         "decode_layer_us": round(layer_us, 3),
+        "decode_layer_GB/s": round(decode_layer_bytes() / (layer_us * 1e3), 1),
         "roofline": roof,
     }
     if not args.no_cpu:
