@@ -629,8 +629,9 @@ def read_traffic(op):
 def main():
     args = parse()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build is single-GPU by design (the primitives are "
-              "row-independent; see DESIGN.md for how they shard). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: this build is single-GPU by design. The primitives are "
+              "row-independent, so G GPUs would each run the same kernels on 1/G of the tokens or streams "
+              "with no exchange. Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     import torch
     import synth_hip as S
