@@ -27,6 +27,34 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
 
 
+def test_headers_compile_and_link_from_plain_c(tmp_path):
+    """The headers are plain C11 (a C caller, such as a ggml backend module
+    written in C, includes them with -pedantic and no warning), and a C
+    program links libsynth_hip.so and gets statuses back through it."""
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    src = tmp_path / "consumer.c"
+    src.write_text(
+        '#include "synth_hip.h"\n#include "synth_graph.h"\n#include "synth_gguf.h"\n#include <stdio.h>\n'
+        "int main(void) {\n"
+        "    shp_tensor y = {0};\n"
+        '    printf("%u %s\\n", shp_abi_version(), shp_status_string(SHP_ERR_INVALID_ARG));\n'
+        "    return shp_rms_norm_mul(NULL, NULL, 1e-6f, &y, NULL) == SHP_ERR_INVALID_ARG ? 0 : 1;\n"
+        "}\n")
+    lib_dir = os.path.dirname(S.LIB_PATH)
+    exe = tmp_path / "consumer"
+    build = subprocess.run([cc, "-std=c11", "-Wall", "-Wextra", "-pedantic", "-Werror", "-I", os.path.join(ROOT, "include"),
+                            str(src), "-L" + lib_dir, "-l:" + os.path.basename(S.LIB_PATH), "-Wl,-rpath," + lib_dir,
+                            "-o", str(exe)], capture_output=True, text=True)
+    assert build.returncode == 0, build.stderr
+    run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert run.returncode == 0, run.stderr
+    assert run.stdout.split()[0] == str(S.load().shp_abi_version())
+
+
 def test_abi_version_and_status_strings():
     assert S.abi_version() == 1
     assert S.status_string(S.OK) == "ok"
