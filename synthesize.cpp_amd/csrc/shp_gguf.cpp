@@ -317,13 +317,20 @@ shp_status_t parse(shp_gguf & g) {
         if (ti.ne[0] % b.elems != 0 || ti.offset % g.alignment != 0) {
             return SHP_ERR_INVALID_ARG;
         }
-        // bytes = blocks per row * block bytes * rows, with overflow checks
-        const unsigned __int128 rows = static_cast<unsigned __int128>(ti.ne[1]) * ti.ne[2] * ti.ne[3];
-        const unsigned __int128 nb   = static_cast<unsigned __int128>(ti.ne[0] / b.elems) * b.bytes * rows;
-        if (nb > (static_cast<unsigned __int128>(1) << 62)) {
-            return SHP_ERR_INVALID_ARG;
+        // bytes = blocks per row * block bytes * ne1 * ne2 * ne3, one factor at a
+        // time: each partial product must neither wrap nor pass 2^62, so every
+        // stride describe() derives (a partial product) and the element count
+        // (at most the byte count) fit an int64 as well.
+        constexpr uint64_t kMaxBytes = uint64_t{ 1 } << 62;
+        uint64_t           nb        = static_cast<uint64_t>(ti.ne[0] / b.elems);
+        const uint64_t     factors[] = { b.bytes, static_cast<uint64_t>(ti.ne[1]), static_cast<uint64_t>(ti.ne[2]),
+                                         static_cast<uint64_t>(ti.ne[3]) };
+        for (const uint64_t f : factors) {
+            if (__builtin_mul_overflow(nb, f, &nb) || nb > kMaxBytes) {
+                return SHP_ERR_INVALID_ARG;
+            }
         }
-        ti.nbytes = static_cast<uint64_t>(nb);
+        ti.nbytes = nb;
         if (!g.by_name.emplace(ti.name, t).second) {
             return SHP_ERR_INVALID_ARG;  // duplicate tensor name
         }

@@ -187,6 +187,14 @@ def test_malformed_files_are_refused(tmp_path):
         b[tinfo(b) + 16:tinfo(b) + 24] = struct.pack("<Q", 32)
     _expect_open(_patched(tmp_path, past_end), inv)
 
+    # Dimensions each within 2^62 whose product wraps 64 (and 128) bits: the
+    # byte count is built one factor at a time and refused once past 2^62.
+    four_d = [("t", G.GGML_F32, [4, 1, 1, 1], bytes(16))]
+    for dims in ([4, 1 << 62, 1 << 62, 16], [4, 1 << 62, 2, 1], [1 << 61, 2, 1, 1], [4, 1 << 30, 1 << 30, 1 << 2]):
+        def huge(b, dims=dims):
+            b[tinfo(b) + 4:tinfo(b) + 36] = struct.pack("<4Q", *dims)
+        _expect_open(_patched(tmp_path, huge, tensors=four_d), inv)
+
     q8_odd = [("t", G.GGML_Q8_0, [32], bytes(34))]
 
     def q8_partial_block(b):
