@@ -1,36 +1,54 @@
 #!/usr/bin/env python3
 """Benchmark of the fused non-GEMM layer primitives on one MI355X.
 
-Default workload: the non-GEMM work of one
-Qwen3-TTS-0.6B talker layer at prefill -- 512 tokens x hidden 1024, f32
-activations ~N(0,1), BF16 norm gains, 16 q / 8 kv heads x 128, NEOX rope theta
-1e6 at positions 0..511, SwiGLU 3072 -- plus the BF16 text-embedding gather
-from a 151936 x 2048 table ~N(0, 0.02) with 512 uniform ids. One step is six
-launches through the C ABI, in graph order:
+Default workload (the largest single-GPU config):
+the non-GEMM work of one Qwen3-TTS-1.7B-shaped talker layer at an 8192-token
+prefill -- hidden 2048, f32 activations ~N(0,1), BF16 norm gains, 16 q / 8 kv
+heads x 128, NEOX rope theta 1e6 at positions 0..8191, SwiGLU 6144. One step
+is five launches through the C ABI, in graph order:
 
-    get_rows(bf16 table)        talker.cpp:44
-    rms_norm_mul (input norm)   operations.cpp:86
-    qk_norm_rope (q and k)      operations.cpp:98-104
-    add_rms_norm_mul (+sum)     operations.cpp:143-145
-    swiglu                      operations.cpp:39-41
-    add (layer output)          operations.cpp:147
+    rms_norm_mul (input norm)           operations.cpp:86
+    qk_norm_rope (q and k)              operations.cpp:94-104
+    add_rms_norm_mul (+sum)             operations.cpp:143-145
+    swiglu                              operations.cpp:39-41
+    add (layer output)                  operations.cpp:147
 
-Each step is replayed from a HIP graph (captured once per input set), the way
-a decode loop would issue it. Cold-cache protocol: inputs rotate over enough
-sets that the working set exceeds 512 MB (twice the 256 MB MALL), so every
-step reads from HBM. value = algorithmic bytes per step x steps / elapsed.
+The step moves 1.41 GB, so two input sets alternate and every step reads from
+HBM (the Infinity Cache is 256 MB). Steps are captured back to back in one
+HIP graph, as a model replays its layers; value = algorithmic bytes per step x
+steps / elapsed, inputs resident in HBM before the timed region.
 
-Also reported: per-op launch durations (each op replayed alone over the same
-rotation), the dominant kernel's roofline, the 28-layer decode step's non-GEMM
-time per layer (config 1 shape), and the CPU restatement of the same step
-timed on this host (ggml-style thread split), as a baseline only.
+The same line carries, each op timed alone from a HIP graph over rotating
+input sets whose total exceeds 512 MB (cold cache):
+  - every op of the configs[4] step, and its roofline (the dominant kernel);
+  - the 16-codebook Q8_0 gather->sum and the plain Q8_0 get_rows
+    (logical bytes, every looked-up row per lookup; compulsory bytes beside);
+  - Snake, SnakeBeta, add->leaky-ReLU and add->leaky-ReLU with the
+    sum carried, on [512,8192], [256,32768] and [128,131072];
+  - the decode step's non-GEMM work per talker layer (28-layer
+    graph), without and with the KV-cache write and the attention softmax;
+  - the 512-token prefill step of the 0.6B talker (with the BF16
+    text-embedding gather) in GB/s and us per step;
+  - configs[4]'s 64-stream decode: us per 28-layer step;
+  - the CPU restatement of the configs[4] step timed on this host's cores, as
+    a baseline only.
+
+Every timed region is wrapped in a ROCTx range ("row:<config>|<op>|<bytes>"),
+so `rocprofv3 --kernel-trace --marker-trace --stats` of this command can be
+turned into per-row kernel durations with --trace-summary.
 """
 import argparse
+import ctypes
+import csv
+import glob
 import json
 import math
 import os
+import platform
+import re
 import statistics
 import sys
+from collections import defaultdict
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "synthesize.cpp_amd"))
@@ -41,87 +59,67 @@ METRIC = "achieved HBM GB/s (% of peak) per fused op; µs/talker-layer non-GEMM 
 SEED = 20260728
 COLD_BYTES = 512 << 20
 CALIB_BYTES = 256 << 20
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_configs1_step.txt")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_large_configs.txt")
+# Worker threads one GPU's share of a GPU box allows (the pool's per-GPU CPU
+# allotment); the CPU baseline never uses more.
+BOX_CPU_SHARE = 16
 
 
 def parse():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=400)
-    p.add_argument("--warmup", type=int, default=40)
-    p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU-baseline sample")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--suite", metavar="JSON", help="instead: measure every op on every BASELINE config "
-                   "(cold-cache protocol), print a markdown table and write the figures to JSON")
-    p.add_argument("--only", default="", help="with --suite: comma-separated config names to run")
-    p.add_argument("--pmc-pass", action="store_true", help="instead: run each op of the step eagerly over every "
-                   "input set a few times, plus a %d MiB device copy of known size, for rocprofv3 --pmc "
-                   "FETCH_SIZE / WRITE_SIZE passes (few dispatches, no graphs)" % (CALIB_BYTES >> 20))
-    p.add_argument("--pmc-large", action="store_true", help="instead: run one launch of each op at the large "
-                   "configs' shapes, three times, for rocprofv3 --pmc occupancy / VALU passes")
+    p.add_argument("--suite", metavar="JSON", help="instead: every op on every BASELINE config, smaller "
+                   "shapes included (cold-cache protocol); a table on stdout, the rows as JSON")
+    p.add_argument("--only", default="", help="with --suite: comma-separated config names (calib,configs0..4,gguf)")
+    p.add_argument("--pmc-large", action="store_true", help="instead: three launches of each large-config op "
+                   "on one input set, plus a %d MiB device copy of known size before and after, for "
+                   "rocprofv3 --pmc passes (few dispatches, no graphs)" % (CALIB_BYTES >> 20))
+    p.add_argument("--trace-summary", nargs=2, metavar=("ROCPROF_DIR", "BENCH_LOG"),
+                   help="instead: summarise a rocprofv3 --kernel-trace --marker-trace run of this command "
+                   "(per-row kernel durations against the bench line in BENCH_LOG); no GPU used")
+    p.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "LOG"),
+                   help="instead: HBM bytes per launch from FETCH_SIZE and WRITE_SIZE passes over --pmc-large "
+                   "(LOG: that run's output, for the op list); no GPU used")
     return p.parse_args()
 
 
 # ---------------------------------------------------------------------------
-# the step
+# ROCTx ranges (no-ops unless a profiler listens)
 # ---------------------------------------------------------------------------
 
-class PrefillStep:
-    T, HIDDEN, HEADS, KV_HEADS, HEAD_DIM, FFN = 512, 1024, 16, 8, 128, 3072
-    VOCAB, TEXT_HIDDEN = 151936, 2048
-    EPS, THETA = 1e-6, 1e6
+class Roctx:
+    def __init__(self):
+        self.lib = None
+        for name in ("librocprofiler-sdk-roctx.so.1", "/opt/rocm/lib/librocprofiler-sdk-roctx.so.1"):
+            try:
+                self.lib = ctypes.CDLL(name)
+                break
+            except OSError:
+                continue
 
-    def __init__(self, S, torch):
-        self.S, self.torch = S, torch
-        T, H, D = self.T, self.HIDDEN, self.HEAD_DIM
-        f32 = 4
-        self.op_bytes = {
-            "get_rows_bf16": T * (4 + self.TEXT_HIDDEN * 2 + self.TEXT_HIDDEN * f32),
-            "rms_norm_mul": 2 * T * H * f32 + H * 2,
-            "qk_norm_rope": 2 * (self.HEADS + self.KV_HEADS) * D * T * f32 + T * 4 + 2 * D * 2,
-            "add_rms_norm_mul": 4 * T * H * f32 + H * 2,
-            "swiglu": 3 * T * self.FFN * f32,
-            "add": 3 * T * H * f32,
-        }
-        self.step_bytes = sum(self.op_bytes.values())
-        per_set = self.step_bytes
-        self.nsets = max(2, -(-COLD_BYTES // per_set) + 1)
-        g = torch.Generator(device="cuda")
-        g.manual_seed(SEED)
-        dev = "cuda"
-        randn = lambda *shape: torch.randn(shape, generator=g, device=dev, dtype=torch.float32)
-        gain = lambda n: (1.0 + 0.1 * randn(n)).to(torch.bfloat16)
-        self.table = (0.02 * randn(self.VOCAB, self.TEXT_HIDDEN)).to(torch.bfloat16)
-        self.w_in, self.w_post = gain(H), gain(H)
-        self.wq, self.wk = gain(D), gain(D)
-        self.pos = torch.arange(T, dtype=torch.int32, device=dev)
-        self.sets = []
-        for _ in range(self.nsets):
-            s = dict(
-                ids=torch.randint(0, self.VOCAB, (T,), generator=g, device=dev, dtype=torch.int32),
-                x=randn(T, H), q=randn(T, self.HEADS, D), k=randn(T, self.KV_HEADS, D), proj=randn(T, H),
-                gate=randn(T, self.FFN), up=randn(T, self.FFN), mlp=randn(T, H),
-            )
-            s.update(emb=torch.empty(T, self.TEXT_HIDDEN, device=dev), normed=torch.empty(T, H, device=dev),
-                     qo=torch.empty_like(s["q"]), ko=torch.empty_like(s["k"]), resid=torch.empty(T, H, device=dev),
-                     mlp_in=torch.empty(T, H, device=dev), act=torch.empty(T, self.FFN, device=dev),
-                     out=torch.empty(T, H, device=dev))
-            self.sets.append(s)
-        torch.cuda.synchronize()
+    def push(self, label):
+        if self.lib is not None:
+            self.lib.roctxRangePushA(label.encode())
 
-    def ops(self, s):
-        S, c = self.S, self.sets[s]
-        return [
-            ("get_rows_bf16", lambda: S.get_rows(self.table, c["ids"], out=c["emb"])),
-            ("rms_norm_mul", lambda: S.rms_norm_mul(c["x"], self.w_in, self.EPS, out=c["normed"])),
-            ("qk_norm_rope", lambda: S.qk_norm_rope(c["q"], c["k"], self.wq, self.wk, self.EPS, self.pos,
-                                                    self.HEAD_DIM, self.THETA, q_out=c["qo"], k_out=c["ko"])),
-            ("add_rms_norm_mul", lambda: S.add_rms_norm_mul(c["x"], c["proj"], self.w_post, self.EPS,
-                                                            out=c["mlp_in"], sum_out=c["resid"])),
-            ("swiglu", lambda: S.swiglu(c["gate"], c["up"], out=c["act"])),
-            ("add", lambda: S.add(c["resid"], c["mlp"], out=c["out"])),
-        ]
+    def pop(self):
+        if self.lib is not None:
+            self.lib.roctxRangePop()
 
+
+ROCTX = Roctx()
+
+
+def row_label(cfg, op, nbytes):
+    return "row:%s|%s|%d" % (cfg, op, nbytes)
+
+
+# ---------------------------------------------------------------------------
+# graphs and timing
+# ---------------------------------------------------------------------------
 
 def capture(torch, fns):
     """One HIP graph replaying `fns` in order (each already run eagerly once)."""
@@ -137,45 +135,319 @@ def capture(torch, fns):
     return graph
 
 
-def time_graphs(torch, graphs, reps):
-    """Replays graphs round-robin `reps` times between two events; returns ms."""
+def time_graphs(torch, graphs, reps, label=None):
+    """Replays graphs round-robin `reps` times between two HIP events recorded
+    on the stream the graphs are launched on; returns ms. `label`: a ROCTx
+    range around the timed replays."""
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    if label:
+        ROCTX.push(label)
     start.record()
     for i in range(reps):
         graphs[i % len(graphs)].replay()
     end.record()
     torch.cuda.synchronize()
+    if label:
+        ROCTX.pop()
     return start.elapsed_time(end)
+
+
+def measure_op(torch, make, nbytes, reps_target=200, cold=True, label=None):
+    """Average launch duration (us) of the op built by make() -> callable, over
+    enough rotating input sets to exceed COLD_BYTES (cold=False: one set,
+    cache resident), replayed from one graph."""
+    nsets = 1 if (nbytes >= COLD_BYTES or not cold) else -(-COLD_BYTES // nbytes) + 1
+    nsets = min(nsets, 4096)
+    fns = [make() for _ in range(nsets)]
+    for f in fns:
+        f()
+    if nsets == 1:
+        fns = fns * (4 if cold else 256)  # enough nodes to amortise the graph launch
+    graph = capture(torch, fns)
+    time_graphs(torch, [graph], 2)
+    reps = max(2, reps_target // len(fns))
+    us = time_graphs(torch, [graph], reps, label) * 1e3 / (reps * len(fns))
+    del graph, fns
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return us, nsets
+
+
+class Rows:
+    """Per-op rows: each op timed alone (measure_op) under a ROCTx range."""
+
+    def __init__(self, torch):
+        self.torch, self.rows = torch, []
+
+    def run(self, cfg, name, nbytes, make, cold=True, extra=None, quiet=False):
+        us, nsets = measure_op(self.torch, make, nbytes, cold=cold, label=row_label(cfg, name, nbytes))
+        gbs = nbytes / (us * 1e-6) / 1e9
+        row = {"config": cfg, "op": name, "bytes": nbytes, "us": round(us, 3), "GB/s": round(gbs, 1),
+               "frac": round(gbs / PEAK_GBS, 4), "sets": nsets}
+        if not cold:
+            row["note"] = "warm (one input set)"
+        for k, v in (extra or {}).items():
+            row[k] = v(us) if callable(v) else v
+        self.rows.append(row)
+        if not quiet:
+            print("%-10s %-40s %12d B %9.3f us %8.1f GB/s %6.1f%%  sets=%d" % (
+                cfg, name, nbytes, us, gbs, 100 * gbs / PEAK_GBS, nsets), file=sys.stderr, flush=True)
+        return row
+
+
+def gen(torch, seed):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    randn = lambda *shape: torch.randn(shape, generator=g, device="cuda", dtype=torch.float32)
+    empty = lambda *shape: torch.empty(shape, device="cuda", dtype=torch.float32)
+    bf16 = lambda n: (1.0 + 0.1 * randn(n)).to(torch.bfloat16)
+    return g, randn, empty, bf16
+
+
+# ---------------------------------------------------------------------------
+# the layer step (configs[4]; configs[1] with the text-embedding gather)
+# ---------------------------------------------------------------------------
+
+class LayerStep:
+    HEADS, KV_HEADS, HEAD_DIM = 16, 8, 128
+    VOCAB, TEXT_HIDDEN = 151936, 2048
+    EPS, THETA = 1e-6, 1e6
+
+    def __init__(self, S, torch, T, hidden, ffn, gather, nsets=None):
+        self.S, self.torch = S, torch
+        self.T, self.HIDDEN, self.FFN, self.gather = T, hidden, ffn, gather
+        H, D, f32 = hidden, self.HEAD_DIM, 4
+        self.op_bytes = {}
+        if gather:
+            self.op_bytes["get_rows_bf16"] = T * (4 + self.TEXT_HIDDEN * 2 + self.TEXT_HIDDEN * f32)
+        self.op_bytes.update({
+            "rms_norm_mul": 2 * T * H * f32 + H * 2,
+            "qk_norm_rope": 2 * (self.HEADS + self.KV_HEADS) * D * T * f32 + T * 4 + 2 * D * 2,
+            "add_rms_norm_mul": 4 * T * H * f32 + H * 2,
+            "swiglu": 3 * T * ffn * f32,
+            "add": 3 * T * H * f32,
+        })
+        self.step_bytes = sum(self.op_bytes.values())
+        self.nsets = nsets or max(2, -(-COLD_BYTES // self.step_bytes) + 1)
+        g, randn, empty, bf16 = gen(torch, SEED)
+        dev = "cuda"
+        if gather:
+            self.table = (0.02 * randn(self.VOCAB, self.TEXT_HIDDEN)).to(torch.bfloat16)
+        self.w_in, self.w_post = bf16(H), bf16(H)
+        self.wq, self.wk = bf16(D), bf16(D)
+        self.pos = torch.arange(T, dtype=torch.int32, device=dev)
+        self.sets = []
+        for _ in range(self.nsets):
+            s = dict(x=randn(T, H), q=randn(T, self.HEADS, D), k=randn(T, self.KV_HEADS, D), proj=randn(T, H),
+                     gate=randn(T, ffn), up=randn(T, ffn), mlp=randn(T, H))
+            if gather:
+                s.update(ids=torch.randint(0, self.VOCAB, (T,), generator=g, device=dev, dtype=torch.int32),
+                         emb=empty(T, self.TEXT_HIDDEN))
+            s.update(normed=empty(T, H), qo=torch.empty_like(s["q"]), ko=torch.empty_like(s["k"]),
+                     resid=empty(T, H), mlp_in=empty(T, H), act=empty(T, ffn), out=empty(T, H))
+            self.sets.append(s)
+        torch.cuda.synchronize()
+
+    def ops(self, s):
+        S, c = self.S, self.sets[s]
+        ops = [("get_rows_bf16", lambda: S.get_rows(self.table, c["ids"], out=c["emb"]))] if self.gather else []
+        return ops + [
+            ("rms_norm_mul", lambda: S.rms_norm_mul(c["x"], self.w_in, self.EPS, out=c["normed"])),
+            ("qk_norm_rope", lambda: S.qk_norm_rope(c["q"], c["k"], self.wq, self.wk, self.EPS, self.pos,
+                                                    self.HEAD_DIM, self.THETA, q_out=c["qo"], k_out=c["ko"])),
+            ("add_rms_norm_mul", lambda: S.add_rms_norm_mul(c["x"], c["proj"], self.w_post, self.EPS,
+                                                            out=c["mlp_in"], sum_out=c["resid"])),
+            ("swiglu", lambda: S.swiglu(c["gate"], c["up"], out=c["act"])),
+            ("add", lambda: S.add(c["resid"], c["mlp"], out=c["out"])),
+        ]
+
+    def time_steps(self, steps, warmup, label=None):
+        """ms per step over exactly `steps` steps, the sets in rotation: a graph
+        of all nsets steps back to back replayed steps // nsets times, then a
+        graph of the first steps % nsets. Checks that replays reproduce the
+        eager results bit for bit."""
+        torch = self.torch
+        per_set = [self.ops(s) for s in range(self.nsets)]
+        for ops in per_set:
+            for _, f in ops:
+                f()
+        torch.cuda.synchronize()
+        ref_out, ref_q = self.sets[0]["out"].clone(), self.sets[0]["qo"].clone()
+        full = capture(torch, [f for ops in per_set for _, f in ops])
+        rems = {k % self.nsets: capture(torch, [f for ops in per_set[:k % self.nsets] for _, f in ops])
+                for k in (warmup, steps) if k % self.nsets}
+
+        def run(k):
+            for _ in range(k // self.nsets):
+                full.replay()
+            if k % self.nsets:
+                rems[k % self.nsets].replay()
+
+        run(warmup)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        if label:
+            ROCTX.push(label)
+        start.record()
+        run(steps)
+        end.record()
+        torch.cuda.synchronize()
+        if label:
+            ROCTX.pop()
+        assert torch.equal(self.sets[0]["out"], ref_out) and torch.equal(self.sets[0]["qo"], ref_q)
+        del full, rems
+        return start.elapsed_time(end) / steps
+
+
+def step_op_rows(R, S, torch, cfg, T, H, F_, seed):
+    """The configs[4] step's ops alone, each on its own rotating sets."""
+    g, randn, empty, bf16 = gen(torch, seed)
+    f32 = 4
+
+    def norm(add):
+        def make():
+            a, b, w, y, s = randn(T, H), randn(T, H), bf16(H), empty(T, H), empty(T, H)
+            if add:
+                return lambda: S.add_rms_norm_mul(a, b, w, 1e-6, out=y, sum_out=s)
+            return lambda: S.rms_norm_mul(a, w, 1e-6, out=y)
+        return make
+
+    def qk():
+        q, k = randn(T, 16, 128), randn(T, 8, 128)
+        qo, ko, wq, wk = torch.empty_like(q), torch.empty_like(k), bf16(128), bf16(128)
+        pos = torch.arange(T, dtype=torch.int32, device="cuda")
+        return lambda: S.qk_norm_rope(q, k, wq, wk, 1e-6, pos, 128, 1e6, q_out=qo, k_out=ko)
+
+    def sw():
+        a, b, y = randn(T, F_), randn(T, F_), empty(T, F_)
+        return lambda: S.swiglu(a, b, out=y)
+
+    def add():
+        a, b, y = randn(T, H), randn(T, H), empty(T, H)
+        return lambda: S.add(a, b, out=y)
+
+    return {
+        "rms_norm_mul": R.run(cfg, "rms_norm_mul [%d,%d]" % (H, T), 2 * T * H * f32 + H * 2, norm(False)),
+        "qk_norm_rope": R.run(cfg, "qk_norm_rope q[128,16,%d] k[128,8,%d]" % (T, T),
+                              2 * 24 * 128 * T * f32 + T * 4 + 512, qk),
+        "add_rms_norm_mul": R.run(cfg, "add_rms_norm_mul+sum [%d,%d]" % (H, T), 4 * T * H * f32 + H * 2,
+                                  norm(True)),
+        "swiglu": R.run(cfg, "swiglu [%d,%d]" % (F_, T), 3 * T * F_ * f32, sw),
+        "add": R.run(cfg, "add [%d,%d]" % (H, T), 3 * T * H * f32, add),
+    }
+
+
+# ---------------------------------------------------------------------------
+# configs[2]: Q8_0 gather->sum and get_rows; configs[3]: vocoder activations
+# ---------------------------------------------------------------------------
+
+def q8_rows(R, S, torch, cfg, seed):
+    import numpy as np
+    import formats as F
+    g, randn, empty, bf16 = gen(torch, seed)
+    rng = np.random.default_rng(seed)
+    row, f32 = 1024 // 32 * 34, 4
+    # Each input set has its own tables, so the rotation exceeds the Infinity
+    # Cache and every launch fetches its rows from HBM.
+    keep = []
+
+    def tables(n):
+        raw = torch.from_numpy(np.stack([F.q8_0_synthetic(rng, 2048, 1024) for _ in range(n)])).cuda()
+        keep.append(raw)
+        return [S.Q8Tensor(raw[t], 1024) for t in range(n)]
+
+    def make_sum():
+        tabs = tables(16)
+        codes = torch.randint(0, 2048, (16, 4096), generator=g, device="cuda", dtype=torch.int32)
+        out = empty(4096, 1024)
+        return lambda: S.get_rows_sum(tabs, codes, out=out)
+
+    def make_q8():
+        tabs = tables(1)
+        ids = torch.randint(0, 2048, (4096,), generator=g, device="cuda", dtype=torch.int32)
+        out = empty(4096, 1024)
+        return lambda: S.get_rows(tabs[0], ids, out=out)
+
+    def compulsory(groups):
+        touched = groups * 2048 * (1.0 - (1.0 - 1.0 / 2048) ** 4096)  # expected distinct rows
+        return int(touched * row) + 4096 * (groups * 4 + 1024 * f32)
+
+    out = []
+    for name, groups, make in (("get_rows_sum q8_0 16x[1024,2048] x4096", 16, make_sum),
+                               ("get_rows q8_0 [1024,2048] x4096", 1, make_q8)):
+        logical = 4096 * (groups * (row + 4) + 1024 * f32)
+        cb = compulsory(groups)
+        out.append(R.run(cfg, name, logical, make, extra={
+            "bytes_kind": "logical (every looked-up row per lookup)", "compulsory_bytes": cb,
+            "compulsory_GB/s": lambda us, cb=cb: round(cb / (us * 1e-6) / 1e9, 1)}))
+        keep.clear()
+    return out
+
+
+def vocoder_rows(R, S, torch, cfg, seed, shapes=((512, 8192), (256, 32768), (128, 131072)), variants=False):
+    g, randn, empty, bf16 = gen(torch, seed)
+    out = []
+    for C, T in shapes:
+        n = C * T
+
+        def make_snake(C=C, T=T):
+            x, y = randn(T, C), empty(T, C)
+            al = torch.exp(torch.empty(C, device="cuda").uniform_(math.log(0.1), math.log(10.0), generator=g))
+            return lambda: S.snake(x, al, out=y)
+
+        def make_beta(C=C, T=T):
+            x, y = randn(T, C), empty(T, C)
+            la = torch.empty(C, device="cuda").uniform_(-3.0, 3.0, generator=g)
+            lb = torch.empty(C, device="cuda").uniform_(-3.0, 3.0, generator=g)
+            return lambda: S.snake_beta(x, la, lb, out=y)
+
+        def make_guarded(C=C, T=T):
+            x, y = randn(T, C), empty(T, C)
+            al = torch.exp(torch.empty(C, device="cuda").uniform_(-3.0, 3.0, generator=g))
+            return lambda: S.snake_guarded(x, al, out=y)
+
+        def make_leaky(C=C, T=T, with_s=False):
+            a, b, y, s = randn(T, C), randn(T, C), empty(T, C), empty(T, C)
+            return lambda: S.add_leaky_relu(a, b, 0.1, out=y, sum_out=s if with_s else None)
+
+        def make_branch(C=C, T=T):
+            ts, y = [randn(T, C) for _ in range(3)], empty(T, C)
+            return lambda: S.sum_scale_leaky_relu(ts, 1.0 / 3.0, 0.1, out=y)
+
+        out.append(R.run(cfg, "snake [%d,%d]" % (C, T), 8 * n + 4 * C, make_snake))
+        out.append(R.run(cfg, "snake_beta [%d,%d]" % (C, T), 8 * n + 8 * C, make_beta))
+        out.append(R.run(cfg, "add_leaky_relu [%d,%d]" % (C, T), 12 * n, make_leaky))
+        out.append(R.run(cfg, "add_leaky_relu+sum [%d,%d]" % (C, T), 16 * n, lambda: make_leaky(with_s=True)))
+        if variants:
+            out.append(R.run(cfg, "snake_guarded [%d,%d]" % (C, T), 8 * n + 4 * C, make_guarded))
+            out.append(R.run(cfg, "branch mean 3->scale->leaky [%d,%d]" % (C, T), 16 * n, make_branch))
+    return out
 
 
 # ---------------------------------------------------------------------------
 # decode step: 28 layers x (add+norm, qk-norm+rope, add+norm, swiglu) at T=1
 # ---------------------------------------------------------------------------
 
-def decode_layer_us(S, torch, layers=28, reps=50, kv=False, total=512, streams=1):
-    """µs per talker layer of the decode step's non-GEMM ops, replayed as one
+def decode_layer_us(S, torch, layers=28, reps=50, kv=False, total=512, streams=1, label=None):
+    """us per talker layer of the decode step's non-GEMM ops, replayed as one
     graph of `layers` layers. kv: qk-norm+rope also writes this step's k and v
     into the layer's cache (slot total-1) and the step adds the attention
     softmax over `total` keys for the 16 heads (5 launches per layer).
     streams: concurrent decode streams batched into each op (one token each)."""
     assert not (kv and streams != 1), "the KV variant models one stream"
-    g = torch.Generator(device="cuda")
-    g.manual_seed(SEED + 1)
-    randn = lambda *shape: torch.randn(shape, generator=g, device="cuda", dtype=torch.float32)
-    gain = lambda n: (1.0 + 0.1 * randn(n)).to(torch.bfloat16)
+    g, randn, empty, bf16 = gen(torch, SEED + 1)
     L = []
     for _ in range(layers):
         n = streams
-        c = dict(a=randn(n, 1024), b=randn(n, 1024), w1=gain(1024), w2=gain(1024), wq=gain(128),
-                 wk=gain(128), q=randn(n, 16, 128), k=randn(n, 8, 128), proj=randn(n, 1024),
-                 gate=randn(n, 3072), up=randn(n, 3072), s1=torch.empty(n, 1024, device="cuda"),
-                 y1=torch.empty(n, 1024, device="cuda"), s2=torch.empty(n, 1024, device="cuda"),
-                 y2=torch.empty(n, 1024, device="cuda"), qo=torch.empty(n, 16, 128, device="cuda"),
-                 ko=torch.empty(n, 8, 128, device="cuda"), act=torch.empty(n, 3072, device="cuda"))
+        c = dict(a=randn(n, 1024), b=randn(n, 1024), w1=bf16(1024), w2=bf16(1024), wq=bf16(128),
+                 wk=bf16(128), q=randn(n, 16, 128), k=randn(n, 8, 128), proj=randn(n, 1024),
+                 gate=randn(n, 3072), up=randn(n, 3072), s1=empty(n, 1024), y1=empty(n, 1024),
+                 s2=empty(n, 1024), y2=empty(n, 1024), qo=empty(n, 16, 128), ko=empty(n, 8, 128),
+                 act=empty(n, 3072))
         if kv:
             c.update(v=randn(1, 8, 128), kc=randn(total, 8, 128), vc=randn(total, 8, 128),
-                     sc=randn(16, 1, total), p=torch.empty(16, 1, total, device="cuda"))
+                     sc=randn(16, 1, total), p=empty(16, 1, total))
         L.append(c)
     pos = torch.full((streams,), total - 1, dtype=torch.int32, device="cuda")
     scale = 1.0 / math.sqrt(128.0)
@@ -198,7 +470,7 @@ def decode_layer_us(S, torch, layers=28, reps=50, kv=False, total=512, streams=1
         f()
     graph = capture(torch, fns)
     time_graphs(torch, [graph], 5)
-    ms = time_graphs(torch, [graph], reps)
+    ms = time_graphs(torch, [graph], reps, label)
     return ms * 1e3 / (reps * layers)
 
 
@@ -222,6 +494,36 @@ def decode_layer_bytes(streams=1, kv=False, total=512):
 # CPU baseline: the same step as ggml node runs on the restatement
 # ---------------------------------------------------------------------------
 
+def cpu_share():
+    """CPUs this process may run on: the affinity mask, the cgroup v2 quota
+    (as the reference's available_cpu_parallelism, cpu-parallelism.h:8-21),
+    and the per-GPU CPU share of the GPU box."""
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+            if q != "max":
+                quota = max(1, math.ceil(int(q) / int(period)))
+    except (OSError, ValueError):
+        pass
+    model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    n = min(affinity, quota or affinity)
+    return {"affinity_cpus": affinity, "cgroup_quota_cpus": quota, "available_cpus": n,
+            "threads_used": max(1, min(n, BOX_CPU_SHARE)), "cpu_model": model}
+
+
 def cpu_baseline(step, torch, seconds):
     import numpy as np
     import ggml_ref as R
@@ -229,169 +531,122 @@ def cpu_baseline(step, torch, seconds):
     c = step.sets[0]
     h = lambda t: t.detach().cpu().contiguous().numpy()
     bits = lambda t: h(t.view(torch.int16)).view(np.uint16)
-    table, ids = bits(step.table), h(c["ids"])
     x, q, k, proj, gate, up, mlp = (h(c[n]) for n in ("x", "q", "k", "proj", "gate", "up", "mlp"))
     w_in, w_post, wq, wk = bits(step.w_in), bits(step.w_post), bits(step.wq), bits(step.wk)
     pos = h(step.pos)
     eps, theta = np.float32(step.EPS), np.float32(step.THETA)
 
-    def build(g):
-        g.get_rows(table, R.BF16, step.TEXT_HIDDEN, ids)
-        R.rms_norm_w(g, x, w_in, eps, R.BF16)
-        R.qk_norm_rope(g, q, k, wq, wk, eps, pos, step.HEAD_DIM, theta, R.BF16)
-        s, _ = R.add_rms_norm_w(g, x, proj, w_post, eps, R.BF16)
-        R.swiglu(g, gate, up)
-        g.add(s, mlp)
-
     g = R.Graph()
-    build(g)
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        cores = os.cpu_count() or 1
-    nth = max(1, min(cores, 16))
+    R.rms_norm_w(g, x, w_in, eps, R.BF16)
+    R.qk_norm_rope(g, q, k, wq, wk, eps, pos, step.HEAD_DIM, theta, R.BF16)
+    s, _ = R.add_rms_norm_w(g, x, proj, w_post, eps, R.BF16)
+    R.swiglu(g, gate, up)
+    g.add(s, mlp)
+
+    share = cpu_share()
+    nth = share["threads_used"]
     probe = g.time(nth, 1, 1)[0]
-    reps = int(max(3, min(400, 0.5 * seconds / max(probe, 1e-6))))
-    t_many = statistics.median(g.time(nth, 2, reps))
+    reps = int(max(3, min(200, 0.5 * seconds / max(probe, 1e-6))))
+    t_many = statistics.median(g.time(nth, 0, reps))
     # max(1, N/2) threads is the reference's default CPU parallelism
-    # (cpu-parallelism.h:21-39); N and 1 bracket it.
+    # (cpu-parallelism.h:24-44); N and 1 bracket it.
     half = max(1, nth // 2)
-    t_half = statistics.median(g.time(half, 1, max(3, reps // 2)))
+    t_half = statistics.median(g.time(half, 0, max(3, reps // 2)))
     probe1 = g.time(1, 0, 1)[0]
-    reps1 = int(max(2, min(100, 0.25 * seconds / max(probe1, 1e-6))))
-    t_one = statistics.median(g.time(1, 1, reps1))
+    reps1 = int(max(1, min(50, 0.25 * seconds / max(probe1, 1e-6))))
+    t_one = statistics.median(g.time(1, 0, reps1))
     gbs = lambda t: step.step_bytes / t / 1e9
-    return {
+    out = {
         "value": round(gbs(t_many), 2), "unit": "GB/s", "cores": nth, "kind": "port",
-        "sample": "the same configs[1] prefill step (gather + norm + qk-norm/rope + add/norm + swiglu + add, "
-                  "%d ggml nodes) on the ggml-CPU restatement, median of %d reps at %d threads; "
-                  "%d threads (the reference's default, N/2): %.2f GB/s; 1 thread: %.2f GB/s (median of %d)" % (
-                      len(g.nodes), reps, nth, half, gbs(t_half), gbs(t_one), reps1),
+        "sample": "the configs[4] step (norm, qk-norm+rope, add+norm, swiglu, add; %d ggml nodes, %d B) on the "
+                  "ggml-CPU restatement (oracle/ggml_cpu_ref.c, -O3, ggml's ith/nth row split), median of %d reps "
+                  "at %d threads; %d threads (the reference's default, N/2): %.2f GB/s; 1 thread: %.2f GB/s "
+                  "(median of %d). This box: %s, %d CPUs in the affinity mask, cgroup quota %s; one GPU's share "
+                  "of the box is %d CPUs, so at most %d threads are used" % (
+                      len(g.nodes), step.step_bytes, reps, nth, half, gbs(t_half), gbs(t_one), reps1,
+                      share["cpu_model"], share["affinity_cpus"], share["cgroup_quota_cpus"], BOX_CPU_SHARE,
+                      BOX_CPU_SHARE),
         "ms_per_step": round(t_many * 1e3, 3), "value_half_threads": round(gbs(t_half), 3), "half_threads": half,
         "value_1thread": round(gbs(t_one), 3),
     }
+    out.update(share)
+    return out
 
 
 # ---------------------------------------------------------------------------
-# --suite: every op on every BASELINE config
+# --suite: every op on every BASELINE config, small shapes included
 # ---------------------------------------------------------------------------
-
-def measure_op(torch, make, nbytes, reps_target=200, cold=True):
-    """Average launch duration (µs) of the op built by make() -> callable, over
-    enough rotating input sets to exceed COLD_BYTES (cold=False: one set,
-    cache resident), replayed from one graph."""
-    nsets = 1 if (nbytes >= COLD_BYTES or not cold) else -(-COLD_BYTES // nbytes) + 1
-    nsets = min(nsets, 4096)
-    fns = [make() for _ in range(nsets)]
-    for f in fns:
-        f()
-    if nsets == 1:
-        fns = fns * (4 if cold else 256)  # warm: enough nodes to amortise the graph launch
-    graph = capture(torch, fns)
-    time_graphs(torch, [graph], 2)
-    reps = max(2, reps_target // len(fns))
-    us = time_graphs(torch, [graph], reps) * 1e3 / (reps * len(fns))
-    del graph, fns
-    torch.cuda.synchronize()
-    torch.cuda.empty_cache()
-    return us, nsets
-
 
 def suite(args, S, torch):
-    g = torch.Generator(device="cuda")
-    g.manual_seed(SEED + 7)
-    randn = lambda *shape: torch.randn(shape, generator=g, device="cuda", dtype=torch.float32)
-    empty = lambda *shape: torch.empty(shape, device="cuda", dtype=torch.float32)
-    bf16 = lambda n: (1.0 + 0.1 * randn(n)).to(torch.bfloat16)
+    R = Rows(torch)
+    g, randn, empty, bf16 = gen(torch, SEED + 7)
     f32 = 4
-    rows = []
-
-    def run(cfg, name, nbytes, make, note="", cold=True):
-        us, nsets = measure_op(torch, make, nbytes, cold=cold)
-        if not cold:
-            note = ("warm " + note).strip()
-        gbs = nbytes / (us * 1e-6) / 1e9
-        rows.append({"config": cfg, "op": name, "bytes": nbytes, "us": round(us, 3), "GB/s": round(gbs, 1),
-                     "frac": round(gbs / PEAK_GBS, 4), "sets": nsets, "note": note})
-        print("%-5s %-38s %12d B %9.3f us %8.1f GB/s %6.1f%%  sets=%d %s" % (cfg, name, nbytes, us, gbs,
-                                                                            100 * gbs / PEAK_GBS, nsets, note),
-              flush=True)
-
     want = set(filter(None, args.only.split(",")))
     on = lambda c: not want or c in want
 
+    def per_layer(cfg, name, us, nbytes, note):
+        R.rows.append({"config": cfg, "op": name, "us": round(us, 3), "bytes": nbytes,
+                       "GB/s": round(nbytes / (us * 1e3), 1), "note": note})
+        print("%-10s %-40s %9.3f us/layer  %d B  %s" % (cfg, name, us, nbytes, note), file=sys.stderr, flush=True)
+
     if on("calib"):
-        # what a plain device copy, a read-only reduction and this library's
-        # copy-like kernel (bare leaky-ReLU: one read, one write) reach on this box
         n = (1 << 30) // 4
         src, dst = randn(n), empty(n)
         acc = torch.empty((), device="cuda", dtype=torch.float32)
-        run("calib", "torch copy_ 1 GiB (read+write)", 2 * n * 4, lambda: (lambda: dst.copy_(src)))
-        run("calib", "torch sum 1 GiB (read only)", n * 4, lambda: (lambda: torch.sum(src, dim=0, out=acc)))
+        R.run("calib", "torch copy_ 1 GiB (read+write)", 2 * n * 4, lambda: (lambda: dst.copy_(src)))
+        R.run("calib", "torch sum 1 GiB (read only)", n * 4, lambda: (lambda: torch.sum(src, dim=0, out=acc)))
         del src, dst
 
         def make_floor():
             x, y = randn(8192, 2048), empty(8192, 2048)
             return lambda: S.leaky_relu(x, 0.1, out=y)
-        run("calib", "copy-like floor: bare leaky [2048,8192]", 8 * 8192 * 2048, make_floor)
+        R.run("calib", "copy-like floor: bare leaky [2048,8192]", 8 * 8192 * 2048, make_floor)
 
-    def norm_case(cfg, T, H, add=False, wsum=True, cold=True):
+    def norm_case(cfg, T, H, add=False, cold=True):
         def make():
             a, b, w, y, s = randn(T, H), randn(T, H), bf16(H), empty(T, H), empty(T, H)
             if add:
-                return lambda: S.add_rms_norm_mul(a, b, w, 1e-6, out=y, sum_out=s if wsum else None,
-                                                  want_sum=wsum)
+                return lambda: S.add_rms_norm_mul(a, b, w, 1e-6, out=y, sum_out=s)
             return lambda: S.rms_norm_mul(a, w, 1e-6, out=y)
-        n = (4 if wsum else 3) if add else 2
-        run(cfg, ("add_rms_norm_mul%s [%d,%d]" % ("+sum" if wsum else "", H, T)) if add else
-            "rms_norm_mul [%d,%d]" % (H, T), n * T * H * f32 + H * 2, make, cold=cold)
+        R.run(cfg, ("add_rms_norm_mul+sum [%d,%d]" if add else "rms_norm_mul [%d,%d]") % (H, T),
+              (4 if add else 2) * T * H * f32 + H * 2, make, cold=cold)
 
     def qk_case(cfg, T, hi, cold=True):
         def make():
             q, k = randn(T, 16, 128), randn(T, 8, 128)
-            qo, ko = torch.empty_like(q), torch.empty_like(k)
-            wq, wk = bf16(128), bf16(128)
+            qo, ko, wq, wk = torch.empty_like(q), torch.empty_like(k), bf16(128), bf16(128)
             pos = torch.randint(0, hi, (T,), generator=g, device="cuda", dtype=torch.int32)
             return lambda: S.qk_norm_rope(q, k, wq, wk, 1e-6, pos, 128, 1e6, q_out=qo, k_out=ko)
-        run(cfg, "qk_norm_rope q[128,16,%d] k[128,8,%d]" % (T, T), 2 * 24 * 128 * T * f32 + T * 4 + 512, make,
-            cold=cold)
+        R.run(cfg, "qk_norm_rope q[128,16,%d] k[128,8,%d]" % (T, T), 2 * 24 * 128 * T * f32 + T * 4 + 512, make,
+              cold=cold)
 
     def swiglu_case(cfg, T, F_, cold=True):
         def make():
             a, b, y = randn(T, F_), randn(T, F_), empty(T, F_)
             return lambda: S.swiglu(a, b, out=y)
-        run(cfg, "swiglu [%d,%d]" % (F_, T), 3 * T * F_ * f32, make, cold=cold)
+        R.run(cfg, "swiglu [%d,%d]" % (F_, T), 3 * T * F_ * f32, make, cold=cold)
 
     def add_case(cfg, T, H, cold=True):
         def make():
             a, b, y = randn(T, H), randn(T, H), empty(T, H)
             return lambda: S.add(a, b, out=y)
-        run(cfg, "add [%d,%d]" % (H, T), 3 * T * H * f32, make, cold=cold)
+        R.run(cfg, "add [%d,%d]" % (H, T), 3 * T * H * f32, make, cold=cold)
 
-    if on("cfg1"):
+    def make_sm(T=1, N=512):
+        sc, p = randn(16, T, N), empty(16, T, N)
+        return lambda: S.soft_max_ext(sc, None, 1.0 / math.sqrt(128.0), out=p)
+
+    if on("configs0"):
         def make_tiny():
             a, b = randn(1), empty(1)
             return lambda: torch.add(a, a, out=b)
-        run("cfg1", "graph launch floor (torch 1-element add)", 12, make_tiny, cold=False)
+        R.run("configs[0]", "graph launch floor (torch 1-element add)", 12, make_tiny, cold=False)
         for cold in (True, False):
-            norm_case("cfg1", 1, 1024, cold=cold)
-            norm_case("cfg1", 1, 1024, add=True, cold=cold)
-            qk_case("cfg1", 1, 64, cold=cold)
-            swiglu_case("cfg1", 1, 3072, cold=cold)
-            add_case("cfg1", 1, 1024, cold=cold)
-        us = decode_layer_us(S, torch)
-        b1 = decode_layer_bytes()
-        rows.append({"config": "cfg1", "op": "talker layer non-GEMM step (28-layer graph, 4 launches/layer)",
-                     "us": round(us, 3), "bytes": b1, "GB/s": round(b1 / (us * 1e3), 1), "note": "per layer"})
-        print("cfg1  decode layer non-GEMM step: %.3f us/layer (%d B, %.1f GB/s)" % (us, b1, b1 / (us * 1e3)),
-              flush=True)
-        us_kv = decode_layer_us(S, torch, kv=True)
-        bkv = decode_layer_bytes(kv=True)
-        rows.append({"config": "cfg1", "op": "talker layer non-GEMM step + KV-cache write + soft_max over 512 keys "
-                     "(28-layer graph, 5 launches/layer)", "us": round(us_kv, 3), "bytes": bkv,
-                     "GB/s": round(bkv / (us_kv * 1e3), 1), "note": "per layer"})
-        print("cfg1  decode layer + KV write + soft_max: %.3f us/layer (%d B, %.1f GB/s)" % (us_kv, bkv,
-                                                                                        bkv / (us_kv * 1e3)), flush=True)
+            norm_case("configs[0]", 1, 1024, cold=cold)
+            norm_case("configs[0]", 1, 1024, add=True, cold=cold)
+            qk_case("configs[0]", 1, 64, cold=cold)
+            swiglu_case("configs[0]", 1, 3072, cold=cold)
+            add_case("configs[0]", 1, 1024, cold=cold)
 
         def make_kv():
             q, k, v = randn(1, 16, 128), randn(1, 8, 128), randn(1, 8, 128)
@@ -399,116 +654,47 @@ def suite(args, S, torch):
             w = bf16(128)
             pos = torch.tensor([511], dtype=torch.int32, device="cuda")
             return lambda: S.qk_norm_rope_kv(q, k, v, w, w, 1e-6, pos, 128, 1e6, kc, vc, 511, q_out=qo)
-        run("cfg1", "qk_norm_rope_kv [128,16+8(+8 v),1]", (2 * 32) * 128 * f32 + 4 + 2 * 128 * 2, make_kv, cold=False)
+        R.run("configs[0]", "qk_norm_rope_kv [128,16+8(+8 v),1]", 64 * 128 * f32 + 4 + 2 * 128 * 2, make_kv,
+              cold=False)
+        R.run("configs[0]", "soft_max_ext [512,1,16]", 2 * 16 * 512 * f32, make_sm, cold=False)
+        per_layer("configs[0]", "talker layer non-GEMM step (28-layer graph, 4 launches/layer)",
+                  decode_layer_us(S, torch), decode_layer_bytes(), "per layer")
+        per_layer("configs[0]", "talker layer non-GEMM step + KV-cache write + soft_max over 512 keys "
+                  "(28-layer graph, 5 launches/layer)", decode_layer_us(S, torch, kv=True),
+                  decode_layer_bytes(kv=True), "per layer")
 
-        def make_sm(T=1, N=512):
-            sc, p = randn(16, T, N), empty(16, T, N)
-            return lambda: S.soft_max_ext(sc, None, 1.0 / math.sqrt(128.0), out=p)
-        run("cfg1", "soft_max_ext [512,1,16]", 2 * 16 * 512 * f32, make_sm, cold=False)
-        run("cfg2", "soft_max_ext causal-size [512,512,16]", 2 * 16 * 512 * 512 * f32, lambda: make_sm(512, 512))
-
-    if on("cfg2"):
-        norm_case("cfg2", 512, 1024)
-        qk_case("cfg2", 512, 512)
-        norm_case("cfg2", 512, 1024, add=True)
-        swiglu_case("cfg2", 512, 3072)
-        add_case("cfg2", 512, 1024)
+    if on("configs1"):
+        norm_case("configs[1]", 512, 1024)
+        qk_case("configs[1]", 512, 512)
+        norm_case("configs[1]", 512, 1024, add=True)
+        swiglu_case("configs[1]", 512, 3072)
+        add_case("configs[1]", 512, 1024)
+        R.run("configs[1]", "soft_max_ext causal-size [512,512,16]", 2 * 16 * 512 * 512 * f32,
+              lambda: make_sm(512, 512))
         table = (0.02 * randn(151936, 2048)).to(torch.bfloat16)
 
         def make_gather():
             ids = torch.randint(0, 151936, (512,), generator=g, device="cuda", dtype=torch.int32)
             out = empty(512, 2048)
             return lambda: S.get_rows(table, ids, out=out)
-        run("cfg2", "get_rows bf16 [2048,151936] x512", 512 * (4 + 2048 * 2 + 2048 * f32), make_gather)
+        R.run("configs[1]", "get_rows bf16 [2048,151936] x512", 512 * (4 + 2048 * 2 + 2048 * f32), make_gather)
         del table
 
-    if on("cfg3"):
-        import numpy as np
-        import formats as F
-        rng = np.random.default_rng(SEED + 3)
-        row = 1024 // 32 * 34
-        # Each input set has its own 16 tables (35.7 MB), so the rotation (8+ sets)
-        # exceeds the Infinity Cache and every launch fetches its tables from HBM.
-        table_sets = []
+    if on("configs2"):
+        q8_rows(R, S, torch, "configs[2]", SEED + 3)
 
-        def tables(n=16):
-            raw = torch.from_numpy(np.stack([F.q8_0_synthetic(rng, 2048, 1024) for _ in range(n)])).cuda()
-            table_sets.append(raw)
-            return [S.Q8Tensor(raw[t], 1024) for t in range(n)]
+    if on("configs3"):
+        vocoder_rows(R, S, torch, "configs[3]", SEED + 4, variants=True)
 
-        def make_sum():
-            tabs = tables()
-            codes = torch.randint(0, 2048, (16, 4096), generator=g, device="cuda", dtype=torch.int32)
-            out = empty(4096, 1024)
-            return lambda: S.get_rows_sum(tabs, codes, out=out)
-        logical = 4096 * (16 * (row + 4) + 1024 * f32)
-        touched = 16 * 2048 * (1.0 - (1.0 - 1.0 / 2048) ** 4096)  # expected distinct rows touched
-        compulsory = int(touched * row) + 4096 * (16 * 4 + 1024 * f32)
-        run("cfg3", "get_rows_sum q8_0 16x[1024,2048] x4096", compulsory, make_sum, "compulsory bytes")
-        rows[-1]["logical_bytes"] = logical
-        rows[-1]["logical_GB/s"] = round(logical / (rows[-1]["us"] * 1e-6) / 1e9, 1)
-        rows[-1]["note"] = "compulsory bytes (distinct rows once + ids + out); logical %.1f GB/s" % rows[-1]["logical_GB/s"]
-        table_sets.clear()
-
-        def make_q8():
-            tabs = tables(1)
-            ids = torch.randint(0, 2048, (4096,), generator=g, device="cuda", dtype=torch.int32)
-            out = empty(4096, 1024)
-            return lambda: S.get_rows(tabs[0], ids, out=out)
-        touched1 = 2048 * (1.0 - (1.0 - 1.0 / 2048) ** 4096)
-        compulsory1 = int(touched1 * row) + 4096 * (4 + 1024 * f32)
-        run("cfg3", "get_rows q8_0 [1024,2048] x4096", compulsory1, make_q8,
-            "compulsory bytes; logical %d B" % (4096 * (row + 4 + 1024 * f32)))
-        table_sets.clear()
-
-    if on("cfg4"):
-        for C, T in ((512, 8192), (256, 32768), (128, 131072)):
-            n = C * T
-
-            def make_snake(C=C, T=T):
-                x, y = randn(T, C), empty(T, C)
-                al = torch.exp(torch.empty(C, device="cuda").uniform_(math.log(0.1), math.log(10.0), generator=g))
-                return lambda: S.snake(x, al, out=y)
-            run("cfg4", "snake [%d,%d]" % (C, T), 8 * n + 4 * C, make_snake)
-
-            def make_leaky(C=C, T=T, with_s=False):
-                a, b, y, s = randn(T, C), randn(T, C), empty(T, C), empty(T, C)
-                return lambda: S.add_leaky_relu(a, b, 0.1, out=y, sum_out=s if with_s else None)
-            run("cfg4", "add_leaky_relu [%d,%d]" % (C, T), 12 * n, make_leaky)
-            run("cfg4", "add_leaky_relu+sum [%d,%d]" % (C, T), 16 * n, lambda: make_leaky(with_s=True))
-
-            def make_snake_var(C=C, T=T, beta=False):
-                x, y = randn(T, C), empty(T, C)
-                la = torch.empty(C, device="cuda").uniform_(-3.0, 3.0, generator=g)
-                if beta:
-                    lb = torch.empty(C, device="cuda").uniform_(-3.0, 3.0, generator=g)
-                    return lambda: S.snake_beta(x, la, lb, out=y)
-                al = torch.exp(la)
-                return lambda: S.snake_guarded(x, al, out=y)
-            run("cfg4", "snake_guarded [%d,%d]" % (C, T), 8 * n + 4 * C, make_snake_var)
-            run("cfg4", "snake_beta [%d,%d]" % (C, T), 8 * n + 8 * C, lambda: make_snake_var(beta=True))
-
-            def make_branch(C=C, T=T):
-                ts, y = [randn(T, C) for _ in range(3)], empty(T, C)
-                return lambda: S.sum_scale_leaky_relu(ts, 1.0 / 3.0, 0.1, out=y)
-            run("cfg4", "branch mean 3->scale->leaky [%d,%d]" % (C, T), 16 * n, make_branch)
-
-    if on("cfg5"):
-        norm_case("cfg5", 8192, 2048)
-        norm_case("cfg5", 8192, 2048, add=True)
-        qk_case("cfg5", 8192, 8192)
-        swiglu_case("cfg5", 8192, 6144)
-        norm_case("cfg5", 64, 1024, add=True)
-        qk_case("cfg5", 64, 8192)
-        swiglu_case("cfg5", 64, 3072)
+    if on("configs4"):
+        step_op_rows(R, S, torch, "configs[4]", 8192, 2048, 6144, SEED + 5)
+        norm_case("configs[4]", 64, 1024, add=True)
+        qk_case("configs[4]", 64, 8192)
+        swiglu_case("configs[4]", 64, 3072)
         us64 = decode_layer_us(S, torch, streams=64)
-        b64 = decode_layer_bytes(streams=64)
-        rows.append({"config": "cfg5", "op": "64 concurrent decode streams: talker layer non-GEMM step "
-                     "(28-layer graph, 4 launches/layer, 64 rows per launch)", "us": round(us64, 3), "bytes": b64,
-                     "GB/s": round(b64 / (us64 * 1e3), 1),
-                     "note": "per layer; per 28-layer step %.1f us, %d B" % (28 * us64, 28 * b64)})
-        print("cfg5  64-stream decode layer non-GEMM step: %.3f us/layer (%d B, %.1f GB/s; 28-layer step %.1f us)"
-              % (us64, b64, b64 / (us64 * 1e3), 28 * us64), flush=True)
+        per_layer("configs[4]", "64 concurrent decode streams: talker layer non-GEMM step (28-layer graph, "
+                  "4 launches/layer, 64 rows per launch)", us64, decode_layer_bytes(streams=64),
+                  "per layer; per 28-layer step %.1f us" % (28 * us64))
 
     if on("gguf"):
         # A package's lookup tables streamed file -> HBM by shp_gguf_load_tensor
@@ -548,86 +734,206 @@ def suite(args, S, torch):
                         best = dt if best is None else min(best, dt)
                         del out
                     gbs = nbytes / best / 1e9
-                    rows.append({"config": "gguf", "op": label, "bytes": nbytes, "us": round(best * 1e6, 1),
-                                 "GB/s": round(gbs, 2), "note": "page cache warm; PCIe host->device bound"})
-                    print("gguf  %-44s %12d B %11.1f us %8.2f GB/s" % (label, nbytes, best * 1e6, gbs), flush=True)
+                    R.rows.append({"config": "gguf", "op": label, "bytes": nbytes, "us": round(best * 1e6, 1),
+                                   "GB/s": round(gbs, 2), "note": "page cache warm; PCIe host->device bound"})
+                    print("gguf       %-44s %12d B %11.1f us %8.2f GB/s" % (label, nbytes, best * 1e6, gbs),
+                          file=sys.stderr, flush=True)
 
     with open(args.suite, "w") as f:
-        json.dump({"peak_GBps": PEAK_GBS, "cold_bytes": COLD_BYTES, "rows": rows}, f, indent=1)
+        json.dump({"peak_GBps": PEAK_GBS, "cold_bytes": COLD_BYTES, "rows": R.rows}, f, indent=1)
 
 
-def pmc_pass(step, torch):
-    """Each op of the step, eagerly, 3 times over every input set, between two
-    copies of CALIB_BYTES (a plain device-to-device copy: CALIB_BYTES read and
-    CALIB_BYTES written), for counter collection."""
+# ---------------------------------------------------------------------------
+# counter passes and profile summaries
+# ---------------------------------------------------------------------------
+
+PMC_OPS = [
+    ("rms_norm_mul [2048,8192]", 134221824), ("add_rms_norm_mul+sum [2048,8192]", 268439552),
+    ("qk_norm_rope q[128,16,8192] k[128,8,8192]", 201359872), ("swiglu [6144,8192]", 603979776),
+    ("add [2048,8192]", 201326592), ("snake [128,131072]", 134218240), ("snake_beta [128,131072]", 134218752),
+    ("add_leaky_relu [128,131072]", 201326592), ("get_rows_sum q8_0 16x[1024,2048] x4096", 88342528),
+    ("get_rows q8_0 [1024,2048] x4096", 21250048), ("soft_max_ext causal-size [512,512,16]", 33554432)]
+
+
+def pmc_large(S, torch):
+    """Three launches of each large-config op on one input set, between two
+    CALIB_BYTES device copies (CALIB_BYTES read and written), for rocprofv3
+    --pmc passes. The op order is PMC_OPS'."""
+    import numpy as np
+    import formats as F
+    g, randn, empty, bf16 = gen(torch, SEED + 9)
+    rng = np.random.default_rng(SEED + 9)
+    x2, x2b, w2 = randn(8192, 2048), randn(8192, 2048), bf16(2048)
+    q, k, wq, wk = randn(8192, 16, 128), randn(8192, 8, 128), bf16(128), bf16(128)
+    pos = torch.arange(8192, dtype=torch.int32, device="cuda")
+    gt, up = randn(8192, 6144), randn(8192, 6144)
+    xs, al = randn(131072, 128), torch.exp(torch.empty(128, device="cuda").uniform_(-2.3, 2.3, generator=g))
+    la = torch.empty(128, device="cuda").uniform_(-3, 3, generator=g)
+    lb = torch.empty(128, device="cuda").uniform_(-3, 3, generator=g)
+    a4, b4 = randn(131072, 128), randn(131072, 128)
+    tabs = [S.Q8Tensor(torch.from_numpy(F.q8_0_synthetic(rng, 2048, 1024)).cuda(), 1024) for _ in range(16)]
+    codes = torch.randint(0, 2048, (16, 4096), generator=g, device="cuda", dtype=torch.int32)
+    sc = randn(16, 512, 512)
+    fns = [lambda: S.rms_norm_mul(x2, w2, 1e-6), lambda: S.add_rms_norm_mul(x2, x2b, w2, 1e-6),
+           lambda: S.qk_norm_rope(q, k, wq, wk, 1e-6, pos, 128, 1e6), lambda: S.swiglu(gt, up),
+           lambda: S.add(x2, x2b), lambda: S.snake(xs, al), lambda: S.snake_beta(xs, la, lb),
+           lambda: S.add_leaky_relu(a4, b4, 0.1), lambda: S.get_rows_sum(tabs, codes),
+           lambda: S.get_rows(tabs[0], codes[0]), lambda: S.soft_max_ext(sc, None, 0.0884)]
     n = CALIB_BYTES // 4
     src = torch.randn(n, device="cuda")
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
     dst.copy_(src)
-    for _ in range(3):
-        for s in range(step.nsets):
-            for _, f in step.ops(s):
-                f()
+    for f in fns:
+        for _ in range(3):
+            f()
     dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"pmc_pass": "done", "sets": step.nsets, "calib_bytes": CALIB_BYTES, "op_bytes": step.op_bytes}))
+    print(json.dumps({"pmc_large": [name for name, _ in PMC_OPS], "calib_bytes": CALIB_BYTES}))
 
 
-def pmc_large(S, torch):
-    """One launch each of the ops at the large configs' shapes, three times
-    (rocprofv3 --pmc occupancy and VALU passes read them per dispatch)."""
-    import numpy as np
-    import formats as F
-    g = torch.Generator(device="cuda")
-    g.manual_seed(SEED + 9)
-    randn = lambda *shape: torch.randn(shape, generator=g, device="cuda", dtype=torch.float32)
-    bf16 = lambda n: (1.0 + 0.1 * randn(n)).to(torch.bfloat16)
-    rng = np.random.default_rng(SEED + 9)
-    x2, w2 = randn(8192, 2048), bf16(2048)
-    q, k, wq, wk = randn(8192, 16, 128), randn(8192, 8, 128), bf16(128), bf16(128)
-    pos = torch.arange(8192, dtype=torch.int32, device="cuda")
-    gt, up = randn(8192, 6144), randn(8192, 6144)
-    xs, al = randn(131072, 128), torch.exp(torch.empty(128, device="cuda").uniform_(-2.3, 2.3, generator=g))
-    la, lb = torch.empty(128, device="cuda").uniform_(-3, 3, generator=g), torch.empty(128, device="cuda").uniform_(
-        -3, 3, generator=g)
-    a4, b4 = randn(131072, 128), randn(131072, 128)
-    tabs = [S.Q8Tensor(torch.from_numpy(F.q8_0_synthetic(rng, 2048, 1024)).cuda(), 1024) for _ in range(16)]
-    codes = torch.randint(0, 2048, (16, 4096), generator=g, device="cuda", dtype=torch.int32)
-    sc = randn(16, 512, 512)
-    ops = [("rms_norm_mul [2048,8192]", lambda: S.rms_norm_mul(x2, w2, 1e-6)),
-           ("add_rms_norm_mul [2048,8192]", lambda: S.add_rms_norm_mul(x2, x2, w2, 1e-6)),
-           ("qk_norm_rope [128,16+8,8192]", lambda: S.qk_norm_rope(q, k, wq, wk, 1e-6, pos, 128, 1e6)),
-           ("swiglu [6144,8192]", lambda: S.swiglu(gt, up)),
-           ("snake [128,131072]", lambda: S.snake(xs, al)),
-           ("snake_beta [128,131072]", lambda: S.snake_beta(xs, la, lb)),
-           ("add_leaky_relu [128,131072]", lambda: S.add_leaky_relu(a4, b4, 0.1)),
-           ("get_rows_sum q8_0 16x4096", lambda: S.get_rows_sum(tabs, codes)),
-           ("get_rows q8_0 x4096", lambda: S.get_rows(tabs[0], codes[0])),
-           ("soft_max_ext [512,512,16]", lambda: S.soft_max_ext(sc, None, 0.0884))]
-    torch.cuda.synchronize()
-    for _ in range(3):
-        for _, f in ops:
-            f()
-    torch.cuda.synchronize()
-    print(json.dumps({"pmc_large": [name for name, _ in ops]}))
+def short_kernel(name):
+    m = re.search(r"(k_[A-Za-z0-9_]+(?:<[^()]*>)?)\(", name)
+    if m:
+        return m.group(1).replace(" ", "")
+    if "copyBuffer" in name:
+        return "__amd_rocclr_copyBuffer"
+    return re.sub(r"<.*", "", name.replace("void ", "", 1)).split("::")[-1].split("(")[0][:40]
+
+
+def _one(pattern):
+    hits = sorted(glob.glob(pattern, recursive=True))
+    if not hits:
+        raise SystemExit("no file matches %s" % pattern)
+    return hits[0]
+
+
+def _grid(r):
+    if "Grid_Size" in r:
+        return int(r["Grid_Size"])
+    return int(r["Grid_Size_X"]) * int(r.get("Grid_Size_Y", 1)) * int(r.get("Grid_Size_Z", 1))
+
+
+def trace_summary(rocdir, log):
+    """Per-row kernel durations of a `rocprofv3 --kernel-trace --marker-trace
+    --stats` run of this command: every dispatch that starts inside a row's
+    ROCTx range belongs to that row."""
+    kt = list(csv.DictReader(open(_one(os.path.join(rocdir, "**", "*kernel_trace.csv")))))
+    mk = list(csv.DictReader(open(_one(os.path.join(rocdir, "**", "*marker_api_trace.csv")))))
+    line = json.loads([l for l in open(log).read().splitlines() if l.startswith("{")][-1])
+    bench_us = {}
+    for r in line.get("ops", {}).values():
+        bench_us[(r["config"], r["op"])] = r["us"]
+    for r in line.get("rows", []):
+        bench_us[(r["config"], r["op"])] = r["us"]
+    text_col = next(c for c in ("Message", "Function", "Name") if c in mk[0])
+    ranges = [(int(m["Start_Timestamp"]), int(m["End_Timestamp"]), m[text_col]) for m in mk
+              if m[text_col].startswith(("row:", "step:"))]
+    kern = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), short_kernel(r["Kernel_Name"]), _grid(r))
+                  for r in kt)
+    out = ["# kernel durations per bench row, from rocprofv3's kernel trace (End-Start per dispatch) and the",
+           "# ROCTx range bench.py puts around each row's timed replays; bytes = the row's algorithmic bytes;",
+           "# trace_GB/s = bytes / avg_ns; frac = trace_GB/s / 8000; bench_us = bench.py's HIP-event time per",
+           "# launch for the row in the same run (graph replay, events on the replay stream).",
+           "%-11s %-44s %-36s %9s %6s %9s %9s %9s %9s %9s %6s" % (
+               "config", "op", "kernel", "grid", "calls", "avg_ns", "med_ns", "min_ns", "bench_us", "trace_GB/s",
+               "frac")]
+    import bisect
+    starts = [k[0] for k in kern]
+    for t0, t1, text in ranges:
+        lo, hi = bisect.bisect_left(starts, t0), bisect.bisect_right(starts, t1)
+        by = defaultdict(list)
+        for s, e, name, grid in kern[lo:hi]:
+            by[(name, grid)].append(e - s)
+        if text.startswith("step:"):
+            out.append("# %s: %d dispatches inside the timed steps" % (text, hi - lo))
+            for (name, grid), d in sorted(by.items(), key=lambda kv: -sum(kv[1])):
+                out.append("#   %-36s %9d %6d avg %9.0f ns" % (name, grid, len(d), statistics.mean(d)))
+            continue
+        cfg, op, nbytes = text.split(":", 1)[1].rsplit("|", 2)
+        nbytes = int(nbytes)
+        if not by:
+            out.append("%-11s %-44s (no dispatch traced)" % (cfg, op))
+            continue
+        (name, grid), d = max(by.items(), key=lambda kv: sum(kv[1]))
+        avg = statistics.mean(d)
+        bu = bench_us.get((cfg, op))
+        gbs = nbytes / avg
+        out.append("%-11s %-44s %-36s %9d %6d %9.0f %9.0f %9.0f %9s %9.1f %6.3f" % (
+            cfg, op[:44], name[:36], grid, len(d), avg, statistics.median(d), min(d),
+            "%.3f" % bu if bu is not None else "-", gbs, gbs / PEAK_GBS))
+    stats = glob.glob(os.path.join(rocdir, "**", "*kernel_stats.csv"), recursive=True)
+    if stats:
+        out += ["", "# rocprofv3 --stats (kernel_stats.csv) of the whole run, by kernel name over every shape it ran",
+                "%-44s %7s %12s %10s %6s" % ("kernel", "calls", "total_ns", "avg_ns", "pct")]
+        for r in list(csv.DictReader(open(sorted(stats)[0])))[:20]:
+            out.append("%-44s %7s %12s %10.0f %6s" % (short_kernel(r["Name"])[:44], r["Calls"], r["TotalDurationNs"],
+                                                     float(r["AverageNs"]), r["Percentage"]))
+    print("\n".join(out))
+
+
+def pmc_summary(fetch_dir, write_dir, log):
+    """HBM bytes per launch of each --pmc-large op from a FETCH_SIZE and a
+    WRITE_SIZE pass, each scaled by what the counter reads for the
+    CALIB_BYTES device copy."""
+    meta = json.loads([l for l in open(log).read().splitlines() if l.startswith("{") and "pmc_large" in l][-1])
+
+    def load(d):
+        rows = list(csv.DictReader(open(_one(os.path.join(d, "**", "*counter_collection.csv")))))
+        rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+        return [(short_kernel(r["Kernel_Name"]), _grid(r), float(r["Counter_Value"])) for r in rows]
+
+    F, W = load(fetch_dir), load(write_dir)
+    copies = [i for i, (k, g, v) in enumerate(F) if k == "__amd_rocclr_copyBuffer" and v > 1e5]
+    first, last = copies[0], copies[-1]
+    cal_f = statistics.mean([F[first][2], F[last][2]])
+    cal_w = statistics.mean([W[first][2], W[last][2]])
+    kib = meta["calib_bytes"] / 1024
+    fs, ws = kib / cal_f, kib / cal_w
+    ours = [i for i in range(first + 1, last) if F[i][0].startswith("k_")]
+    out = ["# HBM bytes per launch of the large-config kernels: two rocprofv3 --pmc passes (FETCH_SIZE, then",
+           "# WRITE_SIZE) over `bench.py --pmc-large`, three launches per op on one input set; each counter is",
+           "# scaled by what it reads for the %d MiB device copy before and after (%d KiB read and written):" % (
+               meta["calib_bytes"] >> 20, kib),
+           "# FETCH_SIZE %.1f KiB -> scale %.4f; WRITE_SIZE %.1f KiB -> scale %.4f." % (cal_f, fs, cal_w, ws),
+           "# hbm_bytes = (FETCH_KiB * fetch_scale + WRITE_KiB * write_scale) * 1024, averaged over the 3 launches;",
+           "# ratio = hbm_bytes / algorithmic bytes (gathers: logical, every looked-up row per lookup). FETCH_SIZE",
+           "# counts what L2 fetches from beyond it (Infinity Cache or HBM)."]
+    assert len(ours) == 3 * len(PMC_OPS), (len(ours), len(PMC_OPS))
+    for j, (op, nbytes) in enumerate(PMC_OPS):
+        idx = ours[3 * j:3 * j + 3]
+        fk = statistics.mean(F[i][2] for i in idx)
+        wk = statistics.mean(W[i][2] for i in idx)
+        hb = (fk * fs + wk * ws) * 1024
+        out.append("op=%s kernel=%s grid=%d fetch_kib=%.1f write_kib=%.1f hbm_bytes=%d algorithmic_bytes=%d "
+                   "ratio=%.4f" % (op.replace(" ", "_"), F[idx[0]][0], F[idx[0]][1], fk, wk, hb, nbytes,
+                                    hb / nbytes))
+    print("\n".join(out))
 
 
 def read_traffic(op):
-    """HBM bytes per launch of `op` from the committed counter summary (two
-    rocprofv3 --pmc passes, FETCH_SIZE then WRITE_SIZE, each scaled by what the
-    counter reads for the calibration copy), or None when it has no line."""
+    """HBM bytes per launch of `op` from the committed counter summary, or None."""
     if not os.path.exists(TRAFFIC_FILE):
         return None
     for line in open(TRAFFIC_FILE):
         fields = dict(kv.split("=", 1) for kv in line.split() if "=" in kv)
-        if fields.get("op") == op and "hbm_bytes" in fields:
+        if fields.get("op") == op.replace(" ", "_") and "hbm_bytes" in fields:
             return int(float(fields["hbm_bytes"]))
     return None
 
 
+# ---------------------------------------------------------------------------
+# the bench line
+# ---------------------------------------------------------------------------
+
 def main():
     args = parse()
+    if args.trace_summary:
+        trace_summary(*args.trace_summary)
+        return
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary)
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build is single-GPU by design. The primitives are "
               "row-independent, so G GPUs would each run the same kernels on 1/G of the tokens or streams "
@@ -644,96 +950,68 @@ def main():
     if args.pmc_large:
         pmc_large(S, torch)
         return
-    step = PrefillStep(S, torch)
-    if args.pmc_pass:
-        pmc_pass(step, torch)
-        return
 
-    # eager run of every op of every set (loads the code objects before capture)
-    per_set_ops = [step.ops(s) for s in range(step.nsets)]
-    for ops in per_set_ops:
-        for _, f in ops:
-            f()
-    torch.cuda.synchronize()
-    ref_out = step.sets[0]["out"].clone()
-    ref_q = step.sets[0]["qo"].clone()
+    # the 8192-token step of the 1.7B-shaped talker layer
+    step = LayerStep(S, torch, T=8192, hidden=2048, ffn=6144, gather=False, nsets=2)
+    ms_per_step = step.time_steps(args.steps, args.warmup, label="step:configs[4]")
+    step_bytes = step.step_bytes
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    cpu = None if args.no_cpu else cpu_baseline(step, torch, args.cpu_seconds)
+    del step
+    torch.cuda.empty_cache()
 
-    # The timed region runs exactly `steps` steps, the sets in rotation. A
-    # model's prefill replays its layers' steps from one graph (as the decode
-    # measurement below replays 28 layers), so the steps are captured
-    # back to back: one graph of all nsets steps, replayed steps // nsets
-    # times, and one graph of the first steps % nsets steps for the rest.
-    # ms_per_step_one_graph_each keeps the time with one graph launch per step.
-    def run_steps(k, full, rem):
-        for _ in range(k // step.nsets):
-            full.replay()
-        if rem is not None:
-            rem.replay()
+    ops4 = step_op_rows(Rows(torch), S, torch, "configs[4]", 8192, 2048, 6144, SEED + 5)
+    R = Rows(torch)
+    q8_rows(R, S, torch, "configs[2]", SEED + 3)
+    vocoder_rows(R, S, torch, "configs[3]", SEED + 4)
 
-    full = capture(torch, [f for ops in per_set_ops for _, f in ops])
-    rems = {k % step.nsets: capture(torch, [f for ops in per_set_ops[:k % step.nsets] for _, f in ops])
-            for k in (args.warmup, args.steps) if k % step.nsets}
-    run_steps(args.warmup, full, rems.get(args.warmup % step.nsets))
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    run_steps(args.steps, full, rems.get(args.steps % step.nsets))
-    end.record()
-    torch.cuda.synchronize()
-    ms_per_step = start.elapsed_time(end) / args.steps
-    value = step.step_bytes / (ms_per_step * 1e-3) / 1e9
-    step_graphs = [capture(torch, [f for _, f in ops]) for ops in per_set_ops]
-    time_graphs(torch, step_graphs, args.warmup)
-    ms_one_graph_each = time_graphs(torch, step_graphs, args.steps) / args.steps
+    dom = max(ops4, key=lambda n: ops4[n]["us"])
+    d = ops4[dom]
+    roof = {"bound": "hbm", "kernel": d["op"], "achieved": d["GB/s"], "peak": PEAK_GBS, "unit": "GB/s",
+            "frac": d["frac"], "traffic": read_traffic(d["op"]), "algorithmic_bytes": d["bytes"],
+            "us_per_launch": d["us"]}
 
-    # replays must reproduce the eager results bit for bit
-    assert torch.equal(step.sets[0]["out"], ref_out) and torch.equal(step.sets[0]["qo"], ref_q)
-
-    # per-op launch durations: each op alone, one graph over all sets
-    names = [n for n, _ in per_set_ops[0]]
-    per_op = {}
-    reps = max(args.steps // step.nsets, 4)
-    for i, name in enumerate(names):
-        graph = capture(torch, [per_set_ops[s][i][1] for s in range(step.nsets)])
-        time_graphs(torch, [graph], 2)
-        us = time_graphs(torch, [graph], reps) * 1e3 / (reps * step.nsets)
-        gbs = step.op_bytes[name] / (us * 1e-6) / 1e9
-        per_op[name] = {"us": round(us, 3), "bytes": step.op_bytes[name], "GB/s": round(gbs, 1),
-                        "frac": round(gbs / PEAK_GBS, 4)}
-    dom = max(per_op, key=lambda n: per_op[n]["us"])
-    # What a one-read-one-write stream of the same bytes reaches at this size in
-    # the same run (this library's bare leaky-ReLU over the same rotation
-    # protocol): a 19 MB launch cannot approach the HBM peak, and this says how
-    # close the dominant kernel is to what its size allows.
-    floor_elems = step.op_bytes[dom] // 8
-    floor_us, _ = measure_op(torch, lambda: (lambda x, y: (lambda: S.leaky_relu(x, 0.1, out=y)))(
-        torch.randn(floor_elems, device="cuda"), torch.empty(floor_elems, device="cuda")), 8 * floor_elems)
-    roof = {"bound": "hbm", "kernel": dom, "achieved": per_op[dom]["GB/s"], "peak": PEAK_GBS, "unit": "GB/s",
-            "frac": per_op[dom]["frac"], "traffic": read_traffic(dom),
-            "algorithmic_bytes": step.op_bytes[dom], "us_per_launch": per_op[dom]["us"],
-            "same_bytes_copy_like_us": round(floor_us, 3),
-            "frac_of_same_bytes_copy_like": round(floor_us / per_op[dom]["us"], 4)}
-
-    layer_us = decode_layer_us(S, torch)
+    # one decode token per layer, 28 layers in one graph
+    dec = decode_layer_us(S, torch, label="step:configs[0] decode, 28 layers x 4 launches")
+    dec_full = decode_layer_us(S, torch, kv=True, label="step:configs[0] decode + kv + softmax, 28 layers x 5 launches")
+    # 64 concurrent decode streams
+    dec64 = decode_layer_us(S, torch, streams=64, label="step:configs[4] 64-stream decode, 28 layers x 4 launches")
+    # the 0.6B talker's 512-token prefill step with the text-embedding gather
+    step1 = LayerStep(S, torch, T=512, hidden=1024, ffn=3072, gather=True)
+    ms1 = step1.time_steps(max(args.steps, 200), args.warmup, label="step:configs[1]")
+    b1 = step1.step_bytes
+    del step1
+    torch.cuda.empty_cache()
 
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
-        "ms_per_step_one_graph_each": round(ms_one_graph_each, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "configs[1]: Qwen3-TTS-0.6B talker layer non-GEMM prefill step, 512 tokens x hidden "
-                               "1024, 16/8 heads x 128, SwiGLU 3072, BF16 gains + BF16 151936x2048 text-embedding "
-                               "gather of 512 ids; the %d rotating input sets' steps (cold cache) replayed "
-                               "back to back from one HIP graph" % step.nsets,
-                   "tokens": step.T, "hidden": step.HIDDEN, "bytes_per_step": step.step_bytes,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "configs[4]: Qwen3-TTS-1.7B-shaped talker layer non-GEMM prefill step, 8192 tokens "
+                               "x hidden 2048, 16/8 heads x 128 (NEOX rope theta 1e6, positions 0..8191), SwiGLU "
+                               "6144, BF16 gains, f32 activations ~N(0,1): rms_norm_mul, qk_norm_rope, "
+                               "add_rms_norm_mul+sum, swiglu, add; two input sets alternating (1.41 GB per "
+                               "step, cold), steps replayed back to back from one HIP graph",
+                   "tokens": 8192, "hidden": 2048, "bytes_per_step": step_bytes,
                    "frac_of_peak": round(value / PEAK_GBS, 4)},
-        "ops": per_op,
-        "decode_layer_us": round(layer_us, 3),
-        "decode_layer_GB/s": round(decode_layer_bytes() / (layer_us * 1e3), 1),
+        "ops": {k: v for k, v in ops4.items()},
+        "rows": R.rows,
         "roofline": roof,
+        "decode_layer_us": round(dec, 3),
+        "decode_layer_full_us": round(dec_full, 3),
+        "decode_layer_note": "configs[0]: us per talker layer of a 28-layer one-token decode graph; _us: "
+                             "add+norm, qk-norm+rope, add+norm, swiglu (4 launches, %d B); _full_us: with the "
+                             "KV-cache write fused into qk-norm+rope and the 16-head softmax over 512 keys "
+                             "(5 launches, %d B)" % (decode_layer_bytes(), decode_layer_bytes(kv=True)),
+        "decode64_step_us": round(28 * dec64, 2),
+        "decode64_note": "configs[4]: 64 concurrent decode streams, us per 28-layer step (%d B per step)" % (
+            28 * decode_layer_bytes(streams=64)),
+        "configs1_step": {"GB/s": round(b1 / (ms1 * 1e-3) / 1e9, 1), "us_per_step": round(ms1 * 1e3, 3),
+                          "bytes": b1, "note": "0.6B talker layer, 512-token prefill incl. the BF16 gather "
+                          "from the 151936x2048 table; rotating sets, back to back from one HIP graph"},
     }
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(step, torch, args.cpu_seconds)
+    if cpu is not None:
+        line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
 
 
