@@ -488,6 +488,9 @@ template <int N, bool HAS_M, bool VEC> __global__ __launch_bounds__(256) void k_
 }
 
 template <int N> shp_status_t launch_sum_scale_leaky(const TermArgs & a, bool vec, hipStream_t stream) {
+    if (dry_run()) {
+        return SHP_OK;
+    }
     int64_t blocks = (a.n + 255) / 256;
     blocks         = blocks < kMaxFlatBlocks ? blocks : kMaxFlatBlocks;
     const dim3 grid(static_cast<unsigned>(blocks));
@@ -507,6 +510,9 @@ template <int N> shp_status_t launch_sum_scale_leaky(const TermArgs & a, bool ve
 
 template <int OP, bool HAS_B, bool BCAST, bool HAS_S>
 shp_status_t launch_ew(const EwArgs & a, bool flat, bool vec, hipStream_t stream) {
+    if (dry_run()) {
+        return SHP_OK;
+    }
     if (flat) {
         int64_t blocks = (a.n4 + 255) / 256;
         blocks         = blocks < kMaxFlatBlocks ? blocks : kMaxFlatBlocks;
@@ -649,7 +655,7 @@ shp_status_t launch_snake(const shp_tensor * x, const shp_tensor * c0, const shp
     }
     EwPlan             plan;
     const shp_status_t st = plan_ew(x, nullptr, false, y, nullptr, plan);
-    if (st != SHP_OK) {
+    if (st != SHP_OK || dry_run()) {
         return st;
     }
     EwArgs & g = plan.args;
@@ -823,6 +829,9 @@ extern "C" shp_status_t shp_cpy(const shp_tensor * x, shp_tensor * y, shp_stream
     }
     if (x->type == SHP_TYPE_F32) {
         return unary_entry<kCopy>(x, y, stream);
+    }
+    if (dry_run()) {
+        return SHP_OK;
     }
     CastArgs a{};
     a.x              = x->data;

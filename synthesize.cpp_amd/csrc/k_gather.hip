@@ -762,6 +762,9 @@ int lanes_for(int64_t units) {
 }
 
 template <int TYPE> shp_status_t launch_get_rows(const GatherArgs & a, bool vec, hipStream_t stream) {
+    if (dry_run()) {
+        return SHP_OK;
+    }
     if (vec) {
         if constexpr (TYPE == SHP_TYPE_Q8_0) {
             if (a.staged) {
@@ -1068,6 +1071,12 @@ extern "C" shp_status_t shp_get_rows_sum(const shp_tensor * tables,
         q8h = t.nb[1] == row_bytes(type, ne0) && t.ne[1] <= INT32_MAX &&
               static_cast<uint64_t>(t.ne[1]) * t.nb[1] < (uint64_t{ 1 } << 31);
     }
+    if ((frames + 3) / 4 > INT32_MAX) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    if (dry_run()) {
+        return SHP_OK;
+    }
     // Slots past the last group (the kernels read whole chunks of slots):
     // a -0.0 row with a row stride of 0, group 0's row count (group 0's id is
     // read for them).
@@ -1094,9 +1103,6 @@ extern "C" shp_status_t shp_get_rows_sum(const shp_tensor * tables,
     a.frames      = frames;
     a.ngroups     = n_tables;
     a.ne0         = static_cast<int32_t>(ne0);
-    if ((frames + 3) / 4 > INT32_MAX) {
-        return SHP_ERR_UNSUPPORTED;
-    }
     const hipStream_t st = as_stream(stream);
     switch (type) {
         case SHP_TYPE_F32:

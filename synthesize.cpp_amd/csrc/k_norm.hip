@@ -252,6 +252,9 @@ template <int WT, int MODE> __global__ __launch_bounds__(256) void k_rms_norm_ge
 }
 
 template <int WT, int MODE> shp_status_t launch_norm(const NormArgs & a, bool vec, hipStream_t stream) {
+    if (dry_run()) {
+        return SHP_OK;
+    }
     auto go = [&](auto kernel, int rows_per_block, int block = 256) {
         const int64_t blocks = (a.nrows + rows_per_block - 1) / rows_per_block;
         hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(block), 0, stream, a);
@@ -316,6 +319,11 @@ template <int MODE> shp_status_t dispatch_norm_w(const NormArgs & a, int wk, boo
     }
 }
 
+// float4 gain loads: 16-byte aligned F32, 8-byte aligned BF16/F16.
+bool gain_aligned(const shp_tensor * w) {
+    return w == nullptr || reinterpret_cast<uintptr_t>(w->data) % (w->type == SHP_TYPE_F32 ? 16 : 8) == 0;
+}
+
 shp_status_t norm_entry(const shp_tensor * a,
                         const shp_tensor * b,
                         const shp_tensor * w,
@@ -359,8 +367,7 @@ shp_status_t norm_entry(const shp_tensor * a,
     args.ne0   = static_cast<int32_t>(a->ne[0]);
     args.eps   = eps;
     args.w     = w != nullptr ? w->data : nullptr;
-    bool vec   = a->ne[0] % 4 == 0 && rows_aligned(*a, 16) && rows_aligned(*y, 16) &&
-               (w == nullptr || reinterpret_cast<uintptr_t>(w->data) % 8 == 0);
+    bool vec   = a->ne[0] % 4 == 0 && rows_aligned(*a, 16) && rows_aligned(*y, 16) && gain_aligned(w);
     if (b != nullptr) {
         args.b  = static_cast<const float *>(b->data);
         args.bm = make_rowmap(*b);
@@ -659,6 +666,9 @@ template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(256) void k_r
 }
 
 template <bool NORM, int WT, bool KV> shp_status_t launch_rope(const RopeArgs & a, bool fast, hipStream_t stream) {
+    if (dry_run()) {
+        return SHP_OK;
+    }
     const int total = a.part[0].heads + a.part[1].heads + a.part[2].heads;
     if (fast) {
         const int rows    = total < kRopeMaxRows ? total : kRopeMaxRows;
@@ -697,11 +707,6 @@ bool rope_part_ok(const shp_tensor * x, const shp_tensor * y) {
 
 bool part_aligned(const shp_tensor & t) {
     return reinterpret_cast<uintptr_t>(t.data) % 16 == 0 && t.nb[1] % 16 == 0 && t.nb[2] % 16 == 0;
-}
-
-// float4 gain loads: 16-byte aligned F32, 8-byte aligned BF16/F16.
-bool gain_aligned(const shp_tensor * w) {
-    return w == nullptr || reinterpret_cast<uintptr_t>(w->data) % (w->type == SHP_TYPE_F32 ? 16 : 8) == 0;
 }
 
 shp_status_t rope_entry(const shp_tensor * q,

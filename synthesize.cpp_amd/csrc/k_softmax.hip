@@ -340,6 +340,9 @@ template <bool MASK> __global__ __launch_bounds__(kSoftMaxBlock) void k_soft_max
 }
 
 template <bool MASK> shp_status_t launch_soft_max(const SoftMaxArgs & a, bool vec, hipStream_t stream) {
+    if (dry_run()) {
+        return SHP_OK;
+    }
     if (a.ne0 > kSoftMaxWaveMax) {
         hipLaunchKernelGGL((k_soft_max_block<MASK>), dim3(static_cast<unsigned>(a.nrows)), dim3(kSoftMaxBlock), 0,
                            stream, a);

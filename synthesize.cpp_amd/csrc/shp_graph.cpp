@@ -70,7 +70,12 @@ bool rope_params_ok(const shp_node & n) {
            nelements(pos) == x.ne[2] && contiguous(pos) && n_dims > 0 && n_dims % 2 == 0 && n_dims <= x.ne[0];
 }
 
-bool single_ok(const shp_node & n) {
+shp_status_t launch_single(const shp_node & n, shp_stream_t st);
+
+// The ggml node's own fields an entry point does not see: sources present
+// and well formed, op parameters this library implements (no ALiBi, no rope
+// frequency factors, no softmax sinks).
+bool node_form_ok(const shp_node & n) {
     for (int k = 0; k < SHP_NODE_MAX_SRC; ++k) {
         if (present(n.src[k]) && !well_formed(&n.src[k])) {
             return false;
@@ -129,6 +134,17 @@ bool single_ok(const shp_node & n) {
     }
 }
 
+// A node runs alone when its form is one this library implements and its
+// entry point, called in a dry run, accepts its operands: supports_op == 1
+// then means the launch goes through.
+bool single_ok(const shp_node & n) {
+    if (!node_form_ok(n)) {
+        return false;
+    }
+    DryRun dry;
+    return launch_single(n, nullptr) == SHP_OK;
+}
+
 // The nodes of a candidate run (at most 2*64 - 1: the longest gather->sum).
 struct Members {
     int v[128];
@@ -170,6 +186,9 @@ struct Launch {
     std::vector<shp_tensor> terms;
     shp_tensor              codes{};
 };
+
+class Planner;
+shp_status_t launch_run(const Planner & pl, const Launch & l, shp_stream_t st);
 
 class Planner {
   public:
@@ -234,7 +253,15 @@ class Planner {
                 continue;
             }
             Launch l;
-            const int used = match(p, l);
+            int    used = match(p, l);
+            if (used > 0) {
+                // a fused run is taken only when its entry point accepts the
+                // operands; otherwise its nodes run one by one
+                DryRun dry;
+                if (launch_run(*this, l, nullptr) != SHP_OK) {
+                    used = 0;
+                }
+            }
             if (used == 0) {
                 l       = Launch{};
                 l.kind  = single_ok(nodes_[i]) ? SHP_RUN_SINGLE : SHP_RUN_UNSUPPORTED;

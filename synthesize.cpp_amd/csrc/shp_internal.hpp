@@ -309,6 +309,29 @@ inline int weight_kind(int32_t type) {
     }
 }
 
+// Argument checks without launching. While a DryRun lives on a thread, every
+// entry point called on that thread runs all of its argument checks and
+// returns their status, but enqueues nothing and makes no HIP call: each
+// launcher returns SHP_OK where it would launch. The node-run executor answers
+// supports_op, and vets each fused run it plans, through the entry points
+// themselves this way, so what it accepts is exactly what they accept.
+inline bool & dry_run_flag() {
+    static thread_local bool flag = false;
+    return flag;
+}
+
+inline bool dry_run() {
+    return dry_run_flag();
+}
+
+struct DryRun {
+    bool prev;
+    DryRun() : prev(dry_run_flag()) { dry_run_flag() = true; }
+    ~DryRun() { dry_run_flag() = prev; }
+    DryRun(const DryRun &)             = delete;
+    DryRun & operator=(const DryRun &) = delete;
+};
+
 inline hipStream_t as_stream(shp_stream_t s) {
     return static_cast<hipStream_t>(s);
 }

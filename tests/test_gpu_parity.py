@@ -369,6 +369,30 @@ def test_rms_norm_mul(gpu, shape, wkind):
     assert same > 0.999  # double-accumulated squares: the GPU lands on the CPU's bits
 
 
+@pytest.mark.parametrize("shape", [(64, 1024), (4100, 1024), (8, 2048)])
+def test_rms_norm_mul_f32_gain_8_byte_aligned(gpu, shape):
+    """An F32 gain vector that starts 8 bytes past a 16-byte boundary (a view
+    into a larger buffer) is read element by element, not with 16-byte loads:
+    same results as the aligned copy of the same gains."""
+    import torch
+    rng = np.random.default_rng(SEED + 11 + shape[0])
+    x = rng.standard_normal(shape).astype(np.float32)
+    w, _ = _weights(rng, shape[-1], "f32")
+    eps = np.float32(1e-6)
+    buf = torch.zeros(shape[-1] + 4, dtype=torch.float32, device="cuda")
+    wv = buf[2:2 + shape[-1]]
+    wv.copy_(_t(gpu, w))
+    assert wv.data_ptr() % 16 == 8
+    ref = R.run(lambda g: R.rms_norm_w(g, x, w, eps, R.F32))
+    got = _np(gpu.rms_norm_mul(_t(gpu, x), wv, eps))
+    _, same = assert_close(got, ref)
+    assert same > 0.999
+    s, y = gpu.add_rms_norm_mul(_t(gpu, x), _t(gpu, x), wv, eps)
+    s_ref, y_ref = R.run(lambda g: R.add_rms_norm_w(g, x, x, w, eps, R.F32))
+    assert_bitexact(_np(s), s_ref)
+    assert_close(_np(y), y_ref)
+
+
 @pytest.mark.parametrize("shape,wkind", [((512, 1024), "bf16"), ((64, 2048), "f32"), ((3, 1000), "f32"),
                                          ((4099, 1024), "f16"), ((4096, 2048), "bf16")])
 def test_add_rms_norm_mul(gpu, shape, wkind):

@@ -216,6 +216,40 @@ def test_singles_and_support():
     assert kinds(g.plan(alibi)) == ["unsupported"]
 
 
+def test_support_is_the_entry_points_own_answer():
+    """supports_op (shp_graph_node_supported) runs the node's entry point with
+    its argument checks only, so a node the structural checks pass but the
+    entry point refuses is reported unsupported and planned as such: a batched
+    get_rows whose ids batch (ne[1]) differs from the table's ne[2], and a
+    softmax mask whose head count does not divide the scores' (ggml broadcasts
+    masks by whole repeats). The well-formed neighbours stay supported, and the
+    same operands through the entry points give the same statuses."""
+    L = S.load()
+
+    def support(g, v):
+        arr, n, _ = g.nodes(v)
+        return L.shp_graph_node_supported(ctypes.byref(arr[n - 1]))
+
+    g = S.Graph()
+    table, ids_bad, ids_ok = z(2, 10, 8), z(3, 4, dtype=torch.int32), z(2, 4, dtype=torch.int32)
+    bad, ok = g.get_rows(table, ids_bad), g.get_rows(table, ids_ok)
+    bad.t = z(3, 4, 8)
+    ok.t = z(2, 4, 8)
+    assert (support(g, bad), support(g, ok)) == (0, 1)
+    assert kinds(g.plan(bad)) == ["unsupported"] and kinds(g.plan(ok)) == ["single"]
+    r = ctypes.byref
+    assert L.shp_get_rows(r(S.desc(table)), r(S.desc(ids_bad)), r(S.desc(z(3, 4, 8))), None) == S.ERR_INVALID_ARG
+
+    g = S.Graph()
+    scores = z(1, 3, 2, 5)  # ggml [5, 2, 3, 1]: 3 heads
+    sm_bad = g.soft_max_ext(scores, z(2, 2, 5), 0.5)  # 2 mask heads do not divide 3
+    sm_ok = g.soft_max_ext(scores, z(1, 2, 5), 0.5)
+    assert (support(g, sm_bad), support(g, sm_ok)) == (0, 1)
+    assert kinds(g.plan(sm_bad)) == ["unsupported"] and kinds(g.plan(sm_ok)) == ["single"]
+    assert L.shp_soft_max_ext(r(S.desc(scores)), r(S.desc(z(2, 2, 5))), ctypes.c_float(0.5), ctypes.c_float(0.0),
+                              r(S.desc(z(1, 3, 2, 5))), None) == S.ERR_INVALID_ARG
+
+
 def test_malformed_lists_are_rejected():
     g = S.Graph()
     y = g.add(g.add(z(4, 8), z(4, 8)), z(4, 8))
