@@ -105,14 +105,6 @@ __device__ __forceinline__ const float * mask_row(const SoftMaxArgs & a, int64_t
                                            (i2 % a.mne2) * a.mnb2 + (i3 % a.mne3) * a.mnb3);
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) {
-        v = fmaxf(v, __shfl_xor(v, off, kWave));
-    }
-    return v;
-}
-
 // The kernel arguments a softmax wave needs before its first load.
 template <bool MASK> __device__ __forceinline__ void softmax_args_in_sgprs(const SoftMaxArgs & a) {
     args_in_sgprs(a.x, a.xm.flat, a.xm.rs, a.y, a.ym.flat, a.ym.rs, a.nrows, a.ne0, a.scale);

@@ -176,13 +176,73 @@ template <int WT> __device__ __forceinline__ float2 load_w2(const void * w, int6
     }
 }
 
-// Sum of a double over groups of W consecutive lanes (W a power of two <= 64).
+// Cross-lane moves inside a row of 16 lanes (DPP), no LDS round trip. Each
+// pattern pairs lanes symmetrically, so `v op move(v)` gives both lanes of a
+// pair the same two operands in swapped order: with a commutative op every
+// lane ends with bit-identical results.
+constexpr int kDppQuadXor1   = 0xB1;   // quad_perm(1,0,3,2): lane ^ 1
+constexpr int kDppQuadXor2   = 0x4E;   // quad_perm(2,3,0,1): lane ^ 2
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror: lane i of each 8 <-> lane 7-i
+constexpr int kDppMirror     = 0x140;  // row_mirror: lane i of each 16 <-> lane 15-i
+
+template <int CTRL> __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+
+template <int CTRL> __device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    return __builtin_bit_cast(double, static_cast<uint64_t>(dpp_u32<CTRL>(static_cast<uint32_t>(u))) |
+                                          (static_cast<uint64_t>(dpp_u32<CTRL>(static_cast<uint32_t>(u >> 32))) << 32));
+}
+
+template <int CTRL> __device__ __forceinline__ float dpp_f32(float v) {
+    return __uint_as_float(dpp_u32<CTRL>(__float_as_uint(v)));
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+    const uint64_t u  = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u), lane));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u >> 32), lane));
+    return __builtin_bit_cast(double, static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32));
+}
+
+// Sum of a double over groups of W consecutive lanes (W a power of two <= 64),
+// the same bits in every lane of a group. Every lane of a group must be
+// active. Groups of 16 and more: four DPP steps give each 16-lane row its
+// sum; rows then combine by one shuffle (W = 32) or, for the whole wave, by
+// reading the four row sums into scalars (the result is then wave-uniform).
 template <int W> __device__ __forceinline__ double group_sum(double v) {
+    if constexpr (W < 16) {
 #pragma unroll
-    for (int off = W / 2; off > 0; off >>= 1) {
-        v += __shfl_xor(v, off, W);
+        for (int off = W / 2; off > 0; off >>= 1) {
+            v += __shfl_xor(v, off, W);
+        }
+        return v;
+    } else {
+        v += dpp_f64<kDppQuadXor1>(v);
+        v += dpp_f64<kDppQuadXor2>(v);
+        v += dpp_f64<kDppHalfMirror>(v);
+        v += dpp_f64<kDppMirror>(v);
+        if constexpr (W == 32) {
+            v += __shfl_xor(v, 16, 32);
+        } else if constexpr (W == 64) {
+            v = (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
+        }
+        return v;
     }
-    return v;
+}
+
+// Maximum of a float over the wave, wave-uniform (same order-free scheme).
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f32<kDppQuadXor1>(v));
+    v = fmaxf(v, dpp_f32<kDppQuadXor2>(v));
+    v = fmaxf(v, dpp_f32<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_f32<kDppMirror>(v));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
 // ---------------------------------------------------------------------------
