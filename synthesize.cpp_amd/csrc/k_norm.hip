@@ -69,13 +69,13 @@ template <int WT> struct WRaw {
 template <int WT> __device__ __forceinline__ WRaw<WT> load_wraw(const void * w, int64_t e) {
     WRaw<WT> r;
     if constexpr (WT == kWF32) {
-        const uint4 u = *reinterpret_cast<const uint4 *>(static_cast<const float *>(w) + e);
+        const uint4 u = *to_global(reinterpret_cast<const uint4 *>(static_cast<const float *>(w) + e));
         r.v[0] = u.x;
         r.v[1] = u.y;
         r.v[2] = u.z;
         r.v[3] = u.w;
     } else if constexpr (WT != kWNone) {
-        const uint2 u = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(w) + e);
+        const uint2 u = *to_global(reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(w) + e));
         r.v[0] = u.x;
         r.v[1] = u.y;
     }
@@ -426,29 +426,93 @@ struct RopeArgs {
 // load. KV: the launch has v rows (copied, no gain).
 struct RowRef {
     const float * x;
-    float *       y;
+    float *       y;      // the output row at position pi (k and v: before the cache slot)
     const void *  w;
-    bool          copy;  // a v row: stored unchanged
-    bool          kv;    // a k or v row: lands in the cache
+    int64_t       ystep;  // k and v rows: bytes per cache row (the slot moves y by slot * ystep); q: 0
+    bool          copy;   // a v row: stored unchanged
+    bool          kv;     // a k or v row: lands in the cache
+
+    __device__ __forceinline__ float * y_at(int64_t slot) const {
+        return reinterpret_cast<float *>(reinterpret_cast<char *>(y) + slot * ystep);
+    }
 };
 
-// slot: the KV launches' first cache row (k and v output rows only).
-template <bool KV>
-__device__ __forceinline__ RowRef rope_row(const RopeArgs & a, int hh, int64_t pi, int64_t slot = 0) {
-    const RopePart & q   = a.part[0];
-    const RopePart & k   = a.part[1];
-    const RopePart & v   = a.part[2];
-    const int        qk  = q.heads + k.heads;
-    const bool       isv = KV && hh >= qk;
-    const bool       isk = !isv && hh >= q.heads;
-    const int64_t    h   = isv ? hh - qk : (isk ? hh - q.heads : hh);
-    const int64_t    py  = KV && (isk || isv) ? pi + slot : pi;
-    const char *     xb  = reinterpret_cast<const char *>(isv ? v.x : (isk ? k.x : q.x));
-    char *           yb  = reinterpret_cast<char *>(isv ? v.y : (isk ? k.y : q.y));
-    const int64_t    xo  = h * (isv ? v.xnb1 : (isk ? k.xnb1 : q.xnb1)) + pi * (isv ? v.xnb2 : (isk ? k.xnb2 : q.xnb2));
-    const int64_t    yo  = h * (isv ? v.ynb1 : (isk ? k.ynb1 : q.ynb1)) + py * (isv ? v.ynb2 : (isk ? k.ynb2 : q.ynb2));
+// One part's fields as scalars, for the per-lane selects of rope_row.
+// Selecting among the kernel-argument fields themselves lets the compiler turn
+// `isk ? k.x : q.x` into one load from a selected argument address, a
+// vector-memory round trip in front of every row load; the fields are named
+// members (not an array a lane indexes), so they stay in registers.
+struct PartFields {
+    const char * x;
+    char *       y;
+    const void * w;
+    int64_t      xnb1;
+    int64_t      xnb2;
+    int64_t      ynb1;
+    int64_t      ynb2;
+    int32_t      heads;
+};
+
+struct RopeFields {
+    PartFields q, k, v;
+};
+
+__device__ __forceinline__ PartFields part_fields(const RopePart & p) {
+    PartFields f{ reinterpret_cast<const char *>(p.x), reinterpret_cast<char *>(p.y), p.w, p.xnb1, p.xnb2, p.ynb1,
+                  p.ynb2, p.heads };
+    args_in_sgprs(f.x, f.y, f.w, f.xnb1, f.xnb2, f.ynb1, f.ynb2, f.heads);
+    return f;
+}
+
+template <bool KV> __device__ __forceinline__ RopeFields rope_fields(const RopeArgs & a) {
+    RopeFields f;
+    f.q = part_fields(a.part[0]);
+    f.k = part_fields(a.part[1]);
+    if constexpr (KV) {
+        f.v = part_fields(a.part[2]);
+    } else {
+        f.v       = f.q;
+        f.v.heads = 0;
+    }
+    return f;
+}
+
+// One of three scalars by masks (mk, mv: all ones or zero, not both), as
+// bitwise arithmetic: a select the compiler cannot turn into a load from a
+// selected address.
+__device__ __forceinline__ uint64_t pick3(uint64_t mk, uint64_t mv, uint64_t q, uint64_t k, uint64_t v) {
+    return (q & ~(mk | mv)) | (k & mk) | (v & mv);
+}
+
+template <class T> __device__ __forceinline__ uint64_t bits(T v) {
+    if constexpr (sizeof(T) == 8) {
+        return __builtin_bit_cast(uint64_t, v);
+    } else {
+        return static_cast<uint64_t>(static_cast<int64_t>(v));
+    }
+}
+
+// Head row hh of position pi: q rows first, then k rows, then (KV) v rows.
+template <bool KV> __device__ __forceinline__ RowRef rope_row(const RopeFields & a, int hh, int64_t pi) {
+    const PartFields & q    = a.q;
+    const PartFields & k    = a.k;
+    const PartFields & v    = a.v;
+    const int          qk   = q.heads + k.heads;
+    const bool         isv  = KV && hh >= qk;
+    const bool         isk  = !isv && hh >= q.heads;
+    const uint64_t     mv   = isv ? ~uint64_t{ 0 } : 0;
+    const uint64_t     mk   = isk ? ~uint64_t{ 0 } : 0;
+    auto               sel  = [&](auto fq, auto fk, auto fv) { return pick3(mk, mv, bits(fq), bits(fk), bits(fv)); };
+    const int64_t      h    = hh - static_cast<int64_t>(sel(0, q.heads, qk));
+    const uint64_t     xb   = sel(q.x, k.x, v.x);
+    const uint64_t     yb   = sel(q.y, k.y, v.y);
+    const int64_t      xo   = h * static_cast<int64_t>(sel(q.xnb1, k.xnb1, v.xnb1)) +
+                       pi * static_cast<int64_t>(sel(q.xnb2, k.xnb2, v.xnb2));
+    const int64_t      ynb2 = static_cast<int64_t>(sel(q.ynb2, k.ynb2, v.ynb2));
+    const int64_t      yo   = h * static_cast<int64_t>(sel(q.ynb1, k.ynb1, v.ynb1)) + pi * ynb2;
     return RowRef{ reinterpret_cast<const float *>(xb + xo), reinterpret_cast<float *>(yb + yo),
-                   isv ? nullptr : (isk ? k.w : q.w), isv, isk || isv };
+                   reinterpret_cast<const void *>(sel(q.w, k.w, static_cast<const void *>(nullptr))),
+                   KV && (isk || isv) ? ynb2 : 0, isv, isk || isv };
 }
 
 // The KV launches' cache slot: 0 without a device slot; with one, its value,
@@ -474,6 +538,10 @@ template <bool KV> __device__ __forceinline__ int64_t rope_slot(const RopeArgs &
 
 template <bool KV> __device__ __forceinline__ int rope_rows(const RopeArgs & a) {
     return a.part[0].heads + a.part[1].heads + (KV ? a.part[2].heads : 0);
+}
+
+template <bool KV> __device__ __forceinline__ int rope_rows(const RopeFields & f) {
+    return f.q.heads + f.k.heads + (KV ? f.v.heads : 0);
 }
 
 // cos/sin of an f32 angle: evaluated in double and rounded once (the fast
@@ -520,21 +588,24 @@ template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(1024) void k_
     __shared__ f32x4 s_cos[16];
     __shared__ f32x4 s_sin[16];
 
-    const int64_t pi    = blockIdx.x;
-    const int     total = rope_rows<KV>(a);
-    const int     slots = blockDim.x / kRopeLanes;
-    const int     g     = threadIdx.x / kRopeLanes;
-    const int     l     = threadIdx.x % kRopeLanes;
+    const int64_t pi = blockIdx.x;
+    // the position first: read before the field copies below, it stays one
+    // scalar load
+    const int32_t    p     = a.pos[pi];
+    const RopeFields f     = rope_fields<KV>(a);
+    const int        total = rope_rows<KV>(f);
+    const int        slots = blockDim.x / kRopeLanes;
+    const int        g     = threadIdx.x / kRopeLanes;
+    const int        l     = threadIdx.x % kRopeLanes;
 
     // 1. this lane's first row, and its gains (both issued before any wait)
-    const bool    live = g < total;
-    const int64_t slot = rope_slot<KV>(a);  // -1: cache rows skipped
-    RowRef        r    = rope_row<KV>(a, live ? g : 0, pi, slot);
+    const bool live = g < total;
+    RowRef     r    = rope_row<KV>(f, live ? g : 0, pi);
     f32x4      lo   = splat4(0.0f);
     f32x4      hi   = splat4(0.0f);
     if (live) {
-        lo = ld_stream(reinterpret_cast<const f32x4 *>(r.x) + l);
-        hi = ld_stream(reinterpret_cast<const f32x4 *>(r.x + 64) + l);
+        lo = ld_stream(to_global(reinterpret_cast<const f32x4 *>(r.x)) + l);
+        hi = ld_stream(to_global(reinterpret_cast<const f32x4 *>(r.x + 64)) + l);
     }
     // Gains stay raw until after the barrier: converting them here would make
     // wave 0 wait for every outstanding load before its theta chain.
@@ -546,10 +617,14 @@ template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(1024) void k_
         }
     }
 
+    // the cache slot (KV launches; read after the row loads went out, which do
+    // not depend on it): -1 when the rows do not fit, then no k or v row is stored
+    const int64_t slot = rope_slot<KV>(a);
+
     // 2. the cos/sin cache of this position (wave 0)
     if (threadIdx.x < 64) {
         const int k   = threadIdx.x;
-        float     th  = static_cast<float>(a.pos[pi]);
+        float     th  = static_cast<float>(p);
         float     mth = th;
 #pragma unroll
         for (int i = 1; i < 64; ++i) {
@@ -569,9 +644,9 @@ template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(1024) void k_
     //    64 heads) are loaded here
     for (int row = g; row < total; row += slots) {
         if (row != g) {
-            r  = rope_row<KV>(a, row, pi, slot);
-            lo = ld_stream(reinterpret_cast<const f32x4 *>(r.x) + l);
-            hi = ld_stream(reinterpret_cast<const f32x4 *>(r.x + 64) + l);
+            r  = rope_row<KV>(f, row, pi);
+            lo = ld_stream(to_global(reinterpret_cast<const f32x4 *>(r.x)) + l);
+            hi = ld_stream(to_global(reinterpret_cast<const f32x4 *>(r.x + 64)) + l);
             if constexpr (NORM && WT != kWNone) {
                 if (!r.copy) {
                     wlo_raw = load_wraw<WT>(r.w, 4 * l);
@@ -600,8 +675,9 @@ template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(1024) void k_
                          lo.w * sn.w + hi.w * cs.w };
         // a v row (whole 16-lane group) stores its input unchanged
         if (!KV || slot >= 0 || !r.kv) {
-            st_stream(reinterpret_cast<f32x4 *>(r.y) + l, KV && r.copy ? rawlo : olo);
-            st_stream(reinterpret_cast<f32x4 *>(r.y + 64) + l, KV && r.copy ? rawhi : ohi);
+            float * y = r.y_at(slot);
+            st_stream(to_global(reinterpret_cast<f32x4 *>(y)) + l, KV && r.copy ? rawlo : olo);
+            st_stream(to_global(reinterpret_cast<f32x4 *>(y + 64)) + l, KV && r.copy ? rawhi : ohi);
         }
     }
 }
@@ -618,9 +694,9 @@ template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(256) void k_r
     const int64_t pi   = row / total;
     const int     hh   = static_cast<int>(row % total);
     const int64_t slot = rope_slot<KV>(a);
-    const RowRef  rr   = rope_row<KV>(a, hh, pi, slot);
+    const RowRef  rr   = rope_row<KV>(rope_fields<KV>(a), hh, pi);
     const float * xr   = rr.x;
-    float *       yr   = rr.y;
+    float *       yr   = rr.y_at(slot);
     if (KV && rr.kv && slot < 0) {
         return;  // the rows do not fit the cache: nothing written
     }

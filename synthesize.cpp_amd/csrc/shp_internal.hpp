@@ -38,6 +38,28 @@ __device__ __forceinline__ void st_stream(float * p, float v) {
     __builtin_nontemporal_store(v, p);
 }
 
+// Global-memory pointers. A pointer rebuilt from integer arithmetic has lost
+// its address space, and accesses through it become flat ones (which also
+// count against the LDS counter); casting it back keeps them global.
+// (The host pass sees plain pointers.)
+#if defined(__HIP_DEVICE_COMPILE__)
+template <class T> using gptr = T __attribute__((address_space(1))) *;
+
+__device__ __forceinline__ f32x4 ld_stream(gptr<const f32x4> p) {
+    return __builtin_nontemporal_load(p);
+}
+
+__device__ __forceinline__ void st_stream(gptr<f32x4> p, f32x4 v) {
+    __builtin_nontemporal_store(v, p);
+}
+#else
+template <class T> using gptr = T *;
+#endif
+
+template <class T> __device__ __forceinline__ gptr<T> to_global(T * p) {
+    return (gptr<T>) p;
+}
+
 __device__ __forceinline__ f32x4 splat4(float v) {
     return f32x4{ v, v, v, v };
 }
