@@ -42,7 +42,7 @@ const char * shp_gguf_tensor_name(const shp_gguf * g, int64_t index); /* NULL wh
 /*
  * The named tensor as an shp_tensor (data NULL): type = its ggml type id,
  * ne = its dimensions (1 past n_dims), ggml's strides (nb[0] the element
- * size, or 34 bytes per Q8_0 block). nbytes and file_offset may be NULL.
+ * size, or the block's bytes: 34 per Q8_0 block, 176 per Q5_K super-block). nbytes and file_offset may be NULL.
  * SHP_ERR_INVALID_ARG when the name is absent (ggml_get_tensor's NULL).
  */
 shp_status_t shp_gguf_tensor_info(const shp_gguf * g,
@@ -61,7 +61,7 @@ shp_status_t shp_gguf_kv_string(const shp_gguf * g, const char * key, char * buf
  * bytes available) through two pinned staging buffers, the read of one chunk
  * overlapping the host-to-device copy of the other, on `stream`; returns once
  * the copy has completed, with desc describing the device tensor (data =
- * device_dst). F32, F16, BF16, Q8_0 and I32 tensors only (SHP_ERR_UNSUPPORTED
+ * device_dst). F32, F16, BF16, Q8_0, Q5_K and I32 tensors only (SHP_ERR_UNSUPPORTED
  * otherwise). The staging buffers (64 MiB pinned) are kept by the handle until
  * shp_gguf_close.
  */
@@ -96,9 +96,8 @@ shp_status_t shp_gguf_load_tensors(shp_gguf *          g,
  * The type the catalog requires of the talker half's matrix tensors -- the
  * text and codec embedding tables included -- under a quantization profile
  * (synthesize.quantization.profile): "BF16" -> BF16, "F16" -> F16,
- * "Q8_MIXED" -> Q8_0 (src/arch/qwen3-tts/catalog.cpp:155-196,
- * tools/synthesize-quantize/policy.cpp:49-98). "Q5_K_MIXED" sets *type to 13
- * (Q5_K) and returns SHP_ERR_UNSUPPORTED: the gathers take no k-quant.
+ * "Q8_MIXED" -> Q8_0, "Q5_K_MIXED" -> Q5_K (src/arch/qwen3-tts/catalog.cpp:
+ * 155-196, tools/synthesize-quantize/policy.cpp:49-98).
  * Unknown profiles give SHP_ERR_INVALID_ARG.
  */
 shp_status_t shp_table_type_for_profile(const char * profile, int32_t * type);

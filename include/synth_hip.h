@@ -47,6 +47,7 @@ typedef int32_t shp_status_t;
 #define SHP_TYPE_F32  0
 #define SHP_TYPE_F16  1
 #define SHP_TYPE_Q8_0 8
+#define SHP_TYPE_Q5_K 13
 #define SHP_TYPE_I32  26
 #define SHP_TYPE_BF16 30
 
@@ -68,9 +69,12 @@ const char * shp_status_string(shp_status_t status);
 
 /*
  * ggml_get_rows(src, ids): dst[:, r, i11, i12] = to_f32(src[:, ids[r, i11, i12], i11, i12]).
- * src F32/F16/BF16/Q8_0; ids I32 [n, ne11, ne12]; dst F32 [ne00, n, ne11, ne12].
+ * src F32/F16/BF16/Q8_0/Q5_K; ids I32 [n, ne11, ne12]; dst F32 [ne00, n, ne11, ne12].
  * Conversions are exact (Q8_0: one product q*d per element), so results are
- * bit-identical to ggml-CPU. An id outside [0, src.ne[1]) is never read:
+ * bit-identical to ggml-CPU. Q5_K (256-element super-blocks of 176 bytes,
+ * the Matrix-role tables of Q5_K_MIXED packages, qwen3-tts/catalog.cpp:
+ * 165-192): y = (d*sc)*q - dmin*m, whose products are exact in f32, so its
+ * one rounding (the subtraction) is ggml-CPU's dequantize_row_q5_K's too. An id outside [0, src.ne[1]) is never read:
  * its output row is filled with quiet NaN (ggml-CPU aborts instead; callers
  * pre-validate ids on the host, src/arch/qwen3-tts/talker-host.cpp:42).
  * Replaces: src/arch/qwen3-tts/talker.cpp:44 and :86,
@@ -83,7 +87,7 @@ shp_status_t shp_get_rows(const shp_tensor * src, const shp_tensor * ids, shp_te
  * Multi-codebook gather->sum: the node run of sum_code_embeddings,
  * src/arch/qwen3-tts/code-predictor.cpp:82-107 (one ggml_get_rows per group,
  * then ggml_add in group order). tables[g] are [ne0, rows_g] of one common
- * type (F32/F16/BF16/Q8_0); ids is I32 [frames, n_tables] contiguous, frames
+ * type (F32/F16/BF16/Q8_0/Q5_K); ids is I32 [frames, n_tables] contiguous, frames
  * fastest (code-predictor.cpp:86-99); dst is F32 [ne0, frames].
  * dst[:, f] = ((row_0 + row_1) + row_2) + ... in f32, in group order, so the
  * result is bit-identical to the unfused node run. Out-of-range ids give a

@@ -132,6 +132,8 @@ static size_t row_bytes(int type, int64_t ne0) {
             return (size_t) ne0 * 2u;
         case ORC_Q8_0:
             return (size_t) (ne0 / 32) * 34u;
+        case ORC_Q5_K:
+            return (size_t) (ne0 / 256) * 176u;
         default:
             return 0;
     }
@@ -148,6 +150,49 @@ static void dequantize_row_q8_0(const uint8_t * x, float * y, int64_t k) {
         const int8_t * qs = (const int8_t *) (blk + 2);
         for (int j = 0; j < 32; ++j) {
             y[b * 32 + j] = (float) qs[j] * d;
+        }
+    }
+}
+
+/* dequantize_row_q5_K with get_scale_min_k4 (upstream ggml's ggml-quants.c;
+ * the tables of the reference's Q5_K_MIXED packages,
+ * src/arch/qwen3-tts/catalog.cpp:165-192). A 176-byte super-block holds 256
+ * elements: f16 d, f16 dmin, scales[12], qh[32], qs[128]. Sub-block s
+ * (0..7, 32 elements each) has a 6-bit scale and min packed in scales -- for
+ * s < 4 the low six bits of scales[s] and scales[s + 4]; for s >= 4 the
+ * nibbles of scales[s + 4] topped with the high two bits of scales[s - 4]
+ * (scale) and scales[s] (min). Its element i takes the low (s even) or high
+ * (s odd) nibble of qs[32*(s/2) + i] and bit s of qh[i] as bit 4. The value
+ * is (d*sc)*q - dmin*m. */
+static void q5k_scale_min(const uint8_t * scales, int s, int * sc, int * m) {
+    if (s < 4) {
+        *sc = scales[s] & 63;
+        *m  = scales[s + 4] & 63;
+    } else {
+        *sc = (scales[s + 4] & 15) | ((scales[s - 4] >> 6) << 4);
+        *m  = (scales[s + 4] >> 4) | ((scales[s] >> 6) << 4);
+    }
+}
+
+static void dequantize_row_q5_k(const uint8_t * x, float * y, int64_t k) {
+    for (int64_t b = 0; b < k / 256; ++b) {
+        const uint8_t * blk = x + b * 176;
+        uint16_t        dh, mh;
+        memcpy(&dh, blk, 2);
+        memcpy(&mh, blk + 2, 2);
+        const float     d    = orc_fp16_to_fp32(dh);
+        const float     dmin = orc_fp16_to_fp32(mh);
+        const uint8_t * qh   = blk + 16;
+        const uint8_t * qs   = blk + 48;
+        for (int s = 0; s < 8; ++s) {
+            int sc, m;
+            q5k_scale_min(blk + 4, s, &sc, &m);
+            const float d1 = d * (float) sc;
+            const float m1 = dmin * (float) m;
+            for (int i = 0; i < 32; ++i) {
+                const int q = ((qs[32 * (s / 2) + i] >> (4 * (s & 1))) & 15) | (((qh[i] >> s) & 1) << 4);
+                y[b * 256 + 32 * s + i] = d1 * (float) q - m1;
+            }
         }
     }
 }
@@ -375,6 +420,8 @@ static void op_get_rows(const orc_node * n, int ith, int nth) {
         const uint8_t * row = (const uint8_t *) n->src0 + (size_t) id * rb;
         if (n->type0 == ORC_Q8_0) {
             dequantize_row_q8_0(row, y, ne0);
+        } else if (n->type0 == ORC_Q5_K) {
+            dequantize_row_q5_k(row, y, ne0);
         } else {
             for (int64_t i = 0; i < ne0; ++i) {
                 y[i] = to_f32(n->type0, row, i);

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-enum orc_type { ORC_F32 = 0, ORC_F16 = 1, ORC_Q8_0 = 8, ORC_I32 = 26, ORC_BF16 = 30 };
+enum orc_type { ORC_F32 = 0, ORC_F16 = 1, ORC_Q8_0 = 8, ORC_Q5_K = 13, ORC_I32 = 26, ORC_BF16 = 30 };
 
 enum orc_op {
     ORC_OP_ADD = 1,      /* dst = src0 + src1                       ggml_add            */

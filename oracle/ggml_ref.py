@@ -21,7 +21,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libggml_cpu_ref.so")
 
-F32, F16, Q8_0, I32, BF16 = 0, 1, 8, 26, 30
+F32, F16, Q8_0, Q5_K, I32, BF16 = 0, 1, 8, 13, 26, 30
 
 (OP_ADD, OP_MUL, OP_DIV, OP_RMS_NORM, OP_ROPE_NEOX, OP_SILU, OP_SIN, OP_SQR, OP_EXP, OP_LEAKY_RELU, OP_SCALE_BIAS,
  OP_GET_ROWS, OP_CAST_F32, OP_GLU_SWIGLU, OP_SOFT_MAX) = range(1, 16)
@@ -170,7 +170,7 @@ class Graph:
     def get_rows(self, table, type0, ne0, ids):
         """table: numpy array of raw rows (any dtype, C-contiguous, one row per
         leading index: (rows, row_elems) for F32/F16(bits)/BF16(bits), (rows,
-        row_bytes) uint8 for Q8_0); ids: (n,) int32 -> (n, ne0) f32."""
+        row_bytes) uint8 for Q8_0 and Q5_K); ids: (n,) int32 -> (n, ne0) f32."""
         table = np.ascontiguousarray(table)
         ids = np.ascontiguousarray(ids, dtype=np.int32)
         dst = np.empty((ids.size, ne0), dtype=np.float32)

@@ -126,6 +126,70 @@ __device__ __forceinline__ float q8_elem(const char * row, int e) {
     return static_cast<float>(q) * f16_bits_to_f32(dh);
 }
 
+// Q5_K, ggml's block_q5_K: 256 elements in 176 bytes -- f16 d at byte 0, f16
+// dmin at 2, scales[12] at 4, qh[32] at 16, qs[128] at 48. Element
+// e = 64j + 32h + i (j < 4, h < 2, i < 32) of a super-block has the 4-bit
+// quant (qs[32j + i] >> 4h) & 15, the fifth bit (qh[i] >> (2j + h)) & 1, and
+// the 6-bit scale and min of its sub-block s = 2j + h: for s < 4,
+// scales[s] & 63 and scales[s + 4] & 63; for s >= 4,
+// (scales[s + 4] & 15) | (scales[s - 4] >> 6) << 4 and
+// (scales[s + 4] >> 4) | (scales[s] >> 6) << 4 (ggml's get_scale_min_k4).
+// The value is (d*sc)*q - dmin*m. d*sc and dmin*m have at most 17
+// significant bits and (d*sc)*q at most 22, so every product is exact in f32
+// and the subtraction is the one rounding -- as in ggml-CPU's
+// dequantize_row_q5_K, whether or not its build fuses the multiply-add.
+//
+// In 32-bit words: w0 = d | dmin << 16, w1..w3 = scales[0..11]. Every byte
+// sub-block s needs sits at the same shift 8*(s & 3) of one of w1..w3.
+struct Q5KCoef {
+    float d1;  // d * sc
+    float m1;  // dmin * m
+};
+
+__device__ __forceinline__ Q5KCoef q5k_coef(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, int s) {
+    const int      sh  = 8 * (s & 3);
+    const uint32_t b1  = (w1 >> sh) & 0xffu;  // scales[s & 3]
+    const uint32_t b2  = (w2 >> sh) & 0xffu;  // scales[4 + (s & 3)]
+    const uint32_t b3  = (w3 >> sh) & 0xffu;  // scales[8 + (s & 3)]
+    const bool     hi  = s >= 4;
+    const uint32_t sc  = hi ? ((b3 & 15u) | ((b1 >> 6) << 4)) : (b1 & 63u);
+    const uint32_t m   = hi ? ((b3 >> 4) | ((b2 >> 6) << 4)) : (b2 & 63u);
+    return Q5KCoef{ f16_bits_to_f32(w0 & 0xffffu) * static_cast<float>(sc),
+                    f16_bits_to_f32(w0 >> 16) * static_cast<float>(m) };
+}
+
+// The 5-bit quant of byte k of a lane's qs and qh words, sub-block s (h = s & 1).
+__device__ __forceinline__ float q5k_quant(uint32_t qs, uint32_t qh, int k, int s) {
+    const uint32_t nib = (qs >> (8 * k + 4 * (s & 1))) & 15u;
+    const uint32_t hb  = (qh >> (8 * k + s)) & 1u;
+    return static_cast<float>(nib | (hb << 4));
+}
+
+__device__ __forceinline__ float q5k_value(const Q5KCoef & c, float q) {
+    return c.d1 * q - c.m1;
+}
+
+__device__ __forceinline__ uint32_t ld_u32(const char * p) {
+    return static_cast<uint32_t>(reinterpret_cast<const uint8_t *>(p)[0]) |
+           (static_cast<uint32_t>(reinterpret_cast<const uint8_t *>(p)[1]) << 8) |
+           (static_cast<uint32_t>(reinterpret_cast<const uint8_t *>(p)[2]) << 16) |
+           (static_cast<uint32_t>(reinterpret_cast<const uint8_t *>(p)[3]) << 24);
+}
+
+// One element of a Q5_K row at any alignment (the generic kernels).
+__device__ __forceinline__ float q5k_elem(const char * row, int e) {
+    const char * blk = row + static_cast<int64_t>(e / 256) * 176;
+    const int    r   = e % 256;
+    const int    j   = r / 64;
+    const int    h   = (r / 32) & 1;
+    const int    i   = r % 32;
+    const int    s   = 2 * j + h;
+    const Q5KCoef c  = q5k_coef(ld_u32(blk), ld_u32(blk + 4), ld_u32(blk + 8), ld_u32(blk + 12), s);
+    const uint32_t qs = reinterpret_cast<const uint8_t *>(blk + 48)[32 * j + i];
+    const uint32_t qh = reinterpret_cast<const uint8_t *>(blk + 16)[i];
+    return q5k_value(c, q5k_quant(qs, qh, 0, s));
+}
+
 template <int TYPE> __device__ __forceinline__ float elem(const char * row, int e) {
     if constexpr (TYPE == SHP_TYPE_F32) {
         return reinterpret_cast<const float *>(row)[e];
@@ -133,6 +197,8 @@ template <int TYPE> __device__ __forceinline__ float elem(const char * row, int 
         return bf16_bits_to_f32(reinterpret_cast<const uint16_t *>(row)[e]);
     } else if constexpr (TYPE == SHP_TYPE_F16) {
         return f16_bits_to_f32(reinterpret_cast<const uint16_t *>(row)[e]);
+    } else if constexpr (TYPE == SHP_TYPE_Q5_K) {
+        return q5k_elem(row, e);
     } else {
         return q8_elem(row, e);
     }
@@ -624,6 +690,76 @@ template <int NQ> __global__ __launch_bounds__(256) void k_get_rows_q8s(const Ga
     q8_row_store<NQ>(drow, l, o);
 }
 
+// ---------------------------------------------------------------------------
+// Q5_K rows (ne0 = 256 * super-blocks, rows 4-byte aligned): lane l owns
+// elements 4l..4l+3 of every super-block, so each float4 store instruction of
+// the wave writes one super-block's contiguous kilobyte. Those four elements
+// lie in sub-block s = l/8 (j = l/16, h = (l/8) & 1, i = 4(l%8)): their quant
+// bytes are the aligned dword qs[32j + i ..] and their fifth bits the aligned
+// dword qh[i ..], read with the super-block's first four dwords (d, dmin and
+// the packed scales; the same for every lane).
+// ---------------------------------------------------------------------------
+
+constexpr int kQ5KChunk = 4;  // super-blocks whose loads go out before the first decode
+
+struct Q5KLane {
+    int qh_dw;  // dword of qh within the super-block
+    int qs_dw;  // dword of qs within the super-block
+    int s;      // sub-block
+};
+
+__device__ __forceinline__ Q5KLane q5k_lane(int l) {
+    return Q5KLane{ 4 + (l % 8), 12 + 8 * (l / 16) + (l % 8), l / 8 };
+}
+
+struct Q5KWords {
+    uint32_t w[4];  // d | dmin, scales
+    uint32_t qh;
+    uint32_t qs;
+};
+
+__device__ __forceinline__ Q5KWords q5k_load(const uint32_t * blk, const Q5KLane & p) {
+    return Q5KWords{ { blk[0], blk[1], blk[2], blk[3] }, blk[p.qh_dw], blk[p.qs_dw] };
+}
+
+__device__ __forceinline__ f32x4 q5k_decode(const Q5KWords & v, const Q5KLane & p) {
+    const Q5KCoef c = q5k_coef(v.w[0], v.w[1], v.w[2], v.w[3], p.s);
+    return f32x4{ q5k_value(c, q5k_quant(v.qs, v.qh, 0, p.s)), q5k_value(c, q5k_quant(v.qs, v.qh, 1, p.s)),
+                  q5k_value(c, q5k_quant(v.qs, v.qh, 2, p.s)), q5k_value(c, q5k_quant(v.qs, v.qh, 3, p.s)) };
+}
+
+// get_rows: one wave per output row.
+__global__ __launch_bounds__(256) void k_get_rows_q5k(const GatherArgs a) {
+    gather_args_in_sgprs(a);
+    const int     l = static_cast<int>(threadIdx.x) % kWave;
+    const int64_t R = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    if (R >= a.total) {
+        return;
+    }
+    int32_t      id;
+    const char * srow;
+    float *      drow;
+    gather_coords(a, R, id, srow, drow);
+    const bool     ok  = id >= 0 && id < a.srows;
+    const int      nsb = a.ne0 / 256;
+    const Q5KLane  p   = q5k_lane(l);
+    f32x4 *        out = reinterpret_cast<f32x4 *>(drow);
+    for (int b0 = 0; b0 < nsb; b0 += kQ5KChunk) {
+        Q5KWords v[kQ5KChunk];
+#pragma unroll
+        for (int k = 0; k < kQ5KChunk; ++k) {
+            const int b = b0 + k < nsb ? b0 + k : b0;  // past the row: re-read one inside it
+            v[k]        = q5k_load(reinterpret_cast<const uint32_t *>((ok ? srow : a.src) + static_cast<int64_t>(b) * 176), p);
+        }
+#pragma unroll
+        for (int k = 0; k < kQ5KChunk; ++k) {
+            if (b0 + k < nsb) {
+                st_stream(out + 64 * (b0 + k) + l, ok ? q5k_decode(v[k], p) : splat4(__uint_as_float(kQNaN)));
+            }
+        }
+    }
+}
+
 // Any type / alignment: one wave per row, element by element.
 template <int TYPE> __global__ __launch_bounds__(256) void k_get_rows_generic(const GatherArgs a) {
     const int     lane = threadIdx.x % kWave;
@@ -766,7 +902,10 @@ template <int TYPE> shp_status_t launch_get_rows(const GatherArgs & a, bool vec,
         return SHP_OK;
     }
     if (vec) {
-        if constexpr (TYPE == SHP_TYPE_Q8_0) {
+        if constexpr (TYPE == SHP_TYPE_Q5_K) {
+            hipLaunchKernelGGL(k_get_rows_q5k, dim3(static_cast<unsigned>((a.total + 3) / 4)), dim3(256), 0, stream, a);
+            return launch_status();
+        } else if constexpr (TYPE == SHP_TYPE_Q8_0) {
             if (a.staged) {
                 const int64_t blocks = (a.total + kQ8StageWaves - 1) / kQ8StageWaves;
                 switch (a.ne0) {
@@ -862,9 +1001,81 @@ template <int NS> void launch_q8w(const GatherSumArgs & a, hipStream_t stream) {
     }
 }
 
+// Q5_K gather->sum: one wave per frame, lane l owning elements 4l..4l+3 of
+// each of the row's super-blocks (as k_get_rows_q5k). Groups go in chunks:
+// the chunk's ids, then every group's words for every super-block, are
+// requested before the first decode; each decoded row is added to the sum in
+// group order, from -0.0f (the identity of f32 addition), so the result is
+// the node run's ((row_0 + row_1) + row_2) + ... bit for bit.
+constexpr int kQ5KSumGroups = 4;
+
+template <int NSB> __global__ __launch_bounds__(256) void k_get_rows_sum_q5k(const GatherSumArgs a) {
+    args_in_sgprs(a.frames, a.ids, a.ids_gstride, a.ngroups);
+    const int     l = static_cast<int>(threadIdx.x) % kWave;
+    const int64_t f = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    if (f >= a.frames) {
+        return;
+    }
+    const Q5KLane p = q5k_lane(l);
+    f32x4         acc[NSB];
+#pragma unroll
+    for (int b = 0; b < NSB; ++b) {
+        acc[b] = splat4(-0.0f);
+    }
+    uint32_t bad = 0;
+    for (int g0 = 0; g0 < a.ngroups; g0 += kQ5KSumGroups) {
+        Q5KWords v[kQ5KSumGroups][NSB];
+#pragma unroll
+        for (int j = 0; j < kQ5KSumGroups; ++j) {
+            const int      g  = g0 + j < a.ngroups ? g0 + j : g0;  // past the last group: re-read one inside
+            const int32_t  id = *reinterpret_cast<const int32_t *>(reinterpret_cast<const char *>(a.ids) +
+                                                                   g * a.ids_gstride + f * 4);
+            const uint32_t ok = static_cast<uint32_t>(id) < static_cast<uint64_t>(a.trows[g]) ? 1u : 0u;
+            bad |= (ok ^ 1u) & (g0 + j < a.ngroups ? 1u : 0u);
+            const char * row = a.tab[g] + (ok ? static_cast<int64_t>(id) : 0) * a.tnb1[g];
+#pragma unroll
+            for (int b = 0; b < NSB; ++b) {
+                v[j][b] = q5k_load(reinterpret_cast<const uint32_t *>(row + b * 176), p);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kQ5KSumGroups; ++j) {
+            if (g0 + j < a.ngroups) {
+#pragma unroll
+                for (int b = 0; b < NSB; ++b) {
+                    const f32x4 y = q5k_decode(v[j][b], p);
+                    acc[b]        = f32x4{ acc[b].x + y.x, acc[b].y + y.y, acc[b].z + y.z, acc[b].w + y.w };
+                }
+            }
+        }
+    }
+    f32x4 * out = reinterpret_cast<f32x4 *>(reinterpret_cast<char *>(a.dst) + f * a.dnb1);
+#pragma unroll
+    for (int b = 0; b < NSB; ++b) {
+        st_stream(out + 64 * b + l, bad != 0 ? splat4(__uint_as_float(kQNaN)) : acc[b]);
+    }
+}
+
 template <int TYPE> shp_status_t launch_get_rows_sum(const GatherSumArgs & a, bool vec, hipStream_t stream) {
     if (vec) {
-        if constexpr (TYPE == SHP_TYPE_Q8_0) {
+        if constexpr (TYPE == SHP_TYPE_Q5_K) {
+            const dim3 grid(static_cast<unsigned>((a.frames + 3) / 4));
+            switch (a.ne0 / 256) {
+                case 1:
+                    hipLaunchKernelGGL(k_get_rows_sum_q5k<1>, grid, dim3(256), 0, stream, a);
+                    break;
+                case 2:
+                    hipLaunchKernelGGL(k_get_rows_sum_q5k<2>, grid, dim3(256), 0, stream, a);
+                    break;
+                case 4:
+                    hipLaunchKernelGGL(k_get_rows_sum_q5k<4>, grid, dim3(256), 0, stream, a);
+                    break;
+                default:
+                    hipLaunchKernelGGL(k_get_rows_sum_q5k<8>, grid, dim3(256), 0, stream, a);
+                    break;
+            }
+            return launch_status();
+        } else if constexpr (TYPE == SHP_TYPE_Q8_0) {
             if (q8_staged_width(a.ne0)) {
                 const int ns = a.ne0 / static_cast<int>(kQ8SlabElems);
                 if (ns == 1) {
@@ -922,7 +1133,12 @@ template <int TYPE> shp_status_t launch_get_rows_sum(const GatherSumArgs & a, bo
 
 
 bool gather_type_ok(int32_t t) {
-    return t == SHP_TYPE_F32 || t == SHP_TYPE_F16 || t == SHP_TYPE_BF16 || t == SHP_TYPE_Q8_0;
+    return t == SHP_TYPE_F32 || t == SHP_TYPE_F16 || t == SHP_TYPE_BF16 || t == SHP_TYPE_Q8_0 || t == SHP_TYPE_Q5_K;
+}
+
+// Q5_K widths of the vector gather->sum (super-blocks held per lane).
+bool q5k_sum_width(int64_t ne0) {
+    return ne0 == 256 || ne0 == 512 || ne0 == 1024 || ne0 == 2048;
 }
 
 }  // namespace
@@ -983,6 +1199,8 @@ extern "C" shp_status_t shp_get_rows(const shp_tensor * src,
         case SHP_TYPE_BF16:
             return launch_get_rows<SHP_TYPE_BF16>(a, dst16 && rows_aligned(*src, 16) && src->ne[0] % 4 == 0 &&
                                                          src->ne[0] <= 8192, st);
+        case SHP_TYPE_Q5_K:
+            return launch_get_rows<SHP_TYPE_Q5_K>(a, dst16 && rows_aligned(*src, 4), st);
         default:
             return launch_get_rows<SHP_TYPE_Q8_0>(a, dst16 && rows_aligned(*src, 4) && src->ne[0] % 64 == 0, st);
     }
@@ -1062,7 +1280,7 @@ extern "C" shp_status_t shp_get_rows_sum(const shp_tensor * tables,
         a.tab[g]   = static_cast<const char *>(t.data);
         a.tnb1[g]  = static_cast<int64_t>(t.nb[1]);
         a.trows[g] = t.ne[1];
-        vec        = vec && rows_aligned(t, type == SHP_TYPE_Q8_0 ? 4 : 16);
+        vec        = vec && rows_aligned(t, block_type(type) ? 4 : 16);
     }
     // Q8_0 half-block path: one row size for every table, 32-bit offsets.
     bool q8h = type == SHP_TYPE_Q8_0;
@@ -1111,6 +1329,8 @@ extern "C" shp_status_t shp_get_rows_sum(const shp_tensor * tables,
             return launch_get_rows_sum<SHP_TYPE_F16>(a, vec && ne0 % 4 == 0 && ne0 <= kSumVecMaxNe0, st);
         case SHP_TYPE_BF16:
             return launch_get_rows_sum<SHP_TYPE_BF16>(a, vec && ne0 % 4 == 0 && ne0 <= kSumVecMaxNe0, st);
+        case SHP_TYPE_Q5_K:
+            return launch_get_rows_sum<SHP_TYPE_Q5_K>(a, vec && q5k_sum_width(ne0), st);
         default:
             return launch_get_rows_sum<SHP_TYPE_Q8_0>(a, vec && q8h, st);
     }

@@ -1,5 +1,5 @@
 // GGUF reader and device loader: the on-disk format of the model packages whose
-// BF16 / F16 / Q8_0 lookup tables feed shp_get_rows and shp_get_rows_sum
+// BF16 / F16 / Q8_0 / Q5_K lookup tables feed shp_get_rows and shp_get_rows_sum
 // (src/arch/qwen3-tts/catalog.cpp:77-104 resolves them by name, type and shape;
 // tools/synthesize-quantize/policy.cpp:49-98 decides their types).
 //
@@ -386,7 +386,8 @@ void describe(const TensorInfo & ti, shp_tensor * out) {
 }
 
 bool loadable_type(uint32_t t) {
-    return t == SHP_TYPE_F32 || t == SHP_TYPE_F16 || t == SHP_TYPE_BF16 || t == SHP_TYPE_Q8_0 || t == SHP_TYPE_I32;
+    return t == SHP_TYPE_F32 || t == SHP_TYPE_F16 || t == SHP_TYPE_BF16 || t == SHP_TYPE_Q8_0 || t == SHP_TYPE_Q5_K ||
+           t == SHP_TYPE_I32;
 }
 
 // Reads n bytes at file offset off into dst; false on a short read. Large
@@ -790,8 +791,7 @@ extern "C" shp_status_t shp_table_type_for_profile(const char * profile, int32_t
     } else if (p == "Q8_MIXED") {
         *type = SHP_TYPE_Q8_0;
     } else if (p == "Q5_K_MIXED") {
-        *type = 13;  // GGML_TYPE_Q5_K: a k-quant the gathers do not take
-        return SHP_ERR_UNSUPPORTED;
+        *type = SHP_TYPE_Q5_K;
     } else {
         return SHP_ERR_INVALID_ARG;
     }

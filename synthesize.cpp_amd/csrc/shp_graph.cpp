@@ -104,7 +104,7 @@ bool node_form_ok(const shp_node & n) {
             const auto & t   = n.src[0];
             const auto & ids = n.src[1];
             const bool   tt  = t.type == SHP_TYPE_F32 || t.type == SHP_TYPE_F16 || t.type == SHP_TYPE_BF16 ||
-                            t.type == SHP_TYPE_Q8_0;
+                            t.type == SHP_TYPE_Q8_0 || t.type == SHP_TYPE_Q5_K;
             return well_formed(&t) && tt && well_formed(&ids) && ids.type == SHP_TYPE_I32 && f32_of(n.dst) &&
                    n.dst.ne[0] == t.ne[0] && n.dst.ne[1] == ids.ne[0] && n.dst.ne[2] == ids.ne[1] &&
                    n.dst.ne[3] == ids.ne[2] && ids.ne[3] == 1;

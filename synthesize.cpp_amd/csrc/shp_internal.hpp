@@ -284,10 +284,27 @@ inline size_t type_size(int32_t type) {
     }
 }
 
-// Bytes of one ne0-long row; Q8_0 rows are ne0/32 blocks of 34 bytes.
+// ggml's block types: elements and bytes per block (Q8_0: {f16 d; int8
+// qs[32]}; Q5_K: {f16 d, dmin; u8 scales[12], qh[32], qs[128]}).
+constexpr int64_t kQ8Elems = 32, kQ5KElems = 256;
+constexpr size_t  kQ8Bytes = 34, kQ5KBytes = 176;
+
+inline bool block_type(int32_t type) {
+    return type == SHP_TYPE_Q8_0 || type == SHP_TYPE_Q5_K;
+}
+
+inline int64_t block_elems(int32_t type) {
+    return type == SHP_TYPE_Q8_0 ? kQ8Elems : kQ5KElems;
+}
+
+inline size_t block_bytes(int32_t type) {
+    return type == SHP_TYPE_Q8_0 ? kQ8Bytes : kQ5KBytes;
+}
+
+// Bytes of one ne0-long row; block types hold ne0/elems blocks.
 inline size_t row_bytes(int32_t type, int64_t ne0) {
-    if (type == SHP_TYPE_Q8_0) {
-        return static_cast<size_t>(ne0 / 32) * 34u;
+    if (block_type(type)) {
+        return static_cast<size_t>(ne0 / block_elems(type)) * block_bytes(type);
     }
     return static_cast<size_t>(ne0) * type_size(type);
 }
@@ -316,8 +333,8 @@ inline bool well_formed(const shp_tensor * t) {
             return false;
         }
     }
-    if (t->type == SHP_TYPE_Q8_0) {
-        return t->ne[0] % 32 == 0 && t->nb[0] == 34u;
+    if (block_type(t->type)) {
+        return t->ne[0] % block_elems(t->type) == 0 && t->nb[0] == block_bytes(t->type);
     }
     const size_t ts = type_size(t->type);
     return ts != 0 && t->nb[0] == ts;
@@ -366,7 +383,7 @@ inline bool rows_aligned(const shp_tensor & t, size_t align) {
 // Fully contiguous (ggml_is_contiguous) in the element-size sense.
 inline bool contiguous(const shp_tensor & t) {
     size_t expect = t.nb[0] * static_cast<size_t>(t.ne[0]);
-    if (t.type == SHP_TYPE_Q8_0) {
+    if (block_type(t.type)) {
         expect = row_bytes(t.type, t.ne[0]);
     }
     for (int d = 1; d < 4; ++d) {

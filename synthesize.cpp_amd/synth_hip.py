@@ -20,9 +20,10 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("SHP_LIB") or os.path.join(HERE, "libsynth_hip.so")
 
 OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_BACKEND = 0, 1, 2, 17
-TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_I32, TYPE_BF16 = 0, 1, 8, 26, 30
+TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q5_K, TYPE_I32, TYPE_BF16 = 0, 1, 8, 13, 26, 30
 ROPE_TYPE_NEOX = 2
 Q8_0_BLOCK_BYTES, Q8_0_BLOCK_ELEMS = 34, 32
+Q5_K_BLOCK_BYTES, Q5_K_BLOCK_ELEMS = 176, 256
 
 
 class ShpTensor(ctypes.Structure):
@@ -137,18 +138,29 @@ def abi_version():
 # descriptors
 # ---------------------------------------------------------------------------
 
-class Q8Tensor:
-    """A Q8_0 tensor held as raw blocks: `data` is a uint8 torch tensor of shape
-    (..., rows, ne0/32*34); ne0 is the logical row length."""
+class BlockTensor:
+    """A block-quantized tensor held as raw blocks: `data` is a uint8 torch
+    tensor of shape (..., rows, ne0/ELEMS*BYTES); ne0 is the logical row length."""
+    TYPE = ELEMS = BYTES = None
 
     def __init__(self, data, ne0):
-        assert ne0 % Q8_0_BLOCK_ELEMS == 0
-        assert data.shape[-1] == ne0 // Q8_0_BLOCK_ELEMS * Q8_0_BLOCK_BYTES
+        assert ne0 % self.ELEMS == 0
+        assert data.shape[-1] == ne0 // self.ELEMS * self.BYTES
         self.data, self.ne0 = data, ne0
 
     @property
     def rows(self):
         return self.data.shape[-2]
+
+
+class Q8Tensor(BlockTensor):
+    """Q8_0: 32-element blocks {f16 d; int8 qs[32]}."""
+    TYPE, ELEMS, BYTES = TYPE_Q8_0, Q8_0_BLOCK_ELEMS, Q8_0_BLOCK_BYTES
+
+
+class Q5KTensor(BlockTensor):
+    """Q5_K: 256-element super-blocks of 176 bytes."""
+    TYPE, ELEMS, BYTES = TYPE_Q5_K, Q5_K_BLOCK_ELEMS, Q5_K_BLOCK_BYTES
 
 
 def _torch_type(t):
@@ -158,17 +170,17 @@ def _torch_type(t):
 
 
 def desc(t):
-    """shp_tensor for a torch tensor (or Q8Tensor); None stays None."""
+    """shp_tensor for a torch tensor (or BlockTensor); None stays None."""
     if t is None:
         return None
     d = ShpTensor()
-    if isinstance(t, Q8Tensor):
+    if isinstance(t, BlockTensor):
         raw = t.data
         shape = list(raw.shape[::-1])
         strides = list(raw.stride()[::-1])
-        d.type = TYPE_Q8_0
+        d.type = t.TYPE
         shape[0] = t.ne0
-        strides[0] = Q8_0_BLOCK_BYTES
+        strides[0] = t.BYTES
         item = 1
     else:
         shape = list(t.shape[::-1]) or [1]
@@ -214,10 +226,10 @@ def _empty_like_f32(shape, device):
 # ---------------------------------------------------------------------------
 
 def get_rows(src, ids, out=None):
-    """ggml_get_rows(src, ids) -> f32. src (rows, ne0) torch F32/F16/BF16 or Q8Tensor;
+    """ggml_get_rows(src, ids) -> f32. src (rows, ne0) torch F32/F16/BF16, Q8Tensor or Q5KTensor;
     ids int32 (n,). Batched forms follow ggml's [ne0, rows, ne2, ne3] x [n, ne2, ne3]."""
-    raw = src.data if isinstance(src, Q8Tensor) else src
-    ne0 = src.ne0 if isinstance(src, Q8Tensor) else src.shape[-1]
+    raw = src.data if isinstance(src, BlockTensor) else src
+    ne0 = src.ne0 if isinstance(src, BlockTensor) else src.shape[-1]
     if out is None:
         out = _empty_like_f32(tuple(ids.shape) + (ne0,), raw.device)
     _check(load().shp_get_rows(_ref(desc(src)), _ref(desc(ids)), _ref(desc(out)), _stream()), "get_rows")
@@ -230,8 +242,8 @@ def get_rows_sum(tables, codes, out=None):
     n = len(tables)
     arr = (ShpTensor * n)(*[desc(t) for t in tables])
     first = tables[0]
-    ne0 = first.ne0 if isinstance(first, Q8Tensor) else first.shape[-1]
-    raw = first.data if isinstance(first, Q8Tensor) else first
+    ne0 = first.ne0 if isinstance(first, BlockTensor) else first.shape[-1]
+    raw = first.data if isinstance(first, BlockTensor) else first
     if out is None:
         out = _empty_like_f32((codes.shape[-1], ne0), raw.device)
     _check(load().shp_get_rows_sum(arr, n, _ref(desc(codes)), _ref(desc(out)), _stream()), "get_rows_sum")
@@ -480,7 +492,7 @@ class ShpGraphRun(ctypes.Structure):
 
 
 class GVal:
-    """A tensor of a Graph: `t` (torch tensor or Q8Tensor) and the node that
+    """A tensor of a Graph: `t` (torch tensor or BlockTensor) and the node that
     computes it (None for a leaf: weights, inputs, outputs of other graphs)."""
 
     def __init__(self, t, node=None):
@@ -527,7 +539,7 @@ class Graph:
     def _like(self, x, shape=None):
         import torch
         t = self._t(x)
-        raw = t.data if isinstance(t, Q8Tensor) else t
+        raw = t.data if isinstance(t, BlockTensor) else t
         return torch.empty(tuple(t.shape) if shape is None else shape, dtype=torch.float32, device=raw.device)
 
     # binary and unary nodes -------------------------------------------------
@@ -573,7 +585,7 @@ class Graph:
 
     def get_rows(self, table, ids):
         t = self._t(table)
-        ne0 = t.ne0 if isinstance(t, Q8Tensor) else t.shape[-1]
+        ne0 = t.ne0 if isinstance(t, BlockTensor) else t.shape[-1]
         return self._op(NODE_GET_ROWS, self._like(ids, tuple(self._t(ids).shape) + (ne0,)), [table, ids])
 
     def cast(self, x):
@@ -671,7 +683,7 @@ class Graph:
 class GgufFile:
     """A GGUF package opened by libsynth_hip's reader. info() and the metadata
     getters run host code only; load() streams a tensor into a new device
-    buffer and returns it as a torch tensor (or Q8Tensor) the gathers take."""
+    buffer and returns it as a torch tensor (or BlockTensor) the gathers take."""
 
     def __init__(self, path):
         self._h = ctypes.c_void_p()
@@ -748,22 +760,23 @@ class GgufFile:
 
 
 def _typed_view(raw, desc):
-    """A loaded tensor's device bytes as the torch tensor (or Q8Tensor) its
+    """A loaded tensor's device bytes as the torch tensor (or BlockTensor) its
     descriptor names."""
     import torch
     ne = [int(desc.ne[k]) for k in range(4)]
     nd = max([k + 1 for k in range(4) if ne[k] != 1] or [1])
-    if desc.type == TYPE_Q8_0:
-        rows = ne[1] * ne[2] * ne[3]
-        return Q8Tensor(raw.view(rows, ne[0] // Q8_0_BLOCK_ELEMS * Q8_0_BLOCK_BYTES), ne[0])
+    for cls in (Q8Tensor, Q5KTensor):
+        if desc.type == cls.TYPE:
+            rows = ne[1] * ne[2] * ne[3]
+            return cls(raw.view(rows, ne[0] // cls.ELEMS * cls.BYTES), ne[0])
     dt = {TYPE_F32: torch.float32, TYPE_F16: torch.float16, TYPE_BF16: torch.bfloat16,
           TYPE_I32: torch.int32}[desc.type]
     return raw.view(dt).view(tuple(reversed(ne[:nd])))
 
 
 def table_type_for_profile(profile):
-    """The table type the catalog requires under a quantization profile (raises
-    ShpError(ERR_UNSUPPORTED) for a k-quant profile)."""
+    """The table type the catalog requires under a quantization profile
+    (ShpError(ERR_INVALID_ARG) for an unknown profile)."""
     t = ctypes.c_int32()
     _check(load().shp_table_type_for_profile(profile.encode(), ctypes.byref(t)), "table_type_for_profile")
     return int(t.value)

@@ -58,11 +58,13 @@ def _tables(rng):
     import formats as F
     bf = F.f32_to_bf16_bits(rng.standard_normal((100, 2048)) * 0.02)
     q8 = F.q8_0_synthetic(rng, 50, 1024)
+    q5 = F.q5_k_synthetic(rng, 20, 1024)
     f16 = F.f32_to_f16_bits(rng.standard_normal((3, 5, 64)))
     f32 = rng.standard_normal(7).astype(np.float32)
     i32 = np.arange(12, dtype=np.int32).reshape(3, 4)
     return [("talker.model.text_embedding.weight", G.GGML_BF16, [2048, 100], bf.tobytes()),
             ("talker.code_predictor.model.codec_embedding.0.weight", G.GGML_Q8_0, [1024, 50], q8.tobytes()),
+            ("talker.code_predictor.model.codec_embedding.1.weight", G.GGML_Q5_K, [1024, 20], q5.tobytes()),
             ("conv.weight", G.GGML_F16, [64, 5, 3], f16.tobytes()),
             ("bias", G.GGML_F32, [7], f32.tobytes()),
             ("ids", G.GGML_I32, [4, 3], i32.tobytes())]
@@ -224,11 +226,11 @@ def test_load_rejects_without_touching_the_device(tmp_path):
     """Argument checks of shp_gguf_load_tensor happen before any HIP call."""
     import ctypes
     p = tmp_path / "k.gguf"
-    G.write(p, [], [("q", G.GGML_Q5_K, [256, 2], bytes(352)), ("t", G.GGML_F32, [8], bytes(32))])
+    G.write(p, [], [("q", 12, [256, 2], bytes(288)), ("t", G.GGML_F32, [8], bytes(32))])  # Q4_K: not loadable
     L = S.load()
     with S.GgufFile(p) as f:
         d = S.ShpTensor()
-        assert f.info("q")[0].type == 13
+        assert f.info("q")[0].type == 12
         fake = ctypes.c_void_p(0x10000)
         assert L.shp_gguf_load_tensor(f._h, b"q", fake, 1 << 20, ctypes.byref(d), None) == S.ERR_UNSUPPORTED
         assert L.shp_gguf_load_tensor(f._h, b"t", fake, 31, ctypes.byref(d), None) == S.ERR_INVALID_ARG
@@ -257,9 +259,7 @@ def test_table_type_for_profile():
     assert S.table_type_for_profile("BF16") == S.TYPE_BF16
     assert S.table_type_for_profile("F16") == S.TYPE_F16
     assert S.table_type_for_profile("Q8_MIXED") == S.TYPE_Q8_0
-    with pytest.raises(S.ShpError) as e:
-        S.table_type_for_profile("Q5_K_MIXED")
-    assert e.value.status == S.ERR_UNSUPPORTED
+    assert S.table_type_for_profile("Q5_K_MIXED") == S.TYPE_Q5_K
     with pytest.raises(S.ShpError) as e:
         S.table_type_for_profile("Q4_K")
     assert e.value.status == S.ERR_INVALID_ARG

@@ -1,0 +1,122 @@
+"""GPU parity of the Q5_K gathers (shp_get_rows and shp_get_rows_sum over
+ggml block_q5_K tables, the talker's embedding tables under the reference's
+Q5_K_MIXED profile, src/arch/qwen3-tts/catalog.cpp:165-192), through the C
+ABI, bit for bit against the oracle's dequantize_row_q5_K restatement (itself
+pinned by the hand-assembled block and the exact formula of
+tests/test_q5k_format.py). Every value is one rounding of exact products, so
+there is no tolerance: raw 32-bit patterns are compared."""
+import numpy as np
+import pytest
+
+import formats as F
+import ggml_ref as R
+from test_gpu_parity import _np, _t, assert_bitexact
+from test_q5k_format import hand_block, hand_values
+
+pytestmark = pytest.mark.gpu
+SEED = 20260728
+
+
+def _table(gpu, raw, ne0):
+    return gpu.Q5KTensor(_t(gpu, raw), ne0)
+
+
+@pytest.mark.parametrize("ne0,rows,n", [(256, 50, 77), (512, 30, 64), (768, 20, 40), (1024, 2048, 4096),
+                                        (2048, 300, 512), (4096, 9, 33)])
+def test_get_rows_q5k_bitexact(gpu, ne0, rows, n):
+    """Widths of 1..16 super-blocks (768: three, a chunk left part-full);
+    (1024, 2048, 4096) is a codec table of configs[2]'s shape."""
+    rng = np.random.default_rng(SEED + ne0 + rows)
+    raw = F.q5_k_synthetic(rng, rows, ne0)
+    ids = rng.integers(0, rows, n).astype(np.int32)
+    ids[:2] = [0, rows - 1]
+    ref = R.run(lambda g: g.get_rows(raw, R.Q5_K, ne0, ids))
+    got = _np(gpu.get_rows(_table(gpu, raw, ne0), _t(gpu, ids)))
+    assert_bitexact(got, ref)
+    assert_bitexact(got, F.q5_k_values(*F.q5_k_fields(np.random.default_rng(SEED + ne0 + rows), rows, ne0))[ids])
+
+
+def test_get_rows_q5k_hand_block_and_bad_ids(gpu):
+    raw = np.frombuffer(hand_block() * 3, np.uint8).reshape(3, 176).copy()
+    ids = np.array([2, 0, -1, 3, 1, 1 << 30], np.int32)
+    got = _np(gpu.get_rows(_table(gpu, raw, 256), _t(gpu, ids)))
+    for r in (0, 1, 4):
+        assert_bitexact(got[r], hand_values())
+    for r in (2, 3, 5):  # out of range: a quiet-NaN row, nothing read
+        assert np.isnan(got[r]).all()
+
+
+def test_get_rows_q5k_special_scales(gpu):
+    """d and dmin over -0, +0, f16 subnormals, the largest f16 and ordinary
+    values (no inf or NaN scale: inf*0 makes a NaN whose sign differs between
+    CPU and GPU arithmetic)."""
+    rng = np.random.default_rng(SEED + 3)
+    rows, ne0 = 64, 1024
+    d, dmin, sc, m, q = F.q5_k_fields(rng, rows, ne0)
+    specials = np.array([0x8000, 0x0000, 0x0001, 0x03FF, 0x7BFF, 0x3C00, 0xBC00, 0x1400], np.uint16)
+    d[:] = specials[rng.integers(0, len(specials), d.shape)]
+    dmin[:] = specials[rng.integers(0, len(specials), dmin.shape)]
+    sc[0], m[0], q[0] = 63, 63, 31
+    sc[1], m[1], q[1] = 0, 0, 0
+    raw = F.q5_k_pack(d, dmin, sc, m, q)
+    ids = np.arange(rows, dtype=np.int32)
+    ref = R.run(lambda g: g.get_rows(raw, R.Q5_K, ne0, ids))
+    assert_bitexact(_np(gpu.get_rows(_table(gpu, raw, ne0), _t(gpu, ids))), ref)
+
+
+def test_get_rows_q5k_batched_and_misaligned(gpu):
+    """ggml's batched form (table [ne0, rows, 2], ids [n, 2]); a table at a
+    2-byte offset and an output at a 4-byte offset take the element-wise
+    kernel, with the same bits."""
+    import torch
+    rng = np.random.default_rng(SEED + 9)
+    ne0, rows = 512, 25
+    raw = np.stack([F.q5_k_synthetic(rng, rows, ne0) for _ in range(2)])
+    ids = rng.integers(0, rows, (2, 31)).astype(np.int32)
+    ref = np.stack([R.run(lambda g, b=b: g.get_rows(raw[b], R.Q5_K, ne0, ids[b])) for b in range(2)])
+    got = _np(gpu.get_rows(gpu.Q5KTensor(_t(gpu, raw), ne0), _t(gpu, ids)))
+    assert_bitexact(got, ref)
+    flat = raw[0]
+    buf = torch.zeros(flat.size + 2, dtype=torch.uint8, device="cuda")
+    buf[2:].copy_(torch.from_numpy(flat.reshape(-1)).cuda())
+    view = buf[2:].view(rows, flat.shape[1])
+    assert view.data_ptr() % 4 == 2
+    out_buf = torch.empty(31 * ne0 + 1, dtype=torch.float32, device="cuda")
+    out = out_buf[1:].view(31, ne0)
+    gpu.get_rows(gpu.Q5KTensor(view, ne0), _t(gpu, ids[0]), out=out)
+    assert_bitexact(_np(out), ref[0])
+
+
+@pytest.mark.parametrize("ne0,groups,frames", [(1024, 16, 4096), (1024, 15, 64), (256, 1, 33), (512, 3, 100),
+                                               (2048, 9, 50), (4096, 4, 20)])
+def test_get_rows_sum_q5k_bitexact(gpu, ne0, groups, frames):
+    """sum_code_embeddings over Q5_K tables (code-predictor.cpp:82-107): the
+    ordered f32 sum of the dequantized rows, bit for bit. (1024, 16, 4096) is
+    configs[2]'s shape with Q5_K codebooks; 4096-wide rows take the
+    element-wise kernel."""
+    rng = np.random.default_rng(SEED + 17 + ne0 + groups)
+    rows = 2048 if frames >= 4096 else 60
+    tabs = [F.q5_k_synthetic(rng, rows, ne0) for _ in range(groups)]
+    codes = rng.integers(0, rows, (groups, frames)).astype(np.int32)
+    ref = R.run(lambda g: R.sum_code_embeddings(g, tabs, R.Q5_K, ne0, codes))
+    got = _np(gpu.get_rows_sum([_table(gpu, t, ne0) for t in tabs], _t(gpu, codes)))
+    assert_bitexact(got, ref)
+
+
+def test_get_rows_sum_q5k_order_and_bad_id(gpu):
+    """The sum is order-dependent in f32 (it is one chain of adds), and an id
+    out of range in any group makes the frame's row NaN."""
+    rng = np.random.default_rng(SEED + 29)
+    ne0, rows, groups = 1024, 30, 5
+    tabs = [F.q5_k_synthetic(rng, rows, ne0, 1e-2, 5e-2) for _ in range(groups)]
+    codes = rng.integers(0, rows, (groups, 40)).astype(np.int32)
+    codes[3, 7] = rows
+    codes[0, 9] = -5
+    dev = [_table(gpu, t, ne0) for t in tabs]
+    got = _np(gpu.get_rows_sum(dev, _t(gpu, codes)))
+    assert np.isnan(got[7]).all() and np.isnan(got[9]).all()
+    ok = [f for f in range(40) if f not in (7, 9)]
+    ref = R.run(lambda g: R.sum_code_embeddings(g, tabs, R.Q5_K, ne0, np.where(codes < 0, 0, np.minimum(codes, rows - 1))))
+    assert_bitexact(got[ok], ref[ok])
+    rev = _np(gpu.get_rows_sum(dev[::-1], _t(gpu, np.ascontiguousarray(codes[::-1]))))
+    assert not np.array_equal(rev[ok].view(np.uint32), got[ok].view(np.uint32))
