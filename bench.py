@@ -22,7 +22,8 @@ The same line carries, each op timed alone from a HIP graph over rotating
 input sets whose total exceeds 512 MB (cold cache):
   - every op of the configs[4] step, and its roofline (the dominant kernel);
   - the 16-codebook Q8_0 gather->sum and the plain Q8_0 get_rows
-    (logical bytes, every looked-up row per lookup; compulsory bytes beside);
+    (logical bytes, every looked-up row per lookup; compulsory bytes beside),
+    and the same two over Q5_K tables (the Q5_K_MIXED profile's);
   - configs[3]: Snake, SnakeBeta, add->leaky-ReLU and add->leaky-ReLU with the
     sum carried, on [512,8192], [256,32768] and [128,131072];
   - the decode step's non-GEMM work per talker layer (28-layer
@@ -342,20 +343,26 @@ def step_op_rows(R, S, torch, cfg, T, H, F_, seed):
 # Q8_0 gather->sum and get_rows; configs[3]: vocoder activations
 # ---------------------------------------------------------------------------
 
-def q8_rows(R, S, torch, cfg, seed):
+def q8_rows(R, S, torch, cfg, seed, kind="q8_0"):
+    """configs[2]'s gathers; kind "q5_k": the same shapes over Q5_K tables (the
+    Q5_K_MIXED profile's)."""
     import numpy as np
     import formats as F
     g, randn, empty, bf16 = gen(torch, seed)
     rng = np.random.default_rng(seed)
-    row, f32 = 1024 // 32 * 34, 4
+    f32 = 4
+    if kind == "q5_k":
+        row, synth, wrap = 1024 // 256 * 176, F.q5_k_synthetic, S.Q5KTensor
+    else:
+        row, synth, wrap = 1024 // 32 * 34, F.q8_0_synthetic, S.Q8Tensor
     # Each input set has its own tables, so the rotation exceeds the Infinity
     # Cache and every launch fetches its rows from HBM.
     keep = []
 
     def tables(n):
-        raw = torch.from_numpy(np.stack([F.q8_0_synthetic(rng, 2048, 1024) for _ in range(n)])).cuda()
+        raw = torch.from_numpy(np.stack([synth(rng, 2048, 1024) for _ in range(n)])).cuda()
         keep.append(raw)
-        return [S.Q8Tensor(raw[t], 1024) for t in range(n)]
+        return [wrap(raw[t], 1024) for t in range(n)]
 
     def make_sum():
         tabs = tables(16)
@@ -374,8 +381,8 @@ def q8_rows(R, S, torch, cfg, seed):
         return int(touched * row) + 4096 * (groups * 4 + 1024 * f32)
 
     out = []
-    for name, groups, make in (("get_rows_sum q8_0 16x[1024,2048] x4096", 16, make_sum),
-                               ("get_rows q8_0 [1024,2048] x4096", 1, make_q8)):
+    for name, groups, make in (("get_rows_sum %s 16x[1024,2048] x4096" % kind, 16, make_sum),
+                               ("get_rows %s [1024,2048] x4096" % kind, 1, make_q8)):
         logical = 4096 * (groups * (row + 4) + 1024 * f32)
         cb = compulsory(groups)
         out.append(R.run(cfg, name, logical, make, extra={
@@ -682,6 +689,7 @@ def suite(args, S, torch):
 
     if on("configs2"):
         q8_rows(R, S, torch, "configs[2]", SEED + 3)
+        q8_rows(R, S, torch, "configs[2]", SEED + 6, kind="q5_k")
 
     if on("configs3"):
         vocoder_rows(R, S, torch, "configs[3]", SEED + 4, variants=True)
@@ -963,6 +971,7 @@ def main():
     ops4 = step_op_rows(Rows(torch), S, torch, "configs[4]", 8192, 2048, 6144, SEED + 5)
     R = Rows(torch)
     q8_rows(R, S, torch, "configs[2]", SEED + 3)
+    q8_rows(R, S, torch, "configs[2]", SEED + 6, kind="q5_k")
     vocoder_rows(R, S, torch, "configs[3]", SEED + 4)
 
     dom = max(ops4, key=lambda n: ops4[n]["us"])

@@ -20,6 +20,7 @@
 #include <atomic>
 
 #include "shp_internal.hpp"
+#include "shp_q5k.hpp"
 #include "shp_q8.hpp"
 
 namespace shp {
@@ -68,12 +69,12 @@ struct GatherSumArgs {
     int32_t         ngroups;
     int32_t         ne0;
     // A slot g past the last group (the kernels read whole chunks of slots)
-    // reads row 0 of a -0.0 row (tab[g] = kQ8NegZeroRow, kNegZeroF32 or
-    // kNegZero16; tnb1[g] = rstride[g] = 0), which adds nothing to the sum,
+    // reads row 0 of a -0.0 row (tab[g] = kQ8NegZeroRow, kQ5KNegZeroRow,
+    // kNegZeroF32 or kNegZero16; tnb1[g] = rstride[g] = 0), which adds nothing to the sum,
     // and carries group 0's row count (group 0's id is read for it, so its
     // bounds check repeats group 0's).
-    // Q8_0 kernels only: every table has fewer than 2^31 bytes, so a row
-    // offset is 32-bit: row id * rstride[g].
+    // Q8_0 and Q5_K window kernels only: every table has fewer than 2^31
+    // bytes, so a row offset is 32-bit: row id * rstride[g].
     uint32_t        rows32[kMaxGroups];
     uint32_t        rstride[kMaxGroups];
 };
@@ -126,34 +127,21 @@ __device__ __forceinline__ float q8_elem(const char * row, int e) {
     return static_cast<float>(q) * f16_bits_to_f32(dh);
 }
 
-// Q5_K, ggml's block_q5_K: 256 elements in 176 bytes -- f16 d at byte 0, f16
-// dmin at 2, scales[12] at 4, qh[32] at 16, qs[128] at 48. Element
-// e = 64j + 32h + i (j < 4, h < 2, i < 32) of a super-block has the 4-bit
-// quant (qs[32j + i] >> 4h) & 15, the fifth bit (qh[i] >> (2j + h)) & 1, and
-// the 6-bit scale and min of its sub-block s = 2j + h: for s < 4,
-// scales[s] & 63 and scales[s + 4] & 63; for s >= 4,
-// (scales[s + 4] & 15) | (scales[s - 4] >> 6) << 4 and
-// (scales[s + 4] >> 4) | (scales[s] >> 6) << 4 (ggml's get_scale_min_k4).
+// Q5_K, ggml's block_q5_K (layout and the scale/min packing in shp_q5k.hpp).
 // The value is (d*sc)*q - dmin*m. d*sc and dmin*m have at most 17
 // significant bits and (d*sc)*q at most 22, so every product is exact in f32
 // and the subtraction is the one rounding -- as in ggml-CPU's
 // dequantize_row_q5_K, whether or not its build fuses the multiply-add.
 //
-// In 32-bit words: w0 = d | dmin << 16, w1..w3 = scales[0..11]. Every byte
-// sub-block s needs sits at the same shift 8*(s & 3) of one of w1..w3.
+// In 32-bit words: w0 = d | dmin << 16, w1..w3 = scales[0..11].
 struct Q5KCoef {
     float d1;  // d * sc
     float m1;  // dmin * m
 };
 
 __device__ __forceinline__ Q5KCoef q5k_coef(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, int s) {
-    const int      sh  = 8 * (s & 3);
-    const uint32_t b1  = (w1 >> sh) & 0xffu;  // scales[s & 3]
-    const uint32_t b2  = (w2 >> sh) & 0xffu;  // scales[4 + (s & 3)]
-    const uint32_t b3  = (w3 >> sh) & 0xffu;  // scales[8 + (s & 3)]
-    const bool     hi  = s >= 4;
-    const uint32_t sc  = hi ? ((b3 & 15u) | ((b1 >> 6) << 4)) : (b1 & 63u);
-    const uint32_t m   = hi ? ((b3 >> 4) | ((b2 >> 6) << 4)) : (b2 & 63u);
+    uint32_t sc, m;
+    q5k_scale_min(w1, w2, w3, static_cast<uint32_t>(s), sc, m);
     return Q5KCoef{ f16_bits_to_f32(w0 & 0xffffu) * static_cast<float>(sc),
                     f16_bits_to_f32(w0 >> 16) * static_cast<float>(m) };
 }
@@ -228,6 +216,10 @@ constexpr uint32_t kQNaN = 0x7fc00000u;
 // (shp_q8.hpp: every block d = -0.0, zero quants). Only read; the host passes
 // its address (hipGetSymbolAddress) in the slot's table pointer.
 __device__ Q8NegZeroRow kQ8NegZeroRow = q8_neg_zero_row();
+
+// The same for the Q5_K windows (shp_q5k.hpp: every super-block d = -0.0,
+// dmin = +0.0, zero scales and quants).
+__device__ __align__(16) Q5KNegZeroRow kQ5KNegZeroRow = q5k_neg_zero_row();
 
 // The same for the F32 / F16 / BF16 gather->sum: rows of up to kSumVecMaxNe0
 // elements that are all -0.0 (f32 0x80000000; f16 and bf16 0x8000 in each
@@ -1001,12 +993,13 @@ template <int NS> void launch_q8w(const GatherSumArgs & a, hipStream_t stream) {
     }
 }
 
-// Q5_K gather->sum: one wave per frame, lane l owning elements 4l..4l+3 of
-// each of the row's super-blocks (as k_get_rows_q5k). Groups go in chunks:
-// the chunk's ids, then every group's words for every super-block, are
-// requested before the first decode; each decoded row is added to the sum in
-// group order, from -0.0f (the identity of f32 addition), so the result is
-// the node run's ((row_0 + row_1) + row_2) + ... bit for bit.
+// Q5_K gather->sum, narrow rows (ne0 = 256 or 512): one wave per frame, lane
+// l owning elements 4l..4l+3 of each of the row's super-blocks (as
+// k_get_rows_q5k). Groups go in chunks: the chunk's ids, then every group's
+// words for every super-block, are requested before the first decode; each
+// decoded row is added to the sum in group order, from -0.0f (the identity of
+// f32 addition), so the result is the node run's ((row_0 + row_1) + row_2) +
+// ... bit for bit.
 constexpr int kQ5KSumGroups = 4;
 
 template <int NSB> __global__ __launch_bounds__(256) void k_get_rows_sum_q5k(const GatherSumArgs a) {
@@ -1056,22 +1049,165 @@ template <int NSB> __global__ __launch_bounds__(256) void k_get_rows_sum_q5k(con
     }
 }
 
+// Q5_K gather->sum by 1024-element slabs (ne0 = 1024*NS, rows 4-byte aligned,
+// every table under 2^31 bytes so a row offset is 32-bit; geometry and its
+// bounds in shp_q5k.hpp). One wave per slab of a frame; lane l owns elements
+// 16l..16l+15 of the slab, all in one sub-block. One vector load brings every
+// group's id (lane g reads group g's; at most 64 groups), checked and clamped
+// there for all groups at once, and readlane makes each scalar. The pieces
+// are raw buffer loads: the table is a scalar resource, the row offset a
+// scalar offset and the lane's place in the row a constant vector offset, so
+// no address is computed per lane.
+//
+// Groups go in chunks of kQ5KWinGroups through two register buffers: chunk
+// c + 1's loads are issued before chunk c is decoded, so every wave keeps a
+// chunk in flight while it decodes. (All of a launch's waves start together;
+// loading a chunk, then decoding it, keeps them in step -- the vector unit
+// idle while they all wait, the memory idle while they all decode: 13 %
+// slower at configs[2]'s shape.) The decode is about five vector
+// instructions per element and group -- the quant assembly of shp_q5k.hpp, a
+// byte conversion, the fma and the add, which the reference's two roundings
+// keep apart -- so at large launches this kernel is bound by instruction
+// issue, not by HBM (the Q8_0 windows, two instructions per element, reach
+// the same time per lookup while moving 1.5x the bytes).
+// Slots past the last group read kQ5KNegZeroRow, which adds exactly nothing;
+// the prefetch past the end of the loop reads it too (or group 63's rows,
+// undecoded, when there are 64 groups).
+//
+// Each value is fma(d*sc, q, -(dmin*m)): the product is exact (at most 22
+// significant bits), so the fused form rounds once, as the reference's
+// y = d1*q - m1 does. The sum starts at -0.0f, the identity of f32 addition,
+// and takes the groups in order, so it is the node run's
+// ((row_0 + row_1) + row_2) + ... bit for bit. At most 4 waves per SIMD (128
+// VGPRs), as for the Q8_0 windows: a 4096-frame sum at ne0 = 1024 is 16
+// waves per CU, all resident at once.
+constexpr int kQ5KWinGroups = 4;
+
+// A raw buffer resource over a table: no stride, every offset below 2^31 in
+// range (the window kernel's tables are under 2^31 bytes), dword data format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t table_rsrc(const char * base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(base), 0, 0x7fffffff, 0x00020000);
+}
+
+// One chunk's pieces per lane: the 16-byte header (d | dmin << 16, scales),
+// four qh dwords, four qs dwords per group.
+struct Q5KChunk {
+    u32x4 hd[kQ5KWinGroups];
+    u32x4 qh[kQ5KWinGroups];
+    u32x4 qs[kQ5KWinGroups];
+};
+
+__device__ __forceinline__ void q5kw_load(const GatherSumArgs & a, int g0, uint32_t ids, uint32_t base,
+                                          const Q5KWinPos & p, Q5KChunk & c) {
+#pragma unroll
+    for (int j = 0; j < kQ5KWinGroups; ++j) {
+        const int                    g   = g0 + j < kMaxGroups ? g0 + j : kMaxGroups - 1;
+        const __amdgpu_buffer_rsrc_t tab = table_rsrc(a.tab[g]);
+        const int ro = static_cast<int>(__builtin_amdgcn_readlane(ids, g) * a.rstride[g] + base);
+        c.hd[j] = __builtin_amdgcn_raw_buffer_load_b128(tab, static_cast<int>(p.hdr), ro, 0);
+        c.qh[j] = __builtin_amdgcn_raw_buffer_load_b128(tab, static_cast<int>(p.qh), ro, 0);
+        c.qs[j] = __builtin_amdgcn_raw_buffer_load_b128(tab, static_cast<int>(p.qs), ro, 0);
+    }
+}
+
+__device__ __forceinline__ void q5kw_decode(const Q5KChunk & c, const Q5KWinPos & p, float (&acc)[16]) {
+#pragma unroll
+    for (int j = 0; j < kQ5KWinGroups; ++j) {
+        const Q5KCoef k5 = q5k_coef(c.hd[j].x, c.hd[j].y, c.hd[j].z, c.hd[j].w, static_cast<int>(p.s));
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t q4 = q5k_quads(c.qs[j][t], c.qh[j][t], p.s);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float q  = static_cast<float>((q4 >> (8 * k)) & 0xffu);
+                acc[4 * t + k] = acc[4 * t + k] + __builtin_fmaf(k5.d1, q, -k5.m1);
+            }
+        }
+    }
+}
+
+template <int NS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_get_rows_sum_q5kw(
+    const GatherSumArgs a) {
+    args_in_sgprs(a.frames, a.ids, a.ids_gstride, a.ngroups);
+    __shared__ f32x4 s_out[4][kQ5KSlabElems / 4];  // one slab per wave, for the store transpose
+    const int     wi   = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    const int64_t wv   = static_cast<int64_t>(blockIdx.x) * 4 + wi;
+    const int64_t f    = wv / NS;
+    const int     slab = static_cast<int>(wv % NS);
+    if (f >= a.frames) {
+        return;
+    }
+    const int       l    = static_cast<int>(threadIdx.x) % kWave;
+    const Q5KWinPos p    = q5k_win_pos(l);
+    const uint32_t  base = static_cast<uint32_t>(slab) * kQ5KSlabBytes;
+    // Group l's id, checked against group l's row count once for every group
+    // (unsigned: a negative id is out of range too) and clamped to row 0 when
+    // out of range. Lanes past the last group take group 0's id and row count,
+    // as their slots do.
+    const uint32_t  idv  = static_cast<uint32_t>(group_id(a, l < a.ngroups ? l : 0, f));
+    const bool      okv  = idv < (&a.rows32[0])[l];
+    const uint64_t  bad  = __builtin_amdgcn_ballot_w64(!okv);
+    const uint32_t  ids  = okv ? idv : 0u;
+    float           acc[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        acc[k] = -0.0f;
+    }
+    Q5KChunk ca, cb;
+    q5kw_load(a, 0, ids, base, p, ca);
+    for (int g0 = 0; g0 < a.ngroups; g0 += 2 * kQ5KWinGroups) {
+        q5kw_load(a, g0 + kQ5KWinGroups, ids, base, p, cb);
+        q5kw_decode(ca, p, acc);
+        q5kw_load(a, g0 + 2 * kQ5KWinGroups, ids, base, p, ca);
+        q5kw_decode(cb, p, acc);
+    }
+    if (bad != 0) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            acc[k] = __uint_as_float(kQNaN);
+        }
+    }
+    // The wave-private LDS transpose of the Q8_0 windows: store k writes the
+    // contiguous kilobyte 256k..256k+255 of the slab.
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        s_out[wi][4 * l + k] = f32x4{ acc[4 * k], acc[4 * k + 1], acc[4 * k + 2], acc[4 * k + 3] };
+    }
+    __syncwarp();
+    f32x4 * out = reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(reinterpret_cast<char *>(a.dst) + f * a.dnb1) +
+                                            kQ5KSlabElems * slab);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        st_stream(out + 64 * k + l, s_out[wi][64 * k + l]);
+    }
+}
+
+template <int NS> void launch_q5kw(const GatherSumArgs & a, hipStream_t stream) {
+    hipLaunchKernelGGL(k_get_rows_sum_q5kw<NS>, dim3(static_cast<unsigned>((a.frames * NS + 3) / 4)), dim3(256), 0,
+                       stream, a);
+}
+
 template <int TYPE> shp_status_t launch_get_rows_sum(const GatherSumArgs & a, bool vec, hipStream_t stream) {
     if (vec) {
         if constexpr (TYPE == SHP_TYPE_Q5_K) {
-            const dim3 grid(static_cast<unsigned>((a.frames + 3) / 4));
-            switch (a.ne0 / 256) {
-                case 1:
-                    hipLaunchKernelGGL(k_get_rows_sum_q5k<1>, grid, dim3(256), 0, stream, a);
+            switch (a.ne0) {
+                case 256:
+                    hipLaunchKernelGGL(k_get_rows_sum_q5k<1>, dim3(static_cast<unsigned>((a.frames + 3) / 4)),
+                                       dim3(256), 0, stream, a);
                     break;
-                case 2:
-                    hipLaunchKernelGGL(k_get_rows_sum_q5k<2>, grid, dim3(256), 0, stream, a);
+                case 512:
+                    hipLaunchKernelGGL(k_get_rows_sum_q5k<2>, dim3(static_cast<unsigned>((a.frames + 3) / 4)),
+                                       dim3(256), 0, stream, a);
                     break;
-                case 4:
-                    hipLaunchKernelGGL(k_get_rows_sum_q5k<4>, grid, dim3(256), 0, stream, a);
+                case 1024:
+                    launch_q5kw<1>(a, stream);
+                    break;
+                case 2048:
+                    launch_q5kw<2>(a, stream);
                     break;
                 default:
-                    hipLaunchKernelGGL(k_get_rows_sum_q5k<8>, grid, dim3(256), 0, stream, a);
+                    launch_q5kw<4>(a, stream);
                     break;
             }
             return launch_status();
@@ -1136,9 +1272,10 @@ bool gather_type_ok(int32_t t) {
     return t == SHP_TYPE_F32 || t == SHP_TYPE_F16 || t == SHP_TYPE_BF16 || t == SHP_TYPE_Q8_0 || t == SHP_TYPE_Q5_K;
 }
 
-// Q5_K widths of the vector gather->sum (super-blocks held per lane).
-bool q5k_sum_width(int64_t ne0) {
-    return ne0 == 256 || ne0 == 512 || ne0 == 1024 || ne0 == 2048;
+// Q5_K widths of the vector gather->sum: super-blocks held per lane (256,
+// 512), or 1024-element slabs over tables with 32-bit row offsets.
+bool q5k_sum_width(int64_t ne0, bool dense32) {
+    return ne0 == 256 || ne0 == 512 || (dense32 && (ne0 == 1024 || ne0 == 2048 || ne0 == 4096));
 }
 
 }  // namespace
@@ -1206,15 +1343,15 @@ extern "C" shp_status_t shp_get_rows(const shp_tensor * src,
     }
 }
 
-// The address of a -0.0 row (kQ8NegZeroRow, kNegZeroF32 or kNegZero16, by
-// table type) on the device that `stream` runs on (the current device for the
+// The address of a -0.0 row (kQ8NegZeroRow, kQ5KNegZeroRow, kNegZeroF32 or
+// kNegZero16, by table type) on the device that `stream` runs on (the current device for the
 // null stream), where each device holds its own copy; looked up once per
 // device and type, with that device made current for the lookup and the
 // caller's device restored after it; null if HIP reports an error.
 const char * neg_zero_row_address(int32_t type, hipStream_t stream) {
     constexpr int                    kMaxDevices = 64;
-    static std::atomic<const char *> cache[kMaxDevices][3];
-    const int                        k   = type == SHP_TYPE_Q8_0 ? 0 : (type == SHP_TYPE_F32 ? 1 : 2);
+    static std::atomic<const char *> cache[kMaxDevices][4];
+    const int k = type == SHP_TYPE_Q8_0 ? 0 : (type == SHP_TYPE_F32 ? 1 : (type == SHP_TYPE_Q5_K ? 3 : 2));
     int                              cur = 0;
     if (hipGetDevice(&cur) != hipSuccess) {
         return nullptr;
@@ -1232,9 +1369,10 @@ const char * neg_zero_row_address(int32_t type, hipStream_t stream) {
             return nullptr;
         }
         void *     q  = nullptr;
-        hipError_t rc = k == 0 ? hipGetSymbolAddress(&q, HIP_SYMBOL(kQ8NegZeroRow))
-                               : (k == 1 ? hipGetSymbolAddress(&q, HIP_SYMBOL(kNegZeroF32))
-                                         : hipGetSymbolAddress(&q, HIP_SYMBOL(kNegZero16)));
+        hipError_t rc = k == 0   ? hipGetSymbolAddress(&q, HIP_SYMBOL(kQ8NegZeroRow))
+                        : k == 1 ? hipGetSymbolAddress(&q, HIP_SYMBOL(kNegZeroF32))
+                        : k == 2 ? hipGetSymbolAddress(&q, HIP_SYMBOL(kNegZero16))
+                                 : hipGetSymbolAddress(&q, HIP_SYMBOL(kQ5KNegZeroRow));
         if (dev != cur && hipSetDevice(cur) != hipSuccess) {
             return nullptr;
         }
@@ -1282,14 +1420,16 @@ extern "C" shp_status_t shp_get_rows_sum(const shp_tensor * tables,
         a.trows[g] = t.ne[1];
         vec        = vec && rows_aligned(t, block_type(type) ? 4 : 16);
     }
-    // Q8_0 half-block path: one row size for every table, 32-bit offsets.
-    bool q8h = type == SHP_TYPE_Q8_0;
-    for (int g = 0; g < n_tables && q8h; ++g) {
+    // Q8_0 and Q5_K window paths: one row size for every table, 32-bit offsets.
+    bool dense32 = type == SHP_TYPE_Q8_0 || type == SHP_TYPE_Q5_K;
+    for (int g = 0; g < n_tables && dense32; ++g) {
         const shp_tensor & t = tables[g];
-        q8h = t.nb[1] == row_bytes(type, ne0) && t.ne[1] <= INT32_MAX &&
-              static_cast<uint64_t>(t.ne[1]) * t.nb[1] < (uint64_t{ 1 } << 31);
+        dense32 = t.nb[1] == row_bytes(type, ne0) && t.ne[1] <= INT32_MAX &&
+                  static_cast<uint64_t>(t.ne[1]) * t.nb[1] < (uint64_t{ 1 } << 31);
     }
-    if ((frames + 3) / 4 > INT32_MAX) {
+    // Four waves per block; the window paths take one wave per 1024-element slab.
+    const int64_t waves_per_frame = block_type(type) && ne0 % 1024 == 0 ? ne0 / 1024 : 1;
+    if (frames > int64_t{ INT32_MAX } * 4 / waves_per_frame) {
         return SHP_ERR_UNSUPPORTED;
     }
     if (dry_run()) {
@@ -1307,7 +1447,7 @@ extern "C" shp_status_t shp_get_rows_sum(const shp_tensor * tables,
         a.tnb1[g]  = 0;
         a.trows[g] = a.trows[0];
     }
-    if (q8h) {
+    if (dense32) {
         for (int g = 0; g < kMaxGroups; ++g) {
             const bool live = g < n_tables;
             a.rows32[g]     = static_cast<uint32_t>(tables[live ? g : 0].ne[1]);
@@ -1330,8 +1470,8 @@ extern "C" shp_status_t shp_get_rows_sum(const shp_tensor * tables,
         case SHP_TYPE_BF16:
             return launch_get_rows_sum<SHP_TYPE_BF16>(a, vec && ne0 % 4 == 0 && ne0 <= kSumVecMaxNe0, st);
         case SHP_TYPE_Q5_K:
-            return launch_get_rows_sum<SHP_TYPE_Q5_K>(a, vec && q5k_sum_width(ne0), st);
+            return launch_get_rows_sum<SHP_TYPE_Q5_K>(a, vec && q5k_sum_width(ne0, dense32), st);
         default:
-            return launch_get_rows_sum<SHP_TYPE_Q8_0>(a, vec && q8h, st);
+            return launch_get_rows_sum<SHP_TYPE_Q8_0>(a, vec && dense32, st);
     }
 }

@@ -88,12 +88,15 @@ def test_get_rows_q5k_batched_and_misaligned(gpu):
 
 
 @pytest.mark.parametrize("ne0,groups,frames", [(1024, 16, 4096), (1024, 15, 64), (256, 1, 33), (512, 3, 100),
-                                               (2048, 9, 50), (4096, 4, 20)])
+                                               (2048, 9, 50), (4096, 4, 20), (1024, 33, 40), (1024, 1, 7),
+                                               (3072, 2, 9)])
 def test_get_rows_sum_q5k_bitexact(gpu, ne0, groups, frames):
     """sum_code_embeddings over Q5_K tables (code-predictor.cpp:82-107): the
     ordered f32 sum of the dequantized rows, bit for bit. (1024, 16, 4096) is
-    configs[2]'s shape with Q5_K codebooks; 4096-wide rows take the
-    element-wise kernel."""
+    configs[2]'s shape with Q5_K codebooks. Widths 1024, 2048 and 4096 take
+    the 1024-element slab windows (groups in chunks of 8: 15, 9, 33 and 1
+    leave slots past the last group), 256 and 512 the narrow kernel, 3072 the
+    element-wise one."""
     rng = np.random.default_rng(SEED + 17 + ne0 + groups)
     rows = 2048 if frames >= 4096 else 60
     tabs = [F.q5_k_synthetic(rng, rows, ne0) for _ in range(groups)]
@@ -120,3 +123,22 @@ def test_get_rows_sum_q5k_order_and_bad_id(gpu):
     assert_bitexact(got[ok], ref[ok])
     rev = _np(gpu.get_rows_sum(dev[::-1], _t(gpu, np.ascontiguousarray(codes[::-1]))))
     assert not np.array_equal(rev[ok].view(np.uint32), got[ok].view(np.uint32))
+
+
+def test_get_rows_sum_q5k_padded_rows(gpu):
+    """Tables whose rows are padded past the 704 bytes of a 1024-wide row (row
+    stride 720) cannot take the windows' 32-bit dense offsets; they take the
+    element-wise kernel, with the same bits."""
+    import torch
+    rng = np.random.default_rng(SEED + 41)
+    ne0, rows, groups, frames = 1024, 50, 4, 64
+    tabs = [F.q5_k_synthetic(rng, rows, ne0) for _ in range(groups)]
+    codes = rng.integers(0, rows, (groups, frames)).astype(np.int32)
+    ref = R.run(lambda g: R.sum_code_embeddings(g, tabs, R.Q5_K, ne0, codes))
+    dev = []
+    for t in tabs:
+        buf = torch.zeros((rows, 720), dtype=torch.uint8, device="cuda")
+        buf[:, :704].copy_(torch.from_numpy(t).cuda())
+        dev.append(gpu.Q5KTensor(buf[:, :704], ne0))
+    assert dev[0].data.stride(0) == 720
+    assert_bitexact(_np(gpu.get_rows_sum(dev, _t(gpu, codes))), ref)

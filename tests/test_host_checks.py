@@ -3,6 +3,9 @@
 - q8_bounds_check: the Q8_0 half-block read geometry of the gather kernels
   (synthesize.cpp_amd/csrc/shp_q8.hpp) reads only inside a row, for every lane
   of every row width the kernels take, and decodes each lane's scale and quants.
+- q5k_window_check: the Q5_K gather->sum windows (shp_q5k.hpp) read only inside
+  each lane's super-block, tile the slab, and decode the scale, min and quants
+  of ggml's byte layout.
 - trig_check: the rope's double-precision cos/sin (shp_trig.hpp) rounds to the
   same f32 as libm's double sin/cos.
 - div_check: Snake's division by a per-channel double reciprocal (shp_div.hpp)
@@ -35,6 +38,12 @@ def test_q8_half_block_reads_stay_inside_the_row(tmp_path):
     rc, out = _build_and_run(tmp_path, "q8_bounds_check")
     checked, failures = map(int, out.split()[-2:])
     assert rc == 0 and failures == 0 and checked > 2000, out
+
+
+def test_q5k_window_reads_and_decoding(tmp_path):
+    rc, out = _build_and_run(tmp_path, "q5k_window_check")
+    checked, failures = map(int, out.split()[-2:])
+    assert rc == 0 and failures == 0 and checked == 2000 * 64, out
 
 
 def test_rope_sincos_is_correctly_rounded(tmp_path):
