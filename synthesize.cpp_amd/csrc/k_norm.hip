@@ -555,6 +555,39 @@ __device__ __forceinline__ void rope_sincos(float th, float & s, float & c) {
     }
 }
 
+// theta_k = p * s * s * ... (k f32 multiplies, each rounded: the CPU cache's
+// recurrence) in lane k of a full wave. One v_mul_f32 per step: before step i
+// the exec mask drops lane i - 1 (s_bitset0_b64 leaves SCC alone), so lane k
+// takes part in exactly the first k multiplies; the mask is restored after.
+// Written out because the compiler's form of the same loop -- every lane
+// multiplying and keeping its step's value by a compare and a select -- costs
+// three vector instructions and a hazard wait per step: 0.5 us of a one-token
+// QK-norm+RoPE launch. Plain v_mul_f32 under the kernel's float mode, so the
+// values are the compiler's multiplies bit for bit.
+#define SHP_THETA_STEP(i) "s_bitset0_b64 exec, " #i "\n\tv_mul_f32 %0, %1, %0\n\t"
+
+__device__ __forceinline__ float theta_chain64(float p, float s) {
+    float    th = p;
+    uint64_t saved;
+    asm volatile("s_mov_b64 %0, exec" : "=s"(saved));
+    asm volatile(
+                 SHP_THETA_STEP(0) SHP_THETA_STEP(1) SHP_THETA_STEP(2) SHP_THETA_STEP(3) SHP_THETA_STEP(4) SHP_THETA_STEP(5) SHP_THETA_STEP(6)
+                 SHP_THETA_STEP(7) SHP_THETA_STEP(8) SHP_THETA_STEP(9) SHP_THETA_STEP(10) SHP_THETA_STEP(11) SHP_THETA_STEP(12) SHP_THETA_STEP(13)
+                 SHP_THETA_STEP(14) SHP_THETA_STEP(15) SHP_THETA_STEP(16) SHP_THETA_STEP(17) SHP_THETA_STEP(18) SHP_THETA_STEP(19) SHP_THETA_STEP(20)
+                 SHP_THETA_STEP(21) SHP_THETA_STEP(22) SHP_THETA_STEP(23) SHP_THETA_STEP(24) SHP_THETA_STEP(25) SHP_THETA_STEP(26) SHP_THETA_STEP(27)
+                 SHP_THETA_STEP(28) SHP_THETA_STEP(29) SHP_THETA_STEP(30) SHP_THETA_STEP(31) SHP_THETA_STEP(32) SHP_THETA_STEP(33) SHP_THETA_STEP(34)
+                 SHP_THETA_STEP(35) SHP_THETA_STEP(36) SHP_THETA_STEP(37) SHP_THETA_STEP(38) SHP_THETA_STEP(39) SHP_THETA_STEP(40) SHP_THETA_STEP(41)
+                 SHP_THETA_STEP(42) SHP_THETA_STEP(43) SHP_THETA_STEP(44) SHP_THETA_STEP(45) SHP_THETA_STEP(46) SHP_THETA_STEP(47) SHP_THETA_STEP(48)
+                 SHP_THETA_STEP(49) SHP_THETA_STEP(50) SHP_THETA_STEP(51) SHP_THETA_STEP(52) SHP_THETA_STEP(53) SHP_THETA_STEP(54) SHP_THETA_STEP(55)
+                 SHP_THETA_STEP(56) SHP_THETA_STEP(57) SHP_THETA_STEP(58) SHP_THETA_STEP(59) SHP_THETA_STEP(60) SHP_THETA_STEP(61) SHP_THETA_STEP(62)
+                 "s_mov_b64 exec, %2"
+                 : "+v"(th)
+                 : "s"(s), "s"(saved));
+    return th;
+}
+
+#undef SHP_THETA_STEP
+
 // cos/sin of the pair-k angle at position p: theta is replayed through the f32
 // recurrence theta <- theta*theta_scale exactly k times (the CPU cache's order),
 // then cos/sin are evaluated in double and rounded once to f32, then scaled by
@@ -577,10 +610,11 @@ __device__ __forceinline__ void rope_cs(int32_t p, int k, const RopeArgs & a, fl
 // so the rotation needs no data exchange and every access is 128-bit. The
 // block has one 16-lane group per head row of the position (q heads, then k
 // heads; 24 rows = 384 lanes for Qwen3-TTS; with the KV-cache write, v heads
-// follow and are stored unchanged), so every row load is issued at once. Meanwhile wave 0 builds the position's 64-entry cos/sin cache: all 64
-// lanes run the same serial f32 theta chain and lane k keeps the k-th value,
-// evaluates its cos/sin in double and writes them to LDS; one barrier later
-// every lane reads the 4 pairs it needs.
+// follow and are stored unchanged), so every row load is issued at once.
+// Meanwhile wave 0 builds the position's 64-entry cos/sin cache: it runs the
+// serial f32 theta chain once, lane k leaving it after k multiplies
+// (theta_chain64), evaluates its cos/sin in double and writes them to LDS;
+// one barrier later every lane reads the 4 pairs it needs.
 constexpr int kRopeLanes   = 16;
 constexpr int kRopeMaxRows = 1024 / kRopeLanes;
 
@@ -623,15 +657,9 @@ template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(1024) void k_
 
     // 2. the cos/sin cache of this position (wave 0)
     if (threadIdx.x < 64) {
-        const int k   = threadIdx.x;
-        float     th  = static_cast<float>(p);
-        float     mth = th;
-#pragma unroll
-        for (int i = 1; i < 64; ++i) {
-            th  = th * a.theta_scale;
-            mth = k == i ? th : mth;
-        }
-        float sv, cv;
+        const int   k   = threadIdx.x;
+        const float mth = theta_chain64(static_cast<float>(p), a.theta_scale);
+        float       sv, cv;
         rope_sincos(a.freq_scale * mth, sv, cv);
         reinterpret_cast<float *>(s_cos)[k] = cv * a.attn_factor;
         reinterpret_cast<float *>(s_sin)[k] = sv * a.attn_factor;
