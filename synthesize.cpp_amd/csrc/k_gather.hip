@@ -204,8 +204,8 @@ __device__ __forceinline__ void gather_coords(const GatherArgs & a, int64_t R, i
     const uint32_t i12 = fastdiv(q, a.fne11);
     const int64_t  r   = R - static_cast<int64_t>(q) * a.fn.d;
     const int64_t  i11 = q - i12 * a.fne11.d;
-    id   = *reinterpret_cast<const int32_t *>(reinterpret_cast<const char *>(a.ids) + r * a.inb0 + i11 * a.inb1 +
-                                            static_cast<int64_t>(i12) * a.inb2);
+    id   = ld_const(reinterpret_cast<const int32_t *>(reinterpret_cast<const char *>(a.ids) + r * a.inb0 + i11 * a.inb1 +
+                                                  static_cast<int64_t>(i12) * a.inb2));
     srow = a.src + static_cast<int64_t>(id) * a.snb1 + i11 * a.snb2 + i12 * a.snb3;
     drow = reinterpret_cast<float *>(reinterpret_cast<char *>(a.dst) + r * a.dnb1 + i11 * a.dnb2 + i12 * a.dnb3);
 }
@@ -257,18 +257,6 @@ template <int TYPE> __device__ __forceinline__ f32x4 cvt_sum_chunk(const typenam
     } else {
         return f32x4{ f16_bits_to_f32(v.x & 0xffffu), f16_bits_to_f32(v.x >> 16), f16_bits_to_f32(v.y & 0xffffu),
                       f16_bits_to_f32(v.y >> 16) };
-    }
-}
-
-// Row index of this lane's group; for LPR >= 64 every lane of a wave has the
-// same row, which readfirstlane makes visible to the compiler so that the id
-// and the table row base are scalar.
-template <int LPR> __device__ __forceinline__ int row_in_block() {
-    const int r = static_cast<int>(threadIdx.x) / LPR;
-    if constexpr (LPR >= kWave) {
-        return __builtin_amdgcn_readfirstlane(r);
-    } else {
-        return r;
     }
 }
 
@@ -630,34 +618,37 @@ template <int NQ> __device__ __forceinline__ void q8_row_stage(uint32_t * lds, c
     }
 }
 
-// Quad k of lane l: the four values q * fp16(d), each one exact product.
-template <int NQ> __device__ __forceinline__ void q8_row_decode(const uint32_t * lds, int l, float (&o)[4 * NQ]) {
+// Quad k of lane l: the four values q * fp16(d), each one exact product,
+// stored as soon as it is decoded (a NaN quad when the id is out of range).
+template <int NQ>
+__device__ __forceinline__ void q8_row_decode_store(const uint32_t * lds, int l, bool ok, float * drow) {
+    f32x4 * out = reinterpret_cast<f32x4 *>(drow);
 #pragma unroll
     for (int k = 0; k < NQ; ++k) {
         const Q8QuadPos p = q8_quad_pos(k, l);
         const uint32_t  q = bytes_at(lds[p.adw + 1], lds[p.adw], p.sh);
         const float     d = f16_bits_to_f32((lds[p.ddw] >> p.dsh) & 0xffffu);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            o[4 * k + i] = sbyte(q, i) * d;
+        f32x4           o{ sbyte(q, 0) * d, sbyte(q, 1) * d, sbyte(q, 2) * d, sbyte(q, 3) * d };
+        if (!ok) {
+            o = splat4(__uint_as_float(kQNaN));
         }
-    }
-}
-
-template <int NQ> __device__ __forceinline__ void q8_row_store(float * drow, int l, const float (&o)[4 * NQ]) {
-    f32x4 * out = reinterpret_cast<f32x4 *>(drow);
-#pragma unroll
-    for (int k = 0; k < NQ; ++k) {
-        st_stream(out + 64 * k + l, f32x4{ o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3] });
+        st_stream(out + 64 * k + l, o);
     }
 }
 
 constexpr int kQ8StageWaves = 4;  // waves (rows or frames) per 256-thread block
 
+// One wave per row. An id out of range reads row 0 of the table and stores
+// NaN, with no branch between the id and the row loads; each quad is stored
+// as soon as it is decoded. Measured on MI355X at [1024,2048] x4096 against
+// the branch on the id with all 16 values stored at the end: 4.54 against
+// 4.68 us.
 template <int NQ> __global__ __launch_bounds__(256) void k_get_rows_q8s(const GatherArgs a) {
     gather_args_in_sgprs(a);
     __shared__ uint32_t s_row[kQ8StageWaves][q8_row_dwords(NQ) + kQ8StagePadDwords];
-    const int           w = static_cast<int>(threadIdx.x) / kWave;
+    // The row is uniform over the wave: readfirstlane lets the id be one scalar
+    // load and the table row base a scalar.
+    const int           w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
     const int           l = static_cast<int>(threadIdx.x) % kWave;
     const int64_t       R = static_cast<int64_t>(blockIdx.x) * kQ8StageWaves + w;
     if (R >= a.total) {
@@ -667,19 +658,11 @@ template <int NQ> __global__ __launch_bounds__(256) void k_get_rows_q8s(const Ga
     const char * srow;
     float *      drow;
     gather_coords(a, R, id, srow, drow);
-    float o[4 * NQ];
-    if (id < 0 || id >= a.srows) {
-#pragma unroll
-        for (int j = 0; j < 4 * NQ; ++j) {
-            o[j] = __uint_as_float(kQNaN);
-        }
-    } else {
-        const Q8Row<NQ> r = q8_row_load<NQ>(srow, l);
-        q8_row_stage<NQ>(s_row[w], r, l);
-        __syncwarp();
-        q8_row_decode<NQ>(s_row[w], l, o);
-    }
-    q8_row_store<NQ>(drow, l, o);
+    const bool      ok = (id >= 0) & (id < a.srows);
+    const Q8Row<NQ> r  = q8_row_load<NQ>(ok ? srow : a.src, l);
+    q8_row_stage<NQ>(s_row[w], r, l);
+    __syncwarp();
+    q8_row_decode_store<NQ>(s_row[w], l, ok, drow);
 }
 
 // ---------------------------------------------------------------------------

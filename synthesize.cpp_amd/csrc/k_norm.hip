@@ -119,7 +119,7 @@ __global__ __launch_bounds__(BLOCK) void k_rms_norm_vec(const NormArgs a) {
         args_in_sgprs(a.s, a.sm.flat, a.sm.rs);
     }
     const int     l     = threadIdx.x % TPR;
-    const int64_t row   = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / TPR;
+    const int64_t row   = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + row_in_block<TPR>();
     const bool    live  = row < a.nrows;
     const int     nvec  = a.ne0 / 4;
     const int64_t rrow  = live ? row : 0;

@@ -60,8 +60,33 @@ template <class T> __device__ __forceinline__ gptr<T> to_global(T * p) {
     return (gptr<T>) p;
 }
 
+// A load of data that no kernel writes while this one runs (ids, positions)
+// through the constant address space: when the address is uniform over the
+// wave it becomes one scalar load (s_load) instead of a vector load plus a
+// readfirstlane, which is the shorter round trip in front of a gather's row
+// loads. A non-uniform address still compiles to a vector load.
+template <class T> __device__ __forceinline__ T ld_const(const T * p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return *(const T __attribute__((address_space(4))) *) p;
+#else
+    return *p;
+#endif
+}
+
 __device__ __forceinline__ f32x4 splat4(float v) {
     return f32x4{ v, v, v, v };
+}
+
+// Index of this lane's LPR-lane group (a row) within its block. For LPR >= 64
+// every lane of a wave has the same row, which readfirstlane makes visible to
+// the compiler, so row bases, ids and bounds become scalar values.
+template <int LPR> __device__ __forceinline__ int row_in_block() {
+    const int r = static_cast<int>(threadIdx.x) / LPR;
+    if constexpr (LPR >= kWave) {
+        return __builtin_amdgcn_readfirstlane(r);
+    } else {
+        return r;
+    }
 }
 
 // Kernel arguments arrive by scalar loads from the kernel-argument segment,
