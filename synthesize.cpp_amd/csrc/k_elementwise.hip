@@ -295,21 +295,28 @@ template <int K> __global__ __launch_bounds__(256) void k_snake_flat(const EwArg
     const int64_t c4   = a.quads.d;
     const int64_t step = static_cast<int64_t>(gridDim.x) * 256;
     args_in_sgprs(X, C0, C1, a.quads.d, a.quads.m, a.quads.l, a.ntask, a.n4, step);
-    for (int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; t < a.ntask; t += step) {
-        const uint32_t rb = fastdiv(static_cast<uint32_t>(t), a.quads);  // row block
-        const uint32_t q  = static_cast<uint32_t>(t) - rb * a.quads.d;  // channel quad
-        const int64_t  i0 = static_cast<int64_t>(rb) * R * c4 + q;
-        const f32x4    c0 = C0[q];
-        f32x4          c1 = splat4(0.0f);
-        if constexpr (K == kSnakeBeta) {
-            c1 = C1[q];
-        }
-        f32x4 xv[R];
+    // A lane's task: its curves and its R rows, requested together, so the
+    // per-channel work waits for one round trip, in parallel with the rows
+    // (the loop runs once unless the grid is capped).
+    int64_t  t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    uint32_t q;
+    int64_t  i0;
+    f32x4    c0, c1, xv[R];
+    auto     load = [&](int64_t tt) {
+        const uint32_t rb = fastdiv(static_cast<uint32_t>(tt), a.quads);  // row block
+        q                 = static_cast<uint32_t>(tt) - rb * a.quads.d;  // channel quad
+        i0                = static_cast<int64_t>(rb) * R * c4 + q;
+        const bool in     = tt < a.ntask;
+        c0                = in ? C0[q] : splat4(1.0f);
+        c1                = K == kSnakeBeta && in ? C1[q] : splat4(0.0f);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int64_t i = i0 + r * c4;
-            xv[r]           = i < a.n4 ? ld_stream(X + i) : splat4(0.0f);
+            xv[r]           = in & (i < a.n4) ? ld_stream(X + i) : splat4(0.0f);
         }
+    };
+    load(t);
+    while (t < a.ntask) {
         const SnakeCoef k0 = snake_coef<K>(c0.x, c1.x);
         const SnakeCoef k1 = snake_coef<K>(c0.y, c1.y);
         const SnakeCoef k2 = snake_coef<K>(c0.z, c1.z);
@@ -324,29 +331,57 @@ template <int K> __global__ __launch_bounds__(256) void k_snake_flat(const EwArg
             const double rc[4] = { 0.0, 0.0, 0.0, 0.0 };
             snake_rows<K, R, false>(xv, al, den, rc, i0, c4, a.n4, Y);
         }
+        t += step;
+        if (t < a.ntask) {
+            load(t);
+        }
     }
 }
 
 
-// SnakeBeta on tensors of at least kSnakeLdsMinTasks lane tasks and at most
-// kSnakeLdsMaxC channels: each block first evaluates every channel's exp
-// curves, guard and double reciprocal once into LDS, then steps through its
-// share of the tasks (2 rows of one channel quad each, as plain Snake) with
-// a grid stride, so the two exps per channel are spread over the block's
-// whole share instead of 8 rows. Measured on MI355X at [128,131072]: 8 %
-// faster than the 8-row kernel; at [256,32768] and below, where a block's
-// share is only one or two tasks, the table does not pay for itself, and for
-// plain Snake, whose per-channel work is only the reciprocal, the grid stride
-// measured 4-7 % slower than one task per lane.
+// SnakeBeta with at most kSnakeLdsMaxC channels, on tensors of at least
+// kSnakeLdsMinTasks 2-row lane tasks or at most kSnakeLdsSmallTasks 4-row
+// tasks: each block first evaluates every channel's exp curves, guard and
+// double reciprocal once into LDS (the first task's rows already requested),
+// then steps through its share of the tasks (R rows of one channel quad each)
+// with a grid stride, so the two exps per channel are spread over the block's
+// whole share instead of 8 rows. Measured on MI355X: at [128,131072] 8 %
+// faster than the 8-row kernel (2 rows per task, 2048 blocks); at [512,8192],
+// one 4-row task per lane over 1024 blocks, 5 % faster (7.9 against 8.3 us).
+// At [256,32768] neither form beats the 8-row kernel. For plain Snake, whose
+// per-channel work is only the reciprocal, the grid stride measured 4-7 %
+// slower than one task per lane.
 constexpr int     kSnakeLdsMaxC     = 1024;
 constexpr int     kSnakeLdsBlocks   = 2048;
 constexpr int64_t kSnakeLdsMinTasks = int64_t{ 4 } * kSnakeLdsBlocks * 256;
+constexpr int64_t kSnakeLdsSmallTasks = int64_t{ 1024 } * 256;
 
-__global__ __launch_bounds__(256) void k_snake_beta_lds(const EwArgs a) {
+template <int R> __global__ __launch_bounds__(256) void k_snake_beta_lds(const EwArgs a) {
     __shared__ __align__(16) float  s_al[kSnakeLdsMaxC];
     __shared__ __align__(16) float  s_den[kSnakeLdsMaxC];
     __shared__ __align__(16) double s_rc[kSnakeLdsMaxC];
-    args_in_sgprs(a.alpha, a.beta, a.quads.d);
+    const f32x4 * X    = reinterpret_cast<const f32x4 *>(a.a);
+    f32x4 *       Y    = reinterpret_cast<f32x4 *>(a.y);
+    const int64_t c4   = a.quads.d;
+    const int64_t step = static_cast<int64_t>(gridDim.x) * 256;
+    args_in_sgprs(X, a.alpha, a.beta, a.quads.d, a.quads.m, a.quads.l, a.ntask, a.n4);
+    // The first task's rows are requested before the table of curves is
+    // built, so their loads overlap its loads and exps.
+    int64_t  t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    uint32_t q;
+    int64_t  i0;
+    f32x4    xv[R];
+    auto     load = [&](int64_t tt) {
+        const uint32_t rb = fastdiv(static_cast<uint32_t>(tt), a.quads);  // row block
+        q                 = static_cast<uint32_t>(tt) - rb * a.quads.d;  // channel quad
+        i0                = static_cast<int64_t>(rb) * R * c4 + q;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int64_t i = i0 + r * c4;
+            xv[r]           = (tt < a.ntask) & (i < a.n4) ? ld_stream(X + i) : splat4(0.0f);
+        }
+    };
+    load(t);
     const int nc = static_cast<int>(a.quads.d) * 4;
     for (int c = threadIdx.x; c < nc; c += 256) {
         const SnakeCoef k = snake_coef<kSnakeBeta>(a.alpha[c], a.beta[c]);
@@ -355,21 +390,7 @@ __global__ __launch_bounds__(256) void k_snake_beta_lds(const EwArgs a) {
         s_rc[c]           = rcp_route_ok(k.den) ? rcp_d(static_cast<double>(k.den)) : 0.0;
     }
     __syncthreads();
-    constexpr int R    = 2;
-    const f32x4 * X    = reinterpret_cast<const f32x4 *>(a.a);
-    f32x4 *       Y    = reinterpret_cast<f32x4 *>(a.y);
-    const int64_t c4   = a.quads.d;
-    const int64_t step = static_cast<int64_t>(gridDim.x) * 256;
-    for (int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; t < a.ntask; t += step) {
-        const uint32_t rb = fastdiv(static_cast<uint32_t>(t), a.quads);  // row block
-        const uint32_t q  = static_cast<uint32_t>(t) - rb * a.quads.d;  // channel quad
-        const int64_t  i0 = static_cast<int64_t>(rb) * R * c4 + q;
-        f32x4          xv[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int64_t i = i0 + r * c4;
-            xv[r]           = i < a.n4 ? ld_stream(X + i) : splat4(0.0f);
-        }
+    while (t < a.ntask) {
         const f32x4  al    = reinterpret_cast<const f32x4 *>(s_al)[q];
         const f32x4  den   = reinterpret_cast<const f32x4 *>(s_den)[q];
         const double rc[4] = { s_rc[4 * q], s_rc[4 * q + 1], s_rc[4 * q + 2], s_rc[4 * q + 3] };
@@ -377,6 +398,10 @@ __global__ __launch_bounds__(256) void k_snake_beta_lds(const EwArgs a) {
             snake_rows<kSnakeBeta, R, true>(xv, al, den, rc, i0, c4, a.n4, Y);
         } else {
             snake_rows<kSnakeBeta, R, false>(xv, al, den, rc, i0, c4, a.n4, Y);
+        }
+        t += step;
+        if (t < a.ntask) {
+            load(t);
         }
     }
 }
@@ -664,12 +689,20 @@ shp_status_t launch_snake(const shp_tensor * x, const shp_tensor * c0, const shp
     const bool c16 =
         reinterpret_cast<uintptr_t>(g.alpha) % 16 == 0 && reinterpret_cast<uintptr_t>(g.beta) % 16 == 0;
     if (K == kSnakeBeta && plan.flat && c16 && x->ne[0] <= kSnakeLdsMaxC) {
-        const int64_t quads = x->ne[0] / 4;
-        const int64_t ntask = (g.n4 / quads + 1) / 2 * quads;
-        if (ntask >= kSnakeLdsMinTasks && ntask <= UINT32_MAX) {
-            g.quads = make_fastdiv(static_cast<uint32_t>(quads));
-            g.ntask = ntask;
-            hipLaunchKernelGGL(k_snake_beta_lds, dim3(kSnakeLdsBlocks), dim3(256), 0, stream, g);
+        const int64_t quads  = x->ne[0] / 4;
+        const int64_t rows   = g.n4 / quads;
+        const int64_t ntask2 = (rows + 1) / 2 * quads;
+        const int64_t ntask4 = (rows + 3) / 4 * quads;
+        g.quads              = make_fastdiv(static_cast<uint32_t>(quads));
+        if (ntask4 <= kSnakeLdsSmallTasks) {
+            g.ntask = ntask4;
+            hipLaunchKernelGGL(k_snake_beta_lds<4>, dim3(static_cast<unsigned>((ntask4 + 255) / 256)), dim3(256), 0,
+                               stream, g);
+            return launch_status();
+        }
+        if (ntask2 >= kSnakeLdsMinTasks && ntask2 <= UINT32_MAX) {
+            g.ntask = ntask2;
+            hipLaunchKernelGGL(k_snake_beta_lds<2>, dim3(kSnakeLdsBlocks), dim3(256), 0, stream, g);
             return launch_status();
         }
     }

@@ -60,27 +60,6 @@ struct SoftMaxArgs {
 constexpr int kSoftMaxWaveMax = 2048;  // widest row of the one-wave kernel
 constexpr int kSoftMaxBlock   = 256;
 
-// exp through the wave's own LDS copy of kExpTable (one ds_read_b64 per
-// lookup; measured ~3% faster on the softmax than reading the table from
-// memory or shuffling a per-lane entry).
-__device__ __forceinline__ float exp_f32_lds(float x, const double * tab) {
-    return exp_f32_rn(x, [tab](int j) { return tab[j]; });
-}
-
-// Fills the calling wave's 64-entry table with the entries the lanes loaded
-// (lane l holds entry l) and makes it visible to the whole wave. The entry is
-// loaded (exp_table_entry) before the row, so both are in flight together.
-__device__ __forceinline__ double exp_table_entry(int lane) {
-    return kExpTable[lane];
-}
-
-__device__ __forceinline__ const double * wave_exp_table(double (*s_tab)[64], int lane, double entry) {
-    double * t = s_tab[threadIdx.x / kWave];
-    t[lane]    = entry;
-    __syncwarp();
-    return t;
-}
-
 // exp with the table read from memory (divergent loops).
 __device__ __forceinline__ float exp_f32(float x) {
     return exp_f32_rn(x, [](int j) { return kExpTable[j]; });
