@@ -48,7 +48,7 @@ struct GatherArgs {
     int64_t         ne11;
     int64_t         total;   // < 2^32
     int32_t         ne0;
-    int32_t         staged;  // Q8_0 through LDS: ne0 in {1024, 2048, 4096}, rows 16-byte aligned
+    int32_t         staged;  // Q8_0 / Q5_K through LDS: ne0 in {1024, 2048, 4096}, rows 16-byte aligned
     // Output row R = r + n*(i11 + ne11*i12) by multiply-shift divisions, with
     // no branch on the batch form: an unbatched gather is n = total, ne11 = 1.
     FastDiv         fn;
@@ -735,6 +735,58 @@ __global__ __launch_bounds__(256) void k_get_rows_q5k(const GatherArgs a) {
     }
 }
 
+// get_rows of 16-byte aligned rows of NSB = ne0/256 super-blocks (ne0 1024,
+// 2048, 4096): the wave copies its row (11 aligned 16-byte words per
+// super-block) into a wave-private LDS buffer with one dwordx4 per lane and
+// round, then decodes each super-block's 4 elements per lane from LDS as
+// above -- a few wide loads in front of the decode instead of six dword loads
+// per super-block and lane. An id out of range reads row 0 and stores NaN.
+template <int NSB> __global__ __launch_bounds__(256) void k_get_rows_q5ks(const GatherArgs a) {
+    gather_args_in_sgprs(a);
+    constexpr int kWords  = 11 * NSB;  // 16-byte words per row
+    constexpr int kRounds = (kWords + kWave - 1) / kWave;
+    __shared__ u32x4 s_row[kQ8StageWaves][kWords];
+    const int        w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    const int        l = static_cast<int>(threadIdx.x) % kWave;
+    const int64_t    R = static_cast<int64_t>(blockIdx.x) * kQ8StageWaves + w;
+    if (R >= a.total) {
+        return;  // no block barrier below: only this wave uses s_row[w]
+    }
+    int32_t      id;
+    const char * srow;
+    float *      drow;
+    gather_coords(a, R, id, srow, drow);
+    const bool    ok  = (id >= 0) & (id < a.srows);
+    const u32x4 * src = reinterpret_cast<const u32x4 *>(ok ? srow : a.src);
+    u32x4         v[kRounds];
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+        const int i = kWave * r + l;
+        if (i < kWords) {
+            v[r] = src[i];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+        const int i = kWave * r + l;
+        if (i < kWords) {
+            s_row[w][i] = v[r];
+        }
+    }
+    __syncwarp();
+    const uint32_t * lds = reinterpret_cast<const uint32_t *>(s_row[w]);
+    const Q5KLane    p   = q5k_lane(l);
+    f32x4 *          out = reinterpret_cast<f32x4 *>(drow);
+#pragma unroll
+    for (int b = 0; b < NSB; ++b) {
+        f32x4 o = q5k_decode(q5k_load(lds + 44 * b, p), p);
+        if (!ok) {
+            o = splat4(__uint_as_float(kQNaN));
+        }
+        st_stream(out + 64 * b + l, o);
+    }
+}
+
 // Any type / alignment: one wave per row, element by element.
 template <int TYPE> __global__ __launch_bounds__(256) void k_get_rows_generic(const GatherArgs a) {
     const int     lane = threadIdx.x % kWave;
@@ -878,7 +930,16 @@ template <int TYPE> shp_status_t launch_get_rows(const GatherArgs & a, bool vec,
     }
     if (vec) {
         if constexpr (TYPE == SHP_TYPE_Q5_K) {
-            hipLaunchKernelGGL(k_get_rows_q5k, dim3(static_cast<unsigned>((a.total + 3) / 4)), dim3(256), 0, stream, a);
+            const dim3 grid(static_cast<unsigned>((a.total + 3) / 4));
+            if (a.staged && a.ne0 == 1024) {
+                hipLaunchKernelGGL(k_get_rows_q5ks<4>, grid, dim3(256), 0, stream, a);
+            } else if (a.staged && a.ne0 == 2048) {
+                hipLaunchKernelGGL(k_get_rows_q5ks<8>, grid, dim3(256), 0, stream, a);
+            } else if (a.staged && a.ne0 == 4096) {
+                hipLaunchKernelGGL(k_get_rows_q5ks<16>, grid, dim3(256), 0, stream, a);
+            } else {
+                hipLaunchKernelGGL(k_get_rows_q5k, grid, dim3(256), 0, stream, a);
+            }
             return launch_status();
         } else if constexpr (TYPE == SHP_TYPE_Q8_0) {
             if (a.staged) {
@@ -959,8 +1020,9 @@ template <int TYPE> shp_status_t launch_get_rows(const GatherArgs & a, bool vec,
     return launch_status();
 }
 
-// Q8_0 widths the LDS-staged get_rows takes (one wave per row, NQ = ne0/256)
-// and the windowed gather->sum takes (ne0/1024 waves per frame).
+// Q8_0 widths the LDS-staged get_rows takes (one wave per row, NQ = ne0/256;
+// the same widths for Q5_K) and the windowed gather->sum takes (ne0/1024
+// waves per frame).
 bool q8_staged_width(int64_t ne0) {
     return ne0 == 1024 || ne0 == 2048 || ne0 == 4096;
 }
@@ -1299,8 +1361,9 @@ extern "C" shp_status_t shp_get_rows(const shp_tensor * src,
     a.n     = ids->ne[0];
     a.ne11  = ids->ne[1];
     a.total = ids->ne[0] * ids->ne[1] * ids->ne[2];
-    a.staged  = src->type == SHP_TYPE_Q8_0 && q8_staged_width(src->ne[0]) && rows_aligned(*src, 16) &&
-               rows_aligned(*dst, 16);
+    // Q8_0 and Q5_K rows through LDS: 1024/2048/4096 wide, 16-byte aligned
+    a.staged  = (src->type == SHP_TYPE_Q8_0 || src->type == SHP_TYPE_Q5_K) && q8_staged_width(src->ne[0]) &&
+               rows_aligned(*src, 16) && rows_aligned(*dst, 16);
     a.ne0   = static_cast<int32_t>(src->ne[0]);
     if (a.total > int64_t{ UINT32_MAX } / 256) {  // output rows (and their lanes) by 32-bit divisions
         return SHP_ERR_UNSUPPORTED;

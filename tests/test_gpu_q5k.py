@@ -87,6 +87,31 @@ def test_get_rows_q5k_batched_and_misaligned(gpu):
     assert_bitexact(_np(out), ref[0])
 
 
+@pytest.mark.parametrize("ne0", [1024, 2048, 4096])
+def test_get_rows_q5k_staged_bad_ids_and_4_byte_table(gpu, ne0):
+    """The LDS-staged widths: ids out of range give a quiet-NaN row while the
+    rows around them stay exact; the same table 4 bytes off a 16-byte boundary
+    takes the per-super-block kernel, with the same bits."""
+    import torch
+    rng = np.random.default_rng(SEED + 11 + ne0)
+    rows = 40
+    raw = F.q5_k_synthetic(rng, rows, ne0)
+    ids = rng.integers(0, rows, 37).astype(np.int32)
+    ids[[3, 17, 36]] = [-1, rows, -(1 << 31)]
+    ok = (ids >= 0) & (ids < rows)
+    ref = R.run(lambda g: g.get_rows(raw, R.Q5_K, ne0, np.where(ok, ids, 0).astype(np.int32)))
+    got = _np(gpu.get_rows(_table(gpu, raw, ne0), _t(gpu, ids)))
+    assert np.isnan(got[~ok]).all()
+    assert_bitexact(got[ok], ref[ok])
+    buf = torch.zeros(raw.size + 4, dtype=torch.uint8, device="cuda")
+    buf[4:].copy_(torch.from_numpy(raw.reshape(-1)).cuda())
+    view = buf[4:].view(rows, raw.shape[1])
+    assert view.data_ptr() % 16 == 4
+    got4 = _np(gpu.get_rows(gpu.Q5KTensor(view, ne0), _t(gpu, ids)))
+    assert np.isnan(got4[~ok]).all()
+    assert_bitexact(got4[ok], ref[ok])
+
+
 @pytest.mark.parametrize("ne0,groups,frames", [(1024, 16, 4096), (1024, 15, 64), (256, 1, 33), (512, 3, 100),
                                                (2048, 9, 50), (4096, 4, 20), (1024, 33, 40), (1024, 1, 7),
                                                (3072, 2, 9)])
