@@ -760,7 +760,8 @@ PMC_OPS = [
     ("qk_norm_rope q[128,16,8192] k[128,8,8192]", 201359872), ("swiglu [6144,8192]", 603979776),
     ("add [2048,8192]", 201326592), ("snake [128,131072]", 134218240), ("snake_beta [128,131072]", 134218752),
     ("add_leaky_relu [128,131072]", 201326592), ("get_rows_sum q8_0 16x[1024,2048] x4096", 88342528),
-    ("get_rows q8_0 [1024,2048] x4096", 21250048), ("soft_max_ext causal-size [512,512,16]", 33554432)]
+    ("get_rows q8_0 [1024,2048] x4096", 21250048), ("soft_max_ext causal-size [512,512,16]", 33554432),
+    ("get_rows_sum q5_k 16x[1024,2048] x4096", 63176704), ("get_rows q5_k [1024,2048] x4096", 19677184)]
 
 
 def pmc_large(S, torch):
@@ -781,12 +782,14 @@ def pmc_large(S, torch):
     a4, b4 = randn(131072, 128), randn(131072, 128)
     tabs = [S.Q8Tensor(torch.from_numpy(F.q8_0_synthetic(rng, 2048, 1024)).cuda(), 1024) for _ in range(16)]
     codes = torch.randint(0, 2048, (16, 4096), generator=g, device="cuda", dtype=torch.int32)
+    tabs5 = [S.Q5KTensor(torch.from_numpy(F.q5_k_synthetic(rng, 2048, 1024)).cuda(), 1024) for _ in range(16)]
     sc = randn(16, 512, 512)
     fns = [lambda: S.rms_norm_mul(x2, w2, 1e-6), lambda: S.add_rms_norm_mul(x2, x2b, w2, 1e-6),
            lambda: S.qk_norm_rope(q, k, wq, wk, 1e-6, pos, 128, 1e6), lambda: S.swiglu(gt, up),
            lambda: S.add(x2, x2b), lambda: S.snake(xs, al), lambda: S.snake_beta(xs, la, lb),
            lambda: S.add_leaky_relu(a4, b4, 0.1), lambda: S.get_rows_sum(tabs, codes),
-           lambda: S.get_rows(tabs[0], codes[0]), lambda: S.soft_max_ext(sc, None, 0.0884)]
+           lambda: S.get_rows(tabs[0], codes[0]), lambda: S.soft_max_ext(sc, None, 0.0884),
+           lambda: S.get_rows_sum(tabs5, codes), lambda: S.get_rows(tabs5[0], codes[0])]
     n = CALIB_BYTES // 4
     src = torch.randn(n, device="cuda")
     dst = torch.empty_like(src)

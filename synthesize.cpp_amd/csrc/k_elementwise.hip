@@ -346,14 +346,15 @@ template <int K> __global__ __launch_bounds__(256) void k_snake_flat(const EwArg
 // then steps through its share of the tasks (R rows of one channel quad each)
 // with a grid stride, so the two exps per channel are spread over the block's
 // whole share instead of 8 rows. Measured on MI355X: at [128,131072] 8 %
-// faster than the 8-row kernel (2 rows per task, 2048 blocks); at [512,8192],
+// faster than the 8-row kernel (2 rows per task, 1024 blocks: 2048 measured
+// 0-4 % slower, one task per lane 6 % slower); at [512,8192],
 // one 4-row task per lane over 1024 blocks, 5 % faster (7.9 against 8.3 us).
 // At [256,32768] neither form beats the 8-row kernel. For plain Snake, whose
 // per-channel work is only the reciprocal, the grid stride measured 4-7 %
 // slower than one task per lane.
 constexpr int     kSnakeLdsMaxC     = 1024;
-constexpr int     kSnakeLdsBlocks   = 2048;
-constexpr int64_t kSnakeLdsMinTasks = int64_t{ 4 } * kSnakeLdsBlocks * 256;
+constexpr int     kSnakeLdsBlocks   = 1024;
+constexpr int64_t kSnakeLdsMinTasks = int64_t{ 8 } * kSnakeLdsBlocks * 256;
 constexpr int64_t kSnakeLdsSmallTasks = int64_t{ 1024 } * 256;
 
 template <int R> __global__ __launch_bounds__(256) void k_snake_beta_lds(const EwArgs a) {
