@@ -710,6 +710,85 @@ template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(1024) void k_
     }
 }
 
+// The same for a few positions (a decode step): the block's row waves take
+// their whole row through the QK-norm (and gains) before the barrier, while
+// one extra wave, after the rows, builds the position's cos/sin cache. The
+// wave that runs the serial theta chain then holds no rows, so the norm is no
+// longer behind the chain on the block's critical path: after the barrier a
+// row wave only rotates and stores. Same arithmetic as k_rope128, bit for
+// bit. At most kRopeDecMaxRows rows (the theta wave makes the block one wave
+// longer).
+constexpr int kRopeDecMaxRows = (1024 - kWave) / kRopeLanes;
+
+template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(1024) void k_rope128_dec(const RopeArgs a) {
+    __shared__ f32x4 s_cos[16];
+    __shared__ f32x4 s_sin[16];
+
+    const int64_t    pi    = blockIdx.x;
+    const int32_t    p     = a.pos[pi];  // before the field copies below: one scalar load
+    const RopeFields f     = rope_fields<KV>(a);
+    const int        total = rope_rows<KV>(f);
+    const int        rowt  = (total * kRopeLanes + kWave - 1) / kWave * kWave;  // threads of the row waves
+    const int        g     = threadIdx.x / kRopeLanes;
+    const int        l     = threadIdx.x % kRopeLanes;
+    const bool       theta = static_cast<int>(threadIdx.x) >= rowt;  // uniform over each wave
+    const bool       live  = !theta & (g < total);
+
+    RowRef r = rope_row<KV>(f, live ? g : 0, pi);
+    f32x4  lo = splat4(0.0f), hi = splat4(0.0f), rawlo = lo, rawhi = hi;
+    if (live) {
+        lo = ld_stream(to_global(reinterpret_cast<const f32x4 *>(r.x)) + l);
+        hi = ld_stream(to_global(reinterpret_cast<const f32x4 *>(r.x + 64)) + l);
+    }
+    WRaw<WT> wlo_raw{}, whi_raw{};
+    if constexpr (NORM && WT != kWNone) {
+        if (live && !r.copy) {
+            wlo_raw = load_wraw<WT>(r.w, 4 * l);
+            whi_raw = load_wraw<WT>(r.w, 64 + 4 * l);
+        }
+    }
+    const int64_t slot = rope_slot<KV>(a);
+    if (theta) {
+        const int   k   = static_cast<int>(threadIdx.x) - rowt;
+        const float mth = theta_chain64(static_cast<float>(p), a.theta_scale);
+        float       sv, cv;
+        rope_sincos(a.freq_scale * mth, sv, cv);
+        reinterpret_cast<float *>(s_cos)[k] = cv * a.attn_factor;
+        reinterpret_cast<float *>(s_sin)[k] = sv * a.attn_factor;
+    } else {
+        rawlo = lo;
+        rawhi = hi;
+        if constexpr (NORM) {
+            double acc        = sq4v(lo) + sq4v(hi);
+            acc               = group_sum<kRopeLanes>(acc);
+            const float scale = norm_scale(acc, 128, a.eps);
+            lo                = f32x4{ lo.x * scale, lo.y * scale, lo.z * scale, lo.w * scale };
+            hi                = f32x4{ hi.x * scale, hi.y * scale, hi.z * scale, hi.w * scale };
+            if constexpr (WT != kWNone) {
+                const f32x4 wlo = cvt_wraw<WT>(wlo_raw);
+                const f32x4 whi = cvt_wraw<WT>(whi_raw);
+                lo = f32x4{ lo.x * wlo.x, lo.y * wlo.y, lo.z * wlo.z, lo.w * wlo.w };
+                hi = f32x4{ hi.x * whi.x, hi.y * whi.y, hi.z * whi.z, hi.w * whi.w };
+            }
+        }
+    }
+    __syncthreads();
+    if (!live) {
+        return;
+    }
+    const f32x4 cs = s_cos[l];
+    const f32x4 sn = s_sin[l];
+    const f32x4 olo{ lo.x * cs.x - hi.x * sn.x, lo.y * cs.y - hi.y * sn.y, lo.z * cs.z - hi.z * sn.z,
+                     lo.w * cs.w - hi.w * sn.w };
+    const f32x4 ohi{ lo.x * sn.x + hi.x * cs.x, lo.y * sn.y + hi.y * cs.y, lo.z * sn.z + hi.z * cs.z,
+                     lo.w * sn.w + hi.w * cs.w };
+    if (!KV || slot >= 0 || !r.kv) {
+        float * y = r.y_at(slot);
+        st_stream(to_global(reinterpret_cast<f32x4 *>(y)) + l, KV && r.copy ? rawlo : olo);
+        st_stream(to_global(reinterpret_cast<f32x4 *>(y + 64)) + l, KV && r.copy ? rawhi : ohi);
+    }
+}
+
 // Any head_dim / n_dims: one wave per head row; the theta recurrence is
 // replayed per pair (fine for the small shapes that take this path).
 template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(256) void k_rope_generic(const RopeArgs a) {
@@ -769,11 +848,23 @@ template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(256) void k_r
     }
 }
 
+// Up to this many positions a launch takes k_rope128_dec (a decode step of
+// a few streams); longer ones k_rope128, whose blocks hide the theta chain
+// behind each other. Measured on MI355X, 28-layer decode graphs: one stream
+// 7.95 -> 7.64 us per layer (4 launches), 64 streams 9.97 -> 10.12 us.
+constexpr int64_t kRopeDecMaxPos = 16;
+
 template <bool NORM, int WT, bool KV> shp_status_t launch_rope(const RopeArgs & a, bool fast, hipStream_t stream) {
     if (dry_run()) {
         return SHP_OK;
     }
     const int total = a.part[0].heads + a.part[1].heads + a.part[2].heads;
+    if (fast && a.npos <= kRopeDecMaxPos && total <= kRopeDecMaxRows) {
+        const int threads = (total * kRopeLanes + kWave - 1) / kWave * kWave + kWave;
+        hipLaunchKernelGGL((k_rope128_dec<NORM, WT, KV>), dim3(static_cast<unsigned>(a.npos)), dim3(threads), 0,
+                           stream, a);
+        return launch_status();
+    }
     if (fast) {
         const int rows    = total < kRopeMaxRows ? total : kRopeMaxRows;
         const int threads = ((rows * kRopeLanes + kWave - 1) / kWave) * kWave;

@@ -443,8 +443,12 @@ def test_rope_in_place_and_scaled(gpu):
                                                           np.float32(1.25), cs_rounded=True)))
 
 
-@pytest.mark.parametrize("T,hi,wkind", [(1, 64, "bf16"), (512, 512, "bf16"), (300, 8192, "f32"), (64, 8192, "f16")])
+@pytest.mark.parametrize("T,hi,wkind", [(1, 64, "bf16"), (512, 512, "bf16"), (300, 8192, "f32"), (64, 8192, "f16"),
+                                        (16, 8192, "f32"), (7, 32768, "f16"), (3, 8192, "bf16")])
 def test_qk_norm_rope(gpu, T, hi, wkind):
+    """T <= 16 takes the decode-step kernel (a separate wave builds the cos/sin
+    cache), longer runs the one whose wave 0 does; both bit-exact against the
+    restatement with correctly rounded cos/sin."""
     rng = np.random.default_rng(SEED + T)
     q = rng.standard_normal((T, 16, 128)).astype(np.float32)
     k = rng.standard_normal((T, 8, 128)).astype(np.float32)
