@@ -82,6 +82,10 @@ def parse():
     p.add_argument("--trace-summary", nargs=2, metavar=("ROCPROF_DIR", "BENCH_LOG"),
                    help="instead: summarise a rocprofv3 --kernel-trace --marker-trace run of this command "
                    "(per-row kernel durations against the bench line in BENCH_LOG); no GPU used")
+    p.add_argument("--occ-summary", nargs="+", metavar="DIR",
+                   help="instead: occupancy, VALU and memory-stall per --pmc-large op from rocprofv3 --pmc passes "
+                   "of OccupancyPercent, MeanOccupancyPerCU, VALUBusy, MemUnitStalled (one DIR each, that order); "
+                   "no GPU used")
     p.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "LOG"),
                    help="instead: HBM bytes per launch from FETCH_SIZE and WRITE_SIZE passes over --pmc-large "
                    "(LOG: that run's output, for the op list); no GPU used")
@@ -422,11 +426,17 @@ def vocoder_rows(R, S, torch, cfg, seed, shapes=((512, 8192), (256, 32768), (128
             ts, y = [randn(T, C) for _ in range(3)], empty(T, C)
             return lambda: S.sum_scale_leaky_relu(ts, 1.0 / 3.0, 0.1, out=y)
 
+        def make_bare(C=C, T=T):
+            x, y = randn(T, C), empty(T, C)
+            return lambda: S.leaky_relu(x, 0.1, out=y)
+
         out.append(R.run(cfg, "snake [%d,%d]" % (C, T), 8 * n + 4 * C, make_snake))
         out.append(R.run(cfg, "snake_beta [%d,%d]" % (C, T), 8 * n + 8 * C, make_beta))
         out.append(R.run(cfg, "add_leaky_relu [%d,%d]" % (C, T), 12 * n, make_leaky))
         out.append(R.run(cfg, "add_leaky_relu+sum [%d,%d]" % (C, T), 16 * n, lambda: make_leaky(with_s=True)))
         if variants:
+            # the size's streaming floor: one read and one write with no work
+            out.append(R.run(cfg, "copy-like floor: bare leaky [%d,%d]" % (C, T), 8 * n, make_bare))
             out.append(R.run(cfg, "snake_guarded [%d,%d]" % (C, T), 8 * n + 4 * C, make_guarded))
             out.append(R.run(cfg, "branch mean 3->scale->leaky [%d,%d]" % (C, T), 16 * n, make_branch))
     return out
@@ -922,6 +932,39 @@ def pmc_summary(fetch_dir, write_dir, log):
     print("\n".join(out))
 
 
+OCC_METRICS = ("OccupancyPercent", "MeanOccupancyPerCU", "VALUBusy", "MemUnitStalled")
+
+
+def occ_summary(dirs):
+    """Per --pmc-large op: the average over its three launches of each derived
+    metric (one rocprofv3 --pmc pass per metric), with the dispatch's register
+    and LDS use from the same records."""
+    if len(dirs) != len(OCC_METRICS):
+        raise SystemExit("--occ-summary takes %d directories: %s" % (len(OCC_METRICS), ", ".join(OCC_METRICS)))
+    passes = []
+    for d in dirs:
+        rows = list(csv.DictReader(open(_one(os.path.join(d, "**", "*counter_collection.csv")))))
+        rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+        passes.append([r for r in rows if short_kernel(r["Kernel_Name"]).startswith("k_")])
+    n = len(passes[0])
+    assert all(len(p) == n for p in passes) and n == 3 * len(PMC_OPS), ([len(p) for p in passes], len(PMC_OPS))
+    out = ["# Occupancy, VALU and memory-unit stall per large-config kernel, MI355X gfx950: one rocprofv3 --pmc",
+           "# pass per derived metric over `bench.py --pmc-large` (three launches per op, one input set), averaged",
+           "# over the three. occ% = resident waves as a % of the maximum (OccupancyPercent); w/CU = waves resident",
+           "# per CU, time-averaged (MeanOccupancyPerCU); valu% = % of time a CU issues VALU (VALUBusy); mstl% =",
+           "# % of time the memory unit is stalled on data (MemUnitStalled); vgpr/sgpr/lds from the dispatch",
+           "# records (lds in bytes per workgroup).",
+           "%-44s %-34s %9s %7s %7s %7s %7s %5s %5s %6s" % ("op", "kernel", "grid", "occ%", "w/CU", "valu%", "mstl%",
+                                                          "vgpr", "sgpr", "lds")]
+    for j, (op, _) in enumerate(PMC_OPS):
+        vals = [statistics.mean(float(p[i]["Counter_Value"]) for i in range(3 * j, 3 * j + 3)) for p in passes]
+        r = passes[0][3 * j]
+        out.append("%-44s %-34s %9d %7.1f %7.2f %7.1f %7.1f %5s %5s %6s" % (
+            op[:44], short_kernel(r["Kernel_Name"])[:34], _grid(r), vals[0], vals[1], vals[2], vals[3],
+            r.get("VGPR_Count", "-"), r.get("SGPR_Count", "-"), r.get("LDS_Block_Size", "-")))
+    print("\n".join(out))
+
+
 def read_traffic(op):
     """HBM bytes per launch of `op` from the committed counter summary, or None."""
     if not os.path.exists(TRAFFIC_FILE):
@@ -944,6 +987,9 @@ def main():
         return
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
+        return
+    if args.occ_summary:
+        occ_summary(args.occ_summary)
         return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build is single-GPU by design. The primitives are "
