@@ -211,10 +211,20 @@ def test_get_rows_batched_and_out_of_range(gpu):
     out = _np(gpu.get_rows(tab, bad))
     assert np.isnan(out[1]).all() and np.isnan(out[2]).all()
     assert_bitexact(out[[0, 3]], _np(tab)[[3, 9]])
-    raw = F.q8_0_synthetic(rng, 10, 1024)
-    out = _np(gpu.get_rows(gpu.Q8Tensor(_t(gpu, raw), 1024), bad))
-    assert np.isnan(out[1]).all() and np.isnan(out[2]).all()
-    assert_bitexact(out[[0, 3]], F.q8_0_dequant(raw, 1024)[[3, 9]])
+    for ne0 in (1024, 2048, 4096):  # the LDS-staged widths: row 0 is read for a bad id, NaN stored
+        raw = F.q8_0_synthetic(rng, 10, ne0)
+        out = _np(gpu.get_rows(gpu.Q8Tensor(_t(gpu, raw), ne0), bad))
+        assert np.isnan(out[1]).all() and np.isnan(out[2]).all()
+        assert_bitexact(out[[0, 3]], F.q8_0_dequant(raw, ne0)[[3, 9]])
+    # the staged Q8_0 kernel in ggml's batch form: table [1024, 12, 2], ids [7, 2]
+    raw2 = np.stack([F.q8_0_synthetic(rng, 12, 1024) for _ in range(2)])
+    ids2 = rng.integers(0, 12, (2, 7)).astype(np.int32)
+    ids2[1, 3] = 12
+    got2 = _np(gpu.get_rows(gpu.Q8Tensor(_t(gpu, raw2), 1024), _t(gpu, ids2)))
+    for b in range(2):
+        ok = ids2[b] < 12
+        assert_bitexact(got2[b][ok], F.q8_0_dequant(raw2[b], 1024)[ids2[b][ok]])
+        assert np.isnan(got2[b][~ok]).all()
     del torch
 
 
