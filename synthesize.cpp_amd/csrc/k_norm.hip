@@ -274,13 +274,22 @@ template <int WT, int MODE> shp_status_t launch_norm(const NormArgs & a, bool ve
         if (nvec <= 128) {
             return go(k_rms_norm_vec<128, 1, WT, MODE>, 2);
         }
-        // Rows of 1024 / 2048: with at least 4096 of them, one wave per row
-        // (no LDS round trip, no barrier) is faster -- measured on MI355X:
-        // rms_norm [1024,8192] -20 %, [2048,4096] and [2048,8192] -6 %,
-        // add+norm [2048,4096] -9 %; with fewer rows, and for the add forms
-        // at 1024 (+3 %), four waves per row keep more loads in flight and win.
+        // Rows of 1024 / 2048 with at least 4096 of them, measured on MI355X
+        // against one 256-lane block per row:
+        //   - plain 1024: one wave per row (no LDS round trip, no barrier),
+        //     -20 % at [1024,8192] (two waves per row: +10 % over one);
+        //   - plain 2048: two waves per row (4 float4 per lane, the partial
+        //     sums combined through LDS), at the same-size copy's speed
+        //     (22.8 against 23.8 us for one wave per row at [2048,8192]);
+        //   - add forms at 2048: one wave per row, -9 % at [2048,4096] (two
+        //     waves per row: +6 %, each lane holding both operands);
+        //   - add forms at 1024, and fewer rows: four waves per row keep more
+        //     loads in flight and win.
         if (a.nrows >= 4096 && nvec == 256 && MODE == kPlain) {
             return go(k_rms_norm_vec<64, 4, WT, MODE>, 4);
+        }
+        if (a.nrows >= 4096 && nvec == 512 && MODE == kPlain) {
+            return go(k_rms_norm_vec<128, 4, WT, MODE>, 2);
         }
         if (a.nrows >= 4096 && nvec == 512) {
             return go(k_rms_norm_vec<64, 8, WT, MODE>, 4);
