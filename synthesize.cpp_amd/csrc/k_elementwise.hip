@@ -149,17 +149,25 @@ template <int OP> __device__ __forceinline__ f32x4 ew4(f32x4 a, f32x4 b, const E
 // HAS_B: a second input; BCAST: b is one row of `period` elements repeated
 // over rows; Snake reads alpha the same way; HAS_S: write the carried sum.
 constexpr int64_t kMaxFlatBlocks = int64_t{ 1 } << 20;
+// From this many float4 per operand (16 MB) the flat kernels launch 64-thread
+// blocks, one wave each: measured on MI355X 1-3.5 % faster from [512,8192]
+// up (SwiGLU [6144,8192] 93.0 -> 91.2 us, add->leaky+sum [128,131072] 44.2 ->
+// 43.6 us), and 1-4 % slower below (a 512-token add, a decode step's SwiGLU),
+// where 256-thread blocks stay. The Snake and RMSNorm kernels keep 256-thread
+// blocks at every size: one-wave blocks measured 2 % (Snake [128,131072]) and
+// 2-6 % (the [2048,8192] norms) slower.
+constexpr int64_t kFlatWaveBlocksFrom = int64_t{ 1 } << 20;
 
-template <int OP, bool HAS_B, bool BCAST, bool HAS_S>
-__global__ __launch_bounds__(256) void k_ew_flat(const EwArgs a) {
+template <int OP, bool HAS_B, bool BCAST, bool HAS_S, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void k_ew_flat(const EwArgs a) {
     const f32x4 * A    = reinterpret_cast<const f32x4 *>(a.a);
     const f32x4 * B    = reinterpret_cast<const f32x4 *>(a.b);
     f32x4 *       Y    = reinterpret_cast<f32x4 *>(a.y);
     f32x4 *       S    = reinterpret_cast<f32x4 *>(a.s);
     const int64_t n4   = a.n4;
-    const int64_t step = static_cast<int64_t>(gridDim.x) * 256;
+    const int64_t step = static_cast<int64_t>(gridDim.x) * BLOCK;
     args_in_sgprs(A, B, Y, n4, step);
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n4; i += step) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * BLOCK + threadIdx.x; i < n4; i += step) {
         const f32x4 av = ld_stream(A + i);
         f32x4       bv = splat4(0.0f);
         if constexpr (HAS_B) {
@@ -286,19 +294,19 @@ __device__ __forceinline__ void snake_rows(const f32x4 (&xv)[R], f32x4 al, f32x4
     }
 }
 
-template <int K> __global__ __launch_bounds__(256) void k_snake_flat(const EwArgs a) {
+template <int K, int BLOCK> __global__ __launch_bounds__(BLOCK) void k_snake_flat(const EwArgs a) {
     constexpr int R    = SnakeRows<K>::R;
     const f32x4 * X    = reinterpret_cast<const f32x4 *>(a.a);
     const f32x4 * C0   = reinterpret_cast<const f32x4 *>(a.alpha);
     const f32x4 * C1   = reinterpret_cast<const f32x4 *>(a.beta);
     f32x4 *       Y    = reinterpret_cast<f32x4 *>(a.y);
     const int64_t c4   = a.quads.d;
-    const int64_t step = static_cast<int64_t>(gridDim.x) * 256;
+    const int64_t step = static_cast<int64_t>(gridDim.x) * BLOCK;
     args_in_sgprs(X, C0, C1, a.quads.d, a.quads.m, a.quads.l, a.ntask, a.n4, step);
     // A lane's task: its curves and its R rows, requested together, so the
     // per-channel work waits for one round trip, in parallel with the rows
     // (the loop runs once unless the grid is capped).
-    int64_t  t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    int64_t  t = static_cast<int64_t>(blockIdx.x) * BLOCK + threadIdx.x;
     uint32_t q;
     int64_t  i0;
     f32x4    c0, c1, xv[R];
@@ -540,10 +548,17 @@ shp_status_t launch_ew(const EwArgs & a, bool flat, bool vec, hipStream_t stream
         return SHP_OK;
     }
     if (flat) {
-        int64_t blocks = (a.n4 + 255) / 256;
-        blocks         = blocks < kMaxFlatBlocks ? blocks : kMaxFlatBlocks;
-        hipLaunchKernelGGL((k_ew_flat<OP, HAS_B, BCAST, HAS_S>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                           stream, a);
+        const bool wave = a.n4 >= kFlatWaveBlocksFrom;
+        const int  bs   = wave ? kWave : 256;
+        int64_t    blocks = (a.n4 + bs - 1) / bs;
+        blocks            = blocks < kMaxFlatBlocks ? blocks : kMaxFlatBlocks;
+        if (wave) {
+            hipLaunchKernelGGL((k_ew_flat<OP, HAS_B, BCAST, HAS_S, kWave>), dim3(static_cast<unsigned>(blocks)),
+                               dim3(kWave), 0, stream, a);
+        } else {
+            hipLaunchKernelGGL((k_ew_flat<OP, HAS_B, BCAST, HAS_S, 256>), dim3(static_cast<unsigned>(blocks)), dim3(256),
+                               0, stream, a);
+        }
         return launch_status();
     }
     const int64_t blocks = a.nrows < 65536 ? a.nrows : 65536;
@@ -715,7 +730,7 @@ shp_status_t launch_snake(const shp_tensor * x, const shp_tensor * c0, const shp
         g.ntask              = (rows + R - 1) / R * quads;
         int64_t       blocks = (g.ntask + 255) / 256;
         blocks               = blocks < kMaxFlatBlocks ? blocks : kMaxFlatBlocks;
-        hipLaunchKernelGGL(k_snake_flat<K>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, g);
+        hipLaunchKernelGGL((k_snake_flat<K, 256>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, g);
         return launch_status();
     }
     const int64_t blocks = g.nrows < 65536 ? g.nrows : 65536;
