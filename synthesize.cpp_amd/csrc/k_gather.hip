@@ -636,21 +636,23 @@ __device__ __forceinline__ void q8_row_decode_store(const uint32_t * lds, int l,
     }
 }
 
-constexpr int kQ8StageWaves = 4;  // waves (rows or frames) per 256-thread block
+// Rows (waves) per block of the LDS-staged get_rows: 4 measured 1-2 % faster
+// than one-wave blocks at [1024,2048] x4096 (Q8_0 and Q5_K).
+constexpr int kStagedWpb = 4;
 
 // One wave per row. An id out of range reads row 0 of the table and stores
 // NaN, with no branch between the id and the row loads; each quad is stored
 // as soon as it is decoded. Measured on MI355X at [1024,2048] x4096 against
 // the branch on the id with all 16 values stored at the end: 4.54 against
 // 4.68 us.
-template <int NQ> __global__ __launch_bounds__(256) void k_get_rows_q8s(const GatherArgs a) {
+template <int NQ, int WPB> __global__ __launch_bounds__(WPB * kWave) void k_get_rows_q8s(const GatherArgs a) {
     gather_args_in_sgprs(a);
-    __shared__ uint32_t s_row[kQ8StageWaves][q8_row_dwords(NQ) + kQ8StagePadDwords];
+    __shared__ uint32_t s_row[WPB][q8_row_dwords(NQ) + kQ8StagePadDwords];
     // The row is uniform over the wave: readfirstlane lets the id be one scalar
     // load and the table row base a scalar.
     const int           w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
     const int           l = static_cast<int>(threadIdx.x) % kWave;
-    const int64_t       R = static_cast<int64_t>(blockIdx.x) * kQ8StageWaves + w;
+    const int64_t       R = static_cast<int64_t>(blockIdx.x) * WPB + w;
     if (R >= a.total) {
         return;  // no block barrier below: only this wave uses s_row[w]
     }
@@ -741,14 +743,14 @@ __global__ __launch_bounds__(256) void k_get_rows_q5k(const GatherArgs a) {
 // round, then decodes each super-block's 4 elements per lane from LDS as
 // above -- a few wide loads in front of the decode instead of six dword loads
 // per super-block and lane. An id out of range reads row 0 and stores NaN.
-template <int NSB> __global__ __launch_bounds__(256) void k_get_rows_q5ks(const GatherArgs a) {
+template <int NSB, int WPB> __global__ __launch_bounds__(WPB * kWave) void k_get_rows_q5ks(const GatherArgs a) {
     gather_args_in_sgprs(a);
     constexpr int kWords  = 11 * NSB;  // 16-byte words per row
     constexpr int kRounds = (kWords + kWave - 1) / kWave;
-    __shared__ u32x4 s_row[kQ8StageWaves][kWords];
+    __shared__ u32x4 s_row[WPB][kWords];
     const int        w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
     const int        l = static_cast<int>(threadIdx.x) % kWave;
-    const int64_t    R = static_cast<int64_t>(blockIdx.x) * kQ8StageWaves + w;
+    const int64_t    R = static_cast<int64_t>(blockIdx.x) * WPB + w;
     if (R >= a.total) {
         return;  // no block barrier below: only this wave uses s_row[w]
     }
@@ -930,29 +932,32 @@ template <int TYPE> shp_status_t launch_get_rows(const GatherArgs & a, bool vec,
     }
     if (vec) {
         if constexpr (TYPE == SHP_TYPE_Q5_K) {
-            const dim3 grid(static_cast<unsigned>((a.total + 3) / 4));
+            const dim3 grid(static_cast<unsigned>((a.total + kStagedWpb - 1) / kStagedWpb));
+            const dim3 block(kStagedWpb * kWave);
             if (a.staged && a.ne0 == 1024) {
-                hipLaunchKernelGGL(k_get_rows_q5ks<4>, grid, dim3(256), 0, stream, a);
+                hipLaunchKernelGGL((k_get_rows_q5ks<4, kStagedWpb>), grid, block, 0, stream, a);
             } else if (a.staged && a.ne0 == 2048) {
-                hipLaunchKernelGGL(k_get_rows_q5ks<8>, grid, dim3(256), 0, stream, a);
+                hipLaunchKernelGGL((k_get_rows_q5ks<8, kStagedWpb>), grid, block, 0, stream, a);
             } else if (a.staged && a.ne0 == 4096) {
-                hipLaunchKernelGGL(k_get_rows_q5ks<16>, grid, dim3(256), 0, stream, a);
+                hipLaunchKernelGGL((k_get_rows_q5ks<16, kStagedWpb>), grid, block, 0, stream, a);
             } else {
-                hipLaunchKernelGGL(k_get_rows_q5k, grid, dim3(256), 0, stream, a);
+                hipLaunchKernelGGL(k_get_rows_q5k, dim3(static_cast<unsigned>((a.total + 3) / 4)), dim3(256), 0, stream,
+                                   a);
             }
             return launch_status();
         } else if constexpr (TYPE == SHP_TYPE_Q8_0) {
             if (a.staged) {
-                const int64_t blocks = (a.total + kQ8StageWaves - 1) / kQ8StageWaves;
+                const dim3 grid(static_cast<unsigned>((a.total + kStagedWpb - 1) / kStagedWpb));
+                const dim3 block(kStagedWpb * kWave);
                 switch (a.ne0) {
                     case 1024:
-                        hipLaunchKernelGGL(k_get_rows_q8s<4>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                        hipLaunchKernelGGL((k_get_rows_q8s<4, kStagedWpb>), grid, block, 0, stream, a);
                         break;
                     case 2048:
-                        hipLaunchKernelGGL(k_get_rows_q8s<8>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                        hipLaunchKernelGGL((k_get_rows_q8s<8, kStagedWpb>), grid, block, 0, stream, a);
                         break;
                     default:
-                        hipLaunchKernelGGL(k_get_rows_q8s<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                        hipLaunchKernelGGL((k_get_rows_q8s<16, kStagedWpb>), grid, block, 0, stream, a);
                         break;
                 }
                 return launch_status();
