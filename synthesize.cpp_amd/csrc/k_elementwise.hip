@@ -208,7 +208,8 @@ template <int K> __device__ __forceinline__ SnakeCoef snake_coef(float c0, float
 // t = x*al. FAST: t is known to be inside the fast sine's range. RCP: divide
 // through the double reciprocal of den (IEEE quotient, shp_div.hpp).
 template <bool FAST, bool RCP> __device__ __forceinline__ float snake_t(float x, float t, float den, double rcp) {
-    const float sn = FAST ? sin_f32_fast(t) : (sin_fast_ok(t) ? sin_f32_fast(t) : sinf(t));
+    // squared below, so the fast path may drop the sine's sign (bit-identical square)
+    const float sn = FAST ? sin_f32_fast_unsigned(t) : (sin_fast_ok(t) ? sin_f32_fast(t) : sinf(t));
     const float q  = sn * sn;
     const float r  = RCP ? div_by_rcp(q, rcp) : q / den;
     return x + r;

@@ -38,6 +38,25 @@ SHP_HD inline bool sin_fast_ok(float t) {
     return std::fabs(t) < kSinFastLimit;
 }
 
+// +-sin t: sin_f32_fast(t) up to its sign, without the quadrant's sign flip.
+// For a caller that squares the sine (Snake's sin^2): (-v)*(-v) and v*v are
+// the same f32 product, so the square is bit for bit sin_f32_fast(t)^2.
+SHP_HD inline float sin_f32_fast_unsigned(float t) {
+    const float k = std::rint(t * 0x1.45f306p-1f);  // t * 2/pi
+    float       r = std::fma(-k, 0x1.921fb6p+0f, t);
+    r             = std::fma(-k, -0x1.777a5cp-25f, r);
+    r             = std::fma(-k, -0x1.ee59dap-50f, r);
+    const float z = r * r;
+    float       s = std::fma(z, -0x1.9ac6cep-13f, 0x1.110c22p-7f);
+    s             = std::fma(z, s, -0x1.555552p-3f);
+    s             = std::fma(r * z, s, r);
+    float c       = std::fma(z, 0x1.9a6dp-16f, -0x1.6c0e02p-10f);
+    c             = std::fma(z, c, 0x1.55554cp-5f);
+    c             = std::fma(z, c, -0.5f);
+    c             = std::fma(z, c, 1.0f);
+    return (static_cast<int>(k) & 1) ? c : s;
+}
+
 SHP_HD inline float sin_f32_fast(float t) {
     const float k = std::rint(t * 0x1.45f306p-1f);  // t * 2/pi
     float       r = std::fma(-k, 0x1.921fb6p+0f, t);
