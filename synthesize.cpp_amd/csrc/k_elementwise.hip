@@ -157,6 +157,10 @@ constexpr int64_t kMaxFlatBlocks = int64_t{ 1 } << 20;
 // blocks at every size: one-wave blocks measured 2 % (Snake [128,131072]) and
 // 2-6 % (the [2048,8192] norms) slower.
 constexpr int64_t kFlatWaveBlocksFrom = int64_t{ 1 } << 20;
+// From 4 MB per operand up to that size, two float4 per lane
+// (k_ew_flat2): SwiGLU [3072,512] 4.81 -> 4.66 us; at [1024,512] (2 MB per
+// operand) it measured 1 % slower than one float4 per lane.
+constexpr int64_t kFlat2From = int64_t{ 1 } << 18;
 
 template <int OP, bool HAS_B, bool BCAST, bool HAS_S, int BLOCK>
 __global__ __launch_bounds__(BLOCK) void k_ew_flat(const EwArgs a) {
@@ -543,10 +547,53 @@ template <int N> shp_status_t launch_sum_scale_leaky(const TermArgs & a, bool ve
     return launch_status();
 }
 
+// Two float4 per lane and operand (a block covers 512 consecutive float4),
+// every load issued before the first store; for mid-size tensors.
+template <int OP, bool HAS_B, bool BCAST, bool HAS_S>
+__global__ __launch_bounds__(256) void k_ew_flat2(const EwArgs a) {
+    const f32x4 * A  = reinterpret_cast<const f32x4 *>(a.a);
+    const f32x4 * B  = reinterpret_cast<const f32x4 *>(a.b);
+    f32x4 *       Y  = reinterpret_cast<f32x4 *>(a.y);
+    f32x4 *       S  = reinterpret_cast<f32x4 *>(a.s);
+    const int64_t n4 = a.n4;
+    args_in_sgprs(A, B, Y, n4);
+    const int64_t i0 = static_cast<int64_t>(blockIdx.x) * 512 + threadIdx.x;
+    f32x4         av[2], bv[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int64_t i = i0 + 256 * k < n4 ? i0 + 256 * k : n4 - 1;  // past the end: re-read the last chunk
+        av[k]           = ld_stream(A + i);
+        bv[k]           = splat4(0.0f);
+        if constexpr (HAS_B) {
+            if constexpr (BCAST) {
+                bv[k] = B[fastmod(static_cast<uint32_t>(i * 4), a.period) / 4];
+            } else {
+                bv[k] = ld_stream(B + i);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int64_t i = i0 + 256 * k;
+        if (i < n4) {
+            f32x4 sv = splat4(0.0f);
+            st_stream(Y + i, ew4<OP>(av[k], bv[k], a, sv));
+            if constexpr (HAS_S) {
+                st_stream(S + i, sv);
+            }
+        }
+    }
+}
+
 template <int OP, bool HAS_B, bool BCAST, bool HAS_S>
 shp_status_t launch_ew(const EwArgs & a, bool flat, bool vec, hipStream_t stream) {
     if (dry_run()) {
         return SHP_OK;
+    }
+    if (flat && a.n4 >= kFlat2From && a.n4 < kFlatWaveBlocksFrom) {
+        hipLaunchKernelGGL((k_ew_flat2<OP, HAS_B, BCAST, HAS_S>), dim3(static_cast<unsigned>((a.n4 + 511) / 512)),
+                           dim3(256), 0, stream, a);
+        return launch_status();
     }
     if (flat) {
         const bool wave = a.n4 >= kFlatWaveBlocksFrom;

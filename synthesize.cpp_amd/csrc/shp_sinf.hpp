@@ -58,21 +58,8 @@ SHP_HD inline float sin_f32_fast_unsigned(float t) {
 }
 
 SHP_HD inline float sin_f32_fast(float t) {
-    const float k = std::rint(t * 0x1.45f306p-1f);  // t * 2/pi
-    float       r = std::fma(-k, 0x1.921fb6p+0f, t);
-    r             = std::fma(-k, -0x1.777a5cp-25f, r);
-    r             = std::fma(-k, -0x1.ee59dap-50f, r);
-    const float z = r * r;
-    float       s = std::fma(z, -0x1.9ac6cep-13f, 0x1.110c22p-7f);
-    s             = std::fma(z, s, -0x1.555552p-3f);
-    s             = std::fma(r * z, s, r);
-    float c       = std::fma(z, 0x1.9a6dp-16f, -0x1.6c0e02p-10f);
-    c             = std::fma(z, c, 0x1.55554cp-5f);
-    c             = std::fma(z, c, -0.5f);
-    c             = std::fma(z, c, 1.0f);
-    const int   q = static_cast<int>(k);
-    const float v = (q & 1) ? c : s;
-    return (q & 2) ? -v : v;
+    const float v = sin_f32_fast_unsigned(t);
+    return (static_cast<int>(std::rint(t * 0x1.45f306p-1f)) & 2) ? -v : v;  // the quadrant's sign
 }
 
 }  // namespace shp

@@ -682,8 +682,12 @@ def test_soft_max_ext_special_rows(gpu):
 # elementwise
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("shape", [(512, 3072), (3, 6144), (7, 1001), (1, 3072), (16, 4)])
+@pytest.mark.parametrize("shape", [(512, 3072), (3, 6144), (7, 1001), (1, 3072), (16, 4), (401, 3071)])
 def test_swiglu_and_silu(gpu, shape):
+    """Every flat launch form: one float4 per lane in 256-lane blocks, two per
+    lane from 4 MB per operand ((512, 3072), and (401, 3071) with a partial
+    last block), one-wave blocks from 16 MB (the configs[4] shape in
+    test_gpu_full_configs.py)."""
     rng = np.random.default_rng(SEED + sum(shape))
     gt = (rng.standard_normal(shape) * 4).astype(np.float32)
     up = rng.standard_normal(shape).astype(np.float32)
@@ -970,7 +974,7 @@ def _specials(n, rng):
     return v
 
 
-@pytest.mark.parametrize("shape", [(128, 8192), (33, 77), (1, 4)])
+@pytest.mark.parametrize("shape", [(128, 8192), (33, 77), (1, 4), (301, 3500), (512, 8192)])
 @pytest.mark.parametrize("slope", [0.1, 0.01])
 def test_add_leaky_relu_bitexact(gpu, shape, slope):
     rng = np.random.default_rng(SEED + shape[1])
@@ -989,10 +993,13 @@ def test_add_leaky_relu_bitexact(gpu, shape, slope):
 
 
 @pytest.mark.parametrize("bshape", ["full", "row"])
-def test_add(gpu, bshape):
-    rng = np.random.default_rng(19)
-    a = rng.standard_normal((37, 1024)).astype(np.float32)
-    b = rng.standard_normal((37, 1024) if bshape == "full" else (1024,)).astype(np.float32)
+@pytest.mark.parametrize("shape", [(37, 1024), (1001, 1100), (4099, 1028)])
+def test_add(gpu, bshape, shape):
+    """A full second operand or one broadcast row, in each flat launch form
+    (2, 4.4 and 16.9 MB per operand)."""
+    rng = np.random.default_rng(19 + shape[0])
+    a = rng.standard_normal(shape).astype(np.float32)
+    b = rng.standard_normal(shape if bshape == "full" else (shape[1],)).astype(np.float32)
     assert_bitexact(_np(gpu.add(_t(gpu, a), _t(gpu, b))), R.run(lambda g: g.add(a, b)))
 
 
