@@ -352,23 +352,22 @@ template <int K, int BLOCK> __global__ __launch_bounds__(BLOCK) void k_snake_fla
 }
 
 
-// SnakeBeta with at most kSnakeLdsMaxC channels, on tensors of at least
-// kSnakeLdsMinTasks 2-row lane tasks or at most kSnakeLdsSmallTasks 4-row
-// tasks: each block first evaluates every channel's exp curves, guard and
-// double reciprocal once into LDS (the first task's rows already requested),
-// then steps through its share of the tasks (R rows of one channel quad each)
-// with a grid stride, so the two exps per channel are spread over the block's
-// whole share instead of 8 rows. Measured on MI355X: at [128,131072] 8 %
-// faster than the 8-row kernel (2 rows per task, 1024 blocks: 2048 measured
-// 0-4 % slower, one task per lane 6 % slower); at [512,8192],
-// one 4-row task per lane over 1024 blocks, 5 % faster (7.9 against 8.3 us).
-// At [256,32768] neither form beats the 8-row kernel. For plain Snake, whose
-// per-channel work is only the reciprocal, the grid stride measured 4-7 %
-// slower than one task per lane.
-constexpr int     kSnakeLdsMaxC     = 1024;
-constexpr int     kSnakeLdsBlocks   = 1024;
-constexpr int64_t kSnakeLdsMinTasks = int64_t{ 8 } * kSnakeLdsBlocks * 256;
-constexpr int64_t kSnakeLdsSmallTasks = int64_t{ 1024 } * 256;
+// SnakeBeta with at most kSnakeLdsMaxC channels: each block requests its
+// lanes' rows, evaluates every channel's exp curves, guard and double
+// reciprocal once into LDS meanwhile, and after one barrier each lane runs its
+// task (R rows of one channel quad) from the table. One task per lane: R = 4
+// up to kSnakeLdsSmallTasks tasks, else R = 8 (the two exps per channel are
+// spread over the block's 2048 or 4096 elements instead of 8 or 32 per lane).
+// Measured on MI355X: [512,8192] 8.4 -> 8.2 us and [256,32768] 13.1 ->
+// 12.7 us against the 8-row flat kernel, [128,131072] 25.4 -> 24.7 us against
+// 2-row tasks over 1024 persistent blocks. Rejected at that shape: 2048
+// persistent blocks, per-wave LDS exp tables, 512- or 1024-thread blocks,
+// each lane keeping its quad's curves in registers for all its tasks. For
+// plain Snake, whose per-channel work is only the reciprocal, a table does
+// not pay.
+constexpr int     kSnakeLdsMaxC       = 1024;
+constexpr int64_t kSnakeLdsSmallTasks = int64_t{ 1024 } * 256;        // 4-row tasks, one per lane
+constexpr int64_t kSnakeLdsMaxTasks   = int64_t{ 1 } << 20;          // 8-row tasks, one per lane
 
 template <int R> __global__ __launch_bounds__(256) void k_snake_beta_lds(const EwArgs a) {
     __shared__ __align__(16) float  s_al[kSnakeLdsMaxC];
@@ -755,8 +754,8 @@ shp_status_t launch_snake(const shp_tensor * x, const shp_tensor * c0, const shp
     if (K == kSnakeBeta && plan.flat && c16 && x->ne[0] <= kSnakeLdsMaxC) {
         const int64_t quads  = x->ne[0] / 4;
         const int64_t rows   = g.n4 / quads;
-        const int64_t ntask2 = (rows + 1) / 2 * quads;
         const int64_t ntask4 = (rows + 3) / 4 * quads;
+        const int64_t ntask8 = (rows + 7) / 8 * quads;
         g.quads              = make_fastdiv(static_cast<uint32_t>(quads));
         if (ntask4 <= kSnakeLdsSmallTasks) {
             g.ntask = ntask4;
@@ -764,9 +763,10 @@ shp_status_t launch_snake(const shp_tensor * x, const shp_tensor * c0, const shp
                                stream, g);
             return launch_status();
         }
-        if (ntask2 >= kSnakeLdsMinTasks && ntask2 <= UINT32_MAX) {
-            g.ntask = ntask2;
-            hipLaunchKernelGGL(k_snake_beta_lds<2>, dim3(kSnakeLdsBlocks), dim3(256), 0, stream, g);
+        if (ntask8 <= kSnakeLdsMaxTasks) {
+            g.ntask = ntask8;
+            hipLaunchKernelGGL(k_snake_beta_lds<8>, dim3(static_cast<unsigned>((ntask8 + 255) / 256)), dim3(256), 0,
+                               stream, g);
             return launch_status();
         }
     }

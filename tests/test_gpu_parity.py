@@ -890,10 +890,10 @@ def test_snake_beta(gpu, T, C):
 
 
 def test_snake_beta_large_channel_table(gpu):
-    """[128, 131072] is large enough for the kernel that evaluates each
-    channel's curves once per block into LDS (at least 4 lane tasks per lane
-    of a 2048-block grid); rows 0 and 1 carry large x, so some sines leave the
-    fast range, and channels 0-3 hold extreme curves."""
+    """[128, 131072] takes the kernel that evaluates each channel's curves
+    once per block into LDS with one 8-row task per lane (more than 2^18
+    4-row tasks); rows 0 and 1 carry large x, so some sines leave the fast
+    range, and channels 0-3 hold extreme curves."""
     rng = np.random.default_rng(SEED + 131)
     T, C = 131072, 128
     x = rng.standard_normal((T, C), dtype=np.float32)
@@ -902,6 +902,18 @@ def test_snake_beta_large_channel_table(gpu):
     lb = rng.uniform(-3, 3, C).astype(np.float32)
     la[:4] = [-30.0, 30.0, 0.0, -3.0]
     lb[:4] = [-30.0, 3.0, 30.0, -25.0]
+    ref = R.run(lambda g: R.snake_beta(g, x, la, lb))
+    assert_snake_close(_np(gpu.snake_beta(_t(gpu, x), _t(gpu, la), _t(gpu, lb))), ref, x)
+
+
+@pytest.mark.parametrize("T,C", [(32771, 128), (8197, 1024)])
+def test_snake_beta_eight_row_tasks_ragged(gpu, T, C):
+    """Shapes just past 2^18 4-row tasks take the 8-row LDS kernel; T is not
+    a multiple of 8, so the last task of each channel quad is partial."""
+    rng = np.random.default_rng(SEED + 137 + C)
+    x = rng.standard_normal((T, C), dtype=np.float32)
+    la = rng.uniform(-3, 3, C).astype(np.float32)
+    lb = rng.uniform(-3, 3, C).astype(np.float32)
     ref = R.run(lambda g: R.snake_beta(g, x, la, lb))
     assert_snake_close(_np(gpu.snake_beta(_t(gpu, x), _t(gpu, la), _t(gpu, lb))), ref, x)
 
