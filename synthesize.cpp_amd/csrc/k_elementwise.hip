@@ -325,7 +325,7 @@ template <int K, int BLOCK> __global__ __launch_bounds__(BLOCK) void k_snake_fla
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int64_t i = i0 + r * c4;
-            xv[r]           = in & (i < a.n4) ? ld_stream(X + i) : splat4(0.0f);
+            xv[r]           = (in & (i < a.n4)) ? ld_stream(X + i) : splat4(0.0f);
         }
     };
     load(t);
@@ -391,7 +391,7 @@ template <int R> __global__ __launch_bounds__(256) void k_snake_beta_lds(const E
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int64_t i = i0 + r * c4;
-            xv[r]           = (tt < a.ntask) & (i < a.n4) ? ld_stream(X + i) : splat4(0.0f);
+            xv[r]           = ((tt < a.ntask) & (i < a.n4)) ? ld_stream(X + i) : splat4(0.0f);
         }
     };
     load(t);

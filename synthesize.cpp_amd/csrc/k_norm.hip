@@ -534,7 +534,9 @@ template <bool KV> __device__ __forceinline__ int64_t rope_slot(const RopeArgs &
         if (a.slot == nullptr) {
             return 0;
         }
-        const int64_t sl = *a.slot;
+        // a scalar load: a vector load here would be waited for (with every
+        // row load before it) at the range check, ahead of the theta chain
+        const int64_t sl = ld_const(a.slot);
         if (sl >= 0 && sl <= a.cap - a.npos) {
             return sl;
         }
@@ -721,12 +723,14 @@ template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(1024) void k_
 
 // The same for a few positions (a decode step): the block's row waves take
 // their whole row through the QK-norm (and gains) before the barrier, while
-// one extra wave, after the rows, builds the position's cos/sin cache. The
-// wave that runs the serial theta chain then holds no rows, so the norm is no
-// longer behind the chain on the block's critical path: after the barrier a
-// row wave only rotates and stores. Same arithmetic as k_rope128, bit for
-// bit. At most kRopeDecMaxRows rows (the theta wave makes the block one wave
-// longer).
+// one extra wave, wave 0, builds the position's cos/sin cache. The wave that
+// runs the serial theta chain then holds no rows, so the norm is no longer
+// behind the chain on the block's critical path: after the barrier a row wave
+// only rotates and stores. The theta wave comes first, so it is dispatched
+// first (measured on MI355X, one-token launch with the KV write: 2.78 us with
+// the theta wave after the rows, 2.63 us with it first). Same arithmetic as
+// k_rope128, bit for bit. At most kRopeDecMaxRows rows (the theta wave makes
+// the block one wave longer).
 constexpr int kRopeDecMaxRows = (1024 - kWave) / kRopeLanes;
 
 template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(1024) void k_rope128_dec(const RopeArgs a) {
@@ -737,10 +741,10 @@ template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(1024) void k_
     const int32_t    p     = a.pos[pi];  // before the field copies below: one scalar load
     const RopeFields f     = rope_fields<KV>(a);
     const int        total = rope_rows<KV>(f);
-    const int        rowt  = (total * kRopeLanes + kWave - 1) / kWave * kWave;  // threads of the row waves
-    const int        g     = threadIdx.x / kRopeLanes;
-    const int        l     = threadIdx.x % kRopeLanes;
-    const bool       theta = static_cast<int>(threadIdx.x) >= rowt;  // uniform over each wave
+    const int        tid   = static_cast<int>(threadIdx.x) - kWave;  // row thread index; < 0 in the theta wave
+    const bool       theta = tid < 0;                                 // uniform over each wave
+    const int        g     = theta ? 0 : tid / kRopeLanes;
+    const int        l     = static_cast<int>(threadIdx.x) % kRopeLanes;
     const bool       live  = !theta & (g < total);
 
     RowRef r = rope_row<KV>(f, live ? g : 0, pi);
@@ -758,7 +762,7 @@ template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(1024) void k_
     }
     const int64_t slot = rope_slot<KV>(a);
     if (theta) {
-        const int   k   = static_cast<int>(threadIdx.x) - rowt;
+        const int   k   = static_cast<int>(threadIdx.x);
         const float mth = theta_chain64(static_cast<float>(p), a.theta_scale);
         float       sv, cv;
         rope_sincos(a.freq_scale * mth, sv, cv);
