@@ -274,25 +274,34 @@ template <int WT, int MODE> shp_status_t launch_norm(const NormArgs & a, bool ve
         if (nvec <= 128) {
             return go(k_rms_norm_vec<128, 1, WT, MODE>, 2);
         }
-        // Rows of 1024 / 2048 with at least 4096 of them, measured on MI355X
-        // against one 256-lane block per row:
-        //   - plain 1024: one wave per row (no LDS round trip, no barrier),
-        //     -20 % at [1024,8192] (two waves per row: +10 % over one);
-        //   - plain 2048: two waves per row (4 float4 per lane, the partial
-        //     sums combined through LDS), at the same-size copy's speed
-        //     (22.8 against 23.8 us for one wave per row at [2048,8192]);
-        //   - add forms at 2048: one wave per row, -9 % at [2048,4096] (two
-        //     waves per row: +6 %, each lane holding both operands);
-        //   - add forms at 1024, and fewer rows: four waves per row keep more
-        //     loads in flight and win.
-        if (a.nrows >= 4096 && nvec == 256 && MODE == kPlain) {
-            return go(k_rms_norm_vec<64, 4, WT, MODE>, 4);
+        // Rows of 1024 / 2048: how many waves share a row, by row count.
+        // Measured on MI355X (cold, us; 4 waves per row first, then the pick):
+        //   plain 1024: 4 waves up to 2048 rows; two waves per row below
+        //     6144 rows ([1024,3072] 6.37 -> 5.67, [1024,4096] 8.15 -> 6.68);
+        //     one wave per row from 6144 ([1024,8192] 13.4 -> 11.5);
+        //   plain 2048: 4 waves (2 float4 each) up to 2048 rows, then two
+        //     waves per row ([2048,3072] 10.3 -> 9.65, [2048,8192] 25.1 ->
+        //     22.9, at the same-size copy's speed);
+        //   add forms 1024: 4 waves below 1024 rows (more loads in flight);
+        //     two waves per row below 4096 ([1024,2048] 7.67 -> 6.51); one
+        //     wave per row below 16384 ([1024,4096] 13.8 -> 11.4, [1024,8192]
+        //     about even); 4 waves again from 16384 ([1024,16384] 44.0
+        //     against 46.0 for one wave);
+        //   add forms 2048: 4 waves below 2048 rows; two waves per row below
+        //     4096 ([2048,2048] 13.5 -> 11.5); one wave per row from 4096
+        //     ([2048,4096] 23.9 -> 21.9).
+        const int64_t nr = a.nrows;
+        if (nvec == 256 && MODE == kPlain && nr > 2048) {
+            return nr < 6144 ? go(k_rms_norm_vec<128, 2, WT, MODE>, 2) : go(k_rms_norm_vec<64, 4, WT, MODE>, 4);
         }
-        if (a.nrows >= 4096 && nvec == 512 && MODE == kPlain) {
+        if (nvec == 256 && MODE != kPlain && nr >= 1024 && nr < 16384) {
+            return nr < 4096 ? go(k_rms_norm_vec<128, 2, WT, MODE>, 2) : go(k_rms_norm_vec<64, 4, WT, MODE>, 4);
+        }
+        if (nvec == 512 && MODE == kPlain && nr > 2048) {
             return go(k_rms_norm_vec<128, 4, WT, MODE>, 2);
         }
-        if (a.nrows >= 4096 && nvec == 512) {
-            return go(k_rms_norm_vec<64, 8, WT, MODE>, 4);
+        if (nvec == 512 && MODE != kPlain && nr >= 2048) {
+            return nr < 4096 ? go(k_rms_norm_vec<128, 4, WT, MODE>, 2) : go(k_rms_norm_vec<64, 8, WT, MODE>, 4);
         }
         switch ((nvec + 255) / 256) {
             case 1:

@@ -358,10 +358,12 @@ def _dev_w(gpu, w, kind):
 @pytest.mark.parametrize("shape,wkind", [((512, 1024), "bf16"), ((64, 2048), "f32"), ((7, 24, 128), "f16"),
                                          ((33, 1000), "f32"), ((5, 8), "f32"), ((3, 4096), "bf16"),
                                          ((40, 3072), "f32"), ((9, 64), "none"), ((4, 256), "bf16"),
-                                         ((6, 512), "f32"), ((4101, 1024), "bf16"), ((4098, 2048), "f32")])
+                                         ((6, 512), "f32"), ((4101, 1024), "bf16"), ((4098, 2048), "f32"),
+                                         ((3073, 1024), "bf16"), ((6147, 1024), "f32"), ((2049, 2048), "f16")])
 def test_rms_norm_mul(gpu, shape, wkind):
-    """(4101, 1024) and (4098, 2048) take the one-wave-per-row launch (>= 4096
-    rows), with a partly empty last block."""
+    """Row counts past each launch-shape boundary, with a partly empty last
+    block: (3073, 1024) and (2049, 2048) two waves per row, (4101, 1024) two
+    waves and (6147, 1024) one wave per row, (4098, 2048) two waves."""
     rng = np.random.default_rng(SEED + sum(shape))
     x = rng.standard_normal(shape).astype(np.float32)
     x[0] = 0.0  # an all-zero row: scale = 1/sqrt(eps), output exactly 0
@@ -404,8 +406,12 @@ def test_rms_norm_mul_f32_gain_8_byte_aligned(gpu, shape):
 
 
 @pytest.mark.parametrize("shape,wkind", [((512, 1024), "bf16"), ((64, 2048), "f32"), ((3, 1000), "f32"),
-                                         ((4099, 1024), "f16"), ((4096, 2048), "bf16")])
+                                         ((4099, 1024), "f16"), ((4096, 2048), "bf16"), ((1025, 1024), "bf16"),
+                                         ((2051, 2048), "f32"), ((4097, 2048), "bf16"), ((16385, 1024), "bf16")])
 def test_add_rms_norm_mul(gpu, shape, wkind):
+    """Row counts on each side of the launch-shape boundaries, most with a
+    partly empty last block: (1025, 1024) and (2051, 2048) two waves per row,
+    (4099, 1024) and (4097, 2048) one wave per row, (16385, 1024) four."""
     rng = np.random.default_rng(SEED + 3 * sum(shape))
     a = rng.standard_normal(shape).astype(np.float32)
     b = rng.standard_normal(shape).astype(np.float32)
