@@ -54,10 +54,17 @@ typedef int32_t shp_status_t;
 /* ggml rope mode bit (GGML_ROPE_TYPE_NEOX); src/arch/qwen3-tts/operations.cpp:16. */
 #define SHP_ROPE_TYPE_NEOX 2
 
+/*
+ * Every extent must be at least 1: a tensor with a zero extent is
+ * SHP_ERR_INVALID_ARG at every entry point, and shp_graph_node_supported
+ * reports a node with one unsupported, so ggml keeps it (an empty node is a
+ * no-op there). The graph builders never emit one on this path: the hosts
+ * reject zero frames and groups first (qwen3-tts/profile.cpp:325,1485).
+ */
 typedef struct shp_tensor {
     int32_t type;     /* SHP_TYPE_* */
     int32_t reserved; /* must be 0 */
-    int64_t ne[4];    /* extents, ne[0] fastest */
+    int64_t ne[4];    /* extents, ne[0] fastest; each >= 1 */
     size_t  nb[4];    /* byte strides */
     void *  data;     /* device pointer */
 } shp_tensor;

@@ -189,6 +189,28 @@ def test_argument_validation():
     assert L.shp_sum_scale_leaky_relu(strided, 1, 1.0, 0.1, None, R(a), None) == S.ERR_UNSUPPORTED
 
 
+def test_zero_extents_are_rejected_before_any_launch():
+    """A tensor with a zero extent (no rows, no ids, no positions) is
+    INVALID_ARG at the entry points, with nothing launched (no GPU here)."""
+    L = S.load()
+    w = mk(S.TYPE_F32, [1024])
+    empty = mk(S.TYPE_F32, [1024, 0])
+    assert L.shp_rms_norm_mul(R(empty), R(w), 1e-6, R(empty), None) == S.ERR_INVALID_ARG
+    assert L.shp_add_rms_norm_mul(R(empty), R(empty), R(w), 1e-6, None, R(empty), None) == S.ERR_INVALID_ARG
+    assert L.shp_swiglu(R(empty), R(empty), R(empty), None) == S.ERR_INVALID_ARG
+    assert L.shp_add(R(empty), R(empty), R(empty), None) == S.ERR_INVALID_ARG
+    tab = mk(S.TYPE_Q8_0, [1024, 100])
+    assert L.shp_get_rows(R(tab), R(mk(S.TYPE_I32, [0])), R(empty), None) == S.ERR_INVALID_ARG
+    q0, k0 = mk(S.TYPE_F32, [128, 16, 0]), mk(S.TYPE_F32, [128, 8, 0])
+    wq = mk(S.TYPE_F32, [128])
+    assert L.shp_qk_norm_rope(R(q0), R(k0), R(wq), R(wq), 1e-6, R(mk(S.TYPE_I32, [0])), 128, 1e6, 1, R(q0), R(k0),
+                              None) == S.ERR_INVALID_ARG
+    c = mk(S.TYPE_F32, [256])
+    e2 = mk(S.TYPE_F32, [256, 0])
+    assert L.shp_snake(R(e2), R(c), R(e2), None) == S.ERR_INVALID_ARG
+    assert L.shp_add_leaky_relu(R(e2), R(e2), 0.1, None, R(e2), None) == S.ERR_INVALID_ARG
+
+
 def test_binding_fails_loudly_without_library(tmp_path):
     with pytest.raises(RuntimeError):
         import importlib

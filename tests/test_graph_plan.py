@@ -214,6 +214,11 @@ def test_singles_and_support():
     g = S.Graph()
     alibi = g.soft_max_ext(z(3, 5), None, 0.5, max_bias=8.0)
     assert kinds(g.plan(alibi)) == ["unsupported"]
+    g = S.Graph()
+    empty = g.exp(z(0, 4))  # no rows: ggml keeps the node (a no-op there)
+    assert kinds(g.plan(empty)) == ["unsupported"]
+    arr, n, _ = g.nodes(empty)
+    assert S.load().shp_graph_node_supported(ctypes.byref(arr[n - 1])) == 0
 
 
 def test_support_is_the_entry_points_own_answer():
