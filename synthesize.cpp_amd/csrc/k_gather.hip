@@ -1349,6 +1349,9 @@ extern "C" shp_status_t shp_get_rows(const shp_tensor * src,
         dst->ne[3] != ids->ne[2] || src->ne[0] > INT32_MAX) {
         return SHP_ERR_INVALID_ARG;
     }
+    if (!i32_aligned(*ids)) {
+        return SHP_ERR_UNSUPPORTED;
+    }
     GatherArgs a{};
     a.src   = static_cast<const char *>(src->data);
     a.snb1  = static_cast<int64_t>(src->nb[1]);
@@ -1455,6 +1458,9 @@ extern "C" shp_status_t shp_get_rows_sum(const shp_tensor * tables,
         !contiguous(*ids) || dst->ne[0] != ne0 || dst->ne[1] != frames || dst->ne[2] != 1 || dst->ne[3] != 1 ||
         ne0 > INT32_MAX) {
         return SHP_ERR_INVALID_ARG;
+    }
+    if (!i32_aligned(*ids)) {
+        return SHP_ERR_UNSUPPORTED;
     }
     GatherSumArgs a{};
     bool          vec = rows_aligned(*dst, 16);

@@ -948,6 +948,9 @@ shp_status_t rope_entry(const shp_tensor * q,
     if (!rope_part_ok(q, q_out) || !well_formed(pos) || pos->type != SHP_TYPE_I32) {
         return SHP_ERR_INVALID_ARG;
     }
+    if (!i32_aligned(*pos)) {
+        return SHP_ERR_UNSUPPORTED;
+    }
     if ((k == nullptr) != (k_out == nullptr) || (v == nullptr) != (v_out == nullptr) || (v != nullptr && k == nullptr)) {
         return SHP_ERR_INVALID_ARG;
     }
@@ -1172,6 +1175,9 @@ extern "C" shp_status_t shp_qk_norm_rope_kv_at(const shp_tensor * q,
         (status != nullptr && (!shp::well_formed(status) || status->type != SHP_TYPE_I32 ||
                                shp::nelements(*status) != 1))) {
         return SHP_ERR_INVALID_ARG;
+    }
+    if (!shp::i32_aligned(*slot) || (status != nullptr && !shp::i32_aligned(*status))) {
+        return SHP_ERR_UNSUPPORTED;
     }
     // The views start at row 0 and must fit T rows; the device slot moves them.
     shp_tensor kview{}, vview{};

@@ -406,6 +406,14 @@ inline bool rows_aligned(const shp_tensor & t, size_t align) {
 }
 
 // Fully contiguous (ggml_is_contiguous) in the element-size sense.
+// An I32 index tensor (ids, positions, a cache slot or status word): the
+// kernels read such values with scalar loads where they are wave-uniform, and
+// a scalar load ignores an address's two low bits, so data and strides must
+// be multiples of 4 (ggml's allocators always give that).
+inline bool i32_aligned(const shp_tensor & t) {
+    return rows_aligned(t, 4);
+}
+
 inline bool contiguous(const shp_tensor & t) {
     size_t expect = t.nb[0] * static_cast<size_t>(t.ne[0]);
     if (block_type(t.type)) {

@@ -64,6 +64,9 @@ shp_status_t check_step(const shp_layer_step & s) {
     if (!well_formed(s.pos) || s.pos->type != SHP_TYPE_I32 || nelements(*s.pos) != t || !contiguous(*s.pos)) {
         return SHP_ERR_INVALID_ARG;
     }
+    if (!i32_aligned(*s.pos)) {
+        return SHP_ERR_UNSUPPORTED;
+    }
     if (!gain(s.w_in, hidden) || !gain(s.w_post, hidden) || !gain(s.wq, head_dim) || !gain(s.wk, head_dim)) {
         return SHP_ERR_INVALID_ARG;
     }

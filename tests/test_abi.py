@@ -189,6 +189,37 @@ def test_argument_validation():
     assert L.shp_sum_scale_leaky_relu(strided, 1, 1.0, 0.1, None, R(a), None) == S.ERR_UNSUPPORTED
 
 
+def test_index_tensors_must_be_four_byte_aligned():
+    """ids, positions, the cache slot and the status word are read with
+    scalar loads where wave-uniform, which need 4-byte aligned addresses: a
+    misaligned index tensor is UNSUPPORTED (ggml keeps the node), before any
+    launch (no GPU here)."""
+    L = S.load()
+    odd = FAKE + 2
+    tab = mk(S.TYPE_Q8_0, [1024, 100])
+    out = mk(S.TYPE_F32, [1024, 7])
+    assert L.shp_get_rows(R(tab), R(mk(S.TYPE_I32, [7], data=odd)), R(out), None) == S.ERR_UNSUPPORTED
+    ids_nb = mk(S.TYPE_I32, [7, 2], nb=[4, 30, 60, 60])  # a row stride that is not a multiple of 4
+    tab2 = mk(S.TYPE_Q8_0, [1024, 100, 2])
+    assert L.shp_get_rows(R(tab2), R(ids_nb), R(mk(S.TYPE_F32, [1024, 7, 2])), None) == S.ERR_UNSUPPORTED
+    tabs = (S.ShpTensor * 2)(mk(S.TYPE_Q8_0, [1024, 100]), mk(S.TYPE_Q8_0, [1024, 100]))
+    assert L.shp_get_rows_sum(tabs, 2, R(mk(S.TYPE_I32, [7, 2], data=odd)), R(out), None) == S.ERR_UNSUPPORTED
+    q = mk(S.TYPE_F32, [128, 16, 5])
+    k = mk(S.TYPE_F32, [128, 8, 5])
+    pos = mk(S.TYPE_I32, [5], data=odd)
+    assert L.shp_rope_ext(R(q), R(pos), 128, 2, 1e6, 1, 0, 1, R(q), None) == S.ERR_UNSUPPORTED
+    w = mk(S.TYPE_F32, [128])
+    assert L.shp_qk_norm_rope(R(q), R(k), R(w), R(w), 1e-6, R(pos), 128, 1e6, 1, R(q), R(k), None) == \
+        S.ERR_UNSUPPORTED
+    kc = mk(S.TYPE_F32, [128, 8, 64])
+    v = mk(S.TYPE_F32, [128, 8, 5])
+    good_pos, i1 = mk(S.TYPE_I32, [5]), mk(S.TYPE_I32, [1])
+    at = lambda sl, stt: L.shp_qk_norm_rope_kv_at(R(q), R(k), R(v), R(w), R(w), 1e-6, R(good_pos), 128, 1e6, 1.0,
+                                                  R(q), R(kc), R(kc), R(sl), R(stt) if stt is not None else None, None)
+    assert at(mk(S.TYPE_I32, [1], data=odd), i1) == S.ERR_UNSUPPORTED  # slot
+    assert at(i1, mk(S.TYPE_I32, [1], data=odd)) == S.ERR_UNSUPPORTED  # status word
+
+
 def test_zero_extents_are_rejected_before_any_launch():
     """A tensor with a zero extent (no rows, no ids, no positions) is
     INVALID_ARG at the entry points, with nothing launched (no GPU here)."""
@@ -284,3 +315,4 @@ def test_layer_step_rejects_a_malformed_step_before_any_launch():
     bad_nb = mk(S.TYPE_F32, [256, 5])
     bad_nb.nb[0] = 8
     assert call(resid=bad_nb) == S.ERR_INVALID_ARG
+    assert call(pos=mk(S.TYPE_I32, [5], data=FAKE + 2)) == S.ERR_UNSUPPORTED  # positions read by scalar loads
