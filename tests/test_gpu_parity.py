@@ -1212,6 +1212,21 @@ def test_golden_g2_summed_embedding_on_gpu(gpu):
     assert np.abs(got.reshape(-1) - np.array(d["expected_summed_embedding"], np.float32)).max() < d["tolerance_cpu"]
 
 
+@pytest.mark.parametrize("C,T", [(16, 37), (512, 257)])
+def test_golden_g4_kokoro_snake_on_gpu(gpu, C, T):
+    """reference_snake, tests/kokoro_decoder_test.cpp:81-90: y = x + sin(a x)^2
+    / a in double on [C, T] (element (c, t) at t*C + c), at the test's 1e-4;
+    the f32 node-by-node form stays within a few ulp of it."""
+    rng = np.random.default_rng(20260728 + C)
+    x = rng.standard_normal((T, C)).astype(np.float32)
+    alpha = np.exp(rng.uniform(np.log(0.1), np.log(10.0), C)).astype(np.float32)
+    got = _np(gpu.snake(_t(gpu, x), _t(gpu, alpha))).astype(np.float64)
+    a = alpha.astype(np.float64)
+    ref = x + np.sin(a * x) ** 2 / a
+    assert np.abs(got - ref).max() < 1e-4
+    assert np.abs(got - ref).max() < 8 * np.finfo(np.float32).eps * np.abs(ref).max()
+
+
 def test_q8_last_row_at_end_of_allocation(gpu):
     """Regression: 16 Q8_0 tables stacked in one allocation of exactly 34 MiB (a
     multiple of the allocator's 2 MiB granularity, so nothing follows the last
