@@ -44,10 +44,16 @@ def test_headers_compile_and_link_from_plain_c(tmp_path):
         '    printf("%u %s\\n", shp_abi_version(), shp_status_string(SHP_ERR_INVALID_ARG));\n'
         "    return shp_rms_norm_mul(NULL, NULL, 1e-6f, &y, NULL) == SHP_ERR_INVALID_ARG ? 0 : 1;\n"
         "}\n")
-    lib_dir = os.path.dirname(S.LIB_PATH)
+    # A sanitizer build (make asan) needs clang's sanitizer runtime at link
+    # time, which a plain gcc link does not bring: the program links the
+    # product library then.
+    lib_path = S.LIB_PATH
+    if "_asan" in os.path.basename(lib_path):
+        lib_path = os.path.join(ROOT, "synthesize.cpp_amd", "libsynth_hip.so")
+    lib_dir = os.path.dirname(lib_path)
     exe = tmp_path / "consumer"
     build = subprocess.run([cc, "-std=c11", "-Wall", "-Wextra", "-pedantic", "-Werror", "-I", os.path.join(ROOT, "include"),
-                            str(src), "-L" + lib_dir, "-l:" + os.path.basename(S.LIB_PATH), "-Wl,-rpath," + lib_dir,
+                            str(src), "-L" + lib_dir, "-l:" + os.path.basename(lib_path), "-Wl,-rpath," + lib_dir,
                             "-o", str(exe)], capture_output=True, text=True)
     assert build.returncode == 0, build.stderr
     run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
