@@ -192,14 +192,27 @@ template <int TYPE> __device__ __forceinline__ float elem(const char * row, int 
     }
 }
 
-// The kernel arguments a gather wave needs before its first load.
-__device__ __forceinline__ void gather_args_in_sgprs(const GatherArgs & a) {
-    args_in_sgprs(a.total, a.ids, a.inb0, a.inb1, a.inb2, a.fn.d, a.fn.m, a.fn.l, a.fne11.d, a.fne11.m, a.fne11.l,
-                  a.src, a.snb1, a.snb2, a.snb3, a.srows, a.ne0);
+// The kernel arguments a gather wave needs before its first load. FLAT: the
+// ids are one vector (ne11 = ne12 = 1), so output row R is lookup R and the
+// batch coordinates, their divisions and strides are not needed.
+template <bool FLAT = false> __device__ __forceinline__ void gather_args_in_sgprs(const GatherArgs & a) {
+    if constexpr (FLAT) {
+        args_in_sgprs(a.total, a.ids, a.inb0, a.src, a.snb1, a.srows, a.ne0, a.dst, a.dnb1);
+    } else {
+        args_in_sgprs(a.total, a.ids, a.inb0, a.inb1, a.inb2, a.fn.d, a.fn.m, a.fn.l, a.fne11.d, a.fne11.m, a.fne11.l,
+                      a.src, a.snb1, a.snb2, a.snb3, a.srows, a.ne0);
+    }
 }
 
+template <bool FLAT = false>
 __device__ __forceinline__ void gather_coords(const GatherArgs & a, int64_t R, int32_t & id, const char *& srow,
                                               float *& drow) {
+    if constexpr (FLAT) {
+        id   = ld_const(reinterpret_cast<const int32_t *>(reinterpret_cast<const char *>(a.ids) + R * a.inb0));
+        srow = a.src + static_cast<int64_t>(id) * a.snb1;
+        drow = reinterpret_cast<float *>(reinterpret_cast<char *>(a.dst) + R * a.dnb1);
+        return;
+    }
     const uint32_t q   = fastdiv(static_cast<uint32_t>(R), a.fn);
     const uint32_t i12 = fastdiv(q, a.fne11);
     const int64_t  r   = R - static_cast<int64_t>(q) * a.fn.d;
@@ -269,8 +282,9 @@ template <int TYPE> __device__ __forceinline__ f32x4 cvt_sum_chunk(const typenam
 // re-reads chunk 0). Table rows use ordinary loads so that rows gathered again
 // (repeated tokens, a table that fits the Infinity Cache) can hit; the f32
 // output is streamed out with nontemporal stores.
-template <int TYPE, int LPR, int CPL> __global__ __launch_bounds__(256) void k_get_rows_vec(const GatherArgs a) {
-    gather_args_in_sgprs(a);
+template <int TYPE, int LPR, int CPL, bool FLAT>
+__global__ __launch_bounds__(256) void k_get_rows_vec(const GatherArgs a) {
+    gather_args_in_sgprs<FLAT>(a);
     typedef typename SumChunk<TYPE>::type Chunk;
     const int     l = threadIdx.x % LPR;
     const int64_t R = static_cast<int64_t>(blockIdx.x) * (256 / LPR) + row_in_block<LPR>();
@@ -280,7 +294,7 @@ template <int TYPE, int LPR, int CPL> __global__ __launch_bounds__(256) void k_g
     int32_t      id;
     const char * srow;
     float *      drow;
-    gather_coords(a, R, id, srow, drow);
+    gather_coords<FLAT>(a, R, id, srow, drow);
     const bool    ok  = id >= 0 && id < a.srows;
     const int     n4  = a.ne0 / 4;
     const Chunk * row = reinterpret_cast<const Chunk *>(ok ? srow : a.src);
@@ -645,8 +659,9 @@ constexpr int kStagedWpb = 4;
 // as soon as it is decoded. Measured on MI355X at [1024,2048] x4096 against
 // the branch on the id with all 16 values stored at the end: 4.54 against
 // 4.68 us.
-template <int NQ, int WPB> __global__ __launch_bounds__(WPB * kWave) void k_get_rows_q8s(const GatherArgs a) {
-    gather_args_in_sgprs(a);
+template <int NQ, int WPB, bool FLAT>
+__global__ __launch_bounds__(WPB * kWave) void k_get_rows_q8s(const GatherArgs a) {
+    gather_args_in_sgprs<FLAT>(a);
     __shared__ uint32_t s_row[WPB][q8_row_dwords(NQ) + kQ8StagePadDwords];
     // The row is uniform over the wave: readfirstlane lets the id be one scalar
     // load and the table row base a scalar.
@@ -659,7 +674,7 @@ template <int NQ, int WPB> __global__ __launch_bounds__(WPB * kWave) void k_get_
     int32_t      id;
     const char * srow;
     float *      drow;
-    gather_coords(a, R, id, srow, drow);
+    gather_coords<FLAT>(a, R, id, srow, drow);
     const bool      ok = (id >= 0) & (id < a.srows);
     const Q8Row<NQ> r  = q8_row_load<NQ>(ok ? srow : a.src, l);
     q8_row_stage<NQ>(s_row[w], r, l);
@@ -743,8 +758,9 @@ __global__ __launch_bounds__(256) void k_get_rows_q5k(const GatherArgs a) {
 // round, then decodes each super-block's 4 elements per lane from LDS as
 // above -- a few wide loads in front of the decode instead of six dword loads
 // per super-block and lane. An id out of range reads row 0 and stores NaN.
-template <int NSB, int WPB> __global__ __launch_bounds__(WPB * kWave) void k_get_rows_q5ks(const GatherArgs a) {
-    gather_args_in_sgprs(a);
+template <int NSB, int WPB, bool FLAT>
+__global__ __launch_bounds__(WPB * kWave) void k_get_rows_q5ks(const GatherArgs a) {
+    gather_args_in_sgprs<FLAT>(a);
     constexpr int kWords  = 11 * NSB;  // 16-byte words per row
     constexpr int kRounds = (kWords + kWave - 1) / kWave;
     __shared__ u32x4 s_row[WPB][kWords];
@@ -757,7 +773,7 @@ template <int NSB, int WPB> __global__ __launch_bounds__(WPB * kWave) void k_get
     int32_t      id;
     const char * srow;
     float *      drow;
-    gather_coords(a, R, id, srow, drow);
+    gather_coords<FLAT>(a, R, id, srow, drow);
     const bool    ok  = (id >= 0) & (id < a.srows);
     const u32x4 * src = reinterpret_cast<const u32x4 *>(ok ? srow : a.src);
     u32x4         v[kRounds];
@@ -926,102 +942,111 @@ int lanes_for(int64_t units) {
     return units >= 64 ? 64 : (units >= 32 ? 32 : 16);
 }
 
+template <int TYPE, bool FLAT> shp_status_t launch_get_rows_vec(const GatherArgs & a, hipStream_t stream);
+
+// One vector of ids (a.total == a.n): the staged and vector kernels take the
+// flat coordinates (measured on MI355X, Q8_0 [1024,2048] x4096: 4.65 -> 4.56
+// us, the same bits).
 template <int TYPE> shp_status_t launch_get_rows(const GatherArgs & a, bool vec, hipStream_t stream) {
     if (dry_run()) {
         return SHP_OK;
     }
     if (vec) {
-        if constexpr (TYPE == SHP_TYPE_Q5_K) {
-            const dim3 grid(static_cast<unsigned>((a.total + kStagedWpb - 1) / kStagedWpb));
-            const dim3 block(kStagedWpb * kWave);
-            if (a.staged && a.ne0 == 1024) {
-                hipLaunchKernelGGL((k_get_rows_q5ks<4, kStagedWpb>), grid, block, 0, stream, a);
-            } else if (a.staged && a.ne0 == 2048) {
-                hipLaunchKernelGGL((k_get_rows_q5ks<8, kStagedWpb>), grid, block, 0, stream, a);
-            } else if (a.staged && a.ne0 == 4096) {
-                hipLaunchKernelGGL((k_get_rows_q5ks<16, kStagedWpb>), grid, block, 0, stream, a);
-            } else {
-                hipLaunchKernelGGL(k_get_rows_q5k, dim3(static_cast<unsigned>((a.total + 3) / 4)), dim3(256), 0, stream,
-                                   a);
-            }
-            return launch_status();
-        } else if constexpr (TYPE == SHP_TYPE_Q8_0) {
-            if (a.staged) {
-                const dim3 grid(static_cast<unsigned>((a.total + kStagedWpb - 1) / kStagedWpb));
-                const dim3 block(kStagedWpb * kWave);
-                switch (a.ne0) {
-                    case 1024:
-                        hipLaunchKernelGGL((k_get_rows_q8s<4, kStagedWpb>), grid, block, 0, stream, a);
-                        break;
-                    case 2048:
-                        hipLaunchKernelGGL((k_get_rows_q8s<8, kStagedWpb>), grid, block, 0, stream, a);
-                        break;
-                    default:
-                        hipLaunchKernelGGL((k_get_rows_q8s<16, kStagedWpb>), grid, block, 0, stream, a);
-                        break;
-                }
-                return launch_status();
-            }
-            const int nhalf = a.ne0 / 16;
-            if (nhalf >= 16 && nhalf <= 256 && (nhalf & (nhalf - 1)) == 0) {
-                const int64_t blocks = (a.total * nhalf + 255) / 256;
-                switch (nhalf) {
-                    case 16:
-                        hipLaunchKernelGGL(k_get_rows_q8h<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
-                        break;
-                    case 32:
-                        hipLaunchKernelGGL(k_get_rows_q8h<32>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
-                        break;
-                    case 64:
-                        hipLaunchKernelGGL(k_get_rows_q8h<64>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
-                        break;
-                    case 128:
-                        hipLaunchKernelGGL(k_get_rows_q8h<128>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
-                        break;
-                    default:
-                        hipLaunchKernelGGL(k_get_rows_q8h<256>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
-                        break;
-                }
-                return launch_status();
-            }
-            const int lpr = lanes_for(a.ne0 / 64);
-            const int64_t blocks = (a.total * lpr + 255) / 256;
-            if (lpr == 64) {
-                hipLaunchKernelGGL(k_get_rows_q8<64>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
-            } else if (lpr == 32) {
-                hipLaunchKernelGGL(k_get_rows_q8<32>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
-            } else {
-                hipLaunchKernelGGL(k_get_rows_q8<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
-            }
-        } else {
-            // 4-element chunks: up to 256 lanes per row, 1..8 chunks per lane.
-            const int64_t n4     = a.ne0 / 4;
-            const int     lpr    = n4 >= 256 ? 256 : (n4 >= 128 ? 128 : lanes_for(n4));
-            const dim3    grid(static_cast<unsigned>((a.total * lpr + 255) / 256));
-            if (lpr == 256) {
-                if (n4 <= 256) {
-                    hipLaunchKernelGGL((k_get_rows_vec<TYPE, 256, 1>), grid, dim3(256), 0, stream, a);
-                } else if (n4 <= 512) {
-                    hipLaunchKernelGGL((k_get_rows_vec<TYPE, 256, 2>), grid, dim3(256), 0, stream, a);
-                } else if (n4 <= 1024) {
-                    hipLaunchKernelGGL((k_get_rows_vec<TYPE, 256, 4>), grid, dim3(256), 0, stream, a);
-                } else {
-                    hipLaunchKernelGGL((k_get_rows_vec<TYPE, 256, 8>), grid, dim3(256), 0, stream, a);
-                }
-            } else if (lpr == 128) {
-                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 128, 2>), grid, dim3(256), 0, stream, a);
-            } else if (lpr == 64) {
-                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 64, 2>), grid, dim3(256), 0, stream, a);
-            } else if (lpr == 32) {
-                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 32, 2>), grid, dim3(256), 0, stream, a);
-            } else {
-                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 16, 2>), grid, dim3(256), 0, stream, a);
-            }
-        }
-        return launch_status();
+        return a.total == a.n ? launch_get_rows_vec<TYPE, true>(a, stream) : launch_get_rows_vec<TYPE, false>(a, stream);
     }
     const int64_t blocks = (a.total + 3) / 4;
     hipLaunchKernelGGL(k_get_rows_generic<TYPE>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+    return launch_status();
+}
+
+template <int TYPE, bool FLAT> shp_status_t launch_get_rows_vec(const GatherArgs & a, hipStream_t stream) {
+    if constexpr (TYPE == SHP_TYPE_Q5_K) {
+        const dim3 grid(static_cast<unsigned>((a.total + kStagedWpb - 1) / kStagedWpb));
+        const dim3 block(kStagedWpb * kWave);
+        if (a.staged && a.ne0 == 1024) {
+            hipLaunchKernelGGL((k_get_rows_q5ks<4, kStagedWpb, FLAT>), grid, block, 0, stream, a);
+        } else if (a.staged && a.ne0 == 2048) {
+            hipLaunchKernelGGL((k_get_rows_q5ks<8, kStagedWpb, FLAT>), grid, block, 0, stream, a);
+        } else if (a.staged && a.ne0 == 4096) {
+            hipLaunchKernelGGL((k_get_rows_q5ks<16, kStagedWpb, FLAT>), grid, block, 0, stream, a);
+        } else {
+            hipLaunchKernelGGL(k_get_rows_q5k, dim3(static_cast<unsigned>((a.total + 3) / 4)), dim3(256), 0, stream,
+                               a);
+        }
+        return launch_status();
+    } else if constexpr (TYPE == SHP_TYPE_Q8_0) {
+        if (a.staged) {
+            const dim3 grid(static_cast<unsigned>((a.total + kStagedWpb - 1) / kStagedWpb));
+            const dim3 block(kStagedWpb * kWave);
+            switch (a.ne0) {
+                case 1024:
+                    hipLaunchKernelGGL((k_get_rows_q8s<4, kStagedWpb, FLAT>), grid, block, 0, stream, a);
+                    break;
+                case 2048:
+                    hipLaunchKernelGGL((k_get_rows_q8s<8, kStagedWpb, FLAT>), grid, block, 0, stream, a);
+                    break;
+                default:
+                    hipLaunchKernelGGL((k_get_rows_q8s<16, kStagedWpb, FLAT>), grid, block, 0, stream, a);
+                    break;
+            }
+            return launch_status();
+        }
+        const int nhalf = a.ne0 / 16;
+        if (nhalf >= 16 && nhalf <= 256 && (nhalf & (nhalf - 1)) == 0) {
+            const int64_t blocks = (a.total * nhalf + 255) / 256;
+            switch (nhalf) {
+                case 16:
+                    hipLaunchKernelGGL(k_get_rows_q8h<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                    break;
+                case 32:
+                    hipLaunchKernelGGL(k_get_rows_q8h<32>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                    break;
+                case 64:
+                    hipLaunchKernelGGL(k_get_rows_q8h<64>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                    break;
+                case 128:
+                    hipLaunchKernelGGL(k_get_rows_q8h<128>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                    break;
+                default:
+                    hipLaunchKernelGGL(k_get_rows_q8h<256>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+                    break;
+            }
+            return launch_status();
+        }
+        const int lpr = lanes_for(a.ne0 / 64);
+        const int64_t blocks = (a.total * lpr + 255) / 256;
+        if (lpr == 64) {
+            hipLaunchKernelGGL(k_get_rows_q8<64>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+        } else if (lpr == 32) {
+            hipLaunchKernelGGL(k_get_rows_q8<32>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+        } else {
+            hipLaunchKernelGGL(k_get_rows_q8<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+        }
+    } else {
+        // 4-element chunks: up to 256 lanes per row, 1..8 chunks per lane.
+        const int64_t n4     = a.ne0 / 4;
+        const int     lpr    = n4 >= 256 ? 256 : (n4 >= 128 ? 128 : lanes_for(n4));
+        const dim3    grid(static_cast<unsigned>((a.total * lpr + 255) / 256));
+        if (lpr == 256) {
+            if (n4 <= 256) {
+                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 256, 1, FLAT>), grid, dim3(256), 0, stream, a);
+            } else if (n4 <= 512) {
+                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 256, 2, FLAT>), grid, dim3(256), 0, stream, a);
+            } else if (n4 <= 1024) {
+                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 256, 4, FLAT>), grid, dim3(256), 0, stream, a);
+            } else {
+                hipLaunchKernelGGL((k_get_rows_vec<TYPE, 256, 8, FLAT>), grid, dim3(256), 0, stream, a);
+            }
+        } else if (lpr == 128) {
+            hipLaunchKernelGGL((k_get_rows_vec<TYPE, 128, 2, FLAT>), grid, dim3(256), 0, stream, a);
+        } else if (lpr == 64) {
+            hipLaunchKernelGGL((k_get_rows_vec<TYPE, 64, 2, FLAT>), grid, dim3(256), 0, stream, a);
+        } else if (lpr == 32) {
+            hipLaunchKernelGGL((k_get_rows_vec<TYPE, 32, 2, FLAT>), grid, dim3(256), 0, stream, a);
+        } else {
+            hipLaunchKernelGGL((k_get_rows_vec<TYPE, 16, 2, FLAT>), grid, dim3(256), 0, stream, a);
+        }
+    }
     return launch_status();
 }
 
