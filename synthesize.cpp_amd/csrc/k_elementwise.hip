@@ -352,16 +352,21 @@ template <int K, int BLOCK> __global__ __launch_bounds__(BLOCK) void k_snake_fla
 }
 
 
-// SnakeBeta with at most kSnakeLdsMaxC channels: each block requests its
-// lanes' rows, evaluates every channel's exp curves, guard and double
-// reciprocal once into LDS meanwhile, and after one barrier each lane runs its
-// task (R rows of one channel quad) from the table. One task per lane: R = 4
-// up to kSnakeLdsSmallTasks tasks, else R = 8 (the two exps per channel are
-// spread over the block's 2048 or 4096 elements instead of 8 or 32 per lane).
-// Measured on MI355X: [512,8192] 8.4 -> 8.2 us and [256,32768] 13.1 ->
-// 12.7 us against the 8-row flat kernel, [128,131072] 25.4 -> 24.7 us against
-// 2-row tasks over 1024 persistent blocks. Rejected at that shape: 2048
-// persistent blocks, per-wave LDS exp tables, 512- or 1024-thread blocks,
+// SnakeBeta with at most kSnakeLdsMaxC channels: each block evaluates every
+// channel's exp curves, guard and double reciprocal once into LDS while its
+// lanes' rows are in flight, and after one barrier each lane runs its task
+// (R rows of one channel quad) from the table. One task per lane: R = 4 up to
+// kSnakeLdsSmallTasks tasks, else R = 8 (the two exps per channel are spread
+// over the block's 2048 or 4096 elements instead of 8 or 32 per lane).
+// CF (the 4-row form): each thread requests its channels' log-curves and its
+// lane's exp-table entry before the rows, so the exps wait for those loads
+// alone (not for the rows queued ahead of them), and looks the table up in a
+// per-wave LDS copy instead of memory; the same values bit for bit.
+// Measured on MI355X against the 8-row flat kernel: [512,8192] 8.4 -> 7.4 us
+// (7.8 without CF), [256,32768] 13.1 -> 12.7 us; [128,131072] 25.4 -> 24.7 us
+// against 2-row tasks over 1024 persistent blocks. CF on the 8-row form is
+// 11 % slower at the two larger shapes. Rejected at [128,131072]: 2048
+// persistent blocks, 512- or 1024-thread blocks, 2-, 4- or 16-row tasks,
 // each lane keeping its quad's curves in registers for all its tasks. For
 // plain Snake, whose per-channel work is only the reciprocal, a table does
 // not pay.
@@ -369,15 +374,31 @@ constexpr int     kSnakeLdsMaxC       = 1024;
 constexpr int64_t kSnakeLdsSmallTasks = int64_t{ 1024 } * 256;        // 4-row tasks, one per lane
 constexpr int64_t kSnakeLdsMaxTasks   = int64_t{ 1 } << 20;          // 8-row tasks, one per lane
 
-template <int R> __global__ __launch_bounds__(256) void k_snake_beta_lds(const EwArgs a) {
+template <int R, bool CF> __global__ __launch_bounds__(256) void k_snake_beta_lds(const EwArgs a) {
+    constexpr int kPer = kSnakeLdsMaxC / 256;  // channels per thread at most
     __shared__ __align__(16) float  s_al[kSnakeLdsMaxC];
     __shared__ __align__(16) float  s_den[kSnakeLdsMaxC];
     __shared__ __align__(16) double s_rc[kSnakeLdsMaxC];
+    __shared__ double               s_tab[CF ? 256 / kWave : 1][kWave];
     const f32x4 * X    = reinterpret_cast<const f32x4 *>(a.a);
     f32x4 *       Y    = reinterpret_cast<f32x4 *>(a.y);
     const int64_t c4   = a.quads.d;
     const int64_t step = static_cast<int64_t>(gridDim.x) * 256;
     args_in_sgprs(X, a.alpha, a.beta, a.quads.d, a.quads.m, a.quads.l, a.ntask, a.n4);
+    const int nc   = static_cast<int>(a.quads.d) * 4;
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    double    entry = 0.0;
+    float     la[kPer], lb[kPer];
+    if constexpr (CF) {
+        entry = exp_table_entry(lane);
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int c  = static_cast<int>(threadIdx.x) + 256 * j;
+            const int cc = c < nc ? c : 0;  // past the channels: re-read channel 0, unused
+            la[j]        = a.alpha[cc];
+            lb[j]        = a.beta[cc];
+        }
+    }
     // The first task's rows are requested before the table of curves is
     // built, so their loads overlap its loads and exps.
     int64_t  t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
@@ -395,12 +416,27 @@ template <int R> __global__ __launch_bounds__(256) void k_snake_beta_lds(const E
         }
     };
     load(t);
-    const int nc = static_cast<int>(a.quads.d) * 4;
-    for (int c = threadIdx.x; c < nc; c += 256) {
-        const SnakeCoef k = snake_coef<kSnakeBeta>(a.alpha[c], a.beta[c]);
-        s_al[c]           = k.al;
-        s_den[c]          = k.den;
-        s_rc[c]           = rcp_route_ok(k.den) ? rcp_d(static_cast<double>(k.den)) : 0.0;
+    if constexpr (CF) {
+        const double * tab = wave_exp_table(s_tab, lane, entry);
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int c = static_cast<int>(threadIdx.x) + 256 * j;
+            if (c < nc) {
+                // snake_coef<kSnakeBeta> with the table in LDS
+                const float al  = exp_f32_lds(la[j], tab);
+                const float den = exp_f32_lds(lb[j], tab) + kSnakeGuard;
+                s_al[c]         = al;
+                s_den[c]        = den;
+                s_rc[c]         = rcp_route_ok(den) ? rcp_d(static_cast<double>(den)) : 0.0;
+            }
+        }
+    } else {
+        for (int c = threadIdx.x; c < nc; c += 256) {
+            const SnakeCoef k = snake_coef<kSnakeBeta>(a.alpha[c], a.beta[c]);
+            s_al[c]           = k.al;
+            s_den[c]          = k.den;
+            s_rc[c]           = rcp_route_ok(k.den) ? rcp_d(static_cast<double>(k.den)) : 0.0;
+        }
     }
     __syncthreads();
     while (t < a.ntask) {
@@ -759,13 +795,13 @@ shp_status_t launch_snake(const shp_tensor * x, const shp_tensor * c0, const shp
         g.quads              = make_fastdiv(static_cast<uint32_t>(quads));
         if (ntask4 <= kSnakeLdsSmallTasks) {
             g.ntask = ntask4;
-            hipLaunchKernelGGL(k_snake_beta_lds<4>, dim3(static_cast<unsigned>((ntask4 + 255) / 256)), dim3(256), 0,
+            hipLaunchKernelGGL((k_snake_beta_lds<4, true>), dim3(static_cast<unsigned>((ntask4 + 255) / 256)), dim3(256), 0,
                                stream, g);
             return launch_status();
         }
         if (ntask8 <= kSnakeLdsMaxTasks) {
             g.ntask = ntask8;
-            hipLaunchKernelGGL(k_snake_beta_lds<8>, dim3(static_cast<unsigned>((ntask8 + 255) / 256)), dim3(256), 0,
+            hipLaunchKernelGGL((k_snake_beta_lds<8, false>), dim3(static_cast<unsigned>((ntask8 + 255) / 256)), dim3(256), 0,
                                stream, g);
             return launch_status();
         }

@@ -882,11 +882,14 @@ def test_snake_guarded(gpu, T, C):
     assert_bitexact(got[:, 0], x[:, 0])  # alpha = 0: the guard keeps sin(0)^2 / 1e-9 = 0
 
 
-@pytest.mark.parametrize("T,C", [(256, 512), (37, 64), (31, 30), (9, 2048), (4, 1028)])
+@pytest.mark.parametrize("T,C", [(256, 512), (37, 64), (31, 30), (9, 2048), (4, 1028), (1001, 1024), (77, 260)])
 def test_snake_beta(gpu, T, C):
     """codec_snake_beta (qwen3-tts): log curves over [-3, 3], so alpha/beta span
-    e^+-3 and the two exps, the guard and the division all matter. The flat
-    kernel takes 8 rows per lane: T = 37, 9 and 4 leave partial groups."""
+    e^+-3 and the two exps, the guard and the division all matter. Up to 1024
+    channels the 4-row LDS-table kernel runs (1024 channels: four per thread
+    in its table; 260: one or two); past 1024 the flat kernel, 8 rows per
+    lane: T = 37, 9 and 4 leave partial groups, as 1001 and 77 do for 4-row
+    tasks."""
     rng = np.random.default_rng(SEED + 11 * T + C)
     x = rng.standard_normal((T, C)).astype(np.float32)
     la = rng.uniform(-3, 3, C).astype(np.float32)
