@@ -549,7 +549,7 @@ template <bool KV> __device__ __forceinline__ int64_t rope_slot(const RopeArgs &
         if (sl >= 0 && sl <= a.cap - a.npos) {
             return sl;
         }
-        if (blockIdx.x == 0 && threadIdx.x == 0 && a.status != nullptr) {
+        if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0 && a.status != nullptr) {
             *a.status = 1;
         }
         return -1;
@@ -730,31 +730,52 @@ template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(1024) void k_
     }
 }
 
-// The same for a few positions (a decode step): the block's row waves take
-// their whole row through the QK-norm (and gains) before the barrier, while
-// one extra wave, wave 0, builds the position's cos/sin cache. The wave that
-// runs the serial theta chain then holds no rows, so the norm is no longer
-// behind the chain on the block's critical path: after the barrier a row wave
-// only rotates and stores. The theta wave comes first, so it is dispatched
-// first (measured on MI355X, one-token launch with the KV write: 2.78 us with
-// the theta wave after the rows, 2.63 us with it first). Same arithmetic as
-// k_rope128, bit for bit. At most kRopeDecMaxRows rows (the theta wave makes
-// the block one wave longer).
-constexpr int kRopeDecMaxRows = (1024 - kWave) / kRopeLanes;
+// The same for a few positions (a decode step). A position's head rows (q,
+// then k, then v) are split into blocks of kRopeDecRows rows (the grid's y),
+// and in each block the row waves take their whole row through the QK-norm
+// (and gains) before the barrier, while one extra wave, wave 0, builds the
+// position's cos/sin cache. The wave that runs the serial theta chain holds
+// no rows, so the norm is not behind the chain on the block's critical path:
+// after the barrier a row wave only rotates and stores. A block of v rows
+// only (the KV-cache write) copies them, with no theta wave work and no
+// barrier. Every block of a position runs the same theta chain, so a block
+// waits for at most 8 rows' loads and norms instead of all of them. Measured
+// on MI355X, one-token launch with the KV write (16 q + 8 k + 8 v rows, back
+// to back): 2.83 us as one block with the theta wave after the rows, 2.63
+// with it first and the slot a scalar load, 2.41 split over four blocks (4
+// rows per block: the same). Same arithmetic as k_rope128, bit for bit.
+constexpr int kRopeDecRows = 8;
 
-template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(1024) void k_rope128_dec(const RopeArgs a) {
+template <bool NORM, int WT, bool KV>
+__global__ __launch_bounds__(kWave + kRopeDecRows * kRopeLanes) void k_rope128_dec(const RopeArgs a) {
     __shared__ f32x4 s_cos[16];
     __shared__ f32x4 s_sin[16];
 
     const int64_t    pi    = blockIdx.x;
-    const int32_t    p     = a.pos[pi];  // before the field copies below: one scalar load
     const RopeFields f     = rope_fields<KV>(a);
     const int        total = rope_rows<KV>(f);
-    const int        tid   = static_cast<int>(threadIdx.x) - kWave;  // row thread index; < 0 in the theta wave
-    const bool       theta = tid < 0;                                 // uniform over each wave
-    const int        g     = theta ? 0 : tid / kRopeLanes;
+    const int        r0    = static_cast<int>(blockIdx.y) * kRopeDecRows;  // this block's first row
     const int        l     = static_cast<int>(threadIdx.x) % kRopeLanes;
-    const bool       live  = !theta & (g < total);
+    if (KV && r0 >= f.q.heads + f.k.heads) {
+        // v rows only: the cache write, a plain copy
+        const int     g    = r0 + static_cast<int>(threadIdx.x) / kRopeLanes;
+        const int64_t slot = rope_slot<KV>(a);
+        if (static_cast<int>(threadIdx.x) >= kRopeDecRows * kRopeLanes || g >= total || slot < 0) {
+            return;
+        }
+        const RowRef r  = rope_row<KV>(f, g, pi);
+        const f32x4  lo = ld_stream(to_global(reinterpret_cast<const f32x4 *>(r.x)) + l);
+        const f32x4  hi = ld_stream(to_global(reinterpret_cast<const f32x4 *>(r.x + 64)) + l);
+        float *      y  = r.y_at(slot);
+        st_stream(to_global(reinterpret_cast<f32x4 *>(y)) + l, lo);
+        st_stream(to_global(reinterpret_cast<f32x4 *>(y + 64)) + l, hi);
+        return;
+    }
+    const int32_t p     = a.pos[pi];
+    const int     tid   = static_cast<int>(threadIdx.x) - kWave;  // row thread index; < 0 in the theta wave
+    const bool    theta = tid < 0;                                 // uniform over each wave
+    const int     g     = r0 + (theta ? 0 : tid / kRopeLanes);
+    const bool    live  = !theta & (g < total);
 
     RowRef r = rope_row<KV>(f, live ? g : 0, pi);
     f32x4  lo = splat4(0.0f), hi = splat4(0.0f), rawlo = lo, rawhi = hi;
@@ -871,20 +892,21 @@ template <bool NORM, int WT, bool KV> __global__ __launch_bounds__(256) void k_r
 }
 
 // Up to this many positions a launch takes k_rope128_dec (a decode step of
-// a few streams); longer ones k_rope128, whose blocks hide the theta chain
-// behind each other. Measured on MI355X, 28-layer decode graphs: one stream
-// 7.95 -> 7.64 us per layer (4 launches), 64 streams 9.97 -> 10.12 us.
-constexpr int64_t kRopeDecMaxPos = 16;
+// up to 64 streams); longer ones k_rope128, whose blocks hide the theta chain
+// behind each other. Measured on MI355X (cold, 16 q + 8 k rows): one position
+// 2.38 -> 2.18 us, 16: 2.52 -> 2.46, 64: 2.62 -> 2.55; at 128 k_rope128 is
+// ahead (2.77 against 2.86).
+constexpr int64_t kRopeDecMaxPos = 64;
 
 template <bool NORM, int WT, bool KV> shp_status_t launch_rope(const RopeArgs & a, bool fast, hipStream_t stream) {
     if (dry_run()) {
         return SHP_OK;
     }
     const int total = a.part[0].heads + a.part[1].heads + a.part[2].heads;
-    if (fast && a.npos <= kRopeDecMaxPos && total <= kRopeDecMaxRows) {
-        const int threads = (total * kRopeLanes + kWave - 1) / kWave * kWave + kWave;
-        hipLaunchKernelGGL((k_rope128_dec<NORM, WT, KV>), dim3(static_cast<unsigned>(a.npos)), dim3(threads), 0,
-                           stream, a);
+    if (fast && a.npos <= kRopeDecMaxPos) {
+        const int chunks = (total + kRopeDecRows - 1) / kRopeDecRows;
+        hipLaunchKernelGGL((k_rope128_dec<NORM, WT, KV>), dim3(static_cast<unsigned>(a.npos), static_cast<unsigned>(chunks)),
+                           dim3(kWave + kRopeDecRows * kRopeLanes), 0, stream, a);
         return launch_status();
     }
     if (fast) {

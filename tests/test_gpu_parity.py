@@ -461,13 +461,14 @@ def test_rope_in_place_and_scaled(gpu):
 
 @pytest.mark.parametrize("T,hi,wkind", [(1, 64, "bf16"), (512, 512, "bf16"), (300, 8192, "f32"), (64, 8192, "f16"),
                                         (16, 8192, "f32"), (7, 32768, "f16"), (3, 8192, "bf16")])
-def test_qk_norm_rope(gpu, T, hi, wkind):
-    """T <= 16 takes the decode-step kernel (a separate wave builds the cos/sin
-    cache), longer runs the one whose wave 0 does; both bit-exact against the
-    restatement with correctly rounded cos/sin."""
+def test_qk_norm_rope(gpu, T, hi, wkind, H=16, KVH=8):
+    """T <= 64 takes the decode-step kernel (blocks of 8 head rows, each with a
+    separate wave building the cos/sin cache), longer runs the one whose wave
+    0 does; both bit-exact against the restatement with correctly rounded
+    cos/sin."""
     rng = np.random.default_rng(SEED + T)
-    q = rng.standard_normal((T, 16, 128)).astype(np.float32)
-    k = rng.standard_normal((T, 8, 128)).astype(np.float32)
+    q = rng.standard_normal((T, H, 128)).astype(np.float32)
+    k = rng.standard_normal((T, KVH, 128)).astype(np.float32)
     wq, wt = _weights(rng, 128, wkind)
     wk, _ = _weights(rng, 128, wkind)
     pos = _positions(rng, T, hi)
@@ -480,6 +481,13 @@ def test_qk_norm_rope(gpu, T, hi, wkind):
     qc, kc = R.run(lambda g: R.qk_norm_rope(g, q, k, wq, wk, eps, pos, 128, theta, wt, cs_rounded=True))
     assert_bitexact(_np(qo), qc)
     assert_bitexact(_np(ko), kc)
+
+
+@pytest.mark.parametrize("T,H,KVH", [(1, 6, 3), (3, 9, 7), (16, 20, 4)])
+def test_qk_norm_rope_head_counts(gpu, T, H, KVH):
+    """Decode-size launches in blocks of 8 head rows: 6 + 3 (one block with q
+    and k), 9 + 7 (blocks straddling q and k), 20 + 4 (three blocks)."""
+    test_qk_norm_rope(gpu, T, 8192, "bf16", H=H, KVH=KVH)
 
 
 def test_qk_norm_rope_generic_head_dim(gpu):
@@ -497,14 +505,13 @@ def test_qk_norm_rope_generic_head_dim(gpu):
 
 @pytest.mark.parametrize("T,filled,cap,hd,wkind", [(1, 37, 64, 128, "bf16"), (16, 0, 16, 128, "f32"),
                                                      (5, 10, 32, 64, "f32"), (3, 4, 8, 128, "f16")])
-def test_qk_norm_rope_kv(gpu, T, filled, cap, hd, wkind):
+def test_qk_norm_rope_kv(gpu, T, filled, cap, hd, wkind, H=16, KVH=8):
     """The fused cache write (operations.cpp:98-116): q_out and the cache rows
     [filled, filled + T) of k equal the unfused qk_norm_rope's outputs bit for
     bit and the oracle's within the rope bar (and bit-exact against the oracle
     with correctly rounded cos/sin); v lands in the same rows unchanged; every
     other cache row keeps its sentinel. hd = 64 takes the generic kernel."""
     rng = np.random.default_rng(SEED + 3 * T + filled)
-    H, KVH = 16, 8
     q = rng.standard_normal((T, H, hd)).astype(np.float32)
     k = rng.standard_normal((T, KVH, hd)).astype(np.float32)
     v = rng.standard_normal((T, KVH, hd)).astype(np.float32)
@@ -533,6 +540,15 @@ def test_qk_norm_rope_kv(gpu, T, filled, cap, hd, wkind):
     outside[rows] = False
     assert_bitexact(kc[outside], sentinel[outside])
     assert_bitexact(vc[outside], sentinel[outside])
+
+
+@pytest.mark.parametrize("T,H,KVH", [(1, 6, 3), (5, 12, 4), (2, 16, 8), (16, 9, 7)])
+def test_qk_norm_rope_kv_head_counts(gpu, T, H, KVH):
+    """Decode-size launches split a position's q, k and v rows into blocks of
+    8 rows: 6 + 3 + 3 puts k and v rows in one block, 12 + 4 + 4 a q/k block
+    and a v block of 4, 16 + 8 + 8 one block of v rows only, 9 + 7 + 7 blocks
+    that straddle every part. Same checks as above."""
+    test_qk_norm_rope_kv(gpu, T, 20, 64, 128, "bf16", H=H, KVH=KVH)
 
 
 def _kv_inputs(rng, T, hd=128, H=16, KVH=8):
