@@ -164,17 +164,18 @@ template <int K, bool MASK> __global__ __launch_bounds__(256) void k_soft_max_wa
 // WPR > 1 spreads the few long rows of a decode or short prefill over more
 // waves; the row's waves then combine their max and sum through LDS, in wave
 // order.
-template <int WPR, int K4, bool MASK> __global__ __launch_bounds__(256) void k_soft_max_rows4(const SoftMaxArgs a) {
+template <int WPR, int K4, bool MASK, int BLOCK = 256>
+__global__ __launch_bounds__(BLOCK) void k_soft_max_rows4(const SoftMaxArgs a) {
     constexpr int kLanes = kWave * WPR;
-    __shared__ float  s_max[256 / kWave];
-    __shared__ double s_sum[256 / kWave];
-    __shared__ double s_tab[256 / kWave][64];
+    __shared__ float  s_max[BLOCK / kWave];
+    __shared__ double s_sum[BLOCK / kWave];
+    __shared__ double s_tab[BLOCK / kWave][64];
     softmax_args_in_sgprs<MASK>(a);
     const int     lane = threadIdx.x % kWave;
     const int     q    = threadIdx.x % kLanes;
     const int     wv   = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
     const int     slot = wv / WPR;  // row of this block
-    const int64_t r    = static_cast<int64_t>(blockIdx.x) * (256 / kLanes) + slot;
+    const int64_t r    = static_cast<int64_t>(blockIdx.x) * (BLOCK / kLanes) + slot;
     const bool    live = r < a.nrows;
     if (WPR == 1 && !live) {
         return;  // whole wave; the one-wave form has no barrier
@@ -327,7 +328,9 @@ template <bool MASK> shp_status_t launch_soft_max(const SoftMaxArgs & a, bool ve
     if (vec) {
         // Few rows (under 8 waves per CU at one wave per row): 2 or 4 waves per
         // row. The decode step's 16 rows of 512 take one wave each (2.30 us
-        // against 2.36 us with two waves and their LDS combine, MI355X).
+        // against 2.36 us with two waves and their LDS combine, MI355X), in
+        // one-wave blocks: each row on its own CU (2.12 -> 1.99 us warm; the
+        // 28-layer decode graph's layer with the softmax 9.62 -> 9.45 us).
         const int n4  = a.ne0 / 4;
         const int wpr = a.nrows >= 2048 ? 1 : (n4 >= 256 ? 4 : (n4 >= 128 && a.nrows > 64 ? 2 : 1));
         const int k4  = (n4 + kWave * wpr - 1) / (kWave * wpr);
@@ -348,6 +351,10 @@ template <bool MASK> shp_status_t launch_soft_max(const SoftMaxArgs & a, bool ve
             }
         } else if (k4 <= 1) {
             hipLaunchKernelGGL((k_soft_max_rows4<1, 1, MASK>), g4, dim3(256), 0, stream, a);
+        } else if (k4 <= 2 && a.nrows <= 64) {
+            // a decode step's few rows: one one-wave block per row
+            hipLaunchKernelGGL((k_soft_max_rows4<1, 2, MASK, kWave>), dim3(static_cast<unsigned>(a.nrows)), dim3(kWave),
+                               0, stream, a);
         } else if (k4 <= 2) {
             hipLaunchKernelGGL((k_soft_max_rows4<1, 2, MASK>), g4, dim3(256), 0, stream, a);
         } else if (k4 <= 4) {

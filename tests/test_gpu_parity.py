@@ -656,9 +656,10 @@ def _ulps_apart(got, ref):
 @pytest.mark.parametrize("H,T,N,mask", [(16, 1, 37, "none"), (16, 64, 64, "causal"), (4, 7, 2500, "heads2"),
                                         (3, 5, 64, "rows+"), (2, 3, 1, "none"), (8, 33, 2048, "causal"),
                                         (2, 2, 4097, "none"), (16, 1, 512, "none"), (3, 1, 512, "rows+"),
-                                        (6, 3, 1024, "heads2"), (16, 512, 512, "causal")])
+                                        (6, 3, 1024, "heads2"), (16, 512, 512, "causal"), (6, 4, 300, "heads2")])
 def test_soft_max_ext(gpu, H, T, N, mask):
-    """ggml_soft_max_ext with scale 1/sqrt(128): decode rows (1 x 37, 1 x 512),
+    """ggml_soft_max_ext with scale 1/sqrt(128): decode rows (1 x 37, 1 x 512;
+    up to 64 rows of 260-512 take one-wave blocks, as 24 rows of 300 do),
     causal prefills, a mask broadcast over 2 heads, a mask with more rows than
     the scores, a one-element row, rows spread over 2 waves (512 wide; 3 rows
     leave the last block half empty) and 4 waves (1024, 2048 wide), and rows
