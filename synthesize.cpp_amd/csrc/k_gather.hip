@@ -1142,9 +1142,10 @@ template <int NSB> __global__ __launch_bounds__(256) void k_get_rows_sum_q5k(con
 // slower at configs[2]'s shape.) The decode is about five vector
 // instructions per element and group -- the quant assembly of shp_q5k.hpp, a
 // byte conversion, the fma and the add, which the reference's two roundings
-// keep apart -- so at large launches this kernel is bound by instruction
-// issue, not by HBM (the Q8_0 windows, two instructions per element, reach
-// the same time per lookup while moving 1.5x the bytes).
+// keep apart. It is not what bounds the kernel: on MI355X at configs[2]'s
+// shape, taking the decode out saves 15 % and taking two of the three loads
+// per group out 5 %; the rest is the chunks' load latency in sequence
+// (persistent waves that carry the pipeline across frames were slower).
 // Slots past the last group read kQ5KNegZeroRow, which adds exactly nothing;
 // the prefetch past the end of the loop reads it too (or group 63's rows,
 // undecoded, when there are 64 groups).
