@@ -1144,8 +1144,9 @@ template <int NSB> __global__ __launch_bounds__(256) void k_get_rows_sum_q5k(con
 // byte conversion, the fma and the add, which the reference's two roundings
 // keep apart. It is not what bounds the kernel: on MI355X at configs[2]'s
 // shape, taking the decode out saves 15 % and taking two of the three loads
-// per group out 5 %; the rest is the chunks' load latency in sequence
-// (persistent waves that carry the pipeline across frames were slower).
+// per group out 5 %, and neither persistent waves that carry the pipeline
+// across frames nor a sliding window of 4-8 groups in flight is faster: the
+// rest is the rate at which scattered 704-byte rows are served.
 // Slots past the last group read kQ5KNegZeroRow, which adds exactly nothing;
 // the prefetch past the end of the loop reads it too (or group 63's rows,
 // undecoded, when there are 64 groups).
