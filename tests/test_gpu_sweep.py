@@ -1,7 +1,7 @@
 """Seeded random sweep: each entry point over shapes drawn across its launch
 forms (row counts either side of the norm's 2048/4096/16384 boundaries, head
 counts that straddle the decode rope's blocks of 8 rows, softmax rows either
-side of 256/512/2048 elements, gathers of 1..4099 ids, 1..20 codebooks, Snake
+side of 256/512/2048 elements, gathers of 1..4099 ids (F32/F16/BF16/Q8_0/Q5_K), 1..20 codebooks (1..33 for Q5_K), Snake
 channel counts that are and are not multiples of 4, ragged last blocks), each
 against the ggml-CPU restatement on the same inputs and to the bars of
 test_gpu_parity.py: bit-exact for gathers, sums of gathers, adds and
@@ -13,6 +13,7 @@ SWEEP_SEED, so a failure names a shape that reruns the same way.
 import numpy as np
 import pytest
 
+import formats as F
 import ggml_ref as R
 from test_gpu_parity import (_dev_table, _dev_w, _np, _positions, _specials, _t, _table, _ulps_apart, _weights,
                              assert_bitexact, assert_close, assert_rope_close, assert_snake_close)
@@ -152,6 +153,36 @@ def test_sweep_get_rows_sum(gpu, kind, ne0, groups, frames):
     codes = rng.integers(0, rows, (groups, frames)).astype(np.int32)
     ref = R.run(lambda g: R.sum_code_embeddings(g, [t for t, _ in tabs], tabs[0][1], ne0, codes))
     got = gpu.get_rows_sum([_dev_table(gpu, t, kind, ne0) for t, _ in tabs], _t(gpu, codes))
+    assert_bitexact(_np(got), ref)
+
+
+def _q5k_case(rng):
+    return (256 * _pick(rng, [1, 2, 3, 4, 5, 8, 12, 16]), _pick(rng, [1, 7, 60, 2048]),
+            _pick(rng, [1, 2, 63, 64, 65, 257, 1000, 4099]))
+
+
+@pytest.mark.parametrize("ne0,rows,n", _gen("get_rows_q5k", _q5k_case))
+def test_sweep_get_rows_q5k(gpu, ne0, rows, n):
+    rng = np.random.default_rng([SWEEP_SEED, 29, ne0, rows, n])
+    raw = F.q5_k_synthetic(rng, rows, ne0)
+    ids = rng.integers(0, rows, n).astype(np.int32)
+    ids[-1] = rows - 1
+    ref = R.run(lambda g: g.get_rows(raw, R.Q5_K, ne0, ids))
+    assert_bitexact(_np(gpu.get_rows(gpu.Q5KTensor(_t(gpu, raw), ne0), _t(gpu, ids))), ref)
+
+
+def _q5k_sum_case(rng):
+    return (256 * _pick(rng, [1, 2, 3, 4, 8, 12, 16]), int(rng.integers(1, 34)), _pick(rng, [1, 3, 64, 301, 1025]))
+
+
+@pytest.mark.parametrize("ne0,groups,frames", _gen("get_rows_sum_q5k", _q5k_sum_case))
+def test_sweep_get_rows_sum_q5k(gpu, ne0, groups, frames):
+    rng = np.random.default_rng([SWEEP_SEED, 31, ne0, groups, frames])
+    rows = 60
+    tabs = [F.q5_k_synthetic(rng, rows, ne0) for _ in range(groups)]
+    codes = rng.integers(0, rows, (groups, frames)).astype(np.int32)
+    ref = R.run(lambda g: R.sum_code_embeddings(g, tabs, R.Q5_K, ne0, codes))
+    got = gpu.get_rows_sum([gpu.Q5KTensor(_t(gpu, t), ne0) for t in tabs], _t(gpu, codes))
     assert_bitexact(_np(got), ref)
 
 
