@@ -1,14 +1,19 @@
 """Seeded random sweep: each entry point over shapes drawn across its launch
-forms (row counts either side of the norm's 2048/4096/16384 boundaries, head
-counts that straddle the decode rope's blocks of 8 rows, softmax rows either
-side of 256/512/2048 elements, gathers of 1..4099 ids (F32/F16/BF16/Q8_0/Q5_K), 1..20 codebooks (1..33 for Q5_K), Snake
-channel counts that are and are not multiples of 4, ragged last blocks), each
-against the ggml-CPU restatement on the same inputs and to the bars of
-test_gpu_parity.py: bit-exact for gathers, sums of gathers, adds and
-leaky-ReLU; 1e-5 relative for the norms, SwiGLU and the Snake family; rope to
-1e-5 of its NEOX pair against libm and bit-exact against the restatement with
-correctly rounded cos/sin; softmax within 2 ulp. The case list is fixed by
-SWEEP_SEED, so a failure names a shape that reruns the same way.
+forms, against the ggml-CPU restatement on the same inputs:
+- norm row counts either side of the 2048 / 4096 / 16384 boundaries;
+- QK-norm+RoPE head counts that straddle the decode kernel's blocks of 8
+  rows, with and without the KV-cache write (slots that fit exactly or not);
+- softmax rows either side of 256 / 512 / 2048 elements;
+- gathers of 1..4099 ids (F32/F16/BF16/Q8_0/Q5_K) and sums of 1..20
+  codebooks (1..33 for Q5_K);
+- Snake channel counts that are and are not multiples of 4, ragged last
+  blocks everywhere.
+The bars are test_gpu_parity.py's: bit-exact for gathers, sums of gathers,
+adds and leaky-ReLU; 1e-5 relative for the norms, SwiGLU and the Snake
+family; rope to 1e-5 of its NEOX pair against libm and bit-exact against the
+restatement with correctly rounded cos/sin; softmax within 2 ulp. The case
+list is fixed by SWEEP_SEED, so a failure names a shape that reruns the same
+way.
 """
 import numpy as np
 import pytest
@@ -113,6 +118,23 @@ def test_sweep_qk_norm_rope(gpu, T, H, KVH, hi, wkind):
     qc, kc = R.run(lambda g: R.qk_norm_rope(g, q, k, wq, wk, eps, pos, 128, theta, wt, cs_rounded=True))
     assert_bitexact(qo, qc)
     assert_bitexact(ko, kc)
+
+
+def _rope_kv_case(rng):
+    T = _pick(rng, [1, 1, 2, 5, 16, 63, 64, 65, 128])
+    H = int(rng.integers(1, 25))
+    KVH = int(rng.integers(1, H + 1))
+    filled = int(rng.integers(0, 200))
+    cap = filled + T + _pick(rng, [0, 1, 37])
+    return (T, H, KVH, filled, cap, _pick(rng, ["f32", "bf16", "f16"]))
+
+
+@pytest.mark.parametrize("T,H,KVH,filled,cap,wkind", _gen("qk_norm_rope_kv", _rope_kv_case))
+def test_sweep_qk_norm_rope_kv(gpu, T, H, KVH, filled, cap, wkind):
+    """The fused cache write: the same bits as the unfused kernel for q and
+    the cache's k rows, v copied, every other cache row untouched."""
+    from test_gpu_parity import test_qk_norm_rope_kv
+    test_qk_norm_rope_kv(gpu, T, filled, cap, 128, wkind, H=H, KVH=KVH)
 
 
 # ---------------------------------------------------------------------------
