@@ -7,7 +7,8 @@ forms, against the ggml-CPU restatement on the same inputs:
 - gathers of 1..4099 ids (F32/F16/BF16/Q8_0/Q5_K) and sums of 1..20
   codebooks (1..33 for Q5_K);
 - Snake channel counts that are and are not multiples of 4, ragged last
-  blocks everywhere.
+  blocks everywhere;
+- the one-call layer step at 1..513 positions.
 The bars are test_gpu_parity.py's: bit-exact for gathers, sums of gathers,
 adds and leaky-ReLU; 1e-5 relative for the norms, SwiGLU and the Snake
 family; rope to 1e-5 of its NEOX pair against libm and bit-exact against the
@@ -135,6 +136,19 @@ def test_sweep_qk_norm_rope_kv(gpu, T, H, KVH, filled, cap, wkind):
     the cache's k rows, v copied, every other cache row untouched."""
     from test_gpu_parity import test_qk_norm_rope_kv
     test_qk_norm_rope_kv(gpu, T, filled, cap, 128, wkind, H=H, KVH=KVH)
+
+
+def _layer_case(rng):
+    return (_pick(rng, [1, 2, 3, 17, 64, 65, 127, 300, 513]), _pick(rng, [128, 128, 64]),
+            _pick(rng, ["f32", "bf16", "f16"]))
+
+
+@pytest.mark.parametrize("T,hd,wkind", _gen("layer_nongemm_step", _layer_case, n=12))
+def test_sweep_layer_nongemm_step(gpu, T, hd, wkind):
+    """One call for a layer's non-GEMM node runs: each output the single
+    entry points' bits and the oracle's, at the talker's widths."""
+    from test_gpu_parity import test_layer_nongemm_step
+    test_layer_nongemm_step(gpu, T, hd, wkind)
 
 
 # ---------------------------------------------------------------------------
