@@ -158,10 +158,34 @@ def time_graphs(torch, graphs, reps, label=None):
     return start.elapsed_time(end)
 
 
+def time_chunks(torch, graph, replays, chunks, label=None):
+    """Replays `graph` chunks x replays times back to back, with a HIP event
+    recorded on the launching stream between chunks; returns each chunk's ms."""
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(chunks + 1)]
+    torch.cuda.synchronize()
+    if label:
+        ROCTX.push(label)
+    evs[0].record()
+    for c in range(chunks):
+        for _ in range(replays):
+            graph.replay()
+        evs[c + 1].record()
+    torch.cuda.synchronize()
+    if label:
+        ROCTX.pop()
+    return [evs[c].elapsed_time(evs[c + 1]) for c in range(chunks)]
+
+
+CHUNKS = 10
+
+
 def measure_op(torch, make, nbytes, reps_target=200, cold=True, label=None):
-    """Average launch duration (us) of the op built by make() -> callable, over
-    enough rotating input sets to exceed COLD_BYTES (cold=False: one set,
-    cache resident), replayed from one graph."""
+    """Launch duration (us) of the op built by make() -> callable, over enough
+    rotating input sets to exceed COLD_BYTES (cold=False: one set, cache
+    resident), replayed from one graph: the graph is replayed in CHUNKS timed
+    chunks of at least reps_target / CHUNKS launches each, and the result is
+    the median over chunks of the mean launch duration in a chunk (the mean
+    over all launches is returned beside it)."""
     nsets = 1 if (nbytes >= COLD_BYTES or not cold) else -(-COLD_BYTES // nbytes) + 1
     nsets = min(nsets, 4096)
     fns = [make() for _ in range(nsets)]
@@ -171,12 +195,14 @@ def measure_op(torch, make, nbytes, reps_target=200, cold=True, label=None):
         fns = fns * (4 if cold else 256)  # enough nodes to amortise the graph launch
     graph = capture(torch, fns)
     time_graphs(torch, [graph], 2)
-    reps = max(2, reps_target // len(fns))
-    us = time_graphs(torch, [graph], reps, label) * 1e3 / (reps * len(fns))
+    replays = max(1, -(-reps_target // (CHUNKS * len(fns))))
+    ms = time_chunks(torch, graph, replays, CHUNKS, label)
+    nf = len(fns)
+    per = [m * 1e3 / (replays * nf) for m in ms]
     del graph, fns
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
-    return us, nsets
+    return statistics.median(per), nsets, statistics.mean(per), CHUNKS * replays * nf
 
 
 class Rows:
@@ -186,10 +212,11 @@ class Rows:
         self.torch, self.rows = torch, []
 
     def run(self, cfg, name, nbytes, make, cold=True, extra=None, quiet=False):
-        us, nsets = measure_op(self.torch, make, nbytes, cold=cold, label=row_label(cfg, name, nbytes))
+        us, nsets, mean, launches = measure_op(self.torch, make, nbytes, cold=cold,
+                                               label=row_label(cfg, name, nbytes))
         gbs = nbytes / (us * 1e-6) / 1e9
         row = {"config": cfg, "op": name, "bytes": nbytes, "us": round(us, 3), "GB/s": round(gbs, 1),
-               "frac": round(gbs / PEAK_GBS, 4), "sets": nsets}
+               "frac": round(gbs / PEAK_GBS, 4), "sets": nsets, "us_mean": round(mean, 3), "launches": launches}
         if not cold:
             row["note"] = "warm (one input set)"
         for k, v in (extra or {}).items():
@@ -446,12 +473,16 @@ def vocoder_rows(R, S, torch, cfg, seed, shapes=((512, 8192), (256, 32768), (128
 # decode step: 28 layers x (add+norm, qk-norm+rope, add+norm, swiglu) at T=1
 # ---------------------------------------------------------------------------
 
-def decode_layer_us(S, torch, layers=28, reps=50, kv=False, total=512, streams=1, label=None):
+DECODE_TOTAL = 38  # configs[0]: the token at position 37 attends over 38 keys
+
+
+def decode_layer_us(S, torch, layers=28, reps=50, kv=False, total=DECODE_TOTAL, streams=1, label=None):
     """us per talker layer of the decode step's non-GEMM ops, replayed as one
-    graph of `layers` layers. kv: qk-norm+rope also writes this step's k and v
-    into the layer's cache (slot total-1) and the step adds the attention
-    softmax over `total` keys for the 16 heads (5 launches per layer).
-    streams: concurrent decode streams batched into each op (one token each)."""
+    graph of `layers` layers (median over CHUNKS timed chunks of replays).
+    kv: qk-norm+rope also writes this step's k and v into the layer's cache
+    (slot total-1) and the step adds the attention softmax over `total` keys
+    for the 16 heads (5 launches per layer). streams: concurrent decode
+    streams batched into each op (one token each), each at position total-1."""
     assert not (kv and streams != 1), "the KV variant models one stream"
     g, randn, empty, bf16 = gen(torch, SEED + 1)
     L = []
@@ -487,11 +518,44 @@ def decode_layer_us(S, torch, layers=28, reps=50, kv=False, total=512, streams=1
         f()
     graph = capture(torch, fns)
     time_graphs(torch, [graph], 5)
-    ms = time_graphs(torch, [graph], reps, label)
-    return ms * 1e3 / (reps * layers)
+    ms = time_chunks(torch, graph, max(1, reps // CHUNKS), CHUNKS, label)
+    return statistics.median(ms) * 1e3 / (max(1, reps // CHUNKS) * layers)
 
 
-def decode_layer_bytes(streams=1, kv=False, total=512):
+def decode_layer_graph_us(S, torch, layers=28, reps=50, total=DECODE_TOTAL, label=None):
+    """us per talker layer of the one-token decode step run through the
+    node-run executor: `layers` chained copies of decoder_layer's non-GEMM node
+    list in the reference's expand order (qwen3_layer.decoder_layer_nodes: the
+    projections, attention scores and outputs as leaves, the KV cache written
+    at slot total-1, the softmax over `total` keys, each layer's output add
+    feeding the next layer's input norm), planned by shp_graph_compute inside
+    one HIP graph capture and replayed (median over CHUNKS timed chunks).
+    Returns (us per layer, the plan's launch count)."""
+    import qwen3_layer as Q
+    g_, randn, empty, bf16 = gen(torch, SEED + 2)
+    g = S.Graph()
+    x, outs = randn(1, 1024), []
+    for _ in range(layers):
+        leaves = dict(q=randn(1, 16, 128), k=randn(1, 8, 128), v=randn(1, 8, 128), scores=randn(16, 1, total),
+                      attn=randn(1, 1024), gate=randn(1, 3072), up=randn(1, 3072), mlp=randn(1, 1024),
+                      w_in=bf16(1024), w_post=bf16(1024), wq=bf16(128), wk=bf16(128),
+                      pos=torch.full((1,), total - 1, dtype=torch.int32, device="cuda"),
+                      kcache=randn(total, 8, 128), vcache=randn(total, 8, 128))
+        o, _ = Q.decoder_layer_nodes(g, x, leaves, total=total)
+        outs += o
+        x = o[-1]
+    launches = sum(1 for k, *_ in g.plan(*outs) if k not in ("nop", "unsupported"))
+    arr, n, keep = g.nodes(*outs)
+    lib, fns = S.load(), [lambda: S._check(S.load().shp_graph_compute(arr, n, S._stream()), "graph_compute")]
+    fns[0]()
+    graph = capture(torch, fns)
+    time_graphs(torch, [graph], 5)
+    ms = time_chunks(torch, graph, max(1, reps // CHUNKS), CHUNKS, label)
+    del graph, keep, lib
+    return statistics.median(ms) * 1e3 / (max(1, reps // CHUNKS) * layers), launches
+
+
+def decode_layer_bytes(streams=1, kv=False, total=DECODE_TOTAL):
     """Algorithmic bytes of one layer of decode_layer_us's graph, every operand
     once: add+norm (a, b read; sum, y written; BF16 gain), qk-norm+rope (q, k
     read and written; two BF16 gains; one I32 position per stream), add+norm
@@ -591,6 +655,140 @@ def cpu_baseline(step, torch, seconds):
 
 
 # ---------------------------------------------------------------------------
+# CPU baseline per op: each row's node run on the restatement
+# ---------------------------------------------------------------------------
+
+def _time_cpu(g, nth, budget):
+    """Seconds per run of the restatement graph `g` at `nth` threads: one
+    warm-up run and one timed run, then the median of as many more as fit in
+    `budget` seconds (at most 20)."""
+    t = g.time(nth, 1, 1)[0]
+    reps = int(min(20, budget / max(t, 1e-7)))
+    if reps >= 3:
+        t = statistics.median(g.time(nth, 0, reps))
+    return t
+
+
+def cpu_op_builders(seed=SEED + 9):
+    """[(config, op name, algorithmic bytes, build(g))] for every row the bench
+    line carries, named as its GPU row: the same node runs over host inputs of
+    the same shapes (one pool of N(0,1) values, each operand a differently
+    offset window of it), as the reference's graphs build them for ggml-CPU."""
+    import numpy as np
+    import formats as F
+    import ggml_ref as R
+    rng = np.random.default_rng(seed)
+    pool = rng.standard_normal(8192 * 6144 + 4096, dtype=np.float32)
+    cursor = [0]
+
+    def take(*shape):
+        n = math.prod(shape)
+        o = (cursor[0] * 61) % 4096
+        cursor[0] += 1
+        return pool[o:o + n].reshape(shape)
+
+    bf16 = lambda n: F.f32_to_bf16_bits(rng.normal(1.0, 0.1, n).astype(np.float32))
+    eps, theta, f32 = np.float32(1e-6), np.float32(1e6), 4
+    out = []
+    T, H, F_ = 8192, 2048, 6144
+    cfg = "configs[4]"
+    out.append((cfg, "rms_norm_mul [%d,%d]" % (H, T), 2 * T * H * f32 + H * 2,
+                lambda g: R.rms_norm_w(g, take(T, H), bf16(H), eps, R.BF16)))
+    out.append((cfg, "qk_norm_rope q[128,16,%d] k[128,8,%d]" % (T, T), 2 * 24 * 128 * T * f32 + T * 4 + 512,
+                lambda g: R.qk_norm_rope(g, take(T, 16, 128), take(T, 8, 128), bf16(128), bf16(128), eps,
+                                         np.arange(T, dtype=np.int32), 128, theta, R.BF16)))
+    out.append((cfg, "add_rms_norm_mul+sum [%d,%d]" % (H, T), 4 * T * H * f32 + H * 2,
+                lambda g: R.add_rms_norm_w(g, take(T, H), take(T, H), bf16(H), eps, R.BF16)))
+    out.append((cfg, "swiglu [%d,%d]" % (F_, T), 3 * T * F_ * f32, lambda g: R.swiglu(g, take(T, F_), take(T, F_))))
+    out.append((cfg, "add [%d,%d]" % (H, T), 3 * T * H * f32, lambda g: g.add(take(T, H), take(T, H))))
+
+    for kind, synth, rb, typ in (("q8_0", F.q8_0_synthetic, 1024 // 32 * 34, R.Q8_0),
+                                 ("q5_k", F.q5_k_synthetic, 1024 // 256 * 176, R.Q5_K)):
+        def gsum(g, synth=synth, typ=typ):
+            tabs = [synth(rng, 2048, 1024) for _ in range(16)]
+            codes = rng.integers(0, 2048, (16, 4096)).astype(np.int32)
+            return R.sum_code_embeddings(g, tabs, typ, 1024, codes)
+
+        def gone(g, synth=synth, typ=typ):
+            return g.get_rows(synth(rng, 2048, 1024), typ, 1024, rng.integers(0, 2048, 4096).astype(np.int32))
+        out.append(("configs[2]", "get_rows_sum %s 16x[1024,2048] x4096" % kind, 4096 * (16 * (rb + 4) + 1024 * f32),
+                    gsum))
+        out.append(("configs[2]", "get_rows %s [1024,2048] x4096" % kind, 4096 * (rb + 4 + 1024 * f32), gone))
+
+    for C, Tv in ((512, 8192), (256, 32768), (128, 131072)):
+        n = C * Tv
+        al = lambda C=C: np.exp(rng.uniform(math.log(0.1), math.log(10.0), C)).astype(np.float32)
+        lg = lambda C=C: rng.uniform(-3.0, 3.0, C).astype(np.float32)
+        cfg = "configs[3]"
+        out.append((cfg, "snake [%d,%d]" % (C, Tv), 8 * n + 4 * C,
+                    lambda g, C=C, Tv=Tv, al=al: R.snake(g, take(Tv, C), al())))
+        out.append((cfg, "snake_beta [%d,%d]" % (C, Tv), 8 * n + 8 * C,
+                    lambda g, C=C, Tv=Tv, lg=lg: R.snake_beta(g, take(Tv, C), lg(), lg())))
+        # ggml-CPU's add node always writes the sum, so one CPU run serves both rows
+        for name, nbytes in (("add_leaky_relu [%d,%d]" % (C, Tv), 12 * n),
+                             ("add_leaky_relu+sum [%d,%d]" % (C, Tv), 16 * n)):
+            out.append((cfg, name, nbytes,
+                        lambda g, C=C, Tv=Tv: R.add_leaky(g, take(Tv, C), take(Tv, C), np.float32(0.1))))
+    return out
+
+
+def cpu_decode_layers(g, layers=28, total=DECODE_TOTAL, seed=SEED + 10):
+    """The configs[0] decode step's non-GEMM nodes on the restatement, as
+    ggml-CPU runs them for the talker today (src/arch/qwen3-tts/model.cpp:
+    99-126), decoder_layer's list per layer (operations.cpp:84-147): the
+    input norm, QK-norm and rope of q and k, the k and v cache copies at slot
+    total-1, the softmax over `total` keys, the residual add and the
+    post-attention norm, SwiGLU and the output add; `layers` layers chained
+    in one node list (the projections' outputs as inputs)."""
+    import numpy as np
+    import formats as F
+    import ggml_ref as R
+    rng = np.random.default_rng(seed)
+    r = lambda *shape: rng.standard_normal(shape).astype(np.float32)
+    bf16 = lambda n: F.f32_to_bf16_bits(rng.normal(1.0, 0.1, n).astype(np.float32))
+    eps, theta = np.float32(1e-6), np.float32(1e6)
+    pos = np.full(1, total - 1, np.int32)
+    x = r(1, 1024)
+    for _ in range(layers):
+        R.rms_norm_w(g, x, bf16(1024), eps, R.BF16)
+        qr, kr = R.qk_norm_rope(g, r(1, 16, 128), r(1, 8, 128), bf16(128), bf16(128), eps, pos, 128, theta, R.BF16)
+        kc, vc, v = r(total, 8, 128), r(total, 8, 128), r(1, 8, 128)
+        g._node(R.OP_CAST_F32, kc[total - 1:], kr, type0=R.F32, ne0=128, nrows=8)
+        g._node(R.OP_CAST_F32, vc[total - 1:], v, type0=R.F32, ne0=128, nrows=8)
+        g.soft_max_ext(r(16, 1, total), None, np.float32(1.0 / math.sqrt(128.0)))
+        after, _ = R.add_rms_norm_w(g, x, r(1, 1024), bf16(1024), eps, R.BF16)
+        R.swiglu(g, r(1, 3072), r(1, 3072))
+        x = g.add(after, r(1, 1024))
+    return g
+
+
+def cpu_op_baselines(seconds):
+    """Each row's node run on the restatement at N, max(1, N/2) and 1 threads
+    (N: this process's CPU share, as cpu_share), within about `seconds` in
+    all. Returns ({(config, op): entry}, decode-layer entry)."""
+    import ggml_ref as R
+    share = cpu_share()
+    nth = share["threads_used"]
+    threads = [nth, max(1, nth // 2), 1]
+    builders = cpu_op_builders()
+    budget = seconds / (3 * (len(builders) + 1))
+    by_row = {}
+    for cfg, name, nbytes, build in builders:
+        g = R.Graph()
+        build(g)
+        ts = [_time_cpu(g, t, budget) for t in threads]
+        by_row[(cfg, name)] = {"threads": threads, "us": [round(t * 1e6, 1) for t in ts],
+                               "GB/s": [round(nbytes / t / 1e9, 2) for t in ts], "nodes": len(g.nodes)}
+        del g
+    g = cpu_decode_layers(R.Graph())
+    ts = [_time_cpu(g, t, budget) / 28 for t in threads]
+    nb = decode_layer_bytes(kv=True)
+    dec = {"threads": threads, "us_per_layer": [round(t * 1e6, 2) for t in ts],
+           "GB/s": [round(nb / t / 1e9, 3) for t in ts], "nodes_per_layer": len(g.nodes) // 28}
+    return by_row, dec
+
+
+# ---------------------------------------------------------------------------
 # --suite: every op on every BASELINE config, small shapes included
 # ---------------------------------------------------------------------------
 
@@ -676,9 +874,11 @@ def suite(args, S, torch):
         R.run("configs[0]", "soft_max_ext [512,1,16]", 2 * 16 * 512 * f32, make_sm, cold=False)
         per_layer("configs[0]", "talker layer non-GEMM step (28-layer graph, 4 launches/layer)",
                   decode_layer_us(S, torch), decode_layer_bytes(), "per layer")
-        per_layer("configs[0]", "talker layer non-GEMM step + KV-cache write + soft_max over 512 keys "
+        per_layer("configs[0]", "talker layer non-GEMM step + KV-cache write + soft_max over 38 keys "
                   "(28-layer graph, 5 launches/layer)", decode_layer_us(S, torch, kv=True),
                   decode_layer_bytes(kv=True), "per layer")
+        per_layer("configs[0]", "talker layer non-GEMM node list through shp_graph_compute (28 layers)",
+                  decode_layer_graph_us(S, torch)[0], decode_layer_bytes(kv=True), "per layer")
 
     if on("configs1"):
         norm_case("configs[1]", 512, 1024)
@@ -1023,15 +1223,24 @@ def main():
     q8_rows(R, S, torch, "configs[2]", SEED + 6, kind="q5_k")
     vocoder_rows(R, S, torch, "configs[3]", SEED + 4)
 
+    if not args.no_cpu:
+        cpu_rows, cpu_dec = cpu_op_baselines(args.cpu_seconds)
+        for row in list(ops4.values()) + R.rows:
+            c = cpu_rows.get((row["config"], row["op"]))
+            if c is not None:
+                row["cpu"] = c
+
     dom = max(ops4, key=lambda n: ops4[n]["us"])
     d = ops4[dom]
     roof = {"bound": "hbm", "kernel": d["op"], "achieved": d["GB/s"], "peak": PEAK_GBS, "unit": "GB/s",
             "frac": d["frac"], "traffic": read_traffic(d["op"]), "algorithmic_bytes": d["bytes"],
             "us_per_launch": d["us"]}
 
-    # one decode token per layer, 28 layers in one graph
+    # one decode token per layer (position 37), 28 layers in one graph
     dec = decode_layer_us(S, torch, label="step:configs[0] decode, 28 layers x 4 launches")
     dec_full = decode_layer_us(S, torch, kv=True, label="step:configs[0] decode + kv + softmax, 28 layers x 5 launches")
+    dec_graph, dec_graph_launches = decode_layer_graph_us(
+        S, torch, label="step:configs[0] decode through shp_graph_compute, 28 layers")
     # 64 concurrent decode streams
     dec64 = decode_layer_us(S, torch, streams=64, label="step:configs[4] 64-stream decode, 28 layers x 4 launches")
     # the 0.6B talker's 512-token prefill step with the text-embedding gather
@@ -1057,10 +1266,16 @@ def main():
         "roofline": roof,
         "decode_layer_us": round(dec, 3),
         "decode_layer_full_us": round(dec_full, 3),
-        "decode_layer_note": "configs[0]: us per talker layer of a 28-layer one-token decode graph; _us: "
-                             "add+norm, qk-norm+rope, add+norm, swiglu (4 launches, %d B); _full_us: with the "
-                             "KV-cache write fused into qk-norm+rope and the 16-head softmax over 512 keys "
-                             "(5 launches, %d B)" % (decode_layer_bytes(), decode_layer_bytes(kv=True)),
+        "decode_layer_graph_us": round(dec_graph, 3),
+        "decode_layer_note": "configs[0]: us per talker layer of a 28-layer one-token decode graph at position 37 "
+                             "(median of %d timed chunks); _us: add+norm, qk-norm+rope, add+norm, swiglu "
+                             "(4 launches, %d B); _full_us: with the KV-cache write fused into qk-norm+rope and "
+                             "the 16-head softmax over 38 keys (5 launches, %d B), entry points called directly; "
+                             "_graph_us: the same work as decoder_layer's non-GEMM node list in the reference's "
+                             "expand order (operations.cpp:84-147; GEMM outputs as leaves, 28 chained layers), "
+                             "planned and launched by shp_graph_compute inside one HIP graph capture: %d launches "
+                             "for 28 layers" % (CHUNKS, decode_layer_bytes(), decode_layer_bytes(kv=True),
+                                                dec_graph_launches),
         "decode64_step_us": round(28 * dec64, 2),
         "decode64_note": "configs[4]: 64 concurrent decode streams, us per 28-layer step (%d B per step)" % (
             28 * decode_layer_bytes(streams=64)),
@@ -1070,6 +1285,14 @@ def main():
     }
     if cpu is not None:
         line["cpu_baseline"] = cpu
+    if not args.no_cpu:
+        line["decode_layer_cpu"] = dict(cpu_dec, note="configs[0]: the same decode layer's non-GEMM nodes (28 "
+                                        "chained layers, %d B per layer) on the ggml-CPU restatement, us per "
+                                        "layer at the threads listed" % decode_layer_bytes(kv=True))
+        line["cpu_rows_note"] = ("each ops/rows entry's 'cpu': its node run on the ggml-CPU restatement "
+                                 "(oracle/ggml_cpu_ref.c, ggml's row split) over host inputs of the same shapes, "
+                                 "at N, max(1, N/2) and 1 threads (N = threads_used); median of up to 20 runs after "
+                                 "a warm-up, within --cpu-seconds in all; a reported baseline only")
     print(json.dumps(line), flush=True)
 
 

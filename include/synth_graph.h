@@ -19,6 +19,13 @@
  *   RMS_NORM [CPY] MUL [ROPE [CPY]]  rms_norm()*w, with the gain cast and a
  *        following NEOX rope and cache copy folded in
  *        (src/arch/qwen3-tts/operations.cpp:20-32, 98-116)
+ *   two such rope runs + [CPY]        the q and k runs of one attention block
+ *        (:98-104) with k's cache copy and v's (:109-116) in one launch: the
+ *        sibling run and the v copy may sit later in the list with other
+ *        nodes between (ggml expands the k and v copies before the q path);
+ *        they are moved up to the first run only when no node between them
+ *        reads or writes what they read or write (byte ranges of the
+ *        descriptors) and none produces what they read
  *   ADD RMS_NORM [CPY] MUL           residual add + post-attention norm
  *        (:143-145, :147 -> :86); the sum is written when read elsewhere
  *   SILU MUL                         SwiGLU (:39-41)
@@ -99,14 +106,18 @@ typedef enum shp_run_kind {
     SHP_RUN_SNAKE,
     SHP_RUN_SNAKE_GUARDED,
     SHP_RUN_SNAKE_BETA,
-    SHP_RUN_GATHER_SUM
+    SHP_RUN_GATHER_SUM,
+    SHP_RUN_QK_NORM_ROPE,     /* q and k rope runs (the k sink may be a cache copy) */
+    SHP_RUN_QK_NORM_ROPE_KV   /* the same plus the v cache copy */
 } shp_run_kind;
 
 typedef struct shp_graph_run {
     int32_t kind;  /* shp_run_kind */
-    int32_t first; /* index of the run's first node */
-    int32_t last;  /* index of its last node (the run's result); view-like nodes
-                      between first and last belong to no run */
+    int32_t first; /* index of the run's first node, where it is launched */
+    int32_t last;  /* index of its last node (the run's result; for the q/k
+                      runs, the last of their nodes); view-like nodes between
+                      first and last belong to no run, and for the q/k runs
+                      so do the other nodes between their parts */
     int32_t nodes; /* nodes the run executes */
 } shp_graph_run;
 

@@ -8,7 +8,7 @@
 // which calls the score again and then `ggml_backend_init`.
 //
 // This file is the half of the module that needs no ggml header:
-//   - ggml_backend_score: non-zero exactly when a gfx950 (MI355X) GPU is
+//   - shp_module_gfx950_score: non-zero exactly when a gfx950 (MI355X) GPU is
 //     visible to this process, read from the KFD topology in sysfs, which is
 //     what the ROCm runtime itself enumerates. It starts no GPU runtime, so a
 //     scan that dlopens and dlcloses the module stays cheap and leaves the
@@ -16,8 +16,15 @@
 //   - ggml_backend_init: the registry (reg, device, buffer and backend
 //     vtables of ggml-backend-impl.h at the pinned ggml's
 //     GGML_BACKEND_API_VERSION) needs those headers, absent from the
-//     reference checkout; without them it returns null, which ggml_backend_load
-//     reports as a module that failed to initialise and skips.
+//     reference checkout; without them it returns null.
+//   - ggml_backend_score: that detection only when the registry is compiled
+//     in (SHP_GGML_REGISTRY, defined by a build against the pinned ggml),
+//     else 0. The discovery keeps the single best-scoring libggml-hip-*.so
+//     and never retries another (src/backend-module.cpp:145-177); a module
+//     that outscored a working ggml HIP build and then failed in
+//     ggml_backend_init would leave the process with no HIP backend. Scoring
+//     0, this build loses to any real module and to the bare libggml-hip.so
+//     fallback (:169-174).
 //
 // The node-run executor those vtables would call (graph_compute, supports_op)
 // is include/synth_graph.h.
@@ -131,8 +138,9 @@ extern "C" {
 // Non-zero when at least one gfx950 device is visible: 1 + the number of them
 // (capped), so a module directory holding builds for several machines ranks
 // this one by what it can use. 0 otherwise, including when the topology
-// cannot be read.
-__attribute__((visibility("default"))) int ggml_backend_score(void) {
+// cannot be read. The score a registry build reports; exported under its own
+// name so the detection can be checked without one.
+__attribute__((visibility("default"))) int shp_module_gfx950_score(void) {
     unsigned long targets[kMaxGpus];
     int           n = gpu_targets(targets);
     n               = apply_visible(std::getenv("ROCR_VISIBLE_DEVICES"), targets, n);
@@ -142,6 +150,16 @@ __attribute__((visibility("default"))) int ggml_backend_score(void) {
         gfx950 += targets[k] == kGfx950 ? 1 : 0;
     }
     return gfx950 == 0 ? 0 : 1 + (gfx950 < 64 ? gfx950 : 64);
+}
+
+// The module's score in the discovery: 0 until ggml_backend_init returns a
+// registry, so that this build is never picked over one that works.
+__attribute__((visibility("default"))) int ggml_backend_score(void) {
+#ifdef SHP_GGML_REGISTRY
+    return shp_module_gfx950_score();
+#else
+    return 0;
+#endif
 }
 
 // The registry needs the pinned ggml's backend interface headers; this build

@@ -9,6 +9,8 @@
 // output. That is the condition under which skipping the intermediate writes
 // cannot be observed. Every fused launch computes what the nodes compute one
 // by one, bit for bit.
+#include <algorithm>
+#include <cstddef>
 #include <cstdint>
 #include <cstring>
 #include <initializer_list>
@@ -167,7 +169,8 @@ struct Members {
     }
 };
 
-// What a run launches: which entry point, and its operands.
+// What a run launches: which entry point, and its operands. The q/k runs put
+// k's operands in x2/w2/y2 and v's copy in x3/y3.
 struct Launch {
     int                     kind  = SHP_RUN_SINGLE;
     int                     first = 0;
@@ -179,6 +182,11 @@ struct Launch {
     const shp_tensor *      c1    = nullptr;
     shp_tensor *            y     = nullptr;
     shp_tensor *            sum   = nullptr;
+    const shp_tensor *      x2    = nullptr;
+    const shp_tensor *      w2    = nullptr;
+    shp_tensor *            y2    = nullptr;
+    const shp_tensor *      x3    = nullptr;
+    shp_tensor *            y3    = nullptr;
     float                   f0    = 0.0f;
     float                   f1    = 0.0f;
     float                   f2    = 0.0f;
@@ -238,20 +246,26 @@ class Planner {
         return SHP_OK;
     }
 
-    // Every run of the list, in order; NOP nodes are runs of their own.
-    std::vector<Launch> plan() const {
+    // Every run of the list, in launch order; NOP nodes are runs of their own,
+    // placed by index. The parts of a q/k run that sat later in the list leave
+    // the window order once taken, so later windows see the list without them.
+    std::vector<Launch> plan() {
         std::vector<Launch> out;
-        size_t              p = 0;
-        int                 i = 0;
-        while (i < n_) {
-            if (nodes_[i].op == SHP_NODE_NOP) {
-                Launch l;
-                l.kind  = SHP_RUN_NOP;
-                l.first = l.last = i;
-                out.push_back(l);
-                ++i;
-                continue;
+        int                 nop = 0;
+        auto                nops_before = [&](int upto) {
+            for (; nop < upto; ++nop) {
+                if (nodes_[nop].op == SHP_NODE_NOP) {
+                    Launch v;
+                    v.kind  = SHP_RUN_NOP;
+                    v.first = v.last = nop;
+                    out.push_back(v);
+                }
             }
+        };
+        size_t p = 0;
+        while (p < order_.size()) {
+            const int i = order_[p];
+            nops_before(i);
             Launch l;
             int    used = match(p, l);
             if (used > 0) {
@@ -269,31 +283,279 @@ class Planner {
                 l.count          = 1;
                 out.push_back(l);
                 ++p;
-                ++i;
                 continue;
             }
             l.first = order_[p];
             l.last  = order_[p + used - 1];
             l.count = used;
-            out.push_back(l);
-            // NOP nodes inside the span become their own runs after it.
-            for (int j = l.first + 1; j < l.last; ++j) {
-                if (nodes_[j].op == SHP_NODE_NOP) {
-                    Launch v;
-                    v.kind  = SHP_RUN_NOP;
-                    v.first = v.last = j;
-                    out.push_back(v);
+            if (l.kind == SHP_RUN_NORM_MUL_ROPE) {
+                Launch qk;
+                if (match_sibling(p, used, l, qk)) {
+                    l = qk;
                 }
             }
+            out.push_back(l);
             p += used;
-            i = l.last + 1;
         }
+        nops_before(n_);
         return out;
     }
 
     const shp_node & node(int i) const { return nodes_[i]; }
 
   private:
+    // Window positions scanned past a rope run for its sibling and v's copy.
+    static constexpr size_t kSiblingScan = 64;
+
+    // A byte range [lo, hi) of device memory.
+    struct Span {
+        uintptr_t lo;
+        uintptr_t hi;
+    };
+
+    // The bytes a descriptor can address: from data to the end of its last row.
+    static Span extent(const shp_tensor & t) {
+        size_t end = row_bytes(t.type, t.ne[0]);
+        for (int d = 1; d < 4; ++d) {
+            end += static_cast<size_t>(t.ne[d] - 1) * t.nb[d];
+        }
+        const uintptr_t lo = reinterpret_cast<uintptr_t>(t.data);
+        return { lo, lo + end };
+    }
+
+    static bool overlaps(const Span & a, const std::vector<Span> & bs) {
+        for (const Span & b : bs) {
+            if (a.lo < b.hi && b.lo < a.hi) {
+                return true;
+            }
+        }
+        return false;
+    }
+
+    // The producer of src k of node m, seen through view-like nodes (-1: none
+    // in the list).
+    int producer(int m, int k) const {
+        int j = nodes_[m].src_node[k];
+        while (j >= 0 && nodes_[j].op == SHP_NODE_NOP) {
+            j = nodes_[j].src_node[0];
+        }
+        return j;
+    }
+
+    // One part of a q/k run: its nodes, the ranges it reads from outside
+    // itself and the one range it writes (its sink's dst).
+    struct Part {
+        Members           nodes;
+        std::vector<Span> reads;
+        std::vector<Span> writes;
+        size_t            pos = 0;  // window position of its first node
+    };
+
+    Part part_of(size_t p, int used, int sink) const {
+        Part pt;
+        pt.pos = p;
+        for (int k = 0; k < used; ++k) {
+            pt.nodes.push(order_[p + k]);
+        }
+        for (int a = 0; a < pt.nodes.n; ++a) {
+            const int m = pt.nodes.v[a];
+            for (int k = 0; k < SHP_NODE_MAX_SRC; ++k) {
+                if (present(nodes_[m].src[k]) && !pt.nodes.has(producer(m, k))) {
+                    pt.reads.push_back(extent(nodes_[m].src[k]));
+                }
+            }
+        }
+        pt.writes.push_back(extent(nodes_[sink].dst));
+        return pt;
+    }
+
+    // A part that sits later in the list can run at window position `at`
+    // instead: every input it takes from the list is produced before `at`
+    // (or is its own), and no node between `at` and the part (other than the
+    // members of the whole run) writes what it reads or writes, or reads what
+    // it writes -- so moving it up changes no value any node sees.
+    bool can_move_up(const Part & pt, size_t at, const Members & all) const {
+        const int first = order_[at];
+        for (int a = 0; a < pt.nodes.n; ++a) {
+            const int m = pt.nodes.v[a];
+            for (int k = 0; k < SHP_NODE_MAX_SRC; ++k) {
+                const int j = producer(m, k);
+                if (j >= first && !pt.nodes.has(j)) {
+                    return false;
+                }
+            }
+        }
+        for (size_t q = at + 1; q < pt.pos; ++q) {
+            const int x = order_[q];
+            if (all.has(x)) {
+                continue;
+            }
+            const shp_node & X = nodes_[x];
+            const Span       w = extent(X.dst);
+            if (overlaps(w, pt.reads) || overlaps(w, pt.writes)) {
+                return false;
+            }
+            for (int k = 0; k < SHP_NODE_MAX_SRC; ++k) {
+                if (present(X.src[k]) && overlaps(extent(X.src[k]), pt.writes)) {
+                    return false;
+                }
+            }
+        }
+        return true;
+    }
+
+    // Two parts of one launch may not see each other's results: what one
+    // writes, no other part reads or writes.
+    static bool independent(const Part & a, const Part & b) {
+        for (const Span & w : a.writes) {
+            if (overlaps(w, b.reads) || overlaps(w, b.writes)) {
+                return false;
+            }
+        }
+        for (const Span & w : b.writes) {
+            if (overlaps(w, a.reads)) {
+                return false;
+            }
+        }
+        return true;
+    }
+
+    // The attention block's q and k runs (src/arch/qwen3-tts/operations.cpp:
+    // 98-104) and the cache copies of k and v (:109-116) as one launch.
+    // `a` is a rope run at window positions [p, p + used); its sibling is the
+    // next rope run within kSiblingScan positions with the same positions,
+    // eps, rope parameters, head size and gain type. The part ending in a
+    // copy is k (the cache write); with none, or both, `a` is q. When k's
+    // part ends in a copy, the first F32 copy of k's input shape in the scan
+    // window that can move up is v's. ggml_build_forward_expand puts the k
+    // and v copies before the q path (:106-116), so either part may come
+    // first.
+    bool match_sibling(size_t p, int used, const Launch & a, Launch & out) {
+        const size_t lim   = std::min(order_.size(), p + used + kSiblingScan);
+        const bool   a_cpy = is(order_[p + used - 1], SHP_NODE_CPY);
+        const Part   pa    = part_of(p, used, order_[p + used - 1]);
+        for (size_t p2 = p + used; p2 < lim; ++p2) {
+            if (!is(order_[p2], SHP_NODE_RMS_NORM)) {
+                continue;
+            }
+            Launch b;
+            int    used_b = 0;
+            for (int k : { 5, 4, 3 }) {
+                if ((used_b = match_norm(p2, k, b)) != 0) {
+                    break;
+                }
+            }
+            if (used_b == 0 || b.kind != SHP_RUN_NORM_MUL_ROPE || !siblings(a, b)) {
+                continue;
+            }
+            const bool   b_cpy = is(order_[p2 + used_b - 1], SHP_NODE_CPY);
+            const Part   pb    = part_of(p2, used_b, order_[p2 + used_b - 1]);
+            Members      all   = pa.nodes;
+            for (int m = 0; m < pb.nodes.n; ++m) {
+                all.push(pb.nodes.v[m]);
+            }
+            if (!independent(pa, pb) || !can_move_up(pb, p, all)) {
+                continue;
+            }
+            const bool     swap = a_cpy && !b_cpy;  // b is q, a is k
+            const Launch & q    = swap ? b : a;
+            const Launch & k    = swap ? a : b;
+            out                 = Launch{};
+            out.kind            = SHP_RUN_QK_NORM_ROPE;
+            out.x               = q.x;
+            out.w               = q.w;
+            out.y               = q.y;
+            out.x2              = k.x;
+            out.w2              = k.w;
+            out.y2              = k.y;
+            out.b               = a.b;
+            out.i0              = a.i0;
+            out.f0              = a.f0;
+            out.f1              = a.f1;
+            out.f2              = a.f2;
+            out.first           = order_[p];
+            out.last            = std::max(order_[p + used - 1], order_[p2 + used_b - 1]);
+            out.count           = used + used_b;
+            {
+                DryRun dry;
+                if (launch_run(*this, out, nullptr) != SHP_OK) {
+                    continue;
+                }
+            }
+            std::vector<size_t> taken;
+            for (int m = 0; m < used_b; ++m) {
+                taken.push_back(p2 + m);
+            }
+            if (swap ? a_cpy : b_cpy) {
+                size_t pv = 0;
+                if (find_v_copy(p, used, p2, used_b, *k.x, pa, pb, all, out, pv)) {
+                    taken.push_back(pv);
+                }
+            }
+            // the moved-up parts leave the window order, last position first
+            std::sort(taken.begin(), taken.end());
+            for (size_t t = taken.size(); t-- > 0;) {
+                order_.erase(order_.begin() + static_cast<std::ptrdiff_t>(taken[t]));
+            }
+            return true;
+        }
+        return false;
+    }
+
+    // v's cache copy for a q/k run: a CPY of an F32 tensor of k's input shape
+    // into an F32 tensor of that shape, at a window position after p other
+    // than the sibling's, that can move up to p next to the other parts. On
+    // success `out` becomes the KV launch and *pos_v its window position.
+    bool find_v_copy(size_t p, int used, size_t p2, int used_b, const shp_tensor & kx, const Part & pa,
+                     const Part & pb, const Members & all, Launch & out, size_t & pos_v) {
+        const size_t lim = std::min(order_.size(), p + used + kSiblingScan);
+        for (size_t pv = p + used; pv < lim; ++pv) {
+            if (pv >= p2 && pv < p2 + used_b) {
+                continue;
+            }
+            const int        c = order_[pv];
+            const shp_node & C = nodes_[c];
+            if (!is(c, SHP_NODE_CPY) || !f32_of(C.src[0]) || !same_shape(C.src[0], kx) || !f32_of(C.dst) ||
+                !same_shape(C.dst, kx)) {
+                continue;
+            }
+            const Part pc   = part_of(pv, 1, c);
+            Members    all3 = all;
+            all3.push(c);
+            if (!independent(pa, pc) || !independent(pb, pc) || !can_move_up(pc, p, all3)) {
+                continue;
+            }
+            Launch kv = out;
+            kv.kind   = SHP_RUN_QK_NORM_ROPE_KV;
+            kv.x3     = &C.src[0];
+            kv.y3     = const_cast<shp_tensor *>(&C.dst);
+            kv.last   = std::max(out.last, c);
+            kv.count  = out.count + 1;
+            DryRun dry;
+            if (launch_run(*this, kv, nullptr) != SHP_OK) {
+                continue;
+            }
+            out   = kv;
+            pos_v = pv;
+            return true;
+        }
+        return false;
+    }
+
+    // Two rope runs one launch can take: the same positions tensor, eps,
+    // n_dims, base and scale (bit for bit), head size and token count, and
+    // gains of one type.
+    static bool siblings(const Launch & a, const Launch & b) {
+        auto bits = [](float f) {
+            uint32_t u;
+            std::memcpy(&u, &f, sizeof(u));
+            return u;
+        };
+        return same_tensor(*a.b, *b.b) && a.i0 == b.i0 && bits(a.f0) == bits(b.f0) && bits(a.f1) == bits(b.f1) &&
+               bits(a.f2) == bits(b.f2) && a.x->ne[0] == b.x->ne[0] && a.x->ne[2] == b.x->ne[2] &&
+               a.w->type == b.w->type;
+    }
+
     const shp_node *              nodes_;
     int                           n_;
     std::vector<int> order_;
@@ -872,6 +1134,11 @@ shp_status_t launch_run(const Planner & pl, const Launch & l, shp_stream_t st) {
             return shp_snake_beta(l.x, l.w, l.c1, l.y, st);
         case SHP_RUN_GATHER_SUM:
             return shp_get_rows_sum(l.terms.data(), static_cast<int32_t>(l.terms.size()), &l.codes, l.y, st);
+        case SHP_RUN_QK_NORM_ROPE:
+            return shp_qk_norm_rope(l.x, l.x2, l.w, l.w2, l.f0, l.b, l.i0, l.f1, l.f2, l.y, l.y2, st);
+        case SHP_RUN_QK_NORM_ROPE_KV:
+            // the copies' destinations are the cache views themselves (filled 0)
+            return shp_qk_norm_rope_kv(l.x, l.x2, l.x3, l.w, l.w2, l.f0, l.b, l.i0, l.f1, l.f2, l.y, l.y2, l.y3, 0, st);
         default:
             return SHP_ERR_UNSUPPORTED;
     }

@@ -108,7 +108,7 @@ def test_qwen3_layer_graph(gpu, T):
 
     g, outs, cache = build(False)
     kinds = [k for k, *_ in g.plan(*outs) if k != "nop"]
-    assert kinds == ["norm_mul_rope", "norm_mul", "norm_mul_rope", "add_norm_mul", "single"]
+    assert kinds == ["qk_norm_rope", "norm_mul", "add_norm_mul", "single"]
     g.compute(*outs)
     _, normed, qr, mlp_in, out, after = [_np(v.t) for v in outs]
     kc = _np(cache)
@@ -130,6 +130,113 @@ def test_qwen3_layer_graph(gpu, T):
     assert_bitexact(after, s_ref)
     assert_close(mlp_in, y_ref)
     assert_bitexact(out, R.run(lambda gr: gr.add(s_ref, d["mlp"])))
+
+
+def _reference_layer_leaves(gpu, rng, T, total, H=1024, heads=16, kv=8, hd=128, ffn=3072):
+    import torch
+    d = _layer_inputs(rng, T, H, heads, kv, hd)
+    d.update(v=rng.standard_normal((T, kv, hd)).astype(np.float32),
+             scores=(4 * rng.standard_normal((heads, T, total))).astype(np.float32),
+             gate=rng.standard_normal((T, ffn)).astype(np.float32),
+             up=rng.standard_normal((T, ffn)).astype(np.float32))
+    dev = {n: (_bf16(gpu, a) if n.startswith("w") else _t(gpu, a)) for n, a in d.items()}
+    return d, dev, lambda: {"kcache": torch.zeros(total, kv, hd, device="cuda"),
+                            "vcache": torch.zeros(total, kv, hd, device="cuda")}
+
+
+@pytest.mark.parametrize("T", [1, 37])
+def test_reference_order_layer_graph(gpu, T):
+    """decoder_layer's non-GEMM nodes (operations.cpp:56-147) in expand order:
+    the input norm, k's path and the k and v cache copies (:106-116) before
+    the q path, then the softmax, the residual add, the post-attention norm,
+    SwiGLU and the output add. The q run is moved up into k's launch with v's
+    copy: five launches and the add. Every output is bit-identical to the same
+    list run node by node and matches the restatement at the usual bars (rope
+    bit-exact with correctly rounded cos/sin, the cache rows bit-exact, the
+    softmax within 2 ulp)."""
+    import torch
+    from test_graph_plan import reference_layer
+    rng = np.random.default_rng(SEED + 320 + T)
+    hd, total, eps, theta = 128, 64, np.float32(1e-6), np.float32(1e6)
+    filled = total - T
+    d, dev, caches = _reference_layer_leaves(gpu, rng, T, total)
+
+    def build(node_by_node):
+        g = gpu.Graph()
+        leaves = dict(dev, **caches())
+        outs, leaves = reference_layer(g, dev["x"], T=T, H=1024, heads=16, kv=8, hd=hd, ffn=3072, total=total,
+                                       leaves=leaves)
+        if node_by_node:
+            outs = outs + [n["val"] for n in g.order(*outs)]
+        return g, outs, leaves
+
+    g, outs, lv = build(False)
+    assert [k for k, *_ in g.plan(*outs) if k != "nop"] == ["norm_mul", "qk_norm_rope_kv", "single",
+                                                             "add_norm_mul", "silu_mul", "single"]
+    g.compute(*outs)
+    g2, outs2, lv2 = build(True)
+    assert all(k in ("single", "nop") for k, *_ in g2.plan(*outs2))
+    g2.compute(*outs2)
+    for a, b in zip(outs, outs2):
+        assert_bitexact(_np(a.t), _np(b.t))
+    assert_bitexact(_np(lv["kcache"]), _np(lv2["kcache"]))
+    assert_bitexact(_np(lv["vcache"]), _np(lv2["vcache"]))
+
+    normed, _, _, qr, probs, mlp_in, act, out = [_np(v.t) for v in outs]
+    kc, vc = _np(lv["kcache"]), _np(lv["vcache"])
+    x, q, k = d["x"], d["q"], d["k"]
+    assert_close(normed, R.run(lambda gr: R.rms_norm_w(gr, x, d["w_in"], eps, R.BF16)))
+    q_ref, k_ref = R.run(lambda gr: R.qk_norm_rope(gr, q, k, d["wq"], d["wk"], eps, d["pos"], hd, theta, R.BF16,
+                                                   cs_rounded=True))
+    assert_bitexact(qr, q_ref)
+    assert_bitexact(kc[filled:], k_ref)
+    assert_bitexact(vc[filled:], d["v"])
+    assert (kc[:filled] == 0).all() and (vc[:filled] == 0).all()
+    p_ref = R.run(lambda gr: gr.soft_max_ext(d["scores"], None, np.float32(hd ** -0.5)))
+    assert np.abs(probs.view(np.int32).astype(np.int64) - p_ref.view(np.int32).astype(np.int64)).max() <= 2
+    s_ref, y_ref = R.run(lambda gr: R.add_rms_norm_w(gr, x, d["attn"], d["w_post"], eps, R.BF16))
+    assert_bitexact(_np(outs[-1].node["srcs"][0].t), s_ref)
+    assert_close(mlp_in, y_ref)
+    assert_close(act, R.run(lambda gr: R.swiglu(gr, d["gate"], d["up"])))
+    assert_bitexact(out, R.run(lambda gr: gr.add(s_ref, d["mlp"])))
+
+
+def test_reference_order_layers_chained(gpu):
+    """Three decoder layers in one list, each layer's output add feeding the
+    next layer's input norm (:147 -> :86): the add and the next norm are one
+    launch that writes the sum, and the whole list is bit-identical to the
+    same list run node by node."""
+    from test_graph_plan import reference_layer
+    rng = np.random.default_rng(SEED + 340)
+    T, total, layers = 1, 38, 3
+
+    def build(node_by_node, per):
+        g = gpu.Graph()
+        x, outs, caches = per[0][1]["x"], [], []
+        for l in range(layers):
+            d, dev, mk = per[l]
+            leaves = dict(dev, **mk())
+            o, leaves = reference_layer(g, x, T=T, H=1024, heads=16, kv=8, hd=128, ffn=3072, total=total,
+                                        leaves=leaves)
+            outs += o
+            caches += [leaves["kcache"], leaves["vcache"]]
+            x = o[-1]
+        if node_by_node:
+            outs = outs + [n["val"] for n in g.order(*outs)]
+        return g, outs, caches
+
+    per = [_reference_layer_leaves(gpu, rng, T, total) for _ in range(layers)]
+    g, outs, caches = build(False, per)
+    kinds = [k for k, *_ in g.plan(*outs) if k != "nop"]
+    assert kinds == ["norm_mul"] + ["qk_norm_rope_kv", "single", "add_norm_mul", "silu_mul", "add_norm_mul"] * 2 + \
+        ["qk_norm_rope_kv", "single", "add_norm_mul", "silu_mul", "single"]
+    g.compute(*outs)
+    g2, outs2, caches2 = build(True, per)
+    g2.compute(*outs2)
+    for a, b in zip(outs, outs2):
+        assert_bitexact(_np(a.t), _np(b.t))
+    for a, b in zip(caches, caches2):
+        assert_bitexact(_np(a), _np(b))
 
 
 @pytest.mark.parametrize("kind", ["plain", "guarded", "beta"])

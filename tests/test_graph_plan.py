@@ -7,6 +7,7 @@ import ctypes
 import pytest
 import torch
 
+import qwen3_layer as Q
 import synth_hip as S
 
 F32 = torch.float32
@@ -45,14 +46,104 @@ def test_qwen3_layer_runs():
     g = S.Graph()
     kc, normed, qr, mlp_in, out = qwen3_layer(g)
     plan = g.plan(kc, normed, qr, mlp_in, out)
-    # expand order: the k path first (the cache write), then the input norm, q, the add+norm, the output add
-    assert kinds(plan) == ["norm_mul_rope", "norm_mul", "norm_mul_rope", "add_norm_mul", "single"]
+    # expand order: the k path first (the cache write), then the input norm, q, the add+norm, the output add;
+    # q's run is taken into k's launch across the input norm (which touches neither)
+    assert kinds(plan) == ["qk_norm_rope", "norm_mul", "add_norm_mul", "single"]
     nodes = [n for k, _, _, n in plan if k != "nop"]
-    assert nodes == [5, 3, 4, 4, 1]
+    assert nodes == [9, 3, 4, 1]
     g = S.Graph()
     res = qwen3_layer(g, cast=False)
-    assert kinds(g.plan(*res)) == ["norm_mul_rope", "norm_mul", "norm_mul_rope", "add_norm_mul", "single"]
-    assert [n for k, _, _, n in g.plan(*res) if k != "nop"] == [4, 2, 3, 3, 1]
+    assert kinds(g.plan(*res)) == ["qk_norm_rope", "norm_mul", "add_norm_mul", "single"]
+    assert [n for k, _, _, n in g.plan(*res) if k != "nop"] == [7, 2, 3, 1]
+
+
+def reference_layer(g, x, T=1, H=64, heads=4, kv=2, hd=16, ffn=96, total=8, cast=True, leaves=None):
+    """decoder_layer's non-GEMM nodes in expand order, small shapes by default
+    (qwen3_layer.decoder_layer_nodes: the GEMM and attention-product outputs
+    are leaves). Returns (outputs in expand order, leaves)."""
+    return Q.decoder_layer_nodes(g, x, {} if leaves is None else leaves, T=T, H=H, heads=heads, kv=kv, hd=hd,
+                                 ffn=ffn, total=total, cast=cast)
+
+
+def test_reference_order_layer_is_five_launches():
+    """The q run comes after k's and v's cache copies in expand order; the
+    planner moves it up into k's launch with v's copy: input norm, one
+    QK-norm+RoPE+KV launch, softmax, add+norm, SwiGLU, add."""
+    g = S.Graph()
+    outs, _ = reference_layer(g, z(1, 64))
+    plan = g.plan(*outs)
+    assert kinds(plan) == ["norm_mul", "qk_norm_rope_kv", "single", "add_norm_mul", "silu_mul", "single"]
+    run = [r for r in plan if r[0] == "qk_norm_rope_kv"][0]
+    assert run[3] == 5 + 1 + 4  # k's run with its copy, v's copy, q's run
+    # the launch sits where k's run starts; the parts that followed it are gone from later windows
+    order = g.order(*outs)
+    assert order[run[1]]["op"] == S.NODE_RMS_NORM and order[run[2]]["op"] == S.NODE_ROPE
+    # 28 chained layers (each layer's output add feeds the next input norm): 5 launches per layer, + the last add
+    g = S.Graph()
+    x, outs = z(1, 64), []
+    for _ in range(28):
+        o, _ = reference_layer(g, x)
+        outs += o
+        x = o[-1]
+    assert kinds(g.plan(*outs)) == ["norm_mul"] + ["qk_norm_rope_kv", "single", "add_norm_mul", "silu_mul",
+                                                   "add_norm_mul"] * 27 + \
+        ["qk_norm_rope_kv", "single", "add_norm_mul", "silu_mul", "single"]
+
+
+def test_sibling_runs_stay_apart_when_moving_one_up_is_visible():
+    """A part that sits later is moved up only when nothing between reads
+    what it writes, writes what it reads or writes, or produces its input."""
+    hd, T = 16, 3
+    pos, wq, wk = z(T, dtype=torch.int32), z(hd), z(hd)
+
+    def runs(between, q_first=True, eps_k=1e-6, pos_k=None, kcache=None):
+        g = S.Graph()
+        q, k = z(T, 4, hd), z(T, 2, hd)
+        kcache = z(8, 2, hd) if kcache is None else kcache
+        qrun = lambda: g.rope_ext(g.mul(g.rms_norm(q, 1e-6), wq), pos, hd, S.ROPE_TYPE_NEOX, 1e6)
+        krun = lambda: g.cpy(g.rope_ext(g.mul(g.rms_norm(k, eps_k), wk), pos if pos_k is None else pos_k, hd,
+                                        S.ROPE_TYPE_NEOX, 1e6), kcache[5:])
+        first = qrun() if q_first else krun()
+        mid = between(g, q, k, kcache, first)
+        second = krun() if q_first else qrun()
+        return kinds(g.plan(first, mid, second))
+
+    read_cache = lambda g, q, k, kc, first: g.add(kc, kc)
+    # q first: k's cache write would move above a read of the cache
+    assert runs(read_cache) == ["norm_mul_rope", "single", "norm_mul_rope"]
+    # k first: q moves up over the read; the cache was written before it either way
+    assert runs(read_cache, q_first=False) == ["qk_norm_rope", "single"]
+    # a node between writes q's input: q cannot move up
+    assert runs(lambda g, q, k, kc, first: g.cpy(z(T, 4, hd), q), q_first=False) == \
+        ["norm_mul_rope", "single", "norm_mul_rope"]
+    # a node between reads the first run's result: fine, the first run does not move
+    assert runs(lambda g, q, k, kc, first: g.add(first, first)) == ["qk_norm_rope", "single"]
+    # unrelated work between: fused
+    assert runs(lambda g, q, k, kc, first: g.exp(z(4, 4))) == ["qk_norm_rope", "single"]
+    # different eps or positions: two launches
+    assert runs(lambda g, q, k, kc, first: g.exp(z(4, 4)), eps_k=1e-5) == \
+        ["norm_mul_rope", "single", "norm_mul_rope"]
+    assert runs(lambda g, q, k, kc, first: g.exp(z(4, 4)), pos_k=z(T, dtype=torch.int32)) == \
+        ["norm_mul_rope", "single", "norm_mul_rope"]
+
+
+def test_v_copy_joins_only_when_it_can_move_up():
+    """v's cache copy joins the q/k launch unless a node between writes its
+    source; the q/k part still fuses."""
+    g = S.Graph()
+    outs, d = reference_layer(g, z(1, 64))
+    assert "qk_norm_rope_kv" in kinds(g.plan(*outs))
+    # a cast into v's source placed between k's run and v's copy (a cast, so
+    # that it cannot itself be taken as the F32 copy of v)
+    g2 = S.Graph()
+    hd, T = 16, 1
+    q, k, v, pos = z(T, 4, hd), z(T, 2, hd), z(T, 2, hd), z(T, dtype=torch.int32)
+    kcache, vcache = z(8, 2, hd), z(8, 2, hd)
+    kc = g2.cpy(g2.rope_ext(g2.mul(g2.rms_norm(k, 1e-6), z(hd)), pos, hd, S.ROPE_TYPE_NEOX, 1e6), kcache[7:])
+    clobber = g2.cpy(z(T, 2, hd, dtype=torch.float16), v)
+    vc = g2.cpy(v, vcache[7:])
+    qr = g2.rope_ext(g2.mul(g2.rms_norm(q, 1e-6), z(hd)), pos, hd, S.ROPE_TYPE_NEOX, 1e6)
+    assert kinds(g2.plan(kc, clobber, vc, qr)) == ["qk_norm_rope", "single", "single"]
 
 
 def test_a_read_in_a_later_split_keeps_a_result_written():
