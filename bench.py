@@ -469,6 +469,63 @@ def vocoder_rows(R, S, torch, cfg, seed, shapes=((512, 8192), (256, 32768), (128
     return out
 
 
+def floor_rows(R, S, torch, seed=SEED + 8):
+    """Same-run floors the op rows are read against, each timed as the op rows
+    are (cold rotating sets, HIP graph, median of chunks):
+      - copy [C,T]: shp_cpy of an F32 tensor (one read and one write of every
+        element, no arithmetic) at each configs[3] shape and at [2048,8192];
+      - write-only [1024,4096]: torch's fill_ of the gathers' output tensor
+        (no reads at all);
+      - id-then-write: shp_get_rows of 4096 ids from an 8-row Q8_0 table
+        [1024,8] (8.7 KB, cache-resident), i.e. the gather's id load, row
+        address and dequantised store with the table fetch taken away.
+    Returns {name: row}."""
+    import numpy as np
+    import formats as F
+    g, randn, empty, bf16 = gen(torch, seed)
+    out = {}
+    for C, T in ((512, 8192), (256, 32768), (128, 131072), (2048, 8192)):
+        def make_copy(C=C, T=T):
+            x, y = randn(T, C), empty(T, C)
+            return lambda: S.cpy(x, out=y)
+        name = "copy [%d,%d]" % (C, T)
+        out[name] = R.run("floor", name, 8 * C * T, make_copy)
+
+    def make_fill():
+        y = empty(4096, 1024)
+        return lambda: y.fill_(1.0)
+    out["write-only [1024,4096]"] = R.run("floor", "write-only [1024,4096]", 4 * 4096 * 1024, make_fill)
+    rng = np.random.default_rng(seed)
+
+    def make_idw():
+        tab = S.Q8Tensor(torch.from_numpy(F.q8_0_synthetic(rng, 8, 1024)).cuda(), 1024)
+        ids = torch.randint(0, 8, (4096,), generator=g, device="cuda", dtype=torch.int32)
+        y = empty(4096, 1024)
+        return lambda: S.get_rows(tab, ids, out=y)
+    name = "id-then-write: get_rows q8_0 [1024,8] x4096"
+    out[name] = R.run("floor", name, 4096 * (4 + 1024 * 4), make_idw)
+    return out
+
+
+def link_floors(rows, floors):
+    """Adds to each op row the floor it is read against: 'of_floor' = the
+    row's GB/s over the floor's (streams: the copy of the same shape), or for
+    the plain gathers 'of_floor_time' = floor us / row us (the row's own
+    launch against the write-only and id-then-write launches)."""
+    for row in rows:
+        op, cfg = row["op"], row["config"]
+        m = re.search(r"\[(\d+),(\d+)\]$", op)
+        if cfg in ("configs[3]", "configs[4]") and m and not op.startswith(("swiglu", "add [", "qk_")):
+            f = floors.get("copy [%s,%s]" % m.groups())
+            if f is not None:
+                row["floor"] = f["op"]
+                row["of_floor"] = round(row["GB/s"] / f["GB/s"], 4)
+        elif cfg == "configs[2]" and op.startswith("get_rows "):
+            row["floor"] = "write-only [1024,4096]; id-then-write: get_rows q8_0 [1024,8] x4096"
+            row["of_floor_time"] = [round(floors["write-only [1024,4096]"]["us"] / row["us"], 4),
+                                    round(floors["id-then-write: get_rows q8_0 [1024,8] x4096"]["us"] / row["us"], 4)]
+
+
 # ---------------------------------------------------------------------------
 # decode step: 28 layers x (add+norm, qk-norm+rope, add+norm, swiglu) at T=1
 # ---------------------------------------------------------------------------
@@ -1222,6 +1279,8 @@ def main():
     q8_rows(R, S, torch, "configs[2]", SEED + 3)
     q8_rows(R, S, torch, "configs[2]", SEED + 6, kind="q5_k")
     vocoder_rows(R, S, torch, "configs[3]", SEED + 4)
+    floors = floor_rows(R, S, torch)
+    link_floors(list(ops4.values()) + R.rows, floors)
 
     if not args.no_cpu:
         cpu_rows, cpu_dec = cpu_op_baselines(args.cpu_seconds)
@@ -1234,7 +1293,10 @@ def main():
     d = ops4[dom]
     roof = {"bound": "hbm", "kernel": d["op"], "achieved": d["GB/s"], "peak": PEAK_GBS, "unit": "GB/s",
             "frac": d["frac"], "traffic": read_traffic(d["op"]), "algorithmic_bytes": d["bytes"],
-            "us_per_launch": d["us"]}
+            "us_per_launch": d["us"],
+            "traffic_source": "read from the committed counter summary profiles/traffic_large_configs.txt "
+                              "(rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of this kernel at this shape, scaled "
+                              "by the same counters over a device copy of known size), not measured in this run"}
 
     # one decode token per layer (position 37), 28 layers in one graph
     dec = decode_layer_us(S, torch, label="step:configs[0] decode, 28 layers x 4 launches")

@@ -257,22 +257,23 @@ constexpr int kSnakeSub = 2;
 template <int K, int R, bool RCP>
 __device__ __forceinline__ void snake_rows(const f32x4 (&xv)[R], f32x4 al, f32x4 den, const double (&rc)[4], int64_t i0,
                                            int64_t c4, int64_t n4, f32x4 * Y) {
-    static_assert(R % kSnakeSub == 0, "rows per lane in whole sub-blocks");
+    constexpr int SUB = R < kSnakeSub ? R : kSnakeSub;
+    static_assert(R % SUB == 0, "rows per lane in whole sub-blocks");
 #pragma unroll
-    for (int r0 = 0; r0 < R; r0 += kSnakeSub) {
-        f32x4    t[kSnakeSub];
+    for (int r0 = 0; r0 < R; r0 += SUB) {
+        f32x4    t[SUB];
         unsigned fast = 1u;  // bitwise: a short-circuit && would branch per element again
 #pragma unroll
-        for (int r = 0; r < kSnakeSub; ++r) {
+        for (int r = 0; r < SUB; ++r) {
             const f32x4 x = xv[r0 + r];
             t[r]          = f32x4{ x.x * al.x, x.y * al.y, x.z * al.z, x.w * al.w };
             fast &= static_cast<unsigned>(sin_fast_ok(t[r].x)) & static_cast<unsigned>(sin_fast_ok(t[r].y)) &
                     static_cast<unsigned>(sin_fast_ok(t[r].z)) & static_cast<unsigned>(sin_fast_ok(t[r].w));
         }
-        f32x4 y[kSnakeSub];
+        f32x4 y[SUB];
         if (fast != 0u) {
 #pragma unroll
-            for (int r = 0; r < kSnakeSub; ++r) {
+            for (int r = 0; r < SUB; ++r) {
                 const f32x4 x = xv[r0 + r];
                 y[r]          = f32x4{ snake_t<true, RCP>(x.x, t[r].x, den.x, rc[0]),
                                        snake_t<true, RCP>(x.y, t[r].y, den.y, rc[1]),
@@ -281,7 +282,7 @@ __device__ __forceinline__ void snake_rows(const f32x4 (&xv)[R], f32x4 al, f32x4
             }
         } else {
 #pragma unroll
-            for (int r = 0; r < kSnakeSub; ++r) {
+            for (int r = 0; r < SUB; ++r) {
                 const f32x4 x = xv[r0 + r];
                 y[r]          = f32x4{ snake_t<false, RCP>(x.x, t[r].x, den.x, rc[0]),
                                        snake_t<false, RCP>(x.y, t[r].y, den.y, rc[1]),
@@ -290,7 +291,7 @@ __device__ __forceinline__ void snake_rows(const f32x4 (&xv)[R], f32x4 al, f32x4
             }
         }
 #pragma unroll
-        for (int r = 0; r < kSnakeSub; ++r) {
+        for (int r = 0; r < SUB; ++r) {
             const int64_t i = i0 + (r0 + r) * c4;
             if (i < n4) {
                 st_stream(Y + i, y[r]);
@@ -299,8 +300,7 @@ __device__ __forceinline__ void snake_rows(const f32x4 (&xv)[R], f32x4 al, f32x4
     }
 }
 
-template <int K, int BLOCK> __global__ __launch_bounds__(BLOCK) void k_snake_flat(const EwArgs a) {
-    constexpr int R    = SnakeRows<K>::R;
+template <int K, int BLOCK, int R = SnakeRows<K>::R> __global__ __launch_bounds__(BLOCK) void k_snake_flat(const EwArgs a) {
     const f32x4 * X    = reinterpret_cast<const f32x4 *>(a.a);
     const f32x4 * C0   = reinterpret_cast<const f32x4 *>(a.alpha);
     const f32x4 * C1   = reinterpret_cast<const f32x4 *>(a.beta);
@@ -373,6 +373,10 @@ template <int K, int BLOCK> __global__ __launch_bounds__(BLOCK) void k_snake_fla
 constexpr int     kSnakeLdsMaxC       = 1024;
 constexpr int64_t kSnakeLdsSmallTasks = int64_t{ 1024 } * 256;        // 4-row tasks, one per lane
 constexpr int64_t kSnakeLdsMaxTasks   = int64_t{ 1 } << 20;          // 8-row tasks, one per lane
+// Up to 128 channels (half a curve per thread to evaluate) the 4-row form with
+// CF stays ahead at any length: [128,131072] 26.4 -> 25.4 us on MI355X, where
+// at 256 channels the 8-row form is 2 % ahead ([256,32768] 14.2 against 14.6).
+constexpr int64_t kSnakeLdsSmallQuads = 32;
 
 template <int R, bool CF> __global__ __launch_bounds__(256) void k_snake_beta_lds(const EwArgs a) {
     constexpr int kPer = kSnakeLdsMaxC / 256;  // channels per thread at most
@@ -793,7 +797,7 @@ shp_status_t launch_snake(const shp_tensor * x, const shp_tensor * c0, const shp
         const int64_t ntask4 = (rows + 3) / 4 * quads;
         const int64_t ntask8 = (rows + 7) / 8 * quads;
         g.quads              = make_fastdiv(static_cast<uint32_t>(quads));
-        if (ntask4 <= kSnakeLdsSmallTasks) {
+        if (ntask4 <= kSnakeLdsSmallTasks || (quads <= kSnakeLdsSmallQuads && ntask4 <= kSnakeLdsMaxTasks)) {
             g.ntask = ntask4;
             hipLaunchKernelGGL((k_snake_beta_lds<4, true>), dim3(static_cast<unsigned>((ntask4 + 255) / 256)), dim3(256), 0,
                                stream, g);

@@ -242,6 +242,25 @@ def test_get_rows_sum_bitexact(gpu, kind, ne0, groups):
     assert_bitexact(_np(got), ref)
 
 
+@pytest.mark.parametrize("kind,groups", [("q8_0", 57), ("q8_0", 63), ("q8_0", 64), ("bf16", 64)])
+def test_get_rows_sum_up_to_64_groups(gpu, kind, groups):
+    """The most groups a sum takes (64) and counts just under it, at ne0 =
+    1024 (the Q8_0 windows' chunks fill every slot at 64 and leave slots past
+    the last group at 57 and 63); an out-of-range id in the last group makes
+    its frame's row NaN, every other frame is the ordered sum bit for bit."""
+    rng = np.random.default_rng(SEED + 71 + groups)
+    ne0, rows, frames = 1024, 40, 200
+    tabs = [_table(rng, kind, rows, ne0) for _ in range(groups)]
+    codes = rng.integers(0, rows, (groups, frames)).astype(np.int32)
+    codes[groups - 1, 11] = rows
+    got = _np(gpu.get_rows_sum([_dev_table(gpu, t, kind, ne0) for t, _ in tabs], _t(gpu, codes)))
+    assert np.isnan(got[11]).all()
+    ok = [f for f in range(frames) if f != 11]
+    ref = R.run(lambda g: R.sum_code_embeddings(g, [t for t, _ in tabs], tabs[0][1], ne0,
+                                                np.minimum(codes, rows - 1)))
+    assert_bitexact(got[ok], ref[ok])
+
+
 def test_get_rows_sum_order_matters_and_nan_on_bad_id(gpu):
     rng = np.random.default_rng(11)
     tabs = [(rng.standard_normal((64, 1024)) * 10.0 ** rng.integers(-3, 3, (64, 1))).astype(np.float32)
@@ -899,14 +918,15 @@ def test_snake_guarded(gpu, T, C):
     assert_bitexact(got[:, 0], x[:, 0])  # alpha = 0: the guard keeps sin(0)^2 / 1e-9 = 0
 
 
-@pytest.mark.parametrize("T,C", [(256, 512), (37, 64), (31, 30), (9, 2048), (4, 1028), (1001, 1024), (77, 260)])
+@pytest.mark.parametrize("T,C", [(256, 512), (37, 64), (31, 30), (9, 2048), (4, 1028), (1001, 1024), (77, 260),
+                                 (32771, 128)])
 def test_snake_beta(gpu, T, C):
     """codec_snake_beta (qwen3-tts): log curves over [-3, 3], so alpha/beta span
     e^+-3 and the two exps, the guard and the division all matter. Up to 1024
     channels the 4-row LDS-table kernel runs (1024 channels: four per thread
-    in its table; 260: one or two); past 1024 the flat kernel, 8 rows per
-    lane: T = 37, 9 and 4 leave partial groups, as 1001 and 77 do for 4-row
-    tasks."""
+    in its table; 260: one or two; 128 channels at any length up to 2^20
+    tasks); past 1024 the flat kernel, 8 rows per lane: T = 37, 9 and 4 leave
+    partial groups, as 1001, 77 and 32771 do for 4-row tasks."""
     rng = np.random.default_rng(SEED + 11 * T + C)
     x = rng.standard_normal((T, C)).astype(np.float32)
     la = rng.uniform(-3, 3, C).astype(np.float32)
@@ -917,9 +937,10 @@ def test_snake_beta(gpu, T, C):
 
 def test_snake_beta_large_channel_table(gpu):
     """[128, 131072] takes the kernel that evaluates each channel's curves
-    once per block into LDS with one 8-row task per lane (more than 2^18
-    4-row tasks); rows 0 and 1 carry large x, so some sines leave the fast
-    range, and channels 0-3 hold extreme curves."""
+    once per block into LDS, one 4-row task per lane (2^20 tasks: at 128
+    channels the 4-row form runs at every length it covers); rows 0 and 1
+    carry large x, so some sines leave the fast range, and channels 0-3 hold
+    extreme curves."""
     rng = np.random.default_rng(SEED + 131)
     T, C = 131072, 128
     x = rng.standard_normal((T, C), dtype=np.float32)
@@ -932,10 +953,11 @@ def test_snake_beta_large_channel_table(gpu):
     assert_snake_close(_np(gpu.snake_beta(_t(gpu, x), _t(gpu, la), _t(gpu, lb))), ref, x)
 
 
-@pytest.mark.parametrize("T,C", [(32771, 128), (8197, 1024)])
+@pytest.mark.parametrize("T,C", [(16387, 256), (8197, 1024)])
 def test_snake_beta_eight_row_tasks_ragged(gpu, T, C):
-    """Shapes just past 2^18 4-row tasks take the 8-row LDS kernel; T is not
-    a multiple of 8, so the last task of each channel quad is partial."""
+    """Shapes of more than 128 channels just past 2^18 4-row tasks take the
+    8-row LDS kernel; T is not a multiple of 8, so the last task of each
+    channel quad is partial."""
     rng = np.random.default_rng(SEED + 137 + C)
     x = rng.standard_normal((T, C), dtype=np.float32)
     la = rng.uniform(-3, 3, C).astype(np.float32)

@@ -11,7 +11,7 @@ import pytest
 import formats as F
 import ggml_ref as R
 from test_gpu_parity import _np, _t, assert_bitexact
-from test_q5k_format import hand_block, hand_values
+from test_q5k_format import hand_block, hand_block2, hand_values, hand_values2
 
 pytestmark = pytest.mark.gpu
 SEED = 20260728
@@ -44,6 +44,25 @@ def test_get_rows_q5k_hand_block_and_bad_ids(gpu):
         assert_bitexact(got[r], hand_values())
     for r in (2, 3, 5):  # out of range: a quiet-NaN row, nothing read
         assert np.isnan(got[r]).all()
+
+
+def test_get_rows_q5k_second_hand_block(gpu):
+    """The second hand-assembled block (every sub-block, every qh bit, both
+    nibbles of every scales[8..11] byte) through the 256-wide kernel and, as
+    the four super-blocks of 1024-wide rows, through the staged one: the
+    worked-out values bit for bit, +0.0 included."""
+    b1, b2 = hand_block(), hand_block2()
+    raw = np.frombuffer(b2 + b1, np.uint8).reshape(2, 176).copy()
+    got = _np(gpu.get_rows(_table(gpu, raw, 256), _t(gpu, np.array([0, 1, 0], np.int32))))
+    for r, want in ((0, hand_values2()), (1, hand_values()), (2, hand_values2())):
+        assert_bitexact(got[r], want)
+    wide = np.frombuffer(b1 + b2 + b2 + b1 + b2 + b1 + b1 + b2, np.uint8).reshape(2, 4 * 176).copy()
+    got = _np(gpu.get_rows(_table(gpu, wide, 1024), _t(gpu, np.array([1, 0, 1, 5], np.int32))))
+    rows = {0: [hand_values(), hand_values2(), hand_values2(), hand_values()],
+            1: [hand_values2(), hand_values(), hand_values(), hand_values2()]}
+    for r, rid in enumerate([1, 0, 1]):
+        assert_bitexact(got[r], np.concatenate(rows[rid]))
+    assert np.isnan(got[3]).all()
 
 
 def test_get_rows_q5k_special_scales(gpu):
@@ -129,6 +148,25 @@ def test_get_rows_sum_q5k_bitexact(gpu, ne0, groups, frames):
     ref = R.run(lambda g: R.sum_code_embeddings(g, tabs, R.Q5_K, ne0, codes))
     got = _np(gpu.get_rows_sum([_table(gpu, t, ne0) for t in tabs], _t(gpu, codes)))
     assert_bitexact(got, ref)
+
+
+@pytest.mark.parametrize("groups", [57, 63, 64])
+def test_get_rows_sum_q5k_many_groups(gpu, groups):
+    """57 to 64 groups over 1024-wide Q5_K tables: the slab windows take
+    groups in chunks of 8, so 57 and 63 leave slots past the last group and 64
+    fills every chunk (the prefetch past the last chunk clamps its slot); one
+    frame holds an out-of-range id in the last group, whose row is NaN, and
+    every other frame equals the restatement's ordered sum bit for bit."""
+    rng = np.random.default_rng(SEED + 53 + groups)
+    ne0, rows, frames = 1024, 40, 300
+    tabs = [F.q5_k_synthetic(rng, rows, ne0) for _ in range(groups)]
+    codes = rng.integers(0, rows, (groups, frames)).astype(np.int32)
+    codes[groups - 1, 17] = rows + 3
+    got = _np(gpu.get_rows_sum([_table(gpu, t, ne0) for t in tabs], _t(gpu, codes)))
+    assert np.isnan(got[17]).all()
+    ok = [f for f in range(frames) if f != 17]
+    ref = R.run(lambda g: R.sum_code_embeddings(g, tabs, R.Q5_K, ne0, np.minimum(codes, rows - 1)))
+    assert_bitexact(got[ok], ref[ok])
 
 
 def test_get_rows_sum_q5k_order_and_bad_id(gpu):
