@@ -79,9 +79,10 @@ def parse():
     p.add_argument("--pmc-large", action="store_true", help="instead: three launches of each large-config op "
                    "on one input set, plus a %d MiB device copy of known size before and after, for "
                    "rocprofv3 --pmc passes (few dispatches, no graphs)" % (CALIB_BYTES >> 20))
-    p.add_argument("--trace-summary", nargs=2, metavar=("ROCPROF_DIR", "BENCH_LOG"),
+    p.add_argument("--trace-summary", nargs=2, metavar=("ROCPROF_DIR", "BENCH_JSON"),
                    help="instead: summarise a rocprofv3 --kernel-trace --marker-trace run of this command "
-                   "(per-row kernel durations against the bench line in BENCH_LOG); no GPU used")
+                   "(per-row kernel durations against the bench line in BENCH_JSON, the stdout of an "
+                   "unprofiled run on the same box); no GPU used")
     p.add_argument("--occ-summary", nargs="+", metavar="DIR",
                    help="instead: occupancy, VALU and memory-stall per --pmc-large op from rocprofv3 --pmc passes "
                    "of OccupancyPercent, MeanOccupancyPerCU, VALUBusy, MemUnitStalled (one DIR each, that order); "
