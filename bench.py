@@ -923,13 +923,14 @@ def suite(args, S, torch):
 
         def make_kv():
             q, k, v = randn(1, 16, 128), randn(1, 8, 128), randn(1, 8, 128)
-            kc, vc, qo = randn(512, 8, 128), randn(512, 8, 128), empty(1, 16, 128)
+            kc, vc, qo = randn(DECODE_TOTAL, 8, 128), randn(DECODE_TOTAL, 8, 128), empty(1, 16, 128)
             w = bf16(128)
-            pos = torch.tensor([511], dtype=torch.int32, device="cuda")
-            return lambda: S.qk_norm_rope_kv(q, k, v, w, w, 1e-6, pos, 128, 1e6, kc, vc, 511, q_out=qo)
-        R.run("configs[0]", "qk_norm_rope_kv [128,16+8(+8 v),1]", 64 * 128 * f32 + 4 + 2 * 128 * 2, make_kv,
+            pos = torch.tensor([DECODE_TOTAL - 1], dtype=torch.int32, device="cuda")
+            return lambda: S.qk_norm_rope_kv(q, k, v, w, w, 1e-6, pos, 128, 1e6, kc, vc, DECODE_TOTAL - 1, q_out=qo)
+        R.run("configs[0]", "qk_norm_rope_kv [128,16+8(+8 v),1] at position 37", 64 * 128 * f32 + 4 + 2 * 128 * 2,
+              make_kv, cold=False)
+        R.run("configs[0]", "soft_max_ext [38,1,16]", 2 * 16 * DECODE_TOTAL * f32, lambda: make_sm(1, DECODE_TOTAL),
               cold=False)
-        R.run("configs[0]", "soft_max_ext [512,1,16]", 2 * 16 * 512 * f32, make_sm, cold=False)
         per_layer("configs[0]", "talker layer non-GEMM step (28-layer graph, 4 launches/layer)",
                   decode_layer_us(S, torch), decode_layer_bytes(), "per layer")
         per_layer("configs[0]", "talker layer non-GEMM step + KV-cache write + soft_max over 38 keys "
