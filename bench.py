@@ -1295,7 +1295,11 @@ def main():
     d = ops4[dom]
     roof = {"bound": "hbm", "kernel": d["op"], "achieved": d["GB/s"], "peak": PEAK_GBS, "unit": "GB/s",
             "frac": d["frac"], "traffic": read_traffic(d["op"]), "algorithmic_bytes": d["bytes"],
-            "us_per_launch": d["us"],
+            "us_per_launch": d["us"], "us_per_launch_mean": d["us_mean"],
+            "achieved_from_mean": round(d["bytes"] / (d["us_mean"] * 1e-6) / 1e9, 1),
+            "timing": "achieved = algorithmic bytes / us_per_launch, the median over 10 timed chunks of the "
+                      "mean launch duration in a chunk (HIP events on the replay stream); achieved_from_mean "
+                      "uses the mean over all the launches",
             "traffic_source": "read from the committed counter summary profiles/traffic_large_configs.txt "
                               "(rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of this kernel at this shape, scaled "
                               "by the same counters over a device copy of known size), not measured in this run"}
