@@ -596,6 +596,11 @@ class Graph:
         """ggml_cpy(x, dst): dst a torch tensor (a view of a cache, say)."""
         return self._op(NODE_CPY, dst, [x])
 
+    def cont(self, x):
+        """ggml_cont(x): x (typically a permuted view) copied into a new
+        contiguous tensor of its shape; the same node kind as ggml_cpy."""
+        return self._op(NODE_CPY, self._like(x), [x])
+
     def glu_swiglu(self, a, b=None, swapped=False):
         t = self._t(a)
         shape = tuple(t.shape) if b is not None else tuple(t.shape[:-1]) + (t.shape[-1] // 2,)

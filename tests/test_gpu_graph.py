@@ -201,6 +201,25 @@ def test_reference_order_layer_graph(gpu, T):
     assert_bitexact(out, R.run(lambda gr: gr.add(s_ref, d["mlp"])))
 
 
+def test_cont_of_permuted_views_graph(gpu):
+    """ggml_cont(ggml_permute(x, 0, 2, 1, 3)) as a copy node (operations.cpp:
+    123-125, 139): the contiguous result equals torch's permuted copy bit for
+    bit, after q's rope run in the same list."""
+    import torch
+    rng = np.random.default_rng(SEED + 350)
+    T, heads, hd = 37, 16, 128
+    q = rng.standard_normal((T, heads, hd)).astype(np.float32)
+    wq = rng.normal(1, 0.1, hd).astype(np.float32)
+    pos = _positions(rng, T, 8192)
+    g = gpu.Graph()
+    qr = g.rope_ext(g.mul(g.rms_norm(_t(gpu, q), 1e-6), _t(gpu, wq)), _t(gpu, pos), hd, gpu.ROPE_TYPE_NEOX, 1e6)
+    q_hd = g.cont(g.view(qr, qr.t.permute(1, 0, 2)))
+    assert [k for k, *_ in g.plan(q_hd, qr) if k != "nop"] == ["norm_mul_rope", "single"]
+    g.compute(q_hd, qr)
+    assert q_hd.t.is_contiguous() and tuple(q_hd.t.shape) == (heads, T, hd)
+    assert_bitexact(_np(q_hd.t), _np(qr.t.permute(1, 0, 2).contiguous()))
+
+
 def test_reference_order_layers_chained(gpu):
     """Three decoder layers in one list, each layer's output add feeding the
     next layer's input norm (:147 -> :86): the add and the next norm are one

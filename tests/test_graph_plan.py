@@ -90,6 +90,22 @@ def test_reference_order_layer_is_five_launches():
         ["qk_norm_rope_kv", "single", "add_norm_mul", "silu_mul", "single"]
 
 
+def test_cont_of_permuted_views():
+    """ggml_cont of the attention's permute(0,2,1,3) views (operations.cpp:
+    123-125, 139) keeps rows contiguous and runs as a copy; the transposing
+    permute(1,0,2,3) (:136) strides ne[0] and is unsupported, so ggml keeps
+    it; q's rope run still plans as its own launch before the copy."""
+    g = S.Graph()
+    q = z(5, 4, 16)  # ggml [16, 4, 5]
+    qr = g.rope_ext(g.mul(g.rms_norm(q, 1e-6), z(16)), z(5, dtype=torch.int32), 16, S.ROPE_TYPE_NEOX, 1e6)
+    q_hd = g.cont(g.view(qr, qr.t.permute(1, 0, 2)))  # ggml permute(q, 0, 2, 1, 3): [16, 5, 4]
+    assert kinds(g.plan(q_hd)) == ["norm_mul_rope", "single"]
+    v_hd = z(2, 7, 16)  # ggml [16, 7, 2]
+    g = S.Graph()
+    v_t = g.cont(g.view(v_hd, v_hd.permute(0, 2, 1)))  # ggml permute(v_hd, 1, 0, 2, 3): ne[0] strided
+    assert kinds(g.plan(v_t)) == ["unsupported"]
+
+
 def test_sibling_runs_stay_apart_when_moving_one_up_is_visible():
     """A part that sits later is moved up only when nothing between reads
     what it writes, writes what it reads or writes, or produces its input."""
