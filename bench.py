@@ -25,7 +25,9 @@ input sets whose total exceeds 512 MB (cold cache):
     (logical bytes, every looked-up row per lookup; compulsory bytes beside),
     and the same two over Q5_K tables (the Q5_K_MIXED profile's);
   - configs[3]: Snake, SnakeBeta, add->leaky-ReLU and add->leaky-ReLU with the
-    sum carried, on [512,8192], [256,32768] and [128,131072];
+    sum carried, and the time-major ggml_cont(ggml_transpose(x)) copy in
+    front of each vocoder convolution, on [512,8192], [256,32768] and
+    [128,131072];
   - the decode step's non-GEMM work per talker layer (28-layer
     graph), without and with the KV-cache write and the attention softmax;
   - the 512-token prefill step of the 0.6B talker (with the BF16
@@ -458,10 +460,18 @@ def vocoder_rows(R, S, torch, cfg, seed, shapes=((512, 8192), (256, 32768), (128
             x, y = randn(T, C), empty(T, C)
             return lambda: S.leaky_relu(x, 0.1, out=y)
 
+        def make_cont(C=C, T=T):
+            # ggml_cont(ggml_transpose(x)), x = ggml [C, T] (torch (T, C)):
+            # the time-major copy in front of each vocoder convolution
+            x, y = randn(T, C), empty(C, T)
+            v = x.t()
+            return lambda: S.cpy(v, out=y)
+
         out.append(R.run(cfg, "snake [%d,%d]" % (C, T), 8 * n + 4 * C, make_snake))
         out.append(R.run(cfg, "snake_beta [%d,%d]" % (C, T), 8 * n + 8 * C, make_beta))
         out.append(R.run(cfg, "add_leaky_relu [%d,%d]" % (C, T), 12 * n, make_leaky))
         out.append(R.run(cfg, "add_leaky_relu+sum [%d,%d]" % (C, T), 16 * n, lambda: make_leaky(with_s=True)))
+        out.append(R.run(cfg, "cont(transpose) [%d,%d]" % (C, T), 8 * n, make_cont))
         if variants:
             # the size's streaming floor: one read and one write with no work
             out.append(R.run(cfg, "copy-like floor: bare leaky [%d,%d]" % (C, T), 8 * n, make_bare))
@@ -787,6 +797,8 @@ def cpu_op_builders(seed=SEED + 9):
                              ("add_leaky_relu+sum [%d,%d]" % (C, Tv), 16 * n)):
             out.append((cfg, name, nbytes,
                         lambda g, C=C, Tv=Tv: R.add_leaky(g, take(Tv, C), take(Tv, C), np.float32(0.1))))
+        out.append((cfg, "cont(transpose) [%d,%d]" % (C, Tv), 8 * n,
+                    lambda g, C=C, Tv=Tv: g.cont_f32(take(Tv, C), [Tv, C], [4 * C, 4])))
     return out
 
 

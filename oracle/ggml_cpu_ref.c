@@ -445,6 +445,32 @@ static void op_cast(const orc_node * n, int ith, int nth) {
     }
 }
 
+/* ggml_cont of an F32 view with arbitrary byte strides into a contiguous F32
+ * tensor of the same shape (ggml-CPU's dup into a contiguous destination: per
+ * (i2, i3) plane each thread takes its share of the ne1 rows and walks each
+ * row's ne0 elements through nb0). Sites: the vocoder's time-major copies,
+ * vits/operations.cpp:72,87,100,108; the attention's permuted copies,
+ * qwen3-tts/operations.cpp:120-125,136,139. src1 holds the view's
+ * int64_t ne[4] then nb[4]. */
+static void op_cont_f32(const orc_node * n, int ith, int nth) {
+    const int64_t * v   = (const int64_t *) n->src1;
+    const int64_t   ne0 = v[0], ne1 = v[1], ne2 = v[2], ne3 = v[3];
+    const int64_t   nb0 = v[4], nb1 = v[5], nb2 = v[6], nb3 = v[7];
+    int64_t         r0, r1;
+    chunk(ne1, ith, nth, &r0, &r1);
+    for (int64_t i3 = 0; i3 < ne3; ++i3) {
+        for (int64_t i2 = 0; i2 < ne2; ++i2) {
+            for (int64_t i1 = r0; i1 < r1; ++i1) {
+                const uint8_t * row = (const uint8_t *) n->src0 + i1 * nb1 + i2 * nb2 + i3 * nb3;
+                float *         y   = (float *) n->dst + ((i3 * ne2 + i2) * ne1 + i1) * ne0;
+                for (int64_t i0 = 0; i0 < ne0; ++i0) {
+                    memcpy(&y[i0], row + i0 * nb0, sizeof(float));
+                }
+            }
+        }
+    }
+}
+
 /* ggml_swiglu (single tensor): gate = first half of each row (second when
  * swapped), y = silu(gate) * other half. */
 static void op_glu_swiglu(const orc_node * n, int ith, int nth) {
@@ -544,6 +570,9 @@ static void run_node(const orc_node * n, int ith, int nth) {
             break;
         case ORC_OP_SOFT_MAX:
             op_soft_max(n, ith, nth);
+            break;
+        case ORC_OP_CONT_F32:
+            op_cont_f32(n, ith, nth);
             break;
         default:
             atomic_store(&g_node_error, -1);

@@ -43,6 +43,7 @@ enum orc_op {
     ORC_OP_CAST_F32,     /* BF16/F16/F32 -> F32                     ggml_cast           */
     ORC_OP_GLU_SWIGLU,   /* single-tensor swiglu                    ggml_swiglu         */
     ORC_OP_SOFT_MAX,     /* softmax(x*scale + mask) per row         ggml_soft_max_ext   */
+    ORC_OP_CONT_F32,     /* strided F32 view -> contiguous          ggml_cont           */
 };
 
 /*
@@ -66,6 +67,9 @@ enum orc_op {
  *   SOFT_MAX  : src0 rows of ne0 scores, ne1 rows per head; src1 = F32 mask or
  *               NULL, with src1_rows rows per mask head and i[0] mask heads
  *               (head h reads mask head h % i[0]); f[0] = scale.
+ *   CONT_F32  : src0 = the first element of an F32 view, src1 = int64_t[8]
+ *               (the view's ne[0..3], then its byte strides nb[0..3]); dst
+ *               contiguous. The only op whose src0 is not contiguous.
  */
 typedef struct orc_node {
     int32_t      op;

@@ -24,7 +24,7 @@ LIB_PATH = os.path.join(HERE, "libggml_cpu_ref.so")
 F32, F16, Q8_0, Q5_K, I32, BF16 = 0, 1, 8, 13, 26, 30
 
 (OP_ADD, OP_MUL, OP_DIV, OP_RMS_NORM, OP_ROPE_NEOX, OP_SILU, OP_SIN, OP_SQR, OP_EXP, OP_LEAKY_RELU, OP_SCALE_BIAS,
- OP_GET_ROWS, OP_CAST_F32, OP_GLU_SWIGLU, OP_SOFT_MAX) = range(1, 16)
+ OP_GET_ROWS, OP_CAST_F32, OP_GLU_SWIGLU, OP_SOFT_MAX, OP_CONT_F32) = range(1, 17)
 
 
 class OrcNode(ctypes.Structure):
@@ -181,6 +181,28 @@ class Graph:
         x = np.ascontiguousarray(x)
         dst = np.empty(x.shape, dtype=np.float32)
         return self._node(OP_CAST_F32, dst, x, type0=type0)
+
+    def cont_f32(self, buf, ne, nb, offset=0):
+        """ggml_cont of an F32 view of `buf` (any C-contiguous numpy array,
+        read as raw bytes): the view starts `offset` bytes in, with ggml
+        extents ne[0..3] and byte strides nb[0..3]. Returns the contiguous
+        result as a numpy array of shape (ne3, ne2, ne1, ne0)."""
+        buf = np.ascontiguousarray(buf)
+        ne = [int(v) for v in ne] + [1] * (4 - len(ne))
+        nb = [int(v) for v in nb] + [0] * (4 - len(nb))
+        last = offset + 4 + sum((n - 1) * b for n, b in zip(ne, nb))
+        if offset < 0 or last > buf.nbytes or min(ne) < 1 or min(nb) < 0:
+            raise ValueError("view outside the buffer")
+        view = np.array(ne + nb, dtype=np.int64)
+        dst = np.empty((ne[3], ne[2], ne[1], ne[0]), dtype=np.float32)
+        n = OrcNode()
+        n.op, n.type0, n.ne0, n.nrows, n.ne1 = OP_CONT_F32, F32, ne[0], ne[1] * ne[2] * ne[3], ne[1]
+        n.src0 = ctypes.c_void_p(buf.ctypes.data + offset)
+        n.src1 = _ptr(view)
+        n.dst = _ptr(dst)
+        self.nodes.append(n)
+        self.keep += [dst, buf, view]
+        return dst
 
     def glu_swiglu(self, a, swapped=False):
         a = self._f32(a)

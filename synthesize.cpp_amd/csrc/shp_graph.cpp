@@ -78,7 +78,9 @@ shp_status_t launch_single(const shp_node & n, shp_stream_t st);
 // and well formed, op parameters this library implements (no ALiBi, no rope
 // frequency factors, no softmax sinks).
 bool node_form_ok(const shp_node & n) {
-    for (int k = 0; k < SHP_NODE_MAX_SRC; ++k) {
+    // A copy may read a transposed or permuted F32 view (rows not contiguous).
+    const bool strided_src = n.op == SHP_NODE_CPY && f32_strided_view_dim(&n.src[0]) != 0;
+    for (int k = strided_src ? 1 : 0; k < SHP_NODE_MAX_SRC; ++k) {
         if (present(n.src[k]) && !well_formed(&n.src[k])) {
             return false;
         }
@@ -98,9 +100,9 @@ bool node_form_ok(const shp_node & n) {
         case SHP_NODE_SCALE:
             return unary_ok(n);
         case SHP_NODE_CPY:
-            return well_formed(&n.src[0]) &&
-                   (n.src[0].type == SHP_TYPE_F32 || n.src[0].type == SHP_TYPE_F16 ||
-                    n.src[0].type == SHP_TYPE_BF16) &&
+            return (strided_src || (well_formed(&n.src[0]) && (n.src[0].type == SHP_TYPE_F32 ||
+                                                                n.src[0].type == SHP_TYPE_F16 ||
+                                                                n.src[0].type == SHP_TYPE_BF16))) &&
                    f32_of(n.dst) && same_shape(n.src[0], n.dst);
         case SHP_NODE_GET_ROWS: {
             const auto & t   = n.src[0];
@@ -313,9 +315,12 @@ class Planner {
         uintptr_t hi;
     };
 
-    // The bytes a descriptor can address: from data to the end of its last row.
+    // The bytes a descriptor can address: from data to the end of its last
+    // element (of its last row, for a block type). A strided view's ne[0]
+    // counts through nb[0].
     static Span extent(const shp_tensor & t) {
-        size_t end = row_bytes(t.type, t.ne[0]);
+        size_t end = block_type(t.type) ? row_bytes(t.type, t.ne[0]) :
+                                          type_size(t.type) + static_cast<size_t>(t.ne[0] - 1) * t.nb[0];
         for (int d = 1; d < 4; ++d) {
             end += static_cast<size_t>(t.ne[d] - 1) * t.nb[d];
         }

@@ -365,6 +365,31 @@ inline bool well_formed(const shp_tensor * t) {
     return ts != 0 && t->nb[0] == ts;
 }
 
+// An F32 view whose rows are not contiguous but one of dims 1..3 is: what
+// ggml_permute / ggml_transpose leave in front of a ggml_cont. Returns that
+// dimension (1..3), or 0 when t is not such a view. Every stride is a
+// multiple of 4 bytes and every extent positive.
+inline int f32_strided_view_dim(const shp_tensor * t) {
+    if (t == nullptr || t->data == nullptr || t->reserved != 0 || t->type != SHP_TYPE_F32 ||
+        reinterpret_cast<uintptr_t>(t->data) % 4 != 0) {
+        return 0;
+    }
+    for (int d = 0; d < 4; ++d) {
+        if (t->ne[d] <= 0 || t->nb[d] % 4 != 0 || t->nb[d] == 0) {
+            return 0;
+        }
+    }
+    if (t->nb[0] == 4) {
+        return 0;
+    }
+    for (int d = 1; d < 4; ++d) {
+        if (t->nb[d] == 4 && t->ne[d] > 1) {
+            return d;
+        }
+    }
+    return 0;
+}
+
 inline RowMap make_rowmap(const shp_tensor & t) {
     RowMap m{};
     m.ne1  = t.ne[1];

@@ -1,0 +1,120 @@
+"""ggml_cont / ggml_cpy of transposed and permuted F32 views through shp_cpy:
+the vocoder's time-major copies around each convolution (vits/operations.cpp:
+72,87,100,108) and the attention's permute(1,0,2,3) copy (qwen3-tts/
+operations.cpp:136). Every result must equal the oracle's ggml_cont
+restatement bit for bit, and torch's own permuted copy too."""
+import numpy as np
+import pytest
+
+import ggml_ref as R
+from test_gpu_parity import _np, assert_bitexact
+
+pytestmark = pytest.mark.gpu
+SEED = 20261202
+
+
+def _oracle_cont(gpu, base, v):
+    """The oracle's ggml_cont of the torch view v of the contiguous tensor
+    base, read through the same ggml extents and byte strides the library
+    sees."""
+    d = gpu.desc(v)
+    g = R.Graph()
+    y = g.cont_f32(_np(base), list(d.ne), list(d.nb), offset=v.data_ptr() - base.data_ptr())
+    g.compute(8)
+    return y.reshape(tuple(v.shape))
+
+
+def _source(rng, shape):
+    import torch
+    return torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).cuda()
+
+
+# (torch shape of the contiguous source, permutation of its axes)
+CASES = [
+    ((37, 70), (1, 0)),            # ragged tiles; ne0 = 37: element-wide path
+    ((64, 64), (1, 0)),            # one full tile
+    ((128, 256), (1, 0)),          # full tiles, 16-byte path
+    ((200, 196), (1, 0)),          # 16-byte path with partial tiles along both dims
+    ((130, 7), (1, 0)),
+    ((1, 33), (1, 0)),             # ne0 = 1
+    ((1000, 3), (1, 0)),
+    ((4, 4096), (1, 0)),
+    ((5, 9, 130), (1, 2, 0)),      # contiguous dim lands on ggml dim 1
+    ((2, 16, 7, 128), (0, 3, 1, 2)),  # contiguous dim lands on ggml dim 2
+    ((7, 9, 11, 12), (3, 0, 1, 2)),   # contiguous dim lands on ggml dim 3
+    ((2, 3, 5, 7), (3, 2, 1, 0)),
+    ((37, 16, 128), (0, 2, 1)),    # ggml permute(x, 1, 0, 2, 3) of x = [128, 16, 37]
+]
+
+
+@pytest.mark.parametrize("shape,perm", CASES)
+def test_transposed_copy_matches_oracle(gpu, shape, perm):
+    rng = np.random.default_rng(SEED + sum(shape))
+    x = _source(rng, shape)
+    v = x.permute(perm)
+    d = gpu.desc(v)
+    print("case", shape, perm, list(d.ne), list(d.nb), flush=True)
+    assert d.nb[0] != 4
+    y = gpu.cpy(v)
+    assert_bitexact(_np(y), _oracle_cont(gpu, x, v))
+    assert_bitexact(_np(y), _np(v.contiguous()))
+
+
+@pytest.mark.parametrize("shift", [0, 1, 2, 3])
+def test_unaligned_views_take_the_narrow_path(gpu, shift):
+    """A view starting 1-3 floats past a 16-byte boundary, or with strides
+    that are not multiples of 16 bytes, is copied element by element; the
+    result is the same."""
+    import torch
+    rng = np.random.default_rng(SEED + 40 + shift)
+    x = _source(rng, (300, 258))
+    v = x[:, shift:shift + 200].t()  # ggml [300, 200] over rows of 258 floats
+    print("shift", shift, flush=True)
+    y = gpu.cpy(v)
+    assert_bitexact(_np(y), _oracle_cont(gpu, x, v))
+    out = torch.empty((200, 300), dtype=torch.float32, device="cuda")
+    gpu.cpy(v, out)
+    assert_bitexact(_np(out), _np(v.contiguous()))
+
+
+def test_into_a_row_strided_destination(gpu):
+    """The destination may be a slice of a wider buffer (rows contiguous, row
+    stride larger): only its own elements are written."""
+    import torch
+    rng = np.random.default_rng(SEED + 60)
+    x = _source(rng, (96, 160))
+    big = torch.full((160, 128), 7.0, dtype=torch.float32, device="cuda")
+    dst = big[:, 16:112]
+    gpu.cpy(x.t(), dst)
+    host = _np(big)
+    assert_bitexact(host[:, 16:112], _np(x.t().contiguous()))
+    assert (host[:, :16] == 7.0).all() and (host[:, 112:] == 7.0).all()
+
+
+@pytest.mark.parametrize("C,T", [(512, 8192), (256, 32768), (128, 131072)])
+def test_vocoder_time_major_copy_full_size(gpu, C, T):
+    """ggml_cont(ggml_transpose(x)) of a vocoder activation x = ggml [C, T]
+    (vits/operations.cpp:72) at the Snake shapes: x stored as torch (T, C)."""
+    rng = np.random.default_rng(SEED + C)
+    x = _source(rng, (T, C))
+    v = x.t()
+    print("C", C, "T", T, flush=True)
+    y = gpu.cpy(v)
+    assert_bitexact(_np(y), _oracle_cont(gpu, x, v))
+    back = gpu.cpy(y.t())  # and back: the depthwise branch's final transpose (:108)
+    assert_bitexact(_np(back), _np(x))
+
+
+def test_transposed_copy_in_a_node_list(gpu):
+    """The executor runs ggml_cont(ggml_transpose(x)) as a copy node between
+    the vocoder's leaky-ReLU and the next consumer, each node on its own."""
+    rng = np.random.default_rng(SEED + 80)
+    x = _source(rng, (1024, 192))  # ggml [192, 1024]
+    g = gpu.Graph()
+    act = g.leaky_relu(x, 0.1)
+    tm = g.cont(g.view(act, act.t.t()))
+    out = g.exp(tm)
+    kinds = [k for k, *_ in g.plan(act, out) if k != "nop"]
+    assert kinds == ["single", "single", "single"], kinds
+    g.compute(act, out)
+    assert_bitexact(_np(tm.t), np.ascontiguousarray(_np(act.t).T))

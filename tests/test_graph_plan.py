@@ -92,9 +92,12 @@ def test_reference_order_layer_is_five_launches():
 
 def test_cont_of_permuted_views():
     """ggml_cont of the attention's permute(0,2,1,3) views (operations.cpp:
-    123-125, 139) keeps rows contiguous and runs as a copy; the transposing
-    permute(1,0,2,3) (:136) strides ne[0] and is unsupported, so ggml keeps
-    it; q's rope run still plans as its own launch before the copy."""
+    123-125, 139) keeps rows contiguous and runs as a copy; so does the
+    transposing permute(1,0,2,3) (:136), whose ne[0] is strided, and the
+    vocoder's ggml_cont(ggml_transpose(x)) (vits/operations.cpp:72); q's rope
+    run still plans as its own launch before the copy. A view with no
+    contiguous dimension, an F16 transposed view and a copy into a
+    non-contiguous destination row stay unsupported."""
     g = S.Graph()
     q = z(5, 4, 16)  # ggml [16, 4, 5]
     qr = g.rope_ext(g.mul(g.rms_norm(q, 1e-6), z(16)), z(5, dtype=torch.int32), 16, S.ROPE_TYPE_NEOX, 1e6)
@@ -103,7 +106,17 @@ def test_cont_of_permuted_views():
     v_hd = z(2, 7, 16)  # ggml [16, 7, 2]
     g = S.Graph()
     v_t = g.cont(g.view(v_hd, v_hd.permute(0, 2, 1)))  # ggml permute(v_hd, 1, 0, 2, 3): ne[0] strided
-    assert kinds(g.plan(v_t)) == ["unsupported"]
+    assert kinds(g.plan(v_t)) == ["single"]
+    x = z(512, 96)  # ggml [96, 512]
+    g = S.Graph()
+    assert kinds(g.plan(g.cont(g.view(x, x.t())))) == ["single"]
+    g = S.Graph()
+    assert kinds(g.plan(g.cont(g.view(x, x[:, ::2].t())))) == ["unsupported"]  # ggml nb [384, 8]: no dim contiguous
+    h = z(64, 96, dtype=torch.float16)
+    g = S.Graph()
+    assert kinds(g.plan(g.cont(g.view(h, h.t())))) == ["unsupported"]
+    g = S.Graph()
+    assert kinds(g.plan(g.cpy(g.view(x, x.t()), z(96, 1024)[:, ::2]))) == ["unsupported"]
 
 
 def test_sibling_runs_stay_apart_when_moving_one_up_is_visible():

@@ -442,3 +442,55 @@ def test_thread_split_invariance():
         many = R.run(build, n_threads=nth)
         for a, b in zip(one, many):
             np.testing.assert_array_equal(bits(a), bits(b))
+
+
+# ---------------------------------------------------------------------------
+# ggml_cont of strided views
+# ---------------------------------------------------------------------------
+
+def _ggml_view(a, perm):
+    """(ne, nb) of the ggml view that numpy's a.transpose(perm) is: numpy axis
+    order reversed into ggml dims."""
+    t = a.transpose(perm)
+    return list(t.shape[::-1]), list(t.strides[::-1]), t
+
+
+@pytest.mark.parametrize("shape,perm", [((37, 70), (1, 0)), ((5, 9, 130), (1, 2, 0)), ((3, 4, 66, 7), (0, 3, 2, 1)),
+                                        ((2, 3, 5, 7), (3, 2, 1, 0)), ((64, 64), (1, 0)), ((1, 33), (1, 0))])
+def test_cont_against_numpy_transpose(shape, perm):
+    """ggml_cont of a transposed/permuted view equals numpy's own transposed
+    copy (an independent implementation), on non-square extents so that a
+    swapped index or stride cannot pass, at 1 and several threads."""
+    rng = np.random.default_rng(sum(shape))
+    a = rng.standard_normal(shape).astype(np.float32)
+    ne, nb, t = _ggml_view(a, perm)
+    for nth in (1, 3, 8):
+        g = R.Graph()
+        y = g.cont_f32(a, ne, nb)
+        g.compute(nth)
+        np.testing.assert_array_equal(bits(y.reshape(t.shape)), bits(np.ascontiguousarray(t)))
+
+
+def test_cont_identities():
+    """A contiguous view copies to itself; transposing twice gives back the
+    source; a view at an offset equals numpy's slice; and a planted mistake
+    (extents and strides of dims 0 and 1 both left unswapped: the transpose
+    dropped) does not equal the transposed copy."""
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal((6, 11, 40)).astype(np.float32)
+    g = R.Graph()
+    same = g.cont_f32(a, [40, 11, 6], [4, 160, 1760])
+    ne, nb, _ = _ggml_view(a, (0, 2, 1))
+    once = g.cont_f32(a, ne, nb)
+    g.compute(2)
+    np.testing.assert_array_equal(bits(same.reshape(a.shape)), bits(a))
+    g = R.Graph()
+    twice = g.cont_f32(once, [40, 11, 6], [44, 4, 1760])
+    sub = g.cont_f32(a, [7, 3, 2], [8, 160, 1760 * 3], offset=4 * (1 + 40 * 2 + 440 * 1))
+    planted = g.cont_f32(a, [ne[1], ne[0]] + ne[2:], [nb[1], nb[0]] + nb[2:])
+    g.compute(1)
+    np.testing.assert_array_equal(bits(twice.reshape(a.shape)), bits(a))
+    np.testing.assert_array_equal(bits(sub.reshape(2, 3, 7)), bits(a[1::3, 2:5, 1:15:2]))
+    assert not np.array_equal(bits(planted), bits(once))
+    with pytest.raises(ValueError):
+        R.Graph().cont_f32(a, [41, 11, 6], [4, 160, 1760])
