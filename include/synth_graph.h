@@ -63,8 +63,10 @@ typedef enum shp_node_op {
     SHP_NODE_SCALE,      /* GGML_OP_SCALE: f32 {s, b} */
     SHP_NODE_CPY,        /* GGML_OP_CPY (ggml_cpy, ggml_cast): src[0] into dst; also
                             GGML_OP_CONT (ggml_cont: src[0] into a contiguous dst of
-                            its shape), e.g. of a permute(0,2,1,3) view; a view whose
-                            ne[0] is strided (a transpose) is unsupported */
+                            its shape), e.g. of a permute(0,2,1,3) view, or of an F32
+                            transpose / permute whose ne[0] is strided and one of dims
+                            1..3 contiguous; a view with no contiguous dimension is
+                            unsupported */
     SHP_NODE_GET_ROWS,   /* GGML_OP_GET_ROWS: src[0] table, src[1] ids */
     SHP_NODE_RMS_NORM,   /* GGML_OP_RMS_NORM: f32 {eps} */
     SHP_NODE_SOFT_MAX,   /* GGML_OP_SOFT_MAX: f32 {scale, max_bias}; src[1] mask or absent */

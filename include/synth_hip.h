@@ -313,7 +313,14 @@ shp_status_t shp_add(const shp_tensor * a, const shp_tensor * b, shp_tensor * y,
  *   shp_sqr  ggml_sqr (qwen3-tts/codec.cpp:196)
  *   shp_cpy  ggml_cpy / ggml_cast into F32 of the same shape from F32, F16
  *            or BF16 (qwen3-tts/operations.cpp:20-25, the KV-cache writes
- *            :109-116); rows may be strided on either side
+ *            :109-116); rows may be strided on either side. An F32 x may
+ *            also be a transposed or permuted view, ne[0] strided and one of
+ *            dims 1..3 contiguous (nb = 4): ggml_cont(ggml_transpose(x)),
+ *            the vocoder's time-major copies (vits/operations.cpp:72,87,100,
+ *            108), and ggml_cont(ggml_permute(v, 1, 0, 2, 3))
+ *            (qwen3-tts/operations.cpp:136); y's rows contiguous. Such a view
+ *            with no contiguous dimension, or of another type, is
+ *            SHP_ERR_UNSUPPORTED
  * All F32 unless stated; y has a's shape.
  */
 shp_status_t shp_mul(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream);
