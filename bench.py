@@ -25,9 +25,9 @@ input sets whose total exceeds 512 MB (cold cache):
     (logical bytes, every looked-up row per lookup; compulsory bytes beside),
     and the same two over Q5_K tables (the Q5_K_MIXED profile's);
   - configs[3]: Snake, SnakeBeta, add->leaky-ReLU and add->leaky-ReLU with the
-    sum carried, and the time-major ggml_cont(ggml_transpose(x)) copy in
-    front of each vocoder convolution, on [512,8192], [256,32768] and
-    [128,131072];
+    sum carried, the time-major ggml_cont(ggml_transpose(x)) copy in
+    front of each vocoder convolution and the [1, C] bias add behind it, on
+    [512,8192], [256,32768] and [128,131072];
   - the decode step's non-GEMM work per talker layer (28-layer
     graph), without and with the KV-cache write and the attention softmax;
   - the 512-token prefill step of the 0.6B talker (with the BF16
@@ -460,6 +460,12 @@ def vocoder_rows(R, S, torch, cfg, seed, shapes=((512, 8192), (256, 32768), (128
             x, y = randn(T, C), empty(T, C)
             return lambda: S.leaky_relu(x, 0.1, out=y)
 
+        def make_bias(C=C, T=T):
+            # the time-major vocoder's conv bias: ggml [T, C] + [1, C], one
+            # value per row (vits/waveform-decoder.cpp:118-121)
+            x, y, b = randn(C, T), empty(C, T), randn(C, 1)
+            return lambda: S.add(x, b, out=y)
+
         def make_cont(C=C, T=T):
             # ggml_cont(ggml_transpose(x)), x = ggml [C, T] (torch (T, C)):
             # the time-major copy in front of each vocoder convolution
@@ -472,6 +478,7 @@ def vocoder_rows(R, S, torch, cfg, seed, shapes=((512, 8192), (256, 32768), (128
         out.append(R.run(cfg, "add_leaky_relu [%d,%d]" % (C, T), 12 * n, make_leaky))
         out.append(R.run(cfg, "add_leaky_relu+sum [%d,%d]" % (C, T), 16 * n, lambda: make_leaky(with_s=True)))
         out.append(R.run(cfg, "cont(transpose) [%d,%d]" % (C, T), 8 * n, make_cont))
+        out.append(R.run(cfg, "add bias[1,C] time-major [%d,%d]" % (C, T), 8 * n + 4 * C, make_bias))
         if variants:
             # the size's streaming floor: one read and one write with no work
             out.append(R.run(cfg, "copy-like floor: bare leaky [%d,%d]" % (C, T), 8 * n, make_bare))
@@ -799,6 +806,8 @@ def cpu_op_builders(seed=SEED + 9):
                         lambda g, C=C, Tv=Tv: R.add_leaky(g, take(Tv, C), take(Tv, C), np.float32(0.1))))
         out.append((cfg, "cont(transpose) [%d,%d]" % (C, Tv), 8 * n,
                     lambda g, C=C, Tv=Tv: g.cont_f32(take(Tv, C), [Tv, C], [4 * C, 4])))
+        out.append((cfg, "add bias[1,C] time-major [%d,%d]" % (C, Tv), 8 * n + 4 * C,
+                    lambda g, C=C, Tv=Tv: g.binbcast(R.OP_ADD, take(C, Tv), take(C, 1))))
     return out
 
 

@@ -245,6 +245,37 @@ static void op_binary(const orc_node * n, int ith, int nth) {
     }
 }
 
+/* ggml_add / ggml_mul / ggml_div with src1 repeated to src0's shape
+ * (ggml_can_repeat: each src1 extent divides src0's): ggml-CPU's binary ops
+ * take src0's rows in thread chunks and read src1's row (i1 % ne11,
+ * i2 % ne12, i3 % ne13); when ne10 < ne00 that row is applied ne00/ne10
+ * times along the row. Sites: the per-channel [1, C] bias and gain vectors,
+ * vits/waveform-decoder.cpp:120,139, qwen3-tts/codec.cpp:180,
+ * omnivoice/codec.cpp:163, omnivoice/reference-encoder.cpp:135-136.
+ * src0, src1 and dst contiguous; src1 points at int64_t[8]: src0's ne[0..3],
+ * src1's ne[0..3], then the src1 data pointer as int64_t; i[0] = the op
+ * (ORC_OP_ADD, ORC_OP_MUL or ORC_OP_DIV). */
+static void op_binbcast(const orc_node * n, int ith, int nth) {
+    const int64_t * v    = (const int64_t *) n->src1;
+    const int64_t   ne00 = v[0], ne01 = v[1], ne02 = v[2], ne03 = v[3];
+    const int64_t   ne10 = v[4], ne11 = v[5], ne12 = v[6], ne13 = v[7];
+    const float *   b    = (const float *) (intptr_t) v[8];
+    int64_t         r0, r1;
+    chunk(ne01 * ne02 * ne03, ith, nth, &r0, &r1);
+    for (int64_t r = r0; r < r1; ++r) {
+        const int64_t i1 = r % ne01, i2 = (r / ne01) % ne02, i3 = r / (ne01 * ne02);
+        const float * a  = (const float *) n->src0 + r * ne00;
+        const float * br = b + ((i3 % ne13) * ne12 * ne11 + (i2 % ne12) * ne11 + (i1 % ne11)) * ne10;
+        float *       d  = (float *) n->dst + r * ne00;
+        for (int64_t k = 0; k < ne00 / ne10; ++k) {
+            for (int64_t i = 0; i < ne10; ++i) {
+                const float av = a[k * ne10 + i], bv = br[i];
+                d[k * ne10 + i] = n->i[0] == ORC_OP_ADD ? av + bv : n->i[0] == ORC_OP_MUL ? av * bv : av / bv;
+            }
+        }
+    }
+}
+
 /* ggml_rms_norm: rows interleaved over threads; f32 squares summed in double,
  * mean rounded to f32, scale = 1/sqrtf(mean + eps), y = x*scale.
  * Sites: qwen3-tts/operations.cpp:31 (via rms_norm :27-32), :86, :98-99, :145. */
@@ -573,6 +604,9 @@ static void run_node(const orc_node * n, int ith, int nth) {
             break;
         case ORC_OP_CONT_F32:
             op_cont_f32(n, ith, nth);
+            break;
+        case ORC_OP_BINBCAST:
+            op_binbcast(n, ith, nth);
             break;
         default:
             atomic_store(&g_node_error, -1);

@@ -44,6 +44,7 @@ enum orc_op {
     ORC_OP_GLU_SWIGLU,   /* single-tensor swiglu                    ggml_swiglu         */
     ORC_OP_SOFT_MAX,     /* softmax(x*scale + mask) per row         ggml_soft_max_ext   */
     ORC_OP_CONT_F32,     /* strided F32 view -> contiguous          ggml_cont           */
+    ORC_OP_BINBCAST,     /* add/mul/div, src1 repeated (can_repeat) ggml_add ...        */
 };
 
 /*
@@ -67,6 +68,9 @@ enum orc_op {
  *   SOFT_MAX  : src0 rows of ne0 scores, ne1 rows per head; src1 = F32 mask or
  *               NULL, with src1_rows rows per mask head and i[0] mask heads
  *               (head h reads mask head h % i[0]); f[0] = scale.
+ *   BINBCAST  : src1 = int64_t[9]: src0's ne[0..3], src1's ne[0..3], the
+ *               src1 data pointer; i[0] = ORC_OP_ADD, _MUL or _DIV. Every
+ *               src1 extent divides src0's; all contiguous.
  *   CONT_F32  : src0 = the first element of an F32 view, src1 = int64_t[8]
  *               (the view's ne[0..3], then its byte strides nb[0..3]); dst
  *               contiguous. The only op whose src0 is not contiguous.

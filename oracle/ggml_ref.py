@@ -24,7 +24,7 @@ LIB_PATH = os.path.join(HERE, "libggml_cpu_ref.so")
 F32, F16, Q8_0, Q5_K, I32, BF16 = 0, 1, 8, 13, 26, 30
 
 (OP_ADD, OP_MUL, OP_DIV, OP_RMS_NORM, OP_ROPE_NEOX, OP_SILU, OP_SIN, OP_SQR, OP_EXP, OP_LEAKY_RELU, OP_SCALE_BIAS,
- OP_GET_ROWS, OP_CAST_F32, OP_GLU_SWIGLU, OP_SOFT_MAX, OP_CONT_F32) = range(1, 17)
+ OP_GET_ROWS, OP_CAST_F32, OP_GLU_SWIGLU, OP_SOFT_MAX, OP_CONT_F32, OP_BINBCAST) = range(1, 18)
 
 
 class OrcNode(ctypes.Structure):
@@ -181,6 +181,27 @@ class Graph:
         x = np.ascontiguousarray(x)
         dst = np.empty(x.shape, dtype=np.float32)
         return self._node(OP_CAST_F32, dst, x, type0=type0)
+
+    def binbcast(self, op, a, b):
+        """ggml_add / ggml_mul / ggml_div (op = OP_ADD, OP_MUL, OP_DIV) with b
+        repeated to a's shape: a and b are numpy arrays in the module's
+        layout (ggml [ne0, ne1, ne2, ne3] = numpy (ne3, ne2, ne1, ne0), up to
+        4 axes); every ggml extent of b must divide a's."""
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        b = np.ascontiguousarray(b, dtype=np.float32)
+        ane = list(a.shape[::-1]) + [1] * (4 - a.ndim)
+        bne = list(b.shape[::-1]) + [1] * (4 - b.ndim)
+        if any(x < 1 or y % x for x, y in zip(bne, ane)):
+            raise ValueError("b does not repeat to a's shape")
+        view = np.array(ane + bne + [b.ctypes.data], dtype=np.int64)
+        dst = np.empty(a.shape, dtype=np.float32)
+        n = OrcNode()
+        n.op, n.type0, n.ne0, n.nrows = OP_BINBCAST, F32, ane[0], ane[1] * ane[2] * ane[3]
+        n.src0, n.src1, n.dst = _ptr(a), _ptr(view), _ptr(dst)
+        n.i[0] = op
+        self.nodes.append(n)
+        self.keep += [dst, a, b, view]
+        return dst
 
     def cont_f32(self, buf, ne, nb, offset=0):
         """ggml_cont of an F32 view of `buf` (any C-contiguous numpy array,

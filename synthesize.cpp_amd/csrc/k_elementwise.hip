@@ -660,7 +660,7 @@ shp_status_t launch_ew(const EwArgs & a, bool flat, bool vec, hipStream_t stream
 }
 
 // Common argument set-up. `b` may be null, may match `a`'s shape, or (when
-// allow_bcast) be a single contiguous row of ne0 elements.
+// allow_bcast) be one row of ne0 elements.
 struct EwPlan {
     EwArgs args{};
     bool   flat  = false;
@@ -685,7 +685,7 @@ shp_status_t plan_ew(const shp_tensor * a,
         return SHP_ERR_INVALID_ARG;
     }
     if (b != nullptr && !same_shape(*a, *b)) {
-        if (!allow_bcast || nelements(*b) != a->ne[0] || !contiguous(*b)) {
+        if (!allow_bcast || !one_row_of(*b, a->ne[0])) {
             return SHP_ERR_INVALID_ARG;
         }
         plan.bcast = true;
@@ -876,12 +876,165 @@ extern "C" shp_status_t shp_add_leaky_relu(const shp_tensor * a,
 namespace shp {
 namespace {
 
-// ggml_add / ggml_mul / ggml_div: b the same shape as a, or one contiguous row
-// of ne0 elements repeated over every row.
+// ggml_add / ggml_mul / ggml_div with b repeated to a's shape in every other
+// form ggml_can_repeat allows (each b->ne[d] divides a->ne[d]; ggml-CPU's
+// binary ops read b at (i0 % b.ne0, i1 % b.ne1, i2 % b.ne2, i3 % b.ne3)). The
+// graphs' per-channel bias and gain vectors reshaped to [1, C] against a
+// time-major [T, C] activation are one value per row: vits/waveform-
+// decoder.cpp:120,139, vits/operations.cpp:106,155, qwen3-tts/codec.cpp:180,
+// omnivoice/codec.cpp:163, omnivoice/reference-encoder.cpp:135-136.
+struct RepeatArgs {
+    const float * a;
+    RowMap        am;
+    float *       y;
+    RowMap        ym;
+    const char *  b;
+    int64_t       bnb1;
+    int64_t       bnb2;
+    int64_t       bnb3;
+    int64_t       brs;    // kRepeatFlat: byte stride between b's values, one per row of a
+    FastDiv       ne1;    // a's extents: row r = i1 + ne1*(i2 + ne2*i3)
+    FastDiv       ne2;
+    FastDiv       bne0;   // b's extents (the repeat periods)
+    FastDiv       bne1;
+    FastDiv       bne2;
+    FastDiv       bne3;
+    FastDiv       quads;  // flat kernel: float4 per row of a
+    int64_t       nrows;
+    int64_t       n4;
+    int32_t       ne0;
+    int32_t       pad;
+};
+
+template <int OP> __device__ __forceinline__ float binop(float a, float b) {
+    if constexpr (OP == kAdd) {
+        return a + b;
+    } else if constexpr (OP == kMul) {
+        return a * b;
+    } else {
+        static_assert(OP == kDiv, "binary op");
+        return a / b;
+    }
+}
+
+// Byte offset of b's row for row r of a.
+__device__ __forceinline__ int64_t repeat_row(const RepeatArgs & g, uint32_t r) {
+    const uint32_t q  = fastdiv(r, g.ne1);
+    const uint32_t i1 = r - q * g.ne1.d;
+    const uint32_t i3 = fastdiv(q, g.ne2);
+    const uint32_t i2 = q - i3 * g.ne2.d;
+    return static_cast<int64_t>(fastmod(i1, g.bne1)) * g.bnb1 + static_cast<int64_t>(fastmod(i2, g.bne2)) * g.bnb2 +
+           static_cast<int64_t>(fastmod(i3, g.bne3)) * g.bnb3;
+}
+
+// One value of b per row of a (b.ne0 == 1), a and y contiguous and 16-byte
+// aligned with ne0 % 4 == 0: one float4 per lane, as the flat kernels. FLAT:
+// b's rows are a's rows one for one at a fixed stride (b = [1, ne1, ne2,
+// ne3]), so the row's value is at row * brs.
+template <int OP, bool FLAT, int BLOCK> __global__ __launch_bounds__(BLOCK) void k_repeat_col(const RepeatArgs g) {
+    const f32x4 * A    = reinterpret_cast<const f32x4 *>(g.a);
+    f32x4 *       Y    = reinterpret_cast<f32x4 *>(g.y);
+    const int64_t step = static_cast<int64_t>(gridDim.x) * BLOCK;
+    for (int64_t e = static_cast<int64_t>(blockIdx.x) * BLOCK + threadIdx.x; e < g.n4; e += step) {
+        const uint32_t r  = fastdiv(static_cast<uint32_t>(e), g.quads);
+        const int64_t  bo = FLAT ? static_cast<int64_t>(r) * g.brs : repeat_row(g, r);
+        const float    bv = *reinterpret_cast<const float *>(g.b + bo);
+        const f32x4    av = ld_stream(A + e);
+        st_stream(Y + e, f32x4{ binop<OP>(av.x, bv), binop<OP>(av.y, bv), binop<OP>(av.z, bv), binop<OP>(av.w, bv) });
+    }
+}
+
+// Any repeat form and any row strides: rows over blocks, elements over threads.
+template <int OP> __global__ __launch_bounds__(256) void k_repeat_rows(const RepeatArgs g) {
+    for (int64_t r = blockIdx.x; r < g.nrows; r += gridDim.x) {
+        const float * ar = reinterpret_cast<const float *>(reinterpret_cast<const char *>(g.a) + row_offset(g.am, r));
+        float *       yr = reinterpret_cast<float *>(reinterpret_cast<char *>(g.y) + row_offset(g.ym, r));
+        const float * br = reinterpret_cast<const float *>(g.b + repeat_row(g, static_cast<uint32_t>(r)));
+        for (int i = static_cast<int>(threadIdx.x); i < g.ne0; i += 256) {
+            yr[i] = binop<OP>(ar[i], br[fastmod(static_cast<uint32_t>(i), g.bne0)]);
+        }
+    }
+}
+
+template <int OP>
+shp_status_t repeat_entry(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream) {
+    if (!well_formed(a) || !well_formed(b) || !well_formed(y)) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    if (a->type != SHP_TYPE_F32 || b->type != SHP_TYPE_F32 || y->type != SHP_TYPE_F32) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    if (!same_shape(*a, *y) || !can_repeat(*b, *a)) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    const int64_t rows = nrows(*a);
+    if (a->ne[0] > INT32_MAX || rows >= (int64_t{ 1 } << 32) || nelements(*a) >= (int64_t{ 1 } << 32)) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    if (dry_run()) {
+        return SHP_OK;
+    }
+    RepeatArgs g{};
+    g.a     = static_cast<const float *>(a->data);
+    g.am    = make_rowmap(*a);
+    g.y     = static_cast<float *>(y->data);
+    g.ym    = make_rowmap(*y);
+    g.b     = static_cast<const char *>(b->data);
+    g.bnb1  = static_cast<int64_t>(b->nb[1]);
+    g.bnb2  = static_cast<int64_t>(b->nb[2]);
+    g.bnb3  = static_cast<int64_t>(b->nb[3]);
+    g.ne1   = make_fastdiv(static_cast<uint32_t>(a->ne[1]));
+    g.ne2   = make_fastdiv(static_cast<uint32_t>(a->ne[2]));
+    g.bne0  = make_fastdiv(static_cast<uint32_t>(b->ne[0]));
+    g.bne1  = make_fastdiv(static_cast<uint32_t>(b->ne[1]));
+    g.bne2  = make_fastdiv(static_cast<uint32_t>(b->ne[2]));
+    g.bne3  = make_fastdiv(static_cast<uint32_t>(b->ne[3]));
+    g.nrows = rows;
+    g.ne0   = static_cast<int32_t>(a->ne[0]);
+    g.n4    = nelements(*a) / 4;
+    const hipStream_t ss   = as_stream(stream);
+    const bool        flat = b->ne[0] == 1 && a->ne[0] % 4 == 0 && contiguous(*a) && contiguous(*y) &&
+                      rows_aligned(*a, 16) && rows_aligned(*y, 16);
+    if (flat) {
+        g.quads = make_fastdiv(static_cast<uint32_t>(a->ne[0] / 4));
+        // b's rows one for one with a's at a fixed stride: b = [1, ne1, ne2, ne3]
+        const RowMap bm       = make_rowmap(*b);
+        const bool   one_one  = b->ne[1] == a->ne[1] && b->ne[2] == a->ne[2] && b->ne[3] == a->ne[3] && bm.flat;
+        g.brs                 = bm.rs;
+        const bool    wave    = g.n4 >= kFlatWaveBlocksFrom;
+        const int     bs      = wave ? kWave : 256;
+        int64_t       blocks  = (g.n4 + bs - 1) / bs;
+        blocks                = blocks < kMaxFlatBlocks ? blocks : kMaxFlatBlocks;
+        const unsigned grid   = static_cast<unsigned>(blocks);
+        if (one_one) {
+            if (wave) {
+                hipLaunchKernelGGL((k_repeat_col<OP, true, kWave>), dim3(grid), dim3(kWave), 0, ss, g);
+            } else {
+                hipLaunchKernelGGL((k_repeat_col<OP, true, 256>), dim3(grid), dim3(256), 0, ss, g);
+            }
+        } else {
+            if (wave) {
+                hipLaunchKernelGGL((k_repeat_col<OP, false, kWave>), dim3(grid), dim3(kWave), 0, ss, g);
+            } else {
+                hipLaunchKernelGGL((k_repeat_col<OP, false, 256>), dim3(grid), dim3(256), 0, ss, g);
+            }
+        }
+        return launch_status();
+    }
+    const int64_t blocks = rows < 65536 ? rows : 65536;
+    hipLaunchKernelGGL((k_repeat_rows<OP>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, ss, g);
+    return launch_status();
+}
+
+// ggml_add / ggml_mul / ggml_div: b the same shape as a, one row of ne0
+// elements repeated over every row, or any other shape that repeats to a's.
 template <int OP>
 shp_status_t binary_entry(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream) {
     if (b == nullptr) {
         return SHP_ERR_INVALID_ARG;
+    }
+    if (a != nullptr && well_formed(a) && well_formed(b) && !same_shape(*a, *b) && !one_row_of(*b, a->ne[0])) {
+        return repeat_entry<OP>(a, b, y, stream);
     }
     EwPlan             plan;
     const shp_status_t st = plan_ew(a, b, true, y, nullptr, plan);

@@ -43,23 +43,27 @@ bool f32_of(const shp_tensor & t) {
     return well_formed(&t) && t.type == SHP_TYPE_F32 && t.ne[0] <= INT32_MAX;
 }
 
-// ggml_mul / ggml_add / ggml_div operand b: a's shape, or one contiguous row of
-// a.ne[0] elements repeated over a's rows.
+// ggml_mul / ggml_add / ggml_div operand b as the fused runs take it: a's
+// shape, or one row of a.ne[0] elements repeated over a's rows.
 bool row_operand(const shp_tensor & a, const shp_tensor & b) {
-    return f32_of(b) && (same_shape(a, b) || (nelements(b) == a.ne[0] && contiguous(b)));
+    return f32_of(b) && (same_shape(a, b) || one_row_of(b, a.ne[0]));
 }
 
-// A gain vector of n elements: F32, BF16 or F16, one contiguous row.
+// A gain vector of n elements, as ggml_mul repeats it: F32, BF16 or F16,
+// [n, 1, 1, 1]. (Another shape of n elements, [1, n] say, ggml repeats
+// differently.)
 bool gain_vector(const shp_tensor & w, int64_t n) {
-    return well_formed(&w) && weight_kind(w.type) >= 0 && nelements(w) == n && contiguous(w);
+    return well_formed(&w) && weight_kind(w.type) >= 0 && one_row_of(w, n);
 }
 
 bool unary_ok(const shp_node & n) {
     return f32_of(n.src[0]) && f32_of(n.dst) && same_shape(n.src[0], n.dst);
 }
 
+// A single binary node also takes every other b that repeats to a's shape.
 bool binary_ok(const shp_node & n) {
-    return f32_of(n.src[0]) && f32_of(n.dst) && same_shape(n.src[0], n.dst) && row_operand(n.src[0], n.src[1]);
+    return f32_of(n.src[0]) && f32_of(n.dst) && same_shape(n.src[0], n.dst) &&
+           (row_operand(n.src[0], n.src[1]) || (f32_of(n.src[1]) && can_repeat(n.src[1], n.src[0])));
 }
 
 bool rope_params_ok(const shp_node & n) {
@@ -761,7 +765,7 @@ class Planner {
         const int     den = src(dv, 1);
         Members members{ ml, sn, sq, dv, ad };
         auto curve_ok = [C](const shp_tensor & c) {
-            return well_formed(&c) && c.type == SHP_TYPE_F32 && nelements(c) == C && contiguous(c);
+            return well_formed(&c) && c.type == SHP_TYPE_F32 && one_row_of(c, C);
         };
         auto guard_ok = [&](int j) {
             return is(j, SHP_NODE_SCALE) && fparam(nodes_[j], 0) == 1.0f && fparam(nodes_[j], 1) == 1e-9f;

@@ -390,6 +390,24 @@ inline int f32_strided_view_dim(const shp_tensor * t) {
     return 0;
 }
 
+// b = [ne0, 1, 1, 1]: one row, repeated over every row of a. A b of ne0
+// elements in another shape is not this: ggml repeats [1, ne0] as one value
+// per row, for instance.
+inline bool one_row_of(const shp_tensor & b, int64_t ne0) {
+    return b.ne[0] == ne0 && b.ne[1] == 1 && b.ne[2] == 1 && b.ne[3] == 1;
+}
+
+// ggml_can_repeat(b, a): each of b's extents divides a's, and ggml's binary
+// ops read b at (i0 % b.ne0, i1 % b.ne1, i2 % b.ne2, i3 % b.ne3).
+inline bool can_repeat(const shp_tensor & b, const shp_tensor & a) {
+    for (int d = 0; d < 4; ++d) {
+        if (b.ne[d] < 1 || a.ne[d] % b.ne[d] != 0) {
+            return false;
+        }
+    }
+    return true;
+}
+
 inline RowMap make_rowmap(const shp_tensor & t) {
     RowMap m{};
     m.ne1  = t.ne[1];

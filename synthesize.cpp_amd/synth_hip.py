@@ -400,7 +400,8 @@ def leaky_relu(a, slope, out=None):
 
 
 def add(a, b, out=None):
-    """ggml_add(a, b), b the same shape or one broadcast row."""
+    """ggml_add(a, b), b of a's shape or any shape that repeats to it
+    (ggml_can_repeat: each ggml extent of b divides a's)."""
     out = a.new_empty(a.shape) if out is None else out
     _check(load().shp_add(_ref(desc(a)), _ref(desc(b)), _ref(desc(out)), _stream()), "add")
     return out
@@ -433,14 +434,14 @@ def layer_nongemm_step(x, w_in, q, k, wq, wk, pos, attn_out, w_post, gate, up, m
 
 
 def mul(a, b, out=None):
-    """ggml_mul(a, b), b the same shape or one broadcast row."""
+    """ggml_mul(a, b), b as in add."""
     out = a.new_empty(a.shape) if out is None else out
     _check(load().shp_mul(_ref(desc(a)), _ref(desc(b)), _ref(desc(out)), _stream()), "mul")
     return out
 
 
 def div(a, b, out=None):
-    """ggml_div(a, b), b the same shape or one broadcast row."""
+    """ggml_div(a, b), b as in add."""
     out = a.new_empty(a.shape) if out is None else out
     _check(load().shp_div(_ref(desc(a)), _ref(desc(b)), _ref(desc(out)), _stream()), "div")
     return out

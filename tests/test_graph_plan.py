@@ -233,8 +233,9 @@ def snake_graph(g, x, alpha, kind):
         sq = g.sin(g.mul(x, per))
         return g.add(x, g.div(g.mul(sq, sq), g.scale_bias(per, 1.0, 1e-9)))
     la, lb = alpha
-    a = g.exp(g.view(la, la.reshape(-1, 1)))
-    b = g.exp(g.view(lb, lb.reshape(-1, 1)))
+    # ggml_reshape_2d(alpha, ne0, 1) (codec.cpp:193-194): ggml [C, 1], torch (1, C)
+    a = g.exp(g.view(la, la.reshape(1, -1)))
+    b = g.exp(g.view(lb, lb.reshape(1, -1)))
     sq = g.sqr(g.sin(g.mul(x, a)))
     return g.add(x, g.div(sq, g.scale_bias(b, 1.0, 1e-9)))
 
@@ -402,3 +403,33 @@ def test_malformed_lists_are_rejected():
     runs = (S.ShpGraphRun * 1)()
     assert L.shp_graph_plan(arr, n, runs, 1, ctypes.byref(count)) == S.ERR_INVALID_ARG  # capacity
     assert L.shp_graph_plan(arr, 0, None, 0, ctypes.byref(count)) == S.OK and count.value == 0
+
+
+def test_repeated_operands_follow_ggml():
+    """A single add/mul/div takes every b that repeats to a's shape
+    (ggml_can_repeat), such as the time-major vocoder's [1, C] bias
+    (vits/waveform-decoder.cpp:120); a shape that does not repeat is
+    unsupported. A fused run takes only the forms it computes: a gain or a
+    Snake curve of n values is fused only as [n, 1, 1, 1]; as [1, n] ggml
+    repeats it as one value per row, so the nodes run alone."""
+    T, C = 64, 16
+    x = z(C, T)  # ggml [T, C], time-major
+    for b in (z(C, 1), z(1, 1), z(C, T // 2), z(1, T), z(2, T)):
+        g = S.Graph()
+        assert kinds(g.plan(g.add(x, b))) == (["single"] if C % b.shape[0] == 0 else ["unsupported"]), b.shape
+    g = S.Graph()
+    assert kinds(g.plan(g.mul(x, z(3, 1)))) == ["unsupported"]  # 16 rows do not repeat 3
+    # norm -> mul with the gain as ggml [1, n]: not the fused form
+    h = z(4, 32)
+    g = S.Graph()
+    assert kinds(g.plan(g.mul(g.rms_norm(h, 1e-6), z(32)))) == ["norm_mul"]
+    g = S.Graph()
+    assert "norm_mul" not in kinds(g.plan(g.mul(g.rms_norm(h, 1e-6), z(32, 1))))
+    # SnakeBeta with its curves as ggml [1, C]
+    g = S.Graph()
+    xs = z(32, 32)
+    la, lb = z(32), z(32)
+    a = g.exp(g.view(la, la.reshape(-1, 1)))
+    bb = g.exp(g.view(lb, lb.reshape(-1, 1)))
+    sq = g.sqr(g.sin(g.mul(xs, a)))
+    assert "snake_beta" not in kinds(g.plan(g.add(xs, g.div(sq, g.scale_bias(bb, 1.0, 1e-9)))))

@@ -494,3 +494,56 @@ def test_cont_identities():
     assert not np.array_equal(bits(planted), bits(once))
     with pytest.raises(ValueError):
         R.Graph().cont_f32(a, [41, 11, 6], [4, 160, 1760])
+
+
+# ---------------------------------------------------------------------------
+# binary ops with b repeated to a's shape
+# ---------------------------------------------------------------------------
+
+def _tile_to(b, shape):
+    """numpy's own tiling of b to `shape` (ggml's repeat: index modulo b's extent)."""
+    b = b.reshape((1,) * (len(shape) - b.ndim) + b.shape)
+    return np.tile(b, [s // t for s, t in zip(shape, b.shape)])
+
+
+@pytest.mark.parametrize("ashape,bshape", [((6, 37), (6, 1)), ((2, 3, 40), (1, 3, 1)), ((4, 6, 12), (2, 3, 4)),
+                                           ((3, 5, 7, 8), (1, 5, 1, 8)), ((3, 5, 7, 8), (1, 1, 1, 1)),
+                                           ((9, 16), (1, 16)), ((9, 16), (3, 8))])
+def test_binbcast_against_numpy_tile(ashape, bshape):
+    """ggml's repeat semantics against numpy's tile, for every op, at 1 and
+    several threads; the same-shape and one-row forms agree with the plain
+    binary node; and block repetition (a planted mistake: b's index i // r
+    instead of i % n) differs wherever b has more than one value along a
+    repeated dim."""
+    rng = np.random.default_rng(sum(ashape) + 7 * sum(bshape))
+    a = rng.standard_normal(ashape).astype(np.float32)
+    b = (rng.standard_normal(bshape) + 3.0).astype(np.float32)
+    bt = _tile_to(b, ashape)
+    for op, f in ((R.OP_ADD, np.add), (R.OP_MUL, np.multiply), (R.OP_DIV, np.divide)):
+        for nth in (1, 4):
+            g = R.Graph()
+            y = g.binbcast(op, a, b)
+            g.compute(nth)
+            np.testing.assert_array_equal(bits(y), bits(f(a, bt)))
+    block = b
+    for axis, (s_, t_) in enumerate(zip(ashape, bshape)):
+        block = np.repeat(block, s_ // t_, axis=axis)
+    if any(t_ > 1 and s_ > t_ for s_, t_ in zip(ashape, bshape)):
+        assert not np.array_equal(bits(a + block), bits(a + bt))
+
+
+def test_binbcast_reduces_to_the_plain_forms():
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal((5, 64)).astype(np.float32)
+    row = rng.standard_normal(64).astype(np.float32)
+    col = rng.standard_normal((5, 1)).astype(np.float32)
+    g = R.Graph()
+    y1 = g.binbcast(R.OP_ADD, a, row.reshape(1, 64))
+    y2 = g.add(a, row)
+    y3 = g.binbcast(R.OP_MUL, a, col)
+    y4 = g.mul(a, col)
+    g.compute(2)
+    np.testing.assert_array_equal(bits(y1), bits(y2))
+    np.testing.assert_array_equal(bits(y3), bits(y4))
+    with pytest.raises(ValueError):
+        R.Graph().binbcast(R.OP_ADD, a, np.zeros((3, 64), np.float32))
