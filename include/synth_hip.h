@@ -293,8 +293,12 @@ shp_status_t shp_add_leaky_relu(const shp_tensor * a,
                                 shp_stream_t       stream);
 
 /*
- * ggml_add(a, b) with b the same shape as a or one row broadcast over
- * rows (ggml_can_repeat_rows). The plain residual add at
+ * ggml_add(a, b) with b the same shape as a or any shape that repeats to it
+ * (ggml_can_repeat: each b->ne[d] divides a->ne[d], and b is read at
+ * (i0 % b.ne0, i1 % b.ne1, i2 % b.ne2, i3 % b.ne3) as ggml-CPU does): one row
+ * broadcast over rows, and the per-channel [1, C] bias of a time-major
+ * [T, C] activation, one value per row (vits/waveform-decoder.cpp:118-121,
+ * qwen3-tts/codec.cpp:180). The plain residual add at
  * src/arch/qwen3-tts/operations.cpp:143,147 when it is not fused into a norm.
  */
 shp_status_t shp_add(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream);
