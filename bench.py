@@ -25,9 +25,10 @@ input sets whose total exceeds 512 MB (cold cache):
     (logical bytes, every looked-up row per lookup; compulsory bytes beside),
     and the same two over Q5_K tables (the Q5_K_MIXED profile's);
   - configs[3]: Snake, SnakeBeta, add->leaky-ReLU and add->leaky-ReLU with the
-    sum carried, the time-major ggml_cont(ggml_transpose(x)) copy in
-    front of each vocoder convolution and the [1, C] bias add behind it, on
-    [512,8192], [256,32768] and [128,131072];
+    sum carried, the time-major ggml_cont(ggml_transpose(x)) copy of each
+    vocoder convolution's output, the [1, C] bias add behind it, and the
+    whole tail (copy, bias, residual, leaky) as one launch, on [512,8192],
+    [256,32768] and [128,131072];
   - the decode step's non-GEMM work per talker layer (28-layer
     graph), without and with the KV-cache write and the attention softmax;
   - the 512-token prefill step of the 0.6B talker (with the BF16
@@ -466,6 +467,15 @@ def vocoder_rows(R, S, torch, cfg, seed, shapes=((512, 8192), (256, 32768), (128
             x, y, b = randn(C, T), empty(C, T), randn(C, 1)
             return lambda: S.add(x, b, out=y)
 
+        def make_tail(C=C, T=T, resid=False):
+            # the time-major conv's tail in one launch (vits/waveform-
+            # decoder.cpp:111,118-121,146-150): the GEMM output ggml [C, T]
+            # transposed, + the [1, C] bias (+ the residual), leaky-ReLU
+            x, y, b = randn(T, C), empty(C, T), randn(C, 1)
+            r, s_ = (randn(C, T), empty(C, T)) if resid else (None, None)
+            v = x.t()
+            return lambda: S.cont_add_leaky_relu(v, b, r, 0.1, out=y, sum_out=s_)
+
         def make_cont(C=C, T=T):
             # ggml_cont(ggml_transpose(x)), x = ggml [C, T] (torch (T, C)):
             # the time-major copy in front of each vocoder convolution
@@ -479,6 +489,10 @@ def vocoder_rows(R, S, torch, cfg, seed, shapes=((512, 8192), (256, 32768), (128
         out.append(R.run(cfg, "add_leaky_relu+sum [%d,%d]" % (C, T), 16 * n, lambda: make_leaky(with_s=True)))
         out.append(R.run(cfg, "cont(transpose) [%d,%d]" % (C, T), 8 * n, make_cont))
         out.append(R.run(cfg, "add bias[1,C] time-major [%d,%d]" % (C, T), 8 * n + 4 * C, make_bias))
+        out.append(R.run(cfg, "conv tail: cont(transpose)+bias->leaky [%d,%d]" % (C, T), 8 * n + 4 * C,
+                         make_tail))
+        out.append(R.run(cfg, "conv tail: cont(transpose)+bias+residual->leaky, sum [%d,%d]" % (C, T),
+                         16 * n + 4 * C, lambda: make_tail(resid=True)))
         if variants:
             # the size's streaming floor: one read and one write with no work
             out.append(R.run(cfg, "copy-like floor: bare leaky [%d,%d]" % (C, T), 8 * n, make_bare))
@@ -808,6 +822,16 @@ def cpu_op_builders(seed=SEED + 9):
                     lambda g, C=C, Tv=Tv: g.cont_f32(take(Tv, C), [Tv, C], [4 * C, 4])))
         out.append((cfg, "add bias[1,C] time-major [%d,%d]" % (C, Tv), 8 * n + 4 * C,
                     lambda g, C=C, Tv=Tv: g.binbcast(R.OP_ADD, take(C, Tv), take(C, 1))))
+
+        def tail(g, C=C, Tv=Tv, resid=False):
+            t = g.cont_f32(take(Tv, C), [Tv, C], [4 * C, 4]).reshape(C, Tv)
+            s_ = g.binbcast(R.OP_ADD, t, take(C, 1))
+            if resid:
+                s_ = g.add(s_, take(C, Tv))
+            return g.leaky_relu(s_, np.float32(0.1))
+        out.append((cfg, "conv tail: cont(transpose)+bias->leaky [%d,%d]" % (C, Tv), 8 * n + 4 * C, tail))
+        out.append((cfg, "conv tail: cont(transpose)+bias+residual->leaky, sum [%d,%d]" % (C, Tv), 16 * n + 4 * C,
+                    lambda g, tail=tail: tail(g, resid=True)))
     return out
 
 

@@ -334,6 +334,31 @@ shp_status_t shp_sqr(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
 shp_status_t shp_cpy(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
 
 /*
+ * The tail of the time-major vocoder convolution, in one pass
+ * (vits/waveform-decoder.cpp:111,118-121, then :147,150 or the next layer's
+ * :146): s = ggml_add(ggml_cont(ggml_transpose(out)), reshape_2d(bias, 1, C)),
+ * then s = ggml_add(s, r) when r is given, then y = ggml_leaky_relu(s, slope)
+ * when apply_leaky (sum, if given, receives s), else y = s (sum must be NULL).
+ * Each add is one f32 rounding, in that order, so y and sum are bit-identical
+ * to the nodes one by one.
+ *   x:   an F32 transposed or permuted view as shp_cpy takes it
+ *   b:   F32 [1, ne1, ne2, ne3]: one value per row of y, rows evenly strided
+ *   r:   NULL or F32 of y's shape and strides (the residual)
+ *   sum: NULL or F32 of y's shape and strides
+ *   y:   F32 of x's shape, rows contiguous
+ * Replaces the CPY, ADD(, ADD)(, LEAKY_RELU) nodes of that tail; no
+ * counterpart entry point in the reference (ggml runs them as nodes).
+ */
+shp_status_t shp_cont_add_leaky_relu(const shp_tensor * x,
+                                     const shp_tensor * b,
+                                     const shp_tensor * r,
+                                     int32_t            apply_leaky,
+                                     float              slope,
+                                     shp_tensor *       sum,
+                                     shp_tensor *       y,
+                                     shp_stream_t       stream);
+
+/*
  * The non-GEMM node runs of one Qwen3 decoder layer,
  * src/arch/qwen3-tts/operations.cpp:84-147, in the layer's order. The
  * layer's matrix products and its attention run between these node runs in

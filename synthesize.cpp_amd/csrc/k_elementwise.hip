@@ -1115,17 +1115,34 @@ struct TransposeArgs {
     FastDiv      na;    // extent of dim a
     uint32_t     ntiles;
     uint32_t     pad;
+    // epilogue (shp_cont_add_leaky_relu)
+    const char * bias;   // one value per destination row, at row number * brs
+    int64_t      brs;
+    int64_t      rowk;   // destination row number per unit of dims k, a, b
+    int64_t      rowa;
+    int64_t      rowb;
+    int64_t      rdelta;  // residual address - destination address (same layout)
+    int64_t      sdelta;  // sum address - destination address (same layout)
+    float        slope;
+    int32_t      pad2;
 };
 
 constexpr int kTile0 = 64;
 constexpr int kTileK = 128;
 
+// Epilogue bits: add the destination row's bias value, then the residual (a
+// second rounding, in the node order), write that sum, apply leaky-ReLU.
+enum TransposeEpi { kEpiBias = 1, kEpiResid = 2, kEpiLeaky = 4, kEpiSum = 8 };
+
 // One tile: loads into registers, LDS, stores. FULL = the tile lies wholly
 // inside the tensor: no guards, so each load's data goes to LDS as it arrives
-// and the LDS reads of two passes issue before their stores.
-template <int V, bool FULL>
-__device__ __forceinline__ void transpose_tile(float (&tile)[kTile0][kTileK + 1], const char * xb, char * yb,
-                                               int64_t xnb0, int64_t ynbk, int n0, int nk) {
+// and the LDS reads of two passes issue before their stores. The epilogue's
+// bias values and residual rows are requested with the tile's loads, before
+// the barrier.
+template <int V, bool FULL, int EPI>
+__device__ __forceinline__ void transpose_tile(float (&tile)[kTile0][kTileK + 1], float (&s_bias)[kTileK],
+                                               const TransposeArgs & a, const char * xb, char * yb, int64_t row0,
+                                               int n0, int nk) {
     typedef float vec __attribute__((ext_vector_type(V)));
     constexpr int RL = kTileK / V, RLINES = 256 / RL, RPASS = kTile0 / RLINES;  // loads: lines along dim k
     constexpr int WL = kTile0 / V, WLINES = 256 / WL, WPASS = kTileK / WLINES;  // stores: lines along dim 0
@@ -1136,9 +1153,29 @@ __device__ __forceinline__ void transpose_tile(float (&tile)[kTile0][kTileK + 1]
     for (int p = 0; p < RPASS; ++p) {
         const int r = rl + p * RLINES;
         if (FULL || (r < n0 && rc < nk)) {
-            v[p] = __builtin_nontemporal_load(reinterpret_cast<const vec *>(xb + static_cast<int64_t>(r) * xnb0 + rc * 4));
+            v[p] = __builtin_nontemporal_load(reinterpret_cast<const vec *>(xb + static_cast<int64_t>(r) * a.xnb0 + rc * 4));
         } else {
             v[p] = vec{};
+        }
+    }
+    // The tile's 128 destination lines take one bias value each: one load per
+    // line into LDS (8 loads per lane otherwise: measured 3-9 % slower).
+    if constexpr ((EPI & kEpiBias) != 0) {
+        const int r = static_cast<int>(threadIdx.x);
+        if (r < kTileK) {
+            const int rr = r < nk ? r : 0;  // a line past the tensor reads line 0's value, unused
+            s_bias[r]    = *reinterpret_cast<const float *>(a.bias + (row0 + rr * a.rowk) * a.brs);
+        }
+    }
+    vec rv[WPASS];
+#pragma unroll
+    for (int p = 0; p < WPASS; ++p) {
+        const int  r  = wl + p * WLINES;  // ik local
+        const bool in = FULL || (r < nk && wc < n0);
+        if constexpr ((EPI & kEpiResid) != 0) {
+            rv[p] = in ? __builtin_nontemporal_load(
+                             reinterpret_cast<const vec *>(yb + a.rdelta + static_cast<int64_t>(r) * a.ynbk + wc * 4)) :
+                         vec{};
         }
     }
 #pragma unroll
@@ -1151,49 +1188,84 @@ __device__ __forceinline__ void transpose_tile(float (&tile)[kTile0][kTileK + 1]
     __syncthreads();
 #pragma unroll
     for (int p = 0; p < WPASS; ++p) {
-        const int r = wl + p * WLINES;  // ik local
-        vec       w;
+        const int   r  = wl + p * WLINES;  // ik local
+        const float bv = (EPI & kEpiBias) != 0 ? s_bias[r] : 0.0f;
+        vec         w;
 #pragma unroll
         for (int e = 0; e < V; ++e) {
             w[e] = tile[wc + e][r];
+            if constexpr ((EPI & kEpiBias) != 0) {
+                w[e] = w[e] + bv;
+            }
+            if constexpr ((EPI & kEpiResid) != 0) {
+                w[e] = w[e] + rv[p][e];
+            }
         }
         if (FULL || (r < nk && wc < n0)) {
-            __builtin_nontemporal_store(w, reinterpret_cast<vec *>(yb + static_cast<int64_t>(r) * ynbk + wc * 4));
+            char * yo = yb + static_cast<int64_t>(r) * a.ynbk + wc * 4;
+            if constexpr ((EPI & kEpiSum) != 0) {
+                __builtin_nontemporal_store(w, reinterpret_cast<vec *>(yo + a.sdelta));
+            }
+            if constexpr ((EPI & kEpiLeaky) != 0) {
+#pragma unroll
+                for (int e = 0; e < V; ++e) {
+                    w[e] = leaky(w[e], a.slope);
+                }
+            }
+            __builtin_nontemporal_store(w, reinterpret_cast<vec *>(yo));
         }
     }
     __syncthreads();
 }
 
-template <int V> __global__ __launch_bounds__(256) void k_transpose_tiles(const TransposeArgs a) {
+template <int V, int EPI> __global__ __launch_bounds__(256) void k_transpose_tiles(const TransposeArgs a) {
     __shared__ float tile[kTile0][kTileK + 1];  // [i0 local][ik local]; the pad staggers a column's banks
+    __shared__ float s_bias[kTileK];              // the epilogue's bias value per destination line
     for (uint32_t t = blockIdx.x; t < a.ntiles; t += gridDim.x) {
-        const uint32_t q0 = fastdiv(t, a.tk);
-        const uint32_t q1 = fastdiv(q0, a.t0);
-        const uint32_t ib = fastdiv(q1, a.na);
-        const int64_t  ik = static_cast<int64_t>(t - q0 * a.tk.d) * kTileK;
-        const int64_t  i0 = static_cast<int64_t>(q0 - q1 * a.t0.d) * kTile0;
-        const int64_t  ia = q1 - ib * a.na.d;
-        const char *   xb = a.x + i0 * a.xnb0 + ik * 4 + ia * a.xnba + ib * a.xnbb;
-        char *         yb = a.y + i0 * 4 + ik * a.ynbk + ia * a.ynba + ib * a.ynbb;
-        const int      n0 = static_cast<int>(a.ne0 - i0 < kTile0 ? a.ne0 - i0 : kTile0);
-        const int      nk = static_cast<int>(a.nek - ik < kTileK ? a.nek - ik : kTileK);
+        const uint32_t q0   = fastdiv(t, a.tk);
+        const uint32_t q1   = fastdiv(q0, a.t0);
+        const uint32_t ib   = fastdiv(q1, a.na);
+        const int64_t  ik   = static_cast<int64_t>(t - q0 * a.tk.d) * kTileK;
+        const int64_t  i0   = static_cast<int64_t>(q0 - q1 * a.t0.d) * kTile0;
+        const int64_t  ia   = q1 - ib * a.na.d;
+        const char *   xb   = a.x + i0 * a.xnb0 + ik * 4 + ia * a.xnba + ib * a.xnbb;
+        char *         yb   = a.y + i0 * 4 + ik * a.ynbk + ia * a.ynba + ib * a.ynbb;
+        const int64_t  row0 = ik * a.rowk + ia * a.rowa + ib * a.rowb;  // destination row number at ik
+        const int      n0   = static_cast<int>(a.ne0 - i0 < kTile0 ? a.ne0 - i0 : kTile0);
+        const int      nk   = static_cast<int>(a.nek - ik < kTileK ? a.nek - ik : kTileK);
         if (n0 == kTile0 && nk == kTileK) {
-            transpose_tile<V, true>(tile, xb, yb, a.xnb0, a.ynbk, n0, nk);
+            transpose_tile<V, true, EPI>(tile, s_bias, a, xb, yb, row0, n0, nk);
         } else {
-            transpose_tile<V, false>(tile, xb, yb, a.xnb0, a.ynbk, n0, nk);
+            transpose_tile<V, false, EPI>(tile, s_bias, a, xb, yb, row0, n0, nk);
         }
     }
 }
 
-// Plans the transposing copy; SHP_ERR_UNSUPPORTED when x has no contiguous
-// dimension or the tile count passes 2^31.
-shp_status_t transpose_entry(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
+// The transposing copy's plan: dims, tiles, strides, and whether 16-byte
+// accesses apply (every line start on both sides 16-byte aligned and both tile
+// extents multiples of 4; the stride of a dimension of extent 1 is never
+// used). SHP_ERR_UNSUPPORTED when x has no contiguous dimension or the tile
+// count passes 2^31.
+struct TransposePlan {
+    TransposeArgs args{};
+    bool          v4    = false;
+    unsigned      grid  = 0;
+    int           k     = 0;
+    int           da    = 0;
+    int           db    = 0;
+};
+
+shp_status_t plan_transpose(const shp_tensor * x, const shp_tensor * y, TransposePlan & pl) {
     const int k = f32_strided_view_dim(x);
     if (k == 0 || !well_formed(y) || y->type != SHP_TYPE_F32) {
         return SHP_ERR_UNSUPPORTED;
     }
     if (!same_shape(*x, *y)) {
         return SHP_ERR_INVALID_ARG;
+    }
+    // A tile's stores land where other tiles still read: y must not overlap x.
+    if (spans_overlap(*x, *y)) {
+        return SHP_ERR_UNSUPPORTED;
     }
     int dims[2], n = 0;
     for (int d = 1; d < 4; ++d) {
@@ -1207,40 +1279,54 @@ shp_status_t transpose_entry(const shp_tensor * x, shp_tensor * y, shp_stream_t 
     if (t0 > INT32_MAX || tk > INT32_MAX || nt > INT32_MAX) {
         return SHP_ERR_UNSUPPORTED;
     }
-    if (dry_run()) {
-        return SHP_OK;
-    }
-    TransposeArgs a{};
-    a.x      = static_cast<const char *>(x->data);
-    a.y      = static_cast<char *>(y->data);
-    a.xnb0   = static_cast<int64_t>(x->nb[0]);
-    a.xnba   = static_cast<int64_t>(x->nb[dims[0]]);
-    a.xnbb   = static_cast<int64_t>(x->nb[dims[1]]);
-    a.ynbk   = static_cast<int64_t>(y->nb[k]);
-    a.ynba   = static_cast<int64_t>(y->nb[dims[0]]);
-    a.ynbb   = static_cast<int64_t>(y->nb[dims[1]]);
-    a.ne0    = x->ne[0];
-    a.nek    = x->ne[k];
-    a.t0     = make_fastdiv(static_cast<uint32_t>(t0));
-    a.tk     = make_fastdiv(static_cast<uint32_t>(tk));
-    a.na     = make_fastdiv(static_cast<uint32_t>(x->ne[dims[0]]));
-    a.ntiles = static_cast<uint32_t>(nt);
-    // 16-byte accesses need every line start on both sides 16-byte aligned and
-    // both tile extents multiples of 4 (the stride of a dimension of extent 1
-    // is never used).
-    const auto a16 = [](int64_t ne, int64_t nb) { return ne == 1 || nb % 16 == 0; };
+    TransposeArgs & a = pl.args;
+    a.x               = static_cast<const char *>(x->data);
+    a.y               = static_cast<char *>(y->data);
+    a.xnb0            = static_cast<int64_t>(x->nb[0]);
+    a.xnba            = static_cast<int64_t>(x->nb[dims[0]]);
+    a.xnbb            = static_cast<int64_t>(x->nb[dims[1]]);
+    a.ynbk            = static_cast<int64_t>(y->nb[k]);
+    a.ynba            = static_cast<int64_t>(y->nb[dims[0]]);
+    a.ynbb            = static_cast<int64_t>(y->nb[dims[1]]);
+    a.ne0             = x->ne[0];
+    a.nek             = x->ne[k];
+    a.t0              = make_fastdiv(static_cast<uint32_t>(t0));
+    a.tk              = make_fastdiv(static_cast<uint32_t>(tk));
+    a.na              = make_fastdiv(static_cast<uint32_t>(x->ne[dims[0]]));
+    a.ntiles          = static_cast<uint32_t>(nt);
+    const int64_t rownum[4] = { 0, 1, y->ne[1], y->ne[1] * y->ne[2] };  // row number per unit of dims 1..3
+    a.rowk                  = rownum[k];
+    a.rowa                  = rownum[dims[0]];
+    a.rowb                  = rownum[dims[1]];
+    const auto    a16 = [](int64_t ne, int64_t nb) { return ne == 1 || nb % 16 == 0; };
     const int64_t nea = x->ne[dims[0]], neb = x->ne[dims[1]];
-    const bool    v4  = reinterpret_cast<uintptr_t>(x->data) % 16 == 0 &&
-                    reinterpret_cast<uintptr_t>(y->data) % 16 == 0 && a16(a.ne0, a.xnb0) && a16(nea, a.xnba) &&
-                    a16(neb, a.xnbb) && a16(a.nek, a.ynbk) && a16(nea, a.ynba) && a16(neb, a.ynbb) &&
-                    a.ne0 % 4 == 0 && a.nek % 4 == 0;
-    const unsigned grid = static_cast<unsigned>(nt < (1 << 20) ? nt : (1 << 20));
-    if (v4) {
-        hipLaunchKernelGGL((k_transpose_tiles<4>), dim3(grid), dim3(256), 0, as_stream(stream), a);
+    pl.v4             = reinterpret_cast<uintptr_t>(x->data) % 16 == 0 &&
+             reinterpret_cast<uintptr_t>(y->data) % 16 == 0 && a16(a.ne0, a.xnb0) && a16(nea, a.xnba) &&
+             a16(neb, a.xnbb) && a16(a.nek, a.ynbk) && a16(nea, a.ynba) && a16(neb, a.ynbb) && a.ne0 % 4 == 0 &&
+             a.nek % 4 == 0;
+    pl.grid = static_cast<unsigned>(nt < (1 << 20) ? nt : (1 << 20));
+    pl.k    = k;
+    pl.da   = dims[0];
+    pl.db   = dims[1];
+    return SHP_OK;
+}
+
+template <int EPI> shp_status_t launch_transpose(const TransposePlan & pl, hipStream_t stream) {
+    if (pl.v4) {
+        hipLaunchKernelGGL((k_transpose_tiles<4, EPI>), dim3(pl.grid), dim3(256), 0, stream, pl.args);
     } else {
-        hipLaunchKernelGGL((k_transpose_tiles<1>), dim3(grid), dim3(256), 0, as_stream(stream), a);
+        hipLaunchKernelGGL((k_transpose_tiles<1, EPI>), dim3(pl.grid), dim3(256), 0, stream, pl.args);
     }
     return launch_status();
+}
+
+shp_status_t transpose_entry(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
+    TransposePlan      pl;
+    const shp_status_t st = plan_transpose(x, y, pl);
+    if (st != SHP_OK || dry_run()) {
+        return st;
+    }
+    return launch_transpose<0>(pl, as_stream(stream));
 }
 
 }  // namespace
@@ -1301,6 +1387,82 @@ extern "C" shp_status_t shp_cpy(const shp_tensor * x, shp_tensor * y, shp_stream
                            as_stream(stream), a);
     }
     return launch_status();
+}
+
+extern "C" shp_status_t shp_cont_add_leaky_relu(const shp_tensor * x,
+                                                const shp_tensor * b,
+                                                const shp_tensor * r,
+                                                int32_t            apply_leaky,
+                                                float              slope,
+                                                shp_tensor *       sum,
+                                                shp_tensor *       y,
+                                                shp_stream_t       stream) {
+    if (b == nullptr || !well_formed(b) || !well_formed(y) || (r != nullptr && !well_formed(r)) ||
+        (sum != nullptr && !well_formed(sum)) || (sum != nullptr && !apply_leaky)) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    if (b->type != SHP_TYPE_F32 || (r != nullptr && r->type != SHP_TYPE_F32) ||
+        (sum != nullptr && sum->type != SHP_TYPE_F32)) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    TransposePlan      pl;
+    const shp_status_t st = plan_transpose(x, y, pl);
+    if (st != SHP_OK) {
+        return st;
+    }
+    // b: one value per row of y, b's rows one for one at a fixed stride
+    // (ggml_add(cont, reshape_2d(bias, 1, C)), vits/waveform-decoder.cpp:118-121);
+    // r and sum: y's shape and strides (the residual and the add's result).
+    const RowMap bm = make_rowmap(*b);
+    if (b->ne[0] != 1 || b->ne[1] != y->ne[1] || b->ne[2] != y->ne[2] || b->ne[3] != y->ne[3] || !bm.flat) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    const auto same_layout = [y](const shp_tensor * t) {
+        return same_shape(*t, *y) && t->nb[1] == y->nb[1] && t->nb[2] == y->nb[2] && t->nb[3] == y->nb[3];
+    };
+    if ((r != nullptr && !same_layout(r)) || (sum != nullptr && !same_layout(sum))) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    // Each element of r is read by the lane that writes that element of y and
+    // sum, so r may be y or sum itself (an in-place add); any other overlap
+    // among x, r, sum and y is refused.
+    const auto apart = [](const shp_tensor * p, const shp_tensor * q) {
+        return p == nullptr || q == nullptr || !spans_overlap(*p, *q);
+    };
+    if (!apart(x, r) || !apart(x, sum) || (sum != nullptr && !apart(sum, y)) ||
+        (r != nullptr && r->data != y->data && !apart(r, y)) ||
+        (r != nullptr && sum != nullptr && r->data != sum->data && !apart(r, sum))) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    if ((r != nullptr && reinterpret_cast<uintptr_t>(r->data) % 16 != 0) ||
+        (sum != nullptr && reinterpret_cast<uintptr_t>(sum->data) % 16 != 0)) {
+        pl.v4 = false;
+    }
+    if (dry_run()) {
+        return SHP_OK;
+    }
+    TransposeArgs & a = pl.args;
+    a.bias            = static_cast<const char *>(b->data);
+    a.brs             = bm.rs;
+    a.slope           = slope;
+    a.rdelta          = r != nullptr ? static_cast<const char *>(r->data) - static_cast<const char *>(y->data) : 0;
+    a.sdelta          = sum != nullptr ? static_cast<const char *>(sum->data) - static_cast<const char *>(y->data) : 0;
+    const hipStream_t ss = as_stream(stream);
+    const int epi = kEpiBias | (r != nullptr ? kEpiResid : 0) | (apply_leaky ? kEpiLeaky : 0) | (sum != nullptr ? kEpiSum : 0);
+    switch (epi) {
+        case kEpiBias:
+            return launch_transpose<kEpiBias>(pl, ss);
+        case kEpiBias | kEpiLeaky:
+            return launch_transpose<kEpiBias | kEpiLeaky>(pl, ss);
+        case kEpiBias | kEpiLeaky | kEpiSum:
+            return launch_transpose<kEpiBias | kEpiLeaky | kEpiSum>(pl, ss);
+        case kEpiBias | kEpiResid:
+            return launch_transpose<kEpiBias | kEpiResid>(pl, ss);
+        case kEpiBias | kEpiResid | kEpiLeaky:
+            return launch_transpose<kEpiBias | kEpiResid | kEpiLeaky>(pl, ss);
+        default:
+            return launch_transpose<kEpiBias | kEpiResid | kEpiLeaky | kEpiSum>(pl, ss);
+    }
 }
 
 extern "C" shp_status_t shp_exp(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {

@@ -323,13 +323,9 @@ class Planner {
     // element (of its last row, for a block type). A strided view's ne[0]
     // counts through nb[0].
     static Span extent(const shp_tensor & t) {
-        size_t end = block_type(t.type) ? row_bytes(t.type, t.ne[0]) :
-                                          type_size(t.type) + static_cast<size_t>(t.ne[0] - 1) * t.nb[0];
-        for (int d = 1; d < 4; ++d) {
-            end += static_cast<size_t>(t.ne[d] - 1) * t.nb[d];
-        }
-        const uintptr_t lo = reinterpret_cast<uintptr_t>(t.data);
-        return { lo, lo + end };
+        Span sp;
+        byte_span(t, sp.lo, sp.hi);
+        return sp;
     }
 
     static bool overlaps(const Span & a, const std::vector<Span> & bs) {
@@ -653,6 +649,8 @@ class Planner {
                 return 0;
             case SHP_NODE_SILU:
                 return match_silu_mul(p, l);
+            case SHP_NODE_CPY:
+                return match_cont_tail(p, l);
             default:
                 return 0;
         }
@@ -1041,6 +1039,65 @@ class Planner {
         return 2;
     }
 
+    // The tail of the time-major vocoder convolution (vits/waveform-decoder.cpp:
+    // 111,118-121 and what follows it, :146-150): CPY of the GEMM output's
+    // transposed view, ADD(copy, bias) with the bias as src1, then
+    // optionally ADD(sum, residual) (either operand order) and LEAKY_RELU of
+    // the last sum. The copy's result is never written and must be read by
+    // the bias add alone; the biased value is written only when no residual
+    // add follows and something outside reads it (as the run's sum).
+    int match_cont_tail(size_t p, Launch & l) const {
+        const int cp = at(p, 0);
+        const int ab = at(p, 1);
+        if (!is(cp, SHP_NODE_CPY) || !is(ab, SHP_NODE_ADD) || src(ab, 0) != cp || src(ab, 1) == cp) {
+            return 0;
+        }
+        const shp_node & C = nodes_[cp];
+        const shp_node & A = nodes_[ab];
+        if (f32_strided_view_dim(&C.src[0]) == 0 || !f32_of(C.dst) || !same_shape(C.src[0], C.dst) ||
+            !f32_of(A.dst) || !same_shape(A.dst, C.dst) || !f32_of(A.src[1])) {
+            return 0;
+        }
+        // optional residual add at position 2
+        const int ar    = at(p, 2);
+        int       other = -1;
+        if (is(ar, SHP_NODE_ADD) && (src(ar, 0) == ab) != (src(ar, 1) == ab)) {
+            other               = src(ar, 0) == ab ? 1 : 0;
+            const shp_node & R2 = nodes_[ar];
+            if (!f32_of(R2.src[other]) || !same_shape(R2.src[other], A.dst) || !f32_of(R2.dst) ||
+                !same_shape(R2.dst, A.dst)) {
+                other = -1;
+            }
+        }
+        for (int with_r = other >= 0 ? 1 : 0; with_r >= 0; --with_r) {
+            const int last = with_r ? ar : ab;
+            const int lk   = at(p, with_r ? 3 : 2);
+            for (int with_l = (is(lk, SHP_NODE_LEAKY_RELU) && src(lk, 0) == last && unary_ok(nodes_[lk])) ? 1 : 0;
+                 with_l >= 0; --with_l) {
+                Members members{ cp, ab };
+                if (with_r) {
+                    members.push(ar);
+                }
+                if (with_l) {
+                    members.push(lk);
+                }
+                if (!internal(cp, members) || (with_r && !internal(ab, members))) {
+                    continue;
+                }
+                l.kind = SHP_RUN_CONT_ADD_LEAKY;
+                l.x    = &C.src[0];
+                l.b    = &A.src[1];
+                l.x3   = with_r ? &nodes_[ar].src[other] : nullptr;
+                l.i0   = with_l;
+                l.f0   = with_l ? fparam(nodes_[lk], 0) : 0.0f;
+                l.sum  = with_l && needed_outside(last, members) ? const_cast<shp_tensor *>(&nodes_[last].dst) : nullptr;
+                l.y    = const_cast<shp_tensor *>(&nodes_[with_l ? lk : last].dst);
+                return members.n;
+            }
+        }
+        return 0;
+    }
+
     // SILU(g) then MUL(silu, u) (either operand order: the product commutes).
     int match_silu_mul(size_t p, Launch & l) const {
         const int si = at(p, 0);
@@ -1148,6 +1205,8 @@ shp_status_t launch_run(const Planner & pl, const Launch & l, shp_stream_t st) {
         case SHP_RUN_QK_NORM_ROPE_KV:
             // the copies' destinations are the cache views themselves (filled 0)
             return shp_qk_norm_rope_kv(l.x, l.x2, l.x3, l.w, l.w2, l.f0, l.b, l.i0, l.f1, l.f2, l.y, l.y2, l.y3, 0, st);
+        case SHP_RUN_CONT_ADD_LEAKY:
+            return shp_cont_add_leaky_relu(l.x, l.b, l.x3, l.i0, l.f0, l.sum, l.y, st);
         default:
             return SHP_ERR_UNSUPPORTED;
     }

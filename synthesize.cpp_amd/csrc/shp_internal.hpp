@@ -408,6 +408,25 @@ inline bool can_repeat(const shp_tensor & b, const shp_tensor & a) {
     return true;
 }
 
+// [lo, hi) of the bytes a descriptor can address: from data to the end of its
+// last element (its last row, for a block type).
+inline void byte_span(const shp_tensor & t, uintptr_t & lo, uintptr_t & hi) {
+    size_t end = block_type(t.type) ? row_bytes(t.type, t.ne[0]) :
+                                      type_size(t.type) + static_cast<size_t>(t.ne[0] - 1) * t.nb[0];
+    for (int d = 1; d < 4; ++d) {
+        end += static_cast<size_t>(t.ne[d] - 1) * t.nb[d];
+    }
+    lo = reinterpret_cast<uintptr_t>(t.data);
+    hi = lo + end;
+}
+
+inline bool spans_overlap(const shp_tensor & a, const shp_tensor & b) {
+    uintptr_t alo, ahi, blo, bhi;
+    byte_span(a, alo, ahi);
+    byte_span(b, blo, bhi);
+    return alo < bhi && blo < ahi;
+}
+
 inline RowMap make_rowmap(const shp_tensor & t) {
     RowMap m{};
     m.ne1  = t.ne[1];

@@ -90,6 +90,7 @@ def load(path=None):
         "shp_sin": [_PT, _PT, vp],
         "shp_sqr": [_PT, _PT, vp],
         "shp_cpy": [_PT, _PT, vp],
+        "shp_cont_add_leaky_relu": [_PT, _PT, _PT, i32, f, _PT, _PT, vp],
         "shp_graph_compute": [ctypes.POINTER(ShpNode), i32, vp],
         "shp_graph_plan": [ctypes.POINTER(ShpNode), i32, ctypes.POINTER(ShpGraphRun), i32, ctypes.POINTER(i32)],
     }
@@ -461,6 +462,19 @@ def sqr(x, out=None):
     return out
 
 
+def cont_add_leaky_relu(x, b, r=None, slope=None, out=None, sum_out=None):
+    """s = ggml_cont(x) + b (+ r), y = leaky_relu(s, slope) when slope is not
+    None (sum_out receives s), else y = s; x a transposed F32 view, b one
+    value per row of y. Returns y."""
+    import torch
+    out = torch.empty(x.shape, dtype=torch.float32, device=x.device) if out is None else out
+    leaky = slope is not None
+    _check(load().shp_cont_add_leaky_relu(_ref(desc(x)), _ref(desc(b)), _ref(desc(r)), int(leaky),
+                                          float(slope if leaky else 0.0), _ref(desc(sum_out)), _ref(desc(out)),
+                                          _stream()), "cont_add_leaky_relu")
+    return out
+
+
 def cpy(x, out=None):
     """ggml_cpy / ggml_cast into F32 of x's shape (x F32, F16 or BF16)."""
     import torch
@@ -478,7 +492,7 @@ def cpy(x, out=None):
 NODE_FLAG_OUTPUT = 1
 RUN_KINDS = {-1: "unsupported", 0: "nop", 1: "single", 2: "norm_mul", 3: "norm_mul_rope", 4: "add_norm_mul",
              5: "silu_mul", 6: "add_leaky", 7: "add_scale_leaky", 8: "snake", 9: "snake_guarded", 10: "snake_beta",
-             11: "gather_sum", 12: "qk_norm_rope", 13: "qk_norm_rope_kv"}
+             11: "gather_sum", 12: "qk_norm_rope", 13: "qk_norm_rope_kv", 14: "cont_add_leaky"}
 
 
 class ShpNode(ctypes.Structure):

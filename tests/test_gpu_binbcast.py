@@ -78,8 +78,9 @@ def test_repeat_large_time_major_bias(gpu):
 def test_repeat_in_a_node_list(gpu):
     """conv1d_time_major's tail (vits/waveform-decoder.cpp:111,118-121): the
     transposing copy of the convolution's output, then the [1, C] bias add,
-    then the next leaky-ReLU; every node alone, the list equal to the
-    restatement."""
+    then the next leaky-ReLU, as one launch (the biased value written, being
+    an output too), equal to the restatement; and with the copy read
+    elsewhere, every node alone."""
     rng = np.random.default_rng(SEED + 11)
     out = rng.standard_normal((2048, 96)).astype(np.float32)   # ggml [C_out=96, T=2048] (GEMM output)
     bias = rng.standard_normal((96, 1)).astype(np.float32)      # ggml [1, 96]
@@ -89,7 +90,19 @@ def test_repeat_in_a_node_list(gpu):
     biased = g.add(tm, _t(gpu, bias))
     act = g.leaky_relu(biased, 0.1)
     kinds = [k for k, *_ in g.plan(biased, act) if k != "nop"]
-    assert kinds == ["single", "single", "single"], kinds
+    assert kinds == ["cont_add_leaky"], kinds
     g.compute(biased, act)
     ref = _oracle(R.OP_ADD, np.ascontiguousarray(out.T), bias)
     assert_bitexact(_np(biased.t), ref)
+    lk = R.Graph()
+    ref_act = lk.leaky_relu(ref, 0.1)
+    lk.compute(1)
+    assert_bitexact(_np(act.t), ref_act)
+    g = gpu.Graph()
+    tm = g.cont(g.view(to, to.t()))
+    biased = g.add(tm, _t(gpu, bias))
+    kinds = [k for k, *_ in g.plan(biased, tm) if k != "nop"]
+    assert kinds == ["single", "single"], kinds
+    g.compute(biased, tm)
+    assert_bitexact(_np(biased.t), ref)
+    assert_bitexact(_np(tm.t), np.ascontiguousarray(out.T))

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import ggml_ref as R
-from test_gpu_parity import _np, assert_bitexact
+from test_gpu_parity import _np, _t, assert_bitexact
 
 pytestmark = pytest.mark.gpu
 SEED = 20261202
@@ -118,3 +118,109 @@ def test_transposed_copy_in_a_node_list(gpu):
     assert kinds == ["single", "single", "single"], kinds
     g.compute(act, out)
     assert_bitexact(_np(tm.t), np.ascontiguousarray(_np(act.t).T))
+
+
+def _oracle_tail(out, bias, r, slope):
+    """The restatement of the tail node by node: ggml_cont of out^T, the
+    [1, C] bias add, the residual add, the leaky-ReLU. out: numpy (T, C) =
+    ggml [C, T]; bias (C, 1); r (C, T) or None. Returns (sum, y)."""
+    g = R.Graph()
+    T, C = out.shape
+    tm = g.cont_f32(out, [T, C], [4 * C, 4])
+    s = g.binbcast(R.OP_ADD, tm.reshape(C, T), bias)
+    if r is not None:
+        s = g.add(s, r)
+    y = g.leaky_relu(s, slope) if slope is not None else s
+    g.compute(8)
+    return s.reshape(C, T), y.reshape(C, T)
+
+
+TAIL_SHAPES = [(2048, 96), (4096, 512), (1000, 37), (130, 64)]
+
+
+@pytest.mark.parametrize("T,C", TAIL_SHAPES)
+@pytest.mark.parametrize("resid,leaky,with_sum", [(False, False, False), (False, True, False), (False, True, True),
+                                                  (True, False, False), (True, True, False), (True, True, True)])
+def test_cont_add_leaky_matches_nodes(gpu, T, C, resid, leaky, with_sum):
+    """shp_cont_add_leaky_relu against the restatement's nodes one by one,
+    bit-exact, for every form (vits/waveform-decoder.cpp:111,118-121,146-150)."""
+    import torch
+    rng = np.random.default_rng(SEED + T + C + 7 * resid + 3 * leaky + with_sum)
+    out = rng.standard_normal((T, C)).astype(np.float32)
+    bias = rng.standard_normal((C, 1)).astype(np.float32)
+    r = rng.standard_normal((C, T)).astype(np.float32) if resid else None
+    slope = 0.1 if leaky else None
+    to = _t(gpu, out)
+    s_out = torch.empty((C, T), dtype=torch.float32, device="cuda") if with_sum else None
+    print("tail", T, C, resid, leaky, with_sum, flush=True)
+    y = gpu.cont_add_leaky_relu(to.t(), _t(gpu, bias), _t(gpu, r) if resid else None, slope, sum_out=s_out)
+    ref_s, ref_y = _oracle_tail(out, bias, r, slope)
+    assert_bitexact(_np(y), ref_y)
+    if with_sum:
+        assert_bitexact(_np(s_out), ref_s)
+
+
+def test_cont_add_leaky_in_place_residual_and_unaligned(gpu):
+    """The residual's buffer reused for the sum (ggml's in-place add), and a
+    source view 1 float off a 16-byte boundary (dword path)."""
+    import torch
+    rng = np.random.default_rng(SEED + 91)
+    T, C = 1024, 64
+    out = rng.standard_normal((T, C + 1)).astype(np.float32)
+    bias = rng.standard_normal((C, 1)).astype(np.float32)
+    r = rng.standard_normal((C, T)).astype(np.float32)
+    to = _t(gpu, out)
+    tr = _t(gpu, r)
+    view = to[:, 1:].t()                                  # ggml [T, C], rows 1 float in
+    y = gpu.cont_add_leaky_relu(view, _t(gpu, bias), tr, 0.2, sum_out=tr)
+    ref_s, ref_y = _oracle_tail(np.ascontiguousarray(out[:, 1:]), bias, r, 0.2)
+    assert_bitexact(_np(y), ref_y)
+    assert_bitexact(_np(tr), ref_s)
+
+
+def test_transposing_copy_refuses_an_overlapping_destination(gpu):
+    """A destination overlapping the transposed source would be read after
+    being written by another tile: refused, nothing launched."""
+    import torch
+    x = torch.zeros((64, 64), dtype=torch.float32, device="cuda")
+    with pytest.raises(gpu.ShpError):
+        gpu.cpy(x.t(), x)
+    with pytest.raises(gpu.ShpError):
+        gpu.cont_add_leaky_relu(x.t(), torch.zeros((64, 1), device="cuda"), None, 0.1, out=x)
+
+
+def test_conv_tail_in_a_node_list(gpu):
+    """Two resblock convolutions' tails in one list (:146-150): copy, bias,
+    leaky into the next GEMM's input; copy, bias, residual add, the next
+    layer's leaky with the sum carried. Two launches, bit-identical to the
+    list run with every result written, and to the restatement."""
+    import torch
+    rng = np.random.default_rng(SEED + 93)
+    T, C = 4096, 128
+    host = {n: rng.standard_normal(sh).astype(np.float32) for n, sh in
+            (("o1", (T, C)), ("o2", (T, C)), ("b1", (C, 1)), ("b2", (C, 1)), ("res", (C, T)))}
+    dev = {n: _t(gpu, a) for n, a in host.items()}
+
+    def build(every):
+        g = gpu.Graph()
+        t1 = g.cont(g.view(dev["o1"], dev["o1"].t()))
+        act = g.leaky_relu(g.add(t1, dev["b1"]), 0.1)
+        t2 = g.cont(g.view(dev["o2"], dev["o2"].t()))
+        state = g.add(g.add(t2, dev["b2"]), dev["res"])
+        nxt = g.leaky_relu(state, 0.1)
+        outs = [act, state, nxt]
+        return g, outs, (outs + [n["val"] for n in g.order(*outs)]) if every else outs
+
+    g, outs, every = build(False)
+    assert [k for k, *_ in g.plan(*every) if k != "nop"] == ["cont_add_leaky", "cont_add_leaky"]
+    g.compute(*every)
+    fused = [_np(o.t).copy() for o in outs]
+    g, outs, every = build(True)
+    assert "cont_add_leaky" not in [k for k, *_ in g.plan(*every)]  # every copy is written: no tail runs
+    g.compute(*every)
+    for a, b in zip(fused, [_np(o.t) for o in outs]):
+        assert_bitexact(a, b)
+    _, act = _oracle_tail(host["o1"], host["b1"], None, 0.1)
+    state, nxt = _oracle_tail(host["o2"], host["b2"], host["res"], 0.1)
+    for a, b in zip(fused, (act, state, nxt)):
+        assert_bitexact(a, b)

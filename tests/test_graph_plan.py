@@ -433,3 +433,48 @@ def test_repeated_operands_follow_ggml():
     bb = g.exp(g.view(lb, lb.reshape(-1, 1)))
     sq = g.sqr(g.sin(g.mul(xs, a)))
     assert "snake_beta" not in kinds(g.plan(g.add(xs, g.div(sq, g.scale_bias(bb, 1.0, 1e-9)))))
+
+
+def _conv_tail(g, T=64, C=16, residual=None, leaky=True, extra_read=None):
+    """conv1d_time_major's tail (vits/waveform-decoder.cpp:111,118-121) and
+    what follows it: the transposing copy of the GEMM output [C, T], the
+    [1, C] bias add, optionally the residual add (:150) and the next
+    leaky-ReLU (:146)."""
+    out = z(T, C)                       # ggml [C, T] (the GEMM's output)
+    tm = g.cont(g.view(out, out.t()))   # ggml [T, C]
+    s = g.add(tm, z(C, 1))              # + ggml [1, C]
+    if residual is not None:
+        s = g.add(s, residual)
+    y = g.leaky_relu(s, 0.1) if leaky else s
+    return tm, s, y
+
+
+def test_conv_tail_runs():
+    """The copy, the bias add, the residual add and the leaky-ReLU run as one
+    shp_cont_add_leaky_relu launch in each form the decoder emits; the
+    copy's result must be read by the bias add alone."""
+    T, C = 64, 16
+    for resid, leaky, n in ((False, True, 3), (True, True, 4), (True, False, 3), (False, False, 2)):
+        g = S.Graph()
+        r = z(C, T) if resid else None
+        tm, s, y = _conv_tail(g, T, C, r, leaky)
+        plan = g.plan(y)
+        assert kinds(plan) == ["cont_add_leaky"], (resid, leaky, kinds(plan))
+        assert [p[3] for p in plan if p[0] == "cont_add_leaky"] == [n]
+    # the sum read later (the next layer's residual): still one launch
+    g = S.Graph()
+    tm, s, y = _conv_tail(g, T, C, z(C, T), True)
+    assert kinds(g.plan(y, g.add(s, s))) == ["cont_add_leaky", "single"]
+    # the copy read elsewhere: it must be written, so the nodes run alone
+    g = S.Graph()
+    tm, s, y = _conv_tail(g, T, C, None, True)
+    assert kinds(g.plan(y, g.exp(tm))) == ["single", "single", "single", "single"]
+    # a plain (untransposed) copy is not this run
+    g = S.Graph()
+    x = z(C, T)
+    assert "cont_add_leaky" not in kinds(g.plan(g.leaky_relu(g.add(g.cont(x), z(C, 1)), 0.1)))
+    # a bias that is one row [T] instead of one value per row: the nodes alone
+    g = S.Graph()
+    out = z(T, C)
+    tm = g.cont(g.view(out, out.t()))
+    assert "cont_add_leaky" not in kinds(g.plan(g.leaky_relu(g.add(tm, z(T)), 0.1)))
