@@ -114,9 +114,11 @@ typedef enum shp_run_kind {
     SHP_RUN_GATHER_SUM,
     SHP_RUN_QK_NORM_ROPE,     /* q and k rope runs (the k sink may be a cache copy) */
     SHP_RUN_QK_NORM_ROPE_KV,  /* the same plus the v cache copy */
-    SHP_RUN_CONT_ADD_LEAKY    /* CPY of a transposed view, ADD of the per-row bias,
+    SHP_RUN_CONT_ADD_LEAKY,   /* CPY of a transposed view, ADD of the per-row bias,
                                  [ADD of a residual], [LEAKY_RELU]:
                                  shp_cont_add_leaky_relu */
+    SHP_RUN_VIEW_BINARY       /* CPY of a row-contiguous F32 view, then ADD, MUL or
+                                 DIV of the copy: the binary op reads the view */
 } shp_run_kind;
 
 typedef struct shp_graph_run {

@@ -650,7 +650,10 @@ class Planner {
             case SHP_NODE_SILU:
                 return match_silu_mul(p, l);
             case SHP_NODE_CPY:
-                return match_cont_tail(p, l);
+                if ((used = match_cont_tail(p, l)) != 0) {
+                    return used;
+                }
+                return match_view_binary(p, l);
             default:
                 return 0;
         }
@@ -1098,6 +1101,41 @@ class Planner {
         return 0;
     }
 
+    // CPY of a row-contiguous F32 view into a tensor of its shape, read only
+    // by an ADD, MUL or DIV as src0: the op reads the view in place of the
+    // copy, which is never written (the causal convolutions' crop, then their
+    // channel bias: qwen3-tts/codec.cpp:64-71,100-104,137-140). The copy is
+    // exact, so the result is the same bits.
+    int match_view_binary(size_t p, Launch & l) const {
+        const int cp = at(p, 0);
+        const int op = at(p, 1);
+        if (!is(cp, SHP_NODE_CPY) || !(is(op, SHP_NODE_ADD) || is(op, SHP_NODE_MUL) || is(op, SHP_NODE_DIV)) ||
+            src(op, 0) != cp || src(op, 1) == cp) {
+            return 0;
+        }
+        const shp_node & C = nodes_[cp];
+        const shp_node & B = nodes_[op];
+        // The op's result may sit in memory the copy's source gave up (the
+        // allocator reuses it once the copy has run): reading the view while
+        // writing it in another row stride would go wrong, so any overlap
+        // leaves the nodes apart.
+        if (!f32_of(C.src[0]) || !f32_of(C.dst) || !same_shape(C.src[0], C.dst) || !internal(cp, Members{ cp, op }) ||
+            spans_overlap(C.src[0], B.dst)) {
+            return 0;
+        }
+        shp_node n = B;  // the op with the view as src0
+        n.src[0]   = C.src[0];
+        if (!binary_ok(n)) {
+            return 0;
+        }
+        l.kind = SHP_RUN_VIEW_BINARY;
+        l.i0   = B.op;
+        l.x    = &C.src[0];
+        l.b    = &B.src[1];
+        l.y    = const_cast<shp_tensor *>(&B.dst);
+        return 2;
+    }
+
     // SILU(g) then MUL(silu, u) (either operand order: the product commutes).
     int match_silu_mul(size_t p, Launch & l) const {
         const int si = at(p, 0);
@@ -1207,6 +1245,10 @@ shp_status_t launch_run(const Planner & pl, const Launch & l, shp_stream_t st) {
             return shp_qk_norm_rope_kv(l.x, l.x2, l.x3, l.w, l.w2, l.f0, l.b, l.i0, l.f1, l.f2, l.y, l.y2, l.y3, 0, st);
         case SHP_RUN_CONT_ADD_LEAKY:
             return shp_cont_add_leaky_relu(l.x, l.b, l.x3, l.i0, l.f0, l.sum, l.y, st);
+        case SHP_RUN_VIEW_BINARY:
+            return l.i0 == SHP_NODE_ADD ? shp_add(l.x, l.b, l.y, st) :
+                   l.i0 == SHP_NODE_MUL ? shp_mul(l.x, l.b, l.y, st) :
+                                          shp_div(l.x, l.b, l.y, st);
         default:
             return SHP_ERR_UNSUPPORTED;
     }

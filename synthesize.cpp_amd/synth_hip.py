@@ -492,7 +492,8 @@ def cpy(x, out=None):
 NODE_FLAG_OUTPUT = 1
 RUN_KINDS = {-1: "unsupported", 0: "nop", 1: "single", 2: "norm_mul", 3: "norm_mul_rope", 4: "add_norm_mul",
              5: "silu_mul", 6: "add_leaky", 7: "add_scale_leaky", 8: "snake", 9: "snake_guarded", 10: "snake_beta",
-             11: "gather_sum", 12: "qk_norm_rope", 13: "qk_norm_rope_kv", 14: "cont_add_leaky"}
+             11: "gather_sum", 12: "qk_norm_rope", 13: "qk_norm_rope_kv", 14: "cont_add_leaky",
+             15: "view_binary"}
 
 
 class ShpNode(ctypes.Structure):

@@ -436,3 +436,40 @@ def test_executor_inside_a_captured_hip_graph(gpu):
         for a, b in zip(got, want):
             assert_bitexact(a, b)
         assert bool(torch.isfinite(junk))
+
+
+def test_codec_crop_bias_snake_beta_graph(gpu):
+    """codec_causal_conv1d's tail and the next SnakeBeta (qwen3-tts/codec.cpp:
+    64-71,100-104,184-199): the crop's copy of the GEMM output's first
+    columns, the channel bias add (one launch that reads the view), then the
+    SnakeBeta run. Bit-identical to the nodes one by one, and the biased crop
+    bit-exact against the restatement."""
+    rng = np.random.default_rng(SEED + 360)
+    C, L, keep = 256, 1030, 1024
+    wide = rng.standard_normal((L, C)).astype(np.float32)          # ggml [C, L]
+    bias = rng.standard_normal(C).astype(np.float32)
+    la = rng.uniform(-3, 3, C).astype(np.float32)
+    lb = rng.uniform(-3, 3, C).astype(np.float32)
+    tw, tb, tla, tlb = _t(gpu, wide), _t(gpu, bias), _t(gpu, la), _t(gpu, lb)
+
+    def build(every):
+        g = gpu.Graph()
+        crop = g.cont(g.view(tw, tw[:keep]))
+        biased = g.add(crop, tb)
+        a = g.exp(g.view(tla, tla.reshape(1, -1)))
+        b = g.exp(g.view(tlb, tlb.reshape(1, -1)))
+        y = g.add(biased, g.div(g.sqr(g.sin(g.mul(biased, a))), g.scale_bias(b, 1.0, 1e-9)))
+        outs = [biased, y]
+        return g, outs, (outs + [n["val"] for n in g.order(*outs)]) if every else outs
+
+    g, outs, every = build(False)
+    assert [k for k, *_ in g.plan(*every) if k != "nop"] == ["view_binary", "snake_beta"]
+    g.compute(*every)
+    fused = [_np(o.t).copy() for o in outs]
+    g, outs, every = build(True)
+    assert "view_binary" not in [k for k, *_ in g.plan(*every)]
+    g.compute(*every)
+    for a, b in zip(fused, [_np(o.t) for o in outs]):
+        assert_bitexact(a, b)
+    ref = R.run(lambda og: og.add(wide[:keep], bias))
+    assert_bitexact(fused[0], ref)

@@ -478,3 +478,32 @@ def test_conv_tail_runs():
     out = z(T, C)
     tm = g.cont(g.view(out, out.t()))
     assert "cont_add_leaky" not in kinds(g.plan(g.leaky_relu(g.add(tm, z(T)), 0.1)))
+
+
+def test_view_copy_then_binary():
+    """keep_prefix's copy of a row-contiguous view, then the channel bias
+    (qwen3-tts/codec.cpp:64-71,100-104): the add reads the view, one launch;
+    kept apart when the copy is read elsewhere, when it is a cast, when the
+    add's result would overlap the view, or for a transposed view (that is
+    the conv-tail run's)."""
+    C, L, keep = 32, 70, 64
+    wide = z(L, C)                                  # ggml [C, L]
+    view = wide[:keep]                              # the first `keep` columns
+    g = S.Graph()
+    crop = g.cont(g.view(wide, view))
+    assert kinds(g.plan(g.add(crop, z(C)))) == ["view_binary"]
+    g = S.Graph()
+    crop = g.cont(g.view(wide, view))
+    assert kinds(g.plan(g.mul(crop, z(keep, C)))) == ["view_binary"]
+    g = S.Graph()
+    crop = g.cont(g.view(wide, view))
+    assert kinds(g.plan(g.add(crop, z(C)), g.exp(crop))) == ["single", "single", "single"]
+    h = z(L, C, dtype=torch.float16)
+    g = S.Graph()
+    crop = g.cont(g.view(h, h[:keep]))
+    assert kinds(g.plan(g.add(crop, z(C)))) == ["single", "single"]
+    # the add's result placed over the view's own memory (shifted one row): apart
+    g = S.Graph()
+    crop = g.cont(g.view(wide, view))
+    added = g._op(S.NODE_ADD, wide[1:keep + 1], [crop, z(C)])
+    assert kinds(g.plan(added)) == ["single", "single"]
