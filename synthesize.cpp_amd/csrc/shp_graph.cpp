@@ -276,9 +276,10 @@ class Planner {
             int    used = match(p, l);
             if (used > 0) {
                 // a fused run is taken only when its entry point accepts the
-                // operands; otherwise its nodes run one by one
+                // operands and its outputs are apart from what it reads;
+                // otherwise its nodes run one by one
                 DryRun dry;
-                if (launch_run(*this, l, nullptr) != SHP_OK) {
+                if (launch_run(*this, l, nullptr) != SHP_OK || !io_apart(p, used, l)) {
                     used = 0;
                 }
             }
@@ -310,6 +311,37 @@ class Planner {
     const shp_node & node(int i) const { return nodes_[i]; }
 
   private:
+    // A run writes its outputs in one launch while it reads its inputs. The
+    // allocator may give an output the memory of a tensor that a node of the
+    // run read last (freed once that node had run), so an output may overlap
+    // an input at another offset or stride: the launch would then read values
+    // it has already overwritten. The run is taken only when every output is
+    // apart from every tensor the run reads from outside, or is that very
+    // tensor (the same bytes and strides: each kernel reads an element or a
+    // row before it writes it).
+    bool io_apart(size_t p, int used, const Launch & l) const {
+        Members members;
+        for (int k = 0; k < used; ++k) {
+            members.push(order_[p + k]);
+        }
+        const shp_tensor * outs[] = { l.y, l.y2, l.y3, l.sum };
+        for (int a = 0; a < members.n; ++a) {
+            const int m = members.v[a];
+            for (int k = 0; k < SHP_NODE_MAX_SRC; ++k) {
+                const shp_tensor & in = nodes_[m].src[k];
+                if (!present(in) || members.has(producer(m, k))) {
+                    continue;
+                }
+                for (const shp_tensor * o : outs) {
+                    if (o != nullptr && spans_overlap(in, *o) && !same_tensor(in, *o)) {
+                        return false;
+                    }
+                }
+            }
+        }
+        return true;
+    }
+
     // Window positions scanned past a rope run for its sibling and v's copy.
     static constexpr size_t kSiblingScan = 64;
 

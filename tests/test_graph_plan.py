@@ -507,3 +507,26 @@ def test_view_copy_then_binary():
     crop = g.cont(g.view(wide, view))
     added = g._op(S.NODE_ADD, wide[1:keep + 1], [crop, z(C)])
     assert kinds(g.plan(added)) == ["single", "single"]
+
+
+def test_runs_keep_outputs_apart_from_inputs():
+    """A fused run reads its inputs while it writes its outputs, so an output
+    the allocator placed over an input at another offset keeps the nodes
+    apart; the output written exactly over its input (in place) is fused."""
+    big = z(9, 64)
+    x = big[:8]
+    w = z(64)
+    g = S.Graph()
+    nrm = g.rms_norm(x, 1e-6)
+    y = g._op(S.NODE_MUL, big[1:9], [nrm, w])      # over x, one row on
+    assert kinds(g.plan(y)) == ["single", "single"]
+    g = S.Graph()
+    nrm = g.rms_norm(x, 1e-6)
+    y = g._op(S.NODE_MUL, x, [nrm, w])              # exactly over x
+    assert kinds(g.plan(y)) == ["norm_mul"]
+    # add -> leaky with the leaky result over b shifted
+    a, b2 = z(8, 64), z(9, 64)
+    g = S.Graph()
+    s_ = g.add(a, b2[:8])
+    y = g._op(S.NODE_LEAKY_RELU, b2[1:9], [s_], floats={0: 0.1})
+    assert kinds(g.plan(y)) == ["single", "single"]
