@@ -1075,7 +1075,9 @@ PMC_OPS = [
     ("add [2048,8192]", 201326592), ("snake [128,131072]", 134218240), ("snake_beta [128,131072]", 134218752),
     ("add_leaky_relu [128,131072]", 201326592), ("get_rows_sum q8_0 16x[1024,2048] x4096", 88342528),
     ("get_rows q8_0 [1024,2048] x4096", 21250048), ("soft_max_ext causal-size [512,512,16]", 33554432),
-    ("get_rows_sum q5_k 16x[1024,2048] x4096", 63176704), ("get_rows q5_k [1024,2048] x4096", 19677184)]
+    ("get_rows_sum q5_k 16x[1024,2048] x4096", 63176704), ("get_rows q5_k [1024,2048] x4096", 19677184),
+    ("cont(transpose) [128,131072]", 134217728), ("add bias[1,C] time-major [128,131072]", 134218240),
+    ("conv tail: cont(transpose)+bias+residual->leaky, sum [128,131072]", 268435968)]
 
 
 def pmc_large(S, torch):
@@ -1098,12 +1100,16 @@ def pmc_large(S, torch):
     codes = torch.randint(0, 2048, (16, 4096), generator=g, device="cuda", dtype=torch.int32)
     tabs5 = [S.Q5KTensor(torch.from_numpy(F.q5_k_synthetic(rng, 2048, 1024)).cuda(), 1024) for _ in range(16)]
     sc = randn(16, 512, 512)
+    xt, tb, tr = randn(131072, 128), randn(128, 1), randn(128, 131072)   # GEMM output ggml [128, T], bias, residual
+    ty, ts = empty(128, 131072), empty(128, 131072)
     fns = [lambda: S.rms_norm_mul(x2, w2, 1e-6), lambda: S.add_rms_norm_mul(x2, x2b, w2, 1e-6),
            lambda: S.qk_norm_rope(q, k, wq, wk, 1e-6, pos, 128, 1e6), lambda: S.swiglu(gt, up),
            lambda: S.add(x2, x2b), lambda: S.snake(xs, al), lambda: S.snake_beta(xs, la, lb),
            lambda: S.add_leaky_relu(a4, b4, 0.1), lambda: S.get_rows_sum(tabs, codes),
            lambda: S.get_rows(tabs[0], codes[0]), lambda: S.soft_max_ext(sc, None, 0.0884),
-           lambda: S.get_rows_sum(tabs5, codes), lambda: S.get_rows(tabs5[0], codes[0])]
+           lambda: S.get_rows_sum(tabs5, codes), lambda: S.get_rows(tabs5[0], codes[0]),
+           lambda: S.cpy(xt.t(), out=ty), lambda: S.add(tr, tb, out=ty),
+           lambda: S.cont_add_leaky_relu(xt.t(), tb, tr, 0.1, out=ty, sum_out=ts)]
     n = CALIB_BYTES // 4
     src = torch.randn(n, device="cuda")
     dst = torch.empty_like(src)
