@@ -342,7 +342,11 @@ shp_status_t shp_cpy(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
  * Each add is one f32 rounding, in that order, so y and sum are bit-identical
  * to the nodes one by one.
  *   x:   an F32 transposed or permuted view as shp_cpy takes it
- *   b:   F32 [1, ne1, ne2, ne3]: one value per row of y, rows evenly strided
+ *   b:   F32 [1, ne1, ne2, ne3]: one value per row of y, rows evenly
+ *        strided; or F32 [ne0]: one row repeated over y's rows (the channel
+ *        bias of a channel-major result, qwen3-tts/codec.cpp:58-59,134-140,
+ *        179-181, where the add precedes the transpose: the add is exact per
+ *        element, so adding after the transposing copy gives the same bits)
  *   r:   NULL or F32 of y's shape and strides (the residual)
  *   sum: NULL or F32 of y's shape and strides
  *   y:   F32 of x's shape, rows contiguous

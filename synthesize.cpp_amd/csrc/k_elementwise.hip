@@ -1130,9 +1130,11 @@ struct TransposeArgs {
 constexpr int kTile0 = 64;
 constexpr int kTileK = 128;
 
-// Epilogue bits: add the destination row's bias value, then the residual (a
-// second rounding, in the node order), write that sum, apply leaky-ReLU.
-enum TransposeEpi { kEpiBias = 1, kEpiResid = 2, kEpiLeaky = 4, kEpiSum = 8 };
+// Epilogue bits: add the bias -- the destination row's value (kEpiBias) or
+// one value per destination column, a row of ne0 repeated over the rows
+// (kEpiBias0) -- then the residual (a second rounding, in the node order),
+// write that sum, apply leaky-ReLU.
+enum TransposeEpi { kEpiBias = 1, kEpiResid = 2, kEpiLeaky = 4, kEpiSum = 8, kEpiBias0 = 16 };
 
 // One tile: loads into registers, LDS, stores. FULL = the tile lies wholly
 // inside the tensor: no guards, so each load's data goes to LDS as it arrives
@@ -1141,8 +1143,8 @@ enum TransposeEpi { kEpiBias = 1, kEpiResid = 2, kEpiLeaky = 4, kEpiSum = 8 };
 // the barrier.
 template <int V, bool FULL, int EPI>
 __device__ __forceinline__ void transpose_tile(float (&tile)[kTile0][kTileK + 1], float (&s_bias)[kTileK],
-                                               const TransposeArgs & a, const char * xb, char * yb, int64_t row0,
-                                               int n0, int nk) {
+                                               const TransposeArgs & a, const char * xb, char * yb, int64_t i0,
+                                               int64_t row0, int n0, int nk) {
     typedef float vec __attribute__((ext_vector_type(V)));
     constexpr int RL = kTileK / V, RLINES = 256 / RL, RPASS = kTile0 / RLINES;  // loads: lines along dim k
     constexpr int WL = kTile0 / V, WLINES = 256 / WL, WPASS = kTileK / WLINES;  // stores: lines along dim 0
@@ -1165,6 +1167,14 @@ __device__ __forceinline__ void transpose_tile(float (&tile)[kTile0][kTileK + 1]
         if (r < kTileK) {
             const int rr = r < nk ? r : 0;  // a line past the tensor reads line 0's value, unused
             s_bias[r]    = *reinterpret_cast<const float *>(a.bias + (row0 + rr * a.rowk) * a.brs);
+        }
+    }
+    // kEpiBias0: the lane's V columns are the same in every pass: one load
+    // (b is one contiguous row of ne0 values).
+    vec b0{};
+    if constexpr ((EPI & kEpiBias0) != 0) {
+        if (FULL || wc < n0) {
+            b0 = *reinterpret_cast<const vec *>(a.bias + (i0 + wc) * 4);
         }
     }
     vec rv[WPASS];
@@ -1196,6 +1206,9 @@ __device__ __forceinline__ void transpose_tile(float (&tile)[kTile0][kTileK + 1]
             w[e] = tile[wc + e][r];
             if constexpr ((EPI & kEpiBias) != 0) {
                 w[e] = w[e] + bv;
+            }
+            if constexpr ((EPI & kEpiBias0) != 0) {
+                w[e] = w[e] + b0[e];
             }
             if constexpr ((EPI & kEpiResid) != 0) {
                 w[e] = w[e] + rv[p][e];
@@ -1234,9 +1247,9 @@ template <int V, int EPI> __global__ __launch_bounds__(256) void k_transpose_til
         const int      n0   = static_cast<int>(a.ne0 - i0 < kTile0 ? a.ne0 - i0 : kTile0);
         const int      nk   = static_cast<int>(a.nek - ik < kTileK ? a.nek - ik : kTileK);
         if (n0 == kTile0 && nk == kTileK) {
-            transpose_tile<V, true, EPI>(tile, s_bias, a, xb, yb, row0, n0, nk);
+            transpose_tile<V, true, EPI>(tile, s_bias, a, xb, yb, i0, row0, n0, nk);
         } else {
-            transpose_tile<V, false, EPI>(tile, s_bias, a, xb, yb, row0, n0, nk);
+            transpose_tile<V, false, EPI>(tile, s_bias, a, xb, yb, i0, row0, n0, nk);
         }
     }
 }
@@ -1411,11 +1424,19 @@ extern "C" shp_status_t shp_cont_add_leaky_relu(const shp_tensor * x,
         return st;
     }
     // b: one value per row of y, b's rows one for one at a fixed stride
-    // (ggml_add(cont, reshape_2d(bias, 1, C)), vits/waveform-decoder.cpp:118-121);
+    // (ggml_add(cont, reshape_2d(bias, 1, C)), vits/waveform-decoder.cpp:118-121),
+    // or one row of ne0 values repeated over y's rows (the channel bias of a
+    // channel-major result, qwen3-tts/codec.cpp:58-59,134-140,179-181);
     // r and sum: y's shape and strides (the residual and the add's result).
-    const RowMap bm = make_rowmap(*b);
-    if (b->ne[0] != 1 || b->ne[1] != y->ne[1] || b->ne[2] != y->ne[2] || b->ne[3] != y->ne[3] || !bm.flat) {
+    const RowMap bm      = make_rowmap(*b);
+    const bool   per_row = b->ne[0] == 1 && b->ne[1] == y->ne[1] && b->ne[2] == y->ne[2] && b->ne[3] == y->ne[3] &&
+                         bm.flat;
+    const bool   per_col = !per_row && one_row_of(*b, y->ne[0]);
+    if (!per_row && !per_col) {
         return SHP_ERR_UNSUPPORTED;
+    }
+    if (per_col && reinterpret_cast<uintptr_t>(b->data) % 16 != 0) {
+        pl.v4 = false;
     }
     const auto same_layout = [y](const shp_tensor * t) {
         return same_shape(*t, *y) && t->nb[1] == y->nb[1] && t->nb[2] == y->nb[2] && t->nb[3] == y->nb[3];
@@ -1448,7 +1469,24 @@ extern "C" shp_status_t shp_cont_add_leaky_relu(const shp_tensor * x,
     a.rdelta          = r != nullptr ? static_cast<const char *>(r->data) - static_cast<const char *>(y->data) : 0;
     a.sdelta          = sum != nullptr ? static_cast<const char *>(sum->data) - static_cast<const char *>(y->data) : 0;
     const hipStream_t ss = as_stream(stream);
-    const int epi = kEpiBias | (r != nullptr ? kEpiResid : 0) | (apply_leaky ? kEpiLeaky : 0) | (sum != nullptr ? kEpiSum : 0);
+    const int rest = (r != nullptr ? kEpiResid : 0) | (apply_leaky ? kEpiLeaky : 0) | (sum != nullptr ? kEpiSum : 0);
+    if (per_col) {
+        switch (rest) {
+            case 0:
+                return launch_transpose<kEpiBias0>(pl, ss);
+            case kEpiLeaky:
+                return launch_transpose<kEpiBias0 | kEpiLeaky>(pl, ss);
+            case kEpiLeaky | kEpiSum:
+                return launch_transpose<kEpiBias0 | kEpiLeaky | kEpiSum>(pl, ss);
+            case kEpiResid:
+                return launch_transpose<kEpiBias0 | kEpiResid>(pl, ss);
+            case kEpiResid | kEpiLeaky:
+                return launch_transpose<kEpiBias0 | kEpiResid | kEpiLeaky>(pl, ss);
+            default:
+                return launch_transpose<kEpiBias0 | kEpiResid | kEpiLeaky | kEpiSum>(pl, ss);
+        }
+    }
+    const int epi = kEpiBias | rest;
     switch (epi) {
         case kEpiBias:
             return launch_transpose<kEpiBias>(pl, ss);

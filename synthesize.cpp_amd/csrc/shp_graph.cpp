@@ -199,6 +199,12 @@ struct Launch {
     int32_t                 i0    = 0;
     std::vector<shp_tensor> terms;
     shp_tensor              codes{};
+    // views the run forms itself (a transposed view of a copy's source, a
+    // [1, C] bias read as one row of C): used in place of x / b when set
+    shp_tensor              xv{};
+    shp_tensor              bv{};
+    bool                    own_x = false;
+    bool                    own_b = false;
 };
 
 class Planner;
@@ -635,6 +641,26 @@ class Planner {
         return true;
     }
 
+    // internal(), with view nodes between j and its readers looked through: a
+    // view (NOP) reader counts when it is no output, no later split reads it,
+    // and its own readers are members (or views of the same kind).
+    bool internal_v(int j, const Members & members, int depth = 0) const {
+        if (depth > 8 || (nodes_[j].flags & SHP_NODE_FLAG_OUTPUT) || readers(j) == 0 ||
+            nodes_[j].uses > readers(j)) {
+            return false;
+        }
+        for (int c = cstart_[j]; c < cstart_[j + 1]; ++c) {
+            const int r = cons_[c];
+            if (members.has(r)) {
+                continue;
+            }
+            if (nodes_[r].op != SHP_NODE_NOP || !internal_v(r, members, depth + 1)) {
+                return false;
+            }
+        }
+        return true;
+    }
+
     // j's result is read outside `members` (or is an output): it must be written.
     bool needed_outside(int j, const Members & members) const {
         return (nodes_[j].flags & SHP_NODE_FLAG_OUTPUT) || !internal(j, members);
@@ -661,6 +687,9 @@ class Planner {
                 }
                 return 0;
             case SHP_NODE_ADD:
+                if ((used = match_transpose_bias(p, l)) != 0) {
+                    return used;
+                }
                 for (int k : { 4, 3 }) {
                     if ((used = match_add_norm(p, k, l)) != 0) {
                         return used;
@@ -682,7 +711,7 @@ class Planner {
             case SHP_NODE_SILU:
                 return match_silu_mul(p, l);
             case SHP_NODE_CPY:
-                if ((used = match_cont_tail(p, l)) != 0) {
+                if ((used = match_transpose_bias(p, l)) != 0 || (used = match_cont_tail(p, l)) != 0) {
                     return used;
                 }
                 return match_view_binary(p, l);
@@ -1133,6 +1162,91 @@ class Planner {
         return 0;
     }
 
+    // t is exactly ggml_transpose(s): s's data with dims 0 and 1 swapped.
+    // (A stride is compared only where its extent is above 1: it is never
+    // used otherwise.)
+    static bool is_transpose_of(const shp_tensor & t, const shp_tensor & s) {
+        const auto same = [&](int dt, int ds) { return t.ne[dt] == 1 || t.nb[dt] == s.nb[ds]; };
+        return t.data == s.data && t.type == s.type && t.ne[0] == s.ne[1] && t.ne[1] == s.ne[0] &&
+               t.ne[2] == s.ne[2] && t.ne[3] == s.ne[3] && same(0, 1) && same(1, 0) && same(2, 2) && same(3, 3);
+    }
+
+    // The channel-major convolutions' tails (qwen3-tts/codec.cpp), as one
+    // transposing copy with the channel bias added per destination column:
+    //  (a) [CPY(row-contiguous view v) ->] ADD(v, b [1, C]) -> CPY(transpose
+    //      of the sum) (the transposed convolution's crop, bias and return,
+    //      :179-181): y = transpose(v) + b read as one row of C;
+    //  (b) CPY(transposed view t) -> CPY(its first rows) -> ADD(crop, b [C])
+    //      (the depthwise convolution's return to channel-major, crop and
+    //      bias, :134-140): y = the first rows of the transposing copy + b.
+    // Each add is exact per element, so adding before or after the transpose
+    // gives the same bits.
+    int match_transpose_bias(size_t p, Launch & l) const {
+        const int n0 = at(p, 0), n1 = at(p, 1), n2 = at(p, 2);
+        // (b)
+        if (is(n0, SHP_NODE_CPY) && is(n1, SHP_NODE_CPY) && is(n2, SHP_NODE_ADD) && producer(n1, 0) == n0 &&
+            src(n2, 0) == n1 && src(n2, 1) != n1) {
+            const shp_node & T = nodes_[n0];
+            const shp_node & K = nodes_[n1];
+            const shp_node & A = nodes_[n2];
+            const shp_tensor & crop = K.src[0];
+            const Members members{ n0, n1, n2 };
+            if (f32_strided_view_dim(&T.src[0]) != 0 && f32_of(T.dst) && same_shape(T.src[0], T.dst) &&
+                f32_of(crop) && crop.data == T.dst.data && crop.ne[0] == T.dst.ne[0] && crop.ne[1] <= T.dst.ne[1] &&
+                crop.ne[2] == T.dst.ne[2] && crop.ne[3] == T.dst.ne[3] &&
+                (crop.ne[1] == 1 || crop.nb[1] == T.dst.nb[1]) && (crop.ne[2] == 1 || crop.nb[2] == T.dst.nb[2]) &&
+                (crop.ne[3] == 1 || crop.nb[3] == T.dst.nb[3]) && f32_of(K.dst) &&
+                same_shape(K.dst, crop) && f32_of(A.dst) && same_shape(A.dst, crop) && internal_v(n0, members) &&
+                internal(n1, members)) {
+                l      = Launch{};
+                l.kind = SHP_RUN_CONT_ADD_LEAKY;
+                l.xv   = T.src[0];
+                l.xv.ne[1] = crop.ne[1];  // only the rows the crop keeps
+                l.own_x    = true;
+                l.b        = &A.src[1];
+                l.y        = const_cast<shp_tensor *>(&A.dst);
+                return 3;
+            }
+        }
+        // (a), with or without the crop's copy in front
+        const bool crop = is(n0, SHP_NODE_CPY);
+        const int  ad = crop ? n1 : n0, cp = crop ? n2 : n1;
+        if (!is(ad, SHP_NODE_ADD) || !is(cp, SHP_NODE_CPY) || (crop && (src(ad, 0) != n0 || src(ad, 1) == n0)) ||
+            producer(cp, 0) != ad) {
+            return 0;
+        }
+        const shp_node & A = nodes_[ad];
+        const shp_node & C = nodes_[cp];
+        const shp_tensor & v = crop ? nodes_[n0].src[0] : A.src[0];
+        const shp_tensor & b = A.src[1];
+        Members members{ ad, cp };
+        if (crop) {
+            members.push(n0);
+        }
+        if (!f32_of(v) || !f32_of(A.dst) || !same_shape(v, A.dst) || (crop && !same_shape(nodes_[n0].dst, v)) ||
+            !is_transpose_of(C.src[0], A.dst) || !f32_of(C.dst) || !same_shape(C.dst, C.src[0]) ||
+            !internal_v(ad, members) || (crop && !internal(n0, members)) || !well_formed(&b) ||
+            b.type != SHP_TYPE_F32 || b.ne[0] != 1 || b.ne[1] != v.ne[1] || b.ne[2] != 1 || b.ne[3] != 1 ||
+            b.nb[1] != 4 || v.ne[2] != 1 || v.ne[3] != 1) {
+            return 0;
+        }
+        l       = Launch{};
+        l.kind  = SHP_RUN_CONT_ADD_LEAKY;
+        l.xv    = v;  // transpose(v): dims 0 and 1 swapped
+        l.xv.ne[0] = v.ne[1];
+        l.xv.ne[1] = v.ne[0];
+        l.xv.nb[0] = v.nb[1];
+        l.xv.nb[1] = v.nb[0];
+        l.own_x    = true;
+        l.bv       = b;  // [1, C] read as one row of C
+        l.bv.ne[0] = b.ne[1];
+        l.bv.ne[1] = 1;
+        l.bv.nb[0] = b.nb[1];
+        l.own_b    = true;
+        l.y        = const_cast<shp_tensor *>(&C.dst);
+        return members.n;
+    }
+
     // CPY of a row-contiguous F32 view into a tensor of its shape, read only
     // by an ADD, MUL or DIV as src0: the op reads the view in place of the
     // copy, which is never written (the causal convolutions' crop, then their
@@ -1276,7 +1390,8 @@ shp_status_t launch_run(const Planner & pl, const Launch & l, shp_stream_t st) {
             // the copies' destinations are the cache views themselves (filled 0)
             return shp_qk_norm_rope_kv(l.x, l.x2, l.x3, l.w, l.w2, l.f0, l.b, l.i0, l.f1, l.f2, l.y, l.y2, l.y3, 0, st);
         case SHP_RUN_CONT_ADD_LEAKY:
-            return shp_cont_add_leaky_relu(l.x, l.b, l.x3, l.i0, l.f0, l.sum, l.y, st);
+            return shp_cont_add_leaky_relu(l.own_x ? &l.xv : l.x, l.own_b ? &l.bv : l.b, l.x3, l.i0, l.f0, l.sum,
+                                           l.y, st);
         case SHP_RUN_VIEW_BINARY:
             return l.i0 == SHP_NODE_ADD ? shp_add(l.x, l.b, l.y, st) :
                    l.i0 == SHP_NODE_MUL ? shp_mul(l.x, l.b, l.y, st) :

@@ -473,3 +473,43 @@ def test_codec_crop_bias_snake_beta_graph(gpu):
         assert_bitexact(a, b)
     ref = R.run(lambda og: og.add(wide[:keep], bias))
     assert_bitexact(fused[0], ref)
+
+
+def test_codec_transpose_bias_graphs(gpu):
+    """qwen3-tts/codec.cpp's channel-major tails as one launch each: the
+    transposed convolution's crop, [1, C] bias and return (:179-181), and the
+    depthwise convolution's return, crop and [C] bias (:134-140).
+    Bit-identical to the nodes with every result written, and to the
+    restatement."""
+    rng = np.random.default_rng(SEED + 370)
+    C, Lw, kept = 96, 2056, 2048
+    wide = rng.standard_normal((C, Lw)).astype(np.float32)       # col2im's ggml [Lw, C]
+    b1 = rng.standard_normal((C, 1)).astype(np.float32)          # ggml [1, C]
+    mm = rng.standard_normal((C, Lw)).astype(np.float32)         # depthwise GEMM output ggml [Lw, C] (:133)
+    b2 = rng.standard_normal(C).astype(np.float32)               # ggml [C]
+    tw, tb1, tmm, tb2 = _t(gpu, wide), _t(gpu, b1), _t(gpu, mm), _t(gpu, b2)
+
+    def build(every):
+        g = gpu.Graph()
+        crop = g.cont(g.view(tw, tw[:, :kept]))
+        s1 = g.add(crop, tb1)
+        y1 = g.cont(g.view(s1, s1.t.t()))                        # ggml [C, kept]
+        cm = g.cont(g.view(tmm, tmm.t()))                        # channel-major ggml [C, Lw]
+        crop2 = g.cont(g.view(cm, cm.t[:kept]))
+        y2 = g.add(crop2, tb2)
+        outs = [y1, y2]
+        return g, outs, (outs + [n["val"] for n in g.order(*outs)]) if every else outs
+
+    g, outs, every = build(False)
+    assert [k for k, *_ in g.plan(*every) if k != "nop"] == ["cont_add_leaky", "cont_add_leaky"]
+    g.compute(*every)
+    fused = [_np(o.t).copy() for o in outs]
+    g, outs, every = build(True)
+    assert "cont_add_leaky" not in [k for k, *_ in g.plan(*every)]
+    g.compute(*every)
+    for a, b in zip(fused, [_np(o.t) for o in outs]):
+        assert_bitexact(a, b)
+    ref1 = R.run(lambda og: og.binbcast(R.OP_ADD, np.ascontiguousarray(wide[:, :kept]), b1))
+    assert_bitexact(fused[0], np.ascontiguousarray(ref1.T))
+    ref2 = R.run(lambda og: og.add(np.ascontiguousarray(mm.T[:kept]), b2))
+    assert_bitexact(fused[1], ref2)

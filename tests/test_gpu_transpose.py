@@ -224,3 +224,30 @@ def test_conv_tail_in_a_node_list(gpu):
     state, nxt = _oracle_tail(host["o2"], host["b2"], host["res"], 0.1)
     for a, b in zip(fused, (act, state, nxt)):
         assert_bitexact(a, b)
+
+
+@pytest.mark.parametrize("T,C", [(4096, 96), (1000, 37), (130, 64)])
+@pytest.mark.parametrize("resid,leaky,with_sum", [(False, False, False), (True, True, True), (False, True, False)])
+def test_cont_add_leaky_column_bias(gpu, T, C, resid, leaky, with_sum):
+    """The bias as one row of ne0 values repeated over y's rows (the channel
+    bias of a channel-major result, qwen3-tts/codec.cpp:58-59,179-181): y =
+    cont(x) + b [+ r], leaky; against the restatement's nodes."""
+    import torch
+    rng = np.random.default_rng(SEED + 2 * T + C + resid)
+    src = rng.standard_normal((C, T)).astype(np.float32)       # ggml [T, C]; y = its transpose, ggml [C, T]
+    bias = rng.standard_normal(C).astype(np.float32)           # ggml [C]
+    r = rng.standard_normal((T, C)).astype(np.float32) if resid else None
+    slope = 0.1 if leaky else None
+    ts = _t(gpu, src)
+    s_out = torch.empty((T, C), dtype=torch.float32, device="cuda") if with_sum else None
+    y = gpu.cont_add_leaky_relu(ts.t(), _t(gpu, bias), _t(gpu, r) if resid else None, slope, sum_out=s_out)
+    g = R.Graph()
+    tm = g.cont_f32(src, [C, T], [4 * T, 4]).reshape(T, C)
+    s_ = g.add(tm, bias)
+    if resid:
+        s_ = g.add(s_, r)
+    yr = g.leaky_relu(s_, slope) if leaky else s_
+    g.compute(4)
+    assert_bitexact(_np(y), yr)
+    if with_sum:
+        assert_bitexact(_np(s_out), s_)

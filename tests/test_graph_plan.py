@@ -530,3 +530,40 @@ def test_runs_keep_outputs_apart_from_inputs():
     s_ = g.add(a, b2[:8])
     y = g._op(S.NODE_LEAKY_RELU, b2[1:9], [s_], floats={0: 0.1})
     assert kinds(g.plan(y)) == ["single", "single"]
+
+
+def test_codec_transpose_bias_runs():
+    """The channel-major convolutions' tails in qwen3-tts/codec.cpp as one
+    transposing launch: the transposed convolution's crop, [1, C] bias and
+    return (:179-181), with or without the crop's copy; the depthwise
+    convolution's return, crop and [C] bias (:134-140). A transpose read
+    elsewhere, or a bias of another shape, keeps the nodes apart."""
+    C, Lw, kept = 32, 80, 64
+    wide = z(C, Lw)                                 # ggml [Lw, C]: col2im's [out_length, out_channels]
+    g = S.Graph()
+    crop = g.cont(g.view(wide, wide[:, :kept]))     # ggml [kept, C]
+    s_ = g.add(crop, z(C, 1))                       # + ggml [1, C]
+    y = g.cont(g.view(s_, s_.t.t()))                # ggml [C, kept]
+    plan = g.plan(y)
+    assert kinds(plan) == ["cont_add_leaky"] and [p[3] for p in plan if p[0] != "nop"] == [3]
+    g = S.Graph()
+    x = z(C, kept)
+    s_ = g.add(x, z(C, 1))
+    y = g.cont(g.view(s_, s_.t.t()))
+    assert kinds(g.plan(y)) == ["cont_add_leaky"]
+    g = S.Graph()
+    s_ = g.add(x, z(C, 1))
+    y = g.cont(g.view(s_, s_.t.t()))
+    assert kinds(g.plan(y, g.exp(s_))) == ["single", "single", "single"]   # the sum read elsewhere
+    # depthwise: GEMM output ggml [out_length, C] -> channel-major, first `kept` rows, + bias [C]
+    mm = z(C, Lw)
+    g = S.Graph()
+    cm = g.cont(g.view(mm, mm.t()))                 # ggml [C, Lw]
+    crop = g.cont(g.view(cm, cm.t[:kept]))          # ggml [C, kept]
+    y = g.add(crop, z(C))
+    plan = g.plan(y)
+    assert kinds(plan) == ["cont_add_leaky"] and [p[3] for p in plan if p[0] != "nop"] == [3]
+    g = S.Graph()
+    cm = g.cont(g.view(mm, mm.t()))
+    crop = g.cont(g.view(cm, cm.t[:kept]))
+    assert "cont_add_leaky" not in kinds(g.plan(g.add(crop, z(kept, 1)), g.exp(cm)))
