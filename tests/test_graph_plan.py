@@ -473,11 +473,15 @@ def test_conv_tail_runs():
     g = S.Graph()
     x = z(C, T)
     assert "cont_add_leaky" not in kinds(g.plan(g.leaky_relu(g.add(g.cont(x), z(C, 1)), 0.1)))
-    # a bias that is one row [T] instead of one value per row: the nodes alone
+    # a bias that is one row [T] repeated over the rows: the same run
     g = S.Graph()
     out = z(T, C)
     tm = g.cont(g.view(out, out.t()))
-    assert "cont_add_leaky" not in kinds(g.plan(g.leaky_relu(g.add(tm, z(T)), 0.1)))
+    assert kinds(g.plan(g.leaky_relu(g.add(tm, z(T)), 0.1))) == ["cont_add_leaky"]
+    # a bias that tiles along the row ([T/2]): the nodes alone
+    g = S.Graph()
+    tm = g.cont(g.view(out, out.t()))
+    assert "cont_add_leaky" not in kinds(g.plan(g.leaky_relu(g.add(tm, z(T // 2)), 0.1)))
 
 
 def test_view_copy_then_binary():
