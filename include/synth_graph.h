@@ -78,6 +78,7 @@ typedef enum shp_node_op {
     SHP_NODE_EXP,        /* GGML_OP_UNARY, GGML_UNARY_OP_EXP */
     SHP_NODE_GLU_SWIGLU, /* GGML_OP_GLU, GGML_GLU_OP_SWIGLU: i32 [1] swapped; src[1] absent
                             (single tensor) or the second half (split form) */
+    SHP_NODE_CONCAT,     /* GGML_OP_CONCAT: i32 {dim}; src[0], src[1] */
     SHP_NODE_OP_COUNT
 } shp_node_op;
 

@@ -334,6 +334,16 @@ shp_status_t shp_sqr(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
 shp_status_t shp_cpy(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
 
 /*
+ * ggml_concat(a, b, dim): y of a's shape except y->ne[dim] = a->ne[dim] +
+ * b->ne[dim]; y(i) = a(i) where i[dim] < a->ne[dim], else b(i) with
+ * i[dim] - a->ne[dim]. All F32, rows contiguous (any row strides). The code
+ * predictor's prefill input, the talker's hidden state and its code embedding
+ * as one two-position block (src/arch/qwen3-tts/model.cpp:1450), and the
+ * encoders' feature joins (qwen3-tts/speaker-encoder.cpp:236,335,358).
+ */
+shp_status_t shp_concat(const shp_tensor * a, const shp_tensor * b, int32_t dim, shp_tensor * y, shp_stream_t stream);
+
+/*
  * The tail of the time-major vocoder convolution, in one pass
  * (vits/waveform-decoder.cpp:111,118-121, then :147,150 or the next layer's
  * :146): s = ggml_add(ggml_cont(ggml_transpose(out)), reshape_2d(bias, 1, C)),

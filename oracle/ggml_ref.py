@@ -269,6 +269,20 @@ class Graph:
 # node runs the reference graph builders emit
 # ---------------------------------------------------------------------------
 
+def concat(a, b, dim):
+    """ggml_concat(a, b, dim) restated (data movement only: every element of
+    the result is a's where its index along ggml dimension dim is below a's
+    extent, else b's at that index minus a's extent). a, b: numpy arrays in
+    this module's layout; ggml dim d is numpy axis ndim - 1 - d. Sites:
+    src/arch/qwen3-tts/model.cpp:1450, qwen3-tts/speaker-encoder.cpp:236,335,358."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    nd = max(a.ndim, b.ndim, dim + 1)
+    a = a.reshape((1,) * (nd - a.ndim) + a.shape)
+    b = b.reshape((1,) * (nd - b.ndim) + b.shape)
+    return np.concatenate([a, b], axis=nd - 1 - dim)
+
+
 def as_f32(g, w, wtype=F32):
     """as_f32, src/arch/qwen3-tts/operations.cpp:20-25 (ggml_cast when not F32)."""
     return w if wtype == F32 else g.cast_f32(w, wtype)

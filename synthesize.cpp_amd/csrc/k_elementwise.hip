@@ -1342,8 +1342,90 @@ shp_status_t transpose_entry(const shp_tensor * x, shp_tensor * y, shp_stream_t 
     return launch_transpose<0>(pl, as_stream(stream));
 }
 
+// ggml_concat: each destination row comes from a or b (dim >= 1) or is a's
+// row followed by b's (dim 0); rows over blocks, elements over threads.
+struct ConcatArgs {
+    const char * a;
+    const char * b;
+    char *       y;
+    int64_t      anb[4];
+    int64_t      bnb[4];
+    int64_t      ynb[4];
+    int64_t      ane[4];
+    int64_t      yne[4];
+    int64_t      nrows;
+    int32_t      dim;
+    int32_t      pad;
+};
+
+__global__ __launch_bounds__(256) void k_concat_rows(const ConcatArgs g) {
+    for (int64_t r = blockIdx.x; r < g.nrows; r += gridDim.x) {
+        int64_t       i[4] = { 0, r % g.yne[1], (r / g.yne[1]) % g.yne[2], r / (g.yne[1] * g.yne[2]) };
+        char *        yr   = g.y + i[1] * g.ynb[1] + i[2] * g.ynb[2] + i[3] * g.ynb[3];
+        const int64_t ne0  = g.yne[0];
+        if (g.dim == 0) {
+            const float * ar = reinterpret_cast<const float *>(g.a + i[1] * g.anb[1] + i[2] * g.anb[2] + i[3] * g.anb[3]);
+            const float * br = reinterpret_cast<const float *>(g.b + i[1] * g.bnb[1] + i[2] * g.bnb[2] + i[3] * g.bnb[3]);
+            const int64_t na = g.ane[0];
+            for (int64_t c = threadIdx.x; c < ne0; c += 256) {
+                reinterpret_cast<float *>(yr)[c] = c < na ? ar[c] : br[c - na];
+            }
+            continue;
+        }
+        const bool   from_a = i[g.dim] < g.ane[g.dim];
+        const char * src;
+        if (from_a) {
+            src = g.a + i[1] * g.anb[1] + i[2] * g.anb[2] + i[3] * g.anb[3];
+        } else {
+            i[g.dim] -= g.ane[g.dim];
+            src = g.b + i[1] * g.bnb[1] + i[2] * g.bnb[2] + i[3] * g.bnb[3];
+        }
+        for (int64_t c = threadIdx.x; c < ne0; c += 256) {
+            reinterpret_cast<float *>(yr)[c] = reinterpret_cast<const float *>(src)[c];
+        }
+    }
+}
+
 }  // namespace
 }  // namespace shp
+
+extern "C" shp_status_t shp_concat(const shp_tensor * a, const shp_tensor * b, int32_t dim, shp_tensor * y,
+                                   shp_stream_t stream) {
+    if (!well_formed(a) || !well_formed(b) || !well_formed(y) || dim < 0 || dim > 3) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    if (a->type != SHP_TYPE_F32 || b->type != SHP_TYPE_F32 || y->type != SHP_TYPE_F32) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    for (int d = 0; d < 4; ++d) {
+        const int64_t want = d == dim ? a->ne[d] + b->ne[d] : a->ne[d];
+        if (y->ne[d] != want || (d != dim && b->ne[d] != a->ne[d])) {
+            return SHP_ERR_INVALID_ARG;
+        }
+    }
+    if (spans_overlap(*a, *y) || spans_overlap(*b, *y)) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    if (dry_run()) {
+        return SHP_OK;
+    }
+    ConcatArgs g{};
+    g.a   = static_cast<const char *>(a->data);
+    g.b   = static_cast<const char *>(b->data);
+    g.y   = static_cast<char *>(y->data);
+    g.dim = dim;
+    for (int d = 0; d < 4; ++d) {
+        g.anb[d] = static_cast<int64_t>(a->nb[d]);
+        g.bnb[d] = static_cast<int64_t>(b->nb[d]);
+        g.ynb[d] = static_cast<int64_t>(y->nb[d]);
+        g.ane[d] = a->ne[d];
+        g.yne[d] = y->ne[d];
+    }
+    g.nrows              = nrows(*y);
+    const int64_t blocks = g.nrows < 65536 ? g.nrows : 65536;
+    hipLaunchKernelGGL(k_concat_rows, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream), g);
+    return launch_status();
+}
 
 extern "C" shp_status_t shp_add(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream) {
     return binary_entry<kAdd>(a, b, y, stream);

@@ -126,6 +126,9 @@ bool node_form_ok(const shp_node & n) {
         }
         case SHP_NODE_ROPE:
             return rope_params_ok(n);
+        case SHP_NODE_CONCAT:
+            return f32_of(n.src[0]) && f32_of(n.src[1]) && f32_of(n.dst) && n.op_params[0] >= 0 &&
+                   n.op_params[0] <= 3;
         case SHP_NODE_GLU_SWIGLU: {
             const auto & a = n.src[0];
             if (!f32_of(a) || !f32_of(n.dst)) {
@@ -1352,6 +1355,8 @@ shp_status_t launch_single(const shp_node & n, shp_stream_t st) {
                 return shp_swiglu(swapped ? &n.src[1] : &n.src[0], swapped ? &n.src[0] : &n.src[1], y, st);
             }
             return shp_glu_swiglu(&n.src[0], n.op_params[1], y, st);
+        case SHP_NODE_CONCAT:
+            return shp_concat(&n.src[0], &n.src[1], n.op_params[0], y, st);
         default:
             return SHP_ERR_UNSUPPORTED;
     }

@@ -91,6 +91,7 @@ def load(path=None):
         "shp_sqr": [_PT, _PT, vp],
         "shp_cpy": [_PT, _PT, vp],
         "shp_cont_add_leaky_relu": [_PT, _PT, _PT, i32, f, _PT, _PT, vp],
+        "shp_concat": [_PT, _PT, i32, _PT, vp],
         "shp_graph_compute": [ctypes.POINTER(ShpNode), i32, vp],
         "shp_graph_plan": [ctypes.POINTER(ShpNode), i32, ctypes.POINTER(ShpGraphRun), i32, ctypes.POINTER(i32)],
     }
@@ -475,6 +476,17 @@ def cont_add_leaky_relu(x, b, r=None, slope=None, out=None, sum_out=None):
     return out
 
 
+def concat(a, b, dim, out=None):
+    """ggml_concat(a, b, dim) (dim a ggml dimension)."""
+    import torch
+    ax = a.dim() - 1 - dim
+    shape = list(a.shape)
+    shape[ax] += b.shape[ax]
+    out = torch.empty(shape, dtype=torch.float32, device=a.device) if out is None else out
+    _check(load().shp_concat(_ref(desc(a)), _ref(desc(b)), int(dim), _ref(desc(out)), _stream()), "concat")
+    return out
+
+
 def cpy(x, out=None):
     """ggml_cpy / ggml_cast into F32 of x's shape (x F32, F16 or BF16)."""
     import torch
@@ -488,7 +500,7 @@ def cpy(x, out=None):
 # ---------------------------------------------------------------------------
 
 (NODE_NOP, NODE_ADD, NODE_MUL, NODE_DIV, NODE_SQR, NODE_SIN, NODE_SCALE, NODE_CPY, NODE_GET_ROWS, NODE_RMS_NORM,
- NODE_SOFT_MAX, NODE_ROPE, NODE_LEAKY_RELU, NODE_SILU, NODE_EXP, NODE_GLU_SWIGLU) = range(16)
+ NODE_SOFT_MAX, NODE_ROPE, NODE_LEAKY_RELU, NODE_SILU, NODE_EXP, NODE_GLU_SWIGLU, NODE_CONCAT) = range(17)
 NODE_FLAG_OUTPUT = 1
 RUN_KINDS = {-1: "unsupported", 0: "nop", 1: "single", 2: "norm_mul", 3: "norm_mul_rope", 4: "add_norm_mul",
              5: "silu_mul", 6: "add_leaky", 7: "add_scale_leaky", 8: "snake", 9: "snake_guarded", 10: "snake_beta",
@@ -616,6 +628,16 @@ class Graph:
         """ggml_cont(x): x (typically a permuted view) copied into a new
         contiguous tensor of its shape; the same node kind as ggml_cpy."""
         return self._op(NODE_CPY, self._like(x), [x])
+
+    def concat(self, a, b, dim):
+        """ggml_concat(a, b, dim) (dim a ggml dimension)."""
+        import torch
+        ta, tb = self._t(a), self._t(b)
+        ax = ta.dim() - 1 - dim
+        shape = list(ta.shape)
+        shape[ax] += tb.shape[ax]
+        return self._op(NODE_CONCAT, torch.empty(shape, dtype=torch.float32, device=ta.device), [a, b],
+                        ints={0: dim})
 
     def glu_swiglu(self, a, b=None, swapped=False):
         t = self._t(a)

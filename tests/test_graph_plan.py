@@ -571,3 +571,15 @@ def test_codec_transpose_bias_runs():
     cm = g.cont(g.view(mm, mm.t()))
     crop = g.cont(g.view(cm, cm.t[:kept]))
     assert "cont_add_leaky" not in kinds(g.plan(g.add(crop, z(kept, 1)), g.exp(cm)))
+
+
+def test_concat_node():
+    """ggml_concat as a single node (src/arch/qwen3-tts/model.cpp:1450: the
+    talker's hidden state and the code embedding as one two-position block)."""
+    g = S.Graph()
+    assert kinds(g.plan(g.concat(z(1, 1024), z(1, 1024), 1))) == ["single"]
+    g = S.Graph()
+    assert kinds(g.plan(g.concat(z(3, 8), z(3, 5), 0))) == ["single"]
+    g = S.Graph()
+    h = z(3, 8, dtype=torch.float16)
+    assert kinds(g.plan(g.concat(h, h, 1))) == ["unsupported"]

@@ -547,3 +547,23 @@ def test_binbcast_reduces_to_the_plain_forms():
     np.testing.assert_array_equal(bits(y3), bits(y4))
     with pytest.raises(ValueError):
         R.Graph().binbcast(R.OP_ADD, a, np.zeros((3, 64), np.float32))
+
+
+@pytest.mark.parametrize("dim", [0, 1, 2, 3])
+def test_concat_against_an_element_loop(dim):
+    """concat along each ggml dimension against the definition, element by
+    element (tiny shapes), and a planted mistake (the operands swapped)
+    rejected."""
+    rng = np.random.default_rng(dim)
+    ashape = [2, 3, 4, 5]            # numpy (ne3, ne2, ne1, ne0)
+    bshape = list(ashape)
+    bshape[3 - dim] = 2
+    a = rng.standard_normal(ashape).astype(np.float32)
+    b = rng.standard_normal(bshape).astype(np.float32)
+    y = R.concat(a, b, dim)
+    na = ashape[3 - dim]
+    for idx in np.ndindex(*y.shape):
+        k = idx[3 - dim]
+        want = a[idx] if k < na else b[tuple(k - na if j == 3 - dim else v for j, v in enumerate(idx))]
+        assert bits(y[idx]) == bits(want)
+    assert not np.array_equal(bits(R.concat(b, a, dim)), bits(y))
