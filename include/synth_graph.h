@@ -79,6 +79,13 @@ typedef enum shp_node_op {
     SHP_NODE_GLU_SWIGLU, /* GGML_OP_GLU, GGML_GLU_OP_SWIGLU: i32 [1] swapped; src[1] absent
                             (single tensor) or the second half (split form) */
     SHP_NODE_CONCAT,     /* GGML_OP_CONCAT: i32 {dim}; src[0], src[1] */
+    SHP_NODE_SUB,        /* GGML_OP_SUB */
+    SHP_NODE_TANH,       /* GGML_OP_UNARY, GGML_UNARY_OP_TANH */
+    SHP_NODE_SIGMOID,    /* GGML_OP_UNARY, GGML_UNARY_OP_SIGMOID */
+    SHP_NODE_ELU,        /* GGML_OP_UNARY, GGML_UNARY_OP_ELU */
+    SHP_NODE_GELU_ERF,   /* GGML_OP_UNARY, GGML_UNARY_OP_GELU_ERF */
+    SHP_NODE_CLAMP,      /* GGML_OP_CLAMP: f32 {min, max} */
+    SHP_NODE_NORM,       /* GGML_OP_NORM: f32 {eps} */
     SHP_NODE_OP_COUNT
 } shp_node_op;
 

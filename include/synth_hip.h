@@ -334,6 +334,30 @@ shp_status_t shp_sqr(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
 shp_status_t shp_cpy(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
 
 /*
+ * The activations and arithmetic the codec, vocoder and speech encoders put
+ * between their GEMMs, as ggml-CPU's vec forms compute them in f32 (the
+ * device's tanhf / expf / expm1f / erff, within the tolerance of glibc's):
+ *   shp_sub      ggml_sub, b as in shp_add (bit-identical)
+ *   shp_tanh     ggml_tanh (vits/waveform-decoder.cpp:228, kokoro/operations.cpp:133)
+ *   shp_sigmoid  ggml_sigmoid, 1 / (1 + expf(-x))
+ *   shp_elu      ggml_elu, x > 0 ? x : expm1f(x)
+ *   shp_gelu_erf ggml_gelu_erf, 0.5 x (1 + erff(x / sqrt 2)) (qwen3-tts/codec.cpp:222)
+ *   shp_clamp    ggml_clamp, MAX(MIN(x, hi), lo) with ggml's macros, so a NaN
+ *                gives hi (qwen3-tts/codec.cpp:481; bit-identical)
+ *   shp_norm     ggml_norm: (x - mean) / sqrtf(variance + eps) per row, mean
+ *                and variance summed in double (qwen3-tts/codec.cpp:216,
+ *                kokoro/operations.cpp:12,93)
+ * All F32; y has x's (a's) shape; rows contiguous, any row strides.
+ */
+shp_status_t shp_sub(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream);
+shp_status_t shp_tanh(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
+shp_status_t shp_sigmoid(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
+shp_status_t shp_elu(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
+shp_status_t shp_gelu_erf(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
+shp_status_t shp_clamp(const shp_tensor * x, float lo, float hi, shp_tensor * y, shp_stream_t stream);
+shp_status_t shp_norm(const shp_tensor * x, float eps, shp_tensor * y, shp_stream_t stream);
+
+/*
  * ggml_concat(a, b, dim): y of a's shape except y->ne[dim] = a->ne[dim] +
  * b->ne[dim]; y(i) = a(i) where i[dim] < a->ne[dim], else b(i) with
  * i[dim] - a->ne[dim]. All F32, rows contiguous (any row strides). The code

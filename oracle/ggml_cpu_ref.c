@@ -237,6 +237,9 @@ static void op_binary(const orc_node * n, int ith, int nth) {
                 case ORC_OP_MUL:
                     d[i] = a[i] * bv;
                     break;
+                case ORC_OP_SUB:
+                    d[i] = a[i] - bv;
+                    break;
                 default:
                     d[i] = a[i] / bv;
                     break;
@@ -270,8 +273,41 @@ static void op_binbcast(const orc_node * n, int ith, int nth) {
         for (int64_t k = 0; k < ne00 / ne10; ++k) {
             for (int64_t i = 0; i < ne10; ++i) {
                 const float av = a[k * ne10 + i], bv = br[i];
-                d[k * ne10 + i] = n->i[0] == ORC_OP_ADD ? av + bv : n->i[0] == ORC_OP_MUL ? av * bv : av / bv;
+                d[k * ne10 + i] = n->i[0] == ORC_OP_ADD ? av + bv :
+                                  n->i[0] == ORC_OP_MUL ? av * bv :
+                                  n->i[0] == ORC_OP_SUB ? av - bv :
+                                                          av / bv;
             }
+        }
+    }
+}
+
+/* ggml_norm (LayerNorm without the affine part): per row, the mean from a
+ * double sum, the centred values v = x - mean in f32, the variance from a
+ * double sum of v*v, scale = 1/sqrtf(variance + eps), y = v*scale; rows
+ * interleaved over threads. Sites: qwen3-tts/codec.cpp:216 (ConvNeXt),
+ * kokoro/operations.cpp:12,93. */
+static void op_norm(const orc_node * n, int ith, int nth) {
+    const int64_t ne0 = n->ne0;
+    const float   eps = n->f[0];
+    for (int64_t r = ith; r < n->nrows; r += nth) {
+        const float * x   = (const float *) n->src0 + r * ne0;
+        float *       y   = (float *) n->dst + r * ne0;
+        double        sum = 0.0;
+        for (int64_t i = 0; i < ne0; ++i) {
+            sum += (double) x[i];
+        }
+        const float mean = (float) (sum / (double) ne0);
+        double      sum2 = 0.0;
+        for (int64_t i = 0; i < ne0; ++i) {
+            const float v = x[i] - mean;
+            y[i]          = v;
+            sum2 += (double) (v * v);
+        }
+        const float variance = (float) (sum2 / (double) ne0);
+        const float scale    = 1.0f / sqrtf(variance + eps);
+        for (int64_t i = 0; i < ne0; ++i) {
+            y[i] *= scale;
         }
     }
 }
@@ -403,6 +439,42 @@ static void op_unary(const orc_node * n, int ith, int nth) {
                     y[i] = expf(x[i]);
                 }
                 break;
+            /* ggml-CPU's vec forms: ggml_vec_tanh_f32, _sigmoid_f32, _elu_f32,
+             * _gelu_erf_f32 and forward_clamp (MAX(MIN(x, max), min) with
+             * ggml's macros, so a NaN gives max). Sites: vits/waveform-
+             * decoder.cpp:228, kokoro/operations.cpp:133, qwen3-tts/codec.cpp:
+             * 222,481. */
+            case ORC_OP_TANH:
+                for (int64_t i = 0; i < ne0; ++i) {
+                    y[i] = tanhf(x[i]);
+                }
+                break;
+            case ORC_OP_SIGMOID:
+                for (int64_t i = 0; i < ne0; ++i) {
+                    y[i] = 1.0f / (1.0f + expf(-x[i]));
+                }
+                break;
+            case ORC_OP_ELU:
+                for (int64_t i = 0; i < ne0; ++i) {
+                    y[i] = (x[i] > 0.0f) ? x[i] : expm1f(x[i]);
+                }
+                break;
+            case ORC_OP_GELU_ERF: {
+                const float sqrt_2_inv = 0.70710678118654752440084436210484f;
+                for (int64_t i = 0; i < ne0; ++i) {
+                    const float v = x[i];
+                    y[i]          = 0.5f * v * (1.0f + erff(v * sqrt_2_inv));
+                }
+                break;
+            }
+            case ORC_OP_CLAMP: {
+                const float lo = n->f[0], hi = n->f[1];
+                for (int64_t i = 0; i < ne0; ++i) {
+                    const float m = x[i] < hi ? x[i] : hi;
+                    y[i]          = m > lo ? m : lo;
+                }
+                break;
+            }
             case ORC_OP_LEAKY_RELU: {
                 const float ns = n->f[0];
                 for (int64_t i = 0; i < ne0; ++i) {
@@ -574,7 +646,18 @@ static void run_node(const orc_node * n, int ith, int nth) {
         case ORC_OP_ADD:
         case ORC_OP_MUL:
         case ORC_OP_DIV:
+        case ORC_OP_SUB:
             op_binary(n, ith, nth);
+            break;
+        case ORC_OP_TANH:
+        case ORC_OP_SIGMOID:
+        case ORC_OP_ELU:
+        case ORC_OP_GELU_ERF:
+        case ORC_OP_CLAMP:
+            op_unary(n, ith, nth);
+            break;
+        case ORC_OP_NORM:
+            op_norm(n, ith, nth);
             break;
         case ORC_OP_RMS_NORM:
             op_rms_norm(n, ith, nth);

@@ -45,6 +45,13 @@ enum orc_op {
     ORC_OP_SOFT_MAX,     /* softmax(x*scale + mask) per row         ggml_soft_max_ext   */
     ORC_OP_CONT_F32,     /* strided F32 view -> contiguous          ggml_cont           */
     ORC_OP_BINBCAST,     /* add/mul/div, src1 repeated (can_repeat) ggml_add ...        */
+    ORC_OP_SUB,          /* dst = src0 - src1                       ggml_sub            */
+    ORC_OP_TANH,         /* tanhf(x)                                ggml_tanh           */
+    ORC_OP_SIGMOID,      /* 1/(1+expf(-x))                          ggml_sigmoid        */
+    ORC_OP_ELU,          /* x > 0 ? x : expm1f(x)                   ggml_elu            */
+    ORC_OP_GELU_ERF,     /* 0.5*x*(1+erff(x/sqrt(2)))               ggml_gelu_erf       */
+    ORC_OP_CLAMP,        /* MAX(MIN(x, f[1]), f[0])                 ggml_clamp          */
+    ORC_OP_NORM,         /* (x-mean)/sqrt(var+eps), f[0] = eps      ggml_norm           */
 };
 
 /*

@@ -24,7 +24,8 @@ LIB_PATH = os.path.join(HERE, "libggml_cpu_ref.so")
 F32, F16, Q8_0, Q5_K, I32, BF16 = 0, 1, 8, 13, 26, 30
 
 (OP_ADD, OP_MUL, OP_DIV, OP_RMS_NORM, OP_ROPE_NEOX, OP_SILU, OP_SIN, OP_SQR, OP_EXP, OP_LEAKY_RELU, OP_SCALE_BIAS,
- OP_GET_ROWS, OP_CAST_F32, OP_GLU_SWIGLU, OP_SOFT_MAX, OP_CONT_F32, OP_BINBCAST) = range(1, 18)
+ OP_GET_ROWS, OP_CAST_F32, OP_GLU_SWIGLU, OP_SOFT_MAX, OP_CONT_F32, OP_BINBCAST, OP_SUB, OP_TANH, OP_SIGMOID,
+ OP_ELU, OP_GELU_ERF, OP_CLAMP, OP_NORM) = range(1, 25)
 
 
 class OrcNode(ctypes.Structure):
@@ -150,6 +151,30 @@ class Graph:
 
     def leaky_relu(self, x, slope):
         return self._unary(OP_LEAKY_RELU, x, f=(slope,))
+
+    def tanh(self, x):
+        return self._unary(OP_TANH, x)
+
+    def sigmoid(self, x):
+        return self._unary(OP_SIGMOID, x)
+
+    def elu(self, x):
+        return self._unary(OP_ELU, x)
+
+    def gelu_erf(self, x):
+        return self._unary(OP_GELU_ERF, x)
+
+    def clamp(self, x, lo, hi):
+        return self._unary(OP_CLAMP, x, f=(lo, hi))
+
+    def norm(self, x, eps):
+        """ggml_norm: x (rows, ne0)."""
+        x = self._f32(x)
+        dst = np.empty(x.shape, dtype=np.float32)
+        return self._node(OP_NORM, dst, x, f=(eps,))
+
+    def sub(self, a, b):
+        return self._binary(OP_SUB, a, b)
 
     def scale_bias(self, x, s, b):
         return self._unary(OP_SCALE_BIAS, x, f=(s, b))

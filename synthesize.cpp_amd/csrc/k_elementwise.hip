@@ -37,7 +37,13 @@ enum EwOp {
     kDiv       = 9,
     kSin       = 10,
     kSqr       = 11,
-    kCopy      = 12
+    kCopy      = 12,
+    kSub       = 13,
+    kTanh      = 14,
+    kSigmoid   = 15,
+    kElu       = 16,
+    kGeluErf   = 17,
+    kClamp     = 18
 };
 
 // Snake family: y = x + sin(x*al)^2 / den with per-channel al and den.
@@ -127,6 +133,23 @@ template <int OP> __device__ __forceinline__ float ew(float a, float b, const Ew
         return a == 0.0f ? a : (sin_fast_ok(a) ? sin_f32_fast(a) : sinf(a));
     } else if constexpr (OP == kSqr) {
         return a * a;
+    } else if constexpr (OP == kSub) {
+        return a - b;
+    } else if constexpr (OP == kTanh) {
+        // ggml's vec forms of the codec / vocoder activations, in f32 with the
+        // device's math functions (vits/waveform-decoder.cpp:228,
+        // kokoro/operations.cpp:133, qwen3-tts/codec.cpp:222,481)
+        return tanhf(a);
+    } else if constexpr (OP == kSigmoid) {
+        return 1.0f / (1.0f + expf(-a));
+    } else if constexpr (OP == kElu) {
+        return a > 0.0f ? a : expm1f(a);
+    } else if constexpr (OP == kGeluErf) {
+        return 0.5f * a * (1.0f + erff(a * 0.70710678118654752440084436210484f));
+    } else if constexpr (OP == kClamp) {
+        // ggml's MAX(MIN(x, max), min): a NaN gives max
+        const float m = a < g.bias ? a : g.bias;
+        return m > g.scale ? m : g.scale;
     } else {
         static_assert(OP == kCopy, "unknown elementwise op");
         return a;
@@ -911,6 +934,8 @@ template <int OP> __device__ __forceinline__ float binop(float a, float b) {
         return a + b;
     } else if constexpr (OP == kMul) {
         return a * b;
+    } else if constexpr (OP == kSub) {
+        return a - b;
     } else {
         static_assert(OP == kDiv, "binary op");
         return a / b;
@@ -1437,6 +1462,37 @@ extern "C" shp_status_t shp_mul(const shp_tensor * a, const shp_tensor * b, shp_
 
 extern "C" shp_status_t shp_div(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream) {
     return binary_entry<kDiv>(a, b, y, stream);
+}
+
+extern "C" shp_status_t shp_sub(const shp_tensor * a, const shp_tensor * b, shp_tensor * y, shp_stream_t stream) {
+    return binary_entry<kSub>(a, b, y, stream);
+}
+
+extern "C" shp_status_t shp_tanh(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
+    return unary_entry<kTanh>(x, y, stream);
+}
+
+extern "C" shp_status_t shp_sigmoid(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
+    return unary_entry<kSigmoid>(x, y, stream);
+}
+
+extern "C" shp_status_t shp_elu(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
+    return unary_entry<kElu>(x, y, stream);
+}
+
+extern "C" shp_status_t shp_gelu_erf(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
+    return unary_entry<kGeluErf>(x, y, stream);
+}
+
+extern "C" shp_status_t shp_clamp(const shp_tensor * x, float lo, float hi, shp_tensor * y, shp_stream_t stream) {
+    EwPlan             plan;
+    const shp_status_t st = plan_ew(x, nullptr, false, y, nullptr, plan);
+    if (st != SHP_OK) {
+        return st;
+    }
+    plan.args.scale = lo;
+    plan.args.bias  = hi;
+    return launch_ew<kClamp, false, false, false>(plan.args, plan.flat, plan.vec, as_stream(stream));
 }
 
 extern "C" shp_status_t shp_sin(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {

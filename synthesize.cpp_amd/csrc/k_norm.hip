@@ -251,6 +251,37 @@ template <int WT, int MODE> __global__ __launch_bounds__(256) void k_rms_norm_ge
     }
 }
 
+// ggml_norm (LayerNorm without the affine part), one wave per row: the mean
+// from a double sum, the variance from a double sum of the f32 centred values
+// v = x - mean, scale = 1/sqrtf(variance + eps), y = v*scale (ggml-CPU's
+// order of roundings; the sums' order differs, within the tolerance). The
+// row is read three times, the later reads from cache. Sites:
+// qwen3-tts/codec.cpp:216 (ConvNeXt), kokoro/operations.cpp:12,93.
+__global__ __launch_bounds__(256) void k_layer_norm(const NormArgs a) {
+    const int     lane = threadIdx.x % kWave;
+    const int64_t row  = static_cast<int64_t>(blockIdx.x) * (256 / kWave) + threadIdx.x / kWave;
+    if (row >= a.nrows) {
+        return;
+    }
+    const float * xr  = reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.x) + row_offset(a.xm, row));
+    float *       yr  = reinterpret_cast<float *>(reinterpret_cast<char *>(a.y) + row_offset(a.ym, row));
+    double        acc = 0.0;
+    for (int i = lane; i < a.ne0; i += kWave) {
+        acc += static_cast<double>(xr[i]);
+    }
+    const float mean = static_cast<float>(group_sum<kWave>(acc) / static_cast<double>(a.ne0));
+    double      acc2 = 0.0;
+    for (int i = lane; i < a.ne0; i += kWave) {
+        const float v = xr[i] - mean;
+        acc2 += static_cast<double>(v * v);
+    }
+    const float variance = static_cast<float>(group_sum<kWave>(acc2) / static_cast<double>(a.ne0));
+    const float scale    = 1.0f / __builtin_sqrtf(variance + a.eps);
+    for (int i = lane; i < a.ne0; i += kWave) {
+        yr[i] = (xr[i] - mean) * scale;
+    }
+}
+
 template <int WT, int MODE> shp_status_t launch_norm(const NormArgs & a, bool vec, hipStream_t stream) {
     if (dry_run()) {
         return SHP_OK;
@@ -1095,6 +1126,33 @@ bool cache_view(const shp_tensor * cache, const shp_tensor * src, int64_t filled
 
 }  // namespace
 }  // namespace shp
+
+extern "C" shp_status_t shp_norm(const shp_tensor * x, float eps, shp_tensor * y, shp_stream_t stream) {
+    using namespace shp;
+    if (!well_formed(x) || !well_formed(y) || !(eps >= 0.0f)) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    if (x->type != SHP_TYPE_F32 || y->type != SHP_TYPE_F32) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    if (!same_shape(*x, *y) || x->ne[0] > INT32_MAX) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    if (dry_run()) {
+        return SHP_OK;
+    }
+    NormArgs a{};
+    a.x                  = static_cast<const float *>(x->data);
+    a.xm                 = make_rowmap(*x);
+    a.y                  = static_cast<float *>(y->data);
+    a.ym                 = make_rowmap(*y);
+    a.nrows              = nrows(*x);
+    a.ne0                = static_cast<int32_t>(x->ne[0]);
+    a.eps                = eps;
+    const int64_t blocks = (a.nrows + 3) / 4;
+    hipLaunchKernelGGL(k_layer_norm, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream), a);
+    return launch_status();
+}
 
 extern "C" shp_status_t shp_rms_norm_mul(const shp_tensor * x,
                                          const shp_tensor * w,

@@ -95,6 +95,7 @@ bool node_form_ok(const shp_node & n) {
         case SHP_NODE_ADD:
         case SHP_NODE_MUL:
         case SHP_NODE_DIV:
+        case SHP_NODE_SUB:
             return binary_ok(n);
         case SHP_NODE_SQR:
         case SHP_NODE_SIN:
@@ -102,7 +103,14 @@ bool node_form_ok(const shp_node & n) {
         case SHP_NODE_EXP:
         case SHP_NODE_LEAKY_RELU:
         case SHP_NODE_SCALE:
+        case SHP_NODE_TANH:
+        case SHP_NODE_SIGMOID:
+        case SHP_NODE_ELU:
+        case SHP_NODE_GELU_ERF:
+        case SHP_NODE_CLAMP:
             return unary_ok(n);
+        case SHP_NODE_NORM:
+            return unary_ok(n) && fparam(n, 0) >= 0.0f;
         case SHP_NODE_CPY:
             return (strided_src || (well_formed(&n.src[0]) && (n.src[0].type == SHP_TYPE_F32 ||
                                                                 n.src[0].type == SHP_TYPE_F16 ||
@@ -1357,6 +1365,20 @@ shp_status_t launch_single(const shp_node & n, shp_stream_t st) {
             return shp_glu_swiglu(&n.src[0], n.op_params[1], y, st);
         case SHP_NODE_CONCAT:
             return shp_concat(&n.src[0], &n.src[1], n.op_params[0], y, st);
+        case SHP_NODE_SUB:
+            return shp_sub(&n.src[0], &n.src[1], y, st);
+        case SHP_NODE_TANH:
+            return shp_tanh(&n.src[0], y, st);
+        case SHP_NODE_SIGMOID:
+            return shp_sigmoid(&n.src[0], y, st);
+        case SHP_NODE_ELU:
+            return shp_elu(&n.src[0], y, st);
+        case SHP_NODE_GELU_ERF:
+            return shp_gelu_erf(&n.src[0], y, st);
+        case SHP_NODE_CLAMP:
+            return shp_clamp(&n.src[0], fparam(n, 0), fparam(n, 1), y, st);
+        case SHP_NODE_NORM:
+            return shp_norm(&n.src[0], fparam(n, 0), y, st);
         default:
             return SHP_ERR_UNSUPPORTED;
     }

@@ -92,6 +92,13 @@ def load(path=None):
         "shp_cpy": [_PT, _PT, vp],
         "shp_cont_add_leaky_relu": [_PT, _PT, _PT, i32, f, _PT, _PT, vp],
         "shp_concat": [_PT, _PT, i32, _PT, vp],
+        "shp_sub": [_PT, _PT, _PT, vp],
+        "shp_tanh": [_PT, _PT, vp],
+        "shp_sigmoid": [_PT, _PT, vp],
+        "shp_elu": [_PT, _PT, vp],
+        "shp_gelu_erf": [_PT, _PT, vp],
+        "shp_clamp": [_PT, f, f, _PT, vp],
+        "shp_norm": [_PT, f, _PT, vp],
         "shp_graph_compute": [ctypes.POINTER(ShpNode), i32, vp],
         "shp_graph_plan": [ctypes.POINTER(ShpNode), i32, ctypes.POINTER(ShpGraphRun), i32, ctypes.POINTER(i32)],
     }
@@ -476,6 +483,53 @@ def cont_add_leaky_relu(x, b, r=None, slope=None, out=None, sum_out=None):
     return out
 
 
+def sub(a, b, out=None):
+    """ggml_sub(a, b), b as in add."""
+    out = a.new_empty(a.shape) if out is None else out
+    _check(load().shp_sub(_ref(desc(a)), _ref(desc(b)), _ref(desc(out)), _stream()), "sub")
+    return out
+
+
+def _unary_call(name, x, out):
+    out = x.new_empty(x.shape) if out is None else out
+    _check(getattr(load(), "shp_" + name)(_ref(desc(x)), _ref(desc(out)), _stream()), name)
+    return out
+
+
+def tanh(x, out=None):
+    """ggml_tanh."""
+    return _unary_call("tanh", x, out)
+
+
+def sigmoid(x, out=None):
+    """ggml_sigmoid."""
+    return _unary_call("sigmoid", x, out)
+
+
+def elu(x, out=None):
+    """ggml_elu."""
+    return _unary_call("elu", x, out)
+
+
+def gelu_erf(x, out=None):
+    """ggml_gelu_erf."""
+    return _unary_call("gelu_erf", x, out)
+
+
+def clamp(x, lo, hi, out=None):
+    """ggml_clamp(x, lo, hi)."""
+    out = x.new_empty(x.shape) if out is None else out
+    _check(load().shp_clamp(_ref(desc(x)), float(lo), float(hi), _ref(desc(out)), _stream()), "clamp")
+    return out
+
+
+def norm(x, eps, out=None):
+    """ggml_norm(x, eps)."""
+    out = x.new_empty(x.shape) if out is None else out
+    _check(load().shp_norm(_ref(desc(x)), float(eps), _ref(desc(out)), _stream()), "norm")
+    return out
+
+
 def concat(a, b, dim, out=None):
     """ggml_concat(a, b, dim) (dim a ggml dimension)."""
     import torch
@@ -500,7 +554,8 @@ def cpy(x, out=None):
 # ---------------------------------------------------------------------------
 
 (NODE_NOP, NODE_ADD, NODE_MUL, NODE_DIV, NODE_SQR, NODE_SIN, NODE_SCALE, NODE_CPY, NODE_GET_ROWS, NODE_RMS_NORM,
- NODE_SOFT_MAX, NODE_ROPE, NODE_LEAKY_RELU, NODE_SILU, NODE_EXP, NODE_GLU_SWIGLU, NODE_CONCAT) = range(17)
+ NODE_SOFT_MAX, NODE_ROPE, NODE_LEAKY_RELU, NODE_SILU, NODE_EXP, NODE_GLU_SWIGLU, NODE_CONCAT, NODE_SUB, NODE_TANH,
+ NODE_SIGMOID, NODE_ELU, NODE_GELU_ERF, NODE_CLAMP, NODE_NORM) = range(24)
 NODE_FLAG_OUTPUT = 1
 RUN_KINDS = {-1: "unsupported", 0: "nop", 1: "single", 2: "norm_mul", 3: "norm_mul_rope", 4: "add_norm_mul",
              5: "silu_mul", 6: "add_leaky", 7: "add_scale_leaky", 8: "snake", 9: "snake_guarded", 10: "snake_beta",
@@ -628,6 +683,27 @@ class Graph:
         """ggml_cont(x): x (typically a permuted view) copied into a new
         contiguous tensor of its shape; the same node kind as ggml_cpy."""
         return self._op(NODE_CPY, self._like(x), [x])
+
+    def sub(self, a, b):
+        return self._op(NODE_SUB, self._like(a), [a, b])
+
+    def tanh(self, x):
+        return self._op(NODE_TANH, self._like(x), [x])
+
+    def sigmoid(self, x):
+        return self._op(NODE_SIGMOID, self._like(x), [x])
+
+    def elu(self, x):
+        return self._op(NODE_ELU, self._like(x), [x])
+
+    def gelu_erf(self, x):
+        return self._op(NODE_GELU_ERF, self._like(x), [x])
+
+    def clamp(self, x, lo, hi):
+        return self._op(NODE_CLAMP, self._like(x), [x], floats={0: lo, 1: hi})
+
+    def norm(self, x, eps):
+        return self._op(NODE_NORM, self._like(x), [x], floats={0: eps})
 
     def concat(self, a, b, dim):
         """ggml_concat(a, b, dim) (dim a ggml dimension)."""

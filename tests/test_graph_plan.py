@@ -583,3 +583,16 @@ def test_concat_node():
     g = S.Graph()
     h = z(3, 8, dtype=torch.float16)
     assert kinds(g.plan(g.concat(h, h, 1))) == ["unsupported"]
+
+
+def test_codec_activation_nodes():
+    """ggml_sub, tanh, sigmoid, elu, gelu_erf, clamp and norm run as single
+    nodes (qwen3-tts/codec.cpp:216-222,481, vits/waveform-decoder.cpp:228,
+    kokoro/operations.cpp:12,133)."""
+    x = z(8, 64)
+    for build in (lambda g: g.sub(x, z(64)), lambda g: g.tanh(x), lambda g: g.sigmoid(x), lambda g: g.elu(x),
+                  lambda g: g.gelu_erf(x), lambda g: g.clamp(x, -1.0, 1.0), lambda g: g.norm(x, 1e-6)):
+        g = S.Graph()
+        assert kinds(g.plan(build(g))) == ["single"]
+    g = S.Graph()
+    assert kinds(g.plan(g.norm(x, -1.0))) == ["unsupported"]

@@ -567,3 +567,92 @@ def test_concat_against_an_element_loop(dim):
         want = a[idx] if k < na else b[tuple(k - na if j == 3 - dim else v for j, v in enumerate(idx))]
         assert bits(y[idx]) == bits(want)
     assert not np.array_equal(bits(R.concat(b, a, dim)), bits(y))
+
+
+# ---------------------------------------------------------------------------
+# the codec / vocoder elementwise ops, sub and LayerNorm
+# ---------------------------------------------------------------------------
+
+def _ulps(got, want):
+    """Distance in f32 ulps of `want`'s binade (want in double)."""
+    want = np.asarray(want, np.float64)
+    ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+    return np.abs(np.asarray(got, np.float64) - want) / ulp
+
+
+def _grid():
+    rng = np.random.default_rng(77)
+    return np.concatenate([rng.standard_normal(4000) * 3, rng.uniform(-30, 30, 2000),
+                           np.linspace(-1e-3, 1e-3, 100)]).astype(np.float32).reshape(61, -1)
+
+
+def test_tanh_sigmoid_elu_gelu_against_double_closed_forms():
+    x = _grid()
+    g = R.Graph()
+    t, s, e, ge = g.tanh(x), g.sigmoid(x), g.elu(x), g.gelu_erf(x)
+    g.compute(2)
+    xd = x.astype(np.float64)
+    assert _ulps(t, np.tanh(xd)).max() <= 2
+    assert _ulps(s, 1.0 / (1.0 + np.exp(-xd))).max() <= 4
+    pos = x > 0
+    assert np.array_equal(bits(e[pos]), bits(x[pos]))
+    assert _ulps(e[~pos], np.expm1(xd[~pos])).max() <= 2
+    import math
+    gd = 0.5 * xd * (1.0 + np.vectorize(math.erf)(xd / math.sqrt(2.0)))
+    # ggml's formula adds erff's result to 1 in f32, so for x < 0 the error is
+    # absolute: about |x|/2 times an ulp of 1 (the cancellation), plus a few
+    # ulps of the result
+    bound = 2.0 * np.abs(xd) * 2.0 ** -24 + 4 * np.spacing(np.abs(gd).astype(np.float32))
+    assert (np.abs(ge - gd) <= bound).all()
+    # a planted mistake: the tanh approximation of GELU is not this op
+    ga = 0.5 * xd * (1.0 + np.tanh(math.sqrt(2.0 / math.pi) * (xd + 0.044715 * xd ** 3)))
+    assert np.abs(ge - ga).max() > 1e-4
+
+
+def test_elementwise_special_values():
+    sp = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-40, 88.0, -104.0, 1e30, -1e30, 3.0],
+                  dtype=np.float32).reshape(1, -1)
+    g = R.Graph()
+    t, s, e, c = g.tanh(sp), g.sigmoid(sp), g.elu(sp), g.clamp(sp, -1.0, 1.0)
+    g.compute(1)
+    assert bits(t[0, 0]) == bits(np.float32(0.0)) and bits(t[0, 1]) == bits(np.float32(-0.0))
+    assert t[0, 2] == 1.0 and t[0, 3] == -1.0 and np.isnan(t[0, 4])
+    assert s[0, 0] == 0.5 and s[0, 2] == 1.0 and s[0, 3] == 0.0 and np.isnan(s[0, 4])
+    assert bits(e[0, 1]) == bits(np.float32(-0.0)) and e[0, 3] == -1.0 and np.isnan(e[0, 4])
+    # ggml's clamp is MAX(MIN(x, max), min): NaN gives max; fminf/fmaxf would give min or max differently
+    assert c[0, 4] == 1.0
+    np.testing.assert_array_equal(c[0, [0, 2, 3, 9, 10, 11]], np.float32([0.0, 1.0, -1.0, 1.0, -1.0, 1.0]))
+
+
+def test_sub_and_its_repeat_forms():
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal((6, 40)).astype(np.float32)
+    b = rng.standard_normal((6, 40)).astype(np.float32)
+    row = rng.standard_normal(40).astype(np.float32)
+    col = rng.standard_normal((6, 1)).astype(np.float32)
+    g = R.Graph()
+    y1, y2, y3 = g.sub(a, b), g.sub(a, row), g.sub(a, col)
+    y4 = g.binbcast(R.OP_SUB, a, rng.standard_normal((3, 20)).astype(np.float32))
+    g.compute(2)
+    np.testing.assert_array_equal(bits(y1), bits(a - b))
+    np.testing.assert_array_equal(bits(y2), bits(a - row))
+    np.testing.assert_array_equal(bits(y3), bits(a - col))
+    assert not np.array_equal(bits(y1), bits(b - a))
+
+
+def test_norm_against_double_and_invariants():
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal((16, 1024)) * 3 + 5).astype(np.float32)
+    g = R.Graph()
+    y = g.norm(x, 1e-6)
+    const = g.norm(np.full((2, 64), 7.0, np.float32), 1e-5)
+    tiny = g.norm((rng.standard_normal((2, 64)) * 1e-4).astype(np.float32), 1e-5)
+    g.compute(3)
+    xd = x.astype(np.float64)
+    m = xd.mean(axis=1, keepdims=True)
+    want = (xd - m) / np.sqrt(((xd - m) ** 2).mean(axis=1, keepdims=True) + 1e-6)
+    assert np.abs(y - want).max() <= 1e-5
+    assert np.abs(y.mean(axis=1)).max() < 1e-5 and np.abs(y.var(axis=1) - 1).max() < 1e-4
+    assert (const == 0).all()
+    # eps is inside the sqrt: with variance ~1e-8 the result is far below 1 in size
+    assert np.abs(tiny).max() < 0.1
