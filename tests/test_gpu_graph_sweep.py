@@ -146,3 +146,114 @@ def test_sweep_exercises_the_moved_launch(gpu):
         else:
             apart += 1
     assert taken >= CASES // 3 and apart >= 1, (taken, apart)
+
+
+# ---------------------------------------------------------------------------
+# the vocoder / codec tails: the conv-tail, codec transpose-bias and
+# view -> binary runs, with readers of the intermediates, outputs flagged,
+# and outputs placed over the source's memory
+# ---------------------------------------------------------------------------
+
+TAIL_CASES = 48
+
+
+def _tail_case(gpu, seed):
+    import torch
+    rng = np.random.default_rng(SEED + 20000 + seed)
+    kind = str(rng.choice(["conv_tail", "codec_tconv", "codec_dw", "crop_bias"]))
+    T = int(rng.choice([64, 130, 1000, 2048]))
+    C = int(rng.choice([8, 37, 64, 96]))
+    kept = T - int(rng.integers(0, 9))
+    resid = bool(rng.integers(0, 2))
+    leaky = bool(rng.integers(0, 2))
+    crop_copy = bool(rng.integers(0, 2))
+    extra = str(rng.choice(["none", "none", "read_first", "read_mid", "flag_mid", "over_source"]))
+    host = {"src": rng.standard_normal((C, T)).astype(np.float32),       # ggml [T, C]
+            "srcT": rng.standard_normal((T, C)).astype(np.float32),      # ggml [C, T]
+            "bC1": rng.standard_normal((C, 1)).astype(np.float32),       # ggml [1, C]
+            "bC": rng.standard_normal(C).astype(np.float32),             # ggml [C]
+            "r": rng.standard_normal((C, T)).astype(np.float32)}
+    dev = {n: _t(gpu, a) for n, a in host.items()}
+
+    def restore():
+        for n in ("src", "srcT", "r"):
+            dev[n].copy_(torch.from_numpy(host[n]).cuda())
+        torch.cuda.synchronize()
+
+    def build(all_outputs):
+        g = gpu.Graph()
+        outs, first, mid = [], None, None
+        if kind == "conv_tail":                      # vits: cont(transpose(out)) + bias [+ r] [-> leaky]
+            o = dev["srcT"]
+            first = g.cont(g.view(o, o.t()))          # ggml [T, C]
+            mid = g.add(first, dev["bC1"])
+            last = g.add(mid, dev["r"]) if resid else mid
+            if leaky:
+                if extra == "over_source":            # the result over the source's bytes, other layout
+                    last = g._op(gpu.NODE_LEAKY_RELU, dev["srcT"].view(C, T), [last], floats={0: 0.1})
+                else:
+                    last = g.leaky_relu(last, 0.1)
+        elif kind == "codec_tconv":                   # qwen3 codec: [cont(crop)] + bias [1, C] -> cont(transpose)
+            w = dev["src"]
+            first = g.cont(g.view(w, w[:, :kept])) if crop_copy else g.view(w, w[:, :kept])
+            mid = g.add(first, dev["bC1"])
+            if extra == "over_source":
+                last = g._op(gpu.NODE_CPY, dev["src"].view(-1)[:kept * C].view(kept, C), [g.view(mid, mid.t.t())])
+            else:
+                last = g.cont(g.view(mid, mid.t.t()))
+        elif kind == "codec_dw":                      # cont(transpose(mm)), cont(first rows), + bias [C]
+            m = dev["src"]
+            first = g.cont(g.view(m, m.t()))          # ggml [C, T]
+            mid = g.cont(g.view(first, first.t[:kept]))
+            last = g.add(mid, dev["bC"])
+        else:                                         # crop, + row bias (view -> binary)
+            w = dev["srcT"]
+            first = g.cont(g.view(w, w[:kept]))
+            mid = first
+            last = g.add(first, dev["bC"])
+        outs.append(last)
+        if extra == "read_first" and isinstance(first, gpu.GVal) and first.node["op"] != gpu.NODE_NOP:
+            outs.append(g.exp(first))
+        elif extra == "read_mid" and mid is not None:
+            outs.append(g.exp(mid))
+        elif extra == "flag_mid" and mid is not None:
+            outs.append(mid)
+        every = outs + [n["val"] for n in g.order(*outs)] if all_outputs else outs
+        return g, outs, every
+
+    return build, restore, dev, (kind, T, C, kept, resid, leaky, crop_copy, extra)
+
+
+@pytest.mark.parametrize("seed", range(TAIL_CASES))
+def test_tail_runs_equal_node_by_node(gpu, seed):
+    import torch
+    build, restore, dev, desc_ = _tail_case(gpu, seed)
+    print("tail case", seed, desc_, flush=True)
+    results = []
+    for every_node in (False, True):
+        restore()
+        g, outs, every = build(every_node)
+        kinds = [k for k, *_ in g.plan(*every) if k != "nop"]
+        print("plan", every_node, kinds, flush=True)
+        g.compute(*every)
+        torch.cuda.synchronize()
+        results.append(([_np(o.t).copy() for o in outs], [_np(dev[n]).copy() for n in ("src", "srcT", "r")]))
+    (fo, fm), (so, sm) = results
+    for a, b in zip(fo, so):
+        assert_bitexact(a, b)
+    for a, b in zip(fm, sm):
+        assert_bitexact(a, b)
+
+
+def test_tail_sweep_exercises_the_runs(gpu):
+    """Across the cases, each tail run is taken somewhere and kept apart
+    somewhere (by a reader, a flag or an overlapping output)."""
+    seen, apart = set(), 0
+    for seed in range(TAIL_CASES):
+        build, restore, dev, d_ = _tail_case(gpu, seed)
+        g, outs, _ = build(False)
+        kinds = [k for k, *_ in g.plan(*outs) if k != "nop"]
+        seen.update(k for k in kinds if k in ("cont_add_leaky", "view_binary"))
+        if d_[-1] != "none" and "cont_add_leaky" not in kinds and "view_binary" not in kinds:
+            apart += 1
+    assert seen == {"cont_add_leaky", "view_binary"} and apart >= 1, (seen, apart)
