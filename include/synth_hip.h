@@ -375,7 +375,10 @@ shp_status_t shp_concat(const shp_tensor * a, const shp_tensor * b, int32_t dim,
  * when apply_leaky (sum, if given, receives s), else y = s (sum must be NULL).
  * Each add is one f32 rounding, in that order, so y and sum are bit-identical
  * to the nodes one by one.
- *   x:   an F32 transposed or permuted view as shp_cpy takes it
+ *   x:   an F32 transposed or permuted view as shp_cpy takes it, ne[0]
+ *        strided; a view with nb[0] == 4 (the transpose of a one-channel
+ *        [1, T] result) is SHP_ERR_UNSUPPORTED: its ggml_cont is a plain
+ *        copy, and such a tail runs as its nodes
  *   b:   F32 [1, ne1, ne2, ne3]: one value per row of y, rows evenly
  *        strided; or F32 [ne0]: one row repeated over y's rows (the channel
  *        bias of a channel-major result, qwen3-tts/codec.cpp:58-59,134-140,

@@ -8,7 +8,11 @@ forms, against the ggml-CPU restatement on the same inputs:
   codebooks (1..33 for Q5_K);
 - Snake channel counts that are and are not multiples of 4, ragged last
   blocks everywhere;
-- the one-call layer step at 1..513 positions.
+- the one-call layer step at 1..513 positions;
+- the transposing copy over 2-4-D permutations and unaligned starts, the
+  fused conv tail with either bias form, every repeat form of
+  add/sub/mul/div, concat along every dimension, LayerNorm and the
+  activations.
 The bars are test_gpu_parity.py's: bit-exact for gathers, sums of gathers,
 adds and leaky-ReLU; 1e-5 relative for the norms, SwiGLU and the Snake
 family; rope to 1e-5 of its NEOX pair against libm and bit-exact against the
@@ -20,6 +24,7 @@ import numpy as np
 import pytest
 
 import formats as F
+from test_gpu_activations import _close as _act_close, _inputs as _act_inputs
 import ggml_ref as R
 from test_gpu_parity import (_dev_table, _dev_w, _np, _positions, _specials, _t, _table, _ulps_apart, _weights,
                              assert_bitexact, assert_close, assert_rope_close, assert_snake_close)
@@ -326,3 +331,132 @@ def test_sweep_add_leaky_relu(gpu, rows, ne0):
     s, y = gpu.add_leaky_relu(_t(gpu, a), _t(gpu, b), float(slope), want_sum=True)
     assert_bitexact(_np(s), s_ref)
     assert_bitexact(_np(y), y_ref)
+
+
+# ---------------------------------------------------------------------------
+# the vocoder / codec neighbours: the transposing copy and the fused tail,
+# repeated operands, concat, LayerNorm, the activations
+# ---------------------------------------------------------------------------
+
+_PERMS = {2: [(1, 0)], 3: [(1, 2, 0), (0, 2, 1), (2, 0, 1), (2, 1, 0)],
+          4: [(0, 3, 1, 2), (3, 0, 1, 2), (0, 1, 3, 2), (3, 2, 1, 0), (1, 0, 3, 2)]}
+
+
+def _transpose_case(rng):
+    nd = int(rng.integers(2, 5))
+    shape = tuple(int(_pick(rng, [1, 2, 3, 5, 17, 64, 100, 128, 255, 1000])) for _ in range(nd))
+    shape = shape[:-1] + (max(shape[-1], 2),)      # the contiguous axis has extent > 1
+    perm = _pick(rng, _PERMS[nd])
+    if perm[-1] == nd - 1 or int(np.prod(shape)) > MAX_ELEMS:
+        return None
+    return (shape, perm, int(rng.integers(0, 4)))
+
+
+@pytest.mark.parametrize("shape,perm,shift", _gen("transpose", _transpose_case))
+def test_sweep_transposing_copy(gpu, shape, perm, shift):
+    rng = np.random.default_rng([SWEEP_SEED, 29, *shape, shift])
+    base = rng.standard_normal(int(np.prod(shape)) + shift).astype(np.float32)
+    tb = _t(gpu, base)
+    x = tb[shift:].view(shape)
+    v = x.permute(perm)
+    d = gpu.desc(v)
+    g = R.Graph()
+    ref = g.cont_f32(base, list(d.ne), list(d.nb), offset=4 * shift)
+    g.compute(8)
+    assert_bitexact(_np(gpu.cpy(v)), ref.reshape(tuple(v.shape)))
+
+
+def _tail_case(rng):
+    T, C = _pick(rng, [3, 64, 130, 1000, 2048, 4099]), _pick(rng, [2, 4, 37, 64, 96, 256])
+    if T * C > MAX_ELEMS:
+        return None
+    leaky = int(rng.integers(0, 2))
+    return (T, C, _pick(rng, ["row", "col"]), int(rng.integers(0, 2)), leaky,
+            leaky * int(rng.integers(0, 2)), int(rng.integers(0, 2)))
+
+
+@pytest.mark.parametrize("T,C,form,resid,leaky,with_sum,shift", _gen("cont_add_leaky", _tail_case))
+def test_sweep_cont_add_leaky(gpu, T, C, form, resid, leaky, with_sum, shift):
+    """y = cont(out^T) + b [+ r] [-> leaky], b one value per row ([1, C]) or
+    one row ([ne0]) of y, out ggml [C, T] starting 0 or 1 float off 16 bytes."""
+    import torch
+    rng = np.random.default_rng([SWEEP_SEED, 31, T, C, resid, leaky, with_sum, shift])
+    base = rng.standard_normal(T * C + shift).astype(np.float32)
+    out = base[shift:].reshape(T, C)
+    b = rng.standard_normal((C, 1) if form == "row" else (T,)).astype(np.float32)
+    r = rng.standard_normal((C, T)).astype(np.float32) if resid else None
+    tb = _t(gpu, base)
+    view = tb[shift:].view(T, C).t()
+    s_out = torch.empty((C, T), dtype=torch.float32, device="cuda") if with_sum else None
+    y = gpu.cont_add_leaky_relu(view, _t(gpu, b), _t(gpu, r) if resid else None, 0.1 if leaky else None,
+                                sum_out=s_out)
+    g = R.Graph()
+    tm = g.cont_f32(out, [T, C], [4 * C, 4]).reshape(C, T)
+    s_ = g.binbcast(R.OP_ADD, tm, b if form == "row" else b.reshape(1, T))
+    if resid:
+        s_ = g.add(s_, r)
+    yr = g.leaky_relu(s_, 0.1) if leaky else s_
+    g.compute(4)
+    assert_bitexact(_np(y), yr)
+    if with_sum:
+        assert_bitexact(_np(s_out), s_)
+
+
+def _repeat_case(rng):
+    nd = int(rng.integers(2, 5))
+    ashape = [int(_pick(rng, [1, 2, 3, 4, 6, 12, 37, 64, 100, 1000])) for _ in range(nd)]
+    bshape = []
+    for n in ashape:
+        divs = [d for d in (1, 2, 3, 4, 6, n) if n % d == 0]
+        bshape.append(int(_pick(rng, divs)))
+    if int(np.prod(ashape)) > MAX_ELEMS or ashape == bshape:
+        return None
+    return (tuple(ashape), tuple(bshape), _pick(rng, ["add", "sub", "mul", "div"]))
+
+
+@pytest.mark.parametrize("ashape,bshape,op", _gen("repeat", _repeat_case))
+def test_sweep_repeated_operand(gpu, ashape, bshape, op):
+    rng = np.random.default_rng([SWEEP_SEED, 37, *ashape, *bshape])
+    a = rng.standard_normal(ashape).astype(np.float32)
+    b = (rng.standard_normal(bshape) + 2.5).astype(np.float32)
+    code = {"add": R.OP_ADD, "sub": R.OP_SUB, "mul": R.OP_MUL, "div": R.OP_DIV}[op]
+    assert_bitexact(_np(getattr(gpu, op)(_t(gpu, a), _t(gpu, b))), R.run(lambda g: g.binbcast(code, a, b)))
+
+
+def _concat_case(rng):
+    nd = int(rng.integers(1, 5))
+    shape = [int(_pick(rng, [1, 2, 3, 7, 64, 100, 1024])) for _ in range(nd)]
+    dim = int(rng.integers(0, nd))
+    other = list(shape)
+    other[nd - 1 - dim] = int(_pick(rng, [1, 2, 5, 64]))
+    if int(np.prod(shape)) + int(np.prod(other)) > MAX_ELEMS:
+        return None
+    return (tuple(shape), tuple(other), dim)
+
+
+@pytest.mark.parametrize("ashape,bshape,dim", _gen("concat", _concat_case))
+def test_sweep_concat(gpu, ashape, bshape, dim):
+    rng = np.random.default_rng([SWEEP_SEED, 41, *ashape, *bshape, dim])
+    a = rng.standard_normal(ashape).astype(np.float32)
+    b = rng.standard_normal(bshape).astype(np.float32)
+    ref = R.concat(a, b, dim)
+    got = _np(gpu.concat(_t(gpu, a), _t(gpu, b), dim))
+    assert_bitexact(got.reshape(ref.shape), ref)
+
+
+@pytest.mark.parametrize("rows,ne0,wkind", _gen("norm", lambda r: _norm_case(r, ["none"])))
+def test_sweep_layer_norm(gpu, rows, ne0, wkind):
+    rng = np.random.default_rng([SWEEP_SEED, 43, rows, ne0])
+    x = (rng.standard_normal((rows, ne0)) * 2 + 1).astype(np.float32)
+    got = _np(gpu.norm(_t(gpu, x), 1e-5))
+    assert np.abs(got - R.run(lambda g: g.norm(x, 1e-5))).max() <= 1e-5
+
+
+@pytest.mark.parametrize("rows,ne0", _gen("activations", _flat_case))
+def test_sweep_activations(gpu, rows, ne0):
+    rng = np.random.default_rng([SWEEP_SEED, 47, rows, ne0])
+    x = _act_inputs(rng, (rows, ne0))
+    tx = _t(gpu, x)
+    for op in ("tanh", "sigmoid", "elu", "gelu_erf"):
+        _act_close(_np(getattr(gpu, op)(tx)), R.run(lambda g: getattr(g, op)(x)), x if op == "gelu_erf" else None)
+    assert_bitexact(_np(gpu.clamp(tx, -2.0, 2.0)), R.run(lambda g: g.clamp(x, -2.0, 2.0)))

@@ -189,6 +189,16 @@ def test_transposing_copy_refuses_an_overlapping_destination(gpu):
         gpu.cont_add_leaky_relu(x.t(), torch.zeros((64, 1), device="cuda"), None, 0.1, out=x)
 
 
+def test_conv_tail_refuses_a_contiguous_view(gpu):
+    """One channel: the transpose of ggml [1, T] has ne[0] contiguous, so its
+    ggml_cont is a plain copy, not this entry point's form: refused, nothing
+    launched."""
+    import torch
+    x = torch.zeros((256, 1), dtype=torch.float32, device="cuda")
+    with pytest.raises(gpu.ShpError):
+        gpu.cont_add_leaky_relu(x.t(), torch.zeros((1, 1), device="cuda"), None, 0.1)
+
+
 def test_conv_tail_in_a_node_list(gpu):
     """Two resblock convolutions' tails in one list (:146-150): copy, bias,
     leaky into the next GEMM's input; copy, bias, residual add, the next

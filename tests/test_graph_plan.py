@@ -482,6 +482,12 @@ def test_conv_tail_runs():
     g = S.Graph()
     tm = g.cont(g.view(out, out.t()))
     assert "cont_add_leaky" not in kinds(g.plan(g.leaky_relu(g.add(tm, z(T // 2)), 0.1)))
+    # one channel: the transpose of [1, T] has ne[0] contiguous, so its copy is
+    # a plain copy of a row-contiguous view, which the bias add reads in place
+    g = S.Graph()
+    out1 = z(T, 1)
+    tm = g.cont(g.view(out1, out1.t()))
+    assert kinds(g.plan(g.leaky_relu(g.add(tm, z(1, 1)), 0.1))) == ["view_binary", "single"]
 
 
 def test_view_copy_then_binary():
