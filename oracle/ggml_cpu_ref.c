@@ -574,6 +574,42 @@ static void op_cont_f32(const orc_node * n, int ith, int nth) {
     }
 }
 
+/* ggml_im2col(kernel, x, s0, 0, p0, 0, d0, 0, is_2D = false, dst_type), the
+ * 1-D form every call site uses (vits/waveform-decoder.cpp:104,
+ * vits/operations.cpp:40,103, kokoro/operations.cpp:76,
+ * omnivoice/codec.cpp:114, omnivoice/reference-encoder.cpp:190,
+ * qwen3-tts/codec.cpp:96,129, qwen3-tts/speaker-encoder.cpp:174,
+ * qwen3-tts/codec-encoder.cpp:359). The kernel tensor gives only its extent K.
+ * With x F32 [IW, IC, N] (rows contiguous) and OW = (IW + 2*p0 - d0*(K-1) -
+ * 1)/s0 + 1 (ggml_calc_conv_output_size, C division), the dst [IC*K, OW, N]
+ * holds dst[n][ow][ic*K + k] = x[n][ic][ow*s0 + k*d0 - p0], and 0 where that
+ * index falls outside [0, IW): a pure gather, no arithmetic. An F16 dst holds
+ * each value rounded to nearest even. ggml-CPU hands thread ith the channels
+ * ith, ith + nth, ... of every (n, ow). */
+static void op_im2col(const orc_node * n, int ith, int nth) {
+    const int64_t * v  = (const int64_t *) n->src1;
+    const int64_t   IW = v[0], IC = v[1], N = v[2], K = v[3], s0 = v[4], p0 = v[5], d0 = v[6];
+    const int64_t   OW = (IW + 2 * p0 - d0 * (K - 1) - 1) / s0 + 1;
+    const float *   x  = (const float *) n->src0;
+    for (int64_t in = 0; in < N; ++in) {
+        for (int64_t ow = 0; ow < OW; ++ow) {
+            for (int64_t ic = ith; ic < IC; ic += nth) {
+                const float * row = x + (in * IC + ic) * IW;
+                const int64_t o   = ((in * OW + ow) * IC + ic) * K;
+                for (int64_t k = 0; k < K; ++k) {
+                    const int64_t iw  = ow * s0 + k * d0 - p0;
+                    const float   val = (iw < 0 || iw >= IW) ? 0.0f : row[iw];
+                    if (n->type0 == ORC_F16) {
+                        ((uint16_t *) n->dst)[o + k] = orc_fp32_to_fp16(val);
+                    } else {
+                        ((float *) n->dst)[o + k] = val;
+                    }
+                }
+            }
+        }
+    }
+}
+
 /* ggml_swiglu (single tensor): gate = first half of each row (second when
  * swapped), y = silu(gate) * other half. */
 static void op_glu_swiglu(const orc_node * n, int ith, int nth) {
@@ -690,6 +726,9 @@ static void run_node(const orc_node * n, int ith, int nth) {
             break;
         case ORC_OP_BINBCAST:
             op_binbcast(n, ith, nth);
+            break;
+        case ORC_OP_IM2COL:
+            op_im2col(n, ith, nth);
             break;
         default:
             atomic_store(&g_node_error, -1);

@@ -52,6 +52,7 @@ enum orc_op {
     ORC_OP_GELU_ERF,     /* 0.5*x*(1+erff(x/sqrt(2)))               ggml_gelu_erf       */
     ORC_OP_CLAMP,        /* MAX(MIN(x, f[1]), f[0])                 ggml_clamp          */
     ORC_OP_NORM,         /* (x-mean)/sqrt(var+eps), f[0] = eps      ggml_norm           */
+    ORC_OP_IM2COL,       /* 1-D convolution columns                 ggml_im2col         */
 };
 
 /*
@@ -81,6 +82,10 @@ enum orc_op {
  *   CONT_F32  : src0 = the first element of an F32 view, src1 = int64_t[8]
  *               (the view's ne[0..3], then its byte strides nb[0..3]); dst
  *               contiguous. The only op whose src0 is not contiguous.
+ *   IM2COL    : src0 = F32 x [IW, IC, N]; src1 = int64_t[7] {IW, IC, N, K,
+ *               s0, p0, d0}; type0 = the dst type, ORC_F32 or ORC_F16; dst
+ *               [IC*K, OW, N], OW = (IW + 2*p0 - d0*(K-1) - 1)/s0 + 1 (C
+ *               division).
  */
 typedef struct orc_node {
     int32_t      op;

@@ -25,7 +25,7 @@ F32, F16, Q8_0, Q5_K, I32, BF16 = 0, 1, 8, 13, 26, 30
 
 (OP_ADD, OP_MUL, OP_DIV, OP_RMS_NORM, OP_ROPE_NEOX, OP_SILU, OP_SIN, OP_SQR, OP_EXP, OP_LEAKY_RELU, OP_SCALE_BIAS,
  OP_GET_ROWS, OP_CAST_F32, OP_GLU_SWIGLU, OP_SOFT_MAX, OP_CONT_F32, OP_BINBCAST, OP_SUB, OP_TANH, OP_SIGMOID,
- OP_ELU, OP_GELU_ERF, OP_CLAMP, OP_NORM) = range(1, 25)
+ OP_ELU, OP_GELU_ERF, OP_CLAMP, OP_NORM, OP_IM2COL) = range(1, 26)
 
 
 class OrcNode(ctypes.Structure):
@@ -250,6 +250,26 @@ class Graph:
         self.keep += [dst, buf, view]
         return dst
 
+    def im2col(self, x, k, s0, p0, d0, dst_type=F32):
+        """ggml_im2col(kernel [k, IC, ...], x, s0, 0, p0, 0, d0, 0, false,
+        dst_type): x numpy (N, IC, IW) or (IC, IW) = ggml [IW, IC, N]. Returns
+        numpy (N, OW, IC*k) = ggml [IC*k, OW, N]: float32, or uint16 F16 bits
+        for dst_type F16."""
+        x = self._f32(x)
+        x = x.reshape((1,) * (3 - x.ndim) + x.shape)
+        n_, ic, iw = x.shape
+        ow = conv_out_len(iw, k, s0, p0, d0)
+        if ow < 1 or dst_type not in (F32, F16):
+            raise ValueError("im2col: no output position, or a dst type other than F32/F16")
+        view = np.array([iw, ic, n_, k, s0, p0, d0], dtype=np.int64)
+        dst = np.empty((n_, ow, ic * k), dtype=np.float32 if dst_type == F32 else np.uint16)
+        nd = OrcNode()
+        nd.op, nd.type0, nd.ne0, nd.nrows = OP_IM2COL, dst_type, ic * k, n_ * ow
+        nd.src0, nd.src1, nd.dst = _ptr(x), _ptr(view), _ptr(dst)
+        self.nodes.append(nd)
+        self.keep += [dst, x, view]
+        return dst
+
     def glu_swiglu(self, a, swapped=False):
         a = self._f32(a)
         nc = a.shape[-1] // 2
@@ -293,6 +313,13 @@ class Graph:
 # ---------------------------------------------------------------------------
 # node runs the reference graph builders emit
 # ---------------------------------------------------------------------------
+
+def conv_out_len(iw, k, s0, p0, d0):
+    """ggml_calc_conv_output_size: (iw + 2*p0 - d0*(k-1) - 1)/s0 + 1 with C's
+    truncating division."""
+    num = iw + 2 * p0 - d0 * (k - 1) - 1
+    return (num // s0 if num >= 0 else -((-num) // s0)) + 1
+
 
 def concat(a, b, dim):
     """ggml_concat(a, b, dim) restated (data movement only: every element of

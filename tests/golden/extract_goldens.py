@@ -11,6 +11,8 @@ Sources:
   G1 tests/qwen3_tts_decoder_layer_test.cpp:30-47   (kExpectedHidden, config)
   G2 tests/qwen3_tts_code_predictor_test.cpp:33-61  (logits, codes, summed embedding)
   G3 tests/qwen3_tts_codec_ops_test.cpp:34-82       (kExpectedSnakeBeta, config)
+  G5 tests/qwen3_tts_codec_ops_test.cpp:34-94,184-210 (kExpectedCausalConv,
+     kExpectedDepthwise, kExpectedTransposed, kExpectedConvNeXt, fill order)
 """
 import json
 import os
@@ -97,7 +99,32 @@ def main():
         "expected_snake_beta": literal_array(t, "kExpectedSnakeBeta"),
     }
 
-    for name, obj in (("qwen3_decoder_layer", g1), ("qwen3_code_predictor", g2), ("qwen3_codec_snake_beta", g3)):
+    C, L, OC, K, S = (constant(t, n) for n in ("kChannels", "kLength", "kOutChannels", "kKernel", "kStride"))
+    g5 = {
+        "source": "tests/qwen3_tts_codec_ops_test.cpp:34-94,184-210,249-251",
+        "length": L, "channels": C, "out_channels": OC, "kernel": K, "stride": S,
+        "dilation": constant(t, "kDilation"), "seed": constant(t, "kSeed"),
+        # (tensor, element count, scale, offset) in LCG fill order (:185-210);
+        # the signal is drawn channel-major and laid out channels fastest (:216-226)
+        "fill_order": [["signal", C * L, 0.5, 0.0], ["conv_weight", K * C * OC, 0.5, 0.0],
+                       ["conv_bias", OC, 0.25, 0.0], ["depthwise_weight", K * C, 0.5, 0.0],
+                       ["depthwise_bias", C, 0.25, 0.0], ["transposed_weight", 2 * S * OC * C, 0.5, 0.0],
+                       ["transposed_bias", OC, 0.25, 0.0], ["snake_alpha", C, 0.5, 0.0],
+                       ["snake_beta", C, 0.5, 0.0], ["dwconv_weight", 7 * C, 0.5, 0.0],
+                       ["dwconv_bias", C, 0.25, 0.0], ["norm_weight", C, 0.25, 1.0], ["norm_bias", C, 0.25, 0.0],
+                       ["pwconv1_weight", C * 4 * C, 0.5, 0.0], ["pwconv1_bias", 4 * C, 0.25, 0.0],
+                       ["pwconv2_weight", 4 * C * C, 0.5, 0.0], ["pwconv2_bias", C, 0.25, 0.0],
+                       ["gamma", C, 0.5, 1.0]],
+        "convnext_kernel": 7, "norm_eps": 1e-6,
+        "tolerance_cpu": 1e-4, "tolerance_gpu": 5e-3,
+        "expected_causal_conv": literal_array(t, "kExpectedCausalConv"),
+        "expected_depthwise": literal_array(t, "kExpectedDepthwise"),
+        "expected_transposed": literal_array(t, "kExpectedTransposed"),
+        "expected_convnext": literal_array(t, "kExpectedConvNeXt"),
+    }
+
+    for name, obj in (("qwen3_decoder_layer", g1), ("qwen3_code_predictor", g2), ("qwen3_codec_snake_beta", g3),
+                      ("qwen3_codec_convs", g5)):
         with open(os.path.join(HERE, name + ".json"), "w") as f:
             json.dump(obj, f, indent=1)
             f.write("\n")

@@ -9,6 +9,10 @@ G3: tests/qwen3_tts_codec_ops_test.cpp:77-82 (SnakeBeta: the sin^2 Snake family
     through exp, sin, sqr, scale_bias, div and add nodes).
 G4: tests/kokoro_decoder_test.cpp:81-90 (double-precision host Snake, layout
     t*C + c).
+G5: tests/qwen3_tts_codec_ops_test.cpp:43-94 (the codec's causal convolution
+    at dilation 2, its depthwise convolution and the ConvNeXt block) -- pins
+    ggml_im2col's column order, padding, dilation and batching, and ggml_norm
+    and ggml_gelu_erf inside the block.
 Each test also plants a plausible mistake in the restatement's composition and
 checks that the golden rejects it, so the golden is shown to constrain the
 part it is claimed to pin.
@@ -215,3 +219,139 @@ def test_g4_kokoro_snake_matches_double_host_reference():
     assert np.abs(got - ref).max() < 1e-4
     # f32 node-by-node rounding stays within a few ulp of the double form
     assert np.abs(got - ref).max() < 8 * np.finfo(np.float32).eps * np.abs(ref).max()
+
+
+# ---------------------------------------------------------------------------
+# G5: the codec's convolutions through ggml_im2col
+# ---------------------------------------------------------------------------
+
+def codec_conv_inputs(d):
+    """The fixture's tensors in LCG fill order; the signal as ggml [C, L] =
+    numpy (L, C) (drawn channel-major, laid out channels fastest)."""
+    s = R.LcgStream(d["seed"])
+    v = {name: s.fill(count, scale, offset) for name, count, scale, offset in d["fill_order"]}
+    C, L = d["channels"], d["length"]
+    return np.ascontiguousarray(v["signal"].reshape(C, L).T), v
+
+
+def causal_conv(x, w, b, dilation, im2col=None):
+    """codec_causal_conv1d (qwen3-tts/codec.cpp:76-106): the time-major copy,
+    ggml_im2col padded by the whole receptive field on both sides, the matrix
+    product, the first L columns, the channel bias. x numpy (L, C); w numpy
+    (OC, C, K) = ggml [K, C, OC]."""
+    L, C = x.shape
+    OC, _, K = w.shape
+    cols = (im2col or R.run)(lambda g: g.im2col(np.ascontiguousarray(x.T), K, 1, (K - 1) * dilation, dilation))[0]
+    return R.mul_mat(w.reshape(OC, C * K), cols)[:L] + b[None, :]
+
+
+def depthwise_conv(x, w, b):
+    """codec_causal_depthwise_conv1d (:108-137): each channel its own batch
+    entry of ggml_im2col ([L, 1, C]), one K-tap product per channel, the first
+    L columns, the channel bias. w numpy (C, 1, K)."""
+    L, C = x.shape
+    K = w.shape[-1]
+    cols = R.run(lambda g: g.im2col(np.ascontiguousarray(x.T).reshape(C, 1, L), K, 1, K - 1, 1))  # (C, OW, K)
+    wide = np.einsum("cok,ck->oc", cols.astype(np.float64), w.reshape(C, K).astype(np.float64)).astype(np.float32)
+    return wide[:L] + b[None, :]
+
+
+def convnext(x, v, d):
+    """codec_convnext_block (:201-221)."""
+    C = d["channels"]
+    h = depthwise_conv(x, v["dwconv_weight"].reshape(C, 1, d["convnext_kernel"]), v["dwconv_bias"])
+    h = R.run(lambda g: g.norm(h, np.float32(d["norm_eps"])))
+    h = h * v["norm_weight"][None, :] + v["norm_bias"][None, :]
+    h = R.mul_mat(v["pwconv1_weight"].reshape(4 * C, C), h) + v["pwconv1_bias"][None, :]
+    h = R.run(lambda g: g.gelu_erf(h))
+    h = R.mul_mat(v["pwconv2_weight"].reshape(C, 4 * C), h) + v["pwconv2_bias"][None, :]
+    return x + h * v["gamma"][None, :]
+
+
+def _dev(got, exp):
+    return np.abs(np.asarray(got, np.float32).reshape(-1) - np.array(exp, np.float32)).max()
+
+
+def test_g5_codec_convolutions():
+    d = _load("qwen3_codec_convs.json")
+    x, v = codec_conv_inputs(d)
+    C, OC, K = d["channels"], d["out_channels"], d["kernel"]
+    tol = d["tolerance_cpu"]
+    assert _dev(causal_conv(x, v["conv_weight"].reshape(OC, C, K), v["conv_bias"], d["dilation"]),
+                d["expected_causal_conv"]) < tol
+    assert _dev(depthwise_conv(x, v["depthwise_weight"].reshape(C, 1, K), v["depthwise_bias"]),
+                d["expected_depthwise"]) < tol
+    assert _dev(convnext(x, v, d), d["expected_convnext"]) < tol
+
+
+def test_g5_rejects_im2col_mistakes():
+    """Reversed taps, dilation 1, padding on the left only (the port pads both
+    sides and keeps the prefix) and the taps channel-minor in the column: each
+    misses the causal golden."""
+    d = _load("qwen3_codec_convs.json")
+    x, v = codec_conv_inputs(d)
+    C, OC, K, dil = d["channels"], d["out_channels"], d["kernel"], d["dilation"]
+    w, b, exp = v["conv_weight"].reshape(OC, C, K), v["conv_bias"], d["expected_causal_conv"]
+    assert _dev(causal_conv(x, w[:, :, ::-1].copy(), b, dil), exp) > 1e-2
+    assert _dev(causal_conv(x, w, b, 1), exp) > 1e-2
+    # left padding only: drop the right padding's columns, keep the first L
+    L = x.shape[0]
+    cols = R.run(lambda g: g.im2col(np.ascontiguousarray(x.T), K, 1, (K - 1) * dil, dil))[0]
+    shifted = np.vstack([cols[(K - 1) * dil:], np.zeros_like(cols[:(K - 1) * dil])])
+    assert _dev(R.mul_mat(w.reshape(OC, C * K), shifted)[:L] + b[None, :], exp) > 1e-2
+    # column index k*C + ic instead of ic*K + k
+    swapped = cols.reshape(-1, C, K).transpose(0, 2, 1).reshape(-1, C * K)
+    assert _dev(R.mul_mat(w.reshape(OC, C * K), swapped)[:L] + b[None, :], exp) > 1e-2
+
+
+def _direct_conv(x, w, s0, p0, d0):
+    """The convolution's definition, summed in double: x (N, IC, IW), w (OC, IC,
+    K); y[n, oc, ow] = sum over ic, k of w[oc, ic, k] * x[n, ic, ow*s0 + k*d0 - p0]
+    (0 outside the input)."""
+    N, IC, IW = x.shape
+    OC, _, K = w.shape
+    OW = R.conv_out_len(IW, K, s0, p0, d0)
+    y = np.zeros((N, OC, OW))
+    for ow in range(OW):
+        for k in range(K):
+            iw = ow * s0 + k * d0 - p0
+            if 0 <= iw < IW:
+                y[:, :, ow] += x[:, :, iw].astype(np.float64) @ w[:, :, k].T.astype(np.float64)
+    return y
+
+
+@pytest.mark.parametrize("N,IC,IW,K,s0,p0,d0", [(1, 3, 17, 3, 1, 1, 1), (2, 5, 40, 7, 1, 9, 3), (1, 4, 33, 11, 1, 25, 5),
+                                                (3, 2, 29, 4, 2, 1, 1), (1, 1, 9, 5, 3, 0, 2), (2, 6, 8, 3, 1, 0, 3),
+                                                (1, 2, 6, 7, 3, 0, 1)])
+def test_im2col_products_equal_the_convolution(N, IC, IW, K, s0, p0, d0):
+    """im2col then one K*IC product per output equals the direct convolution
+    sum for strides, paddings and dilations, including kernels wider than the
+    input (no tap in range: zero columns) and an output length that C's
+    truncating division sets to 1."""
+    rng = np.random.default_rng(N * 1000 + IC * 100 + IW + K + s0 + p0 + d0)
+    x = rng.standard_normal((N, IC, IW)).astype(np.float32)
+    w = rng.standard_normal((3, IC, K)).astype(np.float32)
+    cols = R.run(lambda g: g.im2col(x, K, s0, p0, d0))
+    assert cols.shape == (N, R.conv_out_len(IW, K, s0, p0, d0), IC * K)
+    got = np.einsum("nok,ck->nco", cols.astype(np.float64), w.reshape(3, IC * K).astype(np.float64))
+    np.testing.assert_allclose(got, _direct_conv(x, w, s0, p0, d0), rtol=0, atol=1e-9)
+
+
+def test_im2col_without_an_output_position_is_refused():
+    """ggml_im2col asserts OW > 0: (8 - 8 - 1)/1 + 1 = 0 and (5 - 6 - 1)/2 + 1 = 0."""
+    assert R.conv_out_len(8, 3, 1, 0, 4) == 0 and R.conv_out_len(5, 7, 2, 0, 1) == 0
+    assert R.conv_out_len(6, 7, 3, 0, 1) == 1  # (-1)/3 truncates to 0
+    for args in ((8, 3, 1, 0, 4), (5, 7, 2, 0, 1)):
+        with pytest.raises(ValueError):
+            R.Graph().im2col(np.zeros((1, 2, args[0]), np.float32), *args[1:])
+
+
+def test_im2col_f16_columns_round_to_nearest_even():
+    """An F16 destination holds numpy's (IEEE round-to-nearest-even) half of
+    each F32 column value, ties, subnormals, overflow and zeros included."""
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((2, 3, 50)) * 10.0 ** rng.integers(-8, 6, (2, 3, 50))).astype(np.float32)
+    x.reshape(-1)[:6] = [65520.0, 65519.0, 2.0 ** -25, -(2.0 ** -24) * 1.5, -0.0, 1.0 + 2.0 ** -11]
+    f32 = R.run(lambda g: g.im2col(x, 5, 2, 3, 2))
+    f16 = R.run(lambda g: g.im2col(x, 5, 2, 3, 2, dst_type=R.F16))
+    assert np.array_equal(f16, f32.astype(np.float16).view(np.uint16))
