@@ -368,6 +368,35 @@ shp_status_t shp_norm(const shp_tensor * x, float eps, shp_tensor * y, shp_strea
 shp_status_t shp_concat(const shp_tensor * a, const shp_tensor * b, int32_t dim, shp_tensor * y, shp_stream_t stream);
 
 /*
+ * ggml_im2col(kernel, x, s0, 0, p0, 0, d0, 0, false, y->type): the 1-D column
+ * matrix in front of every convolution GEMM of the vocoders, codecs and
+ * speech encoders (vits/waveform-decoder.cpp:104, vits/operations.cpp:40,103,
+ * kokoro/operations.cpp:76, omnivoice/codec.cpp:114,
+ * omnivoice/reference-encoder.cpp:190, qwen3-tts/codec.cpp:96,129,
+ * qwen3-tts/speaker-encoder.cpp:174, qwen3-tts/codec-encoder.cpp:359).
+ *   kernel: only its extents are read: K = ne[0], ne[1] = x's channel count
+ *           (data may be NULL, as for the shape-only kernel of a packed
+ *           weight, vits/waveform-decoder.cpp:102-103)
+ *   x:      F32 [IW, IC, N, 1], any 4-byte strides: time-contiguous rows, or
+ *           the transposed view of a channel-major [IC, IW] activation (read
+ *           directly, so the ggml_cont in front of the reference's im2col,
+ *           qwen3-tts/codec.cpp:94,125, is not needed)
+ *   y:      F32 or F16 [IC*K, OW, N, 1], contiguous, not overlapping x, with
+ *           OW = (IW + 2*p0 - d0*(K-1) - 1)/s0 + 1 (C division) >= 1:
+ *           y[n][ow][ic*K + k] = x[n][ic][ow*s0 + k*d0 - p0], 0 outside the
+ *           input; an F16 y holds each value rounded to nearest even.
+ * s0, d0 >= 1, p0 >= 0. Bit-exact (a gather). SHP_ERR_INVALID_ARG for shapes
+ * that do not match, SHP_ERR_UNSUPPORTED for other types or an overlap.
+ */
+shp_status_t shp_im2col(const shp_tensor * kernel,
+                        const shp_tensor * x,
+                        int32_t            s0,
+                        int32_t            p0,
+                        int32_t            d0,
+                        shp_tensor *       y,
+                        shp_stream_t       stream);
+
+/*
  * The tail of the time-major vocoder convolution, in one pass
  * (vits/waveform-decoder.cpp:111,118-121, then :147,150 or the next layer's
  * :146): s = ggml_add(ggml_cont(ggml_transpose(out)), reshape_2d(bias, 1, C)),

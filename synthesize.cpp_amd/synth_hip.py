@@ -92,6 +92,7 @@ def load(path=None):
         "shp_cpy": [_PT, _PT, vp],
         "shp_cont_add_leaky_relu": [_PT, _PT, _PT, i32, f, _PT, _PT, vp],
         "shp_concat": [_PT, _PT, i32, _PT, vp],
+        "shp_im2col": [_PT, _PT, i32, i32, i32, _PT, vp],
         "shp_sub": [_PT, _PT, _PT, vp],
         "shp_tanh": [_PT, _PT, vp],
         "shp_sigmoid": [_PT, _PT, vp],
@@ -538,6 +539,40 @@ def concat(a, b, dim, out=None):
     shape[ax] += b.shape[ax]
     out = torch.empty(shape, dtype=torch.float32, device=a.device) if out is None else out
     _check(load().shp_concat(_ref(desc(a)), _ref(desc(b)), int(dim), _ref(desc(out)), _stream()), "concat")
+    return out
+
+
+def conv_out_len(iw, k, s0, p0, d0):
+    """ggml_calc_conv_output_size: (iw + 2*p0 - d0*(k-1) - 1)/s0 + 1, C division."""
+    num = iw + 2 * p0 - d0 * (k - 1) - 1
+    return (num // s0 if num >= 0 else -((-num) // s0)) + 1
+
+
+def kernel_shape(k, ic, oc=1):
+    """A shape-only kernel descriptor [k, ic, oc] (no data), as ggml_im2col reads
+    its kernel operand."""
+    d = ShpTensor()
+    d.type, d.reserved, d.data = TYPE_F32, 0, None
+    for i, n in enumerate((k, ic, oc, 1)):
+        d.ne[i] = n
+    d.nb[0] = 4
+    for i in range(1, 4):
+        d.nb[i] = d.nb[i - 1] * d.ne[i - 1]
+    return d
+
+
+def im2col(x, k, s0=1, p0=0, d0=1, dtype=None, out=None):
+    """ggml_im2col(kernel [k, IC], x, s0, 0, p0, 0, d0, 0, false, dtype): x a
+    torch F32 tensor (N, IC, IW) or (IC, IW) = ggml [IW, IC, N], any strides;
+    returns (N, OW, IC*k) of dtype (float32 or float16)."""
+    import torch
+    if out is None:
+        n_, ic, iw = (1,) + tuple(x.shape) if x.dim() == 2 else tuple(x.shape)
+        ow = conv_out_len(iw, k, s0, p0, d0)
+        out = torch.empty((n_, max(ow, 1), ic * k), dtype=dtype or torch.float32, device=x.device)
+    ic = x.shape[-2]
+    _check(load().shp_im2col(ctypes.byref(kernel_shape(k, ic)), _ref(desc(x)), int(s0), int(p0), int(d0),
+                             _ref(desc(out)), _stream()), "im2col")
     return out
 
 
