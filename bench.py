@@ -483,6 +483,17 @@ def vocoder_rows(R, S, torch, cfg, seed, shapes=((512, 8192), (256, 32768), (128
             v = x.t()
             return lambda: S.cpy(v, out=y)
 
+        def make_im2col(C=C, T=T, K=3, d0=1, chmajor=False, f16=False):
+            # the column matrix in front of a convolution GEMM: x ggml [T, C]
+            # time-contiguous (vits/waveform-decoder.cpp:104, same-length
+            # padding), or the transposed view of a channel-major [C, T]
+            # activation, causal padding (qwen3-tts/codec.cpp:94-96)
+            x = randn(T, C).t() if chmajor else randn(C, T)
+            p0 = (K - 1) * d0 if chmajor else (K - 1) * d0 // 2
+            y = torch.empty((1, S.conv_out_len(T, K, 1, p0, d0), C * K), device="cuda",
+                            dtype=torch.float16 if f16 else torch.float32)
+            return lambda: S.im2col(x, K, 1, p0, d0, out=y)
+
         out.append(R.run(cfg, "snake [%d,%d]" % (C, T), 8 * n + 4 * C, make_snake))
         out.append(R.run(cfg, "snake_beta [%d,%d]" % (C, T), 8 * n + 8 * C, make_beta))
         out.append(R.run(cfg, "add_leaky_relu [%d,%d]" % (C, T), 12 * n, make_leaky))
@@ -493,6 +504,14 @@ def vocoder_rows(R, S, torch, cfg, seed, shapes=((512, 8192), (256, 32768), (128
                          make_tail))
         out.append(R.run(cfg, "conv tail: cont(transpose)+bias+residual->leaky, sum [%d,%d]" % (C, T),
                          16 * n + 4 * C, lambda: make_tail(resid=True)))
+        out.append(R.run(cfg, "im2col K=3 [%d,%d]" % (C, T), 4 * n + 4 * 3 * n, make_im2col))
+        out.append(R.run(cfg, "im2col K=3 channel-major view [%d,%d]" % (C, T),
+                         4 * n + 4 * 3 * (T + 2) * C, lambda: make_im2col(chmajor=True)))
+        if (C, T) == (128, 131072):
+            out.append(R.run(cfg, "im2col K=11 d=5 [%d,%d]" % (C, T), 4 * n + 4 * 11 * n,
+                             lambda: make_im2col(K=11, d0=5)))
+            out.append(R.run(cfg, "im2col K=7 d=3 f16 [%d,%d]" % (C, T), 4 * n + 2 * 7 * n,
+                             lambda: make_im2col(K=7, d0=3, f16=True)))
         if variants:
             # the size's streaming floor: one read and one write with no work
             out.append(R.run(cfg, "copy-like floor: bare leaky [%d,%d]" % (C, T), 8 * n, make_bare))
@@ -832,6 +851,18 @@ def cpu_op_builders(seed=SEED + 9):
         out.append((cfg, "conv tail: cont(transpose)+bias->leaky [%d,%d]" % (C, Tv), 8 * n + 4 * C, tail))
         out.append((cfg, "conv tail: cont(transpose)+bias+residual->leaky, sum [%d,%d]" % (C, Tv), 16 * n + 4 * C,
                     lambda g, tail=tail: tail(g, resid=True)))
+        # im2col: ggml-CPU's column gather; the channel-major form is the
+        # reference's ggml_cont of the transpose, then im2col
+        out.append((cfg, "im2col K=3 [%d,%d]" % (C, Tv), 16 * n,
+                    lambda g, C=C, Tv=Tv: g.im2col(take(C, Tv), 3, 1, 1, 1)))
+        out.append((cfg, "im2col K=3 channel-major view [%d,%d]" % (C, Tv), 4 * n + 12 * (Tv + 2) * C,
+                    lambda g, C=C, Tv=Tv: g.im2col(g.cont_f32(take(Tv, C), [Tv, C], [4 * C, 4]).reshape(C, Tv),
+                                                   3, 1, 2, 1)))
+        if (C, Tv) == (128, 131072):
+            out.append((cfg, "im2col K=11 d=5 [%d,%d]" % (C, Tv), 48 * n,
+                        lambda g, C=C, Tv=Tv: g.im2col(take(C, Tv), 11, 1, 25, 5)))
+            out.append((cfg, "im2col K=7 d=3 f16 [%d,%d]" % (C, Tv), 18 * n,
+                        lambda g, C=C, Tv=Tv: g.im2col(take(C, Tv), 7, 1, 9, 3, dst_type=R.F16)))
     return out
 
 

@@ -10,22 +10,25 @@
 //
 // A pure gather: every output is one input element (or 0), rounded to nearest
 // even for an F16 y, so the result is bit-exact. The write of K copies of the
-// input is the traffic (HBM-bound, no arithmetic to hide).
+// input is the traffic (HBM-bound).
 //
 // One block per tile of OWT output positions x ICT channels of one batch
-// entry:
+// entry (no loop: a block's stores never wait at a barrier):
 //   1. the tile's input window (ICT channel rows of (OWT-1)*s0 + (K-1)*d0 + 1
-//      samples, zeros where the window passes the input's ends) is loaded into
-//      LDS, consecutive lanes on consecutive addresses: along time for a
-//      time-contiguous x, along channels for a channel-contiguous x (the
-//      transposed view of a channel-major activation, so the ggml_cont that
-//      the reference puts in front of im2col is not needed);
-//   2. the tile's outputs are written in y's order (for each position, ICT*K
-//      consecutive values), each lane four values per store, from LDS.
-// ICT = 32 channels makes a position's run 128*K bytes of F32: whole,
-// aligned cache lines whenever IC is a multiple of 32. Tiles with every
-// channel (IC <= 32) cover one contiguous range of y, written in 4-value
-// stores whatever its alignment (scalar stores at its two ends).
+//      samples, zeros past the input's ends) goes to LDS, consecutive lanes on
+//      consecutive addresses: along time for a time-contiguous x, along
+//      channels for a channel-contiguous x (the transposed view of a
+//      channel-major activation, so the ggml_cont the reference puts in front
+//      of im2col is not needed);
+//   2. the tile's outputs are written in y's order, V values (16 bytes) per
+//      store. The LDS offsets of the values a store takes repeat with a short
+//      period -- one position's run of ICT*K values, or for a tile of every
+//      channel (one contiguous range of y) lcm(IC*K, V) values -- so each tile
+//      first tabulates one period's offsets in LDS; a store is then one table
+//      read, V window reads and running sums, with no division.
+// Both phases step their indices by running sums: the kernel is bound by its
+// stores, not by address arithmetic (per-value divisions held an earlier form
+// to ~65 % of HBM peak at [128,131072], K = 3).
 
 #include "shp_internal.hpp"
 
@@ -33,15 +36,41 @@ namespace shp {
 namespace {
 
 constexpr int kIm2colBlock = 256;
-constexpr int kIm2colLds   = 8192;   // floats of LDS window per block (32 KB)
-constexpr int kIm2colIct   = 32;     // channels per tile
-constexpr int kIm2colElems = 16384;  // target outputs per tile
+constexpr int kIm2colLds   = 4480;   // floats of LDS window per block at most (17.5 KB; with the table, 8 blocks per CU)
+constexpr int kIm2colBatch = 8;      // window loads a lane issues before its LDS writes
+constexpr int kIm2colTab   = 1024;   // int16 LDS offsets of the store table (one period)
 
-// Write forms: SEG1 = per-position runs, one value per store; SEG4 = the same,
-// four per store (IC*K a multiple of 4 and y aligned to four values); FLAT4 =
-// the tile's one contiguous range (ICT == IC), four per store between scalar
-// ends.
-enum Im2colForm { kSeg1 = 0, kSeg4 = 1, kFlat4 = 2 };
+// Tile shape: ict channels; at least owt positions, or enough for `elems`
+// outputs; fewer positions when the window passes kIm2colLds. Measured on
+// MI355X over K = 3 / 7 / 11, dilations 1-5, [128,131072] and [512,8192],
+// F32 and F16 columns, both input layouts (% of HBM peak at [128,131072];
+// the same-run copy reaches 75 %):
+//   - runs shorter than a 128-byte line per position (ict*K*esize) cost
+//     2-3x (8 channels: 21-38 %);
+//   - time-contiguous x, F32, K <= 4: 16 x 64 (4096 outputs) 76 %, against
+//     69 % for 32 x 128;
+//   - time-contiguous x otherwise: 32 x 64, K = 11 d = 5 75 % (66-68 % for
+//     16 or 64 channels, or 128 positions); F16 K = 7: 32 x 128 69 %;
+//   - channel-contiguous x: 32 x 128, 76 % (63 % for 16 channels);
+//   - one channel (the depthwise form): 4096 outputs 63 %, 8192 56 %.
+struct TileRule {
+    int ict;
+    int owt;
+    int elems;
+};
+
+inline TileRule tile_rule(bool chfast, bool f16, int64_t ic, int64_t k) {
+    if (ic == 1) {
+        return { 1, 64, 4096 };
+    }
+    if (chfast) {
+        return { 32, 128, 8192 };
+    }
+    if (!f16 && k <= 4) {
+        return { 16, 64, 4096 };
+    }
+    return f16 ? TileRule{ 32, 128, 8192 } : TileRule{ 32, 64, 8192 };
+}
 
 struct Im2colArgs {
     const char * x;
@@ -64,150 +93,221 @@ struct Im2colArgs {
     FastDiv      tic;   // channel tiles
     FastDiv      tow;   // position tiles
     FastDiv      kdiv;  // K
-    FastDiv      wdiv;  // wt (time-contiguous loader)
-    FastDiv      cdiv;  // ict (channel-contiguous loader)
-    FastDiv      vfull; // SEG forms: stores per position run, full channel tile
-    FastDiv      vlast; // ... the last channel tile
-    FastDiv      rdiv;  // FLAT form: row
-    uint32_t     ntiles;
-    uint32_t     pad;
+    FastDiv      rdiv;  // IC*K
+    FastDiv      segf;  // ICT*K: a full channel tile's run per position
+    FastDiv      segl;  // the last channel tile's run
+    // window walk: ns rows of nf values (time-contiguous x: ICT channel rows of
+    // wt samples; channel-contiguous x: wt sample rows of ICT channels); lane
+    // tid starts at (tid / nf, tid % nf) and steps 256 values at a time
+    FastDiv      fdiv;  // nf
+    int32_t      ns;
+    int32_t      ds;    // 256 / nf
+    int32_t      df;    // 256 % nf
+    int32_t      nbs;   // x byte strides of a row and of a value of the walk
+    int32_t      nbf;
+    int32_t      ls;    // LDS strides of the same
+    int32_t      lf;
+    int32_t      pad;
 };
 
-template <bool F16> __device__ __forceinline__ void put1(char * y, int64_t e, float v) {
+// V consecutive values of y from index e (e % V == 0 for V > 1), nontemporal.
+template <int V, bool F16> __device__ __forceinline__ void put(char * y, int64_t e, const float (&v)[V]) {
     if constexpr (F16) {
-        __builtin_nontemporal_store(static_cast<_Float16>(v), reinterpret_cast<_Float16 *>(y) + e);
-    } else {
-        __builtin_nontemporal_store(v, reinterpret_cast<float *>(y) + e);
-    }
-}
-
-template <bool F16> __device__ __forceinline__ void put4(char * y, int64_t e, const float (&v)[4]) {
-    if constexpr (F16) {
-        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-        const h4 h{ static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1]), static_cast<_Float16>(v[2]),
-                    static_cast<_Float16>(v[3]) };
-        __builtin_nontemporal_store(h, reinterpret_cast<h4 *>(y) + e / 4);
-    } else {
-        __builtin_nontemporal_store(f32x4{ v[0], v[1], v[2], v[3] }, reinterpret_cast<f32x4 *>(y) + e / 4);
-    }
-}
-
-// The value at (position owl, channel icl, tap k) of the tile, from LDS.
-__device__ __forceinline__ float tap(const float * lds, const Im2colArgs & a, int owl, int icl, int k) {
-    return lds[icl * a.wtp + owl * a.s0 + k * a.d0];
-}
-
-template <int FORM, bool F16, bool CHFAST> __global__ __launch_bounds__(kIm2colBlock) void k_im2col(const Im2colArgs a) {
-    __shared__ float lds[kIm2colLds];
-    const int        tid = static_cast<int>(threadIdx.x);
-    for (uint32_t t = blockIdx.x; t < a.ntiles; t += gridDim.x) {
-        const uint32_t q    = fastdiv(t, a.tic);
-        const uint32_t n    = fastdiv(q, a.tow);
-        const int64_t  ic0  = static_cast<int64_t>(t - q * a.tic.d) * a.ict;
-        const int64_t  ow0  = static_cast<int64_t>(q - n * a.tow.d) * a.owt;
-        const int      nic  = static_cast<int>(a.ic - ic0 < a.ict ? a.ic - ic0 : a.ict);
-        const int      now  = static_cast<int>(a.ow - ow0 < a.owt ? a.ow - ow0 : a.owt);
-        const int64_t  iw0  = ow0 * a.s0 - a.p0;
-        const char *   xb   = a.x + static_cast<int64_t>(n) * a.xnb2 + ic0 * a.xnb1;
-        // 1. the window, zero-filled past the input's ends (channels past IC
-        //    are never read)
-        const int      nwin = a.ict * a.wt;
-        for (int idx = tid; idx < nwin; idx += kIm2colBlock) {
-            int icl, w;
-            if constexpr (CHFAST) {
-                w   = static_cast<int>(fastdiv(static_cast<uint32_t>(idx), a.cdiv));
-                icl = idx - w * a.ict;
-            } else {
-                icl = static_cast<int>(fastdiv(static_cast<uint32_t>(idx), a.wdiv));
-                w   = idx - icl * a.wt;
-            }
-            const int64_t iw = iw0 + w;
-            float         v  = 0.0f;
-            if (icl < nic && iw >= 0 && iw < a.iw) {
-                v = *reinterpret_cast<const float *>(xb + icl * a.xnb1 + iw * a.xnb0);
-            }
-            lds[icl * a.wtp + w] = v;
-        }
-        __syncthreads();
-        // 2. the outputs, in y's order
-        const int64_t ybase = (static_cast<int64_t>(n) * a.ow + ow0) * a.row + ic0 * a.k;  // first value's index
-        if constexpr (FORM == kFlat4) {
-            // ICT == IC: positions ow0 .. ow0+now-1 are one range of now*row values
-            const int64_t len  = static_cast<int64_t>(now) * a.row;
-            const int     head0 = static_cast<int>((4 - ybase % 4) % 4);
-            const int     head = static_cast<int>(head0 < len ? head0 : len);
-            const int64_t nvec = (len - head) / 4;
-            const int64_t tail = head + nvec * 4;
-            auto          one  = [&](int64_t f) {
-                const uint32_t owl = fastdiv(static_cast<uint32_t>(f), a.rdiv);
-                const uint32_t j   = static_cast<uint32_t>(f) - owl * a.rdiv.d;
-                const uint32_t icl = fastdiv(j, a.kdiv);
-                put1<F16>(a.y, ybase + f, tap(lds, a, static_cast<int>(owl), static_cast<int>(icl),
-                                               static_cast<int>(j - icl * a.kdiv.d)));
-            };
-            if (tid < head) {
-                one(tid);
-            }
-            for (int64_t v = tid; v < nvec; v += kIm2colBlock) {
-                const int64_t f   = head + v * 4;
-                uint32_t      owl = fastdiv(static_cast<uint32_t>(f), a.rdiv);
-                const uint32_t j  = static_cast<uint32_t>(f) - owl * a.rdiv.d;
-                uint32_t      icl = fastdiv(j, a.kdiv);
-                int           k   = static_cast<int>(j - icl * a.kdiv.d);
-                float         vals[4];
+        typedef _Float16 hv __attribute__((ext_vector_type(V)));
+        hv h;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    vals[e] = tap(lds, a, static_cast<int>(owl), static_cast<int>(icl), k);
-                    if (++k == a.k) {
-                        k = 0;
-                        if (++icl == static_cast<uint32_t>(nic)) {
-                            icl = 0;
-                            ++owl;
-                        }
-                    }
-                }
-                put4<F16>(a.y, ybase + f, vals);
+        for (int i = 0; i < V; ++i) {
+            h[i] = static_cast<_Float16>(v[i]);
+        }
+        if constexpr (V == 1) {
+            __builtin_nontemporal_store(h[0], reinterpret_cast<_Float16 *>(y) + e);
+        } else {
+            __builtin_nontemporal_store(h, reinterpret_cast<hv *>(y) + e / V);
+        }
+    } else {
+        if constexpr (V == 1) {
+            __builtin_nontemporal_store(v[0], reinterpret_cast<float *>(y) + e);
+        } else {
+            typedef float fv __attribute__((ext_vector_type(V)));
+            fv f;
+#pragma unroll
+            for (int i = 0; i < V; ++i) {
+                f[i] = v[i];
             }
-            if (tail + tid < len) {
-                one(tail + tid);
+            __builtin_nontemporal_store(f, reinterpret_cast<fv *>(y) + e / V);
+        }
+    }
+}
+
+// LDS offset of value f of the tile, whose values run (position, channel, tap)
+// with rd.d values per position.
+__device__ __forceinline__ int tap_offset(const Im2colArgs & a, uint32_t f, const FastDiv & rd) {
+    const uint32_t owl = fastdiv(f, rd);
+    const uint32_t j   = f - owl * rd.d;
+    const uint32_t icl = fastdiv(j, a.kdiv);
+    return static_cast<int>(icl) * a.wtp + static_cast<int>(owl) * a.s0 + static_cast<int>(j - icl * a.kdiv.d) * a.d0;
+}
+
+// FLAT: the tile holds every channel (ICT == IC): its outputs are one range of
+// y, written in V-value stores between scalar ends (table period lcm(row, V)
+// values). Otherwise each position has a run of ICT*K values, a multiple of V,
+// starting V-aligned (table period: one run). V == 1: no table, one value per
+// lane and step, located by division (layouts the others cannot take).
+template <bool FLAT, int V, bool F16, bool CHFAST>
+__global__ __launch_bounds__(kIm2colBlock) void k_im2col(const Im2colArgs a) {
+    typedef int16_t         tv __attribute__((ext_vector_type(V > 1 ? V : 2)));  // one store's offsets
+    extern __shared__ float lds[];
+    __shared__ tv           tabv[V > 1 ? kIm2colTab / V : 1];
+    int16_t *               tab = reinterpret_cast<int16_t *>(tabv);
+    const int               tid = static_cast<int>(threadIdx.x);
+    const uint32_t          t   = blockIdx.x;
+    const uint32_t          q   = fastdiv(t, a.tic);
+    const uint32_t          n   = fastdiv(q, a.tow);
+    const int64_t           ic0 = static_cast<int64_t>(t - q * a.tic.d) * a.ict;
+    const int64_t           ow0 = static_cast<int64_t>(q - n * a.tow.d) * a.owt;
+    const int               nic = static_cast<int>(a.ic - ic0 < a.ict ? a.ic - ic0 : a.ict);
+    const int               now = static_cast<int>(a.ow - ow0 < a.owt ? a.ow - ow0 : a.owt);
+    const int64_t           iw0 = ow0 * a.s0 - a.p0;
+    // the window's first sample (may lie before x: only in-range samples are read)
+    const char *            xw  = a.x + static_cast<int64_t>(n) * a.xnb2 + ic0 * a.xnb1 + iw0 * a.xnb0;
+    const int               wlo = static_cast<int>(iw0 < 0 ? -iw0 : 0);                      // first sample in x
+    const int               whi = static_cast<int>(a.iw - iw0 < a.wt ? a.iw - iw0 : a.wt);  // past the last
+    // 1. the window, by running sums; zeros outside [wlo, whi) and for
+    //    channels past IC (never read)
+    {
+        const int nf = static_cast<int>(a.fdiv.d);
+        int       s  = static_cast<int>(fastdiv(static_cast<uint32_t>(tid), a.fdiv));
+        int       f  = tid - s * nf;
+        int       ox = s * a.nbs + f * a.nbf;
+        int       ol = s * a.ls + f * a.lf;
+        const int sx = a.ds * a.nbs + a.df * a.nbf, cx = a.nbs - nf * a.nbf;
+        const int sl = a.ds * a.ls + a.df * a.lf, cl = a.ls - nf * a.lf;
+        while (s < a.ns) {
+            float v[kIm2colBatch];
+            int   at[kIm2colBatch];
+#pragma unroll
+            for (int u = 0; u < kIm2colBatch; ++u) {
+                const int icl = CHFAST ? f : s;
+                const int w   = CHFAST ? s : f;
+                at[u]         = s < a.ns ? ol : -1;
+                v[u]          = 0.0f;
+                if (s < a.ns && icl < nic && w >= wlo && w < whi) {
+                    v[u] = *reinterpret_cast<const float *>(xw + ox);
+                }
+                s += a.ds;
+                f += a.df;
+                ox += sx;
+                ol += sl;
+                if (f >= nf) {
+                    f -= nf;
+                    ++s;
+                    ox += cx;
+                    ol += cl;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kIm2colBatch; ++u) {
+                if (at[u] >= 0) {
+                    lds[at[u]] = v[u];
+                }
+            }
+        }
+    }
+    const int64_t ybase = (static_cast<int64_t>(n) * a.ow + ow0) * a.row + ic0 * a.k;  // first value's index
+    const FastDiv sd    = nic == a.ict ? a.segf : a.segl;                              // run per position
+    // the store pattern (V > 1): FLAT ranges start V-aligned after `head`
+    // scalar values; P stores per period, covering cpos positions and cst
+    // values of y
+    int64_t       len  = 0;
+    int           head = 0;
+    int           P = 1, cpos = 1;
+    int64_t       cst  = 0;
+    int64_t       nvec = 0;
+    if constexpr (V > 1) {
+        if constexpr (FLAT) {
+            len              = static_cast<int64_t>(now) * a.row;
+            const int head0  = static_cast<int>((V - ybase % V) % V);
+            head             = static_cast<int>(head0 < len ? head0 : len);
+            const int64_t rw = a.row;
+            const int     g  = rw % V == 0 ? V : (rw % (V / 2) == 0 ? V / 2 : (rw % 2 == 0 ? 2 : 1));  // gcd(row, V)
+            P                = static_cast<int>(rw / g);  // lcm(row, V) / V
+            cpos             = V / g;                     // lcm(row, V) / row
+            cst              = static_cast<int64_t>(P) * V;
+            nvec             = (len - head) / V;
+            for (int r = tid; r < P * V; r += kIm2colBlock) {
+                tab[r] = static_cast<int16_t>(tap_offset(a, static_cast<uint32_t>(head + r), a.rdiv));
             }
         } else {
-            constexpr int V    = FORM == kSeg4 ? 4 : 1;
-            const int     seg  = nic * a.k;  // values per position in this tile
-            const FastDiv vd   = nic == a.ict ? a.vfull : a.vlast;
-            const int     nv   = seg / V;
-            const int     tot  = now * nv;
-            for (int v = tid; v < tot; v += kIm2colBlock) {
-                const uint32_t owl = fastdiv(static_cast<uint32_t>(v), vd);
-                const int      j   = (v - static_cast<int>(owl * vd.d)) * V;
-                int            icl = static_cast<int>(fastdiv(static_cast<uint32_t>(j), a.kdiv));
-                int            k   = j - icl * a.k;
-                const int64_t  e   = ybase + static_cast<int64_t>(owl) * a.row + j;
-                if constexpr (V == 1) {
-                    put1<F16>(a.y, e, tap(lds, a, static_cast<int>(owl), icl, k));
-                } else {
-                    float vals[4];
-#pragma unroll
-                    for (int q4 = 0; q4 < 4; ++q4) {
-                        vals[q4] = tap(lds, a, static_cast<int>(owl), icl, k);
-                        if (++k == a.k) {
-                            k = 0;
-                            ++icl;
-                        }
-                    }
-                    put4<F16>(a.y, e, vals);
-                }
+            const int seg = static_cast<int>(sd.d);
+            P             = seg / V;
+            cst           = a.row;
+            nvec          = static_cast<int64_t>(now) * P;
+            for (int r = tid; r < seg; r += kIm2colBlock) {
+                const uint32_t icl = fastdiv(static_cast<uint32_t>(r), a.kdiv);
+                tab[r]             = static_cast<int16_t>(static_cast<int>(icl) * a.wtp +
+                                                          (r - static_cast<int>(icl * a.kdiv.d)) * a.d0);
             }
         }
-        __syncthreads();
+    }
+    __syncthreads();
+    // 2. the outputs, in y's order
+    if constexpr (V == 1) {
+        const FastDiv rd   = FLAT ? a.rdiv : sd;
+        const int64_t nval = static_cast<int64_t>(now) * rd.d;
+        for (int64_t f = tid; f < nval; f += kIm2colBlock) {
+            const uint32_t owl   = fastdiv(static_cast<uint32_t>(f), rd);
+            const float    v1[1] = { lds[tap_offset(a, static_cast<uint32_t>(f), rd)] };
+            put<1, F16>(a.y, ybase + static_cast<int64_t>(owl) * a.row + (static_cast<uint32_t>(f) - owl * rd.d), v1);
+        }
+    } else {
+        if constexpr (FLAT) {
+            // the scalar ends of the range
+            const int64_t tail = head + nvec * V;
+            if (tid < head) {
+                const float v1[1] = { lds[tap_offset(a, static_cast<uint32_t>(tid), a.rdiv)] };
+                put<1, F16>(a.y, ybase + tid, v1);
+            }
+            if (tail + tid < len) {
+                const float v1[1] = { lds[tap_offset(a, static_cast<uint32_t>(tail + tid), a.rdiv)] };
+                put<1, F16>(a.y, ybase + tail + tid, v1);
+            }
+        }
+        // store vi: period c = vi / P, entry r = vi % P, by running sums (the
+        // block's 256 lanes step 256 stores: dc periods and dr entries)
+        int           c      = tid / P;
+        int           r      = tid - c * P;
+        const int     dc     = kIm2colBlock / P, dr = kIm2colBlock % P;
+        const int     lstep  = cpos * a.s0;  // window offset per period
+        int           lb     = c * lstep;
+        int64_t       ye     = ybase + head + static_cast<int64_t>(c) * cst + static_cast<int64_t>(r) * V;
+        const int64_t ystep  = static_cast<int64_t>(dc) * cst + static_cast<int64_t>(dr) * V;
+        const int64_t ycarry = cst - static_cast<int64_t>(P) * V;
+        for (int64_t vi = tid; vi < nvec; vi += kIm2colBlock) {
+            const tv o = tabv[r];  // one LDS read for the V offsets
+            float    vals[V];
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                vals[e] = lds[lb + o[e]];
+            }
+            put<V, F16>(a.y, ye, vals);
+            r += dr;
+            lb += dc * lstep;
+            ye += ystep;
+            if (r >= P) {
+                r -= P;
+                lb += lstep;
+                ye += ycarry;
+            }
+        }
     }
 }
 
-template <int FORM, bool F16> void launch_form(const Im2colArgs & a, bool chfast, unsigned grid, hipStream_t s) {
+template <bool FLAT, int V, bool F16>
+void launch_form(const Im2colArgs & a, bool chfast, unsigned grid, size_t shmem, hipStream_t s) {
     if (chfast) {
-        hipLaunchKernelGGL((k_im2col<FORM, F16, true>), dim3(grid), dim3(kIm2colBlock), 0, s, a);
+        hipLaunchKernelGGL((k_im2col<FLAT, V, F16, true>), dim3(grid), dim3(kIm2colBlock), shmem, s, a);
     } else {
-        hipLaunchKernelGGL((k_im2col<FORM, F16, false>), dim3(grid), dim3(kIm2colBlock), 0, s, a);
+        hipLaunchKernelGGL((k_im2col<FLAT, V, F16, false>), dim3(grid), dim3(kIm2colBlock), shmem, s, a);
     }
 }
 
@@ -217,6 +317,15 @@ inline int64_t window(int64_t owt, int64_t s0, int64_t k, int64_t d0) {
 
 inline int64_t padded(int64_t w) {
     return w | 1;  // an odd row stride spreads a column of the window over the banks
+}
+
+inline int64_t gcd64(int64_t a, int64_t b) {
+    while (b != 0) {
+        const int64_t r = a % b;
+        a               = b;
+        b               = r;
+    }
+    return a;
 }
 
 }  // namespace
@@ -230,10 +339,12 @@ int64_t im2col_out_len(int64_t iw, int64_t k, int64_t s0, int64_t p0, int64_t d0
 // not (the transposed view of a channel-major activation).
 struct Im2colPlan {
     Im2colArgs args{};
-    int        form   = kSeg1;
+    bool       flat   = false;
+    int        v      = 1;   // values per store: 1, 4 (F32 or F16) or 8 (F16)
     bool       f16    = false;
     bool       chfast = false;
-    unsigned   grid   = 0;
+    unsigned   grid   = 0;   // one block per tile
+    size_t     shmem  = 0;
 };
 
 shp_status_t plan_im2col(const shp_tensor * kernel, const shp_tensor * x, int32_t s0, int32_t p0, int32_t d0,
@@ -281,85 +392,110 @@ shp_status_t plan_im2col(const shp_tensor * kernel, const shp_tensor * x, int32_
     if (spans_overlap(*x, *y)) {
         return SHP_ERR_UNSUPPORTED;
     }
-    // tile: ICT channels, OWT positions, the window in LDS
-    int64_t ict = IC < kIm2colIct ? IC : kIm2colIct;
-    int64_t owt = kIm2colElems / (ict * K);
-    owt         = owt < 1 ? 1 : (owt >= 16 ? owt / 16 * 16 : owt);
-    owt         = owt < OW ? owt : OW;
-    while (owt > 1 && ict * padded(window(owt, s0, K, d0)) > kIm2colLds) {
-        owt = (owt + 1) / 2;
+    // tile: ICT channels, OWT positions, the window in LDS: as many positions
+    // as wanted and fit (window + 1 for the odd row stride <= kIm2colLds /
+    // ICT), fewer channels when not one position fits
+    const int64_t  nb0 = static_cast<int64_t>(x->nb[0]), nb1 = static_cast<int64_t>(x->nb[1]);
+    pl.chfast          = nb1 == 4 && nb0 != 4 && IC > 1;
+    pl.f16             = y->type == SHP_TYPE_F16;
+    const TileRule rule = tile_rule(pl.chfast, pl.f16, IC, K);
+    int64_t        ict  = IC < rule.ict ? IC : rule.ict;
+    int64_t owt = 0;
+    for (;; ict = (ict + 1) / 2) {
+        const int64_t room = kIm2colLds / ict - 1 - (K - 1) * d0 - 1;  // (owt - 1) * s0 at most
+        owt                = room < 0 ? 0 : room / s0 + 1;
+        if (owt >= 1 || ict == 1) {
+            break;
+        }
     }
-    while (ict > 1 && ict * padded(window(owt, s0, K, d0)) > kIm2colLds) {
-        ict = (ict + 1) / 2;
-    }
-    if (ict * padded(window(owt, s0, K, d0)) > kIm2colLds) {
+    if (owt < 1) {
         return SHP_ERR_UNSUPPORTED;  // one channel's receptive field alone passes the window
     }
+    const int64_t want = rule.elems / (ict * K) > rule.owt ? rule.elems / (ict * K) : rule.owt;
+    owt                = owt < want ? owt : want;
+    owt                = owt < OW ? owt : OW;
     const int64_t tic = (IC + ict - 1) / ict, tow = (OW + owt - 1) / owt;
     if (IC * K > INT32_MAX || OW > INT32_MAX || N > INT32_MAX || tic * tow * N > INT32_MAX) {
         return SHP_ERR_UNSUPPORTED;
     }
-    Im2colArgs & a = pl.args;
-    a.x            = static_cast<const char *>(x->data);
-    a.y            = static_cast<char *>(y->data);
-    a.xnb0         = static_cast<int64_t>(x->nb[0]);
-    a.xnb1         = static_cast<int64_t>(x->nb[1]);
-    a.xnb2         = static_cast<int64_t>(x->nb[2]);
-    a.iw           = IW;
-    a.ic           = IC;
-    a.ow           = OW;
-    a.row          = IC * K;
-    a.k            = static_cast<int32_t>(K);
-    a.s0           = s0;
-    a.p0           = p0;
-    a.d0           = d0;
-    a.ict          = static_cast<int32_t>(ict);
-    a.owt          = static_cast<int32_t>(owt);
-    a.wt           = static_cast<int32_t>(window(owt, s0, K, d0));
-    a.wtp          = static_cast<int32_t>(padded(a.wt));
-    a.tic          = make_fastdiv(static_cast<uint32_t>(tic));
-    a.tow          = make_fastdiv(static_cast<uint32_t>(tow));
-    a.kdiv         = make_fastdiv(static_cast<uint32_t>(K));
-    a.wdiv         = make_fastdiv(static_cast<uint32_t>(a.wt));
-    a.cdiv         = make_fastdiv(static_cast<uint32_t>(ict));
-    a.rdiv         = make_fastdiv(static_cast<uint32_t>(IC * K));
-    a.ntiles       = static_cast<uint32_t>(tic * tow * N);
-    pl.f16         = y->type == SHP_TYPE_F16;
-    const size_t esz = pl.f16 ? 2 : 4;
-    if (ict == IC) {
-        pl.form = kFlat4;
-    } else if ((IC * K) % 4 == 0 && (ict * K) % 4 == 0 && reinterpret_cast<uintptr_t>(y->data) % (4 * esz) == 0) {
-        pl.form = kSeg4;
-    } else {
-        pl.form = kSeg1;
+    const int64_t wt = window(owt, s0, K, d0);
+    // the window walk's byte offsets are 32-bit
+    if ((ict - 1) * nb1 + (wt - 1) * nb0 + kIm2colBlock * (nb0 + nb1) > INT32_MAX) {
+        return SHP_ERR_UNSUPPORTED;
     }
-    const int64_t vdiv = pl.form == kSeg4 ? 4 : 1;
-    const int64_t last = IC - (tic - 1) * ict;
-    a.vfull            = make_fastdiv(static_cast<uint32_t>(ict * K / vdiv));
-    a.vlast            = make_fastdiv(static_cast<uint32_t>(last * K / vdiv));
-    if (pl.form == kFlat4 && reinterpret_cast<uintptr_t>(y->data) % (4 * esz) != 0) {
-        pl.form = kSeg1;  // FLAT4 finds its ends from value indices, which needs an aligned y
+    const int64_t last = IC - (tic - 1) * ict;  // channels of the last channel tile
+    Im2colArgs &  a    = pl.args;
+    a.x                = static_cast<const char *>(x->data);
+    a.y                = static_cast<char *>(y->data);
+    a.xnb0             = nb0;
+    a.xnb1             = nb1;
+    a.xnb2             = static_cast<int64_t>(x->nb[2]);
+    a.iw               = IW;
+    a.ic               = IC;
+    a.ow               = OW;
+    a.row              = IC * K;
+    a.k                = static_cast<int32_t>(K);
+    a.s0               = s0;
+    a.p0               = p0;
+    a.d0               = d0;
+    a.ict              = static_cast<int32_t>(ict);
+    a.owt              = static_cast<int32_t>(owt);
+    a.wt               = static_cast<int32_t>(wt);
+    a.wtp              = static_cast<int32_t>(padded(wt));
+    a.tic              = make_fastdiv(static_cast<uint32_t>(tic));
+    a.tow              = make_fastdiv(static_cast<uint32_t>(tow));
+    a.kdiv             = make_fastdiv(static_cast<uint32_t>(K));
+    a.rdiv             = make_fastdiv(static_cast<uint32_t>(IC * K));
+    a.segf             = make_fastdiv(static_cast<uint32_t>(ict * K));
+    a.segl             = make_fastdiv(static_cast<uint32_t>(last * K));
+    const int64_t nf   = pl.chfast ? ict : wt;
+    a.fdiv             = make_fastdiv(static_cast<uint32_t>(nf));
+    a.ns               = static_cast<int32_t>(pl.chfast ? wt : ict);
+    a.ds               = static_cast<int32_t>(kIm2colBlock / nf);
+    a.df               = static_cast<int32_t>(kIm2colBlock % nf);
+    a.nbs              = static_cast<int32_t>(pl.chfast ? nb0 : nb1);
+    a.nbf              = static_cast<int32_t>(pl.chfast ? nb1 : nb0);
+    a.ls               = pl.chfast ? 1 : a.wtp;
+    a.lf               = pl.chfast ? a.wtp : 1;
+    // Stores of 16 bytes where the layout allows (8 values of F16, 4 of F32),
+    // else 8 bytes of F16, else one value. One table period must fit.
+    const size_t    esz   = pl.f16 ? 2 : 4;
+    const uintptr_t yaddr = reinterpret_cast<uintptr_t>(y->data);
+    pl.flat               = ict == IC;
+    pl.v                  = 1;
+    for (int v : { pl.f16 ? 8 : 4, 4 }) {
+        const bool    aligned = yaddr % (v * esz) == 0;
+        const bool    runs    = (IC * K) % v == 0 && (ict * K) % v == 0;
+        const int64_t per     = pl.flat ? IC * K * v / gcd64(IC * K, v) : ict * K;  // table entries
+        if (aligned && (pl.flat || runs) && per <= kIm2colTab) {
+            pl.v = v;
+            break;
+        }
     }
-    pl.chfast = x->nb[1] == 4 && x->nb[0] != 4 && IC > 1;
-    pl.grid   = a.ntiles < (1u << 20) ? a.ntiles : (1u << 20);
+    pl.grid  = static_cast<unsigned>(tic * tow * N);
+    pl.shmem = static_cast<size_t>(ict * a.wtp) * sizeof(float);
     return SHP_OK;
 }
 
 shp_status_t launch_im2col(const Im2colPlan & pl, hipStream_t s) {
     const Im2colArgs & a = pl.args;
-    switch (pl.form) {
-        case kFlat4:
-            pl.f16 ? launch_form<kFlat4, true>(a, pl.chfast, pl.grid, s) :
-                     launch_form<kFlat4, false>(a, pl.chfast, pl.grid, s);
-            break;
-        case kSeg4:
-            pl.f16 ? launch_form<kSeg4, true>(a, pl.chfast, pl.grid, s) :
-                     launch_form<kSeg4, false>(a, pl.chfast, pl.grid, s);
-            break;
-        default:
-            pl.f16 ? launch_form<kSeg1, true>(a, pl.chfast, pl.grid, s) :
-                     launch_form<kSeg1, false>(a, pl.chfast, pl.grid, s);
-            break;
+    const bool         c = pl.chfast;
+    if (pl.f16) {
+        if (pl.flat) {
+            pl.v == 8 ? launch_form<true, 8, true>(a, c, pl.grid, pl.shmem, s) :
+            pl.v == 4 ? launch_form<true, 4, true>(a, c, pl.grid, pl.shmem, s) :
+                        launch_form<true, 1, true>(a, c, pl.grid, pl.shmem, s);
+        } else {
+            pl.v == 8 ? launch_form<false, 8, true>(a, c, pl.grid, pl.shmem, s) :
+            pl.v == 4 ? launch_form<false, 4, true>(a, c, pl.grid, pl.shmem, s) :
+                        launch_form<false, 1, true>(a, c, pl.grid, pl.shmem, s);
+        }
+    } else if (pl.flat) {
+        pl.v == 4 ? launch_form<true, 4, false>(a, c, pl.grid, pl.shmem, s) :
+                    launch_form<true, 1, false>(a, c, pl.grid, pl.shmem, s);
+    } else {
+        pl.v == 4 ? launch_form<false, 4, false>(a, c, pl.grid, pl.shmem, s) :
+                    launch_form<false, 1, false>(a, c, pl.grid, pl.shmem, s);
     }
     return launch_status();
 }
