@@ -37,6 +37,16 @@
  *   EXP MUL SIN SQR|MUL EXP SCALE DIV ADD  SnakeBeta (src/arch/qwen3-tts/codec.cpp:184-200)
  *   GET_ROWS (GET_ROWS ADD)+         multi-codebook gather->sum
  *        (src/arch/qwen3-tts/code-predictor.cpp:82-107)
+ *   CPY ADD [ADD] [LEAKY_RELU]       a time-major convolution's tail: the
+ *        transposing copy, the [1, C] bias, the residual, the next leaky-ReLU
+ *        (src/arch/vits/waveform-decoder.cpp:111,118-121,146-150); also the
+ *        codec's channel bias before or after its transposing copy
+ *        (src/arch/qwen3-tts/codec.cpp:134-140,179-181)
+ *   CPY ADD|MUL|DIV                  a crop's copy of a row-contiguous view,
+ *        then the op on the copy (codec.cpp:64-71,100-104): the op reads the view
+ *   CPY [views] IM2COL               the causal convolution's time-major copy
+ *        and its column matrix (src/arch/qwen3-tts/codec.cpp:94-96): im2col
+ *        reads the channel-major activation through the transposed view
  * Any other supported node runs alone through its entry point in
  * synth_hip.h. View-like nodes (NONE, VIEW, RESHAPE, PERMUTE, TRANSPOSE)
  * are SHP_NODE_NOP: no work.
@@ -86,6 +96,9 @@ typedef enum shp_node_op {
     SHP_NODE_GELU_ERF,   /* GGML_OP_UNARY, GGML_UNARY_OP_GELU_ERF */
     SHP_NODE_CLAMP,      /* GGML_OP_CLAMP: f32 {min, max} */
     SHP_NODE_NORM,       /* GGML_OP_NORM: f32 {eps} */
+    SHP_NODE_IM2COL,     /* GGML_OP_IM2COL: i32 {s0, s1, p0, p1, d0, d1, is_2D}; src[0] the
+                            kernel (its extents only), src[1] the input; the 1-D form
+                            (is_2D 0, p1 0) every src/arch call site builds */
     SHP_NODE_OP_COUNT
 } shp_node_op;
 
@@ -125,8 +138,11 @@ typedef enum shp_run_kind {
     SHP_RUN_CONT_ADD_LEAKY,   /* CPY of a transposed view, ADD of the per-row bias,
                                  [ADD of a residual], [LEAKY_RELU]:
                                  shp_cont_add_leaky_relu */
-    SHP_RUN_VIEW_BINARY       /* CPY of a row-contiguous F32 view, then ADD, MUL or
+    SHP_RUN_VIEW_BINARY,      /* CPY of a row-contiguous F32 view, then ADD, MUL or
                                  DIV of the copy: the binary op reads the view */
+    SHP_RUN_CONT_IM2COL       /* CPY of a transposed channel-major F32 activation,
+                                 [views], IM2COL of the copy: shp_im2col reads the
+                                 activation in place of the copy */
 } shp_run_kind;
 
 typedef struct shp_graph_run {

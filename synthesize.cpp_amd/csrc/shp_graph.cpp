@@ -137,6 +137,11 @@ bool node_form_ok(const shp_node & n) {
         case SHP_NODE_CONCAT:
             return f32_of(n.src[0]) && f32_of(n.src[1]) && f32_of(n.dst) && n.op_params[0] >= 0 &&
                    n.op_params[0] <= 3;
+        case SHP_NODE_IM2COL:
+            // the 1-D form: is_2D 0 and no padding along the absent second
+            // dimension (ggml's 1-D rows read there at -p1: zeros)
+            return n.op_params[6] == 0 && n.op_params[3] == 0 && present(n.src[0]) && f32_of(n.src[1]) &&
+                   (n.dst.type == SHP_TYPE_F32 || n.dst.type == SHP_TYPE_F16);
         case SHP_NODE_GLU_SWIGLU: {
             const auto & a = n.src[0];
             if (!f32_of(a) || !f32_of(n.dst)) {
@@ -208,6 +213,8 @@ struct Launch {
     float                   f1    = 0.0f;
     float                   f2    = 0.0f;
     int32_t                 i0    = 0;
+    int32_t                 i1    = 0;
+    int32_t                 i2    = 0;
     std::vector<shp_tensor> terms;
     shp_tensor              codes{};
     // views the run forms itself (a transposed view of a copy's source, a
@@ -722,7 +729,8 @@ class Planner {
             case SHP_NODE_SILU:
                 return match_silu_mul(p, l);
             case SHP_NODE_CPY:
-                if ((used = match_transpose_bias(p, l)) != 0 || (used = match_cont_tail(p, l)) != 0) {
+                if ((used = match_transpose_bias(p, l)) != 0 || (used = match_cont_tail(p, l)) != 0 ||
+                    (used = match_cont_im2col(p, l)) != 0) {
                     return used;
                 }
                 return match_view_binary(p, l);
@@ -1293,6 +1301,65 @@ class Planner {
         return 2;
     }
 
+    // CPY of a transposed F32 view into a contiguous tensor -- the causal
+    // convolution's ggml_cont(ggml_transpose(x)) of a channel-major activation
+    // -- read only by IM2COL as its input, directly or through view nodes that
+    // add or drop extents of 1 (qwen3-tts/codec.cpp:94-96): shp_im2col reads
+    // the activation through the transposed view, and the copy is never
+    // written. Taken when that view has its channels contiguous, which the
+    // kernel loads coalesced; the depthwise form (channels as batch entries,
+    // :124-129) keeps its copy.
+    int match_cont_im2col(size_t p, Launch & l) const {
+        const int cp = at(p, 0);
+        const int im = at(p, 1);
+        if (!is(cp, SHP_NODE_CPY) || !is(im, SHP_NODE_IM2COL) || producer(im, 1) != cp || producer(im, 0) == cp) {
+            return 0;
+        }
+        const shp_node &   C = nodes_[cp];
+        const shp_node &   I = nodes_[im];
+        const shp_tensor & s = C.src[0];
+        const shp_tensor & b = I.src[1];
+        if (f32_strided_view_dim(&s) == 0 || !f32_of(C.dst) || !same_shape(s, C.dst) || !contiguous(C.dst) ||
+            !f32_of(b) || b.data != C.dst.data || !contiguous(b) || !internal_v(cp, Members{ cp, im })) {
+            return 0;
+        }
+        // b is the copy's result with extents of 1 added or dropped: map each
+        // of its dimensions of extent > 1 to the source's, in order
+        shp_tensor v = b;
+        int        sd[4], bd[4], ns = 0, nb = 0;
+        for (int d = 0; d < 4; ++d) {
+            if (s.ne[d] > 1) {
+                sd[ns++] = d;
+            }
+            if (b.ne[d] > 1) {
+                bd[nb++] = d;
+            }
+        }
+        if (ns != nb) {
+            return 0;
+        }
+        for (int i = 0; i < ns; ++i) {
+            if (s.ne[sd[i]] != b.ne[bd[i]]) {
+                return 0;
+            }
+            v.nb[bd[i]] = s.nb[sd[i]];
+        }
+        v.data = s.data;
+        if (v.nb[1] != 4 || v.nb[0] == 4 || v.ne[1] < 2) {
+            return 0;
+        }
+        l       = Launch{};
+        l.kind  = SHP_RUN_CONT_IM2COL;
+        l.xv    = v;
+        l.own_x = true;
+        l.w     = &I.src[0];
+        l.i0    = I.op_params[0];  // s0
+        l.i1    = I.op_params[2];  // p0
+        l.i2    = I.op_params[4];  // d0
+        l.y     = const_cast<shp_tensor *>(&I.dst);
+        return 2;
+    }
+
     // SILU(g) then MUL(silu, u) (either operand order: the product commutes).
     int match_silu_mul(size_t p, Launch & l) const {
         const int si = at(p, 0);
@@ -1379,6 +1446,8 @@ shp_status_t launch_single(const shp_node & n, shp_stream_t st) {
             return shp_clamp(&n.src[0], fparam(n, 0), fparam(n, 1), y, st);
         case SHP_NODE_NORM:
             return shp_norm(&n.src[0], fparam(n, 0), y, st);
+        case SHP_NODE_IM2COL:
+            return shp_im2col(&n.src[0], &n.src[1], n.op_params[0], n.op_params[2], n.op_params[4], y, st);
         default:
             return SHP_ERR_UNSUPPORTED;
     }
@@ -1423,6 +1492,8 @@ shp_status_t launch_run(const Planner & pl, const Launch & l, shp_stream_t st) {
             return l.i0 == SHP_NODE_ADD ? shp_add(l.x, l.b, l.y, st) :
                    l.i0 == SHP_NODE_MUL ? shp_mul(l.x, l.b, l.y, st) :
                                           shp_div(l.x, l.b, l.y, st);
+        case SHP_RUN_CONT_IM2COL:
+            return shp_im2col(l.w, &l.xv, l.i0, l.i1, l.i2, l.y, st);
         default:
             return SHP_ERR_UNSUPPORTED;
     }

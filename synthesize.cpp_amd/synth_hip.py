@@ -590,12 +590,12 @@ def cpy(x, out=None):
 
 (NODE_NOP, NODE_ADD, NODE_MUL, NODE_DIV, NODE_SQR, NODE_SIN, NODE_SCALE, NODE_CPY, NODE_GET_ROWS, NODE_RMS_NORM,
  NODE_SOFT_MAX, NODE_ROPE, NODE_LEAKY_RELU, NODE_SILU, NODE_EXP, NODE_GLU_SWIGLU, NODE_CONCAT, NODE_SUB, NODE_TANH,
- NODE_SIGMOID, NODE_ELU, NODE_GELU_ERF, NODE_CLAMP, NODE_NORM) = range(24)
+ NODE_SIGMOID, NODE_ELU, NODE_GELU_ERF, NODE_CLAMP, NODE_NORM, NODE_IM2COL) = range(25)
 NODE_FLAG_OUTPUT = 1
 RUN_KINDS = {-1: "unsupported", 0: "nop", 1: "single", 2: "norm_mul", 3: "norm_mul_rope", 4: "add_norm_mul",
              5: "silu_mul", 6: "add_leaky", 7: "add_scale_leaky", 8: "snake", 9: "snake_guarded", 10: "snake_beta",
              11: "gather_sum", 12: "qk_norm_rope", 13: "qk_norm_rope_kv", 14: "cont_add_leaky",
-             15: "view_binary"}
+             15: "view_binary", 16: "cont_im2col"}
 
 
 class ShpNode(ctypes.Structure):
@@ -749,6 +749,18 @@ class Graph:
         shape[ax] += tb.shape[ax]
         return self._op(NODE_CONCAT, torch.empty(shape, dtype=torch.float32, device=ta.device), [a, b],
                         ints={0: dim})
+
+    def im2col(self, kernel, x, s0=1, p0=0, d0=1, dtype=None):
+        """ggml_im2col(kernel, x, s0, 0, p0, 0, d0, 0, false, dtype): kernel a
+        torch tensor (OC, IC, K) = ggml [K, IC, OC] (only its extents are
+        read), x (N, IC, IW) or (IC, IW); the result (N, OW, IC*K)."""
+        import torch
+        k, ic = self._t(kernel).shape[-1], self._t(kernel).shape[-2]
+        t = self._t(x)
+        n_, iw = (t.shape[0] if t.dim() == 3 else 1), t.shape[-1]
+        ow = conv_out_len(iw, k, s0, p0, d0)
+        dst = torch.empty((n_, max(ow, 1), ic * k), dtype=dtype or torch.float32, device=t.device)
+        return self._op(NODE_IM2COL, dst, [kernel, x], ints={0: s0, 2: p0, 4: d0})
 
     def glu_swiglu(self, a, b=None, swapped=False):
         t = self._t(a)

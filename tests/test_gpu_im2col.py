@@ -131,3 +131,69 @@ def test_im2col_refusals(gpu):
         gpu.im2col(buf[:400].view(4, 100), 3, 1, 1, 1, out=buf[:1200].view(1, ow, 12))
     with pytest.raises(gpu.ShpError):  # stride 0
         gpu.im2col(x, 3, 0, 1, 1, out=torch.empty((1, ow, 12), device="cuda"))
+
+
+# ---------------------------------------------------------------------------
+# through the node-run executor
+# ---------------------------------------------------------------------------
+
+def _golden_inputs():
+    from test_oracle_goldens import _load, codec_conv_inputs
+    d = _load("qwen3_codec_convs.json")
+    x, v = codec_conv_inputs(d)
+    return d, x, v
+
+
+def test_codec_convolutions_golden_through_the_executor(gpu):
+    """tests/qwen3_tts_codec_ops_test.cpp:43-56 with the columns built on the
+    GPU from the node list codec_causal_conv1d and codec_causal_depthwise_conv1d
+    emit (codec.cpp:94-96,124-129): the causal convolution's copy and im2col
+    as one launch (the copy never written), the depthwise form's copy then
+    im2col. The products, crop and bias in double on the host, at the test's
+    1e-4."""
+    d, x, v = _golden_inputs()
+    C, L, OC, K, dil = d["channels"], d["length"], d["out_channels"], d["kernel"], d["dilation"]
+    w = v["conv_weight"].reshape(OC, C, K)
+    wd = v["depthwise_weight"].reshape(C, 1, K)
+    tx = _t(gpu, x)                                    # ggml [C, L]
+    g = gpu.Graph()
+    tm = g.cont(g.view(tx, tx.t()))
+    cols = g.im2col(_t(gpu, w), tm, 1, (K - 1) * dil, dil)
+    assert [k for k, *_ in g.plan(cols) if k != "nop"] == ["cont_im2col"]
+    g.compute(cols)
+    wide = _np(cols.t)[0].astype(np.float64) @ w.reshape(OC, C * K).astype(np.float64).T
+    got = (wide[:L] + v["conv_bias"][None, :]).astype(np.float32)
+    assert np.abs(got.reshape(-1) - np.array(d["expected_causal_conv"], np.float32)).max() < d["tolerance_cpu"]
+    g = gpu.Graph()
+    tm = g.cont(g.view(tx, tx.t()))
+    dcols = g.im2col(_t(gpu, wd), g.view(tm, tm.t.view(C, 1, L)), 1, K - 1, 1)
+    assert [k for k, *_ in g.plan(dcols) if k != "nop"] == ["single", "single"]
+    g.compute(dcols)
+    wide = np.einsum("cok,ck->oc", _np(dcols.t).astype(np.float64), wd.reshape(C, K).astype(np.float64))
+    got = (wide[:L] + v["depthwise_bias"][None, :]).astype(np.float32)
+    assert np.abs(got.reshape(-1) - np.array(d["expected_depthwise"], np.float32)).max() < d["tolerance_cpu"]
+
+
+@pytest.mark.parametrize("C,T,K,d0,f16", [(1024, 2000, 7, 1, False), (512, 3001, 3, 3, True), (96, 777, 5, 2, False)])
+def test_cont_im2col_run_equals_its_nodes(gpu, C, T, K, d0, f16):
+    """The fused run against the same list with the copy written (read again
+    after the graph), bit for bit, and against the restatement's im2col of the
+    time-major copy."""
+    import torch
+    rng = np.random.default_rng([SEED, C, T, K])
+    x = rng.standard_normal((T, C)).astype(np.float32)  # ggml [C, T]
+    w = torch.zeros((8, C, K), device="cuda")
+    dt = torch.float16 if f16 else torch.float32
+    outs = []
+    for keep_copy in (False, True):
+        tx = _t(gpu, x)
+        g = gpu.Graph()
+        tm = g.cont(g.view(tx, tx.t()))
+        cols = g.im2col(w, tm, 1, (K - 1) * d0, d0, dtype=dt)
+        kinds = [k for k, *_ in g.plan(*((cols, tm) if keep_copy else (cols,))) if k != "nop"]
+        assert kinds == (["single", "single"] if keep_copy else ["cont_im2col"])
+        g.compute(*((cols, tm) if keep_copy else (cols,)))
+        outs.append(_np(cols.t))
+    assert np.array_equal(outs[0].view(np.uint16 if f16 else np.uint32), outs[1].view(np.uint16 if f16 else np.uint32))
+    ref = _cols_ref(np.ascontiguousarray(x.T), K, 1, (K - 1) * d0, d0, R.F16 if f16 else R.F32)
+    _check(torch.from_numpy(outs[0]), ref, R.F16 if f16 else R.F32)

@@ -519,6 +519,63 @@ def test_view_copy_then_binary():
     assert kinds(g.plan(added)) == ["single", "single"]
 
 
+def test_cont_then_im2col():
+    """The codec's causal convolution (qwen3-tts/codec.cpp:94-96): the
+    time-major copy of a channel-major activation, then its im2col, one launch
+    reading the activation through the transposed view, for F32 and F16
+    columns. Kept apart: the depthwise form (each channel a batch entry,
+    :124-129), the copy read elsewhere, a plain copy, and columns placed over
+    the activation."""
+    C, T, OC, K, d = 64, 300, 32, 3, 2
+    x = z(T, C)                                     # ggml [C, T], channels fastest
+    w = z(OC, C, K)                                 # ggml [K, C, OC]
+    g = S.Graph()
+    tm = g.cont(g.view(x, x.t()))
+    plan = g.plan(g.im2col(w, tm, 1, (K - 1) * d, d))
+    assert kinds(plan) == ["cont_im2col"] and plan[-1][3] == 2
+    g = S.Graph()
+    tm = g.cont(g.view(x, x.t()))
+    assert kinds(g.plan(g.im2col(w, tm, 1, 2, 1, dtype=torch.float16))) == ["cont_im2col"]
+    # depthwise: [T, 1, C] batches; the view would be batch-contiguous
+    g = S.Graph()
+    tm = g.cont(g.view(x, x.t()))
+    batched = g.view(tm, tm.t.view(C, 1, T))
+    assert kinds(g.plan(g.im2col(z(C, 1, 7), batched, 1, 6, 1))) == ["single", "single"]
+    # the copy read elsewhere must be written
+    g = S.Graph()
+    tm = g.cont(g.view(x, x.t()))
+    assert kinds(g.plan(g.im2col(w, tm, 1, 2, 1), g.exp(tm))) == ["single", "single", "single"]
+    # a plain (time-contiguous) copy is not this run
+    g = S.Graph()
+    tm = g.cont(z(C, T))
+    assert kinds(g.plan(g.im2col(w, tm, 1, 2, 1))) == ["single", "single"]
+    # columns over the activation's memory: apart
+    big = z(T * C * K + T * C)
+    xs = big[:T * C].view(T, C)
+    g = S.Graph()
+    tm = g.cont(g.view(xs, xs.t()))
+    cols = g._op(S.NODE_IM2COL, big[:T * C * K].view(1, T, C * K), [w, tm], ints={0: 1, 2: 1, 4: 1})
+    assert "cont_im2col" not in kinds(g.plan(cols))
+
+
+def test_im2col_node_forms():
+    """supports_op for IM2COL: the 1-D form only (is_2D 0, p1 0), F32 input,
+    F32 or F16 columns of the shape ggml_im2col gives."""
+    w, x = z(8, 4, 3), z(4, 50)
+    g = S.Graph()
+    ok = g.im2col(w, x, 1, 1, 1)
+    arr, n, keep = g.nodes(ok)
+    assert S.load().shp_graph_node_supported(ctypes.byref(arr[0])) == 1
+    for k, v in ((6, 1), (3, 1)):  # is_2D, p1
+        arr[0].op_params[k] = v
+        assert S.load().shp_graph_node_supported(ctypes.byref(arr[0])) == 0
+        arr[0].op_params[k] = 0
+    g = S.Graph()
+    bad = g._op(S.NODE_IM2COL, z(1, 49, 12), [w, x], ints={0: 1, 2: 1, 4: 1})  # OW is 50
+    arr, n, keep = g.nodes(bad)
+    assert S.load().shp_graph_node_supported(ctypes.byref(arr[0])) == 0
+
+
 def test_runs_keep_outputs_apart_from_inputs():
     """A fused run reads its inputs while it writes its outputs, so an output
     the allocator placed over an input at another offset keeps the nodes
