@@ -27,7 +27,10 @@ input sets whose total exceeds 512 MB (cold cache):
   - configs[3]: Snake, SnakeBeta, add->leaky-ReLU and add->leaky-ReLU with the
     sum carried, the time-major ggml_cont(ggml_transpose(x)) copy of each
     vocoder convolution's output, the [1, C] bias add behind it, and the
-    whole tail (copy, bias, residual, leaky) as one launch, on [512,8192],
+    whole tail (copy, bias, residual, leaky) as one launch, and the
+    convolution's im2col columns (K = 3 from the time-major input and from the
+    channel-major activation's transposed view; at [128,131072] also K = 11
+    dilation 5 and F16 columns of K = 7 dilation 3), on [512,8192],
     [256,32768] and [128,131072];
   - the decode step's non-GEMM work per talker layer (28-layer
     graph), without and with the KV-cache write and the attention softmax;
@@ -1108,7 +1111,9 @@ PMC_OPS = [
     ("get_rows q8_0 [1024,2048] x4096", 21250048), ("soft_max_ext causal-size [512,512,16]", 33554432),
     ("get_rows_sum q5_k 16x[1024,2048] x4096", 63176704), ("get_rows q5_k [1024,2048] x4096", 19677184),
     ("cont(transpose) [128,131072]", 134217728), ("add bias[1,C] time-major [128,131072]", 134218240),
-    ("conv tail: cont(transpose)+bias+residual->leaky, sum [128,131072]", 268435968)]
+    ("conv tail: cont(transpose)+bias+residual->leaky, sum [128,131072]", 268435968),
+    ("im2col K=3 [128,131072]", 268435456), ("im2col K=3 channel-major view [128,131072]", 268439552),
+    ("im2col K=7 d=3 f16 [128,131072]", 301989888)]
 
 
 def pmc_large(S, torch):
@@ -1133,6 +1138,8 @@ def pmc_large(S, torch):
     sc = randn(16, 512, 512)
     xt, tb, tr = randn(131072, 128), randn(128, 1), randn(128, 131072)   # GEMM output ggml [128, T], bias, residual
     ty, ts = empty(128, 131072), empty(128, 131072)
+    cols3, cols3c = empty(1, 131072, 384), empty(1, 131074, 384)   # im2col columns of tr (ggml [T, C]) and of xt^T
+    cols7 = torch.empty((1, 131072, 896), dtype=torch.float16, device="cuda")
     fns = [lambda: S.rms_norm_mul(x2, w2, 1e-6), lambda: S.add_rms_norm_mul(x2, x2b, w2, 1e-6),
            lambda: S.qk_norm_rope(q, k, wq, wk, 1e-6, pos, 128, 1e6), lambda: S.swiglu(gt, up),
            lambda: S.add(x2, x2b), lambda: S.snake(xs, al), lambda: S.snake_beta(xs, la, lb),
@@ -1140,7 +1147,9 @@ def pmc_large(S, torch):
            lambda: S.get_rows(tabs[0], codes[0]), lambda: S.soft_max_ext(sc, None, 0.0884),
            lambda: S.get_rows_sum(tabs5, codes), lambda: S.get_rows(tabs5[0], codes[0]),
            lambda: S.cpy(xt.t(), out=ty), lambda: S.add(tr, tb, out=ty),
-           lambda: S.cont_add_leaky_relu(xt.t(), tb, tr, 0.1, out=ty, sum_out=ts)]
+           lambda: S.cont_add_leaky_relu(xt.t(), tb, tr, 0.1, out=ty, sum_out=ts),
+           lambda: S.im2col(tr, 3, 1, 1, 1, out=cols3), lambda: S.im2col(xt.t(), 3, 1, 2, 1, out=cols3c),
+           lambda: S.im2col(tr, 7, 1, 9, 3, out=cols7)]
     n = CALIB_BYTES // 4
     src = torch.randn(n, device="cuda")
     dst = torch.empty_like(src)
