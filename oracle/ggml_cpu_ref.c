@@ -610,6 +610,40 @@ static void op_im2col(const orc_node * n, int ith, int nth) {
     }
 }
 
+/* ggml_col2im_1d(columns, stride, OC, padding): the scatter-back of a
+ * transposed convolution computed as a matrix product (columns[l] = the
+ * kernel's K*OC taps times input column l, out-channel-major, tap-minor), at
+ * vits/operations.cpp:118-140, omnivoice/codec.cpp:150-159 and
+ * qwen3-tts/codec.cpp:163-171. Output [T, OC], T = (L-1)*stride + K -
+ * 2*padding:
+ *   dst[oc][t] = sum of columns[l][oc*K + k] over l*stride + k = t + padding,
+ * 0 <= l < L, 0 <= k < K: each column l adds its taps at t = l*stride + k -
+ * padding. The op belongs to the reference's pinned ggml, which is absent;
+ * the sum is accumulated into +0.0f in ascending l (a zero-initialised
+ * scatter in column order). For K <= 2*stride -- every upsampling layer of the
+ * vocoders and codecs -- an output takes at most two terms, and the f32 sum of
+ * two terms from +0 is the same in either order. Threads take channels. */
+static void op_col2im_1d(const orc_node * n, int ith, int nth) {
+    const int64_t * v  = (const int64_t *) n->src1;
+    const int64_t   K = v[0], OC = v[1], L = v[2], S = v[3], P = v[4];
+    const int64_t   T  = (L - 1) * S + K - 2 * P;
+    const float *   c  = (const float *) n->src0;
+    for (int64_t oc = ith; oc < OC; oc += nth) {
+        float * y = (float *) n->dst + oc * T;
+        for (int64_t t = 0; t < T; ++t) {
+            y[t] = 0.0f;
+        }
+        for (int64_t l = 0; l < L; ++l) {
+            for (int64_t k = 0; k < K; ++k) {
+                const int64_t t = l * S + k - P;
+                if (t >= 0 && t < T) {
+                    y[t] += c[l * K * OC + oc * K + k];
+                }
+            }
+        }
+    }
+}
+
 /* ggml_swiglu (single tensor): gate = first half of each row (second when
  * swapped), y = silu(gate) * other half. */
 static void op_glu_swiglu(const orc_node * n, int ith, int nth) {
@@ -729,6 +763,9 @@ static void run_node(const orc_node * n, int ith, int nth) {
             break;
         case ORC_OP_IM2COL:
             op_im2col(n, ith, nth);
+            break;
+        case ORC_OP_COL2IM_1D:
+            op_col2im_1d(n, ith, nth);
             break;
         default:
             atomic_store(&g_node_error, -1);

@@ -53,6 +53,7 @@ enum orc_op {
     ORC_OP_CLAMP,        /* MAX(MIN(x, f[1]), f[0])                 ggml_clamp          */
     ORC_OP_NORM,         /* (x-mean)/sqrt(var+eps), f[0] = eps      ggml_norm           */
     ORC_OP_IM2COL,       /* 1-D convolution columns                 ggml_im2col         */
+    ORC_OP_COL2IM_1D,    /* transposed-convolution scatter-back     ggml_col2im_1d      */
 };
 
 /*
@@ -86,6 +87,9 @@ enum orc_op {
  *               s0, p0, d0}; type0 = the dst type, ORC_F32 or ORC_F16; dst
  *               [IC*K, OW, N], OW = (IW + 2*p0 - d0*(K-1) - 1)/s0 + 1 (C
  *               division).
+ *   COL2IM_1D : src0 = F32 columns [K*OC, L]; src1 = int64_t[5] {K, OC, L,
+ *               stride, padding}; dst F32 [T, OC], T = (L-1)*stride + K -
+ *               2*padding.
  */
 typedef struct orc_node {
     int32_t      op;

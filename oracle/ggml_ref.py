@@ -25,7 +25,7 @@ F32, F16, Q8_0, Q5_K, I32, BF16 = 0, 1, 8, 13, 26, 30
 
 (OP_ADD, OP_MUL, OP_DIV, OP_RMS_NORM, OP_ROPE_NEOX, OP_SILU, OP_SIN, OP_SQR, OP_EXP, OP_LEAKY_RELU, OP_SCALE_BIAS,
  OP_GET_ROWS, OP_CAST_F32, OP_GLU_SWIGLU, OP_SOFT_MAX, OP_CONT_F32, OP_BINBCAST, OP_SUB, OP_TANH, OP_SIGMOID,
- OP_ELU, OP_GELU_ERF, OP_CLAMP, OP_NORM, OP_IM2COL) = range(1, 26)
+ OP_ELU, OP_GELU_ERF, OP_CLAMP, OP_NORM, OP_IM2COL, OP_COL2IM_1D) = range(1, 27)
 
 
 class OrcNode(ctypes.Structure):
@@ -268,6 +268,27 @@ class Graph:
         nd.src0, nd.src1, nd.dst = _ptr(x), _ptr(view), _ptr(dst)
         self.nodes.append(nd)
         self.keep += [dst, x, view]
+        return dst
+
+    def col2im_1d(self, cols, stride, oc, padding):
+        """ggml_col2im_1d(columns, stride, oc, padding): cols numpy (L, K*OC) =
+        ggml [K*OC, L]; returns (OC, T) = ggml [T, OC], T = (L-1)*stride + K -
+        2*padding."""
+        cols = self._f32(cols)
+        L, ko = cols.shape
+        if ko % oc or stride < 1 or padding < 0:
+            raise ValueError("col2im_1d: K*OC not a multiple of OC, or a bad stride / padding")
+        k = ko // oc
+        t = (L - 1) * stride + k - 2 * padding
+        if t < 1:
+            raise ValueError("col2im_1d: no output sample")
+        view = np.array([k, oc, L, stride, padding], dtype=np.int64)
+        dst = np.empty((oc, t), dtype=np.float32)
+        nd = OrcNode()
+        nd.op, nd.type0, nd.ne0, nd.nrows = OP_COL2IM_1D, F32, t, oc
+        nd.src0, nd.src1, nd.dst = _ptr(cols), _ptr(view), _ptr(dst)
+        self.nodes.append(nd)
+        self.keep += [dst, cols, view]
         return dst
 
     def glu_swiglu(self, a, swapped=False):

@@ -13,6 +13,8 @@ Sources:
   G3 tests/qwen3_tts_codec_ops_test.cpp:34-82       (kExpectedSnakeBeta, config)
   G5 tests/qwen3_tts_codec_ops_test.cpp:34-94,184-210 (kExpectedCausalConv,
      kExpectedDepthwise, kExpectedTransposed, kExpectedConvNeXt, fill order)
+  G6 tests/vits_transpose_conv_test.cpp:237-265 (the transposed convolution's
+     known answers and the multichannel cases' shapes and fill rule)
 """
 import json
 import os
@@ -42,6 +44,37 @@ def constant(text, name):
         raise SystemExit("constant %s not found" % name)
     tok = m.group(1).rstrip("fFuU")
     return float(tok) if ("." in tok or "e" in tok.lower()) else int(tok)
+
+
+def call_args(text, name):
+    """The argument lists of every call `name(...)` in text, split at top-level
+    commas (braces and parentheses nest)."""
+    out = []
+    for m in re.finditer(re.escape(name) + r"\(", text):
+        i, depth, args, cur = m.end(), 1, [], ""
+        while depth:
+            ch = text[i]
+            if ch in "({":
+                depth += 1
+            elif ch in ")}":
+                depth -= 1
+            if depth == 1 and ch == ",":
+                args.append(cur.strip())
+                cur = ""
+            elif depth:
+                cur += ch
+            i += 1
+        args.append(cur.strip())
+        out.append(args)
+    return out
+
+
+def float_list(arg):
+    """A float vector argument: `{ a, b, ... }` or `std::vector<float>(n, v)`."""
+    m = re.fullmatch(r"std::vector<float>\((\d+),\s*([-0-9.eE]+)f?\)", arg)
+    if m:
+        return [float(m.group(2))] * int(m.group(1))
+    return [float(t.strip().rstrip("fF")) for t in arg.strip("{} ").split(",") if t.strip()]
 
 
 def main():
@@ -123,8 +156,31 @@ def main():
         "expected_convnext": literal_array(t, "kExpectedConvNeXt"),
     }
 
+    t = read("tests/vits_transpose_conv_test.cpp")
+    single = []
+    for a in call_args(t, "run_transpose_conv_case")[1:]:  # [0] is the definition
+        if len(a) > 6:
+            continue  # the F16-weight repeat of a case (same values)
+        single.append({"kernel": float_list(a[1]), "input": float_list(a[2]), "stride": int(a[3]),
+                       "padding": int(a[4]), "expected": float_list(a[5])})
+    multi = []
+    for a in call_args(t, "run_transpose_conv_multichannel_case")[1:]:
+        if a[1].isdigit():
+            multi.append({k: int(v) for k, v in zip(("kernel", "out_channels", "in_channels", "length", "stride",
+                                                     "padding"), a[1:7])})
+    g6 = {
+        "source": "tests/vits_transpose_conv_test.cpp:82-110,126-134,237-265",
+        # single-channel cases: kernel [K, 1, 1], input [1, L], bias 0, expected [1, T]
+        "single_channel": [dict(c) for c in {tuple(sorted((k, tuple(v) if isinstance(v, list) else v)
+                                                          for k, v in c.items())): c for c in single}.values()],
+        # multichannel cases: kernel [K, OC, IC] with kernel[i] = i % 7 + 1 over its flat
+        # (ic*OC + oc)*K + k order, input [IC, L] with input[i] = i % 5 + 1 (l*IC + ic),
+        # bias 0; the test compares exactly against the definition (:82-110)
+        "multichannel": multi, "kernel_fill": [7, 1], "input_fill": [5, 1],
+    }
+
     for name, obj in (("qwen3_decoder_layer", g1), ("qwen3_code_predictor", g2), ("qwen3_codec_snake_beta", g3),
-                      ("qwen3_codec_convs", g5)):
+                      ("qwen3_codec_convs", g5), ("vits_transpose_conv", g6)):
         with open(os.path.join(HERE, name + ".json"), "w") as f:
             json.dump(obj, f, indent=1)
             f.write("\n")

@@ -10,9 +10,13 @@ G3: tests/qwen3_tts_codec_ops_test.cpp:77-82 (SnakeBeta: the sin^2 Snake family
 G4: tests/kokoro_decoder_test.cpp:81-90 (double-precision host Snake, layout
     t*C + c).
 G5: tests/qwen3_tts_codec_ops_test.cpp:43-94 (the codec's causal convolution
-    at dilation 2, its depthwise convolution and the ConvNeXt block) -- pins
-    ggml_im2col's column order, padding, dilation and batching, and ggml_norm
-    and ggml_gelu_erf inside the block.
+    at dilation 2, its depthwise convolution, its causal transposed
+    convolution and the ConvNeXt block) -- pins ggml_im2col's column order,
+    padding, dilation and batching, ggml_col2im_1d's scatter and crop, and
+    ggml_norm and ggml_gelu_erf inside the block.
+G6: tests/vits_transpose_conv_test.cpp:237-265 (the transposed convolution's
+    exact known answers and multichannel cases) -- pins ggml_col2im_1d's
+    tap placement, padding and channel order.
 Each test also plants a plausible mistake in the restatement's composition and
 checks that the golden rejects it, so the golden is shown to constrain the
 part it is claimed to pin.
@@ -355,3 +359,86 @@ def test_im2col_f16_columns_round_to_nearest_even():
     f32 = R.run(lambda g: g.im2col(x, 5, 2, 3, 2))
     f16 = R.run(lambda g: g.im2col(x, 5, 2, 3, 2, dst_type=R.F16))
     assert np.array_equal(f16, f32.astype(np.float16).view(np.uint16))
+
+
+# ---------------------------------------------------------------------------
+# G6 and G5's transposed convolution: ggml_col2im_1d
+# ---------------------------------------------------------------------------
+
+def transpose_conv(x, w, stride, padding, col2im=None):
+    """vits transpose_conv1d with a zero bias (vits/operations.cpp:118-157):
+    the kernel's (K, OC) pair merged out-channel-major, the product with the
+    input, ggml_col2im_1d, then the transpose back. x numpy (L, IC) = ggml
+    [IC, L]; w numpy (IC, OC, K) = ggml [K, OC, IC]. Returns (T, OC)."""
+    ic, oc, k = w.shape
+    cols = R.mul_mat(w.reshape(ic, oc * k).T.copy(), x)           # (L, K*OC) = ggml [K*OC, L]
+    wide = (col2im or (lambda c: R.run(lambda g: g.col2im_1d(c, stride, oc, padding))))(cols)
+    return np.ascontiguousarray(wide.T)
+
+
+def _definition(x, w, stride, padding):
+    """The transposed convolution from its definition (each input sample
+    spreads its kernel taps), summed in double: (T, OC)."""
+    L, ic = x.shape
+    _, oc, k = w.shape
+    raw = np.zeros((oc, (L - 1) * stride + k))
+    for l in range(L):
+        raw[:, l * stride:l * stride + k] += np.einsum("i,iok->ok", x[l].astype(np.float64), w.astype(np.float64))
+    return raw[:, padding:raw.shape[1] - padding].T
+
+
+def test_g6_transpose_conv_known_answers():
+    """tests/vits_transpose_conv_test.cpp:237-246: exact, as the test compares."""
+    d = _load("vits_transpose_conv.json")
+    for c in d["single_channel"]:
+        x = np.array(c["input"], np.float32).reshape(-1, 1)
+        w = np.array(c["kernel"], np.float32).reshape(1, 1, -1)
+        got = transpose_conv(x, w, c["stride"], c["padding"]).reshape(-1)
+        assert np.array_equal(got, np.array(c["expected"], np.float32)), (got, c["expected"])
+
+
+def test_g6_transpose_conv_multichannel_cases():
+    """:255-264 with the test's fill (:126-134), against the definition,
+    exactly (small integers: exact in every order). The third case (K 3,
+    stride 1) sums three terms per output."""
+    d = _load("vits_transpose_conv.json")
+    km, kb = d["kernel_fill"]
+    im, ib = d["input_fill"]
+    for c in d["multichannel"]:
+        K, OC, IC, L = c["kernel"], c["out_channels"], c["in_channels"], c["length"]
+        w = (np.arange(K * OC * IC) % km + kb).astype(np.float32).reshape(IC, OC, K)
+        x = (np.arange(IC * L) % im + ib).astype(np.float32).reshape(L, IC)
+        got = transpose_conv(x, w, c["stride"], c["padding"])
+        assert np.array_equal(got, _definition(x, w, c["stride"], c["padding"]).astype(np.float32)), c
+
+
+def test_g5_codec_transposed_convolution():
+    """tests/qwen3_tts_codec_ops_test.cpp:57-70: codec_causal_transpose_conv1d
+    (qwen3-tts/codec.cpp:146-181): columns, col2im_1d without padding, the
+    trailing K - stride samples dropped, the channel bias, back to channels
+    fastest; at the test's 1e-4. The kernel's taps reversed, or the columns
+    read tap-major, miss it."""
+    d = _load("qwen3_codec_convs.json")
+    x, v = codec_conv_inputs(d)
+    C, OC, S = d["channels"], d["out_channels"], d["stride"]
+    K = 2 * S
+    w = v["transposed_weight"].reshape(C, OC, K)
+    exp = np.array(d["expected_transposed"], np.float32)
+
+    def causal(out):
+        return out[:out.shape[0] - (K - S)] + v["transposed_bias"][None, :]
+    assert np.abs(causal(transpose_conv(x, w, S, 0)).reshape(-1) - exp).max() < d["tolerance_cpu"]
+    flipped = transpose_conv(x, w[:, :, ::-1].copy(), S, 0)
+    assert np.abs(causal(flipped).reshape(-1) - exp).max() > 1e-2
+    cols = R.mul_mat(w.reshape(C, OC * K).T.copy(), x)
+    tap_major = cols.reshape(-1, OC, K).transpose(0, 2, 1).reshape(-1, OC * K).copy()
+    wrong = R.run(lambda g: g.col2im_1d(tap_major, S, OC, 0)).T
+    assert np.abs(causal(wrong).reshape(-1) - exp).max() > 1e-2
+
+
+def test_col2im_refuses_empty_outputs():
+    """vits/operations.cpp:134-137: a crop of the whole signal has no output
+    (ggml_col2im_1d asserts); one sample less still builds."""
+    with pytest.raises(ValueError):
+        R.Graph().col2im_1d(np.zeros((1, 4 * 3), np.float32), 2, 3, 2)
+    assert R.run(lambda g: g.col2im_1d(np.ones((1, 4 * 3), np.float32), 2, 3, 1)).shape == (3, 2)
