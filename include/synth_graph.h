@@ -99,6 +99,9 @@ typedef enum shp_node_op {
     SHP_NODE_IM2COL,     /* GGML_OP_IM2COL: i32 {s0, s1, p0, p1, d0, d1, is_2D}; src[0] the
                             kernel (its extents only), src[1] the input; the 1-D form
                             (is_2D 0, p1 0) every src/arch call site builds */
+    SHP_NODE_COL2IM_1D,  /* ggml_col2im_1d (an op of the reference's pinned ggml): i32
+                            {stride, out_channels, padding}, which the module's glue fills
+                            from the node's own parameters; src[0] the columns */
     SHP_NODE_OP_COUNT
 } shp_node_op;
 

@@ -388,6 +388,28 @@ shp_status_t shp_concat(const shp_tensor * a, const shp_tensor * b, int32_t dim,
  * s0, d0 >= 1, p0 >= 0. Bit-exact (a gather). SHP_ERR_INVALID_ARG for shapes
  * that do not match, SHP_ERR_UNSUPPORTED for other types or an overlap.
  */
+/*
+ * ggml_col2im_1d(cols, stride, out_channels, padding): the scatter-back of a
+ * transposed convolution computed as a matrix product, the upsampling layers
+ * of the vocoders and codecs (vits/operations.cpp:118-140,
+ * omnivoice/codec.cpp:150-159, qwen3-tts/codec.cpp:163-171).
+ *   cols: F32 [K*OC, L, 1, 1], rows contiguous (any row stride): column l
+ *         holds the K*OC taps of input sample l, out-channel major, tap minor
+ *   y:    F32 [T, OC, 1, 1], T = (L-1)*stride + K - 2*padding >= 1, rows
+ *         contiguous (any row stride), not overlapping cols:
+ *         y[oc][t] = sum of cols[l][oc*K + k] over l*stride + k = t + padding,
+ *         accumulated from +0.0f in ascending l
+ * stride, out_channels >= 1, padding >= 0, K = cols->ne[0] / out_channels.
+ * With K <= 2*stride (every upsampling layer of the reference's models) each
+ * output is a sum of at most two terms, the same in any order.
+ */
+shp_status_t shp_col2im_1d(const shp_tensor * cols,
+                           int32_t            stride,
+                           int32_t            out_channels,
+                           int32_t            padding,
+                           shp_tensor *       y,
+                           shp_stream_t       stream);
+
 shp_status_t shp_im2col(const shp_tensor * kernel,
                         const shp_tensor * x,
                         int32_t            s0,

@@ -137,6 +137,8 @@ bool node_form_ok(const shp_node & n) {
         case SHP_NODE_CONCAT:
             return f32_of(n.src[0]) && f32_of(n.src[1]) && f32_of(n.dst) && n.op_params[0] >= 0 &&
                    n.op_params[0] <= 3;
+        case SHP_NODE_COL2IM_1D:
+            return f32_of(n.src[0]) && f32_of(n.dst);
         case SHP_NODE_IM2COL:
             // the 1-D form: is_2D 0 and no padding along the absent second
             // dimension (ggml's 1-D rows read there at -p1: zeros)
@@ -1448,6 +1450,8 @@ shp_status_t launch_single(const shp_node & n, shp_stream_t st) {
             return shp_norm(&n.src[0], fparam(n, 0), y, st);
         case SHP_NODE_IM2COL:
             return shp_im2col(&n.src[0], &n.src[1], n.op_params[0], n.op_params[2], n.op_params[4], y, st);
+        case SHP_NODE_COL2IM_1D:
+            return shp_col2im_1d(&n.src[0], n.op_params[0], n.op_params[1], n.op_params[2], y, st);
         default:
             return SHP_ERR_UNSUPPORTED;
     }

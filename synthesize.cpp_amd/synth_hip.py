@@ -93,6 +93,7 @@ def load(path=None):
         "shp_cont_add_leaky_relu": [_PT, _PT, _PT, i32, f, _PT, _PT, vp],
         "shp_concat": [_PT, _PT, i32, _PT, vp],
         "shp_im2col": [_PT, _PT, i32, i32, i32, _PT, vp],
+        "shp_col2im_1d": [_PT, i32, i32, i32, _PT, vp],
         "shp_sub": [_PT, _PT, _PT, vp],
         "shp_tanh": [_PT, _PT, vp],
         "shp_sigmoid": [_PT, _PT, vp],
@@ -576,6 +577,18 @@ def im2col(x, k, s0=1, p0=0, d0=1, dtype=None, out=None):
     return out
 
 
+def col2im_1d(cols, stride, out_channels, padding=0, out=None):
+    """ggml_col2im_1d(cols, stride, out_channels, padding): cols a torch F32
+    tensor (L, K*OC) = ggml [K*OC, L]; returns (OC, T) = ggml [T, OC]."""
+    import torch
+    L, ko = cols.shape
+    t = (L - 1) * stride + ko // out_channels - 2 * padding
+    out = torch.empty((out_channels, max(t, 1)), dtype=torch.float32, device=cols.device) if out is None else out
+    _check(load().shp_col2im_1d(_ref(desc(cols)), int(stride), int(out_channels), int(padding), _ref(desc(out)),
+                                _stream()), "col2im_1d")
+    return out
+
+
 def cpy(x, out=None):
     """ggml_cpy / ggml_cast into F32 of x's shape (x F32, F16 or BF16)."""
     import torch
@@ -590,7 +603,7 @@ def cpy(x, out=None):
 
 (NODE_NOP, NODE_ADD, NODE_MUL, NODE_DIV, NODE_SQR, NODE_SIN, NODE_SCALE, NODE_CPY, NODE_GET_ROWS, NODE_RMS_NORM,
  NODE_SOFT_MAX, NODE_ROPE, NODE_LEAKY_RELU, NODE_SILU, NODE_EXP, NODE_GLU_SWIGLU, NODE_CONCAT, NODE_SUB, NODE_TANH,
- NODE_SIGMOID, NODE_ELU, NODE_GELU_ERF, NODE_CLAMP, NODE_NORM, NODE_IM2COL) = range(25)
+ NODE_SIGMOID, NODE_ELU, NODE_GELU_ERF, NODE_CLAMP, NODE_NORM, NODE_IM2COL, NODE_COL2IM_1D) = range(26)
 NODE_FLAG_OUTPUT = 1
 RUN_KINDS = {-1: "unsupported", 0: "nop", 1: "single", 2: "norm_mul", 3: "norm_mul_rope", 4: "add_norm_mul",
              5: "silu_mul", 6: "add_leaky", 7: "add_scale_leaky", 8: "snake", 9: "snake_guarded", 10: "snake_beta",
@@ -761,6 +774,15 @@ class Graph:
         ow = conv_out_len(iw, k, s0, p0, d0)
         dst = torch.empty((n_, max(ow, 1), ic * k), dtype=dtype or torch.float32, device=t.device)
         return self._op(NODE_IM2COL, dst, [kernel, x], ints={0: s0, 2: p0, 4: d0})
+
+    def col2im_1d(self, cols, stride, out_channels, padding=0):
+        """ggml_col2im_1d: cols (L, K*OC) = ggml [K*OC, L]; the result (OC, T)."""
+        import torch
+        t = self._t(cols)
+        L, ko = t.shape
+        n = (L - 1) * stride + ko // out_channels - 2 * padding
+        dst = torch.empty((out_channels, max(n, 1)), dtype=torch.float32, device=t.device)
+        return self._op(NODE_COL2IM_1D, dst, [cols], ints={0: stride, 1: out_channels, 2: padding})
 
     def glu_swiglu(self, a, b=None, swapped=False):
         t = self._t(a)
