@@ -30,8 +30,9 @@ input sets whose total exceeds 512 MB (cold cache):
     whole tail (copy, bias, residual, leaky) as one launch, and the
     convolution's im2col columns (K = 3 from the time-major input and from the
     channel-major activation's transposed view; at [128,131072] also K = 11
-    dilation 5 and F16 columns of K = 7 dilation 3), on [512,8192],
-    [256,32768] and [128,131072];
+    dilation 5 and F16 columns of K = 7 dilation 3), and the upsampling
+    transposed convolution's col2im_1d scatter into each shape, on
+    [512,8192], [256,32768] and [128,131072];
   - the decode step's non-GEMM work per talker layer (28-layer
     graph), without and with the KV-cache write and the attention softmax;
   - the 512-token prefill step of the 0.6B talker (with the BF16
@@ -497,6 +498,17 @@ def vocoder_rows(R, S, torch, cfg, seed, shapes=((512, 8192), (256, 32768), (128
                             dtype=torch.float16 if f16 else torch.float32)
             return lambda: S.im2col(x, K, 1, p0, d0, out=y)
 
+        def make_col2im(C=C, T=T):
+            # the upsampling transposed convolution's scatter-back into this
+            # shape (vits/operations.cpp:118-140): kernel 2*stride, padding
+            # stride/2; stride 8 into [512,8192] and [256,32768], 2 into
+            # [128,131072] (the VITS decoder's upsampling stages)
+            st = 2 if T >= 131072 else 8
+            K, P = 2 * st, st // 2
+            L = (T + 2 * P - K) // st + 1
+            c, y = randn(L, K * C), empty(C, T)
+            return lambda: S.col2im_1d(c, st, C, P, out=y)
+
         out.append(R.run(cfg, "snake [%d,%d]" % (C, T), 8 * n + 4 * C, make_snake))
         out.append(R.run(cfg, "snake_beta [%d,%d]" % (C, T), 8 * n + 8 * C, make_beta))
         out.append(R.run(cfg, "add_leaky_relu [%d,%d]" % (C, T), 12 * n, make_leaky))
@@ -510,6 +522,9 @@ def vocoder_rows(R, S, torch, cfg, seed, shapes=((512, 8192), (256, 32768), (128
         out.append(R.run(cfg, "im2col K=3 [%d,%d]" % (C, T), 4 * n + 4 * 3 * n, make_im2col))
         out.append(R.run(cfg, "im2col K=3 channel-major view [%d,%d]" % (C, T),
                          4 * n + 4 * 3 * (T + 2) * C, lambda: make_im2col(chmajor=True)))
+        st = 2 if T >= 131072 else 8
+        out.append(R.run(cfg, "col2im_1d K=%d s=%d [%d,%d]" % (2 * st, st, C, T),
+                         4 * 2 * st * C * ((T + st - 2 * st) // st + 1) + 4 * n, make_col2im))
         if (C, T) == (128, 131072):
             out.append(R.run(cfg, "im2col K=11 d=5 [%d,%d]" % (C, T), 4 * n + 4 * 11 * n,
                              lambda: make_im2col(K=11, d0=5)))
@@ -861,6 +876,10 @@ def cpu_op_builders(seed=SEED + 9):
         out.append((cfg, "im2col K=3 channel-major view [%d,%d]" % (C, Tv), 4 * n + 12 * (Tv + 2) * C,
                     lambda g, C=C, Tv=Tv: g.im2col(g.cont_f32(take(Tv, C), [Tv, C], [4 * C, 4]).reshape(C, Tv),
                                                    3, 1, 2, 1)))
+        st = 2 if Tv >= 131072 else 8
+        Lc = (Tv + st - 2 * st) // st + 1
+        out.append((cfg, "col2im_1d K=%d s=%d [%d,%d]" % (2 * st, st, C, Tv), 4 * 2 * st * C * Lc + 4 * n,
+                    lambda g, C=C, st=st, Lc=Lc: g.col2im_1d(take(Lc, 2 * st * C), st, C, st // 2)))
         if (C, Tv) == (128, 131072):
             out.append((cfg, "im2col K=11 d=5 [%d,%d]" % (C, Tv), 48 * n,
                         lambda g, C=C, Tv=Tv: g.im2col(take(C, Tv), 11, 1, 25, 5)))
@@ -1113,7 +1132,7 @@ PMC_OPS = [
     ("cont(transpose) [128,131072]", 134217728), ("add bias[1,C] time-major [128,131072]", 134218240),
     ("conv tail: cont(transpose)+bias+residual->leaky, sum [128,131072]", 268435968),
     ("im2col K=3 [128,131072]", 268435456), ("im2col K=3 channel-major view [128,131072]", 268439552),
-    ("im2col K=7 d=3 f16 [128,131072]", 301989888)]
+    ("im2col K=7 d=3 f16 [128,131072]", 301989888), ("col2im_1d K=4 s=2 [128,131072]", 201326592)]
 
 
 def pmc_large(S, torch):
@@ -1140,6 +1159,7 @@ def pmc_large(S, torch):
     ty, ts = empty(128, 131072), empty(128, 131072)
     cols3, cols3c = empty(1, 131072, 384), empty(1, 131074, 384)   # im2col columns of tr (ggml [T, C]) and of xt^T
     cols7 = torch.empty((1, 131072, 896), dtype=torch.float16, device="cuda")
+    c2i = randn(65536, 512)   # col2im_1d columns: K 4 x 128 channels, 65536 samples in, 131072 out
     fns = [lambda: S.rms_norm_mul(x2, w2, 1e-6), lambda: S.add_rms_norm_mul(x2, x2b, w2, 1e-6),
            lambda: S.qk_norm_rope(q, k, wq, wk, 1e-6, pos, 128, 1e6), lambda: S.swiglu(gt, up),
            lambda: S.add(x2, x2b), lambda: S.snake(xs, al), lambda: S.snake_beta(xs, la, lb),
@@ -1149,7 +1169,7 @@ def pmc_large(S, torch):
            lambda: S.cpy(xt.t(), out=ty), lambda: S.add(tr, tb, out=ty),
            lambda: S.cont_add_leaky_relu(xt.t(), tb, tr, 0.1, out=ty, sum_out=ts),
            lambda: S.im2col(tr, 3, 1, 1, 1, out=cols3), lambda: S.im2col(xt.t(), 3, 1, 2, 1, out=cols3c),
-           lambda: S.im2col(tr, 7, 1, 9, 3, out=cols7)]
+           lambda: S.im2col(tr, 7, 1, 9, 3, out=cols7), lambda: S.col2im_1d(c2i, 2, 128, 1, out=ty)]
     n = CALIB_BYTES // 4
     src = torch.randn(n, device="cuda")
     dst = torch.empty_like(src)

@@ -21,6 +21,10 @@
 //   2. each wave takes one channel of the tile at a time, each lane four
 //      consecutive samples (a 16-byte store when y's rows allow), each value
 //      its <= ceil(K/stride) terms from LDS.
+// With K <= 4*stride each lane locates its four samples' terms once per tile
+// (the offsets depend on the sample, not on the channel), so a channel costs
+// its LDS reads, adds and one store: no division in the channel loop (per-value
+// divisions held an earlier form to 35-49 % of HBM peak at the vocoder shapes).
 // Reads are the columns once (plus the rows two neighbouring tiles share),
 // writes the output once: HBM-bound.
 
@@ -32,6 +36,7 @@ namespace {
 constexpr int kC2iBlock = 256;
 constexpr int kC2iLds   = 4608;  // floats of column rows per block at most (18 KB)
 constexpr int kC2iTt    = 256;   // output samples per tile (64 lanes x 4)
+constexpr int kC2iBatch = 8;     // column-row loads a lane issues before its LDS writes
 
 struct Col2imArgs {
     const char * c;     // columns, rows of K*OC values
@@ -47,13 +52,15 @@ struct Col2imArgs {
     int32_t      oct;   // channels per tile
     int32_t      tt;    // samples per tile
     int32_t      nlmax; // column rows per tile at most
-    int32_t      pad;
+    int32_t      rwp;   // LDS row stride: OCT*K, odd (consecutive rows on different banks)
     FastDiv      sdiv;  // stride
     FastDiv      toc;   // channel tiles
     FastDiv      rdiv;  // OCT*K (the loader's row length)
 };
 
-template <bool V4LOAD, bool V4STORE> __global__ __launch_bounds__(kC2iBlock) void k_col2im_1d(const Col2imArgs a) {
+// NT: the most terms an output can take (ceil(K / stride) <= 4); 0: any.
+template <int NT, bool V4LOAD, bool V4STORE>
+__global__ __launch_bounds__(kC2iBlock) void k_col2im_1d(const Col2imArgs a) {
     extern __shared__ float lds[];
     const int      tid = static_cast<int>(threadIdx.x);
     const uint32_t q   = fastdiv(blockIdx.x, a.toc);
@@ -67,50 +74,95 @@ template <bool V4LOAD, bool V4STORE> __global__ __launch_bounds__(kC2iBlock) voi
     const int lb = u0 >= a.k ? static_cast<int>(fastdiv(static_cast<uint32_t>(u0 - a.k), a.sdiv)) + 1 : 0;
     int       le = static_cast<int>(fastdiv(static_cast<uint32_t>(u0 + ntt - 1), a.sdiv));
     le           = le < a.l - 1 ? le : a.l - 1;
-    const int rw = a.oct * a.k;  // LDS row length
-    // 1. the rows
-    const char * cb  = a.c + static_cast<int64_t>(oc0) * a.k * 4;
-    const int    nrw = noc * a.k;  // values of a row this tile reads
-    if (le >= lb) {
-        const int nrows = le - lb + 1;
-        if constexpr (V4LOAD) {
-            const int q4  = nrw / 4;  // this tile's 16-byte pieces per row (nrw % 4 == 0)
-            const int tot = nrows * static_cast<int>(a.rdiv.d);
-            for (int i = tid; i < tot; i += kC2iBlock) {
-                const int r = static_cast<int>(fastdiv(static_cast<uint32_t>(i), a.rdiv));  // rdiv: a full tile's pieces
-                const int j = i - r * static_cast<int>(a.rdiv.d);
-                if (j < q4) {
-                    const f32x4 v = *reinterpret_cast<const f32x4 *>(cb + static_cast<int64_t>(lb + r) * a.cnb1 + j * 16);
-                    *reinterpret_cast<f32x4 *>(lds + r * rw + j * 4) = v;
+    const int rw = a.rwp;  // LDS row stride: OCT*K rounded up to odd
+    // 1. the rows, walked by running sums: lane tid starts at (tid / w, tid %
+    //    w) of the nrows x w pieces and steps 256 pieces (w = a full tile's
+    //    pieces per row; pieces past this tile's channels are skipped)
+    {
+        constexpr int VL  = V4LOAD ? 4 : 1;
+        const int     w   = static_cast<int>(a.rdiv.d);
+        const int     nrw = noc * a.k / VL;  // this tile's pieces per row
+        int           r   = static_cast<int>(fastdiv(static_cast<uint32_t>(tid), a.rdiv));
+        int           j   = tid - r * w;
+        const int     dr = kC2iBlock / w, dj = kC2iBlock % w;
+        const char *  cb = a.c + static_cast<int64_t>(oc0) * a.k * 4 + static_cast<int64_t>(lb) * a.cnb1;
+        typedef float vl __attribute__((ext_vector_type(VL)));
+        while (lb + r <= le) {
+            // kC2iBatch loads in flight per lane, then their LDS writes (one
+            // load, wait, write per step leaves each lane's loads serialised
+            // behind HBM latency: 35-49 % of peak at the vocoder shapes)
+            vl  v[kC2iBatch];
+            int at[kC2iBatch];
+#pragma unroll
+            for (int b = 0; b < kC2iBatch; ++b) {
+                const bool in = lb + r <= le && j < nrw;
+                at[b]         = in ? r * rw + j * VL : -1;
+                if (in) {
+                    v[b] = *reinterpret_cast<const vl *>(cb + static_cast<int64_t>(r) * a.cnb1 + j * VL * 4);
+                }
+                r += dr;
+                j += dj;
+                if (j >= w) {
+                    j -= w;
+                    ++r;
                 }
             }
-        } else {
-            const int tot = nrows * rw;
-            for (int i = tid; i < tot; i += kC2iBlock) {
-                const int r = static_cast<int>(fastdiv(static_cast<uint32_t>(i), a.rdiv));  // rdiv: rw
-                const int j = i - r * rw;
-                if (j < nrw) {
-                    lds[r * rw + j] = *reinterpret_cast<const float *>(cb + static_cast<int64_t>(lb + r) * a.cnb1 + j * 4);
+#pragma unroll
+            for (int b = 0; b < kC2iBatch; ++b) {
+                if (at[b] >= 0) {
+#pragma unroll
+                    for (int i = 0; i < VL; ++i) {  // the odd row stride leaves rows unaligned
+                        lds[at[b] + i] = v[b][i];
+                    }
                 }
             }
         }
     }
     __syncthreads();
-    // 2. the outputs: wave w, channels w, w+4, ...; lane: samples 4*lane..+3
+    // 2. the outputs: wave w takes channels w, w+4, ...; lane: samples
+    //    4*lane..+3 of the tile (and +256.. when the tile is longer)
     const int wave = tid / kWave, lane = tid % kWave;
-    for (int ocl = wave; ocl < noc; ocl += kC2iBlock / kWave) {
-        char * yrow = a.y + static_cast<int64_t>(oc0 + ocl) * a.ynb1;
-        for (int tl = lane * 4; tl < ntt; tl += kWave * 4) {
-            float v[4];
+    for (int tl = lane * 4; tl < ntt; tl += kWave * 4) {
+        // each value's terms (ascending column order), channel offset aside
+        int      off[4][NT > 0 ? NT : 1];
+        uint32_t ok = 0;  // bit e*4 + j: term j of value e exists
+        if constexpr (NT > 0) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int u  = u0 + tl + e;  // t + p
-                int       hi = static_cast<int>(fastdiv(static_cast<uint32_t>(u), a.sdiv));
-                hi           = hi < a.l - 1 ? hi : a.l - 1;
-                const int lo = u >= a.k ? static_cast<int>(fastdiv(static_cast<uint32_t>(u - a.k), a.sdiv)) + 1 : 0;
-                float     acc = 0.0f;
-                for (int l = lo; l <= hi; ++l) {
-                    acc += lds[(l - lb) * rw + ocl * a.k + (u - l * a.s)];
+                const int u  = u0 + tl + e;
+                const int qh = static_cast<int>(fastdiv(static_cast<uint32_t>(u), a.sdiv));  // the latest column
+                const int r  = u - qh * a.s;
+#pragma unroll
+                for (int j = 0; j < NT; ++j) {
+                    const int  l  = qh - (NT - 1 - j);  // ascending
+                    const int  k  = r + (NT - 1 - j) * a.s;
+                    const bool in = tl + e < ntt && k < a.k && l >= 0 && l <= a.l - 1;
+                    off[e][j]     = in ? (l - lb) * rw + k : 0;  // a term that does not exist reads slot 0, unused
+                    ok |= static_cast<uint32_t>(in) << (e * 4 + j);
+                }
+            }
+        }
+        for (int ocl = wave; ocl < noc; ocl += kC2iBlock / kWave) {
+            char *    yrow = a.y + static_cast<int64_t>(oc0 + ocl) * a.ynb1;
+            const int cko  = ocl * a.k;
+            float     v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float acc = 0.0f;
+                if constexpr (NT > 0) {
+#pragma unroll
+                    for (int j = 0; j < NT; ++j) {
+                        const float x = lds[cko + off[e][j]];
+                        acc           = (ok >> (e * 4 + j)) & 1u ? acc + x : acc;
+                    }
+                } else {
+                    const int u  = u0 + tl + e;
+                    int       hi = static_cast<int>(fastdiv(static_cast<uint32_t>(u), a.sdiv));
+                    hi           = hi < a.l - 1 ? hi : a.l - 1;
+                    const int lo = u >= a.k ? static_cast<int>(fastdiv(static_cast<uint32_t>(u - a.k), a.sdiv)) + 1 : 0;
+                    for (int l = lo; l <= hi && tl + e < ntt; ++l) {
+                        acc += lds[(l - lb) * rw + cko + (u - l * a.s)];
+                    }
                 }
                 v[e] = acc;
             }
@@ -135,6 +187,7 @@ struct Col2imPlan {
     Col2imArgs args{};
     bool       v4load  = false;
     bool       v4store = false;
+    int        nt      = 0;  // ceil(K / stride) when at most 4, else 0 (any)
     unsigned   grid    = 0;
     size_t     shmem   = 0;
 };
@@ -165,7 +218,7 @@ shp_status_t plan_col2im_1d(const shp_tensor * cols, int32_t stride, int32_t oc,
     int64_t tt = kC2iTt, nl = 0, oct = 0;
     for (;; tt /= 2) {
         nl  = (tt - 1 + K - 1) / stride + 2;  // column rows a tile can need
-        oct = kC2iLds / (nl * K);
+        oct = (kC2iLds / nl - 1) / K;         // rows of OCT*K values, stride rounded up to odd
         if (oct >= 1 || tt <= 4) {
             break;
         }
@@ -193,6 +246,7 @@ shp_status_t plan_col2im_1d(const shp_tensor * cols, int32_t stride, int32_t oc,
     a.oct          = static_cast<int32_t>(oct);
     a.tt           = static_cast<int32_t>(tt);
     a.nlmax        = static_cast<int32_t>(nl);
+    a.rwp          = static_cast<int32_t>((oct * K) | 1);
     a.sdiv         = make_fastdiv(static_cast<uint32_t>(stride));
     a.toc          = make_fastdiv(static_cast<uint32_t>(toc));
     // 16-byte loads: every tile's row piece starts and ends on 16 bytes
@@ -200,21 +254,43 @@ shp_status_t plan_col2im_1d(const shp_tensor * cols, int32_t stride, int32_t oc,
                 (oct * K) % 4 == 0 && (oc * K) % 4 == 0;
     a.rdiv     = make_fastdiv(static_cast<uint32_t>(pl.v4load ? oct * K / 4 : oct * K));
     pl.v4store = reinterpret_cast<uintptr_t>(y->data) % 16 == 0 && (oc == 1 || a.ynb1 % 16 == 0);
-    pl.grid    = static_cast<unsigned>(toc * tts);
-    pl.shmem   = static_cast<size_t>(nl * oct * K) * sizeof(float);
+    const int64_t nt = (K + stride - 1) / stride;
+    pl.nt            = nt <= 4 ? static_cast<int>(nt) : 0;
+    pl.grid          = static_cast<unsigned>(toc * tts);
+    pl.shmem   = static_cast<size_t>(nl * a.rwp) * sizeof(float);
     return SHP_OK;
 }
 
-shp_status_t launch_col2im_1d(const Col2imPlan & pl, hipStream_t s) {
+template <int NT> void launch_nt(const Col2imPlan & pl, hipStream_t s) {
     const dim3 g(pl.grid), b(kC2iBlock);
     if (pl.v4load && pl.v4store) {
-        hipLaunchKernelGGL((k_col2im_1d<true, true>), g, b, pl.shmem, s, pl.args);
+        hipLaunchKernelGGL((k_col2im_1d<NT, true, true>), g, b, pl.shmem, s, pl.args);
     } else if (pl.v4load) {
-        hipLaunchKernelGGL((k_col2im_1d<true, false>), g, b, pl.shmem, s, pl.args);
+        hipLaunchKernelGGL((k_col2im_1d<NT, true, false>), g, b, pl.shmem, s, pl.args);
     } else if (pl.v4store) {
-        hipLaunchKernelGGL((k_col2im_1d<false, true>), g, b, pl.shmem, s, pl.args);
+        hipLaunchKernelGGL((k_col2im_1d<NT, false, true>), g, b, pl.shmem, s, pl.args);
     } else {
-        hipLaunchKernelGGL((k_col2im_1d<false, false>), g, b, pl.shmem, s, pl.args);
+        hipLaunchKernelGGL((k_col2im_1d<NT, false, false>), g, b, pl.shmem, s, pl.args);
+    }
+}
+
+shp_status_t launch_col2im_1d(const Col2imPlan & pl, hipStream_t s) {
+    switch (pl.nt) {
+        case 1:
+            launch_nt<1>(pl, s);
+            break;
+        case 2:
+            launch_nt<2>(pl, s);
+            break;
+        case 3:
+            launch_nt<3>(pl, s);
+            break;
+        case 4:
+            launch_nt<4>(pl, s);
+            break;
+        default:
+            launch_nt<0>(pl, s);
+            break;
     }
     return launch_status();
 }
