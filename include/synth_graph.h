@@ -102,6 +102,10 @@ typedef enum shp_node_op {
     SHP_NODE_COL2IM_1D,  /* ggml_col2im_1d (an op of the reference's pinned ggml): i32
                             {stride, out_channels, padding}, which the module's glue fills
                             from the node's own parameters; src[0] the columns */
+    SHP_NODE_PAD,        /* GGML_OP_PAD (ggml_pad, ggml_pad_ext): i32 {lp0, rp0, lp1, rp1,
+                            lp2, rp2, lp3, rp3} (a ninth word, circular padding, must be 0) */
+    SHP_NODE_PAD_REFLECT_1D, /* GGML_OP_PAD_REFLECT_1D: i32 {p0, p1} */
+    SHP_NODE_REPEAT,     /* GGML_OP_REPEAT (ggml_repeat, ggml_repeat_4d): dst's shape */
     SHP_NODE_OP_COUNT
 } shp_node_op;
 

@@ -410,6 +410,35 @@ shp_status_t shp_col2im_1d(const shp_tensor * cols,
                            shp_tensor *       y,
                            shp_stream_t       stream);
 
+/*
+ * ggml_pad_ext(x, lp0, rp0, lp1, rp1, lp2, rp2, lp3, rp3) (and ggml_pad, all
+ * left pads 0): y[i] = x[i - lpad] where every i_d - lpad_d lies inside x,
+ * else 0; the right pads are what y's extents leave (y->ne[d] >= x->ne[d] +
+ * lpad[d]). The transposed convolution's zero-stuffed spread and its edge
+ * widening (kokoro/operations.cpp:190-196,253-260), the text encoder's
+ * relative-position tables (vits/text-encoder.cpp:36,50), the encoders' edge
+ * padding (omnivoice/reference-encoder.cpp:482, qwen3-tts/codec-encoder.cpp:351).
+ * x, y F32, rows contiguous (any row strides), not overlapping; lpad[4] >= 0.
+ */
+shp_status_t shp_pad(const shp_tensor * x, const int32_t * lpad, shp_tensor * y, shp_stream_t stream);
+
+/*
+ * ggml_pad_reflect_1d(x, p0, p1): rows widened by p0 and p1 samples mirrored
+ * about the edge samples (not repeating them), as PyTorch's reflect padding
+ * (qwen3-tts/speaker-encoder.cpp:164). 0 <= p0, p1 < x->ne[0]; y F32 [ne0 + p0
+ * + p1, ne1, ne2, ne3].
+ */
+shp_status_t shp_pad_reflect_1d(const shp_tensor * x, int32_t p0, int32_t p1, shp_tensor * y, shp_stream_t stream);
+
+/*
+ * ggml_repeat(x, y's shape) / ggml_repeat_4d: y[i] = x[i_d mod x->ne_d], each
+ * of y's extents a multiple of x's: the vector broadcast over time and the
+ * frame doubling of the Kokoro decoder (kokoro/operations.cpp:21-24,113-120),
+ * the speaker encoder's statistics broadcast (qwen3-tts/speaker-encoder.cpp:
+ * 356-357), the codec encoder's edge replication (codec-encoder.cpp:183,188).
+ */
+shp_status_t shp_repeat(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
+
 shp_status_t shp_im2col(const shp_tensor * kernel,
                         const shp_tensor * x,
                         int32_t            s0,

@@ -644,6 +644,63 @@ static void op_col2im_1d(const orc_node * n, int ith, int nth) {
     }
 }
 
+/* The padding and tiling copies (no arithmetic): each destination element is
+ * one source element or zero. src1 holds the source and destination extents
+ * and the op's offsets (ggml_cpu_ref.h). Threads take destination rows.
+ *   PAD (ggml_pad / ggml_pad_ext; kokoro/operations.cpp:192,196,
+ *        vits/text-encoder.cpp:36, omnivoice/reference-encoder.cpp:482,
+ *        qwen3-tts/codec-encoder.cpp:351): dst[i] = src[i - lp] where every
+ *        i_d - lp_d lies in [0, src.ne_d), else 0 (the right pads are what
+ *        the destination's extents leave).
+ *   PAD_REFLECT_1D (qwen3-tts/speaker-encoder.cpp:164): along dim 0, i < p0
+ *        reads src[p0 - i], the middle src[i - p0], the right end
+ *        src[2*(ne0 - 1) + p0 - i]: reflection about the edge samples, which
+ *        are not repeated.
+ *   REPEAT (ggml_repeat / ggml_repeat_4d; kokoro/operations.cpp:23,118,
+ *        qwen3-tts/speaker-encoder.cpp:356-357, codec-encoder.cpp:183,188):
+ *        dst[i] = src[i_d mod src.ne_d]. */
+static void op_pad_family(const orc_node * n, int ith, int nth) {
+    const int64_t * v = (const int64_t *) n->src1;
+    const int64_t * sne = v, *dne = v + 4, *off = v + 8;
+    const float *   src = (const float *) n->src0;
+    float *         dst = (float *) n->dst;
+    const int64_t   rows = dne[1] * dne[2] * dne[3];
+    for (int64_t r = ith; r < rows; r += nth) {
+        const int64_t i1 = r % dne[1], i2 = (r / dne[1]) % dne[2], i3 = r / (dne[1] * dne[2]);
+        const int64_t i[4] = { 0, i1, i2, i3 };
+        int64_t       s[4];
+        int           in = 1;
+        for (int d = 1; d < 4; ++d) {
+            if (n->op == ORC_OP_REPEAT) {
+                s[d] = i[d] % sne[d];
+            } else if (n->op == ORC_OP_PAD) {
+                s[d] = i[d] - off[d];
+                in &= s[d] >= 0 && s[d] < sne[d];
+            } else {
+                s[d] = i[d];
+            }
+        }
+        float *       y  = dst + r * dne[0];
+        const float * xr = in ? src + ((s[3] * sne[2] + s[2]) * sne[1] + s[1]) * sne[0] : NULL;
+        for (int64_t i0 = 0; i0 < dne[0]; ++i0) {
+            float val = 0.0f;
+            if (xr != NULL) {
+                if (n->op == ORC_OP_REPEAT) {
+                    val = xr[i0 % sne[0]];
+                } else if (n->op == ORC_OP_PAD) {
+                    const int64_t j = i0 - off[0];
+                    val             = (j >= 0 && j < sne[0]) ? xr[j] : 0.0f;
+                } else {
+                    const int64_t p0 = off[0];
+                    const int64_t j  = i0 < p0 ? p0 - i0 : (i0 < p0 + sne[0] ? i0 - p0 : 2 * (sne[0] - 1) + p0 - i0);
+                    val              = xr[j];
+                }
+            }
+            y[i0] = val;
+        }
+    }
+}
+
 /* ggml_swiglu (single tensor): gate = first half of each row (second when
  * swapped), y = silu(gate) * other half. */
 static void op_glu_swiglu(const orc_node * n, int ith, int nth) {
@@ -766,6 +823,11 @@ static void run_node(const orc_node * n, int ith, int nth) {
             break;
         case ORC_OP_COL2IM_1D:
             op_col2im_1d(n, ith, nth);
+            break;
+        case ORC_OP_PAD:
+        case ORC_OP_PAD_REFLECT_1D:
+        case ORC_OP_REPEAT:
+            op_pad_family(n, ith, nth);
             break;
         default:
             atomic_store(&g_node_error, -1);

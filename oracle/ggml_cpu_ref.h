@@ -54,6 +54,9 @@ enum orc_op {
     ORC_OP_NORM,         /* (x-mean)/sqrt(var+eps), f[0] = eps      ggml_norm           */
     ORC_OP_IM2COL,       /* 1-D convolution columns                 ggml_im2col         */
     ORC_OP_COL2IM_1D,    /* transposed-convolution scatter-back     ggml_col2im_1d      */
+    ORC_OP_PAD,          /* zero padding, left and right per dim    ggml_pad_ext        */
+    ORC_OP_PAD_REFLECT_1D, /* reflect padding along dim 0           ggml_pad_reflect_1d */
+    ORC_OP_REPEAT,       /* tile to a larger shape                  ggml_repeat         */
 };
 
 /*
@@ -90,6 +93,10 @@ enum orc_op {
  *   COL2IM_1D : src0 = F32 columns [K*OC, L]; src1 = int64_t[5] {K, OC, L,
  *               stride, padding}; dst F32 [T, OC], T = (L-1)*stride + K -
  *               2*padding.
+ *   PAD, PAD_REFLECT_1D, REPEAT : src0 contiguous F32; src1 = int64_t[12]:
+ *               src0's ne[0..3], dst's ne[0..3], then the left pads lp[0..3]
+ *               (PAD), {p0, p1, 0, 0} (PAD_REFLECT_1D) or zeros (REPEAT);
+ *               dst contiguous F32.
  */
 typedef struct orc_node {
     int32_t      op;

@@ -25,7 +25,8 @@ F32, F16, Q8_0, Q5_K, I32, BF16 = 0, 1, 8, 13, 26, 30
 
 (OP_ADD, OP_MUL, OP_DIV, OP_RMS_NORM, OP_ROPE_NEOX, OP_SILU, OP_SIN, OP_SQR, OP_EXP, OP_LEAKY_RELU, OP_SCALE_BIAS,
  OP_GET_ROWS, OP_CAST_F32, OP_GLU_SWIGLU, OP_SOFT_MAX, OP_CONT_F32, OP_BINBCAST, OP_SUB, OP_TANH, OP_SIGMOID,
- OP_ELU, OP_GELU_ERF, OP_CLAMP, OP_NORM, OP_IM2COL, OP_COL2IM_1D) = range(1, 27)
+ OP_ELU, OP_GELU_ERF, OP_CLAMP, OP_NORM, OP_IM2COL, OP_COL2IM_1D, OP_PAD, OP_PAD_REFLECT_1D,
+ OP_REPEAT) = range(1, 30)
 
 
 class OrcNode(ctypes.Structure):
@@ -290,6 +291,51 @@ class Graph:
         self.nodes.append(nd)
         self.keep += [dst, cols, view]
         return dst
+
+    def _pad_family(self, op, x, dshape, offs):
+        """x numpy (up to 4 axes, this module's layout); dshape the result's
+        numpy shape; offs the op's ggml-order offsets."""
+        x = self._f32(x)
+        nd = max(x.ndim, len(dshape))
+        sne = list(x.shape[::-1]) + [1] * (4 - x.ndim)
+        dne = list(dshape[::-1]) + [1] * (4 - len(dshape))
+        view = np.array(sne + dne + list(offs) + [0] * (4 - len(offs)), dtype=np.int64)
+        dst = np.empty(tuple(dshape), dtype=np.float32)
+        n = OrcNode()
+        n.op, n.type0, n.ne0, n.nrows = op, F32, dne[0], dne[1] * dne[2] * dne[3]
+        n.src0, n.src1, n.dst = _ptr(x), _ptr(view), _ptr(dst)
+        self.nodes.append(n)
+        self.keep += [dst, x, view]
+        return dst
+
+    def pad_ext(self, x, lp, rp):
+        """ggml_pad_ext(x, lp0, rp0, lp1, rp1, ...): lp, rp per ggml dim (up to 4)."""
+        x = self._f32(x)
+        lp = list(lp) + [0] * (4 - len(lp))
+        rp = list(rp) + [0] * (4 - len(rp))
+        sne = list(x.shape[::-1]) + [1] * (4 - x.ndim)
+        dne = [sne[d] + lp[d] + rp[d] for d in range(4)]
+        nd = max(x.ndim, max([d + 1 for d in range(4) if lp[d] or rp[d]] + [1]))
+        return self._pad_family(OP_PAD, x, tuple(dne[:nd][::-1]), lp)
+
+    def pad(self, x, p):
+        """ggml_pad(x, p0, p1, p2, p3): zeros after the end of each dim."""
+        return self.pad_ext(x, [0, 0, 0, 0], p)
+
+    def pad_reflect_1d(self, x, p0, p1):
+        """ggml_pad_reflect_1d(x, p0, p1) (p0, p1 < ne0)."""
+        x = self._f32(x)
+        if p0 >= x.shape[-1] or p1 >= x.shape[-1] or p0 < 0 or p1 < 0:
+            raise ValueError("pad_reflect_1d: a pad of the row's length or more")
+        return self._pad_family(OP_PAD_REFLECT_1D, x, x.shape[:-1] + (x.shape[-1] + p0 + p1,), [p0, 0, 0, 0])
+
+    def repeat(self, x, shape):
+        """ggml_repeat(x, b) with b of numpy shape `shape` (every extent a multiple of x's)."""
+        x = self._f32(x)
+        xs = (1,) * (len(shape) - x.ndim) + x.shape
+        if any(d % s for d, s in zip(shape, xs)):
+            raise ValueError("repeat: an extent not a multiple of the source's")
+        return self._pad_family(OP_REPEAT, x.reshape(xs), tuple(shape), [0, 0, 0, 0])
 
     def glu_swiglu(self, a, swapped=False):
         a = self._f32(a)

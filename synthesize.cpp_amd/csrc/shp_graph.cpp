@@ -139,6 +139,22 @@ bool node_form_ok(const shp_node & n) {
                    n.op_params[0] <= 3;
         case SHP_NODE_COL2IM_1D:
             return f32_of(n.src[0]) && f32_of(n.dst);
+        case SHP_NODE_PAD: {
+            // {lp0, rp0, ..., lp3, rp3}; no circular padding; the extents add up
+            if (n.op_params[8] != 0 || !f32_of(n.src[0]) || !f32_of(n.dst)) {
+                return false;
+            }
+            for (int d = 0; d < 4; ++d) {
+                const int32_t lp = n.op_params[2 * d], rp = n.op_params[2 * d + 1];
+                if (lp < 0 || rp < 0 || n.dst.ne[d] != n.src[0].ne[d] + lp + rp) {
+                    return false;
+                }
+            }
+            return true;
+        }
+        case SHP_NODE_PAD_REFLECT_1D:
+        case SHP_NODE_REPEAT:
+            return f32_of(n.src[0]) && f32_of(n.dst);
         case SHP_NODE_IM2COL:
             // the 1-D form: is_2D 0 and no padding along the absent second
             // dimension (ggml's 1-D rows read there at -p1: zeros)
@@ -1452,6 +1468,14 @@ shp_status_t launch_single(const shp_node & n, shp_stream_t st) {
             return shp_im2col(&n.src[0], &n.src[1], n.op_params[0], n.op_params[2], n.op_params[4], y, st);
         case SHP_NODE_COL2IM_1D:
             return shp_col2im_1d(&n.src[0], n.op_params[0], n.op_params[1], n.op_params[2], y, st);
+        case SHP_NODE_PAD: {
+            const int32_t lp[4] = { n.op_params[0], n.op_params[2], n.op_params[4], n.op_params[6] };
+            return shp_pad(&n.src[0], lp, y, st);
+        }
+        case SHP_NODE_PAD_REFLECT_1D:
+            return shp_pad_reflect_1d(&n.src[0], n.op_params[0], n.op_params[1], y, st);
+        case SHP_NODE_REPEAT:
+            return shp_repeat(&n.src[0], y, st);
         default:
             return SHP_ERR_UNSUPPORTED;
     }

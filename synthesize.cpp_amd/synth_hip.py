@@ -94,6 +94,9 @@ def load(path=None):
         "shp_concat": [_PT, _PT, i32, _PT, vp],
         "shp_im2col": [_PT, _PT, i32, i32, i32, _PT, vp],
         "shp_col2im_1d": [_PT, i32, i32, i32, _PT, vp],
+        "shp_pad": [_PT, ctypes.POINTER(ctypes.c_int32), _PT, vp],
+        "shp_pad_reflect_1d": [_PT, i32, i32, _PT, vp],
+        "shp_repeat": [_PT, _PT, vp],
         "shp_sub": [_PT, _PT, _PT, vp],
         "shp_tanh": [_PT, _PT, vp],
         "shp_sigmoid": [_PT, _PT, vp],
@@ -589,6 +592,36 @@ def col2im_1d(cols, stride, out_channels, padding=0, out=None):
     return out
 
 
+def pad_ext(x, lp, rp, out=None):
+    """ggml_pad_ext(x, lp0, rp0, ...): lp, rp per ggml dimension (up to 4)."""
+    import torch
+    lp = list(lp) + [0] * (4 - len(lp))
+    rp = list(rp) + [0] * (4 - len(rp))
+    if out is None:
+        ne = list(x.shape[::-1]) + [1] * (4 - x.dim())
+        nd = max(x.dim(), max([d + 1 for d in range(4) if lp[d] or rp[d]] + [1]))
+        out = torch.empty([ne[d] + lp[d] + rp[d] for d in range(nd)][::-1], dtype=torch.float32, device=x.device)
+    _check(load().shp_pad(_ref(desc(x)), (ctypes.c_int32 * 4)(*lp), _ref(desc(out)), _stream()), "pad")
+    return out
+
+
+def pad_reflect_1d(x, p0, p1, out=None):
+    """ggml_pad_reflect_1d(x, p0, p1)."""
+    import torch
+    out = torch.empty(tuple(x.shape[:-1]) + (x.shape[-1] + p0 + p1,), dtype=torch.float32,
+                      device=x.device) if out is None else out
+    _check(load().shp_pad_reflect_1d(_ref(desc(x)), int(p0), int(p1), _ref(desc(out)), _stream()), "pad_reflect_1d")
+    return out
+
+
+def repeat(x, shape, out=None):
+    """ggml_repeat(x, a tensor of torch shape `shape`)."""
+    import torch
+    out = torch.empty(tuple(shape), dtype=torch.float32, device=x.device) if out is None else out
+    _check(load().shp_repeat(_ref(desc(x)), _ref(desc(out)), _stream()), "repeat")
+    return out
+
+
 def cpy(x, out=None):
     """ggml_cpy / ggml_cast into F32 of x's shape (x F32, F16 or BF16)."""
     import torch
@@ -603,7 +636,8 @@ def cpy(x, out=None):
 
 (NODE_NOP, NODE_ADD, NODE_MUL, NODE_DIV, NODE_SQR, NODE_SIN, NODE_SCALE, NODE_CPY, NODE_GET_ROWS, NODE_RMS_NORM,
  NODE_SOFT_MAX, NODE_ROPE, NODE_LEAKY_RELU, NODE_SILU, NODE_EXP, NODE_GLU_SWIGLU, NODE_CONCAT, NODE_SUB, NODE_TANH,
- NODE_SIGMOID, NODE_ELU, NODE_GELU_ERF, NODE_CLAMP, NODE_NORM, NODE_IM2COL, NODE_COL2IM_1D) = range(26)
+ NODE_SIGMOID, NODE_ELU, NODE_GELU_ERF, NODE_CLAMP, NODE_NORM, NODE_IM2COL, NODE_COL2IM_1D, NODE_PAD,
+ NODE_PAD_REFLECT_1D, NODE_REPEAT) = range(29)
 NODE_FLAG_OUTPUT = 1
 RUN_KINDS = {-1: "unsupported", 0: "nop", 1: "single", 2: "norm_mul", 3: "norm_mul_rope", 4: "add_norm_mul",
              5: "silu_mul", 6: "add_leaky", 7: "add_scale_leaky", 8: "snake", 9: "snake_guarded", 10: "snake_beta",
@@ -783,6 +817,28 @@ class Graph:
         n = (L - 1) * stride + ko // out_channels - 2 * padding
         dst = torch.empty((out_channels, max(n, 1)), dtype=torch.float32, device=t.device)
         return self._op(NODE_COL2IM_1D, dst, [cols], ints={0: stride, 1: out_channels, 2: padding})
+
+    def pad_ext(self, x, lp, rp):
+        """ggml_pad_ext (ggml_pad: lp all 0)."""
+        import torch
+        t = self._t(x)
+        lp = list(lp) + [0] * (4 - len(lp))
+        rp = list(rp) + [0] * (4 - len(rp))
+        ne = list(t.shape[::-1]) + [1] * (4 - t.dim())
+        nd = max(t.dim(), max([d + 1 for d in range(4) if lp[d] or rp[d]] + [1]))
+        dst = torch.empty([ne[d] + lp[d] + rp[d] for d in range(nd)][::-1], dtype=torch.float32, device=t.device)
+        return self._op(NODE_PAD, dst, [x], ints={2 * d + k: (lp, rp)[k][d] for d in range(4) for k in range(2)})
+
+    def pad(self, x, p):
+        return self.pad_ext(x, [0, 0, 0, 0], p)
+
+    def pad_reflect_1d(self, x, p0, p1):
+        t = self._t(x)
+        return self._op(NODE_PAD_REFLECT_1D, self._like(x, tuple(t.shape[:-1]) + (t.shape[-1] + p0 + p1,)), [x],
+                        ints={0: p0, 1: p1})
+
+    def repeat(self, x, shape):
+        return self._op(NODE_REPEAT, self._like(x, tuple(shape)), [x])
 
     def glu_swiglu(self, a, b=None, swapped=False):
         t = self._t(a)

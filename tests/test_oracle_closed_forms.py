@@ -656,3 +656,66 @@ def test_norm_against_double_and_invariants():
     assert (const == 0).all()
     # eps is inside the sqrt: with variance ~1e-8 the result is far below 1 in size
     assert np.abs(tiny).max() < 0.1
+
+
+# ---------------------------------------------------------------------------
+# ggml_pad / ggml_pad_ext, ggml_pad_reflect_1d, ggml_repeat
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("shape,lp,rp", [((7,), [2], [3]), ((4, 9), [0, 1], [5, 2]), ((3, 1, 5), [1, 0, 0], [0, 7, 2]),
+                                         ((2, 3, 4, 5), [1, 2, 0, 1], [2, 0, 3, 0]), ((6, 10), [0, 0], [0, 0])])
+def test_pad_ext_is_numpy_constant_pad(shape, lp, rp):
+    """ggml_pad_ext: numpy's zero pad, ggml's (lp_d, rp_d) per dim d on the
+    reversed numpy axis; lp and rp swapped differ."""
+    x = np.random.default_rng(len(shape) + sum(lp)).standard_normal(shape).astype(np.float32) + 3
+    nd = len(shape)
+    ref = np.pad(x, [(lp[nd - 1 - a], rp[nd - 1 - a]) for a in range(nd)])
+    got = R.run(lambda g: g.pad_ext(x, lp, rp))
+    assert got.shape == ref.shape and np.array_equal(got, ref)
+    if lp != rp:
+        assert not np.array_equal(R.run(lambda g: g.pad_ext(x, rp, lp)), ref)
+
+
+def test_pad_spreads_frames_with_zeros():
+    """kokoro/operations.cpp:190-193: padding the unit axis of [C, 1, L] by
+    stride - 1 puts stride - 1 zero frames after every frame."""
+    C, L, S = 5, 6, 4
+    x = np.random.default_rng(3).standard_normal((L, 1, C)).astype(np.float32)   # ggml [C, 1, L]
+    got = R.run(lambda g: g.pad(x, [0, S - 1, 0, 0])).reshape(L * S, C)
+    ref = np.zeros((L * S, C), np.float32)
+    ref[::S] = x[:, 0]
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("shape,p0,p1", [((3, 10), 2, 3), ((16,), 1, 1), ((2, 3, 8), 7, 0), ((4, 5), 0, 4)])
+def test_pad_reflect_1d_is_numpy_reflect(shape, p0, p1):
+    """ggml_pad_reflect_1d: numpy's 'reflect' (the edge sample not repeated),
+    which its 'symmetric' mode (edge repeated) is not; pads of the row's
+    length are refused."""
+    x = np.random.default_rng(p0 * 10 + p1).standard_normal(shape).astype(np.float32)
+    pads = [(0, 0)] * (len(shape) - 1) + [(p0, p1)]
+    got = R.run(lambda g: g.pad_reflect_1d(x, p0, p1))
+    assert np.array_equal(got, np.pad(x, pads, mode="reflect"))
+    if p0 or p1:
+        assert not np.array_equal(got, np.pad(x, pads, mode="symmetric"))
+    with pytest.raises(ValueError):
+        R.Graph().pad_reflect_1d(x, shape[-1], 0)
+
+
+@pytest.mark.parametrize("shape,target", [((1, 7), (5, 7)), ((3, 1, 4), (3, 2, 4)), ((2, 3), (4, 9)), ((5,), (2, 3, 10)),
+                                          ((1, 1, 1, 2), (2, 3, 2, 6))])
+def test_repeat_is_numpy_tile(shape, target):
+    """ggml_repeat: numpy's tile of x to the target shape (kokoro's
+    broadcast_over_time and upsample_nearest_2x, :21-24,113-120)."""
+    x = np.random.default_rng(sum(target)).standard_normal(shape).astype(np.float32)
+    xs = x.reshape((1,) * (len(target) - x.ndim) + x.shape)
+    ref = np.tile(xs, [t // s for t, s in zip(target, xs.shape)])
+    assert np.array_equal(R.run(lambda g: g.repeat(x, target)), ref)
+
+
+def test_repeat_doubles_frames():
+    """upsample_nearest_2x (kokoro/operations.cpp:113-120): repeating [C, 1, L]
+    to [C, 2, L] duplicates every frame."""
+    x = np.random.default_rng(4).standard_normal((6, 1, 5)).astype(np.float32)   # ggml [5, 1, 6]
+    got = R.run(lambda g: g.repeat(x, (6, 2, 5))).reshape(12, 5)
+    assert np.array_equal(got, np.repeat(x[:, 0], 2, axis=0))
