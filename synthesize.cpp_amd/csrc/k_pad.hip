@@ -10,12 +10,14 @@
 //     (kokoro/operations.cpp:23,118 -- the frame doubling of
 //     upsample_nearest_2x --, qwen3-tts/speaker-encoder.cpp:356-357,
 //     codec-encoder.cpp:183,188)
-// One lane per four consecutive destination values of a row: one 16-byte
-// nontemporal store when the destination's rows allow; a destination row
-// that the padding puts outside the source is stored as zeros without loads.
-// Source loads are per value, coalesced across lanes (the ops are write-bound:
-// the spread writes stride x its input, the repeat reads a small source many
-// times from cache).
+// One lane per four consecutive destination values of a row, one 16-byte
+// nontemporal store: from the row's start when the destination's rows are
+// 16-byte aligned, else from its first 16-byte boundary, with the few values
+// before it stored one by one (four values per lane at the row's own start
+// made every store instruction a 16-byte-strided scatter: 15 % of HBM peak for
+// a row padded by 3 + 4). The four source values come in one 16-byte load
+// where they are contiguous and aligned. A destination row the padding puts outside the source is stored as
+// zeros without loads.
 
 #include "shp_internal.hpp"
 
@@ -32,14 +34,14 @@ struct PadArgs {
     int64_t      xne[4];
     int64_t      off[4];   // left pads (zero pad), {p0} (reflect)
     int64_t      yne0;
-    FastDiv      quads;    // quads per destination row
+    FastDiv      quads;    // units (V values) per destination row
     FastDiv      yne1;
     FastDiv      yne2;
     FastDiv      xne0;     // repeat: source extents
     FastDiv      xne1;
     FastDiv      xne2;
     FastDiv      xne3;
-    int64_t      total;    // quads in all
+    int64_t      total;    // units in all
 };
 
 template <int MODE> __device__ __forceinline__ int64_t src_index0(const PadArgs & a, int64_t i0, bool & in) {
@@ -57,11 +59,19 @@ template <int MODE> __device__ __forceinline__ int64_t src_index0(const PadArgs 
     }
 }
 
-template <int MODE, bool V4> __global__ __launch_bounds__(256) void k_pad(const PadArgs a) {
+// V values per lane: 4 (consecutive, one 16-byte store: the destination's rows
+// are 16-byte aligned) or 1 (consecutive lanes on consecutive values, so each
+// store instruction is one contiguous run). V4LOAD: the four source values are
+// contiguous and 16-byte aligned whenever they are all inside the source (zero
+// pad with lp0 and x's rows multiples of 4 values; repeat with x's rows so).
+// SHIFT (V = 4, rows not 16-byte aligned): unit 0 of a row is its first h
+// values, up to the first 16-byte boundary (scalar stores), unit u >= 1 the
+// four from h + 4(u-1) (one 16-byte store when whole).
+template <int MODE, int V, bool V4LOAD, bool SHIFT> __global__ __launch_bounds__(256) void k_pad(const PadArgs a) {
     const int64_t step = static_cast<int64_t>(gridDim.x) * 256;
     for (int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; t < a.total; t += step) {
-        const uint32_t r  = fastdiv(static_cast<uint32_t>(t), a.quads);  // destination row
-        const int64_t  i0 = (t - static_cast<int64_t>(r) * a.quads.d) * 4;
+        const uint32_t r  = fastdiv(static_cast<uint32_t>(t), a.quads);  // destination row (quads: units per row)
+        const int64_t  u  = t - static_cast<int64_t>(r) * a.quads.d;
         const uint32_t q1 = fastdiv(r, a.yne1);
         const uint32_t i1 = r - q1 * a.yne1.d;
         const uint32_t i3 = fastdiv(q1, a.yne2);
@@ -84,24 +94,62 @@ template <int MODE, bool V4> __global__ __launch_bounds__(256) void k_pad(const 
             s3 = fastmod(i3, a.xne3);
         }
         const char * xr = a.x + s1 * a.xnb[1] + s2 * a.xnb[2] + s3 * a.xnb[3];
-        float        v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            bool          in = false;
-            const int64_t j  = src_index0<MODE>(a, i0 + e, in);
-            v[e]             = (rin && in && i0 + e < a.yne0) ? reinterpret_cast<const float *>(xr)[j] : 0.0f;
-        }
-        char * yr = a.y + static_cast<int64_t>(i1) * a.ynb[1] + static_cast<int64_t>(i2) * a.ynb[2] +
+        char *       yr = a.y + static_cast<int64_t>(i1) * a.ynb[1] + static_cast<int64_t>(i2) * a.ynb[2] +
                     static_cast<int64_t>(i3) * a.ynb[3];
-        if (V4 && i0 + 3 < a.yne0) {
-            __builtin_nontemporal_store(f32x4{ v[0], v[1], v[2], v[3] }, reinterpret_cast<f32x4 *>(yr + i0 * 4));
+        int64_t i0;
+        if constexpr (SHIFT) {
+            const int h = static_cast<int>(((16 - reinterpret_cast<uintptr_t>(yr) % 16) % 16) / 4);
+            if (u == 0) {  // the head: h values, scalar
+                for (int e = 0; e < h && e < a.yne0; ++e) {
+                    bool          in = false;
+                    const int64_t j  = src_index0<MODE>(a, e, in);
+                    __builtin_nontemporal_store((rin && in) ? reinterpret_cast<const float *>(xr)[j] : 0.0f,
+                                                reinterpret_cast<float *>(yr) + e);
+                }
+                continue;
+            }
+            i0 = h + (u - 1) * 4;
+            if (i0 >= a.yne0) {
+                continue;
+            }
         } else {
+            i0 = u * V;
+        }
+        float        v[V];
+        bool         done = false;
+        if constexpr (V4LOAD && V == 4) {
+            bool          in = false;
+            const int64_t j  = src_index0<MODE>(a, i0, in);
+            if (rin && in && j + 3 < a.xne[0] && i0 + 3 < a.yne0) {
+                const f32x4 w = *reinterpret_cast<const f32x4 *>(xr + j * 4);
+                v[0] = w.x;
+                v[1] = w.y;
+                v[2] = w.z;
+                v[3] = w.w;
+                done = true;
+            }
+        }
+        if (!done) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                if (i0 + e < a.yne0) {
-                    __builtin_nontemporal_store(v[e], reinterpret_cast<float *>(yr) + i0 + e);
+            for (int e = 0; e < V; ++e) {
+                bool          in = false;
+                const int64_t j  = src_index0<MODE>(a, i0 + e, in);
+                v[e]             = (rin && in && i0 + e < a.yne0) ? reinterpret_cast<const float *>(xr)[j] : 0.0f;
+            }
+        }
+        if constexpr (V == 4) {
+            if (i0 + 3 < a.yne0) {
+                __builtin_nontemporal_store(f32x4{ v[0], v[1], v[2], v[3] }, reinterpret_cast<f32x4 *>(yr + i0 * 4));
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (i0 + e < a.yne0) {
+                        __builtin_nontemporal_store(v[e], reinterpret_cast<float *>(yr) + i0 + e);
+                    }
                 }
             }
+        } else {
+            __builtin_nontemporal_store(v[0], reinterpret_cast<float *>(yr) + i0);
         }
     }
 }
@@ -118,7 +166,11 @@ shp_status_t pad_entry(const shp_tensor * x, const int64_t (&off)[4], shp_tensor
     if (spans_overlap(*x, *y)) {
         return SHP_ERR_UNSUPPORTED;
     }
-    const int64_t rows = nrows(*y), quads = (y->ne[0] + 3) / 4;
+    const bool    v4    = rows_aligned(*y, 16);
+    const bool    shift = !v4 && reinterpret_cast<uintptr_t>(y->data) % 4 == 0 && y->nb[1] % 4 == 0 &&
+                       y->nb[2] % 4 == 0 && y->nb[3] % 4 == 0;
+    const int64_t rows  = nrows(*y);
+    const int64_t quads = v4 ? (y->ne[0] + 3) / 4 : (shift ? (y->ne[0] + 3) / 4 + 1 : y->ne[0]);
     if (quads > INT32_MAX || rows > INT32_MAX || y->ne[0] > INT32_MAX || x->ne[0] > INT32_MAX ||
         quads * rows > INT32_MAX) {
         return SHP_ERR_UNSUPPORTED;
@@ -144,13 +196,18 @@ shp_status_t pad_entry(const shp_tensor * x, const int64_t (&off)[4], shp_tensor
     a.xne2  = make_fastdiv(static_cast<uint32_t>(x->ne[2]));
     a.xne3  = make_fastdiv(static_cast<uint32_t>(x->ne[3]));
     a.total = quads * rows;
-    const bool     v4     = rows_aligned(*y, 16);
+    const bool v4load = MODE != kPadReflect && rows_aligned(*x, 16) && x->ne[0] % 4 == 0 && off[0] % 4 == 0;
     const int64_t  blocks = (a.total + 255) / 256;
     const unsigned grid   = static_cast<unsigned>(blocks < (1 << 20) ? blocks : (1 << 20));
-    if (v4) {
-        hipLaunchKernelGGL((k_pad<MODE, true>), dim3(grid), dim3(256), 0, as_stream(stream), a);
+    const dim3     g(grid), b(256);
+    if (v4 && v4load) {
+        hipLaunchKernelGGL((k_pad<MODE, 4, true, false>), g, b, 0, as_stream(stream), a);
+    } else if (v4) {
+        hipLaunchKernelGGL((k_pad<MODE, 4, false, false>), g, b, 0, as_stream(stream), a);
+    } else if (shift) {
+        hipLaunchKernelGGL((k_pad<MODE, 4, false, true>), g, b, 0, as_stream(stream), a);
     } else {
-        hipLaunchKernelGGL((k_pad<MODE, false>), dim3(grid), dim3(256), 0, as_stream(stream), a);
+        hipLaunchKernelGGL((k_pad<MODE, 1, false, false>), g, b, 0, as_stream(stream), a);
     }
     return launch_status();
 }
