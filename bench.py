@@ -30,8 +30,9 @@ input sets whose total exceeds 512 MB (cold cache):
     whole tail (copy, bias, residual, leaky) as one launch, and the
     convolution's im2col columns (K = 3 from the time-major input and from the
     channel-major activation's transposed view; at [128,131072] also K = 11
-    dilation 5 and F16 columns of K = 7 dilation 3), and the upsampling
-    transposed convolution's col2im_1d scatter into each shape, on
+    dilation 5 and F16 columns of K = 7 dilation 3), the upsampling
+    transposed convolution's col2im_1d scatter into each shape, and Kokoro's
+    zero-stuffed spread, frame doubling and a time-axis edge padding, on
     [512,8192], [256,32768] and [128,131072];
   - the decode step's non-GEMM work per talker layer (28-layer
     graph), without and with the KV-cache write and the attention softmax;
@@ -509,6 +510,24 @@ def vocoder_rows(R, S, torch, cfg, seed, shapes=((512, 8192), (256, 32768), (128
             c, y = randn(L, K * C), empty(C, T)
             return lambda: S.col2im_1d(c, st, C, P, out=y)
 
+        def make_spread(C=C, T=T):
+            # kokoro's transposed convolution front (kokoro/operations.cpp:
+            # 190-196): stride - 1 zero frames after every frame of [C, 1, L]
+            st = 2 if T >= 131072 else 8
+            x, y = randn(T // st, 1, C), empty(T // st, st, C)
+            return lambda: S.pad_ext(x, [0, 0], [0, st - 1], out=y)
+
+        def make_double(C=C, T=T):
+            # kokoro's upsample_nearest_2x (:113-120): [C, 1, T/2] to [C, 2, T/2]
+            x, y = randn(T // 2, 1, C), empty(T // 2, 2, C)
+            return lambda: S.repeat(x, (T // 2, 2, C), out=y)
+
+        def make_edge(C=C, T=T):
+            # edge padding along time of a time-contiguous activation
+            # (codec-encoder.cpp:351): rows of T + 7 values, not 16-byte aligned
+            x, y = randn(C, T), empty(C, T + 7)
+            return lambda: S.pad_ext(x, [3], [4], out=y)
+
         out.append(R.run(cfg, "snake [%d,%d]" % (C, T), 8 * n + 4 * C, make_snake))
         out.append(R.run(cfg, "snake_beta [%d,%d]" % (C, T), 8 * n + 8 * C, make_beta))
         out.append(R.run(cfg, "add_leaky_relu [%d,%d]" % (C, T), 12 * n, make_leaky))
@@ -523,6 +542,9 @@ def vocoder_rows(R, S, torch, cfg, seed, shapes=((512, 8192), (256, 32768), (128
         out.append(R.run(cfg, "im2col K=3 channel-major view [%d,%d]" % (C, T),
                          4 * n + 4 * 3 * (T + 2) * C, lambda: make_im2col(chmajor=True)))
         st = 2 if T >= 131072 else 8
+        out.append(R.run(cfg, "pad: spread x%d [%d,1,%d]" % (st, C, T // st), 4 * n // st * (1 + st), make_spread))
+        out.append(R.run(cfg, "repeat: frames x2 [%d,1,%d]" % (C, T // 2), 6 * n, make_double))
+        out.append(R.run(cfg, "pad_ext: time +3/+4 [%d,%d]" % (T, C), 4 * n + 4 * C * (T + 7), make_edge))
         out.append(R.run(cfg, "col2im_1d K=%d s=%d [%d,%d]" % (2 * st, st, C, T),
                          4 * 2 * st * C * ((T + st - 2 * st) // st + 1) + 4 * n, make_col2im))
         if (C, T) == (128, 131072):
@@ -877,6 +899,12 @@ def cpu_op_builders(seed=SEED + 9):
                     lambda g, C=C, Tv=Tv: g.im2col(g.cont_f32(take(Tv, C), [Tv, C], [4 * C, 4]).reshape(C, Tv),
                                                    3, 1, 2, 1)))
         st = 2 if Tv >= 131072 else 8
+        out.append((cfg, "pad: spread x%d [%d,1,%d]" % (st, C, Tv // st), 4 * n // st * (1 + st),
+                    lambda g, C=C, Tv=Tv, st=st: g.pad(take(Tv // st, 1, C), [0, st - 1, 0, 0])))
+        out.append((cfg, "repeat: frames x2 [%d,1,%d]" % (C, Tv // 2), 6 * n,
+                    lambda g, C=C, Tv=Tv: g.repeat(take(Tv // 2, 1, C), (Tv // 2, 2, C))))
+        out.append((cfg, "pad_ext: time +3/+4 [%d,%d]" % (Tv, C), 4 * n + 4 * C * (Tv + 7),
+                    lambda g, C=C, Tv=Tv: g.pad_ext(take(C, Tv), [3], [4])))
         Lc = (Tv + st - 2 * st) // st + 1
         out.append((cfg, "col2im_1d K=%d s=%d [%d,%d]" % (2 * st, st, C, Tv), 4 * 2 * st * C * Lc + 4 * n,
                     lambda g, C=C, st=st, Lc=Lc: g.col2im_1d(take(Lc, 2 * st * C), st, C, st // 2)))
