@@ -35,7 +35,7 @@ namespace {
 
 constexpr int kC2iBlock = 256;
 constexpr int kC2iLds   = 4608;  // floats of column rows per block at most (18 KB)
-constexpr int kC2iTt    = 256;   // output samples per tile (64 lanes x 4)
+constexpr int kC2iTt    = 256;   // output samples per tile, a power of two from 16 to 1024
 constexpr int kC2iBatch = 8;     // column-row loads a lane issues before its LDS writes
 
 struct Col2imArgs {
@@ -119,10 +119,11 @@ __global__ __launch_bounds__(kC2iBlock) void k_col2im_1d(const Col2imArgs a) {
         }
     }
     __syncthreads();
-    // 2. the outputs: wave w takes channels w, w+4, ...; lane: samples
-    //    4*lane..+3 of the tile (and +256.. when the tile is longer)
-    const int wave = tid / kWave, lane = tid % kWave;
-    for (int tl = lane * 4; tl < ntt; tl += kWave * 4) {
+    // 2. the outputs: the tile's tt/4 quads of four samples x its channels,
+    //    256 at a time; with tt/4 dividing 256 a thread keeps one quad (its
+    //    terms' offsets are found once) and steps channels by 256 / (tt/4)
+    const int nq = a.tt / 4;
+    for (int tl = (tid % nq) * 4; tl < ntt; tl += kC2iBlock * 4) {
         // each value's terms (ascending column order), channel offset aside
         int      off[4][NT > 0 ? NT : 1];
         uint32_t ok = 0;  // bit e*4 + j: term j of value e exists
@@ -142,7 +143,7 @@ __global__ __launch_bounds__(kC2iBlock) void k_col2im_1d(const Col2imArgs a) {
                 }
             }
         }
-        for (int ocl = wave; ocl < noc; ocl += kC2iBlock / kWave) {
+        for (int ocl = tid / nq; ocl < noc; ocl += kC2iBlock / nq) {
             char *    yrow = a.y + static_cast<int64_t>(oc0 + ocl) * a.ynb1;
             const int cko  = ocl * a.k;
             float     v[4];
