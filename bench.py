@@ -560,6 +560,26 @@ def vocoder_rows(R, S, torch, cfg, seed, shapes=((512, 8192), (256, 32768), (128
     return out
 
 
+def talker_input_rows(R, S, torch, cfg, seed, T=8192, H=2048, at=16):
+    """The talker's prefill input assembly (qwen3-tts/talker.cpp:86-118):
+    ggml_acc of a codec run of T - at positions into the [H, T] text stream
+    from position `at`, out of place (a's copy with the run added: a read,
+    the run read, y written) and in ggml's inplace form (the window alone)."""
+    g, randn, empty, bf16 = gen(torch, seed)
+    nb1 = 4 * H
+
+    def make(inplace):
+        def build():
+            a, b, y = randn(T, H), randn(T - at, H), empty(T, H)
+            if inplace:
+                return lambda: S.acc(a, b, nb1, nb1 * T, nb1 * T, at * nb1, inplace=True)
+            return lambda: S.acc(a, b, nb1, nb1 * T, nb1 * T, at * nb1, out=y)
+        return build
+    n, m = T * H, (T - at) * H
+    R.run(cfg, "acc: codec run +%d@%d into text [%d,%d]" % (T - at, at, H, T), 4 * (2 * n + m), make(False))
+    R.run(cfg, "acc inplace: codec run +%d@%d [%d,%d]" % (T - at, at, H, T), 12 * m, make(True))
+
+
 def floor_rows(R, S, torch, seed=SEED + 8):
     """Same-run floors the op rows are read against, each timed as the op rows
     are (cold rotating sets, HIP graph, median of chunks):
@@ -849,6 +869,9 @@ def cpu_op_builders(seed=SEED + 9):
                 lambda g: R.add_rms_norm_w(g, take(T, H), take(T, H), bf16(H), eps, R.BF16)))
     out.append((cfg, "swiglu [%d,%d]" % (F_, T), 3 * T * F_ * f32, lambda g: R.swiglu(g, take(T, F_), take(T, F_))))
     out.append((cfg, "add [%d,%d]" % (H, T), 3 * T * H * f32, lambda g: g.add(take(T, H), take(T, H))))
+    at = 16
+    out.append((cfg, "acc: codec run +%d@%d into text [%d,%d]" % (T - at, at, H, T), 4 * (2 * T * H + (T - at) * H),
+                lambda g: g.acc(take(T, H), take(T - at, H), 4 * H, 4 * H * T, 4 * H * T, at * 4 * H)))
 
     for kind, synth, rb, typ in (("q8_0", F.q8_0_synthetic, 1024 // 32 * 34, R.Q8_0),
                                  ("q5_k", F.q5_k_synthetic, 1024 // 256 * 176, R.Q5_K)):
@@ -1420,6 +1443,7 @@ def main():
     q8_rows(R, S, torch, "configs[2]", SEED + 3)
     q8_rows(R, S, torch, "configs[2]", SEED + 6, kind="q5_k")
     vocoder_rows(R, S, torch, "configs[3]", SEED + 4)
+    talker_input_rows(R, S, torch, "configs[4]", SEED + 7)
     floors = floor_rows(R, S, torch)
     link_floors(list(ops4.values()) + R.rows, floors)
 

@@ -106,6 +106,8 @@ typedef enum shp_node_op {
                             lp2, rp2, lp3, rp3} (a ninth word, circular padding, must be 0) */
     SHP_NODE_PAD_REFLECT_1D, /* GGML_OP_PAD_REFLECT_1D: i32 {p0, p1} */
     SHP_NODE_REPEAT,     /* GGML_OP_REPEAT (ggml_repeat, ggml_repeat_4d): dst's shape */
+    SHP_NODE_ACC,        /* GGML_OP_ACC: i32 {nb1, nb2, nb3, offset, inplace} (bytes); src[0]
+                            a, src[1] b; dst a's shape (the same data when inplace) */
     SHP_NODE_OP_COUNT
 } shp_node_op;
 

@@ -439,6 +439,28 @@ shp_status_t shp_pad_reflect_1d(const shp_tensor * x, int32_t p0, int32_t p1, sh
  */
 shp_status_t shp_repeat(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
 
+/*
+ * ggml_acc(a, b, nb1, nb2, nb3, offset): y = a with b added into the view of
+ * y at byte `offset` with byte strides nb1..nb3 (b's extents, element stride
+ * 4): y[offset + 4*i0 + i1*nb1 + i2*nb2 + i3*nb3] = a[same] + b[i0, i1, i2, i3],
+ * every other element a's. The talker's prefill input: the codec stream, the
+ * x-vector's slot and the ICL acoustic block added into the text stream at a
+ * row offset (qwen3-tts/talker.cpp:31,90,109,112,115). a, y F32 contiguous,
+ * same shape; y == a (the same data) is ggml's inplace form and touches the
+ * window only, any other overlap of y with a or b is refused. b F32, rows
+ * contiguous (any row strides). The strides and offset are multiples of 4 and
+ * the view's rows do not overlap (each extent times its stride at most the
+ * next stride, unit dimensions aside); a view past a's end is refused.
+ */
+shp_status_t shp_acc(const shp_tensor * a,
+                     const shp_tensor * b,
+                     int64_t            nb1,
+                     int64_t            nb2,
+                     int64_t            nb3,
+                     int64_t            offset,
+                     shp_tensor *       y,
+                     shp_stream_t       stream);
+
 shp_status_t shp_im2col(const shp_tensor * kernel,
                         const shp_tensor * x,
                         int32_t            s0,

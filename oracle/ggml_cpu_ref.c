@@ -701,6 +701,46 @@ static void op_pad_family(const orc_node * n, int ith, int nth) {
     }
 }
 
+/* ggml_acc(a, b, nb1, nb2, nb3, offset) (qwen3-tts/talker.cpp:31,90,109,112,
+ * 115: the talker's prefill input, the codec stream, the x-vector's slot and
+ * the ICL acoustic block added into the text stream at a row offset): dst is a
+ * copy of a, then every row (i1, i2, i3) of b is added to dst at byte
+ * i1*nb1 + i2*nb2 + i3*nb3 + offset, reading a at the same byte: dst[v] =
+ * a[v] + b[row][i0], one f32 add per element. ggml-CPU copies on thread 0,
+ * waits, then splits b's rows over the threads; a window whose rows do not
+ * overlap (every use in the reference) gives the same values in any split, so
+ * thread 0 does it all here. A window past a's end is refused (ggml asserts). */
+static void op_acc(const orc_node * n, int ith, int nth) {
+    (void) nth;
+    if (ith != 0) {
+        return;
+    }
+    const int64_t * v   = (const int64_t *) n->src1;
+    const int64_t * bne = v;
+    const int64_t   nb1 = v[4], nb2 = v[5], nb3 = v[6], off = v[7];
+    const float *   b   = (const float *) (intptr_t) v[8];
+    const int64_t   nbytes = n->ne0 * n->nrows * (int64_t) sizeof(float);
+    if (bne[0] * bne[1] * bne[2] * bne[3] > 0 &&
+        off + (bne[0] - 1) * 4 + (bne[1] - 1) * nb1 + (bne[2] - 1) * nb2 + (bne[3] - 1) * nb3 >= nbytes) {
+        atomic_store(&g_node_error, -2);
+        return;
+    }
+    memcpy(n->dst, n->src0, (size_t) nbytes);
+    for (int64_t i3 = 0; i3 < bne[3]; ++i3) {
+        for (int64_t i2 = 0; i2 < bne[2]; ++i2) {
+            for (int64_t i1 = 0; i1 < bne[1]; ++i1) {
+                const int64_t at = i3 * nb3 + i2 * nb2 + i1 * nb1 + off;
+                float *       d  = (float *) ((char *) n->dst + at);
+                const float * s  = (const float *) ((const char *) n->src0 + at);
+                const float * br = b + ((i3 * bne[2] + i2) * bne[1] + i1) * bne[0];
+                for (int64_t i0 = 0; i0 < bne[0]; ++i0) {
+                    d[i0] = s[i0] + br[i0];
+                }
+            }
+        }
+    }
+}
+
 /* ggml_swiglu (single tensor): gate = first half of each row (second when
  * swapped), y = silu(gate) * other half. */
 static void op_glu_swiglu(const orc_node * n, int ith, int nth) {
@@ -828,6 +868,9 @@ static void run_node(const orc_node * n, int ith, int nth) {
         case ORC_OP_PAD_REFLECT_1D:
         case ORC_OP_REPEAT:
             op_pad_family(n, ith, nth);
+            break;
+        case ORC_OP_ACC:
+            op_acc(n, ith, nth);
             break;
         default:
             atomic_store(&g_node_error, -1);

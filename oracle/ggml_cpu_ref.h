@@ -57,6 +57,7 @@ enum orc_op {
     ORC_OP_PAD,          /* zero padding, left and right per dim    ggml_pad_ext        */
     ORC_OP_PAD_REFLECT_1D, /* reflect padding along dim 0           ggml_pad_reflect_1d */
     ORC_OP_REPEAT,       /* tile to a larger shape                  ggml_repeat         */
+    ORC_OP_ACC,          /* a copy of src0, src1 added into a view  ggml_acc            */
 };
 
 /*
@@ -97,6 +98,10 @@ enum orc_op {
  *               src0's ne[0..3], dst's ne[0..3], then the left pads lp[0..3]
  *               (PAD), {p0, p1, 0, 0} (PAD_REFLECT_1D) or zeros (REPEAT);
  *               dst contiguous F32.
+ *   ACC       : src0 = a, contiguous F32 of nrows*ne0 elements; src1 =
+ *               int64_t[9]: b's ne[0..3], the view's byte strides nb1, nb2,
+ *               nb3, its byte offset, then the b data pointer (contiguous F32);
+ *               dst contiguous F32 of a's size.
  */
 typedef struct orc_node {
     int32_t      op;

@@ -26,7 +26,7 @@ F32, F16, Q8_0, Q5_K, I32, BF16 = 0, 1, 8, 13, 26, 30
 (OP_ADD, OP_MUL, OP_DIV, OP_RMS_NORM, OP_ROPE_NEOX, OP_SILU, OP_SIN, OP_SQR, OP_EXP, OP_LEAKY_RELU, OP_SCALE_BIAS,
  OP_GET_ROWS, OP_CAST_F32, OP_GLU_SWIGLU, OP_SOFT_MAX, OP_CONT_F32, OP_BINBCAST, OP_SUB, OP_TANH, OP_SIGMOID,
  OP_ELU, OP_GELU_ERF, OP_CLAMP, OP_NORM, OP_IM2COL, OP_COL2IM_1D, OP_PAD, OP_PAD_REFLECT_1D,
- OP_REPEAT) = range(1, 30)
+ OP_REPEAT, OP_ACC) = range(1, 31)
 
 
 class OrcNode(ctypes.Structure):
@@ -336,6 +336,26 @@ class Graph:
         if any(d % s for d, s in zip(shape, xs)):
             raise ValueError("repeat: an extent not a multiple of the source's")
         return self._pad_family(OP_REPEAT, x.reshape(xs), tuple(shape), [0, 0, 0, 0])
+
+    def acc(self, a, b, nb1, nb2, nb3, offset):
+        """ggml_acc(a, b, nb1, nb2, nb3, offset): a copy of a with b added into
+        the view of it at byte `offset` with byte strides nb1..nb3 (b's shape,
+        b's element stride 4). a and b in this module's layout; b may be the
+        output of an earlier node (a contiguous slice of one)."""
+        a = self._f32(a)
+        b = self._f32(b)
+        bne = list(b.shape[::-1]) + [1] * (4 - b.ndim)
+        if b.size and offset + (bne[0] - 1) * 4 + (bne[1] - 1) * nb1 + (bne[2] - 1) * nb2 + \
+                (bne[3] - 1) * nb3 >= a.nbytes:
+            raise ValueError("acc: the view runs past a's end")
+        view = np.array(bne + [nb1, nb2, nb3, offset, b.ctypes.data], dtype=np.int64)
+        dst = np.empty_like(a)
+        n = OrcNode()
+        n.op, n.type0, n.ne0, n.nrows = OP_ACC, F32, a.shape[-1], _rows(a)
+        n.src0, n.src1, n.dst = _ptr(a), _ptr(view), _ptr(dst)
+        self.nodes.append(n)
+        self.keep += [dst, a, b, view]
+        return dst
 
     def glu_swiglu(self, a, swapped=False):
         a = self._f32(a)

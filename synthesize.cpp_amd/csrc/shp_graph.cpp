@@ -155,6 +155,10 @@ bool node_form_ok(const shp_node & n) {
         case SHP_NODE_PAD_REFLECT_1D:
         case SHP_NODE_REPEAT:
             return f32_of(n.src[0]) && f32_of(n.dst);
+        case SHP_NODE_ACC:
+            // {nb1, nb2, nb3, offset, inplace}: ggml's view of the result
+            return f32_of(n.src[0]) && f32_of(n.src[1]) && f32_of(n.dst) && same_shape(n.src[0], n.dst) &&
+                   n.op_params[0] >= 0 && n.op_params[1] >= 0 && n.op_params[2] >= 0 && n.op_params[3] >= 0;
         case SHP_NODE_IM2COL:
             // the 1-D form: is_2D 0 and no padding along the absent second
             // dimension (ggml's 1-D rows read there at -p1: zeros)
@@ -1476,6 +1480,8 @@ shp_status_t launch_single(const shp_node & n, shp_stream_t st) {
             return shp_pad_reflect_1d(&n.src[0], n.op_params[0], n.op_params[1], y, st);
         case SHP_NODE_REPEAT:
             return shp_repeat(&n.src[0], y, st);
+        case SHP_NODE_ACC:
+            return shp_acc(&n.src[0], &n.src[1], n.op_params[0], n.op_params[1], n.op_params[2], n.op_params[3], y, st);
         default:
             return SHP_ERR_UNSUPPORTED;
     }

@@ -63,7 +63,7 @@ def load(path=None):
         raise RuntimeError("libsynth_hip.so is not built (%s); run __graft_entry__.build() or make -C "
                            "synthesize.cpp_amd" % path)
     L = ctypes.CDLL(path)
-    vp, f, i32 = ctypes.c_void_p, ctypes.c_float, ctypes.c_int32
+    vp, f, i32, i64 = ctypes.c_void_p, ctypes.c_float, ctypes.c_int32, ctypes.c_int64
     sigs = {
         "shp_get_rows": [_PT, _PT, _PT, vp],
         "shp_get_rows_sum": [_PT, i32, _PT, _PT, vp],
@@ -97,6 +97,7 @@ def load(path=None):
         "shp_pad": [_PT, ctypes.POINTER(ctypes.c_int32), _PT, vp],
         "shp_pad_reflect_1d": [_PT, i32, i32, _PT, vp],
         "shp_repeat": [_PT, _PT, vp],
+        "shp_acc": [_PT, _PT, i64, i64, i64, i64, _PT, vp],
         "shp_sub": [_PT, _PT, _PT, vp],
         "shp_tanh": [_PT, _PT, vp],
         "shp_sigmoid": [_PT, _PT, vp],
@@ -622,6 +623,20 @@ def repeat(x, shape, out=None):
     return out
 
 
+def acc(a, b, nb1, nb2, nb3, offset, out=None, inplace=False):
+    """ggml_acc(a, b, nb1, nb2, nb3, offset): a with b added into the view at
+    byte `offset` with byte strides nb1..nb3 (b's extents). inplace: into a
+    itself (ggml's inplace form)."""
+    import torch
+    if inplace:
+        out = a
+    elif out is None:
+        out = torch.empty(a.shape, dtype=torch.float32, device=a.device)
+    _check(load().shp_acc(_ref(desc(a)), _ref(desc(b)), int(nb1), int(nb2), int(nb3), int(offset), _ref(desc(out)),
+                          _stream()), "acc")
+    return out
+
+
 def cpy(x, out=None):
     """ggml_cpy / ggml_cast into F32 of x's shape (x F32, F16 or BF16)."""
     import torch
@@ -637,7 +652,7 @@ def cpy(x, out=None):
 (NODE_NOP, NODE_ADD, NODE_MUL, NODE_DIV, NODE_SQR, NODE_SIN, NODE_SCALE, NODE_CPY, NODE_GET_ROWS, NODE_RMS_NORM,
  NODE_SOFT_MAX, NODE_ROPE, NODE_LEAKY_RELU, NODE_SILU, NODE_EXP, NODE_GLU_SWIGLU, NODE_CONCAT, NODE_SUB, NODE_TANH,
  NODE_SIGMOID, NODE_ELU, NODE_GELU_ERF, NODE_CLAMP, NODE_NORM, NODE_IM2COL, NODE_COL2IM_1D, NODE_PAD,
- NODE_PAD_REFLECT_1D, NODE_REPEAT) = range(29)
+ NODE_PAD_REFLECT_1D, NODE_REPEAT, NODE_ACC) = range(30)
 NODE_FLAG_OUTPUT = 1
 RUN_KINDS = {-1: "unsupported", 0: "nop", 1: "single", 2: "norm_mul", 3: "norm_mul_rope", 4: "add_norm_mul",
              5: "silu_mul", 6: "add_leaky", 7: "add_scale_leaky", 8: "snake", 9: "snake_guarded", 10: "snake_beta",
@@ -839,6 +854,13 @@ class Graph:
 
     def repeat(self, x, shape):
         return self._op(NODE_REPEAT, self._like(x, tuple(shape)), [x])
+
+    def acc(self, a, b, nb1, nb2, nb3, offset, inplace=False):
+        """ggml_acc (byte strides and offset of the view of a's copy; inplace:
+        the result is a's own memory)."""
+        t = self._t(a)
+        dst = t if inplace else self._like(a)
+        return self._op(NODE_ACC, dst, [a, b], ints={0: nb1, 1: nb2, 2: nb3, 3: offset, 4: 1 if inplace else 0})
 
     def glu_swiglu(self, a, b=None, swapped=False):
         t = self._t(a)

@@ -659,3 +659,36 @@ def test_codec_activation_nodes():
         assert kinds(g.plan(build(g))) == ["single"]
     g = S.Graph()
     assert kinds(g.plan(g.norm(x, -1.0))) == ["unsupported"]
+
+
+def test_acc_node_forms():
+    """supports_op for ACC is the entry point's own answer: a row window at a
+    row offset and ggml's inplace form are taken; overlapping rows, a view
+    past a's end and an offset inside an element are not."""
+    a, b = z(10, 8), z(4, 8)
+    for params, ok in (((32, 128, 128, 3 * 32), 1), ((16, 128, 128, 0), 0), ((32, 128, 128, 7 * 32), 0),
+                       ((32, 128, 128, 2), 0)):
+        g = S.Graph()
+        y = g.acc(a, b, *params)
+        arr, n, keep = g.nodes(y)
+        assert S.load().shp_graph_node_supported(ctypes.byref(arr[0])) == ok, params
+    g = S.Graph()
+    y = g.acc(a, b, 32, 128, 128, 32, inplace=True)
+    assert kinds(g.plan(y)) == ["single"]
+    assert y.t.data_ptr() == a.data_ptr()
+
+
+def test_talker_prefill_accumulation_plans_as_singles():
+    """talker.cpp:86-118 with the x-vector in the middle of the codec run:
+    get_rows, then three ggml_acc over views of its result, then the ICL
+    block's: one launch each."""
+    H, n, N = 64, 5, 8
+    text, table, ids, sp, ac = z(N, H), z(30, H), z(n, dtype=torch.int32), z(H), z(3, H)
+    g = S.Graph()
+    codec = g.get_rows(table, ids)
+    nb1, nb2 = 4 * H, 4 * H * N
+    out = g.acc(text, g.view(codec, codec.t[:2]), nb1, nb2, nb2, 3 * nb1)
+    out = g.acc(out, g.view(sp, sp.view(1, H)), nb1, nb2, nb2, 5 * nb1)
+    out = g.acc(out, g.view(codec, codec.t[3:]), nb1, nb2, nb2, 6 * nb1)
+    out = g.acc(out, ac, nb1, nb2, nb2, 5 * nb1)
+    assert [k for k in kinds(g.plan(out)) if k != "nop"] == ["single"] * 5

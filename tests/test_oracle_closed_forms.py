@@ -719,3 +719,118 @@ def test_repeat_doubles_frames():
     x = np.random.default_rng(4).standard_normal((6, 1, 5)).astype(np.float32)   # ggml [5, 1, 6]
     got = R.run(lambda g: g.repeat(x, (6, 2, 5))).reshape(12, 5)
     assert np.array_equal(got, np.repeat(x[:, 0], 2, axis=0))
+
+
+# ---------------------------------------------------------------------------
+# ggml_acc (the talker's prefill input)
+# ---------------------------------------------------------------------------
+
+def _acc_numpy(a, b, nb1, nb2, nb3, offset):
+    """numpy's own strided view of a's copy (ggml's view: byte strides 4, nb1,
+    nb2, nb3 from byte `offset`), b added through it."""
+    out = a.copy()
+    flat = out.reshape(-1)[offset // 4:]
+    strides = (nb3, nb2, nb1, 4)[4 - b.ndim:]
+    view = np.lib.stride_tricks.as_strided(flat, shape=b.shape, strides=strides)
+    view += b
+    return out
+
+
+def _acc_span(b, nb, offset):
+    """The byte just past the view's last element."""
+    bne = list(b.shape[::-1]) + [1] * (4 - b.ndim)
+    return offset + 4 * bne[0] + sum((bne[d] - 1) * nb[d - 1] for d in (1, 2, 3))
+
+
+@pytest.mark.parametrize("ashape,bshape,nb,offset", [
+    ((10, 8), (4, 8), (32, 128, 128), 3 * 32),          # whole rows at a row offset (the codec tail)
+    ((10, 8), (1, 8), (32, 32, 32), 9 * 32),            # one row, the last (the x-vector's slot)
+    ((10, 8), (3, 5), (32, 96, 96), 1 * 32 + 2 * 4),    # a narrower window at a column offset
+    ((6, 5, 12), (2, 3, 4), (48, 240, 480), 4 + 48),    # a 3-D window
+    ((40,), (6,), (24, 24, 24), 7 * 4),                 # one row anywhere in a vector
+    ((9, 7), (3, 2), (56, 112, 112), 4),                # rows two apart
+])
+def test_acc_is_numpy_strided_view_add(ashape, bshape, nb, offset):
+    """ggml_acc: a's copy with b added through the byte-strided view; an
+    offset one element off misses."""
+    rng = np.random.default_rng(sum(ashape) + offset)
+    a = rng.standard_normal(ashape).astype(np.float32)
+    b = rng.standard_normal(bshape).astype(np.float32)
+    got = R.run(lambda g: g.acc(a, b, *nb, offset))
+    assert np.array_equal(got, _acc_numpy(a, b, *nb, offset))
+    shifted = offset + 4 if _acc_span(b, nb, offset + 4) <= a.nbytes else offset - 4
+    assert not np.array_equal(R.run(lambda g: g.acc(a, b, *nb, shifted)), got)
+    with pytest.raises(ValueError):   # past a's end
+        R.Graph().acc(a, b, *nb, a.nbytes)
+
+
+def prefill_input(g, text, codec, codec_offset, speaker=None, speaker_index=-1, acoustic=None, acoustic_offset=-1,
+                  tail_slip=0):
+    """The accumulation nodes of build_talker_prefill_input
+    (qwen3-tts/talker.cpp:86-118, accumulate_acoustic :23-32) on an oracle
+    graph: text (N, H) and codec (n, H) are the projected text stream and the
+    codec embeddings (the get_rows output), speaker (H,) the x-vector.
+    tail_slip moves the tail's offset (a planted off-by-one)."""
+    N, H = text.shape
+    nb1, nb2 = 4 * H, 4 * H * N
+    if speaker is None:
+        out = g.acc(text, codec, nb1, nb2, nb2, codec_offset * nb1)
+    else:
+        out = text
+        if speaker_index > 0:
+            out = g.acc(out, codec[:speaker_index], nb1, nb2, nb2, codec_offset * nb1)
+        out = g.acc(out, speaker.reshape(1, H), nb1, nb2, nb2, (codec_offset + speaker_index) * nb1)
+        if codec.shape[0] - speaker_index - 1 > 0:
+            out = g.acc(out, codec[speaker_index + 1:], nb1, nb2, nb2,
+                        (codec_offset + speaker_index + 1 + tail_slip) * nb1)
+    if acoustic is not None:
+        out = g.acc(out, acoustic, nb1, nb2, nb2, acoustic_offset * nb1)
+    return out
+
+
+@pytest.mark.parametrize("codec_offset", [0, 3])
+def test_acc_prefill_speaker_slot_rule(codec_offset):
+    """tests/qwen3_tts_prompt_slot_test.cpp:356-420 (offset 0) and :527-600
+    (a codec run after a text-only prefix): with the x-vector at every slot of
+    the codec run, each position is text + (the x-vector at the slot, else its
+    codec row), the positions before the run bare text, exactly as the plain
+    accumulation; a tail accumulated one row early misses the rule."""
+    rng = np.random.default_rng(11 + codec_offset)
+    n, H = 5, 16
+    N = codec_offset + n
+    text = rng.standard_normal((N, H)).astype(np.float32)
+    codec = rng.standard_normal((n, H)).astype(np.float32)
+    speaker = rng.standard_normal(H).astype(np.float32)
+    plain = R.run(lambda g: prefill_input(g, text, codec, codec_offset))
+    for si in range(n):
+        got = R.run(lambda g: prefill_input(g, text, codec, codec_offset, speaker, si))
+        exp = text.copy()
+        for j in range(n):
+            exp[codec_offset + j] = text[codec_offset + j] + (speaker if j == si else codec[j])
+        assert np.array_equal(got, exp)
+        keep = np.ones(N, bool)
+        keep[codec_offset + si] = False
+        assert np.array_equal(got[keep], plain[keep])
+        if si < n - 2:
+            slipped = R.run(lambda g: prefill_input(g, text, codec, codec_offset, speaker, si, tail_slip=-1))
+            assert not np.array_equal(slipped, exp)
+
+
+def test_acc_prefill_acoustic_block_after_the_codec_sum():
+    """accumulate_acoustic (talker.cpp:23-32): the ICL block's summed groups
+    are added to the already accumulated streams: (text + codec) + acoustic in
+    f32, which the other association misses for some position."""
+    rng = np.random.default_rng(12)
+    N, n, H, m = 9, 6, 64, 4
+    text = rng.standard_normal((N, H)).astype(np.float32)
+    codec = rng.standard_normal((n, H)).astype(np.float32)
+    acoustic = rng.standard_normal((m, H)).astype(np.float32) * 3
+    got = R.run(lambda g: prefill_input(g, text, codec, N - n, acoustic=acoustic, acoustic_offset=N - m))
+    exp = text.copy()
+    exp[N - n:] = exp[N - n:] + codec
+    exp[N - m:] = exp[N - m:] + acoustic
+    assert np.array_equal(got, exp)
+    other = text.copy()
+    other[N - m:] = text[N - m:] + (codec[n - m:] + acoustic)
+    other[N - n:N - m] = text[N - n:N - m] + codec[:n - m]
+    assert not np.array_equal(got, other)
