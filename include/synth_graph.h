@@ -47,6 +47,9 @@
  *   CPY [views] IM2COL               the causal convolution's time-major copy
  *        and its column matrix (src/arch/qwen3-tts/codec.cpp:94-96): im2col
  *        reads the channel-major activation through the transposed view
+ *   MUL SUM_ROWS                     the attention-weighted sums of the speaker
+ *        encoder's statistics pooling (src/arch/qwen3-tts/speaker-encoder.cpp:
+ *        292-293,374): the product is summed as it is formed
  * Any other supported node runs alone through its entry point in
  * synth_hip.h. View-like nodes (NONE, VIEW, RESHAPE, PERMUTE, TRANSPOSE)
  * are SHP_NODE_NOP: no work.
@@ -108,6 +111,12 @@ typedef enum shp_node_op {
     SHP_NODE_REPEAT,     /* GGML_OP_REPEAT (ggml_repeat, ggml_repeat_4d): dst's shape */
     SHP_NODE_ACC,        /* GGML_OP_ACC: i32 {nb1, nb2, nb3, offset, inplace} (bytes); src[0]
                             a, src[1] b; dst a's shape (the same data when inplace) */
+    SHP_NODE_RELU,       /* GGML_OP_UNARY, GGML_UNARY_OP_RELU */
+    SHP_NODE_NEG,        /* GGML_OP_UNARY, GGML_UNARY_OP_NEG */
+    SHP_NODE_STEP,       /* GGML_OP_UNARY, GGML_UNARY_OP_STEP */
+    SHP_NODE_SQRT,       /* GGML_OP_SQRT */
+    SHP_NODE_SUM_ROWS,   /* GGML_OP_SUM_ROWS: dst [1, ne1, ne2, ne3] */
+    SHP_NODE_MEAN,       /* GGML_OP_MEAN: dst [1, ne1, ne2, ne3] */
     SHP_NODE_OP_COUNT
 } shp_node_op;
 
@@ -149,9 +158,11 @@ typedef enum shp_run_kind {
                                  shp_cont_add_leaky_relu */
     SHP_RUN_VIEW_BINARY,      /* CPY of a row-contiguous F32 view, then ADD, MUL or
                                  DIV of the copy: the binary op reads the view */
-    SHP_RUN_CONT_IM2COL       /* CPY of a transposed channel-major F32 activation,
+    SHP_RUN_CONT_IM2COL,      /* CPY of a transposed channel-major F32 activation,
                                  [views], IM2COL of the copy: shp_im2col reads the
                                  activation in place of the copy */
+    SHP_RUN_MUL_SUM_ROWS      /* MUL whose product only SUM_ROWS reads, then that
+                                 SUM_ROWS: shp_mul_sum_rows */
 } shp_run_kind;
 
 typedef struct shp_graph_run {

@@ -358,6 +358,34 @@ shp_status_t shp_clamp(const shp_tensor * x, float lo, float hi, shp_tensor * y,
 shp_status_t shp_norm(const shp_tensor * x, float eps, shp_tensor * y, shp_stream_t stream);
 
 /*
+ * The speaker encoder's and the VITS text encoder / duration predictor's
+ * remaining element and row ops, as ggml-CPU's vec forms compute them:
+ *   shp_relu   ggml_relu, x > 0 ? x : 0 (-0 and NaN give +0; vits/text-encoder.cpp:71,
+ *              qwen3-tts/speaker-encoder.cpp:184)
+ *   shp_neg    ggml_neg, -x (vits/duration-predictor.cpp:113,117,205)
+ *   shp_step   ggml_step, x > 0 ? 1 : 0 (vits/duration-predictor.cpp:89-90)
+ *   shp_sqrt   ggml_sqrt, correctly rounded (qwen3-tts/speaker-encoder.cpp:294)
+ *   shp_sum_rows  ggml_sum_rows: y [1, ne1, ne2, ne3] = each row's sum,
+ *              accumulated in double and rounded to f32 once
+ *              (qwen3-tts/speaker-encoder.cpp:293,374, vits/duration-predictor.cpp:47,93)
+ *   shp_mean   ggml_mean: that sum divided by ne0 in f32 (speaker-encoder.cpp:195,350)
+ *   shp_mul_sum_rows  ggml_mul(x, w) then ggml_sum_rows as one launch: each
+ *              row's f32 products summed as shp_sum_rows sums (the attention-
+ *              weighted statistics, speaker-encoder.cpp:293,374); w x's shape
+ * All F32, rows contiguous, any row strides; the element ops' y has x's shape;
+ * the row sums' y may not overlap x or w. The row sums agree with ggml-CPU's
+ * element-order double sum unless the two double sums fall on opposite sides
+ * of an f32 rounding boundary.
+ */
+shp_status_t shp_relu(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
+shp_status_t shp_neg(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
+shp_status_t shp_step(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
+shp_status_t shp_sqrt(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
+shp_status_t shp_sum_rows(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
+shp_status_t shp_mean(const shp_tensor * x, shp_tensor * y, shp_stream_t stream);
+shp_status_t shp_mul_sum_rows(const shp_tensor * x, const shp_tensor * w, shp_tensor * y, shp_stream_t stream);
+
+/*
  * ggml_concat(a, b, dim): y of a's shape except y->ne[dim] = a->ne[dim] +
  * b->ne[dim]; y(i) = a(i) where i[dim] < a->ne[dim], else b(i) with
  * i[dim] - a->ne[dim]. All F32, rows contiguous (any row strides). The code

@@ -467,6 +467,30 @@ static void op_unary(const orc_node * n, int ith, int nth) {
                 }
                 break;
             }
+            /* ggml-CPU's vec forms ggml_vec_relu_f32, _neg_f32, _step_f32 and
+             * _sqrt_f32 (vits/text-encoder.cpp:71, qwen3-tts/speaker-
+             * encoder.cpp:184,294, vits/duration-predictor.cpp:89-117): a NaN
+             * or -0 gives +0 from relu and 0 from step. */
+            case ORC_OP_RELU:
+                for (int64_t i = 0; i < ne0; ++i) {
+                    y[i] = x[i] > 0.0f ? x[i] : 0.0f;
+                }
+                break;
+            case ORC_OP_NEG:
+                for (int64_t i = 0; i < ne0; ++i) {
+                    y[i] = -x[i];
+                }
+                break;
+            case ORC_OP_STEP:
+                for (int64_t i = 0; i < ne0; ++i) {
+                    y[i] = x[i] > 0.0f ? 1.0f : 0.0f;
+                }
+                break;
+            case ORC_OP_SQRT:
+                for (int64_t i = 0; i < ne0; ++i) {
+                    y[i] = sqrtf(x[i]);
+                }
+                break;
             case ORC_OP_CLAMP: {
                 const float lo = n->f[0], hi = n->f[1];
                 for (int64_t i = 0; i < ne0; ++i) {
@@ -701,6 +725,28 @@ static void op_pad_family(const orc_node * n, int ith, int nth) {
     }
 }
 
+/* ggml_sum_rows and ggml_mean (qwen3-tts/speaker-encoder.cpp:195,292-293,
+ * 350,374, the speaker encoder's statistics pooling; vits/duration-
+ * predictor.cpp:47,93): ggml_vec_sum_f32 accumulates a row's f32 values into
+ * a double in element order and rounds the sum to f32 once; the mean then
+ * divides that f32 by ne0 converted to f32. */
+static void op_sum_rows(const orc_node * n, int ith, int nth) {
+    int64_t r0, r1;
+    chunk(n->nrows, ith, nth, &r0, &r1);
+    for (int64_t r = r0; r < r1; ++r) {
+        const float * x   = (const float *) n->src0 + r * n->ne0;
+        double        sum = 0.0;
+        for (int64_t i = 0; i < n->ne0; ++i) {
+            sum += (double) x[i];
+        }
+        float v = (float) sum;
+        if (n->op == ORC_OP_MEAN) {
+            v /= (float) n->ne0;
+        }
+        ((float *) n->dst)[r] = v;
+    }
+}
+
 /* ggml_acc(a, b, nb1, nb2, nb3, offset) (qwen3-tts/talker.cpp:31,90,109,112,
  * 115: the talker's prefill input, the codec stream, the x-vector's slot and
  * the ICL acoustic block added into the text stream at a row offset): dst is a
@@ -871,6 +917,16 @@ static void run_node(const orc_node * n, int ith, int nth) {
             break;
         case ORC_OP_ACC:
             op_acc(n, ith, nth);
+            break;
+        case ORC_OP_RELU:
+        case ORC_OP_NEG:
+        case ORC_OP_STEP:
+        case ORC_OP_SQRT:
+            op_unary(n, ith, nth);
+            break;
+        case ORC_OP_SUM_ROWS:
+        case ORC_OP_MEAN:
+            op_sum_rows(n, ith, nth);
             break;
         default:
             atomic_store(&g_node_error, -1);

@@ -58,6 +58,12 @@ enum orc_op {
     ORC_OP_PAD_REFLECT_1D, /* reflect padding along dim 0           ggml_pad_reflect_1d */
     ORC_OP_REPEAT,       /* tile to a larger shape                  ggml_repeat         */
     ORC_OP_ACC,          /* a copy of src0, src1 added into a view  ggml_acc            */
+    ORC_OP_RELU,         /* x > 0 ? x : 0                           ggml_relu           */
+    ORC_OP_NEG,          /* -x                                      ggml_neg            */
+    ORC_OP_STEP,         /* x > 0 ? 1 : 0                           ggml_step           */
+    ORC_OP_SQRT,         /* sqrtf(x)                                ggml_sqrt           */
+    ORC_OP_SUM_ROWS,     /* dst[r] = (float) double sum of row r    ggml_sum_rows       */
+    ORC_OP_MEAN,         /* dst[r] = sum_rows / (float) ne0         ggml_mean           */
 };
 
 /*
@@ -98,6 +104,7 @@ enum orc_op {
  *               src0's ne[0..3], dst's ne[0..3], then the left pads lp[0..3]
  *               (PAD), {p0, p1, 0, 0} (PAD_REFLECT_1D) or zeros (REPEAT);
  *               dst contiguous F32.
+ *   SUM_ROWS, MEAN : src0 nrows rows of ne0; dst one value per row.
  *   ACC       : src0 = a, contiguous F32 of nrows*ne0 elements; src1 =
  *               int64_t[9]: b's ne[0..3], the view's byte strides nb1, nb2,
  *               nb3, its byte offset, then the b data pointer (contiguous F32);

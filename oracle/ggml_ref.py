@@ -26,7 +26,7 @@ F32, F16, Q8_0, Q5_K, I32, BF16 = 0, 1, 8, 13, 26, 30
 (OP_ADD, OP_MUL, OP_DIV, OP_RMS_NORM, OP_ROPE_NEOX, OP_SILU, OP_SIN, OP_SQR, OP_EXP, OP_LEAKY_RELU, OP_SCALE_BIAS,
  OP_GET_ROWS, OP_CAST_F32, OP_GLU_SWIGLU, OP_SOFT_MAX, OP_CONT_F32, OP_BINBCAST, OP_SUB, OP_TANH, OP_SIGMOID,
  OP_ELU, OP_GELU_ERF, OP_CLAMP, OP_NORM, OP_IM2COL, OP_COL2IM_1D, OP_PAD, OP_PAD_REFLECT_1D,
- OP_REPEAT, OP_ACC) = range(1, 31)
+ OP_REPEAT, OP_ACC, OP_RELU, OP_NEG, OP_STEP, OP_SQRT, OP_SUM_ROWS, OP_MEAN) = range(1, 37)
 
 
 class OrcNode(ctypes.Structure):
@@ -164,6 +164,28 @@ class Graph:
 
     def gelu_erf(self, x):
         return self._unary(OP_GELU_ERF, x)
+
+    def relu(self, x):
+        return self._unary(OP_RELU, x)
+
+    def neg(self, x):
+        return self._unary(OP_NEG, x)
+
+    def step(self, x):
+        return self._unary(OP_STEP, x)
+
+    def sqrt(self, x):
+        return self._unary(OP_SQRT, x)
+
+    def sum_rows(self, x):
+        """ggml_sum_rows: (..., ne0) -> (..., 1)."""
+        x = self._f32(x)
+        return self._node(OP_SUM_ROWS, np.empty(x.shape[:-1] + (1,), np.float32), x, ne0=x.shape[-1], nrows=_rows(x))
+
+    def mean(self, x):
+        """ggml_mean: (..., ne0) -> (..., 1)."""
+        x = self._f32(x)
+        return self._node(OP_MEAN, np.empty(x.shape[:-1] + (1,), np.float32), x, ne0=x.shape[-1], nrows=_rows(x))
 
     def clamp(self, x, lo, hi):
         return self._unary(OP_CLAMP, x, f=(lo, hi))

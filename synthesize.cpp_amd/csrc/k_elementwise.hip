@@ -43,7 +43,11 @@ enum EwOp {
     kSigmoid   = 15,
     kElu       = 16,
     kGeluErf   = 17,
-    kClamp     = 18
+    kClamp     = 18,
+    kRelu      = 19,
+    kNeg       = 20,
+    kStep      = 21,
+    kSqrt      = 22
 };
 
 // Snake family: y = x + sin(x*al)^2 / den with per-channel al and den.
@@ -150,6 +154,17 @@ template <int OP> __device__ __forceinline__ float ew(float a, float b, const Ew
         // ggml's MAX(MIN(x, max), min): a NaN gives max
         const float m = a < g.bias ? a : g.bias;
         return m > g.scale ? m : g.scale;
+    } else if constexpr (OP == kRelu) {
+        // ggml's x > 0 ? x : 0 (vits/text-encoder.cpp:71, qwen3-tts/speaker-
+        // encoder.cpp:184): -0 and NaN give +0
+        return a > 0.0f ? a : 0.0f;
+    } else if constexpr (OP == kNeg) {
+        return -a;
+    } else if constexpr (OP == kStep) {
+        return a > 0.0f ? 1.0f : 0.0f;
+    } else if constexpr (OP == kSqrt) {
+        // correctly rounded, as sqrtf (qwen3-tts/speaker-encoder.cpp:294)
+        return __builtin_sqrtf(a);
     } else {
         static_assert(OP == kCopy, "unknown elementwise op");
         return a;
@@ -1482,6 +1497,22 @@ extern "C" shp_status_t shp_elu(const shp_tensor * x, shp_tensor * y, shp_stream
 
 extern "C" shp_status_t shp_gelu_erf(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
     return unary_entry<kGeluErf>(x, y, stream);
+}
+
+extern "C" shp_status_t shp_relu(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
+    return unary_entry<kRelu>(x, y, stream);
+}
+
+extern "C" shp_status_t shp_neg(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
+    return unary_entry<kNeg>(x, y, stream);
+}
+
+extern "C" shp_status_t shp_step(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
+    return unary_entry<kStep>(x, y, stream);
+}
+
+extern "C" shp_status_t shp_sqrt(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
+    return unary_entry<kSqrt>(x, y, stream);
 }
 
 extern "C" shp_status_t shp_clamp(const shp_tensor * x, float lo, float hi, shp_tensor * y, shp_stream_t stream) {

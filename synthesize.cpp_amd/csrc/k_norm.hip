@@ -282,6 +282,108 @@ __global__ __launch_bounds__(256) void k_layer_norm(const NormArgs a) {
     }
 }
 
+// ggml_sum_rows / ggml_mean, and the product-sum of ggml_mul then
+// ggml_sum_rows (the speaker encoder's attention-weighted statistics,
+// qwen3-tts/speaker-encoder.cpp:292-293,374): one wave per row, each lane
+// accumulating its f32 values (or f32 products) into a double in element
+// order, the lanes' doubles summed by DPP moves and rounded to f32 once; the
+// mean divides that f32 by ne0 in f32. ggml-CPU accumulates the row in double
+// in element order: the f32 results agree unless the two double sums fall on
+// opposite sides of an f32 rounding boundary.
+enum SumRowsMode { kSumRows = 0, kMeanRows = 1, kMulSumRows = 2 };
+
+struct SumRowsArgs {
+    const float * x;
+    RowMap        xm;
+    const float * w;
+    RowMap        wm;
+    float *       y;
+    RowMap        ym;
+    int64_t       nrows;
+    int32_t       ne0;
+    int32_t       pad;
+};
+
+template <int MODE, bool VEC> __global__ __launch_bounds__(256) void k_sum_rows(const SumRowsArgs a) {
+    const int     lane = threadIdx.x % kWave;
+    const int64_t row  = static_cast<int64_t>(blockIdx.x) * (256 / kWave) + threadIdx.x / kWave;
+    if (row >= a.nrows) {
+        return;
+    }
+    const float * xr  = reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.x) + row_offset(a.xm, row));
+    const float * wr  = MODE == kMulSumRows ?
+                            reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.w) + row_offset(a.wm, row)) :
+                            nullptr;
+    double        acc = 0.0;
+    if constexpr (VEC) {
+        const int nvec = a.ne0 / 4;
+        for (int i = lane; i < nvec; i += kWave) {
+            f32x4 v = ld_stream(reinterpret_cast<const f32x4 *>(xr) + i);
+            if constexpr (MODE == kMulSumRows) {
+                const f32x4 u = ld_stream(reinterpret_cast<const f32x4 *>(wr) + i);
+                v             = f32x4{ v.x * u.x, v.y * u.y, v.z * u.z, v.w * u.w };
+            }
+            acc += static_cast<double>(v.x);
+            acc += static_cast<double>(v.y);
+            acc += static_cast<double>(v.z);
+            acc += static_cast<double>(v.w);
+        }
+    } else {
+        for (int i = lane; i < a.ne0; i += kWave) {
+            const float v = MODE == kMulSumRows ? xr[i] * wr[i] : xr[i];
+            acc += static_cast<double>(v);
+        }
+    }
+    acc = group_sum<kWave>(acc);
+    if (lane == 0) {
+        float v = static_cast<float>(acc);
+        if constexpr (MODE == kMeanRows) {
+            v = v / static_cast<float>(a.ne0);
+        }
+        *reinterpret_cast<float *>(reinterpret_cast<char *>(a.y) + row_offset(a.ym, row)) = v;
+    }
+}
+
+template <int MODE> shp_status_t sum_rows_entry(const shp_tensor * x, const shp_tensor * w, shp_tensor * y,
+                                                 hipStream_t stream) {
+    if (!well_formed(x) || !well_formed(y) || (MODE == kMulSumRows && !well_formed(w))) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    if (x->type != SHP_TYPE_F32 || y->type != SHP_TYPE_F32 || (MODE == kMulSumRows && w->type != SHP_TYPE_F32)) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    if (y->ne[0] != 1 || y->ne[1] != x->ne[1] || y->ne[2] != x->ne[2] || y->ne[3] != x->ne[3] ||
+        x->ne[0] > INT32_MAX || (MODE == kMulSumRows && !same_shape(*x, *w))) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    if (spans_overlap(*x, *y) || (MODE == kMulSumRows && spans_overlap(*w, *y))) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    if (dry_run()) {
+        return SHP_OK;
+    }
+    SumRowsArgs a{};
+    a.x     = static_cast<const float *>(x->data);
+    a.xm    = make_rowmap(*x);
+    a.y     = static_cast<float *>(y->data);
+    a.ym    = make_rowmap(*y);
+    a.nrows = nrows(*x);
+    a.ne0   = static_cast<int32_t>(x->ne[0]);
+    bool vec = x->ne[0] % 4 == 0 && rows_aligned(*x, 16);
+    if constexpr (MODE == kMulSumRows) {
+        a.w  = static_cast<const float *>(w->data);
+        a.wm = make_rowmap(*w);
+        vec  = vec && rows_aligned(*w, 16);
+    }
+    const dim3 grid(static_cast<unsigned>((a.nrows + 3) / 4)), block(256);
+    if (vec) {
+        hipLaunchKernelGGL((k_sum_rows<MODE, true>), grid, block, 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((k_sum_rows<MODE, false>), grid, block, 0, stream, a);
+    }
+    return launch_status();
+}
+
 template <int WT, int MODE> shp_status_t launch_norm(const NormArgs & a, bool vec, hipStream_t stream) {
     if (dry_run()) {
         return SHP_OK;
@@ -1152,6 +1254,19 @@ extern "C" shp_status_t shp_norm(const shp_tensor * x, float eps, shp_tensor * y
     const int64_t blocks = (a.nrows + 3) / 4;
     hipLaunchKernelGGL(k_layer_norm, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream), a);
     return launch_status();
+}
+
+extern "C" shp_status_t shp_sum_rows(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
+    return shp::sum_rows_entry<shp::kSumRows>(x, nullptr, y, shp::as_stream(stream));
+}
+
+extern "C" shp_status_t shp_mean(const shp_tensor * x, shp_tensor * y, shp_stream_t stream) {
+    return shp::sum_rows_entry<shp::kMeanRows>(x, nullptr, y, shp::as_stream(stream));
+}
+
+extern "C" shp_status_t shp_mul_sum_rows(const shp_tensor * x, const shp_tensor * w, shp_tensor * y,
+                                         shp_stream_t stream) {
+    return shp::sum_rows_entry<shp::kMulSumRows>(x, w, y, shp::as_stream(stream));
 }
 
 extern "C" shp_status_t shp_rms_norm_mul(const shp_tensor * x,

@@ -108,7 +108,15 @@ bool node_form_ok(const shp_node & n) {
         case SHP_NODE_ELU:
         case SHP_NODE_GELU_ERF:
         case SHP_NODE_CLAMP:
+        case SHP_NODE_RELU:
+        case SHP_NODE_NEG:
+        case SHP_NODE_STEP:
+        case SHP_NODE_SQRT:
             return unary_ok(n);
+        case SHP_NODE_SUM_ROWS:
+        case SHP_NODE_MEAN:
+            return f32_of(n.src[0]) && f32_of(n.dst) && n.dst.ne[0] == 1 && n.dst.ne[1] == n.src[0].ne[1] &&
+                   n.dst.ne[2] == n.src[0].ne[2] && n.dst.ne[3] == n.src[0].ne[3];
         case SHP_NODE_NORM:
             return unary_ok(n) && fparam(n, 0) >= 0.0f;
         case SHP_NODE_CPY:
@@ -725,7 +733,7 @@ class Planner {
                         return used;
                     }
                 }
-                return 0;
+                return match_mul_sum_rows(p, l);
             case SHP_NODE_ADD:
                 if ((used = match_transpose_bias(p, l)) != 0) {
                     return used;
@@ -1382,6 +1390,28 @@ class Planner {
         return 2;
     }
 
+    // MUL(x, w) then SUM_ROWS of the product, the product read nowhere else:
+    // x and w of one shape (the attention-weighted sums of the speaker
+    // encoder's pooling).
+    int match_mul_sum_rows(size_t p, Launch & l) const {
+        const int mu = at(p, 0);
+        const int sr = at(p, 1);
+        if (!is(mu, SHP_NODE_MUL) || !is(sr, SHP_NODE_SUM_ROWS) || src(sr, 0) != mu) {
+            return 0;
+        }
+        const shp_node & M = nodes_[mu];
+        const shp_node & S = nodes_[sr];
+        if (!f32_of(M.src[0]) || !f32_of(M.src[1]) || !same_shape(M.src[0], M.src[1]) || !f32_of(M.dst) ||
+            !same_shape(M.dst, M.src[0]) || !single_ok(S) || !internal(mu, Members{ mu, sr })) {
+            return 0;
+        }
+        l.kind = SHP_RUN_MUL_SUM_ROWS;
+        l.x    = &M.src[0];
+        l.b    = &M.src[1];
+        l.y    = const_cast<shp_tensor *>(&S.dst);
+        return 2;
+    }
+
     // SILU(g) then MUL(silu, u) (either operand order: the product commutes).
     int match_silu_mul(size_t p, Launch & l) const {
         const int si = at(p, 0);
@@ -1480,6 +1510,18 @@ shp_status_t launch_single(const shp_node & n, shp_stream_t st) {
             return shp_pad_reflect_1d(&n.src[0], n.op_params[0], n.op_params[1], y, st);
         case SHP_NODE_REPEAT:
             return shp_repeat(&n.src[0], y, st);
+        case SHP_NODE_RELU:
+            return shp_relu(&n.src[0], y, st);
+        case SHP_NODE_NEG:
+            return shp_neg(&n.src[0], y, st);
+        case SHP_NODE_STEP:
+            return shp_step(&n.src[0], y, st);
+        case SHP_NODE_SQRT:
+            return shp_sqrt(&n.src[0], y, st);
+        case SHP_NODE_SUM_ROWS:
+            return shp_sum_rows(&n.src[0], y, st);
+        case SHP_NODE_MEAN:
+            return shp_mean(&n.src[0], y, st);
         case SHP_NODE_ACC:
             return shp_acc(&n.src[0], &n.src[1], n.op_params[0], n.op_params[1], n.op_params[2], n.op_params[3], y, st);
         default:
@@ -1526,6 +1568,8 @@ shp_status_t launch_run(const Planner & pl, const Launch & l, shp_stream_t st) {
             return l.i0 == SHP_NODE_ADD ? shp_add(l.x, l.b, l.y, st) :
                    l.i0 == SHP_NODE_MUL ? shp_mul(l.x, l.b, l.y, st) :
                                           shp_div(l.x, l.b, l.y, st);
+        case SHP_RUN_MUL_SUM_ROWS:
+            return shp_mul_sum_rows(l.x, l.b, l.y, st);
         case SHP_RUN_CONT_IM2COL:
             return shp_im2col(l.w, &l.xv, l.i0, l.i1, l.i2, l.y, st);
         default:

@@ -100,6 +100,13 @@ def load(path=None):
         "shp_acc": [_PT, _PT, i64, i64, i64, i64, _PT, vp],
         "shp_sub": [_PT, _PT, _PT, vp],
         "shp_tanh": [_PT, _PT, vp],
+        "shp_relu": [_PT, _PT, vp],
+        "shp_neg": [_PT, _PT, vp],
+        "shp_step": [_PT, _PT, vp],
+        "shp_sqrt": [_PT, _PT, vp],
+        "shp_sum_rows": [_PT, _PT, vp],
+        "shp_mean": [_PT, _PT, vp],
+        "shp_mul_sum_rows": [_PT, _PT, _PT, vp],
         "shp_sigmoid": [_PT, _PT, vp],
         "shp_elu": [_PT, _PT, vp],
         "shp_gelu_erf": [_PT, _PT, vp],
@@ -522,6 +529,49 @@ def gelu_erf(x, out=None):
     return _unary_call("gelu_erf", x, out)
 
 
+def relu(x, out=None):
+    """ggml_relu."""
+    return _unary_call("relu", x, out)
+
+
+def neg(x, out=None):
+    """ggml_neg."""
+    return _unary_call("neg", x, out)
+
+
+def step(x, out=None):
+    """ggml_step."""
+    return _unary_call("step", x, out)
+
+
+def sqrt(x, out=None):
+    """ggml_sqrt."""
+    return _unary_call("sqrt", x, out)
+
+
+def _row_sums(name, x, w, out):
+    import torch
+    out = torch.empty(tuple(x.shape[:-1]) + (1,), dtype=torch.float32, device=x.device) if out is None else out
+    args = [_ref(desc(x))] + ([_ref(desc(w))] if w is not None else []) + [_ref(desc(out)), _stream()]
+    _check(getattr(load(), "shp_" + name)(*args), name)
+    return out
+
+
+def sum_rows(x, out=None):
+    """ggml_sum_rows: (..., ne0) -> (..., 1)."""
+    return _row_sums("sum_rows", x, None, out)
+
+
+def mean(x, out=None):
+    """ggml_mean: (..., ne0) -> (..., 1)."""
+    return _row_sums("mean", x, None, out)
+
+
+def mul_sum_rows(x, w, out=None):
+    """ggml_mul(x, w) then ggml_sum_rows, one launch."""
+    return _row_sums("mul_sum_rows", x, w, out)
+
+
 def clamp(x, lo, hi, out=None):
     """ggml_clamp(x, lo, hi)."""
     out = x.new_empty(x.shape) if out is None else out
@@ -652,12 +702,13 @@ def cpy(x, out=None):
 (NODE_NOP, NODE_ADD, NODE_MUL, NODE_DIV, NODE_SQR, NODE_SIN, NODE_SCALE, NODE_CPY, NODE_GET_ROWS, NODE_RMS_NORM,
  NODE_SOFT_MAX, NODE_ROPE, NODE_LEAKY_RELU, NODE_SILU, NODE_EXP, NODE_GLU_SWIGLU, NODE_CONCAT, NODE_SUB, NODE_TANH,
  NODE_SIGMOID, NODE_ELU, NODE_GELU_ERF, NODE_CLAMP, NODE_NORM, NODE_IM2COL, NODE_COL2IM_1D, NODE_PAD,
- NODE_PAD_REFLECT_1D, NODE_REPEAT, NODE_ACC) = range(30)
+ NODE_PAD_REFLECT_1D, NODE_REPEAT, NODE_ACC, NODE_RELU, NODE_NEG, NODE_STEP, NODE_SQRT, NODE_SUM_ROWS,
+ NODE_MEAN) = range(36)
 NODE_FLAG_OUTPUT = 1
 RUN_KINDS = {-1: "unsupported", 0: "nop", 1: "single", 2: "norm_mul", 3: "norm_mul_rope", 4: "add_norm_mul",
              5: "silu_mul", 6: "add_leaky", 7: "add_scale_leaky", 8: "snake", 9: "snake_guarded", 10: "snake_beta",
              11: "gather_sum", 12: "qk_norm_rope", 13: "qk_norm_rope_kv", 14: "cont_add_leaky",
-             15: "view_binary", 16: "cont_im2col"}
+             15: "view_binary", 16: "cont_im2col", 17: "mul_sum_rows"}
 
 
 class ShpNode(ctypes.Structure):
@@ -795,6 +846,26 @@ class Graph:
 
     def gelu_erf(self, x):
         return self._op(NODE_GELU_ERF, self._like(x), [x])
+
+    def relu(self, x):
+        return self._op(NODE_RELU, self._like(x), [x])
+
+    def neg(self, x):
+        return self._op(NODE_NEG, self._like(x), [x])
+
+    def step(self, x):
+        return self._op(NODE_STEP, self._like(x), [x])
+
+    def sqrt(self, x):
+        return self._op(NODE_SQRT, self._like(x), [x])
+
+    def sum_rows(self, x):
+        t = self._t(x)
+        return self._op(NODE_SUM_ROWS, self._like(x, tuple(t.shape[:-1]) + (1,)), [x])
+
+    def mean(self, x):
+        t = self._t(x)
+        return self._op(NODE_MEAN, self._like(x, tuple(t.shape[:-1]) + (1,)), [x])
 
     def clamp(self, x, lo, hi):
         return self._op(NODE_CLAMP, self._like(x), [x], floats={0: lo, 1: hi})

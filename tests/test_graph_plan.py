@@ -692,3 +692,23 @@ def test_talker_prefill_accumulation_plans_as_singles():
     out = g.acc(out, g.view(codec, codec.t[3:]), nb1, nb2, nb2, 6 * nb1)
     out = g.acc(out, ac, nb1, nb2, nb2, 5 * nb1)
     assert [k for k in kinds(g.plan(out)) if k != "nop"] == ["single"] * 5
+
+
+def test_row_sum_nodes_and_the_weighted_sum_run():
+    """SUM_ROWS and MEAN take [1, ne1, ne2, ne3] results; MUL then SUM_ROWS of
+    the product is one launch unless the product is read elsewhere."""
+    x, w = z(6, 40), z(6, 40)
+    g = S.Graph()
+    s = g.sum_rows(g.mul(x, w))
+    assert kinds(g.plan(s)) == ["mul_sum_rows"]
+    g = S.Graph()
+    p = g.mul(x, w)
+    s = g.sum_rows(p)
+    assert kinds(g.plan(s, p)) == ["single", "single"]
+    g = S.Graph()
+    bad = g._op(S.NODE_MEAN, z(6, 2), [x])
+    arr, n, keep = g.nodes(bad)
+    assert S.load().shp_graph_node_supported(ctypes.byref(arr[0])) == 0
+    g = S.Graph()
+    y = g.sqrt(g.relu(g.neg(g.step(x))))
+    assert kinds(g.plan(y)) == ["single"] * 4

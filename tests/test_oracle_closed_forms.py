@@ -834,3 +834,53 @@ def test_acc_prefill_acoustic_block_after_the_codec_sum():
     other[N - m:] = text[N - m:] + (codec[n - m:] + acoustic)
     other[N - n:N - m] = text[N - n:N - m] + codec[:n - m]
     assert not np.array_equal(got, other)
+
+
+# ---------------------------------------------------------------------------
+# ggml_relu, ggml_neg, ggml_step, ggml_sqrt; ggml_sum_rows, ggml_mean
+# ---------------------------------------------------------------------------
+
+_SPECIALS = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-45, 3.4e38, -3.4e38, 1.0, -1.0],
+                     np.float32)
+
+
+def test_relu_neg_step_sqrt_against_numpy():
+    """relu is numpy's maximum with 0 and step its heaviside at 0 on ordered
+    values, with ggml's x > 0 forms at the rest (-0 and NaN give +0); neg
+    flips exactly the sign bit (zeros and NaN included); sqrt is numpy's
+    correctly rounded f32 square root (NaN below zero)."""
+    x = np.random.default_rng(21).standard_normal((64, 65)).astype(np.float32) * 10
+    x.reshape(-1)[:_SPECIALS.size] = _SPECIALS
+    g = R.Graph()
+    outs = g.relu(x), g.neg(x), g.step(x), g.sqrt(x)
+    g.compute()
+    relu, neg, step, sq = outs
+    ok = ~np.isnan(x) & (x != 0)
+    assert np.array_equal(relu[ok], np.maximum(x[ok], 0))
+    assert (relu[~ok].view(np.uint32) == 0).all()
+    assert np.array_equal(neg.view(np.uint32), x.view(np.uint32) ^ np.uint32(0x80000000))
+    assert np.array_equal(step[~np.isnan(x)], np.heaviside(x[~np.isnan(x)], 0).astype(np.float32))
+    assert (step[np.isnan(x)] == 0).all()
+    with np.errstate(invalid="ignore"):
+        ref = np.sqrt(x)
+    assert np.array_equal(sq.view(np.uint32)[x >= 0], ref.view(np.uint32)[x >= 0])
+    assert np.isnan(sq[(x < 0) | np.isnan(x)]).all()
+
+
+def test_sum_rows_and_mean_are_the_rounded_exact_sum():
+    """ggml_vec_sum_f32's double accumulation of f32 values: the f32 rounding
+    of the exact sum (math.fsum) for every row, over rows with a wide spread
+    of magnitudes, which a running f32 sum misses; the mean is that f32 sum
+    divided by ne0 in f32, which rounding the exact mean once misses."""
+    import math
+    rng = np.random.default_rng(22)
+    x = (rng.standard_normal((512, 300)) * np.exp(rng.uniform(-8, 8, (512, 300)))).astype(np.float32)
+    g = R.Graph()
+    s, m = g.sum_rows(x), g.mean(x)
+    g.compute()
+    exact = np.array([math.fsum(map(float, row)) for row in x])
+    assert s.shape == (512, 1) and np.array_equal(s[:, 0], exact.astype(np.float32))
+    running = np.cumsum(x, axis=1, dtype=np.float32)[:, -1]
+    assert not np.array_equal(s[:, 0], running)
+    assert np.array_equal(m[:, 0], exact.astype(np.float32) / np.float32(300))
+    assert not np.array_equal(m[:, 0], (exact / 300).astype(np.float32))
