@@ -47,6 +47,8 @@
  *   CPY [views] IM2COL               the causal convolution's time-major copy
  *        and its column matrix (src/arch/qwen3-tts/codec.cpp:94-96): im2col
  *        reads the channel-major activation through the transposed view
+ *   DIAG_MASK_INF SOFT_MAX           the codec encoder's causal attention softmax
+ *        (src/arch/qwen3-tts/codec-encoder.cpp:482-483)
  *   MUL SUM_ROWS                     the attention-weighted sums of the speaker
  *        encoder's statistics pooling (src/arch/qwen3-tts/speaker-encoder.cpp:
  *        292-293,374): the product is summed as it is formed
@@ -117,6 +119,7 @@ typedef enum shp_node_op {
     SHP_NODE_SQRT,       /* GGML_OP_SQRT */
     SHP_NODE_SUM_ROWS,   /* GGML_OP_SUM_ROWS: dst [1, ne1, ne2, ne3] */
     SHP_NODE_MEAN,       /* GGML_OP_MEAN: dst [1, ne1, ne2, ne3] */
+    SHP_NODE_DIAG_MASK_INF, /* GGML_OP_DIAG_MASK_INF: i32 {n_past} (dst may be src[0]: inplace) */
     SHP_NODE_OP_COUNT
 } shp_node_op;
 
@@ -161,8 +164,10 @@ typedef enum shp_run_kind {
     SHP_RUN_CONT_IM2COL,      /* CPY of a transposed channel-major F32 activation,
                                  [views], IM2COL of the copy: shp_im2col reads the
                                  activation in place of the copy */
-    SHP_RUN_MUL_SUM_ROWS      /* MUL whose product only SUM_ROWS reads, then that
+    SHP_RUN_MUL_SUM_ROWS,     /* MUL whose product only SUM_ROWS reads, then that
                                  SUM_ROWS: shp_mul_sum_rows */
+    SHP_RUN_DIAG_MASK_SOFT_MAX /* DIAG_MASK_INF whose result only a maskless SOFT_MAX
+                                 reads, then that SOFT_MAX: shp_soft_max_causal */
 } shp_run_kind;
 
 typedef struct shp_graph_run {

@@ -595,6 +595,24 @@ shp_status_t shp_soft_max_ext(const shp_tensor * a,
                               shp_stream_t       stream);
 
 /*
+ * ggml_diag_mask_inf(x, n_past) (and its inplace form, y == x): element i0
+ * of row i1 of each matrix becomes -inf when i0 > n_past + i1, the rest are
+ * copied; the codec encoder's causal attention scores
+ * (qwen3-tts/codec-encoder.cpp:482). x, y F32 of one shape, rows contiguous.
+ */
+shp_status_t shp_diag_mask_inf(const shp_tensor * x, int32_t n_past, shp_tensor * y, shp_stream_t stream);
+
+/*
+ * ggml_diag_mask_inf(a, n_past) then ggml_soft_max_ext(., NULL, scale, 0) as
+ * one launch (qwen3-tts/codec-encoder.cpp:482-483): the masked scores are
+ * replaced by -inf and the rest scaled, then the softmax of
+ * shp_soft_max_ext; bit-identical to the two nodes. scale positive and
+ * finite (-inf times it stays -inf).
+ */
+shp_status_t shp_soft_max_causal(const shp_tensor * a, int32_t n_past, float scale, shp_tensor * y,
+                                 shp_stream_t stream);
+
+/*
  * ggml_exp: y = expf(x) per element, F32 of one shape
  * (src/arch/qwen3-tts/codec.cpp:193-194, vits/latent-sampling.cpp:30).
  */

@@ -725,6 +725,26 @@ static void op_pad_family(const orc_node * n, int ith, int nth) {
     }
 }
 
+/* ggml_diag_mask_inf(x, n_past) (qwen3-tts/codec-encoder.cpp:482): x copied,
+ * then in row j of every matrix each element i >= n_past with i > n_past + j
+ * set to -inf, as ggml-CPU's forward_diag_mask writes them. */
+static void op_diag_mask_inf(const orc_node * n, int ith, int nth) {
+    int64_t r0, r1;
+    chunk(n->nrows, ith, nth, &r0, &r1);
+    const int64_t n_past = n->i[0];
+    for (int64_t r = r0; r < r1; ++r) {
+        const int64_t j = r % n->ne1;
+        const float * x = (const float *) n->src0 + r * n->ne0;
+        float *       y = (float *) n->dst + r * n->ne0;
+        memcpy(y, x, (size_t) n->ne0 * sizeof(float));
+        for (int64_t i = n_past; i < n->ne0; ++i) {
+            if (i > n_past + j) {
+                y[i] = -INFINITY;
+            }
+        }
+    }
+}
+
 /* ggml_sum_rows and ggml_mean (qwen3-tts/speaker-encoder.cpp:195,292-293,
  * 350,374, the speaker encoder's statistics pooling; vits/duration-
  * predictor.cpp:47,93): ggml_vec_sum_f32 accumulates a row's f32 values into
@@ -927,6 +947,9 @@ static void run_node(const orc_node * n, int ith, int nth) {
         case ORC_OP_SUM_ROWS:
         case ORC_OP_MEAN:
             op_sum_rows(n, ith, nth);
+            break;
+        case ORC_OP_DIAG_MASK_INF:
+            op_diag_mask_inf(n, ith, nth);
             break;
         default:
             atomic_store(&g_node_error, -1);

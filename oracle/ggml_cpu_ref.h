@@ -64,6 +64,7 @@ enum orc_op {
     ORC_OP_SQRT,         /* sqrtf(x)                                ggml_sqrt           */
     ORC_OP_SUM_ROWS,     /* dst[r] = (float) double sum of row r    ggml_sum_rows       */
     ORC_OP_MEAN,         /* dst[r] = sum_rows / (float) ne0         ggml_mean           */
+    ORC_OP_DIAG_MASK_INF, /* -inf past n_past + row, else x         ggml_diag_mask_inf  */
 };
 
 /*
@@ -105,6 +106,7 @@ enum orc_op {
  *               (PAD), {p0, p1, 0, 0} (PAD_REFLECT_1D) or zeros (REPEAT);
  *               dst contiguous F32.
  *   SUM_ROWS, MEAN : src0 nrows rows of ne0; dst one value per row.
+ *   DIAG_MASK_INF : src0 nrows rows of ne0, ne1 rows per matrix; i[0] = n_past.
  *   ACC       : src0 = a, contiguous F32 of nrows*ne0 elements; src1 =
  *               int64_t[9]: b's ne[0..3], the view's byte strides nb1, nb2,
  *               nb3, its byte offset, then the b data pointer (contiguous F32);

@@ -51,11 +51,18 @@ struct SoftMaxArgs {
     // from multiply-shift divisions (FastDiv) instead of 64-bit divisions.
     int32_t       mfast;
     int32_t       pad;
+    int64_t       n_past;  // causal form: element i of row r is masked when i > n_past + r % ne1
     FastDiv       fne1;
     FastDiv       fne2;
     FastDiv       fmne2;
     FastDiv       fmne3;
 };
+
+// Mask forms: none, a mask tensor added to the scaled scores, or the causal
+// mask of ggml_diag_mask_inf in front of the softmax (the masked scores
+// replaced by -inf before the scale, as the two nodes compute them: a masked
+// +inf or NaN score drops out instead of turning the row into NaN).
+enum MaskKind { kMaskNone = 0, kMaskTensor = 1, kMaskCausal = 2 };
 
 constexpr int kSoftMaxWaveMax = 2048;  // widest row of the one-wave kernel
 constexpr int kSoftMaxBlock   = 256;
@@ -84,19 +91,28 @@ __device__ __forceinline__ const float * mask_row(const SoftMaxArgs & a, int64_t
                                            (i2 % a.mne2) * a.mnb2 + (i3 % a.mne3) * a.mnb3);
 }
 
+// The causal form's last unmasked element of row r: n_past + i1.
+__device__ __forceinline__ int64_t causal_lim(const SoftMaxArgs & a, int64_t r) {
+    if (a.mfast) {
+        return a.n_past + fastmod(static_cast<uint32_t>(r), a.fne1);
+    }
+    return a.n_past + r % a.ne1;
+}
+
 // The kernel arguments a softmax wave needs before its first load.
-template <bool MASK> __device__ __forceinline__ void softmax_args_in_sgprs(const SoftMaxArgs & a) {
+template <int MK> __device__ __forceinline__ void softmax_args_in_sgprs(const SoftMaxArgs & a) {
     args_in_sgprs(a.x, a.xm.flat, a.xm.rs, a.y, a.ym.flat, a.ym.rs, a.nrows, a.ne0, a.scale);
-    if constexpr (MASK) {
+    if constexpr (MK == kMaskTensor) {
         args_in_sgprs(a.mask, a.mfast, a.fne1.d, a.fne1.m, a.fne1.l, a.fne2.d, a.fne2.m, a.fne2.l, a.fmne2.d,
                       a.fmne2.m, a.fmne2.l, a.fmne3.d, a.fmne3.m, a.fmne3.l, a.mnb1, a.mnb2, a.mnb3);
     }
 }
 
 // One wave per row, element lane + 64k in register k (k < K, 64K >= ne0).
-template <int K, bool MASK> __global__ __launch_bounds__(256) void k_soft_max_wave(const SoftMaxArgs a) {
+template <int K, int MK> __global__ __launch_bounds__(256) void k_soft_max_wave(const SoftMaxArgs a) {
+    constexpr bool MASK = MK == kMaskTensor;
     __shared__ double s_tab[256 / kWave][64];
-    softmax_args_in_sgprs<MASK>(a);
+    softmax_args_in_sgprs<MK>(a);
     const int     lane = threadIdx.x % kWave;
     const int64_t r    = static_cast<int64_t>(blockIdx.x) * (256 / kWave) +
                       __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
@@ -105,7 +121,8 @@ template <int K, bool MASK> __global__ __launch_bounds__(256) void k_soft_max_wa
     }
     const float * xr = reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.x) + row_offset(a.xm, r));
     float *       yr = reinterpret_cast<float *>(reinterpret_cast<char *>(a.y) + row_offset(a.ym, r));
-    const float * mr = MASK ? mask_row(a, r) : nullptr;
+    const float * mr  = MASK ? mask_row(a, r) : nullptr;
+    const int64_t lim = MK == kMaskCausal ? causal_lim(a, r) : 0;
     float         w[K];
     float         mk[K];
     // The exp table's entry is loaded with the row. Loads are unconditional
@@ -133,6 +150,9 @@ template <int K, bool MASK> __global__ __launch_bounds__(256) void k_soft_max_wa
         w[k]        = w[k] * a.scale;
         if constexpr (MASK) {
             w[k] = w[k] + mk[k];
+        }
+        if constexpr (MK == kMaskCausal) {
+            w[k] = i > lim ? -INFINITY : w[k];
         }
         mx = i < a.ne0 ? fmaxf(mx, w[k]) : mx;
     }
@@ -164,13 +184,14 @@ template <int K, bool MASK> __global__ __launch_bounds__(256) void k_soft_max_wa
 // WPR > 1 spreads the few long rows of a decode or short prefill over more
 // waves; the row's waves then combine their max and sum through LDS, in wave
 // order.
-template <int WPR, int K4, bool MASK, int BLOCK = 256>
+template <int WPR, int K4, int MK, int BLOCK = 256>
 __global__ __launch_bounds__(BLOCK) void k_soft_max_rows4(const SoftMaxArgs a) {
-    constexpr int kLanes = kWave * WPR;
+    constexpr bool MASK   = MK == kMaskTensor;
+    constexpr int  kLanes = kWave * WPR;
     __shared__ float  s_max[BLOCK / kWave];
     __shared__ double s_sum[BLOCK / kWave];
     __shared__ double s_tab[BLOCK / kWave][64];
-    softmax_args_in_sgprs<MASK>(a);
+    softmax_args_in_sgprs<MK>(a);
     const int     lane = threadIdx.x % kWave;
     const int     q    = threadIdx.x % kLanes;
     const int     wv   = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
@@ -185,6 +206,7 @@ __global__ __launch_bounds__(BLOCK) void k_soft_max_rows4(const SoftMaxArgs a) {
         reinterpret_cast<const f32x4 *>(reinterpret_cast<const char *>(a.x) + row_offset(a.xm, rr));
     f32x4 *       yr    = reinterpret_cast<f32x4 *>(reinterpret_cast<char *>(a.y) + row_offset(a.ym, rr));
     const f32x4 * mr    = MASK ? reinterpret_cast<const f32x4 *>(mask_row(a, rr)) : nullptr;
+    const int64_t lim   = MK == kMaskCausal ? causal_lim(a, rr) : 0;
     const int     n4 = live ? a.ne0 / 4 : 0;
     f32x4         w[K4];
     f32x4         mk[K4];
@@ -213,6 +235,11 @@ __global__ __launch_bounds__(BLOCK) void k_soft_max_rows4(const SoftMaxArgs a) {
         w[k]        = f32x4{ w[k].x * a.scale, w[k].y * a.scale, w[k].z * a.scale, w[k].w * a.scale };
         if constexpr (MASK) {
             w[k] = f32x4{ w[k].x + mk[k].x, w[k].y + mk[k].y, w[k].z + mk[k].z, w[k].w + mk[k].w };
+        }
+        if constexpr (MK == kMaskCausal) {
+            const int64_t i = static_cast<int64_t>(c) * 4;
+            w[k]            = f32x4{ i > lim ? -INFINITY : w[k].x, i + 1 > lim ? -INFINITY : w[k].y,
+                                     i + 2 > lim ? -INFINITY : w[k].z, i + 3 > lim ? -INFINITY : w[k].w };
         }
         const float m4 = fmaxf(fmaxf(w[k].x, w[k].y), fmaxf(w[k].z, w[k].w));
         mx             = c < n4 ? fmaxf(mx, m4) : mx;
@@ -262,15 +289,20 @@ __global__ __launch_bounds__(BLOCK) void k_soft_max_rows4(const SoftMaxArgs a) {
 }
 
 // One block per row, three passes: the max, the sum, the scaled exps.
-template <bool MASK> __device__ __forceinline__ float sm_w(const SoftMaxArgs & a, const float * xr, const float * mr, int i) {
+template <int MK>
+__device__ __forceinline__ float sm_w(const SoftMaxArgs & a, const float * xr, const float * mr, int64_t lim, int i) {
     float w = xr[i] * a.scale;
-    if constexpr (MASK) {
+    if constexpr (MK == kMaskTensor) {
         w = w + mr[i];
+    }
+    if constexpr (MK == kMaskCausal) {
+        w = i > lim ? -INFINITY : w;
     }
     return w;
 }
 
-template <bool MASK> __global__ __launch_bounds__(kSoftMaxBlock) void k_soft_max_block(const SoftMaxArgs a) {
+template <int MK> __global__ __launch_bounds__(kSoftMaxBlock) void k_soft_max_block(const SoftMaxArgs a) {
+    constexpr bool MASK = MK == kMaskTensor;
     __shared__ float  s_max[kSoftMaxBlock / kWave];
     __shared__ double s_sum[kSoftMaxBlock / kWave];
     const int64_t r    = blockIdx.x;
@@ -279,10 +311,11 @@ template <bool MASK> __global__ __launch_bounds__(kSoftMaxBlock) void k_soft_max
     const float * xr   = reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.x) + row_offset(a.xm, r));
     float *       yr   = reinterpret_cast<float *>(reinterpret_cast<char *>(a.y) + row_offset(a.ym, r));
     const float * mr   = MASK ? mask_row(a, r) : nullptr;
+    const int64_t lim  = MK == kMaskCausal ? causal_lim(a, r) : 0;
 
     float mx = -INFINITY;
     for (int i = threadIdx.x; i < a.ne0; i += kSoftMaxBlock) {
-        mx = fmaxf(mx, sm_w<MASK>(a, xr, mr, i));
+        mx = fmaxf(mx, sm_w<MK>(a, xr, mr, lim, i));
     }
     mx = wave_max(mx);
     if (lane == 0) {
@@ -297,7 +330,7 @@ template <bool MASK> __global__ __launch_bounds__(kSoftMaxBlock) void k_soft_max
 
     double sum = 0.0;
     for (int i = threadIdx.x; i < a.ne0; i += kSoftMaxBlock) {
-        sum += static_cast<double>(exp_f32(sm_w<MASK>(a, xr, mr, i) - mx));
+        sum += static_cast<double>(exp_f32(sm_w<MK>(a, xr, mr, lim, i) - mx));
     }
     sum = group_sum<kWave>(sum);
     if (lane == 0) {
@@ -311,16 +344,16 @@ template <bool MASK> __global__ __launch_bounds__(kSoftMaxBlock) void k_soft_max
     }
     const float inv = static_cast<float>(1.0 / sum);
     for (int i = threadIdx.x; i < a.ne0; i += kSoftMaxBlock) {
-        yr[i] = exp_f32(sm_w<MASK>(a, xr, mr, i) - mx) * inv;
+        yr[i] = exp_f32(sm_w<MK>(a, xr, mr, lim, i) - mx) * inv;
     }
 }
 
-template <bool MASK> shp_status_t launch_soft_max(const SoftMaxArgs & a, bool vec, hipStream_t stream) {
+template <int MK> shp_status_t launch_soft_max(const SoftMaxArgs & a, bool vec, hipStream_t stream) {
     if (dry_run()) {
         return SHP_OK;
     }
     if (a.ne0 > kSoftMaxWaveMax) {
-        hipLaunchKernelGGL((k_soft_max_block<MASK>), dim3(static_cast<unsigned>(a.nrows)), dim3(kSoftMaxBlock), 0,
+        hipLaunchKernelGGL((k_soft_max_block<MK>), dim3(static_cast<unsigned>(a.nrows)), dim3(kSoftMaxBlock), 0,
                            stream, a);
         return launch_status();
     }
@@ -337,46 +370,46 @@ template <bool MASK> shp_status_t launch_soft_max(const SoftMaxArgs & a, bool ve
         const dim3 g4(static_cast<unsigned>((a.nrows * wpr + 3) / 4));
         if (wpr == 4) {
             if (k4 <= 1) {
-                hipLaunchKernelGGL((k_soft_max_rows4<4, 1, MASK>), g4, dim3(256), 0, stream, a);
+                hipLaunchKernelGGL((k_soft_max_rows4<4, 1, MK>), g4, dim3(256), 0, stream, a);
             } else {
-                hipLaunchKernelGGL((k_soft_max_rows4<4, 2, MASK>), g4, dim3(256), 0, stream, a);
+                hipLaunchKernelGGL((k_soft_max_rows4<4, 2, MK>), g4, dim3(256), 0, stream, a);
             }
         } else if (wpr == 2) {
             if (k4 <= 1) {
-                hipLaunchKernelGGL((k_soft_max_rows4<2, 1, MASK>), g4, dim3(256), 0, stream, a);
+                hipLaunchKernelGGL((k_soft_max_rows4<2, 1, MK>), g4, dim3(256), 0, stream, a);
             } else if (k4 <= 2) {
-                hipLaunchKernelGGL((k_soft_max_rows4<2, 2, MASK>), g4, dim3(256), 0, stream, a);
+                hipLaunchKernelGGL((k_soft_max_rows4<2, 2, MK>), g4, dim3(256), 0, stream, a);
             } else {
-                hipLaunchKernelGGL((k_soft_max_rows4<2, 4, MASK>), g4, dim3(256), 0, stream, a);
+                hipLaunchKernelGGL((k_soft_max_rows4<2, 4, MK>), g4, dim3(256), 0, stream, a);
             }
         } else if (k4 <= 1) {
-            hipLaunchKernelGGL((k_soft_max_rows4<1, 1, MASK>), g4, dim3(256), 0, stream, a);
+            hipLaunchKernelGGL((k_soft_max_rows4<1, 1, MK>), g4, dim3(256), 0, stream, a);
         } else if (k4 <= 2 && a.nrows <= 64) {
             // a decode step's few rows: one one-wave block per row
-            hipLaunchKernelGGL((k_soft_max_rows4<1, 2, MASK, kWave>), dim3(static_cast<unsigned>(a.nrows)), dim3(kWave),
+            hipLaunchKernelGGL((k_soft_max_rows4<1, 2, MK, kWave>), dim3(static_cast<unsigned>(a.nrows)), dim3(kWave),
                                0, stream, a);
         } else if (k4 <= 2) {
-            hipLaunchKernelGGL((k_soft_max_rows4<1, 2, MASK>), g4, dim3(256), 0, stream, a);
+            hipLaunchKernelGGL((k_soft_max_rows4<1, 2, MK>), g4, dim3(256), 0, stream, a);
         } else if (k4 <= 4) {
-            hipLaunchKernelGGL((k_soft_max_rows4<1, 4, MASK>), g4, dim3(256), 0, stream, a);
+            hipLaunchKernelGGL((k_soft_max_rows4<1, 4, MK>), g4, dim3(256), 0, stream, a);
         } else {
-            hipLaunchKernelGGL((k_soft_max_rows4<1, 8, MASK>), g4, dim3(256), 0, stream, a);
+            hipLaunchKernelGGL((k_soft_max_rows4<1, 8, MK>), g4, dim3(256), 0, stream, a);
         }
         return launch_status();
     }
     const int k = (a.ne0 + kWave - 1) / kWave;
     if (k <= 1) {
-        hipLaunchKernelGGL((k_soft_max_wave<1, MASK>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((k_soft_max_wave<1, MK>), grid, dim3(256), 0, stream, a);
     } else if (k <= 2) {
-        hipLaunchKernelGGL((k_soft_max_wave<2, MASK>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((k_soft_max_wave<2, MK>), grid, dim3(256), 0, stream, a);
     } else if (k <= 4) {
-        hipLaunchKernelGGL((k_soft_max_wave<4, MASK>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((k_soft_max_wave<4, MK>), grid, dim3(256), 0, stream, a);
     } else if (k <= 8) {
-        hipLaunchKernelGGL((k_soft_max_wave<8, MASK>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((k_soft_max_wave<8, MK>), grid, dim3(256), 0, stream, a);
     } else if (k <= 16) {
-        hipLaunchKernelGGL((k_soft_max_wave<16, MASK>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((k_soft_max_wave<16, MK>), grid, dim3(256), 0, stream, a);
     } else {
-        hipLaunchKernelGGL((k_soft_max_wave<32, MASK>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((k_soft_max_wave<32, MK>), grid, dim3(256), 0, stream, a);
     }
     return launch_status();
 }
@@ -440,6 +473,100 @@ extern "C" shp_status_t shp_soft_max_ext(const shp_tensor * a,
     // 16-byte aligned and whole float4s per row
     const bool vec = a->ne[0] % 4 == 0 && rows_aligned(*a, 16) && rows_aligned(*y, 16) &&
                      (mask == nullptr || rows_aligned(*mask, 16));
-    return mask != nullptr ? launch_soft_max<true>(g, vec, as_stream(stream))
-                           : launch_soft_max<false>(g, vec, as_stream(stream));
+    return mask != nullptr ? launch_soft_max<kMaskTensor>(g, vec, as_stream(stream))
+                           : launch_soft_max<kMaskNone>(g, vec, as_stream(stream));
+}
+
+// ggml_diag_mask_inf(x, n_past): every element past n_past + its row's index
+// in the matrix (i0 > n_past + i1) becomes -inf, the rest copied.
+struct DiagMaskArgs {
+    const float * x;
+    RowMap        xm;
+    float *       y;
+    RowMap        ym;
+    int64_t       n_past;
+    int64_t       ne1;
+    int64_t       total;  // rows x ne0
+    FastDiv       fne0;
+    FastDiv       fne1;
+};
+
+__global__ __launch_bounds__(256) void k_diag_mask_inf(const DiagMaskArgs a) {
+    const int64_t step = static_cast<int64_t>(gridDim.x) * 256;
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; t < a.total; t += step) {
+        const uint32_t r  = fastdiv(static_cast<uint32_t>(t), a.fne0);
+        const uint32_t i0 = static_cast<uint32_t>(t) - r * a.fne0.d;
+        const uint32_t i1 = fastmod(r, a.fne1);
+        const float *  xr = reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.x) + row_offset(a.xm, r));
+        float *        yr = reinterpret_cast<float *>(reinterpret_cast<char *>(a.y) + row_offset(a.ym, r));
+        yr[i0]            = static_cast<int64_t>(i0) > a.n_past + i1 ? -INFINITY : xr[i0];
+    }
+}
+
+extern "C" shp_status_t shp_diag_mask_inf(const shp_tensor * x, int32_t n_past, shp_tensor * y, shp_stream_t stream) {
+    if (!well_formed(x) || !well_formed(y) || n_past < 0) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    if (x->type != SHP_TYPE_F32 || y->type != SHP_TYPE_F32) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    if (!same_shape(*x, *y) || nelements(*x) > INT32_MAX) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    const bool in_place = x->data == y->data && x->nb[1] == y->nb[1] && x->nb[2] == y->nb[2] && x->nb[3] == y->nb[3];
+    if (!in_place && spans_overlap(*x, *y)) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    if (dry_run()) {
+        return SHP_OK;
+    }
+    DiagMaskArgs g{};
+    g.x                  = static_cast<const float *>(x->data);
+    g.xm                 = make_rowmap(*x);
+    g.y                  = static_cast<float *>(y->data);
+    g.ym                 = make_rowmap(*y);
+    g.n_past             = n_past;
+    g.ne1                = x->ne[1];
+    g.total              = nelements(*x);
+    g.fne0               = make_fastdiv(static_cast<uint32_t>(x->ne[0]));
+    g.fne1               = make_fastdiv(static_cast<uint32_t>(x->ne[1]));
+    const int64_t blocks = (g.total + 255) / 256;
+    hipLaunchKernelGGL(k_diag_mask_inf, dim3(static_cast<unsigned>(blocks < (1 << 20) ? blocks : (1 << 20))),
+                       dim3(256), 0, as_stream(stream), g);
+    return launch_status();
+}
+
+extern "C" shp_status_t shp_soft_max_causal(const shp_tensor * a,
+                                            int32_t            n_past,
+                                            float              scale,
+                                            shp_tensor *       y,
+                                            shp_stream_t       stream) {
+    if (!well_formed(a) || !well_formed(y) || n_past < 0) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    if (a->type != SHP_TYPE_F32 || y->type != SHP_TYPE_F32) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    // -inf times the scale is -inf only for a positive finite scale
+    if (!(scale > 0.0f) || !(scale < INFINITY)) {
+        return SHP_ERR_UNSUPPORTED;
+    }
+    if (!same_shape(*a, *y) || a->ne[0] > INT32_MAX || nrows(*a) > INT32_MAX) {
+        return SHP_ERR_INVALID_ARG;
+    }
+    SoftMaxArgs g{};
+    g.x      = static_cast<const float *>(a->data);
+    g.xm     = make_rowmap(*a);
+    g.y      = static_cast<float *>(y->data);
+    g.ym     = make_rowmap(*y);
+    g.nrows  = nrows(*a);
+    g.ne1    = a->ne[1];
+    g.ne2    = a->ne[2];
+    g.ne0    = static_cast<int32_t>(a->ne[0]);
+    g.scale  = scale;
+    g.n_past = n_past;
+    g.mfast  = 1;  // rows below 2^31
+    g.fne1   = make_fastdiv(static_cast<uint32_t>(g.ne1));
+    const bool vec = a->ne[0] % 4 == 0 && rows_aligned(*a, 16) && rows_aligned(*y, 16);
+    return launch_soft_max<kMaskCausal>(g, vec, as_stream(stream));
 }

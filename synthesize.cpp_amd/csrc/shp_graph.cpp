@@ -10,6 +10,7 @@
 // cannot be observed. Every fused launch computes what the nodes compute one
 // by one, bit for bit.
 #include <algorithm>
+#include <cmath>
 #include <cstddef>
 #include <cstdint>
 #include <cstring>
@@ -113,6 +114,8 @@ bool node_form_ok(const shp_node & n) {
         case SHP_NODE_STEP:
         case SHP_NODE_SQRT:
             return unary_ok(n);
+        case SHP_NODE_DIAG_MASK_INF:
+            return unary_ok(n) && n.op_params[0] >= 0;
         case SHP_NODE_SUM_ROWS:
         case SHP_NODE_MEAN:
             return f32_of(n.src[0]) && f32_of(n.dst) && n.dst.ne[0] == 1 && n.dst.ne[1] == n.src[0].ne[1] &&
@@ -758,6 +761,8 @@ class Planner {
                 return 0;
             case SHP_NODE_SILU:
                 return match_silu_mul(p, l);
+            case SHP_NODE_DIAG_MASK_INF:
+                return match_causal_soft_max(p, l);
             case SHP_NODE_CPY:
                 if ((used = match_transpose_bias(p, l)) != 0 || (used = match_cont_tail(p, l)) != 0 ||
                     (used = match_cont_im2col(p, l)) != 0) {
@@ -1390,6 +1395,29 @@ class Planner {
         return 2;
     }
 
+    // DIAG_MASK_INF then a maskless SOFT_MAX of its result with a positive
+    // finite scale, the masked scores read nowhere else.
+    int match_causal_soft_max(size_t p, Launch & l) const {
+        const int dm = at(p, 0);
+        const int sm = at(p, 1);
+        if (!is(dm, SHP_NODE_DIAG_MASK_INF) || !is(sm, SHP_NODE_SOFT_MAX) || src(sm, 0) != dm) {
+            return 0;
+        }
+        const shp_node & D = nodes_[dm];
+        const shp_node & M = nodes_[sm];
+        const float      scale = fparam(M, 0);
+        if (!single_ok(D) || !single_ok(M) || present(M.src[1]) || !(scale > 0.0f) || !(scale < INFINITY) ||
+            !internal(dm, Members{ dm, sm })) {
+            return 0;
+        }
+        l.kind = SHP_RUN_DIAG_MASK_SOFT_MAX;
+        l.x    = &D.src[0];
+        l.i0   = D.op_params[0];
+        l.f0   = scale;
+        l.y    = const_cast<shp_tensor *>(&M.dst);
+        return 2;
+    }
+
     // MUL(x, w) then SUM_ROWS of the product, the product read nowhere else:
     // x and w of one shape (the attention-weighted sums of the speaker
     // encoder's pooling).
@@ -1518,6 +1546,8 @@ shp_status_t launch_single(const shp_node & n, shp_stream_t st) {
             return shp_step(&n.src[0], y, st);
         case SHP_NODE_SQRT:
             return shp_sqrt(&n.src[0], y, st);
+        case SHP_NODE_DIAG_MASK_INF:
+            return shp_diag_mask_inf(&n.src[0], n.op_params[0], y, st);
         case SHP_NODE_SUM_ROWS:
             return shp_sum_rows(&n.src[0], y, st);
         case SHP_NODE_MEAN:
@@ -1570,6 +1600,8 @@ shp_status_t launch_run(const Planner & pl, const Launch & l, shp_stream_t st) {
                                           shp_div(l.x, l.b, l.y, st);
         case SHP_RUN_MUL_SUM_ROWS:
             return shp_mul_sum_rows(l.x, l.b, l.y, st);
+        case SHP_RUN_DIAG_MASK_SOFT_MAX:
+            return shp_soft_max_causal(l.x, l.i0, l.f0, l.y, st);
         case SHP_RUN_CONT_IM2COL:
             return shp_im2col(l.w, &l.xv, l.i0, l.i1, l.i2, l.y, st);
         default:

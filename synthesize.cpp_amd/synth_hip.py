@@ -107,6 +107,8 @@ def load(path=None):
         "shp_sum_rows": [_PT, _PT, vp],
         "shp_mean": [_PT, _PT, vp],
         "shp_mul_sum_rows": [_PT, _PT, _PT, vp],
+        "shp_diag_mask_inf": [_PT, i32, _PT, vp],
+        "shp_soft_max_causal": [_PT, i32, f, _PT, vp],
         "shp_sigmoid": [_PT, _PT, vp],
         "shp_elu": [_PT, _PT, vp],
         "shp_gelu_erf": [_PT, _PT, vp],
@@ -572,6 +574,21 @@ def mul_sum_rows(x, w, out=None):
     return _row_sums("mul_sum_rows", x, w, out)
 
 
+def diag_mask_inf(x, n_past, out=None):
+    """ggml_diag_mask_inf(x, n_past); out=x for the inplace form."""
+    out = x.new_empty(x.shape) if out is None else out
+    _check(load().shp_diag_mask_inf(_ref(desc(x)), int(n_past), _ref(desc(out)), _stream()), "diag_mask_inf")
+    return out
+
+
+def soft_max_causal(x, n_past, scale, out=None):
+    """ggml_diag_mask_inf(x, n_past) then ggml_soft_max_ext(., NULL, scale, 0), one launch."""
+    out = x.new_empty(x.shape) if out is None else out
+    _check(load().shp_soft_max_causal(_ref(desc(x)), int(n_past), float(scale), _ref(desc(out)), _stream()),
+           "soft_max_causal")
+    return out
+
+
 def clamp(x, lo, hi, out=None):
     """ggml_clamp(x, lo, hi)."""
     out = x.new_empty(x.shape) if out is None else out
@@ -703,12 +720,12 @@ def cpy(x, out=None):
  NODE_SOFT_MAX, NODE_ROPE, NODE_LEAKY_RELU, NODE_SILU, NODE_EXP, NODE_GLU_SWIGLU, NODE_CONCAT, NODE_SUB, NODE_TANH,
  NODE_SIGMOID, NODE_ELU, NODE_GELU_ERF, NODE_CLAMP, NODE_NORM, NODE_IM2COL, NODE_COL2IM_1D, NODE_PAD,
  NODE_PAD_REFLECT_1D, NODE_REPEAT, NODE_ACC, NODE_RELU, NODE_NEG, NODE_STEP, NODE_SQRT, NODE_SUM_ROWS,
- NODE_MEAN) = range(36)
+ NODE_MEAN, NODE_DIAG_MASK_INF) = range(37)
 NODE_FLAG_OUTPUT = 1
 RUN_KINDS = {-1: "unsupported", 0: "nop", 1: "single", 2: "norm_mul", 3: "norm_mul_rope", 4: "add_norm_mul",
              5: "silu_mul", 6: "add_leaky", 7: "add_scale_leaky", 8: "snake", 9: "snake_guarded", 10: "snake_beta",
              11: "gather_sum", 12: "qk_norm_rope", 13: "qk_norm_rope_kv", 14: "cont_add_leaky",
-             15: "view_binary", 16: "cont_im2col", 17: "mul_sum_rows"}
+             15: "view_binary", 16: "cont_im2col", 17: "mul_sum_rows", 18: "diag_mask_soft_max"}
 
 
 class ShpNode(ctypes.Structure):
@@ -858,6 +875,9 @@ class Graph:
 
     def sqrt(self, x):
         return self._op(NODE_SQRT, self._like(x), [x])
+
+    def diag_mask_inf(self, x, n_past, inplace=False):
+        return self._op(NODE_DIAG_MASK_INF, self._t(x) if inplace else self._like(x), [x], ints={0: n_past})
 
     def sum_rows(self, x):
         t = self._t(x)

@@ -712,3 +712,22 @@ def test_row_sum_nodes_and_the_weighted_sum_run():
     g = S.Graph()
     y = g.sqrt(g.relu(g.neg(g.step(x))))
     assert kinds(g.plan(y)) == ["single"] * 4
+
+
+def test_causal_soft_max_run():
+    """DIAG_MASK_INF then a maskless SOFT_MAX is one launch; not with a mask
+    tensor, a zero scale, or the masked scores read elsewhere."""
+    x = z(4, 16, 16)
+    g = S.Graph()
+    p = g.soft_max_ext(g.diag_mask_inf(x, 0), None, 0.125)
+    assert kinds(g.plan(p)) == ["diag_mask_soft_max"]
+    g = S.Graph()
+    p = g.soft_max_ext(g.diag_mask_inf(x, 0), None, 0.0)
+    assert kinds(g.plan(p)) == ["single", "single"]
+    g = S.Graph()
+    m = g.diag_mask_inf(x, 0)
+    p = g.soft_max_ext(m, None, 0.125)
+    assert kinds(g.plan(p, m)) == ["single", "single"]
+    g = S.Graph()
+    p = g.soft_max_ext(g.diag_mask_inf(x, 0), z(16, 16), 0.125)
+    assert kinds(g.plan(p)) == ["single", "single"]

@@ -884,3 +884,26 @@ def test_sum_rows_and_mean_are_the_rounded_exact_sum():
     assert not np.array_equal(s[:, 0], running)
     assert np.array_equal(m[:, 0], exact.astype(np.float32) / np.float32(300))
     assert not np.array_equal(m[:, 0], (exact / 300).astype(np.float32))
+
+
+# ---------------------------------------------------------------------------
+# ggml_diag_mask_inf (the codec encoder's causal attention)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n_past", [0, 2])
+def test_diag_mask_inf_is_numpy_triu(n_past):
+    """ggml_diag_mask_inf: -inf exactly on numpy's upper triangle above the
+    diagonal shifted by n_past (np.triu with k = n_past + 1), x elsewhere;
+    k = n_past misses. Followed by the softmax, row 0 at n_past 0 is one-hot
+    and every row sums to 1 with zeros where masked."""
+    x = np.random.default_rng(23 + n_past).standard_normal((3, 7, 9)).astype(np.float32)
+    got = R.run(lambda g: g.diag_mask_inf(x, n_past))
+    up = np.triu(np.ones((7, 9), bool), k=n_past + 1)
+    assert np.array_equal(got, np.where(up, np.float32(-np.inf), x))
+    assert not np.array_equal(got, np.where(np.triu(np.ones((7, 9), bool), k=n_past), np.float32(-np.inf), x))
+    g = R.Graph()
+    p = g.soft_max_ext(g.diag_mask_inf(x, n_past), None, 0.25)
+    g.compute()
+    assert (p[:, up] == 0).all() and np.allclose(p.sum(-1), 1, atol=1e-6)
+    if n_past == 0:
+        assert (p[:, 0, 0] == 1).all()
