@@ -34,6 +34,9 @@ input sets whose total exceeds 512 MB (cold cache):
     transposed convolution's col2im_1d scatter into each shape, and Kokoro's
     zero-stuffed spread, frame doubling and a time-axis edge padding, on
     [512,8192], [256,32768] and [128,131072];
+  - the talker's prefill input assembly at configs[4]'s shape: ggml_acc of
+    an 8176-position codec run into the [2048, 8192] text stream, out of
+    place and in ggml's inplace form;
   - the decode step's non-GEMM work per talker layer (28-layer
     graph), without and with the KV-cache write and the attention softmax;
   - the 512-token prefill step of the 0.6B talker (with the BF16
@@ -1183,7 +1186,10 @@ PMC_OPS = [
     ("cont(transpose) [128,131072]", 134217728), ("add bias[1,C] time-major [128,131072]", 134218240),
     ("conv tail: cont(transpose)+bias+residual->leaky, sum [128,131072]", 268435968),
     ("im2col K=3 [128,131072]", 268435456), ("im2col K=3 channel-major view [128,131072]", 268439552),
-    ("im2col K=7 d=3 f16 [128,131072]", 301989888), ("col2im_1d K=4 s=2 [128,131072]", 201326592)]
+    ("im2col K=7 d=3 f16 [128,131072]", 301989888), ("col2im_1d K=4 s=2 [128,131072]", 201326592),
+    ("pad: spread x2 [128,1,65536]", 100663296), ("repeat: frames x2 [128,1,65536]", 100663296),
+    ("pad_ext: time +3/+4 [131072,128]", 134221312),
+    ("acc: codec run +8176@16 into text [2048,8192]", 201195520)]
 
 
 def pmc_large(S, torch):
@@ -1211,6 +1217,9 @@ def pmc_large(S, torch):
     cols3, cols3c = empty(1, 131072, 384), empty(1, 131074, 384)   # im2col columns of tr (ggml [T, C]) and of xt^T
     cols7 = torch.empty((1, 131072, 896), dtype=torch.float16, device="cuda")
     c2i = randn(65536, 512)   # col2im_1d columns: K 4 x 128 channels, 65536 samples in, 131072 out
+    sp_x, sp_y = randn(65536, 1, 128), empty(65536, 2, 128)   # the spread and the frame doubling
+    ed_x, ed_y = randn(128, 131072), empty(128, 131079)        # edge padding +3/+4 along time
+    ac_a, ac_b, ac_y = randn(8192, 2048), randn(8176, 2048), empty(8192, 2048)
     fns = [lambda: S.rms_norm_mul(x2, w2, 1e-6), lambda: S.add_rms_norm_mul(x2, x2b, w2, 1e-6),
            lambda: S.qk_norm_rope(q, k, wq, wk, 1e-6, pos, 128, 1e6), lambda: S.swiglu(gt, up),
            lambda: S.add(x2, x2b), lambda: S.snake(xs, al), lambda: S.snake_beta(xs, la, lb),
@@ -1220,7 +1229,10 @@ def pmc_large(S, torch):
            lambda: S.cpy(xt.t(), out=ty), lambda: S.add(tr, tb, out=ty),
            lambda: S.cont_add_leaky_relu(xt.t(), tb, tr, 0.1, out=ty, sum_out=ts),
            lambda: S.im2col(tr, 3, 1, 1, 1, out=cols3), lambda: S.im2col(xt.t(), 3, 1, 2, 1, out=cols3c),
-           lambda: S.im2col(tr, 7, 1, 9, 3, out=cols7), lambda: S.col2im_1d(c2i, 2, 128, 1, out=ty)]
+           lambda: S.im2col(tr, 7, 1, 9, 3, out=cols7), lambda: S.col2im_1d(c2i, 2, 128, 1, out=ty),
+           lambda: S.pad_ext(sp_x, [0, 0], [0, 1], out=sp_y), lambda: S.repeat(sp_x, (65536, 2, 128), out=sp_y),
+           lambda: S.pad_ext(ed_x, [3], [4], out=ed_y),
+           lambda: S.acc(ac_a, ac_b, 8192, 8192 * 8192, 8192 * 8192, 16 * 8192, out=ac_y)]
     n = CALIB_BYTES // 4
     src = torch.randn(n, device="cuda")
     dst = torch.empty_like(src)
