@@ -629,8 +629,17 @@ def link_floors(rows, floors):
     for row in rows:
         op, cfg = row["op"], row["config"]
         m = re.search(r"\[(\d+),(\d+)\]$", op)
-        if cfg in ("configs[3]", "configs[4]") and m and not op.startswith(("swiglu", "add [", "qk_")):
-            f = floors.get("copy [%s,%s]" % m.groups())
+        m3 = re.search(r"\[(\d+),1,(\d+)\]$", op)
+        if cfg == "configs[3]" and m3 and op.startswith(("pad: spread", "repeat: frames")):
+            # [C, 1, L] spread or doubled into [C, k, L]: the copy of the output's shape
+            k = int(re.search(r"x(\d+)", op).group(1))
+            f = floors.get("copy [%s,%d]" % (m3.group(1), k * int(m3.group(2))))
+            if f is not None:
+                row["floor"] = f["op"]
+                row["of_floor"] = round(row["GB/s"] / f["GB/s"], 4)
+        elif cfg in ("configs[3]", "configs[4]") and m and not op.startswith(("swiglu", "add [", "qk_")):
+            # ggml [T, C] names (the time-axis padding) take the copy of [C, T]
+            f = floors.get("copy [%s,%s]" % m.groups()) or floors.get("copy [%s,%s]" % m.groups()[::-1])
             if f is not None:
                 row["floor"] = f["op"]
                 row["of_floor"] = round(row["GB/s"] / f["GB/s"], 4)
