@@ -405,7 +405,9 @@ template <int K, int BLOCK, int R = SnakeRows<K>::R> __global__ __launch_bounds_
 // against 2-row tasks over 1024 persistent blocks. CF on the 8-row form is
 // 11 % slower at the two larger shapes. Rejected at [128,131072]: 2048
 // persistent blocks, 512- or 1024-thread blocks, 2-, 4- or 16-row tasks,
-// each lane keeping its quad's curves in registers for all its tasks. For
+// each lane keeping its quad's curves in registers for all its tasks, and a
+// table sized to 128 channels (4 KB of LDS instead of 18 KB, more blocks per
+// CU: 25.6 against 24.9 us at [128,131072]). For
 // plain Snake, whose per-channel work is only the reciprocal, a table does
 // not pay.
 constexpr int     kSnakeLdsMaxC       = 1024;
