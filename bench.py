@@ -37,6 +37,8 @@ input sets whose total exceeds 512 MB (cold cache):
   - the talker's prefill input assembly at configs[4]'s shape: ggml_acc of
     an 8176-position codec run into the [2048, 8192] text stream, out of
     place and in ggml's inplace form;
+  - Kokoro's inverse short-time transform of a 5-second utterance (n_fft 20,
+    hop 5, 24 kHz), which the reference runs on the host after the graph;
   - the decode step's non-GEMM work per talker layer (28-layer
     graph), without and with the KV-cache write and the attention softmax;
   - the 512-token prefill step of the 0.6B talker (with the BF16
@@ -583,6 +585,21 @@ def talker_input_rows(R, S, torch, cfg, seed, T=8192, H=2048, at=16):
     R.run(cfg, "acc inplace: codec run +%d@%d [%d,%d]" % (T - at, at, H, T), 12 * m, make(True))
 
 
+def istft_rows(R, S, torch, cfg, seed, seconds=5, rate=24000, n_fft=20, hop=5):
+    """Kokoro's inverse short-time transform (kokoro/decoder-host.cpp:28-100) of
+    a `seconds`-long utterance at Kokoro's n_fft 20 / hop 5: the generator's
+    spectrum (n_fft + 2 values per frame) read, the waveform written."""
+    g, randn, empty, bf16 = gen(torch, seed)
+    frames = seconds * rate // hop + 1
+
+    def make():
+        spec = torch.rand((frames, n_fft + 2), generator=g, device="cuda") * 5 - 3
+        y = empty((frames - 1) * hop)
+        return lambda: S.inverse_stft(spec, n_fft, hop, out=y)
+    R.run(cfg, "inverse_stft n_fft %d hop %d, %d s at %d Hz" % (n_fft, hop, seconds, rate),
+          4 * frames * (n_fft + 2) + 4 * (frames - 1) * hop, make)
+
+
 def floor_rows(R, S, torch, seed=SEED + 8):
     """Same-run floors the op rows are read against, each timed as the op rows
     are (cold rotating sets, HIP graph, median of chunks):
@@ -881,6 +898,9 @@ def cpu_op_builders(seed=SEED + 9):
                 lambda g: R.add_rms_norm_w(g, take(T, H), take(T, H), bf16(H), eps, R.BF16)))
     out.append((cfg, "swiglu [%d,%d]" % (F_, T), 3 * T * F_ * f32, lambda g: R.swiglu(g, take(T, F_), take(T, F_))))
     out.append((cfg, "add [%d,%d]" % (H, T), 3 * T * H * f32, lambda g: g.add(take(T, H), take(T, H))))
+    fr = 5 * 24000 // 5 + 1
+    out.append(("configs[3]", "inverse_stft n_fft 20 hop 5, 5 s at 24000 Hz", 4 * fr * 22 + 4 * (fr - 1) * 5,
+                lambda g: g.inverse_stft(rng.uniform(-3, 2, (fr, 22)).astype(np.float32), 20, 5)))
     at = 16
     out.append((cfg, "acc: codec run +%d@%d into text [%d,%d]" % (T - at, at, H, T), 4 * (2 * T * H + (T - at) * H),
                 lambda g: g.acc(take(T, H), take(T - at, H), 4 * H, 4 * H * T, 4 * H * T, at * 4 * H)))
@@ -1465,6 +1485,7 @@ def main():
     q8_rows(R, S, torch, "configs[2]", SEED + 6, kind="q5_k")
     vocoder_rows(R, S, torch, "configs[3]", SEED + 4)
     talker_input_rows(R, S, torch, "configs[4]", SEED + 7)
+    istft_rows(R, S, torch, "configs[3]", SEED + 11)
     floors = floor_rows(R, S, torch)
     link_floors(list(ops4.values()) + R.rows, floors)
 

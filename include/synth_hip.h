@@ -386,6 +386,23 @@ shp_status_t shp_mean(const shp_tensor * x, shp_tensor * y, shp_stream_t stream)
 shp_status_t shp_mul_sum_rows(const shp_tensor * x, const shp_tensor * w, shp_tensor * y, shp_stream_t stream);
 
 /*
+ * Kokoro's inverse short-time transform (kokoro/decoder-host.cpp:28-100,
+ * inverse_stft; run by the host at kokoro/model.cpp:1056 on the generator's
+ * output): spectrum F32 [n_fft + 2, frames] -- per frame n_fft/2 + 1
+ * log-magnitudes, then as many raw phases (the phase is their sine) -- into
+ * audio F32 [(frames - 1) * hop]: per frame the real inverse DFT of
+ * exp(log-magnitude) * e^(i sin(phase)), weighted by the periodic Hann window
+ * (rounded to f32) and overlap-added at hop, divided by the overlap-added
+ * squared window (0 where that is below 1e-11), trimmed by n_fft/2; in
+ * double, rounded to f32 once. n_fft even >= 2, hop >= 1, frames >= 2;
+ * frames may sit at any row stride. SHP_ERR_UNSUPPORTED when a block's frames
+ * do not fit the kernel's LDS (n_fft/2 + 1 complex bins per frame; Kokoro's
+ * n_fft 20, hop 5 use 37 KB).
+ */
+shp_status_t shp_inverse_stft(const shp_tensor * spectrum, int32_t n_fft, int32_t hop, shp_tensor * audio,
+                              shp_stream_t stream);
+
+/*
  * ggml_concat(a, b, dim): y of a's shape except y->ne[dim] = a->ne[dim] +
  * b->ne[dim]; y(i) = a(i) where i[dim] < a->ne[dim], else b(i) with
  * i[dim] - a->ne[dim]. All F32, rows contiguous (any row strides). The code

@@ -725,6 +725,77 @@ static void op_pad_family(const orc_node * n, int ith, int nth) {
     }
 }
 
+/* Kokoro's inverse short-time transform (kokoro/decoder-host.cpp:28-100,
+ * called at kokoro/model.cpp:1056 on the generator's output), restated as the
+ * host code computes it, in double: a periodic Hann window rounded to f32;
+ * per frame, the bins' complex values exp(log-magnitude) * e^(i sin(raw
+ * phase)), and each of the frame's n_fft samples as the real inverse DFT (bin
+ * 0 and the Nyquist bin once, the others twice, over n_fft), in bin order;
+ * overlap-add of sample * window and of window^2 in frame order; output
+ * sample t = the sums at t + n_fft/2, their quotient rounded to f32, or 0
+ * where the window sum is below 1e-11. Serial, as the host code is. */
+static void op_istft(const orc_node * n, int ith, int nth) {
+    (void) nth;
+    if (ith != 0) {
+        return;
+    }
+    const double   pi     = 3.14159265358979323846;
+    const int64_t  frames = n->nrows;
+    const int64_t  nfft   = n->i[0];
+    const int64_t  hop    = n->i[1];
+    const int64_t  bins   = nfft / 2 + 1;
+    if (frames < 2 || nfft < 2 || nfft % 2 != 0 || hop <= 0 || n->ne0 != nfft + 2) {
+        atomic_store(&g_node_error, -2);
+        return;
+    }
+    const int64_t total = nfft + hop * (frames - 1);
+    const int64_t kept  = (frames - 1) * hop;
+    float *       win   = (float *) malloc((size_t) nfft * sizeof(float));
+    double *      acc   = (double *) calloc((size_t) total, sizeof(double));
+    double *      env   = (double *) calloc((size_t) total, sizeof(double));
+    double *      frame = (double *) malloc((size_t) nfft * sizeof(double));
+    if (win == NULL || acc == NULL || env == NULL || frame == NULL) {
+        atomic_store(&g_node_error, -3);
+        free(win);
+        free(acc);
+        free(env);
+        free(frame);
+        return;
+    }
+    for (int64_t k = 0; k < nfft; ++k) {
+        win[k] = (float) (0.5 * (1.0 - cos(2.0 * pi * (double) k / (double) nfft)));
+    }
+    for (int64_t f = 0; f < frames; ++f) {
+        const float * row = (const float *) n->src0 + f * n->ne0;
+        for (int64_t s = 0; s < nfft; ++s) {
+            double value = 0.0;
+            for (int64_t b = 0; b < bins; ++b) {
+                const double mag    = exp((double) row[b]);
+                const double angle  = sin((double) row[bins + b]);
+                const double turn   = 2.0 * pi * (double) b * (double) s / (double) nfft;
+                const double re     = mag * cos(angle);
+                const double im     = mag * sin(angle);
+                const double weight = (b == 0 || b == bins - 1) ? 1.0 : 2.0;
+                value += weight * (re * cos(turn) - im * sin(turn));
+            }
+            frame[s] = value / (double) nfft;
+        }
+        for (int64_t s = 0; s < nfft; ++s) {
+            acc[f * hop + s] += frame[s] * (double) win[s];
+            env[f * hop + s] += (double) win[s] * (double) win[s];
+        }
+    }
+    float * y = (float *) n->dst;
+    for (int64_t t = 0; t < kept; ++t) {
+        const double d = env[t + nfft / 2];
+        y[t]           = fabs(d) < (double) 1e-11f ? 0.0f : (float) (acc[t + nfft / 2] / d);
+    }
+    free(win);
+    free(acc);
+    free(env);
+    free(frame);
+}
+
 /* ggml_diag_mask_inf(x, n_past) (qwen3-tts/codec-encoder.cpp:482): x copied,
  * then in row j of every matrix each element i >= n_past with i > n_past + j
  * set to -inf, as ggml-CPU's forward_diag_mask writes them. */
@@ -950,6 +1021,9 @@ static void run_node(const orc_node * n, int ith, int nth) {
             break;
         case ORC_OP_DIAG_MASK_INF:
             op_diag_mask_inf(n, ith, nth);
+            break;
+        case ORC_OP_ISTFT:
+            op_istft(n, ith, nth);
             break;
         default:
             atomic_store(&g_node_error, -1);

@@ -65,6 +65,7 @@ enum orc_op {
     ORC_OP_SUM_ROWS,     /* dst[r] = (float) double sum of row r    ggml_sum_rows       */
     ORC_OP_MEAN,         /* dst[r] = sum_rows / (float) ne0         ggml_mean           */
     ORC_OP_DIAG_MASK_INF, /* -inf past n_past + row, else x         ggml_diag_mask_inf  */
+    ORC_OP_ISTFT,        /* Kokoro's inverse STFT (host code)      kokoro inverse_stft */
 };
 
 /*
@@ -107,6 +108,9 @@ enum orc_op {
  *               dst contiguous F32.
  *   SUM_ROWS, MEAN : src0 nrows rows of ne0; dst one value per row.
  *   DIAG_MASK_INF : src0 nrows rows of ne0, ne1 rows per matrix; i[0] = n_past.
+ *   ISTFT     : src0 = the generator's spectrum, nrows frames of ne0 = n_fft + 2
+ *               values (n_fft/2 + 1 log-magnitudes, then as many raw phases);
+ *               i[0] = n_fft, i[1] = hop; dst (nrows - 1) * hop samples.
  *   ACC       : src0 = a, contiguous F32 of nrows*ne0 elements; src1 =
  *               int64_t[9]: b's ne[0..3], the view's byte strides nb1, nb2,
  *               nb3, its byte offset, then the b data pointer (contiguous F32);

@@ -26,7 +26,8 @@ F32, F16, Q8_0, Q5_K, I32, BF16 = 0, 1, 8, 13, 26, 30
 (OP_ADD, OP_MUL, OP_DIV, OP_RMS_NORM, OP_ROPE_NEOX, OP_SILU, OP_SIN, OP_SQR, OP_EXP, OP_LEAKY_RELU, OP_SCALE_BIAS,
  OP_GET_ROWS, OP_CAST_F32, OP_GLU_SWIGLU, OP_SOFT_MAX, OP_CONT_F32, OP_BINBCAST, OP_SUB, OP_TANH, OP_SIGMOID,
  OP_ELU, OP_GELU_ERF, OP_CLAMP, OP_NORM, OP_IM2COL, OP_COL2IM_1D, OP_PAD, OP_PAD_REFLECT_1D,
- OP_REPEAT, OP_ACC, OP_RELU, OP_NEG, OP_STEP, OP_SQRT, OP_SUM_ROWS, OP_MEAN, OP_DIAG_MASK_INF) = range(1, 38)
+ OP_REPEAT, OP_ACC, OP_RELU, OP_NEG, OP_STEP, OP_SQRT, OP_SUM_ROWS, OP_MEAN, OP_DIAG_MASK_INF,
+ OP_ISTFT) = range(1, 39)
 
 
 class OrcNode(ctypes.Structure):
@@ -182,6 +183,15 @@ class Graph:
         x = self._f32(x)
         return self._node(OP_DIAG_MASK_INF, np.empty_like(x), x, ne1=x.shape[-2] if x.ndim > 1 else 1,
                           i=(int(n_past),))
+
+    def inverse_stft(self, spectrum, n_fft, hop):
+        """Kokoro's inverse_stft: spectrum (frames, n_fft + 2) -> ((frames - 1) * hop,)."""
+        x = self._f32(spectrum)
+        frames = x.shape[0]
+        if x.ndim != 2 or x.shape[1] != n_fft + 2 or frames < 2 or n_fft < 2 or n_fft % 2 or hop <= 0:
+            raise ValueError("inverse_stft: bad spectrum or parameters")
+        return self._node(OP_ISTFT, np.empty((frames - 1) * hop, np.float32), x, ne0=n_fft + 2, nrows=frames,
+                          i=(int(n_fft), int(hop)))
 
     def sum_rows(self, x):
         """ggml_sum_rows: (..., ne0) -> (..., 1)."""

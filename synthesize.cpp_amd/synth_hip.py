@@ -109,6 +109,7 @@ def load(path=None):
         "shp_mul_sum_rows": [_PT, _PT, _PT, vp],
         "shp_diag_mask_inf": [_PT, i32, _PT, vp],
         "shp_soft_max_causal": [_PT, i32, f, _PT, vp],
+        "shp_inverse_stft": [_PT, i32, i32, _PT, vp],
         "shp_sigmoid": [_PT, _PT, vp],
         "shp_elu": [_PT, _PT, vp],
         "shp_gelu_erf": [_PT, _PT, vp],
@@ -586,6 +587,16 @@ def soft_max_causal(x, n_past, scale, out=None):
     out = x.new_empty(x.shape) if out is None else out
     _check(load().shp_soft_max_causal(_ref(desc(x)), int(n_past), float(scale), _ref(desc(out)), _stream()),
            "soft_max_causal")
+    return out
+
+
+def inverse_stft(spectrum, n_fft, hop, out=None):
+    """Kokoro's inverse_stft: spectrum (frames, n_fft + 2) -> ((frames - 1) * hop,)."""
+    import torch
+    frames = spectrum.shape[0]
+    out = torch.empty(((frames - 1) * hop,), dtype=torch.float32, device=spectrum.device) if out is None else out
+    _check(load().shp_inverse_stft(_ref(desc(spectrum)), int(n_fft), int(hop), _ref(desc(out)), _stream()),
+           "inverse_stft")
     return out
 
 

@@ -15,6 +15,8 @@ Sources:
      kExpectedDepthwise, kExpectedTransposed, kExpectedConvNeXt, fill order)
   G6 tests/vits_transpose_conv_test.cpp:237-265 (the transposed convolution's
      known answers and the multichannel cases' shapes and fill rule)
+  G7 tests/kokoro_istft_test.cpp:15-62 (Kokoro's inverse short-time transform
+     against torch.istft: the raw spectrum, n_fft, hop, frames, the audio)
 """
 import json
 import os
@@ -179,8 +181,18 @@ def main():
         "multichannel": multi, "kernel_fill": [7, 1], "input_fill": [5, 1],
     }
 
+    t = read("tests/kokoro_istft_test.cpp")
+    g7 = {
+        "source": "tests/kokoro_istft_test.cpp:15-62",
+        # frames rows of n_fft + 2 values (n_fft/2 + 1 log-magnitudes, then the raw
+        # phases), frame-major; audio (frames - 1) * hop samples; the test's bound
+        "n_fft": constant(t, "kNfft"), "hop": constant(t, "kHop"), "frames": constant(t, "kFrames"),
+        "spectrum": literal_array(t, "kSpectrum"), "expected_audio": literal_array(t, "kExpectedAudio"),
+        "tolerance": 1e-5,
+    }
+
     for name, obj in (("qwen3_decoder_layer", g1), ("qwen3_code_predictor", g2), ("qwen3_codec_snake_beta", g3),
-                      ("qwen3_codec_convs", g5), ("vits_transpose_conv", g6)):
+                      ("qwen3_codec_convs", g5), ("vits_transpose_conv", g6), ("kokoro_istft", g7)):
         with open(os.path.join(HERE, name + ".json"), "w") as f:
             json.dump(obj, f, indent=1)
             f.write("\n")

@@ -442,3 +442,70 @@ def test_col2im_refuses_empty_outputs():
     with pytest.raises(ValueError):
         R.Graph().col2im_1d(np.zeros((1, 4 * 3), np.float32), 2, 3, 2)
     assert R.run(lambda g: g.col2im_1d(np.ones((1, 4 * 3), np.float32), 2, 3, 1)).shape == (3, 2)
+
+
+# ---------------------------------------------------------------------------
+# G7: Kokoro's inverse short-time transform (tests/kokoro_istft_test.cpp)
+# ---------------------------------------------------------------------------
+
+def istft_numpy(spec, n_fft, hop, *, phase=np.sin, weights_nyquist=1.0, normalise=True, offset=None):
+    """An independent restatement through numpy's FFT: each frame is numpy's
+    irfft of exp(log-magnitude) * e^(i phase(raw)) (irfft takes bin 0 and the
+    Nyquist bin once and the rest twice, over n_fft), overlap-added with the
+    periodic Hann window rounded to f32 and divided by the overlap-added
+    squared window, trimmed by n_fft/2 at the front (torch.istft's centred
+    form). The keyword arguments plant the mistakes a restatement could make."""
+    frames = spec.shape[0]
+    bins = n_fft // 2 + 1
+    mag = np.exp(spec[:, :bins].astype(np.float64))
+    ph = phase(spec[:, bins:].astype(np.float64))
+    X = mag * np.exp(1j * ph)
+    if weights_nyquist != 1.0:
+        X[:, -1] *= weights_nyquist
+    fr = np.fft.irfft(X, n=n_fft, axis=1)
+    win = (0.5 * (1.0 - np.cos(2.0 * np.pi * np.arange(n_fft) / n_fft))).astype(np.float32).astype(np.float64)
+    total = n_fft + hop * (frames - 1)
+    acc, env = np.zeros(total), np.zeros(total)
+    for f in range(frames):
+        acc[f * hop:f * hop + n_fft] += fr[f] * win
+        env[f * hop:f * hop + n_fft] += win * win
+    off = n_fft // 2 if offset is None else offset
+    kept = (frames - 1) * hop
+    a, e = acc[off:off + kept], env[off:off + kept]
+    out = np.where(np.abs(e) < np.float32(1e-11), 0.0, a / np.where(e == 0, 1, e) if normalise else a)
+    return out.astype(np.float32)
+
+
+def test_golden_kokoro_istft():
+    """G7: the restatement against tests/kokoro_istft_test.cpp's torch.istft
+    vector at the test's 1e-5; numpy's irfft restatement agrees with it to
+    within an f32 ulp; the phase taken raw instead of through sin, the
+    Nyquist bin counted twice, the window sum left undivided and the trim at
+    0 instead of n_fft/2 each miss the vector by more than 1e-3."""
+    d = _load("kokoro_istft.json")
+    n, hop, frames = d["n_fft"], d["hop"], d["frames"]
+    spec = np.array(d["spectrum"], np.float32).reshape(frames, n + 2)
+    exp = np.array(d["expected_audio"], np.float32)
+    got = R.run(lambda g: g.inverse_stft(spec, n, hop))
+    assert got.shape == exp.shape and np.abs(got - exp).max() < d["tolerance"]
+    ref = istft_numpy(spec, n, hop)
+    assert np.abs(got - ref).max() <= 2 * np.spacing(np.abs(exp).max())
+    for bad in (dict(phase=lambda p: p), dict(weights_nyquist=2.0), dict(normalise=False), dict(offset=0)):
+        assert np.abs(istft_numpy(spec, n, hop, **bad) - exp).max() > 1e-3, bad
+
+
+@pytest.mark.parametrize("n_fft,hop,frames", [(20, 5, 400), (16, 4, 33), (8, 3, 20), (6, 8, 10), (64, 16, 50)])
+def test_istft_against_numpy_irfft(n_fft, hop, frames):
+    """The direct double DFT of the restatement against numpy's irfft path on
+    random spectra, Kokoro's n_fft 20 / hop 5 among them, and hops that do
+    not divide n_fft or leave gaps (a window sum of 0 gives 0): within an f32
+    ulp of the output's scale, > 99 % identical."""
+    rng = np.random.default_rng(n_fft * 100 + hop)
+    spec = rng.uniform(-2, 2, (frames, n_fft + 2)).astype(np.float32)
+    got = R.run(lambda g: g.inverse_stft(spec, n_fft, hop))
+    ref = istft_numpy(spec, n_fft, hop)
+    assert got.shape == ((frames - 1) * hop,)
+    assert np.abs(got - ref).max() <= 2 * np.spacing(np.abs(ref).max())
+    assert (got == ref).mean() > 0.99
+    with pytest.raises(ValueError):
+        R.Graph().inverse_stft(spec, n_fft + 1, hop)
