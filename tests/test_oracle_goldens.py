@@ -509,3 +509,41 @@ def test_istft_against_numpy_irfft(n_fft, hop, frames):
     assert (got == ref).mean() > 0.99
     with pytest.raises(ValueError):
         R.Graph().inverse_stft(spec, n_fft + 1, hop)
+
+
+def _ref_istft_lib():
+    """oracle/_ref's build of the reference's own inverse_stft, or None."""
+    import ctypes
+    path = os.path.join(R.HERE, "_ref", "libkokoro_istft_ref.so")
+    if not os.path.exists(path):
+        return None
+    L = ctypes.CDLL(path)
+    L.ref_inverse_stft.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
+                                   ctypes.c_void_p, ctypes.c_uint64]
+    L.ref_inverse_stft.restype = ctypes.c_int
+    return L
+
+
+@pytest.mark.parametrize("n_fft,hop,frames", [(8, 2, 9), (20, 5, 2401), (16, 4, 33), (8, 3, 20), (6, 8, 10),
+                                              (64, 16, 50)])
+def test_istft_restatement_is_the_reference_build(n_fft, hop, frames):
+    """The restatement against the reference's own inverse_stft compiled from
+    the checkout (oracle/_ref, `make -C oracle ref`): bit for bit on G7's
+    spectrum and on random spectra (both double code in the same order over
+    glibc's exp/sin/cos); the reference's refusals (odd window, no hop, a
+    spectrum of the wrong size) returned as errors. Skipped where the
+    reference checkout was not there to build it."""
+    L = _ref_istft_lib()
+    if L is None:
+        pytest.skip("oracle/_ref not built (no reference checkout)")
+    if (n_fft, hop, frames) == (8, 2, 9):
+        spec = np.array(_load("kokoro_istft.json")["spectrum"], np.float32).reshape(frames, n_fft + 2)
+    else:
+        spec = np.random.default_rng(n_fft * 7 + hop).uniform(-3, 2, (frames, n_fft + 2)).astype(np.float32)
+    out = np.empty((frames - 1) * hop, np.float32)
+    assert L.ref_inverse_stft(spec.ctypes.data, frames, n_fft, hop, out.ctypes.data, out.size) == 0
+    got = R.run(lambda g: g.inverse_stft(spec, n_fft, hop))
+    assert np.array_equal(got.view(np.uint32), out.view(np.uint32))
+    if (n_fft, hop, frames) == (8, 2, 9):
+        assert L.ref_inverse_stft(spec.ctypes.data, frames, 7, hop, out.ctypes.data, out.size) != 0
+        assert L.ref_inverse_stft(spec.ctypes.data, frames, n_fft, 0, out.ctypes.data, out.size) != 0
