@@ -37,8 +37,9 @@ input sets whose total exceeds 512 MB (cold cache):
   - the talker's prefill input assembly at configs[4]'s shape: ggml_acc of
     an 8176-position codec run into the [2048, 8192] text stream, out of
     place and in ggml's inplace form;
-  - Kokoro's inverse short-time transform of a 5-second utterance (n_fft 20,
-    hop 5, 24 kHz), which the reference runs on the host after the graph;
+  - Kokoro's harmonic source and its spectrum, and the inverse short-time
+    transform, of a 5-second utterance (9 harmonics, upsampling 300, n_fft 20,
+    hop 5, 24 kHz): host code in the reference, between and after its graphs;
   - the decode step's non-GEMM work per talker layer (28-layer
     graph), without and with the KV-cache write and the attention softmax;
   - the 512-token prefill step of the 0.6B talker (with the BF16
@@ -600,6 +601,25 @@ def istft_rows(R, S, torch, cfg, seed, seconds=5, rate=24000, n_fft=20, hop=5):
           4 * frames * (n_fft + 2) + 4 * (frames - 1) * hop, make)
 
 
+def source_rows(R, S, torch, cfg, seed, seconds=5, rate=24000, H=9, scale=300, n_fft=20, hop=5):
+    """Kokoro's harmonic source and its spectrum (kokoro/source.cpp:60-184) for
+    a `seconds`-long utterance at Kokoro's dimensions: f0 and the noise draws
+    read, the excitation and the spectrum written."""
+    g, randn, empty, bf16 = gen(torch, seed)
+    L = seconds * rate // scale
+    U, frames = L * scale, L * scale // hop + 1
+
+    def make():
+        f0 = torch.rand((L,), generator=g, device="cuda") * 300 + 60
+        mw, ri = randn(H) * 0.5, torch.rand((H,), generator=g, device="cuda")
+        noise = randn(U, H)
+        out = (empty(U), empty(frames, n_fft + 2))
+        return lambda: S.harmonic_source(f0, mw, 0.1, ri, noise, rate=rate, scale=scale, sine_amp=0.1,
+                                         noise_std=0.003, voiced_threshold=10.0, n_fft=n_fft, hop=hop, out=out)
+    R.run(cfg, "harmonic_source %d harmonics, %d s at %d Hz" % (H, seconds, rate),
+          4 * (L + U * H + U + frames * (n_fft + 2)), make)
+
+
 def floor_rows(R, S, torch, seed=SEED + 8):
     """Same-run floors the op rows are read against, each timed as the op rows
     are (cold rotating sets, HIP graph, median of chunks):
@@ -898,6 +918,15 @@ def cpu_op_builders(seed=SEED + 9):
                 lambda g: R.add_rms_norm_w(g, take(T, H), take(T, H), bf16(H), eps, R.BF16)))
     out.append((cfg, "swiglu [%d,%d]" % (F_, T), 3 * T * F_ * f32, lambda g: R.swiglu(g, take(T, F_), take(T, F_))))
     out.append((cfg, "add [%d,%d]" % (H, T), 3 * T * H * f32, lambda g: g.add(take(T, H), take(T, H))))
+    Ls, Us = 5 * 24000 // 300, 5 * 24000
+    out.append(("configs[3]", "harmonic_source 9 harmonics, 5 s at 24000 Hz",
+                4 * (Ls + Us * 9 + Us + (Us // 5 + 1) * 22),
+                lambda g: g.harmonic_source(rng.uniform(60, 360, Ls).astype(np.float32),
+                                            rng.normal(0, 0.5, 9).astype(np.float32), np.float32(0.1),
+                                            rng.uniform(0, 1, 9).astype(np.float32),
+                                            rng.standard_normal((Us, 9)).astype(np.float32), rate=24000, scale=300,
+                                            sine_amp=np.float32(0.1), noise_std=np.float32(0.003),
+                                            voiced_threshold=np.float32(10.0), n_fft=20, hop=5)))
     fr = 5 * 24000 // 5 + 1
     out.append(("configs[3]", "inverse_stft n_fft 20 hop 5, 5 s at 24000 Hz", 4 * fr * 22 + 4 * (fr - 1) * 5,
                 lambda g: g.inverse_stft(rng.uniform(-3, 2, (fr, 22)).astype(np.float32), 20, 5)))
@@ -1486,6 +1515,7 @@ def main():
     vocoder_rows(R, S, torch, "configs[3]", SEED + 4)
     talker_input_rows(R, S, torch, "configs[4]", SEED + 7)
     istft_rows(R, S, torch, "configs[3]", SEED + 11)
+    source_rows(R, S, torch, "configs[3]", SEED + 12)
     floors = floor_rows(R, S, torch)
     link_floors(list(ops4.values()) + R.rows, floors)
 

@@ -403,6 +403,31 @@ shp_status_t shp_inverse_stft(const shp_tensor * spectrum, int32_t n_fft, int32_
                               shp_stream_t stream);
 
 /*
+ * Kokoro's harmonic-plus-noise source and its short-time spectrum
+ * (kokoro/source.cpp:60-184, build_harmonic_source; run by the host between
+ * the prosody and generator graphs): f0 F32 [L] (the prosody curve),
+ * merge_weight and rand_ini F32 [H] (the 9-to-1 merge and the initial phases),
+ * noise F32 [H, L*upsample_scale] (the additive draws, frame-major) into
+ * excitation F32 [L*upsample_scale] (tanh of the merged harmonics) and har F32
+ * [n_fft + 2, frames] (frames = L*upsample_scale/hop + 1; per frame n_fft/2 + 1
+ * magnitudes, then as many phases): the phase increments accumulated on the
+ * f0 grid in f32 in frame order (bit for bit the host code's sums), resampled
+ * with PyTorch's align_corners=false mapping, sin(phase) * sine_amp for voiced
+ * samples (f0 > voiced_threshold) plus the noise at noise_std (unvoiced:
+ * sine_amp/3), merged in harmonic order from merge_bias; then torch.stft's
+ * centred, reflect-padded framing with the periodic Hann window, the DFT in
+ * double, hypot and atan2. The sine and tanh are the device's f32 ones (an ulp
+ * or two from the host library's). All contiguous; H <= 64, n_fft even in
+ * 2..64, at least two samples; har's memory stages the L*H coarse phases
+ * between the launches (SHP_ERR_UNSUPPORTED when it is smaller).
+ */
+shp_status_t shp_harmonic_source(const shp_tensor * f0, const shp_tensor * merge_weight, float merge_bias,
+                                 const shp_tensor * rand_ini, const shp_tensor * noise, int32_t sampling_rate,
+                                 int32_t upsample_scale, float sine_amp, float noise_std, float voiced_threshold,
+                                 int32_t n_fft, int32_t hop, shp_tensor * excitation, shp_tensor * har,
+                                 shp_stream_t stream);
+
+/*
  * ggml_concat(a, b, dim): y of a's shape except y->ne[dim] = a->ne[dim] +
  * b->ne[dim]; y(i) = a(i) where i[dim] < a->ne[dim], else b(i) with
  * i[dim] - a->ne[dim]. All F32, rows contiguous (any row strides). The code

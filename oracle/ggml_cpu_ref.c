@@ -725,6 +725,144 @@ static void op_pad_family(const orc_node * n, int ith, int nth) {
     }
 }
 
+/* Kokoro's harmonic-plus-noise source and its short-time spectrum
+ * (kokoro/source.cpp:60-184, build_harmonic_source), restated step by step:
+ * f0 repeated `scale` times; per sample and harmonic h the phase increment
+ * frac(f0 * (h+1) / rate) in f32, the random initial phase added on sample 0;
+ * the increments resampled linearly to the f0 grid (PyTorch's
+ * align_corners=false: position (o + 0.5) * in/out - 0.5 in double, clamped
+ * at 0, the weight rounded to f32, a*(1-w) + b*w); a running f32 sum per
+ * harmonic in frame order, scaled by 2*pi*scale in double and rounded; that
+ * phase resampled back to the sample grid; per sample the voiced flag (f0 >
+ * threshold), sin(phase) * amp * uv + gain * noise merged with the weights in
+ * harmonic order from the bias, tanh; then torch.stft's centred framing:
+ * reflect padding by n_fft/2, the periodic Hann window rounded to f32, the
+ * DFT in double, magnitude by hypot and phase by atan2, each rounded to f32. */
+static void resample_linear_f32(const float * in, int64_t in_len, int64_t out_len, int64_t ch, float * out) {
+    const double ratio = (double) in_len / (double) out_len;
+    for (int64_t o = 0; o < out_len; ++o) {
+        double position = ((double) o + 0.5) * ratio - 0.5;
+        if (position < 0.0) {
+            position = 0.0;
+        }
+        const int64_t low  = (int64_t) position;
+        const int64_t high = low + 1 < in_len ? low + 1 : in_len - 1;
+        const float   w    = (float) (position - (double) low);
+        for (int64_t c = 0; c < ch; ++c) {
+            const float a  = in[low * ch + c];
+            const float b  = in[high * ch + c];
+            out[o * ch + c] = a * (1.0f - w) + b * w;
+        }
+    }
+}
+
+static void op_harmonic_source(const orc_node * n, int ith, int nth) {
+    (void) nth;
+    if (ith != 0) {
+        return;
+    }
+    const orc_source_args * a  = (const orc_source_args *) n->src1;
+    const double            pi = 3.14159265358979323846;
+    const int64_t           L  = n->nrows;
+    const int64_t           H  = a->harmonics, S = a->scale, N = a->n_fft, hop = a->hop;
+    if (L < 1 || H < 1 || S < 1 || N < 2 || hop < 1 || a->sampling_rate < 1) {
+        atomic_store(&g_node_error, -2);
+        return;
+    }
+    const int64_t U    = L * S;
+    const float * f0   = (const float *) n->src0;
+    float *       f0u  = (float *) malloc((size_t) U * sizeof(float));
+    float *       rad  = (float *) malloc((size_t) (U * H) * sizeof(float));
+    float *       crs  = (float *) malloc((size_t) (L * H) * sizeof(float));
+    float *       ph   = (float *) malloc((size_t) (L * H) * sizeof(float));
+    float *       fine = (float *) malloc((size_t) (U * H) * sizeof(float));
+    float *       run  = (float *) calloc((size_t) H, sizeof(float));
+    const int64_t half = N / 2, bins = half + 1, frames = U / hop + 1;
+    float *       pad  = (float *) malloc((size_t) (U + 2 * half) * sizeof(float));
+    float *       win  = (float *) malloc((size_t) N * sizeof(float));
+    float *       seg  = (float *) malloc((size_t) N * sizeof(float));
+    if (!f0u || !rad || !crs || !ph || !fine || !run || !pad || !win || !seg) {
+        atomic_store(&g_node_error, -3);
+        goto done;
+    }
+    for (int64_t i = 0; i < L; ++i) {
+        for (int64_t k = 0; k < S; ++k) {
+            f0u[i * S + k] = f0[i];
+        }
+    }
+    {
+        const float rate = (float) a->sampling_rate;
+        for (int64_t u = 0; u < U; ++u) {
+            for (int64_t h = 0; h < H; ++h) {
+                const float v  = f0u[u] * (float) (h + 1) / rate;
+                rad[u * H + h] = v - floorf(v);
+            }
+        }
+    }
+    for (int64_t h = 0; h < H; ++h) {
+        rad[h] += a->rand_ini[h];
+    }
+    resample_linear_f32(rad, U, L, H, crs);
+    for (int64_t j = 0; j < L; ++j) {
+        for (int64_t h = 0; h < H; ++h) {
+            run[h] += crs[j * H + h];
+            ph[j * H + h] = (float) ((double) run[h] * 2.0 * pi * (double) S);
+        }
+    }
+    resample_linear_f32(ph, L, U, H, fine);
+    {
+        float * exc = (float *) n->dst;
+        for (int64_t u = 0; u < U; ++u) {
+            const int   voiced = f0u[u] > a->voiced_threshold;
+            const float uv     = voiced ? 1.0f : 0.0f;
+            const float gain   = uv * a->noise_std + (1.0f - uv) * a->sine_amp / 3.0f;
+            float       merged = a->merge_bias;
+            for (int64_t h = 0; h < H; ++h) {
+                const float sine  = sinf(fine[u * H + h]) * a->sine_amp;
+                const float value = sine * uv + gain * a->noise[u * H + h];
+                merged += a->merge_weight[h] * value;
+            }
+            exc[u] = tanhf(merged);
+        }
+        for (int64_t i = 0; i < U + 2 * half; ++i) {
+            int64_t       src  = i - half;
+            const int64_t last = U - 1;
+            while (src < 0 || src > last) {
+                src = src < 0 ? -src : 2 * last - src;
+            }
+            pad[i] = exc[src];
+        }
+    }
+    for (int64_t k = 0; k < N; ++k) {
+        win[k] = (float) (0.5 * (1.0 - cos(2.0 * pi * (double) k / (double) N)));
+    }
+    for (int64_t f = 0; f < frames; ++f) {
+        for (int64_t k = 0; k < N; ++k) {
+            seg[k] = pad[f * hop + k] * win[k];
+        }
+        for (int64_t b = 0; b < bins; ++b) {
+            double re = 0.0, im = 0.0;
+            for (int64_t k = 0; k < N; ++k) {
+                const double angle = -2.0 * pi * (double) b * (double) k / (double) N;
+                re += (double) seg[k] * cos(angle);
+                im += (double) seg[k] * sin(angle);
+            }
+            a->har[f * 2 * bins + b]        = (float) hypot(re, im);
+            a->har[f * 2 * bins + bins + b] = (float) atan2(im, re);
+        }
+    }
+done:
+    free(f0u);
+    free(rad);
+    free(crs);
+    free(ph);
+    free(fine);
+    free(run);
+    free(pad);
+    free(win);
+    free(seg);
+}
+
 /* Kokoro's inverse short-time transform (kokoro/decoder-host.cpp:28-100,
  * called at kokoro/model.cpp:1056 on the generator's output), restated as the
  * host code computes it, in double: a periodic Hann window rounded to f32;
@@ -1024,6 +1162,9 @@ static void run_node(const orc_node * n, int ith, int nth) {
             break;
         case ORC_OP_ISTFT:
             op_istft(n, ith, nth);
+            break;
+        case ORC_OP_HARMONIC_SOURCE:
+            op_harmonic_source(n, ith, nth);
             break;
         default:
             atomic_store(&g_node_error, -1);

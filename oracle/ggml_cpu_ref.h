@@ -66,6 +66,7 @@ enum orc_op {
     ORC_OP_MEAN,         /* dst[r] = sum_rows / (float) ne0         ggml_mean           */
     ORC_OP_DIAG_MASK_INF, /* -inf past n_past + row, else x         ggml_diag_mask_inf  */
     ORC_OP_ISTFT,        /* Kokoro's inverse STFT (host code)      kokoro inverse_stft */
+    ORC_OP_HARMONIC_SOURCE, /* Kokoro's harmonic source (host code) build_harmonic_source */
 };
 
 /*
@@ -108,6 +109,9 @@ enum orc_op {
  *               dst contiguous F32.
  *   SUM_ROWS, MEAN : src0 nrows rows of ne0; dst one value per row.
  *   DIAG_MASK_INF : src0 nrows rows of ne0, ne1 rows per matrix; i[0] = n_past.
+ *   HARMONIC_SOURCE : src0 = f0 (nrows values); src1 = orc_source_args; dst =
+ *               the excitation (nrows * scale values); the spectrum into
+ *               args->har ((nrows*scale/hop + 1) frames of 2*(n_fft/2 + 1)).
  *   ISTFT     : src0 = the generator's spectrum, nrows frames of ne0 = n_fft + 2
  *               values (n_fft/2 + 1 log-magnitudes, then as many raw phases);
  *               i[0] = n_fft, i[1] = hop; dst (nrows - 1) * hop samples.
@@ -116,6 +120,25 @@ enum orc_op {
  *               nb3, its byte offset, then the b data pointer (contiguous F32);
  *               dst contiguous F32 of a's size.
  */
+/* Kokoro's harmonic source (kokoro/source.cpp): the learned merge, the random
+ * draws and the module's constants. */
+typedef struct orc_source_args {
+    const float * merge_weight;  /* harmonics */
+    const float * rand_ini;      /* harmonics */
+    const float * noise;         /* nrows*scale frames of harmonics */
+    float *       har;           /* out: frames of 2*bins (magnitudes, then phases) */
+    float         merge_bias;
+    float         sine_amp;
+    float         noise_std;
+    float         voiced_threshold;
+    int32_t       sampling_rate;
+    int32_t       harmonics;
+    int32_t       scale;
+    int32_t       n_fft;
+    int32_t       hop;
+    int32_t       pad;
+} orc_source_args;
+
 typedef struct orc_node {
     int32_t      op;
     int32_t      type0;

@@ -27,7 +27,7 @@ F32, F16, Q8_0, Q5_K, I32, BF16 = 0, 1, 8, 13, 26, 30
  OP_GET_ROWS, OP_CAST_F32, OP_GLU_SWIGLU, OP_SOFT_MAX, OP_CONT_F32, OP_BINBCAST, OP_SUB, OP_TANH, OP_SIGMOID,
  OP_ELU, OP_GELU_ERF, OP_CLAMP, OP_NORM, OP_IM2COL, OP_COL2IM_1D, OP_PAD, OP_PAD_REFLECT_1D,
  OP_REPEAT, OP_ACC, OP_RELU, OP_NEG, OP_STEP, OP_SQRT, OP_SUM_ROWS, OP_MEAN, OP_DIAG_MASK_INF,
- OP_ISTFT) = range(1, 39)
+ OP_ISTFT, OP_HARMONIC_SOURCE) = range(1, 40)
 
 
 class OrcNode(ctypes.Structure):
@@ -37,6 +37,16 @@ class OrcNode(ctypes.Structure):
         ("src1_rows", ctypes.c_int64), ("src1_ne0", ctypes.c_int64),
         ("src0", ctypes.c_void_p), ("src1", ctypes.c_void_p), ("dst", ctypes.c_void_p),
         ("f", ctypes.c_float * 4), ("i", ctypes.c_int32 * 4),
+    ]
+
+
+class OrcSourceArgs(ctypes.Structure):
+    _fields_ = [
+        ("merge_weight", ctypes.c_void_p), ("rand_ini", ctypes.c_void_p), ("noise", ctypes.c_void_p),
+        ("har", ctypes.c_void_p), ("merge_bias", ctypes.c_float), ("sine_amp", ctypes.c_float),
+        ("noise_std", ctypes.c_float), ("voiced_threshold", ctypes.c_float), ("sampling_rate", ctypes.c_int32),
+        ("harmonics", ctypes.c_int32), ("scale", ctypes.c_int32), ("n_fft", ctypes.c_int32), ("hop", ctypes.c_int32),
+        ("pad", ctypes.c_int32),
     ]
 
 
@@ -183,6 +193,29 @@ class Graph:
         x = self._f32(x)
         return self._node(OP_DIAG_MASK_INF, np.empty_like(x), x, ne1=x.shape[-2] if x.ndim > 1 else 1,
                           i=(int(n_past),))
+
+    def harmonic_source(self, f0, merge_weight, merge_bias, rand_ini, noise, *, rate, scale, sine_amp, noise_std,
+                        voiced_threshold, n_fft, hop):
+        """Kokoro's build_harmonic_source: f0 (L,), merge_weight and rand_ini
+        (H,), noise (L*scale, H) -> (excitation (L*scale,), spectrum (frames,
+        2*(n_fft/2 + 1)), magnitudes then phases per frame)."""
+        f0 = self._f32(f0)
+        mw, ri, nz = self._f32(merge_weight), self._f32(rand_ini), self._f32(noise)
+        L, H = f0.size, mw.size
+        U = L * scale
+        if ri.size != H or nz.shape != (U, H) or n_fft < 2 or hop < 1 or scale < 1:
+            raise ValueError("harmonic_source: bad shapes or parameters")
+        bins = n_fft // 2 + 1
+        exc = np.empty(U, np.float32)
+        har = np.empty((U // hop + 1, 2 * bins), np.float32)
+        args = OrcSourceArgs(mw.ctypes.data, ri.ctypes.data, nz.ctypes.data, har.ctypes.data, merge_bias, sine_amp,
+                             noise_std, voiced_threshold, int(rate), int(H), int(scale), int(n_fft), int(hop), 0)
+        n = OrcNode()
+        n.op, n.type0, n.ne0, n.nrows = OP_HARMONIC_SOURCE, F32, 1, L
+        n.src0, n.src1, n.dst = _ptr(f0), ctypes.cast(ctypes.pointer(args), ctypes.c_void_p), _ptr(exc)
+        self.nodes.append(n)
+        self.keep += [exc, har, f0, mw, ri, nz, args]
+        return exc, har
 
     def inverse_stft(self, spectrum, n_fft, hop):
         """Kokoro's inverse_stft: spectrum (frames, n_fft + 2) -> ((frames - 1) * hop,)."""

@@ -110,6 +110,7 @@ def load(path=None):
         "shp_diag_mask_inf": [_PT, i32, _PT, vp],
         "shp_soft_max_causal": [_PT, i32, f, _PT, vp],
         "shp_inverse_stft": [_PT, i32, i32, _PT, vp],
+        "shp_harmonic_source": [_PT, _PT, f, _PT, _PT, i32, i32, f, f, f, i32, i32, _PT, _PT, vp],
         "shp_sigmoid": [_PT, _PT, vp],
         "shp_elu": [_PT, _PT, vp],
         "shp_gelu_erf": [_PT, _PT, vp],
@@ -598,6 +599,24 @@ def inverse_stft(spectrum, n_fft, hop, out=None):
     _check(load().shp_inverse_stft(_ref(desc(spectrum)), int(n_fft), int(hop), _ref(desc(out)), _stream()),
            "inverse_stft")
     return out
+
+
+def harmonic_source(f0, merge_weight, merge_bias, rand_ini, noise, *, rate, scale, sine_amp, noise_std,
+                    voiced_threshold, n_fft, hop, out=None):
+    """Kokoro's build_harmonic_source: f0 (L,), merge_weight and rand_ini (H,),
+    noise (L*scale, H) -> (excitation (L*scale,), spectrum (frames, n_fft + 2))."""
+    import torch
+    U = f0.numel() * scale
+    frames = U // hop + 1
+    if out is None:
+        out = (torch.empty((U,), dtype=torch.float32, device=f0.device),
+               torch.empty((frames, n_fft + 2), dtype=torch.float32, device=f0.device))
+    exc, har = out
+    _check(load().shp_harmonic_source(_ref(desc(f0)), _ref(desc(merge_weight)), float(merge_bias), _ref(desc(rand_ini)),
+                                      _ref(desc(noise)), int(rate), int(scale), float(sine_amp), float(noise_std),
+                                      float(voiced_threshold), int(n_fft), int(hop), _ref(desc(exc)), _ref(desc(har)),
+                                      _stream()), "harmonic_source")
+    return exc, har
 
 
 def clamp(x, lo, hi, out=None):

@@ -17,6 +17,9 @@ Sources:
      known answers and the multichannel cases' shapes and fill rule)
   G7 tests/kokoro_istft_test.cpp:15-62 (Kokoro's inverse short-time transform
      against torch.istft: the raw spectrum, n_fft, hop, frames, the audio)
+  G8 tests/kokoro_source_test.cpp:18-88 (Kokoro's harmonic source against the
+     upstream module: f0, the merge, the random draws, the excitation and its
+     spectrum, at reduced dimensions)
 """
 import json
 import os
@@ -191,8 +194,30 @@ def main():
         "tolerance": 1e-5,
     }
 
+    t = read("tests/kokoro_source_test.cpp")
+
+    def assigned(name):
+        m = re.search(r"%s\s*=\s*([-0-9.eE]+)f?\s*;" % re.escape(name), t)
+        if m is None:
+            raise SystemExit("assignment %s not found" % name)
+        return float(m.group(1))
+    g8 = {
+        "source": "tests/kokoro_source_test.cpp:18-88",
+        "scale": constant(t, "kScale"), "harmonics": constant(t, "kHarmonics"), "n_fft": constant(t, "kNfft"),
+        "hop": constant(t, "kHop"), "rate": constant(t, "kRate"),
+        "sine_amp": assigned("h.source.sine_amp"), "noise_std": assigned("h.source.noise_std"),
+        "voiced_threshold": assigned("h.source.voiced_threshold"),
+        "merge_weight": literal_array(t, "kMergeWeight"), "merge_bias": assigned("kMergeBias"),
+        "rand_ini": literal_array(t, "kRandIni"), "noise": literal_array(t, "kNoise"), "f0": literal_array(t, "kF0"),
+        # the excitation (upsampled samples) and the spectrum, frame-major rows of
+        # n_fft/2 + 1 magnitudes then as many phases; the test's bounds (phases on the circle)
+        "expected_source": literal_array(t, "kExpectedSource"), "expected_har": literal_array(t, "kExpectedHar"),
+        "tolerance_source": 1e-5, "tolerance_magnitude": 1e-5, "tolerance_phase": 1e-4,
+    }
+
     for name, obj in (("qwen3_decoder_layer", g1), ("qwen3_code_predictor", g2), ("qwen3_codec_snake_beta", g3),
-                      ("qwen3_codec_convs", g5), ("vits_transpose_conv", g6), ("kokoro_istft", g7)):
+                      ("qwen3_codec_convs", g5), ("vits_transpose_conv", g6), ("kokoro_istft", g7),
+                      ("kokoro_source", g8)):
         with open(os.path.join(HERE, name + ".json"), "w") as f:
             json.dump(obj, f, indent=1)
             f.write("\n")

@@ -547,3 +547,155 @@ def test_istft_restatement_is_the_reference_build(n_fft, hop, frames):
     if (n_fft, hop, frames) == (8, 2, 9):
         assert L.ref_inverse_stft(spec.ctypes.data, frames, 7, hop, out.ctypes.data, out.size) != 0
         assert L.ref_inverse_stft(spec.ctypes.data, frames, n_fft, 0, out.ctypes.data, out.size) != 0
+
+
+# ---------------------------------------------------------------------------
+# G8: Kokoro's harmonic source (tests/kokoro_source_test.cpp)
+# ---------------------------------------------------------------------------
+
+def source_inputs(d):
+    """G8's inputs and constants as harmonic_source's arguments."""
+    H, S = d["harmonics"], d["scale"]
+    f0 = np.array(d["f0"], np.float32)
+    noise = np.array(d["noise"], np.float32).reshape(f0.size * S, H)
+    kw = dict(rate=d["rate"], scale=S, sine_amp=np.float32(d["sine_amp"]), noise_std=np.float32(d["noise_std"]),
+              voiced_threshold=np.float32(d["voiced_threshold"]), n_fft=d["n_fft"], hop=d["hop"])
+    return (f0, np.array(d["merge_weight"], np.float32), np.float32(d["merge_bias"]),
+            np.array(d["rand_ini"], np.float32), noise), kw
+
+
+def phase_gap(a, b):
+    """Distance on the circle."""
+    return np.abs(np.arctan2(np.sin(a - b), np.cos(a - b)))
+
+
+def check_source_golden(exc, har, d):
+    bins = d["n_fft"] // 2 + 1
+    exp_s = np.array(d["expected_source"], np.float32)
+    exp_h = np.array(d["expected_har"], np.float32).reshape(-1, 2 * bins)
+    assert exc.shape == exp_s.shape and har.shape == exp_h.shape
+    assert np.abs(exc - exp_s).max() < d["tolerance_source"]
+    assert np.abs(har[:, :bins] - exp_h[:, :bins]).max() < d["tolerance_magnitude"]
+    assert phase_gap(har[:, bins:].astype(np.float64), exp_h[:, bins:].astype(np.float64)).max() < d["tolerance_phase"]
+
+
+def test_golden_kokoro_source():
+    """G8: the restatement against the upstream module's values at the test's
+    bounds (excitation 1e-5, magnitudes 1e-5, phases 1e-4 on the circle);
+    the phase accumulated on the sample grid instead of the coarse one, the
+    resampling's half-sample offset dropped, the voiced threshold ignored, and
+    the STFT without its reflect padding each miss."""
+    d = _load("kokoro_source.json")
+    args, kw = source_inputs(d)
+    g = R.Graph()
+    exc, har = g.harmonic_source(*args, **kw)
+    g.compute()
+    check_source_golden(exc, har, d)
+    exp_s = np.array(d["expected_source"], np.float32)
+    # planted mistakes, each on a copy of the numpy restatement below
+    for bad in ("fine_grid", "no_half", "all_voiced", "no_reflect"):
+        e, h = source_numpy(*args, **kw, mistake=bad)
+        miss = np.abs(e - exp_s).max() > 1e-3 or np.abs(h[:, :d["n_fft"] // 2 + 1] -
+                                                        np.array(d["expected_har"], np.float32).reshape(h.shape)[:, :d["n_fft"] // 2 + 1]).max() > 1e-3
+        assert miss, bad
+    e, h = source_numpy(*args, **kw)
+    check_source_golden(e, h, d)
+
+
+def source_numpy(f0, mw, bias, ri, noise, *, rate, scale, sine_amp, noise_std, voiced_threshold, n_fft, hop,
+                 mistake=None):
+    """An independent numpy restatement of the source (vectorised; the STFT by
+    numpy's rfft over reflect-padded frames), with planted mistakes."""
+    L, H = f0.size, mw.size
+    U = L * scale
+    f0u = np.repeat(f0, scale)
+    rad = f0u[:, None] * np.arange(1, H + 1, dtype=np.float32)[None, :] / np.float32(rate)
+    rad = (rad - np.floor(rad)).astype(np.float32)
+    rad[0] += ri
+
+    def resample(x, n_out):
+        n_in = x.shape[0]
+        o = np.arange(n_out, dtype=np.float64)
+        pos = (o + 0.5) * (n_in / n_out) - (0.0 if mistake == "no_half" else 0.5)
+        pos = np.maximum(pos, 0.0)
+        lo = pos.astype(np.int64)
+        hi = np.minimum(lo + 1, n_in - 1)
+        w = (pos - lo).astype(np.float32)[:, None]
+        return (x[lo] * (np.float32(1) - w) + x[hi] * w).astype(np.float32)
+    if mistake == "fine_grid":
+        run = np.cumsum(rad, axis=0, dtype=np.float32)
+        fine = (run.astype(np.float64) * 2 * np.pi).astype(np.float32)
+    else:
+        crs = resample(rad, L)
+        run = np.zeros_like(crs)
+        acc = np.zeros(H, np.float32)
+        for j in range(L):
+            acc = (acc + crs[j]).astype(np.float32)
+            run[j] = acc
+        ph = (run.astype(np.float64) * 2.0 * np.pi * scale).astype(np.float32)
+        fine = resample(ph, U)
+    uv = (f0u > voiced_threshold).astype(np.float32) if mistake != "all_voiced" else np.ones(U, np.float32)
+    gain = uv * np.float32(noise_std) + (np.float32(1) - uv) * (np.float32(sine_amp) / np.float32(3))
+    vals = np.sin(fine.astype(np.float64)).astype(np.float32) * np.float32(sine_amp) * uv[:, None] + \
+        gain[:, None] * noise
+    merged = np.full(U, np.float32(bias), np.float32)
+    for h in range(H):
+        merged = (merged + mw[h] * vals[:, h]).astype(np.float32)
+    exc = np.tanh(merged.astype(np.float64)).astype(np.float32)
+    half = n_fft // 2
+    padded = np.pad(exc, half, mode="reflect" if mistake != "no_reflect" else "constant")
+    win = (0.5 * (1.0 - np.cos(2.0 * np.pi * np.arange(n_fft) / n_fft))).astype(np.float32)
+    frames = U // hop + 1
+    segs = np.stack([padded[f * hop:f * hop + n_fft] * win for f in range(frames)]).astype(np.float64)
+    X = np.fft.rfft(segs, axis=1)
+    return exc, np.concatenate([np.abs(X), np.angle(X)], axis=1).astype(np.float32)
+
+
+def _ref_source_lib():
+    import ctypes
+    path = os.path.join(R.HERE, "_ref", "libkokoro_source_ref.so")
+    if not os.path.exists(path):
+        return None
+    L = ctypes.CDLL(path)
+    f, u32, u64, vp = ctypes.c_float, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p
+    L.ref_harmonic_source.argtypes = [vp, u64, vp, f, vp, vp, u32, u32, u32, f, f, f, u32, u32, vp, u64, vp, u64]
+    L.ref_harmonic_source.restype = ctypes.c_int
+    return L
+
+
+def random_source_case(seed, L, H, scale, n_fft, hop):
+    rng = np.random.default_rng(seed)
+    f0 = np.where(rng.random(L) < 0.2, rng.uniform(0, 8, L), rng.uniform(60, 400, L)).astype(np.float32)
+    mw = rng.normal(0, 0.5, H).astype(np.float32)
+    ri = np.concatenate([[0.0], rng.uniform(0, 1, H - 1)]).astype(np.float32)
+    noise = rng.standard_normal((L * scale, H)).astype(np.float32)
+    kw = dict(rate=24000, scale=scale, sine_amp=np.float32(0.1), noise_std=np.float32(0.003),
+              voiced_threshold=np.float32(10.0), n_fft=n_fft, hop=hop)
+    return (f0, mw, np.float32(rng.normal(0, 0.3)), ri, noise), kw
+
+
+@pytest.mark.parametrize("case", ["golden", (50, 9, 300, 20, 5), (37, 3, 4, 8, 2), (20, 5, 16, 16, 4)])
+def test_source_restatement_is_the_reference_build(case):
+    """The restatement against the reference's own build_harmonic_source
+    compiled from the checkout (oracle/_ref): bit for bit, excitation and
+    spectrum, on G8's inputs and on random ones at Kokoro's 9 harmonics,
+    upsampling 300, n_fft 20 and hop 5. Skipped where the reference checkout
+    was not there to build it."""
+    L = _ref_source_lib()
+    if L is None:
+        pytest.skip("oracle/_ref not built (no reference checkout)")
+    if case == "golden":
+        args, kw = source_inputs(_load("kokoro_source.json"))
+    else:
+        args, kw = random_source_case(sum(case), *case)
+    f0, mw, bias, ri, noise = args
+    g = R.Graph()
+    exc, har = g.harmonic_source(*args, **kw)
+    g.compute()
+    e2, h2 = np.empty_like(exc), np.empty_like(har)
+    assert L.ref_harmonic_source(f0.ctypes.data, f0.size, mw.ctypes.data, bias, ri.ctypes.data, noise.ctypes.data,
+                                 mw.size, kw["rate"], kw["scale"], kw["sine_amp"], kw["noise_std"],
+                                 kw["voiced_threshold"], kw["n_fft"], kw["hop"], e2.ctypes.data, e2.size,
+                                 h2.ctypes.data, h2.size) == 0
+    assert np.array_equal(exc.view(np.uint32), e2.view(np.uint32))
+    assert np.array_equal(har.view(np.uint32), h2.view(np.uint32))
