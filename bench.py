@@ -40,6 +40,8 @@ input sets whose total exceeds 512 MB (cold cache):
   - Kokoro's harmonic source and its spectrum, and the inverse short-time
     transform, of a 5-second utterance (9 harmonics, upsampling 300, n_fft 20,
     hop 5, 24 kHz): host code in the reference, between and after its graphs;
+  - the Qwen3-TTS speaker encoder's log-mel of a 10-second reference clip
+    (n_fft 1024, hop 256, 128 Slaney bins): host code in the reference too;
   - the decode step's non-GEMM work per talker layer (28-layer
     graph), without and with the KV-cache write and the attention softmax;
   - the 512-token prefill step of the 0.6B talker (with the BF16
@@ -620,6 +622,23 @@ def source_rows(R, S, torch, cfg, seed, seconds=5, rate=24000, H=9, scale=300, n
           4 * (L + U * H + U + frames * (n_fft + 2)), make)
 
 
+def mel_rows(R, S, torch, cfg, seed, seconds=10, rate=24000):
+    """The Qwen3-TTS speaker encoder's log-mel (qwen3-tts/mel.cpp:174-299) of a
+    `seconds`-long reference clip at the production parameters: the PCM read,
+    [128, frames] log energies written (the filterbank, 263 KB, cache-resident)."""
+    g, randn, empty, bf16 = gen(torch, seed)
+    ns = seconds * rate
+    frames = 1 + (ns + 2 * 384 - 1024) // 256
+
+    def make():
+        pcm = randn(ns) * 0.2
+        fb = torch.from_numpy(S.mel_filterbank(rate, 1024, 128, 0.0, 12000.0)).cuda()
+        y = empty(frames, 128)
+        return lambda: S.log_mel(pcm, fb, 1024, 256, 1024, out=y)
+    R.run(cfg, "log_mel n_fft 1024 hop 256 128 bins, %d s at %d Hz" % (seconds, rate), 4 * ns + 4 * frames * 128,
+          make)
+
+
 def floor_rows(R, S, torch, seed=SEED + 8):
     """Same-run floors the op rows are read against, each timed as the op rows
     are (cold rotating sets, HIP graph, median of chunks):
@@ -918,6 +937,11 @@ def cpu_op_builders(seed=SEED + 9):
                 lambda g: R.add_rms_norm_w(g, take(T, H), take(T, H), bf16(H), eps, R.BF16)))
     out.append((cfg, "swiglu [%d,%d]" % (F_, T), 3 * T * F_ * f32, lambda g: R.swiglu(g, take(T, F_), take(T, F_))))
     out.append((cfg, "add [%d,%d]" % (H, T), 3 * T * H * f32, lambda g: g.add(take(T, H), take(T, H))))
+    nm = 10 * 24000
+    fbm = R.mel_filterbank(24000, 1024, 128, 0.0, 12000.0)
+    out.append(("configs[3]", "log_mel n_fft 1024 hop 256 128 bins, 10 s at 24000 Hz",
+                4 * nm + 4 * (1 + (nm + 768 - 1024) // 256) * 128,
+                lambda g: g.log_mel((rng.standard_normal(nm) * 0.2).astype(np.float32), fbm, 1024, 256, 1024)))
     Ls, Us = 5 * 24000 // 300, 5 * 24000
     out.append(("configs[3]", "harmonic_source 9 harmonics, 5 s at 24000 Hz",
                 4 * (Ls + Us * 9 + Us + (Us // 5 + 1) * 22),
@@ -1516,6 +1540,7 @@ def main():
     talker_input_rows(R, S, torch, "configs[4]", SEED + 7)
     istft_rows(R, S, torch, "configs[3]", SEED + 11)
     source_rows(R, S, torch, "configs[3]", SEED + 12)
+    mel_rows(R, S, torch, "configs[3]", SEED + 13)
     floors = floor_rows(R, S, torch)
     link_floors(list(ops4.values()) + R.rows, floors)
 

@@ -428,6 +428,33 @@ shp_status_t shp_harmonic_source(const shp_tensor * f0, const shp_tensor * merge
                                  shp_stream_t stream);
 
 /*
+ * The Qwen3-TTS speaker encoder's log-mel front end (qwen3-tts/mel.cpp:
+ * 174-299, compute_log_mel; run by the host before the ECAPA graph): pcm F32
+ * [samples] reflect-padded by (n_fft - hop)/2 on each side and framed
+ * without centring (frames = 1 + (samples + 2*pad - n_fft)/hop), the periodic
+ * Hann window of win_length centred in n_fft, the host code's radix-2 FFT on
+ * f32 values with double twiddles and butterflies (stage for stage), the
+ * amplitude sqrt(re^2 + im^2 + 1e-9), the filterbank F32 [n_fft/2 + 1,
+ * mel_bins] weighted sum in double, log(max(energy, 1e-5)), into mel F32
+ * [mel_bins, frames]. n_fft a power of two up to 2048, win_length and hop at
+ * most n_fft, more samples than the pad; all contiguous. Non-finite samples
+ * are not screened here (the reference refuses them; its audio normaliser
+ * does so before this stage on the synthesis path).
+ */
+shp_status_t shp_log_mel(const shp_tensor * pcm, const shp_tensor * filterbank, int32_t n_fft, int32_t hop,
+                         int32_t win_length, shp_tensor * mel, shp_stream_t stream);
+
+/*
+ * The Slaney mel filterbank shp_log_mel weights the amplitudes with
+ * (qwen3-tts/mel.cpp:96-170, librosa's filters.mel with htk=False and
+ * norm='slaney'): mel_bins rows of n_fft/2 + 1 f32 weights into the host
+ * array out. Host code, no device work: computed once per model and
+ * uploaded.
+ */
+shp_status_t shp_mel_filterbank(int32_t sample_rate, int32_t n_fft, int32_t mel_bins, float fmin, float fmax,
+                                float * out);
+
+/*
  * ggml_concat(a, b, dim): y of a's shape except y->ne[dim] = a->ne[dim] +
  * b->ne[dim]; y(i) = a(i) where i[dim] < a->ne[dim], else b(i) with
  * i[dim] - a->ne[dim]. All F32, rows contiguous (any row strides). The code

@@ -725,6 +725,159 @@ static void op_pad_family(const orc_node * n, int ith, int nth) {
     }
 }
 
+/* The Qwen3-TTS speaker encoder's log-mel front end (qwen3-tts/mel.cpp:
+ * 63-94, 131-299), restated: librosa's Slaney mel scale (linear below
+ * 1 kHz, log above) and area-normalised triangular filters in double, rounded
+ * to f32; the PCM reflect-padded by (n_fft - hop)/2 on each side and framed
+ * without centring; the periodic Hann window of win_length (f32), centred in
+ * n_fft; per frame an in-place iterative radix-2 FFT on f32 buffers (the
+ * bit-reversal swap, then butterflies with double twiddles cos/sin((-2 pi /
+ * len) * k), each result rounded to f32); the amplitude sqrt(re^2 + im^2 +
+ * 1e-9) in double rounded to f32; each mel energy summed in double in bin
+ * order; log(max(energy, 1e-5)) rounded to f32. */
+static double mel_slaney_step(void) {
+    return log(6.4) / 27.0;
+}
+
+static double mel_hz_to_mel(double hz) {
+    const double min_log_mel = 1000.0 / (200.0 / 3.0);
+    if (hz >= 1000.0) {
+        return min_log_mel + log(hz / 1000.0) / mel_slaney_step();
+    }
+    return hz / (200.0 / 3.0);
+}
+
+static double mel_mel_to_hz(double mel) {
+    const double min_log_mel = 1000.0 / (200.0 / 3.0);
+    if (mel >= min_log_mel) {
+        return 1000.0 * exp(mel_slaney_step() * (mel - min_log_mel));
+    }
+    return (200.0 / 3.0) * mel;
+}
+
+void orc_mel_filterbank(uint32_t sample_rate, uint32_t n_fft, uint32_t mel_bins, float fmin, float fmax, float * out) {
+    const uint32_t nf = n_fft / 2 + 1;
+    double *       mf = (double *) malloc(sizeof(double) * (mel_bins + 2));
+    if (mf == NULL) {
+        return;
+    }
+    const double lo = mel_hz_to_mel((double) fmin), hi = mel_hz_to_mel((double) fmax);
+    for (uint32_t i = 0; i < mel_bins + 2; ++i) {
+        mf[i] = mel_mel_to_hz(lo + (hi - lo) * (double) i / (double) (mel_bins + 1));
+    }
+    for (uint32_t b = 0; b < mel_bins; ++b) {
+        const double enorm = 2.0 / (mf[b + 2] - mf[b]);
+        for (uint32_t k = 0; k < nf; ++k) {
+            const double f     = (double) k * (double) sample_rate / (double) n_fft;
+            const double lower = (f - mf[b]) / (mf[b + 1] - mf[b]);
+            const double upper = (mf[b + 2] - f) / (mf[b + 2] - mf[b + 1]);
+            const double v     = lower < upper ? lower : upper;
+            out[(size_t) b * nf + k] = (float) ((v > 0.0 ? v : 0.0) * enorm);
+        }
+    }
+    free(mf);
+}
+
+static void fft_radix2_f32(float * re, float * im, size_t n) {
+    const double pi = 3.14159265358979323846;
+    for (size_t i = 1, j = 0; i < n; ++i) {
+        size_t bit = n >> 1;
+        for (; j & bit; bit >>= 1) {
+            j ^= bit;
+        }
+        j ^= bit;
+        if (i < j) {
+            float t = re[i];
+            re[i]   = re[j];
+            re[j]   = t;
+            t       = im[i];
+            im[i]   = im[j];
+            im[j]   = t;
+        }
+    }
+    for (size_t len = 2; len <= n; len <<= 1) {
+        const double angle = -2.0 * pi / (double) len;
+        for (size_t start = 0; start < n; start += len) {
+            for (size_t k = 0; k < len / 2; ++k) {
+                const double theta = angle * (double) k;
+                const double wr = cos(theta), wi = sin(theta);
+                const size_t a = start + k, b = a + len / 2;
+                const double xr = re[b] * wr - im[b] * wi;
+                const double xi = re[b] * wi + im[b] * wr;
+                re[b]           = (float) (re[a] - xr);
+                im[b]           = (float) (im[a] - xi);
+                re[a]           = (float) (re[a] + xr);
+                im[a]           = (float) (im[a] + xi);
+            }
+        }
+    }
+}
+
+static void op_log_mel(const orc_node * n, int ith, int nth) {
+    (void) nth;
+    if (ith != 0) {
+        return;
+    }
+    const double   pi   = 3.14159265358979323846;
+    const float *  pcm  = (const float *) n->src0;
+    const float *  fb   = (const float *) n->src1;
+    const int64_t  ns   = n->ne0;
+    const int64_t  nfft = n->i[0], hop = n->i[1], win = n->i[2], bins = n->i[3];
+    const int64_t  pad  = (nfft - hop) / 2;
+    const int64_t  plen = ns + 2 * pad;
+    if (nfft < 2 || (nfft & (nfft - 1)) != 0 || hop < 1 || win < 1 || win > nfft || hop > nfft || ns <= pad ||
+        plen < nfft) {
+        atomic_store(&g_node_error, -2);
+        return;
+    }
+    const int64_t frames = 1 + (plen - nfft) / hop;
+    const int64_t nf     = nfft / 2 + 1;
+    float *       padded = (float *) malloc(sizeof(float) * (size_t) plen);
+    float *       w      = (float *) calloc((size_t) nfft, sizeof(float));
+    float *       re     = (float *) malloc(sizeof(float) * (size_t) nfft);
+    float *       im     = (float *) malloc(sizeof(float) * (size_t) nfft);
+    float *       mag    = (float *) malloc(sizeof(float) * (size_t) nf);
+    if (!padded || !w || !re || !im || !mag) {
+        atomic_store(&g_node_error, -3);
+        goto done;
+    }
+    for (int64_t i = 0; i < ns; ++i) {
+        padded[pad + i] = pcm[i];
+    }
+    for (int64_t j = 0; j < pad; ++j) {
+        padded[j]            = pcm[pad - j];
+        padded[pad + ns + j] = pcm[ns - 2 - j];
+    }
+    for (int64_t i = 0; i < win; ++i) {
+        w[(nfft - win) / 2 + i] = (float) (0.5 - 0.5 * cos(2.0 * pi * (double) i / (double) win));
+    }
+    for (int64_t f = 0; f < frames; ++f) {
+        for (int64_t i = 0; i < nfft; ++i) {
+            re[i] = padded[f * hop + i] * w[i];
+            im[i] = 0.0f;
+        }
+        fft_radix2_f32(re, im, (size_t) nfft);
+        for (int64_t k = 0; k < nf; ++k) {
+            const double sq = (double) re[k] * (double) re[k] + (double) im[k] * (double) im[k];
+            mag[k]          = (float) sqrt(sq + 1e-9);
+        }
+        float * y = (float *) n->dst + f * bins;
+        for (int64_t b = 0; b < bins; ++b) {
+            double e = 0.0;
+            for (int64_t k = 0; k < nf; ++k) {
+                e += (double) fb[b * nf + k] * (double) mag[k];
+            }
+            y[b] = (float) log(e < 1e-5 ? 1e-5 : e);  /* std::max(e, 1e-5): a NaN passes */
+        }
+    }
+done:
+    free(padded);
+    free(w);
+    free(re);
+    free(im);
+    free(mag);
+}
+
 /* Kokoro's harmonic-plus-noise source and its short-time spectrum
  * (kokoro/source.cpp:60-184, build_harmonic_source), restated step by step:
  * f0 repeated `scale` times; per sample and harmonic h the phase increment
@@ -1165,6 +1318,9 @@ static void run_node(const orc_node * n, int ith, int nth) {
             break;
         case ORC_OP_HARMONIC_SOURCE:
             op_harmonic_source(n, ith, nth);
+            break;
+        case ORC_OP_LOG_MEL:
+            op_log_mel(n, ith, nth);
             break;
         default:
             atomic_store(&g_node_error, -1);

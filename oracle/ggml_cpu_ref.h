@@ -67,6 +67,7 @@ enum orc_op {
     ORC_OP_DIAG_MASK_INF, /* -inf past n_past + row, else x         ggml_diag_mask_inf  */
     ORC_OP_ISTFT,        /* Kokoro's inverse STFT (host code)      kokoro inverse_stft */
     ORC_OP_HARMONIC_SOURCE, /* Kokoro's harmonic source (host code) build_harmonic_source */
+    ORC_OP_LOG_MEL,      /* Qwen3-TTS speaker encoder's log-mel      compute_log_mel     */
 };
 
 /*
@@ -109,6 +110,9 @@ enum orc_op {
  *               dst contiguous F32.
  *   SUM_ROWS, MEAN : src0 nrows rows of ne0; dst one value per row.
  *   DIAG_MASK_INF : src0 nrows rows of ne0, ne1 rows per matrix; i[0] = n_past.
+ *   LOG_MEL   : src0 = PCM (ne0 samples); src1 = the Slaney filterbank
+ *               (i[3] mel bins of n_fft/2 + 1); i[0] = n_fft, i[1] = hop,
+ *               i[2] = win_length; dst frames of i[3] log energies.
  *   HARMONIC_SOURCE : src0 = f0 (nrows values); src1 = orc_source_args; dst =
  *               the excitation (nrows * scale values); the spectrum into
  *               args->har ((nrows*scale/hop + 1) frames of 2*(n_fft/2 + 1)).
@@ -153,6 +157,10 @@ typedef struct orc_node {
     float        f[4];
     int32_t      i[4];
 } orc_node;
+
+/* The Qwen3-TTS speaker encoder's Slaney mel filterbank (qwen3-tts/mel.cpp:
+ * 131-170): mel_bins rows of n_fft/2 + 1 weights into out. */
+void orc_mel_filterbank(uint32_t sample_rate, uint32_t n_fft, uint32_t mel_bins, float fmin, float fmax, float * out);
 
 /* Runs the nodes in order on n_threads threads (1 = inline). Returns 0, or a
  * negative value for an unknown op / bad argument. */

@@ -27,7 +27,7 @@ F32, F16, Q8_0, Q5_K, I32, BF16 = 0, 1, 8, 13, 26, 30
  OP_GET_ROWS, OP_CAST_F32, OP_GLU_SWIGLU, OP_SOFT_MAX, OP_CONT_F32, OP_BINBCAST, OP_SUB, OP_TANH, OP_SIGMOID,
  OP_ELU, OP_GELU_ERF, OP_CLAMP, OP_NORM, OP_IM2COL, OP_COL2IM_1D, OP_PAD, OP_PAD_REFLECT_1D,
  OP_REPEAT, OP_ACC, OP_RELU, OP_NEG, OP_STEP, OP_SQRT, OP_SUM_ROWS, OP_MEAN, OP_DIAG_MASK_INF,
- OP_ISTFT, OP_HARMONIC_SOURCE) = range(1, 40)
+ OP_ISTFT, OP_HARMONIC_SOURCE, OP_LOG_MEL) = range(1, 41)
 
 
 class OrcNode(ctypes.Structure):
@@ -53,6 +53,13 @@ class OrcSourceArgs(ctypes.Structure):
 _lib = None
 
 
+def mel_filterbank(sample_rate, n_fft, mel_bins, fmin, fmax):
+    """The restated Slaney filterbank, (mel_bins, n_fft/2 + 1) f32."""
+    out = np.empty((mel_bins, n_fft // 2 + 1), np.float32)
+    lib().orc_mel_filterbank(int(sample_rate), int(n_fft), int(mel_bins), float(fmin), float(fmax), _ptr(out))
+    return out
+
+
 def lib():
     global _lib
     if _lib is None:
@@ -64,6 +71,9 @@ def lib():
         L.orc_time_nodes.argtypes = [ctypes.POINTER(OrcNode), ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                      ctypes.c_int32, ctypes.POINTER(ctypes.c_double)]
         L.orc_time_nodes.restype = ctypes.c_int
+        L.orc_mel_filterbank.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_float,
+                                         ctypes.c_float, ctypes.c_void_p]
+        L.orc_mel_filterbank.restype = None
         for name in ("orc_fp16_to_fp32", "orc_bf16_to_fp32"):
             getattr(L, name).argtypes = [ctypes.c_uint16]
             getattr(L, name).restype = ctypes.c_float
@@ -216,6 +226,21 @@ class Graph:
         self.nodes.append(n)
         self.keep += [exc, har, f0, mw, ri, nz, args]
         return exc, har
+
+    def log_mel(self, pcm, filterbank, n_fft, hop, win_length):
+        """The speaker encoder's compute_log_mel given the filterbank (mel_bins,
+        n_fft/2 + 1): pcm (samples,) -> (frames, mel_bins)."""
+        x = self._f32(pcm)
+        fb = self._f32(filterbank)
+        bins = fb.shape[0]
+        pad = (n_fft - hop) // 2
+        plen = x.size + 2 * pad
+        if n_fft < 2 or n_fft & (n_fft - 1) or hop < 1 or win_length > n_fft or hop > n_fft or x.size <= pad \
+                or plen < n_fft or fb.shape != (bins, n_fft // 2 + 1):
+            raise ValueError("log_mel: bad input or parameters")
+        frames = 1 + (plen - n_fft) // hop
+        return self._node(OP_LOG_MEL, np.empty((frames, bins), np.float32), x, fb, ne0=x.size, nrows=1,
+                          i=(int(n_fft), int(hop), int(win_length), int(bins)))
 
     def inverse_stft(self, spectrum, n_fft, hop):
         """Kokoro's inverse_stft: spectrum (frames, n_fft + 2) -> ((frames - 1) * hop,)."""

@@ -111,6 +111,8 @@ def load(path=None):
         "shp_soft_max_causal": [_PT, i32, f, _PT, vp],
         "shp_inverse_stft": [_PT, i32, i32, _PT, vp],
         "shp_harmonic_source": [_PT, _PT, f, _PT, _PT, i32, i32, f, f, f, i32, i32, _PT, _PT, vp],
+        "shp_log_mel": [_PT, _PT, i32, i32, i32, _PT, vp],
+        "shp_mel_filterbank": [i32, i32, i32, f, f, vp],
         "shp_sigmoid": [_PT, _PT, vp],
         "shp_elu": [_PT, _PT, vp],
         "shp_gelu_erf": [_PT, _PT, vp],
@@ -617,6 +619,28 @@ def harmonic_source(f0, merge_weight, merge_bias, rand_ini, noise, *, rate, scal
                                       float(voiced_threshold), int(n_fft), int(hop), _ref(desc(exc)), _ref(desc(har)),
                                       _stream()), "harmonic_source")
     return exc, har
+
+
+def mel_filterbank(sample_rate, n_fft, mel_bins, fmin, fmax):
+    """The Slaney filterbank (host code): a numpy (mel_bins, n_fft/2 + 1) f32 array."""
+    import numpy as np
+    out = np.empty((mel_bins, n_fft // 2 + 1), np.float32)
+    _check(load().shp_mel_filterbank(int(sample_rate), int(n_fft), int(mel_bins), float(fmin), float(fmax),
+                                     out.ctypes.data_as(ctypes.c_void_p)), "mel_filterbank")
+    return out
+
+
+def log_mel(pcm, filterbank, n_fft, hop, win_length, out=None):
+    """The speaker encoder's log-mel: pcm (samples,), filterbank (mel_bins,
+    n_fft/2 + 1) on the device -> (frames, mel_bins)."""
+    import torch
+    pad = (n_fft - hop) // 2
+    frames = 1 + (pcm.numel() + 2 * pad - n_fft) // hop
+    out = torch.empty((max(frames, 1), filterbank.shape[0]), dtype=torch.float32, device=pcm.device) if out is None \
+        else out
+    _check(load().shp_log_mel(_ref(desc(pcm)), _ref(desc(filterbank)), int(n_fft), int(hop), int(win_length),
+                              _ref(desc(out)), _stream()), "log_mel")
+    return out
 
 
 def clamp(x, lo, hi, out=None):

@@ -731,3 +731,16 @@ def test_causal_soft_max_run():
     g = S.Graph()
     p = g.soft_max_ext(g.diag_mask_inf(x, 0), z(16, 16), 0.125)
     assert kinds(g.plan(p)) == ["single", "single"]
+
+
+def test_mel_filterbank_is_the_restatement():
+    """shp_mel_filterbank (host code of the library) against the oracle's
+    restated Slaney filterbank, bit for bit, at the production parameters
+    and another rate, window and band."""
+    import numpy as np
+    import ggml_ref as R
+    for args in ((24000, 1024, 128, 0.0, 12000.0), (16000, 512, 80, 20.0, 7600.0), (24000, 2048, 64, 50.0, 8000.0)):
+        a, b = S.mel_filterbank(*args), R.mel_filterbank(*args)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), args
+    with pytest.raises(S.ShpError):
+        S.mel_filterbank(24000, 1, 128, 0.0, 12000.0)

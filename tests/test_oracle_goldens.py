@@ -699,3 +699,108 @@ def test_source_restatement_is_the_reference_build(case):
                                  h2.ctypes.data, h2.size) == 0
     assert np.array_equal(exc.view(np.uint32), e2.view(np.uint32))
     assert np.array_equal(har.view(np.uint32), h2.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# The Qwen3-TTS speaker encoder's log-mel front end (qwen3-tts/mel.cpp)
+# ---------------------------------------------------------------------------
+
+MEL = dict(sample_rate=24000, n_fft=1024, hop=256, win_length=1024, mel_bins=128, fmin=0.0, fmax=12000.0)
+
+
+def _ref_mel_lib():
+    import ctypes
+    path = os.path.join(R.HERE, "_ref", "libqwen3_mel_ref.so")
+    if not os.path.exists(path):
+        return None
+    L = ctypes.CDLL(path)
+    u32, u64, f, vp = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float, ctypes.c_void_p
+    L.ref_log_mel.argtypes = [vp, u64, u32, u32, u32, u32, u32, f, f, vp, u64, ctypes.POINTER(u64)]
+    L.ref_log_mel.restype = ctypes.c_int
+    return L
+
+
+def oracle_log_mel(pcm, p):
+    fb = R.mel_filterbank(p["sample_rate"], p["n_fft"], p["mel_bins"], p["fmin"], p["fmax"])
+    return R.run(lambda g: g.log_mel(pcm, fb, p["n_fft"], p["hop"], p["win_length"]))
+
+
+def test_log_mel_frame_counts_and_slaney_scale():
+    """tests/qwen3_tts_mel_test.cpp:21-60: one second at 24 kHz gives the
+    upstream 93 frames at hop 256 and 46 at hop 512 (what neither a centred
+    nor a plain uncentred STFT gives: 94/47 and 89/44); the Slaney scale's
+    closed forms -- 1 kHz at mel 15, linear below (f / (200/3)), a ratio of
+    6.4 per 27 mels above -- placed through the filterbank's band edges; each
+    filter's weights peak where its centre frequency falls and are
+    area-normalised (2 / band width in Hz times the triangle's height 1)."""
+    pcm = np.full(24000, 0.5, np.float32)
+    assert oracle_log_mel(pcm, MEL).shape == (93, 128)
+    assert oracle_log_mel(pcm, dict(MEL, hop=512)).shape == (46, 128)
+    n, hop = 1024, 256
+    assert (1 + 24000 // hop, 1 + (24000 - n) // hop) != (93, 93)
+    fb = R.mel_filterbank(24000, 1024, 128, 0.0, 12000.0).astype(np.float64)
+    hz = np.arange(513) * 24000 / 1024
+
+    def mel_to_hz(m):
+        return np.where(m >= 15, 1000 * 6.4 ** ((m - 15) / 27), m * 200 / 3)
+    def hz_to_mel(f):
+        return np.where(f >= 1000, 15 + 27 * np.log(f / 1000) / np.log(6.4), f * 3 / 200)
+    edges = mel_to_hz(np.linspace(0, hz_to_mel(12000.0), 130))
+    for b in (0, 10, 64, 127):
+        w = fb[b]
+        inside = (hz > edges[b]) & (hz < edges[b + 2])
+        assert (w[~inside] == 0).all()
+        tri = np.maximum(0, np.minimum((hz - edges[b]) / (edges[b + 1] - edges[b]),
+                                       (edges[b + 2] - hz) / (edges[b + 2] - edges[b + 1])))
+        assert np.allclose(w, (tri * 2 / (edges[b + 2] - edges[b])).astype(np.float32), rtol=1e-6, atol=1e-9)
+
+
+def test_log_mel_tone_and_silence():
+    """A 1 kHz tone puts its largest energy in the filter whose band centre
+    is nearest 1 kHz, in every interior frame; digital silence gives the log
+    floor, log(max(sqrt(1e-9) * filter sum, 1e-5))."""
+    t = np.arange(24000) / 24000
+    tone = (0.5 * np.sin(2 * np.pi * 1000 * t)).astype(np.float32)
+    y = oracle_log_mel(tone, MEL)
+    centres = np.where(np.linspace(0, 15 + 27 * np.log(12) / np.log(6.4), 130)[1:-1] >= 15,
+                       1000 * 6.4 ** ((np.linspace(0, 15 + 27 * np.log(12) / np.log(6.4), 130)[1:-1] - 15) / 27),
+                       np.linspace(0, 15 + 27 * np.log(12) / np.log(6.4), 130)[1:-1] * 200 / 3)
+    assert (np.argmax(y[5:-5], axis=1) == np.argmin(np.abs(centres - 1000))).all()
+    z = oracle_log_mel(np.zeros(24000, np.float32), MEL)
+    fb = R.mel_filterbank(24000, 1024, 128, 0.0, 12000.0).astype(np.float64)
+    floor = np.log(np.maximum(np.float32(np.sqrt(1e-9)) * fb.sum(axis=1), 1e-5)).astype(np.float32)
+    assert np.allclose(z, floor[None, :], atol=1e-6)
+
+
+@pytest.mark.parametrize("case", [("noise", 24000, MEL), ("tone", 7000, dict(MEL, hop=512)),
+                                  ("noise", 3000, dict(MEL, n_fft=512, win_length=400, hop=160, mel_bins=80)),
+                                  ("noise", 385, MEL)])
+def test_log_mel_restatement_is_the_reference_build(case):
+    """The restatement against the reference's own compute_log_mel compiled
+    from the checkout (oracle/_ref): bit for bit, at the production
+    parameters, at hop 512, with a shorter zero-padded window and fewer bins,
+    and at the shortest clip upstream's reflect pad allows (385 samples);
+    384 samples are refused by both. Skipped where the reference checkout
+    was not there to build it."""
+    import ctypes
+    L = _ref_mel_lib()
+    if L is None:
+        pytest.skip("oracle/_ref not built (no reference checkout)")
+    kind, ns, p = case
+    rng = np.random.default_rng(ns)
+    pcm = (rng.standard_normal(ns) * 0.2).astype(np.float32) if kind == "noise" else \
+        (0.3 * np.sin(2 * np.pi * 440 * np.arange(ns) / 24000)).astype(np.float32)
+    got = oracle_log_mel(pcm, p)
+    out = np.empty(got.size + 16, np.float32)
+    frames = ctypes.c_uint64()
+    assert L.ref_log_mel(pcm.ctypes.data, ns, p["sample_rate"], p["n_fft"], p["hop"], p["win_length"],
+                         p["mel_bins"], p["fmin"], p["fmax"], out.ctypes.data, out.size, ctypes.byref(frames)) == 0
+    assert frames.value == got.shape[0]
+    assert np.array_equal(got.reshape(-1).view(np.uint32), out[:got.size].view(np.uint32))
+    if ns == 385:
+        short = pcm[:384].copy()
+        assert L.ref_log_mel(short.ctypes.data, 384, p["sample_rate"], p["n_fft"], p["hop"], p["win_length"],
+                             p["mel_bins"], p["fmin"], p["fmax"], out.ctypes.data, out.size,
+                             ctypes.byref(frames)) != 0
+        with pytest.raises(ValueError):
+            oracle_log_mel(short, p)
