@@ -182,6 +182,145 @@ __global__ __launch_bounds__(kC2iBlock) void k_col2im_1d(const Col2imArgs a) {
     }
 }
 
+// The persistent, double-buffered form (16-byte column loads: a tile's row
+// pieces are at most kC2iLds/4 = 1152, so each lane's share, five at most,
+// fits one batch of registers): a block walks tiles blockIdx.x, +gridDim.x,
+// ...; the next tile's loads are issued before the current tile's outputs
+// are written from the other LDS buffer, so the two overlap within a block;
+// one barrier per tile.
+constexpr int kC2iPersist = 1024;  // blocks: four per CU at 2 x 18 KB of LDS
+
+struct C2iTile {
+    int oc0, t0, noc, ntt, u0, lb, le;
+};
+
+__device__ __forceinline__ C2iTile c2i_tile(const Col2imArgs & a, uint32_t tile) {
+    C2iTile       g;
+    const uint32_t q = fastdiv(tile, a.toc);
+    g.oc0            = static_cast<int>(tile - q * a.toc.d) * a.oct;
+    g.t0             = static_cast<int>(q) * a.tt;
+    g.noc            = a.oc - g.oc0 < a.oct ? a.oc - g.oc0 : a.oct;
+    g.ntt            = a.t - g.t0 < a.tt ? a.t - g.t0 : a.tt;
+    g.u0             = g.t0 + a.p;
+    g.lb             = g.u0 >= a.k ? static_cast<int>(fastdiv(static_cast<uint32_t>(g.u0 - a.k), a.sdiv)) + 1 : 0;
+    g.le             = static_cast<int>(fastdiv(static_cast<uint32_t>(g.u0 + g.ntt - 1), a.sdiv));
+    g.le             = g.le < a.l - 1 ? g.le : a.l - 1;
+    return g;
+}
+
+template <int NT, bool V4STORE>
+__global__ __launch_bounds__(kC2iBlock) void k_col2im_1d_pipe(const Col2imArgs a, uint32_t ntiles) {
+    extern __shared__ float lds2[];
+    const int    tid  = static_cast<int>(threadIdx.x);
+    const int    rw   = a.rwp;
+    const int    bufn = a.nlmax * rw;
+    const int    w    = static_cast<int>(a.rdiv.d);
+    f32x4        v[kC2iBatch];
+    int          at[kC2iBatch];
+    // issue tile's row-piece loads into v / at (LDS offsets, -1 for none)
+    auto issue = [&](const C2iTile & g) {
+        const int    nrw = g.noc * a.k / 4;
+        int          r   = static_cast<int>(fastdiv(static_cast<uint32_t>(tid), a.rdiv));
+        int          j   = tid - r * w;
+        const int    dr = kC2iBlock / w, dj = kC2iBlock % w;
+        const char * cb = a.c + static_cast<int64_t>(g.oc0) * a.k * 4 + static_cast<int64_t>(g.lb) * a.cnb1;
+#pragma unroll
+        for (int b = 0; b < kC2iBatch; ++b) {
+            const bool in = g.lb + r <= g.le && j < nrw;
+            at[b]         = in ? r * rw + j * 4 : -1;
+            if (in) {
+                v[b] = *reinterpret_cast<const f32x4 *>(cb + static_cast<int64_t>(r) * a.cnb1 + j * 16);
+            }
+            r += dr;
+            j += dj;
+            if (j >= w) {
+                j -= w;
+                ++r;
+            }
+        }
+    };
+    auto write = [&](float * buf) {
+#pragma unroll
+        for (int b = 0; b < kC2iBatch; ++b) {
+            if (at[b] >= 0) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    buf[at[b] + i] = v[b][i];
+                }
+            }
+        }
+    };
+    uint32_t tile = blockIdx.x;
+    if (tile >= ntiles) {
+        return;
+    }
+    C2iTile g = c2i_tile(a, tile);
+    issue(g);
+    write(lds2);
+    __syncthreads();
+    int cur = 0;
+    for (; tile < ntiles; tile += gridDim.x) {
+        const uint32_t next = tile + gridDim.x;
+        C2iTile        gn{};
+        if (next < ntiles) {
+            gn = c2i_tile(a, next);
+            issue(gn);  // in flight while this tile's outputs are written
+        }
+        const float * lds = lds2 + cur * bufn;
+        const int     nq  = a.tt / 4;
+        for (int tl = (tid % nq) * 4; tl < g.ntt; tl += kC2iBlock * 4) {
+            int      off[4][NT];
+            uint32_t ok = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int u  = g.u0 + tl + e;
+                const int qh = static_cast<int>(fastdiv(static_cast<uint32_t>(u), a.sdiv));
+                const int r  = u - qh * a.s;
+#pragma unroll
+                for (int j = 0; j < NT; ++j) {
+                    const int  l  = qh - (NT - 1 - j);
+                    const int  k  = r + (NT - 1 - j) * a.s;
+                    const bool in = tl + e < g.ntt && k < a.k && l >= 0 && l <= a.l - 1;
+                    off[e][j]     = in ? (l - g.lb) * rw + k : 0;
+                    ok |= static_cast<uint32_t>(in) << (e * 4 + j);
+                }
+            }
+            for (int ocl = tid / nq; ocl < g.noc; ocl += kC2iBlock / nq) {
+                char *    yrow = a.y + static_cast<int64_t>(g.oc0 + ocl) * a.ynb1;
+                const int cko  = ocl * a.k;
+                float     o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < NT; ++j) {
+                        const float x = lds[cko + off[e][j]];
+                        acc           = (ok >> (e * 4 + j)) & 1u ? acc + x : acc;
+                    }
+                    o[e] = acc;
+                }
+                if (V4STORE && tl + 3 < g.ntt) {
+                    __builtin_nontemporal_store(f32x4{ o[0], o[1], o[2], o[3] },
+                                                reinterpret_cast<f32x4 *>(yrow + static_cast<int64_t>(g.t0 + tl) * 4));
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if (tl + e < g.ntt) {
+                            __builtin_nontemporal_store(o[e], reinterpret_cast<float *>(yrow) + g.t0 + tl + e);
+                        }
+                    }
+                }
+            }
+        }
+        if (next < ntiles) {
+            write(lds2 + (cur ^ 1) * bufn);
+        }
+        __syncthreads();
+        cur ^= 1;
+        g = gn;
+    }
+}
+
 }  // namespace
 
 struct Col2imPlan {
@@ -264,6 +403,20 @@ shp_status_t plan_col2im_1d(const shp_tensor * cols, int32_t stride, int32_t oc,
 
 template <int NT> void launch_nt(const Col2imPlan & pl, hipStream_t s) {
     const dim3 g(pl.grid), b(kC2iBlock);
+    if constexpr (NT > 0) {
+        // the persistent double-buffered form, with four tiles or more per block
+        // (at [128,131072] K=4: 47.6 -> 45.8 us; [256,32768] K=16: 25.6 -> 25.1;
+        // with two per block, [512,8192] K=16, 12.2 -> 13.2: not taken)
+        if (pl.v4load && pl.grid >= 4u * kC2iPersist) {
+            const dim3 gp(pl.grid < kC2iPersist ? pl.grid : kC2iPersist);
+            if (pl.v4store) {
+                hipLaunchKernelGGL((k_col2im_1d_pipe<NT, true>), gp, b, 2 * pl.shmem, s, pl.args, pl.grid);
+            } else {
+                hipLaunchKernelGGL((k_col2im_1d_pipe<NT, false>), gp, b, 2 * pl.shmem, s, pl.args, pl.grid);
+            }
+            return;
+        }
+    }
     if (pl.v4load && pl.v4store) {
         hipLaunchKernelGGL((k_col2im_1d<NT, true, true>), g, b, pl.shmem, s, pl.args);
     } else if (pl.v4load) {
