@@ -9,7 +9,10 @@ ggml-CPU restatement on the same inputs:
 - sum_rows, mean and the fused mul→sum_rows over row lengths either side of
   the wave's width, values spread over 16 binary orders of magnitude;
 - diag_mask_inf at random n_past, and the fused causal softmax against the
-  two nodes it replaces.
+  two nodes it replaces;
+- the host-seam ports (inverse_stft, harmonic_source, log_mel) at random
+  windows, hops, harmonic counts, upsampling factors and bin counts, held to
+  their focused tests' bars.
 The bars are the focused tests': bit-exact for every copy, add, mask, unary
 op and row sum (the restatement accumulates in double and rounds once, as
 ggml does); the fused softmax bit-identical to the two GPU nodes and within
@@ -197,3 +200,73 @@ def test_sweep_diag_mask_and_causal_softmax(gpu, H, T, N, n_past):
     # the neighbouring float moves the whole row by one ulp, so the share of
     # identical elements over a few rows says little
     assert _ulps_apart(fused, ref).max() <= 2
+
+
+# ---------------------------------------------------------------------------
+# the host seams: inverse STFT, harmonic source, log-mel
+# ---------------------------------------------------------------------------
+
+def _istft_case(rng):
+    n_fft = 2 * int(rng.integers(1, 33))
+    hop = int(rng.integers(1, n_fft + 5))
+    frames = _pick(rng, [2, 3, 17, 64, 65, 500, 3001])
+    nf = (63 + n_fft - 1) // hop + 2  # the kernel's smallest tile's frames must fit its LDS budget
+    if (nf * (n_fft // 2 + 1) + n_fft) * 16 > 48 * 1024:
+        return None
+    return (n_fft, hop, frames)
+
+
+@pytest.mark.parametrize("n_fft,hop,frames", _gen("istft", _istft_case))
+def test_sweep_inverse_stft(gpu, n_fft, hop, frames):
+    from test_gpu_istft import _close as istft_close
+    rng = np.random.default_rng([SWEEP_SEED, 4, n_fft, hop, frames])
+    spec = rng.uniform(-3, 2, (frames, n_fft + 2)).astype(np.float32)
+    istft_close(_np(gpu.inverse_stft(_t(gpu, spec), n_fft, hop)), R.run(lambda g: g.inverse_stft(spec, n_fft, hop)))
+
+
+def _source_case(rng):
+    L = _pick(rng, [1, 2, 5, 37, 200])
+    H = _pick(rng, [1, 2, 9, 16, 64])
+    scale = _pick(rng, [2, 3, 8, 60, 300])
+    n_fft = 2 * int(rng.integers(1, 33))
+    hop = int(rng.integers(1, n_fft + 1))
+    n = L * scale
+    if n < 2 or (n_fft + 2) * (n // hop) < L * H or n * H > MAX_ELEMS:
+        return None
+    return (L, H, scale, n_fft, hop)
+
+
+@pytest.mark.parametrize("L,H,scale,n_fft,hop", _gen("source", _source_case, n=16))
+def test_sweep_harmonic_source(gpu, L, H, scale, n_fft, hop):
+    from test_gpu_source import _close as source_close, _run_gpu, _run_ref
+    from test_oracle_goldens import random_source_case
+    args, kw = random_source_case(SWEEP_SEED + L * 7 + H * 13 + scale + n_fft + hop, L, H, scale, n_fft, hop)
+    source_close(_run_gpu(gpu, args, kw), _run_ref(args, kw), n_fft // 2 + 1)
+
+
+def _mel_case(rng):
+    n_fft = _pick(rng, [64, 128, 256, 512, 1024, 2048])
+    hop = int(rng.integers(1, n_fft + 1)) if rng.random() < 0.3 else n_fft // _pick(rng, [1, 2, 4, 8])
+    win = int(rng.integers(n_fft // 2, n_fft + 1))
+    bins = _pick(rng, [1, 8, 40, 80, 128, 256])
+    ns = _pick(rng, [n_fft, 3000, 24000])
+    pad = (n_fft - hop) // 2
+    if ns <= pad or ns + 2 * pad < n_fft or (ns + 2 * pad - n_fft) // hop + 1 > 3000:
+        return None
+    return (n_fft, hop, win, bins, ns)
+
+
+@pytest.mark.parametrize("n_fft,hop,win,bins,ns", _gen("log_mel", _mel_case, n=16))
+def test_sweep_log_mel(gpu, n_fft, hop, win, bins, ns):
+    """Random windows, hops, window lengths (zero-padded Hann) and bin
+    counts; within 1e-5 of the restatement, > 95 % identical (short clips and
+    few bins leave few values to share)."""
+    from test_oracle_goldens import MEL, oracle_log_mel
+    p = dict(MEL, n_fft=n_fft, hop=hop, win_length=win, mel_bins=bins)
+    pcm = (np.random.default_rng([SWEEP_SEED, 5, n_fft, hop, win, bins, ns]).standard_normal(ns) * 0.2).astype(np.float32)
+    fb = gpu.mel_filterbank(p["sample_rate"], n_fft, bins, p["fmin"], p["fmax"])
+    got = _np(gpu.log_mel(_t(gpu, pcm), _t(gpu, fb), n_fft, hop, win))
+    ref = oracle_log_mel(pcm, p)
+    assert got.shape == ref.shape
+    assert np.abs(got - ref).max() <= 1e-5
+    assert (got == ref).mean() > 0.95
