@@ -1370,7 +1370,11 @@ def trace_summary(rocdir, log):
     out = ["# kernel durations per bench row, from rocprofv3's kernel trace (End-Start per dispatch) and the",
            "# ROCTx range bench.py puts around each row's timed replays; bytes = the row's algorithmic bytes;",
            "# trace_GB/s = bytes / avg_ns; frac = trace_GB/s / 8000; bench_us = bench.py's HIP-event time per",
-           "# launch for the row in the same run (graph replay, events on the replay stream).",
+           "# launch for the row in the JSON line given: an unprofiled run on the same box just before (graph",
+           "# replay, events on the replay stream).",
+           "# made by (from /tmp with TMPDIR=/tmp, R the repository root): python3 -u $R/bench.py > bench.json (unprofiled);",
+           "#   rocprofv3 --kernel-trace --marker-trace --stats --output-format csv -d prof -o bench -- python3 -u $R/bench.py;",
+           "#   python3 $R/bench.py --trace-summary prof bench.json",
            "%-11s %-44s %-36s %9s %6s %9s %9s %9s %9s %9s %6s" % (
                "config", "op", "kernel", "grid", "calls", "avg_ns", "med_ns", "min_ns", "bench_us", "trace_GB/s",
                "frac")]
@@ -1434,7 +1438,10 @@ def pmc_summary(fetch_dir, write_dir, log):
            "# FETCH_SIZE %.1f KiB -> scale %.4f; WRITE_SIZE %.1f KiB -> scale %.4f." % (cal_f, fs, cal_w, ws),
            "# hbm_bytes = (FETCH_KiB * fetch_scale + WRITE_KiB * write_scale) * 1024, averaged over the 3 launches;",
            "# ratio = hbm_bytes / algorithmic bytes (gathers: logical, every looked-up row per lookup). FETCH_SIZE",
-           "# counts what L2 fetches from beyond it (Infinity Cache or HBM)."]
+           "# counts what L2 fetches from beyond it (Infinity Cache or HBM).",
+           "# made by (from /tmp with TMPDIR=/tmp, R the repository root), for M in FETCH_SIZE WRITE_SIZE:",
+           "#   rocprofv3 --pmc $M --output-format csv -d pmc_$M -o x -- python3 -u $R/bench.py --pmc-large > pmc_$M.log;",
+           "#   python3 $R/bench.py --pmc-summary pmc_FETCH_SIZE pmc_WRITE_SIZE pmc_FETCH_SIZE.log"]
     assert len(ours) == 3 * len(PMC_OPS), (len(ours), len(PMC_OPS))
     for j, (op, nbytes) in enumerate(PMC_OPS):
         idx = ours[3 * j:3 * j + 3]
@@ -1469,6 +1476,10 @@ def occ_summary(dirs):
            "# per CU, time-averaged (MeanOccupancyPerCU); valu% = % of time a CU issues VALU (VALUBusy); mstl% =",
            "# % of time the memory unit is stalled on data (MemUnitStalled); vgpr/sgpr/lds from the dispatch",
            "# records (lds in bytes per workgroup).",
+           "# made by (from /tmp with TMPDIR=/tmp, R the repository root), for M in OccupancyPercent",
+           "# MeanOccupancyPerCU VALUBusy MemUnitStalled: rocprofv3 --pmc $M --output-format csv -d occ_$M -o o --",
+           "#   python3 -u $R/bench.py --pmc-large; then python3 $R/bench.py --occ-summary occ_OccupancyPercent",
+           "#   occ_MeanOccupancyPerCU occ_VALUBusy occ_MemUnitStalled",
            "%-44s %-34s %9s %7s %7s %7s %7s %5s %5s %6s" % ("op", "kernel", "grid", "occ%", "w/CU", "valu%", "mstl%",
                                                           "vgpr", "sgpr", "lds")]
     for j, (op, _) in enumerate(PMC_OPS):
